@@ -1,0 +1,80 @@
+"""ctypes binding of libgdnx.so (the C ABI declared in include/gdnx.h).
+
+torch is imported first so that the library's libamdhip64.so.7 dependency
+resolves to the HIP runtime torch already loaded (same soname): device
+pointers and streams are then shared with torch.  There is no fallback: if
+the library is missing, every op raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+
+import torch  # noqa: F401  (must precede the CDLL load, see above)
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_HERE, "libgdnx.so")
+
+DTYPE_F32 = 0
+DTYPE_BF16 = 1
+ABI_VERSION = 1
+
+_c_int, _c_ll, _vp = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p
+
+# name -> (restype, argtypes); every entry point declared in include/gdnx.h
+SIGNATURES = {
+    "gdnx_abi_version": (_c_int, []),
+    "gdnx_last_error": (ctypes.c_char_p, []),
+    "gdnx_delta_chunk_size": (_c_int, [_c_int, _c_int]),
+    "gdnx_delta_chunk_states_bytes": (_c_ll, [_c_int] * 6),
+    "gdnx_delta_chunk_fwd": (_c_int, [_vp] * 10 + [_c_int] * 6 + [_vp]),
+}
+
+
+class GdnxError(RuntimeError):
+    pass
+
+
+_lib = None
+
+
+def load():
+    """Load and bind libgdnx.so once; raises GdnxError if it is absent."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    if not os.path.exists(LIB_PATH):
+        raise GdnxError(f"{LIB_PATH} is not built; run `python -m gdnx_amd.build` "
+                        "(there is no non-HIP fallback)")
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.gdnx_abi_version() != ABI_VERSION:
+        raise GdnxError(f"ABI version mismatch: library {lib.gdnx_abi_version()}, "
+                        f"binding {ABI_VERSION}")
+    _lib = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load().gdnx_last_error().decode(errors="replace")
+        raise GdnxError(f"{what} failed ({rc}): {msg}")
+
+
+def ptr(t):
+    return None if t is None else ctypes.c_void_p(t.data_ptr())
+
+
+def stream_of(t) -> ctypes.c_void_p:
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def dtype_code(dt) -> int:
+    if dt == torch.bfloat16:
+        return DTYPE_BF16
+    if dt == torch.float32:
+        return DTYPE_F32
+    raise GdnxError(f"unsupported io dtype {dt} (bfloat16 or float32)")

@@ -1,0 +1,78 @@
+// C-ABI entry points of libgdnx: argument validation, then dispatch.
+#include <stdarg.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "gdnx_internal.hpp"
+
+namespace gdnx {
+
+static thread_local char g_err[512] = "";
+
+int set_error(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int check_launch(const char* what) {
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return set_error(GDNX_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  return GDNX_OK;
+}
+
+int delta_chunk_size(int D, int dtype) {
+  if (D != 64 && D != 128) return 0;
+  return dtype == GDNX_DTYPE_BF16 ? 64 : 32;
+}
+
+static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+static int check_common(const void* q, const void* k, const void* v, int B, int T, int H, int M,
+                        int D, int dtype) {
+  if (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16)
+    return set_error(GDNX_ERR_ARG, "dtype %d is not GDNX_DTYPE_F32/BF16", dtype);
+  if (D != 64 && D != 128) return set_error(GDNX_ERR_SHAPE, "head_dim %d unsupported (64 or 128)", D);
+  if (B < 1 || T < 0 || H < 1 || M < 1)
+    return set_error(GDNX_ERR_SHAPE, "bad sizes B=%d T=%d H=%d M=%d", B, T, H, M);
+  if ((long long)B * H * M > (1LL << 30)) return set_error(GDNX_ERR_SHAPE, "too many chains");
+  if (!q || !k || !v) return set_error(GDNX_ERR_ARG, "q, k, v must be non-null");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v))
+    return set_error(GDNX_ERR_ARG, "q, k, v must be 16-byte aligned");
+  return GDNX_OK;
+}
+
+}  // namespace gdnx
+
+using namespace gdnx;
+
+extern "C" int gdnx_abi_version(void) { return GDNX_ABI_VERSION; }
+
+extern "C" const char* gdnx_last_error(void) { return g_err; }
+
+extern "C" int gdnx_delta_chunk_size(int head_dim, int dtype) { return delta_chunk_size(head_dim, dtype); }
+
+extern "C" long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim, int dtype) {
+  const int C = delta_chunk_size(head_dim, dtype);
+  if (C == 0 || B < 1 || T < 0 || H < 1 || M < 1) return -1;
+  const long long nc = (T + C - 1) / C;
+  const long long esz = dtype == GDNX_DTYPE_BF16 ? 2 : 4;
+  return (long long)B * H * M * nc * head_dim * head_dim * esz;
+}
+
+extern "C" int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v, const float* a_e,
+                                    const float* a_w, const float* log_g, const float* state0, void* y,
+                                    float* state_out, void* chunk_states, int B, int T, int H, int M,
+                                    int head_dim, int dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
+  if (rc) return rc;
+  if (!a_e || !a_w || !log_g || !y) return set_error(GDNX_ERR_ARG, "a_e, a_w, log_g, y must be non-null");
+  if (chunk_states && ((uintptr_t)chunk_states & 15u))
+    return set_error(GDNX_ERR_ARG, "chunk_states must be 16-byte aligned");
+  if (T == 0) return GDNX_OK;
+  DeltaArgs a{q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, B, T, H, M, head_dim, dtype};
+  return delta_fwd_dispatch(a, (hipStream_t)stream);
+}

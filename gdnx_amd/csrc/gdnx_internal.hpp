@@ -1,0 +1,31 @@
+// Internal (non-ABI) declarations shared by the gdnx translation units.
+#pragma once
+#include <hip/hip_runtime.h>
+
+#include "../../include/gdnx.h"
+
+namespace gdnx {
+
+struct DeltaArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* ae;
+  const float* aw;
+  const float* g;
+  const float* s0;
+  void* y;
+  float* s_out;
+  void* chunk_states;
+  int B, T, H, M, D, dtype;
+};
+
+// Record an error message for gdnx_last_error(); returns code.
+int set_error(int code, const char* fmt, ...);
+// Check hipGetLastError() after a launch.
+int check_launch(const char* what);
+
+int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);
+int delta_chunk_size(int D, int dtype);
+
+}  // namespace gdnx

@@ -1,0 +1,68 @@
+/* gdnx -- MI355X-native chunked GDN3 / KMD-2 recurrence, C ABI.
+ *
+ * All entry points are asynchronous on the given HIP stream (passed as
+ * void*), allocate nothing, use no float atomics (results are bitwise
+ * deterministic) and return an int status: 0 on success, a negative
+ * GDNX_ERR_* code otherwise (message via gdnx_last_error(), per thread).
+ * Pointers are device pointers to contiguous row-major tensors; the caller
+ * owns every buffer.  No C++ exception crosses this boundary.
+ *
+ * Layouts (b batch, t token, h head, m lane, d/v feature):
+ *   q, k, v      [B, T, H, D]        io dtype; shared by the M lanes of a head
+ *   a_e, a_w, g  [B, T, H, M]        float32 per-token erase / write
+ *                                    coefficients and natural-log decay
+ *   y, dy        [B, T, H, M, D]     io dtype
+ *   state        [B, H, M, D, D]     float32, key-major [d_k][d_v]
+ */
+#ifndef GDNX_H
+#define GDNX_H
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define GDNX_ABI_VERSION 1
+
+enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1 };
+
+enum {
+  GDNX_OK = 0,
+  GDNX_ERR_ARG = -1,       /* null / misaligned pointer, bad enum */
+  GDNX_ERR_SHAPE = -2,     /* unsupported or inconsistent sizes */
+  GDNX_ERR_WORKSPACE = -3, /* workspace missing or too small */
+  GDNX_ERR_HIP = -4        /* HIP launch or runtime error */
+};
+
+/* Version of this ABI (GDNX_ABI_VERSION). */
+int gdnx_abi_version(void);
+
+/* Message of the last error on the calling thread ("" if none). */
+const char* gdnx_last_error(void);
+
+/* Internal chunk length used for head_dim / dtype (tokens). */
+int gdnx_delta_chunk_size(int head_dim, int dtype);
+
+/* Bytes of the per-chunk state stash the forward writes for the backward. */
+long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim, int dtype);
+
+/* Chunked decoupled-erase delta rule, forward.
+ * Replaces the sequential token loop of
+ *   GDN3LinearAttn._gdn3_recurrent_state  (reference gdn3/gdn3_upgrade.py:403-531,
+ *   frozen oracle gdn3/_reference_recurrence.py:33-94) in its dense regime, and
+ *   the KMD-2 scan core (gdn3/kmd2_fast_scan.py:163-260; oracle
+ *   research/kernel_ab/ref_scan.py:24-48) with scalar decay.
+ * Per chain (b, h, m), token t:  S <- exp(min(g,0)) S;  r = a_w v - a_e S^T k;
+ *   S <- S + k r^T;  y = S^T q.
+ * state0 / state_out / chunk_states may be NULL.  chunk_states (size from
+ * gdnx_delta_chunk_states_bytes) receives the state entering every chunk,
+ * which gdnx_delta_chunk_bwd needs. */
+int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v,
+                         const float* a_e, const float* a_w, const float* log_g,
+                         const float* state0, void* y, float* state_out,
+                         void* chunk_states, int B, int T, int H, int M,
+                         int head_dim, int dtype, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* GDNX_H */
