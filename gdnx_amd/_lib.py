@@ -26,8 +26,10 @@ SIGNATURES = {
     "gdnx_abi_version": (_c_int, []),
     "gdnx_last_error": (ctypes.c_char_p, []),
     "gdnx_delta_chunk_size": (_c_int, [_c_int, _c_int]),
-    "gdnx_delta_chunk_states_bytes": (_c_ll, [_c_int] * 6),
-    "gdnx_delta_chunk_fwd": (_c_int, [_vp] * 10 + [_c_int] * 6 + [_vp]),
+    "gdnx_delta_train_chunk_size": (_c_int, [_c_int, _c_int]),
+    "gdnx_delta_chunk_states_bytes": (_c_ll, [_c_int] * 7),
+    "gdnx_delta_chunk_fwd": (_c_int, [_vp] * 10 + [_c_int] * 7 + [_vp]),
+    "gdnx_delta_chunk_bwd": (_c_int, [_vp] * 17 + [_c_int] * 7 + [_vp]),
 }
 
 

@@ -28,6 +28,19 @@ int delta_chunk_size(int D, int dtype) {
   return dtype == GDNX_DTYPE_BF16 ? 64 : 32;
 }
 
+// chunk used when the forward stashes states for the backward: the gradient
+// kernel keeps S0 / dS value-contiguous in LDS, which bounds the chunk
+int delta_train_chunk_size(int D, int dtype) {
+  if (D != 64 && D != 128) return 0;
+  return dtype == GDNX_DTYPE_BF16 ? 32 : 16;
+}
+
+static bool valid_chunk(int D, int dtype, int C) {
+  if (dtype == GDNX_DTYPE_BF16) return C == 32 || C == 64;
+  return C == 16 || C == 32;
+  (void)D;
+}
+
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
 static int check_common(const void* q, const void* k, const void* v, int B, int T, int H, int M,
@@ -54,9 +67,16 @@ extern "C" const char* gdnx_last_error(void) { return g_err; }
 
 extern "C" int gdnx_delta_chunk_size(int head_dim, int dtype) { return delta_chunk_size(head_dim, dtype); }
 
-extern "C" long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim, int dtype) {
-  const int C = delta_chunk_size(head_dim, dtype);
-  if (C == 0 || B < 1 || T < 0 || H < 1 || M < 1) return -1;
+extern "C" int gdnx_delta_train_chunk_size(int head_dim, int dtype) {
+  return delta_train_chunk_size(head_dim, dtype);
+}
+
+extern "C" long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim, int chunk,
+                                                   int dtype) {
+  const int C = chunk ? chunk : delta_chunk_size(head_dim, dtype);
+  if (C == 0 || !valid_chunk(head_dim, dtype, C) || B < 1 || T < 0 || H < 1 || M < 1 ||
+      (head_dim != 64 && head_dim != 128))
+    return -1;
   const long long nc = (T + C - 1) / C;
   const long long esz = dtype == GDNX_DTYPE_BF16 ? 2 : 4;
   return (long long)B * H * M * nc * head_dim * head_dim * esz;
@@ -65,14 +85,39 @@ extern "C" long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, i
 extern "C" int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v, const float* a_e,
                                     const float* a_w, const float* log_g, const float* state0, void* y,
                                     float* state_out, void* chunk_states, int B, int T, int H, int M,
-                                    int head_dim, int dtype, void* stream) {
+                                    int head_dim, int chunk, int dtype, void* stream) {
   g_err[0] = 0;
   int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
   if (rc) return rc;
   if (!a_e || !a_w || !log_g || !y) return set_error(GDNX_ERR_ARG, "a_e, a_w, log_g, y must be non-null");
   if (chunk_states && ((uintptr_t)chunk_states & 15u))
     return set_error(GDNX_ERR_ARG, "chunk_states must be 16-byte aligned");
+  const int C = chunk ? chunk : delta_chunk_size(head_dim, dtype);
+  if (!valid_chunk(head_dim, dtype, C)) return set_error(GDNX_ERR_SHAPE, "chunk %d invalid for this dtype", chunk);
   if (T == 0) return GDNX_OK;
-  DeltaArgs a{q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, B, T, H, M, head_dim, dtype};
+  DeltaArgs a{q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, B, T, H, M, head_dim, C, dtype};
   return delta_fwd_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v, const float* a_e,
+                                    const float* a_w, const float* log_g, const void* dy,
+                                    const float* dstate_out, const void* chunk_states, void* workspace,
+                                    void* dq, void* dk, void* dv, float* da_e, float* da_w, float* dlog_g,
+                                    float* dstate0, int B, int T, int H, int M, int head_dim, int chunk,
+                                    int dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
+  if (rc) return rc;
+  if (!a_e || !a_w || !log_g || !dy || !dq || !dk || !dv || !da_e || !da_w || !dlog_g)
+    return set_error(GDNX_ERR_ARG, "inputs and gradient outputs must be non-null");
+  if (!chunk_states || !workspace)
+    return set_error(GDNX_ERR_WORKSPACE, "chunk_states (from the forward) and workspace are required");
+  if (((uintptr_t)chunk_states & 15u) || ((uintptr_t)workspace & 15u) || !aligned16(dy))
+    return set_error(GDNX_ERR_ARG, "chunk_states, workspace and dy must be 16-byte aligned");
+  const int C = chunk ? chunk : delta_train_chunk_size(head_dim, dtype);
+  if (!valid_chunk(head_dim, dtype, C)) return set_error(GDNX_ERR_SHAPE, "chunk %d invalid for this dtype", chunk);
+  if (T == 0) return GDNX_OK;
+  DeltaBwdArgs a{q,  k,  v,  a_e,  a_w,  log_g, dy,      dstate_out, chunk_states, workspace, dq, dk,
+                 dv, da_e, da_w, dlog_g, dstate0, B, T, H, M, head_dim, C, dtype};
+  return delta_bwd_dispatch(a, (hipStream_t)stream);
 }

@@ -17,7 +17,28 @@ struct DeltaArgs {
   void* y;
   float* s_out;
   void* chunk_states;
-  int B, T, H, M, D, dtype;
+  int B, T, H, M, D, C, dtype;
+};
+
+struct DeltaBwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* ae;
+  const float* aw;
+  const float* g;
+  const void* dy;
+  const float* ds_final;
+  const void* s_stash;
+  void* ds_stash;
+  void* dq;
+  void* dk;
+  void* dv;
+  float* dae;
+  float* daw;
+  float* dg;
+  float* ds0;
+  int B, T, H, M, D, C, dtype;
 };
 
 // Record an error message for gdnx_last_error(); returns code.
@@ -26,6 +47,8 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
 int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);
+int delta_bwd_dispatch(const DeltaBwdArgs& a, hipStream_t stream);
 int delta_chunk_size(int D, int dtype);
+int delta_train_chunk_size(int D, int dtype);
 
 }  // namespace gdnx

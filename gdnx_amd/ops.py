@@ -22,7 +22,7 @@ def _check_dense(q, k, v, a_e, a_w, log_g):
     _need(q.dim() == 4 and q.shape == k.shape == v.shape, "q, k, v must share shape [B,T,H,D]")
     _need(q.dtype == k.dtype == v.dtype, "q, k, v must share dtype")
     B, T, H, D = q.shape
-    _need(a_e.dim() == 4 and a_e.shape[:3] == (B, T, H), "a_e must be [B,T,H,M]")
+    _need(a_e.dim() == 4 and tuple(a_e.shape[:3]) == (B, T, H), "a_e must be [B,T,H,M]")
     _need(a_e.shape == a_w.shape == log_g.shape, "a_e, a_w, log_g must share shape")
     for t in (a_e, a_w, log_g):
         _need(t.dtype == torch.float32, "a_e, a_w, log_g must be float32")
@@ -32,12 +32,14 @@ def _check_dense(q, k, v, a_e, a_w, log_g):
     return B, T, H, a_e.shape[3], D
 
 
-def chunk_size(head_dim: int, dtype) -> int:
-    return _lib.load().gdnx_delta_chunk_size(head_dim, _lib.dtype_code(dtype))
+def chunk_size(head_dim: int, dtype, train: bool = False) -> int:
+    lib = _lib.load()
+    fn = lib.gdnx_delta_train_chunk_size if train else lib.gdnx_delta_chunk_size
+    return fn(head_dim, _lib.dtype_code(dtype))
 
 
 def delta_chunk_fwd(q, k, v, a_e, a_w, log_g, state0=None, *, return_state=False,
-                    save_states=False):
+                    save_states=False, chunk=0):
     """Forward of the lane-shared decoupled-erase delta rule.
 
     Returns (y, state_out or None, chunk_states or None)."""
@@ -45,19 +47,82 @@ def delta_chunk_fwd(q, k, v, a_e, a_w, log_g, state0=None, *, return_state=False
     B, T, H, M, D = _check_dense(q, k, v, a_e, a_w, log_g)
     code = _lib.dtype_code(q.dtype)
     if state0 is not None:
-        _need(state0.shape == (B, H, M, D, D) and state0.dtype == torch.float32
+        _need(tuple(state0.shape) == (B, H, M, D, D) and state0.dtype == torch.float32
               and state0.is_contiguous(), "state0 must be contiguous float32 [B,H,M,D,D]")
     dev = q.device
     y = torch.empty(B, T, H, M, D, dtype=q.dtype, device=dev)
     s_out = torch.empty(B, H, M, D, D, dtype=torch.float32, device=dev) if return_state else None
     cs = None
     if save_states:
-        nbytes = lib.gdnx_delta_chunk_states_bytes(B, T, H, M, D, code)
+        nbytes = lib.gdnx_delta_chunk_states_bytes(B, T, H, M, D, chunk, code)
+        _need(nbytes >= 0, f"invalid chunk {chunk} for {q.dtype}")
         cs = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         rc = lib.gdnx_delta_chunk_fwd(
             _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w), _lib.ptr(log_g),
             _lib.ptr(state0), _lib.ptr(y), _lib.ptr(s_out), _lib.ptr(cs),
-            B, T, H, M, D, code, _lib.stream_of(q))
+            B, T, H, M, D, chunk, code, _lib.stream_of(q))
     _lib.check(rc, "gdnx_delta_chunk_fwd")
     return y, s_out, cs
+
+
+def delta_chunk_bwd(q, k, v, a_e, a_w, log_g, dy, chunk_states, chunk, dstate_out=None,
+                    want_dstate0=False):
+    """Backward; returns (dq, dk, dv, da_e, da_w, dlog_g, dstate0 or None)."""
+    lib = _lib.load()
+    B, T, H, M, D = _check_dense(q, k, v, a_e, a_w, log_g)
+    code = _lib.dtype_code(q.dtype)
+    dy = dy.to(q.dtype).contiguous()
+    _need(tuple(dy.shape) == (B, T, H, M, D), "dy must be [B,T,H,M,D]")
+    if dstate_out is not None:
+        dstate_out = dstate_out.float().contiguous()
+        _need(tuple(dstate_out.shape) == (B, H, M, D, D), "dstate_out must be [B,H,M,D,D]")
+    dev = q.device
+    ws = torch.empty_like(chunk_states)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    da_e, da_w, dlg = torch.empty_like(a_e), torch.empty_like(a_w), torch.empty_like(log_g)
+    ds0 = torch.empty(B, H, M, D, D, dtype=torch.float32, device=dev) if want_dstate0 else None
+    with torch.cuda.device(dev):
+        rc = lib.gdnx_delta_chunk_bwd(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w), _lib.ptr(log_g),
+            _lib.ptr(dy), _lib.ptr(dstate_out), _lib.ptr(chunk_states), _lib.ptr(ws),
+            _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(da_e), _lib.ptr(da_w), _lib.ptr(dlg),
+            _lib.ptr(ds0), B, T, H, M, D, chunk, code, _lib.stream_of(q))
+    _lib.check(rc, "gdnx_delta_chunk_bwd")
+    return dq, dk, dv, da_e, da_w, dlg, ds0
+
+
+class DeltaRuleFunction(torch.autograd.Function):
+    """y, S_T = lane-shared decoupled-erase delta rule (differentiable in
+    q, k, v, a_e, a_w, log_g and state0)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, a_e, a_w, log_g, state0=None):
+        train = any(ctx.needs_input_grad)
+        D = q.shape[-1]
+        chunk = chunk_size(D, q.dtype, train=train)
+        y, s_out, cs = delta_chunk_fwd(q, k, v, a_e, a_w, log_g, state0, return_state=True,
+                                       save_states=train, chunk=chunk)
+        if train:
+            ctx.save_for_backward(q, k, v, a_e, a_w, log_g, cs)
+            ctx.chunk = chunk
+            ctx.has_state0 = state0 is not None
+        return y, s_out
+
+    @staticmethod
+    def backward(ctx, dy, ds_out):
+        q, k, v, a_e, a_w, log_g, cs = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros(*a_e.shape, q.shape[-1], dtype=q.dtype, device=q.device)
+        dq, dk, dv, dae, daw, dlg, ds0 = delta_chunk_bwd(
+            q, k, v, a_e, a_w, log_g, dy, cs, ctx.chunk, dstate_out=ds_out,
+            want_dstate0=ctx.has_state0 and ctx.needs_input_grad[6])
+        return dq, dk, dv, dae, daw, dlg, ds0
+
+
+def delta_rule(q, k, v, a_e, a_w, log_g, state0=None):
+    """Differentiable lane-shared delta rule; returns (y, final_state)."""
+    args = [t.contiguous() for t in (q, k, v)] + [t.float().contiguous() for t in (a_e, a_w, log_g)]
+    if state0 is not None:
+        state0 = state0.float().contiguous()
+    return DeltaRuleFunction.apply(*args, state0)

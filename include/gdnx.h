@@ -39,11 +39,19 @@ int gdnx_abi_version(void);
 /* Message of the last error on the calling thread ("" if none). */
 const char* gdnx_last_error(void);
 
-/* Internal chunk length used for head_dim / dtype (tokens). */
+/* Default chunk length (tokens) of the forward for head_dim / dtype
+ * (64 for bf16, 32 for float32). */
 int gdnx_delta_chunk_size(int head_dim, int dtype);
 
-/* Bytes of the per-chunk state stash the forward writes for the backward. */
-long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim, int dtype);
+/* Chunk length to use when the forward stashes states for the backward
+ * (32 for bf16, 16 for float32). */
+int gdnx_delta_train_chunk_size(int head_dim, int dtype);
+
+/* Bytes of the per-chunk state stash (one d x d state per chain per chunk,
+ * in the compute dtype) for the given chunk (0 = default); -1 if invalid.
+ * The backward's workspace has the same size. */
+long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim, int chunk,
+                                        int dtype);
 
 /* Chunked decoupled-erase delta rule, forward.
  * Replaces the sequential token loop of
@@ -60,7 +68,24 @@ int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v,
                          const float* a_e, const float* a_w, const float* log_g,
                          const float* state0, void* y, float* state_out,
                          void* chunk_states, int B, int T, int H, int M,
-                         int head_dim, int dtype, void* stream);
+                         int head_dim, int chunk, int dtype, void* stream);
+
+/* Backward of gdnx_delta_chunk_fwd.  Replaces torch autograd through the
+ * reference's chunk graph (gdn3/gdn3_upgrade.py:467-521) and its hand
+ * backward of the KMD-2 TRSM (gdn3/kmd2_fast_scan.py:143-160).
+ * chunk_states: the forward's stash, made with the same chunk (0 = train
+ * default).  workspace: gdnx_delta_chunk_states_bytes bytes.  dstate_out:
+ * gradient w.r.t. the final state (or NULL).  Outputs: dq, dk, dv [B,T,H,D]
+ * (summed over the M lanes), da_e, da_w, dlog_g [B,T,H,M] float32, dstate0
+ * [B,H,M,D,D] float32 (or NULL).  dlog_g is zero where the forward clamped. */
+int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v,
+                         const float* a_e, const float* a_w, const float* log_g,
+                         const void* dy, const float* dstate_out,
+                         const void* chunk_states, void* workspace,
+                         void* dq, void* dk, void* dv,
+                         float* da_e, float* da_w, float* dlog_g, float* dstate0,
+                         int B, int T, int H, int M, int head_dim, int chunk,
+                         int dtype, void* stream);
 
 #ifdef __cplusplus
 }

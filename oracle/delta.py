@@ -38,6 +38,7 @@ import math
 import torch
 
 __all__ = [
+    "lane_delta",
     "stable_alpha",
     "delta_rule_sequential",
     "delta_rule_chunked",
@@ -202,3 +203,28 @@ def gdn3_dense_layer(q, k, v, beta, log_g, chunk=None, dtype=torch.float64):
     else:
         y, _ = delta_rule_chunked(qc, kc, ec, wc, lg, chunk=chunk)
     return y.reshape(B, H, M, T, dv).permute(0, 3, 1, 2, 4)
+
+
+def lane_delta(q, k, v, a_e, a_w, log_g, state0=None, chunk=None, dtype=torch.float64):
+    """Lane-shared delta rule with explicit per-lane coefficients (the HIP
+    op's interface): q, k, v [B,T,H,D], a_e, a_w, log_g [B,T,H,M], state0
+    [B,H,M,D,D] or None.  e = a_e k, w = a_w v, gamma = exp(min(log_g, 0)).
+    Returns (y [B,T,H,M,D], S_T [B,H,M,D,D]); differentiable."""
+    B, T, H, D = k.shape
+    M = a_e.shape[-1]
+    q, k, v, a_e, a_w, log_g = (x.to(dtype) for x in (q, k, v, a_e, a_w, log_g))
+
+    def chains(x):
+        x = x.unsqueeze(3).expand(B, T, H, M, D)
+        return x.permute(0, 2, 3, 1, 4).reshape(B * H * M, T, D)
+
+    qc, kc, vc = chains(q), chains(k), chains(v)
+    ae = a_e.permute(0, 2, 3, 1).reshape(B * H * M, T, 1)
+    aw = a_w.permute(0, 2, 3, 1).reshape(B * H * M, T, 1)
+    lg = log_g.clamp(max=0.0).permute(0, 2, 3, 1).reshape(B * H * M, T)
+    s0 = None if state0 is None else state0.to(dtype).reshape(B * H * M, D, D)
+    if chunk is None:
+        y, S = delta_rule_sequential(qc, kc, kc * ae, vc * aw, lg.exp(), s0)
+    else:
+        y, S = delta_rule_chunked(qc, kc, kc * ae, vc * aw, lg, chunk=chunk, state0=s0)
+    return y.reshape(B, H, M, T, D).permute(0, 3, 1, 2, 4), S.reshape(B, H, M, D, D)
