@@ -686,24 +686,30 @@ __global__ void __launch_bounds__(256) delta_bwd_grads_kernel(DeltaBwdArgs p) {
     }
 }
 
+// stages: bit 0 = reverse state scan, bit 1 = gradient kernel
 template <typename CT, int D, int C>
-static int launch_bwd(const DeltaBwdArgs& a, hipStream_t stream) {
+static int launch_bwd(const DeltaBwdArgs& a, int stages, hipStream_t stream) {
   const int NC = (a.T + C - 1) / C;
-  hipLaunchKernelGGL((delta_bwd_state_kernel<CT, D, C>), dim3(a.B * a.H * a.M), dim3(256), 0, stream, a);
-  int rc = check_launch("delta_bwd_state_kernel");
-  if (rc) return rc;
-  hipLaunchKernelGGL((delta_bwd_grads_kernel<CT, D, C>), dim3(a.B * a.H * NC), dim3(256), 0, stream, a);
-  return check_launch("delta_bwd_grads_kernel");
+  if (stages & 1) {
+    hipLaunchKernelGGL((delta_bwd_state_kernel<CT, D, C>), dim3(a.B * a.H * a.M), dim3(256), 0, stream, a);
+    const int rc = check_launch("delta_bwd_state_kernel");
+    if (rc) return rc;
+  }
+  if (stages & 2) {
+    hipLaunchKernelGGL((delta_bwd_grads_kernel<CT, D, C>), dim3(a.B * a.H * NC), dim3(256), 0, stream, a);
+    return check_launch("delta_bwd_grads_kernel");
+  }
+  return GDNX_OK;
 }
 
-int delta_bwd_dispatch(const DeltaBwdArgs& a, hipStream_t stream) {
+int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream) {
   if (a.dtype == GDNX_DTYPE_BF16) {
-    if (a.D == 128 && a.C == 32) return launch_bwd<bf16, 128, 32>(a, stream);
-    if (a.D == 64 && a.C == 32) return launch_bwd<bf16, 64, 32>(a, stream);
+    if (a.D == 128 && a.C == 32) return launch_bwd<bf16, 128, 32>(a, stages, stream);
+    if (a.D == 64 && a.C == 32) return launch_bwd<bf16, 64, 32>(a, stages, stream);
   } else {
-    if (a.D == 128 && a.C == 16) return launch_bwd<float, 128, 16>(a, stream);
-    if (a.D == 64 && a.C == 16) return launch_bwd<float, 64, 16>(a, stream);
-    if (a.D == 64 && a.C == 32) return launch_bwd<float, 64, 32>(a, stream);
+    if (a.D == 128 && a.C == 16) return launch_bwd<float, 128, 16>(a, stages, stream);
+    if (a.D == 64 && a.C == 16) return launch_bwd<float, 64, 16>(a, stages, stream);
+    if (a.D == 64 && a.C == 32) return launch_bwd<float, 64, 32>(a, stages, stream);
   }
   return set_error(GDNX_ERR_SHAPE, "backward: unsupported head dim %d / chunk %d for this dtype (use "
                    "gdnx_delta_train_chunk_size)", a.D, a.C);

@@ -99,18 +99,18 @@ extern "C" int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v,
   return delta_fwd_dispatch(a, (hipStream_t)stream);
 }
 
-extern "C" int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v, const float* a_e,
-                                    const float* a_w, const float* log_g, const void* dy,
-                                    const float* dstate_out, const void* chunk_states, void* workspace,
-                                    void* dq, void* dk, void* dv, float* da_e, float* da_w, float* dlog_g,
-                                    float* dstate0, int B, int T, int H, int M, int head_dim, int chunk,
-                                    int dtype, void* stream) {
+static int bwd_common(const void* q, const void* k, const void* v, const float* a_e, const float* a_w,
+                      const float* log_g, const void* dy, const float* dstate_out, const void* chunk_states,
+                      void* workspace, void* dq, void* dk, void* dv, float* da_e, float* da_w,
+                      float* dlog_g, float* dstate0, int B, int T, int H, int M, int head_dim, int chunk,
+                      int dtype, int stages, void* stream) {
   g_err[0] = 0;
   int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
   if (rc) return rc;
-  if (!a_e || !a_w || !log_g || !dy || !dq || !dk || !dv || !da_e || !da_w || !dlog_g)
-    return set_error(GDNX_ERR_ARG, "inputs and gradient outputs must be non-null");
-  if (!chunk_states || !workspace)
+  if (!a_e || !log_g || !dy) return set_error(GDNX_ERR_ARG, "a_e, log_g, dy must be non-null");
+  if ((stages & 2) && (!a_w || !dq || !dk || !dv || !da_e || !da_w || !dlog_g))
+    return set_error(GDNX_ERR_ARG, "a_w and the gradient outputs must be non-null");
+  if (!workspace || ((stages & 2) && !chunk_states))
     return set_error(GDNX_ERR_WORKSPACE, "chunk_states (from the forward) and workspace are required");
   if (((uintptr_t)chunk_states & 15u) || ((uintptr_t)workspace & 15u) || !aligned16(dy))
     return set_error(GDNX_ERR_ARG, "chunk_states, workspace and dy must be 16-byte aligned");
@@ -119,5 +119,34 @@ extern "C" int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v,
   if (T == 0) return GDNX_OK;
   DeltaBwdArgs a{q,  k,  v,  a_e,  a_w,  log_g, dy,      dstate_out, chunk_states, workspace, dq, dk,
                  dv, da_e, da_w, dlog_g, dstate0, B, T, H, M, head_dim, C, dtype};
-  return delta_bwd_dispatch(a, (hipStream_t)stream);
+  return delta_bwd_dispatch(a, stages, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v, const float* a_e,
+                                    const float* a_w, const float* log_g, const void* dy,
+                                    const float* dstate_out, const void* chunk_states, void* workspace,
+                                    void* dq, void* dk, void* dv, float* da_e, float* da_w, float* dlog_g,
+                                    float* dstate0, int B, int T, int H, int M, int head_dim, int chunk,
+                                    int dtype, void* stream) {
+  return bwd_common(q, k, v, a_e, a_w, log_g, dy, dstate_out, chunk_states, workspace, dq, dk, dv, da_e,
+                    da_w, dlog_g, dstate0, B, T, H, M, head_dim, chunk, dtype, 3, stream);
+}
+
+extern "C" int gdnx_delta_chunk_bwd_state(const void* q, const void* k, const float* a_e,
+                                          const float* log_g, const void* dy, const float* dstate_out,
+                                          void* workspace, float* dstate0, int B, int T, int H, int M,
+                                          int head_dim, int chunk, int dtype, void* stream) {
+  return bwd_common(q, k, k, a_e, nullptr, log_g, dy, dstate_out, nullptr, workspace, nullptr, nullptr,
+                    nullptr, nullptr, nullptr, nullptr, dstate0, B, T, H, M, head_dim, chunk, dtype, 1,
+                    stream);
+}
+
+extern "C" int gdnx_delta_chunk_bwd_grads(const void* q, const void* k, const void* v, const float* a_e,
+                                          const float* a_w, const float* log_g, const void* dy,
+                                          const void* chunk_states, const void* workspace, void* dq,
+                                          void* dk, void* dv, float* da_e, float* da_w, float* dlog_g,
+                                          int B, int T, int H, int M, int head_dim, int chunk, int dtype,
+                                          void* stream) {
+  return bwd_common(q, k, v, a_e, a_w, log_g, dy, nullptr, chunk_states, (void*)workspace, dq, dk, dv,
+                    da_e, da_w, dlog_g, nullptr, B, T, H, M, head_dim, chunk, dtype, 2, stream);
 }

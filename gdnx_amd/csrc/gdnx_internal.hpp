@@ -47,7 +47,7 @@ int set_error(int code, const char* fmt, ...);
 int check_launch(const char* what);
 
 int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);
-int delta_bwd_dispatch(const DeltaBwdArgs& a, hipStream_t stream);
+int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream);
 int delta_chunk_size(int D, int dtype);
 int delta_train_chunk_size(int D, int dtype);
 

@@ -126,3 +126,35 @@ def delta_rule(q, k, v, a_e, a_w, log_g, state0=None):
     if state0 is not None:
         state0 = state0.float().contiguous()
     return DeltaRuleFunction.apply(*args, state0)
+
+
+def delta_chunk_bwd_stages(q, k, v, a_e, a_w, log_g, dy, chunk_states, chunk, ws=None, out=None):
+    """The two backward stages as separate launches (for timing and
+    profiling).  Returns (workspace, (dq, dk, dv, da_e, da_w, dlog_g))."""
+    lib = _lib.load()
+    B, T, H, M, D = _check_dense(q, k, v, a_e, a_w, log_g)
+    code = _lib.dtype_code(q.dtype)
+    st = _lib.stream_of(q)
+    ws = torch.empty_like(chunk_states) if ws is None else ws
+    if out is None:
+        out = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
+               torch.empty_like(a_e), torch.empty_like(a_w), torch.empty_like(log_g))
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_delta_chunk_bwd_state(_lib.ptr(q), _lib.ptr(k), _lib.ptr(a_e), _lib.ptr(log_g),
+                                            _lib.ptr(dy), None, _lib.ptr(ws), None,
+                                            B, T, H, M, D, chunk, code, st)
+    _lib.check(rc, "gdnx_delta_chunk_bwd_state")
+    return ws, out
+
+
+def delta_chunk_bwd_grads(q, k, v, a_e, a_w, log_g, dy, chunk_states, ws, chunk, out):
+    lib = _lib.load()
+    B, T, H, M, D = _check_dense(q, k, v, a_e, a_w, log_g)
+    code = _lib.dtype_code(q.dtype)
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_delta_chunk_bwd_grads(
+            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w), _lib.ptr(log_g),
+            _lib.ptr(dy), _lib.ptr(chunk_states), _lib.ptr(ws), *(_lib.ptr(t) for t in out),
+            B, T, H, M, D, chunk, code, _lib.stream_of(q))
+    _lib.check(rc, "gdnx_delta_chunk_bwd_grads")
+    return out

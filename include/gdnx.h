@@ -87,6 +87,24 @@ int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v,
                          int B, int T, int H, int M, int head_dim, int chunk,
                          int dtype, void* stream);
 
+/* The two stages of gdnx_delta_chunk_bwd, callable separately (e.g. to
+ * time or overlap them).  Stage 1 runs the reverse state scan and fills
+ * workspace with dS at every chunk end (plus dstate0); stage 2 reads the
+ * forward's chunk_states and that workspace and writes every input gradient.
+ * Same arguments and layouts as gdnx_delta_chunk_bwd. */
+int gdnx_delta_chunk_bwd_state(const void* q, const void* k, const float* a_e,
+                               const float* log_g, const void* dy, const float* dstate_out,
+                               void* workspace, float* dstate0,
+                               int B, int T, int H, int M, int head_dim, int chunk,
+                               int dtype, void* stream);
+int gdnx_delta_chunk_bwd_grads(const void* q, const void* k, const void* v,
+                               const float* a_e, const float* a_w, const float* log_g,
+                               const void* dy, const void* chunk_states, const void* workspace,
+                               void* dq, void* dk, void* dv,
+                               float* da_e, float* da_w, float* dlog_g,
+                               int B, int T, int H, int M, int head_dim, int chunk,
+                               int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
