@@ -15,7 +15,7 @@
 //
 // Two kernels:
 //   delta_bwd_state_kernel  one workgroup per chain, chunks in reverse order,
-//     carries dS in registers (value columns split over the 4 waves, like the
+//     carries dS in registers (value columns split over the waves, like the
 //     forward's S) and stashes dS_C of every chunk.  Needs no S0.
 //   delta_bwd_grads_kernel  one workgroup per (batch, head, chunk), looping
 //     over the M lanes that share q/k/v: recomputes T, R, dR, dB from the two
@@ -44,16 +44,17 @@ struct alignas(16) BwdStateSmem {
   CT aqt[C * Dm::LDC];   // Aq^T [j][i]
   CT tt[C * Dm::LDC];    // T^T  [i][j] = T[j][i]
   float L[C * Dm::LDF];
-  float T[C * Dm::LDF];
+  float LT[C * Dm::LDT];
+  float Td[C * Dm::LDT];
   float G[C], gam[C], dec[C], ae[C];
 };
 
 template <typename CT, int D, int C>
-__global__ void __launch_bounds__(256) delta_bwd_state_kernel(DeltaBwdArgs p) {
+__global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_bwd_state_kernel(DeltaBwdArgs p) {
   typedef Dims<CT, D, C> Dm;
   typedef typename Dm::Frag Frag;
   constexpr int KS = Dm::KS, TPS = Dm::TPS, NDT = Dm::NDT, NCT = Dm::NCT, VS = Dm::VS, NVT = Dm::NVT;
-  constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF;
+  constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF, NT = Dm::NT;
   __shared__ BwdStateSmem<CT, D, C> sm;
 
   const int tid = threadIdx.x;
@@ -73,8 +74,10 @@ __global__ void __launch_bounds__(256) delta_bwd_state_kernel(DeltaBwdArgs p) {
   const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + m;
   const ChunkScalars cs{sm.G, sm.gam, sm.dec, sm.ae, nullptr, nullptr};
 
-  for (int i = tid; i < C * LDF; i += 256) sm.T[i] = 0.f;
-  for (int i = tid; i < C * LDC; i += 256) sm.aqt[i] = from_f<CT>(0.f);
+  for (int i = tid; i < C * LDC; i += NT) {
+    sm.aqt[i] = from_f<CT>(0.f);
+    sm.tt[i] = from_f<CT>(0.f);
+  }
 
   f32x4 dS[NDT][NVT];
 #pragma unroll
@@ -89,53 +92,42 @@ __global__ void __launch_bounds__(256) delta_bwd_state_kernel(DeltaBwdArgs p) {
       }
     }
 
+  const CT* qg = (const CT*)p.q + qoff;
+  const CT* kg = (const CT*)p.k + qoff;
+  const CT* yg = (const CT*)p.dy + yoff;
+  TileRegs rq, rk, ry;
+  ScalarRegs rsc;
+  tile_fetch<CT, D, C>(rq, qg, rs, (NC - 1) * C, p.T, tid);
+  tile_fetch<CT, D, C>(rk, kg, rs, (NC - 1) * C, p.T, tid);
+  tile_fetch<CT, D, C>(ry, yg, rsy, (NC - 1) * C, p.T, tid);
+  if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, nullptr, p.g + soff, st, (NC - 1) * C, p.T, lane);
+
   for (int c = NC - 1; c >= 0; --c) {
     const int t0 = c * C;
     __syncthreads();
-    stage_tile<CT, D, C>((const CT*)p.q + qoff, rs, t0, p.T, sm.q, sm.qt, tid);
-    stage_tile<CT, D, C>((const CT*)p.k + qoff, rs, t0, p.T, sm.k, sm.kt, tid);
-    stage_tile<CT, D, C>((const CT*)p.dy + yoff, rsy, t0, p.T, nullptr, sm.dyt, tid);
-    if (wave == 0) prep_scalars<C>(cs, p.ae + soff, nullptr, p.g + soff, st, t0, p.T, lane);
+    tile_commit<CT, D, C>(rq, sm.q, sm.qt, tid);
+    tile_commit<CT, D, C>(rk, sm.k, sm.kt, tid);
+    tile_commit<CT, D, C>(ry, nullptr, sm.dyt, tid);
+    if (wave == 0) scal_commit<C>(cs, rsc, lane);
     __syncthreads();
-    for (int idx = tid; idx < D * C; idx += 256) {
+    if (c > 0) {
+      tile_fetch<CT, D, C>(rq, qg, rs, t0 - C, p.T, tid);
+      tile_fetch<CT, D, C>(rk, kg, rs, t0 - C, p.T, tid);
+      tile_fetch<CT, D, C>(ry, yg, rsy, t0 - C, p.T, tid);
+      if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, nullptr, p.g + soff, st, t0 - C, p.T, lane);
+    }
+    for (int idx = tid; idx < D * C; idx += NT) {
       const int d = idx / C, i = idx % C;
       sm.qt[d * LDC + i] = from_f<CT>(to_f(sm.qt[d * LDC + i]) * sm.gam[i]);
     }
-    {
-      constexpr int NP = NCT * (NCT + 1) / 2;
-      for (int task = wave; task < 2 * NP; task += 4) {
-        int it, jt;
-        tri_pair(task >> 1, it, jt);
-        if ((task & 1) == 0) {
-          const f32x4 acc = tile_nt<CT, D>(&sm.k[(it * 16 + n16) * LDD], &sm.k[(jt * 16 + n16) * LDD], g4);
-          const int j = jt * 16 + n16;
-          const float Gj = sm.G[j];
+    chunk_grams<CT, D, C>(sm.k, sm.q, sm.L, sm.LT, sm.G, sm.ae, wave, lane, [&](int i, int j0, const float* v) {
 #pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int i = it * 16 + 4 * g4 + ii;
-            sm.L[i * LDF + j] = (j < i) ? __expf(sm.G[i] - Gj) * sm.ae[i] * acc[ii] : 0.f;
-          }
-        } else {
-          // acc[ii] = q_i . k_j, i = it*16+4g+ii, j = jt*16+n  ->  Aq^T[j][i..i+3]
-          const f32x4 acc = tile_nt<CT, D>(&sm.q[(it * 16 + n16) * LDD], &sm.k[(jt * 16 + n16) * LDD], g4);
-          const int j = jt * 16 + n16;
-          const float Gj = sm.G[j];
-          float vals[4];
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int i = it * 16 + 4 * g4 + ii;
-            vals[ii] = (j <= i) ? __expf(sm.G[i] - Gj) * acc[ii] : 0.f;
-          }
-          st4(&sm.aqt[j * LDC + it * 16 + 4 * g4], vals[0], vals[1], vals[2], vals[3]);
-        }
-      }
-    }
+      for (int e = 0; e < 4; ++e) sm.aqt[(j0 + e) * LDC + i] = from_f<CT>(v[e]);
+    });
     __syncthreads();
-    invert_unit_lower<C>(sm.L, sm.T, wave, lane);
-    for (int idx = tid; idx < C * C; idx += 256) {
-      const int i = idx / C, j = idx % C;
-      sm.tt[i * LDC + j] = from_f<CT>(sm.T[j * LDF + i]);
-    }
+    invert_unit_lower<C>(
+        sm.L, sm.LT, sm.Td, wave, lane, [&](int) { return 0; },
+        [&](int i, int j, float t, int) { sm.tt[j * LDC + i] = from_f<CT>(t); });
     __syncthreads();
 
     // stash dS_C of this chunk
@@ -146,11 +138,11 @@ __global__ void __launch_bounds__(256) delta_bwd_state_kernel(DeltaBwdArgs p) {
       for (int vt = 0; vt < NVT; ++vt)
         dSf[kb][vt] = acc_frag((CT*)nullptr, dS[kb * TPS][vt], dS[kb * TPS + TPS - 1][vt]);
     {
-      Frag* cst = (Frag*)p.ds_stash + ((size_t)chain * NC + c) * (256 * Dm::STASH_FRAGS);
+      Frag* cst = (Frag*)p.ds_stash + ((size_t)chain * NC + c) * (NT * Dm::STASH_FRAGS);
 #pragma unroll
       for (int kb = 0; kb < NDT / TPS; ++kb)
 #pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) cst[(kb * NVT + vt) * 256 + tid] = dSf[kb][vt];
+        for (int vt = 0; vt < NVT; ++vt) cst[(kb * NVT + vt) * NT + tid] = dSf[kb][vt];
     }
     // dR = diag(dec) K dS + Aq^T dY
     f32x4 dR[NCT][NVT];
@@ -259,14 +251,14 @@ struct alignas(16) BwdGradSmem {
   float dQK[C * LDF];  // sum over lanes of dL/d(q_i.k_j)
   float dKK[C * LDF];  // sum over lanes of dL/d(k_i.k_j), j < i
   float G[C], gam[C], dec[C], ae[C], aw[C], graw[C], tmp[C];
-  float red[4][4][C];  // [quantity][wave][row] partial sums
-  float scal[4];
+  float red[4][Dm::NW][C];  // [quantity][wave][row] partial sums
+  float scal[Dm::NW];
   union alignas(16) U {
     struct alignas(16) {
       CT dyt[D * LDC];
       CT ta[C * LDC], tb[C * LDC], tt[C * LDC], aqt[C * LDC];
       CT wm[C * LDD];
-      float L[C * LDF], T[C * LDF];
+      float L[C * LDF], LT[C * Dm::LDT], Td[C * Dm::LDT];
     } p1;
     struct alignas(16) {
       CT X[D * LDD];   // S0, then dS  ([d][v], value-contiguous)
@@ -290,12 +282,12 @@ __device__ __forceinline__ float sum16(float x) {
 }
 
 template <typename CT, int D, int C>
-__global__ void __launch_bounds__(256) delta_bwd_grads_kernel(DeltaBwdArgs p) {
+__global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_bwd_grads_kernel(DeltaBwdArgs p) {
   typedef Dims<CT, D, C> Dm;
   typedef typename Dm::Frag Frag;
   constexpr int KS = Dm::KS, TPS = Dm::TPS, NDT = Dm::NDT, NCT = Dm::NCT, VS = Dm::VS, NVT = Dm::NVT;
-  constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF;
-  constexpr int DPW = NDT / 4;  // d tiles per wave in the d-partitioned phase
+  constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF, NT = Dm::NT, NW = Dm::NW;
+  constexpr int DPW = Dm::DPW;  // d tiles per wave in the d-partitioned phase
   constexpr int FL = FragLen<CT>::value;
   __shared__ BwdGradSmem<CT, D, C> sm;
 
@@ -317,7 +309,7 @@ __global__ void __launch_bounds__(256) delta_bwd_grads_kernel(DeltaBwdArgs p) {
   stage_tile<CT, D, C>((const CT*)p.q + qoff, rs, t0, p.T, sm.q, sm.qt, tid);
   stage_tile<CT, D, C>((const CT*)p.k + qoff, rs, t0, p.T, sm.k, sm.kt, tid);
   stage_tile<CT, D, C>((const CT*)p.v + qoff, rs, t0, p.T, nullptr, sm.vt, tid);
-  for (int i = tid; i < C * LDF; i += 256) {
+  for (int i = tid; i < C * LDF; i += NT) {
     sm.dQK[i] = 0.f;
     sm.dKK[i] = 0.f;
   }
@@ -332,7 +324,7 @@ __global__ void __launch_bounds__(256) delta_bwd_grads_kernel(DeltaBwdArgs p) {
   __syncthreads();
   {  // raw grams (shared by the lanes)
     constexpr int NP = NCT * (NCT + 1) / 2;
-    for (int task = wave; task < 2 * NP; task += 4) {
+    for (int task = wave; task < 2 * NP; task += NW) {
       int it, jt;
       tri_pair(task >> 1, it, jt);
       const CT* arow = ((task & 1) == 0) ? &sm.k[(it * 16 + n16) * LDD] : &sm.q[(it * 16 + n16) * LDD];
@@ -352,22 +344,26 @@ __global__ void __launch_bounds__(256) delta_bwd_grads_kernel(DeltaBwdArgs p) {
     stage_tile<CT, D, C>((const CT*)p.dy + yoff, rsy, t0, p.T, sm.dy, sm.u.p1.dyt, tid);
     if (wave == 0) prep_scalars<C>(cs, p.ae + soff, p.aw + soff, p.g + soff, st, t0, p.T, lane);
     __syncthreads();
-    for (int idx = tid; idx < C * C; idx += 256) {
+    for (int idx = tid; idx < C * C; idx += NT) {
       const int i = idx / C, j = idx % C;
       const float Dij = (j <= i) ? __expf(sm.G[i] - sm.G[j]) : 0.f;
-      sm.u.p1.L[i * LDF + j] = (j < i) ? Dij * sm.ae[i] * sm.KK[i * LDF + j] : 0.f;
+      const float Lij = (j < i) ? Dij * sm.ae[i] * sm.KK[i * LDF + j] : 0.f;
+      sm.u.p1.L[i * LDF + j] = Lij;
+      if ((i >> 4) == (j >> 4)) sm.u.p1.LT[j * Dm::LDT + (i & 15)] = Lij;
       sm.u.p1.aqt[j * LDC + i] = from_f<CT>((j <= i) ? Dij * sm.QK[i * LDF + j] : 0.f);
-      sm.u.p1.T[i * LDF + j] = 0.f;
+      sm.u.p1.ta[i * LDC + j] = from_f<CT>(0.f);
+      sm.u.p1.tb[i * LDC + j] = from_f<CT>(0.f);
+      sm.u.p1.tt[i * LDC + j] = from_f<CT>(0.f);
     }
     __syncthreads();
-    invert_unit_lower<C>(sm.u.p1.L, sm.u.p1.T, wave, lane);
-    for (int idx = tid; idx < C * C; idx += 256) {
-      const int i = idx / C, j = idx % C;
-      const float t = sm.u.p1.T[i * LDF + j];
-      sm.u.p1.ta[i * LDC + j] = from_f<CT>(t * sm.aw[j]);
-      sm.u.p1.tb[i * LDC + j] = from_f<CT>(t * sm.ae[j] * sm.gam[j]);
-      sm.u.p1.tt[i * LDC + j] = from_f<CT>(sm.u.p1.T[j * LDF + i]);
-    }
+    invert_unit_lower<C>(
+        sm.u.p1.L, sm.u.p1.LT, sm.u.p1.Td, wave, lane,
+        [&](int j) { return make_float2(sm.aw[j], sm.ae[j] * sm.gam[j]); },
+        [&](int i, int j, float t, float2 f) {
+          sm.u.p1.ta[i * LDC + j] = from_f<CT>(t * f.x);
+          sm.u.p1.tb[i * LDC + j] = from_f<CT>(t * f.y);
+          sm.u.p1.tt[j * LDC + i] = from_f<CT>(t);
+        });
     __syncthreads();
 #pragma unroll
     for (int dd = 0; dd < DPW; ++dd) {
@@ -389,14 +385,14 @@ __global__ void __launch_bounds__(256) delta_bwd_grads_kernel(DeltaBwdArgs p) {
     // ---- phase 1 (value columns split over waves) ----
     Frag Sf[NDT / TPS][NVT], dSf[NDT / TPS][NVT];
     {
-      const Frag* s = (const Frag*)p.s_stash + (chain * NC + c) * (256 * Dm::STASH_FRAGS);
-      const Frag* ds = (const Frag*)p.ds_stash + (chain * NC + c) * (256 * Dm::STASH_FRAGS);
+      const Frag* s = (const Frag*)p.s_stash + (chain * NC + c) * (NT * Dm::STASH_FRAGS);
+      const Frag* ds = (const Frag*)p.ds_stash + (chain * NC + c) * (NT * Dm::STASH_FRAGS);
 #pragma unroll
       for (int kb = 0; kb < NDT / TPS; ++kb)
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) {
-          Sf[kb][vt] = s[(kb * NVT + vt) * 256 + tid];
-          dSf[kb][vt] = ds[(kb * NVT + vt) * 256 + tid];
+          Sf[kb][vt] = s[(kb * NVT + vt) * NT + tid];
+          dSf[kb][vt] = ds[(kb * NVT + vt) * NT + tid];
         }
     }
 #pragma unroll
@@ -533,7 +529,7 @@ __global__ void __launch_bounds__(256) delta_bwd_grads_kernel(DeltaBwdArgs p) {
     // dAq = dY R^T (j <= i) and dL = -dB R^T (j < i), lower tiles
     {
       constexpr int NP = NCT * (NCT + 1) / 2;
-      for (int pidx = wave; pidx < NP; pidx += 4) {
+      for (int pidx = wave; pidx < NP; pidx += NW) {
         int it, jt;
         tri_pair(pidx, it, jt);
         const f32x4 aA = tile_nt<CT, D>(&sm.dy[(it * 16 + n16) * LDD], &sm.u.p2.R[(jt * 16 + n16) * LDD], g4);
@@ -605,7 +601,7 @@ __global__ void __launch_bounds__(256) delta_bwd_grads_kernel(DeltaBwdArgs p) {
       const int i = tid;
       float r1 = 0.f, r2 = 0.f, r3 = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
+      for (int w = 0; w < NW; ++w) {
         dawi += sm.red[0][w][i];
         r1 += sm.red[1][w][i];
         r2 += sm.red[2][w][i];
@@ -621,7 +617,8 @@ __global__ void __launch_bounds__(256) delta_bwd_grads_kernel(DeltaBwdArgs p) {
     __syncthreads();
     if (wave == 0) {
       if (lane == C - 1) {
-        float s = sm.scal[0] + sm.scal[1] + sm.scal[2] + sm.scal[3];
+        float s = 0.f;
+        for (int w = 0; w < NW; ++w) s += sm.scal[w];
         s *= sm.gam[C - 1];
         for (int j = 0; j < C; ++j) s += sm.tmp[j];
         dGi += s;
@@ -646,7 +643,7 @@ __global__ void __launch_bounds__(256) delta_bwd_grads_kernel(DeltaBwdArgs p) {
   }
 
   // ---- gram gradient products, shared over lanes ----
-  for (int idx = tid; idx < C * C; idx += 256) {
+  for (int idx = tid; idx < C * C; idx += NT) {
     const int i = idx / C, j = idx % C;
     sm.u.p3.A1[i * LDC + j] = from_f<CT>((j <= i) ? sm.dQK[i * LDF + j] : 0.f);
     sm.u.p3.A2[i * LDC + j] = from_f<CT>((i <= j) ? sm.dQK[j * LDF + i] : 0.f);
@@ -691,12 +688,12 @@ template <typename CT, int D, int C>
 static int launch_bwd(const DeltaBwdArgs& a, int stages, hipStream_t stream) {
   const int NC = (a.T + C - 1) / C;
   if (stages & 1) {
-    hipLaunchKernelGGL((delta_bwd_state_kernel<CT, D, C>), dim3(a.B * a.H * a.M), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((delta_bwd_state_kernel<CT, D, C>), dim3(a.B * a.H * a.M), dim3(Dims<CT, D, C>::NT), 0, stream, a);
     const int rc = check_launch("delta_bwd_state_kernel");
     if (rc) return rc;
   }
   if (stages & 2) {
-    hipLaunchKernelGGL((delta_bwd_grads_kernel<CT, D, C>), dim3(a.B * a.H * NC), dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((delta_bwd_grads_kernel<CT, D, C>), dim3(a.B * a.H * NC), dim3(Dims<CT, D, C>::NT), 0, stream, a);
     return check_launch("delta_bwd_grads_kernel");
   }
   return GDNX_OK;

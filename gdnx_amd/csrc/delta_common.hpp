@@ -1,6 +1,8 @@
 // Device building blocks shared by the chunked delta-rule kernels
-// (forward, reverse state scan, gradient kernel).  All assume 256 threads
-// (4 waves) per workgroup.
+// (forward, reverse state scan, gradient kernel).  Workgroups have NW = 4
+// waves (one per SIMD): with the whole 512-entry register file per wave the
+// fp32 state, the MFMA accumulators and the next chunk's prefetched tiles all
+// stay in registers (8 waves halve the budget and spill).
 #pragma once
 #include "gdnx_common.hpp"
 #include "gdnx_internal.hpp"
@@ -12,17 +14,21 @@ struct Dims {
   typedef typename FragT<CT>::type Frag;
   static constexpr int KS = FragT<CT>::KSTEP;  // k per MFMA step
   static constexpr int TPS = FragT<CT>::TPS;   // accumulator tiles per k-step
+  static constexpr int NW = 4;                 // waves per workgroup
+  static constexpr int NT = 64 * NW;           // threads per workgroup
   static constexpr int NDT = D / 16;           // 16-row tiles over a feature dim
   static constexpr int NCT = C / 16;           // 16-row tiles over the chunk
-  static constexpr int VS = D / 4;             // feature columns owned by a wave
+  static constexpr int VS = D / NW;            // feature columns owned by a wave
+  static constexpr int DPW = NDT / NW;         // 16-row feature tiles owned by a wave
   static constexpr int NVT = VS / 16;          // 16-col tiles owned by a wave
   static constexpr int LDD = D + 4;            // LDS row length, [*, D] tiles
   static constexpr int LDC = C + 4;            // LDS row length, [*, C] tiles
-  static constexpr int LDF = C + 1;            // fp32 [C, C] scratch rows
+  static constexpr int LDF = C + 4;            // fp32 [C, C] scratch rows (16-byte aligned)
+  static constexpr int LDT = 20;               // fp32 diagonal-block scratch [C][LDT]
   // fragments of one chunk-state stash per workgroup (tile-native layout)
   static constexpr int STASH_FRAGS = (NDT / TPS) * NVT;
   static_assert(C % KS == 0, "chunk must be a multiple of the MFMA k-step");
-  static_assert(NVT >= 1 && NDT % 4 == 0, "head dim must be 64 or 128");
+  static_assert(NVT >= 1 && DPW >= 1 && NDT % NW == 0, "head dim must be 64 or 128");
 };
 
 // Stage C rows (tokens t0..t0+C-1, zero beyond T) of a [.., T, .., D] tensor
@@ -35,7 +41,7 @@ __device__ __forceinline__ void stage_tile(const CT* __restrict__ src, size_t rs
   constexpr int VEC = 16 / sizeof(CT);
   constexpr int DG = D / VEC;
   constexpr int LDD = D + 4, LDC = C + 4;
-  for (int u = tid; u < (C / 4) * DG; u += 256) {
+  for (int u = tid; u < (C / 4) * DG; u += Dims<CT, D, C>::NT) {
     const int tg = u / DG, dg = u % DG;
     CT x[4][VEC];
 #pragma unroll
@@ -72,6 +78,42 @@ struct ChunkScalars {
   float *G, *gam, *dec, *ae, *aw, *graw;
 };
 
+// Prefetched per-token scalars of one lane (token t0 + lane).
+struct ScalarRegs {
+  float ae, aw, g;
+};
+
+template <int C>
+__device__ __forceinline__ void scal_fetch(ScalarRegs& r, const float* ae, const float* aw, const float* g,
+                                           size_t st, int t0, int T, int lane) {
+  r.ae = r.aw = r.g = 0.f;
+  const int t = t0 + lane;
+  if (lane < C && t < T) {
+    if (ae) r.ae = ae[(size_t)t * st];
+    if (aw) r.aw = aw[(size_t)t * st];
+    r.g = g[(size_t)t * st];
+  }
+}
+
+template <int C>
+__device__ __forceinline__ void scal_commit(const ChunkScalars& s, const ScalarRegs& r, int lane) {
+  float G = fmaxf(fminf(r.g, 0.f), kLogFloor);
+#pragma unroll
+  for (int off = 1; off < 64; off <<= 1) {
+    const float o = __shfl_up(G, off, 64);
+    if (lane >= off) G += o;
+  }
+  const float Glast = __shfl(G, C - 1, 64);
+  if (lane < C) {
+    s.G[lane] = G;
+    s.gam[lane] = __expf(G);
+    s.dec[lane] = __expf(Glast - G);
+    if (s.ae) s.ae[lane] = r.ae;
+    if (s.aw) s.aw[lane] = r.aw;
+    if (s.graw) s.graw[lane] = r.g;
+  }
+}
+
 template <int C>
 __device__ __forceinline__ void prep_scalars(const ChunkScalars& s, const float* ae, const float* aw,
                                              const float* g, size_t st, int t0, int T, int lane) {
@@ -100,55 +142,70 @@ __device__ __forceinline__ void prep_scalars(const ChunkScalars& s, const float*
   }
 }
 
-// T = (I + L)^-1 for a unit-lower C x C matrix (L strictly lower, fp32,
-// rows LDF apart; only the lower blocks are read).  T's strictly-upper part
-// must already be zero.  16x16 diagonal blocks by substitution (wave 0, one
-// lane per column), then T_ij = -T_ii sum_{k=j}^{i-1} L_ik T_kj by distance
-// on fp32 MFMA.  Contains barriers: every thread must call it.
-template <int C>
-__device__ __forceinline__ void invert_unit_lower(const float* sL, float* sT, int wave, int lane) {
-  constexpr int NCT = C / 16, LDF = C + 1;
-  const int g4 = lane >> 4, n16 = lane & 15;
-  if (wave == 0) {
-    const int bb = lane >> 4, col = lane & 15;
-    if (bb < NCT) {
-      float x[16];
+// Registers holding one thread's share of a chunk tile ([C][D] rows, 4
+// consecutive tokens x 16 bytes), used to prefetch the next chunk while the
+// current one computes.  Every (C, D, dtype) used here maps to at most one
+// such unit per thread.
+struct TileRegs {
+  uint4 x[4];
+};
+
+template <typename CT, int D, int C>
+__device__ __forceinline__ bool tile_unit(int tid, int& tg, int& dg) {
+  constexpr int VEC = 16 / sizeof(CT);
+  constexpr int DG = D / VEC;
+  static_assert((C / 4) * DG <= Dims<CT, D, C>::NT, "one staging unit per thread");
+  tg = tid / DG;
+  dg = tid % DG;
+  return tid < (C / 4) * DG;
+}
+
+template <typename CT, int D, int C>
+__device__ __forceinline__ void tile_fetch(TileRegs& r, const CT* __restrict__ src, size_t rs, int t0,
+                                           int T, int tid) {
+  constexpr int VEC = 16 / sizeof(CT);
+  int tg, dg;
+  if (!tile_unit<CT, D, C>(tid, tg, dg)) return;
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        float s = (i == col) ? 1.f : 0.f;
-        const float* Lrow = &sL[(16 * bb + i) * LDF + 16 * bb];
+  for (int q = 0; q < 4; ++q) {
+    const int t = t0 + 4 * tg + q;
+    r.x[q] = (t < T) ? *(const uint4*)(src + (size_t)t * rs + dg * VEC) : make_uint4(0, 0, 0, 0);
+  }
+}
+
+__device__ __forceinline__ unsigned word_of(const uint4& v, int w) {
+  return w == 0 ? v.x : (w == 1 ? v.y : (w == 2 ? v.z : v.w));
+}
+
+template <typename CT, int D, int C>
+__device__ __forceinline__ void tile_commit(const TileRegs& r, CT* nat, CT* tr, int tid) {
+  constexpr int VEC = 16 / sizeof(CT);
+  constexpr int LDD = D + 4, LDC = C + 4;
+  int tg, dg;
+  if (!tile_unit<CT, D, C>(tid, tg, dg)) return;
+  if (nat) {
 #pragma unroll
-        for (int j = 0; j < i; ++j) s -= Lrow[j] * x[j];
-        x[i] = s;
-      }
-#pragma unroll
-      for (int i = 0; i < 16; ++i) sT[(16 * bb + i) * LDF + 16 * bb + col] = x[i];
+    for (int q = 0; q < 4; ++q) {
+      uint2* d = (uint2*)(nat + (4 * tg + q) * LDD + dg * VEC);
+      d[0] = make_uint2(r.x[q].x, r.x[q].y);
+      d[1] = make_uint2(r.x[q].z, r.x[q].w);
     }
   }
-  __syncthreads();
+  if (tr) {
+    if constexpr (sizeof(CT) == 2) {
 #pragma unroll
-  for (int dist = 1; dist < NCT; ++dist) {
-    if (wave < NCT - dist) {
-      const int jb = wave, ib = wave + dist;
-      f32x4 X = zero4();
-      for (int kb = jb; kb < ib; ++kb) {
-        f32x4 a, bq;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          a[s] = sL[(16 * ib + n16) * LDF + 16 * kb + 4 * g4 + s];
-          bq[s] = sT[(16 * kb + 4 * g4 + s) * LDF + 16 * jb + n16];
-        }
-        mma(X, a, bq);
+      for (int e = 0; e < 8; ++e) {
+        const int w = e >> 1, sh = (e & 1) * 16;
+        const unsigned a0 = (word_of(r.x[0], w) >> sh) & 0xffffu, a1 = (word_of(r.x[1], w) >> sh) & 0xffffu;
+        const unsigned a2 = (word_of(r.x[2], w) >> sh) & 0xffffu, a3 = (word_of(r.x[3], w) >> sh) & 0xffffu;
+        *(uint2*)&tr[(dg * VEC + e) * LDC + 4 * tg] = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
       }
-      f32x4 a;
+    } else {
 #pragma unroll
-      for (int s = 0; s < 4; ++s) a[s] = sT[(16 * ib + n16) * LDF + 16 * ib + 4 * g4 + s];
-      f32x4 Y = zero4();
-      mma(Y, a, X);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) sT[(16 * ib + 4 * g4 + s) * LDF + 16 * jb + n16] = -Y[s];
+      for (int e = 0; e < 4; ++e)
+        *(uint4*)&tr[(dg * VEC + e) * LDC + 4 * tg] =
+            make_uint4(word_of(r.x[0], e), word_of(r.x[1], e), word_of(r.x[2], e), word_of(r.x[3], e));
     }
-    __syncthreads();
   }
 }
 
@@ -162,6 +219,167 @@ __device__ __forceinline__ void tri_pair(int pidx, int& it, int& jt) {
   it = row;
   jt = pidx - start;
 }
+
+// Grams of a chunk.  L-type tiles (K K^T, strictly lower, scaled by
+// exp(G_i - G_j) a_e,i) go to sL (rows i, fp32) and, for diagonal blocks, to
+// sLT transposed (compact: row j holds L[16b+.][j] at [j*20 + i-16b]);
+// Aq-type tiles (Q K^T, lower incl. diagonal, scaled by exp(G_i - G_j)) are
+// handed to emit_aq(i, j0, v[4]) as 4 consecutive j.  The lower tiles of both
+// grams are dealt round-robin to the NW waves; each task loads all its
+// operand fragments before its MFMAs.
+template <typename CT, int D, int C, typename EmitAq>
+__device__ __forceinline__ void chunk_grams(const CT* sk, const CT* sq, float* sL, float* sLT,
+                                            const float* sG, const float* sae, int wave, int lane,
+                                            EmitAq emit_aq) {
+  typedef typename FragT<CT>::type Frag;
+  constexpr int KS = FragT<CT>::KSTEP, NCT = C / 16, LDD = D + 4, LDF = C + 4;
+  constexpr int NW = Dims<CT, D, C>::NW, NP = NCT * (NCT + 1) / 2;
+  const int g4 = lane >> 4, n16 = lane & 15;
+  for (int task = wave; task < 2 * NP; task += NW) {
+    const int type = task & 1;
+    int it, jt;
+    tri_pair(task >> 1, it, jt);
+    const CT* arow = &sk[((type == 0 ? it : jt) * 16 + n16) * LDD];
+    const CT* brow = (type == 0) ? &sk[(jt * 16 + n16) * LDD] : &sq[(it * 16 + n16) * LDD];
+    Frag a[D / KS], b[D / KS];
+#pragma unroll
+    for (int kb = 0; kb < D / KS; ++kb) {
+      a[kb] = ld_frag(arow + kb * KS, g4);
+      b[kb] = ld_frag(brow + kb * KS, g4);
+    }
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int kb = 0; kb < D / KS; ++kb) mma(acc, a[kb], b[kb]);
+    if (type == 0) {
+      // acc[ii] = k_i . k_j, i = it*16+4g+ii, j = jt*16+n
+      const f32x4 G4 = *(const f32x4*)&sG[it * 16 + 4 * g4];
+      const f32x4 ae4 = *(const f32x4*)&sae[it * 16 + 4 * g4];
+      const int j = jt * 16 + n16;
+      const float Gj = sG[j];
+      f32x4 val;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int i = it * 16 + 4 * g4 + ii;
+        val[ii] = (j < i) ? __expf(G4[ii] - Gj) * ae4[ii] * acc[ii] : 0.f;
+      }
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) sL[(it * 16 + 4 * g4 + ii) * LDF + j] = val[ii];
+      if (jt == it) *(f32x4*)&sLT[j * 20 + 4 * g4] = val;
+    } else {
+      // acc[ii] = q_i . k_j, i = it*16+n, j = jt*16+4g+ii
+      const int i = it * 16 + n16;
+      const float Gi = sG[i];
+      const f32x4 Gj4 = *(const f32x4*)&sG[jt * 16 + 4 * g4];
+      float v[4];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int j = jt * 16 + 4 * g4 + ii;
+        v[ii] = (j <= i) ? __expf(Gi - Gj4[ii]) * acc[ii] : 0.f;
+      }
+      emit_aq(i, jt * 16 + 4 * g4, v);
+    }
+  }
+}
+
+#ifndef GDNX_INV_MARK
+#define GDNX_INV_MARK(k)
+#endif
+template <int C, typename ColPrep, typename Emit>
+__device__ __forceinline__ void invert_unit_lower(const float* sL, const float* sLT, float* sTd, int wave,
+                                                  int lane, ColPrep colprep, Emit emit) {
+  constexpr int NCT = C / 16, LDF = C + 4;
+  const int g4 = lane >> 4, n16 = lane & 15;
+  if (wave < NCT && lane < 16) {
+    const int b = wave, col = lane;
+    float x[16];
+#pragma unroll
+    for (int i = 0; i < 16; ++i) x[i] = (i == col) ? 1.f : 0.f;
+    // right-looking: after step j, x_j is final; row j of the transposed
+    // block holds L[16b+i][16b+j] for all i.  Rows are loaded PF steps ahead
+    // so each step's LDS latency overlaps earlier steps' FMAs.
+    constexpr int PF = 4;
+    f32x4 win[PF][4];
+#pragma unroll
+    for (int r = 0; r < PF; ++r)
+#pragma unroll
+      for (int q = 0; q < 4; ++q) win[r][q] = *(const f32x4*)&sLT[(16 * b + r) * 20 + 4 * q];
+#pragma unroll
+    for (int j = 0; j < 15; ++j) {
+      f32x4 c4[4];
+#pragma unroll
+      for (int q = 0; q < 4; ++q) c4[q] = win[j % PF][q];
+      if (j + PF < 15) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) win[j % PF][q] = *(const f32x4*)&sLT[(16 * b + j + PF) * 20 + 4 * q];
+      }
+#pragma unroll
+      for (int i = j + 1; i < 16; ++i) x[i] -= c4[i >> 2][i & 3] * x[j];
+    }
+    GDNX_INV_MARK(0);
+    const auto f = colprep(16 * b + col);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      sTd[(16 * b + i) * 20 + col] = x[i];
+      emit(16 * b + i, 16 * b + col, x[i], f);   // x[i] == 0 for i < col
+    }
+    GDNX_INV_MARK(1);
+  }
+  __syncthreads();
+  GDNX_INV_MARK(2);
+#pragma unroll
+  for (int jb = 0; jb < NCT - 1; ++jb) {
+    if (wave != jb) continue;   // block column jb (compile-time, so Tk stays in registers)
+    const auto f = colprep(16 * jb + n16);
+    f32x4 Tk[NCT];
+    // T_jj as a B fragment: lane (g, n) holds T_jj[4g+s][n]
+#pragma unroll
+    for (int s = 0; s < 4; ++s) Tk[jb][s] = sTd[(16 * jb + 4 * g4 + s) * 20 + n16];
+#pragma unroll
+    for (int ib = jb + 1; ib < NCT; ++ib) {
+      f32x4 X = zero4();
+#pragma unroll
+      for (int kb = jb; kb < ib; ++kb) {
+        const f32x4 a = *(const f32x4*)&sL[(16 * ib + n16) * LDF + 16 * kb + 4 * g4];
+        mma(X, a, Tk[kb]);
+      }
+      const f32x4 a = *(const f32x4*)&sTd[(16 * ib + n16) * 20 + 4 * g4];
+      f32x4 Y = zero4();
+      mma(Y, a, X);
+      Tk[ib] = -Y;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) emit(16 * ib + 4 * g4 + s, 16 * jb + n16, Tk[ib][s], f);
+    }
+    GDNX_INV_MARK(3);
+  }
+}
+
+// Transpose of a 16x16 fp32 accumulator tile via MFMA with an identity
+// operand: returns Y with lane (g, n) holding X[n][4g+s] in element s.
+// The bf16 variant rounds the values to bf16 (used for bf16 outputs).
+__device__ __forceinline__ f32x4 tile_transpose(bf16*, const f32x4& X, int lane) {
+  const int g4 = lane >> 4, n16 = lane & 15;
+  bf16x8 a, b;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] = (bf16)X[e];
+    a[e + 4] = (bf16)0.f;
+    b[e] = (bf16)((4 * g4 + e == n16) ? 1.f : 0.f);
+    b[e + 4] = (bf16)0.f;
+  }
+  f32x4 y = zero4();
+  mma(y, a, b);
+  return y;
+}
+__device__ __forceinline__ f32x4 tile_transpose(float*, const f32x4& X, int lane) {
+  const int g4 = lane >> 4, n16 = lane & 15;
+  f32x4 b;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) b[e] = (4 * g4 + e == n16) ? 1.f : 0.f;
+  f32x4 y = zero4();
+  mma(y, X, b);
+  return y;
+}
+
 
 // 16x16 NT tile product over K (both operands K-contiguous LDS rows).
 template <typename CT, int K>

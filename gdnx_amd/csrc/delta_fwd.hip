@@ -1,10 +1,10 @@
 // Chunked decoupled-erase delta rule, forward (gfx950).
 //
-// One workgroup (4 waves) per chain = (batch, head, lane).  The lanes of a
+// One workgroup (NW waves, see Dims) per chain = (batch, head, lane).  The lanes of a
 // head share q/k/v (the reference expands them, gdn3/gdn3_upgrade.py:785-787)
 // and differ in the per-token erase/write coefficients a_e, a_w and the
 // log-decay g.  Per chunk of C tokens with carried state S0 [Dk, Dv] (fp32,
-// in registers, wave w owning value columns [w*D/4, (w+1)*D/4)):
+// in registers, wave w owning value columns [w*D/NW, (w+1)*D/NW)):
 //
 //   G_i  = sum_{s<=i} g_s,  D_ij = exp(G_i - G_j) [j<=i]
 //   L_ij = D_ij a_e,i (k_i.k_j) [j<i],  T = (I + L)^-1       (fp32, blocked)
@@ -33,16 +33,17 @@ struct alignas(16) FwdSmem {
   CT tb[C * Dm::LDC];   // T diag(a_e exp G)
   CT aq[C * Dm::LDC];   // D o Q K^T
   float L[C * Dm::LDF];
-  float T[C * Dm::LDF];
+  float LT[C * Dm::LDT];
+  float Td[C * Dm::LDT];
   float G[C], gam[C], dec[C], ae[C], aw[C];
 };
 
 template <typename CT, int D, int C>
-__global__ void __launch_bounds__(256) delta_fwd_kernel(DeltaArgs p) {
+__global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaArgs p) {
   typedef Dims<CT, D, C> Dm;
   typedef typename Dm::Frag Frag;
   constexpr int KS = Dm::KS, TPS = Dm::TPS, NDT = Dm::NDT, NCT = Dm::NCT, VS = Dm::VS, NVT = Dm::NVT;
-  constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF;
+  constexpr int LDD = Dm::LDD, LDC = Dm::LDC, NT = Dm::NT, DPW = Dm::DPW;
 
   __shared__ FwdSmem<CT, D, C> sm;
 
@@ -60,10 +61,16 @@ __global__ void __launch_bounds__(256) delta_fwd_kernel(DeltaArgs p) {
   const size_t st = (size_t)p.H * p.M;                                // scalar token stride
   const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + m;
   const ChunkScalars cs{sm.G, sm.gam, sm.dec, sm.ae, sm.aw, nullptr};
+  const CT* qg = (const CT*)p.q + qoff;
+  const CT* kg = (const CT*)p.k + qoff;
+  const CT* vg = (const CT*)p.v + qoff;
 
-  // strictly-upper parts never written below must read as zero
-  for (int i = tid; i < C * LDF; i += 256) sm.T[i] = 0.f;
-  for (int i = tid; i < C * LDC; i += 256) sm.aq[i] = from_f<CT>(0.f);
+  // never-written strictly-upper parts of TA, TB, Aq must read as zero
+  for (int i = tid; i < C * LDC; i += NT) {
+    sm.ta[i] = from_f<CT>(0.f);
+    sm.tb[i] = from_f<CT>(0.f);
+    sm.aq[i] = from_f<CT>(0.f);
+  }
 
   f32x4 S[NDT][NVT];
 #pragma unroll
@@ -78,77 +85,80 @@ __global__ void __launch_bounds__(256) delta_fwd_kernel(DeltaArgs p) {
       }
     }
 
+  TileRegs rq, rk, rv;
+  ScalarRegs rsc;
+  tile_fetch<CT, D, C>(rq, qg, rs, 0, p.T, tid);
+  tile_fetch<CT, D, C>(rk, kg, rs, 0, p.T, tid);
+  tile_fetch<CT, D, C>(rv, vg, rs, 0, p.T, tid);
+  if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, p.aw + soff, p.g + soff, st, 0, p.T, lane);
+
   for (int c = 0; c < NC; ++c) {
     const int t0 = c * C;
     __syncthreads();
-    stage_tile<CT, D, C>((const CT*)p.q + qoff, rs, t0, p.T, sm.q, nullptr, tid);
-    stage_tile<CT, D, C>((const CT*)p.k + qoff, rs, t0, p.T, sm.k, sm.kt, tid);
-    stage_tile<CT, D, C>((const CT*)p.v + qoff, rs, t0, p.T, nullptr, sm.vt, tid);
-    if (wave == 0) prep_scalars<C>(cs, p.ae + soff, p.aw + soff, p.g + soff, st, t0, p.T, lane);
+    tile_commit<CT, D, C>(rq, sm.q, nullptr, tid);
+    tile_commit<CT, D, C>(rk, sm.k, sm.kt, tid);
+    tile_commit<CT, D, C>(rv, nullptr, sm.vt, tid);
+    if (wave == 0) scal_commit<C>(cs, rsc, lane);
     __syncthreads();
-
-    // ---- grams: L (from K K^T, lower) and Aq (from K Q^T, lower) ----
-    {
-      constexpr int NP = NCT * (NCT + 1) / 2;
-      for (int task = wave; task < 2 * NP; task += 4) {
-        int it, jt;
-        tri_pair(task >> 1, it, jt);
-        if ((task & 1) == 0) {
-          // acc[ii] = k_i . k_j, i = it*16+4g+ii, j = jt*16+n
-          const f32x4 acc = tile_nt<CT, D>(&sm.k[(it * 16 + n16) * LDD], &sm.k[(jt * 16 + n16) * LDD], g4);
-          const int j = jt * 16 + n16;
-          const float Gj = sm.G[j];
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int i = it * 16 + 4 * g4 + ii;
-            sm.L[i * LDF + j] = (j < i) ? __expf(sm.G[i] - Gj) * sm.ae[i] * acc[ii] : 0.f;
-          }
-        } else {
-          // acc[ii] = q_i . k_j, i = it*16+n, j = jt*16+4g+ii
-          const f32x4 acc = tile_nt<CT, D>(&sm.k[(jt * 16 + n16) * LDD], &sm.q[(it * 16 + n16) * LDD], g4);
-          const int i = it * 16 + n16;
-          const float Gi = sm.G[i];
-          float vals[4];
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int j = jt * 16 + 4 * g4 + ii;
-            vals[ii] = (j <= i) ? __expf(Gi - sm.G[j]) * acc[ii] : 0.f;
-          }
-          st4(&sm.aq[i * LDC + jt * 16 + 4 * g4], vals[0], vals[1], vals[2], vals[3]);
-        }
-      }
+    // prefetch the next chunk while this one computes
+    if (c + 1 < NC) {
+      tile_fetch<CT, D, C>(rq, qg, rs, t0 + C, p.T, tid);
+      tile_fetch<CT, D, C>(rk, kg, rs, t0 + C, p.T, tid);
+      tile_fetch<CT, D, C>(rv, vg, rs, t0 + C, p.T, tid);
+      if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, p.aw + soff, p.g + soff, st, t0 + C, p.T, lane);
     }
+
+    // ---- grams: L (K K^T) and Aq (Q K^T) ----
+    chunk_grams<CT, D, C>(sm.k, sm.q, sm.L, sm.LT, sm.G, sm.ae, wave, lane,
+                          [&](int i, int j0, const float* v) { st4(&sm.aq[i * LDC + j0], v[0], v[1], v[2], v[3]); });
     __syncthreads();
-    invert_unit_lower<C>(sm.L, sm.T, wave, lane);
-
-    // ---- TA = T diag(a_w), TB = T diag(a_e exp G) ----
-    for (int idx = tid; idx < C * C; idx += 256) {
-      const int i = idx / C, j = idx % C;
-      const float t = sm.T[i * LDF + j];
-      sm.ta[i * LDC + j] = from_f<CT>(t * sm.aw[j]);
-      sm.tb[i * LDC + j] = from_f<CT>(t * sm.ae[j] * sm.gam[j]);
-    }
+    // ---- T = (I + L)^-1, emitted as TA = T diag(a_w), TB = T diag(a_e exp G) ----
+    invert_unit_lower<C>(
+        sm.L, sm.LT, sm.Td, wave, lane,
+        [&](int j) { return make_float2(sm.aw[j], sm.ae[j] * sm.gam[j]); },
+        [&](int i, int j, float t, float2 f) {
+          sm.ta[i * LDC + j] = from_f<CT>(t * f.x);
+          sm.tb[i * LDC + j] = from_f<CT>(t * f.y);
+        });
     __syncthreads();
 
     // ---- -Wm (rows i, cols d) via Wm^T = K^T TB^T; this wave's d tiles ----
 #pragma unroll
-    for (int dd = 0; dd < NDT / 4; ++dd) {
-      const int dt = wave * (NDT / 4) + dd;
+    for (int dd = 0; dd < DPW; ++dd) {
+      const int dt = wave * DPW + dd;
+      Frag a[C / KS];
+#pragma unroll
+      for (int kb = 0; kb < C / KS; ++kb) a[kb] = ld_frag(&sm.kt[(dt * 16 + n16) * LDC + kb * KS], g4);
 #pragma unroll
       for (int it = 0; it < NCT; ++it) {
+        f32x4 acc = zero4();
+#pragma unroll
+        for (int kb = 0; kb < C / KS; ++kb) mma(acc, a[kb], ld_frag(&sm.tb[(it * 16 + n16) * LDC + kb * KS], g4));
         // acc[ii] = Wm[i = it*16+n][d = dt*16+4g+ii]
-        const f32x4 acc = tile_nt<CT, C>(&sm.kt[(dt * 16 + n16) * LDC], &sm.tb[(it * 16 + n16) * LDC], g4);
         st4(&sm.wm[(it * 16 + n16) * LDD + dt * 16 + 4 * g4], -acc[0], -acc[1], -acc[2], -acc[3]);
       }
     }
     // ---- U = TA V (this wave's value columns) into the R accumulators ----
     f32x4 Racc[NCT][NVT];
-#pragma unroll
-    for (int it = 0; it < NCT; ++it)
+    {
+      Frag bv[NVT][C / KS];
 #pragma unroll
       for (int vt = 0; vt < NVT; ++vt)
-        Racc[it][vt] = tile_nt<CT, C>(&sm.ta[(it * 16 + n16) * LDC], &sm.vt[(v0 + vt * 16 + n16) * LDC], g4);
-    __syncthreads();
+#pragma unroll
+        for (int kb = 0; kb < C / KS; ++kb) bv[vt][kb] = ld_frag(&sm.vt[(v0 + vt * 16 + n16) * LDC + kb * KS], g4);
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) {
+        Frag a[C / KS];
+#pragma unroll
+        for (int kb = 0; kb < C / KS; ++kb) a[kb] = ld_frag(&sm.ta[(it * 16 + n16) * LDC + kb * KS], g4);
+#pragma unroll
+        for (int vt = 0; vt < NVT; ++vt) {
+          Racc[it][vt] = zero4();
+#pragma unroll
+          for (int kb = 0; kb < C / KS; ++kb) mma(Racc[it][vt], a[kb], bv[vt][kb]);
+        }
+      }
+    }
 
     // ---- S0 fragments over k = d (stashed for the backward) ----
     Frag Sf[NDT / TPS][NVT];
@@ -158,70 +168,64 @@ __global__ void __launch_bounds__(256) delta_fwd_kernel(DeltaArgs p) {
       for (int vt = 0; vt < NVT; ++vt)
         Sf[kb][vt] = acc_frag((CT*)nullptr, S[kb * TPS][vt], S[kb * TPS + TPS - 1][vt]);
     if (p.chunk_states) {
-      Frag* cst = (Frag*)p.chunk_states + ((size_t)chain * NC + c) * (256 * Dm::STASH_FRAGS);
+      Frag* cst = (Frag*)p.chunk_states + ((size_t)chain * NC + c) * (NT * Dm::STASH_FRAGS);
 #pragma unroll
       for (int kb = 0; kb < NDT / TPS; ++kb)
 #pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) cst[(kb * NVT + vt) * 256 + tid] = Sf[kb][vt];
+        for (int vt = 0; vt < NVT; ++vt) cst[(kb * NVT + vt) * NT + tid] = Sf[kb][vt];
     }
+    __syncthreads();   // -Wm complete
 
     // ---- R = U - Wm S0 ----
 #pragma unroll
     for (int it = 0; it < NCT; ++it) {
-      const CT* arow = &sm.wm[(it * 16 + n16) * LDD];
 #pragma unroll
       for (int kb = 0; kb < NDT / TPS; ++kb) {
-        const Frag a = ld_frag(arow + kb * KS, g4);
+        const Frag a = ld_frag(&sm.wm[(it * 16 + n16) * LDD + kb * KS], g4);
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) mma(Racc[it][vt], a, Sf[kb][vt]);
       }
     }
-    // ---- Y = diag(exp G) Q S0 + Aq R ----
-    f32x4 Yacc[NCT][NVT];
-#pragma unroll
-    for (int it = 0; it < NCT; ++it) {
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt) Yacc[it][vt] = zero4();
-      const CT* arow = &sm.q[(it * 16 + n16) * LDD];
-#pragma unroll
-      for (int kb = 0; kb < NDT / TPS; ++kb) {
-        const Frag a = ld_frag(arow + kb * KS, g4);
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) mma(Yacc[it][vt], a, Sf[kb][vt]);
-      }
-      const f32x4 gi = *(const f32x4*)&sm.gam[it * 16 + 4 * g4];
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt) Yacc[it][vt] *= gi;
-    }
-    Frag Rf[NCT / TPS][NVT];
-#pragma unroll
-    for (int kb = 0; kb < NCT / TPS; ++kb)
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt)
-        Rf[kb][vt] = acc_frag((CT*)nullptr, Racc[kb * TPS][vt], Racc[kb * TPS + TPS - 1][vt]);
-#pragma unroll
-    for (int it = 0; it < NCT; ++it) {
-      const CT* arow = &sm.aq[(it * 16 + n16) * LDC];
-#pragma unroll
-      for (int kb = 0; kb < NCT / TPS; ++kb) {
-        const Frag a = ld_frag(arow + kb * KS, g4);
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) mma(Yacc[it][vt], a, Rf[kb][vt]);
-      }
-    }
+    // ---- Y = diag(exp G) Q S0 + Aq R, one 16-row block at a time ----
     {
+      Frag Rf[NCT / TPS][NVT];
+#pragma unroll
+      for (int kb = 0; kb < NCT / TPS; ++kb)
+#pragma unroll
+        for (int vt = 0; vt < NVT; ++vt)
+          Rf[kb][vt] = acc_frag((CT*)nullptr, Racc[kb * TPS][vt], Racc[kb * TPS + TPS - 1][vt]);
       CT* yg = (CT*)p.y;
 #pragma unroll
-      for (int it = 0; it < NCT; ++it)
+      for (int it = 0; it < NCT; ++it) {
+        f32x4 Yacc[NVT];
 #pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int t = t0 + it * 16 + 4 * g4 + ii;
+        for (int vt = 0; vt < NVT; ++vt) Yacc[vt] = zero4();
+#pragma unroll
+        for (int kb = 0; kb < NDT / TPS; ++kb) {
+          const Frag a = ld_frag(&sm.q[(it * 16 + n16) * LDD + kb * KS], g4);
+#pragma unroll
+          for (int vt = 0; vt < NVT; ++vt) mma(Yacc[vt], a, Sf[kb][vt]);
+        }
+        const f32x4 gi = *(const f32x4*)&sm.gam[it * 16 + 4 * g4];
+#pragma unroll
+        for (int vt = 0; vt < NVT; ++vt) Yacc[vt] *= gi;
+#pragma unroll
+        for (int kb = 0; kb < NCT / TPS; ++kb) {
+          const Frag a = ld_frag(&sm.aq[(it * 16 + n16) * LDC + kb * KS], g4);
+#pragma unroll
+          for (int vt = 0; vt < NVT; ++vt) mma(Yacc[vt], a, Rf[kb][vt]);
+        }
+        // transposed tiles: lane (g, n) holds row it*16+n, columns 4g..4g+3
+        const int t = t0 + it * 16 + n16;
+#pragma unroll
+        for (int vt = 0; vt < NVT; ++vt) {
+          const f32x4 yt = tile_transpose((CT*)nullptr, Yacc[vt], lane);
           if (t < p.T) {
-            const size_t off = (((size_t)(b * p.T + t) * p.H + h) * p.M + m) * D + v0 + n16;
-#pragma unroll
-            for (int vt = 0; vt < NVT; ++vt) yg[off + vt * 16] = from_f<CT>(Yacc[it][vt][ii]);
+            const size_t off = (((size_t)(b * p.T + t) * p.H + h) * p.M + m) * D + v0 + vt * 16 + 4 * g4;
+            st4(yg + off, yt[0], yt[1], yt[2], yt[3]);
           }
         }
+      }
     }
     // ---- S = exp(G_last) S0 + K^T diag(dec) R ----
     {
@@ -237,12 +241,11 @@ __global__ void __launch_bounds__(256) delta_fwd_kernel(DeltaArgs p) {
       }
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) {
-        const CT* arow = &sm.kt[(dt * 16 + n16) * LDC];
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) S[dt][vt] *= gl;
 #pragma unroll
         for (int kb = 0; kb < NCT / TPS; ++kb) {
-          const Frag a = ld_frag(arow + kb * KS, g4);
+          const Frag a = ld_frag(&sm.kt[(dt * 16 + n16) * LDC + kb * KS], g4);
 #pragma unroll
           for (int vt = 0; vt < NVT; ++vt) mma(S[dt][vt], a, RDf[kb][vt]);
         }
@@ -264,7 +267,7 @@ __global__ void __launch_bounds__(256) delta_fwd_kernel(DeltaArgs p) {
 template <typename CT, int D, int C>
 static int launch_fwd(const DeltaArgs& a, hipStream_t stream) {
   const int nblocks = a.B * a.H * a.M;
-  hipLaunchKernelGGL((delta_fwd_kernel<CT, D, C>), dim3(nblocks), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((delta_fwd_kernel<CT, D, C>), dim3(nblocks), dim3(Dims<CT, D, C>::NT), 0, stream, a);
   return check_launch("delta_fwd_kernel");
 }
 
