@@ -53,7 +53,7 @@ def flops_bwd_grads(B, T, H, M, D, C):
     return 2 * flops_fwd(B, T, H, M, D, C) - flops_bwd_state(B, T, H, M, D, C)
 
 
-def cpu_baseline(T=4096, H=4, warm_T=64):
+def cpu_baseline(T=2048, H=4, warm_T=64):
     """Time the CPU oracle (fp32 sequential recurrence + autograd) on
     B=1, H heads x 4 lanes, T tokens; tokens/s scaled to the 16-head layer."""
     import torch
@@ -80,6 +80,149 @@ def cpu_baseline(T=4096, H=4, warm_T=64):
     }
 
 
+def measured_traffic(kernel):
+    """HBM bytes per launch of ``kernel`` from the committed counter table
+    (FETCH_SIZE + WRITE_SIZE runs, each scaled by the counter's reading for a
+    1 GiB device copy), or None when the table has no entry."""
+    path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        entry = json.load(f).get("kernels", {}).get(kernel)
+    return None if entry is None else entry["traffic"]
+
+
+def decode_bytes(NS, H, NC, D, io_bytes=2):
+    """HBM bytes of one decode step: the fp32 state read and written once,
+    q, k, v read once per head, the per-chain scalars (a_e, a_w, log_g) and
+    y written once per chain."""
+    state = NS * H * NC * D * D * 4
+    return 2 * state + 3 * NS * H * D * io_bytes + 3 * NS * H * NC * 4 + NS * H * NC * D * io_bytes
+
+
+def cpu_baseline_decode(NS_sample=64, H=16, NC=16, D=128, steps=8):
+    """Time the CPU oracle's sequential step (fp32) on NS_sample sequences of
+    the decode workload; tokens/s scaled to the 256 sequences."""
+    import torch
+    from oracle import delta
+    torch.set_num_threads(os.cpu_count() or 1)
+    gen = torch.Generator().manual_seed(1004)
+    S = torch.randn(NS_sample, H, NC, D, D, generator=gen) * 0.02
+    q, k, v = (torch.randn(NS_sample, 1, H, D, generator=gen) for _ in range(3))
+    a = torch.rand(NS_sample, 1, H, NC, generator=gen)
+    lg = torch.full((NS_sample, 1, H, NC), -0.01)
+    delta.lane_delta(q, k, v, a, a, lg, state0=S, dtype=torch.float32)
+    t0 = time.perf_counter()
+    for _ in range(steps):
+        _, S = delta.lane_delta(q, k, v, a, a, lg, state0=S, dtype=torch.float32)
+    secs = (time.perf_counter() - t0) / steps
+    return {
+        "value": NS_sample / secs,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle.delta.lane_delta fp32 one-token step, {NS_sample} of the 256 sequences "
+                  f"x {H} heads x {NC} chains d={D}, mean of {steps} steps ({secs * 1e3:.1f} ms/step); "
+                  f"tokens/s = sequences per step time",
+    }
+
+
+def bench_decode(args):
+    """Config 4: batched one-token decode, 256 sequences x 16 heads x (4 lanes
+    x 4 decays) chains of 128x128 fp32 state, bf16 q/k/v per step.  A step is
+    one gdnx_delta_decode_step over all chains; value = sequences decoded per
+    second (one token each)."""
+    import torch
+    from gdnx_amd import ops
+    import torch.nn.functional as F
+    from oracle import inputs
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    NS, H, M, NT, D = 256, 16, 4, 4, 128
+    NC = M * NT
+    gen = torch.Generator(device=dev).manual_seed(1004)
+    state = torch.randn(NS, H, NC, D, D, device=dev, generator=gen) * 0.02
+    n_in = 8  # distinct per-step inputs cycled through the timed steps
+    q = F.normalize(torch.randn(n_in, NS, H, D, device=dev, generator=gen), dim=-1).bfloat16()
+    k = F.normalize(torch.randn(n_in, NS, H, D, device=dev, generator=gen), dim=-1).bfloat16()
+    v = torch.randn(n_in, NS, H, D, device=dev, generator=gen).bfloat16()
+    beta = torch.sigmoid(torch.randn(n_in, NS, H, M, 1, device=dev, generator=gen))
+    alpha_c = beta * (k.float() ** 2).sum(-1)[..., None, None]
+    a = ((-torch.expm1(-alpha_c)) / alpha_c).mul(beta).expand(n_in, NS, H, M, NT).reshape(n_in, NS, H, NC).contiguous()
+    base = torch.log1p(-torch.tensor(inputs.TAUS, device=dev)).repeat(M)
+    lg = (base + 0.01 * torch.randn(n_in, NS, H, NC, device=dev, generator=gen)).contiguous()
+    y = torch.empty(NS, H, NC, D, device=dev, dtype=torch.bfloat16)
+    stream = torch.cuda.current_stream()
+
+    def step(i):
+        j = i % n_in
+        ops.delta_decode_step(q[j], k[j], v[j], a[j], a[j], lg[j], state, out=y)
+
+    for i in range(args.warmup):
+        step(i)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(args.steps):
+        step(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / args.steps
+    nbytes = decode_bytes(NS, H, NC, D)
+    achieved = nbytes / sec / 1e9
+    traffic = measured_traffic("delta_decode_kernel")
+    line = {
+        "metric": "GDN3 batched decode tokens/s @256 seq x 16 heads x 4 lanes x 4 decays, d=128",
+        "value": NS / sec,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "BASELINE config 4: batched one-token decode, 65,536 fp32 128x128 "
+                               "states (4.29 GB), bf16 q/k/v per step",
+                   "sequences": NS, "heads": H, "chains_per_head": NC, "head_dim": D,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": "delta_decode_kernel", "achieved": achieved,
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": achieved * 1e9 / HBM_PEAK,
+                     "traffic": traffic, "mean_us": sec * 1e6, "algorithmic_bytes": nbytes},
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_decode()
+    print(json.dumps(line), flush=True)
+
+
+def bench_copy(args):
+    """Calibration for the HBM traffic counters: a plain device copy of a
+    known size (1 GiB read + 1 GiB written per launch).  Prints its own JSON
+    line; the FETCH_SIZE / WRITE_SIZE counters of this launch divided by
+    2^30 bytes give the factor that converts the counters' units to bytes."""
+    import torch
+    dev = torch.device("cuda:0")
+    n = 1 << 28
+    src = torch.randn(n, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(args.warmup):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(args.steps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / args.steps
+    print(json.dumps({"metric": "device copy GB/s (traffic-counter calibration)",
+                      "value": 2 * n * 4 / sec / 1e9, "unit": "GB/s", "bytes_read": n * 4,
+                      "bytes_written": n * 4, "steps": args.steps}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser(description=__doc__.splitlines()[0])
     ap.add_argument("--gpus", type=int, default=1)
@@ -87,11 +230,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=10)
+    ap.add_argument("--workload", choices=("train", "decode", "copy"), default="train",
+                    help="train: config 2 scan fwd+bwd (headline); decode: config 4 decode step; "
+                         "copy: 1 GiB device copy used to calibrate the HBM traffic counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the recurrence shards by chains with no "
               "communication (see DESIGN.md); run with --gpus 1", file=sys.stderr)
         sys.exit(2)
+    if args.workload == "decode":
+        return bench_decode(args)
+    if args.workload == "copy":
+        return bench_copy(args)
 
     import torch
     from gdnx_amd import gdn3, ops
@@ -162,11 +312,7 @@ def main():
     dom = max(kernels, key=lambda n: kernels[n][0])
     t_dom, f_dom = kernels[dom]
     achieved = f_dom / t_dom / 1e12
-    traffic = None
-    tr_path = os.path.join(ROOT, "profiles", "hbm_traffic.json")
-    if os.path.exists(tr_path):
-        with open(tr_path) as f:
-            traffic = json.load(f).get(dom)
+    traffic = measured_traffic(dom)
 
     line = {
         "metric": "GDN3 scan tokens/s fwd+bwd @B=4,T=4096 bf16",

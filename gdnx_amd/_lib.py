@@ -32,6 +32,7 @@ SIGNATURES = {
     "gdnx_delta_chunk_bwd": (_c_int, [_vp] * 17 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_bwd_state": (_c_int, [_vp] * 8 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_bwd_grads": (_c_int, [_vp] * 15 + [_c_int] * 7 + [_vp]),
+    "gdnx_delta_decode_step": (_c_int, [_vp] * 8 + [_c_int] * 5 + [_vp]),
 }
 
 

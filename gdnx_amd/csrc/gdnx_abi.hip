@@ -150,3 +150,20 @@ extern "C" int gdnx_delta_chunk_bwd_grads(const void* q, const void* k, const vo
   return bwd_common(q, k, v, a_e, a_w, log_g, dy, nullptr, chunk_states, (void*)workspace, dq, dk, dv,
                     da_e, da_w, dlog_g, nullptr, B, T, H, M, head_dim, chunk, dtype, 2, stream);
 }
+
+extern "C" int gdnx_delta_decode_step(const void* q, const void* k, const void* v, const float* a_e,
+                                      const float* a_w, const float* log_g, float* state, void* y, int NS,
+                                      int H, int M, int head_dim, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16)
+    return set_error(GDNX_ERR_ARG, "dtype %d is not GDNX_DTYPE_F32/BF16", dtype);
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(GDNX_ERR_SHAPE, "head_dim %d unsupported (64 or 128)", head_dim);
+  if (NS < 1 || H < 1 || M < 1 || (long long)NS * H * M > (1LL << 30))
+    return set_error(GDNX_ERR_SHAPE, "bad sizes NS=%d H=%d M=%d", NS, H, M);
+  if (!q || !k || !v || !a_e || !a_w || !log_g || !state || !y)
+    return set_error(GDNX_ERR_ARG, "all pointers must be non-null");
+  if ((uintptr_t)state & 15u) return set_error(GDNX_ERR_ARG, "state must be 16-byte aligned");
+  DecodeArgs a{q, k, v, a_e, a_w, log_g, state, y, NS, H, M, head_dim, dtype};
+  return decode_dispatch(a, (hipStream_t)stream);
+}

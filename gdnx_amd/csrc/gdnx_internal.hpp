@@ -46,6 +46,19 @@ int set_error(int code, const char* fmt, ...);
 // Check hipGetLastError() after a launch.
 int check_launch(const char* what);
 
+struct DecodeArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* ae;
+  const float* aw;
+  const float* g;
+  float* state;
+  void* y;
+  int NS, H, M, D, dtype;
+};
+
+int decode_dispatch(const DecodeArgs& a, hipStream_t stream);
 int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);
 int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream);
 int delta_chunk_size(int D, int dtype);

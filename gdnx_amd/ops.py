@@ -158,3 +158,29 @@ def delta_chunk_bwd_grads(q, k, v, a_e, a_w, log_g, dy, chunk_states, ws, chunk,
             B, T, H, M, D, chunk, code, _lib.stream_of(q))
     _lib.check(rc, "gdnx_delta_chunk_bwd_grads")
     return out
+
+
+def delta_decode_step(q, k, v, a_e, a_w, log_g, state, out=None):
+    """One-token decode step (state updated in place).
+
+    q, k, v [NS, H, D] (bf16/float32, shared by the M chains of a head);
+    a_e, a_w, log_g [NS, H, M] float32; state [NS, H, M, D, D] float32.
+    Returns y [NS, H, M, D] in q's dtype."""
+    lib = _lib.load()
+    _need(q.is_cuda and q.dim() == 3 and q.shape == k.shape == v.shape, "q, k, v must be [NS,H,D] on GPU")
+    NS, H, D = q.shape
+    _need(a_e.dim() == 3 and tuple(a_e.shape[:2]) == (NS, H), "a_e must be [NS,H,M]")
+    M = a_e.shape[2]
+    _need(a_e.shape == a_w.shape == log_g.shape, "a_e, a_w, log_g must share shape")
+    _need(tuple(state.shape) == (NS, H, M, D, D) and state.dtype == torch.float32, "state must be fp32 [NS,H,M,D,D]")
+    for t in (q, k, v, a_e, a_w, log_g, state):
+        _need(t.is_contiguous(), "inputs must be contiguous")
+    for t in (a_e, a_w, log_g):
+        _need(t.dtype == torch.float32, "a_e, a_w, log_g must be float32")
+    y = torch.empty(NS, H, M, D, dtype=q.dtype, device=q.device) if out is None else out
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_delta_decode_step(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w),
+                                        _lib.ptr(log_g), _lib.ptr(state), _lib.ptr(y), NS, H, M, D,
+                                        _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    _lib.check(rc, "gdnx_delta_decode_step")
+    return y

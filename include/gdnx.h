@@ -105,6 +105,20 @@ int gdnx_delta_chunk_bwd_grads(const void* q, const void* k, const void* v,
                                int B, int T, int H, int M, int head_dim, int chunk,
                                int dtype, void* stream);
 
+/* One-token decode step, state updated in place.  The reference has no
+ * decode path (GDN3LinearAttn.forward ignores cache_params,
+ * gdn3/gdn3_upgrade.py:725); this is one iteration of the sequential oracle
+ * (gdn3/_reference_recurrence.py:60-84 dense regime, research/kernel_ab/
+ * ref_scan.py:40-45) on carried state, i.e. gdnx_delta_chunk_fwd with T=1.
+ * q, k, v [NS, H, D] (io dtype, shared by the M chains of a head: lanes x
+ * decay timescales); a_e, a_w, log_g [NS, H, M] float32; state
+ * [NS, H, M, D, D] float32 key-major, read and written once; y [NS, H, M, D]
+ * io dtype. */
+int gdnx_delta_decode_step(const void* q, const void* k, const void* v,
+                           const float* a_e, const float* a_w, const float* log_g,
+                           float* state, void* y, int NS, int H, int M, int head_dim,
+                           int dtype, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
