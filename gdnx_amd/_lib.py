@@ -19,7 +19,7 @@ DTYPE_F32 = 0
 DTYPE_BF16 = 1
 ABI_VERSION = 1
 
-_c_int, _c_ll, _vp = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p
+_c_int, _c_ll, _vp, _c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_float
 
 # name -> (restype, argtypes); every entry point declared in include/gdnx.h
 SIGNATURES = {
@@ -33,6 +33,12 @@ SIGNATURES = {
     "gdnx_delta_chunk_bwd_state": (_c_int, [_vp] * 8 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_bwd_grads": (_c_int, [_vp] * 15 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_decode_step": (_c_int, [_vp] * 8 + [_c_int] * 5 + [_vp]),
+    "gdnx_gdn3_workspace_bytes": (_c_ll, [_c_int] * 5),
+    "gdnx_gdn3_num_compactions": (_c_int, [_c_int] * 3),
+    "gdnx_gdn3_chunk_fwd": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 9
+                            + [_c_int] * 12 + [_c_float, _c_int, _vp]),
+    "gdnx_gdn3_compact": (_c_int, [_vp] * 8 + [_c_int] * 8 + [_c_float, _vp]),
+    "gdnx_kron_read": (_c_int, [_vp] * 6 + [_c_int] * 9 + [_vp]),
 }
 
 

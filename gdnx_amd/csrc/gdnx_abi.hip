@@ -167,3 +167,111 @@ extern "C" int gdnx_delta_decode_step(const void* q, const void* k, const void* 
   DecodeArgs a{q, k, v, a_e, a_w, log_g, state, y, NS, H, M, head_dim, dtype};
   return decode_dispatch(a, (hipStream_t)stream);
 }
+
+// ---------------------------------------------------------------------------
+// GDN3 Kronecker-residual path
+// ---------------------------------------------------------------------------
+namespace gdnx {
+
+static int g3_geom(int D, int R, int av, int ak, int bv, int bk, G3Geom& ge) {
+  if (D != 64 && D != 128) return set_error(GDNX_ERR_SHAPE, "head_dim %d unsupported (64 or 128)", D);
+  if (R < 1 || R > 4) return set_error(GDNX_ERR_SHAPE, "Kronecker rank R=%d unsupported (1..4)", R);
+  if (av < 1 || ak < 1 || bv < 1 || bk < 1 || av * bv != D || ak * bk != D)
+    return set_error(GDNX_ERR_SHAPE, "factors (a_v=%d, a_k=%d, b_v=%d, b_k=%d) need a_v*b_v = a_k*b_k = %d",
+                     av, ak, bv, bk, D);
+  const int m = av * ak, n = bv * bk;
+  if (m > 256 || n > 256) return set_error(GDNX_ERR_SHAPE, "a_v*a_k=%d and b_v*b_k=%d must be <= 256", m, n);
+  if (av * bk > 256) return set_error(GDNX_ERR_SHAPE, "a_v*b_k=%d must be <= 256", av * bk);
+  int q = R + 4;
+  if (m < q) q = m;
+  if (n < q) q = n;
+  ge = G3Geom{R, av, ak, bv, bk, m, n, q};
+  return GDNX_OK;
+}
+
+static bool g3_window_ok(int D, int P) { return (D == 128 && P == 16) || (D == 64 && (P == 16 || P == 32)); }
+
+}  // namespace gdnx
+
+extern "C" long long gdnx_gdn3_workspace_bytes(int B, int H, int M, int head_dim, int dtype) {
+  if (B < 1 || H < 1 || M < 1 || (head_dim != 64 && head_dim != 128) ||
+      (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16))
+    return -1;
+  return (long long)B * H * M * head_dim * head_dim * (dtype == GDNX_DTYPE_BF16 ? 2 : 4);
+}
+
+extern "C" int gdnx_gdn3_num_compactions(int T, int P, int compact_every) {
+  if (T < 0 || P < 1 || compact_every < P || compact_every % P != 0) return -1;
+  return T / compact_every;
+}
+
+extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, int qkv_lanes,
+                                   const float* b_gates, const float* w_gates, int gate_channels,
+                                   const float* decay, const float* sketch, void* y, float* A_out,
+                                   float* B_out, float* U_out, float* Vb_out, double* comp_stats,
+                                   void* workspace, int B, int T, int H, int M, int head_dim, int R, int P,
+                                   int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
+                                   int dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
+  if (rc) return rc;
+  G3Geom ge;
+  if ((rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge))) return rc;
+  if (!g3_window_ok(head_dim, P))
+    return set_error(GDNX_ERR_SHAPE, "residual window P=%d unsupported for head_dim %d (128: 16; 64: 16, 32)",
+                     P, head_dim);
+  if (compact_every < P || compact_every % P != 0)
+    return set_error(GDNX_ERR_SHAPE, "compact_every=%d must be a positive multiple of P=%d", compact_every, P);
+  if (qkv_lanes != 1 && qkv_lanes != M)
+    return set_error(GDNX_ERR_SHAPE, "qkv_lanes=%d must be 1 (shared) or M=%d", qkv_lanes, M);
+  if (gate_channels != 1 && gate_channels != head_dim)
+    return set_error(GDNX_ERR_SHAPE, "gate_channels=%d must be 1 or head_dim=%d", gate_channels, head_dim);
+  if (!b_gates || !w_gates || !decay || !sketch || !y || !workspace)
+    return set_error(GDNX_ERR_ARG, "gates, decay, sketch, y and workspace must be non-null");
+  if (gate_channels > 1 && (!aligned16(b_gates) || !aligned16(w_gates)))
+    return set_error(GDNX_ERR_ARG, "per-channel gates must be 16-byte aligned");
+  if (!aligned16(workspace)) return set_error(GDNX_ERR_ARG, "workspace must be 16-byte aligned");
+  if (!(slow_decay >= 0.f && slow_decay <= 1.f))
+    return set_error(GDNX_ERR_ARG, "slow_decay must lie in [0, 1]");
+  if ((A_out || B_out || U_out || Vb_out) && T % P != 0)
+    return set_error(GDNX_ERR_SHAPE, "final state needs T (%d) to be a multiple of P (%d)", T, P);
+  if (T == 0) return GDNX_OK;
+  G3FwdArgs a{q, k, v, b_gates, w_gates, decay, sketch, y, A_out, B_out, U_out, Vb_out, comp_stats,
+              workspace, ge, B, T, H, M, head_dim, P, compact_every, qkv_lanes, gate_channels, dtype,
+              slow_decay};
+  return gdn3_fwd_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_gdn3_compact(const float* A, const float* Bf, const float* U, const float* Vb,
+                                 const float* sketch, float* A_out, float* B_out, double* comp_stats, int N,
+                                 int head_dim, int R, int P, int a_v, int a_k, int b_v, int b_k,
+                                 float slow_decay, void* stream) {
+  g_err[0] = 0;
+  G3Geom ge;
+  int rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge);
+  if (rc) return rc;
+  if (N < 0 || N > (1 << 30)) return set_error(GDNX_ERR_SHAPE, "bad chain count N=%d", N);
+  if (!g3_window_ok(head_dim, P))
+    return set_error(GDNX_ERR_SHAPE, "residual window P=%d unsupported for head_dim %d", P, head_dim);
+  if (!A || !Bf || !U || !Vb || !sketch || !A_out || !B_out)
+    return set_error(GDNX_ERR_ARG, "state, sketch and output pointers must be non-null");
+  if (!(slow_decay >= 0.f && slow_decay <= 1.f))
+    return set_error(GDNX_ERR_ARG, "slow_decay must lie in [0, 1]");
+  G3CompactArgs a{A, Bf, U, Vb, sketch, A_out, B_out, comp_stats, ge, N, head_dim, P, slow_decay};
+  return gdn3_compact_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_kron_read(const float* A, const float* Bf, const float* U, const float* Vb, const float* x,
+                              float* y, int N, int C, int head_dim, int R, int P, int a_v, int a_k, int b_v,
+                              int b_k, void* stream) {
+  g_err[0] = 0;
+  G3Geom ge;
+  int rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge);
+  if (rc) return rc;
+  if (N < 0 || C < 0 || (long long)N * C > (1LL << 30)) return set_error(GDNX_ERR_SHAPE, "bad sizes N=%d C=%d", N, C);
+  if (P < 0 || P > 64) return set_error(GDNX_ERR_SHAPE, "residual slots P=%d unsupported (0..64)", P);
+  if (!A || !Bf || !x || !y || (P > 0 && (!U || !Vb)))
+    return set_error(GDNX_ERR_ARG, "pointers must be non-null");
+  KronReadArgs a{A, Bf, U, Vb, x, y, ge, N, C, head_dim, P};
+  return kron_read_dispatch(a, (hipStream_t)stream);
+}

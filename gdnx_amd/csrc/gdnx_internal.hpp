@@ -58,6 +58,60 @@ struct DecodeArgs {
   int NS, H, M, D, dtype;
 };
 
+// Kronecker-residual geometry: state S = sum_r A_r (x) B_r + U Vb^T with
+// A_r [a_v, a_k], B_r [b_v, b_k]; m = a_v a_k, n = b_v b_k, q = sketch width.
+struct G3Geom {
+  int R, av, ak, bv, bk, m, n, q;
+};
+
+struct G3FwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* bg;     // erase gates, [B,T,H,M,D] or [B,T,H,M]
+  const float* wg;     // write gates, same layout
+  const float* dec;    // multiplicative decay [B,T,H,M]
+  const float* sketch; // [N, n, q]
+  void* y;             // [B,T,H,M,D]
+  float* A_out;        // [N,R,a_v,a_k] or null
+  float* B_out;        // [N,R,b_v,b_k] or null
+  float* U_out;        // [N,D,P] or null
+  float* Vb_out;       // [N,D,P] or null
+  double* stats;       // [T/Kc, N, 2] (energy, kept) or null
+  void* skron;         // workspace [N, D, D] compute dtype
+  G3Geom ge;
+  int B, T, H, M, D, P, Kc, qkv_lanes, gate_ch, dtype;
+  float sdec;
+};
+
+struct G3CompactArgs {
+  const float* A;
+  const float* Bf;
+  const float* U;      // [N, D, P]
+  const float* Vb;     // [N, D, P]
+  const float* sketch; // [N, n, q]
+  float* A_out;
+  float* B_out;
+  double* stats;       // [N, 2] or null
+  G3Geom ge;
+  int N, D, P;
+  float sdec;
+};
+
+struct KronReadArgs {
+  const float* A;
+  const float* Bf;
+  const float* U;   // [N, D, P]
+  const float* Vb;  // [N, D, P]
+  const float* x;   // [N, C, D]
+  float* y;         // [N, C, D]
+  G3Geom ge;
+  int N, C, D, P;
+};
+
+int gdn3_fwd_dispatch(const G3FwdArgs& a, hipStream_t stream);
+int gdn3_compact_dispatch(const G3CompactArgs& a, hipStream_t stream);
+int kron_read_dispatch(const KronReadArgs& a, hipStream_t stream);
 int decode_dispatch(const DecodeArgs& a, hipStream_t stream);
 int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);
 int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream);

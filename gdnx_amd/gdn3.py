@@ -14,6 +14,11 @@ a = alpha(beta |k|^2) * beta (the exact-alpha write of
 gdn3/gdn3_upgrade.py:641-648).  The elementwise prologue runs in torch
 (autograd carries its gradient into beta and k); the recurrence and its
 backward are the HIP kernels of libgdnx.
+
+``gdn3_recurrent_state`` is the same method in its general regime: a
+P-slot residual window and periodic rearrangement-SVD compaction of the
+Kronecker factors (forward only; the compaction is outside autograd in the
+reference too, gdn3/gdn3_upgrade.py:513-517).
 """
 from __future__ import annotations
 
@@ -46,3 +51,98 @@ def gdn3_scan(q, k, v, beta, log_g, state0=None, return_state=False):
     a = gdn3_coeff(k, beta)
     y, s = ops.delta_rule(q, k, v, a, a, log_g.float(), state0)
     return (y, s) if return_state else y
+
+
+_SKETCHES = {}
+
+
+def default_sketch(N, n, q, device):
+    """The compaction sketch: randn(N, n, q) float32 from a CPU generator
+    seeded 1234 (the reference draws randn(N, n, q) from a generator seeded
+    1234 on R_mat's device, gdn3/gdn3_upgrade.py:681-682; the CPU stream is
+    the one its CPU runs use).  Cached per (device, shape)."""
+    key = (str(device), N, n, q)
+    if key not in _SKETCHES:
+        gen = torch.Generator(device="cpu").manual_seed(1234)
+        _SKETCHES[key] = torch.randn(N, n, q, dtype=torch.float32, generator=gen).to(device)
+    return _SKETCHES[key]
+
+
+def _lane_shared(x):
+    """[B,T,H,M,D] with a stride-0 lane dim (an expand) -> its [B,T,H,D] view."""
+    return x.dim() == 5 and x.stride(3) == 0
+
+
+def _scalar_gate(g):
+    return g.dim() == 5 and g.stride(-1) == 0
+
+
+def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
+                         factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None,
+                         sketch=None, return_state=False):
+    """GDN3LinearAttn._gdn3_recurrent_state on the GPU (forward).
+
+    Reference: gdn3/gdn3_upgrade.py:403-531 with the semantics of its frozen
+    oracle gdn3/_reference_recurrence.py:33-94 (the chunked reference departs
+    from that oracle after the second compaction window).  q, k, b_gates:
+    [B,T,H,M,K]; v, w_gates: [B,T,H,M,V]; decay_factors [B,T,H,M]
+    (q/k/v may also be [B,T,H,D], shared by the lanes, and the gates
+    [B,T,H,M], one scalar per lane)
+    (multiplicative, clamped to [0, 1]).  Lane-expanded q/k/v (stride 0 over
+    M) are read once per head; gates expanded over the channel dim are read
+    as one scalar per lane.  bf16 q/k/v compute on bf16 MFMA operands with
+    fp32 state; other float dtypes run in float32.  compact_every defaults to
+    P (the reference layer compacts every P tokens).  Returns y
+    [B,T,H,M,V] in the compute dtype, plus ((A, B, U, Vb), comp_err) when
+    return_state (comp_err is the reference's summed discarded energy, a
+    device tensor).
+    """
+    B, T, H, M = decay_factors.shape
+    cdt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
+    D = q.shape[-1]
+
+    def lanes5(x):
+        return x.unsqueeze(3) if x.dim() == 4 else x
+    if all(x.dim() == 4 or _lane_shared(x) for x in (q, k, v)):
+        q4, k4, v4 = (x.to(cdt).contiguous() if x.dim() == 4 else x.select(3, 0).to(cdt).contiguous()
+                      for x in (q, k, v))
+    else:
+        q4, k4, v4 = (lanes5(x).to(cdt).expand(B, T, H, M, D).contiguous() for x in (q, k, v))
+
+    def chan5(g):
+        return g.unsqueeze(-1) if g.dim() == 4 else g
+    if all(g.dim() == 4 or _scalar_gate(g) for g in (b_gates, w_gates)):
+        bg, wg = (g.float().contiguous() if g.dim() == 4 else g.select(-1, 0).float().contiguous()
+                  for g in (b_gates, w_gates))
+    else:
+        bg = chan5(b_gates).float().expand(B, T, H, M, D).contiguous()
+        wg = chan5(w_gates).float().expand(B, T, H, M, D).contiguous()
+    a_v, a_k, b_v, b_k = factors
+    N = B * H * M
+    qw = ops.sketch_width(R, a_v * a_k, b_v * b_k)
+    G = default_sketch(N, b_v * b_k, qw, q.device) if sketch is None else sketch.float().contiguous()
+    y, stats, state = ops.gdn3_chunk_fwd(q4, k4, v4, bg, wg, decay_factors.float().contiguous(), G, M=M,
+                                         R=R, P=P, factors=factors, slow_decay=slow_decay,
+                                         compact_every=compact_every, return_state=return_state)
+    if not return_state:
+        return y
+    err = (stats[:, :, 0].sum(1) - stats[:, :, 1].sum(1)).clamp(min=0.0).sum()
+    return y, state, err
+
+
+class GDN3RecurrentState(torch.autograd.Function):
+    """Autograd wrapper of gdn3_recurrent_state.  The Kronecker-residual
+    regime has no HIP backward yet: backward raises instead of returning
+    wrong gradients.  The dense regime (P >= T, scalar gates, shared q/k/v)
+    is differentiable through gdn3_scan."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, b_gates, w_gates, decay_factors, R=4, P=16, factors=(16, 16, 8, 8),
+                slow_decay=0.97, compact_every=None):
+        return gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, R=R, P=P, factors=factors,
+                                    slow_decay=slow_decay, compact_every=compact_every)
+
+    @staticmethod
+    def backward(ctx, dy):
+        raise NotImplementedError("the GDN3 Kronecker-residual backward is not implemented in gdnx_amd; "
+                                  "train in the dense regime (P >= T) through gdn3_scan")

@@ -184,3 +184,114 @@ def delta_decode_step(q, k, v, a_e, a_w, log_g, state, out=None):
                                         _lib.dtype_code(q.dtype), _lib.stream_of(q))
     _lib.check(rc, "gdnx_delta_decode_step")
     return y
+
+
+# ---------------------------------------------------------------------------
+# GDN3 Kronecker-residual regime
+# ---------------------------------------------------------------------------
+def _geom(A, Bk):
+    N, R, a_v, a_k = A.shape
+    b_v, b_k = Bk.shape[-2:]
+    return N, R, a_v, a_k, b_v, b_k
+
+
+def sketch_width(R, m, n):
+    """Columns of the compaction sketch: min(R + 4, m, n) (gdn3/gdn3_upgrade.py:677)."""
+    return min(R + 4, m, n)
+
+
+def kron_read(A, Bk, U, Vb, x):
+    """S x for S = sum_r A_r (x) B_r + U Vb^T (gdnx_kron_read).
+
+    A [N,R,a_v,a_k], Bk [N,R,b_v,b_k], U [N,V,P], Vb [N,K,P], x [N,K] or
+    [N,C,K]; float32 on the GPU.  Returns float32 [N,V] or [N,C,V]."""
+    lib = _lib.load()
+    N, R, a_v, a_k, b_v, b_k = _geom(A, Bk)
+    D = a_v * b_v
+    squeeze = x.dim() == 2
+    x3 = x.unsqueeze(1) if squeeze else x
+    C = x3.shape[1]
+    P = U.shape[-1]
+    for t in (A, Bk, U, Vb, x3):
+        _need(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous(),
+              "kron_read inputs must be contiguous float32 on the GPU")
+    _need(tuple(U.shape) == (N, D, P) and tuple(Vb.shape) == (N, D, P) and x3.shape[0] == N
+          and x3.shape[2] == D, "inconsistent kron_read shapes")
+    y = torch.empty(N, C, D, dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.gdnx_kron_read(_lib.ptr(A), _lib.ptr(Bk), _lib.ptr(U), _lib.ptr(Vb), _lib.ptr(x3), _lib.ptr(y),
+                                N, C, D, R, P, a_v, a_k, b_v, b_k, _lib.stream_of(x))
+    _lib.check(rc, "gdnx_kron_read")
+    return y[:, 0] if squeeze else y
+
+
+def gdn3_compact(A, Bk, U, Vb, sketch, slow_decay=0.97):
+    """One rearrangement-SVD compaction per chain (gdnx_gdn3_compact).
+
+    Returns (A_new, B_new, stats [N,2] float64 = (|R_mat|^2, kept sigma^2));
+    the reference's error is max(0, sum_n stats[:,0] - sum_n stats[:,1])."""
+    lib = _lib.load()
+    N, R, a_v, a_k, b_v, b_k = _geom(A, Bk)
+    D = a_v * b_v
+    P = U.shape[-1]
+    for t in (A, Bk, U, Vb, sketch):
+        _need(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous(),
+              "compaction inputs must be contiguous float32 on the GPU")
+    _need(tuple(sketch.shape) == (N, b_v * b_k, sketch_width(R, a_v * a_k, b_v * b_k)), "bad sketch shape")
+    A_new, B_new = torch.empty_like(A), torch.empty_like(Bk)
+    stats = torch.empty(N, 2, dtype=torch.float64, device=A.device)
+    with torch.cuda.device(A.device):
+        rc = lib.gdnx_gdn3_compact(_lib.ptr(A), _lib.ptr(Bk), _lib.ptr(U), _lib.ptr(Vb), _lib.ptr(sketch),
+                                   _lib.ptr(A_new), _lib.ptr(B_new), _lib.ptr(stats), N, D, R, P,
+                                   a_v, a_k, b_v, b_k, float(slow_decay), _lib.stream_of(A))
+    _lib.check(rc, "gdnx_gdn3_compact")
+    return A_new, B_new, stats
+
+
+def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
+                   factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None, return_state=False):
+    """GDN3 recurrence with residual window and compaction (gdnx_gdn3_chunk_fwd).
+
+    q, k, v: [B,T,H,D] (shared by the M lanes) or [B,T,H,M,D] (per lane),
+    bf16 or float32, contiguous.  b_gates, w_gates: [B,T,H,M] (scalar per
+    lane) or [B,T,H,M,D] float32.  decay [B,T,H,M] float32.  sketch
+    [B*H*M, b_v*b_k, q] float32.  Returns (y [B,T,H,M,D] in q's dtype,
+    stats [T // K_c, N, 2] float64, state (A, B, U, Vb) or None)."""
+    lib = _lib.load()
+    a_v, a_k, b_v, b_k = factors
+    B, T, H = q.shape[:3]
+    D = q.shape[-1]
+    lanes = 1 if q.dim() == 4 else q.shape[3]
+    _need(q.is_cuda and q.dtype in (torch.bfloat16, torch.float32), "q must be bf16/float32 on the GPU")
+    _need(q.shape == k.shape == v.shape and q.dtype == k.dtype == v.dtype, "q, k, v must match")
+    _need(lanes in (1, M), "q/k/v lane dim must be 1 or M")
+    gate_ch = 1 if b_gates.dim() == 4 else b_gates.shape[-1]
+    _need(b_gates.shape == w_gates.shape and tuple(b_gates.shape[:4]) == (B, T, H, M), "bad gate shapes")
+    _need(tuple(decay.shape) == (B, T, H, M), "decay must be [B,T,H,M]")
+    for t in (q, k, v, b_gates, w_gates, decay, sketch):
+        _need(t.is_contiguous(), "inputs must be contiguous")
+    for t in (b_gates, w_gates, decay, sketch):
+        _need(t.dtype == torch.float32, "gates, decay and sketch must be float32")
+    Kc = P if compact_every is None else int(compact_every)
+    N = B * H * M
+    _need(tuple(sketch.shape) == (N, b_v * b_k, sketch_width(R, a_v * a_k, b_v * b_k)) and sketch.is_cuda,
+          "sketch must be [B*H*M, b_v*b_k, min(R+4, a_v*a_k, b_v*b_k)] on the GPU")
+    dt = _lib.dtype_code(q.dtype)
+    y = torch.empty(B, T, H, M, D, dtype=q.dtype, device=q.device)
+    ws = torch.empty(max(1, lib.gdnx_gdn3_workspace_bytes(B, H, M, D, dt)), dtype=torch.uint8, device=q.device)
+    n_ev = lib.gdnx_gdn3_num_compactions(T, P, Kc)
+    _need(n_ev >= 0, f"compact_every={Kc} must be a positive multiple of P={P}")
+    stats = torch.empty(max(n_ev, 1), N, 2, dtype=torch.float64, device=q.device)
+    state = None
+    ptrs = [None] * 4
+    if return_state:
+        state = (torch.empty(N, R, a_v, a_k, device=q.device), torch.empty(N, R, b_v, b_k, device=q.device),
+                 torch.empty(N, D, P, device=q.device), torch.empty(N, D, P, device=q.device))
+        ptrs = [_lib.ptr(t) for t in state]
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_gdn3_chunk_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), lanes, _lib.ptr(b_gates),
+                                     _lib.ptr(w_gates), gate_ch, _lib.ptr(decay), _lib.ptr(sketch), _lib.ptr(y),
+                                     *ptrs, _lib.ptr(stats) if n_ev > 0 else None, _lib.ptr(ws), B, T, H, M, D,
+                                     R, P, Kc, a_v, a_k, b_v, b_k, float(slow_decay), dt, _lib.stream_of(q))
+    _lib.check(rc, "gdnx_gdn3_chunk_fwd")
+    return y, stats[:n_ev], state

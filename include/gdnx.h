@@ -119,6 +119,77 @@ int gdnx_delta_decode_step(const void* q, const void* k, const void* v,
                            float* state, void* y, int NS, int H, int M, int head_dim,
                            int dtype, void* stream);
 
+
+/* ---- GDN3 Kronecker-residual regime --------------------------------------
+ * State per chain n = (b, h, m):  S = sum_r A_r (x) B_r + U Vb^T  (d_v x d_k),
+ * A [R, a_v, a_k], B [R, b_v, b_k] (a_v b_v = a_k b_k = head_dim), and a
+ * P-slot residual buffer U [d_v, P] (net writes), Vb [d_k, P] (keys).  The
+ * reference layouts of gdn3/gdn3_upgrade.py:444-448.  All state float32. */
+
+/* Bytes of the gdnx_gdn3_chunk_fwd workspace (the materialised Kronecker
+ * matrix, one d x d per chain in the compute dtype); -1 if invalid. */
+long long gdnx_gdn3_workspace_bytes(int B, int H, int M, int head_dim, int dtype);
+
+/* Number of compactions gdnx_gdn3_chunk_fwd runs over T tokens (rows of
+ * comp_stats): T / compact_every; -1 if invalid. */
+int gdnx_gdn3_num_compactions(int T, int P, int compact_every);
+
+/* GDN3 recurrence forward with residual window and periodic compaction.
+ * Replaces GDN3LinearAttn._gdn3_recurrent_state (gdn3/gdn3_upgrade.py:403-531)
+ * with the semantics of its frozen oracle gdn3/_reference_recurrence.py:33-94:
+ * per token gamma = clamp(dec, 0, 1) decays A, B and Vb; h = b.k, u = w.v;
+ * r = u - S h; alpha = alpha(k.h); y = S q + alpha (k.q) r; slot t mod P
+ * receives (alpha r, k); after token t with (t+1) % compact_every == 0 the
+ * compaction of gdnx_gdn3_compact runs (no gradient).  Initial state zero.
+ *   q, k, v      [B, T, H, qkv_lanes, D] io dtype (qkv_lanes 1: shared by
+ *                the M lanes; M: per lane)
+ *   b_gates, w_gates [B, T, H, M, gate_channels] float32 (gate_channels 1:
+ *                a scalar gate per lane; head_dim: per channel)
+ *   decay        [B, T, H, M] float32 multiplicative decay
+ *   sketch       [B*H*M, b_v*b_k, min(R+4, a_v*a_k, b_v*b_k)] float32
+ *   y            [B, T, H, M, D] io dtype
+ *   A_out, B_out, U_out, Vb_out  final state (each may be NULL; any non-NULL
+ *                needs T % P == 0)
+ *   comp_stats   [T / compact_every, B*H*M, 2] float64 (|R_mat|^2, kept
+ *                sigma^2 per chain and compaction) or NULL; the reference's
+ *                comp_err is sum over compactions of max(0, sum_n energy -
+ *                sum_n kept)
+ *   workspace    gdnx_gdn3_workspace_bytes bytes
+ * Supported: head_dim 128 with P = 16; head_dim 64 with P = 16 or 32;
+ * R <= 4; a_v a_k <= 256, b_v b_k <= 256; compact_every a multiple of P. */
+int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, int qkv_lanes,
+                        const float* b_gates, const float* w_gates, int gate_channels,
+                        const float* decay, const float* sketch, void* y, float* A_out,
+                        float* B_out, float* U_out, float* Vb_out, double* comp_stats,
+                        void* workspace, int B, int T, int H, int M, int head_dim, int R, int P,
+                        int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
+                        int dtype, void* stream);
+
+/* Rearrangement-SVD compaction with two-timescale blend, one chain per
+ * block.  Replaces GDN3LinearAttn._compact_vec (gdn3/gdn3_upgrade.py:650-719)
+ * and the 'svd' mode of _compact_fast (:565-624):
+ *   R_mat = sum_r vec(A_r) vec(B_r)^T + rearrange(U Vb^T)   [a_v a_k, b_v b_k]
+ *   randomized range finder (sketch, two power iterations), SVD of the
+ *   projection; A <- s A + (1-s) sigma_r u_r, B <- s B + (1-s) v_r (top R).
+ * Signs: each (u_r, v_r) is flipped so that the largest-magnitude entry of
+ * v_r is positive (first index on ties); the reference keeps whatever its
+ * SVD backend returns.  A, Bf, U, Vb as in the state layout above; sketch
+ * [N, b_v*b_k, q]; comp_stats [N, 2] (|R_mat|^2, kept) or NULL.  U and Vb
+ * are left unchanged (as the reference does). */
+int gdnx_gdn3_compact(const float* A, const float* Bf, const float* U, const float* Vb,
+                      const float* sketch, float* A_out, float* B_out, double* comp_stats, int N,
+                      int head_dim, int R, int P, int a_v, int a_k, int b_v, int b_k,
+                      float slow_decay, void* stream);
+
+/* Read of the Kronecker-residual state, y = S x for C vectors per chain:
+ * vec(sum_r A_r X B_r^T) + U (Vb^T x), X = x viewed as [a_k, b_k].  Replaces
+ * _kron_read_vec (gdn3/gdn3_upgrade.py:626-639) and the Triton
+ * kron_read_chunk_triton (gdn3/triton_kernels.py:146-175).  x, y [N, C, D]
+ * float32; P in 0..64 (U, Vb may be NULL when P = 0). */
+int gdnx_kron_read(const float* A, const float* Bf, const float* U, const float* Vb, const float* x,
+                   float* y, int N, int C, int head_dim, int R, int P, int a_v, int a_k, int b_v,
+                   int b_k, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

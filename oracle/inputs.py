@@ -15,6 +15,12 @@ fixed order and returns CPU tensors; config k uses seed 1000 + k by default.
             clamped <= 0 inside the op; partial RoPE on dims 0..31 of q, k
             (16 half-split pairs x[i] <-> x[16+i], theta_i = t * 1e4^(-i/15)).
   config 2: config 1 plus dO ~ N(0,1) [B,T,H,M,d] in bf16.
+  config 3: long context, B=1, T=32768, H=16, d=128, M=4 lanes sharing q/k/v
+            (bf16, partial RoPE as config 1); per-lane scalar erase / write
+            gates b, w = sigmoid(N(0,1)); multiplicative decay
+            exp(log(1 - tau_m) + N(0, 0.01^2)); 64 key/value pairs (k
+            L2-normalised, v ~ N(0,1)) written at distinct random positions
+            in [0, 4096) and queried (q = k_i) at the last 64 positions.
   config 4: batched decode, 256 sequences x H=16 x 4 lanes x 4 decays.
 """
 from __future__ import annotations
@@ -88,6 +94,34 @@ def config0(seed=1000):
 def config1(seed=1001, T=4096, B=4, H=16, d=128, io_dtype=torch.bfloat16):
     return dense_inputs(B, T, H, d, M=4, seed=seed, decay="tau", rope=True,
                         io_dtype=io_dtype)
+
+
+def config3(seed=1003, T=32768, B=1, H=16, d=128, M=4, n_pairs=64, span=4096,
+            io_dtype=torch.bfloat16):
+    """Config 3 (GDN3 long context with compaction).  Returns dict(q, k, v
+    [B,T,H,d] io_dtype; b, w, dec [B,T,H,M] float32; pos [n_pairs] insert
+    positions; qpos [n_pairs] query positions)."""
+    gen = torch.Generator(device="cpu").manual_seed(seed)
+    q = F.normalize(torch.randn(B, T, H, d, generator=gen), dim=-1)
+    k = F.normalize(torch.randn(B, T, H, d, generator=gen), dim=-1)
+    v = torch.randn(B, T, H, d, generator=gen)
+    b = torch.sigmoid(torch.randn(B, T, H, M, generator=gen))
+    w = torch.sigmoid(torch.randn(B, T, H, M, generator=gen))
+    base = torch.tensor([math.log(1.0 - t) for t in TAUS[:M]], dtype=torch.float32)
+    g = base.view(1, 1, 1, M) + 0.01 * torch.randn(B, T, H, M, generator=gen)
+    dec = torch.exp(g.clamp(max=0.0))
+    n_pairs = min(n_pairs, span, T // 2)
+    pos = torch.randperm(min(span, T), generator=gen)[:n_pairs]
+    kp = F.normalize(torch.randn(n_pairs, B, H, d, generator=gen), dim=-1)
+    vp = torch.randn(n_pairs, B, H, d, generator=gen)
+    qpos = torch.arange(T - n_pairs, T)
+    q, k = partial_rope(q), partial_rope(k)
+    for i in range(n_pairs):
+        k[:, pos[i]] = kp[i]
+        v[:, pos[i]] = vp[i]
+        q[:, qpos[i]] = kp[i]
+    return dict(q=q.to(io_dtype), k=k.to(io_dtype), v=v.to(io_dtype), b=b, w=w, dec=dec,
+                pos=pos, qpos=qpos)
 
 
 def config2(seed=1002, T=4096, B=4, H=16, d=128, io_dtype=torch.bfloat16):

@@ -1,0 +1,206 @@
+"""GDN3 Kronecker-residual regime on the GPU against the CPU oracle.
+
+The oracle (oracle/gdn3.py) restates gdn3/_reference_recurrence.py and
+_compact_vec and is pinned by the reference's golden vectors in
+tests/test_oracle_gdn3.py; here it runs in float64 with sign_mode='canonical',
+the sign convention the HIP compaction implements (the reference keeps its
+SVD backend's signs, which no two backends agree on)."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import gdn3 as og
+from oracle import inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def rel_l2(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def _state(N, R, factors, P, seed, scale=1.0):
+    a_v, a_k, b_v, b_k = factors
+    g = torch.Generator().manual_seed(seed)
+    A = torch.randn(N, R, a_v, a_k, generator=g) * scale
+    Bk = torch.randn(N, R, b_v, b_k, generator=g) * scale
+    U = torch.randn(N, a_v * b_v, P, generator=g)
+    Vb = torch.randn(N, a_k * b_k, P, generator=g)
+    return A, Bk, U, Vb
+
+
+@pytest.mark.parametrize("factors,P", [((16, 16, 8, 8), 16), ((8, 8, 8, 8), 16), ((8, 8, 8, 8), 32)])
+def test_kron_read_matches_oracle(gpu_lib, factors, P):
+    from gdnx_amd import ops
+    print(f"case: kron_read factors={factors} P={P}", flush=True)
+    N, R, C = 3, 4, 5
+    A, Bk, U, Vb = _state(N, R, factors, P, seed=7)
+    D = factors[0] * factors[2]
+    x = torch.randn(N, C, D, generator=torch.Generator().manual_seed(8))
+    y = ops.kron_read(*(t.to(DEV) for t in (A, Bk, U, Vb, x)))
+    ref = torch.stack([og.kron_read(A.double(), Bk.double(), U.double(), Vb.double(), x[:, c].double())
+                       for c in range(C)], 1)
+    assert rel_l2(y, ref) <= 1e-5
+    # P = 0: Kronecker part only
+    y0 = ops.kron_read(A.to(DEV), Bk.to(DEV), torch.zeros(N, D, 0, device=DEV),
+                       torch.zeros(N, D, 0, device=DEV), x[:, 0].contiguous().to(DEV))
+    ref0 = og.kron_read(A.double(), Bk.double(), U[..., :0].double(), Vb[..., :0].double(), x[:, 0].double())
+    assert rel_l2(y0, ref0) <= 1e-5
+
+
+@pytest.mark.parametrize("factors,P,scale", [((16, 16, 8, 8), 16, 1.0), ((16, 16, 8, 8), 16, 0.0),
+                                             ((8, 8, 8, 8), 16, 0.3), ((8, 8, 8, 8), 32, 1.0)])
+def test_compact_matches_oracle(gpu_lib, factors, P, scale):
+    from gdnx_amd import ops
+    print(f"case: compact factors={factors} P={P} scale={scale}", flush=True)
+    N, R = 6, 4
+    A, Bk, U, Vb = _state(N, R, factors, P, seed=11, scale=scale)
+    a_v, a_k, b_v, b_k = factors
+    G = og.reference_sketch(N, b_v * b_k, min(R + 4, a_v * a_k, b_v * b_k))
+    An, Bn, st = ops.gdn3_compact(*(t.to(DEV) for t in (A, Bk, U, Vb, G)), slow_decay=0.97)
+    Ar, Br, err = og.compact(A.double(), Bk.double(), U.double(), Vb.double(), 0.97, G,
+                             sign_mode="canonical")
+    assert rel_l2(An, Ar) <= 1e-5
+    assert rel_l2(Bn, Br) <= 1e-5
+    err_gpu = (st[:, 0].sum() - st[:, 1].sum()).clamp(min=0)
+    energy = st[:, 0].sum().item()
+    assert abs(err_gpu.item() - err.item()) <= 1e-6 * energy
+
+
+def _g3_inputs(B, T, H, M, D, seed, io, gate, per_lane):
+    g = torch.Generator().manual_seed(seed)
+    shape_qkv = (B, T, H, M, D) if per_lane else (B, T, H, D)
+    q = F.normalize(torch.randn(*shape_qkv, generator=g), dim=-1)
+    k = F.normalize(torch.randn(*shape_qkv, generator=g), dim=-1)
+    v = torch.randn(*shape_qkv, generator=g)
+    gshape = (B, T, H, M, D) if gate == "channel" else (B, T, H, M)
+    bg = torch.sigmoid(torch.randn(*gshape, generator=g))
+    wg = torch.sigmoid(torch.randn(*gshape, generator=g))
+    taus = torch.tensor(inputs.TAUS[:M] if M <= 4 else [0.05] * M)
+    dec = torch.exp(torch.log1p(-taus).view(1, 1, 1, M) + 0.01 * torch.randn(B, T, H, M, generator=g))
+    return q.to(io), k.to(io), v.to(io), bg, wg, dec.clamp(max=1.0)
+
+
+def _oracle_args(q, k, v, bg, wg, M):
+    def lanes(x):
+        return x.double() if x.dim() == 5 else x.double().unsqueeze(3).expand(*x.shape[:3], M, x.shape[-1])
+
+    def gates(x, D):
+        return x.double() if x.dim() == 5 else x.double().unsqueeze(-1).expand(*x.shape, D)
+    D = q.shape[-1]
+    return lanes(q), lanes(k), lanes(v), gates(bg, D), gates(wg, D)
+
+
+CASES = [
+    # (B, T, H, M, D, factors, P, Kc, io, gate, per_lane)
+    (1, 64, 2, 2, 128, (16, 16, 8, 8), 16, 16, torch.float32, "lane", False),
+    (1, 64, 2, 2, 128, (16, 16, 8, 8), 16, 32, torch.float32, "channel", True),
+    (2, 48, 1, 2, 128, (16, 16, 8, 8), 16, 16, torch.bfloat16, "lane", False),
+    (1, 96, 1, 4, 128, (16, 16, 8, 8), 16, 48, torch.bfloat16, "channel", True),
+    (1, 64, 2, 1, 64, (8, 8, 8, 8), 16, 16, torch.float32, "lane", False),
+    (1, 64, 1, 2, 64, (8, 8, 8, 8), 32, 32, torch.float32, "channel", False),
+    (1, 64, 1, 2, 64, (8, 8, 8, 8), 32, 32, torch.bfloat16, "lane", True),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"c{i}" for i in range(len(CASES))])
+def test_gdn3_forward_matches_oracle(gpu_lib, case):
+    from gdnx_amd import gdn3
+    B, T, H, M, D, factors, P, Kc, io, gate, per_lane = case
+    print(f"case: gdn3 fwd {case}", flush=True)
+    q, k, v, bg, wg, dec = _g3_inputs(B, T, H, M, D, seed=21, io=io, gate=gate, per_lane=per_lane)
+    N = B * H * M
+    a_v, a_k, b_v, b_k = factors
+    G = og.reference_sketch(N, b_v * b_k, min(4 + 4, a_v * a_k, b_v * b_k))
+    y, (A, Bk, U, Vb), err = gdn3.gdn3_recurrent_state(
+        *(t.to(DEV) for t in (q, k, v, bg, wg, dec)), R=4, P=P, factors=factors, compact_every=Kc,
+        sketch=G.to(DEV), return_state=True)
+    torch.cuda.synchronize()
+    oq, ok, ov, ob, ow = _oracle_args(q, k, v, bg, wg, M)
+    yr, (Ar, Br, Ur, Vr), err_r = og.gdn3_recurrence(oq, ok, ov, ob, ow, dec.double(), R=4, P=P,
+                                                     factors=factors, compact_every=Kc, sketch=G,
+                                                     sign_mode="canonical", return_state=True)
+    tol = 1e-2 if io == torch.bfloat16 else 1e-4
+    assert y.shape == (B, T, H, M, D)
+    assert rel_l2(y, yr) <= tol
+    assert rel_l2(U, Ur) <= tol
+    assert rel_l2(Vb, Vr) <= tol
+    assert rel_l2(A, Ar) <= tol
+    assert rel_l2(Bk, Br) <= tol
+    assert abs(err.item() - err_r.item()) <= tol * max(1.0, abs(err_r.item()))
+
+
+def test_gdn3_forward_ragged_tail(gpu_lib):
+    """T not a multiple of P: the last partial window writes y only."""
+    from gdnx_amd import gdn3
+    print("case: gdn3 ragged tail", flush=True)
+    B, T, H, M, D = 1, 41, 1, 2, 128
+    q, k, v, bg, wg, dec = _g3_inputs(B, T, H, M, D, seed=5, io=torch.float32, gate="lane", per_lane=False)
+    G = og.reference_sketch(B * H * M, 64, 8)
+    y = gdn3.gdn3_recurrent_state(*(t.to(DEV) for t in (q, k, v, bg, wg, dec)), sketch=G.to(DEV))
+    oq, ok, ov, ob, ow = _oracle_args(q, k, v, bg, wg, M)
+    yr = og.gdn3_recurrence(oq, ok, ov, ob, ow, dec.double(), sketch=G, sign_mode="canonical")
+    assert rel_l2(y, yr) <= 1e-4
+
+
+def test_gdn3_reference_layer_call_convention(gpu_lib):
+    """Inputs as GDN3LinearAttn.forward builds them (gdn3/gdn3_upgrade.py:785-837):
+    lane-expanded q/k/v views, per-channel sigmoid gates, compaction every P."""
+    from gdnx_amd import gdn3
+    print("case: gdn3 layer call convention", flush=True)
+    B, T, H, M, D = 1, 80, 2, 4, 128
+    g = torch.Generator().manual_seed(9)
+    q = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
+    k = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
+    v = torch.randn(B, T, H, D, generator=g)
+    bg = torch.sigmoid(torch.randn(B, T, H, M, D, generator=g))
+    wg = torch.sigmoid(torch.randn(B, T, H, M, D, generator=g))
+    dec = torch.rand(B, T, H, M, generator=g).mul(0.2).add(0.79)
+    qe, ke, ve = (x.to(DEV).unsqueeze(3).expand(B, T, H, M, D) for x in (q, k, v))
+    y = gdn3.gdn3_recurrent_state(qe, ke, ve, bg.to(DEV), wg.to(DEV), dec.to(DEV))
+    yr = og.gdn3_recurrence(*(x.double().unsqueeze(3).expand(B, T, H, M, D) for x in (q, k, v)),
+                            bg.double(), wg.double(), dec.double(), sign_mode="canonical")
+    assert rel_l2(y, yr) <= 1e-4
+
+
+def test_gdn3_bridge_to_dense_rule(gpu_lib):
+    """Without compaction or window wrap (P >= T), the Kronecker-residual
+    kernel equals the dense delta-rule kernel (two independent HIP paths)."""
+    from gdnx_amd import gdn3
+    print("case: gdn3 bridge to dense", flush=True)
+    B, T, H, M, D = 1, 16, 2, 4, 128
+    x = inputs.dense_inputs(B, T, H, D, M=M, seed=3, decay="tau", rope=True)
+    dec = torch.exp(x["g"].clamp(max=0))
+    beta = x["beta"]
+    y = gdn3.gdn3_recurrent_state(*(t.to(DEV) for t in (x["q"], x["k"], x["v"], beta, beta, dec)),
+                                  compact_every=10 ** 6 // 16 * 16)
+    y_dense = gdn3.gdn3_scan(x["q"].to(DEV), x["k"].to(DEV), x["v"].to(DEV), beta.to(DEV),
+                             torch.log(dec).to(DEV))
+    assert rel_l2(y, y_dense) <= 1e-4
+
+
+def test_gdn3_config3_full_size(gpu_lib):
+    """Config 3: B=1, T=32768, H=16, 4 lanes, compaction every 2048 tokens,
+    64 key/value pairs inserted early and queried at the end.  The whole
+    layer runs on the GPU; the oracle follows the 4 lanes of head 0."""
+    from gdnx_amd import gdn3
+    print("case: gdn3 config3 full size", flush=True)
+    x = inputs.config3()
+    B, T, H, D = x["q"].shape
+    M = x["b"].shape[-1]
+    N = B * H * M
+    G = og.reference_sketch(N, 64, 8)
+    y = gdn3.gdn3_recurrent_state(*(t.to(DEV) for t in (x["q"], x["k"], x["v"], x["b"], x["w"], x["dec"])),
+                                  compact_every=2048, sketch=G.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.isfinite(y.float()).all()
+    sl = slice(0, 1)
+    args = [t[:, :, sl].double().unsqueeze(3).expand(B, T, 1, M, D) for t in (x["q"], x["k"], x["v"])]
+    gates = [t[:, :, sl].double().unsqueeze(-1).expand(B, T, 1, M, D) for t in (x["b"], x["w"])]
+    yr = og.gdn3_recurrence(*args, *gates, x["dec"][:, :, sl].double(), compact_every=2048,
+                            sketch=G[:M], sign_mode="canonical")
+    assert rel_l2(y[:, :, sl], yr) <= 1e-2
+    qp = x["qpos"]
+    assert rel_l2(y[:, qp][:, :, sl], yr[:, qp]) <= 1e-2
