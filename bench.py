@@ -198,6 +198,98 @@ def bench_decode(args):
     print(json.dumps(line), flush=True)
 
 
+def cpu_baseline_gdn3(T=2048, B=1, H=16, M=4, compact_every=2048):
+    """Time the CPU oracle's sequential GDN3 recurrence (fp32, all chains of
+    the layer batched per token) on the first T tokens of the workload."""
+    import torch
+    from oracle import gdn3 as og, inputs
+    torch.set_num_threads(os.cpu_count() or 1)
+    x = inputs.config3(T=T, B=B, H=H, M=M, span=min(4096, T), n_pairs=16)
+    D = x["q"].shape[-1]
+    args = [t.float().unsqueeze(3).expand(B, T, H, M, D) for t in (x["q"], x["k"], x["v"])]
+    gates = [t.unsqueeze(-1).expand(B, T, H, M, D) for t in (x["b"], x["w"])]
+    t0 = time.perf_counter()
+    og.gdn3_recurrence(*args, *gates, x["dec"], compact_every=compact_every, dtype=torch.float32,
+                       sign_mode="canonical")
+    secs = time.perf_counter() - t0
+    return {
+        "value": B * T / secs,
+        "unit": "tokens/s",
+        "cores": torch.get_num_threads(),
+        "kind": "port",
+        "sample": f"oracle.gdn3.gdn3_recurrence fp32, B={B} T={T} H={H}x{M} lanes d={D}, compaction every "
+                  f"{compact_every} ({secs:.1f} s)",
+    }
+
+
+def bench_gdn3(args, layer_default):
+    """GDN3 Kronecker-residual forward.  longctx: config 3 (B=1, T=32768,
+    H=16, 4 lanes, compaction every 2048 tokens).  gdn3-layer: the reference
+    layer's default regime (compaction every P=16 tokens) at config 1 width
+    (B=4, T=4096, H=16, 4 lanes).  One step = one gdn3_recurrent_state call."""
+    import torch
+    from gdnx_amd import gdn3
+    from oracle import inputs
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    if layer_default:
+        B, T, Kc = 4, 4096, 16
+        x = inputs.config3(T=T, B=B, n_pairs=64, span=T)
+    else:
+        B, T, Kc = 1, 32768, 2048
+        x = inputs.config3()
+    _, _, H, D = x["q"].shape
+    M = x["b"].shape[-1]
+    q, k, v, bg, wg, dec = (x[n].to(dev).contiguous() for n in ("q", "k", "v", "b", "w", "dec"))
+    stream = torch.cuda.current_stream()
+
+    def step():
+        return gdn3.gdn3_recurrent_state(q, k, v, bg, wg, dec, compact_every=Kc)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(args.steps):
+        y = step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    sec = e0.elapsed_time(e1) * 1e-3 / args.steps
+    # algorithmic bytes: q, k, v (bf16, shared by lanes), b, w, decay (fp32 per lane), y (bf16)
+    nbytes = 3 * B * T * H * D * 2 + 3 * B * T * H * M * 4 + B * T * H * M * D * 2
+    achieved = nbytes / sec / 1e9
+    name = "gdn3_fwd_kernel"
+    line = {
+        "metric": ("GDN3 Kronecker-residual layer tokens/s fwd @B=4,T=4096, compaction every 16"
+                   if layer_default else "GDN3 long-context tokens/s fwd @B=1,T=32768, compaction every 2048"),
+        "value": B * T / sec,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": ("GDN3 layer default regime (K_c = P = 16) at config 1 width"
+                                if layer_default else "BASELINE config 3: long context with compaction"),
+                   "batch": B, "seq_len": T, "heads": H, "lanes": M, "head_dim": D, "kron": "4 x (16x16 (x) 8x8)",
+                   "window": 16, "compact_every": Kc, "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": name, "achieved": achieved, "peak": HBM_PEAK / 1e9,
+                     "unit": "GB/s", "frac": achieved * 1e9 / HBM_PEAK, "traffic": measured_traffic(name),
+                     "mean_us": sec * 1e6, "algorithmic_bytes": nbytes,
+                     "note": "one workgroup per chain walks the windows in order: latency-bound"},
+        "finite": bool(torch.isfinite(y.float()).all()),
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_gdn3(T=512 if layer_default else 2048, B=B, compact_every=Kc)
+    print(json.dumps(line), flush=True)
+
+
 def bench_copy(args):
     """Calibration for the HBM traffic counters: a plain device copy of a
     known size (1 GiB read + 1 GiB written per launch).  Prints its own JSON
@@ -230,9 +322,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=10)
-    ap.add_argument("--workload", choices=("train", "decode", "copy"), default="train",
+    ap.add_argument("--workload", choices=("train", "decode", "longctx", "gdn3-layer", "copy"),
+                    default="train",
                     help="train: config 2 scan fwd+bwd (headline); decode: config 4 decode step; "
-                         "copy: 1 GiB device copy used to calibrate the HBM traffic counters")
+                         "longctx: config 3 GDN3 with compaction; gdn3-layer: GDN3 compaction every "
+                         "16 tokens; copy: 1 GiB device copy used to calibrate the HBM traffic counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the recurrence shards by chains with no "
@@ -242,6 +336,8 @@ def main():
         return bench_decode(args)
     if args.workload == "copy":
         return bench_copy(args)
+    if args.workload in ("longctx", "gdn3-layer"):
+        return bench_gdn3(args, layer_default=args.workload == "gdn3-layer")
 
     import torch
     from gdnx_amd import gdn3, ops

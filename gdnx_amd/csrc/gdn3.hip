@@ -39,6 +39,21 @@ constexpr int kMN = 256;    // bound on m = a_v a_k and n = b_v b_k
 constexpr int kAB = 1280;   // bound on R (m + n) for m n = d^2, m, n <= 256
 constexpr int kNT = 256;
 
+// Kronecker geometry of the layer (gdn3/gdn3_upgrade.py:73-77: rank 4,
+// a_k = 16, b_k = 8, so (a_v, a_k, b_v, b_k) = (16, 16, 8, 8) at head dim 128;
+// (8, 8, 8, 8) at head dim 64).  Compile-time, so every loop over the
+// factors unrolls and every index split is a shift.
+template <int D> struct G3C;
+template <> struct G3C<128> { static constexpr int R = 4, av = 16, ak = 16, bv = 8, bk = 8, lbv = 3, lbk = 3; };
+template <> struct G3C<64> { static constexpr int R = 4, av = 8, ak = 8, bv = 8, bk = 8, lbv = 3, lbk = 3; };
+template <int D> struct G3D : G3C<D> {
+  static constexpr int m = G3C<D>::av * G3C<D>::ak, n = G3C<D>::bv * G3C<D>::bk;
+  static constexpr int q = (G3C<D>::R + 4 < m ? (G3C<D>::R + 4 < n ? G3C<D>::R + 4 : n) : (m < n ? m : n));
+  static constexpr int ln = G3C<D>::lbv + G3C<D>::lbk;
+  static_assert((1 << G3C<D>::lbv) == G3C<D>::bv && (1 << G3C<D>::lbk) == G3C<D>::bk && m <= kMN && n <= kMN &&
+                    q <= kQ && G3C<D>::R <= kRMax, "geometry");
+};
+
 __device__ __forceinline__ float stable_alpha_f(float c) {
   // (1 - e^{-c}) / c with its series near 0 (gdn3/gdn3_upgrade.py:641-648)
   if (fabsf(c) < 1e-6f) return 1.f - 0.5f * c + c * c * (1.f / 6.f);
@@ -71,16 +86,16 @@ __device__ __forceinline__ void block_sum(double (&v)[NV], double* red, int tid)
 // LDS of one compaction.
 template <int D, int P>
 struct G3Compact {
-  alignas(16) float rm[D * D + kMN];        // R_mat: m rows of n + 1 floats
-  alignas(16) double y[kMN * kQ];           // range basis, rows of kQ
-  alignas(16) double z[kMN * kQ];           // R_mat^T Y (rows of kQ), then Bm = Q^T R_mat [kQ][n]
-  alignas(16) float gs[kMN * kQ];           // sketch, rows of kQ (zero padded)
-  alignas(16) float ut[P][D + 4];           // window net writes U_p
-  alignas(16) double us[kRMax][kMN];        // leading left singular vectors of R_mat
-  alignas(16) double vs[kRMax][kMN];        // leading right singular vectors
+  alignas(16) float rm[D * D + kMN];      // R_mat: m rows of n + 1 floats
+  alignas(16) double y[kMN * kQ];         // range basis, rows of kQ
+  alignas(16) double z[kMN * kQ];         // R_mat^T Y, then Bm^T = R_mat^T Q (rows of kQ)
+  alignas(16) float gs[kMN * kQ];         // sketch, rows of kQ (zero padded)
+  alignas(16) float ut[P][D + 4];         // window net writes U_p
+  alignas(16) double us[kRMax][kMN];      // leading left singular vectors of R_mat
+  alignas(16) double vs[kRMax][kMN];      // leading right singular vectors
   double red[4 * 64];
-  double lmat[kQ * kQ];         // Cholesky factor L (row-major), L^T = R
-  double ev[kQ * kQ];           // eigenvectors of Bm Bm^T (columns)
+  double rinv[kQ * kQ];                   // R^{-1} of the Cholesky QR (row-major, upper)
+  double ev[kQ * kQ];                     // eigenvectors of Bm Bm^T (columns)
   double lam[kQ];
   double sig[kRMax];
   double amax[4][kRMax];
@@ -88,6 +103,44 @@ struct G3Compact {
   int aidx[4][kRMax];
   int order[kQ];
 };
+
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+// C[M x kQ] = A[M x K] B[K x kQ] on fp64 MFMA (v_mfma_f64_16x16x4f64: lane l
+// supplies A[l%16][l/16] and B[l/16][l%16] and holds D[l/16 + 4e][l%16]).
+// A is R_mat (fp32, row stride ldr) read as is (TRANS = false, M = m, K = n)
+// or transposed (TRANS = true, M = n, K = m); B and C are rows of kQ, B fp32
+// or fp64; the 16-column tile carries kQ = 8 live columns.
+template <bool TRANS, typename BT>
+__device__ __forceinline__ void rm_mfma(const float* rm, int ldr, int M, int K, const BT* b, double* c,
+                                        int tid) {
+  const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, n16 = lane & 15;
+  const bool live = n16 < kQ;
+  const int bcol = live ? n16 : 0;
+  for (int mt = wave; mt < M / 16; mt += 4) {
+    f64x4 acc[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc[u] = (f64x4){0.0, 0.0, 0.0, 0.0};
+    const int row = mt * 16 + n16;
+    // 16 k per step: the 8 operand loads of a step are issued together
+    for (int kb = 0; kb < K; kb += 16) {
+      double a[4], bb[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int k = kb + 4 * u + g;
+        a[u] = TRANS ? rm[k * ldr + row] : rm[row * ldr + k];
+        bb[u] = (double)b[k * kQ + bcol];
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        acc[u] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[u], live ? bb[u] : 0.0, acc[u], 0, 0, 0);
+    }
+    if (live)
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        c[(mt * 16 + g + 4 * e) * kQ + n16] = (acc[0][e] + acc[1][e]) + (acc[2][e] + acc[3][e]);
+  }
+}
 
 // Jacobi rotation zeroing a_pq (Numerical Recipes convention):
 // J[p][p] = J[q][q] = c, J[p][q] = s, J[q][p] = -s.
@@ -101,7 +154,7 @@ __device__ __forceinline__ void jacobi_rot(double app, double aqq, double apq, d
   double t;
   if (fabs(th) > 1e150) t = 0.5 / th;
   else t = (th >= 0.0 ? 1.0 : -1.0) / (fabs(th) + sqrt(th * th + 1.0));
-  c = 1.0 / sqrt(t * t + 1.0);
+  c = rsqrt(t * t + 1.0);
   s = t * c;
 }
 
@@ -112,19 +165,26 @@ __device__ __forceinline__ int rr_partner(int x, int st) {
   return (2 * st - x + 14) % 7;
 }
 
-// Y <- Y R^{-1} with Y^T Y = R^T R (Cholesky QR, applied twice).  Columns
-// whose pivot falls below 1e-24 of the largest diagonal are set to zero.
+// Y <- Y R^{-1} with Y^T Y = R^T R (Cholesky QR, `passes` times: one pass
+// keeps the intermediate power-iteration bases well conditioned, the final
+// basis takes two).  Columns whose pivot falls below 1e-24 of the largest
+// diagonal are set to zero.
 template <int D, int P>
-__device__ void orth_rows(G3Compact<D, P>& cs, int m, int tid) {
+__device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int m, int tid, int passes) {
   const int lane = tid & 63, wave = tid >> 6;
   const int seg = (m + 3) / 4;
-  for (int pass = 0; pass < 2; ++pass) {
+  for (int pass = 0; pass < passes; ++pass) {
     {  // Gram, 4 row segments
       const int i = lane >> 3, j = lane & 7;
       const int r0 = wave * seg, r1 = min(m, r0 + seg);
-      double s = 0.0;
-      for (int row = r0; row < r1; ++row) s += cs.y[row * kQ + i] * cs.y[row * kQ + j];
-      cs.red[wave * 64 + lane] = s;
+      double s0 = 0.0, s1 = 0.0;
+      int row = r0;
+      for (; row + 1 < r1; row += 2) {
+        s0 += cs.y[row * kQ + i] * cs.y[row * kQ + j];
+        s1 += cs.y[(row + 1) * kQ + i] * cs.y[(row + 1) * kQ + j];
+      }
+      if (row < r1) s0 += cs.y[row * kQ + i] * cs.y[row * kQ + j];
+      cs.red[wave * 64 + lane] = s0 + s1;
     }
     __syncthreads();
     if (wave == 0) {
@@ -134,34 +194,48 @@ __device__ void orth_rows(G3Compact<D, P>& cs, int m, int tid) {
 #pragma unroll
       for (int k = 0; k < kQ; ++k) dmax = fmax(dmax, __shfl(a, 9 * k, 64));
       const double tol = dmax * 1e-24;
+      // right-looking Cholesky, lane (i, j) holds entry (i, j); column k
+      // becomes L[:, k] at step k
 #pragma unroll
       for (int k = 0; k < kQ; ++k) {
         const double akk = __shfl(a, 9 * k, 64);
         const double aik = __shfl(a, 8 * i + k, 64);
         const double ajk = __shfl(a, 8 * j + k, 64);
-        const double d = (akk > tol && akk > 0.0) ? sqrt(akk) : 0.0;
-        const double lik = d > 0.0 ? aik / d : 0.0, ljk = d > 0.0 ? ajk / d : 0.0;
+        const double rd = (akk > tol && akk > 0.0) ? rsqrt(akk) : 0.0;
+        const double lik = aik * rd, ljk = ajk * rd;
         if (i > k && j > k) a -= lik * ljk;
-        if (j == k && i >= k) a = (i == k) ? d : lik;  // column k becomes L[:, k]
+        if (j == k && i >= k) a = lik;  // lik = sqrt(akk) on the diagonal
       }
-      cs.lmat[lane] = (j <= i) ? a : 0.0;  // L[i][j]
+      double l = (j <= i) ? a : 0.0;  // L[i][j]
+      // R = L^T is upper triangular; invert it column by column: lane
+      // (i, j) computes Rinv[i][j] = (delta_ij - sum_{i<k<=j} R[i][k] Rinv[k][j]) / R[i][i]
+      // row by row from the bottom, all on shuffles
+      const double rij = __shfl(l, 8 * j + i, 64);  // R[i][j] = L[j][i]
+      const double rii = __shfl(l, 9 * i, 64);
+      const double rdi = rii > 0.0 ? 1.0 / rii : 0.0;
+      double x = (i == j) ? rdi : 0.0;  // row i of Rinv, computed for i = 7 .. 0
+#pragma unroll
+      for (int r = kQ - 1; r >= 0; --r) {
+        // rows > r are final; row r: x[r][j] = (delta - sum_{k>r} R[r][k] x[k][j]) / R[r][r]
+        double acc = 0.0;
+#pragma unroll
+        for (int k = r + 1; k < kQ; ++k) acc += __shfl(rij, 8 * r + k, 64) * __shfl(x, 8 * k + j, 64);
+        if (i == r) x = (j >= r) ? ((j == r ? 1.0 : 0.0) - acc) * rdi : 0.0;
+      }
+      cs.rinv[lane] = x;
     }
     __syncthreads();
     if (tid < m) {
-      double yr[kQ], qn[kQ];
+      double yr[kQ];
 #pragma unroll
       for (int j = 0; j < kQ; ++j) yr[j] = cs.y[tid * kQ + j];
-      // q R = y with R[i][j] = L[j][i]
 #pragma unroll
       for (int j = 0; j < kQ; ++j) {
-        double s = yr[j];
+        double s = 0.0;
 #pragma unroll
-        for (int i = 0; i < j; ++i) s -= qn[i] * cs.lmat[j * kQ + i];
-        const double rjj = cs.lmat[j * kQ + j];
-        qn[j] = rjj > 0.0 ? s / rjj : 0.0;
+        for (int i = 0; i <= j; ++i) s += yr[i] * cs.rinv[i * kQ + j];
+        cs.y[tid * kQ + j] = s;
       }
-#pragma unroll
-      for (int j = 0; j < kQ; ++j) cs.y[tid * kQ + j] = qn[j];
     }
     __syncthreads();
   }
@@ -175,10 +249,12 @@ __device__ void orth_rows(G3Compact<D, P>& cs, int m, int tid) {
 // convention: each (u_r, v_r) pair is flipped so that the largest-magnitude
 // entry of v_r is positive (first index on ties).
 template <int D, int P>
-__device__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float (*vbd)[D + 4], const G3Geom& ge,
-                           float gacc, float sdec, const float* __restrict__ sketch, double* stats, int tid) {
-  const int R = ge.R, m = ge.m, n = ge.n, q = ge.q, av = ge.av, ak = ge.ak, bv = ge.bv, bk = ge.bk;
-  const int ldr = n + 1;
+__device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float (*vbd)[D + 4], float gacc, float sdec,
+                           const float* __restrict__ sketch, double* stats, int tid) {
+  typedef G3D<D> Ge;
+  constexpr int R = Ge::R, m = Ge::m, n = Ge::n, q = Ge::q, ak = Ge::ak, bk = Ge::bk;
+  constexpr int lbv = Ge::lbv, lbk = Ge::lbk, ln = Ge::ln;
+  constexpr int ldr = n + 1;
   float* A = ab;
   float* Bv = ab + R * m;
   const int lane = tid & 63, wave = tid >> 6;
@@ -206,10 +282,10 @@ __device__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float (*vbd)[D 
     }
 #pragma unroll
     for (int a = 0; a < 4; ++a) {
-      const int v = v0 + a, iv = v / bv, jv = v % bv;
+      const int v = v0 + a, iv = v >> lbv, jv = v & (Ge::bv - 1);
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const int k = k0 + b, ik = k / bk, jk = k % bk;
+        const int k = k0 + b, ik = k >> lbk, jk = k & (bk - 1);
         cs.rm[(iv * ak + ik) * ldr + jv * bk + jk] = acc[a][b];
       }
     }
@@ -218,67 +294,48 @@ __device__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float (*vbd)[D 
   // Kronecker part (A, B each decayed by e^{gacc}) and the energy |R_mat|^2
   const float sc2 = expf(2.f * gacc);
   double en[1] = {0.0};
-  for (int e = tid; e < m * n; e += kNT) {
-    const int row = e / n, col = e % n;
-    float s = 0.f;
-    for (int r = 0; r < R; ++r) s += A[r * m + row] * Bv[r * n + col];
-    const float val = cs.rm[row * ldr + col] + sc2 * s;
-    cs.rm[row * ldr + col] = val;
-    en[0] += (double)val * (double)val;
+  {
+    // n <= 256 is a power of two: each thread keeps one column
+    const int col = tid & (n - 1), rstep = kNT >> ln;
+    float bcol[kRMax];
+#pragma unroll
+    for (int r = 0; r < kRMax; ++r) bcol[r] = r < R ? sc2 * Bv[r * n + col] : 0.f;
+    double e0 = 0.0;
+#pragma unroll 4
+    for (int row = tid >> ln; row < m; row += rstep) {
+      float s = cs.rm[row * ldr + col];
+#pragma unroll
+      for (int r = 0; r < kRMax; ++r)
+        if (r < R) s += A[r * m + row] * bcol[r];
+      cs.rm[row * ldr + col] = s;
+      e0 += (double)s * (double)s;
+    }
+    en[0] = e0;
   }
   block_sum<1>(en, cs.red, tid);
 
   // range finder with two power iterations; orthonormalising between the
   // products leaves the final basis unchanged (up to column signs)
-  auto mul_rm = [&](const double* zsrc) {  // Y = R_mat Z (zsrc) or R_mat G (null)
-    for (int row = tid; row < m; row += kNT) {
-      double acc[kQ];
-#pragma unroll
-      for (int j = 0; j < kQ; ++j) acc[j] = 0.0;
-      if (zsrc) {
-        for (int c = 0; c < n; ++c) {
-          const double r = cs.rm[row * ldr + c];
-#pragma unroll
-          for (int j = 0; j < kQ; ++j) acc[j] += r * zsrc[c * kQ + j];
-        }
-      } else {
-        for (int c = 0; c < n; ++c) {
-          const double r = cs.rm[row * ldr + c];
-#pragma unroll
-          for (int j = 0; j < kQ; ++j) acc[j] += r * (double)cs.gs[c * kQ + j];
-        }
-      }
-#pragma unroll
-      for (int j = 0; j < kQ; ++j) cs.y[row * kQ + j] = acc[j];
-    }
-    __syncthreads();
-  };
-  mul_rm(nullptr);
-  orth_rows(cs, m, tid);
-  for (int it = 0; it < 2; ++it) {
-    for (int o = tid; o < n * kQ; o += kNT) {
-      const int c = o % n, j = o / n;
-      double acc = 0.0;
-      for (int row = 0; row < m; ++row) acc += (double)cs.rm[row * ldr + c] * cs.y[row * kQ + j];
-      cs.z[c * kQ + j] = acc;
-    }
-    __syncthreads();
-    mul_rm(cs.z);
-    orth_rows(cs, m, tid);
-  }
-  // Bm = Q^T R_mat  [kQ][n]
-  for (int o = tid; o < n * kQ; o += kNT) {
-    const int c = o % n, j = o / n;
-    double acc = 0.0;
-    for (int row = 0; row < m; ++row) acc += cs.y[row * kQ + j] * (double)cs.rm[row * ldr + c];
-    cs.z[j * n + c] = acc;
-  }
+  rm_mfma<false>(cs.rm, ldr, m, n, cs.gs, cs.y, tid);
   __syncthreads();
-  // eigen-decomposition of W = Bm Bm^T by cyclic Jacobi in wave 0
+  orth_rows(cs, m, tid, 1);
+  for (int it = 0; it < 2; ++it) {
+    rm_mfma<true>(cs.rm, ldr, n, m, cs.y, cs.z, tid);
+    __syncthreads();
+    rm_mfma<false>(cs.rm, ldr, m, n, cs.z, cs.y, tid);
+    __syncthreads();
+    orth_rows(cs, m, tid, it == 1 ? 2 : 1);
+  }
+  // Bm^T = R_mat^T Q  [n][kQ]
+  rm_mfma<true>(cs.rm, ldr, n, m, cs.y, cs.z, tid);
+  __syncthreads();
+  // eigen-decomposition of W = Bm Bm^T by cyclic Jacobi in wave 0: lane
+  // (i, j) holds W[i][j] and V[i][j]; the diagonal lane of each index
+  // computes its pair's rotation, the others read it by shuffle
   if (wave == 0) {
     const int i = lane >> 3, j = lane & 7;
     double a = 0.0;
-    for (int c = 0; c < n; ++c) a += cs.z[i * n + c] * cs.z[j * n + c];
+    for (int c = 0; c < n; ++c) a += cs.z[c * kQ + i] * cs.z[c * kQ + j];
     double vv = (i == j) ? 1.0 : 0.0;
     for (int sweep = 0; sweep < 12; ++sweep) {
       double off = (i != j) ? a * a : 0.0, dia = (i == j) ? a * a : 0.0;
@@ -287,20 +344,18 @@ __device__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float (*vbd)[D 
         off += __shfl_xor(off, o2, 64);
         dia += __shfl_xor(dia, o2, 64);
       }
-      if (!(off > 1e-30 * dia)) break;  // uniform across the wave
+      if (!(off > 1e-28 * dia)) break;  // uniform across the wave
       for (int st = 0; st < 7; ++st) {
+        // rotation of the pair containing index i (meaningful on lane (i, i))
+        const int pp = rr_partner(i, st);
+        const int p0 = min(i, pp), p1 = max(i, pp);
+        double c, sn;
+        jacobi_rot(__shfl(a, 9 * p0, 64), __shfl(a, 9 * p1, 64), __shfl(a, 8 * p0 + p1, 64), c, sn);
+        // J[x][x] = c; J[partner][x] = -s if x < partner else +s
+        const double xs = (i < pp) ? -sn : sn;
+        const double ci = __shfl(c, 9 * i, 64), xi = __shfl(xs, 9 * i, 64);
+        const double cj = __shfl(c, 9 * j, 64), xj = __shfl(xs, 9 * j, 64);
         const int pi = rr_partner(i, st), pj = rr_partner(j, st);
-        double ci, si, cj, sj;
-        {
-          const int p = min(i, pi), qq = max(i, pi);
-          jacobi_rot(__shfl(a, 9 * p, 64), __shfl(a, 9 * qq, 64), __shfl(a, 8 * p + qq, 64), ci, si);
-        }
-        {
-          const int p = min(j, pj), qq = max(j, pj);
-          jacobi_rot(__shfl(a, 9 * p, 64), __shfl(a, 9 * qq, 64), __shfl(a, 8 * p + qq, 64), cj, sj);
-        }
-        // J[i][i] = c; J[pi][i] = -s if i < pi else +s
-        const double xi = (i < pi) ? -si : si, xj = (j < pj) ? -sj : sj;
         const double a_ipj = __shfl(a, 8 * i + pj, 64);
         const double a_pij = __shfl(a, 8 * pi + j, 64);
         const double a_pipj = __shfl(a, 8 * pi + pj, 64);
@@ -340,7 +395,7 @@ __device__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float (*vbd)[D 
       const double sg = cs.sig[r];
       double s = 0.0;
 #pragma unroll
-      for (int j = 0; j < kQ; ++j) s += cs.z[j * n + c] * cs.ev[j * kQ + o];
+      for (int j = 0; j < kQ; ++j) s += cs.z[c * kQ + j] * cs.ev[j * kQ + o];
       cs.vs[r][c] = sg > 0.0 ? s / sg : (c == r ? 1.0 : 0.0);
     }
   __syncthreads();
@@ -421,20 +476,12 @@ __device__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float (*vbd)[D 
 // fused forward
 // ---------------------------------------------------------------------------
 template <typename CT, int D, int P>
-struct G3Chunk {
+struct G3WinSmem {
   alignas(16) CT x[3 * P][D + 8];      // rows: H (0..P-1), Q (P..2P-1), K (2P..3P-1)
   alignas(16) float u[P][D + 4];       // w (.) v
   alignas(16) float kr[2 * P][D + 4];  // Kronecker reads of H and Q
-  alignas(16) float pp[4][P][P + 4];   // H K^T, Q K^T, H Vbd^T, Q Vbd^T -> Lm, Aq, Ho, Qo
-};
-
-template <typename CT, int D, int P>
-struct G3Smem {
-  union {
-    G3Chunk<CT, D, P> c;
-    G3Compact<D, P> k;
-  } w;
-  alignas(16) float ab[kAB];           // A (R x m) | B (R x n)
+  alignas(16) float pp[6][P][P + 4];   // H K^T, Q K^T, H Vbd^T, Q Vbd^T -> Lm, Aq, Ho, Qo; T; scratch
+  alignas(16) CT skron[D][D + 8];      // sum_r A_r (x) B_r, rows v
   alignas(16) float vbd[P][D + 4];     // window keys decayed to the chunk start
   alignas(16) CT vbx[P][D + 8];        // the same in the compute dtype
   float G[P], alpha[P], lg[P], kco[P], qco[P], gam[P], vsc[P];
@@ -464,16 +511,18 @@ __device__ __forceinline__ void store8(float* dst, const float* f) {
   *(f32x4*)(dst + 4) = (f32x4){f[4], f[5], f[6], f[7]};
 }
 
+// Chunks [c0, c1) of one compaction interval (or the tail) for every chain;
+// the window state enters and leaves through the workspace.
 template <typename CT, int D, int P>
-__global__ void __launch_bounds__(kNT) gdn3_fwd_kernel(G3FwdArgs p) {
-  __shared__ G3Smem<CT, D, P> sm;
+__global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
+  __shared__ G3WinSmem<CT, D, P> sm;
   constexpr int DG = D / 8;  // 8-element load units per token row
   constexpr int UNITS = P * DG;
   constexpr int W16 = W16Of<CT>::value;
   constexpr int KS = FragT<CT>::KSTEP;
   typedef typename FragT<CT>::type Frag;
   static_assert(UNITS <= kNT && UNITS % 64 == 0, "one load unit per thread");
-  static_assert(sizeof(G3Smem<CT, D, P>) <= 160 * 1024, "LDS budget");
+  static_assert(sizeof(G3WinSmem<CT, D, P>) <= 160 * 1024, "LDS budget");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, n16 = lane & 15;
@@ -481,8 +530,7 @@ __global__ void __launch_bounds__(kNT) gdn3_fwd_kernel(G3FwdArgs p) {
   const int N = p.B * H * M;
   const int chain = xcd_remap(blockIdx.x, N);
   const int b = chain / (H * M), hm = chain % (H * M), h = hm / M, m = hm % M;
-  const G3Geom ge = p.ge;
-  CT* skron = (CT*)p.skron + (size_t)chain * D * D;
+  typedef G3D<D> Ge;
 
   const bool has_unit = tid < UNITS;
   const int ui = tid / DG, ud = 8 * (tid % DG);
@@ -549,14 +597,14 @@ __global__ void __launch_bounds__(kNT) gdn3_fwd_kernel(G3FwdArgs p) {
       uu[e] = ww[e] * vf[e];
       part += kf[e] * hf[e];
     }
-    store8(&sm.w.c.x[ui][ud], hf);
+    store8(&sm.x[ui][ud], hf);
 #pragma unroll
     for (int w = 0; w < W16; ++w) {
-      *(uint4*)&sm.w.c.x[P + ui][ud + w * (16 / sizeof(CT))] = r.q[w];
-      *(uint4*)&sm.w.c.x[2 * P + ui][ud + w * (16 / sizeof(CT))] = r.k[w];
+      *(uint4*)&sm.x[P + ui][ud + w * (16 / sizeof(CT))] = r.q[w];
+      *(uint4*)&sm.x[2 * P + ui][ud + w * (16 / sizeof(CT))] = r.k[w];
     }
-    *(f32x4*)&sm.w.c.u[ui][ud] = (f32x4){uu[0], uu[1], uu[2], uu[3]};
-    *(f32x4*)&sm.w.c.u[ui][ud + 4] = (f32x4){uu[4], uu[5], uu[6], uu[7]};
+    *(f32x4*)&sm.u[ui][ud] = (f32x4){uu[0], uu[1], uu[2], uu[3]};
+    *(f32x4*)&sm.u[ui][ud + 4] = (f32x4){uu[4], uu[5], uu[6], uu[7]};
 #pragma unroll
     for (int off = 1; off < DG; off <<= 1) part += __shfl_xor(part, off, 64);
     if (tid % DG == 0) {
@@ -565,24 +613,50 @@ __global__ void __launch_bounds__(kNT) gdn3_fwd_kernel(G3FwdArgs p) {
     }
   };
 
-  // state: A = B = 0, empty window
-  for (int e = tid; e < kAB; e += kNT) sm.ab[e] = 0.f;
-  for (int e = tid; e < P * (D + 4); e += kNT) (&sm.vbd[0][0])[e] = 0.f;
-  for (int e = tid; e < P * (D + 8); e += kNT) (&sm.vbx[0][0])[e] = (CT)0.f;
-  float uo[P];
+  // window state: zero for the first interval, else from the workspace
+  constexpr int PT = P / 16, VPW = (D / 16) / 4;
+  f32x4 uo[PT][VPW];
+  float* uw = p.uw + (size_t)chain * P * D;
+  float* vw = p.vw + (size_t)chain * P * D;
+  if (p.first) {
+    for (int e = tid; e < P * (D + 4); e += kNT) (&sm.vbd[0][0])[e] = 0.f;
+    for (int e = tid; e < P * (D + 8); e += kNT) (&sm.vbx[0][0])[e] = (CT)0.f;
 #pragma unroll
-  for (int i = 0; i < P; ++i) uo[i] = 0.f;
+    for (int it = 0; it < PT; ++it)
+#pragma unroll
+      for (int a = 0; a < VPW; ++a) uo[it][a] = zero4();
+  } else {
+    for (int e = tid; e < P * D; e += kNT) {
+      const int j = e / D, d = e % D;
+      const float kv = vw[e];
+      sm.vbd[j][d] = kv;
+      sm.vbx[j][d] = from_f<CT>(kv);
+    }
+#pragma unroll
+    for (int it = 0; it < PT; ++it)
+#pragma unroll
+      for (int a = 0; a < VPW; ++a)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) uo[it][a][s] = uw[(it * 16 + 4 * g4 + s) * D + (wave * VPW + a) * 16 + n16];
+  }
+  const bool live = p.live;
+  if (live) {
+    constexpr int PER = 16 / sizeof(CT);  // elements per 16-byte load
+    const uint4* src = (const uint4*)((const CT*)p.skron + (size_t)chain * D * D);
+    for (int e = tid; e < D * D / PER; e += kNT) {
+      const int v = (e * PER) / D, k = (e * PER) % D;
+      *(uint4*)&sm.skron[v][k] = src[e];
+    }
+  }
   float gacc = 0.f;
-  bool live = false;
-  int event = 0;
 
-  const int nchunks = (T + P - 1) / P;
+#define PP(mat, i, j) sm.pp[mat][i][j]
   Raw raw;
-  fetch(raw, 0);
-  for (int c = 0; c < nchunks; ++c) {
+  fetch(raw, p.c0);
+  for (int c = p.c0; c < p.c1; ++c) {
     __syncthreads();
     commit(raw);
-    if (c + 1 < nchunks) fetch(raw, c + 1);
+    if (c + 1 < p.c1) fetch(raw, c + 1);
     __syncthreads();
     // per-token scalars (wave 0) | grams and Kronecker reads (MFMA)
     if (wave == 0) {
@@ -603,129 +677,197 @@ __global__ void __launch_bounds__(kNT) gdn3_fwd_kernel(G3FwdArgs p) {
       }
     }
     {
-      constexpr int NPT = P / 16;
-      const CT* arows = &sm.w.c.x[(wave & 1) ? P : 0][0];
-      const CT* brows = (wave < 2) ? &sm.w.c.x[2 * P][0] : &sm.vbx[0][0];
+      const CT* arows = &sm.x[(wave & 1) ? P : 0][0];
+      const CT* brows = (wave < 2) ? &sm.x[2 * P][0] : &sm.vbx[0][0];
 #pragma unroll
-      for (int ti = 0; ti < NPT * NPT; ++ti) {
-        const int it = ti / NPT, jt = ti % NPT;
+      for (int ti = 0; ti < PT * PT; ++ti) {
+        const int it = ti / PT, jt = ti % PT;
         const f32x4 acc = tile_nt<CT, D>(arows + (it * 16 + n16) * (D + 8), brows + (jt * 16 + n16) * (D + 8), g4);
 #pragma unroll
-        for (int s = 0; s < 4; ++s) sm.w.c.pp[wave][it * 16 + 4 * g4 + s][jt * 16 + n16] = acc[s];
+        for (int s = 0; s < 4; ++s) sm.pp[wave][it * 16 + 4 * g4 + s][jt * 16 + n16] = acc[s];
       }
     }
     if (live) {
-      constexpr int VPW = (D / 16) / 4, NRT = 2 * P / 16;
+      constexpr int NRT = 2 * P / 16;
 #pragma unroll
       for (int a = 0; a < VPW; ++a) {
         const int vt = wave * VPW + a;
-        const CT* brow = skron + (size_t)(vt * 16 + n16) * D;
         Frag bf[D / KS];
 #pragma unroll
-        for (int kb = 0; kb < D / KS; ++kb) bf[kb] = ld_frag(brow + kb * KS, g4);
+        for (int kb = 0; kb < D / KS; ++kb) bf[kb] = ld_frag(&sm.skron[vt * 16 + n16][kb * KS], g4);
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
           f32x4 acc = zero4();
 #pragma unroll
-          for (int kb = 0; kb < D / KS; ++kb) mma(acc, ld_frag(&sm.w.c.x[rt * 16 + n16][kb * KS], g4), bf[kb]);
+          for (int kb = 0; kb < D / KS; ++kb) mma(acc, ld_frag(&sm.x[rt * 16 + n16][kb * KS], g4), bf[kb]);
 #pragma unroll
-          for (int s = 0; s < 4; ++s) sm.w.c.kr[rt * 16 + 4 * g4 + s][vt * 16 + n16] = acc[s];
+          for (int s = 0; s < 4; ++s) sm.kr[rt * 16 + 4 * g4 + s][vt * 16 + n16] = acc[s];
         }
       }
     }
     __syncthreads();
-    // coefficient matrices
-    for (int e = tid; e < P * P; e += kNT) {
-      const int i = e / P, j = e % P;
-      const float gi = sm.G[i], gj = sm.G[j], al = sm.alpha[i], ga = sm.gam[i];
-      const float dij = (j <= i) ? expf(gi - gj) : 0.f;
-      sm.w.c.pp[0][i][j] = (j < i) ? al * dij * sm.w.c.pp[0][i][j] : 0.f;
-      sm.w.c.pp[1][i][j] = dij * sm.w.c.pp[1][i][j];
-      sm.w.c.pp[2][i][j] = (j >= i) ? al * ga * sm.w.c.pp[2][i][j] : 0.f;
-      sm.w.c.pp[3][i][j] = (j >= i) ? ga * sm.w.c.pp[3][i][j] : 0.f;
+    // coefficient matrices; wave 0 also forms T = (I + Lm)^-1
+    if (wave == 0) {
+      for (int e = lane; e < P * P; e += 64) {
+        const int i = e / P, j = e % P;
+        PP(0, i, j) = (j < i) ? sm.alpha[i] * expf(sm.G[i] - sm.G[j]) * PP(0, i, j) : 0.f;
+      }
+      // Lm was written by other lanes of this wave: order the LDS accesses
+      // (wave-local, no workgroup barrier needed)
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      if constexpr (P == 16) {
+        // Lm is strictly lower (nilpotent): (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8),
+        // factors that commute; squarings and products on fp32 MFMA.  An
+        // accumulator tile is a k-fragment, rows of the squares go through LDS.
+        f32x4 xa, ta;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int i = 4 * g4 + s;
+          xa[s] = PP(0, i, n16);
+          ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
+        }
+        int src = 0;
+#pragma unroll
+        for (int step = 0; step < 3; ++step) {
+          const int dst = step & 1 ? 4 : 5;
+          f32x4 sq = zero4();
+          mma(sq, *(const f32x4*)&PP(src, n16, 4 * g4), xa);  // X^2
+          xa = sq;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) PP(dst, 4 * g4 + s, n16) = sq[s];
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+          mma(ta, *(const f32x4*)&PP(dst, n16, 4 * g4), ta);  // T += X^2 T
+          src = dst;
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+        for (int s = 0; s < 4; ++s) PP(4, 4 * g4 + s, n16) = ta[s];
+      } else {
+        // column j of T by forward substitution (lanes j < P)
+        const int j = lane;
+        float t[P];
+#pragma unroll
+        for (int i = 0; i < P; ++i) {
+          float acc = 0.f;
+#pragma unroll
+          for (int k = 0; k < i; ++k) acc += PP(0, i, k) * t[k];
+          t[i] = (i == j) ? 1.f : ((i < j) ? 0.f : -acc);
+        }
+        if (j < P)
+#pragma unroll
+          for (int i = 0; i < P; ++i) PP(4, i, j) = t[i];
+      }
+    } else {
+      for (int e = tid - 64; e < P * P; e += kNT - 64) {
+        const int i = e / P, j = e % P;
+        const float gi = sm.G[i], al = sm.alpha[i], ga = sm.gam[i];
+        const float dij = (j <= i) ? expf(gi - sm.G[j]) : 0.f;
+        PP(1, i, j) = dij * PP(1, i, j);
+        PP(2, i, j) = (j >= i) ? al * ga * PP(2, i, j) : 0.f;
+        PP(3, i, j) = (j >= i) ? ga * PP(3, i, j) : 0.f;
+      }
     }
     __syncthreads();
-    // net writes by substitution and outputs, one value column per thread
-    if (tid < D) {
-      const int v = tid;
-      float un[P];
+    // window algebra on fp32 MFMA, per wave its VPW value tiles:
+    //   Rhs = alpha u - kco KRh - Ho U_old;  U = T Rhs
+    //   Y   = qco KRq + Qo U_old + Aq U
+    // (an accumulator tile over rows = tokens is directly a k-fragment)
+    {
+      auto arow = [&](int mat, int it, int kt) {
+        return *(const f32x4*)&sm.pp[mat][it * 16 + n16][kt * 16 + 4 * g4];
+      };
 #pragma unroll
-      for (int i = 0; i < P; ++i) {
-        float r = sm.alpha[i] * sm.w.c.u[i][v];
-        if (live) r -= sm.kco[i] * sm.w.c.kr[i][v];
+      for (int a = 0; a < VPW; ++a) {
+        const int v = (wave * VPW + a) * 16 + n16;
+        f32x4 rhs[PT], un[PT];
 #pragma unroll
-        for (int q2 = i; q2 < P; ++q2) r -= sm.w.c.pp[2][i][q2] * uo[q2];
+        for (int it = 0; it < PT; ++it) {
+          f32x4 acc = zero4();
 #pragma unroll
-        for (int j = 0; j < i; ++j) r -= sm.w.c.pp[0][i][j] * un[j];
-        un[i] = r;
+          for (int kt = 0; kt < PT; ++kt) mma(acc, arow(2, it, kt), uo[kt][a]);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int i = it * 16 + 4 * g4 + s;
+            float r = sm.alpha[i] * sm.u[i][v] - acc[s];
+            if (live) r -= sm.kco[i] * sm.kr[i][v];
+            rhs[it][s] = r;
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < PT; ++it) {
+          un[it] = zero4();
+#pragma unroll
+          for (int kt = 0; kt <= it; ++kt) mma(un[it], arow(4, it, kt), rhs[kt]);
+        }
+        CT* yp = (CT*)p.y + y_base + v;
+#pragma unroll
+        for (int it = 0; it < PT; ++it) {
+          f32x4 yv = zero4();
+#pragma unroll
+          for (int kt = 0; kt < PT; ++kt) mma(yv, arow(3, it, kt), uo[kt][a]);
+#pragma unroll
+          for (int kt = 0; kt <= it; ++kt) mma(yv, arow(1, it, kt), un[kt]);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int i = it * 16 + 4 * g4 + s;
+            float out = yv[s];
+            if (live) out += sm.qco[i] * sm.kr[P + i][v];
+            const int t = c * P + i;
+            if (t < T) yp[(size_t)t * y_tok] = from_f<CT>(out);
+          }
+        }
+#pragma unroll
+        for (int it = 0; it < PT; ++it) uo[it][a] = un[it];
       }
-      CT* yp = (CT*)p.y + y_base + v;
-#pragma unroll
-      for (int i = 0; i < P; ++i) {
-        float yv = live ? sm.qco[i] * sm.w.c.kr[P + i][v] : 0.f;
-#pragma unroll
-        for (int q2 = i; q2 < P; ++q2) yv += sm.w.c.pp[3][i][q2] * uo[q2];
-#pragma unroll
-        for (int j = 0; j <= i; ++j) yv += sm.w.c.pp[1][i][j] * un[j];
-        const int t = c * P + i;
-        if (t < T) yp[(size_t)t * y_tok] = from_f<CT>(yv);
-      }
-#pragma unroll
-      for (int i = 0; i < P; ++i) uo[i] = un[i];
     }
     // window keys for the next chunk: k_j decayed to this chunk's end
     for (int e = tid; e < P * D; e += kNT) {
       const int j = e / D, d = e % D;
-      const float kv = to_f(sm.w.c.x[2 * P + j][d]) * sm.vsc[j];
+      const float kv = to_f(sm.x[2 * P + j][d]) * sm.vsc[j];
       sm.vbd[j][d] = kv;
       sm.vbx[j][d] = from_f<CT>(kv);
     }
     gacc += sm.G[P - 1];
-    const int tend = (c + 1) * P;
-    if (tend <= T && tend % p.Kc == 0) {
-      __syncthreads();
-      if (tid < D)
-#pragma unroll
-        for (int i = 0; i < P; ++i) sm.w.k.ut[i][tid] = uo[i];
-      __syncthreads();
-      g3_compact<D, P>(sm.w.k, sm.ab, sm.vbd, ge, gacc, p.sdec, p.sketch + (size_t)chain * ge.n * ge.q,
-                       p.stats ? p.stats + ((size_t)event * N + chain) * 2 : nullptr, tid);
-      // materialise sum_r A_r (x) B_r as a [D][D] (v, k) matrix for the reads
-      const float* Af = sm.ab;
-      const float* Bf = sm.ab + ge.R * ge.m;
-      for (int e = tid; e < D * D; e += kNT) {
-        const int v = e / D, k = e % D;
-        const int iv = v / ge.bv, jv = v % ge.bv, ik = k / ge.bk, jk = k % ge.bk;
-        float s = 0.f;
-        for (int r = 0; r < ge.R; ++r) s += Af[r * ge.m + iv * ge.ak + ik] * Bf[r * ge.n + jv * ge.bk + jk];
-        skron[e] = from_f<CT>(s);
-      }
-      __threadfence_block();
-      gacc = 0.f;
-      live = true;
-      ++event;
-    }
   }
+#undef PP
   __syncthreads();
-  // final state (reference layouts); A, B carry the decay since the last compaction
-  const float dk = expf(gacc);
-  if (p.A_out)
-    for (int e = tid; e < ge.R * ge.m; e += kNT) p.A_out[(size_t)chain * ge.R * ge.m + e] = sm.ab[e] * dk;
-  if (p.B_out)
-    for (int e = tid; e < ge.R * ge.n; e += kNT)
-      p.B_out[(size_t)chain * ge.R * ge.n + e] = sm.ab[ge.R * ge.m + e] * dk;
-  if (p.U_out && tid < D)
+  // window state out (and the final state after the last chunk)
 #pragma unroll
-    for (int i = 0; i < P; ++i) p.U_out[((size_t)chain * D + tid) * P + i] = uo[i];
-  if (p.Vb_out)
-    for (int e = tid; e < D * P; e += kNT) {
-      const int k = e / P, i = e % P;
-      p.Vb_out[(size_t)chain * D * P + e] = sm.vbd[i][k];
-    }
+  for (int a = 0; a < VPW; ++a)
+#pragma unroll
+    for (int it = 0; it < PT; ++it)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = it * 16 + 4 * g4 + s, v = (wave * VPW + a) * 16 + n16;
+        uw[i * D + v] = uo[it][a][s];
+        if (p.last && p.U_out) p.U_out[((size_t)chain * D + v) * P + i] = uo[it][a][s];
+      }
+  for (int e = tid; e < P * D; e += kNT) {
+    const int j = e / D, d = e % D;
+    vw[e] = sm.vbd[j][d];
+    if (p.last && p.Vb_out) p.Vb_out[((size_t)chain * D + d) * P + j] = sm.vbd[j][d];
+  }
+  if (tid == 0) p.gsum[chain] = gacc;
+  if (p.last && !p.complete) {  // no compaction follows: A, B decayed since the last one
+    const float dk = expf(gacc);
+    const float* ab = p.ab + (size_t)chain * Ge::R * (Ge::m + Ge::n);
+    if (p.A_out)
+      for (int e = tid; e < Ge::R * Ge::m; e += kNT) p.A_out[(size_t)chain * Ge::R * Ge::m + e] = ab[e] * dk;
+    if (p.B_out)
+      for (int e = tid; e < Ge::R * Ge::n; e += kNT)
+        p.B_out[(size_t)chain * Ge::R * Ge::n + e] = ab[Ge::R * Ge::m + e] * dk;
+  }
 }
 
 // ---------------------------------------------------------------------------
-// standalone compaction (reference layouts)
+// compaction, one chain per block: the chunked forward's step between
+// intervals and the gdnx_gdn3_compact entry point
 // ---------------------------------------------------------------------------
 template <int D, int P>
 struct G3CompactSmem {
@@ -734,26 +876,52 @@ struct G3CompactSmem {
   alignas(16) float vbd[P][D + 4];
 };
 
-template <int D, int P>
+template <int D, int P, typename CT>
 __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
   __shared__ G3CompactSmem<D, P> sm;
   static_assert(sizeof(G3CompactSmem<D, P>) <= 160 * 1024, "LDS budget");
   const int tid = threadIdx.x;
   const int chain = blockIdx.x;
-  const G3Geom ge = p.ge;
-  const int Rm = ge.R * ge.m, Rn = ge.R * ge.n;
+  typedef G3D<D> Ge;
+  constexpr int Rm = Ge::R * Ge::m, Rn = Ge::R * Ge::n;
   for (int e = tid; e < Rm; e += kNT) sm.ab[e] = p.A[(size_t)chain * Rm + e];
   for (int e = tid; e < Rn; e += kNT) sm.ab[Rm + e] = p.Bf[(size_t)chain * Rn + e];
+  const size_t cb = (size_t)chain * D * P;
   for (int e = tid; e < D * P; e += kNT) {
-    const int d = e / P, i = e % P;
-    sm.k.ut[i][d] = p.U[(size_t)chain * D * P + e];
-    sm.vbd[i][d] = p.Vb[(size_t)chain * D * P + e];
+    const int i = e / D, d = e % D;
+    sm.k.ut[i][d] = p.U[cb + (size_t)i * p.u_sp + (size_t)d * p.u_sd];
+    sm.vbd[i][d] = p.Vb[cb + (size_t)i * p.u_sp + (size_t)d * p.u_sd];
   }
+  const float gacc = p.gsum ? p.gsum[chain] : 0.f;
   __syncthreads();
-  g3_compact<D, P>(sm.k, sm.ab, sm.vbd, ge, 0.f, p.sdec, p.sketch + (size_t)chain * ge.n * ge.q,
+  g3_compact<D, P>(sm.k, sm.ab, sm.vbd, gacc, p.sdec, p.sketch + (size_t)chain * Ge::n * Ge::q,
                    p.stats ? p.stats + (size_t)chain * 2 : nullptr, tid);
-  for (int e = tid; e < Rm; e += kNT) p.A_out[(size_t)chain * Rm + e] = sm.ab[e];
-  for (int e = tid; e < Rn; e += kNT) p.B_out[(size_t)chain * Rn + e] = sm.ab[Rm + e];
+  for (int e = tid; e < Rm; e += kNT) {
+    p.A_out[(size_t)chain * Rm + e] = sm.ab[e];
+    if (p.A_fin) p.A_fin[(size_t)chain * Rm + e] = sm.ab[e];
+  }
+  for (int e = tid; e < Rn; e += kNT) {
+    p.B_out[(size_t)chain * Rn + e] = sm.ab[Rm + e];
+    if (p.B_fin) p.B_fin[(size_t)chain * Rn + e] = sm.ab[Rm + e];
+  }
+  if (p.skron) {  // sum_r A_r (x) B_r as a [D][D] (v, k) matrix for the next interval's reads
+    CT* sk = (CT*)p.skron + (size_t)chain * D * D;
+    const float* Af = sm.ab;
+    const float* Bf = sm.ab + Rm;
+    for (int e = tid; e < D * D; e += kNT) {
+      const int v = e / D, k = e % D;
+      const int iv = v >> Ge::lbv, jv = v & (Ge::bv - 1), ik = k >> Ge::lbk, jk = k & (Ge::bk - 1);
+      float s = 0.f;
+#pragma unroll
+      for (int r = 0; r < Ge::R; ++r) s += Af[r * Ge::m + iv * Ge::ak + ik] * Bf[r * Ge::n + jv * Ge::bk + jk];
+      sk[e] = from_f<CT>(s);
+    }
+  }
+}
+
+__global__ void fill_zero_kernel(float* p, long long n) {
+  for (long long e = (long long)blockIdx.x * blockDim.x + threadIdx.x; e < n; e += (long long)gridDim.x * blockDim.x)
+    p[e] = 0.f;
 }
 
 // ---------------------------------------------------------------------------
@@ -801,39 +969,108 @@ __global__ void __launch_bounds__(kNT) kron_read_kernel(KronReadArgs p) {
   }
 }
 
+template <int D, int P>
+int launch_compact(const G3CompactArgs& a, hipStream_t stream) {
+  if (a.skron && a.skron_dtype == GDNX_DTYPE_BF16)
+    hipLaunchKernelGGL((gdn3_compact_kernel<D, P, bf16>), dim3(a.N), dim3(kNT), 0, stream, a);
+  else
+    hipLaunchKernelGGL((gdn3_compact_kernel<D, P, float>), dim3(a.N), dim3(kNT), 0, stream, a);
+  return check_launch("gdn3_compact_kernel");
+}
+
+int compact_dispatch(const G3CompactArgs& a, hipStream_t stream) {
+  if (a.N == 0) return GDNX_OK;
+  if (a.D == 128 && a.P == 16) return launch_compact<128, 16>(a, stream);
+  if (a.D == 64 && a.P == 16) return launch_compact<64, 16>(a, stream);
+  if (a.D == 64 && a.P == 32) return launch_compact<64, 32>(a, stream);
+  return set_error(GDNX_ERR_SHAPE, "gdn3_compact: unsupported head_dim %d / P %d", a.D, a.P);
+}
+
+inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
 template <typename CT, int D, int P>
-int launch_gdn3_fwd(const G3FwdArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL((gdn3_fwd_kernel<CT, D, P>), dim3(a.B * a.H * a.M), dim3(kNT), 0, stream, a);
-  return check_launch("gdn3_fwd_kernel");
+int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
+  typedef G3D<D> Ge;
+  const int N = a.B * a.H * a.M;
+  char* w = (char*)a.workspace;
+  a.skron = w;
+  w += align256((size_t)N * D * D * sizeof(CT));
+  a.ab = (float*)w;
+  w += align256((size_t)N * Ge::R * (Ge::m + Ge::n) * 4);
+  a.uw = (float*)w;
+  w += align256((size_t)N * P * D * 4);
+  a.vw = (float*)w;
+  w += align256((size_t)N * P * D * 4);
+  a.gsum = (float*)w;
+  const long long nab = (long long)N * Ge::R * (Ge::m + Ge::n);
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((nab + 255) / 256 < 4096 ? (nab + 255) / 256 : 4096)),
+                     dim3(256), 0, stream, a.ab, nab);
+  int rc = check_launch("fill_zero_kernel");
+  if (rc) return rc;
+  const int nch = (a.T + P - 1) / P, per = a.Kc / P;
+  int event = 0;
+  for (int c0 = 0; c0 < nch; c0 += per) {
+    const int c1 = c0 + per < nch ? c0 + per : nch;
+    a.c0 = c0;
+    a.c1 = c1;
+    a.first = c0 == 0;
+    a.live = c0 > 0;
+    a.last = c1 == nch;
+    a.complete = (long long)c1 * P <= a.T && ((long long)c1 * P) % a.Kc == 0;
+    hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P>), dim3(N), dim3(kNT), 0, stream, a);
+    if ((rc = check_launch("gdn3_window_kernel"))) return rc;
+    if (a.complete) {
+      G3CompactArgs ca{};
+      ca.A = a.ab;
+      ca.Bf = a.ab + (size_t)N * Ge::R * Ge::m;
+      ca.U = a.uw;
+      ca.Vb = a.vw;
+      ca.sketch = a.sketch;
+      ca.A_out = a.ab;
+      ca.B_out = a.ab + (size_t)N * Ge::R * Ge::m;
+      ca.stats = a.stats ? a.stats + (size_t)event * N * 2 : nullptr;
+      ca.ge = a.ge;
+      ca.N = N;
+      ca.D = D;
+      ca.P = P;
+      ca.sdec = a.sdec;
+      ca.u_sp = D;
+      ca.u_sd = 1;
+      ca.gsum = a.gsum;
+      ca.skron = a.skron;
+      ca.skron_dtype = a.dtype;
+      ca.A_fin = a.last ? a.A_out : nullptr;
+      ca.B_fin = a.last ? a.B_out : nullptr;
+      if ((rc = compact_dispatch(ca, stream))) return rc;
+      ++event;
+    }
+  }
+  return GDNX_OK;
 }
 
 }  // namespace
 
+size_t gdn3_workspace_bytes(int N, int D, int P, int dtype) {
+  const size_t cb = dtype == GDNX_DTYPE_BF16 ? 2 : 4;
+  const int R = 4, mn = D == 128 ? 256 + 64 : 64 + 64;
+  return align256((size_t)N * D * D * cb) + align256((size_t)N * R * mn * 4) + 2 * align256((size_t)N * P * D * 4) +
+         align256((size_t)N * 4);
+}
+
 int gdn3_fwd_dispatch(const G3FwdArgs& a, hipStream_t stream) {
   if (a.dtype == GDNX_DTYPE_BF16) {
-    if (a.D == 128 && a.P == 16) return launch_gdn3_fwd<bf16, 128, 16>(a, stream);
-    if (a.D == 64 && a.P == 16) return launch_gdn3_fwd<bf16, 64, 16>(a, stream);
-    if (a.D == 64 && a.P == 32) return launch_gdn3_fwd<bf16, 64, 32>(a, stream);
+    if (a.D == 128 && a.P == 16) return run_gdn3_fwd<bf16, 128, 16>(a, stream);
+    if (a.D == 64 && a.P == 16) return run_gdn3_fwd<bf16, 64, 16>(a, stream);
+    if (a.D == 64 && a.P == 32) return run_gdn3_fwd<bf16, 64, 32>(a, stream);
   } else {
-    if (a.D == 128 && a.P == 16) return launch_gdn3_fwd<float, 128, 16>(a, stream);
-    if (a.D == 64 && a.P == 16) return launch_gdn3_fwd<float, 64, 16>(a, stream);
-    if (a.D == 64 && a.P == 32) return launch_gdn3_fwd<float, 64, 32>(a, stream);
+    if (a.D == 128 && a.P == 16) return run_gdn3_fwd<float, 128, 16>(a, stream);
+    if (a.D == 64 && a.P == 16) return run_gdn3_fwd<float, 64, 16>(a, stream);
+    if (a.D == 64 && a.P == 32) return run_gdn3_fwd<float, 64, 32>(a, stream);
   }
   return set_error(GDNX_ERR_SHAPE, "gdn3: unsupported head_dim %d / P %d (128/16, 64/16, 64/32)", a.D, a.P);
 }
 
-int gdn3_compact_dispatch(const G3CompactArgs& a, hipStream_t stream) {
-  if (a.N == 0) return GDNX_OK;
-  if (a.D == 128 && a.P == 16)
-    hipLaunchKernelGGL((gdn3_compact_kernel<128, 16>), dim3(a.N), dim3(kNT), 0, stream, a);
-  else if (a.D == 64 && a.P == 16)
-    hipLaunchKernelGGL((gdn3_compact_kernel<64, 16>), dim3(a.N), dim3(kNT), 0, stream, a);
-  else if (a.D == 64 && a.P == 32)
-    hipLaunchKernelGGL((gdn3_compact_kernel<64, 32>), dim3(a.N), dim3(kNT), 0, stream, a);
-  else
-    return set_error(GDNX_ERR_SHAPE, "gdn3_compact: unsupported head_dim %d / P %d", a.D, a.P);
-  return check_launch("gdn3_compact_kernel");
-}
+int gdn3_compact_dispatch(const G3CompactArgs& a, hipStream_t stream) { return compact_dispatch(a, stream); }
 
 int kron_read_dispatch(const KronReadArgs& a, hipStream_t stream) {
   if ((long long)a.N * a.C == 0) return GDNX_OK;

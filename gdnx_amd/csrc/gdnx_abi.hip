@@ -185,19 +185,37 @@ static int g3_geom(int D, int R, int av, int ak, int bv, int bk, G3Geom& ge) {
   int q = R + 4;
   if (m < q) q = m;
   if (n < q) q = n;
-  ge = G3Geom{R, av, ak, bv, bk, m, n, q};
+  auto lg2 = [](int x) {
+    int l = 0;
+    while ((1 << l) < x) ++l;
+    return l;
+  };
+  ge = G3Geom{R, av, ak, bv, bk, m, n, q, lg2(av), lg2(ak), lg2(bv), lg2(bk)};
   return GDNX_OK;
 }
 
 static bool g3_window_ok(int D, int P) { return (D == 128 && P == 16) || (D == 64 && (P == 16 || P == 32)); }
 
+// the fused forward and the compaction are compiled for the layer's
+// geometry: rank 4 with (16, 16, 8, 8) at head dim 128, (8, 8, 8, 8) at 64
+static int g3_layer_geom(int D, const G3Geom& ge) {
+  const bool ok = ge.R == 4 && ((D == 128 && ge.av == 16 && ge.ak == 16 && ge.bv == 8 && ge.bk == 8) ||
+                                (D == 64 && ge.av == 8 && ge.ak == 8 && ge.bv == 8 && ge.bk == 8));
+  if (!ok)
+    return set_error(GDNX_ERR_SHAPE,
+                     "compiled for R=4 with factors (16,16,8,8) at head_dim 128 or (8,8,8,8) at 64; got R=%d "
+                     "(%d,%d,%d,%d) at %d",
+                     ge.R, ge.av, ge.ak, ge.bv, ge.bk, D);
+  return GDNX_OK;
+}
+
 }  // namespace gdnx
 
-extern "C" long long gdnx_gdn3_workspace_bytes(int B, int H, int M, int head_dim, int dtype) {
-  if (B < 1 || H < 1 || M < 1 || (head_dim != 64 && head_dim != 128) ||
+extern "C" long long gdnx_gdn3_workspace_bytes(int B, int H, int M, int head_dim, int P, int dtype) {
+  if (B < 1 || H < 1 || M < 1 || !g3_window_ok(head_dim, P) ||
       (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16))
     return -1;
-  return (long long)B * H * M * head_dim * head_dim * (dtype == GDNX_DTYPE_BF16 ? 2 : 4);
+  return (long long)gdn3_workspace_bytes(B * H * M, head_dim, P, dtype);
 }
 
 extern "C" int gdnx_gdn3_num_compactions(int T, int P, int compact_every) {
@@ -217,6 +235,7 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
   if (rc) return rc;
   G3Geom ge;
   if ((rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge))) return rc;
+  if ((rc = g3_layer_geom(head_dim, ge))) return rc;
   if (!g3_window_ok(head_dim, P))
     return set_error(GDNX_ERR_SHAPE, "residual window P=%d unsupported for head_dim %d (128: 16; 64: 16, 32)",
                      P, head_dim);
@@ -236,9 +255,33 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
   if ((A_out || B_out || U_out || Vb_out) && T % P != 0)
     return set_error(GDNX_ERR_SHAPE, "final state needs T (%d) to be a multiple of P (%d)", T, P);
   if (T == 0) return GDNX_OK;
-  G3FwdArgs a{q, k, v, b_gates, w_gates, decay, sketch, y, A_out, B_out, U_out, Vb_out, comp_stats,
-              workspace, ge, B, T, H, M, head_dim, P, compact_every, qkv_lanes, gate_channels, dtype,
-              slow_decay};
+  G3FwdArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.bg = b_gates;
+  a.wg = w_gates;
+  a.dec = decay;
+  a.sketch = sketch;
+  a.y = y;
+  a.A_out = A_out;
+  a.B_out = B_out;
+  a.U_out = U_out;
+  a.Vb_out = Vb_out;
+  a.stats = comp_stats;
+  a.workspace = workspace;
+  a.ge = ge;
+  a.B = B;
+  a.T = T;
+  a.H = H;
+  a.M = M;
+  a.D = head_dim;
+  a.P = P;
+  a.Kc = compact_every;
+  a.qkv_lanes = qkv_lanes;
+  a.gate_ch = gate_channels;
+  a.dtype = dtype;
+  a.sdec = slow_decay;
   return gdn3_fwd_dispatch(a, (hipStream_t)stream);
 }
 
@@ -250,6 +293,7 @@ extern "C" int gdnx_gdn3_compact(const float* A, const float* Bf, const float* U
   G3Geom ge;
   int rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge);
   if (rc) return rc;
+  if ((rc = g3_layer_geom(head_dim, ge))) return rc;
   if (N < 0 || N > (1 << 30)) return set_error(GDNX_ERR_SHAPE, "bad chain count N=%d", N);
   if (!g3_window_ok(head_dim, P))
     return set_error(GDNX_ERR_SHAPE, "residual window P=%d unsupported for head_dim %d", P, head_dim);
@@ -257,7 +301,22 @@ extern "C" int gdnx_gdn3_compact(const float* A, const float* Bf, const float* U
     return set_error(GDNX_ERR_ARG, "state, sketch and output pointers must be non-null");
   if (!(slow_decay >= 0.f && slow_decay <= 1.f))
     return set_error(GDNX_ERR_ARG, "slow_decay must lie in [0, 1]");
-  G3CompactArgs a{A, Bf, U, Vb, sketch, A_out, B_out, comp_stats, ge, N, head_dim, P, slow_decay};
+  G3CompactArgs a{};
+  a.A = A;
+  a.Bf = Bf;
+  a.U = U;
+  a.Vb = Vb;
+  a.sketch = sketch;
+  a.A_out = A_out;
+  a.B_out = B_out;
+  a.stats = comp_stats;
+  a.ge = ge;
+  a.N = N;
+  a.D = head_dim;
+  a.P = P;
+  a.sdec = slow_decay;
+  a.u_sp = 1;  // reference layout [d][p]
+  a.u_sd = P;
   return gdn3_compact_dispatch(a, (hipStream_t)stream);
 }
 

@@ -60,8 +60,11 @@ struct DecodeArgs {
 
 // Kronecker-residual geometry: state S = sum_r A_r (x) B_r + U Vb^T with
 // A_r [a_v, a_k], B_r [b_v, b_k]; m = a_v a_k, n = b_v b_k, q = sketch width.
+// The factors of a power-of-two head dim are powers of two; l* are their
+// base-2 logarithms.
 struct G3Geom {
   int R, av, ak, bv, bk, m, n, q;
+  int lav, lak, lbv, lbk;
 };
 
 struct G3FwdArgs {
@@ -78,17 +81,24 @@ struct G3FwdArgs {
   float* U_out;        // [N,D,P] or null
   float* Vb_out;       // [N,D,P] or null
   double* stats;       // [T/Kc, N, 2] (energy, kept) or null
-  void* skron;         // workspace [N, D, D] compute dtype
+  void* workspace;     // carved by the dispatcher into the fields below
   G3Geom ge;
   int B, T, H, M, D, P, Kc, qkv_lanes, gate_ch, dtype;
   float sdec;
+  // per launch (set by the dispatcher)
+  void* skron;         // [N, D, D] compute dtype: sum_r A_r (x) B_r
+  float* ab;           // [N, R (m + n)]: A | B as of the last compaction
+  float* uw;           // [N, P, D] window net writes
+  float* vw;           // [N, P, D] window keys decayed to the window end
+  float* gsum;         // [N] log decay since the last compaction
+  int c0, c1, first, live, last, complete;
 };
 
 struct G3CompactArgs {
   const float* A;
   const float* Bf;
-  const float* U;      // [N, D, P]
-  const float* Vb;     // [N, D, P]
+  const float* U;      // net writes: element (chain, slot p, feature d) at chain*D*P + p*u_sp + d*u_sd
+  const float* Vb;     // keys, same layout
   const float* sketch; // [N, n, q]
   float* A_out;
   float* B_out;
@@ -96,6 +106,12 @@ struct G3CompactArgs {
   G3Geom ge;
   int N, D, P;
   float sdec;
+  int u_sp, u_sd;
+  const float* gsum;   // [N] log decay of A and B since they were stored, or null
+  void* skron;         // materialised [N, D, D] Kronecker matrix out, or null
+  int skron_dtype;
+  float* A_fin;        // optional second copy of the result, or null
+  float* B_fin;
 };
 
 struct KronReadArgs {
@@ -110,6 +126,7 @@ struct KronReadArgs {
 };
 
 int gdn3_fwd_dispatch(const G3FwdArgs& a, hipStream_t stream);
+size_t gdn3_workspace_bytes(int N, int D, int P, int dtype);
 int gdn3_compact_dispatch(const G3CompactArgs& a, hipStream_t stream);
 int kron_read_dispatch(const KronReadArgs& a, hipStream_t stream);
 int decode_dispatch(const DecodeArgs& a, hipStream_t stream);

@@ -278,7 +278,9 @@ def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
           "sketch must be [B*H*M, b_v*b_k, min(R+4, a_v*a_k, b_v*b_k)] on the GPU")
     dt = _lib.dtype_code(q.dtype)
     y = torch.empty(B, T, H, M, D, dtype=q.dtype, device=q.device)
-    ws = torch.empty(max(1, lib.gdnx_gdn3_workspace_bytes(B, H, M, D, dt)), dtype=torch.uint8, device=q.device)
+    nws = lib.gdnx_gdn3_workspace_bytes(B, H, M, D, P, dt)
+    _need(nws > 0, f"unsupported GDN3 shape: head_dim {D}, P {P}")
+    ws = torch.empty(nws, dtype=torch.uint8, device=q.device)
     n_ev = lib.gdnx_gdn3_num_compactions(T, P, Kc)
     _need(n_ev >= 0, f"compact_every={Kc} must be a positive multiple of P={P}")
     stats = torch.empty(max(n_ev, 1), N, 2, dtype=torch.float64, device=q.device)

@@ -126,9 +126,10 @@ int gdnx_delta_decode_step(const void* q, const void* k, const void* v,
  * P-slot residual buffer U [d_v, P] (net writes), Vb [d_k, P] (keys).  The
  * reference layouts of gdn3/gdn3_upgrade.py:444-448.  All state float32. */
 
-/* Bytes of the gdnx_gdn3_chunk_fwd workspace (the materialised Kronecker
- * matrix, one d x d per chain in the compute dtype); -1 if invalid. */
-long long gdnx_gdn3_workspace_bytes(int B, int H, int M, int head_dim, int dtype);
+/* Bytes of the gdnx_gdn3_chunk_fwd workspace: per chain the materialised
+ * Kronecker matrix (d x d, compute dtype), A and B, and the P-slot window
+ * carried between compaction intervals; -1 if invalid. */
+long long gdnx_gdn3_workspace_bytes(int B, int H, int M, int head_dim, int P, int dtype);
 
 /* Number of compactions gdnx_gdn3_chunk_fwd runs over T tokens (rows of
  * comp_stats): T / compact_every; -1 if invalid. */

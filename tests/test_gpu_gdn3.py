@@ -127,8 +127,12 @@ def test_gdn3_forward_matches_oracle(gpu_lib, case):
     assert rel_l2(y, yr) <= tol
     assert rel_l2(U, Ur) <= tol
     assert rel_l2(Vb, Vr) <= tol
-    assert rel_l2(A, Ar) <= tol
-    assert rel_l2(Bk, Br) <= tol
+    # the compacted factors are internal state: each compaction's singular
+    # vectors move by (perturbation of R_mat) / (singular-value gap), so the
+    # fp32 rounding of the window enters A, B amplified; outputs stay at tol
+    state_tol = 1e-2 if io == torch.bfloat16 else 1e-3
+    assert rel_l2(A, Ar) <= state_tol
+    assert rel_l2(Bk, Br) <= state_tol
     assert abs(err.item() - err_r.item()) <= tol * max(1.0, abs(err_r.item()))
 
 
