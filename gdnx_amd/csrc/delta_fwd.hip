@@ -36,6 +36,7 @@ struct alignas(16) FwdSmem {
   float LT[C * Dm::LDT];
   float Td[C * Dm::LDT];
   float G[C], gam[C], dec[C], ae[C], aw[C];
+  float rn[4][C];       // per-wave partial |r_i|^2 (scored forward)
 };
 
 template <typename CT, int D, int C>
@@ -185,6 +186,25 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) mma(Racc[it][vt], a, Sf[kb][vt]);
       }
+    }
+    if (p.r_norm) {  // |r_i| per token: squares over this wave's value columns, then across waves
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) {
+        f32x4 ss = zero4();
+#pragma unroll
+        for (int vt = 0; vt < NVT; ++vt) ss += Racc[it][vt] * Racc[it][vt];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          float x = ss[e];
+#pragma unroll
+          for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off, 64);
+          if (n16 == 0) sm.rn[wave][it * 16 + 4 * g4 + e] = x;
+        }
+      }
+      __syncthreads();
+      if (tid < C && t0 + tid < p.T)
+        p.r_norm[((size_t)(b * p.T + t0 + tid) * p.H + h) * p.M + m] =
+            sqrtf((sm.rn[0][tid] + sm.rn[1][tid]) + (sm.rn[2][tid] + sm.rn[3][tid]));
     }
     // ---- Y = diag(exp G) Q S0 + Aq R, one 16-row block at a time ----
     {

@@ -82,10 +82,10 @@ extern "C" long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, i
   return (long long)B * H * M * nc * head_dim * head_dim * esz;
 }
 
-extern "C" int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v, const float* a_e,
-                                    const float* a_w, const float* log_g, const float* state0, void* y,
-                                    float* state_out, void* chunk_states, int B, int T, int H, int M,
-                                    int head_dim, int chunk, int dtype, void* stream) {
+static int fwd_common(const void* q, const void* k, const void* v, const float* a_e, const float* a_w,
+                      const float* log_g, const float* state0, void* y, float* state_out, void* chunk_states,
+                      float* r_norm, int B, int T, int H, int M, int head_dim, int chunk, int dtype,
+                      void* stream) {
   g_err[0] = 0;
   int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
   if (rc) return rc;
@@ -95,8 +95,25 @@ extern "C" int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v,
   const int C = chunk ? chunk : delta_chunk_size(head_dim, dtype);
   if (!valid_chunk(head_dim, dtype, C)) return set_error(GDNX_ERR_SHAPE, "chunk %d invalid for this dtype", chunk);
   if (T == 0) return GDNX_OK;
-  DeltaArgs a{q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, B, T, H, M, head_dim, C, dtype};
+  DeltaArgs a{q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, B, T, H, M, head_dim, C, dtype, r_norm};
   return delta_fwd_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v, const float* a_e,
+                                    const float* a_w, const float* log_g, const float* state0, void* y,
+                                    float* state_out, void* chunk_states, int B, int T, int H, int M,
+                                    int head_dim, int chunk, int dtype, void* stream) {
+  return fwd_common(q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, nullptr, B, T, H, M, head_dim,
+                    chunk, dtype, stream);
+}
+
+extern "C" int gdnx_delta_chunk_fwd_scored(const void* q, const void* k, const void* v, const float* a_e,
+                                           const float* a_w, const float* log_g, const float* state0, void* y,
+                                           float* state_out, void* chunk_states, float* r_norm, int B, int T,
+                                           int H, int M, int head_dim, int chunk, int dtype, void* stream) {
+  if (!r_norm) return set_error(GDNX_ERR_ARG, "r_norm must be non-null");
+  return fwd_common(q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, r_norm, B, T, H, M, head_dim,
+                    chunk, dtype, stream);
 }
 
 static int bwd_common(const void* q, const void* k, const void* v, const float* a_e, const float* a_w,

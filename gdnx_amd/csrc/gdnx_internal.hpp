@@ -18,6 +18,7 @@ struct DeltaArgs {
   float* s_out;
   void* chunk_states;
   int B, T, H, M, D, C, dtype;
+  float* r_norm;  // [B,T,H,M] |net write| per token, or null
 };
 
 struct DeltaBwdArgs {

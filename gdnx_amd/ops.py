@@ -39,10 +39,12 @@ def chunk_size(head_dim: int, dtype, train: bool = False) -> int:
 
 
 def delta_chunk_fwd(q, k, v, a_e, a_w, log_g, state0=None, *, return_state=False,
-                    save_states=False, chunk=0):
+                    save_states=False, chunk=0, r_norm=None):
     """Forward of the lane-shared decoupled-erase delta rule.
 
-    Returns (y, state_out or None, chunk_states or None)."""
+    r_norm: optional float32 [B,T,H,M] output receiving |r_t| (the norm of
+    each token's net write).  Returns (y, state_out or None, chunk_states or
+    None)."""
     lib = _lib.load()
     B, T, H, M, D = _check_dense(q, k, v, a_e, a_w, log_g)
     code = _lib.dtype_code(q.dtype)
@@ -58,10 +60,18 @@ def delta_chunk_fwd(q, k, v, a_e, a_w, log_g, state0=None, *, return_state=False
         _need(nbytes >= 0, f"invalid chunk {chunk} for {q.dtype}")
         cs = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
-        rc = lib.gdnx_delta_chunk_fwd(
-            _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w), _lib.ptr(log_g),
-            _lib.ptr(state0), _lib.ptr(y), _lib.ptr(s_out), _lib.ptr(cs),
-            B, T, H, M, D, chunk, code, _lib.stream_of(q))
+        if r_norm is None:
+            rc = lib.gdnx_delta_chunk_fwd(
+                _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w), _lib.ptr(log_g),
+                _lib.ptr(state0), _lib.ptr(y), _lib.ptr(s_out), _lib.ptr(cs),
+                B, T, H, M, D, chunk, code, _lib.stream_of(q))
+        else:
+            _need(tuple(r_norm.shape) == (B, T, H, M) and r_norm.dtype == torch.float32
+                  and r_norm.is_contiguous(), "r_norm must be contiguous float32 [B,T,H,M]")
+            rc = lib.gdnx_delta_chunk_fwd_scored(
+                _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w), _lib.ptr(log_g),
+                _lib.ptr(state0), _lib.ptr(y), _lib.ptr(s_out), _lib.ptr(cs), _lib.ptr(r_norm),
+                B, T, H, M, D, chunk, code, _lib.stream_of(q))
     _lib.check(rc, "gdnx_delta_chunk_fwd")
     return y, s_out, cs
 
@@ -93,39 +103,45 @@ def delta_chunk_bwd(q, k, v, a_e, a_w, log_g, dy, chunk_states, chunk, dstate_ou
 
 
 class DeltaRuleFunction(torch.autograd.Function):
-    """y, S_T = lane-shared decoupled-erase delta rule (differentiable in
-    q, k, v, a_e, a_w, log_g and state0)."""
+    """y, S_T (and, when asked, the detached net-write norms |r_t|) of the
+    lane-shared decoupled-erase delta rule, differentiable in q, k, v, a_e,
+    a_w, log_g and state0."""
 
     @staticmethod
-    def forward(ctx, q, k, v, a_e, a_w, log_g, state0=None):
+    def forward(ctx, q, k, v, a_e, a_w, log_g, state0=None, want_rnorm=False):
         train = any(ctx.needs_input_grad)
         D = q.shape[-1]
         chunk = chunk_size(D, q.dtype, train=train)
+        rn = torch.empty(a_e.shape, dtype=torch.float32, device=q.device) if want_rnorm else None
         y, s_out, cs = delta_chunk_fwd(q, k, v, a_e, a_w, log_g, state0, return_state=True,
-                                       save_states=train, chunk=chunk)
+                                       save_states=train, chunk=chunk, r_norm=rn)
         if train:
             ctx.save_for_backward(q, k, v, a_e, a_w, log_g, cs)
             ctx.chunk = chunk
             ctx.has_state0 = state0 is not None
-        return y, s_out
+        if rn is None:
+            return y, s_out
+        ctx.mark_non_differentiable(rn)
+        return y, s_out, rn
 
     @staticmethod
-    def backward(ctx, dy, ds_out):
+    def backward(ctx, dy, ds_out, *unused):
         q, k, v, a_e, a_w, log_g, cs = ctx.saved_tensors
         if dy is None:
             dy = torch.zeros(*a_e.shape, q.shape[-1], dtype=q.dtype, device=q.device)
         dq, dk, dv, dae, daw, dlg, ds0 = delta_chunk_bwd(
             q, k, v, a_e, a_w, log_g, dy, cs, ctx.chunk, dstate_out=ds_out,
             want_dstate0=ctx.has_state0 and ctx.needs_input_grad[6])
-        return dq, dk, dv, dae, daw, dlg, ds0
+        return dq, dk, dv, dae, daw, dlg, ds0, None
 
 
-def delta_rule(q, k, v, a_e, a_w, log_g, state0=None):
-    """Differentiable lane-shared delta rule; returns (y, final_state)."""
+def delta_rule(q, k, v, a_e, a_w, log_g, state0=None, want_rnorm=False):
+    """Differentiable lane-shared delta rule; returns (y, final_state) and,
+    with want_rnorm, the detached per-token net-write norms |r_t| [B,T,H,M]."""
     args = [t.contiguous() for t in (q, k, v)] + [t.float().contiguous() for t in (a_e, a_w, log_g)]
     if state0 is not None:
         state0 = state0.float().contiguous()
-    return DeltaRuleFunction.apply(*args, state0)
+    return DeltaRuleFunction.apply(*args, state0, want_rnorm)
 
 
 def delta_chunk_bwd_stages(q, k, v, a_e, a_w, log_g, dy, chunk_states, chunk, ws=None, out=None):

@@ -70,6 +70,17 @@ int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v,
                          void* chunk_states, int B, int T, int H, int M,
                          int head_dim, int chunk, int dtype, void* stream);
 
+/* gdnx_delta_chunk_fwd that also writes r_norm [B, T, H, M] float32, the
+ * norm of each token's net write |r_t| = |a_w v - a_e S_bar^T k|; the KMD-2
+ * update-norm score is |k_t| |r_t| (scan_with_update_norm,
+ * gdn3/kmd2_fast_scan.py:282; reference score research/kmd2_ablation/
+ * exact_cache.py:1231-1295). */
+int gdnx_delta_chunk_fwd_scored(const void* q, const void* k, const void* v,
+                                const float* a_e, const float* a_w, const float* log_g,
+                                const float* state0, void* y, float* state_out,
+                                void* chunk_states, float* r_norm, int B, int T, int H, int M,
+                                int head_dim, int chunk, int dtype, void* stream);
+
 /* Backward of gdnx_delta_chunk_fwd.  Replaces torch autograd through the
  * reference's chunk graph (gdn3/gdn3_upgrade.py:467-521) and its hand
  * backward of the KMD-2 TRSM (gdn3/kmd2_fast_scan.py:143-160).

@@ -1,0 +1,87 @@
+"""KMD-2 scan / scan_with_update_norm on the GPU against the CPU oracle
+(oracle.delta.kmd2_scan, a restatement of research/kernel_ab/ref_scan.py:24-48
+pinned by the reference's known-answer tests in tests/test_oracle_delta.py).
+
+Decay is per token and head, expanded over dk (the form the HIP kernels
+carry); the reference's interface and argument names are kept
+(tests/ablation/test_fast_scan_api.py:13,30-39 enforce them upstream)."""
+import inspect
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import delta
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def rel_l2(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def _inputs(B, T, H, r_out, d, seed, dtype):
+    g = torch.Generator().manual_seed(seed)
+    q = F.normalize(torch.randn(B, T, H, r_out, d, generator=g), dim=-1) * d ** -0.5 * 4
+    k = F.normalize(torch.randn(B, T, H, d, generator=g), dim=-1)
+    v = torch.randn(B, T, H, d, generator=g)
+    gamma = torch.exp(-0.05 * torch.rand(B, T, H, 1, generator=g))       # per-token decay
+    beta_e = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    beta_w = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    mix = torch.softmax(torch.randn(H, r_out, generator=g), -1) if r_out > 1 else None
+    return q.to(dtype), k.to(dtype), v.to(dtype), gamma, beta_e, beta_w, mix
+
+
+def test_signatures_match_reference(gpu_lib):
+    from gdnx_amd import kmd2
+    for fn in (kmd2.scan, kmd2.scan_with_update_norm):
+        params = list(inspect.signature(fn).parameters.values())
+        assert [p.name for p in params] == ["q", "k", "v", "g", "beta_e", "beta_w", "out_mix"]
+        assert params[-1].default is None
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 1e-2)])
+@pytest.mark.parametrize("r_out", [1, 4])
+def test_scan_and_scores_match_oracle(gpu_lib, dtype, tol, r_out):
+    from gdnx_amd import kmd2
+    print(f"case: kmd2 scan r_out={r_out} {dtype}", flush=True)
+    B, T, H, d = 2, 100, 3, 128
+    q, k, v, gamma, be, bw, mix = _inputs(B, T, H, r_out, d, seed=31, dtype=dtype)
+    g = gamma.expand(B, T, H, d)
+    dev = lambda x: None if x is None else x.to(DEV)
+    y, sc = kmd2.scan_with_update_norm(dev(q), dev(k), dev(v), g.to(DEV), dev(be), dev(bw), dev(mix))
+    y2 = kmd2.scan(dev(q), dev(k), dev(v), g.to(DEV), dev(be), dev(bw), dev(mix))
+    yr, scr = delta.kmd2_scan(q, k, v, g, be, bw, mix, return_scores=True)
+    assert y.shape == (B, T, H, d) and sc.shape == (B, T, H) and sc.dtype == torch.float32
+    assert not sc.requires_grad
+    assert rel_l2(y, yr) <= tol
+    assert rel_l2(y2, yr) <= tol
+    assert rel_l2(sc, scr) <= tol
+
+
+def test_scan_gradients_match_oracle(gpu_lib):
+    from gdnx_amd import kmd2
+    print("case: kmd2 grads", flush=True)
+    B, T, H, r_out, d = 1, 48, 2, 4, 64
+    q, k, v, gamma, be, bw, mix = _inputs(B, T, H, r_out, d, seed=5, dtype=torch.float32)
+    dy = torch.randn(B, T, H, d, generator=torch.Generator().manual_seed(6))
+    leaves = [x.to(DEV).requires_grad_(True) for x in (q, k, v, gamma, be, bw, mix)]
+    y = kmd2.scan(leaves[0], leaves[1], leaves[2], leaves[3].expand(B, T, H, d), leaves[4], leaves[5], leaves[6])
+    grads = torch.autograd.grad(y, leaves, dy.to(DEV))
+    ref = [x.double().requires_grad_(True) for x in (q, k, v, gamma, be, bw, mix)]
+    yr = delta.kmd2_scan(ref[0], ref[1], ref[2], ref[3].expand(B, T, H, d), ref[4], ref[5], ref[6])
+    gref = torch.autograd.grad(yr, ref, dy.double())
+    assert rel_l2(y, yr) <= 1e-4
+    for name, a, b in zip(("q", "k", "v", "gamma", "beta_e", "beta_w", "out_mix"), grads, gref):
+        assert rel_l2(a, b) <= 1e-4, name
+
+
+def test_per_channel_decay_is_refused(gpu_lib):
+    from gdnx_amd import kmd2
+    B, T, H, d = 1, 16, 1, 64
+    q, k, v, gamma, be, bw, _ = _inputs(B, T, H, 1, d, seed=2, dtype=torch.float32)
+    g = torch.rand(B, T, H, d) * 0.1 + 0.9  # varies over dk
+    with pytest.raises(NotImplementedError):
+        kmd2.scan(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), be.to(DEV), bw.to(DEV))
