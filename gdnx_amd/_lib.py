@@ -28,8 +28,9 @@ SIGNATURES = {
     "gdnx_delta_chunk_size": (_c_int, [_c_int, _c_int]),
     "gdnx_delta_train_chunk_size": (_c_int, [_c_int, _c_int]),
     "gdnx_delta_chunk_states_bytes": (_c_ll, [_c_int] * 7),
-    "gdnx_delta_chunk_fwd": (_c_int, [_vp] * 10 + [_c_int] * 7 + [_vp]),
-    "gdnx_delta_chunk_fwd_scored": (_c_int, [_vp] * 11 + [_c_int] * 7 + [_vp]),
+    "gdnx_delta_chunk_fwd": (_c_int, [_vp] * 11 + [_c_int] * 7 + [_vp]),
+    "gdnx_delta_chunk_fwd_scored": (_c_int, [_vp] * 12 + [_c_int] * 7 + [_vp]),
+    "gdnx_delta_fwd_workspace_bytes": (_c_ll, [_c_int] * 7),
     "gdnx_delta_chunk_bwd": (_c_int, [_vp] * 17 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_bwd_state": (_c_int, [_vp] * 8 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_bwd_grads": (_c_int, [_vp] * 15 + [_c_int] * 7 + [_vp]),

@@ -78,6 +78,24 @@ struct ChunkScalars {
   float *G, *gam, *dec, *ae, *aw, *graw;
 };
 
+// Per-chunk operands written by the prep kernel, for NR = chains x chunks
+// records (chain-major, a chain's chunks contiguous): TA, TB, Aq as [C][C]
+// compute-dtype matrices, then gam and dec as [2][C] floats per record.
+template <typename CT>
+struct PrepPtrs {
+  CT* ta;
+  CT* tb;
+  CT* aq;
+  float* sc;
+};
+template <typename CT>
+__host__ __device__ __forceinline__ PrepPtrs<CT> prep_ptrs(void* base, size_t NR, int C) {
+  CT* ta = (CT*)base;
+  CT* tb = ta + NR * C * C;
+  CT* aq = tb + NR * C * C;
+  return PrepPtrs<CT>{ta, tb, aq, (float*)(aq + NR * C * C)};
+}
+
 // Prefetched per-token scalars of one lane (token t0 + lane).
 struct ScalarRegs {
   float ae, aw, g;

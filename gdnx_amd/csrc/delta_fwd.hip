@@ -39,7 +39,64 @@ struct alignas(16) FwdSmem {
   float rn[4][C];       // per-wave partial |r_i|^2 (scored forward)
 };
 
-template <typename CT, int D, int C>
+// One thread's share of a chunk's prepped operands (TA, TB, Aq tiles and the
+// gam / dec scalars), fetched a chunk ahead.
+template <typename CT, int C, int NT>
+struct PrepRegs {
+  static constexpr int PER = 16 / sizeof(CT), NU = C * C / PER, UPT = (NU + NT - 1) / NT;
+  uint4 ta[UPT], tb[UPT], aq[UPT];
+  float gam, dec;
+};
+
+template <typename CT, int C, int NT>
+__device__ __forceinline__ void prep_fetch(PrepRegs<CT, C, NT>& r, const PrepPtrs<CT>& po, size_t rec, int tid) {
+  typedef PrepRegs<CT, C, NT> R;
+  const uint4* ta = (const uint4*)(po.ta + rec * C * C);
+  const uint4* tb = (const uint4*)(po.tb + rec * C * C);
+  const uint4* aq = (const uint4*)(po.aq + rec * C * C);
+#pragma unroll
+  for (int u = 0; u < R::UPT; ++u) {
+    const int e = tid + u * NT;
+    if (e < R::NU) {
+      r.ta[u] = ta[e];
+      r.tb[u] = tb[e];
+      r.aq[u] = aq[e];
+    }
+  }
+  if (tid < C) {
+    r.gam = po.sc[rec * 2 * C + tid];
+    r.dec = po.sc[rec * 2 * C + C + tid];
+  }
+}
+
+// LDS rows of [*][LDC] are 8-byte aligned: 16-byte units go as two halves.
+template <typename CT, int C, int LDC, int NT>
+__device__ __forceinline__ void prep_commit(const PrepRegs<CT, C, NT>& r, CT* ta, CT* tb, CT* aq, float* gam,
+                                            float* dec, int tid) {
+  typedef PrepRegs<CT, C, NT> R;
+#pragma unroll
+  for (int u = 0; u < R::UPT; ++u) {
+    const int e = tid + u * NT;
+    if (e < R::NU) {
+      const int i = (e * R::PER) / C, j = (e * R::PER) % C;
+      uint2* d0 = (uint2*)&ta[i * LDC + j];
+      uint2* d1 = (uint2*)&tb[i * LDC + j];
+      uint2* d2 = (uint2*)&aq[i * LDC + j];
+      d0[0] = make_uint2(r.ta[u].x, r.ta[u].y);
+      d0[1] = make_uint2(r.ta[u].z, r.ta[u].w);
+      d1[0] = make_uint2(r.tb[u].x, r.tb[u].y);
+      d1[1] = make_uint2(r.tb[u].z, r.tb[u].w);
+      d2[0] = make_uint2(r.aq[u].x, r.aq[u].y);
+      d2[1] = make_uint2(r.aq[u].z, r.aq[u].w);
+    }
+  }
+  if (tid < C) {
+    gam[tid] = r.gam;
+    dec[tid] = r.dec;
+  }
+}
+
+template <typename CT, int D, int C, bool PREP>
 __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaArgs p) {
   typedef Dims<CT, D, C> Dm;
   typedef typename Dm::Frag Frag;
@@ -88,10 +145,14 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
 
   TileRegs rq, rk, rv;
   ScalarRegs rsc;
+  PrepRegs<CT, C, NT> rp;
+  const PrepPtrs<CT> po = prep_ptrs<CT>(p.prep, (size_t)nchains * NC, C);
+  const size_t rec0 = (size_t)chain * NC;
   tile_fetch<CT, D, C>(rq, qg, rs, 0, p.T, tid);
   tile_fetch<CT, D, C>(rk, kg, rs, 0, p.T, tid);
   tile_fetch<CT, D, C>(rv, vg, rs, 0, p.T, tid);
-  if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, p.aw + soff, p.g + soff, st, 0, p.T, lane);
+  if constexpr (PREP) prep_fetch<CT, C, NT>(rp, po, rec0, tid);
+  else if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, p.aw + soff, p.g + soff, st, 0, p.T, lane);
 
   for (int c = 0; c < NC; ++c) {
     const int t0 = c * C;
@@ -99,29 +160,33 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
     tile_commit<CT, D, C>(rq, sm.q, nullptr, tid);
     tile_commit<CT, D, C>(rk, sm.k, sm.kt, tid);
     tile_commit<CT, D, C>(rv, nullptr, sm.vt, tid);
-    if (wave == 0) scal_commit<C>(cs, rsc, lane);
+    if constexpr (PREP) prep_commit<CT, C, LDC, NT>(rp, sm.ta, sm.tb, sm.aq, sm.gam, sm.dec, tid);
+    else if (wave == 0) scal_commit<C>(cs, rsc, lane);
     __syncthreads();
     // prefetch the next chunk while this one computes
     if (c + 1 < NC) {
       tile_fetch<CT, D, C>(rq, qg, rs, t0 + C, p.T, tid);
       tile_fetch<CT, D, C>(rk, kg, rs, t0 + C, p.T, tid);
       tile_fetch<CT, D, C>(rv, vg, rs, t0 + C, p.T, tid);
-      if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, p.aw + soff, p.g + soff, st, t0 + C, p.T, lane);
+      if constexpr (PREP) prep_fetch<CT, C, NT>(rp, po, rec0 + c + 1, tid);
+      else if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, p.aw + soff, p.g + soff, st, t0 + C, p.T, lane);
     }
 
-    // ---- grams: L (K K^T) and Aq (Q K^T) ----
-    chunk_grams<CT, D, C>(sm.k, sm.q, sm.L, sm.LT, sm.G, sm.ae, wave, lane,
-                          [&](int i, int j0, const float* v) { st4(&sm.aq[i * LDC + j0], v[0], v[1], v[2], v[3]); });
-    __syncthreads();
-    // ---- T = (I + L)^-1, emitted as TA = T diag(a_w), TB = T diag(a_e exp G) ----
-    invert_unit_lower<C>(
-        sm.L, sm.LT, sm.Td, wave, lane,
-        [&](int j) { return make_float2(sm.aw[j], sm.ae[j] * sm.gam[j]); },
-        [&](int i, int j, float t, float2 f) {
-          sm.ta[i * LDC + j] = from_f<CT>(t * f.x);
-          sm.tb[i * LDC + j] = from_f<CT>(t * f.y);
-        });
-    __syncthreads();
+    if constexpr (!PREP) {
+      // ---- grams: L (K K^T) and Aq (Q K^T) ----
+      chunk_grams<CT, D, C>(sm.k, sm.q, sm.L, sm.LT, sm.G, sm.ae, wave, lane,
+                            [&](int i, int j0, const float* v) { st4(&sm.aq[i * LDC + j0], v[0], v[1], v[2], v[3]); });
+      __syncthreads();
+      // ---- T = (I + L)^-1, emitted as TA = T diag(a_w), TB = T diag(a_e exp G) ----
+      invert_unit_lower<C>(
+          sm.L, sm.LT, sm.Td, wave, lane,
+          [&](int j) { return make_float2(sm.aw[j], sm.ae[j] * sm.gam[j]); },
+          [&](int i, int j, float t, float2 f) {
+            sm.ta[i * LDC + j] = from_f<CT>(t * f.x);
+            sm.tb[i * LDC + j] = from_f<CT>(t * f.y);
+          });
+      __syncthreads();
+    }
 
     // ---- -Wm (rows i, cols d) via Wm^T = K^T TB^T; this wave's d tiles ----
 #pragma unroll
@@ -287,7 +352,13 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
 template <typename CT, int D, int C>
 static int launch_fwd(const DeltaArgs& a, hipStream_t stream) {
   const int nblocks = a.B * a.H * a.M;
-  hipLaunchKernelGGL((delta_fwd_kernel<CT, D, C>), dim3(nblocks), dim3(Dims<CT, D, C>::NT), 0, stream, a);
+  if (a.prep) {
+    int rc = delta_prep_dispatch(a, stream);
+    if (rc) return rc;
+    hipLaunchKernelGGL((delta_fwd_kernel<CT, D, C, true>), dim3(nblocks), dim3(Dims<CT, D, C>::NT), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((delta_fwd_kernel<CT, D, C, false>), dim3(nblocks), dim3(Dims<CT, D, C>::NT), 0, stream, a);
+  }
   return check_launch("delta_fwd_kernel");
 }
 

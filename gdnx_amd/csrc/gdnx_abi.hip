@@ -84,36 +84,48 @@ extern "C" long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, i
 
 static int fwd_common(const void* q, const void* k, const void* v, const float* a_e, const float* a_w,
                       const float* log_g, const float* state0, void* y, float* state_out, void* chunk_states,
-                      float* r_norm, int B, int T, int H, int M, int head_dim, int chunk, int dtype,
-                      void* stream) {
+                      float* r_norm, void* workspace, int B, int T, int H, int M, int head_dim, int chunk,
+                      int dtype, void* stream) {
   g_err[0] = 0;
   int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
   if (rc) return rc;
   if (!a_e || !a_w || !log_g || !y) return set_error(GDNX_ERR_ARG, "a_e, a_w, log_g, y must be non-null");
   if (chunk_states && ((uintptr_t)chunk_states & 15u))
     return set_error(GDNX_ERR_ARG, "chunk_states must be 16-byte aligned");
+  if (workspace && ((uintptr_t)workspace & 15u)) return set_error(GDNX_ERR_ARG, "workspace must be 16-byte aligned");
   const int C = chunk ? chunk : delta_chunk_size(head_dim, dtype);
   if (!valid_chunk(head_dim, dtype, C)) return set_error(GDNX_ERR_SHAPE, "chunk %d invalid for this dtype", chunk);
   if (T == 0) return GDNX_OK;
-  DeltaArgs a{q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, B, T, H, M, head_dim, C, dtype, r_norm};
+  DeltaArgs a{q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, B, T, H, M, head_dim, C, dtype,
+              r_norm, workspace};
   return delta_fwd_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" long long gdnx_delta_fwd_workspace_bytes(int B, int T, int H, int M, int head_dim, int chunk,
+                                                    int dtype) {
+  const int C = chunk ? chunk : delta_chunk_size(head_dim, dtype);
+  if (C == 0 || !valid_chunk(head_dim, dtype, C) || B < 1 || T < 0 || H < 1 || M < 1 ||
+      (head_dim != 64 && head_dim != 128))
+    return -1;
+  return (long long)delta_prep_bytes(B * H * M, T, C, dtype);
 }
 
 extern "C" int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v, const float* a_e,
                                     const float* a_w, const float* log_g, const float* state0, void* y,
-                                    float* state_out, void* chunk_states, int B, int T, int H, int M,
-                                    int head_dim, int chunk, int dtype, void* stream) {
-  return fwd_common(q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, nullptr, B, T, H, M, head_dim,
-                    chunk, dtype, stream);
+                                    float* state_out, void* chunk_states, void* workspace, int B, int T, int H,
+                                    int M, int head_dim, int chunk, int dtype, void* stream) {
+  return fwd_common(q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, nullptr, workspace, B, T, H, M,
+                    head_dim, chunk, dtype, stream);
 }
 
 extern "C" int gdnx_delta_chunk_fwd_scored(const void* q, const void* k, const void* v, const float* a_e,
                                            const float* a_w, const float* log_g, const float* state0, void* y,
-                                           float* state_out, void* chunk_states, float* r_norm, int B, int T,
-                                           int H, int M, int head_dim, int chunk, int dtype, void* stream) {
+                                           float* state_out, void* chunk_states, float* r_norm, void* workspace,
+                                           int B, int T, int H, int M, int head_dim, int chunk, int dtype,
+                                           void* stream) {
   if (!r_norm) return set_error(GDNX_ERR_ARG, "r_norm must be non-null");
-  return fwd_common(q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, r_norm, B, T, H, M, head_dim,
-                    chunk, dtype, stream);
+  return fwd_common(q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, r_norm, workspace, B, T, H, M,
+                    head_dim, chunk, dtype, stream);
 }
 
 static int bwd_common(const void* q, const void* k, const void* v, const float* a_e, const float* a_w,

@@ -19,6 +19,7 @@ struct DeltaArgs {
   void* chunk_states;
   int B, T, H, M, D, C, dtype;
   float* r_norm;  // [B,T,H,M] |net write| per token, or null
+  void* prep;     // per-chunk operands (delta_prep_kernel), or null: computed in the scan
 };
 
 struct DeltaBwdArgs {
@@ -132,6 +133,8 @@ int gdn3_compact_dispatch(const G3CompactArgs& a, hipStream_t stream);
 int kron_read_dispatch(const KronReadArgs& a, hipStream_t stream);
 int decode_dispatch(const DecodeArgs& a, hipStream_t stream);
 int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);
+int delta_prep_dispatch(const DeltaArgs& a, hipStream_t stream);
+size_t delta_prep_bytes(int nchains, int T, int C, int dtype);
 int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream);
 int delta_chunk_size(int D, int dtype);
 int delta_train_chunk_size(int D, int dtype);

@@ -39,11 +39,14 @@ def chunk_size(head_dim: int, dtype, train: bool = False) -> int:
 
 
 def delta_chunk_fwd(q, k, v, a_e, a_w, log_g, state0=None, *, return_state=False,
-                    save_states=False, chunk=0, r_norm=None):
+                    save_states=False, chunk=0, r_norm=None, two_pass=False):
     """Forward of the lane-shared decoupled-erase delta rule.
 
     r_norm: optional float32 [B,T,H,M] output receiving |r_t| (the norm of
-    each token's net write).  Returns (y, state_out or None, chunk_states or
+    each token's net write).  two_pass: compute the state-independent chunk
+    operands in a parallel pass first (needs a workspace) instead of inside
+    the sequential scan; off by default because on config 2 the extra pass
+    (253 us) costs more than it saves in the scan (787 -> 589 us).  Returns (y, state_out or None, chunk_states or
     None)."""
     lib = _lib.load()
     B, T, H, M, D = _check_dense(q, k, v, a_e, a_w, log_g)
@@ -59,18 +62,23 @@ def delta_chunk_fwd(q, k, v, a_e, a_w, log_g, state0=None, *, return_state=False
         nbytes = lib.gdnx_delta_chunk_states_bytes(B, T, H, M, D, chunk, code)
         _need(nbytes >= 0, f"invalid chunk {chunk} for {q.dtype}")
         cs = torch.empty(max(nbytes, 16), dtype=torch.uint8, device=dev)
+    ws = None
+    if two_pass:
+        nws = lib.gdnx_delta_fwd_workspace_bytes(B, T, H, M, D, chunk, code)
+        _need(nws >= 0, f"invalid chunk {chunk} for {q.dtype}")
+        ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=dev)
     with torch.cuda.device(dev):
         if r_norm is None:
             rc = lib.gdnx_delta_chunk_fwd(
                 _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w), _lib.ptr(log_g),
-                _lib.ptr(state0), _lib.ptr(y), _lib.ptr(s_out), _lib.ptr(cs),
+                _lib.ptr(state0), _lib.ptr(y), _lib.ptr(s_out), _lib.ptr(cs), _lib.ptr(ws),
                 B, T, H, M, D, chunk, code, _lib.stream_of(q))
         else:
             _need(tuple(r_norm.shape) == (B, T, H, M) and r_norm.dtype == torch.float32
                   and r_norm.is_contiguous(), "r_norm must be contiguous float32 [B,T,H,M]")
             rc = lib.gdnx_delta_chunk_fwd_scored(
                 _lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w), _lib.ptr(log_g),
-                _lib.ptr(state0), _lib.ptr(y), _lib.ptr(s_out), _lib.ptr(cs), _lib.ptr(r_norm),
+                _lib.ptr(state0), _lib.ptr(y), _lib.ptr(s_out), _lib.ptr(cs), _lib.ptr(r_norm), _lib.ptr(ws),
                 B, T, H, M, D, chunk, code, _lib.stream_of(q))
     _lib.check(rc, "gdnx_delta_chunk_fwd")
     return y, s_out, cs

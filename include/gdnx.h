@@ -61,14 +61,24 @@ long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim
  *   research/kernel_ab/ref_scan.py:24-48) with scalar decay.
  * Per chain (b, h, m), token t:  S <- exp(min(g,0)) S;  r = a_w v - a_e S^T k;
  *   S <- S + k r^T;  y = S^T q.
- * state0 / state_out / chunk_states may be NULL.  chunk_states (size from
- * gdnx_delta_chunk_states_bytes) receives the state entering every chunk,
- * which gdnx_delta_chunk_bwd needs. */
+ * state0 / state_out / chunk_states / workspace may be NULL.  chunk_states
+ * (size from gdnx_delta_chunk_states_bytes) receives the state entering
+ * every chunk, which gdnx_delta_chunk_bwd needs; workspace (size from
+ * gdnx_delta_fwd_workspace_bytes) enables the two-pass form. */
 int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v,
                          const float* a_e, const float* a_w, const float* log_g,
                          const float* state0, void* y, float* state_out,
-                         void* chunk_states, int B, int T, int H, int M,
+                         void* chunk_states, void* workspace, int B, int T, int H, int M,
                          int head_dim, int chunk, int dtype, void* stream);
+
+/* Bytes of the optional forward workspace (-1 if invalid).  With a
+ * workspace the forward first computes every chunk's state-independent
+ * operands (T diag(a_w), T diag(a_e exp G), the decay-masked Q K^T and the
+ * decay factors) in one fully parallel pass, and the sequential scan only
+ * carries the state; with workspace = NULL the scan computes them itself.
+ * Results are the same up to rounding order. */
+long long gdnx_delta_fwd_workspace_bytes(int B, int T, int H, int M, int head_dim, int chunk,
+                                         int dtype);
 
 /* gdnx_delta_chunk_fwd that also writes r_norm [B, T, H, M] float32, the
  * norm of each token's net write |r_t| = |a_w v - a_e S_bar^T k|; the KMD-2
@@ -78,8 +88,8 @@ int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v,
 int gdnx_delta_chunk_fwd_scored(const void* q, const void* k, const void* v,
                                 const float* a_e, const float* a_w, const float* log_g,
                                 const float* state0, void* y, float* state_out,
-                                void* chunk_states, float* r_norm, int B, int T, int H, int M,
-                                int head_dim, int chunk, int dtype, void* stream);
+                                void* chunk_states, float* r_norm, void* workspace, int B, int T,
+                                int H, int M, int head_dim, int chunk, int dtype, void* stream);
 
 /* Backward of gdnx_delta_chunk_fwd.  Replaces torch autograd through the
  * reference's chunk graph (gdn3/gdn3_upgrade.py:467-521) and its hand

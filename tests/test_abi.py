@@ -44,13 +44,13 @@ def test_abi_version_and_sizes():
 
 
 def _fwd(lib, **over):
-    args = dict(q=16, k=16, v=16, ae=32, aw=32, g=32, s0=None, y=64, so=None, cs=None,
+    args = dict(q=16, k=16, v=16, ae=32, aw=32, g=32, s0=None, y=64, so=None, cs=None, ws=None,
                 B=1, T=8, H=1, M=1, D=64, C=0, dt=_lib.DTYPE_F32)
     args.update(over)
     vp = lambda x: None if x is None else ctypes.c_void_p(x)
     return lib.gdnx_delta_chunk_fwd(vp(args["q"]), vp(args["k"]), vp(args["v"]), vp(args["ae"]),
                                     vp(args["aw"]), vp(args["g"]), vp(args["s0"]), vp(args["y"]),
-                                    vp(args["so"]), vp(args["cs"]), args["B"], args["T"], args["H"],
+                                    vp(args["so"]), vp(args["cs"]), vp(args["ws"]), args["B"], args["T"], args["H"],
                                     args["M"], args["D"], args["C"], args["dt"], None)
 
 

@@ -103,3 +103,27 @@ def test_config1_full_size_against_oracle_subset(gpu_lib):
     sub = {n: x[n][:1, :, :2] for n in ("q", "k", "v", "beta", "g")}
     ref = _oracle(sub, torch.bfloat16)
     assert rel_l2(y[:1, :, :2], ref) <= 1e-2
+
+
+@pytest.mark.parametrize("dtype,chunk", [(torch.bfloat16, 64), (torch.bfloat16, 32), (torch.float32, 32),
+                                         (torch.float32, 16)])
+def test_two_pass_equals_single_pass(gpu_lib, dtype, chunk):
+    """The parallel operand pass + lean scan gives the single-kernel result
+    (same arithmetic; only the rounding order of the stored operands differs)."""
+    from gdnx_amd import ops
+    print(f"case: two-pass vs single-pass {dtype} C={chunk}", flush=True)
+    x = inputs.dense_inputs(2, 200, 3, 128, M=4, seed=77, decay="tau", rope=True, io_dtype=dtype)
+    a = delta.gdn3_dense_coeffs(x["k"].double(), x["beta"].double()).float()
+    s0 = torch.randn(2, 3, 4, 128, 128, generator=torch.Generator().manual_seed(1)) * 0.02
+    args = [t.to("cuda:0") for t in (x["q"], x["k"], x["v"], a, a, x["g"])]
+    rn1 = torch.empty(2, 200, 3, 4, device="cuda:0")
+    rn2 = torch.empty_like(rn1)
+    y1, s1, c1 = ops.delta_chunk_fwd(*args, s0.to("cuda:0"), return_state=True, save_states=True, chunk=chunk,
+                                     r_norm=rn1, two_pass=True)
+    y2, s2, c2 = ops.delta_chunk_fwd(*args, s0.to("cuda:0"), return_state=True, save_states=True, chunk=chunk,
+                                     r_norm=rn2, two_pass=False)
+    torch.cuda.synchronize()
+    tol = 1e-5 if dtype == torch.float32 else 2e-3
+    assert rel_l2(y1, y2) <= tol
+    assert rel_l2(s1, s2) <= tol
+    assert rel_l2(rn1, rn2) <= tol
