@@ -16,13 +16,14 @@
 // Two kernels:
 //   delta_bwd_state_kernel  one workgroup per chain, chunks in reverse order,
 //     carries dS in registers (value columns split over the waves, like the
-//     forward's S) and stashes dS_C of every chunk.  Needs no S0.
+//     forward's S) and stashes dS_C and dB of every chunk.  Needs no S0.
 //   delta_bwd_grads_kernel  one workgroup per (batch, head, chunk), looping
-//     over the M lanes that share q/k/v: recomputes T, R, dR, dB from the two
-//     state stashes, runs the contractions over value columns with S0 / dS
-//     staged in LDS, and sums the lanes' dq/dk/dv in registers (fixed order,
-//     no atomics), so the lane expansion of the reference
-//     (gdn3/gdn3_upgrade.py:785-787) costs no extra memory traffic.
+//     over the M lanes that share q/k/v: reads S0, R (forward stash) and
+//     dS_C, dB (reverse-scan stash), runs the contractions over value columns
+//     with the state rows read straight from the row-major stashes, and sums
+//     the lanes' dq/dk/dv in registers (fixed order, no atomics), so the lane
+//     expansion of the reference (gdn3/gdn3_upgrade.py:785-787) costs no
+//     extra memory traffic.
 // The reference differentiates its chunk graph with torch autograd
 // (gdn3/gdn3_upgrade.py:467-521) and its KMD-2 TRSM by hand
 // (gdn3/kmd2_fast_scan.py:143-160).
@@ -130,7 +131,7 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_bwd_state_kernel(D
         [&](int i, int j, float t, int) { sm.tt[j * LDC + i] = from_f<CT>(t); });
     __syncthreads();
 
-    // stash dS_C of this chunk
+    // stash dS_C of this chunk (stash_state layout)
     Frag dSf[NDT / TPS][NVT];
 #pragma unroll
     for (int kb = 0; kb < NDT / TPS; ++kb)
@@ -182,6 +183,15 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_bwd_state_kernel(D
             mma(acc, ld_frag(&sm.tt[(it * 16 + n16) * LDC + kb * KS], g4), dRf[kb][vt]);
           dB[it][vt] = acc;
         }
+      {  // stash dB after all state gradients: raw accumulator tiles (stash_tiles layout)
+        CT* bst = (CT*)p.ds_stash + (size_t)nchains * NC * D * D + ((size_t)chain * NC + c) * (C * D);
+#pragma unroll
+        for (int it = 0; it < NCT; ++it)
+#pragma unroll
+          for (int vt = 0; vt < NVT; ++vt)
+            st4(bst + ((it * NDT + wave * NVT + vt) * 64 + lane) * 4, dB[it][vt][0], dB[it][vt][1],
+                dB[it][vt][2], dB[it][vt][3]);
+      }
       // fragments of -diag(a_e exp G) dB over k = i
 #pragma unroll
       for (int kb = 0; kb < NCT / TPS; ++kb) {
@@ -236,63 +246,102 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_bwd_state_kernel(D
 // ---------------------------------------------------------------------------
 // per-chunk gradients, lanes summed in-block
 // ---------------------------------------------------------------------------
+#ifndef GDNX_GRADS_WAVES_PER_EU
+#define GDNX_GRADS_WAVES_PER_EU 2
+#endif
+// One wave per 16-column tile of the key dimension (D/16 waves): each wave
+// keeps only its own rows of S0 / dS_C and its dq/dk/dv tiles in registers.
+template <typename CT, int D>
+struct GradDims {
+  static constexpr int NW = D / 16;
+  static constexpr int NT = 64 * NW;
+};
+
+// Small per-lane arrays, double-buffered by lane parity: the per-token
+// scalar gradients of lane m are formed (by one wave) while the workgroup
+// computes lane m + 1.
+template <int C, int NW, int NP>
+struct alignas(16) GradLaneBuf {
+  float G[C], gam[C], dec[C], ae[C], aw[C], graw[C];
+  float red[4][NW][C];   // [q.P1, k.P2, k.P3, v.dB][wave][row] partial sums
+  float tri[NP][3][16];  // per tile pair: row sums and column sums of Xm, row sums of AE
+  float scal[NW];        // per-wave partial <dS_C, S0>
+};
+
 template <typename CT, int D, int C>
 struct alignas(16) BwdGradSmem {
   typedef Dims<CT, D, C> Dm;
-  static constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF;
+  static constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF, NW = GradDims<CT, D>::NW;
+  static constexpr int NP = (C / 16) * (C / 16 + 1) / 2;  // lower 16x16 tile pairs
   CT q[C * LDD];
   CT k[C * LDD];
-  CT dy[C * LDD];
-  CT qt[D * LDC];
-  CT kt[D * LDC];
-  CT vt[D * LDC];
+  CT v[C * LDD];
   float KK[C * LDF];   // k_i . k_j  (lower)
   float QK[C * LDF];   // q_i . k_j  (lower incl. diagonal)
   float dQK[C * LDF];  // sum over lanes of dL/d(q_i.k_j)
   float dKK[C * LDF];  // sum over lanes of dL/d(k_i.k_j), j < i
-  float G[C], gam[C], dec[C], ae[C], aw[C], graw[C], tmp[C];
-  float red[4][Dm::NW][C];  // [quantity][wave][row] partial sums
-  float scal[Dm::NW];
   union alignas(16) U {
-    struct alignas(16) {
-      CT dyt[D * LDC];
-      CT ta[C * LDC], tb[C * LDC], tt[C * LDC], aqt[C * LDC];
-      CT wm[C * LDD];
-      float L[C * LDF], LT[C * Dm::LDT], Td[C * Dm::LDT];
-    } p1;
-    struct alignas(16) {
-      CT X[D * LDD];   // S0, then dS  ([d][v], value-contiguous)
-      CT R[C * LDD];
-      CT dB[C * LDD];
-      float Xm[C * LDF], AE[C * LDF];
-    } p2;
-    struct alignas(16) {
-      CT A1[C * LDC], A2[C * LDC], A3[C * LDC];
-    } p3;
+    struct alignas(16) {  // one lane's chunk tiles, rows [token][v]
+      CT dy[C * LDD], R[C * LDD], dB[C * LDD];
+    } ln;
+    struct alignas(16) {  // after the lanes: transposed Q, K and the gram-gradient factors
+      CT qt[D * LDC], kt[D * LDC], A1[C * LDC], A2[C * LDC], A3[C * LDC];
+    } fin;
   } u;
+  GradLaneBuf<C, NW, NP> lb[2];
 };
 
-// sum a per-row value over the 16 lanes that share g (lane bits 0..3)
-__device__ __forceinline__ float sum16(float x) {
-  x += __shfl_xor(x, 1, 64);
-  x += __shfl_xor(x, 2, 64);
-  x += __shfl_xor(x, 4, 64);
-  x += __shfl_xor(x, 8, 64);
+// The value unchanged, but opaque to the optimizer.
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
   return x;
 }
 
+// One lane's inputs to the gradient kernel, fetched a lane ahead: this
+// wave's rows of S0 and dS_C (raw tiles, one per 16 value columns), this
+// thread's share of the R / dB tiles and of dY, and (scalar wave) the
+// per-token coefficients.
 template <typename CT, int D, int C>
-__global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_bwd_grads_kernel(DeltaBwdArgs p) {
+struct GradPrefetch {
+  typedef typename Vec4T<CT>::type V4;
+  static constexpr int NDT = D / 16, NCT = C / 16, NT = GradDims<CT, D>::NT;
+  static constexpr int VEC = 16 / sizeof(CT);
+  static constexpr int NDY = (C * D / VEC + NT - 1) / NT;
+  V4 s[NDT], ds[NDT];
+  V4 r[NCT], db[NCT];
+  uint4 dy[NDY];
+  ScalarRegs sc;
+};
+
+// Gradient kernel: one workgroup per (batch, head, chunk), looping over the M
+// lanes that share q/k/v.  Per lane it reads the stashed S0, R (forward) and
+// dS_C, dB (reverse scan) and forms, wave w owning key columns d and value
+// columns v in [16w, 16w+16):
+//   P1 = dY S0^T, P2 = dB S0^T, P3 = R dS_C^T      (S0 / dS_C rows of this wave
+//                                                   as fragments over k = v)
+//   dQ += diag(exp G) P1,  dK += diag(dec) P3 - diag(a_e exp G) P2
+//   dV += diag(a_w) dB,    da_w = rowsum(dB o V)
+//   dAq = dY R^T (j<=i),   dL = -dB R^T (j<i)  -> dQK, dKK (lane sums) and the
+//   per-token decay / erase gradients.
+// After the lanes: dQ += dQK K, dK += dQK^T Q + (dKK + dKK^T) K.
+template <typename CT, int D, int C>
+__global__ void __launch_bounds__((GradDims<CT, D>::NT)) __attribute__((amdgpu_waves_per_eu(GDNX_GRADS_WAVES_PER_EU)))
+delta_bwd_grads_kernel(DeltaBwdArgs p) {
   typedef Dims<CT, D, C> Dm;
   typedef typename Dm::Frag Frag;
-  constexpr int KS = Dm::KS, TPS = Dm::TPS, NDT = Dm::NDT, NCT = Dm::NCT, VS = Dm::VS, NVT = Dm::NVT;
-  constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF, NT = Dm::NT, NW = Dm::NW;
-  constexpr int DPW = Dm::DPW;  // d tiles per wave in the d-partitioned phase
-  constexpr int FL = FragLen<CT>::value;
-  __shared__ BwdGradSmem<CT, D, C> sm;
+  typedef BwdGradSmem<CT, D, C> Sm;
+  typedef GradPrefetch<CT, D, C> Pf;
+  typedef GradLaneBuf<C, GradDims<CT, D>::NW, Sm::NP> LB;
+  typedef typename Vec4T<CT>::type V4;
+  constexpr int KS = Dm::KS, TPS = Dm::TPS, NCT = Dm::NCT, NDT = Dm::NDT, LDD = Dm::LDD, LDC = Dm::LDC;
+  constexpr int LDF = Dm::LDF, NW = GradDims<CT, D>::NW, NT = GradDims<CT, D>::NT, NKV = D / KS, NP = Sm::NP;
+  constexpr int SW = NW - 1;  // the wave that forms the per-token scalar gradients
+  __shared__ Sm sm;
 
-  const int tid = threadIdx.x;
+  const int tid0 = threadIdx.x;
+  const int tid = tid0;
   const int wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
+  const int dcol = wave * 16 + n16;  // this lane's key (and value) column
   const int NC = (p.T + C - 1) / C;
   const int nblocks = p.B * p.H * NC;
   const int blk = xcd_remap(blockIdx.x, nblocks);
@@ -300,387 +349,292 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_bwd_grads_kernel(D
   const int h = (blk / NC) % p.H;
   const int b = blk / (NC * p.H);
   const int t0 = c * C;
-  const int v0 = wave * VS;
   const size_t rs = (size_t)p.H * D;
   const size_t qoff = ((size_t)b * p.T * p.H + h) * D;
   const size_t rsy = (size_t)p.H * p.M * D;
   const size_t st = (size_t)p.H * p.M;
+  const size_t nrec = (size_t)p.B * p.H * p.M * NC;
+  const CT* s_st = (const CT*)p.s_stash;     // [nrec] stash_state: states entering each chunk
+  const CT* r_st = s_st + nrec * D * D;      // [nrec] stash_tiles: net writes R
+  const CT* ds_st = (const CT*)p.ds_stash;   // [nrec] stash_state: state gradients at chunk ends
+  const CT* db_st = ds_st + nrec * D * D;    // [nrec] stash_tiles: dB
 
-  stage_tile<CT, D, C>((const CT*)p.q + qoff, rs, t0, p.T, sm.q, sm.qt, tid);
-  stage_tile<CT, D, C>((const CT*)p.k + qoff, rs, t0, p.T, sm.k, sm.kt, tid);
-  stage_tile<CT, D, C>((const CT*)p.v + qoff, rs, t0, p.T, nullptr, sm.vt, tid);
+  // ---- fetch lane mm's inputs into registers (issued a lane ahead) ----
+  auto prefetch = [&](Pf& f, int mm, int tid_) {
+    const int lane_ = tid_ & 63;
+    const size_t rec = (((size_t)b * p.H + h) * p.M + mm) * NC + c;
+#pragma unroll
+    for (int V = 0; V < NDT; ++V) {
+      f.s[V] = *(const V4*)stash_state_ptr<CT, D, C>(s_st + rec * D * D, wave, V, lane_);
+      f.ds[V] = *(const V4*)stash_state_ptr<CT, D, C>(ds_st + rec * D * D, wave, V, lane_);
+    }
+#pragma unroll
+    for (int it = 0; it < NCT; ++it) {  // tile (it, V = wave) of R and dB
+      const size_t off = rec * C * D + (size_t)((it * NDT + wave) * 64 + lane_) * 4;
+      f.r[it] = *(const V4*)(r_st + off);
+      f.db[it] = *(const V4*)(db_st + off);
+    }
+    const CT* yb = (const CT*)p.dy + (((size_t)b * p.T * p.H + h) * p.M + mm) * D + (size_t)t0 * rsy;
+#pragma unroll
+    for (int j = 0; j < Pf::NDY; ++j) {
+      const int qv = tid_ + j * NT, row = qv / (D / Pf::VEC), col = (qv % (D / Pf::VEC)) * Pf::VEC;
+      f.dy[j] = (qv < C * D / Pf::VEC && t0 + row < p.T) ? *(const uint4*)(yb + (unsigned)row * (unsigned)rsy + col)
+                                                          : make_uint4(0, 0, 0, 0);
+    }
+    if (wave == SW) {
+      const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + mm;
+      scal_fetch<C>(f.sc, p.ae + soff, p.aw + soff, p.g + soff, st, t0, p.T, lane_);
+    }
+  };
+
+  // ---- per-token scalar gradients of lane mm (wave SW, one token per lane) ----
+  auto scalar_grads = [&](int mm, const LB& q) {
+    float dGi = 0.f, daei = 0.f, dawi = 0.f, r3d = 0.f;
+    if (lane < C) {
+      const int i = lane, ib = i >> 4, ir = i & 15;
+      float r1 = 0.f, r2 = 0.f, r3 = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) {
+        r1 += q.red[0][w][i];
+        r2 += q.red[1][w][i];
+        r3 += q.red[2][w][i];
+        dawi += q.red[3][w][i];
+      }
+      dGi = q.gam[i] * r1 - q.gam[i] * q.ae[i] * r2 - q.dec[i] * r3;
+      daei = -q.gam[i] * r2;
+      // Xm row i lives in tiles (ib, jt <= ib); column i in tiles (it >= ib, ib)
+      for (int jt = 0; jt <= ib; ++jt) {
+        const int pr = ib * (ib + 1) / 2 + jt;
+        dGi += q.tri[pr][0][ir];
+        daei += q.tri[pr][2][ir];
+      }
+      for (int it = ib; it < NCT; ++it) dGi -= q.tri[it * (it + 1) / 2 + ib][1][ir];
+      r3d = q.dec[i] * r3;
+    }
+    // chunk-end decay: d/dG_last of gamma_C <dS_C, S0> and of the dec factors
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) r3d += __shfl_xor(r3d, off, 64);
+    if (lane == C - 1) {
+      float s = 0.f;
+#pragma unroll
+      for (int w = 0; w < NW; ++w) s += q.scal[w];
+      dGi += s * q.gam[C - 1] + r3d;
+    }
+    // dg_s = sum_{i >= s} dG_i (suffix sum within the chunk)
+    float sfx = (lane < C) ? dGi : 0.f;
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      const float o = __shfl_down(sfx, off, 64);
+      if (lane + off < 64) sfx += o;
+    }
+    const int t = t0 + lane;
+    if (lane < C && t < p.T) {
+      const size_t si = ((size_t)(b * p.T + t) * p.H + h) * p.M + mm;
+      const float raw = q.graw[lane];
+      p.dae[si] = daei;
+      p.daw[si] = dawi;
+      p.dg[si] = (raw <= 0.f && raw >= kLogFloor) ? sfx : 0.f;
+    }
+  };
+
+  Pf pf;
+  prefetch(pf, 0, tid);
+  stage_tile<CT, D, C, NT>((const CT*)p.q + qoff, rs, t0, p.T, sm.q, nullptr, tid);
+  stage_tile<CT, D, C, NT>((const CT*)p.k + qoff, rs, t0, p.T, sm.k, nullptr, tid);
+  stage_tile<CT, D, C, NT>((const CT*)p.v + qoff, rs, t0, p.T, sm.v, nullptr, tid);
   for (int i = tid; i < C * LDF; i += NT) {
     sm.dQK[i] = 0.f;
     sm.dKK[i] = 0.f;
   }
-  f32x4 dQacc[NCT][DPW], dKacc[NCT][DPW], dVacc[NCT][NVT];
+  f32x4 dQacc[NCT], dKacc[NCT], dVacc[NCT];
 #pragma unroll
-  for (int it = 0; it < NCT; ++it) {
-#pragma unroll
-    for (int dd = 0; dd < DPW; ++dd) dQacc[it][dd] = dKacc[it][dd] = zero4();
-#pragma unroll
-    for (int vt = 0; vt < NVT; ++vt) dVacc[it][vt] = zero4();
-  }
+  for (int it = 0; it < NCT; ++it) dQacc[it] = dKacc[it] = dVacc[it] = zero4();
   __syncthreads();
-  {  // raw grams (shared by the lanes)
-    constexpr int NP = NCT * (NCT + 1) / 2;
-    for (int task = wave; task < 2 * NP; task += NW) {
-      int it, jt;
-      tri_pair(task >> 1, it, jt);
-      const CT* arow = ((task & 1) == 0) ? &sm.k[(it * 16 + n16) * LDD] : &sm.q[(it * 16 + n16) * LDD];
-      const f32x4 acc = tile_nt<CT, D>(arow, &sm.k[(jt * 16 + n16) * LDD], g4);
-      float* dst = ((task & 1) == 0) ? sm.KK : sm.QK;
+  // raw grams (shared by the lanes)
+  for (int task = wave; task < 2 * NP; task += NW) {
+    int it, jt;
+    tri_pair(task >> 1, it, jt);
+    const CT* arow = ((task & 1) == 0) ? &sm.k[(it * 16 + n16) * LDD] : &sm.q[(it * 16 + n16) * LDD];
+    const f32x4 acc = tile_nt<CT, D>(arow, &sm.k[(jt * 16 + n16) * LDD], g4);
+    float* dst = ((task & 1) == 0) ? sm.KK : sm.QK;
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) dst[(it * 16 + 4 * g4 + ii) * LDF + jt * 16 + n16] = acc[ii];
-    }
+    for (int ii = 0; ii < 4; ++ii) dst[(it * 16 + 4 * g4 + ii) * LDF + jt * 16 + n16] = acc[ii];
   }
-  __syncthreads();
 
   for (int m = 0; m < p.M; ++m) {
-    const size_t chain = ((size_t)b * p.H + h) * p.M + m;
-    const size_t yoff = (((size_t)b * p.T * p.H + h) * p.M + m) * D;
-    const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + m;
-    const ChunkScalars cs{sm.G, sm.gam, sm.dec, sm.ae, sm.aw, sm.graw};
-    stage_tile<CT, D, C>((const CT*)p.dy + yoff, rsy, t0, p.T, sm.dy, sm.u.p1.dyt, tid);
-    if (wave == 0) prep_scalars<C>(cs, p.ae + soff, p.aw + soff, p.g + soff, st, t0, p.T, lane);
-    __syncthreads();
-    for (int idx = tid; idx < C * C; idx += NT) {
-      const int i = idx / C, j = idx % C;
-      const float Dij = (j <= i) ? __expf(sm.G[i] - sm.G[j]) : 0.f;
-      const float Lij = (j < i) ? Dij * sm.ae[i] * sm.KK[i * LDF + j] : 0.f;
-      sm.u.p1.L[i * LDF + j] = Lij;
-      if ((i >> 4) == (j >> 4)) sm.u.p1.LT[j * Dm::LDT + (i & 15)] = Lij;
-      sm.u.p1.aqt[j * LDC + i] = from_f<CT>((j <= i) ? Dij * sm.QK[i * LDF + j] : 0.f);
-      sm.u.p1.ta[i * LDC + j] = from_f<CT>(0.f);
-      sm.u.p1.tb[i * LDC + j] = from_f<CT>(0.f);
-      sm.u.p1.tt[i * LDC + j] = from_f<CT>(0.f);
-    }
-    __syncthreads();
-    invert_unit_lower<C>(
-        sm.u.p1.L, sm.u.p1.LT, sm.u.p1.Td, wave, lane,
-        [&](int j) { return make_float2(sm.aw[j], sm.ae[j] * sm.gam[j]); },
-        [&](int i, int j, float t, float2 f) {
-          sm.u.p1.ta[i * LDC + j] = from_f<CT>(t * f.x);
-          sm.u.p1.tb[i * LDC + j] = from_f<CT>(t * f.y);
-          sm.u.p1.tt[j * LDC + i] = from_f<CT>(t);
-        });
-    __syncthreads();
+    // per-thread indices re-derived each lane: keeps the compiler from hoisting
+    // (and spilling) every loop-invariant per-thread address out of the loop
+    const int tid = opaque(tid0);
+    const int lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
+    const int dcol = wave * 16 + n16;
+    LB& lb = sm.lb[m & 1];
+    __syncthreads();  // lane m-1 done with the lane tiles; lane m-2's scalar pass done with lb
+    // ---- commit lane m's prefetched inputs ----
 #pragma unroll
-    for (int dd = 0; dd < DPW; ++dd) {
-      const int dt = wave * DPW + dd;
-#pragma unroll
-      for (int it = 0; it < NCT; ++it) {
-        const f32x4 acc = tile_nt<CT, C>(&sm.kt[(dt * 16 + n16) * LDC], &sm.u.p1.tb[(it * 16 + n16) * LDC], g4);
-        st4(&sm.u.p1.wm[(it * 16 + n16) * LDD + dt * 16 + 4 * g4], -acc[0], -acc[1], -acc[2], -acc[3]);
+    for (int j = 0; j < Pf::NDY; ++j) {
+      const int qv = tid + j * NT, row = qv / (D / Pf::VEC), col = (qv % (D / Pf::VEC)) * Pf::VEC;
+      if (qv < C * D / Pf::VEC) {
+        uint2* d2 = (uint2*)&sm.u.ln.dy[row * LDD + col];
+        d2[0] = make_uint2(pf.dy[j].x, pf.dy[j].y);
+        d2[1] = make_uint2(pf.dy[j].z, pf.dy[j].w);
       }
     }
-    f32x4 Racc[NCT][NVT];
 #pragma unroll
     for (int it = 0; it < NCT; ++it)
 #pragma unroll
-      for (int vt = 0; vt < NVT; ++vt)
-        Racc[it][vt] = tile_nt<CT, C>(&sm.u.p1.ta[(it * 16 + n16) * LDC], &sm.vt[(v0 + vt * 16 + n16) * LDC], g4);
+      for (int i = 0; i < 4; ++i) {
+        sm.u.ln.R[(it * 16 + 4 * g4 + i) * LDD + dcol] = pf.r[it][i];
+        sm.u.ln.dB[(it * 16 + 4 * g4 + i) * LDD + dcol] = pf.db[it][i];
+      }
+    Frag Sf[NKV], dSf[NKV];  // this wave's rows of S0 / dS_C over k = v
+#pragma unroll
+    for (int kb = 0; kb < NKV; ++kb) {
+      f32x4 ys[TPS], yd[TPS];
+#pragma unroll
+      for (int hh = 0; hh < TPS; ++hh) {
+        ys[hh] = tile_transpose_raw(pf.s[kb * TPS + hh], lane);
+        yd[hh] = tile_transpose_raw(pf.ds[kb * TPS + hh], lane);
+      }
+      Sf[kb] = acc_frag((CT*)nullptr, ys[0], ys[TPS - 1]);
+      dSf[kb] = acc_frag((CT*)nullptr, yd[0], yd[TPS - 1]);
+    }
+    if (wave == SW) {
+      const ChunkScalars cs{lb.G, lb.gam, lb.dec, lb.ae, lb.aw, lb.graw};
+      scal_commit<C>(cs, pf.sc, lane);
+    }
     __syncthreads();
+    if (m + 1 < p.M) prefetch(pf, m + 1, tid);
+    if (m > 0 && wave == SW) scalar_grads(m - 1, sm.lb[(m - 1) & 1]);
 
-    // ---- phase 1 (value columns split over waves) ----
-    Frag Sf[NDT / TPS][NVT], dSf[NDT / TPS][NVT];
-    {
-      const Frag* s = (const Frag*)p.s_stash + (chain * NC + c) * (NT * Dm::STASH_FRAGS);
-      const Frag* ds = (const Frag*)p.ds_stash + (chain * NC + c) * (NT * Dm::STASH_FRAGS);
-#pragma unroll
-      for (int kb = 0; kb < NDT / TPS; ++kb)
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) {
-          Sf[kb][vt] = s[(kb * NVT + vt) * NT + tid];
-          dSf[kb][vt] = ds[(kb * NVT + vt) * NT + tid];
-        }
-    }
-#pragma unroll
-    for (int it = 0; it < NCT; ++it) {
-#pragma unroll
-      for (int kb = 0; kb < NDT / TPS; ++kb) {
-        const Frag a = ld_frag(&sm.u.p1.wm[(it * 16 + n16) * LDD + kb * KS], g4);
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) mma(Racc[it][vt], a, Sf[kb][vt]);
-      }
-    }
-    f32x4 dB[NCT][NVT];
-    {
-      f32x4 dR[NCT][NVT];
-#pragma unroll
-      for (int it = 0; it < NCT; ++it) {
-        const f32x4 dj = *(const f32x4*)&sm.dec[it * 16 + 4 * g4];
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int kb = 0; kb < NDT / TPS; ++kb)
-            mma(acc, ld_frag(&sm.k[(it * 16 + n16) * LDD + kb * KS], g4), dSf[kb][vt]);
-          acc *= dj;
-#pragma unroll
-          for (int kb = 0; kb < C; kb += KS)
-            mma(acc, ld_frag(&sm.u.p1.aqt[(it * 16 + n16) * LDC + kb], g4),
-                ld_frag(&sm.u.p1.dyt[(v0 + vt * 16 + n16) * LDC + kb], g4));
-          dR[it][vt] = acc;
-        }
-      }
-      Frag dRf[NCT / TPS][NVT];
-#pragma unroll
-      for (int kb = 0; kb < NCT / TPS; ++kb)
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) dRf[kb][vt] = acc_frag((CT*)nullptr, dR[kb * TPS][vt], dR[kb * TPS + TPS - 1][vt]);
-#pragma unroll
-      for (int it = 0; it < NCT; ++it)
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int kb = 0; kb < NCT / TPS; ++kb)
-            mma(acc, ld_frag(&sm.u.p1.tt[(it * 16 + n16) * LDC + kb * KS], g4), dRf[kb][vt]);
-          dB[it][vt] = acc;
-        }
-    }
-    // dV += diag(a_w) dB ; da_w = rowsum(dB o V)
-#pragma unroll
-    for (int it = 0; it < NCT; ++it) {
-      const f32x4 awi = *(const f32x4*)&sm.aw[it * 16 + 4 * g4];
-      f32x4 part = zero4();
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt) {
-        dVacc[it][vt] += awi * dB[it][vt];
-        const CT* vrow = &sm.vt[(v0 + vt * 16 + n16) * LDC + it * 16 + 4 * g4];
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) part[ii] += dB[it][vt][ii] * to_f(vrow[ii]);
-      }
+    // ---- dAq = dY R^T (j <= i) and dL = -dB R^T (j < i), lower tiles ----
+    for (int pidx = wave; pidx < NP; pidx += NW) {
+      int it, jt;
+      tri_pair(pidx, it, jt);
+      const f32x4 aA = tile_nt<CT, D>(&sm.u.ln.dy[(it * 16 + n16) * LDD], &sm.u.ln.R[(jt * 16 + n16) * LDD], g4);
+      const f32x4 aL = tile_nt<CT, D>(&sm.u.ln.dB[(it * 16 + n16) * LDD], &sm.u.ln.R[(jt * 16 + n16) * LDD], g4);
+      const int j = jt * 16 + n16;
+      const float Gj = lb.G[j];
+      float xm[4], xa[4];
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
-        const float s = sum16(part[ii]);
-        if (n16 == 0) sm.red[0][wave][it * 16 + 4 * g4 + ii] = s;
+        const int i = it * 16 + 4 * g4 + ii;
+        xm[ii] = 0.f;
+        xa[ii] = 0.f;
+        if (j <= i) {
+          const float Dij = __expf(lb.G[i] - Gj);
+          const float dqk = aA[ii] * Dij;
+          sm.dQK[i * LDF + j] += dqk;
+          xm[ii] = dqk * sm.QK[i * LDF + j];
+          if (j < i) {
+            const float dl = -aL[ii];
+            const float kk = sm.KK[i * LDF + j];
+            const float dkk = dl * Dij * lb.ae[i];
+            sm.dKK[i * LDF + j] += dkk;
+            xm[ii] += dkk * kk;
+            xa[ii] = dl * Dij * kk;
+          }
+        }
+      }
+      // row sums (over the 16 columns j, lane 15 of each row) and column sums (over the 16 rows i)
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const float rx = row_prefix16(xm[ii]), ra = row_prefix16(xa[ii]);
+        if (n16 == 15) {
+          lb.tri[pidx][0][4 * g4 + ii] = rx;
+          lb.tri[pidx][2][4 * g4 + ii] = ra;
+        }
+      }
+      float cx = (xm[0] + xm[1]) + (xm[2] + xm[3]);
+      cx += __shfl_xor(cx, 16, 64);
+      cx += __shfl_xor(cx, 32, 64);
+      if (g4 == 0) lb.tri[pidx][1][n16] = cx;
+    }
+
+    // ---- P1 = dY S0^T, P2 = dB S0^T, P3 = R dS^T on this wave's d tile; dV, da_w ----
+#pragma unroll
+    for (int it = 0; it < NCT; ++it) {
+      f32x4 P1 = zero4(), P2 = zero4(), P3 = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKV; ++kb) {
+        mma(P1, ld_frag(&sm.u.ln.dy[(it * 16 + n16) * LDD + kb * KS], g4), Sf[kb]);
+        mma(P2, ld_frag(&sm.u.ln.dB[(it * 16 + n16) * LDD + kb * KS], g4), Sf[kb]);
+        mma(P3, ld_frag(&sm.u.ln.R[(it * 16 + n16) * LDD + kb * KS], g4), dSf[kb]);
+      }
+      const f32x4 gi = *(const f32x4*)&lb.gam[it * 16 + 4 * g4];
+      const f32x4 ei = *(const f32x4*)&lb.ae[it * 16 + 4 * g4];
+      const f32x4 di = *(const f32x4*)&lb.dec[it * 16 + 4 * g4];
+      const f32x4 wi = *(const f32x4*)&lb.aw[it * 16 + 4 * g4];
+      dQacc[it] += gi * P1;
+      dKacc[it] += di * P3 - ei * gi * P2;
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int i = it * 16 + 4 * g4 + ii;
+        const float dbv = to_f(sm.u.ln.dB[i * LDD + dcol]);
+        const float kv = to_f(sm.k[i * LDD + dcol]);
+        dVacc[it][ii] += wi[ii] * dbv;
+        const float s1 = row_prefix16(P1[ii] * to_f(sm.q[i * LDD + dcol]));
+        const float s2 = row_prefix16(P2[ii] * kv);
+        const float s3 = row_prefix16(P3[ii] * kv);
+        const float sw = row_prefix16(dbv * to_f(sm.v[i * LDD + dcol]));
+        if (n16 == 15) {
+          lb.red[0][wave][i] = s1;
+          lb.red[1][wave][i] = s2;
+          lb.red[2][wave][i] = s3;
+          lb.red[3][wave][i] = sw;
+        }
       }
     }
-    {  // <dS_C, S0>
+    {  // <dS_C, S0> over this wave's rows
       float s = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < NDT / TPS; ++kb)
+      for (int kb = 0; kb < NKV; ++kb)
 #pragma unroll
-        for (int vt = 0; vt < NVT; ++vt)
-#pragma unroll
-          for (int e = 0; e < FL; ++e) s += to_f(Sf[kb][vt][e]) * to_f(dSf[kb][vt][e]);
+        for (int e = 0; e < FragLen<CT>::value; ++e) s += to_f(Sf[kb][e]) * to_f(dSf[kb][e]);
 #pragma unroll
       for (int off = 1; off < 64; off <<= 1) s += __shfl_xor(s, off, 64);
-      if (lane == 0) sm.scal[wave] = s;
+      if (lane == 0) lb.scal[wave] = s;
     }
-    __syncthreads();  // phase-1 LDS (union p1) is dead from here on
-
-    // ---- stage R, dB, S0 value-contiguous ----
-#pragma unroll
-    for (int it = 0; it < NCT; ++it)
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt)
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int r = (it * 16 + 4 * g4 + ii) * LDD + v0 + vt * 16 + n16;
-          sm.u.p2.R[r] = from_f<CT>(Racc[it][vt][ii]);
-          sm.u.p2.dB[r] = from_f<CT>(dB[it][vt][ii]);
-        }
-#pragma unroll
-    for (int kb = 0; kb < NDT / TPS; ++kb)
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt)
-#pragma unroll
-        for (int e = 0; e < FL; ++e)
-          sm.u.p2.X[(kb * KS + frag_row<CT>(e, g4)) * LDD + v0 + vt * 16 + n16] = Sf[kb][vt][e];
-    __syncthreads();
-
-    // ---- phase 2 (key columns split over waves): P1 = dY S0^T, P2 = dB S0^T ----
-    {
-      f32x4 r1[NCT], r2[NCT];
-#pragma unroll
-      for (int it = 0; it < NCT; ++it) r1[it] = r2[it] = zero4();
-#pragma unroll
-      for (int dd = 0; dd < DPW; ++dd) {
-        const int dt = wave * DPW + dd;
-        const int d = dt * 16 + n16;
-#pragma unroll
-        for (int it = 0; it < NCT; ++it) {
-          const f32x4 P1 = tile_nt<CT, D>(&sm.dy[(it * 16 + n16) * LDD], &sm.u.p2.X[(dt * 16 + n16) * LDD], g4);
-          const f32x4 P2 = tile_nt<CT, D>(&sm.u.p2.dB[(it * 16 + n16) * LDD], &sm.u.p2.X[(dt * 16 + n16) * LDD], g4);
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int i = it * 16 + 4 * g4 + ii;
-            dQacc[it][dd][ii] += sm.gam[i] * P1[ii];
-            dKacc[it][dd][ii] -= sm.ae[i] * sm.gam[i] * P2[ii];
-            r1[it][ii] += P1[ii] * to_f(sm.q[i * LDD + d]);
-            r2[it][ii] += P2[ii] * to_f(sm.k[i * LDD + d]);
-          }
-        }
-      }
-#pragma unroll
-      for (int it = 0; it < NCT; ++it)
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const float s1 = sum16(r1[it][ii]), s2 = sum16(r2[it][ii]);
-          if (n16 == 0) {
-            sm.red[1][wave][it * 16 + 4 * g4 + ii] = s1;
-            sm.red[2][wave][it * 16 + 4 * g4 + ii] = s2;
-          }
-        }
-    }
-    // dAq = dY R^T (j <= i) and dL = -dB R^T (j < i), lower tiles
-    {
-      constexpr int NP = NCT * (NCT + 1) / 2;
-      for (int pidx = wave; pidx < NP; pidx += NW) {
-        int it, jt;
-        tri_pair(pidx, it, jt);
-        const f32x4 aA = tile_nt<CT, D>(&sm.dy[(it * 16 + n16) * LDD], &sm.u.p2.R[(jt * 16 + n16) * LDD], g4);
-        const f32x4 aL = tile_nt<CT, D>(&sm.u.p2.dB[(it * 16 + n16) * LDD], &sm.u.p2.R[(jt * 16 + n16) * LDD], g4);
-        const int j = jt * 16 + n16;
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const int i = it * 16 + 4 * g4 + ii;
-          float xm = 0.f, ae = 0.f;
-          if (j <= i) {
-            const float Dij = __expf(sm.G[i] - sm.G[j]);
-            const float dqk = aA[ii] * Dij;
-            sm.dQK[i * LDF + j] += dqk;
-            xm = dqk * sm.QK[i * LDF + j];
-            if (j < i) {
-              const float dl = -aL[ii];
-              const float dkk = dl * Dij * sm.ae[i];
-              sm.dKK[i * LDF + j] += dkk;
-              xm += dkk * sm.KK[i * LDF + j];
-              ae = dl * Dij * sm.KK[i * LDF + j];
-            }
-          }
-          sm.u.p2.Xm[i * LDF + j] = xm;
-          sm.u.p2.AE[i * LDF + j] = ae;
-        }
-      }
-    }
-    __syncthreads();
-    // ---- P3 = R dS^T ----
-#pragma unroll
-    for (int kb = 0; kb < NDT / TPS; ++kb)
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt)
-#pragma unroll
-        for (int e = 0; e < FL; ++e)
-          sm.u.p2.X[(kb * KS + frag_row<CT>(e, g4)) * LDD + v0 + vt * 16 + n16] = dSf[kb][vt][e];
-    __syncthreads();
-    {
-      f32x4 r3[NCT];
-#pragma unroll
-      for (int it = 0; it < NCT; ++it) r3[it] = zero4();
-#pragma unroll
-      for (int dd = 0; dd < DPW; ++dd) {
-        const int dt = wave * DPW + dd;
-        const int d = dt * 16 + n16;
-#pragma unroll
-        for (int it = 0; it < NCT; ++it) {
-          const f32x4 P3 = tile_nt<CT, D>(&sm.u.p2.R[(it * 16 + n16) * LDD], &sm.u.p2.X[(dt * 16 + n16) * LDD], g4);
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int j = it * 16 + 4 * g4 + ii;
-            dKacc[it][dd][ii] += sm.dec[j] * P3[ii];
-            r3[it][ii] += P3[ii] * to_f(sm.k[j * LDD + d]);
-          }
-        }
-      }
-#pragma unroll
-      for (int it = 0; it < NCT; ++it)
-#pragma unroll
-        for (int ii = 0; ii < 4; ++ii) {
-          const float s3 = sum16(r3[it][ii]);
-          if (n16 == 0) sm.red[3][wave][it * 16 + 4 * g4 + ii] = s3;
-        }
-    }
-    __syncthreads();
-    // ---- per-token scalar gradients of this lane ----
-    float dGi = 0.f, daei = 0.f, dawi = 0.f;
-    if (tid < C) {
-      const int i = tid;
-      float r1 = 0.f, r2 = 0.f, r3 = 0.f;
-#pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        dawi += sm.red[0][w][i];
-        r1 += sm.red[1][w][i];
-        r2 += sm.red[2][w][i];
-        r3 += sm.red[3][w][i];
-      }
-      dGi = sm.gam[i] * r1 - sm.gam[i] * sm.ae[i] * r2 - sm.dec[i] * r3;
-      daei = -sm.gam[i] * r2;
-      for (int j = 0; j <= i; ++j) dGi += sm.u.p2.Xm[i * LDF + j];
-      for (int j = i; j < C; ++j) dGi -= sm.u.p2.Xm[j * LDF + i];
-      for (int j = 0; j < i; ++j) daei += sm.u.p2.AE[i * LDF + j];
-      sm.tmp[i] = sm.dec[i] * r3;
-    }
-    __syncthreads();
-    if (wave == 0) {
-      if (lane == C - 1) {
-        float s = 0.f;
-        for (int w = 0; w < NW; ++w) s += sm.scal[w];
-        s *= sm.gam[C - 1];
-        for (int j = 0; j < C; ++j) s += sm.tmp[j];
-        dGi += s;
-      }
-      // dg_s = sum_{i >= s} dG_i (suffix sum within the chunk)
-      float sfx = (lane < C) ? dGi : 0.f;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float o = __shfl_down(sfx, off, 64);
-        if (lane + off < 64) sfx += o;
-      }
-      const int t = t0 + lane;
-      if (lane < C && t < p.T) {
-        const size_t si = ((size_t)(b * p.T + t) * p.H + h) * p.M + m;
-        const float raw = sm.graw[lane];
-        p.dae[si] = daei;
-        p.daw[si] = dawi;
-        p.dg[si] = (raw <= 0.f && raw >= kLogFloor) ? sfx : 0.f;
-      }
-    }
-    __syncthreads();
   }
+  __syncthreads();  // lane tiles dead: the union becomes Q^T, K^T and the gram-gradient factors
+  if (wave == SW) scalar_grads(p.M - 1, sm.lb[(p.M - 1) & 1]);
 
   // ---- gram gradient products, shared over lanes ----
   for (int idx = tid; idx < C * C; idx += NT) {
     const int i = idx / C, j = idx % C;
-    sm.u.p3.A1[i * LDC + j] = from_f<CT>((j <= i) ? sm.dQK[i * LDF + j] : 0.f);
-    sm.u.p3.A2[i * LDC + j] = from_f<CT>((i <= j) ? sm.dQK[j * LDF + i] : 0.f);
+    sm.u.fin.A1[i * LDC + j] = from_f<CT>((j <= i) ? sm.dQK[i * LDF + j] : 0.f);
+    sm.u.fin.A2[i * LDC + j] = from_f<CT>((i <= j) ? sm.dQK[j * LDF + i] : 0.f);
     const float s = (j < i) ? sm.dKK[i * LDF + j] : ((i < j) ? sm.dKK[j * LDF + i] : 0.f);
-    sm.u.p3.A3[i * LDC + j] = from_f<CT>(s);
+    sm.u.fin.A3[i * LDC + j] = from_f<CT>(s);
+  }
+  for (int idx = tid; idx < C * D; idx += NT) {
+    const int i = idx / D, d = idx % D;
+    sm.u.fin.qt[d * LDC + i] = sm.q[i * LDD + d];
+    sm.u.fin.kt[d * LDC + i] = sm.k[i * LDD + d];
   }
   __syncthreads();
 #pragma unroll
-  for (int dd = 0; dd < DPW; ++dd) {
-    const int dt = wave * DPW + dd;
-#pragma unroll
-    for (int it = 0; it < NCT; ++it) {
-      dQacc[it][dd] += tile_nt<CT, C>(&sm.u.p3.A1[(it * 16 + n16) * LDC], &sm.kt[(dt * 16 + n16) * LDC], g4);
-      dKacc[it][dd] += tile_nt<CT, C>(&sm.u.p3.A2[(it * 16 + n16) * LDC], &sm.qt[(dt * 16 + n16) * LDC], g4);
-      dKacc[it][dd] += tile_nt<CT, C>(&sm.u.p3.A3[(it * 16 + n16) * LDC], &sm.kt[(dt * 16 + n16) * LDC], g4);
-    }
+  for (int it = 0; it < NCT; ++it) {
+    dQacc[it] += tile_nt<CT, C>(&sm.u.fin.A1[(it * 16 + n16) * LDC], &sm.u.fin.kt[dcol * LDC], g4);
+    dKacc[it] += tile_nt<CT, C>(&sm.u.fin.A2[(it * 16 + n16) * LDC], &sm.u.fin.qt[dcol * LDC], g4);
+    dKacc[it] += tile_nt<CT, C>(&sm.u.fin.A3[(it * 16 + n16) * LDC], &sm.u.fin.kt[dcol * LDC], g4);
   }
+  // stores: transposed tiles, lane (g, n) holds row it*16+n, columns 16*wave + 4g..4g+3
   CT* dq = (CT*)p.dq;
   CT* dk = (CT*)p.dk;
   CT* dv = (CT*)p.dv;
 #pragma unroll
-  for (int it = 0; it < NCT; ++it)
-#pragma unroll
-    for (int ii = 0; ii < 4; ++ii) {
-      const int t = t0 + it * 16 + 4 * g4 + ii;
-      if (t < p.T) {
-        const size_t row = ((size_t)(b * p.T + t) * p.H + h) * D;
-#pragma unroll
-        for (int dd = 0; dd < DPW; ++dd) {
-          const int d = (wave * DPW + dd) * 16 + n16;
-          dq[row + d] = from_f<CT>(dQacc[it][dd][ii]);
-          dk[row + d] = from_f<CT>(dKacc[it][dd][ii]);
-        }
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) dv[row + v0 + vt * 16 + n16] = from_f<CT>(dVacc[it][vt][ii]);
-      }
+  for (int it = 0; it < NCT; ++it) {
+    const int t = t0 + it * 16 + n16;
+    const f32x4 xq = tile_transpose((CT*)nullptr, dQacc[it], lane);
+    const f32x4 xk = tile_transpose((CT*)nullptr, dKacc[it], lane);
+    const f32x4 xv = tile_transpose((CT*)nullptr, dVacc[it], lane);
+    if (t < p.T) {
+      const size_t off = ((size_t)(b * p.T + t) * p.H + h) * D + wave * 16 + 4 * g4;
+      st4(dq + off, xq[0], xq[1], xq[2], xq[3]);
+      st4(dk + off, xk[0], xk[1], xk[2], xk[3]);
+      st4(dv + off, xv[0], xv[1], xv[2], xv[3]);
     }
+  }
 }
 
 // stages: bit 0 = reverse state scan, bit 1 = gradient kernel
@@ -693,7 +647,7 @@ static int launch_bwd(const DeltaBwdArgs& a, int stages, hipStream_t stream) {
     if (rc) return rc;
   }
   if (stages & 2) {
-    hipLaunchKernelGGL((delta_bwd_grads_kernel<CT, D, C>), dim3(a.B * a.H * NC), dim3(Dims<CT, D, C>::NT), 0, stream, a);
+    hipLaunchKernelGGL((delta_bwd_grads_kernel<CT, D, C>), dim3(a.B * a.H * NC), dim3(GradDims<CT, D>::NT), 0, stream, a);
     return check_launch("delta_bwd_grads_kernel");
   }
   return GDNX_OK;

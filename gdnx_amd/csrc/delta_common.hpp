@@ -34,21 +34,24 @@ struct Dims {
 // Stage C rows (tokens t0..t0+C-1, zero beyond T) of a [.., T, .., D] tensor
 // into LDS: `nat` gets rows [C][D+4] (feature-contiguous), `tr` gets the
 // transpose [D][C+4] (token-contiguous), each optional.  `src` points at
-// token 0, feature 0 of this (batch, head[, lane]); rows are `rs` apart.
-template <typename CT, int D, int C>
+// token 0, feature 0 of this (batch, head[, lane]); rows are `rs` apart
+// (C * rs < 2^31: the in-chunk offset is 32-bit).  NTH threads take part.
+template <typename CT, int D, int C, int NTH = Dims<CT, D, C>::NT>
 __device__ __forceinline__ void stage_tile(const CT* __restrict__ src, size_t rs, int t0, int T,
                                            CT* nat, CT* tr, int tid) {
   constexpr int VEC = 16 / sizeof(CT);
   constexpr int DG = D / VEC;
   constexpr int LDD = D + 4, LDC = C + 4;
-  for (int u = tid; u < (C / 4) * DG; u += Dims<CT, D, C>::NT) {
+  const CT* base = src + (size_t)t0 * rs;
+  const unsigned rs32 = (unsigned)rs;
+  for (int u = tid; u < (C / 4) * DG; u += NTH) {
     const int tg = u / DG, dg = u % DG;
     CT x[4][VEC];
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
-      const int t = t0 + 4 * tg + r;
-      if (t < T)
-        *(uint4*)x[r] = *(const uint4*)(src + (size_t)t * rs + dg * VEC);
+      const int tr_ = 4 * tg + r;
+      if (t0 + tr_ < T)
+        *(uint4*)x[r] = *(const uint4*)(base + (unsigned)tr_ * rs32 + dg * VEC);
       else
         *(uint4*)x[r] = make_uint4(0, 0, 0, 0);
     }
@@ -371,6 +374,37 @@ __device__ __forceinline__ void invert_unit_lower(const float* sL, const float* 
   }
 }
 
+// Four consecutive compute-dtype values (8 bytes for bf16, 16 for fp32).
+template <typename CT> struct Vec4T;
+template <> struct Vec4T<bf16> { typedef bf16x4 type; };
+template <> struct Vec4T<float> { typedef f32x4 type; };
+
+// Transpose of a 16x16 tile held as raw values (lane (g, n) holds rows 4g..4g+3
+// of column n): returns lane (g, n) holding row n, columns 4g..4g+3.  Exact.
+__device__ __forceinline__ f32x4 tile_transpose_raw(const bf16x4& x, int lane) {
+  const int g4 = lane >> 4, n16 = lane & 15;
+  bf16x8 a, b;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    a[e] = x[e];
+    a[e + 4] = (bf16)0.f;
+    b[e] = (bf16)((4 * g4 + e == n16) ? 1.f : 0.f);
+    b[e + 4] = (bf16)0.f;
+  }
+  f32x4 y = zero4();
+  mma(y, a, b);
+  return y;
+}
+__device__ __forceinline__ f32x4 tile_transpose_raw(const f32x4& x, int lane) {
+  const int g4 = lane >> 4, n16 = lane & 15;
+  f32x4 b;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) b[e] = (4 * g4 + e == n16) ? 1.f : 0.f;
+  f32x4 y = zero4();
+  mma(y, x, b);
+  return y;
+}
+
 // Transpose of a 16x16 fp32 accumulator tile via MFMA with an identity
 // operand: returns Y with lane (g, n) holding X[n][4g+s] in element s.
 // The bf16 variant rounds the values to bf16 (used for bf16 outputs).
@@ -408,6 +442,41 @@ __device__ __forceinline__ f32x4 tile_nt(const CT* arow, const CT* brow, int g4)
   return acc;
 }
 
+template <typename CT> struct FragLen { static constexpr int value = sizeof(CT) == 2 ? 8 : 4; };
+
+// ---- stash layouts (written by the scans, read by the gradient kernel) ----
+// stash_state: one d x d state per (chain, chunk) record, as the NT threads of
+// a scan workgroup hold it: fragment (kb, vt) of thread tid = 64 wf + 16 g + n
+// (k = d over rows KS kb .. KS kb + KS - 1, value columns of wave wf) at
+// fragment index (kb NVT + vt) NT + tid.
+// stash_tiles: a C x d block per record as raw 16x16 accumulator tiles:
+// tile (it, V) = rows 16 it.., columns 16 V.., lane l = 16 g + n holds rows
+// 16 it + 4 g + i (i = 0..3) of column 16 V + n at ((it (D/16) + V) 64 + l) 4 + i.
+__device__ __forceinline__ f32x4 load4(const bf16* p) {
+  const bf16x4 x = *(const bf16x4*)p;
+  return (f32x4){(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
+}
+__device__ __forceinline__ f32x4 load4(const float* p) { return *(const f32x4*)p; }
+
+// X[16 dt + 4 g + i][16 V + n], i = 0..3, for lane (g, n) of a stash_state record
+template <typename CT, int D, int C>
+__device__ __forceinline__ const CT* stash_state_ptr(const CT* rec, int dt, int V, int lane) {
+  typedef Dims<CT, D, C> Dm;
+  const int kb = dt / Dm::TPS, h = dt % Dm::TPS, wf = V / Dm::NVT, vt = V % Dm::NVT;
+  const int f = (kb * Dm::NVT + vt) * Dm::NT + wf * 64 + lane;
+  return rec + (size_t)f * FragLen<CT>::value + 4 * h;
+}
+
+// Inclusive prefix sum over the 16 lanes of each DPP row (lane bits 0..3);
+// lane 15 of a row ends with the row's total.
+__device__ __forceinline__ float row_prefix16(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, true));
+  return x;
+}
+
 // Frag element e of a tile-native fragment sits at row offset frag_row(e, g4)
 // within the k-step (see gdnx_common.hpp).
 template <typename CT>
@@ -415,6 +484,5 @@ __device__ __forceinline__ int frag_row(int e, int g4) {
   if constexpr (sizeof(CT) == 2) return (e < 4) ? 4 * g4 + e : 16 + 4 * g4 + (e - 4);
   return 4 * g4 + e;
 }
-template <typename CT> struct FragLen { static constexpr int value = sizeof(CT) == 2 ? 8 : 4; };
 
 }  // namespace gdnx

@@ -226,14 +226,14 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
       }
     }
 
-    // ---- S0 fragments over k = d (stashed for the backward) ----
+    // ---- S0 fragments over k = d ----
     Frag Sf[NDT / TPS][NVT];
 #pragma unroll
     for (int kb = 0; kb < NDT / TPS; ++kb)
 #pragma unroll
       for (int vt = 0; vt < NVT; ++vt)
         Sf[kb][vt] = acc_frag((CT*)nullptr, S[kb * TPS][vt], S[kb * TPS + TPS - 1][vt]);
-    if (p.chunk_states) {
+    if (p.chunk_states) {  // stash S0 for the backward: this thread's fragments (stash_state layout)
       Frag* cst = (Frag*)p.chunk_states + ((size_t)chain * NC + c) * (NT * Dm::STASH_FRAGS);
 #pragma unroll
       for (int kb = 0; kb < NDT / TPS; ++kb)
@@ -251,6 +251,15 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
 #pragma unroll
         for (int vt = 0; vt < NVT; ++vt) mma(Racc[it][vt], a, Sf[kb][vt]);
       }
+    }
+    if (p.chunk_states) {  // stash R after all states: raw accumulator tiles (stash_tiles layout)
+      CT* rst = (CT*)p.chunk_states + (size_t)nchains * NC * D * D + ((size_t)chain * NC + c) * (C * D);
+#pragma unroll
+      for (int it = 0; it < NCT; ++it)
+#pragma unroll
+        for (int vt = 0; vt < NVT; ++vt)
+          st4(rst + ((it * NDT + wave * NVT + vt) * 64 + lane) * 4, Racc[it][vt][0], Racc[it][vt][1],
+              Racc[it][vt][2], Racc[it][vt][3]);
     }
     if (p.r_norm) {  // |r_i| per token: squares over this wave's value columns, then across waves
 #pragma unroll

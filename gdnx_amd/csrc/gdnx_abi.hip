@@ -51,6 +51,8 @@ static int check_common(const void* q, const void* k, const void* v, int B, int 
   if (B < 1 || T < 0 || H < 1 || M < 1)
     return set_error(GDNX_ERR_SHAPE, "bad sizes B=%d T=%d H=%d M=%d", B, T, H, M);
   if ((long long)B * H * M > (1LL << 30)) return set_error(GDNX_ERR_SHAPE, "too many chains");
+  // in-chunk tile offsets (64 tokens x the lane-expanded token stride) are 32-bit
+  if ((long long)H * M * D * 64 >= (1LL << 31)) return set_error(GDNX_ERR_SHAPE, "H * M too large");
   if (!q || !k || !v) return set_error(GDNX_ERR_ARG, "q, k, v must be non-null");
   if (!aligned16(q) || !aligned16(k) || !aligned16(v))
     return set_error(GDNX_ERR_ARG, "q, k, v must be 16-byte aligned");
@@ -79,7 +81,7 @@ extern "C" long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, i
     return -1;
   const long long nc = (T + C - 1) / C;
   const long long esz = dtype == GDNX_DTYPE_BF16 ? 2 : 4;
-  return (long long)B * H * M * nc * head_dim * head_dim * esz;
+  return (long long)B * H * M * nc * ((long long)head_dim * head_dim + (long long)C * head_dim) * esz;
 }
 
 static int fwd_common(const void* q, const void* k, const void* v, const float* a_e, const float* a_w,

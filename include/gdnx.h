@@ -47,9 +47,12 @@ int gdnx_delta_chunk_size(int head_dim, int dtype);
  * (32 for bf16, 16 for float32). */
 int gdnx_delta_train_chunk_size(int head_dim, int dtype);
 
-/* Bytes of the per-chunk state stash (one d x d state per chain per chunk,
- * in the compute dtype) for the given chunk (0 = default); -1 if invalid.
- * The backward's workspace has the same size. */
+/* Bytes of the per-chunk stash for the given chunk (0 = default; -1 if
+ * invalid): per chain and chunk, in the compute dtype, the d x d state
+ * entering the chunk (row-major [d_k][d_v]) and the chunk's C x d net writes
+ * R (row-major [token][d_v]); all states first, then all net writes.  The
+ * backward's workspace has the same size and layout (state gradients dS at
+ * chunk ends, then dB = T^T dR). */
 long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim, int chunk,
                                         int dtype);
 

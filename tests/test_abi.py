@@ -36,10 +36,10 @@ def test_abi_version_and_sizes():
     assert lib.gdnx_delta_chunk_size(128, _lib.DTYPE_BF16) == 64
     assert lib.gdnx_delta_train_chunk_size(128, _lib.DTYPE_BF16) == 32
     assert lib.gdnx_delta_chunk_size(100, _lib.DTYPE_BF16) == 0
-    # one d x d state per chain per chunk
+    # per chain and chunk: one d x d state and one C x d block of net writes
     assert lib.gdnx_delta_chunk_states_bytes(4, 4096, 16, 4, 128, 64, _lib.DTYPE_BF16) == \
-        4 * 16 * 4 * 64 * 128 * 128 * 2
-    assert lib.gdnx_delta_chunk_states_bytes(1, 100, 1, 1, 64, 0, _lib.DTYPE_F32) == 4 * 64 * 64 * 4
+        4 * 16 * 4 * 64 * (128 * 128 + 64 * 128) * 2
+    assert lib.gdnx_delta_chunk_states_bytes(1, 100, 1, 1, 64, 0, _lib.DTYPE_F32) == 4 * (64 * 64 + 32 * 64) * 4
     assert lib.gdnx_delta_chunk_states_bytes(1, 100, 1, 1, 64, 48, _lib.DTYPE_F32) == -1
 
 
