@@ -43,9 +43,9 @@ def flops_fwd(B, T, H, M, D, C):
 
 def flops_bwd_state(B, T, H, M, D, C):
     """Reverse state scan: per lane and chunk K dS (2 C D^2), Aq^T dY and
-    T^T dR (2 C^2 D as triangular products) and the dS update (4 C D^2)."""
+    T^T dR (2 C^2 D each) and the dS update (4 C D^2)."""
     nchunks = B * H * ((T + C - 1) // C)
-    return nchunks * M * (6 * C * D * D + 2 * C * C * D)
+    return nchunks * M * (6 * C * D * D + 4 * C * C * D)
 
 
 def flops_bwd_grads(B, T, H, M, D, C):
@@ -375,7 +375,7 @@ def main():
     # ---- per-kernel mean durations (events on the launch stream) ----
     C = ops.chunk_size(D, q.dtype, train=True)
     with torch.no_grad():
-        a = gdn3.gdn3_coeff(k, beta).contiguous()
+        a = gdn3.gdn3_coeff(k, beta.detach())
         lg = g.detach().contiguous()
         qd, kd, vd = q.detach(), k.detach(), v.detach()
         stream = torch.cuda.current_stream()
@@ -401,8 +401,8 @@ def main():
         t_bgr = timed(lambda: ops.delta_chunk_bwd_grads(qd, kd, vd, a, a, lg, dO, state["cs"], ws, C, out),
                       args.kernel_iters)
     kernels = {
-        "delta_fwd_kernel": (t_fwd, flops_fwd(B, T, H, M, D, C)),
-        "delta_bwd_state_kernel": (t_bst, flops_bwd_state(B, T, H, M, D, C)),
+        "delta_prep_kernel+delta_scan_fwd_kernel": (t_fwd, flops_fwd(B, T, H, M, D, C)),
+        "delta_scan_bwd_kernel": (t_bst, flops_bwd_state(B, T, H, M, D, C)),
         "delta_bwd_grads_kernel": (t_bgr, flops_bwd_grads(B, T, H, M, D, C)),
     }
     dom = max(kernels, key=lambda n: kernels[n][0])

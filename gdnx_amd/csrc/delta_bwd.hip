@@ -13,10 +13,11 @@
 //   dG_i = exp(G_i) q_i.(dY S0^T)_i - a_e,i exp(G_i) k_i.(dB S0^T)_i + mask terms
 //          + chunk-end terms; dg = reverse cumulative sum of dG in the chunk.
 //
-// Two kernels:
-//   delta_bwd_state_kernel  one workgroup per chain, chunks in reverse order,
-//     carries dS in registers (value columns split over the waves, like the
-//     forward's S) and stashes dS_C and dB of every chunk.  Needs no S0.
+// Two stages:
+//   delta_scan_bwd_kernel (delta_scan.hip)  the reverse scan: value-split
+//     workgroups per chain walk the chunks in reverse with dS in registers,
+//     reading the forward's prep records (T, Aq, decays), and stash dS_C and
+//     dB of every chunk.  Needs no S0.
 //   delta_bwd_grads_kernel  one workgroup per (batch, head, chunk), looping
 //     over the M lanes that share q/k/v: reads S0, R (forward stash) and
 //     dS_C, dB (reverse-scan stash), runs the contractions over value columns
@@ -30,218 +31,6 @@
 #include "delta_common.hpp"
 
 namespace gdnx {
-
-// ---------------------------------------------------------------------------
-// reverse state scan
-// ---------------------------------------------------------------------------
-template <typename CT, int D, int C>
-struct alignas(16) BwdStateSmem {
-  typedef Dims<CT, D, C> Dm;
-  CT q[C * Dm::LDD];
-  CT k[C * Dm::LDD];
-  CT kt[D * Dm::LDC];
-  CT qt[D * Dm::LDC];    // (diag(exp G) Q)^T
-  CT dyt[D * Dm::LDC];   // dY^T
-  CT aqt[C * Dm::LDC];   // Aq^T [j][i]
-  CT tt[C * Dm::LDC];    // T^T  [i][j] = T[j][i]
-  float L[C * Dm::LDF];
-  float LT[C * Dm::LDT];
-  float Td[C * Dm::LDT];
-  float G[C], gam[C], dec[C], ae[C];
-};
-
-template <typename CT, int D, int C>
-__global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_bwd_state_kernel(DeltaBwdArgs p) {
-  typedef Dims<CT, D, C> Dm;
-  typedef typename Dm::Frag Frag;
-  constexpr int KS = Dm::KS, TPS = Dm::TPS, NDT = Dm::NDT, NCT = Dm::NCT, VS = Dm::VS, NVT = Dm::NVT;
-  constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF, NT = Dm::NT;
-  __shared__ BwdStateSmem<CT, D, C> sm;
-
-  const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
-  const int nchains = p.B * p.H * p.M;
-  const int chain = xcd_remap(blockIdx.x, nchains);
-  const int m = chain % p.M;
-  const int h = (chain / p.M) % p.H;
-  const int b = chain / (p.M * p.H);
-  const int v0 = wave * VS;
-  const int NC = (p.T + C - 1) / C;
-  const size_t rs = (size_t)p.H * D;
-  const size_t qoff = ((size_t)b * p.T * p.H + h) * D;
-  const size_t rsy = (size_t)p.H * p.M * D;
-  const size_t yoff = (((size_t)b * p.T * p.H + h) * p.M + m) * D;
-  const size_t st = (size_t)p.H * p.M;
-  const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + m;
-  const ChunkScalars cs{sm.G, sm.gam, sm.dec, sm.ae, nullptr, nullptr};
-
-  for (int i = tid; i < C * LDC; i += NT) {
-    sm.aqt[i] = from_f<CT>(0.f);
-    sm.tt[i] = from_f<CT>(0.f);
-  }
-
-  f32x4 dS[NDT][NVT];
-#pragma unroll
-  for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-    for (int vt = 0; vt < NVT; ++vt) {
-      dS[dt][vt] = zero4();
-      if (p.ds_final) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          dS[dt][vt][i] = p.ds_final[(size_t)chain * D * D + (dt * 16 + 4 * g4 + i) * D + v0 + vt * 16 + n16];
-      }
-    }
-
-  const CT* qg = (const CT*)p.q + qoff;
-  const CT* kg = (const CT*)p.k + qoff;
-  const CT* yg = (const CT*)p.dy + yoff;
-  TileRegs rq, rk, ry;
-  ScalarRegs rsc;
-  tile_fetch<CT, D, C>(rq, qg, rs, (NC - 1) * C, p.T, tid);
-  tile_fetch<CT, D, C>(rk, kg, rs, (NC - 1) * C, p.T, tid);
-  tile_fetch<CT, D, C>(ry, yg, rsy, (NC - 1) * C, p.T, tid);
-  if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, nullptr, p.g + soff, st, (NC - 1) * C, p.T, lane);
-
-  for (int c = NC - 1; c >= 0; --c) {
-    const int t0 = c * C;
-    __syncthreads();
-    tile_commit<CT, D, C>(rq, sm.q, sm.qt, tid);
-    tile_commit<CT, D, C>(rk, sm.k, sm.kt, tid);
-    tile_commit<CT, D, C>(ry, nullptr, sm.dyt, tid);
-    if (wave == 0) scal_commit<C>(cs, rsc, lane);
-    __syncthreads();
-    if (c > 0) {
-      tile_fetch<CT, D, C>(rq, qg, rs, t0 - C, p.T, tid);
-      tile_fetch<CT, D, C>(rk, kg, rs, t0 - C, p.T, tid);
-      tile_fetch<CT, D, C>(ry, yg, rsy, t0 - C, p.T, tid);
-      if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, nullptr, p.g + soff, st, t0 - C, p.T, lane);
-    }
-    for (int idx = tid; idx < D * C; idx += NT) {
-      const int d = idx / C, i = idx % C;
-      sm.qt[d * LDC + i] = from_f<CT>(to_f(sm.qt[d * LDC + i]) * sm.gam[i]);
-    }
-    chunk_grams<CT, D, C>(sm.k, sm.q, sm.L, sm.LT, sm.G, sm.ae, wave, lane, [&](int i, int j0, const float* v) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sm.aqt[(j0 + e) * LDC + i] = from_f<CT>(v[e]);
-    });
-    __syncthreads();
-    invert_unit_lower<C>(
-        sm.L, sm.LT, sm.Td, wave, lane, [&](int) { return 0; },
-        [&](int i, int j, float t, int) { sm.tt[j * LDC + i] = from_f<CT>(t); });
-    __syncthreads();
-
-    // stash dS_C of this chunk (stash_state layout)
-    Frag dSf[NDT / TPS][NVT];
-#pragma unroll
-    for (int kb = 0; kb < NDT / TPS; ++kb)
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt)
-        dSf[kb][vt] = acc_frag((CT*)nullptr, dS[kb * TPS][vt], dS[kb * TPS + TPS - 1][vt]);
-    {
-      Frag* cst = (Frag*)p.ds_stash + ((size_t)chain * NC + c) * (NT * Dm::STASH_FRAGS);
-#pragma unroll
-      for (int kb = 0; kb < NDT / TPS; ++kb)
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) cst[(kb * NVT + vt) * NT + tid] = dSf[kb][vt];
-    }
-    // dR = diag(dec) K dS + Aq^T dY
-    f32x4 dR[NCT][NVT];
-#pragma unroll
-    for (int it = 0; it < NCT; ++it) {
-      const f32x4 dj = *(const f32x4*)&sm.dec[it * 16 + 4 * g4];
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt) {
-        f32x4 acc = zero4();
-#pragma unroll
-        for (int kb = 0; kb < NDT / TPS; ++kb)
-          mma(acc, ld_frag(&sm.k[(it * 16 + n16) * LDD + kb * KS], g4), dSf[kb][vt]);
-        acc *= dj;
-#pragma unroll
-        for (int kb = 0; kb < C; kb += KS)
-          mma(acc, ld_frag(&sm.aqt[(it * 16 + n16) * LDC + kb], g4),
-              ld_frag(&sm.dyt[(v0 + vt * 16 + n16) * LDC + kb], g4));
-        dR[it][vt] = acc;
-      }
-    }
-    // dB = T^T dR
-    Frag dRf[NCT / TPS][NVT];
-#pragma unroll
-    for (int kb = 0; kb < NCT / TPS; ++kb)
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt) dRf[kb][vt] = acc_frag((CT*)nullptr, dR[kb * TPS][vt], dR[kb * TPS + TPS - 1][vt]);
-    Frag dBf[NCT / TPS][NVT];
-    {
-      f32x4 dB[NCT][NVT];
-#pragma unroll
-      for (int it = 0; it < NCT; ++it)
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int kb = 0; kb < NCT / TPS; ++kb)
-            mma(acc, ld_frag(&sm.tt[(it * 16 + n16) * LDC + kb * KS], g4), dRf[kb][vt]);
-          dB[it][vt] = acc;
-        }
-      {  // stash dB after all state gradients: raw accumulator tiles (stash_tiles layout)
-        CT* bst = (CT*)p.ds_stash + (size_t)nchains * NC * D * D + ((size_t)chain * NC + c) * (C * D);
-#pragma unroll
-        for (int it = 0; it < NCT; ++it)
-#pragma unroll
-          for (int vt = 0; vt < NVT; ++vt)
-            st4(bst + ((it * NDT + wave * NVT + vt) * 64 + lane) * 4, dB[it][vt][0], dB[it][vt][1],
-                dB[it][vt][2], dB[it][vt][3]);
-      }
-      // fragments of -diag(a_e exp G) dB over k = i
-#pragma unroll
-      for (int kb = 0; kb < NCT / TPS; ++kb) {
-        const int r0 = kb * KS + 4 * g4, r1 = kb * KS + (TPS - 1) * 16 + 4 * g4;
-        f32x4 s0, s1;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          s0[e] = -sm.ae[r0 + e] * sm.gam[r0 + e];
-          s1[e] = -sm.ae[r1 + e] * sm.gam[r1 + e];
-        }
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt)
-          dBf[kb][vt] = acc_frag((CT*)nullptr, dB[kb * TPS][vt], dB[kb * TPS + TPS - 1][vt], s0, s1);
-      }
-    }
-    // dS <- gamma_C dS + (diag(exp G) Q)^T dY - (diag(a_e exp G) K)^T dB
-    {
-      const float gl = sm.gam[C - 1];
-      Frag dYf[NCT / TPS][NVT];
-#pragma unroll
-      for (int kb = 0; kb < NCT / TPS; ++kb)
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) dYf[kb][vt] = ld_frag(&sm.dyt[(v0 + vt * 16 + n16) * LDC + kb * KS], g4);
-#pragma unroll
-      for (int dt = 0; dt < NDT; ++dt) {
-#pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) dS[dt][vt] *= gl;
-#pragma unroll
-        for (int kb = 0; kb < NCT / TPS; ++kb) {
-          const Frag aq = ld_frag(&sm.qt[(dt * 16 + n16) * LDC + kb * KS], g4);
-          const Frag ak = ld_frag(&sm.kt[(dt * 16 + n16) * LDC + kb * KS], g4);
-#pragma unroll
-          for (int vt = 0; vt < NVT; ++vt) {
-            mma(dS[dt][vt], aq, dYf[kb][vt]);
-            mma(dS[dt][vt], ak, dBf[kb][vt]);
-          }
-        }
-      }
-    }
-  }
-  if (p.ds0) {
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-      for (int vt = 0; vt < NVT; ++vt)
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-          p.ds0[(size_t)chain * D * D + (dt * 16 + 4 * g4 + i) * D + v0 + vt * 16 + n16] = dS[dt][vt][i];
-  }
-}
 
 // ---------------------------------------------------------------------------
 // per-chunk gradients, lanes summed in-block
@@ -362,7 +151,7 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
   // ---- fetch lane mm's inputs into registers (issued a lane ahead) ----
   auto prefetch = [&](Pf& f, int mm, int tid_) {
     const int lane_ = tid_ & 63;
-    const size_t rec = (((size_t)b * p.H + h) * p.M + mm) * NC + c;
+    const size_t rec = rec_index(((size_t)b * p.H + h) * p.M + mm, c, (size_t)p.B * p.H * p.M);
 #pragma unroll
     for (int V = 0; V < NDT; ++V) {
       f.s[V] = *(const V4*)stash_state_ptr<CT, D, C>(s_st + rec * D * D, wave, V, lane_);
@@ -642,8 +431,7 @@ template <typename CT, int D, int C>
 static int launch_bwd(const DeltaBwdArgs& a, int stages, hipStream_t stream) {
   const int NC = (a.T + C - 1) / C;
   if (stages & 1) {
-    hipLaunchKernelGGL((delta_bwd_state_kernel<CT, D, C>), dim3(a.B * a.H * a.M), dim3(Dims<CT, D, C>::NT), 0, stream, a);
-    const int rc = check_launch("delta_bwd_state_kernel");
+    const int rc = delta_scan_bwd_dispatch(a, stream);
     if (rc) return rc;
   }
   if (stages & 2) {

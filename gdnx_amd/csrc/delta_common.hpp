@@ -25,8 +25,6 @@ struct Dims {
   static constexpr int LDC = C + 4;            // LDS row length, [*, C] tiles
   static constexpr int LDF = C + 4;            // fp32 [C, C] scratch rows (16-byte aligned)
   static constexpr int LDT = 20;               // fp32 diagonal-block scratch [C][LDT]
-  // fragments of one chunk-state stash per workgroup (tile-native layout)
-  static constexpr int STASH_FRAGS = (NDT / TPS) * NVT;
   static_assert(C % KS == 0, "chunk must be a multiple of the MFMA k-step");
   static_assert(NVT >= 1 && DPW >= 1 && NDT % NW == 0, "head dim must be 64 or 128");
 };
@@ -81,22 +79,36 @@ struct ChunkScalars {
   float *G, *gam, *dec, *ae, *aw, *graw;
 };
 
+// Per-chunk records (stashes and prep operands) are chunk-major: record
+// (chain, chunk) = chunk * nchains + chain.  The chains of a scan run in
+// lockstep, so the records written or read at one time are contiguous and
+// spread over the memory channels (chain-major records would sit a whole
+// chain's stash apart and pile onto the same channels).
+__host__ __device__ __forceinline__ size_t rec_index(size_t chain, int chunk, size_t nchains) {
+  return (size_t)chunk * nchains + chain;
+}
+
 // Per-chunk operands written by the prep kernel, for NR = chains x chunks
-// records (chain-major, a chain's chunks contiguous): TA, TB, Aq as [C][C]
-// compute-dtype matrices, then gam and dec as [2][C] floats per record.
+// records (indexed by rec_index): the unit-lower inverse T = (I + L)^-1
+// and the decay-masked Q K^T (Aq) as row-major [C][C] compute-dtype
+// matrices, then per token [4][C] floats: gam = exp(G), dec = exp(G_last - G),
+// aeg = a_e exp(G) and a_w.  Consumers scale T on the fly:
+// T diag(a_w) V and T diag(aeg) K are the chunk's U and Wm.
+enum { kScGam = 0, kScDec = 1, kScAeg = 2, kScAw = 3, kNumSc = 4 };
 template <typename CT>
 struct PrepPtrs {
-  CT* ta;
-  CT* tb;
+  CT* t;
   CT* aq;
   float* sc;
 };
 template <typename CT>
 __host__ __device__ __forceinline__ PrepPtrs<CT> prep_ptrs(void* base, size_t NR, int C) {
-  CT* ta = (CT*)base;
-  CT* tb = ta + NR * C * C;
-  CT* aq = tb + NR * C * C;
-  return PrepPtrs<CT>{ta, tb, aq, (float*)(aq + NR * C * C)};
+  CT* t = (CT*)base;
+  CT* aq = t + NR * C * C;
+  return PrepPtrs<CT>{t, aq, (float*)(aq + NR * C * C)};
+}
+__host__ __device__ __forceinline__ size_t prep_bytes_per_record(int C, size_t es) {
+  return 2 * (size_t)C * C * es + (size_t)kNumSc * C * sizeof(float);
 }
 
 // Prefetched per-token scalars of one lane (token t0 + lane).
@@ -445,13 +457,18 @@ __device__ __forceinline__ f32x4 tile_nt(const CT* arow, const CT* brow, int g4)
 template <typename CT> struct FragLen { static constexpr int value = sizeof(CT) == 2 ? 8 : 4; };
 
 // ---- stash layouts (written by the scans, read by the gradient kernel) ----
-// stash_state: one d x d state per (chain, chunk) record, as the NT threads of
-// a scan workgroup hold it: fragment (kb, vt) of thread tid = 64 wf + 16 g + n
-// (k = d over rows KS kb .. KS kb + KS - 1, value columns of wave wf) at
-// fragment index (kb NVT + vt) NT + tid.
+// stash_state: one d x d state per (chain, chunk) record as MFMA fragments:
+// block (kb, V) (k = d over rows KS kb .. KS kb + KS - 1, value columns
+// 16 V .. 16 V + 15) is 64 lanes x one fragment, lane l = 16 g + n holding
+// column 16 V + n at rows KS kb + frag_row(e, g); blocks at (kb (D/16) + V).
+// Any split of the value columns over waves or workgroups writes whole blocks.
 // stash_tiles: a C x d block per record as raw 16x16 accumulator tiles:
 // tile (it, V) = rows 16 it.., columns 16 V.., lane l = 16 g + n holds rows
 // 16 it + 4 g + i (i = 0..3) of column 16 V + n at ((it (D/16) + V) 64 + l) 4 + i.
+template <typename CT, int D>
+__device__ __forceinline__ size_t stash_frag_index(int kb, int V, int lane) {
+  return ((size_t)kb * (D / 16) + V) * 64 + lane;
+}
 __device__ __forceinline__ f32x4 load4(const bf16* p) {
   const bf16x4 x = *(const bf16x4*)p;
   return (f32x4){(float)x[0], (float)x[1], (float)x[2], (float)x[3]};
@@ -462,9 +479,8 @@ __device__ __forceinline__ f32x4 load4(const float* p) { return *(const f32x4*)p
 template <typename CT, int D, int C>
 __device__ __forceinline__ const CT* stash_state_ptr(const CT* rec, int dt, int V, int lane) {
   typedef Dims<CT, D, C> Dm;
-  const int kb = dt / Dm::TPS, h = dt % Dm::TPS, wf = V / Dm::NVT, vt = V % Dm::NVT;
-  const int f = (kb * Dm::NVT + vt) * Dm::NT + wf * 64 + lane;
-  return rec + (size_t)f * FragLen<CT>::value + 4 * h;
+  const int kb = dt / Dm::TPS, h = dt % Dm::TPS;
+  return rec + stash_frag_index<CT, D>(kb, V, lane) * FragLen<CT>::value + 4 * h;
 }
 
 // Inclusive prefix sum over the 16 lanes of each DPP row (lane bits 0..3);
@@ -483,6 +499,139 @@ template <typename CT>
 __device__ __forceinline__ int frag_row(int e, int g4) {
   if constexpr (sizeof(CT) == 2) return (e < 4) ? 4 * g4 + e : 16 + 4 * g4 + (e - 4);
   return 4 * g4 + e;
+}
+
+// Raw buffer resource over nbytes at base: buffer loads beyond nbytes
+// return zero and buffer stores beyond it are dropped, so a chunk's tail
+// tokens need no branch (a branch around a memory op makes the compiler wait
+// for every outstanding load and store at the next loop iteration).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buf_rsrc(const void* base, unsigned nbytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)nbytes, 0x00020000);
+}
+__device__ __forceinline__ uint4 buf_load16(__amdgpu_buffer_rsrc_t r, unsigned off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+// 4 consecutive values of the compute dtype from floats (8 or 16 bytes)
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, unsigned off, const bf16*, float a, float b,
+                                           float c, float d) {
+  const bf16x4 x = (bf16x4){(bf16)a, (bf16)b, (bf16)c, (bf16)d};
+  typedef unsigned u32x2 __attribute__((ext_vector_type(2)));
+  __builtin_amdgcn_raw_buffer_store_b64(__builtin_bit_cast(u32x2, x), r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void buf_store4(__amdgpu_buffer_rsrc_t r, unsigned off, const float*, float a, float b,
+                                           float c, float d) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  __builtin_amdgcn_raw_buffer_store_b128((u32x4){__float_as_uint(a), __float_as_uint(b), __float_as_uint(c),
+                                                 __float_as_uint(d)},
+                                         r, (int)off, 0, 0);
+}
+
+// Register staging of a [ROWS][COLS] compute-dtype tile for NTH threads:
+// unit u = (RU consecutive rows, 16 bytes of columns); thread tid owns units
+// tid, tid + NTH, ...  Fetched a chunk ahead into registers, then committed
+// to LDS either as rows (commit_nat, row stride LD) or transposed
+// (commit_tr, [col][row] with row stride LD; needs RU = 4: 4 consecutive
+// rows per store).  Every thread issues the same loads (a thread past the
+// last unit repeats it), so the loads are unconditional.
+template <typename CT, int ROWS, int COLS, int RU, int NTH>
+struct Stage {
+  static constexpr int VEC = 16 / sizeof(CT);
+  static constexpr int CG = COLS / VEC;
+  static constexpr int NU = (ROWS / RU) * CG;
+  static constexpr int UPT = (NU + NTH - 1) / NTH;
+  static_assert(COLS % VEC == 0 && ROWS % RU == 0, "tile not a whole number of units");
+  uint4 x[UPT][RU];
+
+  __device__ __forceinline__ static int unit(int tid, int u) {
+    const int e = tid + u * NTH;
+    return (NU % NTH == 0 || e < NU) ? e : NU - 1;
+  }
+  __device__ __forceinline__ static bool owns(int tid, int u) { return NU % NTH == 0 || tid + u * NTH < NU; }
+  // rows rsb bytes apart in a buffer resource (rows past its end read zero)
+  __device__ __forceinline__ void fetch(__amdgpu_buffer_rsrc_t r, unsigned rsb, int tid) {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int e = unit(tid, u), rg = e / CG, cg = e % CG;
+#pragma unroll
+      for (int q = 0; q < RU; ++q) x[u][q] = buf_load16(r, (unsigned)(rg * RU + q) * rsb + cg * 16);
+    }
+  }
+  // a dense row-major [ROWS][COLS] tile
+  __device__ __forceinline__ void fetch_dense(const CT* __restrict__ src, int tid) {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      const int e = unit(tid, u), rg = e / CG, cg = e % CG;
+#pragma unroll
+      for (int q = 0; q < RU; ++q) x[u][q] = *(const uint4*)(src + (rg * RU + q) * COLS + cg * VEC);
+    }
+  }
+  template <int LD>
+  __device__ __forceinline__ void commit_nat(CT* dst, int tid) const {
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      if (!owns(tid, u)) continue;
+      const int e = tid + u * NTH, rg = e / CG, cg = e % CG;
+#pragma unroll
+      for (int q = 0; q < RU; ++q) {
+        uint2* d = (uint2*)(dst + (rg * RU + q) * LD + cg * VEC);
+        d[0] = make_uint2(x[u][q].x, x[u][q].y);
+        d[1] = make_uint2(x[u][q].z, x[u][q].w);
+      }
+    }
+  }
+  template <int LD>
+  __device__ __forceinline__ void commit_tr(CT* dst, int tid) const {
+    static_assert(RU == 4, "transposed commit stores 4 consecutive rows");
+#pragma unroll
+    for (int u = 0; u < UPT; ++u) {
+      if (!owns(tid, u)) continue;
+      const int e = tid + u * NTH, rg = e / CG, cg = e % CG;
+      if constexpr (sizeof(CT) == 2) {
+#pragma unroll
+        for (int c = 0; c < 8; ++c) {
+          const int w = c >> 1, sh = (c & 1) * 16;
+          const unsigned a0 = (word_of(x[u][0], w) >> sh) & 0xffffu, a1 = (word_of(x[u][1], w) >> sh) & 0xffffu;
+          const unsigned a2 = (word_of(x[u][2], w) >> sh) & 0xffffu, a3 = (word_of(x[u][3], w) >> sh) & 0xffffu;
+          *(uint2*)&dst[(cg * VEC + c) * LD + 4 * rg] = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
+        }
+      } else {
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+          *(uint4*)&dst[(cg * VEC + c) * LD + 4 * rg] =
+              make_uint4(word_of(x[u][0], c), word_of(x[u][1], c), word_of(x[u][2], c), word_of(x[u][3], c));
+      }
+    }
+  }
+};
+
+// N floats staged by NTH threads (one dword each, a chunk ahead).
+template <int N, int NTH>
+struct ScalStage {
+  static constexpr int PT = (N + NTH - 1) / NTH;
+  float x[PT];
+  __device__ __forceinline__ void fetch(const float* __restrict__ src, int t) {
+#pragma unroll
+    for (int i = 0; i < PT; ++i) x[i] = src[min(t + i * NTH, N - 1)];
+  }
+  __device__ __forceinline__ void commit(float* dst, int t) const {
+#pragma unroll
+    for (int i = 0; i < PT; ++i)
+      if (N % NTH == 0 || t + i * NTH < N) dst[t + i * NTH] = x[i];
+  }
+};
+
+// A fragment over k with element e (k index kb + frag_row(e, g)) scaled by
+// s[frag_row(e, g)]; s points at the k-step's first scale factor (LDS,
+// 16-byte aligned).
+__device__ __forceinline__ bf16x8 frag_scale(const bf16x8& f, const float* s, int g4) {
+  const f32x4 s0 = *(const f32x4*)&s[4 * g4], s1 = *(const f32x4*)&s[16 + 4 * g4];
+  return (bf16x8){(bf16)((float)f[0] * s0[0]), (bf16)((float)f[1] * s0[1]), (bf16)((float)f[2] * s0[2]),
+                  (bf16)((float)f[3] * s0[3]), (bf16)((float)f[4] * s1[0]), (bf16)((float)f[5] * s1[1]),
+                  (bf16)((float)f[6] * s1[2]), (bf16)((float)f[7] * s1[3])};
+}
+__device__ __forceinline__ f32x4 frag_scale(const f32x4& f, const float* s, int g4) {
+  return f * *(const f32x4*)&s[4 * g4];
 }
 
 }  // namespace gdnx

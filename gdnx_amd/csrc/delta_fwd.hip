@@ -39,64 +39,7 @@ struct alignas(16) FwdSmem {
   float rn[4][C];       // per-wave partial |r_i|^2 (scored forward)
 };
 
-// One thread's share of a chunk's prepped operands (TA, TB, Aq tiles and the
-// gam / dec scalars), fetched a chunk ahead.
-template <typename CT, int C, int NT>
-struct PrepRegs {
-  static constexpr int PER = 16 / sizeof(CT), NU = C * C / PER, UPT = (NU + NT - 1) / NT;
-  uint4 ta[UPT], tb[UPT], aq[UPT];
-  float gam, dec;
-};
-
-template <typename CT, int C, int NT>
-__device__ __forceinline__ void prep_fetch(PrepRegs<CT, C, NT>& r, const PrepPtrs<CT>& po, size_t rec, int tid) {
-  typedef PrepRegs<CT, C, NT> R;
-  const uint4* ta = (const uint4*)(po.ta + rec * C * C);
-  const uint4* tb = (const uint4*)(po.tb + rec * C * C);
-  const uint4* aq = (const uint4*)(po.aq + rec * C * C);
-#pragma unroll
-  for (int u = 0; u < R::UPT; ++u) {
-    const int e = tid + u * NT;
-    if (e < R::NU) {
-      r.ta[u] = ta[e];
-      r.tb[u] = tb[e];
-      r.aq[u] = aq[e];
-    }
-  }
-  if (tid < C) {
-    r.gam = po.sc[rec * 2 * C + tid];
-    r.dec = po.sc[rec * 2 * C + C + tid];
-  }
-}
-
-// LDS rows of [*][LDC] are 8-byte aligned: 16-byte units go as two halves.
-template <typename CT, int C, int LDC, int NT>
-__device__ __forceinline__ void prep_commit(const PrepRegs<CT, C, NT>& r, CT* ta, CT* tb, CT* aq, float* gam,
-                                            float* dec, int tid) {
-  typedef PrepRegs<CT, C, NT> R;
-#pragma unroll
-  for (int u = 0; u < R::UPT; ++u) {
-    const int e = tid + u * NT;
-    if (e < R::NU) {
-      const int i = (e * R::PER) / C, j = (e * R::PER) % C;
-      uint2* d0 = (uint2*)&ta[i * LDC + j];
-      uint2* d1 = (uint2*)&tb[i * LDC + j];
-      uint2* d2 = (uint2*)&aq[i * LDC + j];
-      d0[0] = make_uint2(r.ta[u].x, r.ta[u].y);
-      d0[1] = make_uint2(r.ta[u].z, r.ta[u].w);
-      d1[0] = make_uint2(r.tb[u].x, r.tb[u].y);
-      d1[1] = make_uint2(r.tb[u].z, r.tb[u].w);
-      d2[0] = make_uint2(r.aq[u].x, r.aq[u].y);
-      d2[1] = make_uint2(r.aq[u].z, r.aq[u].w);
-    }
-  }
-  if (tid < C) {
-    gam[tid] = r.gam;
-    dec[tid] = r.dec;
-  }
-}
-
-template <typename CT, int D, int C, bool PREP>
+template <typename CT, int D, int C>
 __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaArgs p) {
   typedef Dims<CT, D, C> Dm;
   typedef typename Dm::Frag Frag;
@@ -145,14 +88,10 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
 
   TileRegs rq, rk, rv;
   ScalarRegs rsc;
-  PrepRegs<CT, C, NT> rp;
-  const PrepPtrs<CT> po = prep_ptrs<CT>(p.prep, (size_t)nchains * NC, C);
-  const size_t rec0 = (size_t)chain * NC;
   tile_fetch<CT, D, C>(rq, qg, rs, 0, p.T, tid);
   tile_fetch<CT, D, C>(rk, kg, rs, 0, p.T, tid);
   tile_fetch<CT, D, C>(rv, vg, rs, 0, p.T, tid);
-  if constexpr (PREP) prep_fetch<CT, C, NT>(rp, po, rec0, tid);
-  else if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, p.aw + soff, p.g + soff, st, 0, p.T, lane);
+  if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, p.aw + soff, p.g + soff, st, 0, p.T, lane);
 
   for (int c = 0; c < NC; ++c) {
     const int t0 = c * C;
@@ -160,19 +99,17 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
     tile_commit<CT, D, C>(rq, sm.q, nullptr, tid);
     tile_commit<CT, D, C>(rk, sm.k, sm.kt, tid);
     tile_commit<CT, D, C>(rv, nullptr, sm.vt, tid);
-    if constexpr (PREP) prep_commit<CT, C, LDC, NT>(rp, sm.ta, sm.tb, sm.aq, sm.gam, sm.dec, tid);
-    else if (wave == 0) scal_commit<C>(cs, rsc, lane);
+    if (wave == 0) scal_commit<C>(cs, rsc, lane);
     __syncthreads();
     // prefetch the next chunk while this one computes
     if (c + 1 < NC) {
       tile_fetch<CT, D, C>(rq, qg, rs, t0 + C, p.T, tid);
       tile_fetch<CT, D, C>(rk, kg, rs, t0 + C, p.T, tid);
       tile_fetch<CT, D, C>(rv, vg, rs, t0 + C, p.T, tid);
-      if constexpr (PREP) prep_fetch<CT, C, NT>(rp, po, rec0 + c + 1, tid);
-      else if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, p.aw + soff, p.g + soff, st, t0 + C, p.T, lane);
+      if (wave == 0) scal_fetch<C>(rsc, p.ae + soff, p.aw + soff, p.g + soff, st, t0 + C, p.T, lane);
     }
 
-    if constexpr (!PREP) {
+    {
       // ---- grams: L (K K^T) and Aq (Q K^T) ----
       chunk_grams<CT, D, C>(sm.k, sm.q, sm.L, sm.LT, sm.G, sm.ae, wave, lane,
                             [&](int i, int j0, const float* v) { st4(&sm.aq[i * LDC + j0], v[0], v[1], v[2], v[3]); });
@@ -233,12 +170,12 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
 #pragma unroll
       for (int vt = 0; vt < NVT; ++vt)
         Sf[kb][vt] = acc_frag((CT*)nullptr, S[kb * TPS][vt], S[kb * TPS + TPS - 1][vt]);
-    if (p.chunk_states) {  // stash S0 for the backward: this thread's fragments (stash_state layout)
-      Frag* cst = (Frag*)p.chunk_states + ((size_t)chain * NC + c) * (NT * Dm::STASH_FRAGS);
+    if (p.chunk_states) {  // stash S0 for the backward (stash_state layout)
+      Frag* cst = (Frag*)p.chunk_states + rec_index(chain, c, nchains) * (D * D / FragLen<CT>::value);
 #pragma unroll
       for (int kb = 0; kb < NDT / TPS; ++kb)
 #pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) cst[(kb * NVT + vt) * NT + tid] = Sf[kb][vt];
+        for (int vt = 0; vt < NVT; ++vt) cst[stash_frag_index<CT, D>(kb, wave * NVT + vt, lane)] = Sf[kb][vt];
     }
     __syncthreads();   // -Wm complete
 
@@ -253,7 +190,7 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
       }
     }
     if (p.chunk_states) {  // stash R after all states: raw accumulator tiles (stash_tiles layout)
-      CT* rst = (CT*)p.chunk_states + (size_t)nchains * NC * D * D + ((size_t)chain * NC + c) * (C * D);
+      CT* rst = (CT*)p.chunk_states + (size_t)nchains * NC * D * D + rec_index(chain, c, nchains) * (C * D);
 #pragma unroll
       for (int it = 0; it < NCT; ++it)
 #pragma unroll
@@ -360,18 +297,11 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
 
 template <typename CT, int D, int C>
 static int launch_fwd(const DeltaArgs& a, hipStream_t stream) {
-  const int nblocks = a.B * a.H * a.M;
-  if (a.prep) {
-    int rc = delta_prep_dispatch(a, stream);
-    if (rc) return rc;
-    hipLaunchKernelGGL((delta_fwd_kernel<CT, D, C, true>), dim3(nblocks), dim3(Dims<CT, D, C>::NT), 0, stream, a);
-  } else {
-    hipLaunchKernelGGL((delta_fwd_kernel<CT, D, C, false>), dim3(nblocks), dim3(Dims<CT, D, C>::NT), 0, stream, a);
-  }
+  hipLaunchKernelGGL((delta_fwd_kernel<CT, D, C>), dim3(a.B * a.H * a.M), dim3(Dims<CT, D, C>::NT), 0, stream, a);
   return check_launch("delta_fwd_kernel");
 }
 
-int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream) {
+static int delta_fused_dispatch(const DeltaArgs& a, hipStream_t stream) {
   if (a.dtype == GDNX_DTYPE_BF16) {
     if (a.D == 128 && a.C == 64) return launch_fwd<bf16, 128, 64>(a, stream);
     if (a.D == 128 && a.C == 32) return launch_fwd<bf16, 128, 32>(a, stream);
@@ -384,6 +314,24 @@ int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream) {
     if (a.D == 64 && a.C == 16) return launch_fwd<float, 64, 16>(a, stream);
   }
   return set_error(GDNX_ERR_SHAPE, "unsupported head dim %d / chunk %d for this dtype", a.D, a.C);
+}
+
+// With somewhere to put the per-chunk operands (the prep region of
+// chunk_states, else the workspace) the forward is the parallel prep kernel
+// plus the value-split lean scan; the scored variant (|r_t| needs every value
+// column of a token in one workgroup) and calls without either buffer run
+// the fused single-kernel scan.  A stash for the backward always gets its
+// prep records, which the reverse scan reads.
+int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream) {
+  DeltaArgs b = a;
+  if (a.chunk_states) b.prep = (char*)a.chunk_states + delta_stash_bytes(a.B * a.H * a.M, a.T, a.D, a.C, a.dtype);
+  if (b.prep && !a.r_norm) {
+    const int rc = delta_prep_dispatch(b, stream);
+    return rc ? rc : delta_scan_fwd_dispatch(b, stream);
+  }
+  const int rc = delta_fused_dispatch(a, stream);
+  if (rc || !a.chunk_states) return rc;
+  return delta_prep_dispatch(b, stream);
 }
 
 }  // namespace gdnx

@@ -1,16 +1,20 @@
 // Per-chunk operands of the chunked delta rule that do not depend on the
 // carried state, computed for every (b, h, chunk) and lane in parallel
-// (gfx950).  The sequential forward scan then only carries the state.
+// (gfx950).  The sequential scans (delta_scan.hip) then only carry the
+// state (forward) or its gradient (backward).
 //
 // For chain (b, h, m) and chunk c with inclusive log-decay prefix G (clamped
-// to [kLogFloor, 0] per token, as in the scan):
+// to [kLogFloor, 0] per token):
 //   L  = (exp(G_i - G_j) a_e,i k_i . k_j)_{j<i},   T = (I + L)^-1
-//   TA = T diag(a_w),  TB = T diag(a_e exp(G)),  Aq = (exp(G_i - G_j) q_i . k_j)_{j<=i}
-//   gam = exp(G),  dec = exp(G_last - G)
-// (the chunk algebra of the forward kernel; reference chunk structure
-// gdn3/gdn3_upgrade.py:467-521, decay ratios replaced by log-space
-// differences).  One workgroup per (b, h, chunk) stages K and Q once for the
-// M lanes, which share them.
+//   Aq = (exp(G_i - G_j) q_i . k_j)_{j<=i}
+//   gam = exp(G),  dec = exp(G_last - G),  aeg = a_e exp(G),  a_w
+// (the reference's chunk structure gdn3/gdn3_upgrade.py:467-521 and the
+// KMD-2 chunk derivation gdn3/kmd2_fast_scan.py:1-18, with the decay ratios
+// prefix_i / prefix_j replaced by log-space differences, which never
+// underflow).  One workgroup per (b, h, chunk): the raw grams K K^T and
+// Q K^T are formed once on MFMA and kept in registers, then each of the M
+// lanes (which share q and k) applies its own decay and erase scaling,
+// inverts its unit-lower L by 16x16 blocks and stores T, Aq and the scalars.
 #include "delta_common.hpp"
 #include "gdnx_internal.hpp"
 
@@ -21,33 +25,35 @@ struct alignas(16) PrepSmem {
   typedef Dims<CT, D, C> Dm;
   CT q[C * Dm::LDD];
   CT k[C * Dm::LDD];
-  CT ta[C * Dm::LDC];
-  CT tb[C * Dm::LDC];
-  CT aq[C * Dm::LDC];
+  CT t[C * Dm::LDC];    // T of the current lane (strictly upper tiles stay zero)
+  CT aq[C * Dm::LDC];   // Aq of the current lane (same)
   float L[C * Dm::LDF];
   float LT[C * Dm::LDT];
   float Td[C * Dm::LDT];
   float G[C], gam[C], dec[C], ae[C], aw[C];
 };
 
-// [C][LDC] LDS tile -> [C][C] global, 16-byte stores
+// [C][LDC] LDS tile -> row-major [C][C] global, 16-byte stores
 template <typename CT, int C, int LDC>
 __device__ __forceinline__ void store_cc(CT* __restrict__ dst, const CT* src, int tid, int nt) {
   constexpr int PER = 16 / sizeof(CT), NU = C * C / PER;
   for (int u = tid; u < NU; u += nt) {
     const int i = (u * PER) / C, j = (u * PER) % C;
-    *(uint4*)&dst[(size_t)u * PER] = *(const uint4*)&src[i * LDC + j];
+    const uint2* s = (const uint2*)&src[i * LDC + j];
+    *(uint4*)&dst[(size_t)u * PER] = make_uint4(s[0].x, s[0].y, s[1].x, s[1].y);
   }
 }
 
 template <typename CT, int D, int C>
 __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_prep_kernel(DeltaArgs p) {
   typedef Dims<CT, D, C> Dm;
-  constexpr int LDC = Dm::LDC, NT = Dm::NT;
+  constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF, NT = Dm::NT, NW = Dm::NW, NCT = Dm::NCT;
+  constexpr int NP = NCT * (NCT + 1) / 2;          // lower 16x16 tile pairs of a C x C gram
+  constexpr int NTPW = (2 * NP + NW - 1) / NW;      // gram tiles per wave (K K^T and Q K^T)
   __shared__ PrepSmem<CT, D, C> sm;
 
   const int tid = threadIdx.x;
-  const int wave = tid >> 6, lane = tid & 63;
+  const int wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
   const int NC = (p.T + C - 1) / C;
   const int nblk = p.B * p.H * NC;
   const int blk = xcd_remap(blockIdx.x, nblk);
@@ -56,45 +62,95 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_prep_kernel(DeltaA
   const size_t rs = (size_t)p.H * D;
   const size_t qoff = ((size_t)b * p.T * p.H + h) * D;
   const size_t st = (size_t)p.H * p.M;
-  const PrepPtrs<CT> po = prep_ptrs<CT>(p.prep, (size_t)p.B * p.H * p.M * NC, C);
+  const size_t NR = (size_t)p.B * p.H * p.M * NC;
+  const PrepPtrs<CT> po = prep_ptrs<CT>(p.prep, NR, C);
 
-  for (int i = tid; i < C * LDC; i += NT) {  // never-written upper parts read as zero
-    sm.ta[i] = from_f<CT>(0.f);
-    sm.tb[i] = from_f<CT>(0.f);
+  for (int i = tid; i < C * LDC; i += NT) {  // strictly upper tiles are never written
+    sm.t[i] = from_f<CT>(0.f);
     sm.aq[i] = from_f<CT>(0.f);
   }
   {
-    TileRegs rq, rk;
-    tile_fetch<CT, D, C>(rq, (const CT*)p.q + qoff, rs, t0, p.T, tid);
-    tile_fetch<CT, D, C>(rk, (const CT*)p.k + qoff, rs, t0, p.T, tid);
-    tile_commit<CT, D, C>(rq, sm.q, nullptr, tid);
-    tile_commit<CT, D, C>(rk, sm.k, nullptr, tid);
+    Stage<CT, C, D, 1, NT> sq, sk;
+    const unsigned rsb = (unsigned)(rs * sizeof(CT)), nb = (unsigned)min(C, p.T - t0) * rsb;
+    sq.fetch(buf_rsrc((const CT*)p.q + qoff + (size_t)t0 * rs, nb), rsb, tid);
+    sk.fetch(buf_rsrc((const CT*)p.k + qoff + (size_t)t0 * rs, nb), rsb, tid);
+    sq.template commit_nat<LDD>(sm.q, tid);
+    sk.template commit_nat<LDD>(sm.k, tid);
   }
+  __syncthreads();
+
+  // raw grams, kept in registers: task s of this wave is tile pair
+  // (wave + NW s) >> 1 of K K^T (even) or Q K^T (odd)
+  f32x4 gram[NTPW];
+#pragma unroll
+  for (int s = 0; s < NTPW; ++s) {
+    const int task = wave + NW * s;
+    gram[s] = zero4();
+    if (task < 2 * NP) {
+      int it, jt;
+      tri_pair(task >> 1, it, jt);
+      // K K^T: acc[ii] = k_i . k_j, i = 16 it + 4 g + ii, j = 16 jt + n
+      // Q K^T: acc[ii] = q_i . k_j, i = 16 it + n,        j = 16 jt + 4 g + ii
+      const CT* arow = &sm.k[(((task & 1) == 0 ? it : jt) * 16 + n16) * LDD];
+      const CT* brow = ((task & 1) == 0) ? &sm.k[(jt * 16 + n16) * LDD] : &sm.q[(it * 16 + n16) * LDD];
+      gram[s] = tile_nt<CT, D>(arow, brow, g4);
+    }
+  }
+
   const ChunkScalars cs{sm.G, sm.gam, sm.dec, sm.ae, sm.aw, nullptr};
   for (int m = 0; m < p.M; ++m) {
     const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + m;
+    const size_t rec = rec_index(((size_t)b * p.H + h) * p.M + m, c, (size_t)p.B * p.H * p.M);
     if (wave == 0) prep_scalars<C>(cs, p.ae + soff, p.aw + soff, p.g + soff, st, t0, p.T, lane);
     __syncthreads();
-    chunk_grams<CT, D, C>(sm.k, sm.q, sm.L, sm.LT, sm.G, sm.ae, wave, lane,
-                          [&](int i, int j0, const float* v) { st4(&sm.aq[i * LDC + j0], v[0], v[1], v[2], v[3]); });
-    __syncthreads();
-    invert_unit_lower<C>(
-        sm.L, sm.LT, sm.Td, wave, lane,
-        [&](int j) { return make_float2(sm.aw[j], sm.ae[j] * sm.gam[j]); },
-        [&](int i, int j, float t, float2 f) {
-          sm.ta[i * LDC + j] = from_f<CT>(t * f.x);
-          sm.tb[i * LDC + j] = from_f<CT>(t * f.y);
-        });
-    __syncthreads();
-    const size_t rec = (((size_t)b * p.H + h) * p.M + m) * NC + c;  // chain-major, chunks contiguous
-    store_cc<CT, C, LDC>(po.ta + rec * C * C, sm.ta, tid, NT);
-    store_cc<CT, C, LDC>(po.tb + rec * C * C, sm.tb, tid, NT);
-    store_cc<CT, C, LDC>(po.aq + rec * C * C, sm.aq, tid, NT);
-    if (tid < C) {
-      po.sc[rec * 2 * C + tid] = sm.gam[tid];
-      po.sc[rec * 2 * C + C + tid] = sm.dec[tid];
+    // this lane's L (fp32, plus transposed diagonal blocks) and Aq
+#pragma unroll
+    for (int s = 0; s < NTPW; ++s) {
+      const int task = wave + NW * s;
+      if (task < 2 * NP) {
+        int it, jt;
+        tri_pair(task >> 1, it, jt);
+        if ((task & 1) == 0) {
+          const f32x4 G4 = *(const f32x4*)&sm.G[it * 16 + 4 * g4];
+          const f32x4 ae4 = *(const f32x4*)&sm.ae[it * 16 + 4 * g4];
+          const int j = jt * 16 + n16;
+          const float Gj = sm.G[j];
+          f32x4 val;
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const int i = it * 16 + 4 * g4 + ii;
+            val[ii] = (j < i) ? __expf(G4[ii] - Gj) * ae4[ii] * gram[s][ii] : 0.f;
+            sm.L[i * LDF + j] = val[ii];
+          }
+          if (jt == it) *(f32x4*)&sm.LT[j * 20 + 4 * g4] = val;
+        } else {
+          const int i = it * 16 + n16;
+          const float Gi = sm.G[i];
+          const f32x4 Gj4 = *(const f32x4*)&sm.G[jt * 16 + 4 * g4];
+          float v[4];
+#pragma unroll
+          for (int ii = 0; ii < 4; ++ii) {
+            const int j = jt * 16 + 4 * g4 + ii;
+            v[ii] = (j <= i) ? __expf(Gi - Gj4[ii]) * gram[s][ii] : 0.f;
+          }
+          st4(&sm.aq[i * LDC + jt * 16 + 4 * g4], v[0], v[1], v[2], v[3]);
+        }
+      }
     }
     __syncthreads();
+    invert_unit_lower<C>(
+        sm.L, sm.LT, sm.Td, wave, lane, [&](int) { return 0; },
+        [&](int i, int j, float t, int) { sm.t[i * LDC + j] = from_f<CT>(t); });
+    __syncthreads();
+    store_cc<CT, C, LDC>(po.t + rec * C * C, sm.t, tid, NT);
+    store_cc<CT, C, LDC>(po.aq + rec * C * C, sm.aq, tid, NT);
+    if (wave == 0 && lane < C) {
+      float* sc = po.sc + rec * kNumSc * C;
+      sc[kScGam * C + lane] = sm.gam[lane];
+      sc[kScDec * C + lane] = sm.dec[lane];
+      sc[kScAeg * C + lane] = sm.ae[lane] * sm.gam[lane];
+      sc[kScAw * C + lane] = sm.aw[lane];
+    }
   }
 }
 
@@ -122,8 +178,7 @@ int delta_prep_dispatch(const DeltaArgs& a, hipStream_t stream) {
 
 size_t delta_prep_bytes(int nchains, int T, int C, int dtype) {
   const size_t NR = (size_t)nchains * ((T + C - 1) / C);
-  const size_t es = dtype == GDNX_DTYPE_BF16 ? 2 : 4;
-  return NR * (3 * (size_t)C * C * es + 2 * (size_t)C * 4);
+  return NR * prep_bytes_per_record(C, dtype == GDNX_DTYPE_BF16 ? 2 : 4);
 }
 
 }  // namespace gdnx

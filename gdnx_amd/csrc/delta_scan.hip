@@ -1,0 +1,500 @@
+// Lean sequential scans of the chunked delta rule (gfx950), fed by the
+// parallel per-chunk operands of delta_prep.hip.
+//
+// Per chain (b, h, m) and chunk of C tokens (T, Aq, gam, dec, aeg, a_w from
+// the prep record; see delta_prep.hip):
+//   forward   U  = T diag(a_w) V,  Wm = T diag(aeg) K
+//             R  = U - Wm S0                                 (net writes)
+//             Y  = diag(gam) Q S0 + Aq R
+//             S  = gam_last S0 + K^T diag(dec) R
+//   backward  dR = diag(dec) K dS + Aq^T dY,   dB = T^T dR
+//             dS0 = gam_last dS + Q^T diag(gam) dY - K^T diag(aeg) dB
+// (gdn3/_reference_recurrence.py:60-84 in the dense regime and
+// research/kernel_ab/ref_scan.py:40-45, restated per chunk).  Every product
+// above is independent across value columns given the prep operands, so a
+// chain's value columns are split over NVB workgroups of NWV waves, each wave
+// owning 16 columns of the fp32 state in registers.  With 256 chains this
+// puts several independent workgroups on every CU, which hide each other's
+// MFMA, LDS and memory latency; the only per-chunk critical path left is
+// the two dependent products R -> S (dR -> dS backward).
+#include "delta_common.hpp"
+#include "gdnx_internal.hpp"
+
+namespace gdnx {
+
+template <typename CT, int D, int C, int NWV>
+struct ScanDims {
+  typedef typename FragT<CT>::type Frag;
+  static constexpr int KS = FragT<CT>::KSTEP;
+  static constexpr int TPS = FragT<CT>::TPS;
+  static constexpr int NT = 64 * NWV;       // threads per workgroup
+  static constexpr int BV = 16 * NWV;       // value columns per workgroup
+  static constexpr int NVB = D / BV;        // workgroups per chain
+  static constexpr int NDT = D / 16;
+  static constexpr int NCT = C / 16;
+  static constexpr int LDD = D + 4;
+  static constexpr int LDC = C + 4;
+  static constexpr int DTW = NDT / NWV;     // key tiles of -Wm formed per wave
+  static_assert(NDT % NWV == 0 && D % BV == 0, "value split must tile the head dim");
+  static_assert(C % KS == 0, "chunk must be a multiple of the MFMA k-step");
+};
+
+// ---------------------------------------------------------------------------
+// forward
+// ---------------------------------------------------------------------------
+template <typename CT, int D, int C, int NWV>
+struct alignas(16) ScanFwdSmem {
+  typedef ScanDims<CT, D, C, NWV> Sd;
+  CT q[C * Sd::LDD];     // Q rows
+  CT kt[D * Sd::LDC];    // K^T
+  CT vt[Sd::BV * Sd::LDC];  // V^T of this workgroup's value columns
+  CT t[C * Sd::LDC];     // T rows
+  CT aq[C * Sd::LDC];    // Aq rows
+  CT wm[C * Sd::LDD];    // -Wm rows
+  float sc[kNumSc * C];  // gam, dec, aeg, a_w
+};
+
+template <typename CT, int D, int C, int NWV, bool STASH>
+__global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) delta_scan_fwd_kernel(DeltaArgs p) {
+  typedef ScanDims<CT, D, C, NWV> Sd;
+  typedef typename Sd::Frag Frag;
+  constexpr int KS = Sd::KS, TPS = Sd::TPS, NDT = Sd::NDT, NCT = Sd::NCT, NT = Sd::NT;
+  constexpr int LDD = Sd::LDD, LDC = Sd::LDC, BV = Sd::BV, DTW = Sd::DTW;
+  __shared__ ScanFwdSmem<CT, D, C, NWV> sm;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
+  const int nchains = p.B * p.H * p.M;
+  const int work = xcd_remap(blockIdx.x, nchains * Sd::NVB);
+  const int chain = work / Sd::NVB, vb = work % Sd::NVB;
+  const int m = chain % p.M, h = (chain / p.M) % p.H, b = chain / (p.M * p.H);
+  const int V = vb * NWV + wave;          // this wave's 16-column value tile
+  const int NC = (p.T + C - 1) / C;
+  const size_t rs = (size_t)p.H * D;
+  const size_t qoff = ((size_t)b * p.T * p.H + h) * D;
+  const size_t NR = (size_t)nchains * NC;
+  // record of chunk c: rec_index(chain, c, nchains)
+  const PrepPtrs<CT> pp = prep_ptrs<CT>(p.prep, NR, C);
+  const CT* qg = (const CT*)p.q + qoff;
+  const CT* kg = (const CT*)p.k + qoff;
+  const CT* vg = (const CT*)p.v + qoff + vb * BV;
+
+  f32x4 S[NDT];   // S[dt][i] = S0[16 dt + 4 g + i][16 V + n]
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    S[dt] = zero4();
+    if (p.s0) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) S[dt][i] = p.s0[(size_t)chain * D * D + (dt * 16 + 4 * g4 + i) * D + 16 * V + n16];
+    }
+  }
+  __builtin_amdgcn_s_waitcnt(0);   // initial state in registers before the loop's own loads
+
+  // Chunk tiles are fetched a chunk ahead: q by every thread, and K, V, T,
+  // Aq (with the scalars) each by one group of NWV/4 waves, so every 16-byte
+  // unit is loaded once.  Memory operations are unconditional within a
+  // group (tail tokens go through buffer resources), so the compiler's wait
+  // for the prefetched loads never covers the stores issued after them.
+  constexpr int GW = NWV / 4, GT = 64 * GW;
+  static_assert(NWV % 4 == 0, "four load groups");
+  const int grp = wave / GW, gt = tid - grp * GT;
+  Stage<CT, C, D, 1, NT> pq;
+  Stage<CT, C, D, 4, GT> pk;
+  Stage<CT, C, BV, 4, GT> pv;
+  Stage<CT, C, C, 1, GT> pt, pa;
+  ScalStage<kNumSc * C, GT> ps;
+  const unsigned rsb = (unsigned)(rs * sizeof(CT));
+  const unsigned ysb = (unsigned)((size_t)p.H * p.M * D * sizeof(CT));
+  auto fetch = [&](int c) {
+    const int t0 = c * C;
+    const unsigned nb = (unsigned)min(C, p.T - t0) * rsb;
+    pq.fetch(buf_rsrc(qg + (size_t)t0 * rs, nb), rsb, tid);
+    if (grp == 0) {
+      pk.fetch(buf_rsrc(kg + (size_t)t0 * rs, nb), rsb, gt);
+    } else if (grp == 1) {
+      pv.fetch(buf_rsrc(vg + (size_t)t0 * rs, nb), rsb, gt);
+    } else if (grp == 2) {
+      pt.fetch_dense(pp.t + rec_index(chain, c, nchains) * C * C, gt);
+      ps.fetch(pp.sc + rec_index(chain, c, nchains) * kNumSc * C, gt);
+    } else {
+      pa.fetch_dense(pp.aq + rec_index(chain, c, nchains) * C * C, gt);
+    }
+  };
+  fetch(0);
+  __builtin_amdgcn_s_waitcnt(0);   // the loop's waits then only track its own loads and stores
+
+  for (int c = 0; c < NC; ++c) {
+    const int t0 = c * C;
+    const size_t rec = rec_index(chain, c, nchains);
+    __syncthreads();
+    pq.template commit_nat<LDD>(sm.q, tid);
+    if (grp == 0) {
+      pk.template commit_tr<LDC>(sm.kt, gt);
+    } else if (grp == 1) {
+      pv.template commit_tr<LDC>(sm.vt, gt);
+    } else if (grp == 2) {
+      pt.template commit_nat<LDC>(sm.t, gt);
+      ps.commit(sm.sc, gt);
+    } else {
+      pa.template commit_nat<LDC>(sm.aq, gt);
+    }
+    __syncthreads();
+    fetch(min(c + 1, NC - 1));   // (the last iteration refetches its own chunk, unused)
+    const float* gam = &sm.sc[kScGam * C];
+    const float* dec = &sm.sc[kScDec * C];
+    const float* aeg = &sm.sc[kScAeg * C];
+    const float* aw = &sm.sc[kScAw * C];
+
+    // ---- -Wm (rows i, key cols d) via Wm^T = K^T (T diag(aeg))^T; this wave's key tiles ----
+    {
+      Frag bt[NCT][C / KS];
+#pragma unroll
+      for (int it = 0; it < NCT; ++it)
+#pragma unroll
+        for (int kb = 0; kb < C / KS; ++kb)
+          bt[it][kb] = frag_scale(ld_frag(&sm.t[(it * 16 + n16) * LDC + kb * KS], g4), aeg + kb * KS, g4);
+#pragma unroll
+      for (int dd = 0; dd < DTW; ++dd) {
+        const int dt = dd * NWV + wave;
+        Frag a[C / KS];
+#pragma unroll
+        for (int kb = 0; kb < C / KS; ++kb) a[kb] = ld_frag(&sm.kt[(dt * 16 + n16) * LDC + kb * KS], g4);
+#pragma unroll
+        for (int it = 0; it < NCT; ++it) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int kb = 0; kb < C / KS; ++kb) mma(acc, a[kb], bt[it][kb]);
+          // acc[ii] = Wm[i = 16 it + n][d = 16 dt + 4 g + ii]
+          st4(&sm.wm[(it * 16 + n16) * LDD + dt * 16 + 4 * g4], -acc[0], -acc[1], -acc[2], -acc[3]);
+        }
+      }
+    }
+    // ---- U = T diag(a_w) V on this wave's columns, into the R accumulators ----
+    f32x4 Racc[NCT];
+    {
+      Frag bv[C / KS];
+#pragma unroll
+      for (int kb = 0; kb < C / KS; ++kb) bv[kb] = ld_frag(&sm.vt[(wave * 16 + n16) * LDC + kb * KS], g4);
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) {
+        Racc[it] = zero4();
+#pragma unroll
+        for (int kb = 0; kb < C / KS; ++kb)
+          mma(Racc[it], frag_scale(ld_frag(&sm.t[(it * 16 + n16) * LDC + kb * KS], g4), aw + kb * KS, g4), bv[kb]);
+      }
+    }
+    // ---- S0 as fragments over k = d; stash for the backward ----
+    Frag Sf[NDT / TPS];
+#pragma unroll
+    for (int kb = 0; kb < NDT / TPS; ++kb) Sf[kb] = acc_frag((CT*)nullptr, S[kb * TPS], S[kb * TPS + TPS - 1]);
+    if constexpr (STASH) {
+      Frag* cst = (Frag*)p.chunk_states + rec * (D * D / FragLen<CT>::value);
+#pragma unroll
+      for (int kb = 0; kb < NDT / TPS; ++kb) cst[stash_frag_index<CT, D>(kb, V, lane)] = Sf[kb];
+    }
+    __syncthreads();   // -Wm complete
+
+    // ---- R = U - Wm S0 ----
+#pragma unroll
+    for (int kb = 0; kb < NDT / TPS; ++kb)
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) mma(Racc[it], ld_frag(&sm.wm[(it * 16 + n16) * LDD + kb * KS], g4), Sf[kb]);
+    if constexpr (STASH) {
+      CT* rst = (CT*)p.chunk_states + NR * D * D + rec * (C * D);
+#pragma unroll
+      for (int it = 0; it < NCT; ++it)
+        st4(rst + ((it * NDT + V) * 64 + lane) * 4, Racc[it][0], Racc[it][1], Racc[it][2], Racc[it][3]);
+    }
+    // ---- Y = diag(gam) Q S0 + Aq R ----
+    {
+      Frag Rf[NCT / TPS];
+#pragma unroll
+      for (int kb = 0; kb < NCT / TPS; ++kb) Rf[kb] = acc_frag((CT*)nullptr, Racc[kb * TPS], Racc[kb * TPS + TPS - 1]);
+      // this chain's rows of y in this chunk; rows past T fall outside the resource
+      const __amdgpu_buffer_rsrc_t yr =
+          buf_rsrc((CT*)p.y + (((size_t)(b * p.T + t0) * p.H + h) * p.M + m) * D, (unsigned)min(C, p.T - t0) * ysb);
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) {
+        f32x4 Y = zero4();
+#pragma unroll
+        for (int kb = 0; kb < NDT / TPS; ++kb) mma(Y, ld_frag(&sm.q[(it * 16 + n16) * LDD + kb * KS], g4), Sf[kb]);
+        Y *= *(const f32x4*)&gam[it * 16 + 4 * g4];
+#pragma unroll
+        for (int kb = 0; kb < NCT / TPS; ++kb) mma(Y, ld_frag(&sm.aq[(it * 16 + n16) * LDC + kb * KS], g4), Rf[kb]);
+        // transposed tile: lane (g, n) holds row 16 it + n, columns 4 g .. 4 g + 3
+        const f32x4 yt = tile_transpose((CT*)nullptr, Y, lane);
+        buf_store4(yr, (unsigned)(it * 16 + n16) * ysb + (16 * V + 4 * g4) * sizeof(CT), (const CT*)nullptr, yt[0],
+                   yt[1], yt[2], yt[3]);
+      }
+    }
+    // ---- S = gam_last S0 + K^T diag(dec) R ----
+    {
+      const float gl = gam[C - 1];
+      Frag RDf[NCT / TPS];
+#pragma unroll
+      for (int kb = 0; kb < NCT / TPS; ++kb) {
+        const f32x4 d0 = *(const f32x4*)&dec[kb * KS + 4 * g4];
+        const f32x4 d1 = *(const f32x4*)&dec[kb * KS + (TPS - 1) * 16 + 4 * g4];
+        RDf[kb] = acc_frag((CT*)nullptr, Racc[kb * TPS], Racc[kb * TPS + TPS - 1], d0, d1);
+      }
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        S[dt] *= gl;
+#pragma unroll
+        for (int kb = 0; kb < NCT / TPS; ++kb) mma(S[dt], ld_frag(&sm.kt[(dt * 16 + n16) * LDC + kb * KS], g4), RDf[kb]);
+      }
+    }
+  }
+
+  if (p.s_out) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p.s_out[(size_t)chain * D * D + (dt * 16 + 4 * g4 + i) * D + 16 * V + n16] = S[dt][i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// backward: reverse scan of the state gradient
+// ---------------------------------------------------------------------------
+template <typename CT, int D, int C, int NWV>
+struct alignas(16) ScanBwdSmem {
+  typedef ScanDims<CT, D, C, NWV> Sd;
+  CT k[C * Sd::LDD];        // K rows
+  CT kt[D * Sd::LDC];       // K^T
+  CT qt[D * Sd::LDC];       // Q^T
+  CT dyt[Sd::BV * Sd::LDC]; // dY^T of this workgroup's value columns
+  CT tt[C * Sd::LDC];       // T^T
+  CT aqt[C * Sd::LDC];      // Aq^T
+  float sc[kNumSc * C];
+};
+
+template <typename CT, int D, int C, int NWV>
+__global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) delta_scan_bwd_kernel(DeltaBwdArgs p) {
+  typedef ScanDims<CT, D, C, NWV> Sd;
+  typedef typename Sd::Frag Frag;
+  constexpr int KS = Sd::KS, TPS = Sd::TPS, NDT = Sd::NDT, NCT = Sd::NCT, NT = Sd::NT;
+  constexpr int LDD = Sd::LDD, LDC = Sd::LDC, BV = Sd::BV;
+  __shared__ ScanBwdSmem<CT, D, C, NWV> sm;
+
+  const int tid = threadIdx.x;
+  const int wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
+  const int nchains = p.B * p.H * p.M;
+  const int work = xcd_remap(blockIdx.x, nchains * Sd::NVB);
+  const int chain = work / Sd::NVB, vb = work % Sd::NVB;
+  const int m = chain % p.M, h = (chain / p.M) % p.H, b = chain / (p.M * p.H);
+  const int V = vb * NWV + wave;
+  const int NC = (p.T + C - 1) / C;
+  const size_t rs = (size_t)p.H * D;
+  const size_t qoff = ((size_t)b * p.T * p.H + h) * D;
+  const size_t rsy = (size_t)p.H * p.M * D;
+  const size_t yoff = (((size_t)b * p.T * p.H + h) * p.M + m) * D + vb * BV;
+  const size_t NR = (size_t)nchains * NC;
+  // record of chunk c: rec_index(chain, c, nchains)
+  // the forward's prep records sit after its state and net-write stashes
+  const PrepPtrs<CT> pp = prep_ptrs<CT>((CT*)p.s_stash + NR * ((size_t)D * D + (size_t)C * D), NR, C);
+  const CT* qg = (const CT*)p.q + qoff;
+  const CT* kg = (const CT*)p.k + qoff;
+  const CT* yg = (const CT*)p.dy + yoff;
+
+  f32x4 dS[NDT];
+#pragma unroll
+  for (int dt = 0; dt < NDT; ++dt) {
+    dS[dt] = zero4();
+    if (p.ds_final) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        dS[dt][i] = p.ds_final[(size_t)chain * D * D + (dt * 16 + 4 * g4 + i) * D + 16 * V + n16];
+    }
+  }
+
+  __builtin_amdgcn_s_waitcnt(0);   // initial gradient in registers before the loop's own loads
+  // chunk tiles fetched a chunk ahead, one group of NWV/4 waves per tile
+  // (see the forward)
+  constexpr int GW = NWV / 4, GT = 64 * GW;
+  static_assert(NWV % 4 == 0, "four load groups");
+  const int grp = wave / GW, gt = tid - grp * GT;
+  Stage<CT, C, D, 4, GT> pq, pk;
+  Stage<CT, C, BV, 4, GT> py;
+  Stage<CT, C, C, 4, GT> pt, pa;
+  ScalStage<3 * C, GT> ps;   // gam, dec, aeg
+  const unsigned rsb = (unsigned)(rs * sizeof(CT));
+  const unsigned ysb = (unsigned)(rsy * sizeof(CT));
+  auto fetch = [&](int c) {
+    const int t0 = c * C;
+    const int nv = min(C, p.T - t0);
+    if (grp == 0) {
+      pq.fetch(buf_rsrc(qg + (size_t)t0 * rs, (unsigned)nv * rsb), rsb, gt);
+    } else if (grp == 1) {
+      pk.fetch(buf_rsrc(kg + (size_t)t0 * rs, (unsigned)nv * rsb), rsb, gt);
+    } else if (grp == 2) {
+      py.fetch(buf_rsrc(yg + (size_t)t0 * rsy, (unsigned)nv * ysb), ysb, gt);
+    } else {
+      pt.fetch_dense(pp.t + rec_index(chain, c, nchains) * C * C, gt);
+      pa.fetch_dense(pp.aq + rec_index(chain, c, nchains) * C * C, gt);
+      ps.fetch(pp.sc + rec_index(chain, c, nchains) * kNumSc * C, gt);
+    }
+  };
+  fetch(NC - 1);
+  __builtin_amdgcn_s_waitcnt(0);   // the loop's waits then only track its own loads and stores
+
+  for (int c = NC - 1; c >= 0; --c) {
+    const size_t rec = rec_index(chain, c, nchains);
+    __syncthreads();
+    if (grp == 0) {
+      pq.template commit_tr<LDC>(sm.qt, gt);
+    } else if (grp == 1) {
+      pk.template commit_nat<LDD>(sm.k, gt);
+      pk.template commit_tr<LDC>(sm.kt, gt);
+    } else if (grp == 2) {
+      py.template commit_tr<LDC>(sm.dyt, gt);
+    } else {
+      pt.template commit_tr<LDC>(sm.tt, gt);
+      pa.template commit_tr<LDC>(sm.aqt, gt);
+      ps.commit(sm.sc, gt);
+    }
+    __syncthreads();
+    fetch(max(c - 1, 0));   // (the first chunk refetches itself, unused)
+    const float* gam = &sm.sc[kScGam * C];
+    const float* dec = &sm.sc[kScDec * C];
+    const float* aeg = &sm.sc[kScAeg * C];
+
+    // ---- dS at the chunk end as fragments over k = d; stash ----
+    Frag dSf[NDT / TPS];
+#pragma unroll
+    for (int kb = 0; kb < NDT / TPS; ++kb) dSf[kb] = acc_frag((CT*)nullptr, dS[kb * TPS], dS[kb * TPS + TPS - 1]);
+    {
+      Frag* cst = (Frag*)p.ds_stash + rec * (D * D / FragLen<CT>::value);
+#pragma unroll
+      for (int kb = 0; kb < NDT / TPS; ++kb) cst[stash_frag_index<CT, D>(kb, V, lane)] = dSf[kb];
+    }
+    // ---- dR = diag(dec) K dS + Aq^T dY ----
+    Frag dYf[C / KS];
+#pragma unroll
+    for (int kb = 0; kb < C / KS; ++kb) dYf[kb] = ld_frag(&sm.dyt[(wave * 16 + n16) * LDC + kb * KS], g4);
+    f32x4 dR[NCT];
+#pragma unroll
+    for (int it = 0; it < NCT; ++it) {
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NDT / TPS; ++kb) mma(acc, ld_frag(&sm.k[(it * 16 + n16) * LDD + kb * KS], g4), dSf[kb]);
+      acc *= *(const f32x4*)&dec[it * 16 + 4 * g4];
+#pragma unroll
+      for (int kb = 0; kb < C / KS; ++kb) mma(acc, ld_frag(&sm.aqt[(it * 16 + n16) * LDC + kb * KS], g4), dYf[kb]);
+      dR[it] = acc;
+    }
+    // ---- dB = T^T dR; stash ----
+    Frag dBf[NCT / TPS];
+    {
+      Frag dRf[NCT / TPS];
+#pragma unroll
+      for (int kb = 0; kb < NCT / TPS; ++kb) dRf[kb] = acc_frag((CT*)nullptr, dR[kb * TPS], dR[kb * TPS + TPS - 1]);
+      f32x4 dB[NCT];
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) {
+        dB[it] = zero4();
+#pragma unroll
+        for (int kb = 0; kb < NCT / TPS; ++kb) mma(dB[it], ld_frag(&sm.tt[(it * 16 + n16) * LDC + kb * KS], g4), dRf[kb]);
+      }
+      CT* bst = (CT*)p.ds_stash + NR * D * D + rec * (C * D);
+#pragma unroll
+      for (int it = 0; it < NCT; ++it)
+        st4(bst + ((it * NDT + V) * 64 + lane) * 4, dB[it][0], dB[it][1], dB[it][2], dB[it][3]);
+      // fragments of -diag(aeg) dB over k = token
+#pragma unroll
+      for (int kb = 0; kb < NCT / TPS; ++kb) {
+        const f32x4 s0 = -*(const f32x4*)&aeg[kb * KS + 4 * g4];
+        const f32x4 s1 = -*(const f32x4*)&aeg[kb * KS + (TPS - 1) * 16 + 4 * g4];
+        dBf[kb] = acc_frag((CT*)nullptr, dB[kb * TPS], dB[kb * TPS + TPS - 1], s0, s1);
+      }
+    }
+    // ---- dS <- gam_last dS + Q^T diag(gam) dY - K^T diag(aeg) dB ----
+    {
+      const float gl = gam[C - 1];
+      Frag gYf[C / KS];
+#pragma unroll
+      for (int kb = 0; kb < C / KS; ++kb) gYf[kb] = frag_scale(dYf[kb], gam + kb * KS, g4);
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        dS[dt] *= gl;
+#pragma unroll
+        for (int kb = 0; kb < C / KS; ++kb) {
+          mma(dS[dt], ld_frag(&sm.qt[(dt * 16 + n16) * LDC + kb * KS], g4), gYf[kb]);
+          mma(dS[dt], ld_frag(&sm.kt[(dt * 16 + n16) * LDC + kb * KS], g4), dBf[kb]);
+        }
+      }
+    }
+  }
+  if (p.ds0) {
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) p.ds0[(size_t)chain * D * D + (dt * 16 + 4 * g4 + i) * D + 16 * V + n16] = dS[dt][i];
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dispatch: one workgroup of D/16 waves per chain (each wave 16 value
+// columns), so the chunk's tiles are loaded and the -Wm product formed once
+// per chain and shared through LDS
+// ---------------------------------------------------------------------------
+template <typename CT, int D, int C>
+struct ScanCfg {
+  static constexpr int NWV = D / 16;
+  static_assert(sizeof(ScanFwdSmem<CT, D, C, NWV>) <= 160 * 1024 && sizeof(ScanBwdSmem<CT, D, C, NWV>) <= 160 * 1024,
+                "scan LDS budget");
+};
+
+template <typename CT, int D, int C>
+static int launch_scan_fwd(const DeltaArgs& a, hipStream_t stream) {
+  constexpr int NWV = ScanCfg<CT, D, C>::NWV;
+  typedef ScanDims<CT, D, C, NWV> Sd;
+  if (a.chunk_states)
+    hipLaunchKernelGGL((delta_scan_fwd_kernel<CT, D, C, NWV, true>), dim3(a.B * a.H * a.M * Sd::NVB), dim3(Sd::NT),
+                       0, stream, a);
+  else
+    hipLaunchKernelGGL((delta_scan_fwd_kernel<CT, D, C, NWV, false>), dim3(a.B * a.H * a.M * Sd::NVB), dim3(Sd::NT),
+                       0, stream, a);
+  return check_launch("delta_scan_fwd_kernel");
+}
+
+template <typename CT, int D, int C>
+static int launch_scan_bwd(const DeltaBwdArgs& a, hipStream_t stream) {
+  constexpr int NWV = ScanCfg<CT, D, C>::NWV;
+  typedef ScanDims<CT, D, C, NWV> Sd;
+  hipLaunchKernelGGL((delta_scan_bwd_kernel<CT, D, C, NWV>), dim3(a.B * a.H * a.M * Sd::NVB), dim3(Sd::NT), 0,
+                     stream, a);
+  return check_launch("delta_scan_bwd_kernel");
+}
+
+int delta_scan_fwd_dispatch(const DeltaArgs& a, hipStream_t stream) {
+  if (a.dtype == GDNX_DTYPE_BF16) {
+    if (a.D == 128 && a.C == 64) return launch_scan_fwd<bf16, 128, 64>(a, stream);
+    if (a.D == 128 && a.C == 32) return launch_scan_fwd<bf16, 128, 32>(a, stream);
+    if (a.D == 64 && a.C == 64) return launch_scan_fwd<bf16, 64, 64>(a, stream);
+    if (a.D == 64 && a.C == 32) return launch_scan_fwd<bf16, 64, 32>(a, stream);
+  } else {
+    if (a.D == 128 && a.C == 32) return launch_scan_fwd<float, 128, 32>(a, stream);
+    if (a.D == 128 && a.C == 16) return launch_scan_fwd<float, 128, 16>(a, stream);
+    if (a.D == 64 && a.C == 32) return launch_scan_fwd<float, 64, 32>(a, stream);
+    if (a.D == 64 && a.C == 16) return launch_scan_fwd<float, 64, 16>(a, stream);
+  }
+  return set_error(GDNX_ERR_SHAPE, "scan: unsupported head_dim %d / chunk %d", a.D, a.C);
+}
+
+int delta_scan_bwd_dispatch(const DeltaBwdArgs& a, hipStream_t stream) {
+  if (a.dtype == GDNX_DTYPE_BF16) {
+    if (a.D == 128 && a.C == 64) return launch_scan_bwd<bf16, 128, 64>(a, stream);
+    if (a.D == 128 && a.C == 32) return launch_scan_bwd<bf16, 128, 32>(a, stream);
+    if (a.D == 64 && a.C == 64) return launch_scan_bwd<bf16, 64, 64>(a, stream);
+    if (a.D == 64 && a.C == 32) return launch_scan_bwd<bf16, 64, 32>(a, stream);
+  } else {
+    if (a.D == 128 && a.C == 32) return launch_scan_bwd<float, 128, 32>(a, stream);
+    if (a.D == 128 && a.C == 16) return launch_scan_bwd<float, 128, 16>(a, stream);
+    if (a.D == 64 && a.C == 32) return launch_scan_bwd<float, 64, 32>(a, stream);
+    if (a.D == 64 && a.C == 16) return launch_scan_bwd<float, 64, 16>(a, stream);
+  }
+  return set_error(GDNX_ERR_SHAPE, "backward scan: unsupported head_dim %d / chunk %d", a.D, a.C);
+}
+
+}  // namespace gdnx

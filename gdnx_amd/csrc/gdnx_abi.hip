@@ -79,9 +79,7 @@ extern "C" long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, i
   if (C == 0 || !valid_chunk(head_dim, dtype, C) || B < 1 || T < 0 || H < 1 || M < 1 ||
       (head_dim != 64 && head_dim != 128))
     return -1;
-  const long long nc = (T + C - 1) / C;
-  const long long esz = dtype == GDNX_DTYPE_BF16 ? 2 : 4;
-  return (long long)B * H * M * nc * ((long long)head_dim * head_dim + (long long)C * head_dim) * esz;
+  return (long long)(delta_stash_bytes(B * H * M, T, head_dim, C, dtype) + delta_prep_bytes(B * H * M, T, C, dtype));
 }
 
 static int fwd_common(const void* q, const void* k, const void* v, const float* a_e, const float* a_w,
@@ -141,7 +139,7 @@ static int bwd_common(const void* q, const void* k, const void* v, const float* 
   if (!a_e || !log_g || !dy) return set_error(GDNX_ERR_ARG, "a_e, log_g, dy must be non-null");
   if ((stages & 2) && (!a_w || !dq || !dk || !dv || !da_e || !da_w || !dlog_g))
     return set_error(GDNX_ERR_ARG, "a_w and the gradient outputs must be non-null");
-  if (!workspace || ((stages & 2) && !chunk_states))
+  if (!workspace || !chunk_states)
     return set_error(GDNX_ERR_WORKSPACE, "chunk_states (from the forward) and workspace are required");
   if (((uintptr_t)chunk_states & 15u) || ((uintptr_t)workspace & 15u) || !aligned16(dy))
     return set_error(GDNX_ERR_ARG, "chunk_states, workspace and dy must be 16-byte aligned");
@@ -165,9 +163,10 @@ extern "C" int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v,
 
 extern "C" int gdnx_delta_chunk_bwd_state(const void* q, const void* k, const float* a_e,
                                           const float* log_g, const void* dy, const float* dstate_out,
-                                          void* workspace, float* dstate0, int B, int T, int H, int M,
-                                          int head_dim, int chunk, int dtype, void* stream) {
-  return bwd_common(q, k, k, a_e, nullptr, log_g, dy, dstate_out, nullptr, workspace, nullptr, nullptr,
+                                          const void* chunk_states, void* workspace, float* dstate0, int B,
+                                          int T, int H, int M, int head_dim, int chunk, int dtype,
+                                          void* stream) {
+  return bwd_common(q, k, k, a_e, nullptr, log_g, dy, dstate_out, chunk_states, workspace, nullptr, nullptr,
                     nullptr, nullptr, nullptr, nullptr, dstate0, B, T, H, M, head_dim, chunk, dtype, 1,
                     stream);
 }
@@ -364,4 +363,36 @@ extern "C" int gdnx_kron_read(const float* A, const float* Bf, const float* U, c
     return set_error(GDNX_ERR_ARG, "pointers must be non-null");
   KronReadArgs a{A, Bf, U, Vb, x, y, ge, N, C, head_dim, P};
   return kron_read_dispatch(a, (hipStream_t)stream);
+}
+
+static int coeff_common(const void* k, const float* beta, int B, int T, int H, int M, int head_dim, int dtype) {
+  g_err[0] = 0;
+  if (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16)
+    return set_error(GDNX_ERR_ARG, "dtype %d is not GDNX_DTYPE_F32/BF16", dtype);
+  if (head_dim != 64 && head_dim != 128) return set_error(GDNX_ERR_SHAPE, "head_dim %d unsupported (64 or 128)", head_dim);
+  if (B < 1 || T < 0 || H < 1 || M < 1 || M > 16) return set_error(GDNX_ERR_SHAPE, "bad sizes B=%d T=%d H=%d M=%d", B, T, H, M);
+  if (!k || !beta) return set_error(GDNX_ERR_ARG, "k and beta must be non-null");
+  if (!aligned16(k)) return set_error(GDNX_ERR_ARG, "k must be 16-byte aligned");
+  return GDNX_OK;
+}
+
+extern "C" int gdnx_gdn3_coeff(const void* k, const float* beta, float* a, int B, int T, int H, int M, int head_dim,
+                               int dtype, void* stream) {
+  int rc = coeff_common(k, beta, B, T, H, M, head_dim, dtype);
+  if (rc) return rc;
+  if (!a) return set_error(GDNX_ERR_ARG, "a must be non-null");
+  if (T == 0) return GDNX_OK;
+  GCoeffArgs ga{k, beta, a, nullptr, nullptr, nullptr, nullptr, B, T, H, M, head_dim, dtype};
+  return gdn3_coeff_dispatch(ga, false, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_gdn3_coeff_bwd(const void* k, const float* beta, const float* da_e, const float* da_w, void* dk,
+                                   float* dbeta, int B, int T, int H, int M, int head_dim, int dtype, void* stream) {
+  int rc = coeff_common(k, beta, B, T, H, M, head_dim, dtype);
+  if (rc) return rc;
+  if (!da_e || !dk || !dbeta) return set_error(GDNX_ERR_ARG, "da_e, dk and dbeta must be non-null");
+  if (!aligned16(dk)) return set_error(GDNX_ERR_ARG, "dk must be 16-byte aligned");
+  if (T == 0) return GDNX_OK;
+  GCoeffArgs ga{k, beta, nullptr, da_e, da_w, dk, dbeta, B, T, H, M, head_dim, dtype};
+  return gdn3_coeff_dispatch(ga, true, (hipStream_t)stream);
 }

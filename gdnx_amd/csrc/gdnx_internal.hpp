@@ -19,7 +19,7 @@ struct DeltaArgs {
   void* chunk_states;
   int B, T, H, M, D, C, dtype;
   float* r_norm;  // [B,T,H,M] |net write| per token, or null
-  void* prep;     // per-chunk operands (delta_prep_kernel), or null: computed in the scan
+  void* prep;     // per-chunk operand records (delta_prep_kernel), or null
 };
 
 struct DeltaBwdArgs {
@@ -31,8 +31,8 @@ struct DeltaBwdArgs {
   const float* g;
   const void* dy;
   const float* ds_final;
-  const void* s_stash;
-  void* ds_stash;
+  const void* s_stash;   // the forward's chunk_states: states, net writes, prep records
+  void* ds_stash;         // state gradients at chunk ends, then dB
   void* dq;
   void* dk;
   void* dv;
@@ -41,6 +41,17 @@ struct DeltaBwdArgs {
   float* dg;
   float* ds0;
   int B, T, H, M, D, C, dtype;
+};
+
+struct GCoeffArgs {
+  const void* k;       // [B,T,H,D] io dtype
+  const float* beta;   // [B,T,H,M]
+  float* a;            // [B,T,H,M] (forward)
+  const float* da_e;   // [B,T,H,M] (backward)
+  const float* da_w;   // [B,T,H,M] or null (backward)
+  void* dk;            // [B,T,H,D] io dtype, accumulated in place (backward)
+  float* dbeta;        // [B,T,H,M] (backward)
+  int B, T, H, M, D, dtype;
 };
 
 // Record an error message for gdnx_last_error(); returns code.
@@ -134,8 +145,16 @@ int kron_read_dispatch(const KronReadArgs& a, hipStream_t stream);
 int decode_dispatch(const DecodeArgs& a, hipStream_t stream);
 int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);
 int delta_prep_dispatch(const DeltaArgs& a, hipStream_t stream);
+int delta_scan_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);
+int delta_scan_bwd_dispatch(const DeltaBwdArgs& a, hipStream_t stream);
 size_t delta_prep_bytes(int nchains, int T, int C, int dtype);
+// bytes of the state + net-write stash (the prep records follow it in chunk_states)
+inline size_t delta_stash_bytes(int nchains, int T, int D, int C, int dtype) {
+  const size_t NR = (size_t)nchains * ((T + C - 1) / C);
+  return NR * ((size_t)D * D + (size_t)C * D) * (dtype == GDNX_DTYPE_BF16 ? 2 : 4);
+}
 int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream);
+int gdn3_coeff_dispatch(const GCoeffArgs& a, bool bwd, hipStream_t stream);
 int delta_chunk_size(int D, int dtype);
 int delta_train_chunk_size(int D, int dtype);
 

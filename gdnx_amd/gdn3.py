@@ -11,9 +11,8 @@ with lane-shared q/k/v and scalar per-lane gates b = w = beta: per chain
 
 i.e. the chunked delta rule with erase = write coefficient
 a = alpha(beta |k|^2) * beta (the exact-alpha write of
-gdn3/gdn3_upgrade.py:641-648).  The elementwise prologue runs in torch
-(autograd carries its gradient into beta and k); the recurrence and its
-backward are the HIP kernels of libgdnx.
+gdn3/gdn3_upgrade.py:641-648).  The coefficient, the recurrence and both
+backwards are HIP kernels of libgdnx.
 
 ``gdn3_recurrent_state`` is the same method in its general regime: a
 P-slot residual window and periodic rearrangement-SVD compaction of the
@@ -27,18 +26,44 @@ import torch
 from . import ops
 
 
-def stable_alpha(c, eps: float = 1e-6):
-    """alpha(c) = -expm1(-c)/c with the Taylor branch 1 - c/2 + c^2/6 for
-    |c| < eps (gdn3/gdn3_upgrade.py:641-648)."""
-    small = c.abs() < eps
-    safe = torch.where(small, torch.ones_like(c), c)
-    return torch.where(small, 1.0 - c / 2.0 + c * c / 6.0, -torch.expm1(-safe) / safe)
-
-
 def gdn3_coeff(k, beta):
-    """a = alpha(beta |k|^2) beta for k [B,T,H,D] shared by beta's M lanes."""
-    c = beta.float() * k.float().square().sum(-1, keepdim=True)
-    return stable_alpha(c) * beta.float()
+    """a = alpha(beta |k|^2) beta for k [B,T,H,D] shared by beta's M lanes,
+    alpha(c) = (1 - exp(-c))/c with the Taylor branch 1 - c/2 + c^2/6 for
+    |c| < 1e-6 (gdn3/gdn3_upgrade.py:641-648); the gdnx_gdn3_coeff kernel
+    (not differentiable; gdn3_scan carries its gradient)."""
+    return ops.gdn3_coeff(k.contiguous(), beta.float().contiguous())
+
+
+class GDN3ScanFunction(torch.autograd.Function):
+    """Dense-regime GDN3 recurrence, differentiable in q, k, v, beta, log_g
+    and state0: the coefficient kernel, then the delta-rule forward; the
+    backward runs the delta-rule backward and folds the coefficient's
+    gradient into dk and dbeta in one kernel (no elementwise torch ops)."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta, log_g, state0):
+        train = any(ctx.needs_input_grad)
+        D = q.shape[-1]
+        a = ops.gdn3_coeff(k, beta)
+        chunk = ops.chunk_size(D, q.dtype, train=train)
+        y, s_out, cs = ops.delta_chunk_fwd(q, k, v, a, a, log_g, state0, return_state=True,
+                                           save_states=train, chunk=chunk)
+        if train:
+            ctx.save_for_backward(q, k, v, beta, a, log_g, cs)
+            ctx.chunk = chunk
+            ctx.has_state0 = state0 is not None
+        return y, s_out
+
+    @staticmethod
+    def backward(ctx, dy, ds_out):
+        q, k, v, beta, a, log_g, cs = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros(*a.shape, q.shape[-1], dtype=q.dtype, device=q.device)
+        dq, dk, dv, dae, daw, dlg, ds0 = ops.delta_chunk_bwd(
+            q, k, v, a, a, log_g, dy, cs, ctx.chunk, dstate_out=ds_out,
+            want_dstate0=ctx.has_state0 and ctx.needs_input_grad[5])
+        dbeta = ops.gdn3_coeff_bwd(k, beta, dae, daw, dk)
+        return dq, dk, dv, dbeta, dlg, ds0
 
 
 def gdn3_scan(q, k, v, beta, log_g, state0=None, return_state=False):
@@ -48,8 +73,10 @@ def gdn3_scan(q, k, v, beta, log_g, state0=None, return_state=False):
     [B,T,H,M] float32 (log_g > 0 is clamped, i.e. gamma <= 1).  Returns
     y [B,T,H,M,D] in q's dtype (and the final state [B,H,M,D,D] fp32).
     """
-    a = gdn3_coeff(k, beta)
-    y, s = ops.delta_rule(q, k, v, a, a, log_g.float(), state0)
+    args = [t.contiguous() for t in (q, k, v)] + [t.float().contiguous() for t in (beta, log_g)]
+    if state0 is not None:
+        state0 = state0.float().contiguous()
+    y, s = GDN3ScanFunction.apply(*args, state0)
     return (y, s) if return_state else y
 
 

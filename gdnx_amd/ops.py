@@ -43,11 +43,11 @@ def delta_chunk_fwd(q, k, v, a_e, a_w, log_g, state0=None, *, return_state=False
     """Forward of the lane-shared decoupled-erase delta rule.
 
     r_norm: optional float32 [B,T,H,M] output receiving |r_t| (the norm of
-    each token's net write).  two_pass: compute the state-independent chunk
-    operands in a parallel pass first (needs a workspace) instead of inside
-    the sequential scan; off by default because on config 2 the extra pass
-    (253 us) costs more than it saves in the scan (787 -> 589 us).  Returns (y, state_out or None, chunk_states or
-    None)."""
+    each token's net write).  two_pass: without save_states, still run the
+    parallel chunk-operand pass plus the value-split scan (it needs a
+    workspace) rather than the fused single-kernel scan; with save_states
+    the two-pass form is always used.  Returns (y, state_out or None,
+    chunk_states or None)."""
     lib = _lib.load()
     B, T, H, M, D = _check_dense(q, k, v, a_e, a_w, log_g)
     code = _lib.dtype_code(q.dtype)
@@ -165,7 +165,7 @@ def delta_chunk_bwd_stages(q, k, v, a_e, a_w, log_g, dy, chunk_states, chunk, ws
                torch.empty_like(a_e), torch.empty_like(a_w), torch.empty_like(log_g))
     with torch.cuda.device(q.device):
         rc = lib.gdnx_delta_chunk_bwd_state(_lib.ptr(q), _lib.ptr(k), _lib.ptr(a_e), _lib.ptr(log_g),
-                                            _lib.ptr(dy), None, _lib.ptr(ws), None,
+                                            _lib.ptr(dy), None, _lib.ptr(chunk_states), _lib.ptr(ws), None,
                                             B, T, H, M, D, chunk, code, st)
     _lib.check(rc, "gdnx_delta_chunk_bwd_state")
     return ws, out
@@ -208,6 +208,41 @@ def delta_decode_step(q, k, v, a_e, a_w, log_g, state, out=None):
                                         _lib.dtype_code(q.dtype), _lib.stream_of(q))
     _lib.check(rc, "gdnx_delta_decode_step")
     return y
+
+
+def gdn3_coeff(k, beta):
+    """a = alpha(beta |k|^2) beta [B,T,H,M] float32 (gdnx_gdn3_coeff) for k
+    [B,T,H,D] (bf16/float32, shared by the M lanes) and beta [B,T,H,M]."""
+    lib = _lib.load()
+    _need(k.is_cuda and k.dim() == 4 and k.is_contiguous(), "k must be contiguous [B,T,H,D] on the GPU")
+    _need(beta.dim() == 4 and tuple(beta.shape[:3]) == tuple(k.shape[:3]) and beta.dtype == torch.float32
+          and beta.is_contiguous(), "beta must be contiguous float32 [B,T,H,M]")
+    B, T, H, D = k.shape
+    M = beta.shape[3]
+    a = torch.empty_like(beta)
+    with torch.cuda.device(k.device):
+        rc = lib.gdnx_gdn3_coeff(_lib.ptr(k), _lib.ptr(beta), _lib.ptr(a), B, T, H, M, D,
+                                 _lib.dtype_code(k.dtype), _lib.stream_of(k))
+    _lib.check(rc, "gdnx_gdn3_coeff")
+    return a
+
+
+def gdn3_coeff_bwd(k, beta, da_e, da_w, dk):
+    """Backward of gdn3_coeff: returns dbeta; adds the key gradient into dk
+    (in place)."""
+    lib = _lib.load()
+    B, T, H, D = k.shape
+    M = beta.shape[3]
+    for t in (da_e, da_w):
+        _need(t is None or (t.shape == beta.shape and t.dtype == torch.float32 and t.is_contiguous()),
+              "da_e / da_w must be contiguous float32 like beta")
+    _need(dk.shape == k.shape and dk.dtype == k.dtype and dk.is_contiguous(), "dk must match k")
+    dbeta = torch.empty_like(beta)
+    with torch.cuda.device(k.device):
+        rc = lib.gdnx_gdn3_coeff_bwd(_lib.ptr(k), _lib.ptr(beta), _lib.ptr(da_e), _lib.ptr(da_w), _lib.ptr(dk),
+                                     _lib.ptr(dbeta), B, T, H, M, D, _lib.dtype_code(k.dtype), _lib.stream_of(k))
+    _lib.check(rc, "gdnx_gdn3_coeff_bwd")
+    return dbeta
 
 
 # ---------------------------------------------------------------------------

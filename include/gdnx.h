@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 1
+#define GDNX_ABI_VERSION 2
 
 enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1 };
 
@@ -48,11 +48,13 @@ int gdnx_delta_chunk_size(int head_dim, int dtype);
 int gdnx_delta_train_chunk_size(int head_dim, int dtype);
 
 /* Bytes of the per-chunk stash for the given chunk (0 = default; -1 if
- * invalid): per chain and chunk, in the compute dtype, the d x d state
- * entering the chunk (row-major [d_k][d_v]) and the chunk's C x d net writes
- * R (row-major [token][d_v]); all states first, then all net writes.  The
- * backward's workspace has the same size and layout (state gradients dS at
- * chunk ends, then dB = T^T dR). */
+ * invalid).  Per chain and chunk, in order: the d x d state entering the
+ * chunk and the chunk's C x d net writes R (compute dtype, MFMA-fragment
+ * tile order; all states first, then all net writes), then the chunk's
+ * state-independent operands (T = (I + L)^-1 and the decay-masked Q K^T as
+ * C x C compute-dtype matrices, and four float32 per-token factors), which
+ * the backward's reverse scan reuses.  The backward's workspace is at least
+ * this size (state gradients dS at chunk ends, then dB = T^T dR). */
 long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim, int chunk,
                                         int dtype);
 
@@ -65,21 +67,23 @@ long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim
  * Per chain (b, h, m), token t:  S <- exp(min(g,0)) S;  r = a_w v - a_e S^T k;
  *   S <- S + k r^T;  y = S^T q.
  * state0 / state_out / chunk_states / workspace may be NULL.  chunk_states
- * (size from gdnx_delta_chunk_states_bytes) receives the state entering
- * every chunk, which gdnx_delta_chunk_bwd needs; workspace (size from
- * gdnx_delta_fwd_workspace_bytes) enables the two-pass form. */
+ * (size from gdnx_delta_chunk_states_bytes) receives what
+ * gdnx_delta_chunk_bwd needs (the state entering every chunk, the net writes
+ * and the chunk operands).  With chunk_states or workspace (size from
+ * gdnx_delta_fwd_workspace_bytes) the forward runs as a fully parallel
+ * per-chunk operand pass plus a value-split state scan; with neither, as one
+ * fused scan.  Results agree up to rounding order. */
 int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v,
                          const float* a_e, const float* a_w, const float* log_g,
                          const float* state0, void* y, float* state_out,
                          void* chunk_states, void* workspace, int B, int T, int H, int M,
                          int head_dim, int chunk, int dtype, void* stream);
 
-/* Bytes of the optional forward workspace (-1 if invalid).  With a
- * workspace the forward first computes every chunk's state-independent
- * operands (T diag(a_w), T diag(a_e exp G), the decay-masked Q K^T and the
- * decay factors) in one fully parallel pass, and the sequential scan only
- * carries the state; with workspace = NULL the scan computes them itself.
- * Results are the same up to rounding order. */
+/* Bytes of the optional forward workspace (-1 if invalid): room for every
+ * chunk's state-independent operands (T = (I + L)^-1, the decay-masked
+ * Q K^T and the per-token decay and coefficient factors), which a fully
+ * parallel pass computes before the value-split state scan.  Not needed
+ * when chunk_states is given (the operands then go there). */
 long long gdnx_delta_fwd_workspace_bytes(int B, int T, int H, int M, int head_dim, int chunk,
                                          int dtype);
 
@@ -112,13 +116,14 @@ int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v,
                          int dtype, void* stream);
 
 /* The two stages of gdnx_delta_chunk_bwd, callable separately (e.g. to
- * time or overlap them).  Stage 1 runs the reverse state scan and fills
- * workspace with dS at every chunk end (plus dstate0); stage 2 reads the
- * forward's chunk_states and that workspace and writes every input gradient.
- * Same arguments and layouts as gdnx_delta_chunk_bwd. */
+ * time or overlap them).  Stage 1 runs the reverse state scan on the
+ * forward's chunk operands (in chunk_states) and fills workspace with dS at
+ * every chunk end and dB (plus dstate0); stage 2 reads the forward's
+ * chunk_states and that workspace and writes every input gradient.  Same
+ * arguments and layouts as gdnx_delta_chunk_bwd. */
 int gdnx_delta_chunk_bwd_state(const void* q, const void* k, const float* a_e,
                                const float* log_g, const void* dy, const float* dstate_out,
-                               void* workspace, float* dstate0,
+                               const void* chunk_states, void* workspace, float* dstate0,
                                int B, int T, int H, int M, int head_dim, int chunk,
                                int dtype, void* stream);
 int gdnx_delta_chunk_bwd_grads(const void* q, const void* k, const void* v,
@@ -142,6 +147,24 @@ int gdnx_delta_decode_step(const void* q, const void* k, const void* v,
                            const float* a_e, const float* a_w, const float* log_g,
                            float* state, void* y, int NS, int H, int M, int head_dim,
                            int dtype, void* stream);
+
+
+/* GDN3 exact-alpha write coefficient in the dense regime (lane-shared keys,
+ * one scalar gate per lane): a = alpha(beta |k|^2) beta with
+ * alpha(c) = (1 - exp(-c)) / c (Taylor 1 - c/2 + c^2/6 below |c| = 1e-6).
+ * Replaces _stable_alpha_vec and its use in the recurrence
+ * (gdn3/gdn3_upgrade.py:641-648; gdn3/_reference_recurrence.py:73-78) for the
+ * b = w = beta case, where erase and write coefficients coincide.
+ * k [B, T, H, D] io dtype; beta, a [B, T, H, M] float32; M <= 16. */
+int gdnx_gdn3_coeff(const void* k, const float* beta, float* a, int B, int T, int H, int M,
+                    int head_dim, int dtype, void* stream);
+
+/* Backward of gdnx_gdn3_coeff: with da = da_e + da_w (da_w may be NULL),
+ * writes dbeta [B, T, H, M] and adds the coefficient's key gradient into
+ * dk [B, T, H, D] (io dtype, in place). */
+int gdnx_gdn3_coeff_bwd(const void* k, const float* beta, const float* da_e, const float* da_w,
+                        void* dk, float* dbeta, int B, int T, int H, int M, int head_dim,
+                        int dtype, void* stream);
 
 
 /* ---- GDN3 Kronecker-residual regime --------------------------------------

@@ -36,10 +36,13 @@ def test_abi_version_and_sizes():
     assert lib.gdnx_delta_chunk_size(128, _lib.DTYPE_BF16) == 64
     assert lib.gdnx_delta_train_chunk_size(128, _lib.DTYPE_BF16) == 32
     assert lib.gdnx_delta_chunk_size(100, _lib.DTYPE_BF16) == 0
-    # per chain and chunk: one d x d state and one C x d block of net writes
+    # per chain and chunk: one d x d state and one C x d block of net writes, then
+    # the chunk operands (T and Aq as C x C, four float32 factors per token)
     assert lib.gdnx_delta_chunk_states_bytes(4, 4096, 16, 4, 128, 64, _lib.DTYPE_BF16) == \
-        4 * 16 * 4 * 64 * (128 * 128 + 64 * 128) * 2
-    assert lib.gdnx_delta_chunk_states_bytes(1, 100, 1, 1, 64, 0, _lib.DTYPE_F32) == 4 * (64 * 64 + 32 * 64) * 4
+        4 * 16 * 4 * 64 * ((128 * 128 + 64 * 128) * 2 + 2 * 64 * 64 * 2 + 4 * 64 * 4)
+    assert lib.gdnx_delta_chunk_states_bytes(1, 100, 1, 1, 64, 0, _lib.DTYPE_F32) == \
+        4 * ((64 * 64 + 32 * 64) * 4 + 2 * 32 * 32 * 4 + 4 * 32 * 4)
+    assert lib.gdnx_delta_fwd_workspace_bytes(1, 100, 1, 1, 64, 0, _lib.DTYPE_F32) == 4 * (2 * 32 * 32 * 4 + 4 * 32 * 4)
     assert lib.gdnx_delta_chunk_states_bytes(1, 100, 1, 1, 64, 48, _lib.DTYPE_F32) == -1
 
 
