@@ -52,8 +52,9 @@ struct GradDims {
 template <int C, int NW, int NP>
 struct alignas(16) GradLaneBuf {
   float G[C], gam[C], dec[C], ae[C], aw[C], graw[C];
-  float red[4][NW][C];   // [q.P1, k.P2, k.P3, v.dB][wave][row] partial sums
-  float tri[NP][3][16];  // per tile pair: row sums and column sums of Xm, row sums of AE
+  float red[C][4][NW];   // [row][q.P1, k.P2, k.P3, v.dB][wave] partial sums (a row's 4 NW contiguous)
+  float tri[NP][5][16];  // per tile pair: row and column sums of Xm (dAq part), row sums of AE,
+                         // row and column sums of Xm (dL part)
   float scal[NW];        // per-wave partial <dS_C, S0>
 };
 
@@ -148,32 +149,36 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
   const CT* ds_st = (const CT*)p.ds_stash;   // [nrec] stash_state: state gradients at chunk ends
   const CT* db_st = ds_st + nrec * D * D;    // [nrec] stash_tiles: dB
 
-  // ---- fetch lane mm's inputs into registers (issued a lane ahead) ----
-  auto prefetch = [&](Pf& f, int mm, int tid_) {
+  // ---- lane mm's inputs, fetched into registers a lane ahead in two parts:
+  // the chunk tiles (dY, R, dB, scalars) at the start of the previous lane,
+  // and this wave's state rows (S0, dS_C) spread through the previous lane's
+  // P products, so the loads stream while the lanes compute.  Every load is
+  // unconditional (dY's tail tokens go through a buffer resource) ----
+  const unsigned ysb = (unsigned)(rsy * sizeof(CT));
+  auto rec_of = [&](int mm) { return rec_index(((size_t)b * p.H + h) * p.M + mm, c, (size_t)p.B * p.H * p.M); };
+  auto prefetch_tiles = [&](Pf& f, int mm, int tid_) {
     const int lane_ = tid_ & 63;
-    const size_t rec = rec_index(((size_t)b * p.H + h) * p.M + mm, c, (size_t)p.B * p.H * p.M);
-#pragma unroll
-    for (int V = 0; V < NDT; ++V) {
-      f.s[V] = *(const V4*)stash_state_ptr<CT, D, C>(s_st + rec * D * D, wave, V, lane_);
-      f.ds[V] = *(const V4*)stash_state_ptr<CT, D, C>(ds_st + rec * D * D, wave, V, lane_);
-    }
+    const size_t rec = rec_of(mm);
 #pragma unroll
     for (int it = 0; it < NCT; ++it) {  // tile (it, V = wave) of R and dB
-      const size_t off = rec * C * D + (size_t)((it * NDT + wave) * 64 + lane_) * 4;
+      const size_t off = rec * C * D + stash_tile_offset<CT, D>(it, wave, lane_);
       f.r[it] = *(const V4*)(r_st + off);
       f.db[it] = *(const V4*)(db_st + off);
     }
     const CT* yb = (const CT*)p.dy + (((size_t)b * p.T * p.H + h) * p.M + mm) * D + (size_t)t0 * rsy;
+    const __amdgpu_buffer_rsrc_t yr = buf_rsrc(yb, (unsigned)min(C, p.T - t0) * ysb);
 #pragma unroll
     for (int j = 0; j < Pf::NDY; ++j) {
       const int qv = tid_ + j * NT, row = qv / (D / Pf::VEC), col = (qv % (D / Pf::VEC)) * Pf::VEC;
-      f.dy[j] = (qv < C * D / Pf::VEC && t0 + row < p.T) ? *(const uint4*)(yb + (unsigned)row * (unsigned)rsy + col)
-                                                          : make_uint4(0, 0, 0, 0);
+      f.dy[j] = buf_load16(yr, (unsigned)row * ysb + col * sizeof(CT));
     }
-    if (wave == SW) {
-      const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + mm;
-      scal_fetch<C>(f.sc, p.ae + soff, p.aw + soff, p.g + soff, st, t0, p.T, lane_);
-    }
+    const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + mm;
+    scal_fetch_all<C>(f.sc, p.ae + soff, p.aw + soff, p.g + soff, st, t0, p.T, lane_);
+  };
+  auto prefetch_state = [&](Pf& f, int mm, int V, int tid_) {
+    const size_t rec = rec_of(mm);
+    f.s[V] = *(const V4*)stash_state_ptr<CT, D, C>(s_st + rec * D * D, wave, V, tid_ & 63);
+    f.ds[V] = *(const V4*)stash_state_ptr<CT, D, C>(ds_st + rec * D * D, wave, V, tid_ & 63);
   };
 
   // ---- per-token scalar gradients of lane mm (wave SW, one token per lane) ----
@@ -181,24 +186,34 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
     float dGi = 0.f, daei = 0.f, dawi = 0.f, r3d = 0.f;
     if (lane < C) {
       const int i = lane, ib = i >> 4, ir = i & 15;
-      float r1 = 0.f, r2 = 0.f, r3 = 0.f;
+      float rs[4];
 #pragma unroll
-      for (int w = 0; w < NW; ++w) {
-        r1 += q.red[0][w][i];
-        r2 += q.red[1][w][i];
-        r3 += q.red[2][w][i];
-        dawi += q.red[3][w][i];
+      for (int a = 0; a < 4; ++a) {   // this row's NW partials, read as 16-byte vectors
+        rs[a] = 0.f;
+#pragma unroll
+        for (int w = 0; w < NW; w += 4) {
+          const f32x4 x = *(const f32x4*)&q.red[i][a][w];
+          rs[a] += (x[0] + x[1]) + (x[2] + x[3]);
+        }
       }
-      dGi = q.gam[i] * r1 - q.gam[i] * q.ae[i] * r2 - q.dec[i] * r3;
-      daei = -q.gam[i] * r2;
-      // Xm row i lives in tiles (ib, jt <= ib); column i in tiles (it >= ib, ib)
-      for (int jt = 0; jt <= ib; ++jt) {
-        const int pr = ib * (ib + 1) / 2 + jt;
-        dGi += q.tri[pr][0][ir];
-        daei += q.tri[pr][2][ir];
+      dawi = rs[3];
+      dGi = q.gam[i] * rs[0] - q.gam[i] * q.ae[i] * rs[1] - q.dec[i] * rs[2];
+      daei = -q.gam[i] * rs[1];
+      // Xm row i lives in tiles (ib, jt <= ib); column i in tiles (it >= ib, ib);
+      // compile-time tile loops, predicated on the lane's row block
+#pragma unroll
+      for (int bi = 0; bi < NCT; ++bi) {
+#pragma unroll
+        for (int bj = 0; bj <= bi; ++bj) {
+          const int pr = bi * (bi + 1) / 2 + bj;
+          if (bi == ib) {
+            dGi += q.tri[pr][0][ir] + q.tri[pr][3][ir];
+            daei += q.tri[pr][2][ir];
+          }
+          if (bj == ib) dGi -= q.tri[pr][1][ir] + q.tri[pr][4][ir];
+        }
       }
-      for (int it = ib; it < NCT; ++it) dGi -= q.tri[it * (it + 1) / 2 + ib][1][ir];
-      r3d = q.dec[i] * r3;
+      r3d = q.dec[i] * rs[2];
     }
     // chunk-end decay: d/dG_last of gamma_C <dS_C, S0> and of the dec factors
 #pragma unroll
@@ -226,11 +241,22 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
     }
   };
 
+  // q, k, v of the chunk first, then lane 0's inputs: the staging commit
+  // below waits only for its own loads
   Pf pf;
-  prefetch(pf, 0, tid);
-  stage_tile<CT, D, C, NT>((const CT*)p.q + qoff, rs, t0, p.T, sm.q, nullptr, tid);
-  stage_tile<CT, D, C, NT>((const CT*)p.k + qoff, rs, t0, p.T, sm.k, nullptr, tid);
-  stage_tile<CT, D, C, NT>((const CT*)p.v + qoff, rs, t0, p.T, sm.v, nullptr, tid);
+  {
+    Stage<CT, C, D, 1, NT> sq, sk, sv;
+    const unsigned rsb = (unsigned)(rs * sizeof(CT)), nb = (unsigned)min(C, p.T - t0) * rsb;
+    sq.fetch(buf_rsrc((const CT*)p.q + qoff + (size_t)t0 * rs, nb), rsb, tid);
+    sk.fetch(buf_rsrc((const CT*)p.k + qoff + (size_t)t0 * rs, nb), rsb, tid);
+    sv.fetch(buf_rsrc((const CT*)p.v + qoff + (size_t)t0 * rs, nb), rsb, tid);
+    prefetch_tiles(pf, 0, tid);
+#pragma unroll
+    for (int V = 0; V < NDT; ++V) prefetch_state(pf, 0, V, tid);
+    sq.template commit_nat<LDD>(sm.q, tid);
+    sk.template commit_nat<LDD>(sm.k, tid);
+    sv.template commit_nat<LDD>(sm.v, tid);
+  }
   for (int i = tid; i < C * LDF; i += NT) {
     sm.dQK[i] = 0.f;
     sm.dKK[i] = 0.f;
@@ -275,32 +301,24 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
         sm.u.ln.R[(it * 16 + 4 * g4 + i) * LDD + dcol] = pf.r[it][i];
         sm.u.ln.dB[(it * 16 + 4 * g4 + i) * LDD + dcol] = pf.db[it][i];
       }
-    Frag Sf[NKV], dSf[NKV];  // this wave's rows of S0 / dS_C over k = v
-#pragma unroll
-    for (int kb = 0; kb < NKV; ++kb) {
-      f32x4 ys[TPS], yd[TPS];
-#pragma unroll
-      for (int hh = 0; hh < TPS; ++hh) {
-        ys[hh] = tile_transpose_raw(pf.s[kb * TPS + hh], lane);
-        yd[hh] = tile_transpose_raw(pf.ds[kb * TPS + hh], lane);
-      }
-      Sf[kb] = acc_frag((CT*)nullptr, ys[0], ys[TPS - 1]);
-      dSf[kb] = acc_frag((CT*)nullptr, yd[0], yd[TPS - 1]);
-    }
     if (wave == SW) {
       const ChunkScalars cs{lb.G, lb.gam, lb.dec, lb.ae, lb.aw, lb.graw};
       scal_commit<C>(cs, pf.sc, lane);
     }
+    const int mn = min(m + 1, p.M - 1);   // (the last lane refetches itself, unused)
+    prefetch_tiles(pf, mn, tid);          // the tile registers are free again: fetch the next lane's
     __syncthreads();
-    if (m + 1 < p.M) prefetch(pf, m + 1, tid);
     if (m > 0 && wave == SW) scalar_grads(m - 1, sm.lb[(m - 1) & 1]);
 
-    // ---- dAq = dY R^T (j <= i) and dL = -dB R^T (j < i), lower tiles ----
-    for (int pidx = wave; pidx < NP; pidx += NW) {
+    // ---- dAq = dY R^T (j <= i) and dL = -dB R^T (j < i), lower tiles: task
+    // pidx < NP is tile pair pidx of dAq, NP + pidx the same pair of dL ----
+    for (int task = wave; task < 2 * NP; task += NW) {
+      const bool isL = task >= NP;
+      const int pidx = isL ? task - NP : task;
       int it, jt;
       tri_pair(pidx, it, jt);
-      const f32x4 aA = tile_nt<CT, D>(&sm.u.ln.dy[(it * 16 + n16) * LDD], &sm.u.ln.R[(jt * 16 + n16) * LDD], g4);
-      const f32x4 aL = tile_nt<CT, D>(&sm.u.ln.dB[(it * 16 + n16) * LDD], &sm.u.ln.R[(jt * 16 + n16) * LDD], g4);
+      const CT* arow = isL ? &sm.u.ln.dB[(it * 16 + n16) * LDD] : &sm.u.ln.dy[(it * 16 + n16) * LDD];
+      const f32x4 acc = tile_nt<CT, D>(arow, &sm.u.ln.R[(jt * 16 + n16) * LDD], g4);
       const int j = jt * 16 + n16;
       const float Gj = lb.G[j];
       float xm[4], xa[4];
@@ -309,80 +327,96 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
         const int i = it * 16 + 4 * g4 + ii;
         xm[ii] = 0.f;
         xa[ii] = 0.f;
-        if (j <= i) {
-          const float Dij = __expf(lb.G[i] - Gj);
-          const float dqk = aA[ii] * Dij;
+        const float Dij = __expf(lb.G[i] - Gj);
+        if (!isL && j <= i) {
+          const float dqk = acc[ii] * Dij;
           sm.dQK[i * LDF + j] += dqk;
           xm[ii] = dqk * sm.QK[i * LDF + j];
-          if (j < i) {
-            const float dl = -aL[ii];
-            const float kk = sm.KK[i * LDF + j];
-            const float dkk = dl * Dij * lb.ae[i];
-            sm.dKK[i * LDF + j] += dkk;
-            xm[ii] += dkk * kk;
-            xa[ii] = dl * Dij * kk;
-          }
+        } else if (isL && j < i) {
+          const float dl = -acc[ii];
+          const float kk = sm.KK[i * LDF + j];
+          const float dkk = dl * Dij * lb.ae[i];
+          sm.dKK[i * LDF + j] += dkk;
+          xm[ii] = dkk * kk;
+          xa[ii] = dl * Dij * kk;
         }
       }
       // row sums (over the 16 columns j, lane 15 of each row) and column sums (over the 16 rows i)
+      const int slot = isL ? 3 : 0;
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const float rx = row_prefix16(xm[ii]), ra = row_prefix16(xa[ii]);
         if (n16 == 15) {
-          lb.tri[pidx][0][4 * g4 + ii] = rx;
-          lb.tri[pidx][2][4 * g4 + ii] = ra;
+          lb.tri[pidx][slot][4 * g4 + ii] = rx;
+          if (isL) lb.tri[pidx][2][4 * g4 + ii] = ra;
         }
       }
       float cx = (xm[0] + xm[1]) + (xm[2] + xm[3]);
       cx += __shfl_xor(cx, 16, 64);
       cx += __shfl_xor(cx, 32, 64);
-      if (g4 == 0) lb.tri[pidx][1][n16] = cx;
+      if (g4 == 0) lb.tri[pidx][slot + 1][n16] = cx;
     }
 
-    // ---- P1 = dY S0^T, P2 = dB S0^T, P3 = R dS^T on this wave's d tile; dV, da_w ----
+    // ---- P1 = dY S0^T, P2 = dB S0^T, P3 = R dS^T on this wave's d tile, k-step
+    // outer: this wave's rows of S0 / dS_C (fetched during the previous lane)
+    // become fragments over k = v one k-step at a time, and their registers
+    // are refilled with the next lane's rows right away, so those loads stream
+    // through the products; then dV, da_w and the row sums ----
+    f32x4 P1[NCT], P2[NCT], P3[NCT];
+#pragma unroll
+    for (int it = 0; it < NCT; ++it) P1[it] = P2[it] = P3[it] = zero4();
+    float sdot = 0.f;   // <dS_C, S0> over this wave's rows
+#pragma unroll
+    for (int kb = 0; kb < NKV; ++kb) {
+      f32x4 ys[TPS], yd[TPS];
+#pragma unroll
+      for (int hh = 0; hh < TPS; ++hh) {
+        ys[hh] = tile_transpose_raw(pf.s[kb * TPS + hh], lane);
+        yd[hh] = tile_transpose_raw(pf.ds[kb * TPS + hh], lane);
+      }
+      const Frag Sf = acc_frag((CT*)nullptr, ys[0], ys[TPS - 1]);
+      const Frag dSf = acc_frag((CT*)nullptr, yd[0], yd[TPS - 1]);
+#pragma unroll
+      for (int e = 0; e < FragLen<CT>::value; ++e) sdot += to_f(Sf[e]) * to_f(dSf[e]);
+#pragma unroll
+      for (int hh = 0; hh < TPS; ++hh) prefetch_state(pf, mn, kb * TPS + hh, tid);
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) {
+        mma(P1[it], ld_frag(&sm.u.ln.dy[(it * 16 + n16) * LDD + kb * KS], g4), Sf);
+        mma(P2[it], ld_frag(&sm.u.ln.dB[(it * 16 + n16) * LDD + kb * KS], g4), Sf);
+        mma(P3[it], ld_frag(&sm.u.ln.R[(it * 16 + n16) * LDD + kb * KS], g4), dSf);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
 #pragma unroll
     for (int it = 0; it < NCT; ++it) {
-      f32x4 P1 = zero4(), P2 = zero4(), P3 = zero4();
-#pragma unroll
-      for (int kb = 0; kb < NKV; ++kb) {
-        mma(P1, ld_frag(&sm.u.ln.dy[(it * 16 + n16) * LDD + kb * KS], g4), Sf[kb]);
-        mma(P2, ld_frag(&sm.u.ln.dB[(it * 16 + n16) * LDD + kb * KS], g4), Sf[kb]);
-        mma(P3, ld_frag(&sm.u.ln.R[(it * 16 + n16) * LDD + kb * KS], g4), dSf[kb]);
-      }
       const f32x4 gi = *(const f32x4*)&lb.gam[it * 16 + 4 * g4];
       const f32x4 ei = *(const f32x4*)&lb.ae[it * 16 + 4 * g4];
       const f32x4 di = *(const f32x4*)&lb.dec[it * 16 + 4 * g4];
       const f32x4 wi = *(const f32x4*)&lb.aw[it * 16 + 4 * g4];
-      dQacc[it] += gi * P1;
-      dKacc[it] += di * P3 - ei * gi * P2;
+      dQacc[it] += gi * P1[it];
+      dKacc[it] += di * P3[it] - ei * gi * P2[it];
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
         const int i = it * 16 + 4 * g4 + ii;
         const float dbv = to_f(sm.u.ln.dB[i * LDD + dcol]);
         const float kv = to_f(sm.k[i * LDD + dcol]);
         dVacc[it][ii] += wi[ii] * dbv;
-        const float s1 = row_prefix16(P1[ii] * to_f(sm.q[i * LDD + dcol]));
-        const float s2 = row_prefix16(P2[ii] * kv);
-        const float s3 = row_prefix16(P3[ii] * kv);
+        const float s1 = row_prefix16(P1[it][ii] * to_f(sm.q[i * LDD + dcol]));
+        const float s2 = row_prefix16(P2[it][ii] * kv);
+        const float s3 = row_prefix16(P3[it][ii] * kv);
         const float sw = row_prefix16(dbv * to_f(sm.v[i * LDD + dcol]));
         if (n16 == 15) {
-          lb.red[0][wave][i] = s1;
-          lb.red[1][wave][i] = s2;
-          lb.red[2][wave][i] = s3;
-          lb.red[3][wave][i] = sw;
+          lb.red[i][0][wave] = s1;
+          lb.red[i][1][wave] = s2;
+          lb.red[i][2][wave] = s3;
+          lb.red[i][3][wave] = sw;
         }
       }
     }
-    {  // <dS_C, S0> over this wave's rows
-      float s = 0.f;
 #pragma unroll
-      for (int kb = 0; kb < NKV; ++kb)
-#pragma unroll
-        for (int e = 0; e < FragLen<CT>::value; ++e) s += to_f(Sf[kb][e]) * to_f(dSf[kb][e]);
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) s += __shfl_xor(s, off, 64);
-      if (lane == 0) lb.scal[wave] = s;
-    }
+    for (int off = 1; off < 64; off <<= 1) sdot += __shfl_xor(sdot, off, 64);
+    if (lane == 0) lb.scal[wave] = sdot;
   }
   __syncthreads();  // lane tiles dead: the union becomes Q^T, K^T and the gram-gradient factors
   if (wave == SW) scalar_grads(p.M - 1, sm.lb[(p.M - 1) & 1]);

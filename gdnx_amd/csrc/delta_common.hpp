@@ -29,48 +29,6 @@ struct Dims {
   static_assert(NVT >= 1 && DPW >= 1 && NDT % NW == 0, "head dim must be 64 or 128");
 };
 
-// Stage C rows (tokens t0..t0+C-1, zero beyond T) of a [.., T, .., D] tensor
-// into LDS: `nat` gets rows [C][D+4] (feature-contiguous), `tr` gets the
-// transpose [D][C+4] (token-contiguous), each optional.  `src` points at
-// token 0, feature 0 of this (batch, head[, lane]); rows are `rs` apart
-// (C * rs < 2^31: the in-chunk offset is 32-bit).  NTH threads take part.
-template <typename CT, int D, int C, int NTH = Dims<CT, D, C>::NT>
-__device__ __forceinline__ void stage_tile(const CT* __restrict__ src, size_t rs, int t0, int T,
-                                           CT* nat, CT* tr, int tid) {
-  constexpr int VEC = 16 / sizeof(CT);
-  constexpr int DG = D / VEC;
-  constexpr int LDD = D + 4, LDC = C + 4;
-  const CT* base = src + (size_t)t0 * rs;
-  const unsigned rs32 = (unsigned)rs;
-  for (int u = tid; u < (C / 4) * DG; u += NTH) {
-    const int tg = u / DG, dg = u % DG;
-    CT x[4][VEC];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tr_ = 4 * tg + r;
-      if (t0 + tr_ < T)
-        *(uint4*)x[r] = *(const uint4*)(base + (unsigned)tr_ * rs32 + dg * VEC);
-      else
-        *(uint4*)x[r] = make_uint4(0, 0, 0, 0);
-    }
-    if (nat) {
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        uint2* d = (uint2*)(nat + (4 * tg + r) * LDD + dg * VEC);
-        const uint2* s = (const uint2*)x[r];
-        d[0] = s[0];
-        d[1] = s[1];
-      }
-    }
-    if (tr) {
-#pragma unroll
-      for (int e = 0; e < VEC; ++e)
-        st4(&tr[(dg * VEC + e) * LDC + 4 * tg], to_f(x[0][e]), to_f(x[1][e]), to_f(x[2][e]),
-            to_f(x[3][e]));
-    }
-  }
-}
-
 // Per-token scalars of one chunk for one chain (wave 0 only): erase/write
 // coefficients, clamped log-decay, inclusive prefix G, exp(G) and the decay
 // to the chunk end exp(G_last - G).  `base` = &arr[b][0][h][m]; tokens are
@@ -126,6 +84,21 @@ __device__ __forceinline__ void scal_fetch(ScalarRegs& r, const float* ae, const
     if (aw) r.aw = aw[(size_t)t * st];
     r.g = g[(size_t)t * st];
   }
+}
+
+// scal_fetch without branches: every lane loads (lanes past the chunk or
+// past T read a clamped token) and the values of tokens outside [t0, T) are
+// zeroed afterwards.
+template <int C>
+__device__ __forceinline__ void scal_fetch_all(ScalarRegs& r, const float* ae, const float* aw, const float* g,
+                                               size_t st, int t0, int T, int lane) {
+  const int t = t0 + lane;
+  const size_t tc = (size_t)min(t, T - 1) * st;
+  const bool ok = lane < C && t < T;
+  const float vae = ae[tc], vaw = aw[tc], vg = g[tc];
+  r.ae = ok ? vae : 0.f;
+  r.aw = ok ? vaw : 0.f;
+  r.g = ok ? vg : 0.f;
 }
 
 template <int C>
@@ -457,17 +430,16 @@ __device__ __forceinline__ f32x4 tile_nt(const CT* arow, const CT* brow, int g4)
 template <typename CT> struct FragLen { static constexpr int value = sizeof(CT) == 2 ? 8 : 4; };
 
 // ---- stash layouts (written by the scans, read by the gradient kernel) ----
-// stash_state: one d x d state per (chain, chunk) record as MFMA fragments:
-// block (kb, V) (k = d over rows KS kb .. KS kb + KS - 1, value columns
-// 16 V .. 16 V + 15) is 64 lanes x one fragment, lane l = 16 g + n holding
-// column 16 V + n at rows KS kb + frag_row(e, g); blocks at (kb (D/16) + V).
-// Any split of the value columns over waves or workgroups writes whole blocks.
-// stash_tiles: a C x d block per record as raw 16x16 accumulator tiles:
-// tile (it, V) = rows 16 it.., columns 16 V.., lane l = 16 g + n holds rows
-// 16 it + 4 g + i (i = 0..3) of column 16 V + n at ((it (D/16) + V) 64 + l) 4 + i.
+// Both stashes hold raw 16x16 accumulator tiles: a record's block X (the
+// d x d state entering or leaving a chunk, or the chunk's C x d net writes
+// / dB) as tile (it, V) = rows 16 it.., columns 16 V.., lane l = 16 g + n
+// holding rows 16 it + 4 g + i (i = 0..3) of column 16 V + n at
+// ((it (D/16) + V) 64 + l) 4 + i.  A wave reads or writes a tile as 64
+// consecutive 4-value groups, and any split of the value columns over waves
+// or workgroups writes whole tiles.
 template <typename CT, int D>
-__device__ __forceinline__ size_t stash_frag_index(int kb, int V, int lane) {
-  return ((size_t)kb * (D / 16) + V) * 64 + lane;
+__device__ __forceinline__ size_t stash_tile_offset(int it, int V, int lane) {
+  return (((size_t)it * (D / 16) + V) * 64 + lane) * 4;
 }
 __device__ __forceinline__ f32x4 load4(const bf16* p) {
   const bf16x4 x = *(const bf16x4*)p;
@@ -475,12 +447,10 @@ __device__ __forceinline__ f32x4 load4(const bf16* p) {
 }
 __device__ __forceinline__ f32x4 load4(const float* p) { return *(const f32x4*)p; }
 
-// X[16 dt + 4 g + i][16 V + n], i = 0..3, for lane (g, n) of a stash_state record
+// X[16 dt + 4 g + i][16 V + n], i = 0..3, for lane (g, n) of a state record
 template <typename CT, int D, int C>
 __device__ __forceinline__ const CT* stash_state_ptr(const CT* rec, int dt, int V, int lane) {
-  typedef Dims<CT, D, C> Dm;
-  const int kb = dt / Dm::TPS, h = dt % Dm::TPS;
-  return rec + stash_frag_index<CT, D>(kb, V, lane) * FragLen<CT>::value + 4 * h;
+  return rec + stash_tile_offset<CT, D>(dt, V, lane);
 }
 
 // Inclusive prefix sum over the 16 lanes of each DPP row (lane bits 0..3);

@@ -170,12 +170,14 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
 #pragma unroll
       for (int vt = 0; vt < NVT; ++vt)
         Sf[kb][vt] = acc_frag((CT*)nullptr, S[kb * TPS][vt], S[kb * TPS + TPS - 1][vt]);
-    if (p.chunk_states) {  // stash S0 for the backward (stash_state layout)
-      Frag* cst = (Frag*)p.chunk_states + rec_index(chain, c, nchains) * (D * D / FragLen<CT>::value);
+    if (p.chunk_states) {  // stash S0 for the backward (raw tiles)
+      CT* cst = (CT*)p.chunk_states + rec_index(chain, c, nchains) * (D * D);
 #pragma unroll
-      for (int kb = 0; kb < NDT / TPS; ++kb)
+      for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
-        for (int vt = 0; vt < NVT; ++vt) cst[stash_frag_index<CT, D>(kb, wave * NVT + vt, lane)] = Sf[kb][vt];
+        for (int vt = 0; vt < NVT; ++vt)
+          st4(cst + stash_tile_offset<CT, D>(dt, wave * NVT + vt, lane), S[dt][vt][0], S[dt][vt][1], S[dt][vt][2],
+              S[dt][vt][3]);
     }
     __syncthreads();   // -Wm complete
 

@@ -45,7 +45,7 @@ __device__ __forceinline__ void store_cc(CT* __restrict__ dst, const CT* src, in
 }
 
 template <typename CT, int D, int C>
-__global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_prep_kernel(DeltaArgs p) {
+__global__ void __launch_bounds__((Dims<CT, D, C>::NT)) __attribute__((amdgpu_waves_per_eu(3))) delta_prep_kernel(DeltaArgs p) {
   typedef Dims<CT, D, C> Dm;
   constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF, NT = Dm::NT, NW = Dm::NW, NCT = Dm::NCT;
   constexpr int NP = NCT * (NCT + 1) / 2;          // lower 16x16 tile pairs of a C x C gram

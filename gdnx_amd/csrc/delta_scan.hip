@@ -188,9 +188,10 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
     for (int kb = 0; kb < NDT / TPS; ++kb) Sf[kb] = acc_frag((CT*)nullptr, S[kb * TPS], S[kb * TPS + TPS - 1]);
     if constexpr (STASH) {
-      Frag* cst = (Frag*)p.chunk_states + rec * (D * D / FragLen<CT>::value);
+      CT* cst = (CT*)p.chunk_states + rec * (D * D);
 #pragma unroll
-      for (int kb = 0; kb < NDT / TPS; ++kb) cst[stash_frag_index<CT, D>(kb, V, lane)] = Sf[kb];
+      for (int dt = 0; dt < NDT; ++dt)
+        st4(cst + stash_tile_offset<CT, D>(dt, V, lane), S[dt][0], S[dt][1], S[dt][2], S[dt][3]);
     }
     __syncthreads();   // -Wm complete
 
@@ -203,7 +204,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
       CT* rst = (CT*)p.chunk_states + NR * D * D + rec * (C * D);
 #pragma unroll
       for (int it = 0; it < NCT; ++it)
-        st4(rst + ((it * NDT + V) * 64 + lane) * 4, Racc[it][0], Racc[it][1], Racc[it][2], Racc[it][3]);
+        st4(rst + stash_tile_offset<CT, D>(it, V, lane), Racc[it][0], Racc[it][1], Racc[it][2], Racc[it][3]);
     }
     // ---- Y = diag(gam) Q S0 + Aq R ----
     {
@@ -364,9 +365,10 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
     for (int kb = 0; kb < NDT / TPS; ++kb) dSf[kb] = acc_frag((CT*)nullptr, dS[kb * TPS], dS[kb * TPS + TPS - 1]);
     {
-      Frag* cst = (Frag*)p.ds_stash + rec * (D * D / FragLen<CT>::value);
+      CT* cst = (CT*)p.ds_stash + rec * (D * D);
 #pragma unroll
-      for (int kb = 0; kb < NDT / TPS; ++kb) cst[stash_frag_index<CT, D>(kb, V, lane)] = dSf[kb];
+      for (int dt = 0; dt < NDT; ++dt)
+        st4(cst + stash_tile_offset<CT, D>(dt, V, lane), dS[dt][0], dS[dt][1], dS[dt][2], dS[dt][3]);
     }
     // ---- dR = diag(dec) K dS + Aq^T dY ----
     Frag dYf[C / KS];
@@ -399,7 +401,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
       CT* bst = (CT*)p.ds_stash + NR * D * D + rec * (C * D);
 #pragma unroll
       for (int it = 0; it < NCT; ++it)
-        st4(bst + ((it * NDT + V) * 64 + lane) * 4, dB[it][0], dB[it][1], dB[it][2], dB[it][3]);
+        st4(bst + stash_tile_offset<CT, D>(it, V, lane), dB[it][0], dB[it][1], dB[it][2], dB[it][3]);
       // fragments of -diag(aeg) dB over k = token
 #pragma unroll
       for (int kb = 0; kb < NCT / TPS; ++kb) {
