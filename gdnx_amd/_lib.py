@@ -42,6 +42,9 @@ SIGNATURES = {
     "gdnx_gdn3_compact": (_c_int, [_vp] * 8 + [_c_int] * 8 + [_c_float, _vp]),
     "gdnx_kron_read": (_c_int, [_vp] * 6 + [_c_int] * 9 + [_vp]),
     "gdnx_gdn3_coeff": (_c_int, [_vp] * 3 + [_c_int] * 6 + [_vp]),
+    "gdnx_delta_chan_states_bytes": (_c_ll, [_c_int] * 4),
+    "gdnx_delta_chan_fwd": (_c_int, [_vp] * 11 + [_c_int] * 4 + [_vp]),
+    "gdnx_delta_chan_bwd": (_c_int, [_vp] * 17 + [_c_int] * 4 + [_vp]),
     "gdnx_gdn3_coeff_bwd": (_c_int, [_vp] * 6 + [_c_int] * 6 + [_vp]),
 }
 

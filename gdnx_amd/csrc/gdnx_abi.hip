@@ -396,3 +396,54 @@ extern "C" int gdnx_gdn3_coeff_bwd(const void* k, const float* beta, const float
   GCoeffArgs ga{k, beta, nullptr, da_e, da_w, dk, dbeta, B, T, H, M, head_dim, dtype};
   return gdn3_coeff_dispatch(ga, true, (hipStream_t)stream);
 }
+
+static int chan_common(const float* q, const float* k, const float* v, const float* be, const float* lg, int B, int T,
+                       int H, int D) {
+  g_err[0] = 0;
+  if (D != 64 && D != 128) return set_error(GDNX_ERR_SHAPE, "head_dim %d unsupported (64 or 128)", D);
+  if (B < 1 || T < 0 || H < 1 || (long long)B * H > (1LL << 30)) return set_error(GDNX_ERR_SHAPE, "bad sizes B=%d T=%d H=%d", B, T, H);
+  if ((long long)H * D * 16 * 4 >= (1LL << 31)) return set_error(GDNX_ERR_SHAPE, "H too large");
+  if (!q || !k || !v || !be || !lg) return set_error(GDNX_ERR_ARG, "q, k, v, beta_e, log_g must be non-null");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(lg))
+    return set_error(GDNX_ERR_ARG, "q, k, v, log_g must be 16-byte aligned");
+  return GDNX_OK;
+}
+
+extern "C" long long gdnx_delta_chan_states_bytes(int B, int T, int H, int head_dim) {
+  if (B < 1 || T < 0 || H < 1 || (head_dim != 64 && head_dim != 128)) return -1;
+  return (long long)chan_states_bytes(B * H, T, head_dim);
+}
+
+extern "C" int gdnx_delta_chan_fwd(const float* q, const float* k, const float* v, const float* beta_e,
+                                   const float* beta_w, const float* log_g, const float* state0, float* y,
+                                   float* state_out, void* chunk_states, float* r_norm, int B, int T, int H,
+                                   int head_dim, void* stream) {
+  int rc = chan_common(q, k, v, beta_e, log_g, B, T, H, head_dim);
+  if (rc) return rc;
+  if (!beta_w || !y) return set_error(GDNX_ERR_ARG, "beta_w and y must be non-null");
+  if (!aligned16(y) || (chunk_states && !aligned16(chunk_states)))
+    return set_error(GDNX_ERR_ARG, "y and chunk_states must be 16-byte aligned");
+  if (T == 0) return GDNX_OK;
+  ChanArgs a{q, k, v, beta_e, beta_w, log_g, state0, y, state_out, chunk_states, r_norm, B, T, H, head_dim};
+  return chan_fwd_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_delta_chan_bwd(const float* q, const float* k, const float* v, const float* beta_e,
+                                   const float* beta_w, const float* log_g, const float* dy,
+                                   const float* dstate_out, const void* chunk_states, void* workspace, float* dq,
+                                   float* dk, float* dv, float* dbeta_e, float* dbeta_w, float* dlog_g,
+                                   float* dstate0, int B, int T, int H, int head_dim, void* stream) {
+  int rc = chan_common(q, k, v, beta_e, log_g, B, T, H, head_dim);
+  if (rc) return rc;
+  if (!beta_w || !dy || !dq || !dk || !dv || !dbeta_e || !dbeta_w || !dlog_g)
+    return set_error(GDNX_ERR_ARG, "beta_w, dy and the gradient outputs must be non-null");
+  if (!chunk_states || !workspace)
+    return set_error(GDNX_ERR_WORKSPACE, "chunk_states (from the forward) and workspace are required");
+  if (!aligned16(dy) || !aligned16(chunk_states) || !aligned16(workspace) || !aligned16(dq) || !aligned16(dk) ||
+      !aligned16(dv) || !aligned16(dlog_g))
+    return set_error(GDNX_ERR_ARG, "dy, chunk_states, workspace and the key-sized outputs must be 16-byte aligned");
+  if (T == 0) return GDNX_OK;
+  ChanBwdArgs a{q, k, v, beta_e, beta_w, log_g, dy, dstate_out, chunk_states, workspace, dq, dk, dv,
+                dbeta_e, dbeta_w, dlog_g, dstate0, B, T, H, head_dim};
+  return chan_bwd_dispatch(a, (hipStream_t)stream);
+}

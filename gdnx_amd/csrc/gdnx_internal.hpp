@@ -54,6 +54,44 @@ struct GCoeffArgs {
   int B, T, H, M, D, dtype;
 };
 
+// Per-key-channel decay (one chain per head): float32 tensors, q/k/v/y/lg
+// [B,T,H,D], be/bw [B,T,H], states [B,H,D,D].
+struct ChanArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* be;
+  const float* bw;
+  const float* lg;     // natural-log decay per key channel
+  const float* s0;
+  float* y;
+  float* s_out;
+  void* chunk_states;
+  float* r_norm;
+  int B, T, H, D;
+};
+
+struct ChanBwdArgs {
+  const float* q;
+  const float* k;
+  const float* v;
+  const float* be;
+  const float* bw;
+  const float* lg;
+  const float* dy;
+  const float* ds_final;
+  const void* s_stash;   // the forward's chunk_states
+  void* ds_stash;        // workspace: state gradients, then dB
+  float* dq;
+  float* dk;
+  float* dv;
+  float* dbe;
+  float* dbw;
+  float* dlg;
+  float* ds0;
+  int B, T, H, D;
+};
+
 // Record an error message for gdnx_last_error(); returns code.
 int set_error(int code, const char* fmt, ...);
 // Check hipGetLastError() after a launch.
@@ -155,6 +193,9 @@ inline size_t delta_stash_bytes(int nchains, int T, int D, int C, int dtype) {
 }
 int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream);
 int gdn3_coeff_dispatch(const GCoeffArgs& a, bool bwd, hipStream_t stream);
+int chan_fwd_dispatch(const ChanArgs& a, hipStream_t stream);
+int chan_bwd_dispatch(const ChanBwdArgs& a, hipStream_t stream);
+size_t chan_states_bytes(int nchains, int T, int D);
 int delta_chunk_size(int D, int dtype);
 int delta_train_chunk_size(int D, int dtype);
 

@@ -16,10 +16,14 @@ score of scan_with_update_norm is |k_t| |beta_w v_t - beta_e m_t|
 
 Shapes: q [B,T,H,r_out,dk], k [B,T,H,dk], v [B,T,H,dv], g [B,T,H,dk]
 (multiplicative decay in (0, 1]), beta_e / beta_w [B,T,H], out_mix [H,r_out]
-(used when r_out > 1).  dk = dv in {64, 128}.  The HIP kernels carry one
-decay per token and head: g must be constant over dk (as in the GDN3 dense
-regime, where the lane decay is broadcast); a per-channel decay raises
-NotImplementedError rather than being approximated.
+(used when r_out > 1).  dk = dv in {64, 128}.
+
+Two kernel paths: a decay constant over dk (a per-token scalar, e.g. an
+expand over dk, or the layer at initialisation where decay_chan = 0) runs
+the scalar-decay kernels in the input dtype (bf16 or float32); a decay that
+varies over the key channels (gdn3/kmd2_native.py:163-164, g =
+exp(g_head + decay_chan)) runs the per-channel kernels (libgdnx
+gdnx_delta_chan_*), in float32.
 """
 from __future__ import annotations
 
@@ -38,39 +42,37 @@ def _mixed_query(q, out_mix):
     return (q.float() * w).sum(3).to(q.dtype)
 
 
-def _scalar_log_decay(g, check):
-    """log of the per-token decay, from g [B,T,H,dk] constant over dk.
-
-    Gradients are exact for a decay expanded over dk (stride 0, e.g.
-    g = gamma[..., None].expand(...)): autograd sums them into gamma.  A
-    materialised per-channel g has per-channel gradients these kernels do
-    not form, so it is refused when it requires grad."""
-    if g.requires_grad and g.shape[-1] > 1 and g.stride(-1) != 0:
-        raise NotImplementedError("gradients of a materialised per-channel decay are not implemented; "
-                                  "pass g as an expand over dk of a per-token decay")
-    g0 = g[..., 0]
-    if check and g.shape[-1] > 1 and g.stride(-1) != 0:
-        if not bool((g.amax(-1) == g.amin(-1)).all()):
-            raise NotImplementedError("per-channel decay (g varying over dk) is not implemented in gdnx_amd; "
-                                      "pass g constant over dk")
-    return torch.log(g0.float().clamp(min=1e-30))
+def _is_channel_constant(g):
+    """True when g [B,T,H,dk] carries one decay per token (stride 0 over dk,
+    or equal values across dk)."""
+    if g.shape[-1] == 1 or g.stride(-1) == 0:
+        return True
+    return bool((g.amax(-1) == g.amin(-1)).all())
 
 
-def _scan(q, k, v, g, beta_e, beta_w, out_mix, want_scores, check_decay=True):
+def _scan(q, k, v, g, beta_e, beta_w, out_mix, want_scores):
     B, T, H, r_out, dk = q.shape
     dv = v.shape[-1]
     if dk != dv:
         raise NotImplementedError(f"dk ({dk}) != dv ({dv}) is not supported")
-    dt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
-    qe = _mixed_query(q, out_mix).to(dt)
-    log_g = _scalar_log_decay(g, check_decay).unsqueeze(-1)
-    a_e = beta_e.float().unsqueeze(-1)
-    a_w = beta_w.float().unsqueeze(-1)
-    out = ops.delta_rule(qe, k.to(dt), v.to(dt), a_e, a_w, log_g, want_rnorm=want_scores)
-    y = out[0][:, :, :, 0]
+    if _is_channel_constant(g) and not (g.requires_grad and g.shape[-1] > 1 and g.stride(-1) != 0):
+        # one decay per token: the scalar-decay kernels (exact gradients also
+        # for an expand over dk, which autograd sums back into the token decay)
+        dt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
+        qe = _mixed_query(q, out_mix).to(dt)
+        log_g = torch.log(g[..., 0].float().clamp(min=1e-30)).unsqueeze(-1)
+        out = ops.delta_rule(qe, k.to(dt), v.to(dt), beta_e.float().unsqueeze(-1), beta_w.float().unsqueeze(-1),
+                             log_g, want_rnorm=want_scores)
+        y = out[0][:, :, :, 0]
+        rn = out[2][..., 0] if want_scores else None
+    else:
+        qe = _mixed_query(q.float(), out_mix)
+        log_g = torch.log(g.float().clamp(min=1e-30))
+        out = ops.delta_rule_chan(qe, k, v, beta_e, beta_w, log_g, want_rnorm=want_scores)
+        y = out[0].to(q.dtype) if q.dtype == torch.bfloat16 else out[0]
+        rn = out[2] if want_scores else None
     if not want_scores:
         return y
-    rn = out[2][..., 0]
     scores = (k.float().norm(dim=-1) * rn).detach()
     return y, scores
 

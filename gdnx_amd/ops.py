@@ -210,6 +210,101 @@ def delta_decode_step(q, k, v, a_e, a_w, log_g, state, out=None):
     return y
 
 
+# ---------------------------------------------------------------------------
+# per-key-channel decay (the general KMD-2 scan), float32, one chain per head
+# ---------------------------------------------------------------------------
+def _check_chan(q, k, v, beta_e, beta_w, log_g):
+    _need(q.is_cuda, "gdnx ops need CUDA (HIP) tensors")
+    _need(q.dim() == 4 and q.shape == k.shape == v.shape == log_g.shape, "q, k, v, log_g must be [B,T,H,D]")
+    _need(beta_e.shape == beta_w.shape == q.shape[:3], "beta_e, beta_w must be [B,T,H]")
+    for t in (q, k, v, beta_e, beta_w, log_g):
+        _need(t.dtype == torch.float32 and t.is_contiguous() and t.device == q.device,
+              "per-channel decay tensors must be contiguous float32 on one device")
+    return q.shape
+
+
+def delta_chan_fwd(q, k, v, beta_e, beta_w, log_g, state0=None, *, save_states=False, r_norm=None):
+    """Forward with a decay per key channel (gdnx_delta_chan_fwd).  Returns
+    (y [B,T,H,D], state_out [B,H,D,D], chunk_states or None)."""
+    lib = _lib.load()
+    B, T, H, D = _check_chan(q, k, v, beta_e, beta_w, log_g)
+    if state0 is not None:
+        _need(tuple(state0.shape) == (B, H, D, D) and state0.dtype == torch.float32 and state0.is_contiguous(),
+              "state0 must be contiguous float32 [B,H,D,D]")
+    if r_norm is not None:
+        _need(r_norm.shape == q.shape[:3] and r_norm.dtype == torch.float32 and r_norm.is_contiguous(),
+              "r_norm must be contiguous float32 [B,T,H]")
+    y = torch.empty_like(q)
+    s_out = torch.empty(B, H, D, D, dtype=torch.float32, device=q.device)
+    cs = None
+    if save_states:
+        cs = torch.empty(max(lib.gdnx_delta_chan_states_bytes(B, T, H, D), 16), dtype=torch.uint8, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_delta_chan_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(beta_e), _lib.ptr(beta_w),
+                                     _lib.ptr(log_g), _lib.ptr(state0), _lib.ptr(y), _lib.ptr(s_out), _lib.ptr(cs),
+                                     _lib.ptr(r_norm), B, T, H, D, _lib.stream_of(q))
+    _lib.check(rc, "gdnx_delta_chan_fwd")
+    return y, s_out, cs
+
+
+def delta_chan_bwd(q, k, v, beta_e, beta_w, log_g, dy, chunk_states, dstate_out=None, want_dstate0=False):
+    """Backward of delta_chan_fwd: (dq, dk, dv, dbeta_e, dbeta_w, dlog_g, dstate0 or None)."""
+    lib = _lib.load()
+    B, T, H, D = _check_chan(q, k, v, beta_e, beta_w, log_g)
+    dy = dy.float().contiguous()
+    if dstate_out is not None:
+        dstate_out = dstate_out.float().contiguous()
+    ws = torch.empty_like(chunk_states)
+    dq, dk, dv, dlg = (torch.empty_like(q) for _ in range(4))
+    dbe, dbw = torch.empty_like(beta_e), torch.empty_like(beta_w)
+    ds0 = torch.empty(B, H, D, D, dtype=torch.float32, device=q.device) if want_dstate0 else None
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_delta_chan_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(beta_e), _lib.ptr(beta_w),
+                                     _lib.ptr(log_g), _lib.ptr(dy), _lib.ptr(dstate_out), _lib.ptr(chunk_states),
+                                     _lib.ptr(ws), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(dbe),
+                                     _lib.ptr(dbw), _lib.ptr(dlg), _lib.ptr(ds0), B, T, H, D, _lib.stream_of(q))
+    _lib.check(rc, "gdnx_delta_chan_bwd")
+    return dq, dk, dv, dbe, dbw, dlg, ds0
+
+
+class ChanRuleFunction(torch.autograd.Function):
+    """y, S_T (and, when asked, the detached |r_t|) of the delta rule with a
+    decay per key channel, differentiable in q, k, v, beta_e, beta_w, log_g
+    and state0."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, beta_e, beta_w, log_g, state0=None, want_rnorm=False):
+        train = any(ctx.needs_input_grad)
+        rn = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if want_rnorm else None
+        y, s_out, cs = delta_chan_fwd(q, k, v, beta_e, beta_w, log_g, state0, save_states=train, r_norm=rn)
+        if train:
+            ctx.save_for_backward(q, k, v, beta_e, beta_w, log_g, cs)
+            ctx.has_state0 = state0 is not None
+        if rn is None:
+            return y, s_out
+        ctx.mark_non_differentiable(rn)
+        return y, s_out, rn
+
+    @staticmethod
+    def backward(ctx, dy, ds_out, *unused):
+        q, k, v, be, bw, lg, cs = ctx.saved_tensors
+        if dy is None:
+            dy = torch.zeros_like(q)
+        dq, dk, dv, dbe, dbw, dlg, ds0 = delta_chan_bwd(q, k, v, be, bw, lg, dy, cs, dstate_out=ds_out,
+                                                        want_dstate0=ctx.has_state0 and ctx.needs_input_grad[6])
+        return dq, dk, dv, dbe, dbw, dlg, ds0, None
+
+
+def delta_rule_chan(q, k, v, beta_e, beta_w, log_g, state0=None, want_rnorm=False):
+    """Differentiable delta rule with a per-key-channel log-decay log_g
+    [B,T,H,D] (one chain per head, float32 arithmetic); returns (y, S_T) and,
+    with want_rnorm, the detached |r_t| [B,T,H]."""
+    args = [t.float().contiguous() for t in (q, k, v, beta_e, beta_w, log_g)]
+    if state0 is not None:
+        state0 = state0.float().contiguous()
+    return ChanRuleFunction.apply(*args, state0, want_rnorm)
+
+
 def gdn3_coeff(k, beta):
     """a = alpha(beta |k|^2) beta [B,T,H,M] float32 (gdnx_gdn3_coeff) for k
     [B,T,H,D] (bf16/float32, shared by the M lanes) and beta [B,T,H,M]."""

@@ -149,6 +149,35 @@ int gdnx_delta_decode_step(const void* q, const void* k, const void* v,
                            int dtype, void* stream);
 
 
+/* ---- Per-key-channel decay (the general KMD-2 scan) -----------------------
+ * One chain per (batch, head), float32:  S <- diag(g_t) S (g per key
+ * channel, log_g = natural log, clamped to <= 0);  r = beta_w v -
+ * beta_e S^T k;  S <- S + k r^T;  y = S^T q.  Replaces the chunked KMD-2 scan
+ * with a per-channel decay (gdn3/kmd2_fast_scan.py:163-260; oracle
+ * research/kernel_ab/ref_scan.py:24-48 and gdn3/kmd2_native.py:109-132,
+ * where g = exp(g_head + decay_chan) [B,T,H,dk]).  Chunks of 16 tokens with
+ * the decay-weighted grams formed exactly per channel.
+ *   q, k, v, y, log_g, dq, dk, dv, dlog_g  [B, T, H, D] float32
+ *   beta_e, beta_w, dbeta_e, dbeta_w       [B, T, H] float32
+ *   state0, state_out, dstate_out, dstate0 [B, H, D, D] float32 (may be NULL)
+ *   r_norm [B, T, H] float32 or NULL: |r_t| (the KMD-2 update score is
+ *   |k_t| |r_t|)
+ * chunk_states (forward, for the backward) and the backward's workspace are
+ * gdnx_delta_chan_states_bytes bytes each. */
+long long gdnx_delta_chan_states_bytes(int B, int T, int H, int head_dim);
+int gdnx_delta_chan_fwd(const float* q, const float* k, const float* v, const float* beta_e,
+                        const float* beta_w, const float* log_g, const float* state0, float* y,
+                        float* state_out, void* chunk_states, float* r_norm, int B, int T, int H,
+                        int head_dim, void* stream);
+/* Backward of gdnx_delta_chan_fwd; dlog_g is zero where the log-decay was
+ * clamped. */
+int gdnx_delta_chan_bwd(const float* q, const float* k, const float* v, const float* beta_e,
+                        const float* beta_w, const float* log_g, const float* dy,
+                        const float* dstate_out, const void* chunk_states, void* workspace,
+                        float* dq, float* dk, float* dv, float* dbeta_e, float* dbeta_w,
+                        float* dlog_g, float* dstate0, int B, int T, int H, int head_dim,
+                        void* stream);
+
 /* GDN3 exact-alpha write coefficient in the dense regime (lane-shared keys,
  * one scalar gate per lane): a = alpha(beta |k|^2) beta with
  * alpha(c) = (1 - exp(-c)) / c (Taylor 1 - c/2 + c^2/6 below |c| = 1e-6).

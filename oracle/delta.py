@@ -29,6 +29,8 @@ Pinning (see tests/test_oracle_delta.py):
       (v=0 => y=0, gamma=0 resets, beta=0 => pure decay).
   kmd2_scan             -- same, plus the r_out mixing identity.
   delta_rule_chunked    -- equals delta_rule_sequential in float64 to 1e-12.
+  delta_rule_chunked_chan -- per-key-channel decay; equals
+                           delta_rule_sequential (per-channel gamma) in float64.
   stable_alpha          -- closed form, Taylor branch and branch continuity.
 """
 from __future__ import annotations
@@ -42,6 +44,7 @@ __all__ = [
     "stable_alpha",
     "delta_rule_sequential",
     "delta_rule_chunked",
+    "delta_rule_chunked_chan",
     "kmd2_scan",
     "gdn3_dense_coeffs",
     "gdn3_dense_layer",
@@ -124,6 +127,53 @@ def delta_rule_chunked(q, k, e, w, log_gamma, chunk: int = 64, state0=None,
         ys.append(gam.unsqueeze(-1) * (Q @ S) + Aq @ R)
         dec = (G[:, -1:] - G).exp()
         S = G[:, -1].exp().view(N, 1, 1) * S + (K * dec.unsqueeze(-1)).transpose(1, 2) @ R
+    return torch.cat(ys, 1), S
+
+
+def delta_rule_chunked_chan(q, k, a_e, w, log_gamma, chunk: int = 16, state0=None,
+                            log_floor: float = -60.0):
+    """Chunk form of ``delta_rule_sequential`` with a decay per key channel.
+
+    q, k: [N, T, dk]; a_e: [N, T] erase coefficient (e_t = a_e,t k_t);
+    w: [N, T, dv]; log_gamma: [N, T, dk] natural log of the decay (clamped
+    to [log_floor, 0]).  Within a chunk with carried state S0 and per-channel
+    inclusive prefix G_i = sum_{s<=i} log g_s ([dk] per token):
+
+        M_ij  = sum_d x_id k_jd exp(G_id - G_jd), j <= i  (every exponent <= 0)
+        (I + L) R = W - diag(a_e) (K o e^G) S0,   L_ij = a_e,i M_ij[x=k], j < i
+        Y     = (Q o e^G) S0 + Aq R,              Aq_ij = M_ij[x=q], j <= i
+        S_C   = diag(e^{G_last}) S0 + (K o e^{G_last - G})^T R
+
+    (gdn3/kmd2_native.py:109-132 restated per chunk; the reference's chunked
+    path gdn3/kmd2_fast_scan.py:198-214 divides by the cumulative product
+    instead).  The decay-weighted grams are formed per channel, so no factor
+    ever exceeds 1.  Differentiable with torch autograd.
+    """
+    N, T, dk = k.shape
+    dv = w.shape[-1]
+    S = k.new_zeros(N, dk, dv) if state0 is None else state0
+    lg = log_gamma.clamp(min=log_floor, max=0.0)
+    ys = []
+    for t0 in range(0, T, chunk):
+        t1 = min(T, t0 + chunk)
+        c = t1 - t0
+        Q, K, ae, W = q[:, t0:t1], k[:, t0:t1], a_e[:, t0:t1], w[:, t0:t1]
+        G = lg[:, t0:t1].cumsum(1)                                   # [N, c, dk]
+        idx = torch.arange(c)
+        incl = (idx.view(c, 1) >= idx.view(1, c)).view(1, c, c, 1)
+        diff = G.unsqueeze(2) - G.unsqueeze(1)                       # [N, i, j, dk]
+        Dx = torch.where(incl, diff, torch.full_like(diff, -math.inf)).exp()
+        Mk = torch.einsum("nid,njd,nijd->nij", K, K, Dx)
+        Mq = torch.einsum("nid,njd,nijd->nij", Q, K, Dx)
+        strict = idx.view(c, 1) > idx.view(1, c)
+        L = torch.where(strict, ae.unsqueeze(-1) * Mk, torch.zeros_like(Mk))
+        E = G.exp()
+        rhs = W - ae.unsqueeze(-1) * ((K * E) @ S)
+        eye = torch.eye(c, dtype=k.dtype).expand(N, c, c)
+        R = torch.linalg.solve_triangular(eye + L, rhs, upper=False, unitriangular=True)
+        ys.append((Q * E) @ S + Mq @ R)
+        F = (G[:, -1:] - G).exp()
+        S = G[:, -1].exp().unsqueeze(-1) * S + (K * F).transpose(1, 2) @ R
     return torch.cat(ys, 1), S
 
 

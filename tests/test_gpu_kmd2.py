@@ -2,8 +2,9 @@
 (oracle.delta.kmd2_scan, a restatement of research/kernel_ab/ref_scan.py:24-48
 pinned by the reference's known-answer tests in tests/test_oracle_delta.py).
 
-Decay is per token and head, expanded over dk (the form the HIP kernels
-carry); the reference's interface and argument names are kept
+Decay per token and head, expanded over dk, runs the scalar-decay kernels; a
+decay that varies over dk (gdn3/kmd2_native.py:163-164) runs the per-channel
+kernels.  The reference's interface and argument names are kept
 (tests/ablation/test_fast_scan_api.py:13,30-39 enforce them upstream)."""
 import inspect
 
@@ -78,10 +79,50 @@ def test_scan_gradients_match_oracle(gpu_lib):
         assert rel_l2(a, b) <= 1e-4, name
 
 
-def test_per_channel_decay_is_refused(gpu_lib):
+def _chan_decay(B, T, H, d, seed):
+    g = torch.Generator().manual_seed(seed)
+    head = -0.05 * torch.rand(B, T, H, 1, generator=g)
+    chan = -torch.rand(1, 1, H, d, generator=g) * 0.5      # decay_chan <= 0 per head and channel
+    return torch.exp(head + chan)
+
+
+@pytest.mark.parametrize("r_out", [1, 4])
+def test_per_channel_decay_matches_oracle(gpu_lib, r_out):
+    """g varying over dk (the reference's g = exp(g_head + decay_chan)):
+    outputs, update scores and every gradient, g's included."""
     from gdnx_amd import kmd2
-    B, T, H, d = 1, 16, 1, 64
-    q, k, v, gamma, be, bw, _ = _inputs(B, T, H, 1, d, seed=2, dtype=torch.float32)
-    g = torch.rand(B, T, H, d) * 0.1 + 0.9  # varies over dk
-    with pytest.raises(NotImplementedError):
-        kmd2.scan(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), be.to(DEV), bw.to(DEV))
+    print(f"case: kmd2 per-channel r_out={r_out}", flush=True)
+    B, T, H, d = 2, 70, 2, 64
+    q, k, v, _, be, bw, mix = _inputs(B, T, H, r_out, d, seed=17, dtype=torch.float32)
+    g = _chan_decay(B, T, H, d, seed=18)
+    dy = torch.randn(B, T, H, d, generator=torch.Generator().manual_seed(19))
+    xs = [x for x in (q, k, v, g, be, bw, mix) if x is not None]
+    leaves = [x.to(DEV).requires_grad_(True) for x in xs]
+    args = leaves + ([None] if mix is None else [])
+    y, sc = kmd2.scan_with_update_norm(*args)
+    grads = torch.autograd.grad(y, leaves, dy.to(DEV))
+    ref = [x.double().requires_grad_(True) for x in xs]
+    rargs = ref + ([None] if mix is None else [])
+    yr, scr = delta.kmd2_scan(*rargs, return_scores=True)
+    gref = torch.autograd.grad(yr, ref, dy.double())
+    torch.cuda.synchronize()
+    assert rel_l2(y, yr) <= 1e-4
+    assert rel_l2(sc, scr) <= 1e-4
+    for name, a, b in zip(("q", "k", "v", "g", "beta_e", "beta_w", "out_mix"), grads, gref):
+        err = rel_l2(a, b)
+        print(f"  d{name} rel-L2 {err:.2e}", flush=True)
+        assert err <= 1e-4, name
+
+
+def test_per_channel_decay_bf16_inputs(gpu_lib):
+    """bf16 q/k/v with a per-channel decay compute in float32 and return y
+    in bf16."""
+    from gdnx_amd import kmd2
+    print("case: kmd2 per-channel bf16", flush=True)
+    B, T, H, d = 1, 40, 2, 128
+    q, k, v, _, be, bw, _ = _inputs(B, T, H, 1, d, seed=23, dtype=torch.bfloat16)
+    g = _chan_decay(B, T, H, d, seed=24)
+    y = kmd2.scan(q.to(DEV), k.to(DEV), v.to(DEV), g.to(DEV), be.to(DEV), bw.to(DEV))
+    yr = delta.kmd2_scan(q, k, v, g, be, bw)
+    assert y.dtype == torch.bfloat16
+    assert rel_l2(y, yr) <= 1e-2

@@ -136,6 +136,51 @@ def test_chunked_gradients_equal_sequential():
         torch.testing.assert_close(a, b, atol=1e-10, rtol=1e-9)
 
 
+def _chan_inputs(N=3, T=45, dk=8, dv=6, seed=5, strong=False):
+    gen = torch.Generator().manual_seed(seed)
+    d = torch.float64
+    q = torch.randn(N, T, dk, generator=gen, dtype=d)
+    k = torch.nn.functional.normalize(torch.randn(N, T, dk, generator=gen, dtype=d), dim=-1)
+    ae = torch.sigmoid(torch.randn(N, T, generator=gen, dtype=d))
+    w = torch.randn(N, T, dv, generator=gen, dtype=d)
+    scale = 6.0 if strong else 1.2
+    lg = -torch.nn.functional.softplus(scale * torch.randn(N, T, dk, generator=gen, dtype=d) - 0.6)
+    return q, k, ae, w, lg
+
+
+@pytest.mark.parametrize("chunk,strong", [(1, False), (16, False), (16, True), (7, True)])
+def test_chunked_chan_equals_sequential_fp64(chunk, strong):
+    """Per-key-channel decay: the chunk algebra (decay-weighted grams formed
+    per channel) equals the token loop, also with decays down to e^-40 per
+    token, where a cumulative-product ratio would under/overflow."""
+    q, k, ae, w, lg = _chan_inputs(strong=strong)
+    y0, s0 = delta.delta_rule_sequential(q, k, k * ae.unsqueeze(-1), w, lg.exp())
+    y1, s1 = delta.delta_rule_chunked_chan(q, k, ae, w, lg, chunk=chunk)
+    torch.testing.assert_close(y1, y0, atol=1e-11, rtol=1e-10)
+    torch.testing.assert_close(s1, s0, atol=1e-11, rtol=1e-10)
+
+
+def test_chunked_chan_reduces_to_scalar_decay():
+    """A decay constant over the channels gives the scalar-decay chunk form."""
+    q, k, ae, w, lg = _chan_inputs()
+    lg1 = lg[..., :1]
+    y0, s0 = delta.delta_rule_chunked(q, k, k * ae.unsqueeze(-1), w, lg1[..., 0], chunk=16)
+    y1, s1 = delta.delta_rule_chunked_chan(q, k, ae, w, lg1.expand_as(lg), chunk=16)
+    torch.testing.assert_close(y1, y0, atol=1e-11, rtol=1e-10)
+
+
+def test_chunked_chan_gradients_equal_sequential():
+    ins = [t.requires_grad_(True) for t in _chan_inputs(T=21)]
+    q, k, ae, w, lg = ins
+    y0, _ = delta.delta_rule_sequential(q, k, k * ae.unsqueeze(-1), w, lg.exp())
+    up = torch.randn_like(y0)
+    g0 = torch.autograd.grad((y0 * up).sum(), ins)
+    y1, _ = delta.delta_rule_chunked_chan(*ins, chunk=8)
+    g1 = torch.autograd.grad((y1 * up).sum(), ins)
+    for a, b in zip(g0, g1):
+        torch.testing.assert_close(a, b, atol=1e-10, rtol=1e-9)
+
+
 def test_invariants_zero_value_zero_decay_zero_beta():
     q, k, e, w, lg = _chain_inputs()
     y, _ = delta.delta_rule_sequential(q, k, e, torch.zeros_like(w), lg.exp())
