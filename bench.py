@@ -290,6 +290,142 @@ def bench_gdn3(args, layer_default):
     print(json.dumps(line), flush=True)
 
 
+MFMA_FP32_PEAK = 157.3e12   # dense fp32 FLOP/s
+
+
+def kmd2_inputs(B, T, H, r_out, d, seed=7):
+    """The reference's scan-benchmark distribution (research/kernel_ab/
+    bench_scan.py:39-55): q ~ N(0, 1/d), unit keys, per-channel decay
+    exp(-softplus(1.2 z - 0.6)) spanning (0, 1), sigmoid gates, out_mix ~ N(0, 1)."""
+    import torch
+    import torch.nn.functional as F
+    g = torch.Generator().manual_seed(seed)
+    q = torch.randn(B, T, H, r_out, d, generator=g) * d ** -0.5
+    k = F.normalize(torch.randn(B, T, H, d, generator=g), dim=-1)
+    v = torch.randn(B, T, H, d, generator=g)
+    dec = torch.exp(-F.softplus(torch.randn(B, T, H, d, generator=g) * 1.2 - 0.6))
+    be = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    bw = torch.sigmoid(torch.randn(B, T, H, generator=g))
+    mix = torch.randn(H, r_out, generator=g)
+    dy = torch.randn(B, T, H, d, generator=g)
+    return (q, k, v, dec, be, bw, mix), dy
+
+
+def flops_chan(B, T, H, D, C=16):
+    """Algorithmic FLOP of the per-channel forward per (b, h, chunk): the two
+    exact decay-weighted grams 4 C^2 D, Wm and U 4 C^2 D, Wm S0 / Q S0 / the
+    carry 6 C D^2, the masked output product 2 C^2 D and the inverse C^3/3;
+    forward + backward = 3x."""
+    nchunks = B * H * ((T + C - 1) // C)
+    return nchunks * (10 * C * C * D + 6 * C * D * D + C ** 3 / 3)
+
+
+def cpu_baseline_kmd2(T=512, B=1, H=16, H_full=16, r_out=4, d=128):
+    """The CPU oracle (fp32 token loop + autograd) on B x T tokens of H heads;
+    tokens/s scaled to the benchmark's 16 heads."""
+    import torch
+    from oracle import delta
+    torch.set_num_threads(os.cpu_count() or 1)
+    xs, dy = kmd2_inputs(B, T, H, r_out, d)
+    leaves = [x.requires_grad_(True) for x in xs]
+    t0 = time.perf_counter()
+    y = delta.kmd2_scan(*leaves, dtype=torch.float32)
+    torch.autograd.grad(y, leaves, dy)
+    secs = time.perf_counter() - t0
+    return {"value": B * T / secs * H / H_full, "unit": "tokens/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"oracle.delta.kmd2_scan fp32 fwd+bwd, B={B} T={T} H={H} r_out={r_out} d={d} "
+                      f"({secs:.1f} s), scaled to H={H_full}"}
+
+
+def bench_kmd2(args):
+    """KMD-2 native scan with per-channel decay, the reference's kernel-search
+    benchmark (research/kernel_ab/bench_scan.py:26-29): primary metric
+    forward+backward tokens/s at the train shape B=2, T=512, H=16, r_out=4,
+    dk=dv=128, float32; also the eval shape's forward (B=1, T=2048).  One step
+    = kmd2.scan forward + gradients of all seven inputs."""
+    import torch
+    from gdnx_amd import kmd2, ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, T, H, R, D = 2, 512, 16, 4, 128
+    xs, dy = kmd2_inputs(B, T, H, R, D)
+    leaves = [x.to(dev).requires_grad_(True) for x in xs]
+    dy = dy.to(dev)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        y = kmd2.scan(*leaves)
+        return torch.autograd.grad(y, leaves, dy)
+
+    def timed(fn, n):
+        for _ in range(max(1, args.warmup)):
+            fn()
+        torch.cuda.synchronize()
+        s0, s1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        s0.record(stream)
+        for _ in range(n):
+            out = fn()
+        s1.record(stream)
+        torch.cuda.synchronize()
+        return s0.elapsed_time(s1) * 1e-3 / n, out
+
+    sec, grads = timed(step, args.steps)
+    finite = all(bool(torch.isfinite(t).all()) for t in grads)
+    # eval shape, forward only
+    xe, _ = kmd2_inputs(1, 2048, H, R, D, seed=8)
+    xe = [x.to(dev) for x in xe]
+    with torch.no_grad():
+        sec_eval, _ = timed(lambda: kmd2.scan(*xe), args.steps)
+
+    # per-kernel means at the train shape
+    with torch.no_grad():
+        q = kmd2._mixed_query(leaves[0].detach(), leaves[6].detach()).contiguous()
+        k, v = leaves[1].detach(), leaves[2].detach()
+        lg = torch.log(leaves[3].detach().clamp(min=1e-30))
+        be, bw = leaves[4].detach(), leaves[5].detach()
+        st = {}
+
+        def fwd():
+            st["y"], _, st["cs"] = ops.delta_chan_fwd(q, k, v, be, bw, lg, save_states=True)
+        t_fwd, _ = timed(fwd, args.kernel_iters)
+        t_bwd, _ = timed(lambda: ops.delta_chan_bwd(q, k, v, be, bw, lg, dy, st["cs"]), args.kernel_iters)
+    f_fwd = flops_chan(B, T, H, D)
+    kernels = {"chan_fwd_kernel": (t_fwd, f_fwd), "chan_bwd_scan_kernel+chan_grads_kernel": (t_bwd, 2 * f_fwd)}
+    dom = max(kernels, key=lambda n: kernels[n][0])
+    t_dom, f_dom = kernels[dom]
+    achieved = f_dom / t_dom / 1e12
+    line = {
+        "metric": "KMD-2 scan tokens/s fwd+bwd @B=2,T=512 (per-channel decay)",
+        "value": B * T / sec,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "reference scan benchmark, train shape: B=2 T=512 H=16 r_out=4 dk=dv=128, "
+                               "per-channel decay exp(-softplus(1.2 z - 0.6))",
+                   "batch": B, "seq_len": T, "heads": H, "r_out": R, "head_dim": D, "chunk": 16,
+                   "parallelism": "single GPU"},
+        "eval_fwd_tokens_per_s": 2048 / sec_eval,
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": MFMA_FP32_PEAK / 1e12,
+                     "unit": "TFLOP/s", "frac": achieved * 1e12 / MFMA_FP32_PEAK,
+                     "traffic": measured_traffic(dom), "mean_us": t_dom * 1e6, "algorithmic_flop": f_dom,
+                     "note": "32 chains of 32 chunks: the two scans run one workgroup per chain"},
+        "kernels_us": {n: round(t * 1e6, 2) for n, (t, _) in kernels.items()},
+        "grads_finite": finite,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_kmd2()
+    print(json.dumps(line), flush=True)
+
+
 def bench_copy(args):
     """Calibration for the HBM traffic counters: a plain device copy of a
     known size (1 GiB read + 1 GiB written per launch).  Prints its own JSON
@@ -322,11 +458,12 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=10)
-    ap.add_argument("--workload", choices=("train", "decode", "longctx", "gdn3-layer", "copy"),
+    ap.add_argument("--workload", choices=("train", "decode", "longctx", "gdn3-layer", "kmd2", "copy"),
                     default="train",
                     help="train: config 2 scan fwd+bwd (headline); decode: config 4 decode step; "
                          "longctx: config 3 GDN3 with compaction; gdn3-layer: GDN3 compaction every "
-                         "16 tokens; copy: 1 GiB device copy used to calibrate the HBM traffic counters")
+                         "16 tokens; kmd2: KMD-2 scan with per-channel decay fwd+bwd (reference scan "
+                         "benchmark, train shape); copy: 1 GiB device copy used to calibrate the HBM traffic counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the recurrence shards by chains with no "
@@ -336,6 +473,8 @@ def main():
         return bench_decode(args)
     if args.workload == "copy":
         return bench_copy(args)
+    if args.workload == "kmd2":
+        return bench_kmd2(args)
     if args.workload in ("longctx", "gdn3-layer"):
         return bench_gdn3(args, layer_default=args.workload == "gdn3-layer")
 

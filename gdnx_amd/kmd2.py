@@ -16,7 +16,10 @@ score of scan_with_update_norm is |k_t| |beta_w v_t - beta_e m_t|
 
 Shapes: q [B,T,H,r_out,dk], k [B,T,H,dk], v [B,T,H,dv], g [B,T,H,dk]
 (multiplicative decay in (0, 1]), beta_e / beta_w [B,T,H], out_mix [H,r_out]
-(used when r_out > 1).  dk = dv in {64, 128}.
+(used when r_out > 1).  dk, dv <= 128: the kernels run at D = 64 or 128
+and narrower dims are zero-padded, which is exact (a zero key channel never
+enters the state, a zero value column stays zero; padded outputs are sliced
+off, so their gradients are zero too).
 
 Two kernel paths: a decay constant over dk (a per-token scalar, e.g. an
 expand over dk, or the layer at initialisation where decay_chan = 0) runs
@@ -50,27 +53,41 @@ def _is_channel_constant(g):
     return bool((g.amax(-1) == g.amin(-1)).all())
 
 
+def _kernel_dim(dk, dv):
+    D = max(dk, dv)
+    if D > 128:
+        raise NotImplementedError(f"dk={dk}, dv={dv}: the kernels carry head dims up to 128")
+    return 64 if D <= 64 else 128
+
+
+def _pad_last(x, D, value=0.0):
+    n = x.shape[-1]
+    return x if n == D else torch.nn.functional.pad(x, (0, D - n), value=value)
+
+
 def _scan(q, k, v, g, beta_e, beta_w, out_mix, want_scores):
     B, T, H, r_out, dk = q.shape
     dv = v.shape[-1]
-    if dk != dv:
-        raise NotImplementedError(f"dk ({dk}) != dv ({dv}) is not supported")
-    if _is_channel_constant(g) and not (g.requires_grad and g.shape[-1] > 1 and g.stride(-1) != 0):
+    D = _kernel_dim(dk, dv)
+    scalar = _is_channel_constant(g) and not (g.requires_grad and g.shape[-1] > 1 and g.stride(-1) != 0)
+    qe = _mixed_query(q if scalar else q.float(), out_mix)
+    qe, kp, vp = _pad_last(qe, D), _pad_last(k, D), _pad_last(v, D)
+    if scalar:
         # one decay per token: the scalar-decay kernels (exact gradients also
         # for an expand over dk, which autograd sums back into the token decay)
         dt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
-        qe = _mixed_query(q, out_mix).to(dt)
         log_g = torch.log(g[..., 0].float().clamp(min=1e-30)).unsqueeze(-1)
-        out = ops.delta_rule(qe, k.to(dt), v.to(dt), beta_e.float().unsqueeze(-1), beta_w.float().unsqueeze(-1),
-                             log_g, want_rnorm=want_scores)
+        out = ops.delta_rule(qe.to(dt), kp.to(dt), vp.to(dt), beta_e.float().unsqueeze(-1),
+                             beta_w.float().unsqueeze(-1), log_g, want_rnorm=want_scores)
         y = out[0][:, :, :, 0]
         rn = out[2][..., 0] if want_scores else None
     else:
-        qe = _mixed_query(q.float(), out_mix)
-        log_g = torch.log(g.float().clamp(min=1e-30))
-        out = ops.delta_rule_chan(qe, k, v, beta_e, beta_w, log_g, want_rnorm=want_scores)
+        # a padded key channel has no key, so its decay (1) never matters
+        log_g = _pad_last(torch.log(g.float().clamp(min=1e-30)), D)
+        out = ops.delta_rule_chan(qe, kp, vp, beta_e, beta_w, log_g, want_rnorm=want_scores)
         y = out[0].to(q.dtype) if q.dtype == torch.bfloat16 else out[0]
         rn = out[2] if want_scores else None
+    y = y[..., :dv] if dv != D else y
     if not want_scores:
         return y
     scores = (k.float().norm(dim=-1) * rn).detach()
