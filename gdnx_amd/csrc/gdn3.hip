@@ -26,45 +26,11 @@
 //
 // One workgroup per chain carries the whole state in LDS; the chunk loop
 // is sequential because every compaction depends on the window it closes.
-#include "delta_common.hpp"
-#include "gdnx_common.hpp"
+#include "gdn3_common.hpp"
 #include "gdnx_internal.hpp"
 
 namespace gdnx {
 namespace {
-
-constexpr int kRMax = 4;    // Kronecker rank bound
-constexpr int kQ = 8;       // sketch width bound: min(R + 4, m, n) <= 8
-constexpr int kMN = 256;    // bound on m = a_v a_k and n = b_v b_k
-constexpr int kAB = 1280;   // bound on R (m + n) for m n = d^2, m, n <= 256
-constexpr int kNT = 256;
-
-// Kronecker geometry of the layer (gdn3/gdn3_upgrade.py:73-77: rank 4,
-// a_k = 16, b_k = 8, so (a_v, a_k, b_v, b_k) = (16, 16, 8, 8) at head dim 128;
-// (8, 8, 8, 8) at head dim 64).  Compile-time, so every loop over the
-// factors unrolls and every index split is a shift.
-template <int D> struct G3C;
-template <> struct G3C<128> { static constexpr int R = 4, av = 16, ak = 16, bv = 8, bk = 8, lbv = 3, lbk = 3; };
-template <> struct G3C<64> { static constexpr int R = 4, av = 8, ak = 8, bv = 8, bk = 8, lbv = 3, lbk = 3; };
-template <int D> struct G3D : G3C<D> {
-  static constexpr int m = G3C<D>::av * G3C<D>::ak, n = G3C<D>::bv * G3C<D>::bk;
-  static constexpr int q = (G3C<D>::R + 4 < m ? (G3C<D>::R + 4 < n ? G3C<D>::R + 4 : n) : (m < n ? m : n));
-  static constexpr int ln = G3C<D>::lbv + G3C<D>::lbk;
-  static_assert((1 << G3C<D>::lbv) == G3C<D>::bv && (1 << G3C<D>::lbk) == G3C<D>::bk && m <= kMN && n <= kMN &&
-                    q <= kQ && G3C<D>::R <= kRMax, "geometry");
-};
-
-__device__ __forceinline__ float stable_alpha_f(float c) {
-  // (1 - e^{-c}) / c with its series near 0 (gdn3/gdn3_upgrade.py:641-648)
-  if (fabsf(c) < 1e-6f) return 1.f - 0.5f * c + c * c * (1.f / 6.f);
-  return -expm1f(-c) / c;
-}
-
-__device__ __forceinline__ float log_decay(float d) {
-  // clamp(dec, 0, 1) as a natural-log decay, floored at kLogFloor
-  d = fminf(d, 1.f);
-  return d > 0.f ? fmaxf(logf(d), kLogFloor) : kLogFloor;
-}
 
 // Sum of NV doubles over the 256 threads of the block, in a fixed order;
 // every thread receives the totals.  red: 4 * NV doubles of LDS.
@@ -824,8 +790,16 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
         }
 #pragma unroll
         for (int it = 0; it < PT; ++it) uo[it][a] = un[it];
+        if (p.ts_u) {   // training stash: this chunk's net writes
+          float* us = p.ts_u + ((size_t)chain * p.nch + c) * P * D + v;
+#pragma unroll
+          for (int it = 0; it < PT; ++it)
+#pragma unroll
+            for (int s = 0; s < 4; ++s) us[(size_t)(it * 16 + 4 * g4 + s) * D] = un[it][s];
+        }
       }
     }
+    if (p.ts_g && tid == 0) p.ts_g[(size_t)chain * p.nch + c] = gacc;
     // window keys for the next chunk: k_j decayed to this chunk's end
     for (int e = tid; e < P * D; e += kNT) {
       const int j = e / D, d = e % D;
@@ -904,18 +878,13 @@ __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
     p.B_out[(size_t)chain * Rn + e] = sm.ab[Rm + e];
     if (p.B_fin) p.B_fin[(size_t)chain * Rn + e] = sm.ab[Rm + e];
   }
+  if (p.ab_stash)
+    for (int e = tid; e < Rm + Rn; e += kNT) p.ab_stash[(size_t)chain * (Rm + Rn) + e] = sm.ab[e];
   if (p.skron) {  // sum_r A_r (x) B_r as a [D][D] (v, k) matrix for the next interval's reads
     CT* sk = (CT*)p.skron + (size_t)chain * D * D;
     const float* Af = sm.ab;
     const float* Bf = sm.ab + Rm;
-    for (int e = tid; e < D * D; e += kNT) {
-      const int v = e / D, k = e % D;
-      const int iv = v >> Ge::lbv, jv = v & (Ge::bv - 1), ik = k >> Ge::lbk, jk = k & (Ge::bk - 1);
-      float s = 0.f;
-#pragma unroll
-      for (int r = 0; r < Ge::R; ++r) s += Af[r * Ge::m + iv * Ge::ak + ik] * Bf[r * Ge::n + jv * Ge::bk + jk];
-      sk[e] = from_f<CT>(s);
-    }
+    for (int e = tid; e < D * D; e += kNT) sk[e] = from_f<CT>(kron_entry<D>(Af, Bf, e / D, e % D));
   }
 }
 
@@ -1008,6 +977,11 @@ int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
   int rc = check_launch("fill_zero_kernel");
   if (rc) return rc;
   const int nch = (a.T + P - 1) / P, per = a.Kc / P;
+  a.nch = nch;
+  G3Stash ts{nullptr, nullptr, nullptr};
+  if (a.train_states) ts = g3_stash(a.train_states, N, nch, a.T / a.Kc, D, P, Ge::RMN);
+  a.ts_u = ts.u;
+  a.ts_g = ts.gacc;
   int event = 0;
   for (int c0 = 0; c0 < nch; c0 += per) {
     const int c1 = c0 + per < nch ? c0 + per : nch;
@@ -1041,6 +1015,7 @@ int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
       ca.skron_dtype = a.dtype;
       ca.A_fin = a.last ? a.A_out : nullptr;
       ca.B_fin = a.last ? a.B_out : nullptr;
+      ca.ab_stash = ts.ab ? ts.ab + (size_t)event * N * Ge::RMN : nullptr;
       if ((rc = compact_dispatch(ca, stream))) return rc;
       ++event;
     }
@@ -1055,6 +1030,12 @@ size_t gdn3_workspace_bytes(int N, int D, int P, int dtype) {
   const int R = 4, mn = D == 128 ? 256 + 64 : 64 + 64;
   return align256((size_t)N * D * D * cb) + align256((size_t)N * R * mn * 4) + 2 * align256((size_t)N * P * D * 4) +
          align256((size_t)N * 4);
+}
+
+size_t gdn3_train_states_bytes(int N, int T, int D, int P, int Kc) {
+  const int nch = (T + P - 1) / P, ncomp = T / Kc;
+  const int rmn = D == 128 ? G3D<128>::RMN : G3D<64>::RMN;
+  return g3_stash_bytes(N, nch, ncomp, D, P, rmn);
 }
 
 int gdn3_fwd_dispatch(const G3FwdArgs& a, hipStream_t stream) {

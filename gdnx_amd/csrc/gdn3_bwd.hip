@@ -1,0 +1,554 @@
+// GDN3 Kronecker-residual recurrence, backward (gfx950).
+//
+// Gradient semantics of the frozen oracle (gdn3/_reference_recurrence.py:
+// 60-90): the compaction runs under no_grad, so the factors A, B it leaves
+// are constants, while the residual slots (U, Vb) keep their graph across
+// compactions.  With chunks aligned to the P-slot window (see gdn3.hip), a
+// chunk's outputs depend on
+//   its own tokens, the previous chunk's net writes U_old and keys decayed to
+//   that chunk's end Vbd_old, the Kronecker matrix S_kron of the last
+//   compaction (a constant) and the log decay Gacc accumulated since it.
+// Per chunk, with G_i the inclusive log-decay prefix, gamma_i = e^{G_i},
+// e2_i = e^{2(Gacc + G_i)}, H = b o k, u = w o v, alpha_i = alpha(k_i . h_i):
+//   Lm_ij = alpha_i e^{G_i-G_j} (h_i.k_j) (j<i),  T = (I + Lm)^-1
+//   Ho_ip = alpha_i gamma_i (h_i.Vbd_old_p) (p>=i), Qo_ip = gamma_i (q_i.Vbd_old_p) (p>=i)
+//   Aq_ij = e^{G_i-G_j} (q_i.k_j) (j<=i)
+//   U = T (diag(alpha) u - diag(alpha e2) H S_kron^T - Ho U_old)
+//   Y = diag(e2) Q S_kron^T + Qo U_old + Aq U
+//   Vbd_j = k_j e^{G_last - G_j} (what the next chunk sees), Gacc' = Gacc + G_last
+// The backward walks the chunks in reverse, one workgroup per chain, carrying
+// dU (for the previous chunk's U), dVbd (for its decayed keys) and dGacc
+// (reset at every compaction boundary), and recomputes each chunk's grams,
+// inverse and coefficients from its inputs and the forward's stash (U per
+// chunk, Gacc per chunk, the factors after every compaction).  Every
+// product is fp32 MFMA.  The reference differentiates its chunk graph with
+// torch autograd (gdn3/gdn3_upgrade.py:467-521).
+#include "gdn3_common.hpp"
+#include "gdnx_internal.hpp"
+
+namespace gdnx {
+namespace {
+
+constexpr int BP = 16;  // the window P of the backward
+
+template <typename CT, int D>
+struct alignas(16) G3BwdSmem {
+  static constexpr int LR = D + 4;                              // fp32 rows
+  static constexpr int LK = D + (sizeof(CT) == 2 ? 8 : 4);      // S_kron^T rows
+  static constexpr int LP = BP + 4;                             // P x P matrices
+  float h[BP][LR], q[BP][LR], k[BP][LR];  // H = b o k, Q, K of the chunk
+  float vb[BP][LR];                       // previous chunk's keys, then decayed to its end (Vbd_old)
+  float dy[BP][LR], u[BP][LR], uo[BP][LR];
+  float dr[BP][LR];                       // dRhs (and the factors while S_kron^T is rebuilt)
+  CT skt[D][LK];                          // S_kron^T: skt[k][v] = sum_r A_r (x) B_r at (v, k)
+  float m0[BP][LP], m2[BP][LP];           // raw H K^T and H Vbd_old^T
+  float lm[BP][LP];                       // Lm
+  float aqt[BP][LP], tt[BP][LP], hot[BP][LP], qot[BP][LP];   // Aq^T, T^T, Ho^T, Qo^T
+  float w[BP][LP], z[BP][LP], vv[BP][LP], wq[BP][LP];        // gram gradient factors
+  float wt[BP][LP], zt[BP][LP], vvt[BP][LP], wqt[BP][LP];    // and their transposes
+  float lg[BP], lgp[BP], dec[BP], alpha[BP], cdot[BP];
+  float G[BP], e2[BP], kco[BP], qco[BP], vsc[BP], dc[BP], su[BP];
+  float red[7][4][BP];                    // per-wave partial per-token sums, slots kR*
+  float carry[4];
+};
+constexpr int kRdA = 0, kRgRow = 1, kRgCol = 2, kRhG = 3, kRqG = 4, kRsvb = 5, kRdb = 6;
+
+template <typename CT>
+__device__ __forceinline__ void load8(const CT* p, float* f);
+template <>
+__device__ __forceinline__ void load8<bf16>(const bf16* p, float* f) {
+  const bf16x8 x = *(const bf16x8*)p;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = (float)x[e];
+}
+template <>
+__device__ __forceinline__ void load8<float>(const float* p, float* f) {
+  const f32x4 a = *(const f32x4*)p, b = *(const f32x4*)(p + 4);
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[e] = a[e];
+    f[4 + e] = b[e];
+  }
+}
+__device__ __forceinline__ void store8f(float* p, const float* f) {
+  *(f32x4*)p = (f32x4){f[0], f[1], f[2], f[3]};
+  *(f32x4*)(p + 4) = (f32x4){f[4], f[5], f[6], f[7]};
+}
+
+// lane (g, n): X[4 g + s][col], s = 0..3 -- a fragment over k = rows of a
+// row-major P x D LDS matrix
+template <int LR>
+__device__ __forceinline__ f32x4 col_frag(const float (*X)[LR], int col, int g4) {
+  return (f32x4){X[4 * g4][col], X[4 * g4 + 1][col], X[4 * g4 + 2][col], X[4 * g4 + 3][col]};
+}
+
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+}
+
+template <typename CT, int D>
+__global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
+  typedef G3D<D> Ge;
+  typedef G3BwdSmem<CT, D> Sm;
+  __shared__ Sm sm;
+  static_assert(sizeof(Sm) <= 160 * 1024, "LDS budget");
+  constexpr int P = BP, DG = D / 8, UNITS = P * DG, NDT = D / 16, VPW = NDT / 4, LR = Sm::LR;
+  static_assert(UNITS <= kNT && VPW >= 1, "one load unit per thread, a tile per wave");
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g4 = lane >> 4, n16 = lane & 15;
+  const int H = p.H, M = p.M, T = p.T;
+  const int N = p.B * H * M;
+  const int chain = xcd_remap(blockIdx.x, N);
+  const int b = chain / (H * M), hm = chain % (H * M), h = hm / M, m = hm % M;
+  const bool has_unit = tid < UNITS;
+  const int ui = tid / DG, ud = 8 * (tid % DG);
+  const int L = p.qkv_lanes, gc = p.gate_ch;
+  const size_t qkv_tok = (size_t)H * L * D;
+  const size_t qkv_base = ((size_t)b * T * H + h) * L * D + (L > 1 ? (size_t)m * D : 0);
+  const size_t gate_tok = (size_t)H * M * gc;
+  const size_t gate_base = (((size_t)b * T * H + h) * M + m) * gc;
+  const size_t dec_tok = (size_t)H * M;
+  const size_t dec_base = ((size_t)b * T * H + h) * M + m;
+  const size_t y_tok = (size_t)H * M * D;
+  const size_t y_base = (((size_t)b * T * H + h) * M + m) * D;
+  const int nch = (T + P - 1) / P, per = p.Kc / P, ncomp = T / p.Kc;
+  const G3Stash ts = g3_stash(const_cast<void*>(p.train_states), N, nch, ncomp, D, P, Ge::RMN);
+
+  f32x4 dUc[VPW], dVc[VPW];   // carried: d/dU and d/dVbd of the chunk being processed (its value / key tiles)
+#pragma unroll
+  for (int a = 0; a < VPW; ++a) dUc[a] = dVc[a] = zero4();
+  float dgacc = 0.f;          // d/dGacc of the chunk after the current one
+
+  for (int c = nch - 1; c >= 0; --c) {
+    const int iv = c / per;
+    const bool live = iv > 0;
+    if ((c + 1) % per == 0 && (long long)(c + 1) * P <= T) dgacc = 0.f;  // compaction after this chunk
+    const float gacc = ts.gacc[(size_t)chain * nch + c];
+    __syncthreads();  // the previous chunk is done with LDS
+
+    // ---- S_kron^T of this interval (the factors of compaction iv - 1), rebuilt on entry ----
+    if (live && (c == nch - 1 || (c + 1) % per == 0)) {
+      const float* ab = ts.ab + ((size_t)(iv - 1) * N + chain) * Ge::RMN;
+      float* st = &sm.dr[0][0];
+      for (int e = tid; e < Ge::RMN; e += kNT) st[e] = ab[e];
+      __syncthreads();
+      if (tid < Ge::m) {
+        const int ivv = tid / Ge::ak, ik = tid % Ge::ak;
+        float a[Ge::R];
+#pragma unroll
+        for (int r = 0; r < Ge::R; ++r) a[r] = st[r * Ge::m + ivv * Ge::ak + ik];
+        const float* Bf = st + Ge::R * Ge::m;
+#pragma unroll 2
+        for (int jv = 0; jv < Ge::bv; ++jv)
+#pragma unroll
+          for (int jk = 0; jk < Ge::bk; ++jk) {
+            float s = 0.f;
+#pragma unroll
+            for (int r = 0; r < Ge::R; ++r) s += a[r] * Bf[r * Ge::n + jv * Ge::bk + jk];
+            sm.skt[ik * Ge::bk + jk][ivv * Ge::bv + jv] = from_f<CT>(s);
+          }
+      }
+    }
+
+    // ---- A: the chunk's inputs (and the previous chunk's keys / decays) ----
+    const int t = c * P + ui;
+    const bool tv = has_unit && t < T;
+    float vf[8], wf[8];
+    {
+      float kf[8], qf[8], bf[8], dyf[8], kp[8], us[8], uos[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kf[e] = qf[e] = vf[e] = bf[e] = wf[e] = dyf[e] = kp[e] = us[e] = uos[e] = 0.f;
+      float dv = 1.f, dvp = 1.f;
+      if (tv) {
+        load8<CT>((const CT*)p.k + qkv_base + (size_t)t * qkv_tok + ud, kf);
+        load8<CT>((const CT*)p.q + qkv_base + (size_t)t * qkv_tok + ud, qf);
+        load8<CT>((const CT*)p.v + qkv_base + (size_t)t * qkv_tok + ud, vf);
+        load8<CT>((const CT*)p.dy + y_base + (size_t)t * y_tok + ud, dyf);
+        if (gc > 1) {
+          load8<float>(p.bg + gate_base + (size_t)t * gate_tok + ud, bf);
+          load8<float>(p.wg + gate_base + (size_t)t * gate_tok + ud, wf);
+        } else {
+          const float bs = p.bg[gate_base + (size_t)t * gate_tok], ws = p.wg[gate_base + (size_t)t * gate_tok];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            bf[e] = bs;
+            wf[e] = ws;
+          }
+        }
+        dv = p.dec[dec_base + (size_t)t * dec_tok];
+        load8<float>(ts.u + ((size_t)chain * nch + c) * P * D + (size_t)ui * D + ud, us);
+      }
+      if (has_unit && c > 0) {
+        const int tp = t - P;
+        load8<CT>((const CT*)p.k + qkv_base + (size_t)tp * qkv_tok + ud, kp);
+        dvp = p.dec[dec_base + (size_t)tp * dec_tok];
+        load8<float>(ts.u + ((size_t)chain * nch + c - 1) * P * D + (size_t)ui * D + ud, uos);
+      }
+      float hf[8], part = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        hf[e] = bf[e] * kf[e];
+        part += kf[e] * hf[e];
+      }
+      if (has_unit) {
+        store8f(&sm.h[ui][ud], hf);
+        store8f(&sm.q[ui][ud], qf);
+        store8f(&sm.k[ui][ud], kf);
+        store8f(&sm.vb[ui][ud], kp);
+        store8f(&sm.dy[ui][ud], dyf);
+        store8f(&sm.u[ui][ud], us);
+        store8f(&sm.uo[ui][ud], uos);
+      }
+#pragma unroll
+      for (int off = 1; off < DG; off <<= 1) part += __shfl_xor(part, off, 64);
+      if (has_unit && tid % DG == 0) {
+        sm.cdot[ui] = part;
+        sm.alpha[ui] = stable_alpha_f(part);
+        sm.lg[ui] = tv ? log_decay(dv) : 0.f;
+        sm.dec[ui] = dv;
+        sm.lgp[ui] = c > 0 ? log_decay(dvp) : 0.f;
+      }
+    }
+    __syncthreads();
+
+    // ---- B: per-token scalars (every wave scans for itself) and the four grams ----
+    float gl = lane < P ? sm.lg[lane] : 0.f, glp = lane < P ? sm.lgp[lane] : 0.f;
+#pragma unroll
+    for (int off = 1; off < P; off <<= 1) {
+      const float o = __shfl_up(gl, off, 64), op = __shfl_up(glp, off, 64);
+      if (lane >= off) {
+        gl += o;
+        glp += op;
+      }
+    }
+    const float gl_last = __shfl(gl, P - 1, 64), glp_last = __shfl(glp, P - 1, 64);
+    const float vscp = expf(glp_last - glp);   // lane p: previous chunk's key p decayed to its end
+    if (wave == 0 && lane < P) {
+      const float e2 = expf(2.f * (gacc + gl));
+      sm.G[lane] = gl;
+      sm.e2[lane] = e2;
+      sm.kco[lane] = sm.alpha[lane] * e2;
+      sm.qco[lane] = e2;
+      sm.vsc[lane] = expf(gl_last - gl);
+    }
+    {
+      const float* ar = (wave & 1) ? &sm.q[0][0] : &sm.h[0][0];
+      const float* br = (wave < 2) ? &sm.k[0][0] : &sm.vb[0][0];
+      const f32x4 acc = tile_nt<float, D>(ar + n16 * LR, br + n16 * LR, g4);
+      const int j = n16;
+      const float Gj = __shfl(gl, j, 64), vj = __shfl(vscp, j, 64);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        const float Gi = __shfl(gl, i, 64);
+        const float al = sm.alpha[i], ga = expf(Gi);
+        if (wave == 0) {
+          sm.m0[i][j] = acc[s];
+          sm.lm[i][j] = (j < i) ? al * expf(Gi - Gj) * acc[s] : 0.f;
+        } else if (wave == 1) {
+          sm.aqt[j][i] = (j <= i) ? expf(Gi - Gj) * acc[s] : 0.f;
+        } else if (wave == 2) {
+          const float m2 = vj * acc[s];
+          sm.m2[i][j] = m2;
+          sm.hot[j][i] = (j >= i) ? al * ga * m2 : 0.f;
+        } else {
+          sm.qot[j][i] = (j >= i) ? ga * vj * acc[s] : 0.f;
+        }
+      }
+    }
+    __syncthreads();
+
+    // ---- C: T = (I + Lm)^-1 (wave 0); the previous chunk's keys decayed to its end ----
+    if (wave == 0) {
+      // Lm is strictly lower: (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8)
+      f32x4 xa, ta;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        xa[s] = sm.lm[i][n16];
+        ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
+      }
+      const float* src = &sm.lm[0][0];
+#pragma unroll
+      for (int step = 0; step < 3; ++step) {
+        float* dst = (step & 1) ? &sm.w[0][0] : &sm.z[0][0];
+        f32x4 sq = zero4();
+        mma(sq, *(const f32x4*)&src[n16 * Sm::LP + 4 * g4], xa);
+        xa = sq;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) dst[(4 * g4 + s) * Sm::LP + n16] = sq[s];
+        wave_lds_sync();
+        mma(ta, *(const f32x4*)&dst[n16 * Sm::LP + 4 * g4], ta);
+        src = dst;
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sm.tt[n16][4 * g4 + s] = ta[s];   // T^T
+    }
+    {
+      const float f = __shfl(vscp, ui & 63, 64);
+      if (has_unit)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sm.vb[ui][ud + e] *= f;
+    }
+    __syncthreads();
+
+    // ---- D: dU_tot = dU + Aq^T dY, dRhs = T^T dU_tot, the previous chunk's dU ----
+#pragma unroll
+    for (int a = 0; a < VPW; ++a) {
+      const int col = 16 * (wave * VPW + a) + n16;
+      const f32x4 dYf = col_frag<LR>(sm.dy, col, g4);
+      f32x4 dut = dUc[a];
+      mma(dut, ld_frag(&sm.aqt[n16][0], g4), dYf);
+      f32x4 drh = zero4();
+      mma(drh, ld_frag(&sm.tt[n16][0], g4), dut);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sm.dr[4 * g4 + s][col] = drh[s];
+      f32x4 nd = zero4();
+      mma(nd, ld_frag(&sm.qot[n16][0], g4), dYf);
+      mma(nd, ld_frag(&sm.hot[n16][0], g4), -drh);
+      dUc[a] = nd;
+    }
+    __syncthreads();
+
+    // ---- E: gradients of the P x P coefficients, the Kronecker products,
+    // the value / write-gate gradients ----
+    {
+      const float* ar = (wave == 0 || wave == 2) ? &sm.dr[0][0] : &sm.dy[0][0];
+      const float* br = (wave < 2) ? &sm.u[0][0] : &sm.uo[0][0];
+      f32x4 acc = tile_nt<float, D>(ar + n16 * LR, br + n16 * LR, g4);
+      if (wave == 0 || wave == 2) acc = -acc;
+      const int j = n16;
+      const float Gj = sm.G[j];
+      float cg = 0.f;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        const float Gi = sm.G[i], al = sm.alpha[i], ga = expf(Gi);
+        float rda = 0.f, rg = 0.f;
+        if (wave == 0) {        // dLm (j < i)
+          const float x = (j < i) ? acc[s] : 0.f, e = expf(Gi - Gj), m0 = sm.m0[i][j];
+          const float wv = x * al * e;
+          sm.w[i][j] = wv;
+          sm.wt[j][i] = wv;
+          rda = x * e * m0;
+          rg = x * al * e * m0;
+          cg += rg;
+        } else if (wave == 1) { // dAq (j <= i)
+          const float x = (j <= i) ? acc[s] : 0.f, e = expf(Gi - Gj);
+          const float zv = x * e;
+          sm.z[i][j] = zv;
+          sm.zt[j][i] = zv;
+          rg = x * sm.aqt[j][i];
+          cg += rg;
+        } else if (wave == 2) { // dHo (p = j >= i)
+          const float x = (j >= i) ? acc[s] : 0.f;
+          const float vv = x * al * ga;
+          sm.vv[i][j] = vv;
+          sm.vvt[j][i] = vv;
+          rda = x * ga * sm.m2[i][j];
+          rg = x * sm.hot[j][i];
+        } else {                // dQo (p = j >= i)
+          const float x = (j >= i) ? acc[s] : 0.f;
+          const float wq = x * ga;
+          sm.wq[i][j] = wq;
+          sm.wqt[j][i] = wq;
+          rg = x * sm.qot[j][i];
+        }
+        rda = row_prefix16(rda);
+        rg = row_prefix16(rg);
+        if (n16 == 15) {
+          sm.red[kRdA][wave][i] = rda;
+          sm.red[kRgRow][wave][i] = rg;
+        }
+      }
+      cg += __shfl_xor(cg, 16, 64);
+      cg += __shfl_xor(cg, 32, 64);
+      if (g4 == 0) sm.red[kRgCol][wave][j] = cg;   // zero for waves 2, 3
+    }
+    // Kronecker products G_h = dRhs S_kron, G_q = dY S_kron on this wave's key tiles,
+    // and per-token partials h . G_h, q . G_q, dVbd . Vbd
+    f32x4 Gh[VPW], Gq[VPW];
+#pragma unroll
+    for (int a = 0; a < VPW; ++a) {
+      const int kt = wave * VPW + a, d = 16 * kt + n16;
+      Gh[a] = Gq[a] = zero4();
+      if (live) {
+#pragma unroll 4
+        for (int kb = 0; kb < D / 16; ++kb) {
+          const f32x4 sf = load4(&sm.skt[d][kb * 16 + 4 * g4]);
+          mma(Gh[a], ld_frag(&sm.dr[n16][kb * 16], g4), sf);
+          mma(Gq[a], ld_frag(&sm.dy[n16][kb * 16], g4), sf);
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int i = 4 * g4 + s;
+      float xh = 0.f, xq = 0.f, xv = 0.f;
+#pragma unroll
+      for (int a = 0; a < VPW; ++a) {
+        const int d = 16 * (wave * VPW + a) + n16;
+        xh += sm.h[i][d] * Gh[a][s];
+        xq += sm.q[i][d] * Gq[a][s];
+        xv += dVc[a][s] * sm.k[i][d];
+      }
+      xh = row_prefix16(xh);
+      xq = row_prefix16(xq);
+      xv = row_prefix16(xv);
+      if (n16 == 15) {
+        sm.red[kRhG][wave][i] = xh;
+        sm.red[kRqG][wave][i] = xq;
+        sm.red[kRsvb][wave][i] = xv;   // times vsc_i below
+      }
+    }
+    // u = w o v: dv = w alpha dRhs, dw = v alpha dRhs, and sum_v w v dRhs per token
+    {
+      float dr8[8], dvo[8], dwo[8], ut = 0.f, dws = 0.f;
+      const float al = has_unit ? sm.alpha[ui] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dr8[e] = has_unit ? sm.dr[ui][ud + e] : 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float du = al * dr8[e];
+        dvo[e] = wf[e] * du;
+        dwo[e] = vf[e] * du;
+        dws += dwo[e];
+        ut += wf[e] * vf[e] * dr8[e];
+      }
+#pragma unroll
+      for (int off = 1; off < DG; off <<= 1) {
+        ut += __shfl_xor(ut, off, 64);
+        dws += __shfl_xor(dws, off, 64);
+      }
+      if (tv) {
+        store8f(p.dv + y_base + (size_t)t * y_tok + ud, dvo);
+        if (gc > 1) store8f(p.dwg + gate_base + (size_t)t * gate_tok + ud, dwo);
+        else if (tid % DG == 0) p.dwg[gate_base + (size_t)t * gate_tok] = dws;
+      }
+      if (has_unit && tid % DG == 0) sm.su[ui] = ut;
+    }
+    __syncthreads();
+
+    // ---- F: per-token scalar gradients (wave 0, lane = token) ----
+    if (wave == 0) {
+      float dG = 0.f, dE = 0.f, svb = 0.f;
+      if (lane < P) {
+        const int i = lane;
+        float da = sm.su[i], dkco = 0.f, dqco = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) {
+          da += sm.red[kRdA][w][i];
+          dG += sm.red[kRgRow][w][i] - sm.red[kRgCol][w][i];
+          svb += sm.red[kRsvb][w][i];
+          if (live) {
+            dkco -= sm.red[kRhG][w][i];
+            dqco += sm.red[kRqG][w][i];
+          }
+        }
+        svb *= sm.vsc[i];
+        const float e2 = sm.e2[i], al = sm.alpha[i];
+        da += dkco * e2;
+        dE = 2.f * e2 * (dkco * al + dqco);
+        dG += dE - svb;
+        sm.dc[i] = da * stable_dalpha_f(sm.cdot[i]);
+      }
+      float svt = svb, det = dE;
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        svt += __shfl_xor(svt, off, 64);
+        det += __shfl_xor(det, off, 64);
+      }
+      if (lane == P - 1) dG += svt + dgacc;   // G_last: the decayed keys and the next chunk's Gacc
+      float sfx = lane < P ? dG : 0.f;       // d log-decay_s = sum_{i >= s} dG_i
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        const float o = __shfl_down(sfx, off, 64);
+        if (lane + off < 64) sfx += o;
+      }
+      const int tt_ = c * P + lane;
+      if (lane < P && tt_ < T) p.ddec[dec_base + (size_t)tt_ * dec_tok] = sfx * dlog_decay(sm.dec[lane]);
+      if (lane == 0) sm.carry[0] = det + dgacc;
+    }
+    __syncthreads();
+    dgacc = sm.carry[0];
+
+    // ---- G: dH, dQ, dK on this wave's key tiles; the previous chunk's dVbd ----
+    float dbs[4] = {0.f, 0.f, 0.f, 0.f};   // per-token partial k . dh (scalar erase gates)
+#pragma unroll
+    for (int a = 0; a < VPW; ++a) {
+      const int d = 16 * (wave * VPW + a) + n16;
+      const f32x4 Kc = col_frag<LR>(sm.k, d, g4), Hc = col_frag<LR>(sm.h, d, g4);
+      const f32x4 Qc = col_frag<LR>(sm.q, d, g4), Vc = col_frag<LR>(sm.vb, d, g4);
+      f32x4 dH = zero4(), dQ = zero4(), dK = zero4(), dVo = zero4();
+      mma(dH, ld_frag(&sm.w[n16][0], g4), Kc);
+      mma(dH, ld_frag(&sm.vv[n16][0], g4), Vc);
+      mma(dQ, ld_frag(&sm.z[n16][0], g4), Kc);
+      mma(dQ, ld_frag(&sm.wq[n16][0], g4), Vc);
+      mma(dK, ld_frag(&sm.wt[n16][0], g4), Hc);
+      mma(dK, ld_frag(&sm.zt[n16][0], g4), Qc);
+      mma(dVo, ld_frag(&sm.vvt[n16][0], g4), Hc);
+      mma(dVo, ld_frag(&sm.wqt[n16][0], g4), Qc);
+      float dbp[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s, tt_ = c * P + i;
+        const bool ok = tt_ < T;
+        const float dci = sm.dc[i];
+        float dh = dH[s] + dci * Kc[s];
+        if (live) dh -= sm.kco[i] * Gh[a][s];
+        const float dq = dQ[s] + (live ? sm.qco[i] * Gq[a][s] : 0.f);
+        float bgv = 0.f;
+        if (ok) bgv = gc > 1 ? p.bg[gate_base + (size_t)tt_ * gate_tok + d] : p.bg[gate_base + (size_t)tt_ * gate_tok];
+        const float dk = dK[s] + dci * Hc[s] + dVc[a][s] * sm.vsc[i] + bgv * dh;
+        dbp[s] = Kc[s] * dh;
+        dbs[s] += dbp[s];
+        if (ok) {
+          const size_t o = y_base + (size_t)tt_ * y_tok + d;
+          p.dq[o] = dq;
+          p.dk[o] = dk;
+          if (gc > 1) p.dbg[gate_base + (size_t)tt_ * gate_tok + d] = dbp[s];
+        }
+      }
+      dVc[a] = dVo;
+    }
+    if (gc == 1) {
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const float x = row_prefix16(dbs[s]);
+        if (n16 == 15) sm.red[kRdb][wave][4 * g4 + s] = x;
+      }
+      __syncthreads();
+      if (tid < P && c * P + tid < T) {
+        float s = 0.f;
+#pragma unroll
+        for (int w = 0; w < 4; ++w) s += sm.red[kRdb][w][tid];
+        p.dbg[gate_base + (size_t)(c * P + tid) * gate_tok] = s;
+      }
+    }
+  }
+}
+
+template <typename CT, int D>
+int launch_bwd(const G3BwdArgs& a, hipStream_t stream) {
+  const int N = a.B * a.H * a.M;
+  hipLaunchKernelGGL((gdn3_bwd_kernel<CT, D>), dim3(N), dim3(kNT), 0, stream, a);
+  return check_launch("gdn3_bwd_kernel");
+}
+
+}  // namespace
+
+int gdn3_bwd_dispatch(const G3BwdArgs& a, hipStream_t stream) {
+  if (a.P != BP) return set_error(GDNX_ERR_SHAPE, "gdn3 backward: window P=%d unsupported (16)", a.P);
+  if (a.dtype == GDNX_DTYPE_BF16) {
+    if (a.D == 128) return launch_bwd<bf16, 128>(a, stream);
+    if (a.D == 64) return launch_bwd<bf16, 64>(a, stream);
+  } else {
+    if (a.D == 128) return launch_bwd<float, 128>(a, stream);
+    if (a.D == 64) return launch_bwd<float, 64>(a, stream);
+  }
+  return set_error(GDNX_ERR_SHAPE, "gdn3 backward: unsupported head_dim %d", a.D);
+}
+
+}  // namespace gdnx

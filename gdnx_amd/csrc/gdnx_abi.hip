@@ -253,11 +253,20 @@ extern "C" int gdnx_gdn3_num_compactions(int T, int P, int compact_every) {
   return T / compact_every;
 }
 
+extern "C" long long gdnx_gdn3_train_states_bytes(int B, int T, int H, int M, int head_dim, int P,
+                                                  int compact_every) {
+  if (B < 1 || T < 0 || H < 1 || M < 1 || !g3_window_ok(head_dim, P) || compact_every < P ||
+      compact_every % P != 0)
+    return -1;
+  return (long long)gdn3_train_states_bytes(B * H * M, T, head_dim, P, compact_every);
+}
+
 extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, int qkv_lanes,
                                    const float* b_gates, const float* w_gates, int gate_channels,
                                    const float* decay, const float* sketch, void* y, float* A_out,
                                    float* B_out, float* U_out, float* Vb_out, double* comp_stats,
-                                   void* workspace, int B, int T, int H, int M, int head_dim, int R, int P,
+                                   void* workspace, void* train_states, int B, int T, int H, int M,
+                                   int head_dim, int R, int P,
                                    int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
                                    int dtype, void* stream) {
   g_err[0] = 0;
@@ -279,7 +288,8 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
     return set_error(GDNX_ERR_ARG, "gates, decay, sketch, y and workspace must be non-null");
   if (gate_channels > 1 && (!aligned16(b_gates) || !aligned16(w_gates)))
     return set_error(GDNX_ERR_ARG, "per-channel gates must be 16-byte aligned");
-  if (!aligned16(workspace)) return set_error(GDNX_ERR_ARG, "workspace must be 16-byte aligned");
+  if (!aligned16(workspace) || (train_states && !aligned16(train_states)))
+    return set_error(GDNX_ERR_ARG, "workspace and train_states must be 16-byte aligned");
   if (!(slow_decay >= 0.f && slow_decay <= 1.f))
     return set_error(GDNX_ERR_ARG, "slow_decay must lie in [0, 1]");
   if ((A_out || B_out || U_out || Vb_out) && T % P != 0)
@@ -300,6 +310,7 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
   a.Vb_out = Vb_out;
   a.stats = comp_stats;
   a.workspace = workspace;
+  a.train_states = train_states;
   a.ge = ge;
   a.B = B;
   a.T = T;
@@ -313,6 +324,38 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
   a.dtype = dtype;
   a.sdec = slow_decay;
   return gdn3_fwd_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_gdn3_chunk_bwd(const void* q, const void* k, const void* v, int qkv_lanes,
+                                   const float* b_gates, const float* w_gates, int gate_channels,
+                                   const float* decay, const void* dy, const void* train_states, float* dq,
+                                   float* dk, float* dv, float* db_gates, float* dw_gates, float* ddecay, int B,
+                                   int T, int H, int M, int head_dim, int R, int P, int compact_every, int a_v,
+                                   int a_k, int b_v, int b_k, int dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
+  if (rc) return rc;
+  G3Geom ge;
+  if ((rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge))) return rc;
+  if ((rc = g3_layer_geom(head_dim, ge))) return rc;
+  if (P != 16) return set_error(GDNX_ERR_SHAPE, "gdn3 backward: residual window P=%d unsupported (16)", P);
+  if (compact_every < P || compact_every % P != 0)
+    return set_error(GDNX_ERR_SHAPE, "compact_every=%d must be a positive multiple of P=%d", compact_every, P);
+  if (qkv_lanes != 1 && qkv_lanes != M)
+    return set_error(GDNX_ERR_SHAPE, "qkv_lanes=%d must be 1 (shared) or M=%d", qkv_lanes, M);
+  if (gate_channels != 1 && gate_channels != head_dim)
+    return set_error(GDNX_ERR_SHAPE, "gate_channels=%d must be 1 or head_dim=%d", gate_channels, head_dim);
+  if (!b_gates || !w_gates || !decay || !dy || !dq || !dk || !dv || !db_gates || !dw_gates || !ddecay)
+    return set_error(GDNX_ERR_ARG, "gates, decay, dy and the gradient outputs must be non-null");
+  if (!train_states) return set_error(GDNX_ERR_WORKSPACE, "train_states (from the forward) is required");
+  if (!aligned16(dy) || !aligned16(train_states) || !aligned16(dq) || !aligned16(dk) || !aligned16(dv) ||
+      (gate_channels > 1 && (!aligned16(b_gates) || !aligned16(w_gates) || !aligned16(dw_gates))))
+    return set_error(GDNX_ERR_ARG, "dy, train_states, the key-sized outputs and per-channel gates must be "
+                     "16-byte aligned");
+  if (T == 0) return GDNX_OK;
+  G3BwdArgs a{q, k, v, b_gates, w_gates, decay, dy, train_states, dq, dk, dv, db_gates, dw_gates, ddecay,
+              B, T, H, M, head_dim, P, compact_every, qkv_lanes, gate_channels, dtype};
+  return gdn3_bwd_dispatch(a, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_gdn3_compact(const float* A, const float* Bf, const float* U, const float* Vb,

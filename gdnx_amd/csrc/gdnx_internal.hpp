@@ -133,9 +133,13 @@ struct G3FwdArgs {
   float* Vb_out;       // [N,D,P] or null
   double* stats;       // [T/Kc, N, 2] (energy, kept) or null
   void* workspace;     // carved by the dispatcher into the fields below
+  void* train_states;  // training stash for the backward (layout G3Stash) or null
   G3Geom ge;
   int B, T, H, M, D, P, Kc, qkv_lanes, gate_ch, dtype;
   float sdec;
+  float* ts_u;         // (set by the dispatcher from train_states)
+  float* ts_g;
+  int nch;
   // per launch (set by the dispatcher)
   void* skron;         // [N, D, D] compute dtype: sum_r A_r (x) B_r
   float* ab;           // [N, R (m + n)]: A | B as of the last compaction
@@ -163,6 +167,26 @@ struct G3CompactArgs {
   int skron_dtype;
   float* A_fin;        // optional second copy of the result, or null
   float* B_fin;
+  float* ab_stash;     // [N][R (m + n)] copy of the result (A | B) for the backward, or null
+};
+
+// Backward of the Kronecker-residual regime (gdn3_bwd.hip)
+struct G3BwdArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  const float* bg;
+  const float* wg;
+  const float* dec;
+  const void* dy;             // [B,T,H,M,D] compute dtype
+  const void* train_states;   // the forward's stash (layout G3Stash)
+  float* dq;                  // [B,T,H,M,D] per lane
+  float* dk;
+  float* dv;
+  float* dbg;                 // gate layout ([.., D] or [..])
+  float* dwg;
+  float* ddec;                // [B,T,H,M]
+  int B, T, H, M, D, P, Kc, qkv_lanes, gate_ch, dtype;
 };
 
 struct KronReadArgs {
@@ -178,6 +202,8 @@ struct KronReadArgs {
 
 int gdn3_fwd_dispatch(const G3FwdArgs& a, hipStream_t stream);
 size_t gdn3_workspace_bytes(int N, int D, int P, int dtype);
+size_t gdn3_train_states_bytes(int N, int T, int D, int P, int Kc);
+int gdn3_bwd_dispatch(const G3BwdArgs& a, hipStream_t stream);
 int gdn3_compact_dispatch(const G3CompactArgs& a, hipStream_t stream);
 int kron_read_dispatch(const KronReadArgs& a, hipStream_t stream);
 int decode_dispatch(const DecodeArgs& a, hipStream_t stream);

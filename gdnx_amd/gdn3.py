@@ -16,8 +16,10 @@ backwards are HIP kernels of libgdnx.
 
 ``gdn3_recurrent_state`` is the same method in its general regime: a
 P-slot residual window and periodic rearrangement-SVD compaction of the
-Kronecker factors (forward only; the compaction is outside autograd in the
-reference too, gdn3/gdn3_upgrade.py:513-517).
+Kronecker factors, differentiable with the frozen oracle's gradient
+semantics (the factors a compaction leaves carry no gradient: it runs under
+no_grad, gdn3/_reference_recurrence.py:86-88; the residual slots keep
+theirs), through the gdnx_gdn3_chunk_bwd kernel.
 """
 from __future__ import annotations
 
@@ -104,10 +106,35 @@ def _scalar_gate(g):
     return g.dim() == 5 and g.stride(-1) == 0
 
 
+class _GDN3Chunk(torch.autograd.Function):
+    """gdnx_gdn3_chunk_fwd / _bwd on normalised inputs: q, k, v [B,T,H,D]
+    (shared) or [B,T,H,M,D] in the compute dtype, gates [B,T,H,M] or
+    [B,T,H,M,D] float32, decay [B,T,H,M] float32."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, bg, wg, dec, sketch, cfg):
+        M, R, P, factors, slow_decay, Kc = cfg
+        y, _, _, tst = ops.gdn3_chunk_fwd(q, k, v, bg, wg, dec, sketch, M=M, R=R, P=P, factors=factors,
+                                          slow_decay=slow_decay, compact_every=Kc, save_states=True)
+        ctx.save_for_backward(q, k, v, bg, wg, dec, tst)
+        ctx.cfg = cfg
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        q, k, v, bg, wg, dec, tst = ctx.saved_tensors
+        M, R, P, factors, _, Kc = ctx.cfg
+        dq, dk, dv, db, dw, ddec = ops.gdn3_chunk_bwd(q, k, v, bg, wg, dec, dy, tst, M=M, R=R, P=P,
+                                                      factors=factors, compact_every=Kc)
+        if q.dim() == 4:   # q, k, v shared by the lanes
+            dq, dk, dv = dq.sum(3), dk.sum(3), dv.sum(3)
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), db, dw, ddec, None, None
+
+
 def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
                          factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None,
                          sketch=None, return_state=False):
-    """GDN3LinearAttn._gdn3_recurrent_state on the GPU (forward).
+    """GDN3LinearAttn._gdn3_recurrent_state on the GPU.
 
     Reference: gdn3/gdn3_upgrade.py:403-531 with the semantics of its frozen
     oracle gdn3/_reference_recurrence.py:33-94 (the chunked reference departs
@@ -122,7 +149,8 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     P (the reference layer compacts every P tokens).  Returns y
     [B,T,H,M,V] in the compute dtype, plus ((A, B, U, Vb), comp_err) when
     return_state (comp_err is the reference's summed discarded energy, a
-    device tensor).
+    device tensor).  When an input requires grad (and return_state is not
+    set) y is differentiable in q, k, v, the gates and the decay (P = 16).
     """
     B, T, H, M = decay_factors.shape
     cdt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
@@ -144,12 +172,16 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     else:
         bg = chan5(b_gates).float().expand(B, T, H, M, D).contiguous()
         wg = chan5(w_gates).float().expand(B, T, H, M, D).contiguous()
+    dec = decay_factors.float().contiguous()
     a_v, a_k, b_v, b_k = factors
     N = B * H * M
     qw = ops.sketch_width(R, a_v * a_k, b_v * b_k)
     G = default_sketch(N, b_v * b_k, qw, q.device) if sketch is None else sketch.float().contiguous()
-    y, stats, state = ops.gdn3_chunk_fwd(q4, k4, v4, bg, wg, decay_factors.float().contiguous(), G, M=M,
-                                         R=R, P=P, factors=factors, slow_decay=slow_decay,
+    train = torch.is_grad_enabled() and any(t.requires_grad for t in (q4, k4, v4, bg, wg, dec))
+    if train and not return_state:
+        return _GDN3Chunk.apply(q4, k4, v4, bg, wg, dec, G, (M, R, P, factors, slow_decay, compact_every))
+    y, stats, state = ops.gdn3_chunk_fwd(q4.detach(), k4.detach(), v4.detach(), bg.detach(), wg.detach(),
+                                         dec.detach(), G, M=M, R=R, P=P, factors=factors, slow_decay=slow_decay,
                                          compact_every=compact_every, return_state=return_state)
     if not return_state:
         return y
@@ -157,19 +189,13 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     return y, state, err
 
 
-class GDN3RecurrentState(torch.autograd.Function):
-    """Autograd wrapper of gdn3_recurrent_state.  The Kronecker-residual
-    regime has no HIP backward yet: backward raises instead of returning
-    wrong gradients.  The dense regime (P >= T, scalar gates, shared q/k/v)
-    is differentiable through gdn3_scan."""
+class GDN3RecurrentState:
+    """Autograd entry with the argument order of the reference method
+    (q, k, v, b_gates, w_gates, decay_factors): ``GDN3RecurrentState.apply``
+    returns y, differentiable through the gdnx_gdn3_chunk_bwd kernel."""
 
     @staticmethod
-    def forward(ctx, q, k, v, b_gates, w_gates, decay_factors, R=4, P=16, factors=(16, 16, 8, 8),
-                slow_decay=0.97, compact_every=None):
+    def apply(q, k, v, b_gates, w_gates, decay_factors, R=4, P=16, factors=(16, 16, 8, 8),
+              slow_decay=0.97, compact_every=None):
         return gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, R=R, P=P, factors=factors,
                                     slow_decay=slow_decay, compact_every=compact_every)
-
-    @staticmethod
-    def backward(ctx, dy):
-        raise NotImplementedError("the GDN3 Kronecker-residual backward is not implemented in gdnx_amd; "
-                                  "train in the dense regime (P >= T) through gdn3_scan")

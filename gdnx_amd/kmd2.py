@@ -45,11 +45,16 @@ def _mixed_query(q, out_mix):
     return (q.float() * w).sum(3).to(q.dtype)
 
 
-def _is_channel_constant(g):
-    """True when g [B,T,H,dk] carries one decay per token (stride 0 over dk,
-    or equal values across dk)."""
+def _scalar_decay(g):
+    """True when g [B,T,H,dk] carries one decay per token, so the scalar-decay
+    kernels give the same values and gradients: g broadcast over dk (stride
+    0), or a no-grad g whose channels are equal.  A full g that requires grad
+    takes the per-channel path without looking at its values (no host sync):
+    its channels get gradients of their own."""
     if g.shape[-1] == 1 or g.stride(-1) == 0:
         return True
+    if g.requires_grad:
+        return False
     return bool((g.amax(-1) == g.amin(-1)).all())
 
 
@@ -69,7 +74,7 @@ def _scan(q, k, v, g, beta_e, beta_w, out_mix, want_scores):
     B, T, H, r_out, dk = q.shape
     dv = v.shape[-1]
     D = _kernel_dim(dk, dv)
-    scalar = _is_channel_constant(g) and not (g.requires_grad and g.shape[-1] > 1 and g.stride(-1) != 0)
+    scalar = _scalar_decay(g)
     qe = _mixed_query(q if scalar else q.float(), out_mix)
     qe, kp, vp = _pad_last(qe, D), _pad_last(k, D), _pad_last(v, D)
     if scalar:

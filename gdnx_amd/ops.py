@@ -403,14 +403,16 @@ def gdn3_compact(A, Bk, U, Vb, sketch, slow_decay=0.97):
 
 
 def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
-                   factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None, return_state=False):
+                   factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None, return_state=False,
+                   save_states=False):
     """GDN3 recurrence with residual window and compaction (gdnx_gdn3_chunk_fwd).
 
     q, k, v: [B,T,H,D] (shared by the M lanes) or [B,T,H,M,D] (per lane),
     bf16 or float32, contiguous.  b_gates, w_gates: [B,T,H,M] (scalar per
     lane) or [B,T,H,M,D] float32.  decay [B,T,H,M] float32.  sketch
     [B*H*M, b_v*b_k, q] float32.  Returns (y [B,T,H,M,D] in q's dtype,
-    stats [T // K_c, N, 2] float64, state (A, B, U, Vb) or None)."""
+    stats [T // K_c, N, 2] float64, state (A, B, U, Vb) or None), and with
+    save_states a fourth item: the training stash gdn3_chunk_bwd reads."""
     lib = _lib.load()
     a_v, a_k, b_v, b_k = factors
     B, T, H = q.shape[:3]
@@ -444,10 +446,45 @@ def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
         state = (torch.empty(N, R, a_v, a_k, device=q.device), torch.empty(N, R, b_v, b_k, device=q.device),
                  torch.empty(N, D, P, device=q.device), torch.empty(N, D, P, device=q.device))
         ptrs = [_lib.ptr(t) for t in state]
+    tst = None
+    if save_states:
+        nts = lib.gdnx_gdn3_train_states_bytes(B, T, H, M, D, P, Kc)
+        _need(nts > 0, f"unsupported GDN3 shape for training: head_dim {D}, P {P}")
+        tst = torch.empty(nts, dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
         rc = lib.gdnx_gdn3_chunk_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), lanes, _lib.ptr(b_gates),
                                      _lib.ptr(w_gates), gate_ch, _lib.ptr(decay), _lib.ptr(sketch), _lib.ptr(y),
-                                     *ptrs, _lib.ptr(stats) if n_ev > 0 else None, _lib.ptr(ws), B, T, H, M, D,
-                                     R, P, Kc, a_v, a_k, b_v, b_k, float(slow_decay), dt, _lib.stream_of(q))
+                                     *ptrs, _lib.ptr(stats) if n_ev > 0 else None, _lib.ptr(ws), _lib.ptr(tst),
+                                     B, T, H, M, D, R, P, Kc, a_v, a_k, b_v, b_k, float(slow_decay), dt,
+                                     _lib.stream_of(q))
     _lib.check(rc, "gdnx_gdn3_chunk_fwd")
+    if save_states:
+        return y, stats[:n_ev], state, tst
     return y, stats[:n_ev], state
+
+
+def gdn3_chunk_bwd(q, k, v, b_gates, w_gates, decay, dy, train_states, *, M, R=4, P=16,
+                   factors=(16, 16, 8, 8), compact_every=None):
+    """Backward of gdn3_chunk_fwd (gdnx_gdn3_chunk_bwd) from the stash its
+    save_states call returned.  Returns float32 (dq, dk, dv [B,T,H,M,D] per
+    lane, db_gates, dw_gates in the gates' layout, ddecay [B,T,H,M])."""
+    lib = _lib.load()
+    a_v, a_k, b_v, b_k = factors
+    B, T, H = q.shape[:3]
+    D = q.shape[-1]
+    lanes = 1 if q.dim() == 4 else q.shape[3]
+    gate_ch = 1 if b_gates.dim() == 4 else b_gates.shape[-1]
+    Kc = P if compact_every is None else int(compact_every)
+    dy = dy.to(q.dtype).contiguous()
+    _need(tuple(dy.shape) == (B, T, H, M, D), "dy must be [B,T,H,M,D]")
+    dq, dk, dv = (torch.empty(B, T, H, M, D, dtype=torch.float32, device=q.device) for _ in range(3))
+    db, dw = torch.empty_like(b_gates), torch.empty_like(w_gates)
+    ddec = torch.empty_like(decay)
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_gdn3_chunk_bwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), lanes, _lib.ptr(b_gates),
+                                     _lib.ptr(w_gates), gate_ch, _lib.ptr(decay), _lib.ptr(dy),
+                                     _lib.ptr(train_states), _lib.ptr(dq), _lib.ptr(dk), _lib.ptr(dv), _lib.ptr(db),
+                                     _lib.ptr(dw), _lib.ptr(ddec), B, T, H, M, D, R, P, Kc, a_v, a_k, b_v, b_k,
+                                     _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    _lib.check(rc, "gdnx_gdn3_chunk_bwd")
+    return dq, dk, dv, db, dw, ddec

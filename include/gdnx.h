@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 2
+#define GDNX_ABI_VERSION 3
 
 enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1 };
 
@@ -232,15 +232,42 @@ int gdnx_gdn3_num_compactions(int T, int P, int compact_every);
  *                comp_err is sum over compactions of max(0, sum_n energy -
  *                sum_n kept)
  *   workspace    gdnx_gdn3_workspace_bytes bytes
+ *   train_states gdnx_gdn3_train_states_bytes bytes receiving what
+ *                gdnx_gdn3_chunk_bwd reads (net writes and accumulated log
+ *                decay per window, the factors after every compaction), or
+ *                NULL for inference
  * Supported: head_dim 128 with P = 16; head_dim 64 with P = 16 or 32;
  * R <= 4; a_v a_k <= 256, b_v b_k <= 256; compact_every a multiple of P. */
 int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, int qkv_lanes,
                         const float* b_gates, const float* w_gates, int gate_channels,
                         const float* decay, const float* sketch, void* y, float* A_out,
                         float* B_out, float* U_out, float* Vb_out, double* comp_stats,
-                        void* workspace, int B, int T, int H, int M, int head_dim, int R, int P,
-                        int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
-                        int dtype, void* stream);
+                        void* workspace, void* train_states, int B, int T, int H, int M,
+                        int head_dim, int R, int P, int compact_every, int a_v, int a_k, int b_v,
+                        int b_k, float slow_decay, int dtype, void* stream);
+
+/* Bytes of the gdnx_gdn3_chunk_fwd training stash; -1 if invalid. */
+long long gdnx_gdn3_train_states_bytes(int B, int T, int H, int M, int head_dim, int P,
+                                       int compact_every);
+
+/* Backward of gdnx_gdn3_chunk_fwd.  Replaces torch autograd through
+ * GDN3LinearAttn._gdn3_recurrent_state (gdn3/gdn3_upgrade.py:403-531) with
+ * the gradient semantics of its frozen oracle (gdn3/_reference_recurrence.py:
+ * 60-90): the factors A, B a compaction leaves carry no gradient (it runs
+ * under no_grad); the residual slots U, Vb keep theirs across compactions.
+ * Inputs as in the forward, dy [B, T, H, M, D] io dtype, train_states as
+ * filled by the forward with the same arguments.  Outputs, float32:
+ *   dq, dk, dv   [B, T, H, M, D] per lane (for shared q/k/v the caller sums
+ *                over the M lanes)
+ *   db_gates, dw_gates  the gates' layout ([..., gate_channels])
+ *   ddecay       [B, T, H, M] (zero where the decay was clamped)
+ * Supported: P = 16, head_dim 128 or 64, the layer's Kronecker geometry. */
+int gdnx_gdn3_chunk_bwd(const void* q, const void* k, const void* v, int qkv_lanes,
+                        const float* b_gates, const float* w_gates, int gate_channels,
+                        const float* decay, const void* dy, const void* train_states, float* dq,
+                        float* dk, float* dv, float* db_gates, float* dw_gates, float* ddecay, int B,
+                        int T, int H, int M, int head_dim, int R, int P, int compact_every, int a_v,
+                        int a_k, int b_v, int b_k, int dtype, void* stream);
 
 /* Rearrangement-SVD compaction with two-timescale blend, one chain per
  * block.  Replaces GDN3LinearAttn._compact_vec (gdn3/gdn3_upgrade.py:650-719)

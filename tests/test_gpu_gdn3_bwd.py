@@ -1,0 +1,152 @@
+"""Backward of the GDN3 Kronecker-residual regime (gdnx_gdn3_chunk_bwd) on the
+GPU: y and the gradients of q, k, v, both gates and the decay against torch
+autograd through the float64 CPU oracle (oracle.gdn3.gdn3_recurrence, the
+restatement of gdn3/_reference_recurrence.py pinned by the reference's
+golden output and gradient vectors in tests/test_oracle_gdn3.py; its
+compaction runs under no_grad, so the compacted factors carry no gradient
+while the residual slots keep theirs across windows).
+
+Tolerances (rel-L2): 1e-4 for float32 IO, 1e-2 for bf16.  slow_decay 0
+makes the Kronecker part carry the whole compacted state, so its gradient
+terms weigh fully; the state is then entirely the fp32 SVD's output, whose
+singular vectors move by (perturbation of R_mat) / (singular-value gap)
+against the float64 oracle's, so those cases get 5e-4 (y as well as the
+gradients; the forward tests bound the factors themselves at 1e-3).  The
+no-compaction case is also checked against the dense delta-rule backward,
+an independent HIP path, at 1e-4."""
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import gdn3 as og
+from oracle import inputs
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def rel_l2(a, b):
+    a, b = a.double().cpu(), b.double().cpu()
+    return ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+
+
+def _inputs(B, T, H, M, D, seed, io, gate, per_lane):
+    g = torch.Generator().manual_seed(seed)
+    shape_qkv = (B, T, H, M, D) if per_lane else (B, T, H, D)
+    q = F.normalize(torch.randn(*shape_qkv, generator=g), dim=-1)
+    k = F.normalize(torch.randn(*shape_qkv, generator=g), dim=-1)
+    v = torch.randn(*shape_qkv, generator=g)
+    gshape = (B, T, H, M, D) if gate == "channel" else (B, T, H, M)
+    bg = torch.sigmoid(torch.randn(*gshape, generator=g))
+    wg = torch.sigmoid(torch.randn(*gshape, generator=g))
+    taus = torch.tensor(inputs.TAUS[:M] if M <= 4 else [0.05] * M)
+    dec = torch.exp(torch.log1p(-taus).view(1, 1, 1, M) + 0.01 * torch.randn(B, T, H, M, generator=g))
+    dy = torch.randn(B, T, H, M, D, generator=g)
+    return [q.to(io), k.to(io), v.to(io), bg, wg, dec.clamp(max=1.0)], dy
+
+
+def _oracle(xs, dy, M, P, Kc, factors, G, slow_decay=0.97):
+    leaves = [x.double().requires_grad_(True) for x in xs]
+    q, k, v, bg, wg, dec = leaves
+    D = q.shape[-1]
+
+    def lanes(x):
+        return x if x.dim() == 5 else x.unsqueeze(3).expand(*x.shape[:3], M, x.shape[-1])
+
+    def gates(x):
+        return x if x.dim() == 5 else x.unsqueeze(-1).expand(*x.shape, D)
+    y = og.gdn3_recurrence(lanes(q), lanes(k), lanes(v), gates(bg), gates(wg), dec, R=4, P=P, factors=factors,
+                           compact_every=Kc, sketch=G, sign_mode="canonical", slow_decay=slow_decay)
+    grads = torch.autograd.grad(y, leaves, dy.double())
+    return y, grads
+
+
+CASES = [
+    # (B, T, H, M, D, factors, Kc, io, gate, per_lane, slow_decay)
+    (1, 64, 2, 2, 128, (16, 16, 8, 8), 16, torch.float32, "lane", False, 0.97),
+    (1, 64, 1, 2, 128, (16, 16, 8, 8), 32, torch.float32, "channel", True, 0.97),
+    (1, 41, 1, 2, 128, (16, 16, 8, 8), 16, torch.float32, "channel", False, 0.97),
+    (1, 80, 1, 2, 128, (16, 16, 8, 8), 16, torch.float32, "lane", True, 0.0),
+    (1, 64, 2, 1, 64, (8, 8, 8, 8), 16, torch.float32, "lane", False, 0.97),
+    (1, 64, 1, 2, 64, (8, 8, 8, 8), 16, torch.float32, "channel", True, 0.0),
+    (2, 48, 1, 2, 128, (16, 16, 8, 8), 16, torch.bfloat16, "lane", False, 0.97),
+    (1, 64, 1, 2, 64, (8, 8, 8, 8), 32, torch.bfloat16, "channel", True, 0.97),
+]
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"c{i}" for i in range(len(CASES))])
+def test_gdn3_backward_matches_oracle(gpu_lib, case):
+    from gdnx_amd import gdn3
+    B, T, H, M, D, factors, Kc, io, gate, per_lane, sdec = case
+    print(f"case: gdn3 bwd {case}", flush=True)
+    xs, dy = _inputs(B, T, H, M, D, seed=33, io=io, gate=gate, per_lane=per_lane)
+    N = B * H * M
+    a_v, a_k, b_v, b_k = factors
+    G = og.reference_sketch(N, b_v * b_k, min(4 + 4, a_v * a_k, b_v * b_k))
+    leaves = [x.to(DEV).requires_grad_(True) for x in xs]
+    y = gdn3.gdn3_recurrent_state(*leaves, R=4, P=16, factors=factors, compact_every=Kc, sketch=G.to(DEV),
+                                  slow_decay=sdec)
+    grads = torch.autograd.grad(y, leaves, dy.to(io).to(DEV))
+    torch.cuda.synchronize()
+    yr, gref = _oracle(xs, dy.to(io), M, 16, Kc, factors, G, slow_decay=sdec)
+    tol = 1e-2 if io == torch.bfloat16 else (5e-4 if sdec == 0.0 else 1e-4)
+    assert rel_l2(y, yr) <= tol
+    for name, a, r in zip(("dq", "dk", "dv", "db_gates", "dw_gates", "ddecay"), grads, gref):
+        err = rel_l2(a, r)
+        print(f"  {name} rel-L2 {err:.2e}", flush=True)
+        assert a.shape == r.shape and a.dtype == xs[("dq", "dk", "dv", "db_gates", "dw_gates",
+                                                     "ddecay").index(name)].dtype
+        assert err <= tol, name
+
+
+def test_gdn3_backward_without_compaction_equals_dense_rule(gpu_lib):
+    """One window and no compaction (T = P = 16, K_c beyond T): the
+    Kronecker-residual backward equals gdn3_scan's dense delta-rule backward
+    (scalar gates b = w = beta), two independent HIP paths, at 1e-4."""
+    from gdnx_amd import gdn3
+    print("case: gdn3 bwd bridge to dense", flush=True)
+    B, T, H, M, D = 1, 16, 2, 4, 128
+    x = inputs.dense_inputs(B, T, H, D, M=M, seed=3, decay="tau", rope=True)
+    dec = torch.exp(x["g"].clamp(max=0))
+    dy = torch.randn(B, T, H, M, D, generator=torch.Generator().manual_seed(4))
+    leaves = [t.to(DEV).requires_grad_(True) for t in (x["q"], x["k"], x["v"], x["beta"], dec)]
+    q, k, v, beta, dc = leaves
+    y = gdn3.gdn3_recurrent_state(q, k, v, beta, beta, dc, compact_every=10 ** 6 // 16 * 16)
+    g1 = torch.autograd.grad(y, leaves, dy.to(DEV))
+    y2 = gdn3.gdn3_scan(q, k, v, beta, torch.log(dc))
+    g2 = torch.autograd.grad(y2, leaves, dy.to(DEV))
+    torch.cuda.synchronize()
+    assert rel_l2(y, y2) <= 1e-4
+    for name, a, r in zip(("dq", "dk", "dv", "dbeta", "ddecay"), g1, g2):
+        err = rel_l2(a, r)
+        print(f"  {name} rel-L2 {err:.2e}", flush=True)
+        assert err <= 1e-4, name
+
+
+def test_gdn3_backward_layer_call_convention(gpu_lib):
+    """Inputs as GDN3LinearAttn.forward builds them (gdn3/gdn3_upgrade.py:785-837):
+    lane-expanded q/k/v views of [B,T,H,D] leaves, per-channel sigmoid gates,
+    compaction every P; gradients reach the un-expanded leaves."""
+    from gdnx_amd import gdn3
+    print("case: gdn3 bwd layer call convention", flush=True)
+    B, T, H, M, D = 1, 48, 2, 4, 128
+    g = torch.Generator().manual_seed(9)
+    q = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
+    k = F.normalize(torch.randn(B, T, H, D, generator=g), dim=-1)
+    v = torch.randn(B, T, H, D, generator=g)
+    bg = torch.sigmoid(torch.randn(B, T, H, M, D, generator=g))
+    wg = torch.sigmoid(torch.randn(B, T, H, M, D, generator=g))
+    dec = torch.rand(B, T, H, M, generator=g).mul(0.2).add(0.79)
+    dy = torch.randn(B, T, H, M, D, generator=g)
+    leaves = [x.to(DEV).requires_grad_(True) for x in (q, k, v, bg, wg, dec)]
+    qe, ke, ve = (x.unsqueeze(3).expand(B, T, H, M, D) for x in leaves[:3])
+    y = gdn3.GDN3RecurrentState.apply(qe, ke, ve, *leaves[3:])
+    grads = torch.autograd.grad(y, leaves, dy.to(DEV))
+    torch.cuda.synchronize()
+    G = og.reference_sketch(B * H * M, 64, 8)
+    yr, gref = _oracle([q, k, v, bg, wg, dec], dy, M, 16, 16, (16, 16, 8, 8), G)
+    assert rel_l2(y, yr) <= 1e-4
+    for name, a, r in zip(("dq", "dk", "dv", "db_gates", "dw_gates", "ddecay"), grads, gref):
+        err = rel_l2(a, r)
+        print(f"  {name} rel-L2 {err:.2e}", flush=True)
+        assert err <= 1e-4, name
