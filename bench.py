@@ -198,35 +198,41 @@ def bench_decode(args):
     print(json.dumps(line), flush=True)
 
 
-def cpu_baseline_gdn3(T=2048, B=1, H=16, M=4, compact_every=2048):
+def cpu_baseline_gdn3(T=2048, B=1, H=16, M=4, compact_every=2048, train=False):
     """Time the CPU oracle's sequential GDN3 recurrence (fp32, all chains of
-    the layer batched per token) on the first T tokens of the workload."""
+    the layer batched per token) on the first T tokens of the workload, with
+    train its torch-autograd backward too."""
     import torch
     from oracle import gdn3 as og, inputs
     torch.set_num_threads(os.cpu_count() or 1)
     x = inputs.config3(T=T, B=B, H=H, M=M, span=min(4096, T), n_pairs=16)
     D = x["q"].shape[-1]
-    args = [t.float().unsqueeze(3).expand(B, T, H, M, D) for t in (x["q"], x["k"], x["v"])]
-    gates = [t.unsqueeze(-1).expand(B, T, H, M, D) for t in (x["b"], x["w"])]
+    leaves = [x[n].float().requires_grad_(train) for n in ("q", "k", "v", "b", "w", "dec")]
     t0 = time.perf_counter()
-    og.gdn3_recurrence(*args, *gates, x["dec"], compact_every=compact_every, dtype=torch.float32,
-                       sign_mode="canonical")
+    args = [t.unsqueeze(3).expand(B, T, H, M, D) for t in leaves[:3]]
+    gates = [t.unsqueeze(-1).expand(B, T, H, M, D) for t in leaves[3:5]]
+    y = og.gdn3_recurrence(*args, *gates, leaves[5], compact_every=compact_every, dtype=torch.float32,
+                           sign_mode="canonical")
+    if train:
+        torch.autograd.grad(y, leaves, torch.ones_like(y))
     secs = time.perf_counter() - t0
     return {
         "value": B * T / secs,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": f"oracle.gdn3.gdn3_recurrence fp32, B={B} T={T} H={H}x{M} lanes d={D}, compaction every "
-                  f"{compact_every} ({secs:.1f} s)",
+        "sample": f"oracle.gdn3.gdn3_recurrence fp32{' fwd+bwd' if train else ''}, B={B} T={T} H={H}x{M} "
+                  f"lanes d={D}, compaction every {compact_every} ({secs:.1f} s)",
     }
 
 
-def bench_gdn3(args, layer_default):
-    """GDN3 Kronecker-residual forward.  longctx: config 3 (B=1, T=32768,
+def bench_gdn3(args, layer_default, train=False):
+    """GDN3 Kronecker-residual regime.  longctx: config 3 (B=1, T=32768,
     H=16, 4 lanes, compaction every 2048 tokens).  gdn3-layer: the reference
     layer's default regime (compaction every P=16 tokens) at config 1 width
-    (B=4, T=4096, H=16, 4 lanes).  One step = one gdn3_recurrent_state call."""
+    (B=4, T=4096, H=16, 4 lanes).  One step = one gdn3_recurrent_state call
+    (forward), or with train forward + gradients of q, k, v, both gates and
+    the decay against a fixed upstream gradient (gdn3-layer-train)."""
     import torch
     from gdnx_amd import gdn3
     from oracle import inputs
@@ -243,8 +249,16 @@ def bench_gdn3(args, layer_default):
     M = x["b"].shape[-1]
     q, k, v, bg, wg, dec = (x[n].to(dev).contiguous() for n in ("q", "k", "v", "b", "w", "dec"))
     stream = torch.cuda.current_stream()
+    leaves = (q, k, v, bg, wg, dec)
+    if train:
+        for t in leaves:
+            t.requires_grad_(True)
+        dy = torch.randn(B, T, H, M, D, generator=torch.Generator().manual_seed(7)).to(q.dtype).to(dev)
 
     def step():
+        if train:
+            out = gdn3.gdn3_recurrent_state(q, k, v, bg, wg, dec, compact_every=Kc)
+            return torch.autograd.grad(out, leaves, dy)[0]
         return gdn3.gdn3_recurrent_state(q, k, v, bg, wg, dec, compact_every=Kc)
 
     for _ in range(args.warmup):
@@ -257,13 +271,21 @@ def bench_gdn3(args, layer_default):
     e1.record(stream)
     torch.cuda.synchronize()
     sec = e0.elapsed_time(e1) * 1e-3 / args.steps
-    # algorithmic bytes: q, k, v (bf16, shared by lanes), b, w, decay (fp32 per lane), y (bf16)
+    # algorithmic bytes: q, k, v (bf16, shared by lanes), b, w, decay (fp32 per lane), y (bf16);
+    # the backward reads them and dy again and writes the same-sized gradients
     nbytes = 3 * B * T * H * D * 2 + 3 * B * T * H * M * 4 + B * T * H * M * D * 2
+    if train:
+        nbytes *= 3
     achieved = nbytes / sec / 1e9
-    name = "gdn3_fwd_kernel"
+    name = "gdn3_window_kernel+gdn3_compact_kernel" + ("+gdn3_bwd_kernel" if train else "")
+    if train:
+        metric = "GDN3 Kronecker-residual layer tokens/s fwd+bwd @B=4,T=4096, compaction every 16"
+    elif layer_default:
+        metric = "GDN3 Kronecker-residual layer tokens/s fwd @B=4,T=4096, compaction every 16"
+    else:
+        metric = "GDN3 long-context tokens/s fwd @B=1,T=32768, compaction every 2048"
     line = {
-        "metric": ("GDN3 Kronecker-residual layer tokens/s fwd @B=4,T=4096, compaction every 16"
-                   if layer_default else "GDN3 long-context tokens/s fwd @B=1,T=32768, compaction every 2048"),
+        "metric": metric,
         "value": B * T / sec,
         "unit": "tokens/s",
         "n_gpus": 1,
@@ -276,6 +298,7 @@ def bench_gdn3(args, layer_default):
         "dtype": "bf16",
         "data": "synthetic",
         "config": {"workload": ("GDN3 layer default regime (K_c = P = 16) at config 1 width"
+                                + (", forward + backward" if train else "")
                                 if layer_default else "BASELINE config 3: long context with compaction"),
                    "batch": B, "seq_len": T, "heads": H, "lanes": M, "head_dim": D, "kron": "4 x (16x16 (x) 8x8)",
                    "window": 16, "compact_every": Kc, "parallelism": "single GPU"},
@@ -286,7 +309,8 @@ def bench_gdn3(args, layer_default):
         "finite": bool(torch.isfinite(y.float()).all()),
     }
     if not args.no_cpu_baseline:
-        line["cpu_baseline"] = cpu_baseline_gdn3(T=512 if layer_default else 2048, B=B, compact_every=Kc)
+        line["cpu_baseline"] = cpu_baseline_gdn3(T=256 if train else (512 if layer_default else 2048), B=B,
+                                                 compact_every=Kc, train=train)
     print(json.dumps(line), flush=True)
 
 
@@ -458,11 +482,11 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=10)
-    ap.add_argument("--workload", choices=("train", "decode", "longctx", "gdn3-layer", "kmd2", "copy"),
+    ap.add_argument("--workload", choices=("train", "decode", "longctx", "gdn3-layer", "gdn3-layer-train", "kmd2", "copy"),
                     default="train",
                     help="train: config 2 scan fwd+bwd (headline); decode: config 4 decode step; "
                          "longctx: config 3 GDN3 with compaction; gdn3-layer: GDN3 compaction every "
-                         "16 tokens; kmd2: KMD-2 scan with per-channel decay fwd+bwd (reference scan "
+                         "16 tokens; gdn3-layer-train: the same forward + backward; kmd2: KMD-2 scan with per-channel decay fwd+bwd (reference scan "
                          "benchmark, train shape); copy: 1 GiB device copy used to calibrate the HBM traffic counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -475,8 +499,8 @@ def main():
         return bench_copy(args)
     if args.workload == "kmd2":
         return bench_kmd2(args)
-    if args.workload in ("longctx", "gdn3-layer"):
-        return bench_gdn3(args, layer_default=args.workload == "gdn3-layer")
+    if args.workload in ("longctx", "gdn3-layer", "gdn3-layer-train"):
+        return bench_gdn3(args, layer_default=args.workload != "longctx", train=args.workload == "gdn3-layer-train")
 
     import torch
     from gdnx_amd import gdn3, ops

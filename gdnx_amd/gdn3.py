@@ -109,26 +109,33 @@ def _scalar_gate(g):
 class _GDN3Chunk(torch.autograd.Function):
     """gdnx_gdn3_chunk_fwd / _bwd on normalised inputs: q, k, v [B,T,H,D]
     (shared) or [B,T,H,M,D] in the compute dtype, gates [B,T,H,M] or
-    [B,T,H,M,D] float32, decay [B,T,H,M] float32."""
+    [B,T,H,M,D] float32, decay [B,T,H,M] float32.  Returns y, the compaction
+    statistics and, with want_state, the final (A, B, U, Vb); only y is
+    differentiable."""
 
     @staticmethod
-    def forward(ctx, q, k, v, bg, wg, dec, sketch, cfg):
+    def forward(ctx, q, k, v, bg, wg, dec, sketch, cfg, want_state):
         M, R, P, factors, slow_decay, Kc = cfg
-        y, _, _, tst = ops.gdn3_chunk_fwd(q, k, v, bg, wg, dec, sketch, M=M, R=R, P=P, factors=factors,
-                                          slow_decay=slow_decay, compact_every=Kc, save_states=True)
+        y, stats, state, tst = ops.gdn3_chunk_fwd(q, k, v, bg, wg, dec, sketch, M=M, R=R, P=P, factors=factors,
+                                                  slow_decay=slow_decay, compact_every=Kc,
+                                                  return_state=want_state, save_states=True)
         ctx.save_for_backward(q, k, v, bg, wg, dec, tst)
         ctx.cfg = cfg
-        return y
+        extra = (stats,) + (tuple(state) if want_state else ())
+        ctx.mark_non_differentiable(*extra)
+        return (y,) + extra
 
     @staticmethod
-    def backward(ctx, dy):
+    def backward(ctx, dy, *unused):
         q, k, v, bg, wg, dec, tst = ctx.saved_tensors
         M, R, P, factors, _, Kc = ctx.cfg
+        if dy is None:
+            return (None,) * 9
         dq, dk, dv, db, dw, ddec = ops.gdn3_chunk_bwd(q, k, v, bg, wg, dec, dy, tst, M=M, R=R, P=P,
                                                       factors=factors, compact_every=Kc)
         if q.dim() == 4:   # q, k, v shared by the lanes
             dq, dk, dv = dq.sum(3), dk.sum(3), dv.sum(3)
-        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), db, dw, ddec, None, None
+        return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), db, dw, ddec, None, None, None
 
 
 def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
@@ -149,8 +156,8 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     P (the reference layer compacts every P tokens).  Returns y
     [B,T,H,M,V] in the compute dtype, plus ((A, B, U, Vb), comp_err) when
     return_state (comp_err is the reference's summed discarded energy, a
-    device tensor).  When an input requires grad (and return_state is not
-    set) y is differentiable in q, k, v, the gates and the decay (P = 16).
+    device tensor).  When an input requires grad, y is differentiable in q,
+    k, v, the gates and the decay (P = 16); the state and comp_err are not.
     """
     B, T, H, M = decay_factors.shape
     cdt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
@@ -178,11 +185,14 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     qw = ops.sketch_width(R, a_v * a_k, b_v * b_k)
     G = default_sketch(N, b_v * b_k, qw, q.device) if sketch is None else sketch.float().contiguous()
     train = torch.is_grad_enabled() and any(t.requires_grad for t in (q4, k4, v4, bg, wg, dec))
-    if train and not return_state:
-        return _GDN3Chunk.apply(q4, k4, v4, bg, wg, dec, G, (M, R, P, factors, slow_decay, compact_every))
-    y, stats, state = ops.gdn3_chunk_fwd(q4.detach(), k4.detach(), v4.detach(), bg.detach(), wg.detach(),
-                                         dec.detach(), G, M=M, R=R, P=P, factors=factors, slow_decay=slow_decay,
-                                         compact_every=compact_every, return_state=return_state)
+    if train:
+        out = _GDN3Chunk.apply(q4, k4, v4, bg, wg, dec, G, (M, R, P, factors, slow_decay, compact_every),
+                               return_state)
+        y, stats, state = out[0], out[1], (tuple(out[2:]) if return_state else None)
+    else:
+        y, stats, state = ops.gdn3_chunk_fwd(q4, k4, v4, bg, wg, dec, G, M=M, R=R, P=P, factors=factors,
+                                             slow_decay=slow_decay, compact_every=compact_every,
+                                             return_state=return_state)
     if not return_state:
         return y
     err = (stats[:, :, 0].sum(1) - stats[:, :, 1].sum(1)).clamp(min=0.0).sum()

@@ -150,3 +150,25 @@ def test_gdn3_backward_layer_call_convention(gpu_lib):
         err = rel_l2(a, r)
         print(f"  {name} rel-L2 {err:.2e}", flush=True)
         assert err <= 1e-4, name
+
+
+def test_gdn3_training_call_returns_state_and_error(gpu_lib):
+    """The layer's call (return_state=True for the compaction error) on the
+    training path: y stays differentiable and y, the final state and the
+    error equal the no-grad call's."""
+    from gdnx_amd import gdn3
+    print("case: gdn3 training call with state", flush=True)
+    B, T, H, M, D = 1, 48, 1, 2, 128
+    xs, dy = _inputs(B, T, H, M, D, seed=44, io=torch.float32, gate="channel", per_lane=False)
+    dev = [x.to(DEV) for x in xs]
+    with torch.no_grad():
+        y0, st0, e0 = gdn3.gdn3_recurrent_state(*dev, return_state=True)
+    leaves = [x.clone().requires_grad_(True) for x in dev]
+    y1, st1, e1 = gdn3.gdn3_recurrent_state(*leaves, return_state=True)
+    assert y1.requires_grad and not any(t.requires_grad for t in st1) and not e1.requires_grad
+    assert torch.equal(y0, y1.detach())
+    for a, b in zip(st0, st1):
+        assert torch.equal(a, b)
+    assert torch.equal(e0, e1)
+    grads = torch.autograd.grad(y1, leaves, dy.to(DEV))
+    assert all(bool(torch.isfinite(g).all()) for g in grads)
