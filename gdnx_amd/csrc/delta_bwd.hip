@@ -52,7 +52,9 @@ struct GradDims {
 template <int C, int NW, int NP>
 struct alignas(16) GradLaneBuf {
   float G[C], gam[C], dec[C], ae[C], aw[C], graw[C];
-  float red[C][4][NW];   // [row][q.P1, k.P2, k.P3, v.dB][wave] partial sums (a row's 4 NW contiguous)
+  // [row][quantity * NW + wave]: q.P1, k.P2, k.P3, v.dB partial sums; rows padded by 4
+  // floats so that one row per lane reads conflict-free as 16-byte vectors
+  float red[C][4 * NW + 4];
   float tri[NP][5][16];  // per tile pair: row and column sums of Xm (dAq part), row sums of AE,
                          // row and column sums of Xm (dL part)
   float scal[NW];        // per-wave partial <dS_C, S0>
@@ -192,7 +194,7 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
         rs[a] = 0.f;
 #pragma unroll
         for (int w = 0; w < NW; w += 4) {
-          const f32x4 x = *(const f32x4*)&q.red[i][a][w];
+          const f32x4 x = *(const f32x4*)&q.red[i][a * NW + w];
           rs[a] += (x[0] + x[1]) + (x[2] + x[3]);
         }
       }
@@ -216,8 +218,7 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
       r3d = q.dec[i] * rs[2];
     }
     // chunk-end decay: d/dG_last of gamma_C <dS_C, S0> and of the dec factors
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) r3d += __shfl_xor(r3d, off, 64);
+    r3d = wave_sum(r3d);
     if (lane == C - 1) {
       float s = 0.f;
 #pragma unroll
@@ -225,12 +226,7 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
       dGi += s * q.gam[C - 1] + r3d;
     }
     // dg_s = sum_{i >= s} dG_i (suffix sum within the chunk)
-    float sfx = (lane < C) ? dGi : 0.f;
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      const float o = __shfl_down(sfx, off, 64);
-      if (lane + off < 64) sfx += o;
-    }
+    const float sfx = lane_suffix<C>((lane < C) ? dGi : 0.f, lane);
     const int t = t0 + lane;
     if (lane < C && t < p.T) {
       const size_t si = ((size_t)(b * p.T + t) * p.H + h) * p.M + mm;
@@ -407,15 +403,14 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
         const float s3 = row_prefix16(P3[it][ii] * kv);
         const float sw = row_prefix16(dbv * to_f(sm.v[i * LDD + dcol]));
         if (n16 == 15) {
-          lb.red[i][0][wave] = s1;
-          lb.red[i][1][wave] = s2;
-          lb.red[i][2][wave] = s3;
-          lb.red[i][3][wave] = sw;
+          lb.red[i][0 * NW + wave] = s1;
+          lb.red[i][1 * NW + wave] = s2;
+          lb.red[i][2 * NW + wave] = s3;
+          lb.red[i][3 * NW + wave] = sw;
         }
       }
     }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) sdot += __shfl_xor(sdot, off, 64);
+    sdot = wave_sum(sdot);
     if (lane == 0) lb.scal[wave] = sdot;
   }
   __syncthreads();  // lane tiles dead: the union becomes Q^T, K^T and the gram-gradient factors

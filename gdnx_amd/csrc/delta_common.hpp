@@ -69,6 +69,74 @@ __host__ __device__ __forceinline__ size_t prep_bytes_per_record(int C, size_t e
   return 2 * (size_t)C * C * es + (size_t)kNumSc * C * sizeof(float);
 }
 
+// Inclusive prefix sum over the 16 lanes of each DPP row (lane bits 0..3);
+// lane 15 of a row ends with the row's total.
+__device__ __forceinline__ float row_prefix16(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, true));
+  return x;
+}
+
+// Inclusive suffix sum over the 16 lanes of each DPP row (row_shl steps).
+__device__ __forceinline__ float row_suffix16(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x101, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x102, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x104, 0xf, 0xf, true));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x108, 0xf, 0xf, true));
+  return x;
+}
+
+__device__ __forceinline__ float lane_value(float x, int src) {
+  return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), src));
+}
+
+// Wave scans on DPP rows plus scalar reads of the row totals (no LDS
+// permutes on the dependent path).  N: the lanes that take part (lanes at
+// or past N must hold 0 for the suffix).
+template <int N>
+__device__ __forceinline__ float lane_prefix(float x, int lane) {
+  const float rp = row_prefix16(x);
+  float add = 0.f;
+  if constexpr (N > 16) {
+    const float t0 = lane_value(rp, 15);
+    add += lane >= 16 ? t0 : 0.f;
+  }
+  if constexpr (N > 32) {
+    const float t1 = lane_value(rp, 31);
+    add += lane >= 32 ? t1 : 0.f;
+  }
+  if constexpr (N > 48) {
+    const float t2 = lane_value(rp, 47);
+    add += lane >= 48 ? t2 : 0.f;
+  }
+  return rp + add;
+}
+template <int N>
+__device__ __forceinline__ float lane_suffix(float x, int lane) {
+  const float rs = row_suffix16(x);
+  float add = 0.f;
+  if constexpr (N > 16) {
+    const float t1 = lane_value(rs, 16);
+    add += lane < 16 ? t1 : 0.f;
+  }
+  if constexpr (N > 32) {
+    const float t2 = lane_value(rs, 32);
+    add += lane < 32 ? t2 : 0.f;
+  }
+  if constexpr (N > 48) {
+    const float t3 = lane_value(rs, 48);
+    add += lane < 48 ? t3 : 0.f;
+  }
+  return rs + add;
+}
+// the sum over all 64 lanes, in every lane
+__device__ __forceinline__ float wave_sum(float x) {
+  const float rp = row_prefix16(x);
+  return (lane_value(rp, 15) + lane_value(rp, 31)) + (lane_value(rp, 47) + lane_value(rp, 63));
+}
+
 // Prefetched per-token scalars of one lane (token t0 + lane).
 struct ScalarRegs {
   float ae, aw, g;
@@ -103,13 +171,8 @@ __device__ __forceinline__ void scal_fetch_all(ScalarRegs& r, const float* ae, c
 
 template <int C>
 __device__ __forceinline__ void scal_commit(const ChunkScalars& s, const ScalarRegs& r, int lane) {
-  float G = fmaxf(fminf(r.g, 0.f), kLogFloor);
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float o = __shfl_up(G, off, 64);
-    if (lane >= off) G += o;
-  }
-  const float Glast = __shfl(G, C - 1, 64);
+  const float G = lane_prefix<C>(fmaxf(fminf(r.g, 0.f), kLogFloor), lane);
+  const float Glast = lane_value(G, C - 1);
   if (lane < C) {
     s.G[lane] = G;
     s.gam[lane] = __expf(G);
@@ -131,13 +194,8 @@ __device__ __forceinline__ void prep_scalars(const ChunkScalars& s, const float*
     raw = g[(size_t)t * st];
     vg = fmaxf(fminf(raw, 0.f), kLogFloor);
   }
-  float G = vg;
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float o = __shfl_up(G, off, 64);
-    if (lane >= off) G += o;
-  }
-  const float Glast = __shfl(G, C - 1, 64);
+  const float G = lane_prefix<C>(vg, lane);
+  const float Glast = lane_value(G, C - 1);
   if (lane < C) {
     s.G[lane] = G;
     s.gam[lane] = __expf(G);
@@ -451,16 +509,6 @@ __device__ __forceinline__ f32x4 load4(const float* p) { return *(const f32x4*)p
 template <typename CT, int D, int C>
 __device__ __forceinline__ const CT* stash_state_ptr(const CT* rec, int dt, int V, int lane) {
   return rec + stash_tile_offset<CT, D>(dt, V, lane);
-}
-
-// Inclusive prefix sum over the 16 lanes of each DPP row (lane bits 0..3);
-// lane 15 of a row ends with the row's total.
-__device__ __forceinline__ float row_prefix16(float x) {
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x111, 0xf, 0xf, true));
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x112, 0xf, 0xf, true));
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x114, 0xf, 0xf, true));
-  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x118, 0xf, 0xf, true));
-  return x;
 }
 
 // Frag element e of a tile-native fragment sits at row offset frag_row(e, g4)
