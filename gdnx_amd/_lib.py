@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(_HERE, "libgdnx.so")
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _c_int, _c_ll, _vp, _c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_float
 
@@ -46,7 +46,8 @@ SIGNATURES = {
     "gdnx_kron_read": (_c_int, [_vp] * 6 + [_c_int] * 9 + [_vp]),
     "gdnx_gdn3_coeff": (_c_int, [_vp] * 3 + [_c_int] * 6 + [_vp]),
     "gdnx_delta_chan_states_bytes": (_c_ll, [_c_int] * 4),
-    "gdnx_delta_chan_fwd": (_c_int, [_vp] * 11 + [_c_int] * 4 + [_vp]),
+    "gdnx_delta_chan_fwd_workspace_bytes": (_c_ll, [_c_int] * 4),
+    "gdnx_delta_chan_fwd": (_c_int, [_vp] * 12 + [_c_int] * 4 + [_vp]),
     "gdnx_delta_chan_bwd": (_c_int, [_vp] * 17 + [_c_int] * 4 + [_vp]),
     "gdnx_gdn3_coeff_bwd": (_c_int, [_vp] * 6 + [_c_int] * 6 + [_vp]),
 }

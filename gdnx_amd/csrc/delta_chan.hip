@@ -134,33 +134,156 @@ __device__ __forceinline__ float chunk_scalar(const float* base, int b, int t0, 
 }  // namespace
 
 // ---------------------------------------------------------------------------
-// forward scan
+// per-chunk operand records (state independent, one workgroup per chunk)
+//   forward:  U = T diag(beta_w) V, -Wm = -T diag(beta_e) (K o e^G), Q o e^G,
+//             (K o e^{G_L - G})^T, Aq, e^{G_L}
+//   backward: K o e^{G_L - G}, (Q o e^G)^T, (K o e^G)^T, T^T, Aq^T, beta_e, e^{G_L}
+// so that the scans carry only the state-dependent products.
 // ---------------------------------------------------------------------------
 template <int D>
-struct alignas(16) ChanFwdSmem {
-  static constexpr int LDD = D + 4;
-  ChanOps<D> o;
-  float qe[CC * LDD];    // Q o e^G (rows)
-  float ket[D * LDC];    // (K o e^G)^T
-  float kft[D * LDC];    // (K o e^{G_L - G})^T
-  float vt[D * LDC];     // V^T
-  float wm[CC * LDD];    // -Wm
-  float rn[ChD<D>::NW][CC];
+struct ChRec {
+  static constexpr int CD = CC * D;
+  static constexpr int F_U = 0, F_NWM = CD, F_QE = 2 * CD, F_KFT = 3 * CD, F_AQ = 4 * CD, F_EGL = 4 * CD + CC * CC;
+  static constexpr int FN = 4 * CD + CC * CC + D;
+  static constexpr int B_KF = 0, B_QET = CD, B_KET = 2 * CD, B_TT = 3 * CD, B_AQT = 3 * CD + CC * CC,
+                       B_BE = 3 * CD + 2 * CC * CC, B_EGL = 3 * CD + 2 * CC * CC + CC;
+  static constexpr int BN = 3 * CD + 2 * CC * CC + CC + D;
+  static_assert(FN % 4 == 0 && BN % 4 == 0 && F_EGL % 4 == 0 && B_EGL % 4 == 0, "16-byte aligned records");
 };
 
-template <int D, bool STASH>
-__global__ void __launch_bounds__(64 * (D / 16)) chan_fwd_kernel(ChanArgs p) {
+template <int D>
+struct alignas(16) ChanPrepSmem {
+  ChanOps<D> o;
+  float ket[D * LDC];    // (K o e^G)^T
+  float kft[D * LDC];    // (K o e^{G_L - G})^T
+  float qet[D * LDC];    // (Q o e^G)^T
+  float vt[D * LDC];     // V^T
+};
+
+template <int D, bool BWD>
+__global__ void __launch_bounds__(64 * (D / 16)) chan_prep_kernel(ChanArgs p) {
   typedef ChD<D> Cd;
-  constexpr int NW = Cd::NW, NT = Cd::NT, NDT = Cd::NDT, LDD = Cd::LDD;
-  __shared__ ChanFwdSmem<D> sm;
+  typedef ChRec<D> Rc;
+  constexpr int NT = Cd::NT, LDD = Cd::LDD;
+  __shared__ ChanPrepSmem<D> sm;
   ChanOps<D>& o = sm.o;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
+  const int NC = (p.T + CC - 1) / CC;
   const int nchains = p.B * p.H;
-  const int chain = xcd_remap(blockIdx.x, nchains);
+  const int blk = xcd_remap(blockIdx.x, nchains * NC);
+  const int c = blk % NC, chain = blk / NC;
   const int h = chain % p.H, b = chain / p.H;
-  const int V = wave;
+  const int t0 = c * CC;
+  const size_t rec = rec_index(chain, c, nchains);
+  float* fr = p.frec + rec * Rc::FN;
+  float* br = BWD ? p.brec + rec * Rc::BN : nullptr;
+  const unsigned rsb = (unsigned)((size_t)p.H * D * 4);
+  {
+    Stage<float, CC, D, 1, NT> sq, sk, sl;
+    Stage<float, CC, D, 4, NT> sv;
+    sq.fetch(chunk_rsrc(p.q, b, t0, p.T, p.H, h, D), rsb, tid);
+    sk.fetch(chunk_rsrc(p.k, b, t0, p.T, p.H, h, D), rsb, tid);
+    sl.fetch(chunk_rsrc(p.lg, b, t0, p.T, p.H, h, D), rsb, tid);
+    sv.fetch(chunk_rsrc(p.v, b, t0, p.T, p.H, h, D), rsb, tid);
+    const float be = chunk_scalar(p.be, b, t0, tid % CC, p.T, p.H, h);
+    const float bw = chunk_scalar(p.bw, b, t0, tid % CC, p.T, p.H, h);
+    sq.template commit_nat<LDD>(o.q, tid);
+    sk.template commit_nat<LDD>(o.k, tid);
+    sl.template commit_nat<LDD>(o.G, tid);
+    sv.template commit_tr<LDC>(sm.vt, tid);
+    if (tid < CC) {
+      o.be[tid] = be;
+      o.bw[tid] = bw;
+    }
+  }
+  __syncthreads();
+  chan_prefix<D>(o, tid);
+  __syncthreads();
+  chan_grams<D>(o, wave, lane);
+  for (int e = tid; e < CC * D; e += NT) {
+    const int i = e / D, d = e % D;
+    const float G = o.G[i * LDD + d], GL = o.G[(CC - 1) * LDD + d];
+    const float E = __expf(G), F = __expf(GL - G), kv = o.k[i * LDD + d], qv = o.q[i * LDD + d] * E;
+    fr[Rc::F_QE + e] = qv;
+    sm.ket[d * LDC + i] = kv * E;
+    sm.kft[d * LDC + i] = kv * F;
+    if constexpr (BWD) {
+      br[Rc::B_KF + e] = kv * F;
+      sm.qet[d * LDC + i] = qv;
+    }
+  }
+  __syncthreads();
+  chan_inverse<D>(o, wave, lane);
+  __syncthreads();
+  {  // -Wm on this wave's key tile: acc[s] = Wm[n][16 wave + 4 g + s]
+    const f32x4 bt = frag_scale(ld_frag(&o.T[n16 * LDC], g4), o.be, g4);
+    f32x4 acc = zero4();
+    mma(acc, ld_frag(&sm.ket[(16 * wave + n16) * LDC], g4), bt);
+    *(f32x4*)&fr[Rc::F_NWM + n16 * D + 16 * wave + 4 * g4] = -acc;
+  }
+  {  // U = T diag(beta_w) V on value tile wave, stored as rows
+    f32x4 acc = zero4();
+    mma(acc, frag_scale(ld_frag(&o.T[n16 * LDC], g4), o.bw, g4), ld_frag(&sm.vt[(16 * wave + n16) * LDC], g4));
+    *(f32x4*)&fr[Rc::F_U + n16 * D + 16 * wave + 4 * g4] = tile_transpose((float*)nullptr, acc, lane);
+  }
+  for (int e = tid; e < D * CC; e += NT) {
+    const int d = e / CC, i = e % CC;
+    fr[Rc::F_KFT + e] = sm.kft[d * LDC + i];
+    if constexpr (BWD) {
+      br[Rc::B_QET + e] = sm.qet[d * LDC + i];
+      br[Rc::B_KET + e] = sm.ket[d * LDC + i];
+    }
+  }
+  for (int e = tid; e < CC * CC; e += NT) {
+    const int i = e / CC, j = e % CC;
+    fr[Rc::F_AQ + e] = o.Aq[i * LDC + j];
+    if constexpr (BWD) {
+      br[Rc::B_TT + e] = o.T[j * LDC + i];
+      br[Rc::B_AQT + e] = o.Aq[j * LDC + i];
+    }
+  }
+  for (int e = tid; e < D; e += NT) {
+    fr[Rc::F_EGL + e] = o.eGL[e];
+    if constexpr (BWD) br[Rc::B_EGL + e] = o.eGL[e];
+  }
+  if constexpr (BWD)
+    if (tid < CC) br[Rc::B_BE + tid] = o.be[tid];
+}
+
+// ---------------------------------------------------------------------------
+// forward state scan: one workgroup of NWV waves per (chain, block of 16 NWV
+// value columns); per chunk, from the record:
+//   R = U - Wm S0,  Y = (Q o e^G) S0 + Aq R,  S = diag(e^{G_L}) S0 + (K o e^{G_L - G})^T R
+// With SCORE (|r_t| requested) a chain's value columns stay in one workgroup.
+// ---------------------------------------------------------------------------
+template <int D, int NWV>
+struct alignas(16) ChanScanFSmem {
+  static constexpr int LDD = D + 4, BV = 16 * NWV, LDU = BV + 4;
+  float nwm[CC * LDD];
+  float qe[CC * LDD];
+  float kft[D * LDC];
+  float aq[CC * LDC];
+  float egl[D];
+  float u[CC * LDU];
+  float rn[NWV][CC];
+};
+
+template <int D, int NWV, bool STASH, bool SCORE>
+__global__ void __launch_bounds__(64 * NWV) chan_scan_fwd_kernel(ChanArgs p) {
+  typedef ChRec<D> Rc;
+  typedef ChanScanFSmem<D, NWV> Sm;
+  constexpr int NT = 64 * NWV, NDT = D / 16, LDD = Sm::LDD, BV = Sm::BV, LDU = Sm::LDU, NVB = D / BV;
+  static_assert(!SCORE || NVB == 1, "the update norm sums over all value columns in one workgroup");
+  __shared__ Sm sm;
+  const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
+  const int nchains = p.B * p.H;
+  const int work = xcd_remap(blockIdx.x, nchains * NVB);
+  const int chain = work / NVB, vb = work % NVB;
+  const int h = chain % p.H, b = chain / p.H;
+  const int V = vb * NWV + wave;
   const int NC = (p.T + CC - 1) / CC;
   const size_t NR = (size_t)nchains * NC;
+  const unsigned rsb = (unsigned)((size_t)p.H * D * 4);
 
   f32x4 S[NDT];   // S[dt][i] = S0[16 dt + 4 g + i][16 V + n]
 #pragma unroll
@@ -173,18 +296,19 @@ __global__ void __launch_bounds__(64 * (D / 16)) chan_fwd_kernel(ChanArgs p) {
   }
   __builtin_amdgcn_s_waitcnt(0);
 
-  Stage<float, CC, D, 1, NT> pq, pk, pl;
-  Stage<float, CC, D, 4, NT> pv;
-  float pbe = 0.f, pbw = 0.f;
-  const unsigned rsb = (unsigned)((size_t)p.H * D * 4);
+  Stage<float, CC, D, 1, NT> pn, pq;
+  Stage<float, D, CC, 1, NT> pk;
+  Stage<float, CC, CC, 1, NT> pa;
+  Stage<float, 1, D, 1, NT> pe;
+  Stage<float, CC, BV, 1, NT> pu;
   auto fetch = [&](int c) {
-    const int t0 = c * CC;
-    pq.fetch(chunk_rsrc(p.q, b, t0, p.T, p.H, h, D), rsb, tid);
-    pk.fetch(chunk_rsrc(p.k, b, t0, p.T, p.H, h, D), rsb, tid);
-    pl.fetch(chunk_rsrc(p.lg, b, t0, p.T, p.H, h, D), rsb, tid);
-    pv.fetch(chunk_rsrc(p.v, b, t0, p.T, p.H, h, D), rsb, tid);
-    pbe = chunk_scalar(p.be, b, t0, tid % CC, p.T, p.H, h);
-    pbw = chunk_scalar(p.bw, b, t0, tid % CC, p.T, p.H, h);
+    const float* fr = p.frec + rec_index(chain, c, nchains) * Rc::FN;
+    pn.fetch_dense(fr + Rc::F_NWM, tid);
+    pq.fetch_dense(fr + Rc::F_QE, tid);
+    pk.fetch_dense(fr + Rc::F_KFT, tid);
+    pa.fetch_dense(fr + Rc::F_AQ, tid);
+    pe.fetch_dense(fr + Rc::F_EGL, tid);
+    pu.fetch(buf_rsrc(fr + Rc::F_U + vb * BV, (unsigned)(Rc::CD * 4)), (unsigned)(D * 4), tid);
   };
   fetch(0);
   __builtin_amdgcn_s_waitcnt(0);
@@ -193,85 +317,60 @@ __global__ void __launch_bounds__(64 * (D / 16)) chan_fwd_kernel(ChanArgs p) {
     const int t0 = c * CC;
     const size_t rec = rec_index(chain, c, nchains);
     __syncthreads();
-    pq.template commit_nat<LDD>(o.q, tid);
-    pk.template commit_nat<LDD>(o.k, tid);
-    pl.template commit_nat<LDD>(o.G, tid);
-    pv.template commit_tr<LDC>(sm.vt, tid);
-    if (tid < CC) {
-      o.be[tid] = pbe;
-      o.bw[tid] = pbw;
-    }
+    pn.template commit_nat<LDD>(sm.nwm, tid);
+    pq.template commit_nat<LDD>(sm.qe, tid);
+    pk.template commit_nat<LDC>(sm.kft, tid);
+    pa.template commit_nat<LDC>(sm.aq, tid);
+    pe.template commit_nat<D>(sm.egl, tid);
+    pu.template commit_nat<LDU>(sm.u, tid);
     __syncthreads();
     fetch(min(c + 1, NC - 1));
-    chan_prefix<D>(o, tid);
-    __syncthreads();
-    chan_grams<D>(o, wave, lane);
-    for (int e = tid; e < CC * D; e += NT) {
-      const int i = e / D, d = e % D;
-      const float G = o.G[i * LDD + d], GL = o.G[(CC - 1) * LDD + d];
-      const float E = __expf(G), kv = o.k[i * LDD + d];
-      sm.qe[i * LDD + d] = o.q[i * LDD + d] * E;
-      sm.ket[d * LDC + i] = kv * E;
-      sm.kft[d * LDC + i] = kv * __expf(GL - G);
-    }
-    __syncthreads();
-    chan_inverse<D>(o, wave, lane);
-    __syncthreads();
-    // -Wm = -T diag(beta_e) (K o e^G): Wm^T[d][i] on this wave's key tile
-    {
-      const f32x4 bt = frag_scale(ld_frag(&o.T[n16 * LDC], g4), o.be, g4);
-      f32x4 acc = zero4();
-      mma(acc, ld_frag(&sm.ket[(16 * wave + n16) * LDC], g4), bt);
-      st4(&sm.wm[n16 * LDD + 16 * wave + 4 * g4], -acc[0], -acc[1], -acc[2], -acc[3]);
-    }
-    // U = T diag(beta_w) V on this wave's value columns
-    f32x4 R = zero4();
-    mma(R, frag_scale(ld_frag(&o.T[n16 * LDC], g4), o.bw, g4), ld_frag(&sm.vt[(16 * V + n16) * LDC], g4));
     if constexpr (STASH) {
       float* cst = (float*)p.chunk_states + rec * (D * D);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) *(f32x4*)(cst + stash_tile_offset<float, D>(dt, V, lane)) = S[dt];
     }
-    __syncthreads();   // -Wm complete
-    // R = U - Wm S0
+    // R = U - Wm S0 (two accumulators)
+    f32x4 R0, R1 = zero4();
 #pragma unroll
-    for (int kb = 0; kb < NDT; ++kb) mma(R, ld_frag(&sm.wm[n16 * LDD + kb * 16], g4), S[kb]);
+    for (int s = 0; s < 4; ++s) R0[s] = sm.u[(4 * g4 + s) * LDU + 16 * wave + n16];
+#pragma unroll
+    for (int kb = 0; kb < NDT; ++kb) mma((kb & 1) ? R1 : R0, ld_frag(&sm.nwm[n16 * LDD + kb * 16], g4), S[kb]);
+    const f32x4 R = R0 + R1;
     if constexpr (STASH) {
       float* rst = (float*)p.chunk_states + NR * D * D + rec * (CC * D);
       *(f32x4*)(rst + stash_tile_offset<float, D>(0, V, lane)) = R;
     }
-    if (p.r_norm) {   // |r_i|: squares over this wave's columns, then across waves
+    if constexpr (SCORE) {
       const f32x4 sq = R * R;
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        float x = sq[e];
-#pragma unroll
-        for (int off = 1; off < 16; off <<= 1) x += __shfl_xor(x, off, 64);
-        if (n16 == 0) sm.rn[wave][4 * g4 + e] = x;
+        const float x = row_prefix16(sq[e]);
+        if (n16 == 15) sm.rn[wave][4 * g4 + e] = x;
       }
     }
     // Y = (Q o e^G) S0 + Aq R
     {
-      f32x4 Y = zero4();
+      f32x4 Y0 = zero4(), Y1 = zero4();
 #pragma unroll
-      for (int kb = 0; kb < NDT; ++kb) mma(Y, ld_frag(&sm.qe[n16 * LDD + kb * 16], g4), S[kb]);
-      mma(Y, ld_frag(&o.Aq[n16 * LDC], g4), R);
-      const f32x4 yt = tile_transpose((float*)nullptr, Y, lane);
+      for (int kb = 0; kb < NDT; ++kb) mma((kb & 1) ? Y1 : Y0, ld_frag(&sm.qe[n16 * LDD + kb * 16], g4), S[kb]);
+      mma(Y0, ld_frag(&sm.aq[n16 * LDC], g4), R);
+      const f32x4 yt = tile_transpose((float*)nullptr, Y0 + Y1, lane);
       const __amdgpu_buffer_rsrc_t yr = chunk_rsrc((const float*)p.y, b, t0, p.T, p.H, h, D);
       buf_store4(yr, (unsigned)n16 * rsb + (16 * V + 4 * g4) * 4, (const float*)nullptr, yt[0], yt[1], yt[2], yt[3]);
     }
     // S = diag(e^{G_L}) S0 + (K o e^{G_L - G})^T R
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      S[dt] *= *(const f32x4*)&o.eGL[dt * 16 + 4 * g4];
+      S[dt] *= *(const f32x4*)&sm.egl[dt * 16 + 4 * g4];
       mma(S[dt], ld_frag(&sm.kft[(dt * 16 + n16) * LDC], g4), R);
     }
-    if (p.r_norm) {
+    if constexpr (SCORE) {
       __syncthreads();
       if (tid < CC && t0 + tid < p.T) {
         float s = 0.f;
 #pragma unroll
-        for (int w = 0; w < NW; ++w) s += sm.rn[w][tid];
+        for (int w = 0; w < NWV; ++w) s += sm.rn[w][tid];
         p.r_norm[((size_t)b * p.T + t0 + tid) * p.H + h] = sqrtf(s);
       }
     }
@@ -285,35 +384,38 @@ __global__ void __launch_bounds__(64 * (D / 16)) chan_fwd_kernel(ChanArgs p) {
 }
 
 // ---------------------------------------------------------------------------
-// reverse scan of the state gradient
+// reverse scan of the state gradient, value-split like the forward:
 //   dR = Aq^T dY + (K o e^{G_L - G}) dS,  dB = T^T dR
 //   dS0 = diag(e^{G_L}) dS + (Q o e^G)^T dY - (K o e^G)^T diag(beta_e) dB
 // ---------------------------------------------------------------------------
-template <int D>
-struct alignas(16) ChanBwdSmem {
-  static constexpr int LDD = D + 4;
-  ChanOps<D> o;
-  float kf[CC * LDD];    // K o e^{G_L - G} (rows)
-  float qet[D * LDC];    // (Q o e^G)^T
-  float ket[D * LDC];    // (K o e^G)^T
-  float dyt[D * LDC];    // dY^T
-  float aqt[CC * LDC];   // Aq^T
-  float tt[CC * LDC];    // T^T
+template <int D, int NWV>
+struct alignas(16) ChanScanBSmem {
+  static constexpr int LDD = D + 4, BV = 16 * NWV;
+  float kf[CC * LDD];
+  float qet[D * LDC];
+  float ket[D * LDC];
+  float tt[CC * LDC];
+  float aqt[CC * LDC];
+  float be[CC];
+  float egl[D];
+  float dyt[BV * LDC];
 };
 
-template <int D>
-__global__ void __launch_bounds__(64 * (D / 16)) chan_bwd_scan_kernel(ChanBwdArgs p) {
-  typedef ChD<D> Cd;
-  constexpr int NT = Cd::NT, NDT = Cd::NDT, LDD = Cd::LDD;
-  __shared__ ChanBwdSmem<D> sm;
-  ChanOps<D>& o = sm.o;
+template <int D, int NWV>
+__global__ void __launch_bounds__(64 * NWV) chan_scan_bwd_kernel(ChanBwdArgs p) {
+  typedef ChRec<D> Rc;
+  typedef ChanScanBSmem<D, NWV> Sm;
+  constexpr int NT = 64 * NWV, NDT = D / 16, LDD = Sm::LDD, BV = Sm::BV, NVB = D / BV;
+  __shared__ Sm sm;
   const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
   const int nchains = p.B * p.H;
-  const int chain = xcd_remap(blockIdx.x, nchains);
+  const int work = xcd_remap(blockIdx.x, nchains * NVB);
+  const int chain = work / NVB, vb = work % NVB;
   const int h = chain % p.H, b = chain / p.H;
-  const int V = wave;
+  const int V = vb * NWV + wave;
   const int NC = (p.T + CC - 1) / CC;
   const size_t NR = (size_t)nchains * NC;
+  const float* brec = (const float*)p.s_stash + NR * ((size_t)D * D + CC * D + Rc::FN);
 
   f32x4 dS[NDT];
 #pragma unroll
@@ -327,17 +429,23 @@ __global__ void __launch_bounds__(64 * (D / 16)) chan_bwd_scan_kernel(ChanBwdArg
   }
   __builtin_amdgcn_s_waitcnt(0);
 
-  Stage<float, CC, D, 1, NT> pq, pk, pl;
-  Stage<float, CC, D, 4, NT> py;
-  float pbe = 0.f;
+  Stage<float, CC, D, 1, NT> pf;
+  Stage<float, D, CC, 1, NT> pqt, pkt;
+  Stage<float, CC, CC, 1, NT> ptt, pat;
+  Stage<float, 1, CC, 1, NT> pb;
+  Stage<float, 1, D, 1, NT> pe;
+  Stage<float, CC, BV, 4, NT> py;
   const unsigned rsb = (unsigned)((size_t)p.H * D * 4);
   auto fetch = [&](int c) {
-    const int t0 = c * CC;
-    pq.fetch(chunk_rsrc(p.q, b, t0, p.T, p.H, h, D), rsb, tid);
-    pk.fetch(chunk_rsrc(p.k, b, t0, p.T, p.H, h, D), rsb, tid);
-    pl.fetch(chunk_rsrc(p.lg, b, t0, p.T, p.H, h, D), rsb, tid);
-    py.fetch(chunk_rsrc(p.dy, b, t0, p.T, p.H, h, D), rsb, tid);
-    pbe = chunk_scalar(p.be, b, t0, tid % CC, p.T, p.H, h);
+    const float* br = brec + rec_index(chain, c, nchains) * Rc::BN;
+    pf.fetch_dense(br + Rc::B_KF, tid);
+    pqt.fetch_dense(br + Rc::B_QET, tid);
+    pkt.fetch_dense(br + Rc::B_KET, tid);
+    ptt.fetch_dense(br + Rc::B_TT, tid);
+    pat.fetch_dense(br + Rc::B_AQT, tid);
+    pb.fetch_dense(br + Rc::B_BE, tid);
+    pe.fetch_dense(br + Rc::B_EGL, tid);
+    py.fetch(chunk_rsrc(p.dy + vb * BV, b, c * CC, p.T, p.H, h, D), rsb, tid);
   };
   fetch(NC - 1);
   __builtin_amdgcn_s_waitcnt(0);
@@ -345,56 +453,37 @@ __global__ void __launch_bounds__(64 * (D / 16)) chan_bwd_scan_kernel(ChanBwdArg
   for (int c = NC - 1; c >= 0; --c) {
     const size_t rec = rec_index(chain, c, nchains);
     __syncthreads();
-    pq.template commit_nat<LDD>(o.q, tid);
-    pk.template commit_nat<LDD>(o.k, tid);
-    pl.template commit_nat<LDD>(o.G, tid);
+    pf.template commit_nat<LDD>(sm.kf, tid);
+    pqt.template commit_nat<LDC>(sm.qet, tid);
+    pkt.template commit_nat<LDC>(sm.ket, tid);
+    ptt.template commit_nat<LDC>(sm.tt, tid);
+    pat.template commit_nat<LDC>(sm.aqt, tid);
+    pb.template commit_nat<CC>(sm.be, tid);
+    pe.template commit_nat<D>(sm.egl, tid);
     py.template commit_tr<LDC>(sm.dyt, tid);
-    if (tid < CC) o.be[tid] = pbe;
     __syncthreads();
     fetch(max(c - 1, 0));
-    chan_prefix<D>(o, tid);
-    __syncthreads();
-    chan_grams<D>(o, wave, lane);
-    for (int e = tid; e < CC * D; e += NT) {
-      const int i = e / D, d = e % D;
-      const float G = o.G[i * LDD + d], GL = o.G[(CC - 1) * LDD + d];
-      const float E = __expf(G), kv = o.k[i * LDD + d];
-      sm.kf[i * LDD + d] = kv * __expf(GL - G);
-      sm.qet[d * LDC + i] = o.q[i * LDD + d] * E;
-      sm.ket[d * LDC + i] = kv * E;
-    }
-    __syncthreads();
-    chan_inverse<D>(o, wave, lane);
-    for (int e = tid; e < CC * CC; e += NT) {   // transposed Aq (already complete) and T
-      const int i = e / CC, jj = e % CC;
-      sm.aqt[jj * LDC + i] = o.Aq[i * LDC + jj];
-      sm.tt[jj * LDC + i] = o.T[i * LDC + jj];
-    }
-    __syncthreads();
-
     {
       float* cst = (float*)p.ds_stash + rec * (D * D);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt) *(f32x4*)(cst + stash_tile_offset<float, D>(dt, V, lane)) = dS[dt];
     }
-    // dR = Aq^T dY + (K o e^{G_L - G}) dS
-    const f32x4 dYf = ld_frag(&sm.dyt[(16 * V + n16) * LDC], g4);
-    f32x4 dR = zero4();
+    const f32x4 dYf = ld_frag(&sm.dyt[(16 * wave + n16) * LDC], g4);
+    f32x4 dR0 = zero4(), dR1 = zero4();
 #pragma unroll
-    for (int kb = 0; kb < NDT; ++kb) mma(dR, ld_frag(&sm.kf[n16 * LDD + kb * 16], g4), dS[kb]);
-    mma(dR, ld_frag(&sm.aqt[n16 * LDC], g4), dYf);
-    // dB = T^T dR
+    for (int kb = 0; kb < NDT; ++kb) mma((kb & 1) ? dR1 : dR0, ld_frag(&sm.kf[n16 * LDD + kb * 16], g4), dS[kb]);
+    mma(dR0, ld_frag(&sm.aqt[n16 * LDC], g4), dYf);
+    const f32x4 dR = dR0 + dR1;
     f32x4 dB = zero4();
     mma(dB, ld_frag(&sm.tt[n16 * LDC], g4), dR);
     {
       float* bst = (float*)p.ds_stash + NR * D * D + rec * (CC * D);
       *(f32x4*)(bst + stash_tile_offset<float, D>(0, V, lane)) = dB;
     }
-    // dS <- diag(e^{G_L}) dS + (Q o e^G)^T dY - (K o e^G)^T diag(beta_e) dB
-    const f32x4 dBf = -dB * *(const f32x4*)&o.be[4 * g4];
+    const f32x4 dBf = -dB * *(const f32x4*)&sm.be[4 * g4];
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt) {
-      dS[dt] *= *(const f32x4*)&o.eGL[dt * 16 + 4 * g4];
+      dS[dt] *= *(const f32x4*)&sm.egl[dt * 16 + 4 * g4];
       mma(dS[dt], ld_frag(&sm.qet[(dt * 16 + n16) * LDC], g4), dYf);
       mma(dS[dt], ld_frag(&sm.ket[(dt * 16 + n16) * LDC], g4), dBf);
     }
@@ -633,20 +722,41 @@ __global__ void __launch_bounds__(64 * (D / 16)) chan_grads_kernel(ChanBwdArgs p
 }
 
 template <int D>
-static int launch_chan_fwd(const ChanArgs& a, hipStream_t stream) {
-  const dim3 grid(a.B * a.H), block(64 * (D / 16));
-  if (a.chunk_states)
-    hipLaunchKernelGGL((chan_fwd_kernel<D, true>), grid, block, 0, stream, a);
+static int launch_chan_fwd(ChanArgs a, hipStream_t stream) {
+  typedef ChRec<D> Rc;
+  const int nchains = a.B * a.H, NC = (a.T + CC - 1) / CC;
+  const size_t NR = (size_t)nchains * NC;
+  const bool train = a.chunk_states != nullptr;
+  a.frec = train ? (float*)a.chunk_states + NR * ((size_t)D * D + CC * D) : (float*)a.workspace;
+  a.brec = train ? a.frec + NR * Rc::FN : nullptr;
+  if (train)
+    hipLaunchKernelGGL((chan_prep_kernel<D, true>), dim3(nchains * NC), dim3(64 * (D / 16)), 0, stream, a);
   else
-    hipLaunchKernelGGL((chan_fwd_kernel<D, false>), grid, block, 0, stream, a);
-  return check_launch("chan_fwd_kernel");
+    hipLaunchKernelGGL((chan_prep_kernel<D, false>), dim3(nchains * NC), dim3(64 * (D / 16)), 0, stream, a);
+  int rc = check_launch("chan_prep_kernel");
+  if (rc) return rc;
+  if (a.r_norm) {   // one workgroup per chain: the update norm sums every value column
+    constexpr int NW = D / 16;
+    if (train)
+      hipLaunchKernelGGL((chan_scan_fwd_kernel<D, NW, true, true>), dim3(nchains), dim3(64 * NW), 0, stream, a);
+    else
+      hipLaunchKernelGGL((chan_scan_fwd_kernel<D, NW, false, true>), dim3(nchains), dim3(64 * NW), 0, stream, a);
+  } else {
+    constexpr int NW = 4, NVB = D / 64;
+    if (train)
+      hipLaunchKernelGGL((chan_scan_fwd_kernel<D, NW, true, false>), dim3(nchains * NVB), dim3(64 * NW), 0, stream, a);
+    else
+      hipLaunchKernelGGL((chan_scan_fwd_kernel<D, NW, false, false>), dim3(nchains * NVB), dim3(64 * NW), 0, stream, a);
+  }
+  return check_launch("chan_scan_fwd_kernel");
 }
 
 template <int D>
 static int launch_chan_bwd(const ChanBwdArgs& a, hipStream_t stream) {
   const int NC = (a.T + CC - 1) / CC;
-  hipLaunchKernelGGL((chan_bwd_scan_kernel<D>), dim3(a.B * a.H), dim3(64 * (D / 16)), 0, stream, a);
-  int rc = check_launch("chan_bwd_scan_kernel");
+  constexpr int NW = 4, NVB = D / 64;
+  hipLaunchKernelGGL((chan_scan_bwd_kernel<D, NW>), dim3(a.B * a.H * NVB), dim3(64 * NW), 0, stream, a);
+  int rc = check_launch("chan_scan_bwd_kernel");
   if (rc) return rc;
   hipLaunchKernelGGL((chan_grads_kernel<D>), dim3(a.B * a.H * NC), dim3(64 * (D / 16)), 0, stream, a);
   return check_launch("chan_grads_kernel");
@@ -666,7 +776,13 @@ int chan_bwd_dispatch(const ChanBwdArgs& a, hipStream_t stream) {
 
 size_t chan_states_bytes(int nchains, int T, int D) {
   const size_t NR = (size_t)nchains * ((T + CC - 1) / CC);
-  return NR * ((size_t)D * D + (size_t)CC * D) * 4;
+  const size_t rec = D == 128 ? ChRec<128>::FN + ChRec<128>::BN : ChRec<64>::FN + ChRec<64>::BN;
+  return NR * ((size_t)D * D + (size_t)CC * D + rec) * 4;
+}
+
+size_t chan_fwd_workspace_bytes(int nchains, int T, int D) {
+  const size_t NR = (size_t)nchains * ((T + CC - 1) / CC);
+  return NR * (size_t)(D == 128 ? ChRec<128>::FN : ChRec<64>::FN) * 4;
 }
 
 }  // namespace gdnx

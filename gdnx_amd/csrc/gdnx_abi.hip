@@ -457,17 +457,25 @@ extern "C" long long gdnx_delta_chan_states_bytes(int B, int T, int H, int head_
   return (long long)chan_states_bytes(B * H, T, head_dim);
 }
 
+extern "C" long long gdnx_delta_chan_fwd_workspace_bytes(int B, int T, int H, int head_dim) {
+  if (B < 1 || T < 0 || H < 1 || (head_dim != 64 && head_dim != 128)) return -1;
+  return (long long)chan_fwd_workspace_bytes(B * H, T, head_dim);
+}
+
 extern "C" int gdnx_delta_chan_fwd(const float* q, const float* k, const float* v, const float* beta_e,
                                    const float* beta_w, const float* log_g, const float* state0, float* y,
-                                   float* state_out, void* chunk_states, float* r_norm, int B, int T, int H,
-                                   int head_dim, void* stream) {
+                                   float* state_out, void* chunk_states, void* workspace, float* r_norm, int B,
+                                   int T, int H, int head_dim, void* stream) {
   int rc = chan_common(q, k, v, beta_e, log_g, B, T, H, head_dim);
   if (rc) return rc;
   if (!beta_w || !y) return set_error(GDNX_ERR_ARG, "beta_w and y must be non-null");
-  if (!aligned16(y) || (chunk_states && !aligned16(chunk_states)))
-    return set_error(GDNX_ERR_ARG, "y and chunk_states must be 16-byte aligned");
+  if (!chunk_states && !workspace)
+    return set_error(GDNX_ERR_WORKSPACE, "chunk_states (training) or workspace (inference) is required");
+  if (!aligned16(y) || (chunk_states && !aligned16(chunk_states)) || (workspace && !aligned16(workspace)))
+    return set_error(GDNX_ERR_ARG, "y, chunk_states and workspace must be 16-byte aligned");
   if (T == 0) return GDNX_OK;
-  ChanArgs a{q, k, v, beta_e, beta_w, log_g, state0, y, state_out, chunk_states, r_norm, B, T, H, head_dim};
+  ChanArgs a{q, k, v, beta_e, beta_w, log_g, state0, y, state_out, chunk_states, r_norm, B, T, H, head_dim,
+             workspace, nullptr, nullptr};
   return chan_fwd_dispatch(a, (hipStream_t)stream);
 }
 

@@ -69,6 +69,9 @@ struct ChanArgs {
   void* chunk_states;
   float* r_norm;
   int B, T, H, D;
+  void* workspace;     // forward operand records when chunk_states is null
+  float* frec;         // (set by the dispatcher) forward / backward operand records
+  float* brec;
 };
 
 struct ChanBwdArgs {
@@ -222,6 +225,7 @@ int gdn3_coeff_dispatch(const GCoeffArgs& a, bool bwd, hipStream_t stream);
 int chan_fwd_dispatch(const ChanArgs& a, hipStream_t stream);
 int chan_bwd_dispatch(const ChanBwdArgs& a, hipStream_t stream);
 size_t chan_states_bytes(int nchains, int T, int D);
+size_t chan_fwd_workspace_bytes(int nchains, int T, int D);
 int delta_chunk_size(int D, int dtype);
 int delta_train_chunk_size(int D, int dtype);
 

@@ -236,13 +236,16 @@ def delta_chan_fwd(q, k, v, beta_e, beta_w, log_g, state0=None, *, save_states=F
               "r_norm must be contiguous float32 [B,T,H]")
     y = torch.empty_like(q)
     s_out = torch.empty(B, H, D, D, dtype=torch.float32, device=q.device)
-    cs = None
+    cs = ws = None
     if save_states:
         cs = torch.empty(max(lib.gdnx_delta_chan_states_bytes(B, T, H, D), 16), dtype=torch.uint8, device=q.device)
+    else:
+        ws = torch.empty(max(lib.gdnx_delta_chan_fwd_workspace_bytes(B, T, H, D), 16), dtype=torch.uint8,
+                         device=q.device)
     with torch.cuda.device(q.device):
         rc = lib.gdnx_delta_chan_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(beta_e), _lib.ptr(beta_w),
                                      _lib.ptr(log_g), _lib.ptr(state0), _lib.ptr(y), _lib.ptr(s_out), _lib.ptr(cs),
-                                     _lib.ptr(r_norm), B, T, H, D, _lib.stream_of(q))
+                                     _lib.ptr(ws), _lib.ptr(r_norm), B, T, H, D, _lib.stream_of(q))
     _lib.check(rc, "gdnx_delta_chan_fwd")
     return y, s_out, cs
 

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 3
+#define GDNX_ABI_VERSION 4
 
 enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1 };
 
@@ -162,13 +162,16 @@ int gdnx_delta_decode_step(const void* q, const void* k, const void* v,
  *   state0, state_out, dstate_out, dstate0 [B, H, D, D] float32 (may be NULL)
  *   r_norm [B, T, H] float32 or NULL: |r_t| (the KMD-2 update score is
  *   |k_t| |r_t|)
- * chunk_states (forward, for the backward) and the backward's workspace are
- * gdnx_delta_chan_states_bytes bytes each. */
+ * chunk_states (forward, for the backward: state stash plus each chunk's
+ * operand records) and the backward's workspace are
+ * gdnx_delta_chan_states_bytes bytes each; a forward without chunk_states
+ * needs workspace (gdnx_delta_chan_fwd_workspace_bytes) for the records. */
 long long gdnx_delta_chan_states_bytes(int B, int T, int H, int head_dim);
+long long gdnx_delta_chan_fwd_workspace_bytes(int B, int T, int H, int head_dim);
 int gdnx_delta_chan_fwd(const float* q, const float* k, const float* v, const float* beta_e,
                         const float* beta_w, const float* log_g, const float* state0, float* y,
-                        float* state_out, void* chunk_states, float* r_norm, int B, int T, int H,
-                        int head_dim, void* stream);
+                        float* state_out, void* chunk_states, void* workspace, float* r_norm, int B,
+                        int T, int H, int head_dim, void* stream);
 /* Backward of gdnx_delta_chan_fwd; dlog_g is zero where the log-decay was
  * clamped. */
 int gdnx_delta_chan_bwd(const float* q, const float* k, const float* v, const float* beta_e,
