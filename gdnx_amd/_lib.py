@@ -35,6 +35,7 @@ SIGNATURES = {
     "gdnx_delta_chunk_bwd_state": (_c_int, [_vp] * 9 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_bwd_grads": (_c_int, [_vp] * 15 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_decode_step": (_c_int, [_vp] * 8 + [_c_int] * 5 + [_vp]),
+    "gdnx_delta_decode_step_slots": (_c_int, [_vp] * 9 + [_c_int] * 6 + [_vp]),
     "gdnx_gdn3_workspace_bytes": (_c_ll, [_c_int] * 6),
     "gdnx_gdn3_num_compactions": (_c_int, [_c_int] * 3),
     "gdnx_gdn3_chunk_fwd": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 10

@@ -1,4 +1,6 @@
-// One-token decode step of the decoupled-erase delta rule (gfx950).
+// One-token decode step of the decoupled-erase delta rule (gfx950), on a
+// contiguous state per row or on a state pool indexed by a slot per row (a
+// decode-state cache: sequences join and leave without moving states).
 //
 // The reference has no decode path (its layers swallow cache_params,
 // gdn3/gdn3_upgrade.py:725); the step is one iteration of the sequential
@@ -40,12 +42,21 @@ __global__ void __launch_bounds__(TH) delta_decode_kernel(DecodeArgs p) {
   const int chain = xcd_remap(blockIdx.x, nch);
   const int head = chain / p.M;                 // (seq, head) index
   const int cg = tid % CG, rg = tid / CG;
+  size_t sidx = chain;                          // this chain's state
+  if (p.slots) {                                // state pool: row s uses slot slots[s]
+    const int hm = p.H * p.M, sl = p.slots[chain / hm];
+    if (sl < 0 || sl >= p.nslots) {             // an empty row: zero output, no state touched
+      if (tid < D) ((IO*)p.y)[(size_t)chain * D + tid] = from_f<IO>(0.f);
+      return;
+    }
+    sidx = (size_t)sl * hm + chain % hm;
+  }
   const float ae = p.ae[chain], aw = p.aw[chain];
   const float gam = __expf(fmaxf(fminf(p.g[chain], 0.f), kLogFloor));
   const IO* kg = (const IO*)p.k + (size_t)head * D;
   const IO* qg = (const IO*)p.q + (size_t)head * D;
   const IO* vg = (const IO*)p.v + (size_t)head * D;
-  float* S = p.state + (size_t)chain * D * D;
+  float* S = p.state + sidx * D * D;
 
   // state loads first: they are the HBM stream
   f32x4 s[RPT];

@@ -194,7 +194,26 @@ extern "C" int gdnx_delta_decode_step(const void* q, const void* k, const void* 
   if (!q || !k || !v || !a_e || !a_w || !log_g || !state || !y)
     return set_error(GDNX_ERR_ARG, "all pointers must be non-null");
   if ((uintptr_t)state & 15u) return set_error(GDNX_ERR_ARG, "state must be 16-byte aligned");
-  DecodeArgs a{q, k, v, a_e, a_w, log_g, state, y, NS, H, M, head_dim, dtype};
+  DecodeArgs a{q, k, v, a_e, a_w, log_g, state, y, NS, H, M, head_dim, dtype, nullptr, 0};
+  return decode_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_delta_decode_step_slots(const void* q, const void* k, const void* v, const float* a_e,
+                                            const float* a_w, const float* log_g, float* state_pool,
+                                            const int* slots, void* y, int NS, int n_slots, int H, int M,
+                                            int head_dim, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16)
+    return set_error(GDNX_ERR_ARG, "dtype %d is not GDNX_DTYPE_F32/BF16", dtype);
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(GDNX_ERR_SHAPE, "head_dim %d unsupported (64 or 128)", head_dim);
+  if (NS < 1 || n_slots < 1 || H < 1 || M < 1 || (long long)NS * H * M > (1LL << 30) ||
+      (long long)n_slots * H * M > (1LL << 30))
+    return set_error(GDNX_ERR_SHAPE, "bad sizes NS=%d n_slots=%d H=%d M=%d", NS, n_slots, H, M);
+  if (!q || !k || !v || !a_e || !a_w || !log_g || !state_pool || !slots || !y)
+    return set_error(GDNX_ERR_ARG, "all pointers must be non-null");
+  if ((uintptr_t)state_pool & 15u) return set_error(GDNX_ERR_ARG, "state_pool must be 16-byte aligned");
+  DecodeArgs a{q, k, v, a_e, a_w, log_g, state_pool, y, NS, H, M, head_dim, dtype, slots, n_slots};
   return decode_dispatch(a, (hipStream_t)stream);
 }
 

@@ -110,6 +110,8 @@ struct DecodeArgs {
   float* state;
   void* y;
   int NS, H, M, D, dtype;
+  const int* slots;    // [NS] state-pool slot of each row, or null (row s uses state s)
+  int nslots;
 };
 
 // Kronecker-residual geometry: state S = sum_r A_r (x) B_r + U Vb^T with

@@ -210,6 +210,36 @@ def delta_decode_step(q, k, v, a_e, a_w, log_g, state, out=None):
     return y
 
 
+def delta_decode_step_slots(q, k, v, a_e, a_w, log_g, state_pool, slots, out=None):
+    """One-token decode step on a state pool (gdnx_delta_decode_step_slots):
+    row s of q, k, v [NS,H,D] and a_e, a_w, log_g [NS,H,M] updates
+    state_pool[slots[s]] ([n_slots,H,M,D,D] float32) in place; slots is an
+    int32 device tensor [NS] (a slot outside [0, n_slots) marks an empty row:
+    y = 0, no state touched).  Returns y [NS,H,M,D] in q's dtype."""
+    lib = _lib.load()
+    _need(q.is_cuda and q.dim() == 3 and q.shape == k.shape == v.shape, "q, k, v must be [NS,H,D] on GPU")
+    NS, H, D = q.shape
+    _need(a_e.dim() == 3 and tuple(a_e.shape[:2]) == (NS, H), "a_e must be [NS,H,M]")
+    M = a_e.shape[2]
+    _need(a_e.shape == a_w.shape == log_g.shape, "a_e, a_w, log_g must share shape")
+    _need(state_pool.dim() == 5 and tuple(state_pool.shape[1:]) == (H, M, D, D)
+          and state_pool.dtype == torch.float32, "state_pool must be fp32 [n_slots,H,M,D,D]")
+    _need(slots.dtype == torch.int32 and tuple(slots.shape) == (NS,) and slots.device == q.device,
+          "slots must be an int32 device tensor [NS]")
+    for t in (q, k, v, a_e, a_w, log_g, state_pool, slots):
+        _need(t.is_contiguous(), "inputs must be contiguous")
+    for t in (a_e, a_w, log_g):
+        _need(t.dtype == torch.float32, "a_e, a_w, log_g must be float32")
+    y = torch.empty(NS, H, M, D, dtype=q.dtype, device=q.device) if out is None else out
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_delta_decode_step_slots(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w),
+                                              _lib.ptr(log_g), _lib.ptr(state_pool), _lib.ptr(slots), _lib.ptr(y),
+                                              NS, state_pool.shape[0], H, M, D, _lib.dtype_code(q.dtype),
+                                              _lib.stream_of(q))
+    _lib.check(rc, "gdnx_delta_decode_step_slots")
+    return y
+
+
 # ---------------------------------------------------------------------------
 # per-key-channel decay (the general KMD-2 scan), float32, one chain per head
 # ---------------------------------------------------------------------------

@@ -148,6 +148,18 @@ int gdnx_delta_decode_step(const void* q, const void* k, const void* v,
                            float* state, void* y, int NS, int H, int M, int head_dim,
                            int dtype, void* stream);
 
+/* The same step on a decode-state cache: state_pool [n_slots, H, M, D, D]
+ * float32 holds one state per slot, and row s of the batch (q, k, v, the
+ * coefficients and y as above) updates slot slots[s] (int32 [NS], device
+ * memory).  A row whose slot lies outside [0, n_slots) is empty: its y is
+ * zero and no state is read or written.  No counterpart in the reference
+ * (it keeps no recurrent cache); for serving loops whose sequences join and
+ * leave the batch without moving their states.  Rows sharing a slot race. */
+int gdnx_delta_decode_step_slots(const void* q, const void* k, const void* v,
+                                 const float* a_e, const float* a_w, const float* log_g,
+                                 float* state_pool, const int* slots, void* y, int NS,
+                                 int n_slots, int H, int M, int head_dim, int dtype, void* stream);
+
 
 /* ---- Per-key-channel decay (the general KMD-2 scan) -----------------------
  * One chain per (batch, head), float32:  S <- diag(g_t) S (g per key
