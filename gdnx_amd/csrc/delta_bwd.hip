@@ -339,12 +339,17 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
       }
       // row sums (over the 16 columns j, lane 15 of each row) and column sums (over the 16 rows i)
       const int slot = isL ? 3 : 0;
+      float rx[4], ra[4];
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
-        const float rx = row_prefix16(xm[ii]), ra = row_prefix16(xa[ii]);
-        if (n16 == 15) {
-          lb.tri[pidx][slot][4 * g4 + ii] = rx;
-          if (isL) lb.tri[pidx][2][4 * g4 + ii] = ra;
+        rx[ii] = row_prefix16(xm[ii]);
+        ra[ii] = row_prefix16(xa[ii]);
+      }
+      if (n16 == 15) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          lb.tri[pidx][slot][4 * g4 + ii] = rx[ii];
+          if (isL) lb.tri[pidx][2][4 * g4 + ii] = ra[ii];
         }
       }
       float cx = (xm[0] + xm[1]) + (xm[2] + xm[3]);
@@ -384,30 +389,39 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
       }
       __builtin_amdgcn_sched_barrier(0);
     }
+    // per row tile: this lane's column of q, k, v, dB read first, then 16
+    // independent DPP row-sum chains, then one masked block of stores
 #pragma unroll
     for (int it = 0; it < NCT; ++it) {
+      float xq[4], xk[4], xv[4], xb[4];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii) {
+        const int i = it * 16 + 4 * g4 + ii;
+        xb[ii] = to_f(sm.u.ln.dB[i * LDD + dcol]);
+        xk[ii] = to_f(sm.k[i * LDD + dcol]);
+        xq[ii] = to_f(sm.q[i * LDD + dcol]);
+        xv[ii] = to_f(sm.v[i * LDD + dcol]);
+      }
       const f32x4 gi = *(const f32x4*)&lb.gam[it * 16 + 4 * g4];
       const f32x4 ei = *(const f32x4*)&lb.ae[it * 16 + 4 * g4];
       const f32x4 di = *(const f32x4*)&lb.dec[it * 16 + 4 * g4];
       const f32x4 wi = *(const f32x4*)&lb.aw[it * 16 + 4 * g4];
       dQacc[it] += gi * P1[it];
       dKacc[it] += di * P3[it] - ei * gi * P2[it];
+      float rsum[4][4];   // [ii][q.P1, k.P2, k.P3, v.dB]
 #pragma unroll
       for (int ii = 0; ii < 4; ++ii) {
-        const int i = it * 16 + 4 * g4 + ii;
-        const float dbv = to_f(sm.u.ln.dB[i * LDD + dcol]);
-        const float kv = to_f(sm.k[i * LDD + dcol]);
-        dVacc[it][ii] += wi[ii] * dbv;
-        const float s1 = row_prefix16(P1[it][ii] * to_f(sm.q[i * LDD + dcol]));
-        const float s2 = row_prefix16(P2[it][ii] * kv);
-        const float s3 = row_prefix16(P3[it][ii] * kv);
-        const float sw = row_prefix16(dbv * to_f(sm.v[i * LDD + dcol]));
-        if (n16 == 15) {
-          lb.red[i][0 * NW + wave] = s1;
-          lb.red[i][1 * NW + wave] = s2;
-          lb.red[i][2 * NW + wave] = s3;
-          lb.red[i][3 * NW + wave] = sw;
-        }
+        dVacc[it][ii] += wi[ii] * xb[ii];
+        rsum[ii][0] = row_prefix16(P1[it][ii] * xq[ii]);
+        rsum[ii][1] = row_prefix16(P2[it][ii] * xk[ii]);
+        rsum[ii][2] = row_prefix16(P3[it][ii] * xk[ii]);
+        rsum[ii][3] = row_prefix16(xb[ii] * xv[ii]);
+      }
+      if (n16 == 15) {
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+          for (int q4 = 0; q4 < 4; ++q4) lb.red[it * 16 + 4 * g4 + ii][q4 * NW + wave] = rsum[ii][q4];
       }
     }
     sdot = wave_sum(sdot);
