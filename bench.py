@@ -470,6 +470,177 @@ def bench_kmd2(args):
     print(json.dumps(line), flush=True)
 
 
+def boundary_bytes(B, T, H, M, K, V, io=2):
+    """Algorithmic HBM bytes per launch of the four boundary kernels: every
+    input read once and every output written once (per (b, t, h) row), plus
+    the RoPE tables (read once per launch: 2 M T K/2 float32) and norm."""
+    rows = B * T * H
+    f = 4
+    tables = 2 * M * T * (K // 2) * f
+    pro_f = rows * ((2 * K + M * K + M * V + 2 + 4 * M) * io + 2 * M * K * io + (M * K + M * V + M) * f) + tables
+    pro_b = rows * ((M * K + M * V + 2 + 4 * M) * io + (2 * M * K + M * K + M * V + M) * f
+                    + (2 * K + M * K + M * V + 2 + 4 * M) * f) + tables
+    epi_f = rows * ((M * V + M) * io + V * io) + V * f
+    epi_b = rows * ((M * V + M + V) * io + M * V * io + M * f) + V * f
+    return {"g3_prologue_fwd_kernel": pro_f, "g3_prologue_bwd_kernel": pro_b,
+            "g3_epilogue_fwd_kernel": epi_f, "g3_epilogue_bwd_kernel": epi_b}
+
+
+def boundary_inputs(B, T, H, M, K, V, seed=31):
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    xs = {"q": torch.randn(B, T, H, K, generator=g), "k": torch.randn(B, T, H, K, generator=g),
+          "b_proj": torch.randn(B, T, H, M, K, generator=g), "proj_a": torch.randn(B, T, H, generator=g),
+          "w_proj": torch.randn(B, T, H, M, V, generator=g), "proj_b": torch.randn(B, T, H, generator=g),
+          "decay_proj": torch.randn(B, T, H, M, 4, generator=g) * 3,
+          "y": torch.randn(B, T, H, M, V, generator=g), "router_logits": torch.randn(B, T, H, M, generator=g),
+          "norm": 0.5 + torch.rand(V, generator=g), "d_out": torch.randn(B, T, H, V, generator=g)}
+    return xs
+
+
+def cpu_baseline_boundary(T=4096, B=2, H=16, M=4, K=128, V=128):
+    """The float64 oracle (oracle/gdn3_layer.py, torch autograd, float64 as
+    it is written) on B=2, T=4096, H=16 -- half of the 262144 rows -- forward
+    and backward of prologue and epilogue, scaled to tokens/s."""
+    import torch
+    from oracle import gdn3_layer as gl
+    torch.set_num_threads(os.cpu_count() or 1)
+    xs = boundary_inputs(B, T, H, M, K, V, seed=32)
+    rates = torch.tensor([0.05, 0.02, 0.005, 0.001])
+    names = ("q", "k", "b_proj", "proj_a", "w_proj", "proj_b", "decay_proj")
+    t0 = time.perf_counter()
+    leaves = [xs[n].double().requires_grad_(True) for n in names]
+    outs = gl.prologue(*leaves, rates, 0.999)
+    torch.autograd.grad(outs, leaves, [torch.ones_like(o) for o in outs])
+    el = [xs[n].double().requires_grad_(True) for n in ("y", "router_logits", "norm")]
+    out = gl.epilogue(*el)
+    torch.autograd.grad(out, el, xs["d_out"].double())
+    sec = time.perf_counter() - t0
+    return {"value": B * T / sec, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle prologue+epilogue fwd+bwd, float64 autograd, B={B} T={T} H={H} M={M} K=V={K} "
+                      f"({B * T * H} rows), {sec:.2f} s"}
+
+
+def torch_eager_boundary(xs, rates, clamp, K, V):
+    """The reference's own element-wise ops (gdn3/gdn3_upgrade.py:796-851,
+    _apply_partial_rope with its clone and in-place slices) in torch eager on
+    the GPU, forward + backward: what the fused kernels replace."""
+    import math
+    import torch
+    import torch.nn.functional as F
+    from gdnx_amd import layer
+    q, k, bp, pa, wp, pb, dp = (xs[n] for n in ("q", "k", "b_proj", "proj_a", "w_proj", "proj_b", "decay_proj"))
+    B, T, H, M, _ = bp.shape
+    cos, sin = layer.lane_rope_tables(M, T, K, q.device)
+    pairs = layer.ops.gdn3_lane_rope_pairs(M, K)
+
+    def rope(x):
+        res = x.unsqueeze(3).expand(B, T, H, M, K).clone()
+        for m, d in enumerate(pairs):
+            if d == 0:
+                continue
+            lane = res[:, :, :, m, :]
+            c = cos[m, :, :d].view(1, T, 1, d)
+            s = sin[m, :, :d].view(1, T, 1, d)
+            x1, x2 = lane[..., :d], lane[..., d:2 * d]
+            lane[..., :d] = x1 * c - x2 * s
+            lane[..., d:2 * d] = x1 * s + x2 * c
+            res[:, :, :, m, :] = lane
+        return res
+    bg = torch.sigmoid(bp + pa.unsqueeze(3).unsqueeze(4) * 0.1)
+    wg = torch.sigmoid(wp + pb.unsqueeze(3).unsqueeze(4) * 0.1)
+    dec = torch.exp(-F.softplus(dp).clamp(max=5.0) * rates).mean(-1).clamp(max=clamp)
+    outs = (rope(q), rope(k), bg, wg, dec)
+    y, lg, nm = xs["y"], xs["router_logits"], xs["norm"]
+    w = F.softmax(lg, dim=-1)
+    routed = (w.unsqueeze(-1) * y).sum(dim=3)
+    out = F.normalize(routed, p=2, dim=-1, eps=1e-6) * math.sqrt(V) * nm
+    leaves = [xs[n] for n in ("q", "k", "b_proj", "proj_a", "w_proj", "proj_b", "decay_proj", "y",
+                              "router_logits", "norm")]
+    return torch.autograd.grad(list(outs) + [out], leaves, [torch.ones_like(o) for o in outs] + [xs["d_out"]])
+
+
+def bench_boundary(args):
+    """Fused GDN3 layer boundary (gdnx_gdn3_prologue_* / _epilogue_*) at the
+    layer shape of config 1: B=4, T=4096, H=16, M=4, K=V=128, bf16 IO.  One
+    step = prologue forward + epilogue forward + epilogue backward + prologue
+    backward on resident inputs; all four kernels are HBM-bound."""
+    import torch
+    from gdnx_amd import layer, ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, T, H, M, K, V = 4, 4096, 16, 4, 128, 128
+    io = torch.bfloat16
+    xs = {n: t.to(dev) for n, t in boundary_inputs(B, T, H, M, K, V).items()}
+    for n in ("q", "k", "b_proj", "proj_a", "w_proj", "proj_b", "decay_proj", "y", "router_logits", "d_out"):
+        xs[n] = xs[n].to(io).contiguous()
+    rates = torch.tensor([0.05, 0.02, 0.005, 0.001], device=dev)
+    cos, sin = layer.lane_rope_tables(M, T, K, dev)
+    pro_in = [xs[n] for n in ("q", "k", "b_proj", "proj_a", "w_proj", "proj_b", "decay_proj")]
+    go = [torch.randn(B, T, H, M, K, device=dev), torch.randn(B, T, H, M, K, device=dev),
+          torch.randn(B, T, H, M, K, device=dev), torch.randn(B, T, H, M, V, device=dev),
+          torch.randn(B, T, H, M, device=dev)]
+    stream = torch.cuda.current_stream()
+    calls = {
+        "g3_prologue_fwd_kernel": lambda: ops.gdn3_prologue_fwd(*pro_in, rates, cos, sin, 0.999),
+        "g3_epilogue_fwd_kernel": lambda: ops.gdn3_epilogue_fwd(xs["y"], xs["router_logits"], xs["norm"]),
+        "g3_epilogue_bwd_kernel": lambda: ops.gdn3_epilogue_bwd(xs["y"], xs["router_logits"], xs["norm"],
+                                                                xs["d_out"]),
+        "g3_prologue_bwd_kernel": lambda: ops.gdn3_prologue_bwd(*pro_in[2:], rates, cos, sin, *go, 0.999),
+    }
+
+    def timed(fn, n):
+        for _ in range(max(1, args.warmup)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / n
+
+    def step():
+        for fn in calls.values():
+            fn()
+    sec = timed(step, args.steps)
+    per = {n: timed(fn, args.kernel_iters) for n, fn in calls.items()}
+    nbytes = boundary_bytes(B, T, H, M, K, V)
+    dom = max(per, key=per.get)
+    achieved = nbytes[dom] / per[dom] / 1e9
+    # the same work as torch eager ops (the reference's path), for context
+    ex = {n: (t.detach().requires_grad_(True) if n != "d_out" else t) for n, t in xs.items()}
+    eager = timed(lambda: torch_eager_boundary(ex, rates, 0.999, K, V), max(2, args.steps // 4))
+    line = {
+        "metric": "GDN3 layer boundary pre/post-ops tokens/s fwd+bwd @B=4,T=4096,H=16,M=4",
+        "value": B * T / sec,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "GDN3LinearAttn.forward lines 796-851 around the recurrence: gates, braided "
+                               "decay, lane RoPE, routing + head norm; forward and backward",
+                   "batch": B, "seq_len": T, "heads": H, "lanes": M, "key_dim": K, "value_dim": V,
+                   "parallelism": "single GPU"},
+        "roofline": {"bound": "hbm", "kernel": dom, "achieved": achieved, "peak": HBM_PEAK / 1e9, "unit": "GB/s",
+                     "frac": achieved * 1e9 / HBM_PEAK, "traffic": measured_traffic(dom),
+                     "mean_us": per[dom] * 1e6, "algorithmic_bytes": nbytes[dom]},
+        "kernels": {n: {"us": round(per[n] * 1e6, 2), "GB/s": round(nbytes[n] / per[n] / 1e9, 1)} for n in per},
+        "torch_eager_ms_per_step": eager * 1e3,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_boundary()
+    print(json.dumps(line), flush=True)
+
+
 def bench_copy(args):
     """Calibration for the HBM traffic counters: a plain device copy of a
     known size (1 GiB read + 1 GiB written per launch).  Prints its own JSON
@@ -502,12 +673,13 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=10)
-    ap.add_argument("--workload", choices=("train", "decode", "longctx", "gdn3-layer", "gdn3-layer-train", "kmd2", "copy"),
+    ap.add_argument("--workload", choices=("train", "decode", "longctx", "gdn3-layer", "gdn3-layer-train", "kmd2",
+                                               "gdn3-boundary", "copy"),
                     default="train",
                     help="train: config 2 scan fwd+bwd (headline); decode: config 4 decode step; "
                          "longctx: config 3 GDN3 with compaction; gdn3-layer: GDN3 compaction every "
                          "16 tokens; gdn3-layer-train: the same forward + backward; kmd2: KMD-2 scan with per-channel decay fwd+bwd (reference scan "
-                         "benchmark, train shape); copy: 1 GiB device copy used to calibrate the HBM traffic counters")
+                         "benchmark, train shape); gdn3-boundary: the layer's fused pre-/post-ops fwd+bwd; copy: 1 GiB device copy used to calibrate the HBM traffic counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the recurrence shards by chains with no "
@@ -519,6 +691,8 @@ def main():
         return bench_copy(args)
     if args.workload == "kmd2":
         return bench_kmd2(args)
+    if args.workload == "gdn3-boundary":
+        return bench_boundary(args)
     if args.workload in ("longctx", "gdn3-layer", "gdn3-layer-train"):
         return bench_gdn3(args, layer_default=args.workload != "longctx", train=args.workload == "gdn3-layer-train")
 

@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(_HERE, "libgdnx.so")
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _c_int, _c_ll, _vp, _c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_float
 
@@ -51,6 +51,12 @@ SIGNATURES = {
     "gdnx_delta_chan_fwd": (_c_int, [_vp] * 12 + [_c_int] * 4 + [_vp]),
     "gdnx_delta_chan_bwd": (_c_int, [_vp] * 17 + [_c_int] * 4 + [_vp]),
     "gdnx_gdn3_coeff_bwd": (_c_int, [_vp] * 6 + [_c_int] * 6 + [_vp]),
+    "gdnx_gdn3_lane_rope_pairs": (_c_int, [_c_int, _c_int, _vp]),
+    "gdnx_gdn3_prologue_fwd": (_c_int, [_vp] * 15 + [_c_int] * 6 + [_c_float, _c_int, _vp]),
+    "gdnx_gdn3_prologue_bwd": (_c_int, [_vp] * 20 + [_c_int] * 6 + [_c_float, _c_int, _vp]),
+    "gdnx_gdn3_epilogue_fwd": (_c_int, [_vp] * 4 + [_c_int] * 6 + [_vp]),
+    "gdnx_gdn3_epilogue_workspace_bytes": (_c_ll, [_c_int] * 4),
+    "gdnx_gdn3_epilogue_bwd": (_c_int, [_vp] * 8 + [_c_int] * 6 + [_vp]),
 }
 
 

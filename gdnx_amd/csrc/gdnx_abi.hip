@@ -1,4 +1,5 @@
 // C-ABI entry points of libgdnx: argument validation, then dispatch.
+#include <initializer_list>
 #include <stdarg.h>
 #include <stdint.h>
 #include <stdio.h>
@@ -516,4 +517,121 @@ extern "C" int gdnx_delta_chan_bwd(const float* q, const float* k, const float* 
   ChanBwdArgs a{q, k, v, beta_e, beta_w, log_g, dy, dstate_out, chunk_states, workspace, dq, dk, dv,
                 dbeta_e, dbeta_w, dlog_g, dstate0, B, T, H, head_dim};
   return chan_bwd_dispatch(a, (hipStream_t)stream);
+}
+
+// ---------------------------------------------------------------------------
+// GDN3 layer boundary: fused pre-ops / post-ops
+// ---------------------------------------------------------------------------
+namespace gdnx {
+
+static int layer_sizes(int B, int T, int H, int M, int K, int V, int dtype, bool need_k) {
+  if (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16)
+    return set_error(GDNX_ERR_ARG, "dtype %d is not GDNX_DTYPE_F32/BF16", dtype);
+  if (B < 1 || T < 0 || H < 1 || M < 1 || M > 4)
+    return set_error(GDNX_ERR_SHAPE, "bad sizes B=%d T=%d H=%d M=%d (lanes 1..4)", B, T, H, M);
+  if (need_k && (K < 4 || K > 256 || K % 4))
+    return set_error(GDNX_ERR_SHAPE, "key_dim %d unsupported (multiple of 4, <= 256)", K);
+  if (V < 4 || V > 256 || V % 4) return set_error(GDNX_ERR_SHAPE, "value_dim %d unsupported (multiple of 4, <= 256)", V);
+  return GDNX_OK;
+}
+
+static bool all_aligned(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (!p || !aligned16(p)) return false;
+  return true;
+}
+
+}  // namespace gdnx
+
+extern "C" int gdnx_gdn3_lane_rope_pairs(int M, int key_dim, int* pairs) {
+  g_err[0] = 0;
+  if (M < 1 || M > 4 || key_dim < 1 || !pairs)
+    return set_error(GDNX_ERR_ARG, "need 1 <= M <= 4, key_dim >= 1 and a pairs array");
+  int p[4];
+  gdn3_lane_pairs(M, key_dim, p);
+  for (int m = 0; m < M; ++m) pairs[m] = p[m];
+  return GDNX_OK;
+}
+
+extern "C" int gdnx_gdn3_prologue_fwd(const void* q, const void* k, const void* b_proj, const void* proj_a,
+                                      const void* w_proj, const void* proj_b, const void* decay_proj,
+                                      const float* rates, const float* rope_cos, const float* rope_sin,
+                                      void* q_rope, void* k_rope, float* b_gates, float* w_gates, float* decay,
+                                      int B, int T, int H, int M, int key_dim, int value_dim, float decay_clamp,
+                                      int dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = layer_sizes(B, T, H, M, key_dim, value_dim, dtype, true);
+  if (rc != GDNX_OK) return rc;
+  if (!all_aligned({q, k, b_proj, w_proj, decay_proj, q_rope, k_rope, b_gates, w_gates}) || !proj_a ||
+      !proj_b || !rates || !rope_cos || !rope_sin || !decay)
+    return set_error(GDNX_ERR_ARG, "pointers must be non-null; tensors 16-byte aligned");
+  G3ProArgs a{};
+  a.q = q; a.k = k; a.bp = b_proj; a.pa = proj_a; a.wp = w_proj; a.pb = proj_b; a.dp = decay_proj;
+  a.rates = rates; a.cs = rope_cos; a.sn = rope_sin;
+  a.qr = q_rope; a.kr = k_rope; a.bg = b_gates; a.wg = w_gates; a.dec = decay;
+  a.rows = (long long)B * T * H;
+  a.T = T; a.H = H; a.M = M; a.K = key_dim; a.V = value_dim; a.clamp = decay_clamp;
+  gdn3_lane_pairs(M, key_dim, a.pairs);
+  return gdn3_prologue_dispatch(a, false, dtype, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_gdn3_prologue_bwd(const void* b_proj, const void* proj_a, const void* w_proj,
+                                      const void* proj_b, const void* decay_proj, const float* rates,
+                                      const float* rope_cos, const float* rope_sin, const float* d_q_rope,
+                                      const float* d_k_rope, const float* d_b_gates, const float* d_w_gates,
+                                      const float* d_decay, float* dq, float* dk, float* d_b_proj,
+                                      float* d_proj_a, float* d_w_proj, float* d_proj_b, float* d_decay_proj,
+                                      int B, int T, int H, int M, int key_dim, int value_dim, float decay_clamp,
+                                      int dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = layer_sizes(B, T, H, M, key_dim, value_dim, dtype, true);
+  if (rc != GDNX_OK) return rc;
+  if (!all_aligned({b_proj, w_proj, decay_proj, d_q_rope, d_k_rope, d_b_gates, d_w_gates, dq, dk, d_b_proj,
+                    d_w_proj, d_decay_proj}) ||
+      !proj_a || !proj_b || !rates || !rope_cos || !rope_sin || !d_decay || !d_proj_a || !d_proj_b)
+    return set_error(GDNX_ERR_ARG, "pointers must be non-null; tensors 16-byte aligned");
+  G3ProArgs a{};
+  a.bp = b_proj; a.pa = proj_a; a.wp = w_proj; a.pb = proj_b; a.dp = decay_proj;
+  a.rates = rates; a.cs = rope_cos; a.sn = rope_sin;
+  a.dqr = d_q_rope; a.dkr = d_k_rope; a.dbg = d_b_gates; a.dwg = d_w_gates; a.ddec = d_decay;
+  a.dq = dq; a.dk = dk; a.dbp = d_b_proj; a.dpa = d_proj_a; a.dwp = d_w_proj; a.dpb = d_proj_b;
+  a.ddp = d_decay_proj;
+  a.rows = (long long)B * T * H;
+  a.T = T; a.H = H; a.M = M; a.K = key_dim; a.V = value_dim; a.clamp = decay_clamp;
+  gdn3_lane_pairs(M, key_dim, a.pairs);
+  return gdn3_prologue_dispatch(a, true, dtype, (hipStream_t)stream);
+}
+
+extern "C" long long gdnx_gdn3_epilogue_workspace_bytes(int B, int T, int H, int value_dim) {
+  if (B < 1 || T < 0 || H < 1 || value_dim < 1) return -1;
+  return (long long)gdn3_epilogue_workspace_bytes((long long)B * T * H, value_dim);
+}
+
+extern "C" int gdnx_gdn3_epilogue_fwd(const void* y, const void* router_logits, const float* norm, void* out,
+                                      int B, int T, int H, int M, int value_dim, int dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = layer_sizes(B, T, H, M, 0, value_dim, dtype, false);
+  if (rc != GDNX_OK) return rc;
+  if (!all_aligned({y, out, norm}) || !router_logits)
+    return set_error(GDNX_ERR_ARG, "pointers must be non-null; y, norm and out 16-byte aligned");
+  G3EpiArgs a{};
+  a.y = y; a.lg = router_logits; a.norm = norm; a.out = out;
+  a.rows = (long long)B * T * H; a.M = M; a.V = value_dim;
+  return gdn3_epilogue_dispatch(a, false, dtype, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_gdn3_epilogue_bwd(const void* y, const void* router_logits, const float* norm,
+                                      const void* d_out, void* d_y, float* d_router_logits, float* d_norm,
+                                      void* workspace, int B, int T, int H, int M, int value_dim, int dtype,
+                                      void* stream) {
+  g_err[0] = 0;
+  int rc = layer_sizes(B, T, H, M, 0, value_dim, dtype, false);
+  if (rc != GDNX_OK) return rc;
+  if (!all_aligned({y, norm, d_out, d_y, workspace}) || !router_logits || !d_router_logits || !d_norm)
+    return set_error(GDNX_ERR_ARG, "pointers must be non-null; y, norm, d_out, d_y, workspace 16-byte aligned");
+  G3EpiArgs a{};
+  a.y = y; a.lg = router_logits; a.norm = norm; a.dout = d_out; a.dy = d_y; a.dlg = d_router_logits;
+  a.dnorm = d_norm; a.part = (float*)workspace;
+  a.rows = (long long)B * T * H; a.M = M; a.V = value_dim;
+  return gdn3_epilogue_dispatch(a, true, dtype, (hipStream_t)stream);
 }

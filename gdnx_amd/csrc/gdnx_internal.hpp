@@ -205,6 +205,54 @@ struct KronReadArgs {
   int N, C, D, P;
 };
 
+struct G3ProArgs {
+  const void* q;
+  const void* k;
+  const void* bp;   // [rows, M, K]
+  const void* pa;   // [rows]
+  const void* wp;   // [rows, M, V]
+  const void* pb;   // [rows]
+  const void* dp;   // [rows, M, 4]
+  const float* rates;
+  const float* cs;  // [M, T, K/2]
+  const float* sn;
+  void* qr;         // [rows, M, K]
+  void* kr;
+  float* bg;
+  float* wg;
+  float* dec;       // [rows, M]
+  const float* dqr; // backward inputs, float32, forward-output layouts
+  const float* dkr;
+  const float* dbg;
+  const float* dwg;
+  const float* ddec;
+  float* dq;        // backward outputs, float32, forward-input layouts
+  float* dk;
+  float* dbp;
+  float* dpa;
+  float* dwp;
+  float* dpb;
+  float* ddp;
+  long long rows;
+  int T, H, M, K, V;
+  int pairs[4];
+  float clamp;
+};
+
+struct G3EpiArgs {
+  const void* y;     // [rows, M, V]
+  const void* lg;    // [rows, M]
+  const float* norm; // [V]
+  void* out;         // [rows, V]
+  const void* dout;  // backward: [rows, V]
+  void* dy;          // [rows, M, V]
+  float* dlg;        // [rows, M]
+  float* part;       // [gridDim.x, V] partial d_norm
+  float* dnorm;      // [V]
+  long long rows;
+  int M, V;
+};
+
 int gdn3_fwd_dispatch(const G3FwdArgs& a, hipStream_t stream);
 size_t gdn3_workspace_bytes(int N, int D, int P, int dtype);
 size_t gdn3_train_states_bytes(int N, int T, int D, int P, int Kc);
@@ -224,6 +272,10 @@ inline size_t delta_stash_bytes(int nchains, int T, int D, int C, int dtype) {
 }
 int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream);
 int gdn3_coeff_dispatch(const GCoeffArgs& a, bool bwd, hipStream_t stream);
+void gdn3_lane_pairs(int M, int K, int pairs[4]);
+size_t gdn3_epilogue_workspace_bytes(long long rows, int V);
+int gdn3_prologue_dispatch(const G3ProArgs& a, bool bwd, int dtype, hipStream_t stream);
+int gdn3_epilogue_dispatch(const G3EpiArgs& a, bool bwd, int dtype, hipStream_t stream);
 int chan_fwd_dispatch(const ChanArgs& a, hipStream_t stream);
 int chan_bwd_dispatch(const ChanBwdArgs& a, hipStream_t stream);
 size_t chan_states_bytes(int nchains, int T, int D);

@@ -521,3 +521,121 @@ def gdn3_chunk_bwd(q, k, v, b_gates, w_gates, decay, dy, train_states, *, M, R=4
                                      _lib.dtype_code(q.dtype), _lib.stream_of(q))
     _lib.check(rc, "gdnx_gdn3_chunk_bwd")
     return dq, dk, dv, db, dw, ddec
+
+
+# ---------------------------------------------------------------------------
+# GDN3 layer boundary (gdnx_gdn3_prologue_* / gdnx_gdn3_epilogue_*)
+# ---------------------------------------------------------------------------
+def gdn3_lane_rope_pairs(M: int, key_dim: int):
+    """Lane RoPE pair counts d_m (0: identity lane), by the library's rule."""
+    import ctypes
+    lib = _lib.load()
+    out = (ctypes.c_int * 4)()
+    _lib.check(lib.gdnx_gdn3_lane_rope_pairs(M, key_dim, ctypes.cast(out, ctypes.c_void_p)),
+               "gdnx_gdn3_lane_rope_pairs")
+    return [out[m] for m in range(M)]
+
+
+def _row_io(t, shape, dt, name):
+    _need(tuple(t.shape) == tuple(shape), f"{name} must be {list(shape)}, got {list(t.shape)}")
+    return t.to(dt).contiguous()
+
+
+def gdn3_prologue_fwd(q, k, b_proj, proj_a, w_proj, proj_b, decay_proj, rates, rope_cos, rope_sin,
+                      decay_clamp=0.999):
+    """q, k [B,T,H,K] (bf16/float32; the other IO inputs are cast to it);
+    b_proj [B,T,H,M,K]; w_proj [B,T,H,M,V]; proj_a, proj_b [B,T,H];
+    decay_proj [B,T,H,M,4]; rates [4]; rope tables [M,T,K//2] float32.
+    Returns (q_rope, k_rope [B,T,H,M,K] in q's dtype, b_gates, w_gates,
+    decay float32)."""
+    lib = _lib.load()
+    _need(q.is_cuda and q.dim() == 4 and q.shape == k.shape, "q, k must be [B,T,H,K] on the GPU")
+    B, T, H, K = q.shape
+    _need(b_proj.dim() == 5, "b_proj must be [B,T,H,M,K]")
+    M, V = b_proj.shape[3], w_proj.shape[-1]
+    dt = q.dtype
+    q, k = q.contiguous(), k.to(dt).contiguous()
+    bp = _row_io(b_proj, (B, T, H, M, K), dt, "b_proj")
+    wp = _row_io(w_proj, (B, T, H, M, V), dt, "w_proj")
+    pa = _row_io(proj_a, (B, T, H), dt, "proj_a")
+    pb = _row_io(proj_b, (B, T, H), dt, "proj_b")
+    dp = _row_io(decay_proj, (B, T, H, M, 4), dt, "decay_proj")
+    rates = _row_io(rates, (4,), torch.float32, "rates")
+    _need(tuple(rope_cos.shape) == tuple(rope_sin.shape) == (M, T, K // 2) and rope_cos.dtype == torch.float32,
+          "rope tables must be float32 [M, T, K//2]")
+    qr = torch.empty(B, T, H, M, K, dtype=dt, device=q.device)
+    kr = torch.empty_like(qr)
+    bg = torch.empty(B, T, H, M, K, dtype=torch.float32, device=q.device)
+    wg = torch.empty(B, T, H, M, V, dtype=torch.float32, device=q.device)
+    dec = torch.empty(B, T, H, M, dtype=torch.float32, device=q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_gdn3_prologue_fwd(*map(_lib.ptr, (q, k, bp, pa, wp, pb, dp, rates, rope_cos.contiguous(),
+                                                        rope_sin.contiguous(), qr, kr, bg, wg, dec)),
+                                        B, T, H, M, K, V, float(decay_clamp), _lib.dtype_code(dt),
+                                        _lib.stream_of(q))
+    _lib.check(rc, "gdnx_gdn3_prologue_fwd")
+    return qr, kr, bg, wg, dec
+
+
+def gdn3_prologue_bwd(b_proj, proj_a, w_proj, proj_b, decay_proj, rates, rope_cos, rope_sin,
+                      d_q_rope, d_k_rope, d_b_gates, d_w_gates, d_decay, decay_clamp=0.999):
+    """Backward of gdn3_prologue_fwd; the IO inputs in the forward's compute
+    dtype.  Returns float32 (dq, dk [B,T,H,K], d_b_proj, d_proj_a, d_w_proj,
+    d_proj_b, d_decay_proj)."""
+    lib = _lib.load()
+    B, T, H, M, K = b_proj.shape
+    V = w_proj.shape[-1]
+    dev = b_proj.device
+    f32 = [t.float().contiguous() for t in (d_q_rope, d_k_rope, d_b_gates, d_w_gates, d_decay)]
+    _need(tuple(f32[0].shape) == tuple(f32[1].shape) == (B, T, H, M, K), "d_q_rope / d_k_rope must be [B,T,H,M,K]")
+    _need(tuple(f32[2].shape) == (B, T, H, M, K) and tuple(f32[3].shape) == (B, T, H, M, V)
+          and tuple(f32[4].shape) == (B, T, H, M), "bad gate / decay gradient shapes")
+    dq = torch.empty(B, T, H, K, dtype=torch.float32, device=dev)
+    dk = torch.empty_like(dq)
+    dbp = torch.empty(B, T, H, M, K, dtype=torch.float32, device=dev)
+    dwp = torch.empty(B, T, H, M, V, dtype=torch.float32, device=dev)
+    dpa = torch.empty(B, T, H, dtype=torch.float32, device=dev)
+    dpb = torch.empty_like(dpa)
+    ddp = torch.empty(B, T, H, M, 4, dtype=torch.float32, device=dev)
+    with torch.cuda.device(dev):
+        rc = lib.gdnx_gdn3_prologue_bwd(*map(_lib.ptr, (b_proj, proj_a, w_proj, proj_b, decay_proj, rates, rope_cos,
+                                                        rope_sin, *f32, dq, dk, dbp, dpa, dwp, dpb, ddp)),
+                                        B, T, H, M, K, V, float(decay_clamp), _lib.dtype_code(b_proj.dtype),
+                                        _lib.stream_of(b_proj))
+    _lib.check(rc, "gdnx_gdn3_prologue_bwd")
+    return dq, dk, dbp, dpa, dwp, dpb, ddp
+
+
+def gdn3_epilogue_fwd(y, router_logits, norm):
+    """y [B,T,H,M,V] (bf16/float32), router_logits [B,T,H,M], norm [V] ->
+    [B,T,H,V] in y's dtype."""
+    lib = _lib.load()
+    _need(y.is_cuda and y.dim() == 5, "y must be [B,T,H,M,V] on the GPU")
+    B, T, H, M, V = y.shape
+    y = y.contiguous()
+    lg = _row_io(router_logits, (B, T, H, M), y.dtype, "router_logits")
+    nm = _row_io(norm, (V,), torch.float32, "norm")
+    out = torch.empty(B, T, H, V, dtype=y.dtype, device=y.device)
+    with torch.cuda.device(y.device):
+        rc = lib.gdnx_gdn3_epilogue_fwd(_lib.ptr(y), _lib.ptr(lg), _lib.ptr(nm), _lib.ptr(out), B, T, H, M, V,
+                                        _lib.dtype_code(y.dtype), _lib.stream_of(y))
+    _lib.check(rc, "gdnx_gdn3_epilogue_fwd")
+    return out
+
+
+def gdn3_epilogue_bwd(y, router_logits, norm, d_out):
+    """Backward of gdn3_epilogue_fwd: (d_y [B,T,H,M,V] in y's dtype,
+    d_router_logits [B,T,H,M], d_norm [V] float32)."""
+    lib = _lib.load()
+    B, T, H, M, V = y.shape
+    dout = _row_io(d_out, (B, T, H, V), y.dtype, "d_out")
+    dy = torch.empty_like(y)
+    dlg = torch.empty(B, T, H, M, dtype=torch.float32, device=y.device)
+    dnm = torch.empty(V, dtype=torch.float32, device=y.device)
+    ws = torch.empty(max(lib.gdnx_gdn3_epilogue_workspace_bytes(B, T, H, V), 16), dtype=torch.uint8,
+                     device=y.device)
+    with torch.cuda.device(y.device):
+        rc = lib.gdnx_gdn3_epilogue_bwd(*map(_lib.ptr, (y, router_logits, norm, dout, dy, dlg, dnm, ws)),
+                                        B, T, H, M, V, _lib.dtype_code(y.dtype), _lib.stream_of(y))
+    _lib.check(rc, "gdnx_gdn3_epilogue_bwd")
+    return dy, dlg, dnm

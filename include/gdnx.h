@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 4
+#define GDNX_ABI_VERSION 5
 
 enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1 };
 
@@ -308,6 +308,73 @@ int gdnx_gdn3_compact(const float* A, const float* Bf, const float* U, const flo
 int gdnx_kron_read(const float* A, const float* Bf, const float* U, const float* Vb, const float* x,
                    float* y, int N, int C, int head_dim, int R, int P, int a_v, int a_k, int b_v,
                    int b_k, void* stream);
+
+/* ---- GDN3 layer boundary: the element-wise pre-ops and post-ops of
+ * GDN3LinearAttn.forward (gdn3/gdn3_upgrade.py:785-856), each direction one
+ * pass over HBM.  The reference runs them in line as torch ops (no function
+ * boundary); these entry points replace lines 796-828 (prologue) and 842-851
+ * (epilogue).  Rows are (b, t, h) in [B, T, H] order; IO tensors are in
+ * `dtype`, everything else float32.  Lanes M <= 4 (the reference's lane RoPE
+ * table lists four lanes, :181-182); key_dim and value_dim multiples of 4,
+ * <= 256. */
+
+/* Lane RoPE pairs d_m by the reference's rule (gdn3/gdn3_upgrade.py:342-376):
+ * d = floor(key_dim f_m / 2), f = (0.5, 0.25, 0.5, 0.5); 0 (identity) for a
+ * lane with scale 1 whose d exceeds floor(key_dim / 4) / 2.  Host only: fills
+ * pairs[0..M-1] in host memory. */
+int gdnx_gdn3_lane_rope_pairs(int M, int key_dim, int* pairs);
+
+/* Prologue (gdn3/gdn3_upgrade.py:796-828, lane RoPE :378-401):
+ *   b_gates = sigmoid(b_proj + 0.1 proj_a)        [B,T,H,M,key_dim]
+ *   w_gates = sigmoid(w_proj + 0.1 proj_b)        [B,T,H,M,value_dim]
+ *   decay   = min(mean_tau exp(-min(softplus(decay_proj), 5) rates[tau]), decay_clamp)   [B,T,H,M]
+ *   q_rope, k_rope [B,T,H,M,key_dim]: lane m of q, k [B,T,H,key_dim] with
+ *     x_i' = x_i c - x_{d+i} s,  x_{d+i}' = x_i' s + x_{d+i} c   (i < d_m)
+ *   where the second half reads the updated first half (rounded to dtype),
+ *   as the reference's in-place update does.
+ * proj_a, proj_b [B,T,H]; decay_proj [B,T,H,M,4]; rates [4] float32;
+ * rope_cos, rope_sin [M, T, key_dim/2] float32: lane m's angles at column
+ * i < d_m (the values of _lane_rope_factors; other columns unread). */
+int gdnx_gdn3_prologue_fwd(const void* q, const void* k, const void* b_proj, const void* proj_a,
+                           const void* w_proj, const void* proj_b, const void* decay_proj,
+                           const float* rates, const float* rope_cos, const float* rope_sin,
+                           void* q_rope, void* k_rope, float* b_gates, float* w_gates, float* decay,
+                           int B, int T, int H, int M, int key_dim, int value_dim, float decay_clamp,
+                           int dtype, void* stream);
+
+/* Prologue backward: from float32 gradients of the five outputs (forward
+ * output layouts) to float32 gradients of the inputs: dq, dk [B,T,H,key_dim]
+ * (summed over the lanes), d_b_proj, d_w_proj, d_decay_proj in their input
+ * layouts, d_proj_a, d_proj_b [B,T,H].  Clamps pass the gradient where their
+ * input is <= the bound (torch's convention). */
+int gdnx_gdn3_prologue_bwd(const void* b_proj, const void* proj_a, const void* w_proj,
+                           const void* proj_b, const void* decay_proj, const float* rates,
+                           const float* rope_cos, const float* rope_sin, const float* d_q_rope,
+                           const float* d_k_rope, const float* d_b_gates, const float* d_w_gates,
+                           const float* d_decay, float* dq, float* dk, float* d_b_proj,
+                           float* d_proj_a, float* d_w_proj, float* d_proj_b, float* d_decay_proj,
+                           int B, int T, int H, int M, int key_dim, int value_dim, float decay_clamp,
+                           int dtype, void* stream);
+
+/* Epilogue (gdn3/gdn3_upgrade.py:842-851): y [B,T,H,M,value_dim] (the
+ * recurrence output), router_logits [B,T,H,M] (dtype), norm [value_dim]
+ * float32 ->
+ *   out = u / max(|u|, 1e-6) * sqrt(value_dim) * norm,  u = sum_m softmax_m(logits) y_m
+ * [B,T,H,value_dim] in dtype (the tensor _agg_proj receives). */
+int gdnx_gdn3_epilogue_fwd(const void* y, const void* router_logits, const float* norm, void* out,
+                           int B, int T, int H, int M, int value_dim, int dtype, void* stream);
+
+/* Bytes of the epilogue backward's workspace (per-workgroup partial sums of
+ * d_norm, reduced in a fixed order: the result is deterministic). */
+long long gdnx_gdn3_epilogue_workspace_bytes(int B, int T, int H, int value_dim);
+
+/* Epilogue backward: d_out [B,T,H,value_dim] (dtype) -> d_y [B,T,H,M,value_dim]
+ * (dtype), d_router_logits [B,T,H,M] and d_norm [value_dim] (float32; d_norm
+ * is written, not accumulated). */
+int gdnx_gdn3_epilogue_bwd(const void* y, const void* router_logits, const float* norm,
+                           const void* d_out, void* d_y, float* d_router_logits, float* d_norm,
+                           void* workspace, int B, int T, int H, int M, int value_dim, int dtype,
+                           void* stream);
 
 #ifdef __cplusplus
 }

@@ -5,6 +5,7 @@ import os
 import re
 
 import pytest
+import torch
 
 from gdnx_amd import _lib
 
@@ -80,3 +81,47 @@ def test_backward_requires_stash_and_workspace():
     rc = lib.gdnx_delta_chunk_bwd(*ptrs, 1, 8, 1, 1, 64, 0, _lib.DTYPE_F32, None)
     assert rc == -3
     assert "workspace" in lib.gdnx_last_error().decode()
+
+
+@pytest.mark.parametrize("M,K", [(4, 128), (4, 64), (3, 96), (2, 8), (1, 4), (4, 256)])
+def test_lane_rope_pairs_follow_the_oracle_rule(M, K):
+    """The library's lane RoPE pairs (host-only call) equal the oracle's
+    restatement of _lane_rope_factors; identity lanes are 0."""
+    from gdnx_amd import ops
+    from oracle import gdn3_layer as gl
+    want = [0 if ident else d for d, _, _, ident in gl.lane_rope_params(M, K)]
+    assert ops.gdn3_lane_rope_pairs(M, K) == want
+
+
+def test_lane_rope_tables_match_the_oracle():
+    """The product's table builder (torch float32 ops, here on the CPU) equals
+    the oracle's tables bitwise."""
+    from gdnx_amd import layer
+    from oracle import gdn3_layer as gl
+    for M, T, K in ((4, 37, 128), (4, 9, 64)):
+        c1, s1 = layer.lane_rope_tables(M, T, K, "cpu")
+        c2, s2 = gl.lane_rope_tables(M, T, K)
+        for m, (d, _, _, ident) in enumerate(gl.lane_rope_params(M, K)):
+            if ident:
+                continue
+            assert torch.equal(c1[m, :, :d], c2[m, :, :d]) and torch.equal(s1[m, :, :d], s2[m, :, :d])
+
+
+def test_layer_boundary_entry_points_reject_bad_arguments():
+    lib = _lib.load()
+    vp = ctypes.c_void_p
+    p16 = [vp(16)] * 15
+    assert lib.gdnx_gdn3_prologue_fwd(*p16, 1, 4, 1, 5, 128, 128, 0.999, _lib.DTYPE_BF16, None) == -2
+    assert "lanes" in lib.gdnx_last_error().decode()
+    assert lib.gdnx_gdn3_prologue_fwd(*p16, 1, 4, 1, 4, 130, 128, 0.999, _lib.DTYPE_BF16, None) == -2
+    assert "key_dim" in lib.gdnx_last_error().decode()
+    bad = [vp(16)] * 2 + [vp(24)] + [vp(16)] * 12
+    assert lib.gdnx_gdn3_prologue_fwd(*bad, 1, 4, 1, 4, 128, 128, 0.999, _lib.DTYPE_BF16, None) == -1
+    assert lib.gdnx_gdn3_prologue_bwd(*([vp(16)] * 19 + [None]), 1, 4, 1, 4, 128, 128, 0.999,
+                                      _lib.DTYPE_F32, None) == -1
+    assert lib.gdnx_gdn3_epilogue_fwd(vp(16), vp(16), vp(16), vp(16), 1, 4, 1, 4, 130, 3, None) == -1
+    assert "dtype" in lib.gdnx_last_error().decode()
+    assert lib.gdnx_gdn3_epilogue_bwd(*([vp(16)] * 7 + [None]), 1, 4, 1, 4, 128, _lib.DTYPE_F32, None) == -1
+    assert lib.gdnx_gdn3_epilogue_workspace_bytes(4, 4096, 16, 128) == 2048 * 128 * 4
+    assert lib.gdnx_gdn3_epilogue_workspace_bytes(1, 3, 1, 128) == 1 * 128 * 4
+    assert lib.gdnx_gdn3_epilogue_workspace_bytes(1, 17, 1, 64) == 2 * 64 * 4
