@@ -641,6 +641,144 @@ def bench_boundary(args):
     print(json.dumps(line), flush=True)
 
 
+def rls_inputs(B, T, H, r, r_out, dk, dv, seed=41):
+    import torch
+    g = torch.Generator().manual_seed(seed)
+    q = torch.nn.functional.normalize(torch.randn(B, T, H, r_out, dk, generator=g), dim=-1)
+    K = torch.nn.functional.normalize(torch.randn(B, T, H, r, dk, generator=g), dim=-1)
+    V = torch.randn(B, T, H, r, dv, generator=g)
+    Bg = torch.sigmoid(torch.randn(B, T, H, r, dk, generator=g))
+    Wg = torch.sigmoid(torch.randn(B, T, H, r, dv, generator=g))
+    a = torch.sigmoid(torch.randn(B, T, H, dk, generator=g) * 0.5 + 6.0).clamp(max=0.999)
+    dy = torch.randn(B, T, H, dv, generator=g)
+    return [q, K, V, Bg, Wg, a], dy
+
+
+def flops_rls(B, T, H, r, r_out, dk, dv):
+    """Algorithmic FLOP of one forward: per token and chain, decay dv dk,
+    S Kt^T 2 r dv dk, erase + write 4 r dv dk, reads 2 r_out dv dk, plus the
+    T-factor (2 r^2 dk + r^3)."""
+    per = dv * dk * (1 + 2 * r + 4 * r + 2 * r_out) + 2 * r * r * dk + r ** 3
+    return B * T * H * per
+
+
+def cpu_baseline_rls(T=1024, B=1, H=16, r=1, r_out=1, dk=64, dv=64):
+    """The float64 oracle (oracle/rls.py, per-token torch loop with autograd)
+    on B=1, T=1024, H=16 -- 1/8 of the workload's tokens -- forward and
+    backward, scaled to tokens/s."""
+    import torch
+    from oracle import rls as orls
+    torch.set_num_threads(os.cpu_count() or 1)
+    xs, dy = rls_inputs(B, T, H, r, r_out, dk, dv, seed=42)
+    t0 = time.perf_counter()
+    leaves = [x.double().requires_grad_(True) for x in xs]
+    y = orls.rls_scan(*leaves)
+    torch.autograd.grad(y, leaves, dy.double())
+    sec = time.perf_counter() - t0
+    return {"value": B * T / sec, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"oracle rls_scan fwd+bwd, float64 autograd, B={B} T={T} H={H} r={r} dk=dv={dk}, {sec:.2f} s"}
+
+
+def torch_eager_rls(xs, eps):
+    """The reference's own per-token torch loop (KMD2LinearAttn._scan's r = 1
+    path, gdn3/kmd2.py:193-200) on the GPU, forward + backward."""
+    import torch
+    q, K, V, Bg, Wg, a = xs
+    B, T, H, _, dk = q.shape
+    dv = V.shape[-1]
+    N = B * H
+
+    def flat(x, *tail):
+        return x.permute(1, 0, 2, *range(3, x.dim())).reshape(T, N, *tail)
+    q_, K_, V_, Bg_, Wg_, a_ = flat(q, dk), flat(K, dk), flat(V, dv), flat(Bg, dk), flat(Wg, dv), flat(a, dk)
+    S = torch.zeros(N, dv, dk, device=q.device)
+    outs = []
+    for t in range(T):
+        S = S * a_[t].unsqueeze(1)
+        ktil = Bg_[t] * K_[t]
+        Sk = torch.bmm(S, ktil.unsqueeze(2)).squeeze(2)
+        denom = eps + ktil.square().sum(-1, keepdim=True)
+        S = S - torch.bmm((Sk / denom).unsqueeze(2), ktil.unsqueeze(1))
+        S = S + torch.bmm((Wg_[t] * V_[t]).unsqueeze(2), K_[t].unsqueeze(1))
+        outs.append(torch.bmm(S, q_[t].unsqueeze(2)).squeeze(2))
+    Y = torch.stack(outs, 0)
+    return torch.autograd.grad(Y.sum(), xs)
+
+
+def bench_rls(args):
+    """Rank-r RLS T-factor scan (KMD2LinearAttn._scan, gdn3/kmd2.py:166-214) at
+    the reference layer's defaults (H=16, dk=dv=64, r=1, r_out=1, eps 0.5) on
+    B=8 sequences of T=1024: one step = rls_scan forward + gradients of all
+    six inputs, float32."""
+    import torch
+    from gdnx_amd import rls
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    B, T, H, r, ro, dk, dv = 8, 1024, 16, 1, 1, 64, 64
+    xs, dy = rls_inputs(B, T, H, r, ro, dk, dv)
+    leaves = [x.to(dev).requires_grad_(True) for x in xs]
+    dy = dy.to(dev)
+    stream = torch.cuda.current_stream()
+
+    def timed(fn, n):
+        for _ in range(max(1, args.warmup)):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(n):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / n
+
+    def step():
+        y = rls.rls_scan(*leaves)
+        return torch.autograd.grad(y, leaves, dy)
+    sec = timed(step, args.steps)
+    flat = [x.detach().contiguous() for x in xs]
+    flat = [t.to(dev) for t in flat]
+    with torch.no_grad():
+        t_fwd = timed(lambda: rls.rls_fwd(*flat, checkpoint=True), args.kernel_iters)
+    f = flops_rls(B, T, H, r, ro, dk, dv)
+    t_bwd = max(sec - t_fwd, 1e-9)
+    kernels = {"rls_fwd_kernel": (t_fwd, f), "rls_bwd_kernel": (t_bwd, 3 * f)}
+    dom = max(kernels, key=lambda n: kernels[n][0])
+    achieved = kernels[dom][1] / kernels[dom][0] / 1e12
+    ex = [x.to(dev).requires_grad_(True) for x in xs]
+    Te = 256   # the eager loop is launch-bound: time a prefix and scale
+    exs = [x[:, :Te].detach().clone().requires_grad_(True) for x in ex]
+    eager = timed(lambda: torch_eager_rls(exs, 0.5), 2) * T / Te
+    line = {
+        "metric": "RLS T-factor scan tokens/s fwd+bwd @B=8,T=1024,H=16,dk=dv=64,r=1",
+        "value": B * T / sec,
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": sec * 1e3,
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32",
+        "data": "synthetic",
+        "config": {"workload": "KMD2LinearAttn._scan (rank-r block-Householder delta, RLS T-factor), reference "
+                               "layer defaults", "batch": B, "seq_len": T, "heads": H, "slots": r, "r_out": ro,
+                   "key_dim": dk, "value_dim": dv, "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": MFMA_FP32_PEAK / 1e12,
+                     "unit": "TFLOP/s", "frac": achieved * 1e12 / MFMA_FP32_PEAK, "traffic": measured_traffic(dom),
+                     "mean_us": kernels[dom][0] * 1e6, "algorithmic_flop": kernels[dom][1],
+                     "note": "sequential per-token recurrence, one workgroup per chain (128 chains): latency-bound; "
+                             "the backward's time is the step minus the forward"},
+        "kernels_us": {n: round(t * 1e6, 2) for n, (t, _) in kernels.items()},
+        "torch_eager_ms_per_step": eager * 1e3,
+    }
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline_rls()
+    print(json.dumps(line), flush=True)
+
+
 def bench_copy(args):
     """Calibration for the HBM traffic counters: a plain device copy of a
     known size (1 GiB read + 1 GiB written per launch).  Prints its own JSON
@@ -674,12 +812,12 @@ def main():
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--kernel-iters", type=int, default=10)
     ap.add_argument("--workload", choices=("train", "decode", "longctx", "gdn3-layer", "gdn3-layer-train", "kmd2",
-                                               "gdn3-boundary", "copy"),
+                                               "gdn3-boundary", "rls", "copy"),
                     default="train",
                     help="train: config 2 scan fwd+bwd (headline); decode: config 4 decode step; "
                          "longctx: config 3 GDN3 with compaction; gdn3-layer: GDN3 compaction every "
                          "16 tokens; gdn3-layer-train: the same forward + backward; kmd2: KMD-2 scan with per-channel decay fwd+bwd (reference scan "
-                         "benchmark, train shape); gdn3-boundary: the layer's fused pre-/post-ops fwd+bwd; copy: 1 GiB device copy used to calibrate the HBM traffic counters")
+                         "benchmark, train shape); gdn3-boundary: the layer's fused pre-/post-ops fwd+bwd; rls: the rank-r RLS T-factor scan fwd+bwd; copy: 1 GiB device copy used to calibrate the HBM traffic counters")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU only: the recurrence shards by chains with no "
@@ -693,6 +831,8 @@ def main():
         return bench_kmd2(args)
     if args.workload == "gdn3-boundary":
         return bench_boundary(args)
+    if args.workload == "rls":
+        return bench_rls(args)
     if args.workload in ("longctx", "gdn3-layer", "gdn3-layer-train"):
         return bench_gdn3(args, layer_default=args.workload != "longctx", train=args.workload == "gdn3-layer-train")
 

@@ -635,3 +635,69 @@ extern "C" int gdnx_gdn3_epilogue_bwd(const void* y, const void* router_logits, 
   a.rows = (long long)B * T * H; a.M = M; a.V = value_dim;
   return gdn3_epilogue_dispatch(a, true, dtype, (hipStream_t)stream);
 }
+
+// ---------------------------------------------------------------------------
+// Rank-r RLS T-factor scan
+// ---------------------------------------------------------------------------
+namespace gdnx {
+
+static int rls_sizes(int B, int T, int H, int R, int RO, int dk, int dv, float eps) {
+  if (B < 1 || T < 0 || H < 1) return set_error(GDNX_ERR_SHAPE, "bad sizes B=%d T=%d H=%d", B, T, H);
+  if (R < 1 || R > 4 || RO < 1 || RO > 4) return set_error(GDNX_ERR_SHAPE, "slots R=%d, R_out=%d (1..4)", R, RO);
+  if (dk != 32 && dk != 64 && dk != 128) return set_error(GDNX_ERR_SHAPE, "key_dim %d unsupported (32, 64, 128)", dk);
+  if (dv < 16 || dv > 128 || dv % 16) return set_error(GDNX_ERR_SHAPE, "value_dim %d unsupported (multiple of 16, <= 128)", dv);
+  if (!(eps > 0.0f)) return set_error(GDNX_ERR_ARG, "eps must be positive");
+  if ((long long)B * H > (1LL << 30)) return set_error(GDNX_ERR_SHAPE, "too many chains");
+  return GDNX_OK;
+}
+
+static bool aligned_or_null(std::initializer_list<const void*> ps) {
+  for (const void* p : ps)
+    if (p && !aligned16(p)) return false;
+  return true;
+}
+
+}  // namespace gdnx
+
+extern "C" long long gdnx_rls_ckpt_bytes(int B, int T, int H, int R, int key_dim, int value_dim) {
+  if (rls_sizes(B, T, H, R, 1, key_dim, value_dim, 1.0f) != GDNX_OK) return -1;
+  return (long long)rls_ckpt_bytes(B * H, T, R, key_dim, value_dim);
+}
+
+extern "C" int gdnx_rls_fwd(const float* q, const float* K, const float* V, const float* Bg, const float* Wg,
+                            const float* a, const float* out_mix, const float* state0, float* y, float* state_out,
+                            float* ckpt, int B, int T, int H, int R, int R_out, int key_dim, int value_dim,
+                            float eps, void* stream) {
+  g_err[0] = 0;
+  int rc = rls_sizes(B, T, H, R, R_out, key_dim, value_dim, eps);
+  if (rc != GDNX_OK) return rc;
+  if (!all_aligned({q, K, V, Bg, Wg, a, y}) || (R_out > 1 && !out_mix) ||
+      !aligned_or_null({state0, state_out, ckpt}))
+    return set_error(GDNX_ERR_ARG, "q, K, V, Bg, Wg, a, y (and out_mix when R_out > 1) must be non-null; "
+                                   "all tensors 16-byte aligned");
+  RlsDesc d{};
+  d.q = q; d.K = K; d.V = V; d.Bg = Bg; d.Wg = Wg; d.a = a; d.mix = out_mix; d.state0 = state0;
+  d.y = y; d.state_out = state_out; d.ckpt = ckpt;
+  d.B = B; d.T = T; d.H = H; d.R = R; d.RO = R_out; d.dk = key_dim; d.dv = value_dim; d.eps = eps;
+  return rls_dispatch(d, false, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_rls_bwd(const float* q, const float* K, const float* V, const float* Bg, const float* Wg,
+                            const float* a, const float* out_mix, const float* ckpt, const float* dy,
+                            const float* d_state, float* dq, float* dK, float* dV, float* dBg, float* dWg,
+                            float* da, float* d_out_mix_seq, float* d_state0, int B, int T, int H, int R,
+                            int R_out, int key_dim, int value_dim, float eps, void* stream) {
+  g_err[0] = 0;
+  int rc = rls_sizes(B, T, H, R, R_out, key_dim, value_dim, eps);
+  if (rc != GDNX_OK) return rc;
+  if (!ckpt) return set_error(GDNX_ERR_WORKSPACE, "the backward needs the forward's checkpoints (ckpt)");
+  if (!all_aligned({q, K, V, Bg, Wg, a, ckpt, dy, dq, dK, dV, dBg, dWg, da, d_out_mix_seq}) ||
+      (R_out > 1 && !out_mix) || !aligned_or_null({d_state, d_state0}))
+    return set_error(GDNX_ERR_ARG, "inputs, checkpoints and gradient outputs must be non-null and 16-byte aligned");
+  RlsDesc d{};
+  d.q = q; d.K = K; d.V = V; d.Bg = Bg; d.Wg = Wg; d.a = a; d.mix = out_mix; d.ckpt = const_cast<float*>(ckpt);
+  d.dy = dy; d.dstate = d_state; d.dq = dq; d.dK = dK; d.dV = dV; d.dBg = dBg; d.dWg = dWg; d.da = da;
+  d.dmix = d_out_mix_seq; d.dstate0 = d_state0;
+  d.B = B; d.T = T; d.H = H; d.R = R; d.RO = R_out; d.dk = key_dim; d.dv = value_dim; d.eps = eps;
+  return rls_dispatch(d, true, (hipStream_t)stream);
+}

@@ -272,6 +272,35 @@ inline size_t delta_stash_bytes(int nchains, int T, int D, int C, int dtype) {
 }
 int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream);
 int gdn3_coeff_dispatch(const GCoeffArgs& a, bool bwd, hipStream_t stream);
+// Rank-r RLS T-factor scan (rls.hip); all tensors float32
+struct RlsDesc {
+  const float* q;
+  const float* K;
+  const float* V;
+  const float* Bg;
+  const float* Wg;
+  const float* a;
+  const float* mix;
+  const float* state0;
+  const float* dy;
+  const float* dstate;
+  float* y;
+  float* state_out;
+  float* ckpt;
+  float* dq;
+  float* dK;
+  float* dV;
+  float* dBg;
+  float* dWg;
+  float* da;
+  float* dmix;
+  float* dstate0;
+  int B, T, H, R, RO, dk, dv;
+  float eps;
+};
+size_t rls_ckpt_bytes(int nchains, int T, int R, int dk, int dv);
+int rls_dispatch(const RlsDesc& d, bool bwd, hipStream_t stream);
+
 void gdn3_lane_pairs(int M, int K, int pairs[4]);
 size_t gdn3_epilogue_workspace_bytes(long long rows, int V);
 int gdn3_prologue_dispatch(const G3ProArgs& a, bool bwd, int dtype, hipStream_t stream);

@@ -1,0 +1,781 @@
+// Rank-r block-Householder delta rule with the RLS T-factor: the recurrence of
+// KMD2LinearAttn._scan (gdn3/kmd2.py:166-214) and of the testbed mixer
+// (research/testbed_mqar.py:226-262).  Per chain (b, h), state S [dv, dk]
+// (value-major, as the reference), per token with R write slots:
+//
+//   S  <- S diag(a)                          channel decay (key axis)
+//   Kt  = Bg * K                             [R, dk] gated erase keys
+//   S  <- S - (S Kt^T) (eps I + Kt Kt^T)^-1 Kt
+//   S  <- S + (Wg * V)^T K                   rank-R gated write
+//   y   = sum_o mix_o S q_o                  RO query slots
+//
+// The value rows of S evolve independently, so a workgroup holds one chain
+// with every lane owning 4 rows x CPL = dk/16 key columns; the 16 lanes of a
+// DPP row span the key axis, and all per-row dot products (S Kt^T, S q,
+// Kt Kt^T) are DPP reductions inside the row -- no barrier on the token
+// path.  Token inputs are staged per chunk of C tokens through LDS, the next
+// chunk's global loads in flight while the current one is scanned.
+//
+// Backward: the forward stores S every CK tokens; the reverse pass reloads a
+// checkpoint, recomputes the CK states in registers and runs the adjoint
+// token by token.  Per-row gradients (dV, dWg) are written directly; the
+// column gradients (dq, dK, dBg, da: sums over the value rows) are reduced
+// within the wave by lane swaps, across waves through LDS once per CK tokens,
+// in a fixed order (deterministic).
+#include "gdnx_common.hpp"
+#include "gdnx_internal.hpp"
+
+namespace gdnx {
+namespace {
+
+constexpr int kMaxPre = 4;    // staged float4 per thread per chunk
+
+__device__ __forceinline__ float row_sum16(float x) {
+  // rotations 8, 4, 2, 1 inside the DPP row: all 16 lanes form the same sums
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x122, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xf, 0xf, false));
+  return x;
+}
+
+// sum over the four DPP rows of the wave (lanes l, l^16, l^32, l^48)
+__device__ __forceinline__ float cross_rows4(float x) {
+  x += __shfl_xor(x, 16);
+  x += __shfl_xor(x, 32);
+  return x;
+}
+
+template <int N> __device__ __forceinline__ void lds_vec(const float* p, float* out) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int j = 0; j < N; j += 4) {
+      const f32x4 v = *(const f32x4*)(p + j);
+      out[j] = v[0];
+      out[j + 1] = v[1];
+      out[j + 2] = v[2];
+      out[j + 3] = v[3];
+    }
+  } else {
+#pragma unroll
+    for (int j = 0; j < N; ++j) out[j] = p[j];
+  }
+}
+
+// (eps I + G)^-1 for the SPD R x R matrix, Gauss-Jordan in registers
+template <int R> __device__ __forceinline__ void tfactor(const float G[R][R], float eps, float T[R][R]) {
+  if constexpr (R == 1) {
+    T[0][0] = 1.0f / (eps + G[0][0]);
+  } else {
+    float A[R][R];
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        A[i][j] = G[i][j] + (i == j ? eps : 0.0f);
+        T[i][j] = i == j ? 1.0f : 0.0f;
+      }
+#pragma unroll
+    for (int p = 0; p < R; ++p) {
+      const float inv = 1.0f / A[p][p];
+#pragma unroll
+      for (int j = 0; j < R; ++j) {
+        A[p][j] *= inv;
+        T[p][j] *= inv;
+      }
+#pragma unroll
+      for (int i = 0; i < R; ++i) {
+        if (i == p) continue;
+        const float f = A[i][p];
+#pragma unroll
+        for (int j = 0; j < R; ++j) {
+          A[i][j] -= f * A[p][j];
+          T[i][j] -= f * T[p][j];
+        }
+      }
+    }
+  }
+}
+
+struct RlsArgs {
+  const float* q;      // [B,T,H,RO,dk]
+  const float* K;      // [B,T,H,R,dk]
+  const float* V;      // [B,T,H,R,dv]
+  const float* Bg;     // [B,T,H,R,dk]
+  const float* Wg;     // [B,T,H,R,dv]
+  const float* a;      // [B,T,H,dk]
+  const float* mix;    // [H,RO] (RO > 1)
+  const float* state0; // [B,H,dv,dk] or null
+  const float* dy;     // [B,T,H,dv] (backward)
+  const float* dstate; // [B,H,dv,dk] gradient of the final state or null (backward)
+  float* y;            // [B,T,H,dv]
+  float* state_out;    // [B,H,dv,dk] or null
+  float* ckpt;         // [B*H, ceil(T/CK), dv, dk]
+  float* dq;
+  float* dK;
+  float* dV;
+  float* dBg;
+  float* dWg;
+  float* da;
+  float* dmix;         // [B*H, RO] per chain
+  float* dstate0;      // [B,H,dv,dk] or null
+  int B, T, H, RO, dk, dv, C, CK;
+  float eps;
+};
+
+// Token record layout in LDS (floats): K [R][dk], Bg [R][dk], a [dk],
+// q [RO][dk], V [R][dv], Wg [R][dv], (backward) dy [dv].
+struct RecLayout {
+  int oK, oBg, oA, oQ, oV, oW, oDy, stride;
+  __device__ RecLayout(int R, int RO, int dk, int dv, bool bwd) {
+    oK = 0;
+    oBg = R * dk;
+    oA = 2 * R * dk;
+    oQ = oA + dk;
+    oV = oQ + RO * dk;
+    oW = oV + R * dv;
+    oDy = oW + R * dv;
+    stride = oDy + (bwd ? dv : 0);
+  }
+};
+
+// Cooperative chunk staging: global -> registers (issued early) -> LDS.  The
+// first kMaxPre float4 per thread are prefetched while the previous chunk is
+// scanned; a chunk larger than that is completed synchronously at commit.
+struct Stager {
+  f32x4 pre[kMaxPre];
+  int chain, t0, ntok;
+  __device__ f32x4 load(const RlsArgs& g, const RecLayout& L, int R, int f, bool bwd) const {
+    const int b = chain / g.H, h = chain % g.H;
+    const int U = L.stride / 4;
+    const int lens[7] = {R * g.dk, R * g.dk, g.dk, g.RO * g.dk, R * g.dv, R * g.dv, bwd ? g.dv : 0};
+    const float* bases[7] = {g.K, g.Bg, g.a, g.q, g.V, g.Wg, g.dy};
+    const int tl = f / U;
+    int o = 4 * (f - tl * U);
+    int arr = 0;
+#pragma unroll
+    for (int z = 0; z < 6; ++z)
+      if (arr == z && o >= lens[z]) {
+        o -= lens[z];
+        arr = z + 1;
+      }
+    const float* base = bases[0];
+    int len = lens[0];
+#pragma unroll
+    for (int z = 1; z < 7; ++z)
+      if (arr == z) {
+        base = bases[z];
+        len = lens[z];
+      }
+    return *(const f32x4*)(base + (((size_t)b * g.T + t0 + tl) * g.H + h) * len + o);
+  }
+  __device__ void fetch(const RlsArgs& g, const RecLayout& L, int R, int ch, int t, int n, bool bwd) {
+    chain = ch;
+    t0 = t;
+    ntok = n;
+    const int U = L.stride / 4, nthr = blockDim.x;
+#pragma unroll
+    for (int k = 0; k < kMaxPre; ++k) {
+      const int f = threadIdx.x + k * nthr;
+      pre[k] = f < ntok * U ? load(g, L, R, f, bwd) : zero4();
+    }
+  }
+  __device__ void commit(float* buf, const RlsArgs& g, const RecLayout& L, int R, bool bwd) {
+    const int U = L.stride / 4, nthr = blockDim.x;
+#pragma unroll
+    for (int k = 0; k < kMaxPre; ++k) {
+      const int f = threadIdx.x + k * nthr;
+      if (f < ntok * U) *(f32x4*)(buf + 4 * f) = pre[k];
+    }
+    for (int f = threadIdx.x + kMaxPre * nthr; f < ntok * U; f += nthr) *(f32x4*)(buf + 4 * f) = load(g, L, R, f, bwd);
+  }
+};
+
+// Per-token operands of one lane, read from the staged record.
+template <int CPL, int R> struct TokIn {
+  float a[CPL], K[R][CPL], Kt[R][CPL], Bg[R][CPL];
+  float w[R][4];   // w' = Wg * V of the lane's 4 rows
+  float T[R][R];
+};
+
+template <int CPL, int R>
+__device__ __forceinline__ void load_tok(TokIn<CPL, R>& in, const float* rec, const RecLayout& L, int dk,
+                                         int dv, int l16, int rg, float eps) {
+  const int c0 = CPL * l16;
+  lds_vec<CPL>(rec + L.oA + c0, in.a);
+  float G[R][R];
+#pragma unroll
+  for (int s = 0; s < R; ++s) {
+    lds_vec<CPL>(rec + L.oK + s * dk + c0, in.K[s]);
+    lds_vec<CPL>(rec + L.oBg + s * dk + c0, in.Bg[s]);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) in.Kt[s][j] = in.Bg[s][j] * in.K[s][j];
+    float v4[4], g4[4];
+    lds_vec<4>(rec + L.oV + s * dv + 4 * rg, v4);
+    lds_vec<4>(rec + L.oW + s * dv + 4 * rg, g4);
+#pragma unroll
+    for (int i = 0; i < 4; ++i) in.w[s][i] = g4[i] * v4[i];
+  }
+#pragma unroll
+  for (int s = 0; s < R; ++s)
+#pragma unroll
+    for (int u = s; u < R; ++u) {
+      float x = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) x += in.Kt[s][j] * in.Kt[u][j];
+      G[s][u] = G[u][s] = row_sum16(x);
+    }
+  tfactor<R>(G, eps, in.T);
+}
+
+// One token of the recurrence on the lane's 4 x CPL block; returns p and z
+// (the erase projections) for the backward.
+template <int CPL, int R>
+__device__ __forceinline__ void token_step(float s[4][CPL], const TokIn<CPL, R>& in, float p[R][4], float z[R][4]) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) s[i][j] *= in.a[j];
+#pragma unroll
+  for (int u = 0; u < R; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) x += s[i][j] * in.Kt[u][j];
+      p[u][i] = row_sum16(x);
+    }
+#pragma unroll
+  for (int u = 0; u < R; ++u)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      float x = 0.0f;
+#pragma unroll
+      for (int v = 0; v < R; ++v) x += p[v][i] * in.T[v][u];
+      z[u][i] = x;
+    }
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      float x = s[i][j];
+#pragma unroll
+      for (int u = 0; u < R; ++u) x += in.w[u][i] * in.K[u][j] - z[u][i] * in.Kt[u][j];
+      s[i][j] = x;
+    }
+}
+
+template <int CPL, int R>
+__global__ __launch_bounds__(512) void rls_fwd_kernel(RlsArgs g) {
+  extern __shared__ float lds[];
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15;
+  const int rg = tid >> 4;   // row group: rows 4 rg .. 4 rg + 3
+  const int chain = blockIdx.x, h = chain % g.H;
+  const int dk = g.dk, dv = g.dv, T = g.T, C = g.C, RO = g.RO;
+  const RecLayout L(R, RO, dk, dv, false);
+  const int c0 = CPL * l16;
+  float mix[4];
+#pragma unroll
+  for (int o = 0; o < 4; ++o) mix[o] = o < RO ? (RO > 1 ? g.mix[h * RO + o] : 1.0f) : 0.0f;
+
+  float s[4][CPL];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      s[i][j] = g.state0 ? g.state0[((size_t)chain * dv + 4 * rg + i) * dk + c0 + j] : 0.0f;
+
+  const int nch = (T + C - 1) / C;
+  Stager st;
+  if (nch > 0) {
+    st.fetch(g, L, R, chain, 0, min(C, T), false);
+    st.commit(lds, g, L, R, false);
+  }
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    const int t0 = c * C, ntok = min(C, T - t0);
+    float* buf = lds + (c & 1) * C * L.stride;
+    if (c + 1 < nch) st.fetch(g, L, R, chain, t0 + C, min(C, T - t0 - C), false);
+    for (int tl = 0; tl < ntok; ++tl) {
+      const int t = t0 + tl;
+      if (g.ckpt && t % g.CK == 0) {
+        float* ck = g.ckpt + (((size_t)chain * ((T + g.CK - 1) / g.CK) + t / g.CK) * dv + 4 * rg) * dk + c0;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) ck[(size_t)i * dk + j] = s[i][j];
+      }
+      const float* rec = buf + tl * L.stride;
+      TokIn<CPL, R> in;
+      load_tok<CPL, R>(in, rec, L, dk, dv, l16, rg, g.eps);
+      float p[R][4], z[R][4];
+      token_step<CPL, R>(s, in, p, z);
+      float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+      for (int o = 0; o < 4; ++o) {
+        if (o < RO) {
+          float qv[CPL];
+          lds_vec<CPL>(rec + L.oQ + o * dk + c0, qv);
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            float x = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) x += s[i][j] * qv[j];
+            y[i] += mix[o] * row_sum16(x);
+          }
+        }
+      }
+      if (l16 == 0)
+        *(f32x4*)(g.y + (((size_t)(chain / g.H) * T + t) * g.H + h) * dv + 4 * rg) = (f32x4){y[0], y[1], y[2], y[3]};
+    }
+    if (c + 1 < nch) st.commit(lds + ((c + 1) & 1) * C * L.stride, g, L, R, false);
+    __syncthreads();
+  }
+  if (g.state_out) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) g.state_out[((size_t)chain * dv + 4 * rg + i) * dk + c0 + j] = s[i][j];
+  }
+}
+
+// Column partials of one token: g = sum_v dy s3 (dk), dK (R dk), dKt (R dk),
+// da (dk), then dT (R^2).
+__host__ __device__ constexpr int part_len(int R, int dk) { return (2 + 2 * R) * dk + R * R; }
+
+template <int CPL, int R, int CK>
+__global__ __launch_bounds__(512) void rls_bwd_kernel(RlsArgs g) {
+  extern __shared__ float lds[];
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, dr = lane >> 4, wave = tid >> 6;
+  const int rg = tid >> 4;
+  const int nw = blockDim.x >> 6;
+  const int chain = blockIdx.x, b = chain / g.H, h = chain % g.H;
+  const int dk = g.dk, dv = g.dv, T = g.T, C = g.C, RO = g.RO;
+  const RecLayout L(R, RO, dk, dv, true);
+  const int c0 = CPL * l16;
+  const int PL = part_len(R, dk);
+  float* red = lds + 2 * C * L.stride;        // [nw][CK][PL]
+  float* tsh = red + (size_t)nw * CK * PL;    // [CK][R*R] T-factors of the sub-chunk
+  float mix[4];
+#pragma unroll
+  for (int o = 0; o < 4; ++o) mix[o] = o < RO ? (RO > 1 ? g.mix[h * RO + o] : 1.0f) : 0.0f;
+  float dmix_acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  const int nck = (T + g.CK - 1) / g.CK;
+
+  float ds[4][CPL];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j)
+      ds[i][j] = g.dstate ? g.dstate[((size_t)chain * dv + 4 * rg + i) * dk + c0 + j] : 0.0f;
+
+  const int nch = (T + C - 1) / C;
+  // checkpoints are visited in decreasing order; the next one is in flight
+  // while a sub-chunk is processed
+  auto ck_ptr = [&](int k) { return g.ckpt + (((size_t)chain * nck + k) * dv + 4 * rg) * dk + c0; };
+  float ckn[4][CPL];
+  if (nck > 0) {
+    const float* ck = ck_ptr(nck - 1);
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) ckn[i][j] = ck[(size_t)i * dk + j];
+  }
+  Stager st;
+  if (nch > 0) {
+    const int t0 = (nch - 1) * C;
+    st.fetch(g, L, R, chain, t0, T - t0, true);
+    st.commit(lds + ((nch - 1) & 1) * C * L.stride, g, L, R, true);
+  }
+  __syncthreads();
+  for (int c = nch - 1; c >= 0; --c) {
+    const int t0 = c * C, ntok = min(C, T - t0);
+    const float* buf = lds + (c & 1) * C * L.stride;
+    if (c > 0) st.fetch(g, L, R, chain, t0 - C, C, true);
+    const int nsub = (ntok + CK - 1) / CK;
+    for (int sc = nsub - 1; sc >= 0; --sc) {
+      const int u0 = sc * CK, nu = min(CK, ntok - u0);   // tokens t0 + u0 .. + nu - 1
+      // ---- recompute the states before each token of the sub-chunk
+      float S0[CK][4][CPL];
+      {
+        const int k = (t0 + u0) / CK;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) S0[0][i][j] = ckn[i][j];
+        if (k > 0) {
+          const float* ck = ck_ptr(k - 1);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) ckn[i][j] = ck[(size_t)i * dk + j];
+        }
+      }
+#pragma unroll
+      for (int u = 1; u < CK; ++u) {
+        if (u < nu) {
+          TokIn<CPL, R> in;
+          load_tok<CPL, R>(in, buf + (u0 + u - 1) * L.stride, L, dk, dv, l16, rg, g.eps);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) S0[u][i][j] = S0[u - 1][i][j];
+          float p[R][4], z[R][4];
+          token_step<CPL, R>(S0[u], in, p, z);
+        }
+      }
+      // ---- adjoint, last token first
+#pragma unroll
+      for (int u = CK - 1; u >= 0; --u) {
+        if (u < nu) {
+          const float* rec = buf + (u0 + u) * L.stride;
+          const int t = t0 + u0 + u;
+          TokIn<CPL, R> in;
+          load_tok<CPL, R>(in, rec, L, dk, dv, l16, rg, g.eps);
+          float s1[4][CPL], s3[4][CPL];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) s3[i][j] = S0[u][i][j];
+          float p[R][4], z[R][4];
+          token_step<CPL, R>(s3, in, p, z);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) s1[i][j] = S0[u][i][j] * in.a[j];
+          // read: ds3 += sum_o mix_o dy q_o ; column partial gsum = sum_v dy s3
+          float dyv[4];
+          lds_vec<4>(rec + L.oDy + 4 * rg, dyv);
+          float gcol[CPL];
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            float x = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) x += dyv[i] * s3[i][j];
+            gcol[j] = x;
+          }
+#pragma unroll
+          for (int o = 0; o < 4; ++o) {
+            if (o < RO) {
+              float qv[CPL];
+              lds_vec<CPL>(rec + L.oQ + o * dk + c0, qv);
+#pragma unroll
+              for (int i = 0; i < 4; ++i)
+#pragma unroll
+                for (int j = 0; j < CPL; ++j) ds[i][j] += mix[o] * dyv[i] * qv[j];
+            }
+          }
+          // write: dw'_u = ds3 K_u (rows), column partial dK_u = sum_v w'_u ds3
+          float pK[R][CPL], pKt[R][CPL];
+#pragma unroll
+          for (int u2 = 0; u2 < R; ++u2) {
+            float dw[4];
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float x = 0.0f;
+#pragma unroll
+              for (int j = 0; j < CPL; ++j) x += ds[i][j] * in.K[u2][j];
+              dw[i] = row_sum16(x);
+            }
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+              float x = 0.0f;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) x += in.w[u2][i] * ds[i][j];
+              pK[u2][j] = x;
+            }
+            if (l16 == 0) {
+              float v4[4], g4[4];
+              lds_vec<4>(rec + L.oV + u2 * dv + 4 * rg, v4);
+              lds_vec<4>(rec + L.oW + u2 * dv + 4 * rg, g4);
+              const size_t o = ((((size_t)b * T + t) * g.H + h) * R + u2) * dv + 4 * rg;
+              *(f32x4*)(g.dV + o) = (f32x4){dw[0] * g4[0], dw[1] * g4[1], dw[2] * g4[2], dw[3] * g4[3]};
+              *(f32x4*)(g.dWg + o) = (f32x4){dw[0] * v4[0], dw[1] * v4[1], dw[2] * v4[2], dw[3] * v4[3]};
+            }
+          }
+          // erase: dz = -ds2 Kt^T (rows), dKt -= sum_v z ds2; dp = dz T; dT = p^T dz
+          float dz[R][4];
+#pragma unroll
+          for (int u2 = 0; u2 < R; ++u2)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float x = 0.0f;
+#pragma unroll
+              for (int j = 0; j < CPL; ++j) x += ds[i][j] * in.Kt[u2][j];
+              dz[u2][i] = -row_sum16(x);
+            }
+#pragma unroll
+          for (int u2 = 0; u2 < R; ++u2)
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+              float x = 0.0f;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) x += z[u2][i] * ds[i][j];
+              pKt[u2][j] = -x;
+            }
+          float dp[R][4];
+#pragma unroll
+          for (int u2 = 0; u2 < R; ++u2)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float x = 0.0f;
+#pragma unroll
+              for (int v = 0; v < R; ++v) x += dz[v][i] * in.T[u2][v];
+              dp[u2][i] = x;
+            }
+          float dT[R][R];
+#pragma unroll
+          for (int u2 = 0; u2 < R; ++u2)
+#pragma unroll
+            for (int v = 0; v < R; ++v) {
+              float x = 0.0f;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) x += p[u2][i] * dz[v][i];
+              dT[u2][v] = l16 == 0 ? x : 0.0f;   // p, dz are replicated over the DPP row
+            }
+          // ds1 = ds2 + dp Kt ; dKt += sum_v dp s1 ; da = sum_v ds1 s0 ; ds0 = ds1 a
+          float pa[CPL];
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+#pragma unroll
+            for (int u2 = 0; u2 < R; ++u2) {
+              float x = 0.0f;
+#pragma unroll
+              for (int i = 0; i < 4; ++i) x += dp[u2][i] * s1[i][j];
+              pKt[u2][j] += x;
+            }
+            float x = 0.0f;
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+              float d1 = ds[i][j];
+#pragma unroll
+              for (int u2 = 0; u2 < R; ++u2) d1 += dp[u2][i] * in.Kt[u2][j];
+              x += d1 * S0[u][i][j];
+              ds[i][j] = d1 * in.a[j];
+            }
+            pa[j] = x;
+          }
+          // wave partials of the column sums -> LDS
+          float* rp = red + ((size_t)wave * CK + u) * PL;
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            const float v0 = cross_rows4(gcol[j]);
+            const float v1 = cross_rows4(pa[j]);
+            if (dr == 0) {
+              rp[c0 + j] = v0;
+              rp[(1 + 2 * R) * dk + c0 + j] = v1;
+            }
+#pragma unroll
+            for (int u2 = 0; u2 < R; ++u2) {
+              const float w0 = cross_rows4(pK[u2][j]);
+              const float w1 = cross_rows4(pKt[u2][j]);
+              if (dr == 0) {
+                rp[(1 + u2) * dk + c0 + j] = w0;
+                rp[(1 + R + u2) * dk + c0 + j] = w1;
+              }
+            }
+          }
+#pragma unroll
+          for (int u2 = 0; u2 < R; ++u2)
+#pragma unroll
+            for (int v = 0; v < R; ++v) {
+              // dT summed over the lanes l16 == 0 of the wave's four DPP rows
+              const float x = cross_rows4(dT[u2][v]);
+              if (lane == 0) rp[(2 + 2 * R) * dk + u2 * R + v] = x;
+            }
+          if (tid == 0) {
+#pragma unroll
+            for (int u2 = 0; u2 < R; ++u2)
+#pragma unroll
+              for (int v = 0; v < R; ++v) tsh[u * R * R + u2 * R + v] = in.T[u2][v];
+          }
+        }
+      }
+      __syncthreads();
+      // ---- combine the waves' partials: per token and key column
+      for (int e = tid; e < nu * dk; e += blockDim.x) {
+        const int u = e / dk, col = e - u * dk;
+        const int t = t0 + u0 + u;
+        const float* rec = buf + (u0 + u) * L.stride;
+        float gs = 0.0f, pa = 0.0f, pK[R], pKt[R], dT[R][R];
+#pragma unroll
+        for (int u2 = 0; u2 < R; ++u2) pK[u2] = pKt[u2] = 0.0f;
+#pragma unroll
+        for (int u2 = 0; u2 < R; ++u2)
+#pragma unroll
+          for (int v = 0; v < R; ++v) dT[u2][v] = 0.0f;
+        for (int w = 0; w < nw; ++w) {
+          const float* rp = red + ((size_t)w * CK + u) * PL;
+          gs += rp[col];
+          pa += rp[(1 + 2 * R) * dk + col];
+#pragma unroll
+          for (int u2 = 0; u2 < R; ++u2) {
+            pK[u2] += rp[(1 + u2) * dk + col];
+            pKt[u2] += rp[(1 + R + u2) * dk + col];
+          }
+#pragma unroll
+          for (int u2 = 0; u2 < R; ++u2)
+#pragma unroll
+            for (int v = 0; v < R; ++v) dT[u2][v] += rp[(2 + 2 * R) * dk + u2 * R + v];
+        }
+        // dM = -T dT T (T symmetric); dKt += (dM + dM^T) Kt
+        float Tm[R][R], dM[R][R];
+#pragma unroll
+        for (int u2 = 0; u2 < R; ++u2)
+#pragma unroll
+          for (int v = 0; v < R; ++v) Tm[u2][v] = tsh[u * R * R + u2 * R + v];
+#pragma unroll
+        for (int u2 = 0; u2 < R; ++u2)
+#pragma unroll
+          for (int v = 0; v < R; ++v) {
+            float x = 0.0f;
+#pragma unroll
+            for (int m = 0; m < R; ++m)
+#pragma unroll
+              for (int n = 0; n < R; ++n) x += Tm[u2][m] * dT[m][n] * Tm[n][v];
+            dM[u2][v] = -x;
+          }
+        const size_t tok = ((size_t)b * T + t) * g.H + h;
+#pragma unroll
+        for (int u2 = 0; u2 < R; ++u2) {
+          float dkt = pKt[u2];
+#pragma unroll
+          for (int v = 0; v < R; ++v)
+            dkt += (dM[u2][v] + dM[v][u2]) * rec[L.oBg + v * dk + col] * rec[L.oK + v * dk + col];
+          const float kk = rec[L.oK + u2 * dk + col], bg = rec[L.oBg + u2 * dk + col];
+          g.dBg[(tok * R + u2) * dk + col] = dkt * kk;
+          g.dK[(tok * R + u2) * dk + col] = pK[u2] + dkt * bg;
+        }
+#pragma unroll
+        for (int o = 0; o < 4; ++o) {
+          if (o < RO) {
+            g.dq[(tok * RO + o) * dk + col] = mix[o] * gs;
+            dmix_acc[o] += rec[L.oQ + o * dk + col] * gs;
+          }
+        }
+        g.da[tok * dk + col] = pa;
+      }
+      __syncthreads();
+    }
+    if (c > 0) st.commit(lds + ((c - 1) & 1) * C * L.stride, g, L, R, true);
+    __syncthreads();
+  }
+  if (g.dstate0) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) g.dstate0[((size_t)chain * dv + 4 * rg + i) * dk + c0 + j] = ds[i][j];
+  }
+  // d out_mix of this chain: fixed-order block sum
+#pragma unroll
+  for (int o = 0; o < 4; ++o) {
+    if (o < RO) {
+      red[tid] = dmix_acc[o];
+      __syncthreads();
+      if (tid == 0) {
+        float x = 0.0f;
+        for (int k = 0; k < (int)blockDim.x; ++k) x += red[k];
+        g.dmix[(size_t)chain * RO + o] = x;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+
+// ---------------------------------------------------------------------------
+// host side
+// ---------------------------------------------------------------------------
+// checkpoint interval: the backward keeps CK states per lane in registers
+int rls_ck(int dk, int R) { return dk <= 32 && R <= 3 ? 4 : 2; }
+
+struct RlsGeom {
+  int C, CK, threads;
+  size_t lds;
+};
+
+static RlsGeom rls_geom(int R, int RO, int dk, int dv, bool bwd) {
+  RlsGeom G{};
+  G.CK = rls_ck(dk, R);
+  G.threads = 4 * dv;
+  const int stride = (2 * R + 1 + RO) * dk + 2 * R * dv + (bwd ? dv : 0);
+  const int nw = G.threads / 64;
+  const size_t red = bwd ? ((size_t)nw * G.CK * part_len(R, dk) + (size_t)G.CK * R * R) * 4 : 0;
+  const size_t budget = 156 * 1024;
+  // largest chunk that fits LDS, preferring one whose loads all prefetch
+  G.C = 0;
+  for (int pass = 0; pass < 2 && G.C == 0; ++pass)
+    for (int C = 32; C >= G.CK; C >>= 1) {
+      const size_t lds = (size_t)2 * C * stride * 4 + red;
+      if (lds <= budget && (pass == 1 || C * (stride / 4) <= kMaxPre * G.threads)) {
+        G.C = C;
+        G.lds = lds;
+        break;
+      }
+    }
+  return G;
+}
+
+template <int CPL, int R>
+static int launch_rls(const RlsArgs& a0, bool bwd, hipStream_t stream) {
+  const RlsGeom G = rls_geom(R, a0.RO, a0.dk, a0.dv, bwd);
+  if (G.C == 0) return set_error(GDNX_ERR_SHAPE, "RLS scan: R=%d, R_out=%d, key_dim=%d, value_dim=%d do not fit LDS",
+                                 R, a0.RO, a0.dk, a0.dv);
+  RlsArgs a = a0;
+  a.C = G.C;
+  a.CK = G.CK;
+  const unsigned nchains = (unsigned)(a.B * a.H);
+  if (!bwd) {
+    auto k = rls_fwd_kernel<CPL, R>;
+    if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)G.lds) != hipSuccess)
+      return set_error(GDNX_ERR_HIP, "rls_fwd_kernel: cannot reserve %zu bytes of LDS", G.lds);
+    hipLaunchKernelGGL(k, dim3(nchains), dim3(G.threads), G.lds, stream, a);
+    return check_launch("rls_fwd_kernel");
+  }
+  if (G.CK == 2) {
+    auto k = rls_bwd_kernel<CPL, R, 2>;
+    if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)G.lds) != hipSuccess)
+      return set_error(GDNX_ERR_HIP, "rls_bwd_kernel: cannot reserve %zu bytes of LDS", G.lds);
+    hipLaunchKernelGGL(k, dim3(nchains), dim3(G.threads), G.lds, stream, a);
+  } else {
+    auto k = rls_bwd_kernel<CPL, R, 4>;
+    if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)G.lds) != hipSuccess)
+      return set_error(GDNX_ERR_HIP, "rls_bwd_kernel: cannot reserve %zu bytes of LDS", G.lds);
+    hipLaunchKernelGGL(k, dim3(nchains), dim3(G.threads), G.lds, stream, a);
+  }
+  return check_launch("rls_bwd_kernel");
+}
+
+template <int CPL>
+static int launch_rls_r(const RlsArgs& a, int R, bool bwd, hipStream_t stream) {
+  switch (R) {
+    case 1: return launch_rls<CPL, 1>(a, bwd, stream);
+    case 2: return launch_rls<CPL, 2>(a, bwd, stream);
+    case 3: return launch_rls<CPL, 3>(a, bwd, stream);
+    default: return launch_rls<CPL, 4>(a, bwd, stream);
+  }
+}
+
+}  // namespace
+
+size_t rls_ckpt_bytes(int nchains, int T, int R, int dk, int dv) {
+  const int CK = rls_ck(dk, R);
+  return (size_t)nchains * ((T + CK - 1) / CK) * dv * dk * sizeof(float);
+}
+
+int rls_dispatch(const RlsDesc& d, bool bwd, hipStream_t stream) {
+  RlsArgs a{};
+  a.q = d.q; a.K = d.K; a.V = d.V; a.Bg = d.Bg; a.Wg = d.Wg; a.a = d.a; a.mix = d.mix;
+  a.state0 = d.state0; a.dy = d.dy; a.dstate = d.dstate; a.y = d.y; a.state_out = d.state_out;
+  a.ckpt = d.ckpt; a.dq = d.dq; a.dK = d.dK; a.dV = d.dV; a.dBg = d.dBg; a.dWg = d.dWg; a.da = d.da;
+  a.dmix = d.dmix; a.dstate0 = d.dstate0;
+  a.B = d.B; a.T = d.T; a.H = d.H; a.RO = d.RO; a.dk = d.dk; a.dv = d.dv; a.eps = d.eps;
+  if (d.T == 0) return GDNX_OK;
+  switch (d.dk) {
+    case 32: return launch_rls_r<2>(a, d.R, bwd, stream);
+    case 64: return launch_rls_r<4>(a, d.R, bwd, stream);
+    default: return launch_rls_r<8>(a, d.R, bwd, stream);
+  }
+}
+
+}  // namespace gdnx

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 5
+#define GDNX_ABI_VERSION 6
 
 enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1 };
 
@@ -375,6 +375,40 @@ int gdnx_gdn3_epilogue_bwd(const void* y, const void* router_logits, const float
                            const void* d_out, void* d_y, float* d_router_logits, float* d_norm,
                            void* workspace, int B, int T, int H, int M, int value_dim, int dtype,
                            void* stream);
+
+/* ---- Rank-r block-Householder delta rule with the RLS T-factor: the scan of
+ * KMD2LinearAttn._scan (gdn3/kmd2.py:166-214) and of the testbed mixer
+ * (research/testbed_mqar.py:226-262, without its compaction).  Per chain
+ * (b, h), state S [value_dim, key_dim] (value-major), per token, R slots:
+ *   S <- S diag(a);  Kt = Bg * K;  S <- S - (S Kt^T)(eps I + Kt Kt^T)^-1 Kt
+ *   S <- S + (Wg * V)^T K;  y = sum_o mix_o S q_o  (mix = out_mix[h], or 1 when R_out = 1)
+ * All tensors float32: q [B,T,H,R_out,key_dim]; K, Bg [B,T,H,R,key_dim];
+ * V, Wg [B,T,H,R,value_dim]; a [B,T,H,key_dim]; out_mix [H,R_out];
+ * states [B,H,value_dim,key_dim]; y [B,T,H,value_dim].  key_dim 32, 64 or 128;
+ * value_dim a multiple of 16 up to 128; R, R_out 1..4 (callers zero-pad
+ * other dims: zero key / value columns and a = 1 leave the scan unchanged). */
+
+/* Bytes of the state checkpoints the backward needs (one state every few
+ * tokens per chain). */
+long long gdnx_rls_ckpt_bytes(int B, int T, int H, int R, int key_dim, int value_dim);
+
+/* Forward.  state0 (initial state), state_out (final state) and ckpt (the
+ * backward's checkpoints, gdnx_rls_ckpt_bytes) may be NULL. */
+int gdnx_rls_fwd(const float* q, const float* K, const float* V, const float* Bg, const float* Wg,
+                 const float* a, const float* out_mix, const float* state0, float* y, float* state_out,
+                 float* ckpt, int B, int T, int H, int R, int R_out, int key_dim, int value_dim,
+                 float eps, void* stream);
+
+/* Backward from dy [B,T,H,value_dim] (and d_state, the gradient of the final
+ * state, or NULL) through the forward's checkpoints: gradients of every
+ * input in its layout; d_out_mix_seq [B,H,R_out] holds each sequence's share
+ * of out_mix's gradient (sum it over B); d_state0 (or NULL) the initial
+ * state's.  Deterministic. */
+int gdnx_rls_bwd(const float* q, const float* K, const float* V, const float* Bg, const float* Wg,
+                 const float* a, const float* out_mix, const float* ckpt, const float* dy,
+                 const float* d_state, float* dq, float* dK, float* dV, float* dBg, float* dWg,
+                 float* da, float* d_out_mix_seq, float* d_state0, int B, int T, int H, int R,
+                 int R_out, int key_dim, int value_dim, float eps, void* stream);
 
 #ifdef __cplusplus
 }
