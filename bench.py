@@ -746,6 +746,16 @@ def bench_rls(args):
     kernels = {"rls_fwd_kernel": (t_fwd, f), "rls_bwd_kernel": (t_bwd, 3 * f)}
     dom = max(kernels, key=lambda n: kernels[n][0])
     achieved = kernels[dom][1] / kernels[dom][0] / 1e12
+    # the testbed mixer's shape with its SVD compaction (research/testbed_mqar.py:75-78 defaults
+    # H=4, dk=dv=32, r=4; compaction every 32 tokens to rank 8)
+    xt, dyt = rls_inputs(16, 512, 4, 4, 1, 32, 32, seed=43)
+    lt = [x.to(dev).requires_grad_(True) for x in xt]
+    dyt = dyt.to(dev)
+
+    def step_tb():
+        y = rls.rls_scan(*lt, compact_P=32, compact_R=8)
+        return torch.autograd.grad(y, lt, dyt)
+    sec_tb = timed(step_tb, args.steps)
     ex = [x.to(dev).requires_grad_(True) for x in xs]
     Te = 256   # the eager loop is launch-bound: time a prefix and scale
     exs = [x[:, :Te].detach().clone().requires_grad_(True) for x in ex]
@@ -773,6 +783,8 @@ def bench_rls(args):
                              "the backward's time is the step minus the forward"},
         "kernels_us": {n: round(t * 1e6, 2) for n, (t, _) in kernels.items()},
         "torch_eager_ms_per_step": eager * 1e3,
+        "testbed_compaction": {"shape": "B=16 T=512 H=4 r=4 dk=dv=32, SVD compaction every 32 tokens to rank 8",
+                               "tokens_per_s": 16 * 512 / sec_tb, "ms_per_step": sec_tb * 1e3},
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_rls()

@@ -5,6 +5,6 @@ with ctypes and wrapped as torch.autograd.Functions that keep the reference's
 call signatures.  There is no CPU or Triton fallback: ops raise if the HIP
 library is not built.
 """
-from . import _lib, gdn3, kmd2, layer, ops  # noqa: F401
+from . import _lib, gdn3, kmd2, layer, ops, rls  # noqa: F401
 
-__all__ = ["ops", "gdn3", "kmd2", "layer"]
+__all__ = ["ops", "gdn3", "kmd2", "layer", "rls"]

@@ -57,9 +57,9 @@ SIGNATURES = {
     "gdnx_gdn3_epilogue_fwd": (_c_int, [_vp] * 4 + [_c_int] * 6 + [_vp]),
     "gdnx_gdn3_epilogue_workspace_bytes": (_c_ll, [_c_int] * 4),
     "gdnx_gdn3_epilogue_bwd": (_c_int, [_vp] * 8 + [_c_int] * 6 + [_vp]),
-    "gdnx_rls_ckpt_bytes": (_c_ll, [_c_int] * 6),
-    "gdnx_rls_fwd": (_c_int, [_vp] * 11 + [_c_int] * 7 + [_c_float, _vp]),
-    "gdnx_rls_bwd": (_c_int, [_vp] * 18 + [_c_int] * 7 + [_c_float, _vp]),
+    "gdnx_rls_ckpt_bytes": (_c_ll, [_c_int] * 7),
+    "gdnx_rls_fwd": (_c_int, [_vp] * 11 + [_c_int] * 7 + [_c_float, _c_int, _c_int, _c_float, _vp]),
+    "gdnx_rls_bwd": (_c_int, [_vp] * 18 + [_c_int] * 7 + [_c_float, _c_int, _c_int, _c_float, _c_int, _vp]),
 }
 
 

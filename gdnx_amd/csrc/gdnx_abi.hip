@@ -651,6 +651,17 @@ static int rls_sizes(int B, int T, int H, int R, int RO, int dk, int dv, float e
   return GDNX_OK;
 }
 
+static int rls_compact_args(int dk, int dv, int cP, int cR, float sd) {
+  if (cP == 0) return GDNX_OK;
+  if (cP < 0 || cP % 2) return set_error(GDNX_ERR_ARG, "compact_P=%d must be 0 or a positive even count", cP);
+  const int m = dv < dk ? dv : dk;
+  if (m > 64 || dk * dv > 4096)
+    return set_error(GDNX_ERR_SHAPE, "compaction needs min(key_dim, value_dim) <= 64 and key_dim*value_dim <= 4096");
+  if (cR < 1 || cR > m) return set_error(GDNX_ERR_ARG, "compact_R=%d must be in 1..%d", cR, m);
+  if (!(sd >= 0.0f && sd <= 1.0f)) return set_error(GDNX_ERR_ARG, "slow_decay must be in [0, 1]");
+  return GDNX_OK;
+}
+
 static bool aligned_or_null(std::initializer_list<const void*> ps) {
   for (const void* p : ps)
     if (p && !aligned16(p)) return false;
@@ -659,17 +670,19 @@ static bool aligned_or_null(std::initializer_list<const void*> ps) {
 
 }  // namespace gdnx
 
-extern "C" long long gdnx_rls_ckpt_bytes(int B, int T, int H, int R, int key_dim, int value_dim) {
+extern "C" long long gdnx_rls_ckpt_bytes(int B, int T, int H, int R, int key_dim, int value_dim, int compact_P) {
   if (rls_sizes(B, T, H, R, 1, key_dim, value_dim, 1.0f) != GDNX_OK) return -1;
-  return (long long)rls_ckpt_bytes(B * H, T, R, key_dim, value_dim);
+  if (compact_P < 0 || compact_P % 2) return -1;
+  return (long long)rls_ckpt_bytes(B * H, T, R, key_dim, value_dim, compact_P);
 }
 
 extern "C" int gdnx_rls_fwd(const float* q, const float* K, const float* V, const float* Bg, const float* Wg,
                             const float* a, const float* out_mix, const float* state0, float* y, float* state_out,
                             float* ckpt, int B, int T, int H, int R, int R_out, int key_dim, int value_dim,
-                            float eps, void* stream) {
+                            float eps, int compact_P, int compact_R, float slow_decay, void* stream) {
   g_err[0] = 0;
   int rc = rls_sizes(B, T, H, R, R_out, key_dim, value_dim, eps);
+  if (rc == GDNX_OK) rc = rls_compact_args(key_dim, value_dim, compact_P, compact_R, slow_decay);
   if (rc != GDNX_OK) return rc;
   if (!all_aligned({q, K, V, Bg, Wg, a, y}) || (R_out > 1 && !out_mix) ||
       !aligned_or_null({state0, state_out, ckpt}))
@@ -679,6 +692,7 @@ extern "C" int gdnx_rls_fwd(const float* q, const float* K, const float* V, cons
   d.q = q; d.K = K; d.V = V; d.Bg = Bg; d.Wg = Wg; d.a = a; d.mix = out_mix; d.state0 = state0;
   d.y = y; d.state_out = state_out; d.ckpt = ckpt;
   d.B = B; d.T = T; d.H = H; d.R = R; d.RO = R_out; d.dk = key_dim; d.dv = value_dim; d.eps = eps;
+  d.cP = compact_P; d.cR = compact_R; d.cs = slow_decay;
   return rls_dispatch(d, false, (hipStream_t)stream);
 }
 
@@ -686,9 +700,11 @@ extern "C" int gdnx_rls_bwd(const float* q, const float* K, const float* V, cons
                             const float* a, const float* out_mix, const float* ckpt, const float* dy,
                             const float* d_state, float* dq, float* dK, float* dV, float* dBg, float* dWg,
                             float* da, float* d_out_mix_seq, float* d_state0, int B, int T, int H, int R,
-                            int R_out, int key_dim, int value_dim, float eps, void* stream) {
+                            int R_out, int key_dim, int value_dim, float eps, int compact_P, int compact_R,
+                            float slow_decay, int straight_through, void* stream) {
   g_err[0] = 0;
   int rc = rls_sizes(B, T, H, R, R_out, key_dim, value_dim, eps);
+  if (rc == GDNX_OK) rc = rls_compact_args(key_dim, value_dim, compact_P, compact_R, slow_decay);
   if (rc != GDNX_OK) return rc;
   if (!ckpt) return set_error(GDNX_ERR_WORKSPACE, "the backward needs the forward's checkpoints (ckpt)");
   if (!all_aligned({q, K, V, Bg, Wg, a, ckpt, dy, dq, dK, dV, dBg, dWg, da, d_out_mix_seq}) ||
@@ -699,5 +715,6 @@ extern "C" int gdnx_rls_bwd(const float* q, const float* K, const float* V, cons
   d.dy = dy; d.dstate = d_state; d.dq = dq; d.dK = dK; d.dV = dV; d.dBg = dBg; d.dWg = dWg; d.da = da;
   d.dmix = d_out_mix_seq; d.dstate0 = d_state0;
   d.B = B; d.T = T; d.H = H; d.R = R; d.RO = R_out; d.dk = key_dim; d.dv = value_dim; d.eps = eps;
+  d.cP = compact_P; d.cR = compact_R; d.cs = slow_decay; d.ste = straight_through != 0;
   return rls_dispatch(d, true, (hipStream_t)stream);
 }

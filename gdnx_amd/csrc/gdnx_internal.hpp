@@ -297,8 +297,10 @@ struct RlsDesc {
   float* dstate0;
   int B, T, H, R, RO, dk, dv;
   float eps;
+  int cP, cR, ste;   // testbed compaction (cP = 0: off)
+  float cs;
 };
-size_t rls_ckpt_bytes(int nchains, int T, int R, int dk, int dv);
+size_t rls_ckpt_bytes(int nchains, int T, int R, int dk, int dv, int cP);
 int rls_dispatch(const RlsDesc& d, bool bwd, hipStream_t stream);
 
 void gdn3_lane_pairs(int M, int K, int pairs[4]);

@@ -121,6 +121,8 @@ struct RlsArgs {
   float* dstate0;      // [B,H,dv,dk] or null
   int B, T, H, RO, dk, dv, C, CK;
   float eps;
+  int cP, cR, ste;     // testbed compaction: every cP tokens to rank cR (cP = 0: off)
+  float cs;            // its slow decay (blend weight of the truncation)
 };
 
 // Token record layout in LDS (floats): K [R][dk], Bg [R][dk], a [dk],
@@ -265,7 +267,166 @@ __device__ __forceinline__ void token_step(float s[4][CPL], const TokIn<CPL, R>&
     }
 }
 
-template <int CPL, int R>
+
+// ---------------------------------------------------------------------------
+// Testbed compaction (research/testbed_mqar.py:245-260): after the write of
+// every cP-th token, S <- cs S_lr + (1 - cs) S with S_lr the best rank-cR
+// approximation of S.  The workgroup writes S to LDS, forms the smaller Gram
+// (S S^T or S^T S, m = min(dv, dk) <= 64), diagonalises it by parallel cyclic
+// Jacobi (round-robin pairing: m/2 disjoint rotations per round, m - 1 rounds
+// per sweep, until the off-diagonal mass is below 1e-12 of the total), keeps
+// the eigenvectors of the cR largest eigenvalues and projects.
+// ---------------------------------------------------------------------------
+__host__ __device__ inline size_t compact_lds_floats(int dk, int dv, int cR, int nthr) {
+  const int m = dv <= dk ? dv : dk, n = dv <= dk ? dk : dv;
+  return (size_t)dv * dk + 2 * (size_t)m * (m + 1) + m + 2 * m + (size_t)cR * n + nthr + 4;
+}
+
+template <int CPL>
+__device__ void compact_state(float s[4][CPL], const RlsArgs& g, float* sm, int rg, int c0) {
+  const int dk = g.dk, dv = g.dv, nthr = blockDim.x, tid = threadIdx.x;
+  const bool vside = dv <= dk;
+  const int m = vside ? dv : dk, n = vside ? dk : dv, ld = m + 1, cR = g.cR;
+  float* S = sm;                                  // [dv][dk]
+  float* A = S + dv * dk;                         // [m][ld]
+  float* E = A + m * ld;                          // [m][ld] eigenvectors in columns
+  float* rot = E + m * ld;                        // [m/2][2]
+  int* sel = (int*)(rot + m);                     // [cR]
+  float* Pm = (float*)(sel + 2 * m);              // [cR][n]
+  float* red = Pm + cR * n;                       // [nthr]
+  int* flag = (int*)(red + nthr);
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) S[(4 * rg + i) * dk + c0 + j] = s[i][j];
+  __syncthreads();
+  float tot = 0.0f;
+  for (int e = tid; e < m * m; e += nthr) {
+    const int i = e / m, j = e - i * m;
+    float x = 0.0f;
+    if (vside)
+      for (int c = 0; c < n; ++c) x += S[i * dk + c] * S[j * dk + c];
+    else
+      for (int v = 0; v < n; ++v) x += S[v * dk + i] * S[v * dk + j];
+    A[i * ld + j] = x;
+    E[i * ld + j] = i == j ? 1.0f : 0.0f;
+    tot += x * x;
+  }
+  red[tid] = tot;
+  __syncthreads();
+  if (tid == 0) {
+    float t = 0.0f;
+    for (int k = 0; k < nthr; ++k) t += red[k];
+    red[0] = t;
+  }
+  __syncthreads();
+  const float total = red[0];
+  __syncthreads();
+  const int half = m / 2;
+  for (int sweep = 0; sweep < 16; ++sweep) {
+    for (int r = 0; r < m - 1; ++r) {
+      // round r pairs (r, m-1) and ((r+q) mod (m-1), (r-q) mod (m-1)), q = 1 .. m/2 - 1
+      for (int q = tid; q < half; q += nthr) {
+        const int p0 = q == 0 ? r : (r + q) % (m - 1);
+        const int q0 = q == 0 ? m - 1 : (r - q + (m - 1)) % (m - 1);
+        const float app = A[p0 * ld + p0], aqq = A[q0 * ld + q0], apq = A[p0 * ld + q0];
+        float c = 1.0f, sn = 0.0f;
+        if (fabsf(apq) > 1e-30f && fabsf(apq) > 1e-9f * sqrtf(fabsf(app * aqq))) {
+          const float tau = (aqq - app) / (2.0f * apq);
+          const float at = fabsf(tau);
+          const float t = (tau >= 0.0f ? 1.0f : -1.0f) / (at > 1e15f ? 2.0f * at : at + sqrtf(1.0f + tau * tau));
+          c = 1.0f / sqrtf(1.0f + t * t);
+          sn = t * c;
+        }
+        rot[2 * q] = c;
+        rot[2 * q + 1] = sn;
+      }
+      __syncthreads();
+      // rows p, q of A <- J^T A
+      for (int e = tid; e < half * m; e += nthr) {
+        const int q = e / m, j = e - q * m;
+        const int p0 = q == 0 ? r : (r + q) % (m - 1);
+        const int q0 = q == 0 ? m - 1 : (r - q + (m - 1)) % (m - 1);
+        const float c = rot[2 * q], sn = rot[2 * q + 1];
+        const float a = A[p0 * ld + j], b = A[q0 * ld + j];
+        A[p0 * ld + j] = c * a - sn * b;
+        A[q0 * ld + j] = sn * a + c * b;
+      }
+      __syncthreads();
+      // columns p, q of A <- A J, and of the eigenvectors E <- E J
+      for (int e = tid; e < half * m; e += nthr) {
+        const int q = e / m, i = e - q * m;
+        const int p0 = q == 0 ? r : (r + q) % (m - 1);
+        const int q0 = q == 0 ? m - 1 : (r - q + (m - 1)) % (m - 1);
+        const float c = rot[2 * q], sn = rot[2 * q + 1];
+        const float a = A[i * ld + p0], b = A[i * ld + q0];
+        A[i * ld + p0] = c * a - sn * b;
+        A[i * ld + q0] = sn * a + c * b;
+        const float x = E[i * ld + p0], y = E[i * ld + q0];
+        E[i * ld + p0] = c * x - sn * y;
+        E[i * ld + q0] = sn * x + c * y;
+      }
+      __syncthreads();
+    }
+    float off = 0.0f;
+    for (int e = tid; e < m * m; e += nthr) {
+      const int i = e / m, j = e - i * m;
+      if (i != j) off += A[i * ld + j] * A[i * ld + j];
+    }
+    red[tid] = off;
+    __syncthreads();
+    if (tid == 0) {
+      float t = 0.0f;
+      for (int k = 0; k < nthr; ++k) t += red[k];
+      *flag = t <= 1e-12f * total;
+    }
+    __syncthreads();
+    const bool done = *flag;
+    __syncthreads();
+    if (done) break;
+  }
+  // the cR largest eigenvalues (first index on ties)
+  if (tid == 0) {
+    for (int k = 0; k < cR; ++k) {
+      int best = -1;
+      float bv = 0.0f;
+      for (int i = 0; i < m; ++i) {
+        bool used = false;
+        for (int u = 0; u < k; ++u) used |= sel[u] == i;
+        if (!used && (best < 0 || A[i * ld + i] > bv)) {
+          best = i;
+          bv = A[i * ld + i];
+        }
+      }
+      sel[k] = best;
+    }
+  }
+  __syncthreads();
+  // projection onto the kept eigenvectors: Pm = E_R^T S (value side) or (S E_R)^T (key side)
+  for (int e = tid; e < cR * n; e += nthr) {
+    const int k = e / n, x = e - k * n, col = sel[k];
+    float acc = 0.0f;
+    if (vside)
+      for (int v = 0; v < m; ++v) acc += E[v * ld + col] * S[v * dk + x];
+    else
+      for (int c = 0; c < m; ++c) acc += S[x * dk + c] * E[c * ld + col];
+    Pm[k * n + x] = acc;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      const int v = 4 * rg + i, c = c0 + j;
+      float lr = 0.0f;
+      for (int k = 0; k < cR; ++k)
+        lr += vside ? E[v * ld + sel[k]] * Pm[k * n + c] : Pm[k * n + v] * E[c * ld + sel[k]];
+      s[i][j] = g.cs * lr + (1.0f - g.cs) * s[i][j];
+    }
+  __syncthreads();
+}
+
+template <int CPL, int R, bool COMPACT>
 __global__ __launch_bounds__(512) void rls_fwd_kernel(RlsArgs g) {
   extern __shared__ float lds[];
   const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15;
@@ -299,7 +460,7 @@ __global__ __launch_bounds__(512) void rls_fwd_kernel(RlsArgs g) {
     for (int tl = 0; tl < ntok; ++tl) {
       const int t = t0 + tl;
       if (g.ckpt && t % g.CK == 0) {
-        float* ck = g.ckpt + (((size_t)chain * ((T + g.CK - 1) / g.CK) + t / g.CK) * dv + 4 * rg) * dk + c0;
+        float* ck = g.ckpt + (((size_t)chain * ((T + g.CK - 1) / g.CK + 1) + t / g.CK) * dv + 4 * rg) * dk + c0;
 #pragma unroll
         for (int i = 0; i < 4; ++i)
 #pragma unroll
@@ -310,6 +471,9 @@ __global__ __launch_bounds__(512) void rls_fwd_kernel(RlsArgs g) {
       load_tok<CPL, R>(in, rec, L, dk, dv, l16, rg, g.eps);
       float p[R][4], z[R][4];
       token_step<CPL, R>(s, in, p, z);
+      if constexpr (COMPACT) {
+        if ((t + 1) % g.cP == 0) compact_state<CPL>(s, g, lds + 2 * C * L.stride, rg, c0);
+      }
       float y[4] = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
       for (int o = 0; o < 4; ++o) {
@@ -336,6 +500,14 @@ __global__ __launch_bounds__(512) void rls_fwd_kernel(RlsArgs g) {
     for (int i = 0; i < 4; ++i)
 #pragma unroll
       for (int j = 0; j < CPL; ++j) g.state_out[((size_t)chain * dv + 4 * rg + i) * dk + c0 + j] = s[i][j];
+  }
+  if (g.ckpt) {   // the final state closes the checkpoint list
+    const int nck = (T + g.CK - 1) / g.CK;
+    float* ck = g.ckpt + (((size_t)chain * (nck + 1) + nck) * dv + 4 * rg) * dk + c0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) ck[(size_t)i * dk + j] = s[i][j];
   }
 }
 
@@ -372,7 +544,7 @@ __global__ __launch_bounds__(512) void rls_bwd_kernel(RlsArgs g) {
   const int nch = (T + C - 1) / C;
   // checkpoints are visited in decreasing order; the next one is in flight
   // while a sub-chunk is processed
-  auto ck_ptr = [&](int k) { return g.ckpt + (((size_t)chain * nck + k) * dv + 4 * rg) * dk + c0; };
+  auto ck_ptr = [&](int k) { return g.ckpt + (((size_t)chain * (nck + 1) + k) * dv + 4 * rg) * dk + c0; };
   float ckn[4][CPL];
   if (nck > 0) {
     const float* ck = ck_ptr(nck - 1);
@@ -446,6 +618,14 @@ __global__ __launch_bounds__(512) void rls_bwd_kernel(RlsArgs g) {
           // read: ds3 += sum_o mix_o dy q_o ; column partial gsum = sum_v dy s3
           float dyv[4];
           lds_vec<4>(rec + L.oDy + 4 * rg, dyv);
+          const bool compacted = g.cP && (t + 1) % g.cP == 0;
+          if (compacted) {   // the read saw the compacted state: the next checkpoint
+            const float* ck = ck_ptr((t + 1) / CK);
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int j = 0; j < CPL; ++j) s3[i][j] = ck[(size_t)i * dk + j];
+          }
           float gcol[CPL];
 #pragma unroll
           for (int j = 0; j < CPL; ++j) {
@@ -464,6 +644,12 @@ __global__ __launch_bounds__(512) void rls_bwd_kernel(RlsArgs g) {
 #pragma unroll
                 for (int j = 0; j < CPL; ++j) ds[i][j] += mix[o] * dyv[i] * qv[j];
             }
+          }
+          if (compacted && !g.ste) {   // S_c = cs S_lr + (1 - cs) S, S_lr without gradient
+#pragma unroll
+            for (int i = 0; i < 4; ++i)
+#pragma unroll
+              for (int j = 0; j < CPL; ++j) ds[i][j] *= 1.0f - g.cs;
           }
           // write: dw'_u = ds3 K_u (rows), column partial dK_u = sum_v w'_u ds3
           float pK[R][CPL], pKt[R][CPL];
@@ -686,21 +872,26 @@ __global__ __launch_bounds__(512) void rls_bwd_kernel(RlsArgs g) {
 // ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
-// checkpoint interval: the backward keeps CK states per lane in registers
-int rls_ck(int dk, int R) { return dk <= 32 && R <= 3 ? 4 : 2; }
+// checkpoint interval: the backward keeps CK states per lane in registers; a
+// compaction falls on the last token of a CK group (cP a multiple of CK)
+int rls_ck(int dk, int R, int cP) {
+  const int ck = dk <= 32 && R <= 3 ? 4 : 2;
+  return cP % ck == 0 ? ck : 2;
+}
 
 struct RlsGeom {
   int C, CK, threads;
   size_t lds;
 };
 
-static RlsGeom rls_geom(int R, int RO, int dk, int dv, bool bwd) {
+static RlsGeom rls_geom(int R, int RO, int dk, int dv, bool bwd, int cP, int cR) {
   RlsGeom G{};
-  G.CK = rls_ck(dk, R);
+  G.CK = rls_ck(dk, R, cP);
   G.threads = 4 * dv;
   const int stride = (2 * R + 1 + RO) * dk + 2 * R * dv + (bwd ? dv : 0);
   const int nw = G.threads / 64;
-  const size_t red = bwd ? ((size_t)nw * G.CK * part_len(R, dk) + (size_t)G.CK * R * R) * 4 : 0;
+  const size_t red = bwd ? ((size_t)nw * G.CK * part_len(R, dk) + (size_t)G.CK * R * R) * 4
+                         : (cP ? compact_lds_floats(dk, dv, cR, G.threads) * 4 : 0);
   const size_t budget = 156 * 1024;
   // largest chunk that fits LDS, preferring one whose loads all prefetch
   G.C = 0;
@@ -718,7 +909,7 @@ static RlsGeom rls_geom(int R, int RO, int dk, int dv, bool bwd) {
 
 template <int CPL, int R>
 static int launch_rls(const RlsArgs& a0, bool bwd, hipStream_t stream) {
-  const RlsGeom G = rls_geom(R, a0.RO, a0.dk, a0.dv, bwd);
+  const RlsGeom G = rls_geom(R, a0.RO, a0.dk, a0.dv, bwd, a0.cP, a0.cR);
   if (G.C == 0) return set_error(GDNX_ERR_SHAPE, "RLS scan: R=%d, R_out=%d, key_dim=%d, value_dim=%d do not fit LDS",
                                  R, a0.RO, a0.dk, a0.dv);
   RlsArgs a = a0;
@@ -726,7 +917,7 @@ static int launch_rls(const RlsArgs& a0, bool bwd, hipStream_t stream) {
   a.CK = G.CK;
   const unsigned nchains = (unsigned)(a.B * a.H);
   if (!bwd) {
-    auto k = rls_fwd_kernel<CPL, R>;
+    auto k = a.cP ? rls_fwd_kernel<CPL, R, true> : rls_fwd_kernel<CPL, R, false>;
     if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)G.lds) != hipSuccess)
       return set_error(GDNX_ERR_HIP, "rls_fwd_kernel: cannot reserve %zu bytes of LDS", G.lds);
     hipLaunchKernelGGL(k, dim3(nchains), dim3(G.threads), G.lds, stream, a);
@@ -758,9 +949,9 @@ static int launch_rls_r(const RlsArgs& a, int R, bool bwd, hipStream_t stream) {
 
 }  // namespace
 
-size_t rls_ckpt_bytes(int nchains, int T, int R, int dk, int dv) {
-  const int CK = rls_ck(dk, R);
-  return (size_t)nchains * ((T + CK - 1) / CK) * dv * dk * sizeof(float);
+size_t rls_ckpt_bytes(int nchains, int T, int R, int dk, int dv, int cP) {
+  const int CK = rls_ck(dk, R, cP);
+  return (size_t)nchains * ((T + CK - 1) / CK + 1) * dv * dk * sizeof(float);
 }
 
 int rls_dispatch(const RlsDesc& d, bool bwd, hipStream_t stream) {
@@ -770,6 +961,7 @@ int rls_dispatch(const RlsDesc& d, bool bwd, hipStream_t stream) {
   a.ckpt = d.ckpt; a.dq = d.dq; a.dK = d.dK; a.dV = d.dV; a.dBg = d.dBg; a.dWg = d.dWg; a.da = d.da;
   a.dmix = d.dmix; a.dstate0 = d.dstate0;
   a.B = d.B; a.T = d.T; a.H = d.H; a.RO = d.RO; a.dk = d.dk; a.dv = d.dv; a.eps = d.eps;
+  a.cP = d.cP; a.cR = d.cR; a.cs = d.cs; a.ste = d.ste;
   if (d.T == 0) return GDNX_OK;
   switch (d.dk) {
     case 32: return launch_rls_r<2>(a, d.R, bwd, stream);

@@ -381,34 +381,45 @@ int gdnx_gdn3_epilogue_bwd(const void* y, const void* router_logits, const float
  * (research/testbed_mqar.py:226-262, without its compaction).  Per chain
  * (b, h), state S [value_dim, key_dim] (value-major), per token, R slots:
  *   S <- S diag(a);  Kt = Bg * K;  S <- S - (S Kt^T)(eps I + Kt Kt^T)^-1 Kt
- *   S <- S + (Wg * V)^T K;  y = sum_o mix_o S q_o  (mix = out_mix[h], or 1 when R_out = 1)
+ *   S <- S + (Wg * V)^T K;
+ *   (compact_P > 0, after the write of every compact_P-th token, the testbed's
+ *    compaction research/testbed_mqar.py:245-260:  S <- s S_lr + (1-s) S, S_lr
+ *    the best rank-compact_R approximation of S, s = slow_decay)
+ *   y = sum_o mix_o S q_o  (mix = out_mix[h], or 1 when R_out = 1)
  * All tensors float32: q [B,T,H,R_out,key_dim]; K, Bg [B,T,H,R,key_dim];
  * V, Wg [B,T,H,R,value_dim]; a [B,T,H,key_dim]; out_mix [H,R_out];
  * states [B,H,value_dim,key_dim]; y [B,T,H,value_dim].  key_dim 32, 64 or 128;
  * value_dim a multiple of 16 up to 128; R, R_out 1..4 (callers zero-pad
- * other dims: zero key / value columns and a = 1 leave the scan unchanged). */
+ * other dims: zero key / value columns and a = 1 leave the scan unchanged).
+ * Compaction: compact_P even, 1 <= compact_R <= min(key_dim, value_dim) <= 64,
+ * key_dim * value_dim <= 4096; the truncation is exact (Jacobi eigensolver of
+ * the smaller Gram of S, converged to 1e-12 of its mass). */
 
 /* Bytes of the state checkpoints the backward needs (one state every few
- * tokens per chain). */
-long long gdnx_rls_ckpt_bytes(int B, int T, int H, int R, int key_dim, int value_dim);
+ * tokens per chain, plus the final state). */
+long long gdnx_rls_ckpt_bytes(int B, int T, int H, int R, int key_dim, int value_dim, int compact_P);
 
 /* Forward.  state0 (initial state), state_out (final state) and ckpt (the
  * backward's checkpoints, gdnx_rls_ckpt_bytes) may be NULL. */
 int gdnx_rls_fwd(const float* q, const float* K, const float* V, const float* Bg, const float* Wg,
                  const float* a, const float* out_mix, const float* state0, float* y, float* state_out,
                  float* ckpt, int B, int T, int H, int R, int R_out, int key_dim, int value_dim,
-                 float eps, void* stream);
+                 float eps, int compact_P, int compact_R, float slow_decay, void* stream);
 
 /* Backward from dy [B,T,H,value_dim] (and d_state, the gradient of the final
  * state, or NULL) through the forward's checkpoints: gradients of every
  * input in its layout; d_out_mix_seq [B,H,R_out] holds each sequence's share
  * of out_mix's gradient (sum it over B); d_state0 (or NULL) the initial
- * state's.  Deterministic. */
+ * state's.  Through a compaction the gradient is the testbed's: the truncation
+ * carries none (it runs under no_grad), so the state's gradient is scaled by
+ * 1 - slow_decay; with straight_through != 0 it passes unchanged (the
+ * testbed's compact_ste).  Deterministic. */
 int gdnx_rls_bwd(const float* q, const float* K, const float* V, const float* Bg, const float* Wg,
                  const float* a, const float* out_mix, const float* ckpt, const float* dy,
                  const float* d_state, float* dq, float* dK, float* dV, float* dBg, float* dWg,
                  float* da, float* d_out_mix_seq, float* d_state0, int B, int T, int H, int R,
-                 int R_out, int key_dim, int value_dim, float eps, void* stream);
+                 int R_out, int key_dim, int value_dim, float eps, int compact_P, int compact_R,
+                 float slow_decay, int straight_through, void* stream);
 
 #ifdef __cplusplus
 }

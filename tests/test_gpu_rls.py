@@ -139,3 +139,66 @@ def test_rls_backward_is_deterministic(gpu_lib):
     torch.cuda.synchronize()
     for a, b in zip(g1, g2):
         assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("case,ste", [("tb_plain", False), ("tb_ste", True)])
+def test_rls_compaction_matches_testbed_golden(gpu_lib, case, ste):
+    """The testbed mixer's scan with SVD compaction every P tokens (its own
+    forward, research/testbed_mqar.py:245-260), gates and decay through the
+    mixer's sigmoids (torch, outside the kernel); key dim 16 / value dim 16
+    run zero-padded."""
+    from gdnx_amd import rls
+    print(f"case: rls compaction golden {case}", flush=True)
+    z = np.load(GOLD, allow_pickle=False)
+    t = {k.split("/")[1]: torch.from_numpy(z[k]) for k in z.files if k.startswith(case + "/")}
+    names = ["q", "K", "V", "bg_logit", "wg_logit", "dec_logit"]
+    lv = {n: t[n].to(DEV).requires_grad_(True) for n in names}
+    y = rls.rls_scan(lv["q"], lv["K"], lv["V"], torch.sigmoid(lv["bg_logit"]), torch.sigmoid(lv["wg_logit"]),
+                     torch.sigmoid(lv["dec_logit"]).clamp(max=0.9995), eps=float(t["eps"][0]),
+                     compact_P=int(t["P"][0]), compact_R=int(t["R"][0]), slow_decay=0.97, straight_through=ste)
+    grads = torch.autograd.grad(y, list(lv.values()), t["dy"].to(DEV))
+    torch.cuda.synchronize()
+    err = rel_l2(y, t["y"])
+    print(f"  y rel-L2 {err:.2e}", flush=True)
+    assert err <= 1e-4
+    for n, d in zip(names, grads):
+        err = rel_l2(d, t["d" + n])
+        print(f"  d{n} rel-L2 {err:.2e}", flush=True)
+        assert err <= 1e-4, n
+
+
+COMPACT_CASES = [
+    # (B, T, H, r, dk, dv, P, R, ste)
+    (1, 40, 2, 2, 32, 32, 8, 3, False),
+    (1, 40, 2, 2, 32, 32, 8, 3, True),
+    (1, 48, 1, 1, 64, 64, 16, 8, False),
+    (2, 30, 1, 2, 32, 48, 10, 5, False),
+    (1, 36, 1, 1, 64, 32, 12, 4, True),
+]
+
+
+@pytest.mark.parametrize("case", COMPACT_CASES, ids=[f"k{i}" for i in range(len(COMPACT_CASES))])
+def test_rls_compaction_matches_oracle(gpu_lib, case):
+    """In-kernel truncated SVD (Jacobi on the smaller Gram of S) and the
+    compaction's gradient (no-grad truncation, or straight-through) against
+    the float64 oracle.  Bound 1e-4: the truncation moves with the state's
+    float32 error amplified by sigma_1 / (sigma_R - sigma_{R+1})."""
+    from gdnx_amd import rls
+    B, T, H, r, dk, dv, P, R, ste = case
+    print(f"case: rls compaction {case}", flush=True)
+    xs, _ = _inputs(B, T, H, r, 1, dk, dv, seed=51)
+    dy = torch.randn(B, T, H, dv, generator=torch.Generator().manual_seed(52))
+    leaves = [x.to(DEV).requires_grad_(True) for x in xs]
+    y = rls.rls_scan(*leaves, compact_P=P, compact_R=R, slow_decay=0.97, straight_through=ste)
+    grads = torch.autograd.grad(y, leaves, dy.to(DEV))
+    torch.cuda.synchronize()
+    rl = [x.double().requires_grad_(True) for x in xs]
+    yr = orls.rls_scan(*rl, compact_P=P, compact_R=R, slow_decay=0.97, ste=ste)
+    gr = torch.autograd.grad(yr, rl, dy.double())
+    err = rel_l2(y, yr)
+    print(f"  y rel-L2 {err:.2e}", flush=True)
+    assert err <= 1e-4
+    for n, a, b in zip(["dq", "dK", "dV", "dBg", "dWg", "da"], grads, gr):
+        err = rel_l2(a, b)
+        print(f"  {n} rel-L2 {err:.2e}", flush=True)
+        assert err <= 1e-4, n
