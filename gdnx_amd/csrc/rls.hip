@@ -511,6 +511,126 @@ __global__ __launch_bounds__(512) void rls_fwd_kernel(RlsArgs g) {
   }
 }
 
+// ---------------------------------------------------------------------------
+// Forward without compaction, rows spread over workgroups.  The value rows of
+// S are independent, so a workgroup takes 16 rows of one chain -- one row per
+// DPP row, CPL key columns per lane -- and a chain runs on dv / 16
+// workgroups: a lane carries CPL state elements instead of 4 CPL, which cuts
+// the per-token instruction path (this scan's bound) about 4x.  Token
+// operands are staged per chunk through LDS as in rls_fwd_kernel (one copy
+// per workgroup, the next chunk's loads in flight); checkpoints and the
+// final state use its layout.
+// ---------------------------------------------------------------------------
+template <int CPL, int R>
+__global__ __launch_bounds__(256) void rls_fwd_rb_kernel(RlsArgs g) {
+  extern __shared__ float lds[];
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15;
+  const int nrb = g.dv / 16;
+  const int chain = blockIdx.x / nrb, v = 16 * (blockIdx.x % nrb) + (tid >> 4);
+  const int b = chain / g.H, h = chain % g.H;
+  const int dk = g.dk, dv = g.dv, T = g.T, C = g.C, RO = g.RO;
+  const RecLayout L(R, RO, dk, dv, false);
+  const int c0 = CPL * l16;
+  const int nck = (T + g.CK - 1) / g.CK;
+  float mix[4];
+#pragma unroll
+  for (int o = 0; o < 4; ++o) mix[o] = o < RO ? (RO > 1 ? g.mix[h * RO + o] : 1.0f) : 0.0f;
+  float s[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) s[j] = g.state0 ? g.state0[((size_t)chain * dv + v) * dk + c0 + j] : 0.0f;
+
+  const int nch = (T + C - 1) / C;
+  Stager st;
+  if (nch > 0) {
+    st.fetch(g, L, R, chain, 0, min(C, T), false);
+    st.commit(lds, g, L, R, false);
+  }
+  __syncthreads();
+  for (int c = 0; c < nch; ++c) {
+    const int t0 = c * C, ntok = min(C, T - t0);
+    const float* buf = lds + (c & 1) * C * L.stride;
+    if (c + 1 < nch) st.fetch(g, L, R, chain, t0 + C, min(C, T - t0 - C), false);
+    for (int tl = 0; tl < ntok; ++tl) {
+      const int t = t0 + tl;
+      const float* rec = buf + tl * L.stride;
+      if (g.ckpt && t % g.CK == 0) {
+        float* ck = g.ckpt + (((size_t)chain * (nck + 1) + t / g.CK) * dv + v) * dk + c0;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) ck[j] = s[j];
+      }
+      float a[CPL], K[R][CPL], Kt[R][CPL], w[R], G[R][R], Tf[R][R];
+      lds_vec<CPL>(rec + L.oA + c0, a);
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float bg[CPL];
+        lds_vec<CPL>(rec + L.oK + r * dk + c0, K[r]);
+        lds_vec<CPL>(rec + L.oBg + r * dk + c0, bg);
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) Kt[r][j] = bg[j] * K[r][j];
+        w[r] = rec[L.oW + r * dv + v] * rec[L.oV + r * dv + v];
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r)
+#pragma unroll
+        for (int r2 = r; r2 < R; ++r2) {
+          float d = 0.0f;
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) d += Kt[r][j] * Kt[r2][j];
+          G[r][r2] = G[r2][r] = row_sum16(d);
+        }
+      tfactor<R>(G, g.eps, Tf);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) s[j] *= a[j];
+      float p[R], z[R];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) d += s[j] * Kt[r][j];
+        p[r] = row_sum16(d);
+      }
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        float d = 0.0f;
+#pragma unroll
+        for (int r2 = 0; r2 < R; ++r2) d += p[r2] * Tf[r2][r];
+        z[r] = d;
+      }
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) {
+        float d = s[j];
+#pragma unroll
+        for (int r = 0; r < R; ++r) d += w[r] * K[r][j] - z[r] * Kt[r][j];
+        s[j] = d;
+      }
+      float y = 0.0f;
+#pragma unroll
+      for (int o = 0; o < 4; ++o) {
+        if (o < RO) {
+          float qv[CPL];
+          lds_vec<CPL>(rec + L.oQ + o * dk + c0, qv);
+          float d = 0.0f;
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) d += s[j] * qv[j];
+          y += mix[o] * row_sum16(d);
+        }
+      }
+      if (l16 == 0) g.y[(((size_t)b * T + t) * g.H + h) * dv + v] = y;
+    }
+    if (c + 1 < nch) st.commit(lds + ((c + 1) & 1) * C * L.stride, g, L, R, false);
+    __syncthreads();
+  }
+  if (g.state_out) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) g.state_out[((size_t)chain * dv + v) * dk + c0 + j] = s[j];
+  }
+  if (g.ckpt) {
+    float* ck = g.ckpt + (((size_t)chain * (nck + 1) + nck) * dv + v) * dk + c0;
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) ck[j] = s[j];
+  }
+}
+
 // Column partials of one token: g = sum_v dy s3 (dk), dK (R dk), dKt (R dk),
 // da (dk), then dT (R^2).
 __host__ __device__ constexpr int part_len(int R, int dk) { return (2 + 2 * R) * dk + R * R; }
@@ -875,7 +995,7 @@ __global__ __launch_bounds__(512) void rls_bwd_kernel(RlsArgs g) {
 // checkpoint interval: the backward keeps CK states per lane in registers; a
 // compaction falls on the last token of a CK group (cP a multiple of CK)
 int rls_ck(int dk, int R, int cP) {
-  const int ck = dk <= 32 && R <= 3 ? 4 : 2;
+  const int ck = (dk <= 32 && R <= 3) || (dk == 64 && R == 1) ? 4 : 2;
   return cP % ck == 0 ? ck : 2;
 }
 
@@ -909,13 +1029,25 @@ static RlsGeom rls_geom(int R, int RO, int dk, int dv, bool bwd, int cP, int cR)
 
 template <int CPL, int R>
 static int launch_rls(const RlsArgs& a0, bool bwd, hipStream_t stream) {
+  RlsArgs a = a0;
+  a.CK = rls_ck(a.dk, R, a.cP);
+  const unsigned nchains = (unsigned)(a.B * a.H);
+  if (!bwd && !a.cP) {
+    // the workgroup stages a chunk for 256 threads (16 rows)
+    const int stride = (2 * R + 1 + a.RO) * a.dk + 2 * R * a.dv;
+    int C = 32;
+    while (C > a.CK && ((size_t)2 * C * stride * 4 > 64 * 1024 || C * (stride / 4) > kMaxPre * 256)) C >>= 1;
+    if ((size_t)2 * C * stride * 4 > 64 * 1024) return set_error(GDNX_ERR_SHAPE, "RLS scan: record too large for LDS");
+    a.C = C;
+    const size_t lds = (size_t)2 * C * stride * 4;
+    auto k = rls_fwd_rb_kernel<CPL, R>;
+    hipLaunchKernelGGL(k, dim3(nchains * (unsigned)(a.dv / 16)), dim3(256), lds, stream, a);
+    return check_launch("rls_fwd_rb_kernel");
+  }
   const RlsGeom G = rls_geom(R, a0.RO, a0.dk, a0.dv, bwd, a0.cP, a0.cR);
   if (G.C == 0) return set_error(GDNX_ERR_SHAPE, "RLS scan: R=%d, R_out=%d, key_dim=%d, value_dim=%d do not fit LDS",
                                  R, a0.RO, a0.dk, a0.dv);
-  RlsArgs a = a0;
   a.C = G.C;
-  a.CK = G.CK;
-  const unsigned nchains = (unsigned)(a.B * a.H);
   if (!bwd) {
     auto k = a.cP ? rls_fwd_kernel<CPL, R, true> : rls_fwd_kernel<CPL, R, false>;
     if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)G.lds) != hipSuccess)
