@@ -75,6 +75,14 @@ def gdn3_scan(q, k, v, beta, log_g, state0=None, return_state=False):
     [B,T,H,M] float32 (log_g > 0 is clamped, i.e. gamma <= 1).  Returns
     y [B,T,H,M,D] in q's dtype (and the final state [B,H,M,D,D] fp32).
     """
+    if q.shape[1] == 0:
+        B, _, H, D = q.shape
+        M = beta.shape[3]
+        y = ops.empty_result((B, 0, H, M, D), q.dtype, q.device, q, k, v, beta, log_g)
+        if not return_state:
+            return y
+        s = state0.float() + 0 if state0 is not None else torch.zeros(B, H, M, D, D, device=q.device)
+        return y, s
     args = [t.contiguous() for t in (q, k, v)] + [t.float().contiguous() for t in (beta, log_g)]
     if state0 is not None:
         state0 = state0.float().contiguous()
@@ -162,6 +170,15 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     B, T, H, M = decay_factors.shape
     cdt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
     D = q.shape[-1]
+    if T == 0:   # empty sequence: zero output, the initial (zero) state, no compaction
+        y = ops.empty_result((B, 0, H, M, D), cdt, q.device, q, k, v, b_gates, w_gates, decay_factors)
+        if not return_state:
+            return y
+        a_v, a_k, b_v, b_k = factors
+        N, dev = B * H * M, q.device
+        state = (torch.zeros(N, R, a_v, a_k, device=dev), torch.zeros(N, R, b_v, b_k, device=dev),
+                 torch.zeros(N, D, P, device=dev), torch.zeros(N, D, P, device=dev))
+        return y, state, torch.zeros((), dtype=torch.float64, device=dev)
 
     def lanes5(x):
         return x.unsqueeze(3) if x.dim() == 4 else x

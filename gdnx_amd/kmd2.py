@@ -73,6 +73,10 @@ def _pad_last(x, D, value=0.0):
 def _scan(q, k, v, g, beta_e, beta_w, out_mix, want_scores):
     B, T, H, r_out, dk = q.shape
     dv = v.shape[-1]
+    if T == 0:
+        y = ops.empty_result((B, 0, H, dv), q.dtype if q.dtype == torch.bfloat16 else torch.float32, q.device,
+                             q, k, v, g, beta_e, beta_w, out_mix)
+        return (y, torch.zeros(B, 0, H, device=q.device)) if want_scores else y
     D = _kernel_dim(dk, dv)
     scalar = _scalar_decay(g)
     qe = _mixed_query(q if scalar else q.float(), out_mix)

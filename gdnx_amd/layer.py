@@ -127,6 +127,16 @@ def gdn3_prologue(q, k, b_proj, proj_a, w_proj, proj_b, decay_proj, base_decay_r
     w_proj [B,T,H,M,V], proj_a, proj_b [B,T,H], decay_proj [B,T,H,M,4],
     base_decay_rates [4].  Returns (q_rope, k_rope [B,T,H,M,K] in q's dtype,
     b_gates [B,T,H,M,K], w_gates [B,T,H,M,V], decay [B,T,H,M] float32)."""
+    if q.numel() == 0:
+        B, T, H, K = q.shape
+        M, V = b_proj.shape[3], w_proj.shape[-1]
+        srcs = (q, k, b_proj, proj_a, w_proj, proj_b, decay_proj)
+        dt = q.dtype
+        return (ops.empty_result((B, T, H, M, K), dt, q.device, *srcs),
+                ops.empty_result((B, T, H, M, K), dt, q.device, *srcs),
+                ops.empty_result((B, T, H, M, K), torch.float32, q.device, *srcs),
+                ops.empty_result((B, T, H, M, V), torch.float32, q.device, *srcs),
+                ops.empty_result((B, T, H, M), torch.float32, q.device, *srcs))
     return _Prologue.apply(q, k, b_proj, proj_a, w_proj, proj_b, decay_proj, base_decay_rates, float(decay_clamp))
 
 
@@ -134,6 +144,9 @@ def gdn3_epilogue(y, router_logits, norm):
     """Lane routing and head norm of GDN3LinearAttn.forward
     (gdn3/gdn3_upgrade.py:842-851): y [B,T,H,M,V] (the recurrence output),
     router_logits [B,T,H,M], norm [V] -> [B,T,H,V] in y's dtype."""
+    if y.numel() == 0:
+        B, T, H, M, V = y.shape
+        return ops.empty_result((B, T, H, V), y.dtype, y.device, y, router_logits, norm)
     return _Epilogue.apply(y, router_logits, norm)
 
 

@@ -17,6 +17,18 @@ def _need(cond, msg):
         raise ValueError(msg)
 
 
+def empty_result(shape, dtype, device, *srcs):
+    """Zeros of ``shape`` for a call over an empty sequence (T = 0), attached to
+    the autograd graph of ``srcs`` so that backward gives their (zero or empty)
+    gradients, as the equivalent torch ops on empty tensors would."""
+    z = torch.zeros(shape, dtype=dtype, device=device)
+    if torch.is_grad_enabled():
+        for s in srcs:
+            if s is not None and s.requires_grad:
+                z = z + (s.sum() * 0).to(dtype)
+    return z
+
+
 def _check_dense(q, k, v, a_e, a_w, log_g):
     _need(q.is_cuda, "gdnx ops need CUDA (HIP) tensors")
     _need(q.dim() == 4 and q.shape == k.shape == v.shape, "q, k, v must share shape [B,T,H,D]")
@@ -554,6 +566,10 @@ def gdn3_prologue_fwd(q, k, b_proj, proj_a, w_proj, proj_b, decay_proj, rates, r
     _need(b_proj.dim() == 5, "b_proj must be [B,T,H,M,K]")
     M, V = b_proj.shape[3], w_proj.shape[-1]
     dt = q.dtype
+    if B * T * H == 0:
+        return (torch.empty(B, T, H, M, K, dtype=dt, device=q.device), torch.empty(B, T, H, M, K, dtype=dt, device=q.device),
+                torch.empty(B, T, H, M, K, device=q.device), torch.empty(B, T, H, M, V, device=q.device),
+                torch.empty(B, T, H, M, device=q.device))
     q, k = q.contiguous(), k.to(dt).contiguous()
     bp = _row_io(b_proj, (B, T, H, M, K), dt, "b_proj")
     wp = _row_io(w_proj, (B, T, H, M, V), dt, "w_proj")

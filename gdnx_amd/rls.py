@@ -29,7 +29,7 @@ from __future__ import annotations
 import torch
 import torch.nn.functional as F
 
-from . import _lib
+from . import _lib, ops
 
 
 def _need(cond, msg):
@@ -153,6 +153,12 @@ def rls_scan(q, K, V, Bg, Wg, a, eps=0.5, out_mix=None, state0=None, return_stat
     _need(K.shape == Bg.shape and tuple(K.shape[:3]) == (B, T, H), "K and Bg must be [B,T,H,r,dk]")
     _need(V.shape == Wg.shape and tuple(V.shape[:4]) == (B, T, H, R), "V and Wg must be [B,T,H,r,dv]")
     _need(tuple(a.shape) == (B, T, H, dk), "a must be [B,T,H,dk]")
+    if T == 0:   # empty sequence: no output, the state is the initial one
+        y = ops.empty_result((B, 0, H, dv), torch.float32, q.device, q, K, V, Bg, Wg, a, out_mix)
+        if not return_state:
+            return y
+        st = state0.float() + 0 if state0 is not None else torch.zeros(B, H, dv, dk, device=q.device)
+        return y, st
     compact = (int(compact_P), int(compact_R), float(slow_decay), bool(straight_through))
     out = _RLSScan.apply(q, K, V, Bg, Wg, a, out_mix if RO > 1 else None, state0, float(eps), bool(return_state),
                          compact)
