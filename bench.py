@@ -743,7 +743,7 @@ def bench_rls(args):
         t_fwd = timed(lambda: rls.rls_fwd(*flat, checkpoint=True), args.kernel_iters)
     f = flops_rls(B, T, H, r, ro, dk, dv)
     t_bwd = max(sec - t_fwd, 1e-9)
-    kernels = {"rls_fwd_rb_kernel": (t_fwd, f), "rls_bwd_kernel": (t_bwd, 3 * f)}
+    kernels = {"rls_fwd_rb_kernel": (t_fwd, f), "rls_bwd_rb_kernel+rls_bwd_reduce_kernel": (t_bwd, 3 * f)}
     dom = max(kernels, key=lambda n: kernels[n][0])
     achieved = kernels[dom][1] / kernels[dom][0] / 1e12
     # the testbed mixer's shape with its SVD compaction (research/testbed_mqar.py:75-78 defaults
@@ -779,8 +779,8 @@ def bench_rls(args):
         "roofline": {"bound": "mfma", "kernel": dom, "achieved": achieved, "peak": MFMA_FP32_PEAK / 1e12,
                      "unit": "TFLOP/s", "frac": achieved * 1e12 / MFMA_FP32_PEAK, "traffic": measured_traffic(dom),
                      "mean_us": kernels[dom][0] * 1e6, "algorithmic_flop": kernels[dom][1],
-                     "note": "sequential per-token recurrence: latency-bound (forward: 16 rows per workgroup, "
-                             "backward: one workgroup per chain, 128 chains); the backward's time is the step minus "
+                     "note": "sequential per-token recurrence: latency-bound (16 value rows per workgroup, "
+                             "dv/16 workgroups per chain, 128 chains); the backward's time is the step minus "
                              "the forward"},
         "kernels_us": {n: round(t * 1e6, 2) for n, (t, _) in kernels.items()},
         "torch_eager_ms_per_step": eager * 1e3,

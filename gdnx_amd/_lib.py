@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(_HERE, "libgdnx.so")
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 _c_int, _c_ll, _vp, _c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_float
 
@@ -59,7 +59,8 @@ SIGNATURES = {
     "gdnx_gdn3_epilogue_bwd": (_c_int, [_vp] * 8 + [_c_int] * 6 + [_vp]),
     "gdnx_rls_ckpt_bytes": (_c_ll, [_c_int] * 7),
     "gdnx_rls_fwd": (_c_int, [_vp] * 11 + [_c_int] * 7 + [_c_float, _c_int, _c_int, _c_float, _vp]),
-    "gdnx_rls_bwd": (_c_int, [_vp] * 18 + [_c_int] * 7 + [_c_float, _c_int, _c_int, _c_float, _c_int, _vp]),
+    "gdnx_rls_bwd_workspace_bytes": (_c_ll, [_c_int] * 6),
+    "gdnx_rls_bwd": (_c_int, [_vp] * 18 + [_c_int] * 7 + [_c_float, _c_int, _c_int, _c_float, _c_int, _vp, _vp]),
 }
 
 

@@ -676,6 +676,11 @@ extern "C" long long gdnx_rls_ckpt_bytes(int B, int T, int H, int R, int key_dim
   return (long long)rls_ckpt_bytes(B * H, T, R, key_dim, value_dim, compact_P);
 }
 
+extern "C" long long gdnx_rls_bwd_workspace_bytes(int B, int T, int H, int R, int key_dim, int value_dim) {
+  if (rls_sizes(B, T, H, R, 1, key_dim, value_dim, 1.0f) != GDNX_OK) return -1;
+  return (long long)rls_bwd_workspace_bytes(B * H, T, R, key_dim, value_dim);
+}
+
 extern "C" int gdnx_rls_fwd(const float* q, const float* K, const float* V, const float* Bg, const float* Wg,
                             const float* a, const float* out_mix, const float* state0, float* y, float* state_out,
                             float* ckpt, int B, int T, int H, int R, int R_out, int key_dim, int value_dim,
@@ -701,7 +706,7 @@ extern "C" int gdnx_rls_bwd(const float* q, const float* K, const float* V, cons
                             const float* d_state, float* dq, float* dK, float* dV, float* dBg, float* dWg,
                             float* da, float* d_out_mix_seq, float* d_state0, int B, int T, int H, int R,
                             int R_out, int key_dim, int value_dim, float eps, int compact_P, int compact_R,
-                            float slow_decay, int straight_through, void* stream) {
+                            float slow_decay, int straight_through, void* workspace, void* stream) {
   g_err[0] = 0;
   int rc = rls_sizes(B, T, H, R, R_out, key_dim, value_dim, eps);
   if (rc == GDNX_OK) rc = rls_compact_args(key_dim, value_dim, compact_P, compact_R, slow_decay);
@@ -716,5 +721,7 @@ extern "C" int gdnx_rls_bwd(const float* q, const float* K, const float* V, cons
   d.dmix = d_out_mix_seq; d.dstate0 = d_state0;
   d.B = B; d.T = T; d.H = H; d.R = R; d.RO = R_out; d.dk = key_dim; d.dv = value_dim; d.eps = eps;
   d.cP = compact_P; d.cR = compact_R; d.cs = slow_decay; d.ste = straight_through != 0;
+  if (workspace && !aligned16(workspace)) return set_error(GDNX_ERR_ARG, "workspace must be 16-byte aligned");
+  d.workspace = workspace;
   return rls_dispatch(d, true, (hipStream_t)stream);
 }

@@ -299,8 +299,10 @@ struct RlsDesc {
   float eps;
   int cP, cR, ste;   // testbed compaction (cP = 0: off)
   float cs;
+  void* workspace;   // backward without compaction: row-block partials (or null)
 };
 size_t rls_ckpt_bytes(int nchains, int T, int R, int dk, int dv, int cP);
+size_t rls_bwd_workspace_bytes(int nchains, int T, int R, int dk, int dv);
 int rls_dispatch(const RlsDesc& d, bool bwd, hipStream_t stream);
 
 void gdn3_lane_pairs(int M, int K, int pairs[4]);

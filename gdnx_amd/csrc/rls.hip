@@ -123,6 +123,8 @@ struct RlsArgs {
   float eps;
   int cP, cR, ste;     // testbed compaction: every cP tokens to rank cR (cP = 0: off)
   float cs;            // its slow decay (blend weight of the truncation)
+  float* part;         // split backward: per (chain, row block, token) column partials
+  float* mixpart;      // split backward: per (chain, token block) out_mix partials
 };
 
 // Token record layout in LDS (floats): K [R][dk], Bg [R][dk], a [dk],
@@ -990,6 +992,372 @@ __global__ __launch_bounds__(512) void rls_bwd_kernel(RlsArgs g) {
 
 
 // ---------------------------------------------------------------------------
+// Backward on row blocks (no compaction): a workgroup takes 16 value rows of
+// one chain, one row per DPP row, as rls_fwd_rb_kernel does, and a chain runs
+// on dv / 16 workgroups.  Row gradients (dV, dWg) are stored directly; each
+// workgroup writes its per-token column partials (sum over its 16 rows of
+// dy s3, w' ds3, -z ds2 + dp s1, ds1 s0 and p^T dz) to a buffer, and
+// rls_bwd_reduce_kernel sums the row blocks in a fixed order and forms dq,
+// dK, dBg, da and the out_mix partials.
+// ---------------------------------------------------------------------------
+template <int CPL, int R, int CK>
+__global__ __launch_bounds__(256) void rls_bwd_rb_kernel(RlsArgs g) {
+  extern __shared__ float lds[];
+  const int tid = threadIdx.x, lane = tid & 63, l16 = lane & 15, dr = lane >> 4, wave = tid >> 6;
+  const int G = g.dv / 16;
+  const int chain = blockIdx.x / G, rb = blockIdx.x % G, v = 16 * rb + (tid >> 4);
+  const int b = chain / g.H, h = chain % g.H;
+  const int dk = g.dk, dv = g.dv, T = g.T, C = g.C, RO = g.RO;
+  const RecLayout L(R, RO, dk, dv, true);
+  const int c0 = CPL * l16;
+  const int PL = part_len(R, dk);
+  float* red = lds + 2 * C * L.stride;        // [4 waves][CK][PL]
+  float mix[4];
+#pragma unroll
+  for (int o = 0; o < 4; ++o) mix[o] = o < RO ? (RO > 1 ? g.mix[h * RO + o] : 1.0f) : 0.0f;
+  const int nck = (T + CK - 1) / CK;
+  float ds[CPL];
+#pragma unroll
+  for (int j = 0; j < CPL; ++j) ds[j] = g.dstate ? g.dstate[((size_t)chain * dv + v) * dk + c0 + j] : 0.0f;
+  auto ck_ptr = [&](int k) { return g.ckpt + (((size_t)chain * (nck + 1) + k) * dv + v) * dk + c0; };
+  float ckn[CPL];
+  if (nck > 0) {
+    const float* ck = ck_ptr(nck - 1);
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) ckn[j] = ck[j];
+  }
+  // operands of one token for this lane's row
+  struct Tok {
+    float a[CPL], K[R][CPL], Kt[R][CPL], w[R], T[R][R];
+  };
+  auto load = [&](Tok& x, const float* rec) {
+    lds_vec<CPL>(rec + L.oA + c0, x.a);
+    float G2[R][R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float bg[CPL];
+      lds_vec<CPL>(rec + L.oK + r * dk + c0, x.K[r]);
+      lds_vec<CPL>(rec + L.oBg + r * dk + c0, bg);
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) x.Kt[r][j] = bg[j] * x.K[r][j];
+      x.w[r] = rec[L.oW + r * dv + v] * rec[L.oV + r * dv + v];
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int r2 = r; r2 < R; ++r2) {
+        float d = 0.0f;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) d += x.Kt[r][j] * x.Kt[r2][j];
+        G2[r][r2] = G2[r2][r] = row_sum16(d);
+      }
+    tfactor<R>(G2, g.eps, x.T);
+  };
+  // s (state before the token) -> s after it; p, z the erase projections
+  auto step = [&](float st[CPL], const Tok& x, float p[R], float z[R]) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) st[j] *= x.a[j];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float d = 0.0f;
+#pragma unroll
+      for (int j = 0; j < CPL; ++j) d += st[j] * x.Kt[r][j];
+      p[r] = row_sum16(d);
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float d = 0.0f;
+#pragma unroll
+      for (int r2 = 0; r2 < R; ++r2) d += p[r2] * x.T[r2][r];
+      z[r] = d;
+    }
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) {
+      float d = st[j];
+#pragma unroll
+      for (int r = 0; r < R; ++r) d += x.w[r] * x.K[r][j] - z[r] * x.Kt[r][j];
+      st[j] = d;
+    }
+  };
+
+  const int nch = (T + C - 1) / C;
+  Stager stg;
+  if (nch > 0) {
+    const int t0 = (nch - 1) * C;
+    stg.fetch(g, L, R, chain, t0, T - t0, true);
+    stg.commit(lds + ((nch - 1) & 1) * C * L.stride, g, L, R, true);
+  }
+  __syncthreads();
+  for (int c = nch - 1; c >= 0; --c) {
+    const int t0 = c * C, ntok = min(C, T - t0);
+    const float* buf = lds + (c & 1) * C * L.stride;
+    if (c > 0) stg.fetch(g, L, R, chain, t0 - C, C, true);
+    const int nsub = (ntok + CK - 1) / CK;
+    for (int sc = nsub - 1; sc >= 0; --sc) {
+      const int u0 = sc * CK, nu = min(CK, ntok - u0);
+      float S0[CK][CPL];
+      {
+        const int k = (t0 + u0) / CK;
+#pragma unroll
+        for (int j = 0; j < CPL; ++j) S0[0][j] = ckn[j];
+        if (k > 0) {
+          const float* ck = ck_ptr(k - 1);
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) ckn[j] = ck[j];
+        }
+      }
+#pragma unroll
+      for (int u = 1; u < CK; ++u) {
+        if (u < nu) {
+          Tok x;
+          load(x, buf + (u0 + u - 1) * L.stride);
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) S0[u][j] = S0[u - 1][j];
+          float p[R], z[R];
+          step(S0[u], x, p, z);
+        }
+      }
+#pragma unroll
+      for (int u = CK - 1; u >= 0; --u) {
+        if (u < nu) {
+          const float* rec = buf + (u0 + u) * L.stride;
+          const int t = t0 + u0 + u;
+          const size_t tok = ((size_t)b * T + t) * g.H + h;
+          Tok x;
+          load(x, rec);
+          float s1[CPL], s3[CPL], p[R], z[R];
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            s1[j] = S0[u][j] * x.a[j];
+            s3[j] = S0[u][j];
+          }
+          step(s3, x, p, z);
+          const float dyv = rec[L.oDy + v];
+          float gcol[CPL];
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) gcol[j] = dyv * s3[j];
+#pragma unroll
+          for (int o = 0; o < 4; ++o) {
+            if (o < RO) {
+              float qv[CPL];
+              lds_vec<CPL>(rec + L.oQ + o * dk + c0, qv);
+#pragma unroll
+              for (int j = 0; j < CPL; ++j) ds[j] += mix[o] * dyv * qv[j];
+            }
+          }
+          float pK[R][CPL], pKt[R][CPL], dz[R], dp[R], dT[R][R];
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float d = 0.0f, e = 0.0f;
+#pragma unroll
+            for (int j = 0; j < CPL; ++j) {
+              d += ds[j] * x.K[r][j];
+              e += ds[j] * x.Kt[r][j];
+              pK[r][j] = x.w[r] * ds[j];
+              pKt[r][j] = -z[r] * ds[j];
+            }
+            const float dw = row_sum16(d);
+            dz[r] = -row_sum16(e);
+            if (l16 == 0) {
+              const float vv = rec[L.oV + r * dv + v], gw = rec[L.oW + r * dv + v];
+              g.dV[(tok * R + r) * dv + v] = dw * gw;
+              g.dWg[(tok * R + r) * dv + v] = dw * vv;
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            float d = 0.0f;
+#pragma unroll
+            for (int r2 = 0; r2 < R; ++r2) d += dz[r2] * x.T[r][r2];
+            dp[r] = d;
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int r2 = 0; r2 < R; ++r2) dT[r][r2] = l16 == 0 ? p[r] * dz[r2] : 0.0f;
+          float pa[CPL];
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            float d1 = ds[j];
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              pKt[r][j] += dp[r] * s1[j];
+              d1 += dp[r] * x.Kt[r][j];
+            }
+            pa[j] = d1 * S0[u][j];
+            ds[j] = d1 * x.a[j];
+          }
+          // the wave's four rows -> LDS
+          float* rp = red + ((size_t)wave * CK + u) * PL;
+#pragma unroll
+          for (int j = 0; j < CPL; ++j) {
+            const float v0 = cross_rows4(gcol[j]);
+            const float v1 = cross_rows4(pa[j]);
+            if (dr == 0) {
+              rp[c0 + j] = v0;
+              rp[(1 + 2 * R) * dk + c0 + j] = v1;
+            }
+#pragma unroll
+            for (int r = 0; r < R; ++r) {
+              const float w0 = cross_rows4(pK[r][j]);
+              const float w1 = cross_rows4(pKt[r][j]);
+              if (dr == 0) {
+                rp[(1 + r) * dk + c0 + j] = w0;
+                rp[(1 + R + r) * dk + c0 + j] = w1;
+              }
+            }
+          }
+#pragma unroll
+          for (int r = 0; r < R; ++r)
+#pragma unroll
+            for (int r2 = 0; r2 < R; ++r2) {
+              const float xx = cross_rows4(dT[r][r2]);
+              if (lane == 0) rp[(2 + 2 * R) * dk + r * R + r2] = xx;
+            }
+        }
+      }
+      __syncthreads();
+      // this row block's partials of the sub-chunk's tokens, waves summed in order
+      for (int e = tid; e < nu * PL; e += 256) {
+        const int u = e / PL, xi = e - u * PL;
+        const float* rp = red + (size_t)u * PL + xi;
+        const size_t wstride = (size_t)CK * PL;
+        g.part[(((size_t)chain * G + rb) * T + t0 + u0 + u) * PL + xi] =
+            (rp[0] + rp[wstride]) + (rp[2 * wstride] + rp[3 * wstride]);
+      }
+      __syncthreads();
+    }
+    if (c > 0) stg.commit(lds + ((c - 1) & 1) * C * L.stride, g, L, R, true);
+    __syncthreads();
+  }
+  if (g.dstate0) {
+#pragma unroll
+    for (int j = 0; j < CPL; ++j) g.dstate0[((size_t)chain * dv + v) * dk + c0 + j] = ds[j];
+  }
+}
+
+// Column gradients from the row-block partials: one workgroup per (chain,
+// block of kRedTok tokens); per token the T-factor is recomputed from K, Bg
+// and dT = sum of the blocks' p^T dz turns into dM = -T dT T.
+constexpr int kRedTok = 16;
+
+template <int R>
+__global__ __launch_bounds__(256) void rls_bwd_reduce_kernel(RlsArgs g) {
+  __shared__ float Tm[kRedTok][R * R], dTm[kRedTok][R * R], red[256];
+  const int tid = threadIdx.x;
+  const int nblk = (g.T + kRedTok - 1) / kRedTok;
+  const int chain = blockIdx.x / nblk, blk = blockIdx.x % nblk;
+  const int b = chain / g.H, h = chain % g.H;
+  const int dk = g.dk, T = g.T, RO = g.RO, G = g.dv / 16;
+  const int PL = part_len(R, dk);
+  const int t0 = blk * kRedTok, nt = min(kRedTok, T - t0);
+  // per token: the Gram of the erase keys and the row blocks' dT
+  if (tid < nt) {
+    const int t = t0 + tid;
+    const size_t tok = ((size_t)b * T + t) * g.H + h;
+    float Gm[R][R], Tf[R][R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int r2 = r; r2 < R; ++r2) {
+        float d = 0.0f;
+        for (int c = 0; c < dk; ++c) {
+          const float x1 = g.Bg[(tok * R + r) * dk + c] * g.K[(tok * R + r) * dk + c];
+          const float x2 = g.Bg[(tok * R + r2) * dk + c] * g.K[(tok * R + r2) * dk + c];
+          d += x1 * x2;
+        }
+        Gm[r][r2] = Gm[r2][r] = d;
+      }
+    tfactor<R>(Gm, g.eps, Tf);
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int r2 = 0; r2 < R; ++r2) {
+        float d = 0.0f;
+        for (int k = 0; k < G; ++k)
+          d += g.part[(((size_t)chain * G + k) * T + t) * PL + (2 + 2 * R) * dk + r * R + r2];
+        dTm[tid][r * R + r2] = d;
+        Tm[tid][r * R + r2] = Tf[r][r2];
+      }
+  }
+  __syncthreads();
+  float mixacc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  float mixv[4];
+#pragma unroll
+  for (int o = 0; o < 4; ++o) mixv[o] = o < RO ? (RO > 1 ? g.mix[h * RO + o] : 1.0f) : 0.0f;
+  for (int e = tid; e < nt * dk; e += 256) {
+    const int u = e / dk, col = e - u * dk;
+    const int t = t0 + u;
+    const size_t tok = ((size_t)b * T + t) * g.H + h;
+    float gs = 0.0f, pa = 0.0f, pK[R], pKt[R];
+#pragma unroll
+    for (int r = 0; r < R; ++r) pK[r] = pKt[r] = 0.0f;
+    for (int k = 0; k < G; ++k) {
+      const float* pp = g.part + (((size_t)chain * G + k) * T + t) * PL;
+      gs += pp[col];
+      pa += pp[(1 + 2 * R) * dk + col];
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        pK[r] += pp[(1 + r) * dk + col];
+        pKt[r] += pp[(1 + R + r) * dk + col];
+      }
+    }
+    float dM[R][R];
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int r2 = 0; r2 < R; ++r2) {
+        float x = 0.0f;
+#pragma unroll
+        for (int m = 0; m < R; ++m)
+#pragma unroll
+          for (int n = 0; n < R; ++n) x += Tm[u][r * R + m] * dTm[u][m * R + n] * Tm[u][n * R + r2];
+        dM[r][r2] = -x;
+      }
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float dkt = pKt[r];
+#pragma unroll
+      for (int r2 = 0; r2 < R; ++r2)
+        dkt += (dM[r][r2] + dM[r2][r]) * g.Bg[(tok * R + r2) * dk + col] * g.K[(tok * R + r2) * dk + col];
+      const float kk = g.K[(tok * R + r) * dk + col], bg = g.Bg[(tok * R + r) * dk + col];
+      g.dBg[(tok * R + r) * dk + col] = dkt * kk;
+      g.dK[(tok * R + r) * dk + col] = pK[r] + dkt * bg;
+    }
+#pragma unroll
+    for (int o = 0; o < 4; ++o) {
+      if (o < RO) {
+        g.dq[(tok * RO + o) * dk + col] = mixv[o] * gs;
+        mixacc[o] += g.q[(tok * RO + o) * dk + col] * gs;
+      }
+    }
+    g.da[tok * dk + col] = pa;
+  }
+#pragma unroll
+  for (int o = 0; o < 4; ++o) {
+    if (o < RO) {
+      red[tid] = mixacc[o];
+      __syncthreads();
+      if (tid == 0) {
+        float x = 0.0f;
+        for (int k = 0; k < 256; ++k) x += red[k];
+        g.mixpart[((size_t)chain * nblk + blk) * RO + o] = x;
+      }
+      __syncthreads();
+    }
+  }
+}
+
+__global__ void rls_mix_sum_kernel(RlsArgs g, int nblk) {
+  const int e = blockIdx.x * blockDim.x + threadIdx.x;
+  if (e >= g.B * g.H * g.RO) return;
+  const int chain = e / g.RO, o = e % g.RO;
+  float x = 0.0f;
+  for (int k = 0; k < nblk; ++k) x += g.mixpart[((size_t)chain * nblk + k) * g.RO + o];
+  g.dmix[e] = x;
+}
+
+// ---------------------------------------------------------------------------
 // host side
 // ---------------------------------------------------------------------------
 // checkpoint interval: the backward keeps CK states per lane in registers; a
@@ -1044,6 +1412,44 @@ static int launch_rls(const RlsArgs& a0, bool bwd, hipStream_t stream) {
     hipLaunchKernelGGL(k, dim3(nchains * (unsigned)(a.dv / 16)), dim3(256), lds, stream, a);
     return check_launch("rls_fwd_rb_kernel");
   }
+  if (bwd && !a.cP && a.part) {
+    // row blocks of 16 value rows: chunk records + the waves' partials in LDS
+    const int strideb = (2 * R + 1 + a.RO) * a.dk + 2 * R * a.dv + a.dv;
+    const size_t red = (size_t)4 * a.CK * part_len(R, a.dk) * 4;
+    int C = 0;
+    size_t lds = 0;
+    for (int pass = 0; pass < 2 && C == 0; ++pass)
+      for (int c = 32; c >= a.CK; c >>= 1) {
+        const size_t l = (size_t)2 * c * strideb * 4 + red;
+        if (l <= 156 * 1024 && (pass == 1 || c * (strideb / 4) <= kMaxPre * 256)) {
+          C = c;
+          lds = l;
+          break;
+        }
+      }
+    if (C == 0) return set_error(GDNX_ERR_SHAPE, "RLS backward: record too large for LDS");
+    a.C = C;
+    const unsigned G = (unsigned)(a.dv / 16);
+    if (a.CK == 2) {
+      auto k = rls_bwd_rb_kernel<CPL, R, 2>;
+      if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return set_error(GDNX_ERR_HIP, "rls_bwd_rb_kernel: cannot reserve %zu bytes of LDS", lds);
+      hipLaunchKernelGGL(k, dim3(nchains * G), dim3(256), lds, stream, a);
+    } else {
+      auto k = rls_bwd_rb_kernel<CPL, R, 4>;
+      if (hipFuncSetAttribute((const void*)k, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds) != hipSuccess)
+        return set_error(GDNX_ERR_HIP, "rls_bwd_rb_kernel: cannot reserve %zu bytes of LDS", lds);
+      hipLaunchKernelGGL(k, dim3(nchains * G), dim3(256), lds, stream, a);
+    }
+    int rc = check_launch("rls_bwd_rb_kernel");
+    if (rc != GDNX_OK) return rc;
+    const int nblk = (a.T + kRedTok - 1) / kRedTok;
+    hipLaunchKernelGGL((rls_bwd_reduce_kernel<R>), dim3(nchains * (unsigned)nblk), dim3(256), 0, stream, a);
+    rc = check_launch("rls_bwd_reduce_kernel");
+    if (rc != GDNX_OK) return rc;
+    hipLaunchKernelGGL(rls_mix_sum_kernel, dim3((nchains * a.RO + 255) / 256), dim3(256), 0, stream, a, nblk);
+    return check_launch("rls_mix_sum_kernel");
+  }
   const RlsGeom G = rls_geom(R, a0.RO, a0.dk, a0.dv, bwd, a0.cP, a0.cR);
   if (G.C == 0) return set_error(GDNX_ERR_SHAPE, "RLS scan: R=%d, R_out=%d, key_dim=%d, value_dim=%d do not fit LDS",
                                  R, a0.RO, a0.dk, a0.dv);
@@ -1081,6 +1487,12 @@ static int launch_rls_r(const RlsArgs& a, int R, bool bwd, hipStream_t stream) {
 
 }  // namespace
 
+size_t rls_bwd_workspace_bytes(int nchains, int T, int R, int dk, int dv) {
+  const size_t part = (size_t)nchains * (dv / 16) * T * part_len(R, dk);
+  const size_t mix = (size_t)nchains * ((T + kRedTok - 1) / kRedTok) * 4;
+  return (part + mix) * sizeof(float) + 256;
+}
+
 size_t rls_ckpt_bytes(int nchains, int T, int R, int dk, int dv, int cP) {
   const int CK = rls_ck(dk, R, cP);
   return (size_t)nchains * ((T + CK - 1) / CK + 1) * dv * dk * sizeof(float);
@@ -1094,6 +1506,10 @@ int rls_dispatch(const RlsDesc& d, bool bwd, hipStream_t stream) {
   a.dmix = d.dmix; a.dstate0 = d.dstate0;
   a.B = d.B; a.T = d.T; a.H = d.H; a.RO = d.RO; a.dk = d.dk; a.dv = d.dv; a.eps = d.eps;
   a.cP = d.cP; a.cR = d.cR; a.cs = d.cs; a.ste = d.ste;
+  if (d.workspace && !d.cP) {
+    a.part = (float*)d.workspace;
+    a.mixpart = a.part + (size_t)(d.B * d.H) * (d.dv / 16) * d.T * part_len(d.R, d.dk);
+  }
   if (d.T == 0) return GDNX_OK;
   switch (d.dk) {
     case 32: return launch_rls_r<2>(a, d.R, bwd, stream);

@@ -123,10 +123,14 @@ class _RLSScan(torch.autograd.Function):
         dmix = torch.empty(B, H, RO, dtype=torch.float32, device=dev)
         ds0 = torch.empty(B, H, vd, kd, dtype=torch.float32, device=dev) if has_s0 else None
         mix = out_mix.float().contiguous() if RO > 1 else None
+        ws = None
+        if not cP:   # value rows spread over workgroups, column sums reduced by a second kernel
+            n = lib.gdnx_rls_bwd_workspace_bytes(B, T, H, R, kd, vd)
+            ws = torch.empty(max(n, 16), dtype=torch.uint8, device=dev)
         with torch.cuda.device(dev):
             rc = lib.gdnx_rls_bwd(*map(_lib.ptr, (q_, K_, V_, Bg_, Wg_, a_, mix, ck, dy_, dst, *outs, dmix, ds0)),
                                   B, T, H, R, RO, kd, vd, eps, int(cP), int(cR), float(sd), int(bool(ste)),
-                                  _lib.stream_of(q_))
+                                  _lib.ptr(ws), _lib.stream_of(q_))
         _lib.check(rc, "gdnx_rls_bwd")
         dq, dK, dV, dBg, dWg, da = outs
         dq, dK, dBg, da = (t[..., :dk] for t in (dq, dK, dBg, da))

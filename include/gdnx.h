@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 6
+#define GDNX_ABI_VERSION 7
 
 enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1 };
 
@@ -413,13 +413,18 @@ int gdnx_rls_fwd(const float* q, const float* K, const float* V, const float* Bg
  * state's.  Through a compaction the gradient is the testbed's: the truncation
  * carries none (it runs under no_grad), so the state's gradient is scaled by
  * 1 - slow_decay; with straight_through != 0 it passes unchanged (the
- * testbed's compact_ste).  Deterministic. */
+ * testbed's compact_ste).  Deterministic.  Without compaction and with a
+ * workspace (gdnx_rls_bwd_workspace_bytes) the value rows are spread over
+ * workgroups (16 rows each) and the column sums reduced by a second kernel;
+ * with workspace NULL (or with compaction) one workgroup runs each chain. */
+long long gdnx_rls_bwd_workspace_bytes(int B, int T, int H, int R, int key_dim, int value_dim);
+
 int gdnx_rls_bwd(const float* q, const float* K, const float* V, const float* Bg, const float* Wg,
                  const float* a, const float* out_mix, const float* ckpt, const float* dy,
                  const float* d_state, float* dq, float* dK, float* dV, float* dBg, float* dWg,
                  float* da, float* d_out_mix_seq, float* d_state0, int B, int T, int H, int R,
                  int R_out, int key_dim, int value_dim, float eps, int compact_P, int compact_R,
-                 float slow_decay, int straight_through, void* stream);
+                 float slow_decay, int straight_through, void* workspace, void* stream);
 
 #ifdef __cplusplus
 }
