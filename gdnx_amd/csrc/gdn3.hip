@@ -60,7 +60,7 @@ struct G3Compact {
   alignas(16) double us[kRMax][kMN];      // leading left singular vectors of R_mat
   alignas(16) double vs[kRMax][kMN];      // leading right singular vectors
   double red[4 * 64];
-  double rinv[kQ * kQ];                   // R^{-1} of the Cholesky QR (row-major, upper)
+  double rinv[kQ * kQ];                   // R of the Cholesky QR (row-major, upper; 1 / R[i][i] on the diagonal)
   double ev[kQ * kQ];                     // eigenvectors of Bm Bm^T (columns)
   double lam[kQ];
   double sig[kRMax];
@@ -76,52 +76,75 @@ typedef double f64x4 __attribute__((ext_vector_type(4)));
 // supplies A[l%16][l/16] and B[l/16][l%16] and holds D[l/16 + 4e][l%16]).
 // A is R_mat (fp32, row stride ldr) read as is (TRANS = false, M = m, K = n)
 // or transposed (TRANS = true, M = n, K = m); B and C are rows of kQ, B fp32
-// or fp64; the 16-column tile carries kQ = 8 live columns.
-template <bool TRANS, typename BT>
-__device__ __forceinline__ void rm_mfma(const float* rm, int ldr, int M, int K, const BT* b, double* c,
-                                        int tid) {
+// or fp64; the 16-column tile carries kQ = 8 live columns.  Wave w owns the
+// 16-row tiles w, w + 4, ...; the k loop is unrolled so that the operand
+// loads of later steps are issued under the MFMAs of earlier ones.  A wave
+// with one tile keeps 4 accumulator chains, one with several keeps one chain
+// per tile (the B operand of a step is shared by its tiles).
+template <bool TRANS, int M, int K, typename BT>
+__device__ __forceinline__ void rm_mfma(const float* rm, int ldr, const BT* b, double* c, int tid) {
+  static_assert(M % 64 == 0 && K % 16 == 0, "whole 16-row tiles on 4 waves, 16 k per step");
+  constexpr int TPW = M / 64, NA = TPW >= 4 ? 1 : 4 / TPW;
   const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, n16 = lane & 15;
   const bool live = n16 < kQ;
   const int bcol = live ? n16 : 0;
-  for (int mt = wave; mt < M / 16; mt += 4) {
-    f64x4 acc[4];
+  f64x4 acc[TPW][NA];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) acc[u] = (f64x4){0.0, 0.0, 0.0, 0.0};
-    const int row = mt * 16 + n16;
-    // 16 k per step: the 8 operand loads of a step are issued together
-    for (int kb = 0; kb < K; kb += 16) {
-      double a[4], bb[4];
+  for (int t = 0; t < TPW; ++t)
 #pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const int k = kb + 4 * u + g;
-        a[u] = TRANS ? rm[k * ldr + row] : rm[row * ldr + k];
-        bb[u] = (double)b[k * kQ + bcol];
+    for (int u = 0; u < NA; ++u) acc[t][u] = (f64x4){0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int kb = 0; kb < K; kb += 16) {
+    double a[TPW][4], bb[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int k = kb + 4 * u + g;
+      const double bv = (double)b[k * kQ + bcol];
+      bb[u] = live ? bv : 0.0;
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int row = (wave + 4 * t) * 16 + n16;
+        a[t][u] = TRANS ? rm[k * ldr + row] : rm[row * ldr + k];
       }
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        acc[u] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[u], live ? bb[u] : 0.0, acc[u], 0, 0, 0);
     }
-    if (live)
 #pragma unroll
-      for (int e = 0; e < 4; ++e)
-        c[(mt * 16 + g + 4 * e) * kQ + n16] = (acc[0][e] + acc[1][e]) + (acc[2][e] + acc[3][e]);
+    for (int u = 0; u < 4; ++u)
+#pragma unroll
+      for (int t = 0; t < TPW; ++t)
+        acc[t][u % NA] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[t][u], bb[u], acc[t][u % NA], 0, 0, 0);
   }
+  if (live)
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        double v = acc[t][0][e];
+        if constexpr (NA == 4) v = (acc[t][0][e] + acc[t][1][e]) + (acc[t][2][e] + acc[t][3][e]);
+        c[((wave + 4 * t) * 16 + g + 4 * e) * kQ + n16] = v;
+      }
 }
 
 // Jacobi rotation zeroing a_pq (Numerical Recipes convention):
-// J[p][p] = J[q][q] = c, J[p][q] = s, J[q][p] = -s.
+// J[p][p] = J[q][q] = c, J[p][q] = s, J[q][p] = -s, with the smaller angle
+// t = sgn(th) / (|th| + sqrt(th^2 + 1)), th = (a_qq - a_pp) / (2 a_pq).
+// Multiplying through by |2 a_pq| gives it without divisions: with
+// d = a_qq - a_pp, e = 2 a_pq, h = sqrt(d^2 + e^2) and w = |d| + h,
+// t = sgn(th) |e| / w, so c = w / sqrt(w^2 + e^2), s = sgn(th) |e| / sqrt(w^2 + e^2)
+// (c^2 + s^2 = 1 by construction).
 __device__ __forceinline__ void jacobi_rot(double app, double aqq, double apq, double& c, double& s) {
-  if (apq == 0.0) {
-    c = 1.0;
-    s = 0.0;
-    return;
-  }
-  const double th = (aqq - app) / (2.0 * apq);
-  double t;
-  if (fabs(th) > 1e150) t = 0.5 / th;
-  else t = (th >= 0.0 ? 1.0 : -1.0) / (fabs(th) + sqrt(th * th + 1.0));
-  c = rsqrt(t * t + 1.0);
-  s = t * c;
+  // selects only (no branches), so the two rotations a lane forms per round
+  // interleave; sqrt(x) is taken as x rsqrt(max(x, DBL_MIN)), 0 at x = 0
+  const double d = aqq - app, e = 2.0 * apq;
+  const double x = fma(d, d, e * e);
+  const double h = x * rsqrt(fmax(x, 2.2250738585072014e-308));
+  const double w = fabs(d) + h;
+  const double q = fma(w, w, e * e);
+  const double r = rsqrt(q);
+  // sgn(th) |e| = sgn(d) e for d != 0, and |e| for d == 0 (th = +-0 counts as >= 0)
+  const double num = d == 0.0 ? fabs(e) : (d > 0.0 ? e : -e);
+  const bool ok = q > 0.0;  // false only when a_pq = 0 and a_pp = a_qq (or both underflow)
+  c = ok ? w * r : 1.0;
+  s = ok ? num * r : 0.0;
 }
 
 // Round-robin (circle method) partner of index x in round st of 7 for 8 indices.
@@ -131,26 +154,62 @@ __device__ __forceinline__ int rr_partner(int x, int st) {
   return (2 * st - x + 14) % 7;
 }
 
+// Partial Gram X^T X of NR rows of X (rows of kQ doubles) on fp64 MFMA: lane
+// l supplies X[k][l % 16] (zero for columns >= kQ) both as A[l % 16][l / 16]
+// of A = X^T and as B[l / 16][l % 16]; it returns G[l / 16 + 4e][l % 16] in
+// element e (rows and columns < kQ = 8 live, so e = 0, 1).
+template <int NR>
+__device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
+  static_assert(NR % 4 == 0, "4 rows per MFMA step");
+  const int g = lane >> 4, n16 = lane & 15;
+  f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int k = 0; k < NR; k += 4) {
+    const double v = x[(k + g) * kQ + (n16 & (kQ - 1))];
+    const double vl = n16 < kQ ? v : 0.0;
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(vl, vl, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// Sum over the 64 lanes of a wave, the same bits in every lane: DPP row
+// rotations by 8, 4, 2, 1 (a butterfly inside each 16-lane row, so all lanes
+// of a row form the same sum), then across the four rows.
+template <int CTL>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const long long b = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(b & 0xffffffffll), CTL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTL, 0xf, 0xf, false);
+  return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+__device__ __forceinline__ double wave_sum_f64(double x) {
+  x += dpp_f64<0x128>(x);
+  x += dpp_f64<0x124>(x);
+  x += dpp_f64<0x122>(x);
+  x += dpp_f64<0x121>(x);
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
 // Y <- Y R^{-1} with Y^T Y = R^T R (Cholesky QR, `passes` times: one pass
 // keeps the intermediate power-iteration bases well conditioned, the final
 // basis takes two).  Columns whose pivot falls below 1e-24 of the largest
-// diagonal are set to zero.
-template <int D, int P>
-__device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int m, int tid, int passes) {
+// diagonal are set to zero.  The Gram runs on fp64 MFMA over 4 row segments;
+// each row of Y is then solved against R by forward substitution.
+template <int D, int P, int M>
+__device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int tid, int passes) {
+  static_assert(M % 16 == 0 && M <= kNT, "rows: 4 segments of whole MFMA steps, one row per thread");
   const int lane = tid & 63, wave = tid >> 6;
-  const int seg = (m + 3) / 4;
+  constexpr int seg = M / 4;
   for (int pass = 0; pass < passes; ++pass) {
-    {  // Gram, 4 row segments
-      const int i = lane >> 3, j = lane & 7;
-      const int r0 = wave * seg, r1 = min(m, r0 + seg);
-      double s0 = 0.0, s1 = 0.0;
-      int row = r0;
-      for (; row + 1 < r1; row += 2) {
-        s0 += cs.y[row * kQ + i] * cs.y[row * kQ + j];
-        s1 += cs.y[(row + 1) * kQ + i] * cs.y[(row + 1) * kQ + j];
+    {
+      const f64x4 g = gram_mfma<seg>(cs.y + wave * seg * kQ, lane);
+      const int r = lane >> 4, c = lane & 15;
+      if (c < kQ) {
+        cs.red[wave * 64 + r * kQ + c] = g[0];
+        cs.red[wave * 64 + (r + 4) * kQ + c] = g[1];
       }
-      if (row < r1) s0 += cs.y[row * kQ + i] * cs.y[row * kQ + j];
-      cs.red[wave * 64 + lane] = s0 + s1;
     }
     __syncthreads();
     if (wave == 0) {
@@ -161,7 +220,7 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int m, int tid, i
       for (int k = 0; k < kQ; ++k) dmax = fmax(dmax, __shfl(a, 9 * k, 64));
       const double tol = dmax * 1e-24;
       // right-looking Cholesky, lane (i, j) holds entry (i, j); column k
-      // becomes L[:, k] at step k
+      // becomes L[:, k] at step k (only the lower triangle is read)
 #pragma unroll
       for (int k = 0; k < kQ; ++k) {
         const double akk = __shfl(a, 9 * k, 64);
@@ -170,38 +229,28 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int m, int tid, i
         const double rd = (akk > tol && akk > 0.0) ? rsqrt(akk) : 0.0;
         const double lik = aik * rd, ljk = ajk * rd;
         if (i > k && j > k) a -= lik * ljk;
-        if (j == k && i >= k) a = lik;  // lik = sqrt(akk) on the diagonal
+        if (j == k && i >= k) a = lik;  // lik = sqrt(akk) on the diagonal, 0 for a dropped column
       }
-      double l = (j <= i) ? a : 0.0;  // L[i][j]
-      // R = L^T is upper triangular; invert it column by column: lane
-      // (i, j) computes Rinv[i][j] = (delta_ij - sum_{i<k<=j} R[i][k] Rinv[k][j]) / R[i][i]
-      // row by row from the bottom, all on shuffles
-      const double rij = __shfl(l, 8 * j + i, 64);  // R[i][j] = L[j][i]
-      const double rii = __shfl(l, 9 * i, 64);
-      const double rdi = rii > 0.0 ? 1.0 / rii : 0.0;
-      double x = (i == j) ? rdi : 0.0;  // row i of Rinv, computed for i = 7 .. 0
-#pragma unroll
-      for (int r = kQ - 1; r >= 0; --r) {
-        // rows > r are final; row r: x[r][j] = (delta - sum_{k>r} R[r][k] x[k][j]) / R[r][r]
-        double acc = 0.0;
-#pragma unroll
-        for (int k = r + 1; k < kQ; ++k) acc += __shfl(rij, 8 * r + k, 64) * __shfl(x, 8 * k + j, 64);
-        if (i == r) x = (j >= r) ? ((j == r ? 1.0 : 0.0) - acc) * rdi : 0.0;
-      }
-      cs.rinv[lane] = x;
+      // R = L^T (upper), row-major; its diagonal holds 1 / R[i][i] (0 for a
+      // dropped column)
+      if (j < i) cs.rinv[j * kQ + i] = a;
+      if (j == i) cs.rinv[i * kQ + i] = a > 0.0 ? 1.0 / a : 0.0;
     }
     __syncthreads();
-    if (tid < m) {
-      double yr[kQ];
+    if (tid < M) {
+      double x[kQ];
 #pragma unroll
-      for (int j = 0; j < kQ; ++j) yr[j] = cs.y[tid * kQ + j];
+      for (int j = 0; j < kQ; ++j) x[j] = cs.y[tid * kQ + j];
+      // x R = y, column by column: x_j = (y_j - sum_{i<j} x_i R[i][j]) / R[j][j]
 #pragma unroll
       for (int j = 0; j < kQ; ++j) {
-        double s = 0.0;
+        double s = x[j];
 #pragma unroll
-        for (int i = 0; i <= j; ++i) s += yr[i] * cs.rinv[i * kQ + j];
-        cs.y[tid * kQ + j] = s;
+        for (int i = 0; i < j; ++i) s -= x[i] * cs.rinv[i * kQ + j];
+        x[j] = s * cs.rinv[j * kQ + j];
       }
+#pragma unroll
+      for (int j = 0; j < kQ; ++j) cs.y[tid * kQ + j] = x[j];
     }
     __syncthreads();
   }
@@ -225,9 +274,14 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
   float* Bv = ab + R * m;
   const int lane = tid & 63, wave = tid >> 6;
 
-  for (int e = tid; e < n * kQ; e += kNT) {
-    const int c = e / kQ, j = e % kQ;
-    cs.gs[e] = j < q ? sketch[c * q + j] : 0.f;
+  // the sketch's global loads are issued first and land in LDS after the
+  // residual part (which does not read them)
+  constexpr int NGS = (n * kQ + kNT - 1) / kNT;
+  float gsv[NGS];
+#pragma unroll
+  for (int u = 0; u < NGS; ++u) {
+    const int e = tid + u * kNT, c = e / kQ, j = e % kQ;
+    gsv[u] = (e < n * kQ && j < q) ? sketch[c * q + j] : 0.f;
   }
   // residual part rearrange(U Vb^T), 4x4 register blocks over (v, k)
   for (int blk = tid; blk < (D / 4) * (D / 4); blk += kNT) {
@@ -256,6 +310,11 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
       }
     }
   }
+#pragma unroll
+  for (int u = 0; u < NGS; ++u) {
+    const int e = tid + u * kNT;
+    if (e < n * kQ) cs.gs[e] = gsv[u];
+  }
   __syncthreads();
   // Kronecker part (A, B each decayed by e^{gacc}) and the energy |R_mat|^2
   const float sc2 = expf(2.f * gacc);
@@ -282,50 +341,51 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
 
   // range finder with two power iterations; orthonormalising between the
   // products leaves the final basis unchanged (up to column signs)
-  rm_mfma<false>(cs.rm, ldr, m, n, cs.gs, cs.y, tid);
+  rm_mfma<false, m, n>(cs.rm, ldr, cs.gs, cs.y, tid);
   __syncthreads();
-  orth_rows(cs, m, tid, 1);
+  orth_rows<D, P, m>(cs, tid, 1);
   for (int it = 0; it < 2; ++it) {
-    rm_mfma<true>(cs.rm, ldr, n, m, cs.y, cs.z, tid);
+    rm_mfma<true, n, m>(cs.rm, ldr, cs.y, cs.z, tid);
     __syncthreads();
-    rm_mfma<false>(cs.rm, ldr, m, n, cs.z, cs.y, tid);
+    rm_mfma<false, m, n>(cs.rm, ldr, cs.z, cs.y, tid);
     __syncthreads();
-    orth_rows(cs, m, tid, it == 1 ? 2 : 1);
+    orth_rows<D, P, m>(cs, tid, it == 1 ? 2 : 1);
   }
   // Bm^T = R_mat^T Q  [n][kQ]
-  rm_mfma<true>(cs.rm, ldr, n, m, cs.y, cs.z, tid);
+  rm_mfma<true, n, m>(cs.rm, ldr, cs.y, cs.z, tid);
   __syncthreads();
   // eigen-decomposition of W = Bm Bm^T by cyclic Jacobi in wave 0: lane
-  // (i, j) holds W[i][j] and V[i][j]; the diagonal lane of each index
-  // computes its pair's rotation, the others read it by shuffle
+  // (i, j) holds W[i][j] and V[i][j].  Each round rotates 4 disjoint pairs;
+  // a lane gathers every operand of its round in one exchange and forms the
+  // rotations of both its pairs (that of i and that of j) itself, from the
+  // same entries the lanes of those indices use.
   if (wave == 0) {
     const int i = lane >> 3, j = lane & 7;
-    double a = 0.0;
-    for (int c = 0; c < n; ++c) a += cs.z[c * kQ + i] * cs.z[c * kQ + j];
+    double a;
+    {  // W from the MFMA layout (lane l: W[l/16 + 4e][l%16]), upper entry for both (i, j) and (j, i)
+      const f64x4 w = gram_mfma<n>(cs.z, lane);
+      const int r = min(i, j), c = max(i, j);
+      const double w0 = __shfl(w[0], (r & 3) * 16 + c, 64), w1 = __shfl(w[1], (r & 3) * 16 + c, 64);
+      a = r < 4 ? w0 : w1;
+    }
     double vv = (i == j) ? 1.0 : 0.0;
     for (int sweep = 0; sweep < 12; ++sweep) {
-      double off = (i != j) ? a * a : 0.0, dia = (i == j) ? a * a : 0.0;
-#pragma unroll
-      for (int o2 = 32; o2 > 0; o2 >>= 1) {
-        off += __shfl_xor(off, o2, 64);
-        dia += __shfl_xor(dia, o2, 64);
-      }
+      const double off = wave_sum_f64(i != j ? a * a : 0.0);
+      const double dia = wave_sum_f64(i == j ? a * a : 0.0);
       if (!(off > 1e-28 * dia)) break;  // uniform across the wave
+#pragma unroll
       for (int st = 0; st < 7; ++st) {
-        // rotation of the pair containing index i (meaningful on lane (i, i))
-        const int pp = rr_partner(i, st);
-        const int p0 = min(i, pp), p1 = max(i, pp);
-        double c, sn;
-        jacobi_rot(__shfl(a, 9 * p0, 64), __shfl(a, 9 * p1, 64), __shfl(a, 8 * p0 + p1, 64), c, sn);
-        // J[x][x] = c; J[partner][x] = -s if x < partner else +s
-        const double xs = (i < pp) ? -sn : sn;
-        const double ci = __shfl(c, 9 * i, 64), xi = __shfl(xs, 9 * i, 64);
-        const double cj = __shfl(c, 9 * j, 64), xj = __shfl(xs, 9 * j, 64);
         const int pi = rr_partner(i, st), pj = rr_partner(j, st);
-        const double a_ipj = __shfl(a, 8 * i + pj, 64);
-        const double a_pij = __shfl(a, 8 * pi + j, 64);
-        const double a_pipj = __shfl(a, 8 * pi + pj, 64);
-        const double v_ipj = __shfl(vv, 8 * i + pj, 64);
+        const int i0 = min(i, pi), i1 = max(i, pi), j0 = min(j, pj), j1 = max(j, pj);
+        const double ai0 = __shfl(a, 9 * i0, 64), ai1 = __shfl(a, 9 * i1, 64), aio = __shfl(a, 8 * i0 + i1, 64);
+        const double aj0 = __shfl(a, 9 * j0, 64), aj1 = __shfl(a, 9 * j1, 64), ajo = __shfl(a, 8 * j0 + j1, 64);
+        const double a_ipj = __shfl(a, 8 * i + pj, 64), a_pij = __shfl(a, 8 * pi + j, 64);
+        const double a_pipj = __shfl(a, 8 * pi + pj, 64), v_ipj = __shfl(vv, 8 * i + pj, 64);
+        double ci, si, cj, sj;
+        jacobi_rot(ai0, ai1, aio, ci, si);
+        jacobi_rot(aj0, aj1, ajo, cj, sj);
+        // J[x][x] = c; J[partner][x] = -s if x < partner else +s
+        const double xi = (i < pi) ? -si : si, xj = (j < pj) ? -sj : sj;
         a = ci * cj * a + ci * xj * a_ipj + xi * cj * a_pij + xi * xj * a_pipj;
         vv = vv * cj + v_ipj * xj;
       }
@@ -880,11 +940,39 @@ __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
   }
   if (p.ab_stash)
     for (int e = tid; e < Rm + Rn; e += kNT) p.ab_stash[(size_t)chain * (Rm + Rn) + e] = sm.ab[e];
-  if (p.skron) {  // sum_r A_r (x) B_r as a [D][D] (v, k) matrix for the next interval's reads
+  if (p.skron) {
+    // sum_r A_r (x) B_r as a [D][D] (v, k) matrix for the next interval's
+    // reads, in blocks: a thread takes one factor entry (iv, ik) (TPP threads
+    // share one, splitting its b_v rows) and writes the entries
+    // (iv b_v + jv, ik b_k + jk) it scales, 8 contiguous k per store
+    constexpr int TPP = kNT / Ge::m, RPT = Ge::bv / TPP;
+    static_assert(kNT % Ge::m == 0 && Ge::bv % TPP == 0 && Ge::bk == 8, "skron blocking");
     CT* sk = (CT*)p.skron + (size_t)chain * D * D;
     const float* Af = sm.ab;
     const float* Bf = sm.ab + Rm;
-    for (int e = tid; e < D * D; e += kNT) sk[e] = from_f<CT>(kron_entry<D>(Af, Bf, e / D, e % D));
+    const int pr = tid / TPP, part = tid % TPP;
+    const int iv = pr / Ge::ak, ik = pr % Ge::ak;
+    float a[Ge::R];
+#pragma unroll
+    for (int r = 0; r < Ge::R; ++r) a[r] = Af[r * Ge::m + pr];
+#pragma unroll
+    for (int jj = 0; jj < RPT; ++jj) {
+      const int jv = part * RPT + jj;
+      float sv[8];
+#pragma unroll
+      for (int jk = 0; jk < 8; ++jk) sv[jk] = 0.f;
+#pragma unroll
+      for (int r = 0; r < Ge::R; ++r) {
+        const f32x4 b0 = *(const f32x4*)&Bf[r * Ge::n + jv * Ge::bk];
+        const f32x4 b1 = *(const f32x4*)&Bf[r * Ge::n + jv * Ge::bk + 4];
+#pragma unroll
+        for (int jk = 0; jk < 4; ++jk) {
+          sv[jk] += a[r] * b0[jk];
+          sv[4 + jk] += a[r] * b1[jk];
+        }
+      }
+      store8(sk + (size_t)(iv * Ge::bv + jv) * D + ik * Ge::bk, sv);
+    }
   }
 }
 
