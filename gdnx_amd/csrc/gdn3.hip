@@ -320,22 +320,34 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
   const float sc2 = expf(2.f * gacc);
   double en[1] = {0.0};
   {
-    // n <= 256 is a power of two: each thread keeps one column
-    const int col = tid & (n - 1), rstep = kNT >> ln;
+    // n <= 256 is a power of two: thread (group, col) updates one column on
+    // the group's block of RPG consecutive rows; the A entries of 4 rows are
+    // one broadcast vector load per factor, the energy runs in 4 chains
+    constexpr int NG = kNT >> ln, RPG = m / NG;
+    static_assert(m % NG == 0 && RPG % 4 == 0, "row blocks of whole 4-row steps");
+    const int col = tid & (n - 1), r0 = (tid >> ln) * RPG;
     float bcol[kRMax];
 #pragma unroll
     for (int r = 0; r < kRMax; ++r) bcol[r] = r < R ? sc2 * Bv[r * n + col] : 0.f;
-    double e0 = 0.0;
-#pragma unroll 4
-    for (int row = tid >> ln; row < m; row += rstep) {
-      float s = cs.rm[row * ldr + col];
+    double e4[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll 2
+    for (int rb = 0; rb < RPG; rb += 4) {
+      const int row = r0 + rb;
+      f32x4 av[kRMax];
 #pragma unroll
       for (int r = 0; r < kRMax; ++r)
-        if (r < R) s += A[r * m + row] * bcol[r];
-      cs.rm[row * ldr + col] = s;
-      e0 += (double)s * (double)s;
+        if (r < R) av[r] = *(const f32x4*)&A[r * m + row];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        float sv = cs.rm[(row + u) * ldr + col];
+#pragma unroll
+        for (int r = 0; r < kRMax; ++r)
+          if (r < R) sv += av[r][u] * bcol[r];
+        cs.rm[(row + u) * ldr + col] = sv;
+        e4[u] += (double)sv * (double)sv;
+      }
     }
-    en[0] = e0;
+    en[0] = (e4[0] + e4[1]) + (e4[2] + e4[3]);
   }
   block_sum<1>(en, cs.red, tid);
 
