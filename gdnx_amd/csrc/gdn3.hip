@@ -283,30 +283,38 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
     const int e = tid + u * kNT, c = e / kQ, j = e % kQ;
     gsv[u] = (e < n * kQ && j < q) ? sketch[c * q + j] : 0.f;
   }
-  // residual part rearrange(U Vb^T), 4x4 register blocks over (v, k)
-  for (int blk = tid; blk < (D / 4) * (D / 4); blk += kNT) {
-    const int v0 = 4 * (blk / (D / 4)), k0 = 4 * (blk % (D / 4));
-    float acc[4][4];
+  // residual part rearrange(U Vb^T) on fp32 MFMA: out[v][k] = sum_p U_p[v] Vb_p[k]
+  // (A[v][p] = U_p[v], B[p][k] = Vb_p[k]); wave w owns the value-row tiles
+  // w VTW .. w VTW + VTW - 1 against every key-column tile, and scatters each
+  // entry to its rearranged place (iv a_k + ik, jv b_k + jk)
+  {
+    constexpr int NT16 = D / 16, VTW = NT16 / 4;
+    static_assert(NT16 % 4 == 0 && P % 16 == 0, "whole 16x16 tiles on 4 waves, 16 window slots per step");
+    const int g4 = lane >> 4, n16 = lane & 15;
 #pragma unroll
-    for (int a = 0; a < 4; ++a)
+    for (int vi = 0; vi < VTW; ++vi) {
+      const int vt = wave * VTW + vi;
+      f32x4 ua[P / 16];
 #pragma unroll
-      for (int b = 0; b < 4; ++b) acc[a][b] = 0.f;
-#pragma unroll 4
-    for (int p = 0; p < P; ++p) {
-      const f32x4 uu = *(const f32x4*)&cs.ut[p][v0];
-      const f32x4 kk = *(const f32x4*)&vbd[p][k0];
+      for (int pb = 0; pb < P / 16; ++pb)
 #pragma unroll
-      for (int a = 0; a < 4; ++a)
+        for (int s4 = 0; s4 < 4; ++s4) ua[pb][s4] = cs.ut[pb * 16 + 4 * g4 + s4][vt * 16 + n16];
+#pragma unroll 2
+      for (int kt = 0; kt < NT16; ++kt) {
+        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int b = 0; b < 4; ++b) acc[a][b] += uu[a] * kk[b];
-    }
+        for (int pb = 0; pb < P / 16; ++pb) {
+          f32x4 kb4;
 #pragma unroll
-    for (int a = 0; a < 4; ++a) {
-      const int v = v0 + a, iv = v >> lbv, jv = v & (Ge::bv - 1);
+          for (int s4 = 0; s4 < 4; ++s4) kb4[s4] = vbd[pb * 16 + 4 * g4 + s4][kt * 16 + n16];
+          mma(acc, ua[pb], kb4);
+        }
+        const int k = kt * 16 + n16, ik = k >> lbk, jk = k & (bk - 1);
 #pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const int k = k0 + b, ik = k >> lbk, jk = k & (bk - 1);
-        cs.rm[(iv * ak + ik) * ldr + jv * bk + jk] = acc[a][b];
+        for (int i = 0; i < 4; ++i) {
+          const int v = vt * 16 + 4 * g4 + i, iv = v >> lbv, jv = v & (Ge::bv - 1);
+          cs.rm[(iv * ak + ik) * ldr + jv * bk + jk] = acc[i];
+        }
       }
     }
   }
@@ -427,65 +435,48 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
       for (int j = 0; j < kQ; ++j) s += cs.y[row * kQ + j] * cs.ev[j * kQ + o];
       cs.us[r][row] = s;
     }
-  for (int c = tid; c < n; c += kNT)
-    for (int r = 0; r < R; ++r) {
-      const int o = cs.order[r];
-      const double sg = cs.sig[r];
-      double s = 0.0;
-#pragma unroll
-      for (int j = 0; j < kQ; ++j) s += cs.z[c * kQ + j] * cs.ev[j * kQ + o];
-      cs.vs[r][c] = sg > 0.0 ? s / sg : (c == r ? 1.0 : 0.0);
-    }
-  __syncthreads();
-  // canonical signs: argmax_c |v_r[c]|, first index on ties
-  {
-    double bv_[kRMax];
+  // v_r = Bm^T ev_r / sigma_r in wave 0 (one column per lane, n <= 64),
+  // which also fixes each pair's canonical sign: argmax_c |v_r[c]|, first
+  // index on ties (an xor butterfly, so every lane holds the same winner)
+  static_assert(n <= 64, "right singular vectors: one column per lane of a wave");
+  if (wave == 0) {
+    const int c = lane;
+    const bool on = c < n;
+    double vr[kRMax], bv_[kRMax];
     int bi[kRMax];
 #pragma unroll
     for (int r = 0; r < kRMax; ++r) {
-      bv_[r] = -1.0;
-      bi[r] = 0x7fffffff;
+      vr[r] = 0.0;
+      if (r < R && on) {
+        const int o = cs.order[r];
+        const double sg = cs.sig[r];
+        double sv = 0.0;
+#pragma unroll
+        for (int j = 0; j < kQ; ++j) sv += cs.z[c * kQ + j] * cs.ev[j * kQ + o];
+        vr[r] = sg > 0.0 ? sv / sg : (c == r ? 1.0 : 0.0);
+        cs.vs[r][c] = vr[r];
+      }
+      bv_[r] = on ? fabs(vr[r]) : -1.0;
+      bi[r] = on ? c : 0x7fffffff;
     }
-    for (int c = tid; c < n; c += kNT)
+    // the R reductions run side by side
+#pragma unroll
+    for (int o2 = 32; o2 > 0; o2 >>= 1)
 #pragma unroll
       for (int r = 0; r < kRMax; ++r)
         if (r < R) {
-          const double ad = fabs(cs.vs[r][c]);
-          if (ad > bv_[r]) {
-            bv_[r] = ad;
-            bi[r] = c;
-          }
+          const double ov = __shfl_xor(bv_[r], o2, 64);
+          const int oi = __shfl_xor(bi[r], o2, 64);
+          const bool take = (ov > bv_[r]) | ((ov == bv_[r]) & (oi < bi[r]));  // selects, no branches
+          bv_[r] = take ? ov : bv_[r];
+          bi[r] = take ? oi : bi[r];
         }
 #pragma unroll
-    for (int r = 0; r < kRMax; ++r) {
-#pragma unroll
-      for (int o2 = 32; o2 > 0; o2 >>= 1) {
-        const double ov = __shfl_xor(bv_[r], o2, 64);
-        const int oi = __shfl_xor(bi[r], o2, 64);
-        if (ov > bv_[r] || (ov == bv_[r] && oi < bi[r])) {
-          bv_[r] = ov;
-          bi[r] = oi;
-        }
+    for (int r = 0; r < kRMax; ++r)
+      if (r < R) {
+        const double vb = __shfl(vr[r], bi[r] & 63, 64);
+        if (lane == 0) cs.sgn[r] = (bi[r] != 0x7fffffff && vb < 0.0) ? -1.0 : 1.0;
       }
-      if (lane == 0) {
-        cs.amax[wave][r] = bv_[r];
-        cs.aidx[wave][r] = bi[r];
-      }
-    }
-  }
-  __syncthreads();
-  if (tid < R) {
-    double bv_ = cs.amax[0][tid];
-    int bi = cs.aidx[0][tid];
-    for (int w = 1; w < 4; ++w) {
-      const double ov = cs.amax[w][tid];
-      const int oi = cs.aidx[w][tid];
-      if (ov > bv_ || (ov == bv_ && oi < bi)) {
-        bv_ = ov;
-        bi = oi;
-      }
-    }
-    cs.sgn[tid] = (bi != 0x7fffffff && cs.vs[tid][bi] < 0.0) ? -1.0 : 1.0;
   }
   __syncthreads();
   // two-timescale blend of the decayed factors with the SVD factors
