@@ -133,10 +133,13 @@ __device__ __forceinline__ void rm_mfma(const float* rm, int ldr, const BT* b, d
 // (c^2 + s^2 = 1 by construction).
 __device__ __forceinline__ void jacobi_rot(double app, double aqq, double apq, double& c, double& s) {
   // selects only (no branches), so the two rotations a lane forms per round
-  // interleave; sqrt(x) is taken as x rsqrt(max(x, DBL_MIN)), 0 at x = 0
+  // interleave.  h only sets the angle: it is x times the hardware reciprocal
+  // square root (about 2^-23 relative, 0 at x = 0), and a rotation that
+  // leaves 1e-7 of a_pq behind still converges within the same sweeps; c and
+  // s are normalised by the refined rsqrt, so c^2 + s^2 = 1 to rounding.
   const double d = aqq - app, e = 2.0 * apq;
   const double x = fma(d, d, e * e);
-  const double h = x * rsqrt(fmax(x, 2.2250738585072014e-308));
+  const double h = x * __builtin_amdgcn_rsq(fmax(x, 2.2250738585072014e-308));
   const double w = fabs(d) + h;
   const double q = fma(w, w, e * e);
   const double r = rsqrt(q);
@@ -226,7 +229,8 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int tid, int pass
         const double akk = __shfl(a, 9 * k, 64);
         const double aik = __shfl(a, 8 * i + k, 64);
         const double ajk = __shfl(a, 8 * j + k, 64);
-        const double rd = (akk > tol && akk > 0.0) ? rsqrt(akk) : 0.0;
+        const double rq = rsqrt(fmax(akk, 2.2250738585072014e-308));  // unconditional: a select, no branch
+        const double rd = (akk > tol && akk > 0.0) ? rq : 0.0;
         const double lik = aik * rd, ljk = ajk * rd;
         if (i > k && j > k) a -= lik * ljk;
         if (j == k && i >= k) a = lik;  // lik = sqrt(akk) on the diagonal, 0 for a dropped column
