@@ -638,8 +638,16 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
     }
     *(f32x4*)&sm.u[ui][ud] = (f32x4){uu[0], uu[1], uu[2], uu[3]};
     *(f32x4*)&sm.u[ui][ud + 4] = (f32x4){uu[4], uu[5], uu[6], uu[7]};
+    if constexpr (DG == 16) {
+      // the 16 lanes of a token row are one DPP row: rotations by 8, 4, 2, 1
+      part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x128, 0xf, 0xf, false));
+      part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x124, 0xf, 0xf, false));
+      part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x122, 0xf, 0xf, false));
+      part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x121, 0xf, 0xf, false));
+    } else {
 #pragma unroll
-    for (int off = 1; off < DG; off <<= 1) part += __shfl_xor(part, off, 64);
+      for (int off = 1; off < DG; off <<= 1) part += __shfl_xor(part, off, 64);
+    }
     if (tid % DG == 0) {
       sm.alpha[ui] = stable_alpha_f(part);
       sm.lg[ui] = log_decay(r.dec);
@@ -691,14 +699,16 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
     commit(raw);
     if (c + 1 < p.c1) fetch(raw, c + 1);
     __syncthreads();
-    // per-token scalars (wave 0) | grams and Kronecker reads (MFMA)
-    if (wave == 0) {
-      float gl = lane < P ? sm.lg[lane] : 0.f;
+    // per-token scalars | grams and Kronecker reads (MFMA).  Every wave forms
+    // the log-decay prefix sums G (lane i holds G_i); wave 0 publishes the
+    // per-token coefficients.
+    float gl = lane < P ? sm.lg[lane] : 0.f;
 #pragma unroll
-      for (int off = 1; off < P; off <<= 1) {
-        const float o = __shfl_up(gl, off, 64);
-        if (lane >= off) gl += o;
-      }
+    for (int off = 1; off < P; off <<= 1) {
+      const float o = __shfl_up(gl, off, 64);
+      if (lane >= off) gl += o;
+    }
+    if (wave == 0) {
       const float gl_last = __shfl(gl, P - 1, 64);
       if (lane < P) {
         const float e2 = expf(2.f * (gacc + gl));
@@ -715,16 +725,81 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
 #pragma unroll
       for (int ti = 0; ti < PT * PT; ++ti) {
         const int it = ti / PT, jt = ti % PT;
-        const f32x4 acc = tile_nt<CT, D>(arows + (it * 16 + n16) * (D + 8), brows + (jt * 16 + n16) * (D + 8), g4);
+        f32x4 acc = tile_nt<CT, D>(arows + (it * 16 + n16) * (D + 8), brows + (jt * 16 + n16) * (D + 8), g4);
+        if constexpr (P == 16) {
+          // waves 1..3 scale their tile here (one tile each):
+          //   Aq = [j <= i] e^{G_i - G_j} q_i.k_j,  Ho = [j >= i] alpha_i gam_i h_i.Vbd_j,
+          //   Qo = [j >= i] gam_i q_i.Vbd_j
+          if (wave > 0) {
+            const float gj = __shfl(gl, n16, 64);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const int i = 4 * g4 + s;
+              const float gi = __shfl(gl, i, 64);
+              float v;
+              if (wave == 1) v = (n16 <= i) ? expf(gi - gj) * acc[s] : 0.f;
+              else if (wave == 2) v = (n16 >= i) ? sm.alpha[i] * expf(gi) * acc[s] : 0.f;
+              else v = (n16 >= i) ? expf(gi) * acc[s] : 0.f;
+              acc[s] = v;
+            }
+          }
+        }
 #pragma unroll
         for (int s = 0; s < 4; ++s) sm.pp[wave][it * 16 + 4 * g4 + s][jt * 16 + n16] = acc[s];
       }
     }
-    if (live) {
-      constexpr int NRT = 2 * P / 16;
+    if constexpr (P == 16) {
+      // T = (I + Lm)^-1 needs only wave 0's own Gram tile (H K^T), the decay
+      // scan and alpha: wave 0 forms it now, while waves 1..3 do the
+      // Kronecker reads
+      if (wave == 0) {
+        // the scan's G and the Gram tile were written by other lanes of this
+        // wave: order the LDS accesses (wave-local)
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        // Lm[i][j] = alpha_i e^{G_i - G_j} (h_i . k_j), j < i, is strictly lower
+        // (nilpotent): (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8), factors
+        // that commute; squarings and products on fp32 MFMA.  An accumulator
+        // tile is a k-fragment (B operand); the A operand of each square goes
+        // through LDS.
+        f32x4 xa, ta;
 #pragma unroll
-      for (int a = 0; a < VPW; ++a) {
-        const int vt = wave * VPW + a;
+        for (int s = 0; s < 4; ++s) {
+          const int i = 4 * g4 + s;
+          xa[s] = (n16 < i) ? sm.alpha[i] * expf(sm.G[i] - sm.G[n16]) * PP(0, i, n16) : 0.f;
+          PP(5, i, n16) = xa[s];
+          ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
+        }
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        int src = 5;
+#pragma unroll
+        for (int step = 0; step < 3; ++step) {
+          const int dst = step & 1 ? 5 : 0;
+          f32x4 sq = zero4();
+          mma(sq, *(const f32x4*)&PP(src, n16, 4 * g4), xa);  // X^2
+          xa = sq;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) PP(dst, 4 * g4 + s, n16) = sq[s];
+          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+          __builtin_amdgcn_wave_barrier();
+          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+          mma(ta, *(const f32x4*)&PP(dst, n16, 4 * g4), ta);  // T += X^2 T
+          src = dst;
+        }
+#pragma unroll
+        for (int s = 0; s < 4; ++s) PP(4, 4 * g4 + s, n16) = ta[s];
+      }
+    }
+    if (live) {
+      constexpr int NRT = 2 * P / 16, NVT = D / 16;
+      // value tiles of this wave: P == 16 spreads them over waves 1..3
+      const int vt0 = (P == 16) ? wave - 1 : wave * VPW, vstep = (P == 16) ? 3 : 1;
+      const int nvt = (P == 16) ? (wave == 0 ? 0 : (NVT - (wave - 1) + 2) / 3) : VPW;
+      for (int a = 0; a < nvt; ++a) {
+        const int vt = vt0 + a * vstep;
         Frag bf[D / KS];
 #pragma unroll
         for (int kb = 0; kb < D / KS; ++kb) bf[kb] = ld_frag(&sm.skron[vt * 16 + n16][kb * KS], g4);
@@ -739,49 +814,19 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
       }
     }
     __syncthreads();
-    // coefficient matrices; wave 0 also forms T = (I + Lm)^-1
-    if (wave == 0) {
-      for (int e = lane; e < P * P; e += 64) {
-        const int i = e / P, j = e % P;
-        PP(0, i, j) = (j < i) ? sm.alpha[i] * expf(sm.G[i] - sm.G[j]) * PP(0, i, j) : 0.f;
-      }
-      // Lm was written by other lanes of this wave: order the LDS accesses
-      // (wave-local, no workgroup barrier needed)
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      if constexpr (P == 16) {
-        // Lm is strictly lower (nilpotent): (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8),
-        // factors that commute; squarings and products on fp32 MFMA.  An
-        // accumulator tile is a k-fragment, rows of the squares go through LDS.
-        f32x4 xa, ta;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int i = 4 * g4 + s;
-          xa[s] = PP(0, i, n16);
-          ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
+    // coefficient matrices (P != 16; at P = 16 they were formed above): wave 0
+    // forms T = (I + Lm)^-1, the others scale Aq, Ho, Qo
+    if constexpr (P != 16) {
+      if (wave == 0) {
+        for (int e = lane; e < P * P; e += 64) {
+          const int i = e / P, j = e % P;
+          PP(0, i, j) = (j < i) ? sm.alpha[i] * expf(sm.G[i] - sm.G[j]) * PP(0, i, j) : 0.f;
         }
-        int src = 0;
-#pragma unroll
-        for (int step = 0; step < 3; ++step) {
-          const int dst = step & 1 ? 4 : 5;
-          f32x4 sq = zero4();
-          mma(sq, *(const f32x4*)&PP(src, n16, 4 * g4), xa);  // X^2
-          xa = sq;
-#pragma unroll
-          for (int s = 0; s < 4; ++s) PP(dst, 4 * g4 + s, n16) = sq[s];
-          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-          __builtin_amdgcn_wave_barrier();
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-          mma(ta, *(const f32x4*)&PP(dst, n16, 4 * g4), ta);  // T += X^2 T
-          src = dst;
-        }
+        // Lm was written by other lanes of this wave: order the LDS accesses
+        // (wave-local, no workgroup barrier needed)
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-#pragma unroll
-        for (int s = 0; s < 4; ++s) PP(4, 4 * g4 + s, n16) = ta[s];
-      } else {
         // column j of T by forward substitution (lanes j < P)
         const int j = lane;
         float t[P];
@@ -795,18 +840,18 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
         if (j < P)
 #pragma unroll
           for (int i = 0; i < P; ++i) PP(4, i, j) = t[i];
+      } else {
+        for (int e = tid - 64; e < P * P; e += kNT - 64) {
+          const int i = e / P, j = e % P;
+          const float gi = sm.G[i], al = sm.alpha[i], ga = sm.gam[i];
+          const float dij = (j <= i) ? expf(gi - sm.G[j]) : 0.f;
+          PP(1, i, j) = dij * PP(1, i, j);
+          PP(2, i, j) = (j >= i) ? al * ga * PP(2, i, j) : 0.f;
+          PP(3, i, j) = (j >= i) ? ga * PP(3, i, j) : 0.f;
+        }
       }
-    } else {
-      for (int e = tid - 64; e < P * P; e += kNT - 64) {
-        const int i = e / P, j = e % P;
-        const float gi = sm.G[i], al = sm.alpha[i], ga = sm.gam[i];
-        const float dij = (j <= i) ? expf(gi - sm.G[j]) : 0.f;
-        PP(1, i, j) = dij * PP(1, i, j);
-        PP(2, i, j) = (j >= i) ? al * ga * PP(2, i, j) : 0.f;
-        PP(3, i, j) = (j >= i) ? ga * PP(3, i, j) : 0.f;
-      }
+      __syncthreads();
     }
-    __syncthreads();
     // window algebra on fp32 MFMA, per wave its VPW value tiles:
     //   Rhs = alpha u - kco KRh - Ho U_old;  U = T Rhs
     //   Y   = qco KRq + Qo U_old + Aq U
@@ -867,12 +912,21 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
       }
     }
     if (p.ts_g && tid == 0) p.ts_g[(size_t)chain * p.nch + c] = gacc;
-    // window keys for the next chunk: k_j decayed to this chunk's end
-    for (int e = tid; e < P * D; e += kNT) {
-      const int j = e / D, d = e % D;
-      const float kv = to_f(sm.x[2 * P + j][d]) * sm.vsc[j];
-      sm.vbd[j][d] = kv;
-      sm.vbx[j][d] = from_f<CT>(kv);
+    // window keys for the next chunk: k_j decayed to this chunk's end, 8
+    // consecutive keys per thread
+    for (int u8 = tid; u8 < P * D / 8; u8 += kNT) {
+      const int j = u8 / DG, d = 8 * (u8 % DG);
+      uint4 w[W16];
+#pragma unroll
+      for (int q16 = 0; q16 < W16; ++q16) w[q16] = *(const uint4*)&sm.x[2 * P + j][d + q16 * (16 / sizeof(CT))];
+      float kf[8];
+      unpack8(w, kf, (const CT*)nullptr);
+      const float sc = sm.vsc[j];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) kf[e] *= sc;
+      *(f32x4*)&sm.vbd[j][d] = (f32x4){kf[0], kf[1], kf[2], kf[3]};
+      *(f32x4*)&sm.vbd[j][d + 4] = (f32x4){kf[4], kf[5], kf[6], kf[7]};
+      store8(&sm.vbx[j][d], kf);
     }
     gacc += sm.G[P - 1];
   }
