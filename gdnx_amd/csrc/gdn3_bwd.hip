@@ -74,6 +74,12 @@ __device__ __forceinline__ void store8f(float* p, const float* f) {
   *(f32x4*)p = (f32x4){f[0], f[1], f[2], f[3]};
   *(f32x4*)(p + 4) = (f32x4){f[4], f[5], f[6], f[7]};
 }
+// 8 values to 8 consecutive entries of the compute dtype (16-byte aligned)
+__device__ __forceinline__ void store8c(float* p, const float* f) { store8f(p, f); }
+__device__ __forceinline__ void store8c(bf16* p, const float* f) {
+  *(bf16x8*)p = (bf16x8){(bf16)f[0], (bf16)f[1], (bf16)f[2], (bf16)f[3],
+                         (bf16)f[4], (bf16)f[5], (bf16)f[6], (bf16)f[7]};
+}
 
 // lane (g, n): X[4 g + s][col], s = 0..3 -- a fragment over k = rows of a
 // row-major P x D LDS matrix
@@ -121,6 +127,21 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
   for (int a = 0; a < VPW; ++a) dUc[a] = dVc[a] = zero4();
   float dgacc = 0.f;          // d/dGacc of the chunk after the current one
 
+  // the factors of the interval a chunk rebuilds S_kron^T from, fetched into
+  // registers a chunk ahead (their loads land while the chunk before computes)
+  constexpr int NAB = (Ge::RMN + kNT - 1) / kNT;
+  float abr[NAB];
+  auto rebuilds = [&](int cc) { return cc / per > 0 && (cc == nch - 1 || (cc + 1) % per == 0); };
+  auto fetch_ab = [&](int cc) {
+    const float* ab = ts.ab + ((size_t)(cc / per - 1) * N + chain) * Ge::RMN;
+#pragma unroll
+    for (int u = 0; u < NAB; ++u) {
+      const int e = tid + u * kNT;
+      abr[u] = e < Ge::RMN ? ab[e] : 0.f;
+    }
+  };
+  if (nch > 0 && rebuilds(nch - 1)) fetch_ab(nch - 1);
+
   for (int c = nch - 1; c >= 0; --c) {
     const int iv = c / per;
     const bool live = iv > 0;
@@ -128,29 +149,49 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     const float gacc = ts.gacc[(size_t)chain * nch + c];
     __syncthreads();  // the previous chunk is done with LDS
 
-    // ---- S_kron^T of this interval (the factors of compaction iv - 1), rebuilt on entry ----
-    if (live && (c == nch - 1 || (c + 1) % per == 0)) {
-      const float* ab = ts.ab + ((size_t)(iv - 1) * N + chain) * Ge::RMN;
+    // ---- S_kron^T of this interval (the factors of compaction iv - 1), rebuilt on entry:
+    // skt[k][v], k = ik b_k + jk, v = iv' b_v + jv.  A thread takes one row k
+    // and a group of 8 values of iv': the 8 x 8 products of A_r[iv'][ik] and
+    // B_r[jv][jk] are 64 consecutive v of that row (eight 16-byte stores);
+    // consecutive lanes take consecutive rows, so the stores spread over the
+    // banks ----
+    if (live && rebuilds(c)) {
+      static_assert(Ge::bv == 8 && Ge::av % 8 == 0, "blocks of 8 x 8 factor entries");
+      constexpr int NGA = Ge::av / 8;                 // groups of iv' per row
       float* st = &sm.dr[0][0];
-      for (int e = tid; e < Ge::RMN; e += kNT) st[e] = ab[e];
+#pragma unroll
+      for (int u = 0; u < NAB; ++u) {
+        const int e = tid + u * kNT;
+        if (e < Ge::RMN) st[e] = abr[u];
+      }
       __syncthreads();
-      if (tid < Ge::m) {
-        const int ivv = tid / Ge::ak, ik = tid % Ge::ak;
-        float a[Ge::R];
-#pragma unroll
-        for (int r = 0; r < Ge::R; ++r) a[r] = st[r * Ge::m + ivv * Ge::ak + ik];
+      if (tid < D * NGA) {
+        const int kr = tid % D, grp = tid / D, ik = kr / Ge::bk, jk = kr % Ge::bk;
         const float* Bf = st + Ge::R * Ge::m;
+        float bb[Ge::R][8];
+#pragma unroll
+        for (int r = 0; r < Ge::R; ++r)
+#pragma unroll
+          for (int jv = 0; jv < 8; ++jv) bb[r][jv] = Bf[r * Ge::n + jv * Ge::bk + jk];
 #pragma unroll 2
-        for (int jv = 0; jv < Ge::bv; ++jv)
+        for (int i8 = 0; i8 < 8; ++i8) {
+          const int ivv = grp * 8 + i8;
+          float a[Ge::R];
 #pragma unroll
-          for (int jk = 0; jk < Ge::bk; ++jk) {
-            float s = 0.f;
+          for (int r = 0; r < Ge::R; ++r) a[r] = st[r * Ge::m + ivv * Ge::ak + ik];
+          float sv[8];
 #pragma unroll
-            for (int r = 0; r < Ge::R; ++r) s += a[r] * Bf[r * Ge::n + jv * Ge::bk + jk];
-            sm.skt[ik * Ge::bk + jk][ivv * Ge::bv + jv] = from_f<CT>(s);
+          for (int jv = 0; jv < 8; ++jv) {
+            float x = 0.f;
+#pragma unroll
+            for (int r = 0; r < Ge::R; ++r) x += a[r] * bb[r][jv];
+            sv[jv] = x;
           }
+          store8c(&sm.skt[kr][ivv * Ge::bv], sv);
+        }
       }
     }
+    if (c > 0 && rebuilds(c - 1)) fetch_ab(c - 1);
 
     // ---- A: the chunk's inputs (and the previous chunk's keys / decays) ----
     const int t = c * P + ui;
