@@ -74,6 +74,39 @@ __device__ __forceinline__ void store8f(float* p, const float* f) {
   *(f32x4*)p = (f32x4){f[0], f[1], f[2], f[3]};
   *(f32x4*)(p + 4) = (f32x4){f[4], f[5], f[6], f[7]};
 }
+// A bf16 k-step fragment (k = 4 g + i and 16 + 4 g + i, i < 4) of an fp32 LDS
+// row as hi + lo bf16 parts: x - hi - lo is ~2^-17 of x
+__device__ __forceinline__ void split_frag(const float* p, int g, bf16x8& hi, bf16x8& lo) {
+  const f32x4 x0 = *(const f32x4*)(p + 4 * g), x1 = *(const f32x4*)(p + 16 + 4 * g);
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bf16 h0 = (bf16)x0[i], h1 = (bf16)x1[i];
+    hi[i] = h0;
+    hi[4 + i] = h1;
+    lo[i] = (bf16)(x0[i] - (float)h0);
+    lo[4 + i] = (bf16)(x1[i] - (float)h1);
+  }
+}
+
+// 16x16 NT tile product over K of fp32 LDS rows on bf16 MFMA: each operand
+// enters as hi + lo parts (an operand that holds bf16 values exactly needs no
+// lo part); lo x lo is dropped, so the product is within ~2^-16 of fp32
+template <int K>
+__device__ __forceinline__ f32x4 tile_nt_split(const float* arow, const float* brow, int g4, bool a_exact,
+                                               bool b_exact) {
+  f32x4 acc = zero4();
+#pragma unroll
+  for (int kb = 0; kb < K; kb += 32) {
+    bf16x8 ah, al, bh, bl;
+    split_frag(arow + kb, g4, ah, al);
+    split_frag(brow + kb, g4, bh, bl);
+    mma(acc, ah, bh);
+    if (!b_exact) mma(acc, ah, bl);
+    if (!a_exact) mma(acc, al, bh);
+  }
+  return acc;
+}
+
 // 8 values to 8 consecutive entries of the compute dtype (16-byte aligned)
 __device__ __forceinline__ void store8c(float* p, const float* f) { store8f(p, f); }
 __device__ __forceinline__ void store8c(bf16* p, const float* f) {
@@ -358,7 +391,11 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     {
       const float* ar = (wave == 0 || wave == 2) ? &sm.dr[0][0] : &sm.dy[0][0];
       const float* br = (wave < 2) ? &sm.u[0][0] : &sm.uo[0][0];
-      f32x4 acc = tile_nt<float, D>(ar + n16 * LR, br + n16 * LR, g4);
+      f32x4 acc;
+      if constexpr (sizeof(CT) == 2)   // bf16 IO: dY holds bf16 values exactly
+        acc = tile_nt_split<D>(ar + n16 * LR, br + n16 * LR, g4, wave == 1 || wave == 3, false);
+      else
+        acc = tile_nt<float, D>(ar + n16 * LR, br + n16 * LR, g4);
       if (wave == 0 || wave == 2) acc = -acc;
       const int j = n16;
       const float Gj = sm.G[j];
@@ -416,11 +453,26 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
       const int kt = wave * VPW + a, d = 16 * kt + n16;
       Gh[a] = Gq[a] = zero4();
       if (live) {
+        if constexpr (sizeof(CT) == 2) {
+          // bf16 MFMA: S_kron^T is bf16, dY holds bf16 values exactly, dRhs
+          // enters as hi + lo parts
+#pragma unroll 2
+          for (int kb = 0; kb < D / 32; ++kb) {
+            const bf16x8 sf = ld_frag(&sm.skt[d][kb * 32], g4);
+            bf16x8 rh, rl, yh, yl;
+            split_frag(&sm.dr[n16][kb * 32], g4, rh, rl);
+            split_frag(&sm.dy[n16][kb * 32], g4, yh, yl);
+            mma(Gh[a], rh, sf);
+            mma(Gh[a], rl, sf);
+            mma(Gq[a], yh, sf);
+          }
+        } else {
 #pragma unroll 4
-        for (int kb = 0; kb < D / 16; ++kb) {
-          const f32x4 sf = load4(&sm.skt[d][kb * 16 + 4 * g4]);
-          mma(Gh[a], ld_frag(&sm.dr[n16][kb * 16], g4), sf);
-          mma(Gq[a], ld_frag(&sm.dy[n16][kb * 16], g4), sf);
+          for (int kb = 0; kb < D / 16; ++kb) {
+            const f32x4 sf = load4(&sm.skt[d][kb * 16 + 4 * g4]);
+            mma(Gh[a], ld_frag(&sm.dr[n16][kb * 16], g4), sf);
+            mma(Gq[a], ld_frag(&sm.dy[n16][kb * 16], g4), sf);
+          }
         }
       }
     }
