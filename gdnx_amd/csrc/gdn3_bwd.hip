@@ -74,6 +74,33 @@ __device__ __forceinline__ void store8f(float* p, const float* f) {
   *(f32x4*)p = (f32x4){f[0], f[1], f[2], f[3]};
   *(f32x4*)(p + 4) = (f32x4){f[4], f[5], f[6], f[7]};
 }
+// 8 consecutive elements held raw (one 16-byte vector per 8 bf16, two per 8
+// floats), converted to float where they are used
+template <typename CT> struct Row8 { uint4 w[sizeof(CT) / 2]; };
+template <typename CT>
+__device__ __forceinline__ void raw8(const CT* p, Row8<CT>& r) {
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(CT) / 2); ++i) r.w[i] = ((const uint4*)p)[i];
+}
+__device__ __forceinline__ void cvt8(const Row8<bf16>& r, float* f) {
+  const bf16x8 x = *(const bf16x8*)&r.w[0];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) f[e] = (float)x[e];
+}
+__device__ __forceinline__ void cvt8(const Row8<float>& r, float* f) {
+  const f32x4 a = *(const f32x4*)&r.w[0], b = *(const f32x4*)&r.w[1];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    f[e] = a[e];
+    f[4 + e] = b[e];
+  }
+}
+template <typename CT>
+__device__ __forceinline__ void zero8(Row8<CT>& r) {
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(CT) / 2); ++i) r.w[i] = make_uint4(0u, 0u, 0u, 0u);
+}
+
 // A bf16 k-step fragment (k = 4 g + i and 16 + 4 g + i, i < 4) of an fp32 LDS
 // row as hi + lo bf16 parts: x - hi - lo is ~2^-17 of x
 __device__ __forceinline__ void split_frag(const float* p, int g, bf16x8& hi, bf16x8& lo) {
@@ -182,6 +209,36 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     const float gacc = ts.gacc[(size_t)chain * nch + c];
     __syncthreads();  // the previous chunk is done with LDS
 
+    // the chunk's inputs (and the previous chunk's keys / decays), loaded raw
+    // before the S_kron^T rebuild so that their latency hides behind it
+    const int t = c * P + ui;
+    const bool tv = has_unit && t < T;
+    Row8<CT> rk, rq, rv, rdy, rkp;
+    Row8<float> rb, rw, ru, ruo;
+    float bs = 0.f, ws = 0.f, dv = 1.f, dvp = 1.f;
+    zero8(rk), zero8(rq), zero8(rv), zero8(rdy), zero8(rkp), zero8(rb), zero8(rw), zero8(ru), zero8(ruo);
+    if (tv) {
+      raw8<CT>((const CT*)p.k + qkv_base + (size_t)t * qkv_tok + ud, rk);
+      raw8<CT>((const CT*)p.q + qkv_base + (size_t)t * qkv_tok + ud, rq);
+      raw8<CT>((const CT*)p.v + qkv_base + (size_t)t * qkv_tok + ud, rv);
+      raw8<CT>((const CT*)p.dy + y_base + (size_t)t * y_tok + ud, rdy);
+      if (gc > 1) {
+        raw8<float>(p.bg + gate_base + (size_t)t * gate_tok + ud, rb);
+        raw8<float>(p.wg + gate_base + (size_t)t * gate_tok + ud, rw);
+      } else {
+        bs = p.bg[gate_base + (size_t)t * gate_tok];
+        ws = p.wg[gate_base + (size_t)t * gate_tok];
+      }
+      dv = p.dec[dec_base + (size_t)t * dec_tok];
+      raw8<float>(ts.u + ((size_t)chain * nch + c) * P * D + (size_t)ui * D + ud, ru);
+    }
+    if (has_unit && c > 0) {
+      const int tp = t - P;
+      raw8<CT>((const CT*)p.k + qkv_base + (size_t)tp * qkv_tok + ud, rkp);
+      dvp = p.dec[dec_base + (size_t)tp * dec_tok];
+      raw8<float>(ts.u + ((size_t)chain * nch + c - 1) * P * D + (size_t)ui * D + ud, ruo);
+    }
+
     // ---- S_kron^T of this interval (the factors of compaction iv - 1), rebuilt on entry:
     // skt[k][v], k = ik b_k + jk, v = iv' b_v + jv.  A thread takes one row k
     // and a group of 8 values of iv': the 8 x 8 products of A_r[iv'][ik] and
@@ -226,39 +283,26 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     }
     if (c > 0 && rebuilds(c - 1)) fetch_ab(c - 1);
 
-    // ---- A: the chunk's inputs (and the previous chunk's keys / decays) ----
-    const int t = c * P + ui;
-    const bool tv = has_unit && t < T;
+    // ---- A: the chunk's inputs to LDS (h = b o k, alpha, log decays) ----
     float vf[8], wf[8];
     {
       float kf[8], qf[8], bf[8], dyf[8], kp[8], us[8], uos[8];
+      cvt8(rk, kf);
+      cvt8(rq, qf);
+      cvt8(rv, vf);
+      cvt8(rdy, dyf);
+      cvt8(rkp, kp);
+      cvt8(ru, us);
+      cvt8(ruo, uos);
+      if (gc > 1) {
+        cvt8(rb, bf);
+        cvt8(rw, wf);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) kf[e] = qf[e] = vf[e] = bf[e] = wf[e] = dyf[e] = kp[e] = us[e] = uos[e] = 0.f;
-      float dv = 1.f, dvp = 1.f;
-      if (tv) {
-        load8<CT>((const CT*)p.k + qkv_base + (size_t)t * qkv_tok + ud, kf);
-        load8<CT>((const CT*)p.q + qkv_base + (size_t)t * qkv_tok + ud, qf);
-        load8<CT>((const CT*)p.v + qkv_base + (size_t)t * qkv_tok + ud, vf);
-        load8<CT>((const CT*)p.dy + y_base + (size_t)t * y_tok + ud, dyf);
-        if (gc > 1) {
-          load8<float>(p.bg + gate_base + (size_t)t * gate_tok + ud, bf);
-          load8<float>(p.wg + gate_base + (size_t)t * gate_tok + ud, wf);
-        } else {
-          const float bs = p.bg[gate_base + (size_t)t * gate_tok], ws = p.wg[gate_base + (size_t)t * gate_tok];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            bf[e] = bs;
-            wf[e] = ws;
-          }
+        for (int e = 0; e < 8; ++e) {
+          bf[e] = bs;
+          wf[e] = ws;
         }
-        dv = p.dec[dec_base + (size_t)t * dec_tok];
-        load8<float>(ts.u + ((size_t)chain * nch + c) * P * D + (size_t)ui * D + ud, us);
-      }
-      if (has_unit && c > 0) {
-        const int tp = t - P;
-        load8<CT>((const CT*)p.k + qkv_base + (size_t)tp * qkv_tok + ud, kp);
-        dvp = p.dec[dec_base + (size_t)tp * dec_tok];
-        load8<float>(ts.u + ((size_t)chain * nch + c - 1) * P * D + (size_t)ui * D + ud, uos);
       }
       float hf[8], part = 0.f;
 #pragma unroll
@@ -310,7 +354,11 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     {
       const float* ar = (wave & 1) ? &sm.q[0][0] : &sm.h[0][0];
       const float* br = (wave < 2) ? &sm.k[0][0] : &sm.vb[0][0];
-      const f32x4 acc = tile_nt<float, D>(ar + n16 * LR, br + n16 * LR, g4);
+      f32x4 acc;
+      if constexpr (sizeof(CT) == 2)   // bf16 IO: q, k and the raw previous keys are bf16 values exactly
+        acc = tile_nt_split<D>(ar + n16 * LR, br + n16 * LR, g4, (wave & 1) != 0, true);
+      else
+        acc = tile_nt<float, D>(ar + n16 * LR, br + n16 * LR, g4);
       const int j = n16;
       const float Gj = __shfl(gl, j, 64), vj = __shfl(vscp, j, 64);
 #pragma unroll
