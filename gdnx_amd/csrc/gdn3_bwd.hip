@@ -74,6 +74,16 @@ __device__ __forceinline__ void store8f(float* p, const float* f) {
   *(f32x4*)p = (f32x4){f[0], f[1], f[2], f[3]};
   *(f32x4*)(p + 4) = (f32x4){f[4], f[5], f[6], f[7]};
 }
+// Sum over the 16 lanes of each DPP row, the same bits in all 16 (a
+// butterfly of row rotations by 8, 4, 2, 1)
+__device__ __forceinline__ float row_sum16(float x) {
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x128, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x124, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x122, 0xf, 0xf, false));
+  x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x121, 0xf, 0xf, false));
+  return x;
+}
+
 // 8 consecutive elements held raw (one 16-byte vector per 8 bf16, two per 8
 // floats), converted to float where they are used
 template <typename CT> struct Row8 { uint4 w[sizeof(CT) / 2]; };
@@ -319,8 +329,12 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         store8f(&sm.u[ui][ud], us);
         store8f(&sm.uo[ui][ud], uos);
       }
+      if constexpr (DG == 16) {   // a token row is one DPP row
+        part = row_sum16(part);
+      } else {
 #pragma unroll
-      for (int off = 1; off < DG; off <<= 1) part += __shfl_xor(part, off, 64);
+        for (int off = 1; off < DG; off <<= 1) part += __shfl_xor(part, off, 64);
+      }
       if (has_unit && tid % DG == 0) {
         sm.cdot[ui] = part;
         sm.alpha[ui] = stable_alpha_f(part);
@@ -558,10 +572,15 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         dws += dwo[e];
         ut += wf[e] * vf[e] * dr8[e];
       }
+      if constexpr (DG == 16) {
+        ut = row_sum16(ut);
+        dws = row_sum16(dws);
+      } else {
 #pragma unroll
-      for (int off = 1; off < DG; off <<= 1) {
-        ut += __shfl_xor(ut, off, 64);
-        dws += __shfl_xor(dws, off, 64);
+        for (int off = 1; off < DG; off <<= 1) {
+          ut += __shfl_xor(ut, off, 64);
+          dws += __shfl_xor(dws, off, 64);
+        }
       }
       if (tv) {
         store8f(p.dv + y_base + (size_t)t * y_tok + ud, dvo);
@@ -595,19 +614,15 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         dG += dE - svb;
         sm.dc[i] = da * stable_dalpha_f(sm.cdot[i]);
       }
-      float svt = svb, det = dE;
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        svt += __shfl_xor(svt, off, 64);
-        det += __shfl_xor(det, off, 64);
-      }
+      float svt = row_sum16(svb), det = row_sum16(dE);   // then across the four DPP rows
+      svt += __shfl_xor(svt, 16, 64);
+      det += __shfl_xor(det, 16, 64);
+      svt += __shfl_xor(svt, 32, 64);
+      det += __shfl_xor(det, 32, 64);
       if (lane == P - 1) dG += svt + dgacc;   // G_last: the decayed keys and the next chunk's Gacc
-      float sfx = lane < P ? dG : 0.f;       // d log-decay_s = sum_{i >= s} dG_i
-#pragma unroll
-      for (int off = 1; off < 64; off <<= 1) {
-        const float o = __shfl_down(sfx, off, 64);
-        if (lane + off < 64) sfx += o;
-      }
+      // d log-decay_s = sum_{i >= s} dG_i: the P = 16 tokens are DPP row 0
+      static_assert(P == 16, "one DPP row of tokens");
+      const float sfx = row_suffix16(lane < P ? dG : 0.f);
       const int tt_ = c * P + lane;
       if (lane < P && tt_ < T) p.ddec[dec_base + (size_t)tt_ * dec_tok] = sfx * dlog_decay(sm.dec[lane]);
       if (lane == 0) sm.carry[0] = det + dgacc;
