@@ -60,7 +60,7 @@ struct G3Compact {
   alignas(16) double us[kRMax][kMN];      // leading left singular vectors of R_mat
   alignas(16) double vs[kRMax][kMN];      // leading right singular vectors
   double red[4 * 64];
-  double rinv[kQ * kQ];                   // R of the Cholesky QR (row-major, upper; 1 / R[i][i] on the diagonal)
+  double rinv[kQ * kQ];                   // the summed Gram Y^T Y of a Cholesky-QR pass (row-major)
   double ev[kQ * kQ];                     // eigenvectors of Bm Bm^T (columns)
   double lam[kQ];
   double sig[kRMax];
@@ -215,43 +215,45 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int tid, int pass
       }
     }
     __syncthreads();
-    if (wave == 0) {
-      const int i = lane >> 3, j = lane & 7;
-      double a = (cs.red[lane] + cs.red[64 + lane]) + (cs.red[128 + lane] + cs.red[192 + lane]);
-      double dmax = 0.0;
-#pragma unroll
-      for (int k = 0; k < kQ; ++k) dmax = fmax(dmax, __shfl(a, 9 * k, 64));
-      const double tol = dmax * 1e-24;
-      // right-looking Cholesky, lane (i, j) holds entry (i, j); column k
-      // becomes L[:, k] at step k (only the lower triangle is read)
-#pragma unroll
-      for (int k = 0; k < kQ; ++k) {
-        const double akk = __shfl(a, 9 * k, 64);
-        const double aik = __shfl(a, 8 * i + k, 64);
-        const double ajk = __shfl(a, 8 * j + k, 64);
-        const double rq = rsqrt(fmax(akk, 2.2250738585072014e-308));  // unconditional: a select, no branch
-        const double rd = (akk > tol && akk > 0.0) ? rq : 0.0;
-        const double lik = aik * rd, ljk = ajk * rd;
-        if (i > k && j > k) a -= lik * ljk;
-        if (j == k && i >= k) a = lik;  // lik = sqrt(akk) on the diagonal, 0 for a dropped column
-      }
-      // R = L^T (upper), row-major; its diagonal holds 1 / R[i][i] (0 for a
-      // dropped column)
-      if (j < i) cs.rinv[j * kQ + i] = a;
-      if (j == i) cs.rinv[i * kQ + i] = a > 0.0 ? 1.0 / a : 0.0;
-    }
+    if (wave == 0)   // the Gram, summed over the segments (rinv holds it row-major)
+      cs.rinv[lane] = (cs.red[lane] + cs.red[64 + lane]) + (cs.red[128 + lane] + cs.red[192 + lane]);
     __syncthreads();
+    // every thread factors the 8 x 8 Gram itself, in registers (right-looking
+    // Cholesky, lower triangle; a dropped column gets rd = 0), and solves its
+    // row of Y against R = L^T: no second exchange through LDS
+    double L[kQ][kQ], rdv[kQ];
+#pragma unroll
+    for (int i = 0; i < kQ; ++i)
+#pragma unroll
+      for (int j = 0; j <= i; ++j) L[i][j] = cs.rinv[i * kQ + j];
+    double dmax = 0.0;
+#pragma unroll
+    for (int k = 0; k < kQ; ++k) dmax = fmax(dmax, L[k][k]);
+    const double tol = dmax * 1e-24;
+#pragma unroll
+    for (int k = 0; k < kQ; ++k) {
+      const double akk = L[k][k];
+      const double rq = rsqrt(fmax(akk, 2.2250738585072014e-308));  // unconditional: a select, no branch
+      const double rd = (akk > tol && akk > 0.0) ? rq : 0.0;
+      rdv[k] = rd;   // 1 / R[k][k] (R[k][k] = akk rd = sqrt(akk))
+#pragma unroll
+      for (int i = k + 1; i < kQ; ++i) L[i][k] *= rd;
+#pragma unroll
+      for (int i = k + 1; i < kQ; ++i)
+#pragma unroll
+        for (int j = k + 1; j <= i; ++j) L[i][j] -= L[i][k] * L[j][k];
+    }
     if (tid < M) {
       double x[kQ];
 #pragma unroll
       for (int j = 0; j < kQ; ++j) x[j] = cs.y[tid * kQ + j];
-      // x R = y, column by column: x_j = (y_j - sum_{i<j} x_i R[i][j]) / R[j][j]
+      // x R = y, column by column: x_j = (y_j - sum_{i<j} x_i R[i][j]) / R[j][j], R[i][j] = L[j][i]
 #pragma unroll
       for (int j = 0; j < kQ; ++j) {
-        double s = x[j];
+        double sacc = x[j];
 #pragma unroll
-        for (int i = 0; i < j; ++i) s -= x[i] * cs.rinv[i * kQ + j];
-        x[j] = s * cs.rinv[j * kQ + j];
+        for (int i = 0; i < j; ++i) sacc -= x[i] * L[j][i];
+        x[j] = sacc * rdv[j];
       }
 #pragma unroll
       for (int j = 0; j < kQ; ++j) cs.y[tid * kQ + j] = x[j];
