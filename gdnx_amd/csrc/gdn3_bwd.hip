@@ -242,6 +242,17 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
       dv = p.dec[dec_base + (size_t)t * dec_tok];
       raw8<float>(ts.u + ((size_t)chain * nch + c) * P * D + (size_t)ui * D + ud, ru);
     }
+    // the erase gates at this wave's key tiles (used in G), loaded with the rest:
+    // in G they would sit between stores the compiler cannot reorder them past
+    float bgc[VPW][4];
+#pragma unroll
+    for (int a = 0; a < VPW; ++a)
+#pragma unroll
+      for (int s4 = 0; s4 < 4; ++s4) {
+        const int tt_ = c * P + 4 * g4 + s4, d = 16 * (wave * VPW + a) + n16;
+        bgc[a][s4] = tt_ < T ? (gc > 1 ? p.bg[gate_base + (size_t)tt_ * gate_tok + d]
+                                       : p.bg[gate_base + (size_t)tt_ * gate_tok]) : 0.f;
+      }
     if (has_unit && c > 0) {
       const int tp = t - P;
       raw8<CT>((const CT*)p.k + qkv_base + (size_t)tp * qkv_tok + ud, rkp);
@@ -655,8 +666,7 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         float dh = dH[s] + dci * Kc[s];
         if (live) dh -= sm.kco[i] * Gh[a][s];
         const float dq = dQ[s] + (live ? sm.qco[i] * Gq[a][s] : 0.f);
-        float bgv = 0.f;
-        if (ok) bgv = gc > 1 ? p.bg[gate_base + (size_t)tt_ * gate_tok + d] : p.bg[gate_base + (size_t)tt_ * gate_tok];
+        const float bgv = bgc[a][s];
         const float dk = dK[s] + dci * Hc[s] + dVc[a][s] * sm.vsc[i] + bgv * dh;
         dbp[s] = Kc[s] * dh;
         dbs[s] += dbp[s];
