@@ -32,14 +32,32 @@
 namespace gdnx {
 namespace {
 
+// Sum over the 64 lanes of a wave, the same bits in every lane: DPP row
+// rotations by 8, 4, 2, 1 (a butterfly inside each 16-lane row, so all lanes
+// of a row form the same sum), then across the four rows.
+template <int CTL>
+__device__ __forceinline__ double dpp_f64(double x) {
+  const long long b = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_update_dpp(0, (int)(b & 0xffffffffll), CTL, 0xf, 0xf, false);
+  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTL, 0xf, 0xf, false);
+  return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+__device__ __forceinline__ double wave_sum_f64(double x) {
+  x += dpp_f64<0x128>(x);
+  x += dpp_f64<0x124>(x);
+  x += dpp_f64<0x122>(x);
+  x += dpp_f64<0x121>(x);
+  x += __shfl_xor(x, 16, 64);
+  x += __shfl_xor(x, 32, 64);
+  return x;
+}
+
 // Sum of NV doubles over the 256 threads of the block, in a fixed order;
 // every thread receives the totals.  red: 4 * NV doubles of LDS.
 template <int NV>
 __device__ __forceinline__ void block_sum(double (&v)[NV], double* red, int tid) {
 #pragma unroll
-  for (int off = 32; off > 0; off >>= 1)
-#pragma unroll
-    for (int e = 0; e < NV; ++e) v[e] += __shfl_xor(v[e], off, 64);
+  for (int e = 0; e < NV; ++e) v[e] = wave_sum_f64(v[e]);
   if ((tid & 63) == 0)
 #pragma unroll
     for (int e = 0; e < NV; ++e) red[(tid >> 6) * NV + e] = v[e];
@@ -173,26 +191,6 @@ __device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
     acc = __builtin_amdgcn_mfma_f64_16x16x4f64(vl, vl, acc, 0, 0, 0);
   }
   return acc;
-}
-
-// Sum over the 64 lanes of a wave, the same bits in every lane: DPP row
-// rotations by 8, 4, 2, 1 (a butterfly inside each 16-lane row, so all lanes
-// of a row form the same sum), then across the four rows.
-template <int CTL>
-__device__ __forceinline__ double dpp_f64(double x) {
-  const long long b = __double_as_longlong(x);
-  const int lo = __builtin_amdgcn_update_dpp(0, (int)(b & 0xffffffffll), CTL, 0xf, 0xf, false);
-  const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTL, 0xf, 0xf, false);
-  return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
-}
-__device__ __forceinline__ double wave_sum_f64(double x) {
-  x += dpp_f64<0x128>(x);
-  x += dpp_f64<0x124>(x);
-  x += dpp_f64<0x122>(x);
-  x += dpp_f64<0x121>(x);
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
 }
 
 // Y <- Y R^{-1} with Y^T Y = R^T R (Cholesky QR, `passes` times: one pass
