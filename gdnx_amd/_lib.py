@@ -17,7 +17,7 @@ LIB_PATH = os.path.join(_HERE, "libgdnx.so")
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _c_int, _c_ll, _vp, _c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_float
 
@@ -40,6 +40,12 @@ SIGNATURES = {
     "gdnx_gdn3_num_compactions": (_c_int, [_c_int] * 3),
     "gdnx_gdn3_chunk_fwd": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 10
                             + [_c_int] * 12 + [_c_float, _c_int, _vp]),
+    "gdnx_gdn3_num_compactions_from": (_c_int, [_c_int] * 4),
+    "gdnx_gdn3_chunk_fwd_state": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 6 + [_c_int]
+                                  + [_vp] * 7 + [_c_int] * 12 + [_c_float, _c_int, _vp]),
+    "gdnx_gdn3_decode_step": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 10
+                              + [_c_int] * 12 + [_c_float, _c_int, _vp]),
+    "gdnx_delta_decode_step_chan": (_c_int, [_vp] * 9 + [_c_int] * 6 + [_vp]),
     "gdnx_gdn3_train_states_bytes": (_c_ll, [_c_int] * 7),
     "gdnx_gdn3_chunk_bwd": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 9
                             + [_c_int] * 13 + [_vp]),

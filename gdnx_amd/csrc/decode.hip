@@ -10,6 +10,9 @@
 //   g' = exp(min(log_g, 0));  m = g' S^T e;  r = w - m;
 //   S <- g' S + k r^T;        y = S^T q = g' S^T q + (k.q) r
 //   with e = a_e k, w = a_w v.
+// With a decay per key channel (the KMD-2 native scan, research/kernel_ab/
+// ref_scan.py:40-45, g [.., d_k]) g' scales the rows of S: m = S^T (g' e),
+// y = S^T (g' q) + (k.q) r, S <- diag(g') S + k r^T.
 //
 // HBM-bound: every step reads and writes each d x d fp32 state once, with
 // non-temporal loads and stores (the state is not reused within a step, so
@@ -34,7 +37,7 @@ __global__ void __launch_bounds__(TH) delta_decode_kernel(DecodeArgs p) {
   constexpr int RPT = D / RG;        // rows per thread
   constexpr int NWV = TH / 64;       // waves
   static_assert(RG * RPT == D && TH >= D, "launch shape");
-  __shared__ float s_k[D], s_q[D], s_red[2][NWV][D];
+  __shared__ float s_k[D], s_q[D], s_g[D], s_red[2][NWV][D];
   __shared__ float s_kq;
 
   const int tid = threadIdx.x;
@@ -52,7 +55,7 @@ __global__ void __launch_bounds__(TH) delta_decode_kernel(DecodeArgs p) {
     sidx = (size_t)sl * hm + chain % hm;
   }
   const float ae = p.ae[chain], aw = p.aw[chain];
-  const float gam = __expf(fmaxf(fminf(p.g[chain], 0.f), kLogFloor));
+  const float gam = p.chan ? 1.f : __expf(fmaxf(fminf(p.g[chain], 0.f), kLogFloor));
   const IO* kg = (const IO*)p.k + (size_t)head * D;
   const IO* qg = (const IO*)p.q + (size_t)head * D;
   const IO* vg = (const IO*)p.v + (size_t)head * D;
@@ -67,6 +70,7 @@ __global__ void __launch_bounds__(TH) delta_decode_kernel(DecodeArgs p) {
   if (tid < D) {
     s_k[tid] = to_f(kg[tid]);
     s_q[tid] = to_f(qg[tid]);
+    s_g[tid] = p.chan ? __expf(fmaxf(fminf(p.g[(size_t)chain * D + tid], 0.f), kLogFloor)) : gam;
   }
   __syncthreads();
   if (tid < 64) {
@@ -79,7 +83,8 @@ __global__ void __launch_bounds__(TH) delta_decode_kernel(DecodeArgs p) {
   f32x4 pe = zero4(), pq = zero4();
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
-    const float kk = s_k[rg + RG * j], qq = s_q[rg + RG * j];
+    const float gj = p.chan ? s_g[rg + RG * j] : 1.f;
+    const float kk = s_k[rg + RG * j] * gj, qq = s_q[rg + RG * j] * gj;
     pe += s[j] * kk;
     pq += s[j] * qq;
   }
@@ -113,7 +118,7 @@ __global__ void __launch_bounds__(TH) delta_decode_kernel(DecodeArgs p) {
 #pragma unroll
   for (int j = 0; j < RPT; ++j) {
     const float kk = s_k[rg + RG * j];
-    const f32x4 o = gam * s[j] + kk * r;
+    const f32x4 o = s_g[rg + RG * j] * s[j] + kk * r;
     __builtin_nontemporal_store(o, (f32x4*)&S[(size_t)(rg + RG * j) * D + 4 * cg]);
   }
   if (rg == 0) {

@@ -582,9 +582,10 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
     f32x4 b0, b1, w0, w1;
     float dec;
   };
+  // chunk c covers global tokens [c P, c P + P): local token c P + i - t0
   auto fetch = [&](Raw& r, int c) {
-    const int t = c * P + ui;
-    if (has_unit && t < T) {
+    const int t = c * P + ui - p.t0;
+    if (has_unit && t >= 0 && t < T) {
       const uint4* kp = (const uint4*)((const CT*)p.k + qkv_base + (size_t)t * qkv_tok + ud);
       const uint4* qp = (const uint4*)((const CT*)p.q + qkv_base + (size_t)t * qkv_tok + ud);
       const uint4* vp = (const uint4*)((const CT*)p.v + qkv_base + (size_t)t * qkv_tok + ud);
@@ -695,6 +696,10 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
   Raw raw;
   fetch(raw, p.c0);
   for (int c = p.c0; c < p.c1; ++c) {
+    // slots [lo, hi) receive this call's tokens; the others (the head of a
+    // window a previous call began, the tail after the last token) keep the
+    // writes they hold and stay visible to every token of the window
+    const int lo = max(0, p.t0 - c * P), hi = min(P, p.t0 + T - c * P);
     __syncthreads();
     commit(raw);
     if (c + 1 < p.c1) fetch(raw, c + 1);
@@ -738,8 +743,8 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
               const float gi = __shfl(gl, i, 64);
               float v;
               if (wave == 1) v = (n16 <= i) ? expf(gi - gj) * acc[s] : 0.f;
-              else if (wave == 2) v = (n16 >= i) ? sm.alpha[i] * expf(gi) * acc[s] : 0.f;
-              else v = (n16 >= i) ? expf(gi) * acc[s] : 0.f;
+              else if (wave == 2) v = (n16 >= i || n16 < lo) ? sm.alpha[i] * expf(gi) * acc[s] : 0.f;
+              else v = (n16 >= i || n16 < lo) ? expf(gi) * acc[s] : 0.f;
               acc[s] = v;
             }
           }
@@ -846,8 +851,8 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
           const float gi = sm.G[i], al = sm.alpha[i], ga = sm.gam[i];
           const float dij = (j <= i) ? expf(gi - sm.G[j]) : 0.f;
           PP(1, i, j) = dij * PP(1, i, j);
-          PP(2, i, j) = (j >= i) ? al * ga * PP(2, i, j) : 0.f;
-          PP(3, i, j) = (j >= i) ? ga * PP(3, i, j) : 0.f;
+          PP(2, i, j) = (j >= i || j < lo) ? al * ga * PP(2, i, j) : 0.f;
+          PP(3, i, j) = (j >= i || j < lo) ? ga * PP(3, i, j) : 0.f;
         }
       }
       __syncthreads();
@@ -896,12 +901,17 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
             const int i = it * 16 + 4 * g4 + s;
             float out = yv[s];
             if (live) out += sm.qco[i] * sm.kr[P + i][v];
-            const int t = c * P + i;
-            if (t < T) yp[(size_t)t * y_tok] = from_f<CT>(out);
+            const int t = c * P + i - p.t0;
+            if (t >= 0 && t < T) yp[(size_t)t * y_tok] = from_f<CT>(out);
           }
         }
 #pragma unroll
-        for (int it = 0; it < PT; ++it) uo[it][a] = un[it];
+        for (int it = 0; it < PT; ++it)
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int i = it * 16 + 4 * g4 + s;
+            if (i >= lo && i < hi) uo[it][a][s] = un[it][s];
+          }
         if (p.ts_u) {   // training stash: this chunk's net writes
           float* us = p.ts_u + ((size_t)chain * p.nch + c) * P * D + v;
 #pragma unroll
@@ -921,7 +931,13 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
       for (int q16 = 0; q16 < W16; ++q16) w[q16] = *(const uint4*)&sm.x[2 * P + j][d + q16 * (16 / sizeof(CT))];
       float kf[8];
       unpack8(w, kf, (const CT*)nullptr);
-      const float sc = sm.vsc[j];
+      float sc = sm.vsc[j];
+      if (j < lo || j >= hi) {   // a slot this chunk did not write: its old key, decayed over the chunk
+        sc = sm.gam[P - 1];
+        const f32x4 o0 = *(const f32x4*)&sm.vbd[j][d], o1 = *(const f32x4*)&sm.vbd[j][d + 4];
+        kf[0] = o0[0], kf[1] = o0[1], kf[2] = o0[2], kf[3] = o0[3];
+        kf[4] = o1[0], kf[5] = o1[1], kf[6] = o1[2], kf[7] = o1[3];
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) kf[e] *= sc;
       *(f32x4*)&sm.vbd[j][d] = (f32x4){kf[0], kf[1], kf[2], kf[3]};
@@ -950,13 +966,14 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
   }
   if (tid == 0) p.gsum[chain] = gacc;
   if (p.last && !p.complete) {  // no compaction follows: A, B decayed since the last one
+    // the workspace holds every chain's A [N][R m], then every chain's B [N][R n]
     const float dk = expf(gacc);
-    const float* ab = p.ab + (size_t)chain * Ge::R * (Ge::m + Ge::n);
+    const float* af = p.ab + (size_t)chain * Ge::R * Ge::m;
+    const float* bf = p.ab + (size_t)N * Ge::R * Ge::m + (size_t)chain * Ge::R * Ge::n;
     if (p.A_out)
-      for (int e = tid; e < Ge::R * Ge::m; e += kNT) p.A_out[(size_t)chain * Ge::R * Ge::m + e] = ab[e] * dk;
+      for (int e = tid; e < Ge::R * Ge::m; e += kNT) p.A_out[(size_t)chain * Ge::R * Ge::m + e] = af[e] * dk;
     if (p.B_out)
-      for (int e = tid; e < Ge::R * Ge::n; e += kNT)
-        p.B_out[(size_t)chain * Ge::R * Ge::n + e] = ab[Ge::R * Ge::m + e] * dk;
+      for (int e = tid; e < Ge::R * Ge::n; e += kNT) p.B_out[(size_t)chain * Ge::R * Ge::n + e] = bf[e] * dk;
   }
 }
 
@@ -971,12 +988,56 @@ struct G3CompactSmem {
   alignas(16) float vbd[P][D + 4];
 };
 
+// sum_r A_r (x) B_r as a [D][D] (v, k) matrix for the window kernel's reads,
+// from the factors Af [R][m], Bf [R][n] (LDS), in blocks: a thread takes one
+// factor entry (iv, ik) (TPP threads share one, splitting its b_v rows) and
+// writes the entries (iv b_v + jv, ik b_k + jk) it scales, 8 contiguous k
+// per store
+template <int D, typename CT>
+__device__ __forceinline__ void write_skron(CT* sk, const float* Af, const float* Bf, int tid) {
+  typedef G3D<D> Ge;
+  constexpr int TPP = kNT / Ge::m, RPT = Ge::bv / TPP;
+  static_assert(kNT % Ge::m == 0 && Ge::bv % TPP == 0 && Ge::bk == 8, "skron blocking");
+  const int pr = tid / TPP, part = tid % TPP;
+  const int iv = pr / Ge::ak, ik = pr % Ge::ak;
+  float a[Ge::R];
+#pragma unroll
+  for (int r = 0; r < Ge::R; ++r) a[r] = Af[r * Ge::m + pr];
+#pragma unroll
+  for (int jj = 0; jj < RPT; ++jj) {
+    const int jv = part * RPT + jj;
+    float sv[8];
+#pragma unroll
+    for (int jk = 0; jk < 8; ++jk) sv[jk] = 0.f;
+#pragma unroll
+    for (int r = 0; r < Ge::R; ++r) {
+      const f32x4 b0 = *(const f32x4*)&Bf[r * Ge::n + jv * Ge::bk];
+      const f32x4 b1 = *(const f32x4*)&Bf[r * Ge::n + jv * Ge::bk + 4];
+#pragma unroll
+      for (int jk = 0; jk < 4; ++jk) {
+        sv[jk] += a[r] * b0[jk];
+        sv[4 + jk] += a[r] * b1[jk];
+      }
+    }
+    store8(sk + (size_t)(iv * Ge::bv + jv) * D + ik * Ge::bk, sv);
+  }
+}
+
 template <int D, int P, typename CT>
 __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
   __shared__ G3CompactSmem<D, P> sm;
   static_assert(sizeof(G3CompactSmem<D, P>) <= 160 * 1024, "LDS budget");
   const int tid = threadIdx.x;
-  const int chain = blockIdx.x;
+  int chain = blockIdx.x;
+  if (p.pos) {   // decode batch: only the rows whose token closes a compaction interval
+    const int row = blockIdx.x / p.hm;
+    if ((p.pos[row] + 1) % p.Kc != 0) return;
+    if (p.slots) {
+      const int sl = p.slots[row];
+      if (sl < 0 || sl >= p.nslots) return;
+      chain = sl * p.hm + blockIdx.x % p.hm;
+    }
+  }
   typedef G3D<D> Ge;
   constexpr int Rm = Ge::R * Ge::m, Rn = Ge::R * Ge::n;
   for (int e = tid; e < Rm; e += kNT) sm.ab[e] = p.A[(size_t)chain * Rm + e];
@@ -990,7 +1051,7 @@ __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
   const float gacc = p.gsum ? p.gsum[chain] : 0.f;
   __syncthreads();
   g3_compact<D, P>(sm.k, sm.ab, sm.vbd, gacc, p.sdec, p.sketch + (size_t)chain * Ge::n * Ge::q,
-                   p.stats ? p.stats + (size_t)chain * 2 : nullptr, tid);
+                   p.stats ? p.stats + (size_t)blockIdx.x * 2 : nullptr, tid);
   for (int e = tid; e < Rm; e += kNT) {
     p.A_out[(size_t)chain * Rm + e] = sm.ab[e];
     if (p.A_fin) p.A_fin[(size_t)chain * Rm + e] = sm.ab[e];
@@ -1001,40 +1062,39 @@ __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
   }
   if (p.ab_stash)
     for (int e = tid; e < Rm + Rn; e += kNT) p.ab_stash[(size_t)chain * (Rm + Rn) + e] = sm.ab[e];
-  if (p.skron) {
-    // sum_r A_r (x) B_r as a [D][D] (v, k) matrix for the next interval's
-    // reads, in blocks: a thread takes one factor entry (iv, ik) (TPP threads
-    // share one, splitting its b_v rows) and writes the entries
-    // (iv b_v + jv, ik b_k + jk) it scales, 8 contiguous k per store
-    constexpr int TPP = kNT / Ge::m, RPT = Ge::bv / TPP;
-    static_assert(kNT % Ge::m == 0 && Ge::bv % TPP == 0 && Ge::bk == 8, "skron blocking");
-    CT* sk = (CT*)p.skron + (size_t)chain * D * D;
-    const float* Af = sm.ab;
-    const float* Bf = sm.ab + Rm;
-    const int pr = tid / TPP, part = tid % TPP;
-    const int iv = pr / Ge::ak, ik = pr % Ge::ak;
-    float a[Ge::R];
-#pragma unroll
-    for (int r = 0; r < Ge::R; ++r) a[r] = Af[r * Ge::m + pr];
-#pragma unroll
-    for (int jj = 0; jj < RPT; ++jj) {
-      const int jv = part * RPT + jj;
-      float sv[8];
-#pragma unroll
-      for (int jk = 0; jk < 8; ++jk) sv[jk] = 0.f;
-#pragma unroll
-      for (int r = 0; r < Ge::R; ++r) {
-        const f32x4 b0 = *(const f32x4*)&Bf[r * Ge::n + jv * Ge::bk];
-        const f32x4 b1 = *(const f32x4*)&Bf[r * Ge::n + jv * Ge::bk + 4];
-#pragma unroll
-        for (int jk = 0; jk < 4; ++jk) {
-          sv[jk] += a[r] * b0[jk];
-          sv[4 + jk] += a[r] * b1[jk];
-        }
-      }
-      store8(sk + (size_t)(iv * Ge::bv + jv) * D + ik * Ge::bk, sv);
-    }
+  if (p.skron) write_skron<D, CT>((CT*)p.skron + (size_t)chain * D * D, sm.ab, sm.ab + Rm, tid);
+}
+
+// The carried state (A0, B0, U0, Vb0 in the output layouts) in the window
+// kernel's workspace form: the factors, their Kronecker matrix, the window's
+// writes and keys slot-major, and no decay accumulated since the factors.
+template <int D, int P, typename CT>
+__global__ void __launch_bounds__(kNT) gdn3_state_in_kernel(G3FwdArgs p) {
+  typedef G3D<D> Ge;
+  constexpr int Rm = Ge::R * Ge::m, Rn = Ge::R * Ge::n;
+  __shared__ float ab[Rm + Rn];
+  const int tid = threadIdx.x, chain = blockIdx.x;
+  const int N = p.B * p.H * p.M;
+  for (int e = tid; e < Rm; e += kNT) {
+    const float a = p.A0[(size_t)chain * Rm + e];
+    ab[e] = a;
+    p.ab[(size_t)chain * Rm + e] = a;
   }
+  for (int e = tid; e < Rn; e += kNT) {
+    const float b = p.B0[(size_t)chain * Rn + e];
+    ab[Rm + e] = b;
+    p.ab[(size_t)N * Rm + (size_t)chain * Rn + e] = b;
+  }
+  // [D][P] -> [P][D]: consecutive threads read consecutive (d, slot) entries
+  const size_t cb = (size_t)chain * D * P;
+  for (int e = tid; e < D * P; e += kNT) {
+    const int d = e / P, j = e % P;
+    p.uw[cb + (size_t)j * D + d] = p.U0[cb + e];
+    p.vw[cb + (size_t)j * D + d] = p.Vb0[cb + e];
+  }
+  if (tid == 0) p.gsum[chain] = 0.f;
+  __syncthreads();
+  write_skron<D, CT>((CT*)p.skron + (size_t)chain * D * D, ab, ab + Rm, tid);
 }
 
 __global__ void fill_zero_kernel(float* p, long long n) {
@@ -1120,26 +1180,39 @@ int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
   a.vw = (float*)w;
   w += align256((size_t)N * P * D * 4);
   a.gsum = (float*)w;
-  const long long nab = (long long)N * Ge::R * (Ge::m + Ge::n);
-  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((nab + 255) / 256 < 4096 ? (nab + 255) / 256 : 4096)),
-                     dim3(256), 0, stream, a.ab, nab);
-  int rc = check_launch("fill_zero_kernel");
+  const bool carried = a.A0 != nullptr;
+  int rc;
+  if (carried) {
+    hipLaunchKernelGGL((gdn3_state_in_kernel<D, P, CT>), dim3(N), dim3(kNT), 0, stream, a);
+    rc = check_launch("gdn3_state_in_kernel");
+  } else {
+    const long long nab = (long long)N * Ge::R * (Ge::m + Ge::n);
+    hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)((nab + 255) / 256 < 4096 ? (nab + 255) / 256 : 4096)),
+                       dim3(256), 0, stream, a.ab, nab);
+    rc = check_launch("fill_zero_kernel");
+  }
   if (rc) return rc;
-  const int nch = (a.T + P - 1) / P, per = a.Kc / P;
-  a.nch = nch;
+  // chunks are global: chunk c covers tokens [c P, c P + P) of the whole
+  // sequence, of which this call holds [t0, t0 + T)
+  const long long tend = (long long)a.t0 + a.T;
+  const int cg0 = a.t0 / P, cg1 = (int)((tend + P - 1) / P);
+  a.nch = (a.T + P - 1) / P;
   G3Stash ts{nullptr, nullptr, nullptr};
-  if (a.train_states) ts = g3_stash(a.train_states, N, nch, a.T / a.Kc, D, P, Ge::RMN);
+  if (a.train_states) ts = g3_stash(a.train_states, N, a.nch, a.T / a.Kc, D, P, Ge::RMN);
   a.ts_u = ts.u;
   a.ts_g = ts.gacc;
+  const int per = a.Kc / P;
   int event = 0;
-  for (int c0 = 0; c0 < nch; c0 += per) {
-    const int c1 = c0 + per < nch ? c0 + per : nch;
+  bool first = true;
+  for (int c0 = cg0; c0 < cg1;) {
+    int c1 = (c0 / per + 1) * per;   // the next compaction boundary
+    if (c1 > cg1) c1 = cg1;
     a.c0 = c0;
     a.c1 = c1;
-    a.first = c0 == 0;
-    a.live = c0 > 0;
-    a.last = c1 == nch;
-    a.complete = (long long)c1 * P <= a.T && ((long long)c1 * P) % a.Kc == 0;
+    a.first = first && !carried;     // zero window state
+    a.live = !first || carried;      // the Kronecker factors may be nonzero
+    a.last = c1 == cg1;
+    a.complete = (long long)c1 * P <= tend && c1 % per == 0;
     hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P>), dim3(N), dim3(kNT), 0, stream, a);
     if ((rc = check_launch("gdn3_window_kernel"))) return rc;
     if (a.complete) {
@@ -1168,6 +1241,8 @@ int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
       if ((rc = compact_dispatch(ca, stream))) return rc;
       ++event;
     }
+    first = false;
+    c0 = c1;
   }
   return GDNX_OK;
 }

@@ -218,6 +218,26 @@ extern "C" int gdnx_delta_decode_step_slots(const void* q, const void* k, const 
   return decode_dispatch(a, (hipStream_t)stream);
 }
 
+extern "C" int gdnx_delta_decode_step_chan(const void* q, const void* k, const void* v, const float* a_e,
+                                           const float* a_w, const float* log_g, float* state_pool,
+                                           const int* slots, void* y, int NS, int n_slots, int H, int M,
+                                           int head_dim, int dtype, void* stream) {
+  g_err[0] = 0;
+  if (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16)
+    return set_error(GDNX_ERR_ARG, "dtype %d is not GDNX_DTYPE_F32/BF16", dtype);
+  if (head_dim != 64 && head_dim != 128)
+    return set_error(GDNX_ERR_SHAPE, "head_dim %d unsupported (64 or 128)", head_dim);
+  if (!slots) n_slots = NS;
+  if (NS < 1 || n_slots < 1 || H < 1 || M < 1 || (long long)NS * H * M > (1LL << 30) ||
+      (long long)n_slots * H * M > (1LL << 30))
+    return set_error(GDNX_ERR_SHAPE, "bad sizes NS=%d n_slots=%d H=%d M=%d", NS, n_slots, H, M);
+  if (!q || !k || !v || !a_e || !a_w || !log_g || !state_pool || !y)
+    return set_error(GDNX_ERR_ARG, "all pointers but slots must be non-null");
+  if ((uintptr_t)state_pool & 15u) return set_error(GDNX_ERR_ARG, "state_pool must be 16-byte aligned");
+  DecodeArgs a{q, k, v, a_e, a_w, log_g, state_pool, y, NS, H, M, head_dim, dtype, slots, n_slots, 1};
+  return decode_dispatch(a, (hipStream_t)stream);
+}
+
 // ---------------------------------------------------------------------------
 // GDN3 Kronecker-residual path
 // ---------------------------------------------------------------------------
@@ -281,15 +301,14 @@ extern "C" long long gdnx_gdn3_train_states_bytes(int B, int T, int H, int M, in
   return (long long)gdn3_train_states_bytes(B * H * M, T, head_dim, P, compact_every);
 }
 
-extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, int qkv_lanes,
-                                   const float* b_gates, const float* w_gates, int gate_channels,
-                                   const float* decay, const float* sketch, void* y, float* A_out,
-                                   float* B_out, float* U_out, float* Vb_out, double* comp_stats,
-                                   void* workspace, void* train_states, int B, int T, int H, int M,
-                                   int head_dim, int R, int P,
-                                   int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
-                                   int dtype, void* stream) {
-  g_err[0] = 0;
+namespace gdnx {
+// validation and argument packing shared by the two GDN3 forward entry points
+static int g3_fwd_args(G3FwdArgs& a, const void* q, const void* k, const void* v, int qkv_lanes,
+                       const float* b_gates, const float* w_gates, int gate_channels, const float* decay,
+                       const float* sketch, void* y, float* A_out, float* B_out, float* U_out, float* Vb_out,
+                       double* comp_stats, void* workspace, int B, int T, int H, int M, int head_dim, int R,
+                       int P, int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
+                       int dtype) {
   int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
   if (rc) return rc;
   G3Geom ge;
@@ -308,14 +327,10 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
     return set_error(GDNX_ERR_ARG, "gates, decay, sketch, y and workspace must be non-null");
   if (gate_channels > 1 && (!aligned16(b_gates) || !aligned16(w_gates)))
     return set_error(GDNX_ERR_ARG, "per-channel gates must be 16-byte aligned");
-  if (!aligned16(workspace) || (train_states && !aligned16(train_states)))
-    return set_error(GDNX_ERR_ARG, "workspace and train_states must be 16-byte aligned");
+  if (!aligned16(workspace)) return set_error(GDNX_ERR_ARG, "workspace must be 16-byte aligned");
   if (!(slow_decay >= 0.f && slow_decay <= 1.f))
     return set_error(GDNX_ERR_ARG, "slow_decay must lie in [0, 1]");
-  if ((A_out || B_out || U_out || Vb_out) && T % P != 0)
-    return set_error(GDNX_ERR_SHAPE, "final state needs T (%d) to be a multiple of P (%d)", T, P);
-  if (T == 0) return GDNX_OK;
-  G3FwdArgs a{};
+  a = G3FwdArgs{};
   a.q = q;
   a.k = k;
   a.v = v;
@@ -330,7 +345,6 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
   a.Vb_out = Vb_out;
   a.stats = comp_stats;
   a.workspace = workspace;
-  a.train_states = train_states;
   a.ge = ge;
   a.B = B;
   a.T = T;
@@ -343,7 +357,146 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
   a.gate_ch = gate_channels;
   a.dtype = dtype;
   a.sdec = slow_decay;
+  return GDNX_OK;
+}
+}  // namespace gdnx
+
+extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, int qkv_lanes,
+                                   const float* b_gates, const float* w_gates, int gate_channels,
+                                   const float* decay, const float* sketch, void* y, float* A_out,
+                                   float* B_out, float* U_out, float* Vb_out, double* comp_stats,
+                                   void* workspace, void* train_states, int B, int T, int H, int M,
+                                   int head_dim, int R, int P,
+                                   int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
+                                   int dtype, void* stream) {
+  g_err[0] = 0;
+  G3FwdArgs a;
+  int rc = g3_fwd_args(a, q, k, v, qkv_lanes, b_gates, w_gates, gate_channels, decay, sketch, y, A_out, B_out,
+                       U_out, Vb_out, comp_stats, workspace, B, T, H, M, head_dim, R, P, compact_every, a_v, a_k,
+                       b_v, b_k, slow_decay, dtype);
+  if (rc) return rc;
+  if (train_states && !aligned16(train_states)) return set_error(GDNX_ERR_ARG, "train_states must be 16-byte aligned");
+  if (T == 0) {   // the final state of an empty run is the zero initial state
+    const int N = B * H * M;
+    const size_t n[4] = {(size_t)N * R * a_v * a_k, (size_t)N * R * b_v * b_k, (size_t)N * head_dim * P,
+                         (size_t)N * head_dim * P};
+    float* outs[4] = {A_out, B_out, U_out, Vb_out};
+    for (int i = 0; i < 4; ++i)
+      if (outs[i] && hipMemsetAsync(outs[i], 0, n[i] * 4, (hipStream_t)stream) != hipSuccess)
+        return set_error(GDNX_ERR_HIP, "gdn3 forward: clearing the final state failed");
+    return GDNX_OK;
+  }
+  a.train_states = train_states;
   return gdn3_fwd_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_gdn3_num_compactions_from(int t0, int T, int P, int compact_every) {
+  if (t0 < 0 || T < 0 || P < 1 || compact_every < P || compact_every % P != 0 ||
+      (long long)t0 + T > 0x7fffffffLL)
+    return -1;
+  return (t0 + T) / compact_every - t0 / compact_every;
+}
+
+extern "C" int gdnx_gdn3_chunk_fwd_state(const void* q, const void* k, const void* v, int qkv_lanes,
+                                         const float* b_gates, const float* w_gates, int gate_channels,
+                                         const float* decay, const float* sketch, const float* A0,
+                                         const float* B0, const float* U0, const float* Vb0, int t0, void* y,
+                                         float* A_out, float* B_out, float* U_out, float* Vb_out,
+                                         double* comp_stats, void* workspace, int B, int T, int H, int M,
+                                         int head_dim, int R, int P, int compact_every, int a_v, int a_k,
+                                         int b_v, int b_k, float slow_decay, int dtype, void* stream) {
+  g_err[0] = 0;
+  G3FwdArgs a;
+  int rc = g3_fwd_args(a, q, k, v, qkv_lanes, b_gates, w_gates, gate_channels, decay, sketch, y, A_out, B_out,
+                       U_out, Vb_out, comp_stats, workspace, B, T, H, M, head_dim, R, P, compact_every, a_v, a_k,
+                       b_v, b_k, slow_decay, dtype);
+  if (rc) return rc;
+  const int nin = (A0 != nullptr) + (B0 != nullptr) + (U0 != nullptr) + (Vb0 != nullptr);
+  if (nin != 0 && nin != 4) return set_error(GDNX_ERR_ARG, "A0, B0, U0, Vb0 must all be given or all be null");
+  if (t0 < 0 || (long long)t0 + T > 0x7fffffffLL) return set_error(GDNX_ERR_SHAPE, "bad start position t0=%d", t0);
+  const int N = B * H * M;
+  const size_t n[4] = {(size_t)N * R * a_v * a_k, (size_t)N * R * b_v * b_k, (size_t)N * head_dim * P,
+                       (size_t)N * head_dim * P};
+  if (T == 0) {   // the state passes through unchanged
+    const float* ins[4] = {A0, B0, U0, Vb0};
+    float* outs[4] = {A_out, B_out, U_out, Vb_out};
+    for (int i = 0; i < 4; ++i) {
+      if (!outs[i]) continue;
+      const hipError_t e = ins[i] ? (outs[i] == ins[i] ? hipSuccess
+                                     : hipMemcpyAsync(outs[i], ins[i], n[i] * 4, hipMemcpyDeviceToDevice,
+                                                      (hipStream_t)stream))
+                                  : hipMemsetAsync(outs[i], 0, n[i] * 4, (hipStream_t)stream);
+      if (e != hipSuccess) return set_error(GDNX_ERR_HIP, "gdn3 forward: passing the state through failed");
+    }
+    return GDNX_OK;
+  }
+  a.t0 = t0;
+  a.A0 = A0;
+  a.B0 = B0;
+  a.U0 = U0;
+  a.Vb0 = Vb0;
+  return gdn3_fwd_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" int gdnx_gdn3_decode_step(const void* q, const void* k, const void* v, int qkv_lanes,
+                                     const float* b_gates, const float* w_gates, int gate_channels,
+                                     const float* decay, const float* sketch, float* A, float* Bf, float* U,
+                                     float* Vb, const int* slots, const int* pos, void* y, double* comp_stats,
+                                     int NS, int n_slots, int H, int M, int head_dim, int R, int P,
+                                     int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
+                                     int dtype, void* stream) {
+  g_err[0] = 0;
+  if (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16)
+    return set_error(GDNX_ERR_ARG, "dtype %d is not GDNX_DTYPE_F32/BF16", dtype);
+  G3Geom ge;
+  int rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge);
+  if (rc) return rc;
+  if ((rc = g3_layer_geom(head_dim, ge))) return rc;
+  if (!g3_window_ok(head_dim, P))
+    return set_error(GDNX_ERR_SHAPE, "residual window P=%d unsupported for head_dim %d", P, head_dim);
+  if (compact_every < P || compact_every % P != 0)
+    return set_error(GDNX_ERR_SHAPE, "compact_every=%d must be a positive multiple of P=%d", compact_every, P);
+  if (!slots) n_slots = NS;
+  if (NS < 1 || n_slots < 1 || H < 1 || M < 1 || (long long)NS * H * M > (1LL << 30) ||
+      (long long)n_slots * H * M > (1LL << 30))
+    return set_error(GDNX_ERR_SHAPE, "bad sizes NS=%d n_slots=%d H=%d M=%d", NS, n_slots, H, M);
+  if (qkv_lanes != 1 && qkv_lanes != M)
+    return set_error(GDNX_ERR_SHAPE, "qkv_lanes=%d must be 1 (shared) or M=%d", qkv_lanes, M);
+  if (gate_channels != 1 && gate_channels != head_dim)
+    return set_error(GDNX_ERR_SHAPE, "gate_channels=%d must be 1 or head_dim=%d", gate_channels, head_dim);
+  if (!q || !k || !v || !b_gates || !w_gates || !decay || !sketch || !A || !Bf || !U || !Vb || !pos || !y)
+    return set_error(GDNX_ERR_ARG, "inputs, state, pos and y must be non-null (slots may be null)");
+  if (!aligned16(A) || !aligned16(Bf) || !aligned16(U) || !aligned16(Vb))
+    return set_error(GDNX_ERR_ARG, "A, Bf, U, Vb must be 16-byte aligned");
+  if (!(slow_decay >= 0.f && slow_decay <= 1.f))
+    return set_error(GDNX_ERR_ARG, "slow_decay must lie in [0, 1]");
+  G3DecArgs a{q, k, v, b_gates, w_gates, decay, A, Bf, U, Vb, slots, pos, y, comp_stats,
+              NS, n_slots, H, M, head_dim, P, qkv_lanes, gate_channels, dtype};
+  if ((rc = gdn3_decode_dispatch(a, (hipStream_t)stream))) return rc;
+  // the rows whose token closes a compaction interval: the compaction of
+  // gdnx_gdn3_compact on their chains, in place (the others return at once)
+  G3CompactArgs ca{};
+  ca.A = A;
+  ca.Bf = Bf;
+  ca.U = U;
+  ca.Vb = Vb;
+  ca.sketch = sketch;
+  ca.A_out = A;
+  ca.B_out = Bf;
+  ca.stats = comp_stats;
+  ca.ge = ge;
+  ca.N = NS * H * M;
+  ca.D = head_dim;
+  ca.P = P;
+  ca.sdec = slow_decay;
+  ca.u_sp = 1;
+  ca.u_sd = P;
+  ca.pos = pos;
+  ca.slots = slots;
+  ca.hm = H * M;
+  ca.Kc = compact_every;
+  ca.nslots = n_slots;
+  return gdn3_compact_dispatch(ca, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_gdn3_chunk_bwd(const void* q, const void* k, const void* v, int qkv_lanes,

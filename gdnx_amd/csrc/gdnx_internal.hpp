@@ -112,6 +112,27 @@ struct DecodeArgs {
   int NS, H, M, D, dtype;
   const int* slots;    // [NS] state-pool slot of each row, or null (row s uses state s)
   int nslots;
+  int chan;            // 1: g is a log decay per key channel, [NS, H, M, D]
+};
+
+// One-token step of the GDN3 Kronecker-residual state (gdn3_decode.hip).
+// Row s of the batch advances state index slots[s] (or s) of every (h, m).
+struct G3DecArgs {
+  const void* q;       // [NS, H, qkv_lanes, D] io dtype
+  const void* k;
+  const void* v;
+  const float* bg;     // [NS, H, M, gate_ch]
+  const float* wg;
+  const float* dec;    // [NS, H, M]
+  float* A;            // [n_slots, H, M, R, a_v, a_k] (updated in place)
+  float* Bf;           // [n_slots, H, M, R, b_v, b_k]
+  float* U;            // [n_slots, H, M, D, P]
+  float* Vb;           // [n_slots, H, M, D, P]
+  const int* slots;    // [NS] or null
+  const int* pos;      // [NS] global token index of the row's token
+  void* y;             // [NS, H, M, D] io dtype
+  double* stats;       // [NS, H, M, 2] or null (zeroed; a compaction overwrites its chain's)
+  int NS, nslots, H, M, D, P, qkv_lanes, gate_ch, dtype;
 };
 
 // Kronecker-residual geometry: state S = sum_r A_r (x) B_r + U Vb^T with
@@ -142,6 +163,14 @@ struct G3FwdArgs {
   G3Geom ge;
   int B, T, H, M, D, P, Kc, qkv_lanes, gate_ch, dtype;
   float sdec;
+  // carried state: token 0 of this call is global token t0 (it writes slot
+  // t0 mod P; compactions follow global tokens t with (t + 1) mod Kc == 0);
+  // A0/B0/U0/Vb0 in the output layouts, or all null for a zero state
+  int t0;
+  const float* A0;
+  const float* B0;
+  const float* U0;
+  const float* Vb0;
   float* ts_u;         // (set by the dispatcher from train_states)
   float* ts_g;
   int nch;
@@ -173,6 +202,13 @@ struct G3CompactArgs {
   float* A_fin;        // optional second copy of the result, or null
   float* B_fin;
   float* ab_stash;     // [N][R (m + n)] copy of the result (A | B) for the backward, or null
+  // decode: block n is chain n of a batch of rows (hm = H M chains per row);
+  // it compacts only when (pos[row] + 1) % Kc == 0, on state index
+  // slots[row] * hm + n % hm (or n without slots; a slot outside
+  // [0, nslots) is an empty row).  pos null: every block compacts chain n.
+  const int* pos;
+  const int* slots;
+  int hm, Kc, nslots;
 };
 
 // Backward of the Kronecker-residual regime (gdn3_bwd.hip)
@@ -260,6 +296,7 @@ int gdn3_bwd_dispatch(const G3BwdArgs& a, hipStream_t stream);
 int gdn3_compact_dispatch(const G3CompactArgs& a, hipStream_t stream);
 int kron_read_dispatch(const KronReadArgs& a, hipStream_t stream);
 int decode_dispatch(const DecodeArgs& a, hipStream_t stream);
+int gdn3_decode_dispatch(const G3DecArgs& a, hipStream_t stream);
 int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);
 int delta_prep_dispatch(const DeltaArgs& a, hipStream_t stream);
 int delta_scan_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);

@@ -23,6 +23,8 @@ theirs), through the gdnx_gdn3_chunk_bwd kernel.
 """
 from __future__ import annotations
 
+import collections
+
 import torch
 
 from . import ops
@@ -90,19 +92,27 @@ def gdn3_scan(q, k, v, beta, log_g, state0=None, return_state=False):
     return (y, s) if return_state else y
 
 
-_SKETCHES = {}
+_SKETCHES = collections.OrderedDict()
+_SKETCH_CACHE = 8
 
 
 def default_sketch(N, n, q, device):
     """The compaction sketch: randn(N, n, q) float32 from a CPU generator
     seeded 1234 (the reference draws randn(N, n, q) from a generator seeded
     1234 on R_mat's device, gdn3/gdn3_upgrade.py:681-682; the CPU stream is
-    the one its CPU runs use).  Cached per (device, shape)."""
+    the one its CPU runs use, so this matches the reference on the CPU, not
+    its GPU runs).  Row n depends only on n, not on N.  The last few
+    (device, shape) draws are kept (least recently used dropped first)."""
     key = (str(device), N, n, q)
-    if key not in _SKETCHES:
-        gen = torch.Generator(device="cpu").manual_seed(1234)
-        _SKETCHES[key] = torch.randn(N, n, q, dtype=torch.float32, generator=gen).to(device)
-    return _SKETCHES[key]
+    if key in _SKETCHES:
+        _SKETCHES.move_to_end(key)
+        return _SKETCHES[key]
+    gen = torch.Generator(device="cpu").manual_seed(1234)
+    G = torch.randn(N, n, q, dtype=torch.float32, generator=gen).to(device)
+    _SKETCHES[key] = G
+    while len(_SKETCHES) > _SKETCH_CACHE:
+        _SKETCHES.popitem(last=False)
+    return G
 
 
 def _lane_shared(x):
@@ -148,7 +158,7 @@ class _GDN3Chunk(torch.autograd.Function):
 
 def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
                          factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None,
-                         sketch=None, return_state=False):
+                         sketch=None, return_state=False, state0=None, t0=0):
     """GDN3LinearAttn._gdn3_recurrent_state on the GPU.
 
     Reference: gdn3/gdn3_upgrade.py:403-531 with the semantics of its frozen
@@ -166,18 +176,30 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     return_state (comp_err is the reference's summed discarded energy, a
     device tensor).  When an input requires grad, y is differentiable in q,
     k, v, the gates and the decay (P = 16); the state and comp_err are not.
+
+    state0 = (A, B, U, Vb) and t0 continue a sequence from the state a
+    previous call returned after t0 tokens (inference only: no gradient flows
+    into or through a carried state); two calls over [0, T1) and [T1, T)
+    equal one over [0, T).
     """
     B, T, H, M = decay_factors.shape
     cdt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
     D = q.shape[-1]
-    if T == 0:   # empty sequence: zero output, the initial (zero) state, no compaction
+    a_v, a_k, b_v, b_k = factors
+    N = B * H * M
+    carried = state0 is not None or t0 != 0
+    if state0 is not None:
+        state0 = tuple(t.float().contiguous() for t in state0)
+    if T == 0:   # empty sequence: zero output, the initial state passes through, no compaction
         y = ops.empty_result((B, 0, H, M, D), cdt, q.device, q, k, v, b_gates, w_gates, decay_factors)
         if not return_state:
             return y
-        a_v, a_k, b_v, b_k = factors
-        N, dev = B * H * M, q.device
-        state = (torch.zeros(N, R, a_v, a_k, device=dev), torch.zeros(N, R, b_v, b_k, device=dev),
-                 torch.zeros(N, D, P, device=dev), torch.zeros(N, D, P, device=dev))
+        dev = q.device
+        if state0 is not None:
+            state = tuple(t.clone() for t in state0)
+        else:
+            state = (torch.zeros(N, R, a_v, a_k, device=dev), torch.zeros(N, R, b_v, b_k, device=dev),
+                     torch.zeros(N, D, P, device=dev), torch.zeros(N, D, P, device=dev))
         return y, state, torch.zeros((), dtype=torch.float64, device=dev)
 
     def lanes5(x):
@@ -197,12 +219,20 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
         bg = chan5(b_gates).float().expand(B, T, H, M, D).contiguous()
         wg = chan5(w_gates).float().expand(B, T, H, M, D).contiguous()
     dec = decay_factors.float().contiguous()
-    a_v, a_k, b_v, b_k = factors
-    N = B * H * M
     qw = ops.sketch_width(R, a_v * a_k, b_v * b_k)
     G = default_sketch(N, b_v * b_k, qw, q.device) if sketch is None else sketch.float().contiguous()
     train = torch.is_grad_enabled() and any(t.requires_grad for t in (q4, k4, v4, bg, wg, dec))
-    if train:
+    if train and carried:
+        raise ValueError("gdn3_recurrent_state: a carried state (state0 / t0) is inference only; "
+                         "run under torch.no_grad() or without state0")
+    if train and P != 16:
+        raise ValueError(f"gdn3_recurrent_state: the backward supports P = 16 (got P = {P}); "
+                         "run under torch.no_grad() for inference at this P")
+    if carried:
+        y, stats, state = ops.gdn3_chunk_fwd(q4, k4, v4, bg, wg, dec, G, M=M, R=R, P=P, factors=factors,
+                                             slow_decay=slow_decay, compact_every=compact_every,
+                                             return_state=return_state, state0=state0, t0=t0)
+    elif train:
         out = _GDN3Chunk.apply(q4, k4, v4, bg, wg, dec, G, (M, R, P, factors, slow_decay, compact_every),
                                return_state)
         y, stats, state = out[0], out[1], (tuple(out[2:]) if return_state else None)
@@ -226,3 +256,65 @@ class GDN3RecurrentState:
               slow_decay=0.97, compact_every=None):
         return gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, R=R, P=P, factors=factors,
                                     slow_decay=slow_decay, compact_every=compact_every)
+
+
+def gdn3_decode_step(q, k, v, b_gates, w_gates, decay_factors, state, pos, *, R=4, P=16,
+                     factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None, sketch=None,
+                     slots=None, return_stats=False):
+    """One token of the GDN3 recurrence per row, on a carried state updated in
+    place: one iteration of the frozen oracle's loop
+    (gdn3/_reference_recurrence.py:60-90) with the compaction after tokens
+    whose (pos + 1) % compact_every == 0 (the reference has no decode path).
+
+    q, k, v [NS,H,M,D] (a stride-0 lane dim is read once per head) or
+    [NS,H,D]; b_gates, w_gates [NS,H,M,K] / [NS,H,M,V] (an expand over the
+    channels is read as one scalar per lane) or [NS,H,M]; decay_factors
+    [NS,H,M].  state = (A, B, U, Vb) as gdn3_recurrent_state returns it
+    ([N, ...] with N = rows*H*M, rows = NS without slots) or with leading
+    dims [n_slots, H, M]; updated in place.  pos: each row's global token
+    index (int, sequence or int32 tensor [NS]); slots: int32 device tensor
+    [NS] of state rows (None: row s is state row s).  The sketch defaults to
+    the rows gdn3_recurrent_state draws for the same chains.  Returns y
+    [NS,H,M,V] in the compute dtype (and the compaction statistics [NS,H,M,2])."""
+    NS, H, M = decay_factors.shape
+    D = q.shape[-1]
+    dev = q.device
+    cdt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
+    a_v, a_k, b_v, b_k = factors
+
+    def shared(x):
+        return x.dim() == 3 or (x.dim() == 4 and x.stride(2) == 0)
+    if all(shared(x) for x in (q, k, v)):
+        q3, k3, v3 = (x if x.dim() == 3 else x.select(2, 0) for x in (q, k, v))
+    else:
+        q3, k3, v3 = (x.expand(NS, H, M, D) if x.dim() == 4 else x.unsqueeze(2).expand(NS, H, M, D)
+                      for x in (q, k, v))
+    q3, k3, v3 = (x.to(cdt).contiguous() for x in (q3, k3, v3))
+
+    def scalar(g):
+        return g.dim() == 3 or g.stride(-1) == 0
+    if all(scalar(g) for g in (b_gates, w_gates)):
+        bg, wg = (g if g.dim() == 3 else g.select(-1, 0) for g in (b_gates, w_gates))
+    else:
+        bg, wg = (g.unsqueeze(-1).expand(NS, H, M, D) if g.dim() == 3 else g for g in (b_gates, w_gates))
+    bg, wg = bg.float().contiguous(), wg.float().contiguous()
+    dec = decay_factors.float().contiguous()
+
+    A, Bf, U, Vb = state
+    if A.dim() == 4:   # [N, R, a_v, a_k]: view as [rows, H, M, ...] (same storage)
+        n_rows = A.shape[0] // (H * M)
+        A, Bf, U, Vb = (t.view(n_rows, H, M, *t.shape[1:]) for t in (A, Bf, U, Vb))
+    n_slots = A.shape[0]
+    if not isinstance(pos, torch.Tensor):
+        pos = [int(pos)] * NS if isinstance(pos, int) else [int(x) for x in pos]
+        pos = torch.tensor(pos, dtype=torch.int32)
+    pos = pos.to(device=dev, dtype=torch.int32).contiguous()
+    if slots is not None and not isinstance(slots, torch.Tensor):
+        slots = torch.tensor([int(x) for x in slots], dtype=torch.int32)
+    if slots is not None:
+        slots = slots.to(device=dev, dtype=torch.int32).contiguous()
+    qw = ops.sketch_width(R, a_v * a_k, b_v * b_k)
+    G = default_sketch(n_slots * H * M, b_v * b_k, qw, dev) if sketch is None else sketch.float().contiguous()
+    return ops.gdn3_decode_step(q3, k3, v3, bg, wg, dec, G, (A, Bf, U, Vb), pos, R=R, P=P, factors=factors,
+                                slow_decay=slow_decay, compact_every=compact_every, slots=slots,
+                                return_stats=return_stats)

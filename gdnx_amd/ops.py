@@ -196,6 +196,18 @@ def delta_chunk_bwd_grads(q, k, v, a_e, a_w, log_g, dy, chunk_states, ws, chunk,
     return out
 
 
+def _decode_out(out, shape, dtype, device):
+    """The y buffer of a decode step: a new tensor, or the caller's ``out``
+    after checking that the kernel can write it as [NS,H,M,D] contiguous."""
+    if out is None:
+        return torch.empty(shape, dtype=dtype, device=device)
+    _need(tuple(out.shape) == tuple(shape), f"out must be {list(shape)}, got {list(out.shape)}")
+    _need(out.dtype == dtype, f"out must be {dtype}, got {out.dtype}")
+    _need(out.is_contiguous(), "out must be contiguous")
+    _need(out.device == device, "out must be on q's device")
+    return out
+
+
 def delta_decode_step(q, k, v, a_e, a_w, log_g, state, out=None):
     """One-token decode step (state updated in place).
 
@@ -211,9 +223,11 @@ def delta_decode_step(q, k, v, a_e, a_w, log_g, state, out=None):
     _need(tuple(state.shape) == (NS, H, M, D, D) and state.dtype == torch.float32, "state must be fp32 [NS,H,M,D,D]")
     for t in (q, k, v, a_e, a_w, log_g, state):
         _need(t.is_contiguous(), "inputs must be contiguous")
+        _need(t.device == q.device, "inputs and state must be on one device")
     for t in (a_e, a_w, log_g):
         _need(t.dtype == torch.float32, "a_e, a_w, log_g must be float32")
-    y = torch.empty(NS, H, M, D, dtype=q.dtype, device=q.device) if out is None else out
+    _need(k.dtype == v.dtype == q.dtype, "q, k, v must share dtype")
+    y = _decode_out(out, (NS, H, M, D), q.dtype, q.device)
     with torch.cuda.device(q.device):
         rc = lib.gdnx_delta_decode_step(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w),
                                         _lib.ptr(log_g), _lib.ptr(state), _lib.ptr(y), NS, H, M, D,
@@ -240,15 +254,51 @@ def delta_decode_step_slots(q, k, v, a_e, a_w, log_g, state_pool, slots, out=Non
           "slots must be an int32 device tensor [NS]")
     for t in (q, k, v, a_e, a_w, log_g, state_pool, slots):
         _need(t.is_contiguous(), "inputs must be contiguous")
+        _need(t.device == q.device, "inputs, state_pool and slots must be on one device")
     for t in (a_e, a_w, log_g):
         _need(t.dtype == torch.float32, "a_e, a_w, log_g must be float32")
-    y = torch.empty(NS, H, M, D, dtype=q.dtype, device=q.device) if out is None else out
+    _need(k.dtype == v.dtype == q.dtype, "q, k, v must share dtype")
+    y = _decode_out(out, (NS, H, M, D), q.dtype, q.device)
     with torch.cuda.device(q.device):
         rc = lib.gdnx_delta_decode_step_slots(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w),
                                               _lib.ptr(log_g), _lib.ptr(state_pool), _lib.ptr(slots), _lib.ptr(y),
                                               NS, state_pool.shape[0], H, M, D, _lib.dtype_code(q.dtype),
                                               _lib.stream_of(q))
     _lib.check(rc, "gdnx_delta_decode_step_slots")
+    return y
+
+
+def delta_decode_step_chan(q, k, v, a_e, a_w, log_g, state_pool, slots=None, out=None):
+    """One-token decode step with a log-decay per key channel
+    (gdnx_delta_decode_step_chan): q, k, v [NS,H,D]; a_e, a_w [NS,H,M];
+    log_g [NS,H,M,D]; state_pool [n_slots,H,M,D,D] float32 updated in place
+    (row s updates slot slots[s], an int32 device tensor [NS], or state s
+    when slots is None).  Returns y [NS,H,M,D] in q's dtype."""
+    lib = _lib.load()
+    _need(q.is_cuda and q.dim() == 3 and q.shape == k.shape == v.shape, "q, k, v must be [NS,H,D] on GPU")
+    _need(k.dtype == v.dtype == q.dtype, "q, k, v must share dtype")
+    NS, H, D = q.shape
+    _need(a_e.dim() == 3 and tuple(a_e.shape[:2]) == (NS, H) and a_e.shape == a_w.shape, "a_e, a_w must be [NS,H,M]")
+    M = a_e.shape[2]
+    _need(tuple(log_g.shape) == (NS, H, M, D), "log_g must be [NS,H,M,D]")
+    _need(state_pool.dim() == 5 and tuple(state_pool.shape[1:]) == (H, M, D, D)
+          and state_pool.dtype == torch.float32, "state_pool must be fp32 [n_slots,H,M,D,D]")
+    if slots is None:
+        _need(state_pool.shape[0] == NS, "without slots the state must be [NS,H,M,D,D]")
+    else:
+        _need(slots.dtype == torch.int32 and tuple(slots.shape) == (NS,), "slots must be an int32 tensor [NS]")
+    for t in (q, k, v, a_e, a_w, log_g, state_pool) + ((slots,) if slots is not None else ()):
+        _need(t.is_contiguous(), "inputs must be contiguous")
+        _need(t.device == q.device, "inputs, state_pool and slots must be on one device")
+    for t in (a_e, a_w, log_g):
+        _need(t.dtype == torch.float32, "a_e, a_w, log_g must be float32")
+    y = _decode_out(out, (NS, H, M, D), q.dtype, q.device)
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_delta_decode_step_chan(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), _lib.ptr(a_e), _lib.ptr(a_w),
+                                             _lib.ptr(log_g), _lib.ptr(state_pool), _lib.ptr(slots), _lib.ptr(y),
+                                             NS, state_pool.shape[0], H, M, D, _lib.dtype_code(q.dtype),
+                                             _lib.stream_of(q))
+    _lib.check(rc, "gdnx_delta_decode_step_chan")
     return y
 
 
@@ -447,17 +497,32 @@ def gdn3_compact(A, Bk, U, Vb, sketch, slow_decay=0.97):
     return A_new, B_new, stats
 
 
+def _g3_state_check(state, N, R, factors, D, P, device):
+    a_v, a_k, b_v, b_k = factors
+    shapes = ((N, R, a_v, a_k), (N, R, b_v, b_k), (N, D, P), (N, D, P))
+    _need(len(state) == 4, "state must be (A, B, U, Vb)")
+    for t, shp, name in zip(state, shapes, ("A", "B", "U", "Vb")):
+        _need(tuple(t.shape) == shp, f"state {name} must be {list(shp)}, got {list(t.shape)}")
+        _need(t.dtype == torch.float32 and t.is_contiguous() and t.device == device,
+              f"state {name} must be contiguous float32 on the inputs' device")
+
+
 def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
                    factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None, return_state=False,
-                   save_states=False):
+                   save_states=False, state0=None, t0=0):
     """GDN3 recurrence with residual window and compaction (gdnx_gdn3_chunk_fwd).
 
     q, k, v: [B,T,H,D] (shared by the M lanes) or [B,T,H,M,D] (per lane),
     bf16 or float32, contiguous.  b_gates, w_gates: [B,T,H,M] (scalar per
     lane) or [B,T,H,M,D] float32.  decay [B,T,H,M] float32.  sketch
     [B*H*M, b_v*b_k, q] float32.  Returns (y [B,T,H,M,D] in q's dtype,
-    stats [T // K_c, N, 2] float64, state (A, B, U, Vb) or None), and with
-    save_states a fourth item: the training stash gdn3_chunk_bwd reads."""
+    stats [n_compactions, N, 2] float64, state (A, B, U, Vb) or None), and
+    with save_states a fourth item: the training stash gdn3_chunk_bwd reads.
+
+    state0 = (A, B, U, Vb) and t0 continue a sequence (gdnx_gdn3_chunk_fwd_state):
+    the call's token t is global token t0 + t (slot (t0 + t) % P, compaction
+    after it when (t0 + t + 1) % K_c == 0), from the state a previous call
+    returned; inference only."""
     lib = _lib.load()
     a_v, a_k, b_v, b_k = factors
     B, T, H = q.shape[:3]
@@ -478,12 +543,16 @@ def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
     _need(tuple(sketch.shape) == (N, b_v * b_k, sketch_width(R, a_v * a_k, b_v * b_k)) and sketch.is_cuda,
           "sketch must be [B*H*M, b_v*b_k, min(R+4, a_v*a_k, b_v*b_k)] on the GPU")
     dt = _lib.dtype_code(q.dtype)
+    carried = state0 is not None or t0 != 0
+    _need(not (carried and save_states), "a carried state (state0 / t0) is inference only")
+    if state0 is not None:
+        _g3_state_check(state0, N, R, factors, D, P, q.device)
     y = torch.empty(B, T, H, M, D, dtype=q.dtype, device=q.device)
     nws = lib.gdnx_gdn3_workspace_bytes(B, H, M, D, P, dt)
     _need(nws > 0, f"unsupported GDN3 shape: head_dim {D}, P {P}")
     ws = torch.empty(nws, dtype=torch.uint8, device=q.device)
-    n_ev = lib.gdnx_gdn3_num_compactions(T, P, Kc)
-    _need(n_ev >= 0, f"compact_every={Kc} must be a positive multiple of P={P}")
+    n_ev = lib.gdnx_gdn3_num_compactions_from(int(t0), T, P, Kc)
+    _need(n_ev >= 0, f"compact_every={Kc} must be a positive multiple of P={P} (t0={t0} >= 0)")
     stats = torch.empty(max(n_ev, 1), N, 2, dtype=torch.float64, device=q.device)
     state = None
     ptrs = [None] * 4
@@ -497,15 +566,75 @@ def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
         _need(nts > 0, f"unsupported GDN3 shape for training: head_dim {D}, P {P}")
         tst = torch.empty(nts, dtype=torch.uint8, device=q.device)
     with torch.cuda.device(q.device):
-        rc = lib.gdnx_gdn3_chunk_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), lanes, _lib.ptr(b_gates),
-                                     _lib.ptr(w_gates), gate_ch, _lib.ptr(decay), _lib.ptr(sketch), _lib.ptr(y),
-                                     *ptrs, _lib.ptr(stats) if n_ev > 0 else None, _lib.ptr(ws), _lib.ptr(tst),
-                                     B, T, H, M, D, R, P, Kc, a_v, a_k, b_v, b_k, float(slow_decay), dt,
-                                     _lib.stream_of(q))
+        if carried:
+            s0 = [None] * 4 if state0 is None else [_lib.ptr(t) for t in state0]
+            rc = lib.gdnx_gdn3_chunk_fwd_state(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), lanes, _lib.ptr(b_gates),
+                                               _lib.ptr(w_gates), gate_ch, _lib.ptr(decay), _lib.ptr(sketch), *s0,
+                                               int(t0), _lib.ptr(y), *ptrs, _lib.ptr(stats) if n_ev > 0 else None,
+                                               _lib.ptr(ws), B, T, H, M, D, R, P, Kc, a_v, a_k, b_v, b_k,
+                                               float(slow_decay), dt, _lib.stream_of(q))
+        else:
+            rc = lib.gdnx_gdn3_chunk_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), lanes, _lib.ptr(b_gates),
+                                         _lib.ptr(w_gates), gate_ch, _lib.ptr(decay), _lib.ptr(sketch), _lib.ptr(y),
+                                         *ptrs, _lib.ptr(stats) if n_ev > 0 else None, _lib.ptr(ws), _lib.ptr(tst),
+                                         B, T, H, M, D, R, P, Kc, a_v, a_k, b_v, b_k, float(slow_decay), dt,
+                                         _lib.stream_of(q))
     _lib.check(rc, "gdnx_gdn3_chunk_fwd")
     if save_states:
         return y, stats[:n_ev], state, tst
     return y, stats[:n_ev], state
+
+
+def gdn3_decode_step(q, k, v, b_gates, w_gates, decay, sketch, state, pos, *, R=4, P=16,
+                     factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None, slots=None,
+                     return_stats=False, out=None):
+    """One token of the GDN3 Kronecker-residual recurrence per row on a
+    carried state (gdnx_gdn3_decode_step), updated in place.
+
+    q, k, v [NS,H,D] (shared by the lanes) or [NS,H,M,D]; b_gates, w_gates
+    [NS,H,M] or [NS,H,M,D] float32; decay [NS,H,M]; state = (A, B, U, Vb)
+    with leading dims [n_slots, H, M] (n_slots = NS without slots); sketch
+    [n_slots*H*M, b_v*b_k, q]; pos int32 device [NS]: each row's global token
+    index (slot pos % P; compaction after it when (pos + 1) % K_c == 0);
+    slots int32 device [NS] or None.  Returns y [NS,H,M,D] in q's dtype (and
+    the per-chain compaction statistics [NS,H,M,2] float64)."""
+    lib = _lib.load()
+    a_v, a_k, b_v, b_k = factors
+    _need(q.is_cuda and q.dim() in (3, 4) and q.shape == k.shape == v.shape, "q, k, v must be [NS,H,(M,)D] on GPU")
+    _need(q.dtype in (torch.bfloat16, torch.float32) and q.dtype == k.dtype == v.dtype, "q, k, v: bf16 or float32")
+    NS, H = q.shape[:2]
+    D = q.shape[-1]
+    _need(decay.dim() == 3 and tuple(decay.shape[:2]) == (NS, H), "decay must be [NS,H,M]")
+    M = decay.shape[2]
+    lanes = 1 if q.dim() == 3 else q.shape[2]
+    _need(lanes in (1, M), "q/k/v lane dim must be 1 or M")
+    gate_ch = 1 if b_gates.dim() == 3 else b_gates.shape[-1]
+    _need(b_gates.shape == w_gates.shape and tuple(b_gates.shape[:3]) == (NS, H, M), "bad gate shapes")
+    A, Bf, U, Vb = state
+    n_slots = A.shape[0]
+    _need(slots is not None or n_slots == NS, "without slots the state's leading dim must be NS")
+    N = n_slots * H * M
+    _g3_state_check([t.view(N, *t.shape[3:]) for t in state], N, R, factors, D, P, q.device)
+    _need(tuple(A.shape[:3]) == (n_slots, H, M), "state leading dims must be [n_slots, H, M]")
+    _need(tuple(sketch.shape) == (N, b_v * b_k, sketch_width(R, a_v * a_k, b_v * b_k)), "bad sketch shape")
+    _need(pos.dtype == torch.int32 and tuple(pos.shape) == (NS,), "pos must be an int32 tensor [NS]")
+    if slots is not None:
+        _need(slots.dtype == torch.int32 and tuple(slots.shape) == (NS,), "slots must be an int32 tensor [NS]")
+    for t in (q, k, v, b_gates, w_gates, decay, sketch, pos) + ((slots,) if slots is not None else ()):
+        _need(t.is_contiguous() and t.device == q.device, "inputs must be contiguous on one device")
+    for t in (b_gates, w_gates, decay, sketch):
+        _need(t.dtype == torch.float32, "gates, decay and sketch must be float32")
+    Kc = P if compact_every is None else int(compact_every)
+    y = _decode_out(out, (NS, H, M, D), q.dtype, q.device)
+    stats = torch.empty(NS, H, M, 2, dtype=torch.float64, device=q.device) if return_stats else None
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_gdn3_decode_step(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), lanes, _lib.ptr(b_gates),
+                                       _lib.ptr(w_gates), gate_ch, _lib.ptr(decay), _lib.ptr(sketch),
+                                       *(_lib.ptr(t) for t in state), _lib.ptr(slots), _lib.ptr(pos), _lib.ptr(y),
+                                       _lib.ptr(stats), NS, n_slots, H, M, D, R, P, Kc, a_v, a_k, b_v, b_k,
+                                       float(slow_decay), _lib.dtype_code(q.dtype), _lib.stream_of(q))
+    _lib.check(rc, "gdnx_gdn3_decode_step")
+    return (y, stats) if return_stats else y
 
 
 def gdn3_chunk_bwd(q, k, v, b_gates, w_gates, decay, dy, train_states, *, M, R=4, P=16,

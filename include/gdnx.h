@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 7
+#define GDNX_ABI_VERSION 8
 
 enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1 };
 
@@ -160,6 +160,18 @@ int gdnx_delta_decode_step_slots(const void* q, const void* k, const void* v,
                                  float* state_pool, const int* slots, void* y, int NS,
                                  int n_slots, int H, int M, int head_dim, int dtype, void* stream);
 
+/* The decode step with a decay per key channel, for the KMD-2 native state
+ * (one step of research/kernel_ab/ref_scan.py:40-45 and of
+ * gdn3/kmd2_native.py:109-132; the reference has no decode path):
+ * S <- diag(g) S;  r = a_w v - a_e S^T k;  S <- S + k r^T;  y = S^T q, with
+ * log_g [NS, H, M, D] float32 (natural log, clamped to <= 0, per key
+ * channel).  Other arguments as gdnx_delta_decode_step_slots; slots may be
+ * NULL (row s updates state s; n_slots ignored).  KMD-2's query slots enter
+ * as their mixed query sum_r out_mix[h, r] q_r (the read is linear in q). */
+int gdnx_delta_decode_step_chan(const void* q, const void* k, const void* v,
+                                const float* a_e, const float* a_w, const float* log_g,
+                                float* state_pool, const int* slots, void* y, int NS,
+                                int n_slots, int H, int M, int head_dim, int dtype, void* stream);
 
 /* ---- Per-key-channel decay (the general KMD-2 scan) -----------------------
  * One chain per (batch, head), float32:  S <- diag(g_t) S (g per key
@@ -240,8 +252,9 @@ int gdnx_gdn3_num_compactions(int T, int P, int compact_every);
  *   decay        [B, T, H, M] float32 multiplicative decay
  *   sketch       [B*H*M, b_v*b_k, min(R+4, a_v*a_k, b_v*b_k)] float32
  *   y            [B, T, H, M, D] io dtype
- *   A_out, B_out, U_out, Vb_out  final state (each may be NULL; any non-NULL
- *                needs T % P == 0)
+ *   A_out, B_out, U_out, Vb_out  final state in the layouts above (each
+ *                may be NULL), for any T: U / Vb slot t mod P holds the write
+ *                and key of the last token t that used it
  *   comp_stats   [T / compact_every, B*H*M, 2] float64 (|R_mat|^2, kept
  *                sigma^2 per chain and compaction) or NULL; the reference's
  *                comp_err is sum over compactions of max(0, sum_n energy -
@@ -260,6 +273,61 @@ int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, int qkv_lan
                         void* workspace, void* train_states, int B, int T, int H, int M,
                         int head_dim, int R, int P, int compact_every, int a_v, int a_k, int b_v,
                         int b_k, float slow_decay, int dtype, void* stream);
+
+/* Number of compactions a call over global tokens [t0, t0 + T) runs (rows
+ * of its comp_stats): those after tokens t with (t + 1) % compact_every == 0;
+ * -1 if invalid. */
+int gdnx_gdn3_num_compactions_from(int t0, int T, int P, int compact_every);
+
+/* gdnx_gdn3_chunk_fwd on a carried state, for prefill and continuation (no
+ * counterpart in the reference, whose recurrence always starts from zero
+ * state at slot 0: gdn3/_reference_recurrence.py:52-56; its layer ignores
+ * cache_params, gdn3/gdn3_upgrade.py:725).  Token t of the call is global
+ * token t0 + t of the sequence: it writes slot (t0 + t) % P, and a
+ * compaction follows it when (t0 + t + 1) % compact_every == 0, so two calls
+ * over [0, T1) and [T1, T) (the second from the first's final state, t0 = T1)
+ * equal one call over [0, T).  A0 [N,R,a_v,a_k], B0 [N,R,b_v,b_k],
+ * U0 [N,D,P], Vb0 [N,D,P] (N = B H M, all four or none; none = zero state)
+ * as a previous call returned them; t0 is the same for every chain.  The
+ * final state may alias the initial one.  comp_stats has
+ * gdnx_gdn3_num_compactions_from(t0, T, P, compact_every) rows.  Inference
+ * only (no training stash); other arguments as gdnx_gdn3_chunk_fwd. */
+int gdnx_gdn3_chunk_fwd_state(const void* q, const void* k, const void* v, int qkv_lanes,
+                              const float* b_gates, const float* w_gates, int gate_channels,
+                              const float* decay, const float* sketch, const float* A0, const float* B0,
+                              const float* U0, const float* Vb0, int t0, void* y, float* A_out,
+                              float* B_out, float* U_out, float* Vb_out, double* comp_stats,
+                              void* workspace, int B, int T, int H, int M, int head_dim, int R, int P,
+                              int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
+                              int dtype, void* stream);
+
+/* One-token GDN3 decode step on a carried Kronecker-residual state, updated
+ * in place.  One iteration of the frozen oracle's token loop
+ * (gdn3/_reference_recurrence.py:60-90; the reference itself has no decode
+ * path): gamma = clamp(dec, 0, 1) decays A, B, Vb; r = w.v - S (b.k);
+ * y = S q + alpha(k.b.k) (k.q) r; slot pos % P receives (alpha r, k); after a
+ * token with (pos + 1) % compact_every == 0 the compaction of
+ * gdnx_gdn3_compact runs on that row's chains (same sign convention).
+ *   q, k, v      [NS, H, qkv_lanes, D] io dtype (qkv_lanes 1 or M)
+ *   b_gates, w_gates [NS, H, M, gate_channels] float32; decay [NS, H, M]
+ *   A [n_slots,H,M,R,a_v,a_k], Bf [n_slots,H,M,R,b_v,b_k], U, Vb
+ *                [n_slots,H,M,D,P] float32: the state, in place
+ *   sketch       [n_slots*H*M, b_v*b_k, q] float32 (rows by state index)
+ *   slots        [NS] int32 device: row s advances state slots[s] (a slot
+ *                outside [0, n_slots) is an empty row: y = 0, nothing
+ *                touched); NULL: row s advances state s (n_slots ignored)
+ *   pos          [NS] int32 device, >= 0: global index of row s's token
+ *   y            [NS, H, M, D] io dtype
+ *   comp_stats   [NS, H, M, 2] float64 or NULL: (|R_mat|^2, kept sigma^2)
+ *                for chains compacted by this step, zero for the others
+ * Rows that name the same slot race.  Supported shapes as gdnx_gdn3_chunk_fwd. */
+int gdnx_gdn3_decode_step(const void* q, const void* k, const void* v, int qkv_lanes,
+                          const float* b_gates, const float* w_gates, int gate_channels,
+                          const float* decay, const float* sketch, float* A, float* Bf, float* U,
+                          float* Vb, const int* slots, const int* pos, void* y, double* comp_stats,
+                          int NS, int n_slots, int H, int M, int head_dim, int R, int P,
+                          int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
+                          int dtype, void* stream);
 
 /* Bytes of the gdnx_gdn3_chunk_fwd training stash; -1 if invalid. */
 long long gdnx_gdn3_train_states_bytes(int B, int T, int H, int M, int head_dim, int P,

@@ -178,7 +178,7 @@ def delta_rule_chunked_chan(q, k, a_e, w, log_gamma, chunk: int = 16, state0=Non
 
 
 def kmd2_scan(q, k, v, g, beta_e, beta_w, out_mix=None, return_scores=False,
-              dtype=torch.float64):
+              dtype=torch.float64, state0=None, return_state=False):
     """KMD-2 native scan: ``scan(q, k, v, g, beta_e, beta_w, out_mix)``.
 
     Restates research/kernel_ab/ref_scan.py:24-48 (identical maths to
@@ -187,13 +187,15 @@ def kmd2_scan(q, k, v, g, beta_e, beta_w, out_mix=None, return_scores=False,
     q [B,T,H,r_out,dk], k [B,T,H,dk], v [B,T,H,dv], g [B,T,H,dk]
     (multiplicative per-channel decay), beta_e/beta_w [B,T,H],
     out_mix [H,r_out] (required iff r_out > 1).  Returns y [B,T,H,dv]
-    (and scores [B,T,H], detached, when return_scores).
+    (and scores [B,T,H], detached, when return_scores).  state0
+    [B,H,dk,dv] starts the loop from a carried state instead of zero (the
+    reference always starts at zero); return_state appends the final state.
     """
     B, T, H, r_out, dk = q.shape
     dv = v.shape[-1]
     q, k, v, g, be, bw = (x.to(dtype) for x in (q, k, v, g, beta_e, beta_w))
     mix = None if out_mix is None else out_mix.to(dtype)
-    S = torch.zeros(B, H, dk, dv, dtype=dtype)
+    S = torch.zeros(B, H, dk, dv, dtype=dtype) if state0 is None else state0.to(dtype)
     ys, scores = [], []
     for t in range(T):
         Sb = g[:, t].unsqueeze(-1) * S
@@ -207,10 +209,11 @@ def kmd2_scan(q, k, v, g, beta_e, beta_w, out_mix=None, return_scores=False,
         else:
             ys.append((reads * mix.view(1, H, r_out, 1)).sum(2))
         scores.append(key.norm(dim=-1) * upd.norm(dim=-1))
-    y = torch.stack(ys, 1)
-    if return_scores:
-        return y, torch.stack(scores, 1).detach()
-    return y
+    y = torch.stack(ys, 1) if T > 0 else torch.zeros(B, 0, H, dv, dtype=dtype)
+    out = (y, torch.stack(scores, 1).detach()) if return_scores else y
+    if return_state:
+        return (*out, S) if return_scores else (out, S)
+    return out
 
 
 def gdn3_dense_coeffs(k, beta):

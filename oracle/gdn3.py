@@ -121,7 +121,7 @@ def compact(A, Bk, U, Vb, slow_decay, sketch, sign_mode="lapack"):
 def gdn3_recurrence(q, k, v, b_gates, w_gates, dec, *, R=4, P=16,
                     factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None,
                     sketch=None, sign_mode="lapack", dtype=torch.float64,
-                    return_state=False):
+                    return_state=False, state0=None, t0=0):
     """Sequential GDN3 recurrence, ``reference_recurrent_state`` generalised.
 
     Restates gdn3/_reference_recurrence.py:33-94.  q,k,b_gates [B,T,H,M,K],
@@ -129,6 +129,14 @@ def gdn3_recurrence(q, k, v, b_gates, w_gates, dec, *, R=4, P=16,
     [0,1]).  factors = (a_v, a_k, b_v, b_k) with a_v*b_v = V, a_k*b_k = K.
     compact_every = K_c (default P).  Returns y [B,T,H,M,V] (and the final
     state (A, Bk, U, Vb) plus the summed compaction error when return_state).
+
+    Carried state (no counterpart in the reference, whose loop always starts
+    from zero at p = 0): state0 = (A, Bk, U, Vb) in the layouts above, as a
+    previous call returned them, and t0 = the number of tokens that call had
+    processed.  Token t of this call is then global token t0 + t: it writes
+    slot (t0 + t) mod P and a compaction follows it when (t0 + t + 1) mod K_c
+    == 0, so running [0, T1) and then [T1, T) from the returned state equals
+    one run over [0, T).
     """
     B, T, H, M, K = q.shape
     V = v.shape[-1]
@@ -147,20 +155,26 @@ def gdn3_recurrence(q, k, v, b_gates, w_gates, dec, *, R=4, P=16,
     qrank = min(R + 4, a_v * a_k, b_v * b_k)
     G = reference_sketch(N, b_v * b_k, qrank) if sketch is None else sketch
 
-    A = torch.zeros(N, R, a_v, a_k, dtype=dtype)
-    Bk = torch.zeros(N, R, b_v, b_k, dtype=dtype)
-    U = torch.zeros(N, V, P, dtype=dtype)
-    Vb = torch.zeros(N, K, P, dtype=dtype)
+    if state0 is None:
+        A = torch.zeros(N, R, a_v, a_k, dtype=dtype)
+        Bk = torch.zeros(N, R, b_v, b_k, dtype=dtype)
+        U = torch.zeros(N, V, P, dtype=dtype)
+        Vb = torch.zeros(N, K, P, dtype=dtype)
+    else:
+        A, Bk, U, Vb = (x.to(dtype) for x in state0)
+        assert A.shape == (N, R, a_v, a_k) and Bk.shape == (N, R, b_v, b_k)
+        assert U.shape == (N, V, P) and Vb.shape == (N, K, P)
     ys = []
     err_total = torch.zeros((), dtype=dtype)
-    for t in range(T):
-        gam = dc[t].clamp(0.0, 1.0)
+    for tl in range(T):
+        t = t0 + tl
+        gam = dc[tl].clamp(0.0, 1.0)
         A = A * gam.view(N, 1, 1, 1)
         Bk = Bk * gam.view(N, 1, 1, 1)
         Vb = Vb * gam.view(N, 1, 1)
-        kt, qt = kf[t], qf[t]
-        h = bg[t] * kt
-        u = wg[t] * vf[t]
+        kt, qt = kf[tl], qf[tl]
+        h = bg[tl] * kt
+        u = wg[tl] * vf[tl]
         r = u - kron_read(A, Bk, U, Vb, h)
         alpha = stable_alpha((kt * h).sum(-1))
         s_q = kron_read(A, Bk, U, Vb, qt)

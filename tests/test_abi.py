@@ -125,3 +125,94 @@ def test_layer_boundary_entry_points_reject_bad_arguments():
     assert lib.gdnx_gdn3_epilogue_workspace_bytes(4, 4096, 16, 128) == 2048 * 128 * 4
     assert lib.gdnx_gdn3_epilogue_workspace_bytes(1, 3, 1, 128) == 1 * 128 * 4
     assert lib.gdnx_gdn3_epilogue_workspace_bytes(1, 17, 1, 64) == 2 * 64 * 4
+
+
+def test_gdn3_compaction_count_from_a_start_position():
+    lib = _lib.load()
+    f = lib.gdnx_gdn3_num_compactions_from
+    assert f(0, 64, 16, 16) == 4           # after tokens 15, 31, 47, 63
+    assert f(5, 40, 16, 16) == 2           # tokens 5..44: after 15 and 31
+    assert f(30, 2, 16, 16) == 1           # token 31 closes an interval
+    assert f(37, 100, 16, 48) == 2         # after 47 and 95
+    assert f(0, 0, 16, 16) == 0
+    assert f(-1, 4, 16, 16) == -1 and f(0, 4, 16, 24) == -1
+    assert lib.gdnx_gdn3_num_compactions(64, 16, 32) == f(0, 64, 16, 32)
+
+
+def _g3_state_fwd(lib, A0=16, B0=16, U0=16, Vb0=16, t0=0, D=128, P=16, Kc=16, ws=16):
+    vp = lambda x: None if x is None else ctypes.c_void_p(x)
+    return lib.gdnx_gdn3_chunk_fwd_state(vp(16), vp(16), vp(16), 1, vp(16), vp(16), 1, vp(16), vp(16),
+                                         vp(A0), vp(B0), vp(U0), vp(Vb0), t0, vp(16), None, None, None, None, None,
+                                         vp(ws), 1, 8, 1, 1, D, 4, P, Kc, 16 if D == 128 else 8,
+                                         16 if D == 128 else 8, 8, 8, 0.97, _lib.DTYPE_F32, None)
+
+
+def test_gdn3_state_forward_rejects_bad_arguments():
+    lib = _lib.load()
+    assert _g3_state_fwd(lib, B0=None) == -1
+    assert "all be given" in lib.gdnx_last_error().decode()
+    assert _g3_state_fwd(lib, t0=-3) == -2
+    assert "t0" in lib.gdnx_last_error().decode()
+    assert _g3_state_fwd(lib, P=32) == -2
+    assert "P=32" in lib.gdnx_last_error().decode()
+    assert _g3_state_fwd(lib, Kc=24) == -2
+    assert _g3_state_fwd(lib, ws=None) == -1
+
+
+def _g3_decode(lib, pos=16, A=16, qkv_lanes=1, gate_ch=1, NS=2, slots=None, P=16):
+    vp = lambda x: None if x is None else ctypes.c_void_p(x)
+    return lib.gdnx_gdn3_decode_step(vp(16), vp(16), vp(16), qkv_lanes, vp(16), vp(16), gate_ch, vp(16), vp(16),
+                                     vp(A), vp(16), vp(16), vp(16), vp(slots), vp(pos), vp(16), None, NS, 4, 2, 2,
+                                     128, 4, P, 16, 16, 16, 8, 8, 0.97, _lib.DTYPE_BF16, None)
+
+
+def test_gdn3_decode_step_rejects_bad_arguments():
+    lib = _lib.load()
+    assert _g3_decode(lib, pos=None) == -1
+    assert "pos" in lib.gdnx_last_error().decode()
+    assert _g3_decode(lib, A=24) == -1
+    assert "aligned" in lib.gdnx_last_error().decode()
+    assert _g3_decode(lib, qkv_lanes=3) == -2
+    assert _g3_decode(lib, gate_ch=5) == -2
+    assert _g3_decode(lib, NS=0) == -2
+    assert _g3_decode(lib, P=64) == -2
+
+
+def test_chan_decode_step_rejects_bad_arguments():
+    lib = _lib.load()
+    vp = ctypes.c_void_p
+    args = [vp(16)] * 7 + [None, vp(16)]
+    assert lib.gdnx_delta_decode_step_chan(*args, 2, 0, 1, 1, 96, _lib.DTYPE_F32, None) == -2
+    assert "head_dim" in lib.gdnx_last_error().decode()
+    bad = [vp(16)] * 6 + [vp(24), None, vp(16)]
+    assert lib.gdnx_delta_decode_step_chan(*bad, 2, 0, 1, 1, 128, _lib.DTYPE_F32, None) == -1
+    assert lib.gdnx_delta_decode_step_chan(*([vp(16)] * 5 + [None, vp(16), None, vp(16)]), 2, 0, 1, 1, 128,
+                                           _lib.DTYPE_F32, None) == -1
+
+
+def test_decode_cache_host_slot_logic():
+    """Slot bookkeeping runs on the host: a free list checked as a whole and
+    duplicate rows refused before any launch (CPU tensors stand in for the
+    pool; no compute call is made)."""
+    from gdnx_amd.decode_cache import DecodeStateCache
+    for kind in ("dense", "gdn3"):
+        c = DecodeStateCache(4, 2, 2, 64, device="cpu", kind=kind)
+        a, b, d = c.alloc(3)
+        with pytest.raises(ValueError):
+            c.free([a, a])
+        assert len(c._free) == 1            # nothing freed by the failed call
+        with pytest.raises(ValueError):
+            c.free([a, 3 if 3 not in (a, b, d) else 0])
+        assert len(c._free) == 1
+        c.free([a, b])
+        assert len(c._free) == 3
+        with pytest.raises(ValueError):
+            c._slot_tensor([d, -1, d])
+        assert c._slot_tensor([d, -1, -1]).tolist() == [d, -1, -1]
+    with pytest.raises(ValueError):
+        DecodeStateCache(2, 2, 2, 64, device="cpu", kind="chan")
+    g = DecodeStateCache(3, 2, 2, 64, device="cpu", kind="gdn3", P=32)
+    s0, s1 = g.alloc(2)
+    g.pos[s0] = 5
+    with pytest.raises(ValueError):         # prefill of slots at different token counts
+        g.prefill([s0, s1], *([torch.zeros(2, 3, 2, 64)] * 3 + [torch.zeros(2, 3, 2, 2)] * 3))

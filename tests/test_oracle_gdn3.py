@@ -151,3 +151,30 @@ def test_bridge_gdn3_without_compaction_is_the_dense_rule():
                               factors=(4, 4, 4, 4))
     y2 = delta.gdn3_dense_layer(x["q"], x["k"], x["v"], beta, x["g"])
     torch.testing.assert_close(y1, y2, atol=1e-12, rtol=1e-10)
+
+
+@pytest.mark.parametrize("P,Kc,splits", [(16, 16, (7, 33)), (16, 48, (16, 50)), (32, 32, (31, 32, 65))])
+def test_carried_state_split_equals_whole_run(P, Kc, splits):
+    """The oracle's carried state (state0, t0) continues the whole-run loop
+    exactly: runs over [0, s1), [s1, s2), ... from each returned state equal
+    one run, through slot wrap-arounds and compactions (mid-window splits
+    included).  The whole run itself is pinned by the golden vectors above."""
+    g = torch.Generator().manual_seed(5)
+    B, T, H, M, D = 1, 80, 1, 2, 64
+    q, k = (torch.nn.functional.normalize(torch.randn(B, T, H, M, D, generator=g), dim=-1) for _ in range(2))
+    v = torch.randn(B, T, H, M, D, generator=g)
+    bg, wg = (torch.sigmoid(torch.randn(B, T, H, M, D, generator=g)) for _ in range(2))
+    dec = torch.rand(B, T, H, M, generator=g) * 0.1 + 0.9
+    kw = dict(R=4, P=P, factors=(8, 8, 8, 8), compact_every=Kc, return_state=True)
+    y, st, err = gdn3.gdn3_recurrence(q, k, v, bg, wg, dec, **kw)
+    bounds = (0,) + splits + (T,)
+    ys, s, e_tot = [], None, 0.0
+    for a, b in zip(bounds[:-1], bounds[1:]):
+        yy, s, e = gdn3.gdn3_recurrence(q[:, a:b], k[:, a:b], v[:, a:b], bg[:, a:b], wg[:, a:b], dec[:, a:b],
+                                      state0=s, t0=a, **kw)
+        ys.append(yy)
+        e_tot += e.item()
+    assert torch.allclose(torch.cat(ys, 1), y, rtol=0, atol=1e-12)
+    for x1, x2 in zip(s, st):
+        assert torch.allclose(x1, x2, rtol=0, atol=1e-12)
+    assert abs(e_tot - err.item()) <= 1e-9 * max(1.0, err.item())
