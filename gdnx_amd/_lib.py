@@ -43,6 +43,9 @@ SIGNATURES = {
     "gdnx_gdn3_num_compactions_from": (_c_int, [_c_int] * 4),
     "gdnx_gdn3_chunk_fwd_state": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 6 + [_c_int]
                                   + [_vp] * 7 + [_c_int] * 12 + [_c_float, _c_int, _vp]),
+    "gdnx_gdn3_noalloc_scratch_bytes": (_c_ll, []),
+    "gdnx_gdn3_chunk_fwd_state_noalloc": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 6
+                                          + [_c_int] + [_vp] * 6 + [_c_int] * 12 + [_c_float, _c_int, _vp]),
     "gdnx_gdn3_decode_step": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 10
                               + [_c_int] * 12 + [_c_float, _c_int, _vp]),
     "gdnx_delta_decode_step_chan": (_c_int, [_vp] * 9 + [_c_int] * 6 + [_vp]),

@@ -26,6 +26,8 @@
 //
 // One workgroup per chain carries the whole state in LDS; the chunk loop
 // is sequential because every compaction depends on the window it closes.
+#include <mutex>
+
 #include "gdn3_common.hpp"
 #include "gdnx_internal.hpp"
 
@@ -1248,6 +1250,43 @@ int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
 }
 
 }  // namespace
+
+// Static scratch for gdnx_gdn3_chunk_fwd_state_noalloc: the forward's
+// workspace (Kronecker matrices, factors, window state) for callers that
+// cannot allocate (graph capture, serving loops).  Each device the library
+// runs on holds its own copy for the life of the process; host code reaches
+// it only through the address hipGetSymbolAddress returns for that device.
+static __device__ __align__(256) unsigned char scratch[kG3ScratchBytes];
+
+namespace {
+std::mutex g_scratch_mu;
+constexpr int kMaxDevices = 64;
+void* g_scratch_ptr[kMaxDevices] = {};
+}  // namespace
+
+int gdn3_scratch(void** out) {
+  int dev = -1;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
+    return set_error(GDNX_ERR_HIP, "no current HIP device (or device index >= %d)", kMaxDevices);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !ptr)
+      return set_error(GDNX_ERR_HIP, "scratch address on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return GDNX_OK;
+}
+
+int gdn3_zero_fill(float* p, size_t n, hipStream_t stream) {
+  if (n == 0) return GDNX_OK;
+  const size_t nb = (n + 255) / 256;
+  hipLaunchKernelGGL(fill_zero_kernel, dim3((unsigned)(nb < 4096 ? nb : 4096)), dim3(256), 0, stream, p,
+                     (long long)n);
+  return check_launch("fill_zero_kernel");
+}
 
 size_t gdn3_workspace_bytes(int N, int D, int P, int dtype) {
   const size_t cb = dtype == GDNX_DTYPE_BF16 ? 2 : 4;

@@ -308,7 +308,7 @@ static int g3_fwd_args(G3FwdArgs& a, const void* q, const void* k, const void* v
                        const float* sketch, void* y, float* A_out, float* B_out, float* U_out, float* Vb_out,
                        double* comp_stats, void* workspace, int B, int T, int H, int M, int head_dim, int R,
                        int P, int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
-                       int dtype) {
+                       int dtype, bool need_workspace = true) {
   int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
   if (rc) return rc;
   G3Geom ge;
@@ -323,11 +323,11 @@ static int g3_fwd_args(G3FwdArgs& a, const void* q, const void* k, const void* v
     return set_error(GDNX_ERR_SHAPE, "qkv_lanes=%d must be 1 (shared) or M=%d", qkv_lanes, M);
   if (gate_channels != 1 && gate_channels != head_dim)
     return set_error(GDNX_ERR_SHAPE, "gate_channels=%d must be 1 or head_dim=%d", gate_channels, head_dim);
-  if (!b_gates || !w_gates || !decay || !sketch || !y || !workspace)
+  if (!b_gates || !w_gates || !decay || !sketch || !y || (need_workspace && !workspace))
     return set_error(GDNX_ERR_ARG, "gates, decay, sketch, y and workspace must be non-null");
   if (gate_channels > 1 && (!aligned16(b_gates) || !aligned16(w_gates)))
     return set_error(GDNX_ERR_ARG, "per-channel gates must be 16-byte aligned");
-  if (!aligned16(workspace)) return set_error(GDNX_ERR_ARG, "workspace must be 16-byte aligned");
+  if (need_workspace && !aligned16(workspace)) return set_error(GDNX_ERR_ARG, "workspace must be 16-byte aligned");
   if (!(slow_decay >= 0.f && slow_decay <= 1.f))
     return set_error(GDNX_ERR_ARG, "slow_decay must lie in [0, 1]");
   a = G3FwdArgs{};
@@ -382,8 +382,7 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
                          (size_t)N * head_dim * P};
     float* outs[4] = {A_out, B_out, U_out, Vb_out};
     for (int i = 0; i < 4; ++i)
-      if (outs[i] && hipMemsetAsync(outs[i], 0, n[i] * 4, (hipStream_t)stream) != hipSuccess)
-        return set_error(GDNX_ERR_HIP, "gdn3 forward: clearing the final state failed");
+      if (outs[i] && (rc = gdn3_zero_fill(outs[i], n[i], (hipStream_t)stream))) return rc;
     return GDNX_OK;
   }
   a.train_states = train_states;
@@ -396,6 +395,36 @@ extern "C" int gdnx_gdn3_num_compactions_from(int t0, int T, int P, int compact_
     return -1;
   return (t0 + T) / compact_every - t0 / compact_every;
 }
+
+namespace gdnx {
+// the carried-state forward once its arguments are checked: the initial
+// state's pass-through for T = 0, else the dispatch (workspace set by caller
+// unless T = 0)
+static int g3_state_check(const float* A0, const float* B0, const float* U0, const float* Vb0, int t0, int T) {
+  const int nin = (A0 != nullptr) + (B0 != nullptr) + (U0 != nullptr) + (Vb0 != nullptr);
+  if (nin != 0 && nin != 4) return set_error(GDNX_ERR_ARG, "A0, B0, U0, Vb0 must all be given or all be null");
+  if (t0 < 0 || (long long)t0 + T > 0x7fffffffLL) return set_error(GDNX_ERR_SHAPE, "bad start position t0=%d", t0);
+  return GDNX_OK;
+}
+
+static int g3_state_passthrough(const float* A0, const float* B0, const float* U0, const float* Vb0, float* A_out,
+                                float* B_out, float* U_out, float* Vb_out, int N, int R, int a_v, int a_k, int b_v,
+                                int b_k, int D, int P, hipStream_t stream) {
+  const size_t n[4] = {(size_t)N * R * a_v * a_k, (size_t)N * R * b_v * b_k, (size_t)N * D * P, (size_t)N * D * P};
+  const float* ins[4] = {A0, B0, U0, Vb0};
+  float* outs[4] = {A_out, B_out, U_out, Vb_out};
+  for (int i = 0; i < 4; ++i) {
+    if (!outs[i] || outs[i] == ins[i]) continue;
+    if (!ins[i]) {
+      const int rc = gdn3_zero_fill(outs[i], n[i], stream);
+      if (rc) return rc;
+    } else if (hipMemcpyAsync(outs[i], ins[i], n[i] * 4, hipMemcpyDeviceToDevice, stream) != hipSuccess) {
+      return set_error(GDNX_ERR_HIP, "gdn3 forward: passing the state through failed");
+    }
+  }
+  return GDNX_OK;
+}
+}  // namespace gdnx
 
 extern "C" int gdnx_gdn3_chunk_fwd_state(const void* q, const void* k, const void* v, int qkv_lanes,
                                          const float* b_gates, const float* w_gates, int gate_channels,
@@ -411,25 +440,47 @@ extern "C" int gdnx_gdn3_chunk_fwd_state(const void* q, const void* k, const voi
                        U_out, Vb_out, comp_stats, workspace, B, T, H, M, head_dim, R, P, compact_every, a_v, a_k,
                        b_v, b_k, slow_decay, dtype);
   if (rc) return rc;
-  const int nin = (A0 != nullptr) + (B0 != nullptr) + (U0 != nullptr) + (Vb0 != nullptr);
-  if (nin != 0 && nin != 4) return set_error(GDNX_ERR_ARG, "A0, B0, U0, Vb0 must all be given or all be null");
-  if (t0 < 0 || (long long)t0 + T > 0x7fffffffLL) return set_error(GDNX_ERR_SHAPE, "bad start position t0=%d", t0);
-  const int N = B * H * M;
-  const size_t n[4] = {(size_t)N * R * a_v * a_k, (size_t)N * R * b_v * b_k, (size_t)N * head_dim * P,
-                       (size_t)N * head_dim * P};
-  if (T == 0) {   // the state passes through unchanged
-    const float* ins[4] = {A0, B0, U0, Vb0};
-    float* outs[4] = {A_out, B_out, U_out, Vb_out};
-    for (int i = 0; i < 4; ++i) {
-      if (!outs[i]) continue;
-      const hipError_t e = ins[i] ? (outs[i] == ins[i] ? hipSuccess
-                                     : hipMemcpyAsync(outs[i], ins[i], n[i] * 4, hipMemcpyDeviceToDevice,
-                                                      (hipStream_t)stream))
-                                  : hipMemsetAsync(outs[i], 0, n[i] * 4, (hipStream_t)stream);
-      if (e != hipSuccess) return set_error(GDNX_ERR_HIP, "gdn3 forward: passing the state through failed");
-    }
-    return GDNX_OK;
-  }
+  if ((rc = g3_state_check(A0, B0, U0, Vb0, t0, T))) return rc;
+  if (T == 0)
+    return g3_state_passthrough(A0, B0, U0, Vb0, A_out, B_out, U_out, Vb_out, B * H * M, R, a_v, a_k, b_v, b_k,
+                                head_dim, P, (hipStream_t)stream);
+  a.t0 = t0;
+  a.A0 = A0;
+  a.B0 = B0;
+  a.U0 = U0;
+  a.Vb0 = Vb0;
+  return gdn3_fwd_dispatch(a, (hipStream_t)stream);
+}
+
+extern "C" long long gdnx_gdn3_noalloc_scratch_bytes(void) { return (long long)kG3ScratchBytes; }
+
+extern "C" int gdnx_gdn3_chunk_fwd_state_noalloc(const void* q, const void* k, const void* v, int qkv_lanes,
+                                                 const float* b_gates, const float* w_gates, int gate_channels,
+                                                 const float* decay, const float* sketch, const float* A0,
+                                                 const float* B0, const float* U0, const float* Vb0, int t0,
+                                                 void* y, float* A_out, float* B_out, float* U_out, float* Vb_out,
+                                                 double* comp_stats, int B, int T, int H, int M, int head_dim,
+                                                 int R, int P, int compact_every, int a_v, int a_k, int b_v,
+                                                 int b_k, float slow_decay, int dtype, void* stream) {
+  g_err[0] = 0;
+  G3FwdArgs a;
+  int rc = g3_fwd_args(a, q, k, v, qkv_lanes, b_gates, w_gates, gate_channels, decay, sketch, y, A_out, B_out,
+                       U_out, Vb_out, comp_stats, nullptr, B, T, H, M, head_dim, R, P, compact_every, a_v, a_k,
+                       b_v, b_k, slow_decay, dtype, /*need_workspace=*/false);
+  if (rc) return rc;
+  if ((rc = g3_state_check(A0, B0, U0, Vb0, t0, T))) return rc;
+  const size_t need = gdn3_workspace_bytes(B * H * M, head_dim, P, dtype);
+  if (need > kG3ScratchBytes)
+    return set_error(GDNX_ERR_WORKSPACE,
+                     "gdn3 no-alloc forward: %d chains need %zu bytes of scratch; the library's static scratch "
+                     "holds %zu (use gdnx_gdn3_chunk_fwd_state with a workspace, or fewer chains per call)",
+                     B * H * M, need, kG3ScratchBytes);
+  if (T == 0)
+    return g3_state_passthrough(A0, B0, U0, Vb0, A_out, B_out, U_out, Vb_out, B * H * M, R, a_v, a_k, b_v, b_k,
+                                head_dim, P, (hipStream_t)stream);
+  void* ws = nullptr;
+  if ((rc = gdn3_scratch(&ws))) return rc;
+  a.workspace = ws;
   a.t0 = t0;
   a.A0 = A0;
   a.B0 = B0;

@@ -290,6 +290,12 @@ struct G3EpiArgs {
 };
 
 int gdn3_fwd_dispatch(const G3FwdArgs& a, hipStream_t stream);
+// bytes of the static scratch of gdnx_gdn3_chunk_fwd_state_noalloc (per device)
+constexpr size_t kG3ScratchBytes = (size_t)64 << 20;
+// that scratch's address on the current device (resolved once per device)
+int gdn3_scratch(void** out);
+// p[0, n) = 0 on the stream (a fill kernel: safe inside graph capture)
+int gdn3_zero_fill(float* p, size_t n, hipStream_t stream);
 size_t gdn3_workspace_bytes(int N, int D, int P, int dtype);
 size_t gdn3_train_states_bytes(int N, int T, int D, int P, int Kc);
 int gdn3_bwd_dispatch(const G3BwdArgs& a, hipStream_t stream);

@@ -301,6 +301,27 @@ int gdnx_gdn3_chunk_fwd_state(const void* q, const void* k, const void* v, int q
                               int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
                               int dtype, void* stream);
 
+/* gdnx_gdn3_chunk_fwd_state without a workspace argument: it allocates
+ * nothing and takes no caller memory beyond inputs and outputs.  No
+ * counterpart in the reference; for callers that cannot allocate (code under
+ * HIP graph capture, serving loops, harnesses that forbid hipMalloc).  The
+ * workspace lives in a static device array of
+ * gdnx_gdn3_noalloc_scratch_bytes() bytes (64 MiB) that each GPU the library
+ * runs on holds until the process ends; calls needing more
+ * (gdnx_gdn3_workspace_bytes > that: about 1,250 chains in bf16, 780 in
+ * float32 at head_dim 128) return GDNX_ERR_WORKSPACE before any launch.  All
+ * calls on one GPU share its array: calls that overlap on one GPU (other
+ * streams or threads) race.  Results equal gdnx_gdn3_chunk_fwd_state's. */
+long long gdnx_gdn3_noalloc_scratch_bytes(void);
+int gdnx_gdn3_chunk_fwd_state_noalloc(const void* q, const void* k, const void* v, int qkv_lanes,
+                                      const float* b_gates, const float* w_gates, int gate_channels,
+                                      const float* decay, const float* sketch, const float* A0,
+                                      const float* B0, const float* U0, const float* Vb0, int t0, void* y,
+                                      float* A_out, float* B_out, float* U_out, float* Vb_out,
+                                      double* comp_stats, int B, int T, int H, int M, int head_dim, int R,
+                                      int P, int compact_every, int a_v, int a_k, int b_v, int b_k,
+                                      float slow_decay, int dtype, void* stream);
+
 /* One-token GDN3 decode step on a carried Kronecker-residual state, updated
  * in place.  One iteration of the frozen oracle's token loop
  * (gdn3/_reference_recurrence.py:60-90; the reference itself has no decode

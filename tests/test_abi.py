@@ -216,3 +216,17 @@ def test_decode_cache_host_slot_logic():
     g.pos[s0] = 5
     with pytest.raises(ValueError):         # prefill of slots at different token counts
         g.prefill([s0, s1], *([torch.zeros(2, 3, 2, 64)] * 3 + [torch.zeros(2, 3, 2, 2)] * 3))
+
+
+def test_noalloc_forward_refuses_before_any_launch():
+    """The allocation-free GDN3 forward checks its static scratch's size
+    before touching a device: too many chains is GDNX_ERR_WORKSPACE here too."""
+    lib = _lib.load()
+    assert lib.gdnx_gdn3_noalloc_scratch_bytes() == 64 << 20
+    vp = ctypes.c_void_p
+    rc = lib.gdnx_gdn3_chunk_fwd_state_noalloc(vp(256), vp(256), vp(256), 1, vp(256), vp(256), 1, vp(256), vp(256),
+                                               None, None, None, None, 0, vp(256), None, None, None, None, None,
+                                               64, 32, 16, 4, 128, 4, 16, 16, 16, 16, 8, 8, 0.97,
+                                               _lib.DTYPE_BF16, None)
+    assert rc == -3
+    assert "scratch" in lib.gdnx_last_error().decode()
