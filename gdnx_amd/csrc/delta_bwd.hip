@@ -35,15 +35,26 @@ namespace gdnx {
 // ---------------------------------------------------------------------------
 // per-chunk gradients, lanes summed in-block
 // ---------------------------------------------------------------------------
-#ifndef GDNX_GRADS_WAVES_PER_EU
-#define GDNX_GRADS_WAVES_PER_EU 2
-#endif
-// One wave per 16-column tile of the key dimension (D/16 waves): each wave
-// keeps only its own rows of S0 / dS_C and its dq/dk/dv tiles in registers.
-template <typename CT, int D>
+// Wave w owns one 16-column tile of the key dimension (and the same tile of
+// the value dimension): its rows of S0 / dS_C, its dq/dk/dv tiles and its
+// share of the P products stay in registers.
+//   C <= 32: one workgroup of D/16 waves per (b, h, chunk), two waves per SIMD.
+//   C = 64: the per-wave arrays double (the chunk's 64 rows) and need ~370
+//   registers, so a workgroup has four waves, one per SIMD with the whole
+//   512-entry register file, and covers 64 key columns: KH = D/64 workgroups
+//   per (b, h, chunk) split the key (and value) columns.  Each reads only its
+//   rows of the states (the dominant traffic) and computes the lane-shared
+//   C x C gram gradients itself; the per-token scalar gradients are linear in
+//   the key-split row sums, so each workgroup writes a partial and a second
+//   kernel adds them (the pair runs side by side on one XCD, so the chunk
+//   tiles both read come from L2 the second time).
+template <typename CT, int D, int C>
 struct GradDims {
-  static constexpr int NW = D / 16;
+  static constexpr int KT = 1;                          // key tiles per wave
+  static constexpr int NW = C >= 64 ? 4 : D / 16;       // waves per workgroup
+  static constexpr int KH = D / (16 * NW);              // workgroups per (b, h, chunk)
   static constexpr int NT = 64 * NW;
+  static constexpr int WPE = C >= 64 ? 1 : 2;           // waves per SIMD the kernel is compiled for
 };
 
 // Small per-lane arrays, double-buffered by lane parity: the per-token
@@ -63,15 +74,13 @@ struct alignas(16) GradLaneBuf {
 template <typename CT, int D, int C>
 struct alignas(16) BwdGradSmem {
   typedef Dims<CT, D, C> Dm;
-  static constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF, NW = GradDims<CT, D>::NW;
+  static constexpr int LDD = Dm::LDD, LDC = Dm::LDC, NW = GradDims<CT, D, C>::NW;
   static constexpr int NP = (C / 16) * (C / 16 + 1) / 2;  // lower 16x16 tile pairs
   CT q[C * LDD];
   CT k[C * LDD];
   CT v[C * LDD];
-  float KK[C * LDF];   // k_i . k_j  (lower)
-  float QK[C * LDF];   // q_i . k_j  (lower incl. diagonal)
-  float dQK[C * LDF];  // sum over lanes of dL/d(q_i.k_j)
-  float dKK[C * LDF];  // sum over lanes of dL/d(k_i.k_j), j < i
+  // (the grams q_i.k_j, k_i.k_j and their lane-summed gradients live in the
+  // registers of the wave that owns each 16x16 tile)
   union alignas(16) U {
     struct alignas(16) {  // one lane's chunk tiles, rows [token][v]
       CT dy[C * LDD], R[C * LDD], dB[C * LDD];
@@ -90,17 +99,20 @@ __device__ __forceinline__ int opaque(int x) {
 }
 
 // One lane's inputs to the gradient kernel, fetched a lane ahead: this
-// wave's rows of S0 and dS_C (raw tiles, one per 16 value columns), this
-// thread's share of the R / dB tiles and of dY, and (scalar wave) the
-// per-token coefficients.
+// wave's rows of S0 and dS_C (raw tiles, one per 16 value columns, for each
+// of its key tiles), this thread's share of the R / dB tiles and of dY (all
+// value columns: the workgroup's NW waves take value tiles wave + NW j), and
+// (scalar wave) the per-token coefficients.
 template <typename CT, int D, int C>
 struct GradPrefetch {
   typedef typename Vec4T<CT>::type V4;
-  static constexpr int NDT = D / 16, NCT = C / 16, NT = GradDims<CT, D>::NT;
+  static constexpr int KT = GradDims<CT, D, C>::KT;
+  static constexpr int NVL = D / 16 / GradDims<CT, D, C>::NW;   // value tiles loaded per wave
+  static constexpr int NDT = D / 16, NCT = C / 16, NT = GradDims<CT, D, C>::NT;
   static constexpr int VEC = 16 / sizeof(CT);
   static constexpr int NDY = (C * D / VEC + NT - 1) / NT;
-  V4 s[NDT], ds[NDT];
-  V4 r[NCT], db[NCT];
+  V4 s[KT][NDT], ds[KT][NDT];
+  V4 r[NVL][NCT], db[NVL][NCT];
   uint4 dy[NDY];
   ScalarRegs sc;
 };
@@ -108,7 +120,7 @@ struct GradPrefetch {
 // Gradient kernel: one workgroup per (batch, head, chunk), looping over the M
 // lanes that share q/k/v.  Per lane it reads the stashed S0, R (forward) and
 // dS_C, dB (reverse scan) and forms, wave w owning key columns d and value
-// columns v in [16w, 16w+16):
+// columns v in its KT tiles:
 //   P1 = dY S0^T, P2 = dB S0^T, P3 = R dS_C^T      (S0 / dS_C rows of this wave
 //                                                   as fragments over k = v)
 //   dQ += diag(exp G) P1,  dK += diag(dec) P3 - diag(a_e exp G) P2
@@ -117,29 +129,37 @@ struct GradPrefetch {
 //   per-token decay / erase gradients.
 // After the lanes: dQ += dQK K, dK += dQK^T Q + (dKK + dKK^T) K.
 template <typename CT, int D, int C>
-__global__ void __launch_bounds__((GradDims<CT, D>::NT)) __attribute__((amdgpu_waves_per_eu(GDNX_GRADS_WAVES_PER_EU)))
+__global__ void __launch_bounds__((GradDims<CT, D, C>::NT))
+__attribute__((amdgpu_waves_per_eu(GradDims<CT, D, C>::WPE, GradDims<CT, D, C>::WPE)))
 delta_bwd_grads_kernel(DeltaBwdArgs p) {
   typedef Dims<CT, D, C> Dm;
   typedef typename Dm::Frag Frag;
   typedef BwdGradSmem<CT, D, C> Sm;
   typedef GradPrefetch<CT, D, C> Pf;
-  typedef GradLaneBuf<C, GradDims<CT, D>::NW, Sm::NP> LB;
+  typedef GradLaneBuf<C, GradDims<CT, D, C>::NW, Sm::NP> LB;
   typedef typename Vec4T<CT>::type V4;
   constexpr int KS = Dm::KS, TPS = Dm::TPS, NCT = Dm::NCT, NDT = Dm::NDT, LDD = Dm::LDD, LDC = Dm::LDC;
-  constexpr int LDF = Dm::LDF, NW = GradDims<CT, D>::NW, NT = GradDims<CT, D>::NT, NKV = D / KS, NP = Sm::NP;
+  constexpr int NW = GradDims<CT, D, C>::NW, NT = GradDims<CT, D, C>::NT, KT = GradDims<CT, D, C>::KT;
+  constexpr int NKV = D / KS, NP = Sm::NP;
   constexpr int SW = NW - 1;  // the wave that forms the per-token scalar gradients
   __shared__ Sm sm;
 
   const int tid0 = threadIdx.x;
   const int tid = tid0;
   const int wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
-  const int dcol = wave * 16 + n16;  // this lane's key (and value) column
+  constexpr int KH = GradDims<CT, D, C>::KH;
   const int NC = (p.T + C - 1) / C;
-  const int nblocks = p.B * p.H * NC;
-  const int blk = xcd_remap(blockIdx.x, nblocks);
-  const int c = blk % NC;
-  const int h = (blk / NC) % p.H;
-  const int b = blk / (NC * p.H);
+  const int nblocks = p.B * p.H * NC * KH;
+  const int work = xcd_remap(blockIdx.x, nblocks);
+  // key halves fastest (the pair lands on one XCD), then chunks in ascending
+  // order over all heads: the records the reverse scan wrote last (low
+  // chunks) are read first, some still from the memory-side cache (measured
+  // 4 % faster than head-major order)
+  const int kh = work % KH, blk = work / KH;
+  const int c = blk / (p.B * p.H);
+  const int h = (blk % (p.B * p.H)) % p.H;
+  const int b = (blk % (p.B * p.H)) / p.H;
+  const int tile0 = (kh * NW + wave) * KT;   // this wave's first key (and value) tile
   const int t0 = c * C;
   const size_t rs = (size_t)p.H * D;
   const size_t qoff = ((size_t)b * p.T * p.H + h) * D;
@@ -162,11 +182,13 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
     const int lane_ = tid_ & 63;
     const size_t rec = rec_of(mm);
 #pragma unroll
-    for (int it = 0; it < NCT; ++it) {  // tile (it, V = wave) of R and dB
-      const size_t off = rec * C * D + stash_tile_offset<CT, D>(it, wave, lane_);
-      f.r[it] = *(const V4*)(r_st + off);
-      f.db[it] = *(const V4*)(db_st + off);
-    }
+    for (int j = 0; j < Pf::NVL; ++j)
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) {  // tile (it, V = wave + NW j) of R and dB
+        const size_t off = rec * C * D + stash_tile_offset<CT, D>(it, wave + NW * j, lane_);
+        f.r[j][it] = *(const V4*)(r_st + off);
+        f.db[j][it] = *(const V4*)(db_st + off);
+      }
     const CT* yb = (const CT*)p.dy + (((size_t)b * p.T * p.H + h) * p.M + mm) * D + (size_t)t0 * rsy;
     const __amdgpu_buffer_rsrc_t yr = buf_rsrc(yb, (unsigned)min(C, p.T - t0) * ysb);
 #pragma unroll
@@ -179,8 +201,11 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
   };
   auto prefetch_state = [&](Pf& f, int mm, int V, int tid_) {
     const size_t rec = rec_of(mm);
-    f.s[V] = *(const V4*)stash_state_ptr<CT, D, C>(s_st + rec * D * D, wave, V, tid_ & 63);
-    f.ds[V] = *(const V4*)stash_state_ptr<CT, D, C>(ds_st + rec * D * D, wave, V, tid_ & 63);
+#pragma unroll
+    for (int kt = 0; kt < KT; ++kt) {
+      f.s[kt][V] = *(const V4*)stash_state_ptr<CT, D, C>(s_st + rec * D * D, tile0 + kt, V, tid_ & 63);
+      f.ds[kt][V] = *(const V4*)stash_state_ptr<CT, D, C>(ds_st + rec * D * D, tile0 + kt, V, tid_ & 63);
+    }
   };
 
   // ---- per-token scalar gradients of lane mm (wave SW, one token per lane) ----
@@ -190,29 +215,33 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
       const int i = lane, ib = i >> 4, ir = i & 15;
       float rs[4];
 #pragma unroll
-      for (int a = 0; a < 4; ++a) {   // this row's NW partials, read as 16-byte vectors
+      for (int a = 0; a < 4; ++a) {   // this row's NW partials (16-byte vectors when NW % 4 == 0)
         rs[a] = 0.f;
+        if constexpr (NW % 4 == 0) {
 #pragma unroll
-        for (int w = 0; w < NW; w += 4) {
-          const f32x4 x = *(const f32x4*)&q.red[i][a * NW + w];
-          rs[a] += (x[0] + x[1]) + (x[2] + x[3]);
+          for (int w = 0; w < NW; w += 4) {
+            const f32x4 x = *(const f32x4*)&q.red[i][a * NW + w];
+            rs[a] += (x[0] + x[1]) + (x[2] + x[3]);
+          }
+        } else {
+#pragma unroll
+          for (int w = 0; w < NW; ++w) rs[a] += q.red[i][a * NW + w];
         }
       }
       dawi = rs[3];
       dGi = q.gam[i] * rs[0] - q.gam[i] * q.ae[i] * rs[1] - q.dec[i] * rs[2];
       daei = -q.gam[i] * rs[1];
-      // Xm row i lives in tiles (ib, jt <= ib); column i in tiles (it >= ib, ib);
-      // compile-time tile loops, predicated on the lane's row block
-#pragma unroll
-      for (int bi = 0; bi < NCT; ++bi) {
-#pragma unroll
-        for (int bj = 0; bj <= bi; ++bj) {
-          const int pr = bi * (bi + 1) / 2 + bj;
-          if (bi == ib) {
-            dGi += q.tri[pr][0][ir] + q.tri[pr][3][ir];
-            daei += q.tri[pr][2][ir];
-          }
-          if (bj == ib) dGi -= q.tri[pr][1][ir] + q.tri[pr][4][ir];
+      // Xm row i lives in tiles (ib, jt <= ib); column i in tiles (it >= ib, ib)
+      // (every key part has them: the first one adds them)
+      if (kh == 0) {
+        for (int bj = 0; bj <= ib; ++bj) {
+          const int pr = ib * (ib + 1) / 2 + bj;
+          dGi += q.tri[pr][0][ir] + q.tri[pr][3][ir];
+          daei += q.tri[pr][2][ir];
+        }
+        for (int bi = ib; bi < NCT; ++bi) {
+          const int pr = bi * (bi + 1) / 2 + ib;
+          dGi -= q.tri[pr][1][ir] + q.tri[pr][4][ir];
         }
       }
       r3d = q.dec[i] * rs[2];
@@ -231,9 +260,18 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
     if (lane < C && t < p.T) {
       const size_t si = ((size_t)(b * p.T + t) * p.H + h) * p.M + mm;
       const float raw = q.graw[lane];
-      p.dae[si] = daei;
-      p.daw[si] = dawi;
-      p.dg[si] = (raw <= 0.f && raw >= kLogFloor) ? sfx : 0.f;
+      const float dgv = (raw <= 0.f && raw >= kLogFloor) ? sfx : 0.f;
+      if constexpr (KH == 1) {
+        p.dae[si] = daei;
+        p.daw[si] = dawi;
+        p.dg[si] = dgv;
+      } else {   // this key part's share, [KH][3][rows] after dS and dB in the workspace
+        const size_t rows = (size_t)p.B * p.T * p.H * p.M;
+        float* part = (float*)(db_st + nrec * C * D) + (size_t)kh * 3 * rows;
+        part[si] = daei;
+        part[rows + si] = dawi;
+        part[2 * rows + si] = dgv;
+      }
     }
   };
 
@@ -253,23 +291,28 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
     sk.template commit_nat<LDD>(sm.k, tid);
     sv.template commit_nat<LDD>(sm.v, tid);
   }
-  for (int i = tid; i < C * LDF; i += NT) {
-    sm.dQK[i] = 0.f;
-    sm.dKK[i] = 0.f;
-  }
-  f32x4 dQacc[NCT], dKacc[NCT], dVacc[NCT];
+  f32x4 dQacc[KT][NCT], dKacc[KT][NCT], dVacc[KT][NCT];
 #pragma unroll
-  for (int it = 0; it < NCT; ++it) dQacc[it] = dKacc[it] = dVacc[it] = zero4();
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int it = 0; it < NCT; ++it) dQacc[kt][it] = dKacc[kt][it] = dVacc[kt][it] = zero4();
   __syncthreads();
-  // raw grams (shared by the lanes)
-  for (int task = wave; task < 2 * NP; task += NW) {
-    int it, jt;
-    tri_pair(task >> 1, it, jt);
-    const CT* arow = ((task & 1) == 0) ? &sm.k[(it * 16 + n16) * LDD] : &sm.q[(it * 16 + n16) * LDD];
-    const f32x4 acc = tile_nt<CT, D>(arow, &sm.k[(jt * 16 + n16) * LDD], g4);
-    float* dst = ((task & 1) == 0) ? sm.KK : sm.QK;
+  // raw grams (shared by the lanes) in the registers of the wave that owns the
+  // tile: task pidx < NP is tile pair pidx of Q K^T (with the gradient dQK),
+  // NP + pidx the same pair of K K^T (with dKK); wave w owns tasks w + NW j
+  constexpr int NTASK = (2 * NP + NW - 1) / NW;
+  f32x4 gram[NTASK], dgram[NTASK];
 #pragma unroll
-    for (int ii = 0; ii < 4; ++ii) dst[(it * 16 + 4 * g4 + ii) * LDF + jt * 16 + n16] = acc[ii];
+  for (int j = 0; j < NTASK; ++j) {
+    const int task = wave + NW * j;
+    gram[j] = dgram[j] = zero4();
+    if (task < 2 * NP) {
+      const bool isL = task >= NP;
+      int it, jt;
+      tri_pair(isL ? task - NP : task, it, jt);
+      const CT* arow = isL ? &sm.k[(it * 16 + n16) * LDD] : &sm.q[(it * 16 + n16) * LDD];
+      gram[j] = tile_nt<CT, D>(arow, &sm.k[(jt * 16 + n16) * LDD], g4);
+    }
   }
 
   for (int m = 0; m < p.M; ++m) {
@@ -277,9 +320,11 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
     // (and spilling) every loop-invariant per-thread address out of the loop
     const int tid = opaque(tid0);
     const int lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
-    const int dcol = wave * 16 + n16;
     LB& lb = sm.lb[m & 1];
     __syncthreads();  // lane m-1 done with the lane tiles; lane m-2's scalar pass done with lb
+    if constexpr (C >= 64) {
+      if (m > 0) prefetch_tiles(pf, m, tid);   // (C = 64: no registers to hold them a lane ahead)
+    }
     // ---- commit lane m's prefetched inputs ----
 #pragma unroll
     for (int j = 0; j < Pf::NDY; ++j) {
@@ -291,24 +336,30 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
       }
     }
 #pragma unroll
-    for (int it = 0; it < NCT; ++it)
+    for (int j = 0; j < Pf::NVL; ++j)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        sm.u.ln.R[(it * 16 + 4 * g4 + i) * LDD + dcol] = pf.r[it][i];
-        sm.u.ln.dB[(it * 16 + 4 * g4 + i) * LDD + dcol] = pf.db[it][i];
-      }
+      for (int it = 0; it < NCT; ++it)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int col = (wave + NW * j) * 16 + n16;
+          sm.u.ln.R[(it * 16 + 4 * g4 + i) * LDD + col] = pf.r[j][it][i];
+          sm.u.ln.dB[(it * 16 + 4 * g4 + i) * LDD + col] = pf.db[j][it][i];
+        }
     if (wave == SW) {
       const ChunkScalars cs{lb.G, lb.gam, lb.dec, lb.ae, lb.aw, lb.graw};
       scal_commit<C>(cs, pf.sc, lane);
     }
     const int mn = min(m + 1, p.M - 1);   // (the last lane refetches itself, unused)
-    prefetch_tiles(pf, mn, tid);          // the tile registers are free again: fetch the next lane's
+    if constexpr (C < 64) prefetch_tiles(pf, mn, tid);   // the tile registers are free again: the next lane's
     __syncthreads();
     if (m > 0 && wave == SW) scalar_grads(m - 1, sm.lb[(m - 1) & 1]);
 
     // ---- dAq = dY R^T (j <= i) and dL = -dB R^T (j < i), lower tiles: task
     // pidx < NP is tile pair pidx of dAq, NP + pidx the same pair of dL ----
-    for (int task = wave; task < 2 * NP; task += NW) {
+#pragma unroll
+    for (int jj = 0; jj < NTASK; ++jj) {
+      const int task = wave + NW * jj;
+      if (task >= 2 * NP) continue;
       const bool isL = task >= NP;
       const int pidx = isL ? task - NP : task;
       int it, jt;
@@ -326,13 +377,13 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
         const float Dij = __expf(lb.G[i] - Gj);
         if (!isL && j <= i) {
           const float dqk = acc[ii] * Dij;
-          sm.dQK[i * LDF + j] += dqk;
-          xm[ii] = dqk * sm.QK[i * LDF + j];
+          dgram[jj][ii] += dqk;
+          xm[ii] = dqk * gram[jj][ii];
         } else if (isL && j < i) {
           const float dl = -acc[ii];
-          const float kk = sm.KK[i * LDF + j];
+          const float kk = gram[jj][ii];
           const float dkk = dl * Dij * lb.ae[i];
-          sm.dKK[i * LDF + j] += dkk;
+          dgram[jj][ii] += dkk;
           xm[ii] = dkk * kk;
           xa[ii] = dl * Dij * kk;
         }
@@ -356,87 +407,115 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
       cx += __shfl_xor(cx, 16, 64);
       cx += __shfl_xor(cx, 32, 64);
       if (g4 == 0) lb.tri[pidx][slot + 1][n16] = cx;
+      __builtin_amdgcn_sched_barrier(0);   // one task's fragments in flight at a time
     }
 
-    // ---- P1 = dY S0^T, P2 = dB S0^T, P3 = R dS^T on this wave's d tile, k-step
-    // outer: this wave's rows of S0 / dS_C (fetched during the previous lane)
-    // become fragments over k = v one k-step at a time, and their registers
-    // are refilled with the next lane's rows right away, so those loads stream
-    // through the products; then dV, da_w and the row sums ----
-    f32x4 P1[NCT], P2[NCT], P3[NCT];
-#pragma unroll
-    for (int it = 0; it < NCT; ++it) P1[it] = P2[it] = P3[it] = zero4();
+    // ---- P1 = dY S0^T, P2 = dB S0^T, P3 = R dS^T on this wave's key tiles:
+    // this wave's rows of S0 / dS_C (fetched during the previous lane) become
+    // fragments over k = v once, and their registers are refilled with the
+    // next lane's rows right away, so those loads stream through the
+    // products; then per row tile (one tile's P products live at a time) the
+    // products, dV, da_w and the row sums ----
+    Frag Sf[KT][NKV], dSf[KT][NKV];
     float sdot = 0.f;   // <dS_C, S0> over this wave's rows
 #pragma unroll
     for (int kb = 0; kb < NKV; ++kb) {
-      f32x4 ys[TPS], yd[TPS];
 #pragma unroll
-      for (int hh = 0; hh < TPS; ++hh) {
-        ys[hh] = tile_transpose_raw(pf.s[kb * TPS + hh], lane);
-        yd[hh] = tile_transpose_raw(pf.ds[kb * TPS + hh], lane);
+      for (int kt = 0; kt < KT; ++kt) {
+        f32x4 ys[TPS], yd[TPS];
+#pragma unroll
+        for (int hh = 0; hh < TPS; ++hh) {
+          ys[hh] = tile_transpose_raw(pf.s[kt][kb * TPS + hh], lane);
+          yd[hh] = tile_transpose_raw(pf.ds[kt][kb * TPS + hh], lane);
+        }
+        Sf[kt][kb] = acc_frag((CT*)nullptr, ys[0], ys[TPS - 1]);
+        dSf[kt][kb] = acc_frag((CT*)nullptr, yd[0], yd[TPS - 1]);
+#pragma unroll
+        for (int e = 0; e < FragLen<CT>::value; ++e) sdot += to_f(Sf[kt][kb][e]) * to_f(dSf[kt][kb][e]);
       }
-      const Frag Sf = acc_frag((CT*)nullptr, ys[0], ys[TPS - 1]);
-      const Frag dSf = acc_frag((CT*)nullptr, yd[0], yd[TPS - 1]);
-#pragma unroll
-      for (int e = 0; e < FragLen<CT>::value; ++e) sdot += to_f(Sf[e]) * to_f(dSf[e]);
-#pragma unroll
-      for (int hh = 0; hh < TPS; ++hh) prefetch_state(pf, mn, kb * TPS + hh, tid);
-#pragma unroll
-      for (int it = 0; it < NCT; ++it) {
-        mma(P1[it], ld_frag(&sm.u.ln.dy[(it * 16 + n16) * LDD + kb * KS], g4), Sf);
-        mma(P2[it], ld_frag(&sm.u.ln.dB[(it * 16 + n16) * LDD + kb * KS], g4), Sf);
-        mma(P3[it], ld_frag(&sm.u.ln.R[(it * 16 + n16) * LDD + kb * KS], g4), dSf);
-      }
-      __builtin_amdgcn_sched_barrier(0);
     }
-    // per row tile: this lane's column of q, k, v, dB read first, then 16
-    // independent DPP row-sum chains, then one masked block of stores
 #pragma unroll
     for (int it = 0; it < NCT; ++it) {
-      float xq[4], xk[4], xv[4], xb[4];
+      f32x4 P1[KT], P2[KT], P3[KT];
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        const int i = it * 16 + 4 * g4 + ii;
-        xb[ii] = to_f(sm.u.ln.dB[i * LDD + dcol]);
-        xk[ii] = to_f(sm.k[i * LDD + dcol]);
-        xq[ii] = to_f(sm.q[i * LDD + dcol]);
-        xv[ii] = to_f(sm.v[i * LDD + dcol]);
+      for (int kt = 0; kt < KT; ++kt) P1[kt] = P2[kt] = P3[kt] = zero4();
+#pragma unroll
+      for (int kb = 0; kb < NKV; ++kb) {
+        const Frag fy = ld_frag(&sm.u.ln.dy[(it * 16 + n16) * LDD + kb * KS], g4);
+        const Frag fb = ld_frag(&sm.u.ln.dB[(it * 16 + n16) * LDD + kb * KS], g4);
+        const Frag fr = ld_frag(&sm.u.ln.R[(it * 16 + n16) * LDD + kb * KS], g4);
+#pragma unroll
+        for (int kt = 0; kt < KT; ++kt) {
+          mma(P1[kt], fy, Sf[kt][kb]);
+          mma(P2[kt], fb, Sf[kt][kb]);
+          mma(P3[kt], fr, dSf[kt][kb]);
+        }
+        __builtin_amdgcn_sched_barrier(0);   // keep the fragment loads of one k-step at a time in flight
       }
+      // this lane's columns of q, k, v, dB, then 16 independent DPP row-sum
+      // chains (summed over the wave's key tiles), then one masked block of stores
       const f32x4 gi = *(const f32x4*)&lb.gam[it * 16 + 4 * g4];
       const f32x4 ei = *(const f32x4*)&lb.ae[it * 16 + 4 * g4];
       const f32x4 di = *(const f32x4*)&lb.dec[it * 16 + 4 * g4];
       const f32x4 wi = *(const f32x4*)&lb.aw[it * 16 + 4 * g4];
-      dQacc[it] += gi * P1[it];
-      dKacc[it] += di * P3[it] - ei * gi * P2[it];
-      float rsum[4][4];   // [ii][q.P1, k.P2, k.P3, v.dB]
+      float part[4][4];   // [ii][q.P1, k.P2, k.P3, v.dB] over this wave's columns
 #pragma unroll
-      for (int ii = 0; ii < 4; ++ii) {
-        dVacc[it][ii] += wi[ii] * xb[ii];
-        rsum[ii][0] = row_prefix16(P1[it][ii] * xq[ii]);
-        rsum[ii][1] = row_prefix16(P2[it][ii] * xk[ii]);
-        rsum[ii][2] = row_prefix16(P3[it][ii] * xk[ii]);
-        rsum[ii][3] = row_prefix16(xb[ii] * xv[ii]);
+      for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) part[ii][q4] = 0.f;
+#pragma unroll
+      for (int kt = 0; kt < KT; ++kt) {
+        const int dcol = (tile0 + kt) * 16 + n16;
+        float xq[4], xk[4], xb[4], xv[4];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          const int i = it * 16 + 4 * g4 + ii;
+          xb[ii] = to_f(sm.u.ln.dB[i * LDD + dcol]);
+          xk[ii] = to_f(sm.k[i * LDD + dcol]);
+          xq[ii] = to_f(sm.q[i * LDD + dcol]);
+          xv[ii] = to_f(sm.v[i * LDD + dcol]);
+        }
+        dQacc[kt][it] += gi * P1[kt];
+        dKacc[kt][it] += di * P3[kt] - ei * gi * P2[kt];
+#pragma unroll
+        for (int ii = 0; ii < 4; ++ii) {
+          dVacc[kt][it][ii] += wi[ii] * xb[ii];
+          part[ii][0] += P1[kt][ii] * xq[ii];
+          part[ii][1] += P2[kt][ii] * xk[ii];
+          part[ii][2] += P3[kt][ii] * xk[ii];
+          part[ii][3] += xb[ii] * xv[ii];
+        }
       }
+      float rsum[4][4];
+#pragma unroll
+      for (int ii = 0; ii < 4; ++ii)
+#pragma unroll
+        for (int q4 = 0; q4 < 4; ++q4) rsum[ii][q4] = row_prefix16(part[ii][q4]);
       if (n16 == 15) {
 #pragma unroll
         for (int ii = 0; ii < 4; ++ii)
 #pragma unroll
           for (int q4 = 0; q4 < 4; ++q4) lb.red[it * 16 + 4 * g4 + ii][q4 * NW + wave] = rsum[ii][q4];
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
+    // the next lane's state rows: in flight through this lane's reductions and
+    // the next lane's commit and C x C tiles
+#pragma unroll
+    for (int V = 0; V < NDT; ++V) prefetch_state(pf, mn, V, tid);
     sdot = wave_sum(sdot);
     if (lane == 0) lb.scal[wave] = sdot;
   }
   __syncthreads();  // lane tiles dead: the union becomes Q^T, K^T and the gram-gradient factors
   if (wave == SW) scalar_grads(p.M - 1, sm.lb[(p.M - 1) & 1]);
 
-  // ---- gram gradient products, shared over lanes ----
-  for (int idx = tid; idx < C * C; idx += NT) {
-    const int i = idx / C, j = idx % C;
-    sm.u.fin.A1[i * LDC + j] = from_f<CT>((j <= i) ? sm.dQK[i * LDF + j] : 0.f);
-    sm.u.fin.A2[i * LDC + j] = from_f<CT>((i <= j) ? sm.dQK[j * LDF + i] : 0.f);
-    const float s = (j < i) ? sm.dKK[i * LDF + j] : ((i < j) ? sm.dKK[j * LDF + i] : 0.f);
-    sm.u.fin.A3[i * LDC + j] = from_f<CT>(s);
+  // ---- gram gradient products, shared over lanes: A1 = dQK (lower incl.
+  // diagonal), A2 = dQK^T, A3 = dKK + dKK^T, written from the owning waves'
+  // registers (the masked entries of a tile are zero) over zeroed matrices ----
+  for (int idx = tid; idx < C * LDC; idx += NT) {
+    sm.u.fin.A1[idx] = from_f<CT>(0.f);
+    sm.u.fin.A2[idx] = from_f<CT>(0.f);
+    sm.u.fin.A3[idx] = from_f<CT>(0.f);
   }
   for (int idx = tid; idx < C * D; idx += NT) {
     const int i = idx / D, d = idx % D;
@@ -445,27 +524,74 @@ delta_bwd_grads_kernel(DeltaBwdArgs p) {
   }
   __syncthreads();
 #pragma unroll
-  for (int it = 0; it < NCT; ++it) {
-    dQacc[it] += tile_nt<CT, C>(&sm.u.fin.A1[(it * 16 + n16) * LDC], &sm.u.fin.kt[dcol * LDC], g4);
-    dKacc[it] += tile_nt<CT, C>(&sm.u.fin.A2[(it * 16 + n16) * LDC], &sm.u.fin.qt[dcol * LDC], g4);
-    dKacc[it] += tile_nt<CT, C>(&sm.u.fin.A3[(it * 16 + n16) * LDC], &sm.u.fin.kt[dcol * LDC], g4);
+  for (int jj = 0; jj < NTASK; ++jj) {
+    const int task = wave + NW * jj;
+    if (task >= 2 * NP) continue;
+    const bool isL = task >= NP;
+    int it, jt;
+    tri_pair(isL ? task - NP : task, it, jt);
+    const int j = jt * 16 + n16;
+#pragma unroll
+    for (int ii = 0; ii < 4; ++ii) {
+      const int i = it * 16 + 4 * g4 + ii;
+      const CT x = from_f<CT>(dgram[jj][ii]);
+      if (!isL) {
+        if (j <= i) {
+          sm.u.fin.A1[i * LDC + j] = x;
+          sm.u.fin.A2[j * LDC + i] = x;
+        }
+      } else if (j < i) {
+        sm.u.fin.A3[i * LDC + j] = x;
+        sm.u.fin.A3[j * LDC + i] = x;
+      }
+    }
   }
-  // stores: transposed tiles, lane (g, n) holds row it*16+n, columns 16*wave + 4g..4g+3
+  __syncthreads();
+#pragma unroll
+  for (int kt = 0; kt < KT; ++kt) {
+    const int dcol = (tile0 + kt) * 16 + n16;
+#pragma unroll
+    for (int it = 0; it < NCT; ++it) {
+      dQacc[kt][it] += tile_nt<CT, C>(&sm.u.fin.A1[(it * 16 + n16) * LDC], &sm.u.fin.kt[dcol * LDC], g4);
+      dKacc[kt][it] += tile_nt<CT, C>(&sm.u.fin.A2[(it * 16 + n16) * LDC], &sm.u.fin.qt[dcol * LDC], g4);
+      dKacc[kt][it] += tile_nt<CT, C>(&sm.u.fin.A3[(it * 16 + n16) * LDC], &sm.u.fin.kt[dcol * LDC], g4);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // stores: transposed tiles, lane (g, n) holds row it*16+n, columns 16*tile + 4g..4g+3
   CT* dq = (CT*)p.dq;
   CT* dk = (CT*)p.dk;
   CT* dv = (CT*)p.dv;
 #pragma unroll
-  for (int it = 0; it < NCT; ++it) {
-    const int t = t0 + it * 16 + n16;
-    const f32x4 xq = tile_transpose((CT*)nullptr, dQacc[it], lane);
-    const f32x4 xk = tile_transpose((CT*)nullptr, dKacc[it], lane);
-    const f32x4 xv = tile_transpose((CT*)nullptr, dVacc[it], lane);
-    if (t < p.T) {
-      const size_t off = ((size_t)(b * p.T + t) * p.H + h) * D + wave * 16 + 4 * g4;
-      st4(dq + off, xq[0], xq[1], xq[2], xq[3]);
-      st4(dk + off, xk[0], xk[1], xk[2], xk[3]);
-      st4(dv + off, xv[0], xv[1], xv[2], xv[3]);
+  for (int kt = 0; kt < KT; ++kt)
+#pragma unroll
+    for (int it = 0; it < NCT; ++it) {
+      const int t = t0 + it * 16 + n16;
+      const f32x4 xq = tile_transpose((CT*)nullptr, dQacc[kt][it], lane);
+      const f32x4 xk = tile_transpose((CT*)nullptr, dKacc[kt][it], lane);
+      const f32x4 xv = tile_transpose((CT*)nullptr, dVacc[kt][it], lane);
+      if (t < p.T) {
+        const size_t off = ((size_t)(b * p.T + t) * p.H + h) * D + (tile0 + kt) * 16 + 4 * g4;
+        st4(dq + off, xq[0], xq[1], xq[2], xq[3]);
+        st4(dk + off, xk[0], xk[1], xk[2], xk[3]);
+        st4(dv + off, xv[0], xv[1], xv[2], xv[3]);
+      }
     }
+}
+
+// the per-token scalar gradients of the KH key parts, added in a fixed order
+template <int KH>
+__global__ void __launch_bounds__(256) delta_bwd_parts_kernel(const float* __restrict__ part, float* dae,
+                                                              float* daw, float* dg, long long rows) {
+  for (long long i = (long long)blockIdx.x * 256 + threadIdx.x; i < rows; i += (long long)gridDim.x * 256) {
+    float s[3] = {0.f, 0.f, 0.f};
+#pragma unroll
+    for (int k = 0; k < KH; ++k)
+#pragma unroll
+      for (int q = 0; q < 3; ++q) s[q] += part[((size_t)k * 3 + q) * rows + i];
+    dae[i] = s[0];
+    daw[i] = s[1];
+    dg[i] = s[2];
   }
 }
 
@@ -478,14 +604,26 @@ static int launch_bwd(const DeltaBwdArgs& a, int stages, hipStream_t stream) {
     if (rc) return rc;
   }
   if (stages & 2) {
-    hipLaunchKernelGGL((delta_bwd_grads_kernel<CT, D, C>), dim3(a.B * a.H * NC), dim3(GradDims<CT, D>::NT), 0, stream, a);
-    return check_launch("delta_bwd_grads_kernel");
+    constexpr int KH = GradDims<CT, D, C>::KH;
+    hipLaunchKernelGGL((delta_bwd_grads_kernel<CT, D, C>), dim3(a.B * a.H * NC * KH), dim3(GradDims<CT, D, C>::NT),
+                       0, stream, a);
+    int rc = check_launch("delta_bwd_grads_kernel");
+    if (rc || KH == 1) return rc;
+    const size_t nrec = (size_t)a.B * a.H * a.M * NC, esz = sizeof(CT);
+    const float* part = (const float*)((const char*)a.ds_stash + nrec * ((size_t)a.D * a.D + (size_t)C * a.D) * esz);
+    const long long rows = (long long)a.B * a.T * a.H * a.M;
+    const long long nb = (rows + 255) / 256;
+    hipLaunchKernelGGL((delta_bwd_parts_kernel<KH>), dim3((unsigned)(nb < 2048 ? nb : 2048)), dim3(256), 0, stream,
+                       part, a.dae, a.daw, a.dg, rows);
+    return check_launch("delta_bwd_parts_kernel");
   }
   return GDNX_OK;
 }
 
 int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream) {
   if (a.dtype == GDNX_DTYPE_BF16) {
+    if (a.D == 128 && a.C == 64) return launch_bwd<bf16, 128, 64>(a, stages, stream);
+    if (a.D == 64 && a.C == 64) return launch_bwd<bf16, 64, 64>(a, stages, stream);
     if (a.D == 128 && a.C == 32) return launch_bwd<bf16, 128, 32>(a, stages, stream);
     if (a.D == 64 && a.C == 32) return launch_bwd<bf16, 64, 32>(a, stages, stream);
   } else {

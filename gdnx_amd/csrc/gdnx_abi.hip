@@ -29,8 +29,10 @@ int delta_chunk_size(int D, int dtype) {
   return dtype == GDNX_DTYPE_BF16 ? 64 : 32;
 }
 
-// chunk used when the forward stashes states for the backward: the gradient
-// kernel keeps S0 / dS value-contiguous in LDS, which bounds the chunk
+// chunk used when the forward stashes states for the backward: 32 for bf16,
+// 16 for float32.  A 64-token bf16 chunk halves the state stashes but ran
+// the config-2 step 40 % slower (the scans and the gradient kernel are bound
+// by the latency of a chunk's work, not by its bytes); it stays selectable.
 int delta_train_chunk_size(int D, int dtype) {
   if (D != 64 && D != 128) return 0;
   return dtype == GDNX_DTYPE_BF16 ? 32 : 16;

@@ -44,7 +44,7 @@ const char* gdnx_last_error(void);
 int gdnx_delta_chunk_size(int head_dim, int dtype);
 
 /* Chunk length to use when the forward stashes states for the backward
- * (32 for bf16, 16 for float32). */
+ * (32 for bf16, 16 for float32; the backward also takes 64 for bf16). */
 int gdnx_delta_train_chunk_size(int head_dim, int dtype);
 
 /* Bytes of the per-chunk stash for the given chunk (0 = default; -1 if
