@@ -17,7 +17,8 @@ LIB_PATH = os.path.join(_HERE, "libgdnx.so")
 
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
-ABI_VERSION = 8
+DTYPE_F64 = 2      # gdnx_check_finite only
+ABI_VERSION = 9
 
 _c_int, _c_ll, _vp, _c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_float
 
@@ -25,6 +26,8 @@ _c_int, _c_ll, _vp, _c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p,
 SIGNATURES = {
     "gdnx_abi_version": (_c_int, []),
     "gdnx_last_error": (ctypes.c_char_p, []),
+    "gdnx_set_check_finite": (_c_int, [_c_int]),
+    "gdnx_check_finite": (_c_int, [_vp, _c_ll, _c_int, _vp]),
     "gdnx_delta_chunk_size": (_c_int, [_c_int, _c_int]),
     "gdnx_delta_train_chunk_size": (_c_int, [_c_int, _c_int]),
     "gdnx_delta_chunk_states_bytes": (_c_ll, [_c_int] * 7),
@@ -39,20 +42,20 @@ SIGNATURES = {
     "gdnx_gdn3_workspace_bytes": (_c_ll, [_c_int] * 6),
     "gdnx_gdn3_num_compactions": (_c_int, [_c_int] * 3),
     "gdnx_gdn3_chunk_fwd": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 10
-                            + [_c_int] * 12 + [_c_float, _c_int, _vp]),
+                            + [_c_int] * 12 + [_c_float, _c_int, _c_int, _vp]),
     "gdnx_gdn3_num_compactions_from": (_c_int, [_c_int] * 4),
     "gdnx_gdn3_chunk_fwd_state": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 6 + [_c_int]
-                                  + [_vp] * 7 + [_c_int] * 12 + [_c_float, _c_int, _vp]),
+                                  + [_vp] * 7 + [_c_int] * 12 + [_c_float, _c_int, _c_int, _vp]),
     "gdnx_gdn3_noalloc_scratch_bytes": (_c_ll, []),
     "gdnx_gdn3_chunk_fwd_state_noalloc": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 6
-                                          + [_c_int] + [_vp] * 6 + [_c_int] * 12 + [_c_float, _c_int, _vp]),
+                                          + [_c_int] + [_vp] * 6 + [_c_int] * 12 + [_c_float, _c_int, _c_int, _vp]),
     "gdnx_gdn3_decode_step": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 10
-                              + [_c_int] * 12 + [_c_float, _c_int, _vp]),
+                              + [_c_int] * 12 + [_c_float, _c_int, _c_int, _vp]),
     "gdnx_delta_decode_step_chan": (_c_int, [_vp] * 9 + [_c_int] * 6 + [_vp]),
     "gdnx_gdn3_train_states_bytes": (_c_ll, [_c_int] * 7),
     "gdnx_gdn3_chunk_bwd": (_c_int, [_vp] * 3 + [_c_int] + [_vp] * 2 + [_c_int] + [_vp] * 9
                             + [_c_int] * 13 + [_vp]),
-    "gdnx_gdn3_compact": (_c_int, [_vp] * 8 + [_c_int] * 8 + [_c_float, _vp]),
+    "gdnx_gdn3_compact": (_c_int, [_vp] * 8 + [_c_int] * 8 + [_c_float, _c_int, _vp]),
     "gdnx_kron_read": (_c_int, [_vp] * 6 + [_c_int] * 9 + [_vp]),
     "gdnx_gdn3_coeff": (_c_int, [_vp] * 3 + [_c_int] * 6 + [_vp]),
     "gdnx_delta_chan_states_bytes": (_c_ll, [_c_int] * 4),
@@ -75,6 +78,15 @@ SIGNATURES = {
 
 class GdnxError(RuntimeError):
     pass
+
+
+class GdnxNonFinite(GdnxError):
+    """A recurrence's outputs held NaN or infinity (GDNX_ERR_NONFINITE, only
+    with set_check_finite(True)): the counterpart of the reference trainer's
+    guard that drops such a step (train/train_gdn3_distill.py:329-354)."""
+
+
+ERR_NONFINITE = -5
 
 
 _lib = None
@@ -103,7 +115,16 @@ def load():
 def check(rc: int, what: str) -> None:
     if rc != 0:
         msg = load().gdnx_last_error().decode(errors="replace")
-        raise GdnxError(f"{what} failed ({rc}): {msg}")
+        cls = GdnxNonFinite if rc == ERR_NONFINITE else GdnxError
+        raise cls(f"{what} failed ({rc}): {msg}")
+
+
+def set_check_finite(on: bool) -> bool:
+    """Turn the library's non-finite checking on or off (process-wide;
+    gdnx_set_check_finite).  When on, every recurrence call scans its outputs
+    and synchronises its stream, raising GdnxNonFinite on NaN or infinity.
+    Returns the previous setting."""
+    return bool(load().gdnx_set_check_finite(1 if on else 0))
 
 
 def ptr(t):

@@ -262,6 +262,24 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int tid, int pass
   }
 }
 
+// Sums of squares of the first kRMax columns of a row-major [M][kQ] double
+// array, into out[0..kRMax) (every thread waits for them).
+template <int M>
+__device__ __forceinline__ void col_sumsq(const double* y, double* red, double* out, int tid) {
+  const int r = tid & (kRMax - 1), lane = tid & 63, wave = tid >> 6;
+  double part = 0.0;
+  for (int row = tid / kRMax; row < M; row += kNT / kRMax) {
+    const double x = y[row * kQ + r];
+    part += x * x;
+  }
+#pragma unroll
+  for (int off = kRMax; off < 64; off <<= 1) part += __shfl_xor(part, off, 64);
+  if (lane < kRMax) red[wave * kRMax + lane] = part;
+  __syncthreads();
+  if (tid < kRMax) out[tid] = (red[tid] + red[kRMax + tid]) + (red[2 * kRMax + tid] + red[3 * kRMax + tid]);
+  __syncthreads();
+}
+
 // Compaction of one chain (gdn3/gdn3_upgrade.py:650-719) on LDS inputs:
 // ab = [A (R x m) | B (R x n)] as stored (the Kronecker part is decayed by
 // e^{gacc} per factor), cs.ut = window net writes [P][D], vbd = window keys
@@ -269,9 +287,14 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int tid, int pass
 // thread 0, stats = (|R_mat|^2, sum of the R kept sigma^2).  Sign
 // convention: each (u_r, v_r) pair is flipped so that the largest-magnitude
 // entry of v_r is positive (first index on ties).
+// mode 1 is the reference's 'sketch' / 'sketch_noqr' (both run the same
+// branch, gdn3/gdn3_upgrade.py:579-592): no range finder and no SVD, with a
+// sketch of qs = R columns, Q = the column-normalised R_mat G,
+// Bm = Q^T R_mat, A_svd_r = |Bm_r| Q_r, B_svd_r = Bm_r / |Bm_r| (norms
+// clamped at 1e-12); it reports no error (stats = (|R_mat|^2, |R_mat|^2)).
 template <int D, int P>
 __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float (*vbd)[D + 4], float gacc, float sdec,
-                           const float* __restrict__ sketch, double* stats, int tid) {
+                           const float* __restrict__ sketch, double* stats, int tid, int mode = 0) {
   typedef G3D<D> Ge;
   constexpr int R = Ge::R, m = Ge::m, n = Ge::n, q = Ge::q, ak = Ge::ak, bk = Ge::bk;
   constexpr int lbv = Ge::lbv, lbk = Ge::lbk, ln = Ge::ln;
@@ -283,11 +306,12 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
   // the sketch's global loads are issued first and land in LDS after the
   // residual part (which does not read them)
   constexpr int NGS = (n * kQ + kNT - 1) / kNT;
+  const int qs = mode ? R : q;   // the sketch's columns
   float gsv[NGS];
 #pragma unroll
   for (int u = 0; u < NGS; ++u) {
     const int e = tid + u * kNT, c = e / kQ, j = e % kQ;
-    gsv[u] = (e < n * kQ && j < q) ? sketch[c * q + j] : 0.f;
+    gsv[u] = (e < n * kQ && j < qs) ? sketch[c * qs + j] : 0.f;
   }
   // residual part rearrange(U Vb^T) on fp32 MFMA: out[v][k] = sum_p U_p[v] Vb_p[k]
   // (A[v][p] = U_p[v], B[p][k] = Vb_p[k]); wave w owns the value-row tiles
@@ -364,6 +388,38 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
     en[0] = (e4[0] + e4[1]) + (e4[2] + e4[3]);
   }
   block_sum<1>(en, cs.red, tid);
+
+  if (mode) {   // 'sketch': one product, column and row normalisation
+    rm_mfma<false, m, n>(cs.rm, ldr, cs.gs, cs.y, tid);   // Y = R_mat G (columns >= R are zero)
+    __syncthreads();
+    col_sumsq<m>(cs.y, cs.red, cs.lam, tid);
+    for (int e = tid; e < m * kQ; e += kNT) {
+      const int j = e % kQ;
+      cs.y[e] = j < R ? cs.y[e] / fmax(sqrt(cs.lam[j]), 1e-12) : 0.0;   // Q
+    }
+    __syncthreads();
+    rm_mfma<true, n, m>(cs.rm, ldr, cs.y, cs.z, tid);      // Bm^T = R_mat^T Q
+    __syncthreads();
+    col_sumsq<n>(cs.z, cs.red, cs.sig, tid);
+    const float dk = expf(gacc);
+    const float s1 = sdec, s2 = 1.f - sdec;
+    for (int e = tid; e < R * m; e += kNT) {
+      const int r = e / m, row = e % m;
+      const double sv = cs.y[row * kQ + r] * fmax(sqrt(cs.sig[r]), 1e-12);
+      A[e] = s1 * (A[e] * dk) + s2 * (float)sv;
+    }
+    for (int e = tid; e < R * n; e += kNT) {
+      const int r = e / n, col = e % n;
+      const double sv = cs.z[col * kQ + r] / fmax(sqrt(cs.sig[r]), 1e-12);
+      Bv[e] = s1 * (Bv[e] * dk) + s2 * (float)sv;
+    }
+    if (tid == 0 && stats) {
+      stats[0] = en[0];
+      stats[1] = en[0];
+    }
+    __syncthreads();
+    return;
+  }
 
   // range finder with two power iterations; orthonormalising between the
   // products leaves the final basis unchanged (up to column signs)
@@ -1052,8 +1108,9 @@ __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
   }
   const float gacc = p.gsum ? p.gsum[chain] : 0.f;
   __syncthreads();
-  g3_compact<D, P>(sm.k, sm.ab, sm.vbd, gacc, p.sdec, p.sketch + (size_t)chain * Ge::n * Ge::q,
-                   p.stats ? p.stats + (size_t)blockIdx.x * 2 : nullptr, tid);
+  const int qs = p.mode ? Ge::R : Ge::q;   // sketch columns
+  g3_compact<D, P>(sm.k, sm.ab, sm.vbd, gacc, p.sdec, p.sketch + (size_t)chain * Ge::n * qs,
+                   p.stats ? p.stats + (size_t)blockIdx.x * 2 : nullptr, tid, p.mode);
   for (int e = tid; e < Rm; e += kNT) {
     p.A_out[(size_t)chain * Rm + e] = sm.ab[e];
     if (p.A_fin) p.A_fin[(size_t)chain * Rm + e] = sm.ab[e];
@@ -1240,6 +1297,7 @@ int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
       ca.A_fin = a.last ? a.A_out : nullptr;
       ca.B_fin = a.last ? a.B_out : nullptr;
       ca.ab_stash = ts.ab ? ts.ab + (size_t)event * N * Ge::RMN : nullptr;
+      ca.mode = a.cmode;
       if ((rc = compact_dispatch(ca, stream))) return rc;
       ++event;
     }

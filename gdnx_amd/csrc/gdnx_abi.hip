@@ -101,7 +101,11 @@ static int fwd_common(const void* q, const void* k, const void* v, const float* 
   if (T == 0) return GDNX_OK;
   DeltaArgs a{q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, B, T, H, M, head_dim, C, dtype,
               r_norm, workspace};
-  return delta_fwd_dispatch(a, (hipStream_t)stream);
+  if ((rc = delta_fwd_dispatch(a, (hipStream_t)stream))) return rc;
+  const size_t rows = (size_t)B * T * H * M, D = head_dim;
+  const FiniteBuf outs[] = {{y, rows * D, dtype}, {state_out, (size_t)B * H * M * D * D, GDNX_DTYPE_F32},
+                            {r_norm, rows, GDNX_DTYPE_F32}};
+  return finite_outputs(outs, 3, (hipStream_t)stream);
 }
 
 extern "C" long long gdnx_delta_fwd_workspace_bytes(int B, int T, int H, int M, int head_dim, int chunk,
@@ -151,7 +155,14 @@ static int bwd_common(const void* q, const void* k, const void* v, const float* 
   if (T == 0) return GDNX_OK;
   DeltaBwdArgs a{q,  k,  v,  a_e,  a_w,  log_g, dy,      dstate_out, chunk_states, workspace, dq, dk,
                  dv, da_e, da_w, dlog_g, dstate0, B, T, H, M, head_dim, C, dtype};
-  return delta_bwd_dispatch(a, stages, (hipStream_t)stream);
+  if ((rc = delta_bwd_dispatch(a, stages, (hipStream_t)stream))) return rc;
+  const size_t rows = (size_t)B * T * H * M, D = head_dim, tok = (size_t)B * T * H * D;
+  const bool g = (stages & 2) != 0;
+  const FiniteBuf outs[] = {{g ? dq : nullptr, tok, dtype}, {g ? dk : nullptr, tok, dtype},
+                            {g ? dv : nullptr, tok, dtype}, {g ? da_e : nullptr, rows, GDNX_DTYPE_F32},
+                            {g ? da_w : nullptr, rows, GDNX_DTYPE_F32}, {g ? dlog_g : nullptr, rows, GDNX_DTYPE_F32},
+                            {dstate0, (size_t)B * H * M * D * D, GDNX_DTYPE_F32}};
+  return finite_outputs(outs, 7, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v, const float* a_e,
@@ -198,7 +209,10 @@ extern "C" int gdnx_delta_decode_step(const void* q, const void* k, const void* 
     return set_error(GDNX_ERR_ARG, "all pointers must be non-null");
   if ((uintptr_t)state & 15u) return set_error(GDNX_ERR_ARG, "state must be 16-byte aligned");
   DecodeArgs a{q, k, v, a_e, a_w, log_g, state, y, NS, H, M, head_dim, dtype, nullptr, 0};
-  return decode_dispatch(a, (hipStream_t)stream);
+  const int rc = decode_dispatch(a, (hipStream_t)stream);
+  if (rc) return rc;
+  const FiniteBuf outs[] = {{y, (size_t)NS * H * M * head_dim, dtype}};
+  return finite_outputs(outs, 1, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_delta_decode_step_slots(const void* q, const void* k, const void* v, const float* a_e,
@@ -217,7 +231,10 @@ extern "C" int gdnx_delta_decode_step_slots(const void* q, const void* k, const 
     return set_error(GDNX_ERR_ARG, "all pointers must be non-null");
   if ((uintptr_t)state_pool & 15u) return set_error(GDNX_ERR_ARG, "state_pool must be 16-byte aligned");
   DecodeArgs a{q, k, v, a_e, a_w, log_g, state_pool, y, NS, H, M, head_dim, dtype, slots, n_slots};
-  return decode_dispatch(a, (hipStream_t)stream);
+  const int rc = decode_dispatch(a, (hipStream_t)stream);
+  if (rc) return rc;
+  const FiniteBuf outs[] = {{y, (size_t)NS * H * M * head_dim, dtype}};
+  return finite_outputs(outs, 1, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_delta_decode_step_chan(const void* q, const void* k, const void* v, const float* a_e,
@@ -237,7 +254,10 @@ extern "C" int gdnx_delta_decode_step_chan(const void* q, const void* k, const v
     return set_error(GDNX_ERR_ARG, "all pointers but slots must be non-null");
   if ((uintptr_t)state_pool & 15u) return set_error(GDNX_ERR_ARG, "state_pool must be 16-byte aligned");
   DecodeArgs a{q, k, v, a_e, a_w, log_g, state_pool, y, NS, H, M, head_dim, dtype, slots, n_slots, 1};
-  return decode_dispatch(a, (hipStream_t)stream);
+  const int rc = decode_dispatch(a, (hipStream_t)stream);
+  if (rc) return rc;
+  const FiniteBuf outs[] = {{y, (size_t)NS * H * M * head_dim, dtype}};
+  return finite_outputs(outs, 1, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -310,8 +330,10 @@ static int g3_fwd_args(G3FwdArgs& a, const void* q, const void* k, const void* v
                        const float* sketch, void* y, float* A_out, float* B_out, float* U_out, float* Vb_out,
                        double* comp_stats, void* workspace, int B, int T, int H, int M, int head_dim, int R,
                        int P, int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
-                       int dtype, bool need_workspace = true) {
+                       int dtype, int compact_mode, bool need_workspace = true) {
   int rc = check_common(q, k, v, B, T, H, M, head_dim, dtype);
+  if (compact_mode != 0 && compact_mode != 1)
+    return set_error(GDNX_ERR_ARG, "compact_mode %d is not 0 (svd) or 1 (sketch)", compact_mode);
   if (rc) return rc;
   G3Geom ge;
   if ((rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge))) return rc;
@@ -359,7 +381,23 @@ static int g3_fwd_args(G3FwdArgs& a, const void* q, const void* k, const void* v
   a.gate_ch = gate_channels;
   a.dtype = dtype;
   a.sdec = slow_decay;
+  a.cmode = compact_mode;
   return GDNX_OK;
+}
+
+// the GDN3 forward dispatch, then (when checking is on) its outputs' scan
+static int g3_fwd_run(const G3FwdArgs& a, hipStream_t stream) {
+  int rc = gdn3_fwd_dispatch(a, stream);
+  if (rc || !check_finite_on()) return rc;
+  const size_t N = (size_t)a.B * a.H * a.M, D = a.D;
+  const size_t nev = (size_t)((a.t0 + a.T) / a.Kc - a.t0 / a.Kc);
+  const FiniteBuf outs[] = {{a.y, (size_t)a.B * a.T * a.H * a.M * D, a.dtype},
+                            {a.A_out, N * a.ge.R * a.ge.m, GDNX_DTYPE_F32},
+                            {a.B_out, N * a.ge.R * a.ge.n, GDNX_DTYPE_F32},
+                            {a.U_out, N * D * a.P, GDNX_DTYPE_F32},
+                            {a.Vb_out, N * D * a.P, GDNX_DTYPE_F32},
+                            {a.stats, nev * N * 2, GDNX_DTYPE_F64}};
+  return finite_check(outs, 6, stream);
 }
 }  // namespace gdnx
 
@@ -370,12 +408,12 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
                                    void* workspace, void* train_states, int B, int T, int H, int M,
                                    int head_dim, int R, int P,
                                    int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
-                                   int dtype, void* stream) {
+                                   int dtype, int compact_mode, void* stream) {
   g_err[0] = 0;
   G3FwdArgs a;
   int rc = g3_fwd_args(a, q, k, v, qkv_lanes, b_gates, w_gates, gate_channels, decay, sketch, y, A_out, B_out,
                        U_out, Vb_out, comp_stats, workspace, B, T, H, M, head_dim, R, P, compact_every, a_v, a_k,
-                       b_v, b_k, slow_decay, dtype);
+                       b_v, b_k, slow_decay, dtype, compact_mode);
   if (rc) return rc;
   if (train_states && !aligned16(train_states)) return set_error(GDNX_ERR_ARG, "train_states must be 16-byte aligned");
   if (T == 0) {   // the final state of an empty run is the zero initial state
@@ -388,7 +426,7 @@ extern "C" int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, 
     return GDNX_OK;
   }
   a.train_states = train_states;
-  return gdn3_fwd_dispatch(a, (hipStream_t)stream);
+  return g3_fwd_run(a, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_gdn3_num_compactions_from(int t0, int T, int P, int compact_every) {
@@ -435,12 +473,13 @@ extern "C" int gdnx_gdn3_chunk_fwd_state(const void* q, const void* k, const voi
                                          float* A_out, float* B_out, float* U_out, float* Vb_out,
                                          double* comp_stats, void* workspace, int B, int T, int H, int M,
                                          int head_dim, int R, int P, int compact_every, int a_v, int a_k,
-                                         int b_v, int b_k, float slow_decay, int dtype, void* stream) {
+                                         int b_v, int b_k, float slow_decay, int dtype, int compact_mode,
+                                         void* stream) {
   g_err[0] = 0;
   G3FwdArgs a;
   int rc = g3_fwd_args(a, q, k, v, qkv_lanes, b_gates, w_gates, gate_channels, decay, sketch, y, A_out, B_out,
                        U_out, Vb_out, comp_stats, workspace, B, T, H, M, head_dim, R, P, compact_every, a_v, a_k,
-                       b_v, b_k, slow_decay, dtype);
+                       b_v, b_k, slow_decay, dtype, compact_mode);
   if (rc) return rc;
   if ((rc = g3_state_check(A0, B0, U0, Vb0, t0, T))) return rc;
   if (T == 0)
@@ -451,7 +490,7 @@ extern "C" int gdnx_gdn3_chunk_fwd_state(const void* q, const void* k, const voi
   a.B0 = B0;
   a.U0 = U0;
   a.Vb0 = Vb0;
-  return gdn3_fwd_dispatch(a, (hipStream_t)stream);
+  return g3_fwd_run(a, (hipStream_t)stream);
 }
 
 extern "C" long long gdnx_gdn3_noalloc_scratch_bytes(void) { return (long long)kG3ScratchBytes; }
@@ -463,12 +502,13 @@ extern "C" int gdnx_gdn3_chunk_fwd_state_noalloc(const void* q, const void* k, c
                                                  void* y, float* A_out, float* B_out, float* U_out, float* Vb_out,
                                                  double* comp_stats, int B, int T, int H, int M, int head_dim,
                                                  int R, int P, int compact_every, int a_v, int a_k, int b_v,
-                                                 int b_k, float slow_decay, int dtype, void* stream) {
+                                                 int b_k, float slow_decay, int dtype, int compact_mode,
+                                                 void* stream) {
   g_err[0] = 0;
   G3FwdArgs a;
   int rc = g3_fwd_args(a, q, k, v, qkv_lanes, b_gates, w_gates, gate_channels, decay, sketch, y, A_out, B_out,
                        U_out, Vb_out, comp_stats, nullptr, B, T, H, M, head_dim, R, P, compact_every, a_v, a_k,
-                       b_v, b_k, slow_decay, dtype, /*need_workspace=*/false);
+                       b_v, b_k, slow_decay, dtype, compact_mode, /*need_workspace=*/false);
   if (rc) return rc;
   if ((rc = g3_state_check(A0, B0, U0, Vb0, t0, T))) return rc;
   const size_t need = gdn3_workspace_bytes(B * H * M, head_dim, P, dtype);
@@ -488,7 +528,7 @@ extern "C" int gdnx_gdn3_chunk_fwd_state_noalloc(const void* q, const void* k, c
   a.B0 = B0;
   a.U0 = U0;
   a.Vb0 = Vb0;
-  return gdn3_fwd_dispatch(a, (hipStream_t)stream);
+  return g3_fwd_run(a, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_gdn3_decode_step(const void* q, const void* k, const void* v, int qkv_lanes,
@@ -497,10 +537,12 @@ extern "C" int gdnx_gdn3_decode_step(const void* q, const void* k, const void* v
                                      float* Vb, const int* slots, const int* pos, void* y, double* comp_stats,
                                      int NS, int n_slots, int H, int M, int head_dim, int R, int P,
                                      int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
-                                     int dtype, void* stream) {
+                                     int dtype, int compact_mode, void* stream) {
   g_err[0] = 0;
   if (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16)
     return set_error(GDNX_ERR_ARG, "dtype %d is not GDNX_DTYPE_F32/BF16", dtype);
+  if (compact_mode != 0 && compact_mode != 1)
+    return set_error(GDNX_ERR_ARG, "compact_mode %d is not 0 (svd) or 1 (sketch)", compact_mode);
   G3Geom ge;
   int rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge);
   if (rc) return rc;
@@ -549,7 +591,11 @@ extern "C" int gdnx_gdn3_decode_step(const void* q, const void* k, const void* v
   ca.hm = H * M;
   ca.Kc = compact_every;
   ca.nslots = n_slots;
-  return gdn3_compact_dispatch(ca, (hipStream_t)stream);
+  ca.mode = compact_mode;
+  if ((rc = gdn3_compact_dispatch(ca, (hipStream_t)stream))) return rc;
+  const size_t nch = (size_t)NS * H * M;
+  const FiniteBuf outs[] = {{y, nch * head_dim, dtype}, {comp_stats, nch * 2, GDNX_DTYPE_F64}};
+  return finite_outputs(outs, 2, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_gdn3_chunk_bwd(const void* q, const void* k, const void* v, int qkv_lanes,
@@ -581,14 +627,21 @@ extern "C" int gdnx_gdn3_chunk_bwd(const void* q, const void* k, const void* v, 
   if (T == 0) return GDNX_OK;
   G3BwdArgs a{q, k, v, b_gates, w_gates, decay, dy, train_states, dq, dk, dv, db_gates, dw_gates, ddecay,
               B, T, H, M, head_dim, P, compact_every, qkv_lanes, gate_channels, dtype};
-  return gdn3_bwd_dispatch(a, (hipStream_t)stream);
+  if ((rc = gdn3_bwd_dispatch(a, (hipStream_t)stream))) return rc;
+  const size_t rows = (size_t)B * T * H * M;
+  const FiniteBuf outs[] = {{dq, rows * head_dim, GDNX_DTYPE_F32}, {dk, rows * head_dim, GDNX_DTYPE_F32},
+                            {dv, rows * head_dim, GDNX_DTYPE_F32}, {db_gates, rows * gate_channels, GDNX_DTYPE_F32},
+                            {dw_gates, rows * gate_channels, GDNX_DTYPE_F32}, {ddecay, rows, GDNX_DTYPE_F32}};
+  return finite_outputs(outs, 6, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_gdn3_compact(const float* A, const float* Bf, const float* U, const float* Vb,
                                  const float* sketch, float* A_out, float* B_out, double* comp_stats, int N,
                                  int head_dim, int R, int P, int a_v, int a_k, int b_v, int b_k,
-                                 float slow_decay, void* stream) {
+                                 float slow_decay, int compact_mode, void* stream) {
   g_err[0] = 0;
+  if (compact_mode != 0 && compact_mode != 1)
+    return set_error(GDNX_ERR_ARG, "compact_mode %d is not 0 (svd) or 1 (sketch)", compact_mode);
   G3Geom ge;
   int rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge);
   if (rc) return rc;
@@ -616,6 +669,7 @@ extern "C" int gdnx_gdn3_compact(const float* A, const float* Bf, const float* U
   a.sdec = slow_decay;
   a.u_sp = 1;  // reference layout [d][p]
   a.u_sd = P;
+  a.mode = compact_mode;
   return gdn3_compact_dispatch(a, (hipStream_t)stream);
 }
 
@@ -702,7 +756,12 @@ extern "C" int gdnx_delta_chan_fwd(const float* q, const float* k, const float* 
   if (T == 0) return GDNX_OK;
   ChanArgs a{q, k, v, beta_e, beta_w, log_g, state0, y, state_out, chunk_states, r_norm, B, T, H, head_dim,
              workspace, nullptr, nullptr};
-  return chan_fwd_dispatch(a, (hipStream_t)stream);
+  if ((rc = chan_fwd_dispatch(a, (hipStream_t)stream))) return rc;
+  const size_t rows = (size_t)B * T * H;
+  const FiniteBuf outs[] = {{y, rows * head_dim, GDNX_DTYPE_F32},
+                            {state_out, (size_t)B * H * head_dim * head_dim, GDNX_DTYPE_F32},
+                            {r_norm, rows, GDNX_DTYPE_F32}};
+  return finite_outputs(outs, 3, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_delta_chan_bwd(const float* q, const float* k, const float* v, const float* beta_e,
@@ -722,7 +781,13 @@ extern "C" int gdnx_delta_chan_bwd(const float* q, const float* k, const float* 
   if (T == 0) return GDNX_OK;
   ChanBwdArgs a{q, k, v, beta_e, beta_w, log_g, dy, dstate_out, chunk_states, workspace, dq, dk, dv,
                 dbeta_e, dbeta_w, dlog_g, dstate0, B, T, H, head_dim};
-  return chan_bwd_dispatch(a, (hipStream_t)stream);
+  if ((rc = chan_bwd_dispatch(a, (hipStream_t)stream))) return rc;
+  const size_t rows = (size_t)B * T * H, tok = rows * head_dim;
+  const FiniteBuf outs[] = {{dq, tok, GDNX_DTYPE_F32},     {dk, tok, GDNX_DTYPE_F32},
+                            {dv, tok, GDNX_DTYPE_F32},     {dlog_g, tok, GDNX_DTYPE_F32},
+                            {dbeta_e, rows, GDNX_DTYPE_F32}, {dbeta_w, rows, GDNX_DTYPE_F32},
+                            {dstate0, (size_t)B * H * head_dim * head_dim, GDNX_DTYPE_F32}};
+  return finite_outputs(outs, 7, (hipStream_t)stream);
 }
 
 // ---------------------------------------------------------------------------
@@ -904,7 +969,10 @@ extern "C" int gdnx_rls_fwd(const float* q, const float* K, const float* V, cons
   d.y = y; d.state_out = state_out; d.ckpt = ckpt;
   d.B = B; d.T = T; d.H = H; d.R = R; d.RO = R_out; d.dk = key_dim; d.dv = value_dim; d.eps = eps;
   d.cP = compact_P; d.cR = compact_R; d.cs = slow_decay;
-  return rls_dispatch(d, false, (hipStream_t)stream);
+  if ((rc = rls_dispatch(d, false, (hipStream_t)stream))) return rc;
+  const FiniteBuf outs[] = {{y, (size_t)B * T * H * value_dim, GDNX_DTYPE_F32},
+                            {state_out, (size_t)B * H * value_dim * key_dim, GDNX_DTYPE_F32}};
+  return finite_outputs(outs, 2, (hipStream_t)stream);
 }
 
 extern "C" int gdnx_rls_bwd(const float* q, const float* K, const float* V, const float* Bg, const float* Wg,
@@ -929,5 +997,12 @@ extern "C" int gdnx_rls_bwd(const float* q, const float* K, const float* V, cons
   d.cP = compact_P; d.cR = compact_R; d.cs = slow_decay; d.ste = straight_through != 0;
   if (workspace && !aligned16(workspace)) return set_error(GDNX_ERR_ARG, "workspace must be 16-byte aligned");
   d.workspace = workspace;
-  return rls_dispatch(d, true, (hipStream_t)stream);
+  if ((rc = rls_dispatch(d, true, (hipStream_t)stream))) return rc;
+  const size_t rows = (size_t)B * T * H;
+  const FiniteBuf outs[] = {{dq, rows * R_out * key_dim, GDNX_DTYPE_F32},  {dK, rows * R * key_dim, GDNX_DTYPE_F32},
+                            {dV, rows * R * value_dim, GDNX_DTYPE_F32},    {dBg, rows * R * key_dim, GDNX_DTYPE_F32},
+                            {dWg, rows * R * value_dim, GDNX_DTYPE_F32},   {da, rows * key_dim, GDNX_DTYPE_F32},
+                            {d_out_mix_seq, (size_t)B * H * R_out, GDNX_DTYPE_F32},
+                            {d_state0, (size_t)B * H * value_dim * key_dim, GDNX_DTYPE_F32}};
+  return finite_outputs(outs, 8, (hipStream_t)stream);
 }

@@ -95,6 +95,19 @@ struct ChanBwdArgs {
   int B, T, H, D;
 };
 
+// Opt-in non-finite detection (finite.hip): with gdnx_set_check_finite(1),
+// finite_outputs scans the buffers, synchronises the stream and returns
+// GDNX_ERR_NONFINITE if any element is NaN or infinite; otherwise GDNX_OK
+// at no cost.
+struct FiniteBuf {
+  const void* p;
+  size_t n;
+  int dtype;   // GDNX_DTYPE_*
+};
+bool check_finite_on();
+int finite_check(const FiniteBuf* bufs, int nbuf, hipStream_t stream);
+int finite_outputs(const FiniteBuf* bufs, int nbuf, hipStream_t stream);
+
 // Record an error message for gdnx_last_error(); returns code.
 int set_error(int code, const char* fmt, ...);
 // Check hipGetLastError() after a launch.
@@ -167,6 +180,7 @@ struct G3FwdArgs {
   // t0 mod P; compactions follow global tokens t with (t + 1) mod Kc == 0);
   // A0/B0/U0/Vb0 in the output layouts, or all null for a zero state
   int t0;
+  int cmode;           // compaction mode (G3CompactArgs::mode)
   const float* A0;
   const float* B0;
   const float* U0;
@@ -209,6 +223,7 @@ struct G3CompactArgs {
   const int* pos;
   const int* slots;
   int hm, Kc, nslots;
+  int mode;            // 0: 'svd' (range finder + SVD), 1: 'sketch' (normalised sketch, no SVD)
 };
 
 // Backward of the Kronecker-residual regime (gdn3_bwd.hip)

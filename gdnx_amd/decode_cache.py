@@ -36,7 +36,8 @@ KINDS = ("dense", "chan", "gdn3")
 
 class DecodeStateCache:
     def __init__(self, n_slots: int, H: int, M: int, D: int, device="cuda", kind: str = "dense", *,
-                 R: int = 4, P: int = 16, factors=None, slow_decay: float = 0.97, compact_every=None):
+                 R: int = 4, P: int = 16, factors=None, slow_decay: float = 0.97, compact_every=None,
+                 compact_mode: str = "svd"):
         if kind not in KINDS:
             raise ValueError(f"kind must be one of {KINDS}, got {kind!r}")
         if kind == "chan" and M != 1:
@@ -50,12 +51,13 @@ class DecodeStateCache:
             a_v, a_k, b_v, b_k = factors
             self.R, self.P, self.factors, self.slow_decay = R, P, tuple(factors), slow_decay
             self.compact_every = P if compact_every is None else int(compact_every)
+            self.compact_mode = ops.compact_mode_code(compact_mode)
             dev = self.device
             self.A = torch.zeros(n_slots, H, M, R, a_v, a_k, device=dev)
             self.B = torch.zeros(n_slots, H, M, R, b_v, b_k, device=dev)
             self.U = torch.zeros(n_slots, H, M, D, P, device=dev)
             self.Vb = torch.zeros(n_slots, H, M, D, P, device=dev)
-            qw = ops.sketch_width(R, a_v * a_k, b_v * b_k)
+            qw = ops.sketch_width(R, a_v * a_k, b_v * b_k, self.compact_mode)
             self.sketch = gdn3.default_sketch(n_slots * H * M, b_v * b_k, qw, dev)
             self.pos = [0] * n_slots          # tokens each slot has seen
         else:
@@ -136,7 +138,7 @@ class DecodeStateCache:
                                                      factors=self.factors, slow_decay=self.slow_decay,
                                                      compact_every=self.compact_every,
                                                      sketch=G.reshape(Bn * HM, *G.shape[2:]), return_state=True,
-                                                     state0=st0, t0=t0)
+                                                     state0=st0, t0=t0, compact_mode=self.compact_mode)
             for pool, s_new in zip((self.A, self.B, self.U, self.Vb), st):
                 pool.index_copy_(0, idx, s_new.view(Bn, self.H, self.M, *s_new.shape[1:]))
             T = log_g.shape[1]
@@ -169,7 +171,8 @@ class DecodeStateCache:
             with torch.no_grad():
                 y = gdn3.gdn3_decode_step(q, k, v, a_e, a_w, log_g, (self.A, self.B, self.U, self.Vb), pos,
                                           R=self.R, P=self.P, factors=self.factors, slow_decay=self.slow_decay,
-                                          compact_every=self.compact_every, sketch=self.sketch, slots=st)
+                                          compact_every=self.compact_every, sketch=self.sketch, slots=st,
+                                          compact_mode=self.compact_mode)
             for s in host:
                 if 0 <= s < self.n_slots:
                     self.pos[s] += 1

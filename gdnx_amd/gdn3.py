@@ -133,10 +133,10 @@ class _GDN3Chunk(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, bg, wg, dec, sketch, cfg, want_state):
-        M, R, P, factors, slow_decay, Kc = cfg
+        M, R, P, factors, slow_decay, Kc, cmode = cfg
         y, stats, state, tst = ops.gdn3_chunk_fwd(q, k, v, bg, wg, dec, sketch, M=M, R=R, P=P, factors=factors,
                                                   slow_decay=slow_decay, compact_every=Kc,
-                                                  return_state=want_state, save_states=True)
+                                                  return_state=want_state, save_states=True, compact_mode=cmode)
         ctx.save_for_backward(q, k, v, bg, wg, dec, tst)
         ctx.cfg = cfg
         extra = (stats,) + (tuple(state) if want_state else ())
@@ -146,7 +146,7 @@ class _GDN3Chunk(torch.autograd.Function):
     @staticmethod
     def backward(ctx, dy, *unused):
         q, k, v, bg, wg, dec, tst = ctx.saved_tensors
-        M, R, P, factors, _, Kc = ctx.cfg
+        M, R, P, factors, _, Kc, _ = ctx.cfg
         if dy is None:
             return (None,) * 9
         dq, dk, dv, db, dw, ddec = ops.gdn3_chunk_bwd(q, k, v, bg, wg, dec, dy, tst, M=M, R=R, P=P,
@@ -158,7 +158,7 @@ class _GDN3Chunk(torch.autograd.Function):
 
 def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
                          factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None,
-                         sketch=None, return_state=False, state0=None, t0=0):
+                         sketch=None, return_state=False, state0=None, t0=0, compact_mode="svd"):
     """GDN3LinearAttn._gdn3_recurrent_state on the GPU.
 
     Reference: gdn3/gdn3_upgrade.py:403-531 with the semantics of its frozen
@@ -181,7 +181,12 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     previous call returned after t0 tokens (inference only: no gradient flows
     into or through a carried state); two calls over [0, T1) and [T1, T)
     equal one over [0, T).
+
+    compact_mode: the layer's mode (gdn3/gdn3_upgrade.py:579-592): 'svd'
+    (default) or 'sketch' / 'sketch_noqr', one sketched product per
+    compaction with a sketch [N, b_v*b_k, R] and a compaction error of 0.
     """
+    cm = ops.compact_mode_code(compact_mode)
     B, T, H, M = decay_factors.shape
     cdt = torch.bfloat16 if q.dtype == torch.bfloat16 else torch.float32
     D = q.shape[-1]
@@ -219,7 +224,7 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
         bg = chan5(b_gates).float().expand(B, T, H, M, D).contiguous()
         wg = chan5(w_gates).float().expand(B, T, H, M, D).contiguous()
     dec = decay_factors.float().contiguous()
-    qw = ops.sketch_width(R, a_v * a_k, b_v * b_k)
+    qw = ops.sketch_width(R, a_v * a_k, b_v * b_k, cm)
     G = default_sketch(N, b_v * b_k, qw, q.device) if sketch is None else sketch.float().contiguous()
     train = torch.is_grad_enabled() and any(t.requires_grad for t in (q4, k4, v4, bg, wg, dec))
     if train and carried:
@@ -231,15 +236,15 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     if carried:
         y, stats, state = ops.gdn3_chunk_fwd(q4, k4, v4, bg, wg, dec, G, M=M, R=R, P=P, factors=factors,
                                              slow_decay=slow_decay, compact_every=compact_every,
-                                             return_state=return_state, state0=state0, t0=t0)
+                                             return_state=return_state, state0=state0, t0=t0, compact_mode=cm)
     elif train:
-        out = _GDN3Chunk.apply(q4, k4, v4, bg, wg, dec, G, (M, R, P, factors, slow_decay, compact_every),
+        out = _GDN3Chunk.apply(q4, k4, v4, bg, wg, dec, G, (M, R, P, factors, slow_decay, compact_every, cm),
                                return_state)
         y, stats, state = out[0], out[1], (tuple(out[2:]) if return_state else None)
     else:
         y, stats, state = ops.gdn3_chunk_fwd(q4, k4, v4, bg, wg, dec, G, M=M, R=R, P=P, factors=factors,
                                              slow_decay=slow_decay, compact_every=compact_every,
-                                             return_state=return_state)
+                                             return_state=return_state, compact_mode=cm)
     if not return_state:
         return y
     err = (stats[:, :, 0].sum(1) - stats[:, :, 1].sum(1)).clamp(min=0.0).sum()
@@ -253,14 +258,14 @@ class GDN3RecurrentState:
 
     @staticmethod
     def apply(q, k, v, b_gates, w_gates, decay_factors, R=4, P=16, factors=(16, 16, 8, 8),
-              slow_decay=0.97, compact_every=None):
+              slow_decay=0.97, compact_every=None, compact_mode="svd"):
         return gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, R=R, P=P, factors=factors,
-                                    slow_decay=slow_decay, compact_every=compact_every)
+                                    slow_decay=slow_decay, compact_every=compact_every, compact_mode=compact_mode)
 
 
 def gdn3_decode_step(q, k, v, b_gates, w_gates, decay_factors, state, pos, *, R=4, P=16,
                      factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None, sketch=None,
-                     slots=None, return_stats=False):
+                     slots=None, return_stats=False, compact_mode="svd"):
     """One token of the GDN3 recurrence per row, on a carried state updated in
     place: one iteration of the frozen oracle's loop
     (gdn3/_reference_recurrence.py:60-90) with the compaction after tokens
@@ -275,7 +280,9 @@ def gdn3_decode_step(q, k, v, b_gates, w_gates, decay_factors, state, pos, *, R=
     index (int, sequence or int32 tensor [NS]); slots: int32 device tensor
     [NS] of state rows (None: row s is state row s).  The sketch defaults to
     the rows gdn3_recurrent_state draws for the same chains.  Returns y
-    [NS,H,M,V] in the compute dtype (and the compaction statistics [NS,H,M,2])."""
+    [NS,H,M,V] in the compute dtype (and the compaction statistics [NS,H,M,2]).
+    compact_mode as in gdn3_recurrent_state."""
+    cm = ops.compact_mode_code(compact_mode)
     NS, H, M = decay_factors.shape
     D = q.shape[-1]
     dev = q.device
@@ -313,8 +320,8 @@ def gdn3_decode_step(q, k, v, b_gates, w_gates, decay_factors, state, pos, *, R=
         slots = torch.tensor([int(x) for x in slots], dtype=torch.int32)
     if slots is not None:
         slots = slots.to(device=dev, dtype=torch.int32).contiguous()
-    qw = ops.sketch_width(R, a_v * a_k, b_v * b_k)
+    qw = ops.sketch_width(R, a_v * a_k, b_v * b_k, cm)
     G = default_sketch(n_slots * H * M, b_v * b_k, qw, dev) if sketch is None else sketch.float().contiguous()
     return ops.gdn3_decode_step(q3, k3, v3, bg, wg, dec, G, (A, Bf, U, Vb), pos, R=R, P=P, factors=factors,
                                 slow_decay=slow_decay, compact_every=compact_every, slots=slots,
-                                return_stats=return_stats)
+                                return_stats=return_stats, compact_mode=cm)

@@ -444,9 +444,24 @@ def _geom(A, Bk):
     return N, R, a_v, a_k, b_v, b_k
 
 
-def sketch_width(R, m, n):
-    """Columns of the compaction sketch: min(R + 4, m, n) (gdn3/gdn3_upgrade.py:677)."""
-    return min(R + 4, m, n)
+COMPACT_MODES = {"svd": 0, "sketch": 1, "sketch_noqr": 1}
+
+
+def compact_mode_code(mode) -> int:
+    """The ABI's compact_mode for a reference mode name (gdn3/gdn3_upgrade.py:
+    579-592 runs 'sketch' and 'sketch_noqr' through one branch), or an int."""
+    if isinstance(mode, int):
+        _need(mode in (0, 1), f"compact_mode {mode} must be 0 (svd) or 1 (sketch)")
+        return mode
+    key = str(mode).lower()
+    _need(key in COMPACT_MODES, f"compact_mode {mode!r} must be one of {sorted(COMPACT_MODES)}")
+    return COMPACT_MODES[key]
+
+
+def sketch_width(R, m, n, mode=0):
+    """Columns of the compaction sketch: min(R + 4, m, n) for svd
+    (gdn3/gdn3_upgrade.py:677), R for the sketch modes (:580)."""
+    return R if compact_mode_code(mode) == 1 else min(R + 4, m, n)
 
 
 def kron_read(A, Bk, U, Vb, x):
@@ -474,11 +489,14 @@ def kron_read(A, Bk, U, Vb, x):
     return y[:, 0] if squeeze else y
 
 
-def gdn3_compact(A, Bk, U, Vb, sketch, slow_decay=0.97):
+def gdn3_compact(A, Bk, U, Vb, sketch, slow_decay=0.97, compact_mode="svd"):
     """One rearrangement-SVD compaction per chain (gdnx_gdn3_compact).
 
     Returns (A_new, B_new, stats [N,2] float64 = (|R_mat|^2, kept sigma^2));
-    the reference's error is max(0, sum_n stats[:,0] - sum_n stats[:,1])."""
+    the reference's error is max(0, sum_n stats[:,0] - sum_n stats[:,1]).
+    compact_mode 'sketch' / 'sketch_noqr' (sketch [N, b_v*b_k, R]): one
+    sketched product, error 0 (stats = (|R_mat|^2, |R_mat|^2))."""
+    cm = compact_mode_code(compact_mode)
     lib = _lib.load()
     N, R, a_v, a_k, b_v, b_k = _geom(A, Bk)
     D = a_v * b_v
@@ -486,13 +504,13 @@ def gdn3_compact(A, Bk, U, Vb, sketch, slow_decay=0.97):
     for t in (A, Bk, U, Vb, sketch):
         _need(t.is_cuda and t.dtype == torch.float32 and t.is_contiguous(),
               "compaction inputs must be contiguous float32 on the GPU")
-    _need(tuple(sketch.shape) == (N, b_v * b_k, sketch_width(R, a_v * a_k, b_v * b_k)), "bad sketch shape")
+    _need(tuple(sketch.shape) == (N, b_v * b_k, sketch_width(R, a_v * a_k, b_v * b_k, cm)), "bad sketch shape")
     A_new, B_new = torch.empty_like(A), torch.empty_like(Bk)
     stats = torch.empty(N, 2, dtype=torch.float64, device=A.device)
     with torch.cuda.device(A.device):
         rc = lib.gdnx_gdn3_compact(_lib.ptr(A), _lib.ptr(Bk), _lib.ptr(U), _lib.ptr(Vb), _lib.ptr(sketch),
                                    _lib.ptr(A_new), _lib.ptr(B_new), _lib.ptr(stats), N, D, R, P,
-                                   a_v, a_k, b_v, b_k, float(slow_decay), _lib.stream_of(A))
+                                   a_v, a_k, b_v, b_k, float(slow_decay), cm, _lib.stream_of(A))
     _lib.check(rc, "gdnx_gdn3_compact")
     return A_new, B_new, stats
 
@@ -509,7 +527,7 @@ def _g3_state_check(state, N, R, factors, D, P, device):
 
 def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
                    factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None, return_state=False,
-                   save_states=False, state0=None, t0=0):
+                   save_states=False, state0=None, t0=0, compact_mode="svd"):
     """GDN3 recurrence with residual window and compaction (gdnx_gdn3_chunk_fwd).
 
     q, k, v: [B,T,H,D] (shared by the M lanes) or [B,T,H,M,D] (per lane),
@@ -522,8 +540,10 @@ def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
     state0 = (A, B, U, Vb) and t0 continue a sequence (gdnx_gdn3_chunk_fwd_state):
     the call's token t is global token t0 + t (slot (t0 + t) % P, compaction
     after it when (t0 + t + 1) % K_c == 0), from the state a previous call
-    returned; inference only."""
+    returned; inference only.  compact_mode: 'svd' (default) or 'sketch' /
+    'sketch_noqr' (sketch [B*H*M, b_v*b_k, R])."""
     lib = _lib.load()
+    cm = compact_mode_code(compact_mode)
     a_v, a_k, b_v, b_k = factors
     B, T, H = q.shape[:3]
     D = q.shape[-1]
@@ -540,8 +560,9 @@ def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
         _need(t.dtype == torch.float32, "gates, decay and sketch must be float32")
     Kc = P if compact_every is None else int(compact_every)
     N = B * H * M
-    _need(tuple(sketch.shape) == (N, b_v * b_k, sketch_width(R, a_v * a_k, b_v * b_k)) and sketch.is_cuda,
-          "sketch must be [B*H*M, b_v*b_k, min(R+4, a_v*a_k, b_v*b_k)] on the GPU")
+    qw = sketch_width(R, a_v * a_k, b_v * b_k, cm)
+    _need(tuple(sketch.shape) == (N, b_v * b_k, qw) and sketch.is_cuda,
+          f"sketch must be [B*H*M, b_v*b_k, {qw}] on the GPU")
     dt = _lib.dtype_code(q.dtype)
     carried = state0 is not None or t0 != 0
     _need(not (carried and save_states), "a carried state (state0 / t0) is inference only")
@@ -572,13 +593,13 @@ def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
                                                _lib.ptr(w_gates), gate_ch, _lib.ptr(decay), _lib.ptr(sketch), *s0,
                                                int(t0), _lib.ptr(y), *ptrs, _lib.ptr(stats) if n_ev > 0 else None,
                                                _lib.ptr(ws), B, T, H, M, D, R, P, Kc, a_v, a_k, b_v, b_k,
-                                               float(slow_decay), dt, _lib.stream_of(q))
+                                               float(slow_decay), dt, cm, _lib.stream_of(q))
         else:
             rc = lib.gdnx_gdn3_chunk_fwd(_lib.ptr(q), _lib.ptr(k), _lib.ptr(v), lanes, _lib.ptr(b_gates),
                                          _lib.ptr(w_gates), gate_ch, _lib.ptr(decay), _lib.ptr(sketch), _lib.ptr(y),
                                          *ptrs, _lib.ptr(stats) if n_ev > 0 else None, _lib.ptr(ws), _lib.ptr(tst),
                                          B, T, H, M, D, R, P, Kc, a_v, a_k, b_v, b_k, float(slow_decay), dt,
-                                         _lib.stream_of(q))
+                                         cm, _lib.stream_of(q))
     _lib.check(rc, "gdnx_gdn3_chunk_fwd")
     if save_states:
         return y, stats[:n_ev], state, tst
@@ -587,7 +608,7 @@ def gdn3_chunk_fwd(q, k, v, b_gates, w_gates, decay, sketch, *, M, R=4, P=16,
 
 def gdn3_decode_step(q, k, v, b_gates, w_gates, decay, sketch, state, pos, *, R=4, P=16,
                      factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None, slots=None,
-                     return_stats=False, out=None):
+                     return_stats=False, out=None, compact_mode="svd"):
     """One token of the GDN3 Kronecker-residual recurrence per row on a
     carried state (gdnx_gdn3_decode_step), updated in place.
 
@@ -597,8 +618,10 @@ def gdn3_decode_step(q, k, v, b_gates, w_gates, decay, sketch, state, pos, *, R=
     [n_slots*H*M, b_v*b_k, q]; pos int32 device [NS]: each row's global token
     index (slot pos % P; compaction after it when (pos + 1) % K_c == 0);
     slots int32 device [NS] or None.  Returns y [NS,H,M,D] in q's dtype (and
-    the per-chain compaction statistics [NS,H,M,2] float64)."""
+    the per-chain compaction statistics [NS,H,M,2] float64).  compact_mode as
+    in gdn3_chunk_fwd."""
     lib = _lib.load()
+    cm = compact_mode_code(compact_mode)
     a_v, a_k, b_v, b_k = factors
     _need(q.is_cuda and q.dim() in (3, 4) and q.shape == k.shape == v.shape, "q, k, v must be [NS,H,(M,)D] on GPU")
     _need(q.dtype in (torch.bfloat16, torch.float32) and q.dtype == k.dtype == v.dtype, "q, k, v: bf16 or float32")
@@ -616,7 +639,7 @@ def gdn3_decode_step(q, k, v, b_gates, w_gates, decay, sketch, state, pos, *, R=
     N = n_slots * H * M
     _g3_state_check([t.view(N, *t.shape[3:]) for t in state], N, R, factors, D, P, q.device)
     _need(tuple(A.shape[:3]) == (n_slots, H, M), "state leading dims must be [n_slots, H, M]")
-    _need(tuple(sketch.shape) == (N, b_v * b_k, sketch_width(R, a_v * a_k, b_v * b_k)), "bad sketch shape")
+    _need(tuple(sketch.shape) == (N, b_v * b_k, sketch_width(R, a_v * a_k, b_v * b_k, cm)), "bad sketch shape")
     _need(pos.dtype == torch.int32 and tuple(pos.shape) == (NS,), "pos must be an int32 tensor [NS]")
     if slots is not None:
         _need(slots.dtype == torch.int32 and tuple(slots.shape) == (NS,), "slots must be an int32 tensor [NS]")
@@ -632,7 +655,7 @@ def gdn3_decode_step(q, k, v, b_gates, w_gates, decay, sketch, state, pos, *, R=
                                        _lib.ptr(w_gates), gate_ch, _lib.ptr(decay), _lib.ptr(sketch),
                                        *(_lib.ptr(t) for t in state), _lib.ptr(slots), _lib.ptr(pos), _lib.ptr(y),
                                        _lib.ptr(stats), NS, n_slots, H, M, D, R, P, Kc, a_v, a_k, b_v, b_k,
-                                       float(slow_decay), _lib.dtype_code(q.dtype), _lib.stream_of(q))
+                                       float(slow_decay), _lib.dtype_code(q.dtype), cm, _lib.stream_of(q))
     _lib.check(rc, "gdnx_gdn3_decode_step")
     return (y, stats) if return_stats else y
 

@@ -21,16 +21,17 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 8
+#define GDNX_ABI_VERSION 9
 
-enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1 };
+enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1, GDNX_DTYPE_F64 = 2 /* gdnx_check_finite only */ };
 
 enum {
   GDNX_OK = 0,
   GDNX_ERR_ARG = -1,       /* null / misaligned pointer, bad enum */
   GDNX_ERR_SHAPE = -2,     /* unsupported or inconsistent sizes */
   GDNX_ERR_WORKSPACE = -3, /* workspace missing or too small */
-  GDNX_ERR_HIP = -4        /* HIP launch or runtime error */
+  GDNX_ERR_HIP = -4,       /* HIP launch or runtime error */
+  GDNX_ERR_NONFINITE = -5  /* NaN or infinity in the outputs (checking on) */
 };
 
 /* Version of this ABI (GDNX_ABI_VERSION). */
@@ -38,6 +39,19 @@ int gdnx_abi_version(void);
 
 /* Message of the last error on the calling thread ("" if none). */
 const char* gdnx_last_error(void);
+
+/* Non-finite checking, the counterpart of the reference trainer's NaN/inf
+ * guard (train/train_gdn3_distill.py:329-354), which drops a step whose loss
+ * or gradient norm is not finite.  Off by default.  When on (process-wide),
+ * the recurrence entry points (delta, per-channel, GDN3 and RLS forwards and
+ * backwards, the decode steps) scan the outputs they wrote, synchronise their
+ * stream and return GDNX_ERR_NONFINITE if any is NaN or infinite.  Returns
+ * the previous setting. */
+int gdnx_set_check_finite(int on);
+
+/* Scans x[0, n) (GDNX_DTYPE_F32, _BF16 or _F64) on the stream and waits for
+ * it: GDNX_OK if every element is finite, else GDNX_ERR_NONFINITE. */
+int gdnx_check_finite(const void* x, long long n, int dtype, void* stream);
 
 /* Default chunk length (tokens) of the forward for head_dim / dtype
  * (64 for bf16, 32 for float32). */
@@ -250,7 +264,12 @@ int gdnx_gdn3_num_compactions(int T, int P, int compact_every);
  *   b_gates, w_gates [B, T, H, M, gate_channels] float32 (gate_channels 1:
  *                a scalar gate per lane; head_dim: per channel)
  *   decay        [B, T, H, M] float32 multiplicative decay
- *   sketch       [B*H*M, b_v*b_k, min(R+4, a_v*a_k, b_v*b_k)] float32
+ *   sketch       [B*H*M, b_v*b_k, q] float32, q = min(R+4, a_v*a_k, b_v*b_k)
+ *                for compact_mode 0, q = R for compact_mode 1
+ *   compact_mode 0: 'svd' (randomized range finder + SVD, the default of
+ *                gdn3/gdn3_upgrade.py:81); 1: 'sketch' / 'sketch_noqr' (the
+ *                two names run one branch, :579-592): R_mat G column-normalised
+ *                to Q, Bm = Q^T R_mat row-normalised; reports no error
  *   y            [B, T, H, M, D] io dtype
  *   A_out, B_out, U_out, Vb_out  final state in the layouts above (each
  *                may be NULL), for any T: U / Vb slot t mod P holds the write
@@ -272,7 +291,7 @@ int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, int qkv_lan
                         float* B_out, float* U_out, float* Vb_out, double* comp_stats,
                         void* workspace, void* train_states, int B, int T, int H, int M,
                         int head_dim, int R, int P, int compact_every, int a_v, int a_k, int b_v,
-                        int b_k, float slow_decay, int dtype, void* stream);
+                        int b_k, float slow_decay, int dtype, int compact_mode, void* stream);
 
 /* Number of compactions a call over global tokens [t0, t0 + T) runs (rows
  * of its comp_stats): those after tokens t with (t + 1) % compact_every == 0;
@@ -299,7 +318,7 @@ int gdnx_gdn3_chunk_fwd_state(const void* q, const void* k, const void* v, int q
                               float* B_out, float* U_out, float* Vb_out, double* comp_stats,
                               void* workspace, int B, int T, int H, int M, int head_dim, int R, int P,
                               int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
-                              int dtype, void* stream);
+                              int dtype, int compact_mode, void* stream);
 
 /* gdnx_gdn3_chunk_fwd_state without a workspace argument: it allocates
  * nothing and takes no caller memory beyond inputs and outputs.  No
@@ -320,7 +339,7 @@ int gdnx_gdn3_chunk_fwd_state_noalloc(const void* q, const void* k, const void* 
                                       float* A_out, float* B_out, float* U_out, float* Vb_out,
                                       double* comp_stats, int B, int T, int H, int M, int head_dim, int R,
                                       int P, int compact_every, int a_v, int a_k, int b_v, int b_k,
-                                      float slow_decay, int dtype, void* stream);
+                                      float slow_decay, int dtype, int compact_mode, void* stream);
 
 /* One-token GDN3 decode step on a carried Kronecker-residual state, updated
  * in place.  One iteration of the frozen oracle's token loop
@@ -348,7 +367,7 @@ int gdnx_gdn3_decode_step(const void* q, const void* k, const void* v, int qkv_l
                           float* Vb, const int* slots, const int* pos, void* y, double* comp_stats,
                           int NS, int n_slots, int H, int M, int head_dim, int R, int P,
                           int compact_every, int a_v, int a_k, int b_v, int b_k, float slow_decay,
-                          int dtype, void* stream);
+                          int dtype, int compact_mode, void* stream);
 
 /* Bytes of the gdnx_gdn3_chunk_fwd training stash; -1 if invalid. */
 long long gdnx_gdn3_train_states_bytes(int B, int T, int H, int M, int head_dim, int P,
@@ -382,12 +401,13 @@ int gdnx_gdn3_chunk_bwd(const void* q, const void* k, const void* v, int qkv_lan
  * Signs: each (u_r, v_r) is flipped so that the largest-magnitude entry of
  * v_r is positive (first index on ties); the reference keeps whatever its
  * SVD backend returns.  A, Bf, U, Vb as in the state layout above; sketch
- * [N, b_v*b_k, q]; comp_stats [N, 2] (|R_mat|^2, kept) or NULL.  U and Vb
+ * [N, b_v*b_k, q] (q as in gdnx_gdn3_chunk_fwd); comp_stats [N, 2]
+ * (|R_mat|^2, kept; kept = |R_mat|^2 for compact_mode 1) or NULL.  U and Vb
  * are left unchanged (as the reference does). */
 int gdnx_gdn3_compact(const float* A, const float* Bf, const float* U, const float* Vb,
                       const float* sketch, float* A_out, float* B_out, double* comp_stats, int N,
                       int head_dim, int R, int P, int a_v, int a_k, int b_v, int b_k,
-                      float slow_decay, void* stream);
+                      float slow_decay, int compact_mode, void* stream);
 
 /* Read of the Kronecker-residual state, y = S x for C vectors per chain:
  * vec(sum_r A_r X B_r^T) + U (Vb^T x), X = x viewed as [a_k, b_k].  Replaces

@@ -42,7 +42,7 @@ import torch
 
 from .delta import stable_alpha
 
-__all__ = ["kron_read", "reference_sketch", "compact", "gdn3_recurrence"]
+__all__ = ["kron_read", "reference_sketch", "sketch_width", "compact", "compact_sketch", "gdn3_recurrence"]
 
 
 def kron_read(A, Bk, U, Vb, x):
@@ -78,12 +78,13 @@ def _canonical_signs(Us, Vs):
     return Us * sgn, Vs * sgn
 
 
-def compact(A, Bk, U, Vb, slow_decay, sketch, sign_mode="lapack"):
-    """Rearrangement-SVD compaction with two-timescale blend.
+def sketch_width(R, m, n, mode="svd"):
+    """Columns of the compaction sketch: min(R + 4, m, n) for 'svd'
+    (gdn3/gdn3_upgrade.py:677), R for 'sketch' / 'sketch_noqr' (:580)."""
+    return R if mode in ("sketch", "sketch_noqr") else min(R + 4, m, n)
 
-    Restates gdn3/gdn3_upgrade.py:650-719.  Returns (A_new, B_new, err); the
-    residual buffer U, Vb is left unchanged by the reference (:719).
-    """
+
+def _rearranged(A, Bk, U, Vb):
     N, R, a_v, a_k = A.shape
     b_v, b_k = Bk.shape[-2:]
     vecA = A.reshape(N, R, a_v * a_k)
@@ -92,7 +93,44 @@ def compact(A, Bk, U, Vb, slow_decay, sketch, sign_mode="lapack"):
     Sres = torch.einsum("nvp,nkp->nvk", U, Vb)
     Sres = (Sres.reshape(N, a_v, b_v, a_k, b_k).permute(0, 1, 3, 2, 4)
             .reshape(N, a_v * a_k, b_v * b_k))
-    Rm = Rm + Sres
+    return Rm + Sres
+
+
+def compact_sketch(A, Bk, U, Vb, slow_decay, sketch):
+    """The 'sketch' and 'sketch_noqr' compaction modes (one branch in the
+    reference, gdn3/gdn3_upgrade.py:579-592): no range finder, no SVD.  With
+    the sketch G [N, n, R]: Y = R_mat G; Q = Y with unit columns (norms
+    clamped at 1e-12); Bm = Q^T R_mat; A_svd_r = |Bm_r| Q_r,
+    B_svd_r = Bm_r / |Bm_r|; the blend as in ``compact``; error 0."""
+    N, R, a_v, a_k = A.shape
+    b_v, b_k = Bk.shape[-2:]
+    Rm = _rearranged(A, Bk, U, Vb)
+    G = sketch.to(Rm.dtype)
+    assert G.shape == (N, b_v * b_k, R), (G.shape, (N, b_v * b_k, R))
+    Y = Rm @ G
+    Q = Y / Y.square().sum(1).sqrt().clamp_min(1e-12)[:, None, :]
+    Bm = Q.transpose(-2, -1) @ Rm
+    b_scale = Bm.square().sum(-1).sqrt().clamp_min(1e-12)
+    A_svd = (Q * b_scale[:, None, :]).permute(0, 2, 1).reshape(N, R, a_v, a_k)
+    B_svd = (Bm / b_scale[:, :, None]).reshape(N, R, b_v, b_k)
+    s = slow_decay
+    return s * A + (1 - s) * A_svd, s * Bk + (1 - s) * B_svd, torch.zeros((), dtype=Rm.dtype)
+
+
+def compact(A, Bk, U, Vb, slow_decay, sketch, sign_mode="lapack", mode="svd"):
+    """Rearrangement-SVD compaction with two-timescale blend.
+
+    Restates gdn3/gdn3_upgrade.py:650-719.  Returns (A_new, B_new, err); the
+    residual buffer U, Vb is left unchanged by the reference (:719).  mode
+    'sketch' / 'sketch_noqr' runs ``compact_sketch`` instead.
+    """
+    if mode in ("sketch", "sketch_noqr"):
+        return compact_sketch(A, Bk, U, Vb, slow_decay, sketch)
+    if mode != "svd":
+        raise ValueError(f"unknown compaction mode {mode!r}")
+    N, R, a_v, a_k = A.shape
+    b_v, b_k = Bk.shape[-2:]
+    Rm = _rearranged(A, Bk, U, Vb)
     energy = (Rm ** 2).sum()
     m, n = Rm.shape[-2:]
     qr = min(R + 4, m, n)
@@ -121,7 +159,7 @@ def compact(A, Bk, U, Vb, slow_decay, sketch, sign_mode="lapack"):
 def gdn3_recurrence(q, k, v, b_gates, w_gates, dec, *, R=4, P=16,
                     factors=(16, 16, 8, 8), slow_decay=0.97, compact_every=None,
                     sketch=None, sign_mode="lapack", dtype=torch.float64,
-                    return_state=False, state0=None, t0=0):
+                    return_state=False, state0=None, t0=0, compact_mode="svd"):
     """Sequential GDN3 recurrence, ``reference_recurrent_state`` generalised.
 
     Restates gdn3/_reference_recurrence.py:33-94.  q,k,b_gates [B,T,H,M,K],
@@ -152,7 +190,7 @@ def gdn3_recurrence(q, k, v, b_gates, w_gates, dec, *, R=4, P=16,
     qf, kf, vf = flat(q, K), flat(k, K), flat(v, V)
     bg, wg = flat(b_gates, K), flat(w_gates, V)
     dc = dec.permute(1, 0, 2, 3).reshape(T, N).to(dtype)
-    qrank = min(R + 4, a_v * a_k, b_v * b_k)
+    qrank = sketch_width(R, a_v * a_k, b_v * b_k, compact_mode)
     G = reference_sketch(N, b_v * b_k, qrank) if sketch is None else sketch
 
     if state0 is None:
@@ -185,7 +223,7 @@ def gdn3_recurrence(q, k, v, b_gates, w_gates, dec, *, R=4, P=16,
         if (t + 1) % Kc == 0:
             with torch.no_grad():
                 A, Bk, err = compact(A.detach(), Bk.detach(), U, Vb, slow_decay, G,
-                                     sign_mode)
+                                     sign_mode, mode=compact_mode)
             err_total = err_total + err
     Y = torch.stack(ys, 0).reshape(T, B, H, M, V).permute(1, 0, 2, 3, 4)
     if return_state:

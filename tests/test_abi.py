@@ -139,12 +139,12 @@ def test_gdn3_compaction_count_from_a_start_position():
     assert lib.gdnx_gdn3_num_compactions(64, 16, 32) == f(0, 64, 16, 32)
 
 
-def _g3_state_fwd(lib, A0=16, B0=16, U0=16, Vb0=16, t0=0, D=128, P=16, Kc=16, ws=16):
+def _g3_state_fwd(lib, A0=16, B0=16, U0=16, Vb0=16, t0=0, D=128, P=16, Kc=16, ws=16, mode=0):
     vp = lambda x: None if x is None else ctypes.c_void_p(x)
     return lib.gdnx_gdn3_chunk_fwd_state(vp(16), vp(16), vp(16), 1, vp(16), vp(16), 1, vp(16), vp(16),
                                          vp(A0), vp(B0), vp(U0), vp(Vb0), t0, vp(16), None, None, None, None, None,
                                          vp(ws), 1, 8, 1, 1, D, 4, P, Kc, 16 if D == 128 else 8,
-                                         16 if D == 128 else 8, 8, 8, 0.97, _lib.DTYPE_F32, None)
+                                         16 if D == 128 else 8, 8, 8, 0.97, _lib.DTYPE_F32, mode, None)
 
 
 def test_gdn3_state_forward_rejects_bad_arguments():
@@ -157,13 +157,15 @@ def test_gdn3_state_forward_rejects_bad_arguments():
     assert "P=32" in lib.gdnx_last_error().decode()
     assert _g3_state_fwd(lib, Kc=24) == -2
     assert _g3_state_fwd(lib, ws=None) == -1
+    assert _g3_state_fwd(lib, mode=2) == -1
+    assert "compact_mode" in lib.gdnx_last_error().decode()
 
 
 def _g3_decode(lib, pos=16, A=16, qkv_lanes=1, gate_ch=1, NS=2, slots=None, P=16):
     vp = lambda x: None if x is None else ctypes.c_void_p(x)
     return lib.gdnx_gdn3_decode_step(vp(16), vp(16), vp(16), qkv_lanes, vp(16), vp(16), gate_ch, vp(16), vp(16),
                                      vp(A), vp(16), vp(16), vp(16), vp(slots), vp(pos), vp(16), None, NS, 4, 2, 2,
-                                     128, 4, P, 16, 16, 16, 8, 8, 0.97, _lib.DTYPE_BF16, None)
+                                     128, 4, P, 16, 16, 16, 8, 8, 0.97, _lib.DTYPE_BF16, 0, None)
 
 
 def test_gdn3_decode_step_rejects_bad_arguments():
@@ -227,6 +229,30 @@ def test_noalloc_forward_refuses_before_any_launch():
     rc = lib.gdnx_gdn3_chunk_fwd_state_noalloc(vp(256), vp(256), vp(256), 1, vp(256), vp(256), 1, vp(256), vp(256),
                                                None, None, None, None, 0, vp(256), None, None, None, None, None,
                                                64, 32, 16, 4, 128, 4, 16, 16, 16, 16, 8, 8, 0.97,
-                                               _lib.DTYPE_BF16, None)
+                                               _lib.DTYPE_BF16, 0, None)
     assert rc == -3
     assert "scratch" in lib.gdnx_last_error().decode()
+
+
+def test_hip_and_nonfinite_error_codes():
+    """GDNX_ERR_HIP (-4): a call that passes argument checking fails at its
+    first HIP call when there is no device; the -5 code maps to
+    GdnxNonFinite.  (With a GPU present the launches would run on the fake
+    pointers, so the first half only runs on a machine without one.)"""
+    lib = _lib.load()
+    with pytest.raises(_lib.GdnxNonFinite):
+        _lib.check(_lib.ERR_NONFINITE, "probe")
+    for rc, cls in ((-1, _lib.GdnxError), (-2, _lib.GdnxError), (-3, _lib.GdnxError), (-4, _lib.GdnxError)):
+        with pytest.raises(cls):
+            _lib.check(rc, "probe")
+    assert lib.gdnx_check_finite(ctypes.c_void_p(256), 8, 9, None) == -1
+    assert lib.gdnx_check_finite(None, 8, _lib.DTYPE_F32, None) == -1
+    assert lib.gdnx_check_finite(None, -1, _lib.DTYPE_F32, None) == -1
+    prev = lib.gdnx_set_check_finite(1)
+    assert lib.gdnx_set_check_finite(prev) == 1
+    if torch.cuda.device_count() > 0:
+        pytest.skip("a GPU is present: the no-device half of this test would launch on fake pointers")
+    assert _fwd(lib) == -4
+    assert lib.gdnx_last_error().decode()
+    assert lib.gdnx_check_finite(ctypes.c_void_p(256), 8, _lib.DTYPE_F32, None) == -4
+    assert "device" in lib.gdnx_last_error().decode()

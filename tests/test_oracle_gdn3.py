@@ -178,3 +178,72 @@ def test_carried_state_split_equals_whole_run(P, Kc, splits):
     for x1, x2 in zip(s, st):
         assert torch.allclose(x1, x2, rtol=0, atol=1e-12)
     assert abs(e_tot - err.item()) <= 1e-9 * max(1.0, err.item())
+
+
+def _rearrange_loops(S, a_v, a_k, b_v, b_k):
+    """R_mat[(i, j), (k, l)] = S[i*b_v + k, j*b_k + l], by explicit loops (the
+    Van Loan-Pitsianis rearrangement: sum_r kron(A_r, B_r) <-> sum_r vec(A_r) vec(B_r)^T)."""
+    Rm = torch.empty(a_v * a_k, b_v * b_k, dtype=S.dtype)
+    for i in range(a_v):
+        for j in range(a_k):
+            for kk in range(b_v):
+                for ll in range(b_k):
+                    Rm[i * a_k + j, kk * b_k + ll] = S[i * b_v + kk, j * b_k + ll]
+    return Rm
+
+
+def test_compact_sketch_closed_form():
+    """slow_decay 0: the new Kronecker sum is Q Q^T R_mat, Q = the columns of
+    R_mat G normalised to unit length; B rows have unit norm; error 0; the
+    blend is linear in slow_decay."""
+    gen = torch.Generator().manual_seed(5)
+    d = torch.float64
+    N, R, a_v, a_k, b_v, b_k, P = 2, 3, 4, 2, 3, 5, 6
+    A = torch.randn(N, R, a_v, a_k, generator=gen, dtype=d)
+    Bk = torch.randn(N, R, b_v, b_k, generator=gen, dtype=d)
+    U = torch.randn(N, a_v * b_v, P, generator=gen, dtype=d)
+    Vb = torch.randn(N, a_k * b_k, P, generator=gen, dtype=d)
+    G = torch.randn(N, b_v * b_k, R, generator=gen, dtype=d)
+    A0, B0, err = gdn3.compact(A, Bk, U, Vb, 0.0, G, mode="sketch")
+    assert err.item() == 0.0
+    S = _kron_sum(A, Bk) + U @ Vb.transpose(1, 2)
+    S_new = _kron_sum(A0, B0)
+    for n in range(N):
+        Rm = _rearrange_loops(S[n], a_v, a_k, b_v, b_k).numpy()
+        Y = Rm @ G[n].numpy()
+        Q = Y / np.linalg.norm(Y, axis=0, keepdims=True)
+        np.testing.assert_allclose(_rearrange_loops(S_new[n], a_v, a_k, b_v, b_k).numpy(), Q @ Q.T @ Rm,
+                                   rtol=1e-10, atol=1e-10)
+    np.testing.assert_allclose(B0.reshape(N, R, -1).norm(dim=-1).numpy(), 1.0, rtol=1e-12)
+    A1, B1, _ = gdn3.compact(A, Bk, U, Vb, 0.9, G, mode="sketch_noqr")
+    torch.testing.assert_close(A1, 0.9 * A + 0.1 * A0, atol=1e-12, rtol=1e-12)
+    torch.testing.assert_close(B1, 0.9 * Bk + 0.1 * B0, atol=1e-12, rtol=1e-12)
+    with pytest.raises(ValueError):
+        gdn3.compact(A, Bk, U, Vb, 0.9, G, mode="qr")
+
+
+def test_compact_sketch_rank_one_known_answers():
+    """A rank-one R_mat = a b^T: one sketch column recovers it exactly; R
+    columns, all parallel to a, give R a b^T (the sketch modes skip the
+    orthogonalisation)."""
+    gen = torch.Generator().manual_seed(9)
+    d = torch.float64
+    a = torch.randn(1, 1, 4, 2, generator=gen, dtype=d)
+    b = torch.randn(1, 1, 3, 5, generator=gen, dtype=d)
+    zU, zV = torch.zeros(1, 12, 4, dtype=d), torch.zeros(1, 10, 4, dtype=d)
+    A1, B1, _ = gdn3.compact(a, b, zU, zV, 0.0, torch.randn(1, 15, 1, generator=gen, dtype=d), mode="sketch")
+    torch.testing.assert_close(_kron_sum(A1, B1), _kron_sum(a, b), atol=1e-12, rtol=1e-12)
+    for R in (2, 3):
+        A = torch.cat([a, torch.zeros(1, R - 1, 4, 2, dtype=d)], 1)
+        Bk = torch.cat([b, torch.zeros(1, R - 1, 3, 5, dtype=d)], 1)
+        A1, B1, _ = gdn3.compact(A, Bk, zU, zV, 0.0, torch.randn(1, 15, R, generator=gen, dtype=d),
+                                 mode="sketch")
+        torch.testing.assert_close(_kron_sum(A1, B1), R * _kron_sum(a, b), atol=1e-12, rtol=1e-12)
+
+
+def test_recurrence_sketch_mode_width():
+    """The recurrence draws a width-R sketch in the sketch modes and a
+    width-min(R+4, m, n) one for svd."""
+    assert gdn3.sketch_width(4, 256, 64, "sketch") == 4
+    assert gdn3.sketch_width(4, 256, 64, "svd") == 8
+    assert gdn3.sketch_width(4, 6, 64, "svd") == 6

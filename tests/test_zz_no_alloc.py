@@ -45,7 +45,7 @@ def _run(lib, noalloc, x, st0, t0, B, T, H, M, D, io, P=16, Kc=32):
     stream = _lib.stream_of(q)
     common = [p(q), p(k), p(v), 1, p(bg), p(wg), 1, p(dec), p(G), *(p(t) for t in st0), t0, p(y),
               *(p(t) for t in out), p(stats)]
-    dims = [B, T, H, M, D, 4, P, Kc, 16, 16, 8, 8, ctypes.c_float(0.97), dt, stream]
+    dims = [B, T, H, M, D, 4, P, Kc, 16, 16, 8, 8, ctypes.c_float(0.97), dt, 0, stream]
     if noalloc:
         rc = lib.gdnx_gdn3_chunk_fwd_state_noalloc(*common, *dims)
     else:
@@ -82,6 +82,6 @@ def test_noalloc_forward_refuses_beyond_its_scratch(gpu_lib):
     rc = lib.gdnx_gdn3_chunk_fwd_state_noalloc(vp(256), vp(256), vp(256), 1, vp(256), vp(256), 1, vp(256), vp(256),
                                                None, None, None, None, 0, vp(256), None, None, None, None, None,
                                                B, 32, H, M, D, 4, 16, 16, 16, 16, 8, 8, ctypes.c_float(0.97),
-                                               _lib.DTYPE_BF16, None)
+                                               _lib.DTYPE_BF16, 0, None)
     assert rc == -3
     assert "scratch" in lib.gdnx_last_error().decode()
