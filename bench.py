@@ -53,30 +53,40 @@ def flops_bwd_grads(B, T, H, M, D, C):
     return 2 * flops_fwd(B, T, H, M, D, C) - flops_bwd_state(B, T, H, M, D, C)
 
 
-def cpu_baseline(T=2048, H=4, warm_T=64):
+def median_time(fn, runs=3):
+    """CPU baseline timing: one warm-up run of ``fn``
+    at the sample size, then the median wall time of ``runs`` runs."""
+    fn()
+    times = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return sorted(times)[len(times) // 2]
+
+
+def cpu_baseline(T=2048, H=4):
     """Time the CPU oracle (fp32 sequential recurrence + autograd) on
-    B=1, H heads x 4 lanes, T tokens; tokens/s scaled to the 16-head layer."""
+    B=1, H heads x 4 lanes, T tokens (one warm-up, median of 3); tokens/s
+    scaled to the 16-head layer."""
     import torch
     from oracle import delta, inputs
     torch.set_num_threads(os.cpu_count() or 1)
-    out = {}
-    for t_len in (warm_T, T):
-        x = inputs.dense_inputs(1, t_len, H, 128, M=4, seed=1002, decay="tau", rope=True,
-                                with_grad_out=True)
+    x = inputs.dense_inputs(1, T, H, 128, M=4, seed=1002, decay="tau", rope=True, with_grad_out=True)
+
+    def run():
         ins = [x[n].float().requires_grad_(True) for n in ("q", "k", "v", "beta", "g")]
-        t0 = time.perf_counter()
         a = delta.gdn3_dense_coeffs(ins[1], ins[3])
         y, _ = delta.lane_delta(ins[0], ins[1], ins[2], a, a, ins[4], dtype=torch.float32)
         (y * x["dO"].float()).sum().backward()
-        out[t_len] = time.perf_counter() - t0
-    secs = out[T]
+    secs = median_time(run)
     return {
         "value": T * (H / 16.0) / secs,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"oracle.delta.lane_delta fp32 sequential fwd+bwd, B=1 T={T} H={H}x4 lanes "
-                  f"d=128 ({secs:.1f} s), scaled by H/16 to the layer's 16 heads",
+                  f"d=128, one warm-up then median of 3 ({secs:.1f} s), scaled by H/16 to the layer's 16 heads",
     }
 
 
@@ -111,18 +121,20 @@ def cpu_baseline_decode(NS_sample=64, H=16, NC=16, D=128, steps=8):
     q, k, v = (torch.randn(NS_sample, 1, H, D, generator=gen) for _ in range(3))
     a = torch.rand(NS_sample, 1, H, NC, generator=gen)
     lg = torch.full((NS_sample, 1, H, NC), -0.01)
-    delta.lane_delta(q, k, v, a, a, lg, state0=S, dtype=torch.float32)
-    t0 = time.perf_counter()
-    for _ in range(steps):
-        _, S = delta.lane_delta(q, k, v, a, a, lg, state0=S, dtype=torch.float32)
-    secs = (time.perf_counter() - t0) / steps
+    st = {"S": S}
+
+    def run():
+        for _ in range(steps):
+            _, st["S"] = delta.lane_delta(q, k, v, a, a, lg, state0=st["S"], dtype=torch.float32)
+    secs = median_time(run) / steps
     return {
         "value": NS_sample / secs,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"oracle.delta.lane_delta fp32 one-token step, {NS_sample} of the 256 sequences "
-                  f"x {H} heads x {NC} chains d={D}, mean of {steps} steps ({secs * 1e3:.1f} ms/step); "
+                  f"x {H} heads x {NC} chains d={D}, {steps} steps per run, one warm-up run then median of 3 "
+                  f"({secs * 1e3:.1f} ms/step); "
                   f"tokens/s = sequences per step time",
     }
 
@@ -226,22 +238,23 @@ def cpu_baseline_gdn3(T=2048, B=1, H=16, M=4, compact_every=2048, train=False):
     torch.set_num_threads(os.cpu_count() or 1)
     x = inputs.config3(T=T, B=B, H=H, M=M, span=min(4096, T), n_pairs=16)
     D = x["q"].shape[-1]
-    leaves = [x[n].float().requires_grad_(train) for n in ("q", "k", "v", "b", "w", "dec")]
-    t0 = time.perf_counter()
-    args = [t.unsqueeze(3).expand(B, T, H, M, D) for t in leaves[:3]]
-    gates = [t.unsqueeze(-1).expand(B, T, H, M, D) for t in leaves[3:5]]
-    y = og.gdn3_recurrence(*args, *gates, leaves[5], compact_every=compact_every, dtype=torch.float32,
-                           sign_mode="canonical")
-    if train:
-        torch.autograd.grad(y, leaves, torch.ones_like(y))
-    secs = time.perf_counter() - t0
+
+    def run():
+        leaves = [x[n].float().requires_grad_(train) for n in ("q", "k", "v", "b", "w", "dec")]
+        args = [t.unsqueeze(3).expand(B, T, H, M, D) for t in leaves[:3]]
+        gates = [t.unsqueeze(-1).expand(B, T, H, M, D) for t in leaves[3:5]]
+        y = og.gdn3_recurrence(*args, *gates, leaves[5], compact_every=compact_every, dtype=torch.float32,
+                               sign_mode="canonical")
+        if train:
+            torch.autograd.grad(y, leaves, torch.ones_like(y))
+    secs = median_time(run)
     return {
         "value": B * T / secs,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"oracle.gdn3.gdn3_recurrence fp32{' fwd+bwd' if train else ''}, B={B} T={T} H={H}x{M} "
-                  f"lanes d={D}, compaction every {compact_every} ({secs:.1f} s)",
+                  f"lanes d={D}, compaction every {compact_every}, one warm-up then median of 3 ({secs:.1f} s)",
     }
 
 
@@ -370,15 +383,16 @@ def cpu_baseline_kmd2(T=512, B=1, H=16, H_full=16, r_out=4, d=128):
     from oracle import delta
     torch.set_num_threads(os.cpu_count() or 1)
     xs, dy = kmd2_inputs(B, T, H, r_out, d)
-    leaves = [x.requires_grad_(True) for x in xs]
-    t0 = time.perf_counter()
-    y = delta.kmd2_scan(*leaves, dtype=torch.float32)
-    torch.autograd.grad(y, leaves, dy)
-    secs = time.perf_counter() - t0
+
+    def run():
+        leaves = [x.detach().requires_grad_(True) for x in xs]
+        y = delta.kmd2_scan(*leaves, dtype=torch.float32)
+        torch.autograd.grad(y, leaves, dy)
+    secs = median_time(run)
     return {"value": B * T / secs * H / H_full, "unit": "tokens/s", "cores": torch.get_num_threads(),
             "kind": "port",
             "sample": f"oracle.delta.kmd2_scan fp32 fwd+bwd, B={B} T={T} H={H} r_out={r_out} d={d} "
-                      f"({secs:.1f} s), scaled to H={H_full}"}
+                      f"(one warm-up then median of 3: {secs:.1f} s), scaled to H={H_full}"}
 
 
 def bench_kmd2(args):
@@ -508,23 +522,25 @@ def cpu_baseline_boundary(T=4096, B=2, H=16, M=4, K=128, V=128):
     xs = boundary_inputs(B, T, H, M, K, V, seed=32)
     rates = torch.tensor([0.05, 0.02, 0.005, 0.001])
     names = ("q", "k", "b_proj", "proj_a", "w_proj", "proj_b", "decay_proj")
-    t0 = time.perf_counter()
-    leaves = [xs[n].double().requires_grad_(True) for n in names]
-    outs = gl.prologue(*leaves, rates, 0.999)
-    torch.autograd.grad(outs, leaves, [torch.ones_like(o) for o in outs])
-    el = [xs[n].double().requires_grad_(True) for n in ("y", "router_logits", "norm")]
-    out = gl.epilogue(*el)
-    torch.autograd.grad(out, el, xs["d_out"].double())
-    sec = time.perf_counter() - t0
+
+    def run():
+        leaves = [xs[n].double().requires_grad_(True) for n in names]
+        outs = gl.prologue(*leaves, rates, 0.999)
+        torch.autograd.grad(outs, leaves, [torch.ones_like(o) for o in outs])
+        el = [xs[n].double().requires_grad_(True) for n in ("y", "router_logits", "norm")]
+        out = gl.epilogue(*el)
+        torch.autograd.grad(out, el, xs["d_out"].double())
+    sec = median_time(run)
     return {"value": B * T / sec, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"oracle prologue+epilogue fwd+bwd, float64 autograd, B={B} T={T} H={H} M={M} K=V={K} "
-                      f"({B * T * H} rows), {sec:.2f} s"}
+                      f"({B * T * H} rows), one warm-up then median of 3: {sec:.2f} s"}
 
 
 def torch_eager_boundary(xs, rates, clamp, K, V):
-    """The reference's own element-wise ops (gdn3/gdn3_upgrade.py:796-851,
-    _apply_partial_rope with its clone and in-place slices) in torch eager on
-    the GPU, forward + backward: what the fused kernels replace."""
+    """A torch-eager restatement (this repository's code) of the reference's
+    element-wise boundary ops (gdn3/gdn3_upgrade.py:796-851, with
+    _apply_partial_rope's clone and in-place slices) on the GPU, forward +
+    backward: the op sequence the fused kernels replace, timed as a comparator."""
     import math
     import torch
     import torch.nn.functional as F
@@ -670,18 +686,20 @@ def cpu_baseline_rls(T=1024, B=1, H=16, r=1, r_out=1, dk=64, dv=64):
     from oracle import rls as orls
     torch.set_num_threads(os.cpu_count() or 1)
     xs, dy = rls_inputs(B, T, H, r, r_out, dk, dv, seed=42)
-    t0 = time.perf_counter()
-    leaves = [x.double().requires_grad_(True) for x in xs]
-    y = orls.rls_scan(*leaves)
-    torch.autograd.grad(y, leaves, dy.double())
-    sec = time.perf_counter() - t0
+
+    def run():
+        leaves = [x.double().requires_grad_(True) for x in xs]
+        y = orls.rls_scan(*leaves)
+        torch.autograd.grad(y, leaves, dy.double())
+    sec = median_time(run)
     return {"value": B * T / sec, "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
-            "sample": f"oracle rls_scan fwd+bwd, float64 autograd, B={B} T={T} H={H} r={r} dk=dv={dk}, {sec:.2f} s"}
+            "sample": f"oracle rls_scan fwd+bwd, float64 autograd, B={B} T={T} H={H} r={r} dk=dv={dk}, one warm-up then median of 3: {sec:.2f} s"}
 
 
 def torch_eager_rls(xs, eps):
-    """The reference's own per-token torch loop (KMD2LinearAttn._scan's r = 1
-    path, gdn3/kmd2.py:193-200) on the GPU, forward + backward."""
+    """A torch-eager restatement (this repository's code) of the reference's
+    per-token loop (KMD2LinearAttn._scan's r = 1 path, gdn3/kmd2.py:193-200)
+    on the GPU, forward + backward, timed as a comparator."""
     import torch
     q, K, V, Bg, Wg, a = xs
     B, T, H, _, dk = q.shape
