@@ -83,6 +83,19 @@ def test_bf16_gradients(gpu_lib, D, T):
     _check(vals, dO, 1e-2)
 
 
+@pytest.mark.parametrize("T", [31, 64, 97, 330])
+def test_bf16_state_gradients_ragged(gpu_lib, T):
+    """bf16 at head dim 128 (the training configuration): a single partial
+    chunk, whole chunks and ragged tails, with initial and final state
+    gradients."""
+    print(f"case: bf16 state grads T={T}", flush=True)
+    vals, dO = _case(1, T, 3, 128, 4, seed=24, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(25)
+    s0 = torch.randn(1, 3, 4, 128, 128, generator=gen) * 0.05
+    ds = torch.randn(1, 3, 4, 128, 128, generator=gen) * 0.1
+    _check(vals, dO, 1e-2, state0=s0, dstate=ds)
+
+
 def test_state_gradients_fp32(gpu_lib):
     print("case: state0/dstate grads", flush=True)
     vals, dO = _case(1, 70, 2, 64, 2, seed=23, dtype=torch.float32)

@@ -140,9 +140,12 @@ def test_two_pass_equals_single_pass(gpu_lib, dtype, chunk):
     assert torch.equal(y1, y3) and torch.equal(s1, s3)
     # states and net writes (compute dtype) agree to rounding; the chunk
     # operands come from the same prep kernel on both paths: bitwise equal
-    es = 4 if dtype == torch.float32 else 2
-    nrec = 2 * 3 * 4 * ((200 + chunk - 1) // chunk)
-    nst = nrec * (128 * 128 + chunk * 128) * es
+    # the stash precedes the chunk operands: its size is the whole buffer's
+    # less the operand records' (bf16 C = 32 keeps one record per chunk pair)
+    lib = gpu_lib
+    code = 1 if dtype == torch.bfloat16 else 0
+    nst = (lib.gdnx_delta_chunk_states_bytes(2, 200, 3, 4, 128, chunk, code)
+           - lib.gdnx_delta_fwd_workspace_bytes(2, 200, 3, 4, 128, chunk, code))
     ct = torch.float32 if dtype == torch.float32 else torch.bfloat16
     assert rel_l2(c1[:nst].view(ct).float(), c2[:nst].view(ct).float()) <= tol
     assert torch.equal(c1[nst:], c2[nst:])
