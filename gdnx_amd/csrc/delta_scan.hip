@@ -42,24 +42,38 @@ struct ScanDims {
 // ---------------------------------------------------------------------------
 // forward
 // ---------------------------------------------------------------------------
+// Staging is double-buffered by chunk parity: chunk c + 1's tiles are
+// committed into the other buffer while chunk c computes, so a chunk step
+// needs one workgroup barrier.  The net writes are formed per wave as
+//   R = T (diag(a_w) V - diag(aeg) (K S0))
+// on the wave's own value columns (K S0 contracts over the keys, which the
+// wave's state columns hold whole), so no product is shared between waves.
+template <typename CT, int D, int C, int NWV>
+struct alignas(16) ScanFwdBuf {
+  typedef ScanDims<CT, D, C, NWV> Sd;
+  CT q[C * Sd::LDD];        // Q rows
+  CT k[C * Sd::LDD];        // K rows
+  CT kt[D * Sd::LDC];       // K^T
+  CT vt[Sd::BV * Sd::LDC];  // V^T of this workgroup's value columns
+  CT t[C * Sd::LDC];        // T rows
+  CT aq[C * Sd::LDC];       // Aq rows
+  float sc[kNumSc * C];     // gam, dec, aeg, a_w
+};
+// two staging buffers where they fit in LDS (one at 64-token chunks, with a
+// second barrier before each commit)
 template <typename CT, int D, int C, int NWV>
 struct alignas(16) ScanFwdSmem {
-  typedef ScanDims<CT, D, C, NWV> Sd;
-  CT q[C * Sd::LDD];     // Q rows
-  CT kt[D * Sd::LDC];    // K^T
-  CT vt[Sd::BV * Sd::LDC];  // V^T of this workgroup's value columns
-  CT t[C * Sd::LDC];     // T rows
-  CT aq[C * Sd::LDC];    // Aq rows
-  CT wm[C * Sd::LDD];    // -Wm rows
-  float sc[kNumSc * C];  // gam, dec, aeg, a_w
+  static constexpr int NBUF = 2 * sizeof(ScanFwdBuf<CT, D, C, NWV>) <= 160 * 1024 ? 2 : 1;
+  ScanFwdBuf<CT, D, C, NWV> buf[NBUF];
 };
 
 template <typename CT, int D, int C, int NWV, bool STASH>
 __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) delta_scan_fwd_kernel(DeltaArgs p) {
   typedef ScanDims<CT, D, C, NWV> Sd;
   typedef typename Sd::Frag Frag;
+  typedef typename Vec4T<CT>::type V4;
   constexpr int KS = Sd::KS, TPS = Sd::TPS, NDT = Sd::NDT, NCT = Sd::NCT, NT = Sd::NT;
-  constexpr int LDD = Sd::LDD, LDC = Sd::LDC, BV = Sd::BV, DTW = Sd::DTW;
+  constexpr int LDD = Sd::LDD, LDC = Sd::LDC, BV = Sd::BV;
   __shared__ ScanFwdSmem<CT, D, C, NWV> sm;
 
   const int tid = threadIdx.x;
@@ -90,11 +104,12 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
   }
   __builtin_amdgcn_s_waitcnt(0);   // initial state in registers before the loop's own loads
 
-  // Chunk tiles are fetched a chunk ahead: q by every thread, and K, V, T,
-  // Aq (with the scalars) each by one group of NWV/4 waves, so every 16-byte
-  // unit is loaded once.  Memory operations are unconditional within a
-  // group (tail tokens go through buffer resources), so the compiler's wait
-  // for the prefetched loads never covers the stores issued after them.
+  // Chunk tiles are fetched into registers two chunks ahead of their use:
+  // q by every thread, and K, V, T, Aq (with the scalars) each by one group
+  // of NWV/4 waves, so every 16-byte unit is loaded once.  Memory operations
+  // are unconditional within a group (tail tokens go through buffer
+  // resources), so the compiler's wait for the prefetched loads never covers
+  // the stores issued after them.
   constexpr int GW = NWV / 4, GT = 64 * GW;
   static_assert(NWV % 4 == 0, "four load groups");
   const int grp = wave / GW, gt = tid - grp * GT;
@@ -120,69 +135,37 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
       pa.fetch_dense(pp.aq + rec_index(chain, c, nchains) * C * C, gt);
     }
   };
+  constexpr int NBUF = ScanFwdSmem<CT, D, C, NWV>::NBUF;
+  auto commit = [&](ScanFwdBuf<CT, D, C, NWV>& B) {
+    pq.template commit_nat<LDD>(B.q, tid);
+    if (grp == 0) {
+      pk.template commit_nat<LDD>(B.k, gt);
+      pk.template commit_tr<LDC>(B.kt, gt);
+    } else if (grp == 1) {
+      pv.template commit_tr<LDC>(B.vt, gt);
+    } else if (grp == 2) {
+      pt.template commit_nat<LDC>(B.t, gt);
+      ps.commit(B.sc, gt);
+    } else {
+      pa.template commit_nat<LDC>(B.aq, gt);
+    }
+  };
   fetch(0);
+  __builtin_amdgcn_s_waitcnt(0);
+  commit(sm.buf[0]);
+  fetch(min(1, NC - 1));
   __builtin_amdgcn_s_waitcnt(0);   // the loop's waits then only track its own loads and stores
+  __syncthreads();
 
   for (int c = 0; c < NC; ++c) {
     const int t0 = c * C;
     const size_t rec = rec_index(chain, c, nchains);
-    __syncthreads();
-    pq.template commit_nat<LDD>(sm.q, tid);
-    if (grp == 0) {
-      pk.template commit_tr<LDC>(sm.kt, gt);
-    } else if (grp == 1) {
-      pv.template commit_tr<LDC>(sm.vt, gt);
-    } else if (grp == 2) {
-      pt.template commit_nat<LDC>(sm.t, gt);
-      ps.commit(sm.sc, gt);
-    } else {
-      pa.template commit_nat<LDC>(sm.aq, gt);
-    }
-    __syncthreads();
-    fetch(min(c + 1, NC - 1));   // (the last iteration refetches its own chunk, unused)
-    const float* gam = &sm.sc[kScGam * C];
-    const float* dec = &sm.sc[kScDec * C];
-    const float* aeg = &sm.sc[kScAeg * C];
-    const float* aw = &sm.sc[kScAw * C];
+    const auto& B = sm.buf[c % NBUF];
+    const float* gam = &B.sc[kScGam * C];
+    const float* dec = &B.sc[kScDec * C];
+    const float* aeg = &B.sc[kScAeg * C];
+    const float* aw = &B.sc[kScAw * C];
 
-    // ---- -Wm (rows i, key cols d) via Wm^T = K^T (T diag(aeg))^T; this wave's key tiles ----
-    {
-      Frag bt[NCT][C / KS];
-#pragma unroll
-      for (int it = 0; it < NCT; ++it)
-#pragma unroll
-        for (int kb = 0; kb < C / KS; ++kb)
-          bt[it][kb] = frag_scale(ld_frag(&sm.t[(it * 16 + n16) * LDC + kb * KS], g4), aeg + kb * KS, g4);
-#pragma unroll
-      for (int dd = 0; dd < DTW; ++dd) {
-        const int dt = dd * NWV + wave;
-        Frag a[C / KS];
-#pragma unroll
-        for (int kb = 0; kb < C / KS; ++kb) a[kb] = ld_frag(&sm.kt[(dt * 16 + n16) * LDC + kb * KS], g4);
-#pragma unroll
-        for (int it = 0; it < NCT; ++it) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int kb = 0; kb < C / KS; ++kb) mma(acc, a[kb], bt[it][kb]);
-          // acc[ii] = Wm[i = 16 it + n][d = 16 dt + 4 g + ii]
-          st4(&sm.wm[(it * 16 + n16) * LDD + dt * 16 + 4 * g4], -acc[0], -acc[1], -acc[2], -acc[3]);
-        }
-      }
-    }
-    // ---- U = T diag(a_w) V on this wave's columns, into the R accumulators ----
-    f32x4 Racc[NCT];
-    {
-      Frag bv[C / KS];
-#pragma unroll
-      for (int kb = 0; kb < C / KS; ++kb) bv[kb] = ld_frag(&sm.vt[(wave * 16 + n16) * LDC + kb * KS], g4);
-#pragma unroll
-      for (int it = 0; it < NCT; ++it) {
-        Racc[it] = zero4();
-#pragma unroll
-        for (int kb = 0; kb < C / KS; ++kb)
-          mma(Racc[it], frag_scale(ld_frag(&sm.t[(it * 16 + n16) * LDC + kb * KS], g4), aw + kb * KS, g4), bv[kb]);
-      }
-    }
     // ---- S0 as fragments over k = d; stash for the backward ----
     Frag Sf[NDT / TPS];
 #pragma unroll
@@ -193,42 +176,36 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
       for (int dt = 0; dt < NDT; ++dt)
         st4(cst + stash_tile_offset<CT, D>(dt, V, lane), S[dt][0], S[dt][1], S[dt][2], S[dt][3]);
     }
-    __syncthreads();   // -Wm complete
 
-    // ---- R = U - Wm S0 ----
+    // ---- X = diag(a_w) V - diag(aeg) (K S0) on this wave's columns ----
+    f32x4 X[NCT];
 #pragma unroll
-    for (int kb = 0; kb < NDT / TPS; ++kb)
+    for (int it = 0; it < NCT; ++it) {
+      f32x4 acc = zero4();
 #pragma unroll
-      for (int it = 0; it < NCT; ++it) mma(Racc[it], ld_frag(&sm.wm[(it * 16 + n16) * LDD + kb * KS], g4), Sf[kb]);
-    if constexpr (STASH) {
-      CT* rst = (CT*)p.chunk_states + NR * D * D + rec * (C * D);
-#pragma unroll
-      for (int it = 0; it < NCT; ++it)
-        st4(rst + stash_tile_offset<CT, D>(it, V, lane), Racc[it][0], Racc[it][1], Racc[it][2], Racc[it][3]);
+      for (int kb = 0; kb < NDT / TPS; ++kb) mma(acc, ld_frag(&B.k[(it * 16 + n16) * LDD + kb * KS], g4), Sf[kb]);
+      const f32x4 vv = load4(&B.vt[(wave * 16 + n16) * LDC + it * 16 + 4 * g4]);
+      const f32x4 a4 = *(const f32x4*)&aw[it * 16 + 4 * g4];
+      const f32x4 e4 = *(const f32x4*)&aeg[it * 16 + 4 * g4];
+      X[it] = a4 * vv - e4 * acc;
     }
-    // ---- Y = diag(gam) Q S0 + Aq R ----
+    // ---- R = T X ----
+    f32x4 Racc[NCT];
     {
-      Frag Rf[NCT / TPS];
+      Frag Xf[NCT / TPS];
 #pragma unroll
-      for (int kb = 0; kb < NCT / TPS; ++kb) Rf[kb] = acc_frag((CT*)nullptr, Racc[kb * TPS], Racc[kb * TPS + TPS - 1]);
-      // this chain's rows of y in this chunk; rows past T fall outside the resource
-      const __amdgpu_buffer_rsrc_t yr =
-          buf_rsrc((CT*)p.y + (((size_t)(b * p.T + t0) * p.H + h) * p.M + m) * D, (unsigned)min(C, p.T - t0) * ysb);
+      for (int kb = 0; kb < NCT / TPS; ++kb) Xf[kb] = acc_frag((CT*)nullptr, X[kb * TPS], X[kb * TPS + TPS - 1]);
 #pragma unroll
       for (int it = 0; it < NCT; ++it) {
-        f32x4 Y = zero4();
+        Racc[it] = zero4();
 #pragma unroll
-        for (int kb = 0; kb < NDT / TPS; ++kb) mma(Y, ld_frag(&sm.q[(it * 16 + n16) * LDD + kb * KS], g4), Sf[kb]);
-        Y *= *(const f32x4*)&gam[it * 16 + 4 * g4];
-#pragma unroll
-        for (int kb = 0; kb < NCT / TPS; ++kb) mma(Y, ld_frag(&sm.aq[(it * 16 + n16) * LDC + kb * KS], g4), Rf[kb]);
-        // transposed tile: lane (g, n) holds row 16 it + n, columns 4 g .. 4 g + 3
-        const f32x4 yt = tile_transpose((CT*)nullptr, Y, lane);
-        buf_store4(yr, (unsigned)(it * 16 + n16) * ysb + (16 * V + 4 * g4) * sizeof(CT), (const CT*)nullptr, yt[0],
-                   yt[1], yt[2], yt[3]);
+        for (int kb = 0; kb < C / KS; ++kb) mma(Racc[it], ld_frag(&B.t[(it * 16 + n16) * LDC + kb * KS], g4), Xf[kb]);
       }
     }
-    // ---- S = gam_last S0 + K^T diag(dec) R ----
+    // ---- S = gam_last S0 + K^T diag(dec) R (the recurrence first; Y after) ----
+    Frag Rf[NCT / TPS];
+#pragma unroll
+    for (int kb = 0; kb < NCT / TPS; ++kb) Rf[kb] = acc_frag((CT*)nullptr, Racc[kb * TPS], Racc[kb * TPS + TPS - 1]);
     {
       const float gl = gam[C - 1];
       Frag RDf[NCT / TPS];
@@ -242,9 +219,39 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
       for (int dt = 0; dt < NDT; ++dt) {
         S[dt] *= gl;
 #pragma unroll
-        for (int kb = 0; kb < NCT / TPS; ++kb) mma(S[dt], ld_frag(&sm.kt[(dt * 16 + n16) * LDC + kb * KS], g4), RDf[kb]);
+        for (int kb = 0; kb < NCT / TPS; ++kb) mma(S[dt], ld_frag(&B.kt[(dt * 16 + n16) * LDC + kb * KS], g4), RDf[kb]);
       }
     }
+    if constexpr (STASH) {
+      CT* rst = (CT*)p.chunk_states + NR * D * D + rec * (C * D);
+#pragma unroll
+      for (int it = 0; it < NCT; ++it)
+        st4(rst + stash_tile_offset<CT, D>(it, V, lane), Racc[it][0], Racc[it][1], Racc[it][2], Racc[it][3]);
+    }
+    // ---- Y = diag(gam) Q S0 + Aq R ----
+    {
+      // this chain's rows of y in this chunk; rows past T fall outside the resource
+      const __amdgpu_buffer_rsrc_t yr =
+          buf_rsrc((CT*)p.y + (((size_t)(b * p.T + t0) * p.H + h) * p.M + m) * D, (unsigned)min(C, p.T - t0) * ysb);
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) {
+        f32x4 Y = zero4();
+#pragma unroll
+        for (int kb = 0; kb < NDT / TPS; ++kb) mma(Y, ld_frag(&B.q[(it * 16 + n16) * LDD + kb * KS], g4), Sf[kb]);
+        Y *= *(const f32x4*)&gam[it * 16 + 4 * g4];
+#pragma unroll
+        for (int kb = 0; kb < NCT / TPS; ++kb) mma(Y, ld_frag(&B.aq[(it * 16 + n16) * LDC + kb * KS], g4), Rf[kb]);
+        // transposed tile: lane (g, n) holds row 16 it + n, columns 4 g .. 4 g + 3
+        const f32x4 yt = tile_transpose((CT*)nullptr, Y, lane);
+        buf_store4(yr, (unsigned)(it * 16 + n16) * ysb + (16 * V + 4 * g4) * sizeof(CT), (const CT*)nullptr, yt[0],
+                   yt[1], yt[2], yt[3]);
+      }
+    }
+    // ---- chunk c + 1's tiles into the other buffer, chunk c + 2's loads ----
+    if constexpr (NBUF == 1) __syncthreads();   // (one buffer: every wave done with chunk c's tiles)
+    if (c + 1 < NC) commit(sm.buf[(c + 1) % NBUF]);
+    fetch(min(c + 2, NC - 1));   // (the last chunks refetch, unused)
+    __syncthreads();
   }
 
   if (p.s_out) {
@@ -259,7 +266,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
 // backward: reverse scan of the state gradient
 // ---------------------------------------------------------------------------
 template <typename CT, int D, int C, int NWV>
-struct alignas(16) ScanBwdSmem {
+struct alignas(16) ScanBwdBuf {
   typedef ScanDims<CT, D, C, NWV> Sd;
   CT k[C * Sd::LDD];        // K rows
   CT kt[D * Sd::LDC];       // K^T
@@ -268,6 +275,12 @@ struct alignas(16) ScanBwdSmem {
   CT tt[C * Sd::LDC];       // T^T
   CT aqt[C * Sd::LDC];      // Aq^T
   float sc[kNumSc * C];
+};
+// staging double-buffered by chunk parity where it fits in LDS (see the forward)
+template <typename CT, int D, int C, int NWV>
+struct alignas(16) ScanBwdSmem {
+  static constexpr int NBUF = 2 * sizeof(ScanBwdBuf<CT, D, C, NWV>) <= 160 * 1024 ? 2 : 1;
+  ScanBwdBuf<CT, D, C, NWV> buf[NBUF];
 };
 
 template <typename CT, int D, int C, int NWV>
@@ -336,29 +349,34 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
       ps.fetch(pp.sc + rec_index(chain, c, nchains) * kNumSc * C, gt);
     }
   };
+  constexpr int NBUF = ScanBwdSmem<CT, D, C, NWV>::NBUF;
+  auto commit = [&](ScanBwdBuf<CT, D, C, NWV>& B) {
+    if (grp == 0) {
+      pq.template commit_tr<LDC>(B.qt, gt);
+    } else if (grp == 1) {
+      pk.template commit_nat<LDD>(B.k, gt);
+      pk.template commit_tr<LDC>(B.kt, gt);
+    } else if (grp == 2) {
+      py.template commit_tr<LDC>(B.dyt, gt);
+    } else {
+      pt.template commit_tr<LDC>(B.tt, gt);
+      pa.template commit_tr<LDC>(B.aqt, gt);
+      ps.commit(B.sc, gt);
+    }
+  };
   fetch(NC - 1);
+  __builtin_amdgcn_s_waitcnt(0);
+  commit(sm.buf[(NC - 1) % NBUF]);
+  fetch(max(NC - 2, 0));
   __builtin_amdgcn_s_waitcnt(0);   // the loop's waits then only track its own loads and stores
+  __syncthreads();
 
   for (int c = NC - 1; c >= 0; --c) {
     const size_t rec = rec_index(chain, c, nchains);
-    __syncthreads();
-    if (grp == 0) {
-      pq.template commit_tr<LDC>(sm.qt, gt);
-    } else if (grp == 1) {
-      pk.template commit_nat<LDD>(sm.k, gt);
-      pk.template commit_tr<LDC>(sm.kt, gt);
-    } else if (grp == 2) {
-      py.template commit_tr<LDC>(sm.dyt, gt);
-    } else {
-      pt.template commit_tr<LDC>(sm.tt, gt);
-      pa.template commit_tr<LDC>(sm.aqt, gt);
-      ps.commit(sm.sc, gt);
-    }
-    __syncthreads();
-    fetch(max(c - 1, 0));   // (the first chunk refetches itself, unused)
-    const float* gam = &sm.sc[kScGam * C];
-    const float* dec = &sm.sc[kScDec * C];
-    const float* aeg = &sm.sc[kScAeg * C];
+    const auto& sb = sm.buf[c % NBUF];
+    const float* gam = &sb.sc[kScGam * C];
+    const float* dec = &sb.sc[kScDec * C];
+    const float* aeg = &sb.sc[kScAeg * C];
 
     // ---- dS at the chunk end as fragments over k = d; stash ----
     Frag dSf[NDT / TPS];
@@ -373,16 +391,16 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
     // ---- dR = diag(dec) K dS + Aq^T dY ----
     Frag dYf[C / KS];
 #pragma unroll
-    for (int kb = 0; kb < C / KS; ++kb) dYf[kb] = ld_frag(&sm.dyt[(wave * 16 + n16) * LDC + kb * KS], g4);
+    for (int kb = 0; kb < C / KS; ++kb) dYf[kb] = ld_frag(&sb.dyt[(wave * 16 + n16) * LDC + kb * KS], g4);
     f32x4 dR[NCT];
 #pragma unroll
     for (int it = 0; it < NCT; ++it) {
       f32x4 acc = zero4();
 #pragma unroll
-      for (int kb = 0; kb < NDT / TPS; ++kb) mma(acc, ld_frag(&sm.k[(it * 16 + n16) * LDD + kb * KS], g4), dSf[kb]);
+      for (int kb = 0; kb < NDT / TPS; ++kb) mma(acc, ld_frag(&sb.k[(it * 16 + n16) * LDD + kb * KS], g4), dSf[kb]);
       acc *= *(const f32x4*)&dec[it * 16 + 4 * g4];
 #pragma unroll
-      for (int kb = 0; kb < C / KS; ++kb) mma(acc, ld_frag(&sm.aqt[(it * 16 + n16) * LDC + kb * KS], g4), dYf[kb]);
+      for (int kb = 0; kb < C / KS; ++kb) mma(acc, ld_frag(&sb.aqt[(it * 16 + n16) * LDC + kb * KS], g4), dYf[kb]);
       dR[it] = acc;
     }
     // ---- dB = T^T dR; stash ----
@@ -396,7 +414,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
       for (int it = 0; it < NCT; ++it) {
         dB[it] = zero4();
 #pragma unroll
-        for (int kb = 0; kb < NCT / TPS; ++kb) mma(dB[it], ld_frag(&sm.tt[(it * 16 + n16) * LDC + kb * KS], g4), dRf[kb]);
+        for (int kb = 0; kb < NCT / TPS; ++kb) mma(dB[it], ld_frag(&sb.tt[(it * 16 + n16) * LDC + kb * KS], g4), dRf[kb]);
       }
       CT* bst = (CT*)p.ds_stash + NR * D * D + rec * (C * D);
 #pragma unroll
@@ -421,11 +439,16 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
         dS[dt] *= gl;
 #pragma unroll
         for (int kb = 0; kb < C / KS; ++kb) {
-          mma(dS[dt], ld_frag(&sm.qt[(dt * 16 + n16) * LDC + kb * KS], g4), gYf[kb]);
-          mma(dS[dt], ld_frag(&sm.kt[(dt * 16 + n16) * LDC + kb * KS], g4), dBf[kb]);
+          mma(dS[dt], ld_frag(&sb.qt[(dt * 16 + n16) * LDC + kb * KS], g4), gYf[kb]);
+          mma(dS[dt], ld_frag(&sb.kt[(dt * 16 + n16) * LDC + kb * KS], g4), dBf[kb]);
         }
       }
     }
+    // ---- chunk c - 1's tiles into the other buffer, chunk c - 2's loads ----
+    if constexpr (NBUF == 1) __syncthreads();   // (one buffer: every wave done with chunk c's tiles)
+    if (c > 0) commit(sm.buf[(c - 1) % NBUF]);
+    fetch(max(c - 2, 0));   // (the first chunks refetch, unused)
+    __syncthreads();
   }
   if (p.ds0) {
 #pragma unroll
