@@ -566,13 +566,13 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
 // ---------------------------------------------------------------------------
 // fused forward
 // ---------------------------------------------------------------------------
-template <typename CT, int D, int P>
+template <typename CT, int D, int P, int NVB>
 struct G3WinSmem {
   alignas(16) CT x[3 * P][D + 8];      // rows: H (0..P-1), Q (P..2P-1), K (2P..3P-1)
   alignas(16) float u[P][D + 4];       // w (.) v
   alignas(16) float kr[2 * P][D + 4];  // Kronecker reads of H and Q
   alignas(16) float pp[6][P][P + 4];   // H K^T, Q K^T, H Vbd^T, Q Vbd^T -> Lm, Aq, Ho, Qo; T; scratch
-  alignas(16) CT skron[D][D + 8];      // sum_r A_r (x) B_r, rows v
+  alignas(16) CT skron[D / NVB][D + 8];  // sum_r A_r (x) B_r, this workgroup's rows v
   alignas(16) float vbd[P][D + 4];     // window keys decayed to the chunk start
   alignas(16) CT vbx[P][D + 8];        // the same in the compute dtype
   float G[P], alpha[P], lg[P], kco[P], qco[P], gam[P], vsc[P];
@@ -603,25 +603,32 @@ __device__ __forceinline__ void store8(float* dst, const float* f) {
 }
 
 // Chunks [c0, c1) of one compaction interval (or the tail) for every chain;
-// the window state enters and leaves through the workspace.
-template <typename CT, int D, int P>
+// the window state enters and leaves through the workspace.  A chain's value
+// columns are split over NVB workgroups (D / 16 / NVB value tiles each): the
+// window's grams, the triangular inverse and the window keys depend on no
+// value column and are formed by each of them; the Kronecker reads, the
+// window algebra, the net writes U and y are split.
+template <typename CT, int D, int P, int NVB>
 __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
-  __shared__ G3WinSmem<CT, D, P> sm;
+  __shared__ G3WinSmem<CT, D, P, NVB> sm;
   constexpr int DG = D / 8;  // 8-element load units per token row
   constexpr int UNITS = P * DG;
   constexpr int W16 = W16Of<CT>::value;
   constexpr int KS = FragT<CT>::KSTEP;
   typedef typename FragT<CT>::type Frag;
   static_assert(UNITS <= kNT && UNITS % 64 == 0, "one load unit per thread");
-  static_assert(sizeof(G3WinSmem<CT, D, P>) <= 160 * 1024, "LDS budget");
+  static_assert(sizeof(G3WinSmem<CT, D, P, NVB>) <= 160 * 1024, "LDS budget");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, n16 = lane & 15;
   const int H = p.H, M = p.M, T = p.T;
   const int N = p.B * H * M;
-  const int chain = xcd_remap(blockIdx.x, N);
+  const int work = xcd_remap(blockIdx.x, N * NVB);   // a chain's NVB workgroups land on one XCD
+  const int chain = work / NVB, vb = work % NVB;
   const int b = chain / (H * M), hm = chain % (H * M), h = hm / M, m = hm % M;
   typedef G3D<D> Ge;
+  constexpr int NVTW = D / 16 / NVB;   // value tiles of this workgroup: vb NVTW + [0, NVTW)
+  static_assert(NVTW >= 1 && (D / 16) % NVB == 0, "value split");
 
   const bool has_unit = tid < UNITS;
   const int ui = tid / DG, ud = 8 * (tid % DG);
@@ -713,8 +720,12 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
     }
   };
 
-  // window state: zero for the first interval, else from the workspace
-  constexpr int PT = P / 16, VPW = (D / 16) / 4;
+  // window state: zero for the first interval, else from the workspace.
+  // Wave w holds value tiles vtile(a) = vb NVTW + w + 4 a of the workgroup's
+  // (a < VPW, where w + 4 a < NVTW)
+  constexpr int PT = P / 16, VPW = (NVTW + 3) / 4;
+  auto vown = [&](int a) { return wave + 4 * a < NVTW; };
+  auto vtile = [&](int a) { return vb * NVTW + wave + 4 * a; };
   f32x4 uo[PT][VPW];
   float* uw = p.uw + (size_t)chain * P * D;
   float* vw = p.vw + (size_t)chain * P * D;
@@ -737,14 +748,15 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
 #pragma unroll
       for (int a = 0; a < VPW; ++a)
 #pragma unroll
-        for (int s = 0; s < 4; ++s) uo[it][a][s] = uw[(it * 16 + 4 * g4 + s) * D + (wave * VPW + a) * 16 + n16];
+        for (int s = 0; s < 4; ++s)
+          uo[it][a][s] = vown(a) ? uw[(it * 16 + 4 * g4 + s) * D + vtile(a) * 16 + n16] : 0.f;
   }
   const bool live = p.live;
-  if (live) {
+  if (live) {   // this workgroup's value rows of the Kronecker matrix
     constexpr int PER = 16 / sizeof(CT);  // elements per 16-byte load
-    const uint4* src = (const uint4*)((const CT*)p.skron + (size_t)chain * D * D);
-    for (int e = tid; e < D * D / PER; e += kNT) {
-      const int v = (e * PER) / D, k = (e * PER) % D;
+    const uint4* src = (const uint4*)((const CT*)p.skron + ((size_t)chain * D + vb * NVTW * 16) * D);
+    for (int e = tid; e < NVTW * 16 * D / PER; e += kNT) {
+      const int v = (e * PER) / D, k = (e * PER) % D;   // (local row)
       *(uint4*)&sm.skron[v][k] = src[e];
     }
   }
@@ -857,15 +869,15 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
       }
     }
     if (live) {
-      constexpr int NRT = 2 * P / 16, NVT = D / 16;
-      // value tiles of this wave: P == 16 spreads them over waves 1..3
-      const int vt0 = (P == 16) ? wave - 1 : wave * VPW, vstep = (P == 16) ? 3 : 1;
-      const int nvt = (P == 16) ? (wave == 0 ? 0 : (NVT - (wave - 1) + 2) / 3) : VPW;
-      for (int a = 0; a < nvt; ++a) {
-        const int vt = vt0 + a * vstep;
+      constexpr int NRT = 2 * P / 16;
+      // this workgroup's value tiles: P == 16 spreads them over waves 1..3
+      // (wave 0 forms the inverse meanwhile), otherwise over all four
+      const int l0 = (P == 16) ? wave - 1 : wave, lstep = (P == 16) ? 3 : 4;
+      for (int l = l0; P == 16 && wave == 0 ? false : l < NVTW; l += lstep) {
+        const int vt = vb * NVTW + l;
         Frag bf[D / KS];
 #pragma unroll
-        for (int kb = 0; kb < D / KS; ++kb) bf[kb] = ld_frag(&sm.skron[vt * 16 + n16][kb * KS], g4);
+        for (int kb = 0; kb < D / KS; ++kb) bf[kb] = ld_frag(&sm.skron[l * 16 + n16][kb * KS], g4);
 #pragma unroll
         for (int rt = 0; rt < NRT; ++rt) {
           f32x4 acc = zero4();
@@ -925,7 +937,8 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
       };
 #pragma unroll
       for (int a = 0; a < VPW; ++a) {
-        const int v = (wave * VPW + a) * 16 + n16;
+        if (!vown(a)) continue;
+        const int v = vtile(a) * 16 + n16;
         f32x4 rhs[PT], un[PT];
 #pragma unroll
         for (int it = 0; it < PT; ++it) {
@@ -979,7 +992,7 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
         }
       }
     }
-    if (p.ts_g && tid == 0) p.ts_g[(size_t)chain * p.nch + c] = gacc;
+    if (p.ts_g && tid == 0 && vb == 0) p.ts_g[(size_t)chain * p.nch + c] = gacc;
     // window keys for the next chunk: k_j decayed to this chunk's end, 8
     // consecutive keys per thread
     for (int u8 = tid; u8 < P * D / 8; u8 += kNT) {
@@ -1006,17 +1019,21 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
   }
 #undef PP
   __syncthreads();
-  // window state out (and the final state after the last chunk)
+  // window state out (and the final state after the last chunk): the value
+  // columns from their workgroup, the keys and decays from the first
 #pragma unroll
-  for (int a = 0; a < VPW; ++a)
+  for (int a = 0; a < VPW; ++a) {
+    if (!vown(a)) continue;
 #pragma unroll
     for (int it = 0; it < PT; ++it)
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int i = it * 16 + 4 * g4 + s, v = (wave * VPW + a) * 16 + n16;
+        const int i = it * 16 + 4 * g4 + s, v = vtile(a) * 16 + n16;
         uw[i * D + v] = uo[it][a][s];
         if (p.last && p.U_out) p.U_out[((size_t)chain * D + v) * P + i] = uo[it][a][s];
       }
+  }
+  if (vb != 0) return;
   for (int e = tid; e < P * D; e += kNT) {
     const int j = e / D, d = e % D;
     vw[e] = sm.vbd[j][d];
@@ -1272,7 +1289,18 @@ int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
     a.live = !first || carried;      // the Kronecker factors may be nonzero
     a.last = c1 == cg1;
     a.complete = (long long)c1 * P <= tend && c1 % per == 0;
-    hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P>), dim3(N), dim3(kNT), 0, stream, a);
+    // value split: ~512 workgroups, two per CU (NVB workgroups per chain, at
+    // least one value tile each)
+    constexpr int V2 = D / 16 < 2 ? D / 16 : 2, V4 = D / 16 < 4 ? D / 16 : 4, V8 = D / 16 < 8 ? D / 16 : 8;
+    const int nvb = N >= 512 ? 1 : N >= 256 ? V2 : N >= 128 ? V4 : V8;
+    if (nvb == 1)
+      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, 1>), dim3(N), dim3(kNT), 0, stream, a);
+    else if (nvb == V2)
+      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, V2>), dim3(N * V2), dim3(kNT), 0, stream, a);
+    else if (nvb == V4)
+      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, V4>), dim3(N * V4), dim3(kNT), 0, stream, a);
+    else
+      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, V8>), dim3(N * V8), dim3(kNT), 0, stream, a);
     if ((rc = check_launch("gdn3_window_kernel"))) return rc;
     if (a.complete) {
       G3CompactArgs ca{};
