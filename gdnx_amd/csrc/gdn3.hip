@@ -76,7 +76,8 @@ struct G3Compact {
   alignas(16) double y[kMN * kQ];         // range basis, rows of kQ
   alignas(16) double z[kMN * kQ];         // R_mat^T Y, then Bm^T = R_mat^T Q (rows of kQ)
   alignas(16) float gs[kMN * kQ];         // sketch, rows of kQ (zero padded)
-  alignas(16) float ut[P][D + 4];         // window net writes U_p
+  alignas(16) float ut[16][D + 4];        // a block of 16 window slots: net writes U_p
+  alignas(16) float vt[16][D + 4];        // and keys Vb_p
   alignas(16) double us[kRMax][kMN];      // leading left singular vectors of R_mat
   alignas(16) double vs[kRMax][kMN];      // leading right singular vectors
   double red[4 * 64];
@@ -280,10 +281,10 @@ __device__ __forceinline__ void col_sumsq(const double* y, double* red, double* 
   __syncthreads();
 }
 
-// Compaction of one chain (gdn3/gdn3_upgrade.py:650-719) on LDS inputs:
-// ab = [A (R x m) | B (R x n)] as stored (the Kronecker part is decayed by
-// e^{gacc} per factor), cs.ut = window net writes [P][D], vbd = window keys
-// decayed to now [P][D].  Writes the blended A, B back into ab and, from
+// Compaction of one chain (gdn3/gdn3_upgrade.py:650-719): ab = [A (R x m) |
+// B (R x n)] in LDS as stored (the Kronecker part is decayed by e^{gacc} per
+// factor); the window's P net writes U and keys Vb (decayed to now) are read
+// from global memory, slot p column d at p u_sp + d u_sd.  Writes the blended A, B back into ab and, from
 // thread 0, stats = (|R_mat|^2, sum of the R kept sigma^2).  Sign
 // convention: each (u_r, v_r) pair is flipped so that the largest-magnitude
 // entry of v_r is positive (first index on ties).
@@ -293,8 +294,10 @@ __device__ __forceinline__ void col_sumsq(const double* y, double* red, double* 
 // Bm = Q^T R_mat, A_svd_r = |Bm_r| Q_r, B_svd_r = Bm_r / |Bm_r| (norms
 // clamped at 1e-12); it reports no error (stats = (|R_mat|^2, |R_mat|^2)).
 template <int D, int P>
-__device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float (*vbd)[D + 4], float gacc, float sdec,
-                           const float* __restrict__ sketch, double* stats, int tid, int mode = 0) {
+__device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float* __restrict__ U,
+                                           const float* __restrict__ Vb, size_t u_sp, size_t u_sd, float gacc,
+                                           float sdec, const float* __restrict__ sketch, double* stats, int tid,
+                                           int mode = 0) {
   typedef G3D<D> Ge;
   constexpr int R = Ge::R, m = Ge::m, n = Ge::n, q = Ge::q, ak = Ge::ak, bk = Ge::bk;
   constexpr int lbv = Ge::lbv, lbk = Ge::lbk, ln = Ge::ln;
@@ -314,36 +317,53 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
     gsv[u] = (e < n * kQ && j < qs) ? sketch[c * qs + j] : 0.f;
   }
   // residual part rearrange(U Vb^T) on fp32 MFMA: out[v][k] = sum_p U_p[v] Vb_p[k]
-  // (A[v][p] = U_p[v], B[p][k] = Vb_p[k]); wave w owns the value-row tiles
+  // (A[v][p] = U_p[v], B[p][k] = Vb_p[k]), accumulated over the window's
+  // blocks of 16 slots staged through LDS; wave w owns the value-row tiles
   // w VTW .. w VTW + VTW - 1 against every key-column tile, and scatters each
   // entry to its rearranged place (iv a_k + ik, jv b_k + jk)
   {
     constexpr int NT16 = D / 16, VTW = NT16 / 4;
-    static_assert(NT16 % 4 == 0 && P % 16 == 0, "whole 16x16 tiles on 4 waves, 16 window slots per step");
+    static_assert(NT16 % 4 == 0 && P % 16 == 0, "whole 16x16 tiles on 4 waves, blocks of 16 window slots");
     const int g4 = lane >> 4, n16 = lane & 15;
+    f32x4 racc[VTW][NT16];
+#pragma unroll
+    for (int vi = 0; vi < VTW; ++vi)
+#pragma unroll
+      for (int kt = 0; kt < NT16; ++kt) racc[vi][kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    for (int pb = 0; pb < P / 16; ++pb) {
+      if (pb > 0) __syncthreads();   // the previous block is consumed
+      for (int e = tid; e < 16 * D; e += kNT) {
+        const int i = e / D, d = e % D;
+        const size_t o = (size_t)(16 * pb + i) * u_sp + (size_t)d * u_sd;
+        cs.ut[i][d] = U[o];
+        cs.vt[i][d] = Vb[o];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int vi = 0; vi < VTW; ++vi) {
+        const int vt = wave * VTW + vi;
+        f32x4 ua;
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) ua[s4] = cs.ut[4 * g4 + s4][vt * 16 + n16];
+#pragma unroll
+        for (int kt = 0; kt < NT16; ++kt) {
+          f32x4 kb4;
+#pragma unroll
+          for (int s4 = 0; s4 < 4; ++s4) kb4[s4] = cs.vt[4 * g4 + s4][kt * 16 + n16];
+          mma(racc[vi][kt], ua, kb4);
+        }
+      }
+    }
 #pragma unroll
     for (int vi = 0; vi < VTW; ++vi) {
       const int vt = wave * VTW + vi;
-      f32x4 ua[P / 16];
 #pragma unroll
-      for (int pb = 0; pb < P / 16; ++pb)
-#pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) ua[pb][s4] = cs.ut[pb * 16 + 4 * g4 + s4][vt * 16 + n16];
-#pragma unroll 2
       for (int kt = 0; kt < NT16; ++kt) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int pb = 0; pb < P / 16; ++pb) {
-          f32x4 kb4;
-#pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) kb4[s4] = vbd[pb * 16 + 4 * g4 + s4][kt * 16 + n16];
-          mma(acc, ua[pb], kb4);
-        }
         const int k = kt * 16 + n16, ik = k >> lbk, jk = k & (bk - 1);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int v = vt * 16 + 4 * g4 + i, iv = v >> lbv, jv = v & (Ge::bv - 1);
-          cs.rm[(iv * ak + ik) * ldr + jv * bk + jk] = acc[i];
+          cs.rm[(iv * ak + ik) * ldr + jv * bk + jk] = racc[vi][kt][i];
         }
       }
     }
@@ -566,17 +586,31 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
 // ---------------------------------------------------------------------------
 // fused forward
 // ---------------------------------------------------------------------------
+// The window runs in sub-chunks of kSC = 16 tokens aligned with the slots:
+// the P slots are NB = P / 16 blocks, block b holding slots 16 b .. 16 b + 15.
+// Sub-chunk c (global tokens 16 c .. 16 c + 15) writes block c mod NB.  Token
+// i of it sees the other NB - 1 blocks whole (the writes of sub-chunks c - 1
+// .. c - NB + 1) and, of block c mod NB, the slots p >= i the writes of
+// sub-chunk c - NB still hold; at P = 16 that is the banded previous chunk.
+constexpr int kSC = 16;
+
 template <typename CT, int D, int P, int NVB>
 struct G3WinSmem {
-  alignas(16) CT x[3 * P][D + 8];      // rows: H (0..P-1), Q (P..2P-1), K (2P..3P-1)
-  alignas(16) float u[P][D + 4];       // w (.) v
-  alignas(16) float kr[2 * P][D + 4];  // Kronecker reads of H and Q
-  alignas(16) float pp[6][P][P + 4];   // H K^T, Q K^T, H Vbd^T, Q Vbd^T -> Lm, Aq, Ho, Qo; T; scratch
+  static constexpr int NB = P / kSC;
+  static constexpr bool KF = sizeof(CT) == 4;  // fp32 IO: the grams read the fp32 window keys
+  alignas(16) CT x[3 * kSC][D + 8];      // rows: H (0..15), Q (16..31), K (32..47)
+  alignas(16) float u[kSC][D + 4];       // w (.) v
+  alignas(16) float kr[2 * kSC][D + 4];  // Kronecker reads of H and Q
+  alignas(16) float pp[4][kSC][kSC + 4]; // H K^T (then inverse scratch), Aq, T, inverse scratch
+  alignas(16) float po[2][kSC][P + 4];   // Ho, Qo over the P slots
   alignas(16) CT skron[D / NVB][D + 8];  // sum_r A_r (x) B_r, this workgroup's rows v
-  alignas(16) float vbd[P][D + 4];     // window keys decayed to the chunk start
-  alignas(16) CT vbx[P][D + 8];        // the same in the compute dtype
-  float G[P], alpha[P], lg[P], kco[P], qco[P], gam[P], vsc[P];
+  alignas(16) float vbd[P][D + 4];       // window keys: block b decayed to e^{-boff_b} of now
+  alignas(16) CT vbx[KF ? 1 : P][D + 8]; // the same in the compute dtype (bf16 IO)
+  float G[kSC], alpha[kSC], lg[kSC], kco[kSC], qco[kSC], gam[kSC], vsc[kSC];
+  float boff[NB];                        // log decay of block b's keys since they were last rebased
 };
+template <typename CT, int D, int P, int NVB>
+constexpr bool win_fits() { return sizeof(G3WinSmem<CT, D, P, NVB>) <= 160 * 1024; }
 
 template <typename CT> struct W16Of { static constexpr int value = 8 * sizeof(CT) / 16; };
 
@@ -602,22 +636,25 @@ __device__ __forceinline__ void store8(float* dst, const float* f) {
   *(f32x4*)(dst + 4) = (f32x4){f[4], f[5], f[6], f[7]};
 }
 
-// Chunks [c0, c1) of one compaction interval (or the tail) for every chain;
-// the window state enters and leaves through the workspace.  A chain's value
-// columns are split over NVB workgroups (D / 16 / NVB value tiles each): the
-// window's grams, the triangular inverse and the window keys depend on no
-// value column and are formed by each of them; the Kronecker reads, the
+// Sub-chunks [c0, c1) of one compaction interval (or the tail) for every
+// chain; the window state enters and leaves through the workspace.  A
+// chain's value columns are split over NVB workgroups (D / 16 / NVB value
+// tiles each): the grams, the triangular inverse and the window keys depend
+// on no value column and are formed by each of them; the Kronecker reads, the
 // window algebra, the net writes U and y are split.
 template <typename CT, int D, int P, int NVB>
 __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
-  __shared__ G3WinSmem<CT, D, P, NVB> sm;
+  typedef G3WinSmem<CT, D, P, NVB> Sm;
+  __shared__ Sm sm;
+  constexpr int NB = Sm::NB;
   constexpr int DG = D / 8;  // 8-element load units per token row
-  constexpr int UNITS = P * DG;
+  constexpr int UNITS = kSC * DG;
   constexpr int W16 = W16Of<CT>::value;
   constexpr int KS = FragT<CT>::KSTEP;
   typedef typename FragT<CT>::type Frag;
   static_assert(UNITS <= kNT && UNITS % 64 == 0, "one load unit per thread");
-  static_assert(sizeof(G3WinSmem<CT, D, P, NVB>) <= 160 * 1024, "LDS budget");
+  static_assert(P % kSC == 0 && NB >= 1 && NB <= 4, "whole 16-slot blocks, at most 4");
+  static_assert(sizeof(Sm) <= 160 * 1024, "LDS budget");
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g4 = lane >> 4, n16 = lane & 15;
@@ -647,9 +684,9 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
     f32x4 b0, b1, w0, w1;
     float dec;
   };
-  // chunk c covers global tokens [c P, c P + P): local token c P + i - t0
+  // sub-chunk c covers global tokens [16 c, 16 c + 16): local token 16 c + i - t0
   auto fetch = [&](Raw& r, int c) {
-    const int t = c * P + ui - p.t0;
+    const int t = c * kSC + ui - p.t0;
     if (has_unit && t >= 0 && t < T) {
       const uint4* kp = (const uint4*)((const CT*)p.k + qkv_base + (size_t)t * qkv_tok + ud);
       const uint4* qp = (const uint4*)((const CT*)p.q + qkv_base + (size_t)t * qkv_tok + ud);
@@ -699,8 +736,8 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
     store8(&sm.x[ui][ud], hf);
 #pragma unroll
     for (int w = 0; w < W16; ++w) {
-      *(uint4*)&sm.x[P + ui][ud + w * (16 / sizeof(CT))] = r.q[w];
-      *(uint4*)&sm.x[2 * P + ui][ud + w * (16 / sizeof(CT))] = r.k[w];
+      *(uint4*)&sm.x[kSC + ui][ud + w * (16 / sizeof(CT))] = r.q[w];
+      *(uint4*)&sm.x[2 * kSC + ui][ud + w * (16 / sizeof(CT))] = r.k[w];
     }
     *(f32x4*)&sm.u[ui][ud] = (f32x4){uu[0], uu[1], uu[2], uu[3]};
     *(f32x4*)&sm.u[ui][ud + 4] = (f32x4){uu[4], uu[5], uu[6], uu[7]};
@@ -722,35 +759,37 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
 
   // window state: zero for the first interval, else from the workspace.
   // Wave w holds value tiles vtile(a) = vb NVTW + w + 4 a of the workgroup's
-  // (a < VPW, where w + 4 a < NVTW)
-  constexpr int PT = P / 16, VPW = (NVTW + 3) / 4;
+  // (a < VPW, where w + 4 a < NVTW), of every block
+  constexpr int VPW = (NVTW + 3) / 4;
   auto vown = [&](int a) { return wave + 4 * a < NVTW; };
   auto vtile = [&](int a) { return vb * NVTW + wave + 4 * a; };
-  f32x4 uo[PT][VPW];
+  f32x4 uo[NB][VPW];
   float* uw = p.uw + (size_t)chain * P * D;
   float* vw = p.vw + (size_t)chain * P * D;
   if (p.first) {
     for (int e = tid; e < P * (D + 4); e += kNT) (&sm.vbd[0][0])[e] = 0.f;
-    for (int e = tid; e < P * (D + 8); e += kNT) (&sm.vbx[0][0])[e] = (CT)0.f;
+    if constexpr (!Sm::KF)
+      for (int e = tid; e < P * (D + 8); e += kNT) (&sm.vbx[0][0])[e] = (CT)0.f;
 #pragma unroll
-    for (int it = 0; it < PT; ++it)
+    for (int bl = 0; bl < NB; ++bl)
 #pragma unroll
-      for (int a = 0; a < VPW; ++a) uo[it][a] = zero4();
+      for (int a = 0; a < VPW; ++a) uo[bl][a] = zero4();
   } else {
     for (int e = tid; e < P * D; e += kNT) {
       const int j = e / D, d = e % D;
       const float kv = vw[e];
       sm.vbd[j][d] = kv;
-      sm.vbx[j][d] = from_f<CT>(kv);
+      if constexpr (!Sm::KF) sm.vbx[j][d] = from_f<CT>(kv);
     }
 #pragma unroll
-    for (int it = 0; it < PT; ++it)
+    for (int bl = 0; bl < NB; ++bl)
 #pragma unroll
       for (int a = 0; a < VPW; ++a)
 #pragma unroll
         for (int s = 0; s < 4; ++s)
-          uo[it][a][s] = vown(a) ? uw[(it * 16 + 4 * g4 + s) * D + vtile(a) * 16 + n16] : 0.f;
+          uo[bl][a][s] = vown(a) ? uw[(bl * kSC + 4 * g4 + s) * D + vtile(a) * 16 + n16] : 0.f;
   }
+  if (tid < NB) sm.boff[tid] = 0.f;
   const bool live = p.live;
   if (live) {   // this workgroup's value rows of the Kronecker matrix
     constexpr int PER = 16 / sizeof(CT);  // elements per 16-byte load
@@ -761,31 +800,36 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
     }
   }
   float gacc = 0.f;
+  // after sub-chunk c: its block is rebased (boff 0), the others decayed by its G_last
+  auto advance_boff = [&](int c, float glast) {
+    if (tid < NB) sm.boff[tid] = (tid == c % NB) ? 0.f : sm.boff[tid] + glast;
+  };
 
-#define PP(mat, i, j) sm.pp[mat][i][j]
   Raw raw;
   fetch(raw, p.c0);
   for (int c = p.c0; c < p.c1; ++c) {
-    // slots [lo, hi) receive this call's tokens; the others (the head of a
-    // window a previous call began, the tail after the last token) keep the
-    // writes they hold and stay visible to every token of the window
-    const int lo = max(0, p.t0 - c * P), hi = min(P, p.t0 + T - c * P);
+    // slots [lo, hi) of block beta receive this call's tokens; the others (the
+    // head a previous call wrote, the tail after the last token) keep the
+    // writes they hold and stay visible to every token of the sub-chunk
+    const int lo = max(0, p.t0 - c * kSC), hi = min(kSC, p.t0 + T - c * kSC);
+    const int beta = c % NB;
     __syncthreads();
+    if (c > p.c0) advance_boff(c - 1, sm.G[kSC - 1]);
     commit(raw);
     if (c + 1 < p.c1) fetch(raw, c + 1);
     __syncthreads();
     // per-token scalars | grams and Kronecker reads (MFMA).  Every wave forms
     // the log-decay prefix sums G (lane i holds G_i); wave 0 publishes the
     // per-token coefficients.
-    float gl = lane < P ? sm.lg[lane] : 0.f;
+    float gl = lane < kSC ? sm.lg[lane] : 0.f;
 #pragma unroll
-    for (int off = 1; off < P; off <<= 1) {
+    for (int off = 1; off < kSC; off <<= 1) {
       const float o = __shfl_up(gl, off, 64);
       if (lane >= off) gl += o;
     }
     if (wave == 0) {
-      const float gl_last = __shfl(gl, P - 1, 64);
-      if (lane < P) {
+      const float gl_last = __shfl(gl, kSC - 1, 64);
+      if (lane < kSC) {
         const float e2 = expf(2.f * (gacc + gl));
         sm.G[lane] = gl;
         sm.gam[lane] = expf(gl);
@@ -794,92 +838,102 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
         sm.vsc[lane] = expf(gl_last - gl);
       }
     }
+    // grams, 2 + 2 NB tiles over the waves (tile ti on wave ti mod 4):
+    //   0: H K^T (raw; wave 0 turns it into T),  1: Aq = [j <= i] e^{G_i - G_j} q_i.k_j,
+    //   2 + 2 b: Ho_b = vis alpha_i e^{G_i + boff_b} h_i.Vb_b[j],  3 + 2 b: Qo_b = vis e^{G_i + boff_b} q_i.Vb_b[j]
+    // with vis = [b != beta or j >= i or j < lo]
     {
-      const CT* arows = &sm.x[(wave & 1) ? P : 0][0];
-      const CT* brows = (wave < 2) ? &sm.x[2 * P][0] : &sm.vbx[0][0];
+      const float gj = __shfl(gl, n16, 64);
+      float gi[4];
 #pragma unroll
-      for (int ti = 0; ti < PT * PT; ++ti) {
-        const int it = ti / PT, jt = ti % PT;
-        f32x4 acc = tile_nt<CT, D>(arows + (it * 16 + n16) * (D + 8), brows + (jt * 16 + n16) * (D + 8), g4);
-        if constexpr (P == 16) {
-          // waves 1..3 scale their tile here (one tile each):
-          //   Aq = [j <= i] e^{G_i - G_j} q_i.k_j,  Ho = [j >= i] alpha_i gam_i h_i.Vbd_j,
-          //   Qo = [j >= i] gam_i q_i.Vbd_j
-          if (wave > 0) {
-            const float gj = __shfl(gl, n16, 64);
+      for (int s = 0; s < 4; ++s) gi[s] = __shfl(gl, 4 * g4 + s, 64);
+#pragma unroll
+      for (int r = 0; r < (2 + 2 * NB + 3) / 4; ++r) {
+        const int ti = wave + 4 * r;
+        if (ti < 2 + 2 * NB) {
+          const bool isq = ti & 1;
+          const CT* arow = &sm.x[(isq ? kSC : 0) + n16][0];
+          const int bl = (ti - 2) >> 1;
+          const CT* brow;
+          if (ti < 2) brow = &sm.x[2 * kSC + n16][0];
+          else if constexpr (Sm::KF) brow = (const CT*)&sm.vbd[kSC * bl + n16][0];
+          else brow = &sm.vbx[kSC * bl + n16][0];
+          const f32x4 acc = tile_nt<CT, D>(arow, brow, g4);
+          const int j = n16;
+          if (ti == 0) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) sm.pp[0][4 * g4 + s][j] = acc[s];
+          } else if (ti == 1) {
 #pragma unroll
             for (int s = 0; s < 4; ++s) {
               const int i = 4 * g4 + s;
-              const float gi = __shfl(gl, i, 64);
-              float v;
-              if (wave == 1) v = (n16 <= i) ? expf(gi - gj) * acc[s] : 0.f;
-              else if (wave == 2) v = (n16 >= i || n16 < lo) ? sm.alpha[i] * expf(gi) * acc[s] : 0.f;
-              else v = (n16 >= i || n16 < lo) ? expf(gi) * acc[s] : 0.f;
-              acc[s] = v;
+              sm.pp[1][i][j] = (j <= i) ? expf(gi[s] - gj) * acc[s] : 0.f;
+            }
+          } else {
+            const float bo = sm.boff[bl];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const int i = 4 * g4 + s;
+              const bool vis = bl != beta || j >= i || j < lo;
+              const float sc = expf(gi[s] + bo) * (isq ? 1.f : sm.alpha[i]);
+              sm.po[isq ? 1 : 0][i][kSC * bl + j] = vis ? sc * acc[s] : 0.f;
             }
           }
         }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) sm.pp[wave][it * 16 + 4 * g4 + s][jt * 16 + n16] = acc[s];
       }
     }
-    if constexpr (P == 16) {
-      // T = (I + Lm)^-1 needs only wave 0's own Gram tile (H K^T), the decay
-      // scan and alpha: wave 0 forms it now, while waves 1..3 do the
-      // Kronecker reads
-      if (wave == 0) {
-        // the scan's G and the Gram tile were written by other lanes of this
-        // wave: order the LDS accesses (wave-local)
+    // T = (I + Lm)^-1 needs only wave 0's own Gram tile (H K^T), the decay
+    // scan and alpha: wave 0 forms it now, while waves 1..3 do the Kronecker
+    // reads
+    if (wave == 0) {
+      // the scan's G and the Gram tile were written by other lanes of this
+      // wave: order the LDS accesses (wave-local)
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      // Lm[i][j] = alpha_i e^{G_i - G_j} (h_i . k_j), j < i, is strictly lower
+      // (nilpotent): (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8), factors
+      // that commute; squarings and products on fp32 MFMA.  An accumulator
+      // tile is a k-fragment (B operand); the A operand of each square goes
+      // through LDS.
+      f32x4 xa, ta;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        xa[s] = (n16 < i) ? sm.alpha[i] * expf(sm.G[i] - sm.G[n16]) * sm.pp[0][i][n16] : 0.f;
+        sm.pp[3][i][n16] = xa[s];
+        ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      int src = 3;
+#pragma unroll
+      for (int step = 0; step < 3; ++step) {
+        const int dst = step & 1 ? 3 : 0;
+        f32x4 sq = zero4();
+        mma(sq, *(const f32x4*)&sm.pp[src][n16][4 * g4], xa);  // X^2
+        xa = sq;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) sm.pp[dst][4 * g4 + s][n16] = sq[s];
         __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
         __builtin_amdgcn_wave_barrier();
         __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        // Lm[i][j] = alpha_i e^{G_i - G_j} (h_i . k_j), j < i, is strictly lower
-        // (nilpotent): (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8), factors
-        // that commute; squarings and products on fp32 MFMA.  An accumulator
-        // tile is a k-fragment (B operand); the A operand of each square goes
-        // through LDS.
-        f32x4 xa, ta;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int i = 4 * g4 + s;
-          xa[s] = (n16 < i) ? sm.alpha[i] * expf(sm.G[i] - sm.G[n16]) * PP(0, i, n16) : 0.f;
-          PP(5, i, n16) = xa[s];
-          ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
-        }
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        int src = 5;
-#pragma unroll
-        for (int step = 0; step < 3; ++step) {
-          const int dst = step & 1 ? 5 : 0;
-          f32x4 sq = zero4();
-          mma(sq, *(const f32x4*)&PP(src, n16, 4 * g4), xa);  // X^2
-          xa = sq;
-#pragma unroll
-          for (int s = 0; s < 4; ++s) PP(dst, 4 * g4 + s, n16) = sq[s];
-          __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-          __builtin_amdgcn_wave_barrier();
-          __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-          mma(ta, *(const f32x4*)&PP(dst, n16, 4 * g4), ta);  // T += X^2 T
-          src = dst;
-        }
-#pragma unroll
-        for (int s = 0; s < 4; ++s) PP(4, 4 * g4 + s, n16) = ta[s];
+        mma(ta, *(const f32x4*)&sm.pp[dst][n16][4 * g4], ta);  // T += X^2 T
+        src = dst;
       }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sm.pp[2][4 * g4 + s][n16] = ta[s];
     }
-    if (live) {
-      constexpr int NRT = 2 * P / 16;
-      // this workgroup's value tiles: P == 16 spreads them over waves 1..3
-      // (wave 0 forms the inverse meanwhile), otherwise over all four
-      const int l0 = (P == 16) ? wave - 1 : wave, lstep = (P == 16) ? 3 : 4;
-      for (int l = l0; P == 16 && wave == 0 ? false : l < NVTW; l += lstep) {
+    if (live && wave > 0) {
+      // this workgroup's value tiles over waves 1..3 (wave 0 forms the inverse)
+      for (int l = wave - 1; l < NVTW; l += 3) {
         const int vt = vb * NVTW + l;
         Frag bf[D / KS];
 #pragma unroll
         for (int kb = 0; kb < D / KS; ++kb) bf[kb] = ld_frag(&sm.skron[l * 16 + n16][kb * KS], g4);
 #pragma unroll
-        for (int rt = 0; rt < NRT; ++rt) {
+        for (int rt = 0; rt < 2; ++rt) {
           f32x4 acc = zero4();
 #pragma unroll
           for (int kb = 0; kb < D / KS; ++kb) mma(acc, ld_frag(&sm.x[rt * 16 + n16][kb * KS], g4), bf[kb]);
@@ -889,155 +943,106 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
       }
     }
     __syncthreads();
-    // coefficient matrices (P != 16; at P = 16 they were formed above): wave 0
-    // forms T = (I + Lm)^-1, the others scale Aq, Ho, Qo
-    if constexpr (P != 16) {
-      if (wave == 0) {
-        for (int e = lane; e < P * P; e += 64) {
-          const int i = e / P, j = e % P;
-          PP(0, i, j) = (j < i) ? sm.alpha[i] * expf(sm.G[i] - sm.G[j]) * PP(0, i, j) : 0.f;
-        }
-        // Lm was written by other lanes of this wave: order the LDS accesses
-        // (wave-local, no workgroup barrier needed)
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        // column j of T by forward substitution (lanes j < P)
-        const int j = lane;
-        float t[P];
-#pragma unroll
-        for (int i = 0; i < P; ++i) {
-          float acc = 0.f;
-#pragma unroll
-          for (int k = 0; k < i; ++k) acc += PP(0, i, k) * t[k];
-          t[i] = (i == j) ? 1.f : ((i < j) ? 0.f : -acc);
-        }
-        if (j < P)
-#pragma unroll
-          for (int i = 0; i < P; ++i) PP(4, i, j) = t[i];
-      } else {
-        for (int e = tid - 64; e < P * P; e += kNT - 64) {
-          const int i = e / P, j = e % P;
-          const float gi = sm.G[i], al = sm.alpha[i], ga = sm.gam[i];
-          const float dij = (j <= i) ? expf(gi - sm.G[j]) : 0.f;
-          PP(1, i, j) = dij * PP(1, i, j);
-          PP(2, i, j) = (j >= i || j < lo) ? al * ga * PP(2, i, j) : 0.f;
-          PP(3, i, j) = (j >= i || j < lo) ? ga * PP(3, i, j) : 0.f;
-        }
-      }
-      __syncthreads();
-    }
     // window algebra on fp32 MFMA, per wave its VPW value tiles:
-    //   Rhs = alpha u - kco KRh - Ho U_old;  U = T Rhs
-    //   Y   = qco KRq + Qo U_old + Aq U
+    //   Rhs = alpha u - kco KRh - sum_b Ho_b U_b;  U = T Rhs
+    //   Y   = qco KRq + sum_b Qo_b U_b + Aq U
     // (an accumulator tile over rows = tokens is directly a k-fragment)
-    {
-      auto arow = [&](int mat, int it, int kt) {
-        return *(const f32x4*)&sm.pp[mat][it * 16 + n16][kt * 16 + 4 * g4];
-      };
 #pragma unroll
-      for (int a = 0; a < VPW; ++a) {
-        if (!vown(a)) continue;
-        const int v = vtile(a) * 16 + n16;
-        f32x4 rhs[PT], un[PT];
+    for (int a = 0; a < VPW; ++a) {
+      if (!vown(a)) continue;
+      const int v = vtile(a) * 16 + n16;
+      f32x4 acc = zero4();
 #pragma unroll
-        for (int it = 0; it < PT; ++it) {
-          f32x4 acc = zero4();
+      for (int bl = 0; bl < NB; ++bl) mma(acc, *(const f32x4*)&sm.po[0][n16][kSC * bl + 4 * g4], uo[bl][a]);
+      f32x4 rhs;
 #pragma unroll
-          for (int kt = 0; kt < PT; ++kt) mma(acc, arow(2, it, kt), uo[kt][a]);
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        float r = sm.alpha[i] * sm.u[i][v] - acc[s];
+        if (live) r -= sm.kco[i] * sm.kr[i][v];
+        rhs[s] = r;
+      }
+      f32x4 un = zero4();
+      mma(un, *(const f32x4*)&sm.pp[2][n16][4 * g4], rhs);
+      f32x4 yv = zero4();
 #pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const int i = it * 16 + 4 * g4 + s;
-            float r = sm.alpha[i] * sm.u[i][v] - acc[s];
-            if (live) r -= sm.kco[i] * sm.kr[i][v];
-            rhs[it][s] = r;
-          }
-        }
+      for (int bl = 0; bl < NB; ++bl) mma(yv, *(const f32x4*)&sm.po[1][n16][kSC * bl + 4 * g4], uo[bl][a]);
+      mma(yv, *(const f32x4*)&sm.pp[1][n16][4 * g4], un);
+      CT* yp = (CT*)p.y + y_base + v;
 #pragma unroll
-        for (int it = 0; it < PT; ++it) {
-          un[it] = zero4();
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        float out = yv[s];
+        if (live) out += sm.qco[i] * sm.kr[kSC + i][v];
+        const int t = c * kSC + i - p.t0;
+        if (t >= 0 && t < T) yp[(size_t)t * y_tok] = from_f<CT>(out);
+      }
 #pragma unroll
-          for (int kt = 0; kt <= it; ++kt) mma(un[it], arow(4, it, kt), rhs[kt]);
-        }
-        CT* yp = (CT*)p.y + y_base + v;
-#pragma unroll
-        for (int it = 0; it < PT; ++it) {
-          f32x4 yv = zero4();
-#pragma unroll
-          for (int kt = 0; kt < PT; ++kt) mma(yv, arow(3, it, kt), uo[kt][a]);
-#pragma unroll
-          for (int kt = 0; kt <= it; ++kt) mma(yv, arow(1, it, kt), un[kt]);
+      for (int bl = 0; bl < NB; ++bl)
+        if (bl == beta)
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
-            const int i = it * 16 + 4 * g4 + s;
-            float out = yv[s];
-            if (live) out += sm.qco[i] * sm.kr[P + i][v];
-            const int t = c * P + i - p.t0;
-            if (t >= 0 && t < T) yp[(size_t)t * y_tok] = from_f<CT>(out);
+            const int i = 4 * g4 + s;
+            if (i >= lo && i < hi) uo[bl][a][s] = un[s];
           }
-        }
+      if (p.ts_u) {   // training stash: this sub-chunk's net writes
+        float* us = p.ts_u + ((size_t)chain * p.nch + c) * kSC * D + v;
 #pragma unroll
-        for (int it = 0; it < PT; ++it)
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const int i = it * 16 + 4 * g4 + s;
-            if (i >= lo && i < hi) uo[it][a][s] = un[it][s];
-          }
-        if (p.ts_u) {   // training stash: this chunk's net writes
-          float* us = p.ts_u + ((size_t)chain * p.nch + c) * P * D + v;
-#pragma unroll
-          for (int it = 0; it < PT; ++it)
-#pragma unroll
-            for (int s = 0; s < 4; ++s) us[(size_t)(it * 16 + 4 * g4 + s) * D] = un[it][s];
-        }
+        for (int s = 0; s < 4; ++s) us[(size_t)(4 * g4 + s) * D] = un[s];
       }
     }
     if (p.ts_g && tid == 0 && vb == 0) p.ts_g[(size_t)chain * p.nch + c] = gacc;
-    // window keys for the next chunk: k_j decayed to this chunk's end, 8
-    // consecutive keys per thread
-    for (int u8 = tid; u8 < P * D / 8; u8 += kNT) {
-      const int j = u8 / DG, d = 8 * (u8 % DG);
-      uint4 w[W16];
+    // block beta's keys for the next sub-chunks: the slots this sub-chunk
+    // wrote take k_j decayed to its end, the others their old keys decayed
+    // over it (8 consecutive keys per thread); the block's offset restarts
+    {
+      const float olds = expf(sm.boff[beta] + sm.G[kSC - 1]);
+      for (int u8 = tid; u8 < kSC * D / 8; u8 += kNT) {
+        const int j = u8 / DG, d = 8 * (u8 % DG), sl = kSC * beta + j;
+        uint4 w[W16];
 #pragma unroll
-      for (int q16 = 0; q16 < W16; ++q16) w[q16] = *(const uint4*)&sm.x[2 * P + j][d + q16 * (16 / sizeof(CT))];
-      float kf[8];
-      unpack8(w, kf, (const CT*)nullptr);
-      float sc = sm.vsc[j];
-      if (j < lo || j >= hi) {   // a slot this chunk did not write: its old key, decayed over the chunk
-        sc = sm.gam[P - 1];
-        const f32x4 o0 = *(const f32x4*)&sm.vbd[j][d], o1 = *(const f32x4*)&sm.vbd[j][d + 4];
-        kf[0] = o0[0], kf[1] = o0[1], kf[2] = o0[2], kf[3] = o0[3];
-        kf[4] = o1[0], kf[5] = o1[1], kf[6] = o1[2], kf[7] = o1[3];
+        for (int q16 = 0; q16 < W16; ++q16) w[q16] = *(const uint4*)&sm.x[2 * kSC + j][d + q16 * (16 / sizeof(CT))];
+        float kf[8];
+        unpack8(w, kf, (const CT*)nullptr);
+        float sc = sm.vsc[j];
+        if (j < lo || j >= hi) {
+          sc = olds;
+          const f32x4 o0 = *(const f32x4*)&sm.vbd[sl][d], o1 = *(const f32x4*)&sm.vbd[sl][d + 4];
+          kf[0] = o0[0], kf[1] = o0[1], kf[2] = o0[2], kf[3] = o0[3];
+          kf[4] = o1[0], kf[5] = o1[1], kf[6] = o1[2], kf[7] = o1[3];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[e] *= sc;
+        *(f32x4*)&sm.vbd[sl][d] = (f32x4){kf[0], kf[1], kf[2], kf[3]};
+        *(f32x4*)&sm.vbd[sl][d + 4] = (f32x4){kf[4], kf[5], kf[6], kf[7]};
+        if constexpr (!Sm::KF) store8(&sm.vbx[sl][d], kf);
       }
-#pragma unroll
-      for (int e = 0; e < 8; ++e) kf[e] *= sc;
-      *(f32x4*)&sm.vbd[j][d] = (f32x4){kf[0], kf[1], kf[2], kf[3]};
-      *(f32x4*)&sm.vbd[j][d + 4] = (f32x4){kf[4], kf[5], kf[6], kf[7]};
-      store8(&sm.vbx[j][d], kf);
     }
-    gacc += sm.G[P - 1];
+    gacc += sm.G[kSC - 1];
   }
-#undef PP
   __syncthreads();
-  // window state out (and the final state after the last chunk): the value
-  // columns from their workgroup, the keys and decays from the first
+  if (p.c1 > p.c0) advance_boff(p.c1 - 1, sm.G[kSC - 1]);
+  __syncthreads();
+  // window state out (and the final state after the last sub-chunk): the
+  // value columns from their workgroup, the keys and decays from the first
 #pragma unroll
   for (int a = 0; a < VPW; ++a) {
     if (!vown(a)) continue;
 #pragma unroll
-    for (int it = 0; it < PT; ++it)
+    for (int bl = 0; bl < NB; ++bl)
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int i = it * 16 + 4 * g4 + s, v = vtile(a) * 16 + n16;
-        uw[i * D + v] = uo[it][a][s];
-        if (p.last && p.U_out) p.U_out[((size_t)chain * D + v) * P + i] = uo[it][a][s];
+        const int i = bl * kSC + 4 * g4 + s, v = vtile(a) * 16 + n16;
+        uw[i * D + v] = uo[bl][a][s];
+        if (p.last && p.U_out) p.U_out[((size_t)chain * D + v) * P + i] = uo[bl][a][s];
       }
   }
   if (vb != 0) return;
   for (int e = tid; e < P * D; e += kNT) {
     const int j = e / D, d = e % D;
-    vw[e] = sm.vbd[j][d];
-    if (p.last && p.Vb_out) p.Vb_out[((size_t)chain * D + d) * P + j] = sm.vbd[j][d];
+    const float kv = sm.vbd[j][d] * expf(sm.boff[j / kSC]);
+    vw[e] = kv;
+    if (p.last && p.Vb_out) p.Vb_out[((size_t)chain * D + d) * P + j] = kv;
   }
   if (tid == 0) p.gsum[chain] = gacc;
   if (p.last && !p.complete) {  // no compaction follows: A, B decayed since the last one
@@ -1060,7 +1065,6 @@ template <int D, int P>
 struct G3CompactSmem {
   G3Compact<D, P> k;
   alignas(16) float ab[kAB];
-  alignas(16) float vbd[P][D + 4];
 };
 
 // sum_r A_r (x) B_r as a [D][D] (v, k) matrix for the window kernel's reads,
@@ -1118,15 +1122,10 @@ __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
   for (int e = tid; e < Rm; e += kNT) sm.ab[e] = p.A[(size_t)chain * Rm + e];
   for (int e = tid; e < Rn; e += kNT) sm.ab[Rm + e] = p.Bf[(size_t)chain * Rn + e];
   const size_t cb = (size_t)chain * D * P;
-  for (int e = tid; e < D * P; e += kNT) {
-    const int i = e / D, d = e % D;
-    sm.k.ut[i][d] = p.U[cb + (size_t)i * p.u_sp + (size_t)d * p.u_sd];
-    sm.vbd[i][d] = p.Vb[cb + (size_t)i * p.u_sp + (size_t)d * p.u_sd];
-  }
   const float gacc = p.gsum ? p.gsum[chain] : 0.f;
   __syncthreads();
   const int qs = p.mode ? Ge::R : Ge::q;   // sketch columns
-  g3_compact<D, P>(sm.k, sm.ab, sm.vbd, gacc, p.sdec, p.sketch + (size_t)chain * Ge::n * qs,
+  g3_compact<D, P>(sm.k, sm.ab, p.U + cb, p.Vb + cb, (size_t)p.u_sp, (size_t)p.u_sd, gacc, p.sdec, p.sketch + (size_t)chain * Ge::n * qs,
                    p.stats ? p.stats + (size_t)blockIdx.x * 2 : nullptr, tid, p.mode);
   for (int e = tid; e < Rm; e += kNT) {
     p.A_out[(size_t)chain * Rm + e] = sm.ab[e];
@@ -1235,12 +1234,42 @@ int launch_compact(const G3CompactArgs& a, hipStream_t stream) {
 int compact_dispatch(const G3CompactArgs& a, hipStream_t stream) {
   if (a.N == 0) return GDNX_OK;
   if (a.D == 128 && a.P == 16) return launch_compact<128, 16>(a, stream);
+  if (a.D == 128 && a.P == 32) return launch_compact<128, 32>(a, stream);
+  if (a.D == 128 && a.P == 64) return launch_compact<128, 64>(a, stream);
   if (a.D == 64 && a.P == 16) return launch_compact<64, 16>(a, stream);
   if (a.D == 64 && a.P == 32) return launch_compact<64, 32>(a, stream);
+  if (a.D == 64 && a.P == 64) return launch_compact<64, 64>(a, stream);
   return set_error(GDNX_ERR_SHAPE, "gdn3_compact: unsupported head_dim %d / P %d", a.D, a.P);
 }
 
 inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// value split: ~512 workgroups, two per CU (NVB workgroups per chain, at
+// least one value tile each), or the smallest larger split whose LDS fits
+template <typename CT, int D, int P>
+int launch_window(const G3FwdArgs& a, int N, hipStream_t stream) {
+  constexpr int V2 = D / 16 < 2 ? D / 16 : 2, V4 = D / 16 < 4 ? D / 16 : 4, V8 = D / 16 < 8 ? D / 16 : 8;
+  static_assert(win_fits<CT, D, P, V8>(), "the widest split fits");
+  const int nvb = N >= 512 ? 1 : N >= 256 ? V2 : N >= 128 ? V4 : V8;
+  bool done = false;
+  if constexpr (win_fits<CT, D, P, 1>())
+    if (!done && nvb <= 1) {
+      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, 1>), dim3(N), dim3(kNT), 0, stream, a);
+      done = true;
+    }
+  if constexpr (win_fits<CT, D, P, V2>())
+    if (!done && nvb <= V2) {
+      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, V2>), dim3(N * V2), dim3(kNT), 0, stream, a);
+      done = true;
+    }
+  if constexpr (win_fits<CT, D, P, V4>())
+    if (!done && nvb <= V4) {
+      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, V4>), dim3(N * V4), dim3(kNT), 0, stream, a);
+      done = true;
+    }
+  if (!done) hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, V8>), dim3(N * V8), dim3(kNT), 0, stream, a);
+  return check_launch("gdn3_window_kernel");
+}
 
 template <typename CT, int D, int P>
 int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
@@ -1268,16 +1297,16 @@ int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
     rc = check_launch("fill_zero_kernel");
   }
   if (rc) return rc;
-  // chunks are global: chunk c covers tokens [c P, c P + P) of the whole
-  // sequence, of which this call holds [t0, t0 + T)
+  // sub-chunks are global: sub-chunk c covers tokens [16 c, 16 c + 16) of
+  // the whole sequence, of which this call holds [t0, t0 + T)
   const long long tend = (long long)a.t0 + a.T;
-  const int cg0 = a.t0 / P, cg1 = (int)((tend + P - 1) / P);
-  a.nch = (a.T + P - 1) / P;
+  const int cg0 = a.t0 / kSC, cg1 = (int)((tend + kSC - 1) / kSC);
+  a.nch = (a.T + kSC - 1) / kSC;
   G3Stash ts{nullptr, nullptr, nullptr};
-  if (a.train_states) ts = g3_stash(a.train_states, N, a.nch, a.T / a.Kc, D, P, Ge::RMN);
+  if (a.train_states) ts = g3_stash(a.train_states, N, a.nch, a.T / a.Kc, D, kSC, Ge::RMN);
   a.ts_u = ts.u;
   a.ts_g = ts.gacc;
-  const int per = a.Kc / P;
+  const int per = a.Kc / kSC;
   int event = 0;
   bool first = true;
   for (int c0 = cg0; c0 < cg1;) {
@@ -1288,20 +1317,8 @@ int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
     a.first = first && !carried;     // zero window state
     a.live = !first || carried;      // the Kronecker factors may be nonzero
     a.last = c1 == cg1;
-    a.complete = (long long)c1 * P <= tend && c1 % per == 0;
-    // value split: ~512 workgroups, two per CU (NVB workgroups per chain, at
-    // least one value tile each)
-    constexpr int V2 = D / 16 < 2 ? D / 16 : 2, V4 = D / 16 < 4 ? D / 16 : 4, V8 = D / 16 < 8 ? D / 16 : 8;
-    const int nvb = N >= 512 ? 1 : N >= 256 ? V2 : N >= 128 ? V4 : V8;
-    if (nvb == 1)
-      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, 1>), dim3(N), dim3(kNT), 0, stream, a);
-    else if (nvb == V2)
-      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, V2>), dim3(N * V2), dim3(kNT), 0, stream, a);
-    else if (nvb == V4)
-      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, V4>), dim3(N * V4), dim3(kNT), 0, stream, a);
-    else
-      hipLaunchKernelGGL((gdn3_window_kernel<CT, D, P, V8>), dim3(N * V8), dim3(kNT), 0, stream, a);
-    if ((rc = check_launch("gdn3_window_kernel"))) return rc;
+    a.complete = (long long)c1 * kSC <= tend && c1 % per == 0;
+    if ((rc = launch_window<CT, D, P>(a, N, stream))) return rc;
     if (a.complete) {
       G3CompactArgs ca{};
       ca.A = a.ab;
@@ -1382,22 +1399,29 @@ size_t gdn3_workspace_bytes(int N, int D, int P, int dtype) {
 }
 
 size_t gdn3_train_states_bytes(int N, int T, int D, int P, int Kc) {
-  const int nch = (T + P - 1) / P, ncomp = T / Kc;
+  (void)P;   // the stash is kept per 16-token sub-chunk whatever the window
+  const int nch = (T + kSC - 1) / kSC, ncomp = T / Kc;
   const int rmn = D == 128 ? G3D<128>::RMN : G3D<64>::RMN;
-  return g3_stash_bytes(N, nch, ncomp, D, P, rmn);
+  return g3_stash_bytes(N, nch, ncomp, D, kSC, rmn);
 }
 
 int gdn3_fwd_dispatch(const G3FwdArgs& a, hipStream_t stream) {
   if (a.dtype == GDNX_DTYPE_BF16) {
     if (a.D == 128 && a.P == 16) return run_gdn3_fwd<bf16, 128, 16>(a, stream);
+    if (a.D == 128 && a.P == 32) return run_gdn3_fwd<bf16, 128, 32>(a, stream);
+    if (a.D == 128 && a.P == 64) return run_gdn3_fwd<bf16, 128, 64>(a, stream);
     if (a.D == 64 && a.P == 16) return run_gdn3_fwd<bf16, 64, 16>(a, stream);
     if (a.D == 64 && a.P == 32) return run_gdn3_fwd<bf16, 64, 32>(a, stream);
+    if (a.D == 64 && a.P == 64) return run_gdn3_fwd<bf16, 64, 64>(a, stream);
   } else {
     if (a.D == 128 && a.P == 16) return run_gdn3_fwd<float, 128, 16>(a, stream);
+    if (a.D == 128 && a.P == 32) return run_gdn3_fwd<float, 128, 32>(a, stream);
+    if (a.D == 128 && a.P == 64) return run_gdn3_fwd<float, 128, 64>(a, stream);
     if (a.D == 64 && a.P == 16) return run_gdn3_fwd<float, 64, 16>(a, stream);
     if (a.D == 64 && a.P == 32) return run_gdn3_fwd<float, 64, 32>(a, stream);
+    if (a.D == 64 && a.P == 64) return run_gdn3_fwd<float, 64, 64>(a, stream);
   }
-  return set_error(GDNX_ERR_SHAPE, "gdn3: unsupported head_dim %d / P %d (128/16, 64/16, 64/32)", a.D, a.P);
+  return set_error(GDNX_ERR_SHAPE, "gdn3: unsupported head_dim %d / P %d (64 or 128 / 16, 32 or 64)", a.D, a.P);
 }
 
 int gdn3_compact_dispatch(const G3CompactArgs& a, hipStream_t stream) { return compact_dispatch(a, stream); }

@@ -286,7 +286,7 @@ static int g3_geom(int D, int R, int av, int ak, int bv, int bk, G3Geom& ge) {
   return GDNX_OK;
 }
 
-static bool g3_window_ok(int D, int P) { return (D == 128 && P == 16) || (D == 64 && (P == 16 || P == 32)); }
+static bool g3_window_ok(int D, int P) { return (D == 128 || D == 64) && (P == 16 || P == 32 || P == 64); }
 
 // the fused forward and the compaction are compiled for the layer's
 // geometry: rank 4 with (16, 16, 8, 8) at head dim 128, (8, 8, 8, 8) at 64
@@ -339,7 +339,7 @@ static int g3_fwd_args(G3FwdArgs& a, const void* q, const void* k, const void* v
   if ((rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge))) return rc;
   if ((rc = g3_layer_geom(head_dim, ge))) return rc;
   if (!g3_window_ok(head_dim, P))
-    return set_error(GDNX_ERR_SHAPE, "residual window P=%d unsupported for head_dim %d (128: 16; 64: 16, 32)",
+    return set_error(GDNX_ERR_SHAPE, "residual window P=%d unsupported for head_dim %d (16, 32 or 64)",
                      P, head_dim);
   if (compact_every < P || compact_every % P != 0)
     return set_error(GDNX_ERR_SHAPE, "compact_every=%d must be a positive multiple of P=%d", compact_every, P);

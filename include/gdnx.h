@@ -283,8 +283,10 @@ int gdnx_gdn3_num_compactions(int T, int P, int compact_every);
  *                gdnx_gdn3_chunk_bwd reads (net writes and accumulated log
  *                decay per window, the factors after every compaction), or
  *                NULL for inference
- * Supported: head_dim 128 with P = 16; head_dim 64 with P = 16 or 32;
- * R <= 4; a_v a_k <= 256, b_v b_k <= 256; compact_every a multiple of P. */
+ * Supported: head_dim 128 or 64 with P = 16, 32 or 64 (GDN3_P,
+ * gdn3/gdn3_upgrade.py:74); the layer's Kronecker geometry (R = 4 with
+ * factors (16, 16, 8, 8) at head_dim 128, (8, 8, 8, 8) at 64);
+ * compact_every a multiple of P. */
 int gdnx_gdn3_chunk_fwd(const void* q, const void* k, const void* v, int qkv_lanes,
                         const float* b_gates, const float* w_gates, int gate_channels,
                         const float* decay, const float* sketch, void* y, float* A_out,

@@ -153,8 +153,10 @@ def test_gdn3_state_forward_rejects_bad_arguments():
     assert "all be given" in lib.gdnx_last_error().decode()
     assert _g3_state_fwd(lib, t0=-3) == -2
     assert "t0" in lib.gdnx_last_error().decode()
-    assert _g3_state_fwd(lib, P=32) == -2
-    assert "P=32" in lib.gdnx_last_error().decode()
+    assert _g3_state_fwd(lib, P=48, Kc=48) == -2
+    assert "P=48" in lib.gdnx_last_error().decode()
+    assert _g3_state_fwd(lib, P=32) == -2   # compact_every 16 is not a multiple of 32
+    assert "compact_every" in lib.gdnx_last_error().decode()
     assert _g3_state_fwd(lib, Kc=24) == -2
     assert _g3_state_fwd(lib, ws=None) == -1
     assert _g3_state_fwd(lib, mode=2) == -1
@@ -177,7 +179,7 @@ def test_gdn3_decode_step_rejects_bad_arguments():
     assert _g3_decode(lib, qkv_lanes=3) == -2
     assert _g3_decode(lib, gate_ch=5) == -2
     assert _g3_decode(lib, NS=0) == -2
-    assert _g3_decode(lib, P=64) == -2
+    assert _g3_decode(lib, P=48) == -2
 
 
 def test_chan_decode_step_rejects_bad_arguments():

@@ -31,7 +31,8 @@ def _state(N, R, factors, P, seed, scale=1.0):
     return A, Bk, U, Vb
 
 
-@pytest.mark.parametrize("factors,P", [((16, 16, 8, 8), 16), ((8, 8, 8, 8), 16), ((8, 8, 8, 8), 32)])
+@pytest.mark.parametrize("factors,P", [((16, 16, 8, 8), 16), ((8, 8, 8, 8), 16), ((8, 8, 8, 8), 32),
+                                       ((16, 16, 8, 8), 64)])
 def test_kron_read_matches_oracle(gpu_lib, factors, P):
     from gdnx_amd import ops
     print(f"case: kron_read factors={factors} P={P}", flush=True)
@@ -51,7 +52,9 @@ def test_kron_read_matches_oracle(gpu_lib, factors, P):
 
 
 @pytest.mark.parametrize("factors,P,scale", [((16, 16, 8, 8), 16, 1.0), ((16, 16, 8, 8), 16, 0.0),
-                                             ((8, 8, 8, 8), 16, 0.3), ((8, 8, 8, 8), 32, 1.0)])
+                                             ((8, 8, 8, 8), 16, 0.3), ((8, 8, 8, 8), 32, 1.0),
+                                             ((16, 16, 8, 8), 32, 1.0), ((16, 16, 8, 8), 64, 0.5),
+                                             ((8, 8, 8, 8), 64, 1.0)])
 def test_compact_matches_oracle(gpu_lib, factors, P, scale):
     from gdnx_amd import ops
     print(f"case: compact factors={factors} P={P} scale={scale}", flush=True)
@@ -102,6 +105,12 @@ CASES = [
     (1, 64, 2, 1, 64, (8, 8, 8, 8), 16, 16, torch.float32, "lane", False),
     (1, 64, 1, 2, 64, (8, 8, 8, 8), 32, 32, torch.float32, "channel", False),
     (1, 64, 1, 2, 64, (8, 8, 8, 8), 32, 32, torch.bfloat16, "lane", True),
+    # P = 32 and 64: the window runs as 2 / 4 blocks of 16 slots
+    (1, 96, 1, 2, 128, (16, 16, 8, 8), 32, 64, torch.float32, "lane", False),
+    (1, 160, 1, 2, 128, (16, 16, 8, 8), 64, 64, torch.bfloat16, "channel", True),
+    (1, 200, 2, 1, 128, (16, 16, 8, 8), 64, 128, torch.float32, "channel", False),
+    (1, 256, 2, 1, 64, (8, 8, 8, 8), 64, 64, torch.float32, "lane", False),
+    (2, 100, 1, 2, 64, (8, 8, 8, 8), 64, 128, torch.bfloat16, "lane", True),
 ]
 
 
