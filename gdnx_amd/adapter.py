@@ -12,7 +12,7 @@ device tensor, or a Python float when GDN3_SYNC_COMP_ERR=1).
 class (the reference's GDN3LinearAttn, a subclass, or any object with those
 attributes).  Lane-expanded q/k/v (stride-0 views over M, as the layer builds
 them at :785-787) are read once per head.  y is differentiable in q, k, v,
-the gates and the decay (P = 16); the compaction error is not.
+the gates and the decay (P = 16, 32 or 64); the compaction error is not.
 """
 from __future__ import annotations
 

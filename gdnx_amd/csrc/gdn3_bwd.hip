@@ -29,29 +29,35 @@
 namespace gdnx {
 namespace {
 
-constexpr int BP = 16;  // the window P of the backward
+constexpr int BP = 16;  // tokens per sub-chunk (the forward's): the P-slot window is P / 16 blocks
 
-template <typename CT, int D>
+// S_kron^T stays in LDS when it fits beside the window blocks (SKL), else
+// each wave keeps the fragments of its key tiles in registers
+template <typename CT, int D, int P, bool SKL>
 struct alignas(16) G3BwdSmem {
+  static constexpr int NB = P / BP;
   static constexpr int LR = D + 4;                              // fp32 rows
-  static constexpr int LK = D + (sizeof(CT) == 2 ? 8 : 4);      // S_kron^T rows
-  static constexpr int LP = BP + 4;                             // P x P matrices
-  float h[BP][LR], q[BP][LR], k[BP][LR];  // H = b o k, Q, K of the chunk
-  float vb[BP][LR];                       // previous chunk's keys, then decayed to its end (Vbd_old)
-  float dy[BP][LR], u[BP][LR], uo[BP][LR];
+  static constexpr int LK = D + (sizeof(CT) == 2 ? 8 : 4);      // compute-dtype rows
+  static constexpr int LP = BP + 4;                             // 16 x 16 matrices
+  float h[BP][LR], q[BP][LR], k[BP][LR];  // H = b o k, Q, K of the sub-chunk
+  float dy[BP][LR], u[BP][LR];
   float dr[BP][LR];                       // dRhs (and the factors while S_kron^T is rebuilt)
-  CT skt[D][LK];                          // S_kron^T: skt[k][v] = sum_r A_r (x) B_r at (v, k)
-  float m0[BP][LP], m2[BP][LP];           // raw H K^T and H Vbd_old^T
-  float lm[BP][LP];                       // Lm
-  float aqt[BP][LP], tt[BP][LP], hot[BP][LP], qot[BP][LP];   // Aq^T, T^T, Ho^T, Qo^T
-  float w[BP][LP], z[BP][LP], vv[BP][LP], wq[BP][LP];        // gram gradient factors
-  float wt[BP][LP], zt[BP][LP], vvt[BP][LP], wqt[BP][LP];    // and their transposes
-  float lg[BP], lgp[BP], dec[BP], alpha[BP], cdot[BP];
+  CT kb[P][LK];                           // raw keys of the window blocks (block b: slots 16 b ..)
+  float uo[P][LR];                        // the blocks' net writes
+  CT skt[SKL ? D : 1][LK];                // S_kron^T: skt[k][v] = sum_r A_r (x) B_r at (v, k)
+  float m0[BP][LP], lm[BP][LP];           // raw H K^T, Lm
+  float aqt[BP][LP], tt[BP][LP];          // Aq^T, T^T
+  float w[BP][LP], z[BP][LP], wt[BP][LP], zt[BP][LP];   // dLm, dAq gradient factors and transposes
+  float m2[NB][BP][LP];                   // per block: raw H Vbd_b^T (keys decayed)
+  float hot[NB][BP][LP], qot[NB][BP][LP]; // Ho_b^T, Qo_b^T
+  float vv[NB][BP][LP], wq[NB][BP][LP];   // dHo_b, dQo_b gradient factors
+  float kd[P];                            // block slot: its key's decay to the start of the sub-chunk
+  float lg[BP], lgp[P], dec[BP], alpha[BP], cdot[BP];
   float G[BP], e2[BP], kco[BP], qco[BP], vsc[BP], dc[BP], su[BP];
-  float red[7][4][BP];                    // per-wave partial per-token sums, slots kR*
+  float red[8][4][BP];                    // per-wave partial per-token sums, slots kR*
   float carry[4];
 };
-constexpr int kRdA = 0, kRgRow = 1, kRgCol = 2, kRhG = 3, kRqG = 4, kRsvb = 5, kRdb = 6;
+constexpr int kRdA = 0, kRgRow = 1, kRgCol = 2, kRhG = 3, kRqG = 4, kRsvb = 5, kRdb = 6, kRdd = 7;
 
 template <typename CT>
 __device__ __forceinline__ void load8(const CT* p, float* f);
@@ -144,6 +150,25 @@ __device__ __forceinline__ f32x4 tile_nt_split(const float* arow, const float* b
   return acc;
 }
 
+// The same with B a raw compute-dtype row: bf16 values are exact (no lo part)
+template <int K>
+__device__ __forceinline__ f32x4 tile_nt_fb(const float* arow, const bf16* brow, int g4, bool a_exact) {
+  f32x4 acc = zero4();
+#pragma unroll
+  for (int kb = 0; kb < K; kb += 32) {
+    bf16x8 ah, al;
+    split_frag(arow + kb, g4, ah, al);
+    const bf16x8 bh = ld_frag(brow + kb, g4);
+    mma(acc, ah, bh);
+    if (!a_exact) mma(acc, al, bh);
+  }
+  return acc;
+}
+template <int K>
+__device__ __forceinline__ f32x4 tile_nt_fb(const float* arow, const float* brow, int g4, bool) {
+  return tile_nt<float, K>(arow, brow, g4);
+}
+
 // 8 values to 8 consecutive entries of the compute dtype (16-byte aligned)
 __device__ __forceinline__ void store8c(float* p, const float* f) { store8f(p, f); }
 __device__ __forceinline__ void store8c(bf16* p, const float* f) {
@@ -164,14 +189,20 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
-template <typename CT, int D>
+template <typename CT, int D, int P>
 __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
   typedef G3D<D> Ge;
-  typedef G3BwdSmem<CT, D> Sm;
+  constexpr bool SKL = sizeof(G3BwdSmem<CT, D, P, true>) <= 160 * 1024;
+  typedef G3BwdSmem<CT, D, P, SKL> Sm;
   __shared__ Sm sm;
   static_assert(sizeof(Sm) <= 160 * 1024, "LDS budget");
-  constexpr int P = BP, DG = D / 8, UNITS = P * DG, NDT = D / 16, VPW = NDT / 4, LR = Sm::LR;
+  constexpr int NB = Sm::NB, DG = D / 8, UNITS = BP * DG, NDT = D / 16, VPW = NDT / 4, LR = Sm::LR;
   static_assert(UNITS <= kNT && VPW >= 1, "one load unit per thread, a tile per wave");
+  static_assert(P % BP == 0 && NB >= 1 && NB <= 4, "whole blocks of 16 slots, at most 4");
+  constexpr int NT = 2 + 2 * NB;      // gram / gradient tiles: H K^T, Q K^T, then H, Q against block b
+  constexpr int TPW = (NT + 3) / 4;   // tile ti on wave ti mod 4
+  constexpr int KS = FragT<CT>::KSTEP;
+  typedef typename FragT<CT>::type Frag;
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g4 = lane >> 4, n16 = lane & 15;
   const int H = p.H, M = p.M, T = p.T;
@@ -189,16 +220,24 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
   const size_t dec_base = ((size_t)b * T * H + h) * M + m;
   const size_t y_tok = (size_t)H * M * D;
   const size_t y_base = (((size_t)b * T * H + h) * M + m) * D;
-  const int nch = (T + P - 1) / P, per = p.Kc / P, ncomp = T / p.Kc;
-  const G3Stash ts = g3_stash(const_cast<void*>(p.train_states), N, nch, ncomp, D, P, Ge::RMN);
+  const int nch = (T + BP - 1) / BP, per = p.Kc / BP, ncomp = T / p.Kc;
+  const G3Stash ts = g3_stash(const_cast<void*>(p.train_states), N, nch, ncomp, D, BP, Ge::RMN);
 
-  f32x4 dUc[VPW], dVc[VPW];   // carried: d/dU and d/dVbd of the chunk being processed (its value / key tiles)
+  // carried per window block b (this wave's value / key tiles): dUa, d/dU of
+  // the sub-chunk the block holds (complete once every later reader is
+  // processed), and dVa, d/dVbd of its keys as seen at the start of the
+  // sub-chunk after the one being processed
+  f32x4 dUa[NB][VPW], dVa[NB][VPW];
 #pragma unroll
-  for (int a = 0; a < VPW; ++a) dUc[a] = dVc[a] = zero4();
-  float dgacc = 0.f;          // d/dGacc of the chunk after the current one
+  for (int bl = 0; bl < NB; ++bl)
+#pragma unroll
+    for (int a = 0; a < VPW; ++a) dUa[bl][a] = dVa[bl][a] = zero4();
+  float dgacc = 0.f;          // d/dGacc of the sub-chunk after the current one
+  Frag skf[SKL ? 1 : VPW][SKL ? 1 : D / KS];   // S_kron^T fragments of this wave's key tiles (!SKL)
 
-  // the factors of the interval a chunk rebuilds S_kron^T from, fetched into
-  // registers a chunk ahead (their loads land while the chunk before computes)
+  // the factors of the interval a sub-chunk rebuilds S_kron^T from, fetched
+  // into registers a sub-chunk ahead (their loads land while the one before
+  // computes)
   constexpr int NAB = (Ge::RMN + kNT - 1) / kNT;
   float abr[NAB];
   auto rebuilds = [&](int cc) { return cc / per > 0 && (cc == nch - 1 || (cc + 1) % per == 0); };
@@ -212,21 +251,57 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
   };
   if (nch > 0 && rebuilds(nch - 1)) fetch_ab(nch - 1);
 
+  // a window block: sub-chunk mb's raw keys and net writes (zero before the
+  // sequence) into block mb mod NB
+  auto load_block = [&](int mb, Row8<CT>& rk, Row8<float>& ru) {
+    zero8(rk), zero8(ru);
+    if (has_unit && mb >= 0) {
+      raw8<CT>((const CT*)p.k + qkv_base + (size_t)(mb * BP + ui) * qkv_tok + ud, rk);
+      raw8<float>(ts.u + ((size_t)chain * nch + mb) * BP * D + (size_t)ui * D + ud, ru);
+    }
+  };
+  auto store_block = [&](int mb, const Row8<CT>& rk, const Row8<float>& ru) {
+    if (!has_unit) return;
+    const int sl = BP * (((mb % NB) + NB) % NB) + ui;
+#pragma unroll
+    for (int i = 0; i < (int)(sizeof(CT) / 2); ++i) *(uint4*)&sm.kb[sl][ud + i * (16 / sizeof(CT))] = rk.w[i];
+    *(uint4*)&sm.uo[sl][ud] = ru.w[0];
+    *(uint4*)&sm.uo[sl][ud + 4] = ru.w[1];
+  };
+  // the blocks the last sub-chunk sees whole (sub-chunks nch - NB .. nch - 2)
+  for (int mb = nch - NB; mb <= nch - 2; ++mb) {
+    Row8<CT> rk;
+    Row8<float> ru;
+    load_block(mb, rk, ru);
+    store_block(mb, rk, ru);
+  }
+
   for (int c = nch - 1; c >= 0; --c) {
     const int iv = c / per;
     const bool live = iv > 0;
-    if ((c + 1) % per == 0 && (long long)(c + 1) * P <= T) dgacc = 0.f;  // compaction after this chunk
+    const int beta = c % NB;
+    if ((c + 1) % per == 0 && (long long)(c + 1) * BP <= T) dgacc = 0.f;  // compaction after this sub-chunk
     const float gacc = ts.gacc[(size_t)chain * nch + c];
-    __syncthreads();  // the previous chunk is done with LDS
+    f32x4 dUc[VPW], dVc[VPW];   // this sub-chunk's complete d/dU and d/d(keys decayed to its end)
+#pragma unroll
+    for (int bl = 0; bl < NB; ++bl)
+      if (bl == beta)
+#pragma unroll
+        for (int a = 0; a < VPW; ++a) {
+          dUc[a] = dUa[bl][a];
+          dVc[a] = dVa[bl][a];
+        }
+    __syncthreads();  // the previous sub-chunk is done with LDS
 
-    // the chunk's inputs (and the previous chunk's keys / decays), loaded raw
+    // the sub-chunk's inputs, the block entering the window (sub-chunk c -
+    // NB) and the decays of the P tokens before the sub-chunk, loaded raw
     // before the S_kron^T rebuild so that their latency hides behind it
-    const int t = c * P + ui;
+    const int t = c * BP + ui;
     const bool tv = has_unit && t < T;
     Row8<CT> rk, rq, rv, rdy, rkp;
     Row8<float> rb, rw, ru, ruo;
     float bs = 0.f, ws = 0.f, dv = 1.f, dvp = 1.f;
-    zero8(rk), zero8(rq), zero8(rv), zero8(rdy), zero8(rkp), zero8(rb), zero8(rw), zero8(ru), zero8(ruo);
+    zero8(rk), zero8(rq), zero8(rv), zero8(rdy), zero8(rb), zero8(rw), zero8(ru);
     if (tv) {
       raw8<CT>((const CT*)p.k + qkv_base + (size_t)t * qkv_tok + ud, rk);
       raw8<CT>((const CT*)p.q + qkv_base + (size_t)t * qkv_tok + ud, rq);
@@ -240,7 +315,7 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         ws = p.wg[gate_base + (size_t)t * gate_tok];
       }
       dv = p.dec[dec_base + (size_t)t * dec_tok];
-      raw8<float>(ts.u + ((size_t)chain * nch + c) * P * D + (size_t)ui * D + ud, ru);
+      raw8<float>(ts.u + ((size_t)chain * nch + c) * BP * D + (size_t)ui * D + ud, ru);
     }
     // the erase gates at this wave's key tiles (used in G), loaded with the rest:
     // in G they would sit between stores the compiler cannot reorder them past
@@ -249,26 +324,18 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     for (int a = 0; a < VPW; ++a)
 #pragma unroll
       for (int s4 = 0; s4 < 4; ++s4) {
-        const int tt_ = c * P + 4 * g4 + s4, d = 16 * (wave * VPW + a) + n16;
+        const int tt_ = c * BP + 4 * g4 + s4, d = 16 * (wave * VPW + a) + n16;
         bgc[a][s4] = tt_ < T ? (gc > 1 ? p.bg[gate_base + (size_t)tt_ * gate_tok + d]
                                        : p.bg[gate_base + (size_t)tt_ * gate_tok]) : 0.f;
       }
-    if (has_unit && c > 0) {
-      const int tp = t - P;
-      raw8<CT>((const CT*)p.k + qkv_base + (size_t)tp * qkv_tok + ud, rkp);
-      dvp = p.dec[dec_base + (size_t)tp * dec_tok];
-      raw8<float>(ts.u + ((size_t)chain * nch + c - 1) * P * D + (size_t)ui * D + ud, ruo);
+    load_block(c - NB, rkp, ruo);
+    if (tid < P) {
+      const int tp = c * BP - P + tid;
+      if (tp >= 0) dvp = p.dec[dec_base + (size_t)tp * dec_tok];
     }
 
-    // ---- S_kron^T of this interval (the factors of compaction iv - 1), rebuilt on entry:
-    // skt[k][v], k = ik b_k + jk, v = iv' b_v + jv.  A thread takes one row k
-    // and a group of 8 values of iv': the 8 x 8 products of A_r[iv'][ik] and
-    // B_r[jv][jk] are 64 consecutive v of that row (eight 16-byte stores);
-    // consecutive lanes take consecutive rows, so the stores spread over the
-    // banks ----
+    // ---- S_kron^T of this interval (the factors of compaction iv - 1), rebuilt on entry ----
     if (live && rebuilds(c)) {
-      static_assert(Ge::bv == 8 && Ge::av % 8 == 0, "blocks of 8 x 8 factor entries");
-      constexpr int NGA = Ge::av / 8;                 // groups of iv' per row
       float* st = &sm.dr[0][0];
 #pragma unroll
       for (int u = 0; u < NAB; ++u) {
@@ -276,45 +343,77 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         if (e < Ge::RMN) st[e] = abr[u];
       }
       __syncthreads();
-      if (tid < D * NGA) {
-        const int kr = tid % D, grp = tid / D, ik = kr / Ge::bk, jk = kr % Ge::bk;
-        const float* Bf = st + Ge::R * Ge::m;
-        float bb[Ge::R][8];
+      const float* Bf = st + Ge::R * Ge::m;
+      if constexpr (SKL) {
+        // skt[k][v], k = ik b_k + jk, v = iv' b_v + jv.  A thread takes one row
+        // k and a group of 8 values of iv': the 8 x 8 products of A_r[iv'][ik]
+        // and B_r[jv][jk] are 64 consecutive v of that row (eight 16-byte
+        // stores); consecutive lanes take consecutive rows, so the stores
+        // spread over the banks
+        static_assert(Ge::bv == 8 && Ge::av % 8 == 0, "blocks of 8 x 8 factor entries");
+        constexpr int NGA = Ge::av / 8;                 // groups of iv' per row
+        if (tid < D * NGA) {
+          const int kr = tid % D, grp = tid / D, ik = kr / Ge::bk, jk = kr % Ge::bk;
+          float bb[Ge::R][8];
 #pragma unroll
-        for (int r = 0; r < Ge::R; ++r)
+          for (int r = 0; r < Ge::R; ++r)
 #pragma unroll
-          for (int jv = 0; jv < 8; ++jv) bb[r][jv] = Bf[r * Ge::n + jv * Ge::bk + jk];
+            for (int jv = 0; jv < 8; ++jv) bb[r][jv] = Bf[r * Ge::n + jv * Ge::bk + jk];
 #pragma unroll 2
-        for (int i8 = 0; i8 < 8; ++i8) {
-          const int ivv = grp * 8 + i8;
-          float a[Ge::R];
+          for (int i8 = 0; i8 < 8; ++i8) {
+            const int ivv = grp * 8 + i8;
+            float a[Ge::R];
 #pragma unroll
-          for (int r = 0; r < Ge::R; ++r) a[r] = st[r * Ge::m + ivv * Ge::ak + ik];
-          float sv[8];
+            for (int r = 0; r < Ge::R; ++r) a[r] = st[r * Ge::m + ivv * Ge::ak + ik];
+            float sv[8];
 #pragma unroll
-          for (int jv = 0; jv < 8; ++jv) {
-            float x = 0.f;
+            for (int jv = 0; jv < 8; ++jv) {
+              float x = 0.f;
 #pragma unroll
-            for (int r = 0; r < Ge::R; ++r) x += a[r] * bb[r][jv];
-            sv[jv] = x;
+              for (int r = 0; r < Ge::R; ++r) x += a[r] * bb[r][jv];
+              sv[jv] = x;
+            }
+            store8c(&sm.skt[kr][ivv * Ge::bv], sv);
           }
-          store8c(&sm.skt[kr][ivv * Ge::bv], sv);
+        }
+      } else {
+        // the fragments this lane feeds the Kronecker products: row k = d of
+        // its key tiles, values v = kb KS + (the fragment's k set)
+#pragma unroll
+        for (int a = 0; a < VPW; ++a) {
+          const int d = 16 * (wave * VPW + a) + n16, ik = d >> Ge::lbk, jk = d & (Ge::bk - 1);
+#pragma unroll
+          for (int kb = 0; kb < D / KS; ++kb) {
+            float sv[sizeof(CT) == 2 ? 8 : 4];
+#pragma unroll
+            for (int e = 0; e < (int)(sizeof(CT) == 2 ? 8 : 4); ++e) {
+              const int v = kb * KS + (e < 4 ? 4 * g4 + e : 16 + 4 * g4 + e - 4);
+              const int ivv = v >> Ge::lbv, jv = v & (Ge::bv - 1);
+              float x = 0.f;
+#pragma unroll
+              for (int r = 0; r < Ge::R; ++r) x += st[r * Ge::m + ivv * Ge::ak + ik] * Bf[r * Ge::n + jv * Ge::bk + jk];
+              sv[e] = x;
+            }
+            if constexpr (sizeof(CT) == 2)
+              skf[a][kb] = (bf16x8){(bf16)sv[0], (bf16)sv[1], (bf16)sv[2], (bf16)sv[3],
+                                    (bf16)sv[4], (bf16)sv[5], (bf16)sv[6], (bf16)sv[7]};
+            else
+              skf[a][kb] = (f32x4){sv[0], sv[1], sv[2], sv[3]};
+          }
         }
       }
     }
     if (c > 0 && rebuilds(c - 1)) fetch_ab(c - 1);
 
-    // ---- A: the chunk's inputs to LDS (h = b o k, alpha, log decays) ----
+    // ---- A: the sub-chunk's inputs to LDS (h = b o k, alpha, log decays), the entering block ----
     float vf[8], wf[8];
     {
-      float kf[8], qf[8], bf[8], dyf[8], kp[8], us[8], uos[8];
+      float kf[8], qf[8], bf[8], dyf[8], us[8];
       cvt8(rk, kf);
       cvt8(rq, qf);
       cvt8(rv, vf);
       cvt8(rdy, dyf);
-      cvt8(rkp, kp);
       cvt8(ru, us);
-      cvt8(ruo, uos);
       if (gc > 1) {
         cvt8(rb, bf);
         cvt8(rw, wf);
@@ -335,11 +434,10 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         store8f(&sm.h[ui][ud], hf);
         store8f(&sm.q[ui][ud], qf);
         store8f(&sm.k[ui][ud], kf);
-        store8f(&sm.vb[ui][ud], kp);
         store8f(&sm.dy[ui][ud], dyf);
         store8f(&sm.u[ui][ud], us);
-        store8f(&sm.uo[ui][ud], uos);
       }
+      store_block(c - NB, rkp, ruo);
       if constexpr (DG == 16) {   // a token row is one DPP row
         part = row_sum16(part);
       } else {
@@ -351,63 +449,97 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         sm.alpha[ui] = stable_alpha_f(part);
         sm.lg[ui] = tv ? log_decay(dv) : 0.f;
         sm.dec[ui] = dv;
-        sm.lgp[ui] = c > 0 ? log_decay(dvp) : 0.f;
       }
+      if (tid < P) sm.lgp[tid] = c * BP - P + tid >= 0 ? log_decay(dvp) : 0.f;
     }
     __syncthreads();
 
-    // ---- B: per-token scalars (every wave scans for itself) and the four grams ----
-    float gl = lane < P ? sm.lg[lane] : 0.f, glp = lane < P ? sm.lgp[lane] : 0.f;
+    // ---- B: per-token scalars and key decays (every wave scans for itself), the grams ----
+    float gl = lane < BP ? sm.lg[lane] : 0.f;
+#pragma unroll
+    for (int off = 1; off < BP; off <<= 1) {
+      const float o = __shfl_up(gl, off, 64);
+      if (lane >= off) gl += o;
+    }
+    // lane j < P: token 16 c - P + j (block (c + j / 16) mod NB, slot j mod 16),
+    // its key decayed to the start of this sub-chunk by exp(sum of the later log decays)
+    float lp = lane < P ? sm.lgp[lane] : 0.f;
 #pragma unroll
     for (int off = 1; off < P; off <<= 1) {
-      const float o = __shfl_up(gl, off, 64), op = __shfl_up(glp, off, 64);
-      if (lane >= off) {
-        gl += o;
-        glp += op;
-      }
+      const float o = __shfl_up(lp, off, 64);
+      if (lane >= off) lp += o;
     }
-    const float gl_last = __shfl(gl, P - 1, 64), glp_last = __shfl(glp, P - 1, 64);
-    const float vscp = expf(glp_last - glp);   // lane p: previous chunk's key p decayed to its end
-    if (wave == 0 && lane < P) {
-      const float e2 = expf(2.f * (gacc + gl));
-      sm.G[lane] = gl;
-      sm.e2[lane] = e2;
-      sm.kco[lane] = sm.alpha[lane] * e2;
-      sm.qco[lane] = e2;
-      sm.vsc[lane] = expf(gl_last - gl);
+    const float kdv = expf(__shfl(lp, P - 1, 64) - lp);
+    const float gl_last = __shfl(gl, BP - 1, 64);
+    if (wave == 0) {
+      if (lane < BP) {
+        const float e2 = expf(2.f * (gacc + gl));
+        sm.G[lane] = gl;
+        sm.e2[lane] = e2;
+        sm.kco[lane] = sm.alpha[lane] * e2;
+        sm.qco[lane] = e2;
+        sm.vsc[lane] = expf(gl_last - gl);
+      }
+      if (lane < P) sm.kd[BP * ((c + lane / BP) % NB) + lane % BP] = kdv;
     }
     {
-      const float* ar = (wave & 1) ? &sm.q[0][0] : &sm.h[0][0];
-      const float* br = (wave < 2) ? &sm.k[0][0] : &sm.vb[0][0];
-      f32x4 acc;
-      if constexpr (sizeof(CT) == 2)   // bf16 IO: q, k and the raw previous keys are bf16 values exactly
-        acc = tile_nt_split<D>(ar + n16 * LR, br + n16 * LR, g4, (wave & 1) != 0, true);
-      else
-        acc = tile_nt<float, D>(ar + n16 * LR, br + n16 * LR, g4);
       const int j = n16;
-      const float Gj = __shfl(gl, j, 64), vj = __shfl(vscp, j, 64);
+      const float Gj = __shfl(gl, j, 64);
+      float Gi[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int i = 4 * g4 + s;
-        const float Gi = __shfl(gl, i, 64);
-        const float al = sm.alpha[i], ga = expf(Gi);
-        if (wave == 0) {
-          sm.m0[i][j] = acc[s];
-          sm.lm[i][j] = (j < i) ? al * expf(Gi - Gj) * acc[s] : 0.f;
-        } else if (wave == 1) {
-          sm.aqt[j][i] = (j <= i) ? expf(Gi - Gj) * acc[s] : 0.f;
-        } else if (wave == 2) {
-          const float m2 = vj * acc[s];
-          sm.m2[i][j] = m2;
-          sm.hot[j][i] = (j >= i) ? al * ga * m2 : 0.f;
-        } else {
-          sm.qot[j][i] = (j >= i) ? ga * vj * acc[s] : 0.f;
+      for (int s = 0; s < 4; ++s) Gi[s] = __shfl(gl, 4 * g4 + s, 64);
+#pragma unroll
+      for (int r = 0; r < TPW; ++r) {
+        const int ti = wave + 4 * r;
+        if (ti < NT) {
+          const bool isq = ti & 1;
+          const float* ar = isq ? &sm.q[0][0] : &sm.h[0][0];
+          const int bl = (ti - 2) >> 1;
+          f32x4 acc;
+          if (ti < 2) {
+            if constexpr (sizeof(CT) == 2)   // bf16 IO: q and k are bf16 values exactly
+              acc = tile_nt_split<D>(ar + n16 * LR, &sm.k[n16][0], g4, isq, true);
+            else
+              acc = tile_nt<float, D>(ar + n16 * LR, &sm.k[n16][0], g4);
+          } else {
+            acc = tile_nt_fb<D>(ar + n16 * LR, &sm.kb[BP * bl + n16][0], g4, isq);
+          }
+          if (ti == 0) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const int i = 4 * g4 + s;
+              sm.m0[i][j] = acc[s];
+              sm.lm[i][j] = (j < i) ? sm.alpha[i] * expf(Gi[s] - Gj) * acc[s] : 0.f;
+            }
+          } else if (ti == 1) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const int i = 4 * g4 + s;
+              sm.aqt[j][i] = (j <= i) ? expf(Gi[s] - Gj) * acc[s] : 0.f;
+            }
+          } else {
+            // block bl holds window tokens jb 16 .. jb 16 + 15 (jb = (bl - c) mod NB)
+            const int jb = ((bl - c) % NB + NB) % NB;
+            const float kdj = __shfl(kdv, jb * BP + j, 64);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const int i = 4 * g4 + s;
+              const bool vis = bl != beta || j >= i;
+              const float ga = expf(Gi[s]), m2 = kdj * acc[s];
+              if (!isq) {
+                sm.m2[bl][i][j] = m2;
+                sm.hot[bl][j][i] = vis ? sm.alpha[i] * ga * m2 : 0.f;
+              } else {
+                sm.qot[bl][j][i] = vis ? ga * m2 : 0.f;
+              }
+            }
+          }
         }
       }
     }
     __syncthreads();
 
-    // ---- C: T = (I + Lm)^-1 (wave 0); the previous chunk's keys decayed to its end ----
+    // ---- C: T = (I + Lm)^-1 (wave 0) ----
     if (wave == 0) {
       // Lm is strictly lower: (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8)
       f32x4 xa, ta;
@@ -433,15 +565,9 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
 #pragma unroll
       for (int s = 0; s < 4; ++s) sm.tt[n16][4 * g4 + s] = ta[s];   // T^T
     }
-    {
-      const float f = __shfl(vscp, ui & 63, 64);
-      if (has_unit)
-#pragma unroll
-        for (int e = 0; e < 8; ++e) sm.vb[ui][ud + e] *= f;
-    }
     __syncthreads();
 
-    // ---- D: dU_tot = dU + Aq^T dY, dRhs = T^T dU_tot, the previous chunk's dU ----
+    // ---- D: dU_tot = dU + Aq^T dY, dRhs = T^T dU_tot, the blocks' dU ----
 #pragma unroll
     for (int a = 0; a < VPW; ++a) {
       const int col = 16 * (wave * VPW + a) + n16;
@@ -452,71 +578,84 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
       mma(drh, ld_frag(&sm.tt[n16][0], g4), dut);
 #pragma unroll
       for (int s = 0; s < 4; ++s) sm.dr[4 * g4 + s][col] = drh[s];
-      f32x4 nd = zero4();
-      mma(nd, ld_frag(&sm.qot[n16][0], g4), dYf);
-      mma(nd, ld_frag(&sm.hot[n16][0], g4), -drh);
-      dUc[a] = nd;
+#pragma unroll
+      for (int bl = 0; bl < NB; ++bl) {
+        f32x4 nd = zero4();
+        mma(nd, ld_frag(&sm.qot[bl][n16][0], g4), dYf);
+        mma(nd, ld_frag(&sm.hot[bl][n16][0], g4), -drh);
+        dUa[bl][a] = (bl == beta) ? nd : dUa[bl][a] + nd;
+      }
     }
     __syncthreads();
 
-    // ---- E: gradients of the P x P coefficients, the Kronecker products,
-    // the value / write-gate gradients ----
+    // ---- E: gradients of the 16 x 16 coefficient tiles, the Kronecker
+    // products, the value / write-gate gradients ----
     {
-      const float* ar = (wave == 0 || wave == 2) ? &sm.dr[0][0] : &sm.dy[0][0];
-      const float* br = (wave < 2) ? &sm.u[0][0] : &sm.uo[0][0];
-      f32x4 acc;
-      if constexpr (sizeof(CT) == 2)   // bf16 IO: dY holds bf16 values exactly
-        acc = tile_nt_split<D>(ar + n16 * LR, br + n16 * LR, g4, wave == 1 || wave == 3, false);
-      else
-        acc = tile_nt<float, D>(ar + n16 * LR, br + n16 * LR, g4);
-      if (wave == 0 || wave == 2) acc = -acc;
       const int j = n16;
       const float Gj = sm.G[j];
-      float cg = 0.f;
+      float cg = 0.f, rda[4] = {0.f, 0.f, 0.f, 0.f}, rg[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int r = 0; r < TPW; ++r) {
+        const int ti = wave + 4 * r;
+        if (ti < NT) {
+          const bool isq = ti & 1;   // dY rows (else -dRhs)
+          const float* ar = isq ? &sm.dy[0][0] : &sm.dr[0][0];
+          const int bl = (ti - 2) >> 1;
+          const float* br = ti < 2 ? &sm.u[0][0] : &sm.uo[BP * bl][0];
+          f32x4 acc;
+          if constexpr (sizeof(CT) == 2)   // bf16 IO: dY holds bf16 values exactly
+            acc = tile_nt_split<D>(ar + n16 * LR, br + n16 * LR, g4, isq, false);
+          else
+            acc = tile_nt<float, D>(ar + n16 * LR, br + n16 * LR, g4);
+          if (!isq) acc = -acc;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int i = 4 * g4 + s;
+            const float Gi = sm.G[i], al = sm.alpha[i], ga = expf(Gi);
+            if (ti == 0) {          // dLm (j < i)
+              const float x = (j < i) ? acc[s] : 0.f, e = expf(Gi - Gj), m0 = sm.m0[i][j];
+              const float wv = x * al * e;
+              sm.w[i][j] = wv;
+              sm.wt[j][i] = wv;
+              rda[s] += x * e * m0;
+              const float g = x * al * e * m0;
+              rg[s] += g;
+              cg += g;
+            } else if (ti == 1) {   // dAq (j <= i)
+              const float x = (j <= i) ? acc[s] : 0.f, e = expf(Gi - Gj);
+              const float zv = x * e;
+              sm.z[i][j] = zv;
+              sm.zt[j][i] = zv;
+              const float g = x * sm.aqt[j][i];
+              rg[s] += g;
+              cg += g;
+            } else {
+              const bool vis = bl != beta || j >= i;
+              const float x = vis ? acc[s] : 0.f;
+              if (!isq) {           // dHo_b
+                sm.vv[bl][i][j] = x * al * ga;
+                rda[s] += x * ga * sm.m2[bl][i][j];
+                rg[s] += x * sm.hot[bl][j][i];
+              } else {              // dQo_b
+                sm.wq[bl][i][j] = x * ga;
+                rg[s] += x * sm.qot[bl][j][i];
+              }
+            }
+          }
+        }
+      }
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int i = 4 * g4 + s;
-        const float Gi = sm.G[i], al = sm.alpha[i], ga = expf(Gi);
-        float rda = 0.f, rg = 0.f;
-        if (wave == 0) {        // dLm (j < i)
-          const float x = (j < i) ? acc[s] : 0.f, e = expf(Gi - Gj), m0 = sm.m0[i][j];
-          const float wv = x * al * e;
-          sm.w[i][j] = wv;
-          sm.wt[j][i] = wv;
-          rda = x * e * m0;
-          rg = x * al * e * m0;
-          cg += rg;
-        } else if (wave == 1) { // dAq (j <= i)
-          const float x = (j <= i) ? acc[s] : 0.f, e = expf(Gi - Gj);
-          const float zv = x * e;
-          sm.z[i][j] = zv;
-          sm.zt[j][i] = zv;
-          rg = x * sm.aqt[j][i];
-          cg += rg;
-        } else if (wave == 2) { // dHo (p = j >= i)
-          const float x = (j >= i) ? acc[s] : 0.f;
-          const float vv = x * al * ga;
-          sm.vv[i][j] = vv;
-          sm.vvt[j][i] = vv;
-          rda = x * ga * sm.m2[i][j];
-          rg = x * sm.hot[j][i];
-        } else {                // dQo (p = j >= i)
-          const float x = (j >= i) ? acc[s] : 0.f;
-          const float wq = x * ga;
-          sm.wq[i][j] = wq;
-          sm.wqt[j][i] = wq;
-          rg = x * sm.qot[j][i];
-        }
-        rda = row_prefix16(rda);
-        rg = row_prefix16(rg);
+        const float a_ = row_prefix16(rda[s]), g_ = row_prefix16(rg[s]);
         if (n16 == 15) {
-          sm.red[kRdA][wave][i] = rda;
-          sm.red[kRgRow][wave][i] = rg;
+          sm.red[kRdA][wave][i] = a_;
+          sm.red[kRgRow][wave][i] = g_;
         }
       }
       cg += __shfl_xor(cg, 16, 64);
       cg += __shfl_xor(cg, 32, 64);
-      if (g4 == 0) sm.red[kRgCol][wave][j] = cg;   // zero for waves 2, 3
+      if (g4 == 0) sm.red[kRgCol][wave][j] = cg;   // zero on waves without tile 0 or 1
     }
     // Kronecker products G_h = dRhs S_kron, G_q = dY S_kron on this wave's key tiles,
     // and per-token partials h . G_h, q . G_q, dVbd . Vbd
@@ -531,7 +670,9 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
           // enters as hi + lo parts
 #pragma unroll 2
           for (int kb = 0; kb < D / 32; ++kb) {
-            const bf16x8 sf = ld_frag(&sm.skt[d][kb * 32], g4);
+            bf16x8 sf;
+            if constexpr (SKL) sf = ld_frag(&sm.skt[d][kb * 32], g4);
+            else sf = skf[a][kb];
             bf16x8 rh, rl, yh, yl;
             split_frag(&sm.dr[n16][kb * 32], g4, rh, rl);
             split_frag(&sm.dy[n16][kb * 32], g4, yh, yl);
@@ -542,7 +683,9 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         } else {
 #pragma unroll 4
           for (int kb = 0; kb < D / 16; ++kb) {
-            const f32x4 sf = load4(&sm.skt[d][kb * 16 + 4 * g4]);
+            f32x4 sf;
+            if constexpr (SKL) sf = load4(&sm.skt[d][kb * 16 + 4 * g4]);
+            else sf = skf[a][kb];
             mma(Gh[a], ld_frag(&sm.dr[n16][kb * 16], g4), sf);
             mma(Gq[a], ld_frag(&sm.dy[n16][kb * 16], g4), sf);
           }
@@ -568,6 +711,27 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         sm.red[kRqG][wave][i] = xq;
         sm.red[kRsvb][wave][i] = xv;   // times vsc_i below
       }
+    }
+    // the blocks this sub-chunk leaves in the window decay by e^{G_last}:
+    // sum over them of dVa . (keys decayed to the start of this sub-chunk)
+    if constexpr (NB > 1) {
+      float xd = 0.f;
+#pragma unroll
+      for (int bl = 0; bl < NB; ++bl)
+        if (bl != beta)
+#pragma unroll
+          for (int a = 0; a < VPW; ++a) {
+            const int d = 16 * (wave * VPW + a) + n16;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const int sl = BP * bl + 4 * g4 + s;
+              xd += dVa[bl][a][s] * (float)sm.kb[sl][d] * sm.kd[sl];
+            }
+          }
+      xd = row_sum16(xd);
+      xd += __shfl_xor(xd, 16, 64);
+      xd += __shfl_xor(xd, 32, 64);
+      if (lane == 0) sm.red[kRdd][wave][0] = xd;
     }
     // u = w o v: dv = w alpha dRhs, dw = v alpha dRhs, and sum_v w v dRhs per token
     {
@@ -603,9 +767,10 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     __syncthreads();
 
     // ---- F: per-token scalar gradients (wave 0, lane = token) ----
+    const float egl = expf(sm.G[BP - 1]);   // the sub-chunk's total decay
     if (wave == 0) {
       float dG = 0.f, dE = 0.f, svb = 0.f;
-      if (lane < P) {
+      if (lane < BP) {
         const int i = lane;
         float da = sm.su[i], dkco = 0.f, dqco = 0.f;
 #pragma unroll
@@ -630,37 +795,58 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
       det += __shfl_xor(det, 16, 64);
       svt += __shfl_xor(svt, 32, 64);
       det += __shfl_xor(det, 32, 64);
-      if (lane == P - 1) dG += svt + dgacc;   // G_last: the decayed keys and the next chunk's Gacc
-      // d log-decay_s = sum_{i >= s} dG_i: the P = 16 tokens are DPP row 0
-      static_assert(P == 16, "one DPP row of tokens");
-      const float sfx = row_suffix16(lane < P ? dG : 0.f);
-      const int tt_ = c * P + lane;
-      if (lane < P && tt_ < T) p.ddec[dec_base + (size_t)tt_ * dec_tok] = sfx * dlog_decay(sm.dec[lane]);
+      float gdd = 0.f;   // G_last through the older blocks' decay
+      if constexpr (NB > 1)
+        gdd = egl * ((sm.red[kRdd][0][0] + sm.red[kRdd][1][0]) + (sm.red[kRdd][2][0] + sm.red[kRdd][3][0]));
+      // G_last: the decayed keys, the next sub-chunk's Gacc and the older blocks
+      if (lane == BP - 1) dG += svt + dgacc + gdd;
+      // d log-decay_s = sum_{i >= s} dG_i: the 16 tokens are DPP row 0
+      const float sfx = row_suffix16(lane < BP ? dG : 0.f);
+      const int tt_ = c * BP + lane;
+      if (lane < BP && tt_ < T) p.ddec[dec_base + (size_t)tt_ * dec_tok] = sfx * dlog_decay(sm.dec[lane]);
       if (lane == 0) sm.carry[0] = det + dgacc;
     }
     __syncthreads();
     dgacc = sm.carry[0];
 
-    // ---- G: dH, dQ, dK on this wave's key tiles; the previous chunk's dVbd ----
+    // ---- G: dH, dQ, dK on this wave's key tiles; the blocks' dVbd ----
     float dbs[4] = {0.f, 0.f, 0.f, 0.f};   // per-token partial k . dh (scalar erase gates)
 #pragma unroll
     for (int a = 0; a < VPW; ++a) {
       const int d = 16 * (wave * VPW + a) + n16;
       const f32x4 Kc = col_frag<LR>(sm.k, d, g4), Hc = col_frag<LR>(sm.h, d, g4);
-      const f32x4 Qc = col_frag<LR>(sm.q, d, g4), Vc = col_frag<LR>(sm.vb, d, g4);
-      f32x4 dH = zero4(), dQ = zero4(), dK = zero4(), dVo = zero4();
+      const f32x4 Qc = col_frag<LR>(sm.q, d, g4);
+      f32x4 dH = zero4(), dQ = zero4(), dK = zero4();
       mma(dH, ld_frag(&sm.w[n16][0], g4), Kc);
-      mma(dH, ld_frag(&sm.vv[n16][0], g4), Vc);
       mma(dQ, ld_frag(&sm.z[n16][0], g4), Kc);
-      mma(dQ, ld_frag(&sm.wq[n16][0], g4), Vc);
       mma(dK, ld_frag(&sm.wt[n16][0], g4), Hc);
       mma(dK, ld_frag(&sm.zt[n16][0], g4), Qc);
-      mma(dVo, ld_frag(&sm.vvt[n16][0], g4), Hc);
-      mma(dVo, ld_frag(&sm.wqt[n16][0], g4), Qc);
+#pragma unroll
+      for (int bl = 0; bl < NB; ++bl) {
+        // the block's keys decayed to the start of this sub-chunk (k = slot)
+        f32x4 Vc;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int sl = BP * bl + 4 * g4 + s;
+          Vc[s] = (float)sm.kb[sl][d] * sm.kd[sl];
+        }
+        mma(dH, ld_frag(&sm.vv[bl][n16][0], g4), Vc);
+        mma(dQ, ld_frag(&sm.wq[bl][n16][0], g4), Vc);
+        // d/dVbd_b = dHo_b^T H + dQo_b^T Q (A operand: the transposes, read by column)
+        f32x4 dVo = zero4(), vvt, wqt;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          vvt[s] = sm.vv[bl][4 * g4 + s][n16];
+          wqt[s] = sm.wq[bl][4 * g4 + s][n16];
+        }
+        mma(dVo, vvt, Hc);
+        mma(dVo, wqt, Qc);
+        dVa[bl][a] = (bl == beta) ? dVo : egl * dVa[bl][a] + dVo;
+      }
       float dbp[4];
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int i = 4 * g4 + s, tt_ = c * P + i;
+        const int i = 4 * g4 + s, tt_ = c * BP + i;
         const bool ok = tt_ < T;
         const float dci = sm.dc[i];
         float dh = dH[s] + dci * Kc[s];
@@ -677,7 +863,6 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
           if (gc > 1) p.dbg[gate_base + (size_t)tt_ * gate_tok + d] = dbp[s];
         }
       }
-      dVc[a] = dVo;
     }
     if (gc == 1) {
 #pragma unroll
@@ -686,33 +871,40 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         if (n16 == 15) sm.red[kRdb][wave][4 * g4 + s] = x;
       }
       __syncthreads();
-      if (tid < P && c * P + tid < T) {
+      if (tid < BP && c * BP + tid < T) {
         float s = 0.f;
 #pragma unroll
         for (int w = 0; w < 4; ++w) s += sm.red[kRdb][w][tid];
-        p.dbg[gate_base + (size_t)(c * P + tid) * gate_tok] = s;
+        p.dbg[gate_base + (size_t)(c * BP + tid) * gate_tok] = s;
       }
     }
   }
 }
 
-template <typename CT, int D>
+template <typename CT, int D, int P>
 int launch_bwd(const G3BwdArgs& a, hipStream_t stream) {
   const int N = a.B * a.H * a.M;
-  hipLaunchKernelGGL((gdn3_bwd_kernel<CT, D>), dim3(N), dim3(kNT), 0, stream, a);
+  hipLaunchKernelGGL((gdn3_bwd_kernel<CT, D, P>), dim3(N), dim3(kNT), 0, stream, a);
   return check_launch("gdn3_bwd_kernel");
+}
+
+template <typename CT, int D>
+int launch_bwd_p(const G3BwdArgs& a, hipStream_t stream) {
+  if (a.P == 16) return launch_bwd<CT, D, 16>(a, stream);
+  if (a.P == 32) return launch_bwd<CT, D, 32>(a, stream);
+  if (a.P == 64) return launch_bwd<CT, D, 64>(a, stream);
+  return set_error(GDNX_ERR_SHAPE, "gdn3 backward: window P=%d unsupported (16, 32 or 64)", a.P);
 }
 
 }  // namespace
 
 int gdn3_bwd_dispatch(const G3BwdArgs& a, hipStream_t stream) {
-  if (a.P != BP) return set_error(GDNX_ERR_SHAPE, "gdn3 backward: window P=%d unsupported (16)", a.P);
   if (a.dtype == GDNX_DTYPE_BF16) {
-    if (a.D == 128) return launch_bwd<bf16, 128>(a, stream);
-    if (a.D == 64) return launch_bwd<bf16, 64>(a, stream);
+    if (a.D == 128) return launch_bwd_p<bf16, 128>(a, stream);
+    if (a.D == 64) return launch_bwd_p<bf16, 64>(a, stream);
   } else {
-    if (a.D == 128) return launch_bwd<float, 128>(a, stream);
-    if (a.D == 64) return launch_bwd<float, 64>(a, stream);
+    if (a.D == 128) return launch_bwd_p<float, 128>(a, stream);
+    if (a.D == 64) return launch_bwd_p<float, 64>(a, stream);
   }
   return set_error(GDNX_ERR_SHAPE, "gdn3 backward: unsupported head_dim %d", a.D);
 }

@@ -610,7 +610,8 @@ extern "C" int gdnx_gdn3_chunk_bwd(const void* q, const void* k, const void* v, 
   G3Geom ge;
   if ((rc = g3_geom(head_dim, R, a_v, a_k, b_v, b_k, ge))) return rc;
   if ((rc = g3_layer_geom(head_dim, ge))) return rc;
-  if (P != 16) return set_error(GDNX_ERR_SHAPE, "gdn3 backward: residual window P=%d unsupported (16)", P);
+  if (!g3_window_ok(head_dim, P))
+    return set_error(GDNX_ERR_SHAPE, "gdn3 backward: residual window P=%d unsupported (16, 32 or 64)", P);
   if (compact_every < P || compact_every % P != 0)
     return set_error(GDNX_ERR_SHAPE, "compact_every=%d must be a positive multiple of P=%d", compact_every, P);
   if (qkv_lanes != 1 && qkv_lanes != M)

@@ -175,7 +175,8 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     [B,T,H,M,V] in the compute dtype, plus ((A, B, U, Vb), comp_err) when
     return_state (comp_err is the reference's summed discarded energy, a
     device tensor).  When an input requires grad, y is differentiable in q,
-    k, v, the gates and the decay (P = 16); the state and comp_err are not.
+    k, v, the gates and the decay (P = 16, 32 or 64); the state and comp_err
+    are not.
 
     state0 = (A, B, U, Vb) and t0 continue a sequence from the state a
     previous call returned after t0 tokens (inference only: no gradient flows
@@ -230,9 +231,6 @@ def gdn3_recurrent_state(q, k, v, b_gates, w_gates, decay_factors, *, R=4, P=16,
     if train and carried:
         raise ValueError("gdn3_recurrent_state: a carried state (state0 / t0) is inference only; "
                          "run under torch.no_grad() or without state0")
-    if train and P != 16:
-        raise ValueError(f"gdn3_recurrent_state: the backward supports P = 16 (got P = {P}); "
-                         "run under torch.no_grad() for inference at this P")
     if carried:
         y, stats, state = ops.gdn3_chunk_fwd(q4, k4, v4, bg, wg, dec, G, M=M, R=R, P=P, factors=factors,
                                              slow_decay=slow_decay, compact_every=compact_every,

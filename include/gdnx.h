@@ -386,7 +386,8 @@ long long gdnx_gdn3_train_states_bytes(int B, int T, int H, int M, int head_dim,
  *                over the M lanes)
  *   db_gates, dw_gates  the gates' layout ([..., gate_channels])
  *   ddecay       [B, T, H, M] (zero where the decay was clamped)
- * Supported: P = 16, head_dim 128 or 64, the layer's Kronecker geometry. */
+ * Supported: P = 16, 32 or 64, head_dim 128 or 64, the layer's Kronecker
+ * geometry. */
 int gdnx_gdn3_chunk_bwd(const void* q, const void* k, const void* v, int qkv_lanes,
                         const float* b_gates, const float* w_gates, int gate_channels,
                         const float* decay, const void* dy, const void* train_states, float* dq,

@@ -74,21 +74,20 @@ CASES = [
 ]
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"c{i}" for i in range(len(CASES))])
-def test_gdn3_backward_matches_oracle(gpu_lib, case):
+def _check_backward(case, P=16):
     from gdnx_amd import gdn3
     B, T, H, M, D, factors, Kc, io, gate, per_lane, sdec = case
-    print(f"case: gdn3 bwd {case}", flush=True)
+    print(f"case: gdn3 bwd P={P} {case}", flush=True)
     xs, dy = _inputs(B, T, H, M, D, seed=33, io=io, gate=gate, per_lane=per_lane)
     N = B * H * M
     a_v, a_k, b_v, b_k = factors
     G = og.reference_sketch(N, b_v * b_k, min(4 + 4, a_v * a_k, b_v * b_k))
     leaves = [x.to(DEV).requires_grad_(True) for x in xs]
-    y = gdn3.gdn3_recurrent_state(*leaves, R=4, P=16, factors=factors, compact_every=Kc, sketch=G.to(DEV),
+    y = gdn3.gdn3_recurrent_state(*leaves, R=4, P=P, factors=factors, compact_every=Kc, sketch=G.to(DEV),
                                   slow_decay=sdec)
     grads = torch.autograd.grad(y, leaves, dy.to(io).to(DEV))
     torch.cuda.synchronize()
-    yr, gref = _oracle(xs, dy.to(io), M, 16, Kc, factors, G, slow_decay=sdec)
+    yr, gref = _oracle(xs, dy.to(io), M, P, Kc, factors, G, slow_decay=sdec)
     tol = 1e-2 if io == torch.bfloat16 else (5e-4 if sdec == 0.0 else 1e-4)
     assert rel_l2(y, yr) <= tol
     for name, a, r in zip(("dq", "dk", "dv", "db_gates", "dw_gates", "ddecay"), grads, gref):
@@ -97,6 +96,35 @@ def test_gdn3_backward_matches_oracle(gpu_lib, case):
         assert a.shape == r.shape and a.dtype == xs[("dq", "dk", "dv", "db_gates", "dw_gates",
                                                      "ddecay").index(name)].dtype
         assert err <= tol, name
+
+
+@pytest.mark.parametrize("case", CASES, ids=[f"c{i}" for i in range(len(CASES))])
+def test_gdn3_backward_matches_oracle(gpu_lib, case):
+    _check_backward(case)
+
+
+P_CASES = [
+    # (P, (B, T, H, M, D, factors, Kc, io, gate, per_lane, slow_decay)): windows of 2 and 4 blocks of 16
+    # slots, ragged tails, both head dims and IO dtypes
+    (32, (1, 96, 1, 2, 64, (8, 8, 8, 8), 32, torch.float32, "lane", False, 0.97)),
+    (64, (1, 160, 1, 1, 64, (8, 8, 8, 8), 64, torch.float32, "channel", True, 0.97)),
+    (64, (1, 100, 1, 2, 64, (8, 8, 8, 8), 128, torch.bfloat16, "lane", True, 0.97)),
+    (32, (1, 100, 1, 2, 128, (16, 16, 8, 8), 64, torch.bfloat16, "channel", False, 0.97)),
+    (32, (1, 64, 1, 2, 128, (16, 16, 8, 8), 32, torch.float32, "channel", True, 0.0)),
+    (64, (1, 80, 1, 2, 128, (16, 16, 8, 8), 64, torch.float32, "lane", True, 0.97)),
+    (64, (1, 150, 1, 2, 128, (16, 16, 8, 8), 64, torch.bfloat16, "lane", False, 0.0)),
+]
+
+
+@pytest.mark.parametrize("P,case", P_CASES, ids=[f"p{c[0]}c{i}" for i, c in enumerate(P_CASES)])
+def test_gdn3_backward_window_p(gpu_lib, P, case):
+    _check_backward(case, P)
+
+
+def test_gdn3_backward_config0_gdn3_mode(gpu_lib):
+    """Config 0's GDN3 mode (B=1, H=2, T=256, d=64, one lane, 8x8 factors,
+    P = 64 = the chunk, compaction every 64, fp32) forward and backward."""
+    _check_backward((1, 256, 2, 1, 64, (8, 8, 8, 8), 64, torch.float32, "lane", False, 0.97), 64)
 
 
 def test_gdn3_backward_without_compaction_equals_dense_rule(gpu_lib):
