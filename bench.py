@@ -41,6 +41,14 @@ def flops_fwd(B, T, H, M, D, C):
     return nchunks * (4 * C * C * D + M * (6 * C * D * D + 4 * C * C * D + C ** 3 / 3))
 
 
+def flops_prep(B, T, H, M, D, C):
+    """The intra-chunk phase (delta_prep_kernel): per (b, h, chunk) the
+    lane-shared grams K K^T and Q K^T (2 C^2 D each) and, per lane, the
+    unit-lower inverse (C^3 / 3)."""
+    nchunks = B * H * ((T + C - 1) // C)
+    return nchunks * (4 * C * C * D + M * C ** 3 / 3)
+
+
 def flops_bwd_state(B, T, H, M, D, C):
     """Reverse state scan: per lane and chunk K dS (2 C D^2), Aq^T dY and
     T^T dR (2 C^2 D each) and the dS update (4 C D^2)."""
@@ -100,6 +108,26 @@ def measured_traffic(kernel):
     with open(path) as f:
         entry = json.load(f).get("kernels", {}).get(kernel)
     return None if entry is None else entry["traffic"]
+
+
+def intra_chunk_entry(t_prep, flop):
+    """Roofline of the intra-chunk phase (delta_prep_kernel, timed alone with
+    HIP events): algorithmic FLOP against the dense bf16 MFMA peak, its
+    measured HBM traffic against 8 TB/s, and the MFMA-busy fraction read by
+    the SQ_VALU_MFMA_BUSY_CYCLES counter in the committed profile."""
+    name = "delta_prep_kernel"
+    achieved = flop / t_prep / 1e12
+    traffic = measured_traffic(name)
+    entry = {"kernel": name, "bound": "hbm", "achieved_tflops": achieved,
+             "peak_tflops": MFMA_BF16_PEAK / 1e12, "frac_mfma": achieved * 1e12 / MFMA_BF16_PEAK,
+             "mean_us": t_prep * 1e6, "algorithmic_flop": flop, "traffic": traffic,
+             "hbm_gbs": None if traffic is None else traffic / t_prep / 1e9,
+             "frac_hbm": None if traffic is None else traffic / t_prep / HBM_PEAK}
+    path = os.path.join(ROOT, "profiles", "mfma_busy.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            entry["mfma_busy_counter"] = json.load(f).get("kernels", {}).get(name)
+    return entry
 
 
 def decode_bytes(NS, H, NC, D, io_bytes=2):
@@ -928,6 +956,8 @@ def main():
                                                          ws=ws, out=out), args.kernel_iters)
         t_bgr = timed(lambda: ops.delta_chunk_bwd_grads(qd, kd, vd, a, a, lg, dO, state["cs"], ws, C, out),
                       args.kernel_iters)
+        pws = ops.delta_chunk_prep(qd, kd, a, a, lg, chunk=C)
+        t_prep = timed(lambda: ops.delta_chunk_prep(qd, kd, a, a, lg, chunk=C, ws=pws), args.kernel_iters)
     kernels = {
         "delta_prep_kernel+delta_scan_fwd_kernel": (t_fwd, flops_fwd(B, T, H, M, D, C)),
         "delta_scan_bwd_kernel": (t_bst, flops_bwd_state(B, T, H, M, D, C)),
@@ -959,6 +989,7 @@ def main():
                      "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": achieved * 1e12 / MFMA_BF16_PEAK, "traffic": traffic,
                      "mean_us": t_dom * 1e6, "algorithmic_flop": f_dom},
+        "roofline_intra_chunk": intra_chunk_entry(t_prep, flops_prep(B, T, H, M, D, C)),
         "kernels_us": {n: round(t * 1e6, 2) for n, (t, _) in kernels.items()},
         "grads_finite": finite,
     }

@@ -34,6 +34,7 @@ SIGNATURES = {
     "gdnx_delta_chunk_fwd": (_c_int, [_vp] * 11 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_fwd_scored": (_c_int, [_vp] * 12 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_fwd_workspace_bytes": (_c_ll, [_c_int] * 7),
+    "gdnx_delta_chunk_prep": (_c_int, [_vp] * 6 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_bwd": (_c_int, [_vp] * 17 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_bwd_state": (_c_int, [_vp] * 9 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_bwd_grads": (_c_int, [_vp] * 15 + [_c_int] * 7 + [_vp]),

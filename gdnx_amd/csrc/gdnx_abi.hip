@@ -117,6 +117,23 @@ extern "C" long long gdnx_delta_fwd_workspace_bytes(int B, int T, int H, int M, 
   return (long long)delta_prep_bytes(B * H * M, T, C, dtype);
 }
 
+extern "C" int gdnx_delta_chunk_prep(const void* q, const void* k, const float* a_e, const float* a_w,
+                                     const float* log_g, void* workspace, int B, int T, int H, int M,
+                                     int head_dim, int chunk, int dtype, void* stream) {
+  g_err[0] = 0;
+  int rc = check_common(q, k, k, B, T, H, M, head_dim, dtype);
+  if (rc) return rc;
+  if (!a_e || !a_w || !log_g) return set_error(GDNX_ERR_ARG, "a_e, a_w, log_g must be non-null");
+  if (!workspace) return set_error(GDNX_ERR_WORKSPACE, "workspace is required");
+  if ((uintptr_t)workspace & 15u) return set_error(GDNX_ERR_ARG, "workspace must be 16-byte aligned");
+  const int C = chunk ? chunk : delta_chunk_size(head_dim, dtype);
+  if (!valid_chunk(head_dim, dtype, C)) return set_error(GDNX_ERR_SHAPE, "chunk %d invalid for this dtype", chunk);
+  if (T == 0) return GDNX_OK;
+  DeltaArgs a{q, k, nullptr, a_e, a_w, log_g, nullptr, nullptr, nullptr, nullptr, B, T, H, M, head_dim, C, dtype,
+              nullptr, workspace};
+  return delta_prep_dispatch(a, (hipStream_t)stream);
+}
+
 extern "C" int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v, const float* a_e,
                                     const float* a_w, const float* log_g, const float* state0, void* y,
                                     float* state_out, void* chunk_states, void* workspace, int B, int T, int H,

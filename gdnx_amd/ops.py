@@ -96,6 +96,26 @@ def delta_chunk_fwd(q, k, v, a_e, a_w, log_g, state0=None, *, return_state=False
     return y, s_out, cs
 
 
+def delta_chunk_prep(q, k, a_e, a_w, log_g, *, chunk=0, ws=None):
+    """The intra-chunk phase alone (gdnx_delta_chunk_prep): every chunk's
+    state-independent operands (T = (I + L)^-1, decay-masked Q K^T, per-token
+    factors) into a uint8 workspace, which is returned (pass ``ws`` to reuse
+    one of gdnx_delta_fwd_workspace_bytes bytes)."""
+    lib = _lib.load()
+    B, T, H, M, D = _check_dense(q, k, k, a_e, a_w, log_g)
+    code = _lib.dtype_code(q.dtype)
+    nws = lib.gdnx_delta_fwd_workspace_bytes(B, T, H, M, D, chunk, code)
+    _need(nws >= 0, f"invalid chunk {chunk} for {q.dtype}")
+    if ws is None:
+        ws = torch.empty(max(nws, 16), dtype=torch.uint8, device=q.device)
+    _need(ws.dtype == torch.uint8 and ws.numel() >= nws and ws.is_contiguous(), "ws too small")
+    with torch.cuda.device(q.device):
+        rc = lib.gdnx_delta_chunk_prep(_lib.ptr(q), _lib.ptr(k), _lib.ptr(a_e), _lib.ptr(a_w), _lib.ptr(log_g),
+                                       _lib.ptr(ws), B, T, H, M, D, chunk, code, _lib.stream_of(q))
+    _lib.check(rc, "gdnx_delta_chunk_prep")
+    return ws
+
+
 def delta_chunk_bwd(q, k, v, a_e, a_w, log_g, dy, chunk_states, chunk, dstate_out=None,
                     want_dstate0=False):
     """Backward; returns (dq, dk, dv, da_e, da_w, dlog_g, dstate0 or None)."""

@@ -101,6 +101,16 @@ int gdnx_delta_chunk_fwd(const void* q, const void* k, const void* v,
 long long gdnx_delta_fwd_workspace_bytes(int B, int T, int H, int M, int head_dim, int chunk,
                                          int dtype);
 
+/* The intra-chunk phase alone: every chunk's state-independent operands
+ * (the decay-masked grams, T = (I + L)^-1 by 16x16 blocks, Aq and the
+ * per-token factors; the per-chunk part of the reference's chunk loop,
+ * gdn3/gdn3_upgrade.py:467-521) into workspace (gdnx_delta_fwd_workspace_bytes
+ * bytes), the records the parallel forward pass writes before its state
+ * scan.  Reads q, k, a_e, a_w, log_g. */
+int gdnx_delta_chunk_prep(const void* q, const void* k, const float* a_e, const float* a_w,
+                          const float* log_g, void* workspace, int B, int T, int H, int M,
+                          int head_dim, int chunk, int dtype, void* stream);
+
 /* gdnx_delta_chunk_fwd that also writes r_norm [B, T, H, M] float32, the
  * norm of each token's net write |r_t| = |a_w v - a_e S_bar^T k|; the KMD-2
  * update-norm score is |k_t| |r_t| (scan_with_update_norm,

@@ -83,6 +83,18 @@ def test_backward_requires_stash_and_workspace():
     assert "workspace" in lib.gdnx_last_error().decode()
 
 
+def test_prep_requires_workspace():
+    lib = _lib.load()
+    vp = ctypes.c_void_p
+    rc = lib.gdnx_delta_chunk_prep(vp(16), vp(16), vp(16), vp(16), vp(16), None, 1, 8, 1, 1, 64, 0,
+                                   _lib.DTYPE_F32, None)
+    assert rc == -3
+    assert "workspace" in lib.gdnx_last_error().decode()
+    rc = lib.gdnx_delta_chunk_prep(vp(16), vp(16), None, vp(16), vp(16), vp(16), 1, 8, 1, 1, 64, 0,
+                                   _lib.DTYPE_F32, None)
+    assert rc == -1
+
+
 @pytest.mark.parametrize("M,K", [(4, 128), (4, 64), (3, 96), (2, 8), (1, 4), (4, 256)])
 def test_lane_rope_pairs_follow_the_oracle_rule(M, K):
     """The library's lane RoPE pairs (host-only call) equal the oracle's

@@ -149,3 +149,7 @@ def test_two_pass_equals_single_pass(gpu_lib, dtype, chunk):
     ct = torch.float32 if dtype == torch.float32 else torch.bfloat16
     assert rel_l2(c1[:nst].view(ct).float(), c2[:nst].view(ct).float()) <= tol
     assert torch.equal(c1[nst:], c2[nst:])
+    # the intra-chunk phase alone (gdnx_delta_chunk_prep) writes the same records
+    pw = ops.delta_chunk_prep(args[0], args[1], args[3], args[4], args[5], chunk=chunk)
+    torch.cuda.synchronize()
+    assert torch.equal(pw[:c1.numel() - nst], c1[nst:])
