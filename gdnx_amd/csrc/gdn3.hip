@@ -636,6 +636,126 @@ __device__ __forceinline__ void store8(float* dst, const float* f) {
   *(f32x4*)(dst + 4) = (f32x4){f[4], f[5], f[6], f[7]};
 }
 
+// A thread's share of a sub-chunk's token rows as loaded: 8 consecutive
+// channels of one token (raw q, k, v; gates and decay as float).  The loads
+// always go to an in-bounds token and the validity is applied when the rows
+// are committed: loaded registers that branches merge would make the
+// prefetch wait for its own loads.
+template <typename CT> struct G3Raw {
+  uint4 k[W16Of<CT>::value], q[W16Of<CT>::value], v[W16Of<CT>::value];
+  f32x4 b0, b1, w0, w1;   // per-channel gates
+  float bs, ws, dec;      // scalar gates, decay
+  bool ok;                // a token of this call (else zeros and decay 1)
+};
+
+// Per-chain offsets of the token-major inputs and outputs
+struct G3Tok {
+  size_t qkv_tok, qkv_base, gate_tok, gate_base, dec_tok, dec_base, y_tok, y_base;
+  int gc;
+  __device__ __forceinline__ G3Tok(const G3FwdArgs& p, int chain, int D) {
+    const int H = p.H, M = p.M, T = p.T, L = p.qkv_lanes;
+    const int b = chain / (H * M), hm = chain % (H * M), h = hm / M, m = hm % M;
+    gc = p.gate_ch;
+    qkv_tok = (size_t)H * L * D;
+    qkv_base = ((size_t)b * T * H + h) * L * D + (L > 1 ? (size_t)m * D : 0);
+    gate_tok = (size_t)H * M * gc;
+    gate_base = (((size_t)b * T * H + h) * M + m) * gc;
+    dec_tok = (size_t)H * M;
+    dec_base = ((size_t)b * T * H + h) * M + m;
+    y_tok = (size_t)H * M * D;
+    y_base = (((size_t)b * T * H + h) * M + m) * D;
+  }
+};
+
+// local token t (marked invalid outside [0, T) or for a thread without a
+// unit; the loads then read token min(max(t, 0), T - 1)).  GL: the gate
+// layout, 1 a scalar per lane, 2 per channel, 0 read from o.gc (a runtime
+// branch, whose merge costs the prefetch a wait)
+template <typename CT, int GL = 0>
+__device__ __forceinline__ void g3_fetch(const G3FwdArgs& p, const G3Tok& o, G3Raw<CT>& r, int t, bool on,
+                                         int ud) {
+  constexpr int W16 = W16Of<CT>::value;
+  r.ok = on && t >= 0 && t < p.T;
+  const size_t tc = (size_t)min(max(t, 0), p.T - 1);
+  const uint4* kp = (const uint4*)((const CT*)p.k + o.qkv_base + tc * o.qkv_tok + ud);
+  const uint4* qp = (const uint4*)((const CT*)p.q + o.qkv_base + tc * o.qkv_tok + ud);
+  const uint4* vp = (const uint4*)((const CT*)p.v + o.qkv_base + tc * o.qkv_tok + ud);
+#pragma unroll
+  for (int w = 0; w < W16; ++w) {
+    r.k[w] = kp[w];
+    r.q[w] = qp[w];
+    r.v[w] = vp[w];
+  }
+  // both branches define every gate field, so no loaded register is merged
+  if (GL == 2 || (GL == 0 && o.gc > 1)) {
+    const float* bp = p.bg + o.gate_base + tc * o.gate_tok + ud;
+    const float* wp = p.wg + o.gate_base + tc * o.gate_tok + ud;
+    r.b0 = *(const f32x4*)bp;
+    r.b1 = *(const f32x4*)(bp + 4);
+    r.w0 = *(const f32x4*)wp;
+    r.w1 = *(const f32x4*)(wp + 4);
+    if constexpr (GL == 0) r.bs = r.ws = 0.f;
+  } else {
+    r.bs = p.bg[o.gate_base + tc * o.gate_tok];
+    r.ws = p.wg[o.gate_base + tc * o.gate_tok];
+    if constexpr (GL == 0) r.b0 = r.b1 = r.w0 = r.w1 = zero4();
+  }
+  r.dec = p.dec[o.dec_base + tc * o.dec_tok];
+}
+
+// the raw q / k vector w of a thread's row, zero for an invalid token
+template <typename CT>
+__device__ __forceinline__ uint4 g3_raw(const G3Raw<CT>& r, const uint4& x) {
+  return r.ok ? x : make_uint4(0u, 0u, 0u, 0u);
+}
+
+// h = b o k and u = w o v of the thread's 8 channels (gc: gate channels);
+// returns the row sum of k . h over the token's DG threads (consecutive lanes)
+template <typename CT, int DG, int GL = 0>
+__device__ __forceinline__ float g3_unpack(const G3Raw<CT>& r, int gc, float* hf, float* uu) {
+  float kf[8], vf[8], bb[8], ww[8];
+  unpack8(r.k, kf, (const CT*)nullptr);
+  unpack8(r.v, vf, (const CT*)nullptr);
+  if (GL == 2 || (GL == 0 && gc > 1)) {
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      bb[e] = r.b0[e];
+      bb[4 + e] = r.b1[e];
+      ww[e] = r.w0[e];
+      ww[4 + e] = r.w1[e];
+    }
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      bb[e] = r.bs;
+      ww[e] = r.ws;
+    }
+  }
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {   // an invalid token commits zeros
+    kf[e] = r.ok ? kf[e] : 0.f;
+    vf[e] = r.ok ? vf[e] : 0.f;
+  }
+  float part = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    hf[e] = bb[e] * kf[e];
+    uu[e] = ww[e] * vf[e];
+    part += kf[e] * hf[e];
+  }
+  if constexpr (DG == 16) {
+    // the 16 lanes of a token row are one DPP row: rotations by 8, 4, 2, 1
+    part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x128, 0xf, 0xf, false));
+    part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x124, 0xf, 0xf, false));
+    part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x122, 0xf, 0xf, false));
+    part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x121, 0xf, 0xf, false));
+  } else {
+#pragma unroll
+    for (int off = 1; off < DG; off <<= 1) part += __shfl_xor(part, off, 64);
+  }
+  return part;
+}
+
 // Sub-chunks [c0, c1) of one compaction interval (or the tail) for every
 // chain; the window state enters and leaves through the workspace.  A
 // chain's value columns are split over NVB workgroups (D / 16 / NVB value
@@ -662,98 +782,31 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
   const int N = p.B * H * M;
   const int work = xcd_remap(blockIdx.x, N * NVB);   // a chain's NVB workgroups land on one XCD
   const int chain = work / NVB, vb = work % NVB;
-  const int b = chain / (H * M), hm = chain % (H * M), h = hm / M, m = hm % M;
   typedef G3D<D> Ge;
   constexpr int NVTW = D / 16 / NVB;   // value tiles of this workgroup: vb NVTW + [0, NVTW)
   static_assert(NVTW >= 1 && (D / 16) % NVB == 0, "value split");
 
   const bool has_unit = tid < UNITS;
   const int ui = tid / DG, ud = 8 * (tid % DG);
-  const int L = p.qkv_lanes, gc = p.gate_ch;
-  const size_t qkv_tok = (size_t)H * L * D;
-  const size_t qkv_base = ((size_t)b * T * H + h) * L * D + (L > 1 ? (size_t)m * D : 0);
-  const size_t gate_tok = (size_t)H * M * gc;
-  const size_t gate_base = (((size_t)b * T * H + h) * M + m) * gc;
-  const size_t dec_tok = (size_t)H * M;
-  const size_t dec_base = ((size_t)b * T * H + h) * M + m;
-  const size_t y_tok = (size_t)H * M * D;
-  const size_t y_base = (((size_t)b * T * H + h) * M + m) * D;
-
-  struct Raw {
-    uint4 k[W16], q[W16], v[W16];
-    f32x4 b0, b1, w0, w1;
-    float dec;
-  };
+  typedef G3Raw<CT> Raw;
+  const G3Tok tk(p, chain, D);
   // sub-chunk c covers global tokens [16 c, 16 c + 16): local token 16 c + i - t0
-  auto fetch = [&](Raw& r, int c) {
-    const int t = c * kSC + ui - p.t0;
-    if (has_unit && t >= 0 && t < T) {
-      const uint4* kp = (const uint4*)((const CT*)p.k + qkv_base + (size_t)t * qkv_tok + ud);
-      const uint4* qp = (const uint4*)((const CT*)p.q + qkv_base + (size_t)t * qkv_tok + ud);
-      const uint4* vp = (const uint4*)((const CT*)p.v + qkv_base + (size_t)t * qkv_tok + ud);
-#pragma unroll
-      for (int w = 0; w < W16; ++w) {
-        r.k[w] = kp[w];
-        r.q[w] = qp[w];
-        r.v[w] = vp[w];
-      }
-      if (gc > 1) {
-        const float* bp = p.bg + gate_base + (size_t)t * gate_tok + ud;
-        const float* wp = p.wg + gate_base + (size_t)t * gate_tok + ud;
-        r.b0 = *(const f32x4*)bp;
-        r.b1 = *(const f32x4*)(bp + 4);
-        r.w0 = *(const f32x4*)wp;
-        r.w1 = *(const f32x4*)(wp + 4);
-      } else {
-        const float bs = p.bg[gate_base + (size_t)t * gate_tok];
-        const float ws = p.wg[gate_base + (size_t)t * gate_tok];
-        r.b0 = r.b1 = (f32x4){bs, bs, bs, bs};
-        r.w0 = r.w1 = (f32x4){ws, ws, ws, ws};
-      }
-      r.dec = p.dec[dec_base + (size_t)t * dec_tok];
-    } else {
-#pragma unroll
-      for (int w = 0; w < W16; ++w) r.k[w] = r.q[w] = r.v[w] = make_uint4(0u, 0u, 0u, 0u);
-      r.b0 = r.b1 = r.w0 = r.w1 = zero4();
-      r.dec = 1.f;
-    }
-  };
+  auto fetch = [&](Raw& r, int c) { g3_fetch<CT>(p, tk, r, c * kSC + ui - p.t0, has_unit, ud); };
   auto commit = [&](const Raw& r) {
     if (!has_unit) return;
-    float kf[8], qf[8], vf[8];
-    unpack8(r.k, kf, (const CT*)nullptr);
-    unpack8(r.q, qf, (const CT*)nullptr);
-    unpack8(r.v, vf, (const CT*)nullptr);
-    const float bb[8] = {r.b0[0], r.b0[1], r.b0[2], r.b0[3], r.b1[0], r.b1[1], r.b1[2], r.b1[3]};
-    const float ww[8] = {r.w0[0], r.w0[1], r.w0[2], r.w0[3], r.w1[0], r.w1[1], r.w1[2], r.w1[3]};
-    float hf[8], uu[8], part = 0.f;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      hf[e] = bb[e] * kf[e];
-      uu[e] = ww[e] * vf[e];
-      part += kf[e] * hf[e];
-    }
+    float hf[8], uu[8];
+    const float part = g3_unpack<CT, DG>(r, tk.gc, hf, uu);
     store8(&sm.x[ui][ud], hf);
 #pragma unroll
     for (int w = 0; w < W16; ++w) {
-      *(uint4*)&sm.x[kSC + ui][ud + w * (16 / sizeof(CT))] = r.q[w];
-      *(uint4*)&sm.x[2 * kSC + ui][ud + w * (16 / sizeof(CT))] = r.k[w];
+      *(uint4*)&sm.x[kSC + ui][ud + w * (16 / sizeof(CT))] = g3_raw(r, r.q[w]);
+      *(uint4*)&sm.x[2 * kSC + ui][ud + w * (16 / sizeof(CT))] = g3_raw(r, r.k[w]);
     }
     *(f32x4*)&sm.u[ui][ud] = (f32x4){uu[0], uu[1], uu[2], uu[3]};
     *(f32x4*)&sm.u[ui][ud + 4] = (f32x4){uu[4], uu[5], uu[6], uu[7]};
-    if constexpr (DG == 16) {
-      // the 16 lanes of a token row are one DPP row: rotations by 8, 4, 2, 1
-      part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x128, 0xf, 0xf, false));
-      part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x124, 0xf, 0xf, false));
-      part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x122, 0xf, 0xf, false));
-      part += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(part), 0x121, 0xf, 0xf, false));
-    } else {
-#pragma unroll
-      for (int off = 1; off < DG; off <<= 1) part += __shfl_xor(part, off, 64);
-    }
     if (tid % DG == 0) {
       sm.alpha[ui] = stable_alpha_f(part);
-      sm.lg[ui] = log_decay(r.dec);
+      sm.lg[ui] = log_decay(r.ok ? r.dec : 1.f);
     }
   };
 
@@ -968,14 +1021,14 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
 #pragma unroll
       for (int bl = 0; bl < NB; ++bl) mma(yv, *(const f32x4*)&sm.po[1][n16][kSC * bl + 4 * g4], uo[bl][a]);
       mma(yv, *(const f32x4*)&sm.pp[1][n16][4 * g4], un);
-      CT* yp = (CT*)p.y + y_base + v;
+      CT* yp = (CT*)p.y + tk.y_base + v;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int i = 4 * g4 + s;
         float out = yv[s];
         if (live) out += sm.qco[i] * sm.kr[kSC + i][v];
         const int t = c * kSC + i - p.t0;
-        if (t >= 0 && t < T) yp[(size_t)t * y_tok] = from_f<CT>(out);
+        if (t >= 0 && t < T) yp[(size_t)t * tk.y_tok] = from_f<CT>(out);
       }
 #pragma unroll
       for (int bl = 0; bl < NB; ++bl)
@@ -1048,6 +1101,409 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
   if (p.last && !p.complete) {  // no compaction follows: A, B decayed since the last one
     // the workspace holds every chain's A [N][R m], then every chain's B [N][R n]
     const float dk = expf(gacc);
+    const float* af = p.ab + (size_t)chain * Ge::R * Ge::m;
+    const float* bf = p.ab + (size_t)N * Ge::R * Ge::m + (size_t)chain * Ge::R * Ge::n;
+    if (p.A_out)
+      for (int e = tid; e < Ge::R * Ge::m; e += kNT) p.A_out[(size_t)chain * Ge::R * Ge::m + e] = af[e] * dk;
+    if (p.B_out)
+      for (int e = tid; e < Ge::R * Ge::n; e += kNT) p.B_out[(size_t)chain * Ge::R * Ge::n + e] = bf[e] * dk;
+  }
+}
+
+// Long intervals: the same sub-chunk recurrence as a two-stage software
+// pipeline over the sub-chunks with one barrier per step.  In step c:
+//   wave 0: the G scan and per-token coefficients of sub-chunk c, H K^T and
+//           the inverse T (the longest chain of a step);
+//   wave 1: Ho_b, Qo_b against the window keys of sub-chunk c, then sub-chunk
+//           c's keys into block c mod NB (the window keys are read and
+//           written by wave 1 alone);
+//   waves 2, 3: the window algebra of sub-chunk c - 1 on their value tiles (U
+//           resident in their registers; wave 2 takes the first), then
+//           sub-chunk c's Kronecker reads; wave 3 also forms Aq = Q K^T;
+//   waves 0, 2, 3: the token rows of sub-chunk c + 1 into LDS (loaded a step
+//           ahead), wave 3 also wave 1's.
+// What a step writes for the next alternates by sub-chunk parity; the
+// per-token inputs sub-chunk c + 1 commits while sub-chunk c - 1's algebra
+// still reads its own rotate over three.
+template <typename CT, int D, int P, int NVB>
+struct G3PipeSmem {
+  static constexpr int NB = P / kSC;
+  static constexpr int NVTW = D / 16 / NVB;
+  static constexpr int VW = NVTW * 16;        // this workgroup's value columns
+  static constexpr bool KF = sizeof(CT) == 4; // fp32 IO: the grams read the fp32 window keys
+  alignas(16) CT x[2][3 * kSC][D + 8];        // H, Q, K rows (parity)
+  alignas(16) float uu[3][kSC][VW + 4];       // w (.) v at this workgroup's value columns (c mod 3)
+  alignas(16) float kr[2][2 * kSC][VW + 4];   // Kronecker reads of H and Q at those columns (parity)
+  alignas(16) float ws[2][kSC][kSC + 4];      // wave 0's inverse scratch
+  alignas(16) float tt[2][kSC][kSC + 4];      // T (parity)
+  alignas(16) float aq[2][kSC][kSC + 4];      // Aq (parity)
+  alignas(16) float po[2][2][kSC][P + 4];     // Ho, Qo over the P slots (parity)
+  alignas(16) CT skron[VW][D + 8];            // sum_r A_r (x) B_r, this workgroup's rows v
+  alignas(16) float vbd[P][D + 4];            // window keys: block b decayed to e^{-boff_b} of now
+  alignas(16) CT vbx[KF ? 1 : P][D + 8];      // the same in the compute dtype (bf16 IO)
+  float cr[2][kSC], dr[2][kSC];               // k . h and the decay as committed (parity)
+  float al[2][kSC];                           // alpha (parity)
+  float kco[2][kSC], qco[2][kSC];             // alpha e^{2(Gacc + G)}, e^{2(Gacc + G)} (parity)
+  float boff[NB];                             // log decay of block b's keys since they were rebased
+  float gfin;                                 // Gacc after the last sub-chunk
+};
+template <typename CT, int D, int P, int NVB>
+constexpr size_t pipe_lds() { return sizeof(G3PipeSmem<CT, D, P, NVB>); }
+
+template <typename CT, int D, int P, int NVB, int GL>
+__global__ void __launch_bounds__(kNT) gdn3_window_pipe_kernel(G3FwdArgs p) {
+  typedef G3PipeSmem<CT, D, P, NVB> Sm;
+  __shared__ Sm sm;
+  constexpr int NB = Sm::NB, NVTW = Sm::NVTW, VW = Sm::VW;
+  constexpr int DG = D / 8, UNITS = kSC * DG, W16 = W16Of<CT>::value, KS = FragT<CT>::KSTEP;
+  typedef typename FragT<CT>::type Frag;
+  static_assert(UNITS <= kNT && UNITS % 64 == 0, "one load unit per thread");
+  static_assert(P % kSC == 0 && NB >= 1 && NB <= 4, "whole 16-slot blocks, at most 4");
+  static_assert(NVTW >= 1 && (D / 16) % NVB == 0, "value split");
+  static_assert(sizeof(Sm) <= 160 * 1024, "LDS budget");
+  typedef G3D<D> Ge;
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g4 = lane >> 4, n16 = lane & 15;
+  const int T = p.T;
+  const int N = p.B * p.H * p.M;
+  const int work = xcd_remap(blockIdx.x, N * NVB);   // a chain's NVB workgroups land on one XCD
+  const int chain = work / NVB, vb = work % NVB;
+  typedef G3Raw<CT> Raw;
+  const G3Tok tk(p, chain, D);
+  const bool live = p.live;
+
+  // load unit un (< UNITS: token row un / DG, channels 8 (un mod DG) ..);
+  // sub-chunk c covers global tokens [16 c, 16 c + 16): local token 16 c + i - t0
+  auto fetch = [&](Raw& r, int c, int un) {
+    g3_fetch<CT, GL>(p, tk, r, c * kSC + un / DG - p.t0, un < UNITS, 8 * (un % DG));
+  };
+  auto commit = [&](const Raw& r, int c, int un) {
+    if (un >= UNITS) return;
+    const int ui = un / DG, ud = 8 * (un % DG);
+    float hf[8], uu[8];
+    const float part = g3_unpack<CT, DG, GL>(r, tk.gc, hf, uu);
+    const int s2 = c & 1, s3 = c % 3;
+    store8(&sm.x[s2][ui][ud], hf);
+#pragma unroll
+    for (int w = 0; w < W16; ++w) {
+      *(uint4*)&sm.x[s2][kSC + ui][ud + w * (16 / sizeof(CT))] = g3_raw(r, r.q[w]);
+      *(uint4*)&sm.x[s2][2 * kSC + ui][ud + w * (16 / sizeof(CT))] = g3_raw(r, r.k[w]);
+    }
+    const int uc = ud - vb * VW;   // this workgroup's value columns only
+    if (uc >= 0 && uc < VW) {
+      *(f32x4*)&sm.uu[s3][ui][uc] = (f32x4){uu[0], uu[1], uu[2], uu[3]};
+      *(f32x4*)&sm.uu[s3][ui][uc + 4] = (f32x4){uu[4], uu[5], uu[6], uu[7]};
+    }
+    if (un % DG == 0) {   // alpha and the log decay are formed lane-parallel in stage A
+      sm.cr[s2][ui] = part;
+      sm.dr[s2][ui] = r.ok ? r.dec : 1.f;
+    }
+  };
+  // the units a wave commits: its own (waves 0, 2, 3) and, for wave 3, wave 1's
+  const int u_own = tid, u_w1 = 64 + lane;
+  // stage A's per-token scalars of sub-chunk c: lane i < 16 gets G_i (the
+  // log-decay prefix) and alpha_i
+  auto scan_g = [&](int c) {
+    float gl = lane < kSC ? log_decay(sm.dr[c & 1][lane]) : 0.f;
+#pragma unroll
+    for (int off = 1; off < kSC; off <<= 1) {
+      const float o = __shfl_up(gl, off, 64);
+      if (lane >= off) gl += o;
+    }
+    return gl;
+  };
+  auto token_scalars = [&](int c, float& alpha_l, float& gl) {
+    alpha_l = lane < kSC ? stable_alpha_f(sm.cr[c & 1][lane]) : 0.f;
+    gl = scan_g(c);
+  };
+
+  // window state: zero for the first interval, else from the workspace.
+  // Algebra wave 2 + w2 holds the workgroup's local value tiles w2 + 2 a
+  // (a < VPW, where w2 + 2 a < NVTW), of every block
+  constexpr int VPW = (NVTW + 1) / 2;
+  const int w2 = wave - 2;
+  auto vown = [&](int a) { return w2 >= 0 && w2 + 2 * a < NVTW; };
+  f32x4 uo[NB][VPW];
+  float* uw = p.uw + (size_t)chain * P * D;
+  float* vw = p.vw + (size_t)chain * P * D;
+  if (p.first) {
+    for (int e = tid; e < P * (D + 4); e += kNT) (&sm.vbd[0][0])[e] = 0.f;
+    if constexpr (!Sm::KF)
+      for (int e = tid; e < P * (D + 8); e += kNT) (&sm.vbx[0][0])[e] = (CT)0.f;
+#pragma unroll
+    for (int bl = 0; bl < NB; ++bl)
+#pragma unroll
+      for (int a = 0; a < VPW; ++a) uo[bl][a] = zero4();
+  } else {
+    for (int e = tid; e < P * D; e += kNT) {
+      const int j = e / D, d = e % D;
+      const float kv = vw[e];
+      sm.vbd[j][d] = kv;
+      if constexpr (!Sm::KF) sm.vbx[j][d] = from_f<CT>(kv);
+    }
+#pragma unroll
+    for (int bl = 0; bl < NB; ++bl)
+#pragma unroll
+      for (int a = 0; a < VPW; ++a)
+#pragma unroll
+        for (int s = 0; s < 4; ++s)
+          uo[bl][a][s] = vown(a) ? uw[(bl * kSC + 4 * g4 + s) * D + vb * VW + (w2 + 2 * a) * 16 + n16] : 0.f;
+  }
+  if (tid < NB) sm.boff[tid] = 0.f;
+  if (live) {   // this workgroup's value rows of the Kronecker matrix
+    constexpr int PER = 16 / sizeof(CT);  // elements per 16-byte load
+    const uint4* src = (const uint4*)((const CT*)p.skron + ((size_t)chain * D + vb * VW) * D);
+    for (int e = tid; e < VW * D / PER; e += kNT) {
+      const int v = (e * PER) / D, k = (e * PER) % D;   // (local row)
+      *(uint4*)&sm.skron[v][k] = src[e];
+    }
+  }
+  float gacc = 0.f;   // (wave 0) log decay since the last compaction, at the current sub-chunk
+
+  Raw raw, raw1;   // raw1: wave 3's copy of wave 1's units
+  fetch(raw, p.c0, u_own);
+  commit(raw, p.c0, u_own);
+  if (p.c0 + 1 < p.c1) fetch(raw, p.c0 + 1, u_own);
+  if (wave == 3 && p.c0 + 1 < p.c1) fetch(raw1, p.c0 + 1, u_w1);
+  __syncthreads();
+  for (int c = p.c0; c <= p.c1; ++c) {
+    const bool sa = c < p.c1, sb = c > p.c0;   // stage A of c, stage B of c - 1
+    const int s2 = c & 1;
+    if (wave == 0 && sa) {
+      // per-token coefficients and T = (I + Lm)^-1 of sub-chunk c
+      float alpha_l, gl;
+      token_scalars(c, alpha_l, gl);
+      const float gl_last = __shfl(gl, kSC - 1, 64);
+      if (lane < kSC) {
+        const float e2 = expf(2.f * (gacc + gl));
+        sm.al[s2][lane] = alpha_l;
+        sm.kco[s2][lane] = alpha_l * e2;
+        sm.qco[s2][lane] = e2;
+      }
+      if (p.ts_g && lane == 0 && vb == 0) p.ts_g[(size_t)chain * p.nch + c] = gacc;
+      gacc += gl_last;
+      const f32x4 acc = tile_nt<CT, D>(&sm.x[s2][n16][0], &sm.x[s2][2 * kSC + n16][0], g4);
+      // Lm[i][j] = alpha_i e^{G_i - G_j} (h_i . k_j), j < i, is strictly lower
+      // (nilpotent): (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8), factors
+      // that commute; squarings and products on fp32 MFMA.  An accumulator
+      // tile is a k-fragment (B operand); the A operand of each square goes
+      // through LDS.
+      const float gj = __shfl(gl, n16, 64);
+      f32x4 xa, ta;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        const float gi = __shfl(gl, i, 64), ai = __shfl(alpha_l, i, 64);
+        xa[s] = (n16 < i) ? ai * expf(gi - gj) * acc[s] : 0.f;
+        sm.ws[0][i][n16] = xa[s];
+        ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+#pragma unroll
+      for (int step = 0; step < 3; ++step) {
+        const int src = step & 1, dst = src ^ 1;
+        f32x4 sq = zero4();
+        mma(sq, *(const f32x4*)&sm.ws[src][n16][4 * g4], xa);  // X^2
+        xa = sq;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) sm.ws[dst][4 * g4 + s][n16] = sq[s];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        mma(ta, *(const f32x4*)&sm.ws[dst][n16][4 * g4], ta);  // T += X^2 T
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) sm.tt[s2][4 * g4 + s][n16] = ta[s];
+    } else if (wave == 1 && sa) {
+      // Ho_b, Qo_b of sub-chunk c, then its keys into block c mod NB:
+      //   Ho_b = vis alpha_i e^{G_i + boff_b} h_i.Vb_b[j],  Qo_b = vis e^{G_i + boff_b} q_i.Vb_b[j]
+      // with vis = [b != beta or j >= i or j < lo]
+      const int beta = c % NB, lo = max(0, p.t0 - c * kSC), hi = min(kSC, p.t0 + T - c * kSC);
+      float alpha_l, gl;
+      token_scalars(c, alpha_l, gl);
+      float gi[4], ai[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        gi[s] = __shfl(gl, 4 * g4 + s, 64);
+        ai[s] = __shfl(alpha_l, 4 * g4 + s, 64);
+      }
+#pragma unroll
+      for (int t2 = 0; t2 < 2 * NB; ++t2) {
+        const int bl = t2 >> 1;
+        const bool isq = t2 & 1;
+        const CT* brow;
+        if constexpr (Sm::KF) brow = (const CT*)&sm.vbd[kSC * bl + n16][0];
+        else brow = &sm.vbx[kSC * bl + n16][0];
+        const f32x4 acc = tile_nt<CT, D>(&sm.x[s2][(isq ? kSC : 0) + n16][0], brow, g4);
+        const float bo = sm.boff[bl];
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int i = 4 * g4 + s;
+          const bool vis = bl != beta || n16 >= i || n16 < lo;
+          const float sc = expf(gi[s] + bo) * (isq ? 1.f : ai[s]);
+          sm.po[s2][isq ? 1 : 0][i][kSC * bl + n16] = vis ? sc * acc[s] : 0.f;
+        }
+      }
+      // block beta's keys for the next sub-chunks: the slots sub-chunk c wrote
+      // take k_j decayed to its end, the others their old keys decayed over
+      // it; then the block's offset restarts and the others' grow by G_last
+      const float gl_last = __shfl(gl, kSC - 1, 64);
+      const float vsc = expf(gl_last - gl);   // lane j < 16
+      const float olds = expf(sm.boff[beta] + gl_last);
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      for (int u8 = lane; u8 < kSC * D / 8; u8 += 64) {
+        const int j = u8 / DG, d = 8 * (u8 % DG), sl = kSC * beta + j;
+        uint4 w[W16];
+#pragma unroll
+        for (int q16 = 0; q16 < W16; ++q16)
+          w[q16] = *(const uint4*)&sm.x[s2][2 * kSC + j][d + q16 * (16 / sizeof(CT))];
+        float kf[8];
+        unpack8(w, kf, (const CT*)nullptr);
+        float sc = __shfl(vsc, j, 64);
+        if (j < lo || j >= hi) {
+          sc = olds;
+          const f32x4 o0 = *(const f32x4*)&sm.vbd[sl][d], o1 = *(const f32x4*)&sm.vbd[sl][d + 4];
+          kf[0] = o0[0], kf[1] = o0[1], kf[2] = o0[2], kf[3] = o0[3];
+          kf[4] = o1[0], kf[5] = o1[1], kf[6] = o1[2], kf[7] = o1[3];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[e] *= sc;
+        *(f32x4*)&sm.vbd[sl][d] = (f32x4){kf[0], kf[1], kf[2], kf[3]};
+        *(f32x4*)&sm.vbd[sl][d + 4] = (f32x4){kf[4], kf[5], kf[6], kf[7]};
+        if constexpr (!Sm::KF) store8(&sm.vbx[sl][d], kf);
+      }
+      if (lane < NB) sm.boff[lane] = (lane == beta) ? 0.f : sm.boff[lane] + gl_last;
+    } else if (wave >= 2) {
+      if (wave == 3 && sa) {   // Aq = [j <= i] e^{G_i - G_j} q_i.k_j of sub-chunk c
+        const float gl = scan_g(c);
+        const float gj = __shfl(gl, n16, 64);
+        const f32x4 acc = tile_nt<CT, D>(&sm.x[s2][kSC + n16][0], &sm.x[s2][2 * kSC + n16][0], g4);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int i = 4 * g4 + s;
+          const float gi = __shfl(gl, i, 64);
+          sm.aq[s2][i][n16] = (n16 <= i) ? expf(gi - gj) * acc[s] : 0.f;
+        }
+      }
+      if (sb) {
+        // window algebra of sub-chunk cb = c - 1 on fp32 MFMA, per value tile:
+        //   Rhs = alpha u - kco KRh - sum_b Ho_b U_b;  U = T Rhs
+        //   Y   = qco KRq + sum_b Qo_b U_b + Aq U
+        const int cb = c - 1, t2 = cb & 1, t3 = cb % 3, beta = cb % NB;   // uu by c mod 3, the rest by parity
+        const int lo = max(0, p.t0 - cb * kSC), hi = min(kSC, p.t0 + T - cb * kSC);
+#pragma unroll
+        for (int a = 0; a < VPW; ++a) {
+          if (!vown(a)) continue;
+          const int vl = (w2 + 2 * a) * 16 + n16, v = vb * VW + vl;
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int bl = 0; bl < NB; ++bl) mma(acc, *(const f32x4*)&sm.po[t2][0][n16][kSC * bl + 4 * g4], uo[bl][a]);
+          f32x4 rhs;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int i = 4 * g4 + s;
+            float r = sm.al[t2][i] * sm.uu[t3][i][vl] - acc[s];
+            if (live) r -= sm.kco[t2][i] * sm.kr[t2][i][vl];
+            rhs[s] = r;
+          }
+          f32x4 un = zero4();
+          mma(un, *(const f32x4*)&sm.tt[t2][n16][4 * g4], rhs);
+          f32x4 yv = zero4();
+#pragma unroll
+          for (int bl = 0; bl < NB; ++bl) mma(yv, *(const f32x4*)&sm.po[t2][1][n16][kSC * bl + 4 * g4], uo[bl][a]);
+          mma(yv, *(const f32x4*)&sm.aq[t2][n16][4 * g4], un);
+          CT* yp = (CT*)p.y + tk.y_base + v;
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int i = 4 * g4 + s;
+            float out = yv[s];
+            if (live) out += sm.qco[t2][i] * sm.kr[t2][kSC + i][vl];
+            const int t = cb * kSC + i - p.t0;
+            if (t >= 0 && t < T) yp[(size_t)t * tk.y_tok] = from_f<CT>(out);
+          }
+#pragma unroll
+          for (int bl = 0; bl < NB; ++bl)
+            if (bl == beta)
+#pragma unroll
+              for (int s = 0; s < 4; ++s) {
+                const int i = 4 * g4 + s;
+                if (i >= lo && i < hi) uo[bl][a][s] = un[s];
+              }
+          if (p.ts_u) {   // training stash: this sub-chunk's net writes
+            float* us = p.ts_u + ((size_t)chain * p.nch + cb) * kSC * D + v;
+#pragma unroll
+            for (int s = 0; s < 4; ++s) us[(size_t)(4 * g4 + s) * D] = un[s];
+          }
+        }
+      }
+      if (sa && live) {
+        // Kronecker reads of sub-chunk c at this wave's value tiles
+#pragma unroll
+        for (int a = 0; a < VPW; ++a) {
+          if (!vown(a)) continue;
+          const int l = w2 + 2 * a;
+          Frag bf[D / KS];
+#pragma unroll
+          for (int kb = 0; kb < D / KS; ++kb) bf[kb] = ld_frag(&sm.skron[l * 16 + n16][kb * KS], g4);
+#pragma unroll
+          for (int rt = 0; rt < 2; ++rt) {
+            f32x4 acc = zero4();
+#pragma unroll
+            for (int kb = 0; kb < D / KS; ++kb) mma(acc, ld_frag(&sm.x[s2][rt * 16 + n16][kb * KS], g4), bf[kb]);
+#pragma unroll
+            for (int s = 0; s < 4; ++s) sm.kr[s2][rt * 16 + 4 * g4 + s][l * 16 + n16] = acc[s];
+          }
+        }
+      }
+    }
+    // the rows of sub-chunk c + 1 (and the loads of c + 2, which stay in
+    // flight across the LDS-only barrier): waves 0, 2, 3 their own, wave 3
+    // wave 1's
+    if (c + 1 < p.c1) {
+      if (wave != 1) {
+        commit(raw, c + 1, u_own);
+        if (c + 2 < p.c1) fetch(raw, c + 2, u_own);
+      }
+      if (wave == 3) {
+        commit(raw1, c + 1, u_w1);
+        if (c + 2 < p.c1) fetch(raw1, c + 2, u_w1);
+      }
+    }
+    lds_barrier();
+  }
+  if (tid == 0) sm.gfin = gacc;
+  __syncthreads();
+  // window state out (and the final state after the last sub-chunk): the
+  // value columns from their workgroup, the keys and decays from the first
+#pragma unroll
+  for (int a = 0; a < VPW; ++a) {
+    if (!vown(a)) continue;
+#pragma unroll
+    for (int bl = 0; bl < NB; ++bl)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = bl * kSC + 4 * g4 + s, v = vb * VW + (w2 + 2 * a) * 16 + n16;
+        uw[i * D + v] = uo[bl][a][s];
+        if (p.last && p.U_out) p.U_out[((size_t)chain * D + v) * P + i] = uo[bl][a][s];
+      }
+  }
+  if (vb != 0) return;
+  const float gfin = sm.gfin;
+  for (int e = tid; e < P * D; e += kNT) {
+    const int j = e / D, d = e % D;
+    const float kv = sm.vbd[j][d] * expf(sm.boff[j / kSC]);
+    vw[e] = kv;
+    if (p.last && p.Vb_out) p.Vb_out[((size_t)chain * D + d) * P + j] = kv;
+  }
+  if (tid == 0) p.gsum[chain] = gfin;
+  if (p.last && !p.complete) {  // no compaction follows: A, B decayed since the last one
+    // the workspace holds every chain's A [N][R m], then every chain's B [N][R n]
+    const float dk = expf(gfin);
     const float* af = p.ab + (size_t)chain * Ge::R * Ge::m;
     const float* bf = p.ab + (size_t)N * Ge::R * Ge::m + (size_t)chain * Ge::R * Ge::n;
     if (p.A_out)
@@ -1246,8 +1702,70 @@ inline size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 // value split: ~512 workgroups, two per CU (NVB workgroups per chain, at
 // least one value tile each), or the smallest larger split whose LDS fits
+// The pipelined window kernel for intervals of several sub-chunks: the
+// value split whose workgroups all run at once (at most two per CU, as LDS
+// allows) with the fewest rounds, the widest among equals
+int cu_count() {
+  static int n = 0;
+  if (n == 0) {
+    int dev = 0, v = 0;
+    if (hipGetDevice(&dev) == hipSuccess && hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) ==
+                                                hipSuccess && v > 0)
+      n = v;
+    else
+      n = 256;
+  }
+  return n;
+}
+
+template <typename CT, int D, int P, int NVB>
+void pipe_score(int N, int& best_nvb, long long& best_rounds) {
+  constexpr size_t lds = pipe_lds<CT, D, P, NVB>();
+  if constexpr (lds <= 160 * 1024) {
+    const int per_cu = lds <= 80 * 1024 ? 2 : 1;
+    const long long cap = (long long)cu_count() * per_cu, wgs = (long long)N * NVB;
+    const long long rounds = (wgs + cap - 1) / cap;
+    if (rounds <= best_rounds) {
+      best_rounds = rounds;
+      best_nvb = NVB;
+    }
+  }
+}
+
+template <typename CT, int D, int P, int NVB>
+void pipe_launch(const G3FwdArgs& a, int N, hipStream_t stream) {
+  if (a.gate_ch > 1)
+    hipLaunchKernelGGL((gdn3_window_pipe_kernel<CT, D, P, NVB, 2>), dim3(N * NVB), dim3(kNT), 0, stream, a);
+  else
+    hipLaunchKernelGGL((gdn3_window_pipe_kernel<CT, D, P, NVB, 1>), dim3(N * NVB), dim3(kNT), 0, stream, a);
+}
+
+template <typename CT, int D, int P>
+int launch_pipe(const G3FwdArgs& a, int N, hipStream_t stream) {
+  constexpr int V2 = D / 16 < 2 ? D / 16 : 2, V4 = D / 16 < 4 ? D / 16 : 4, V8 = D / 16 < 8 ? D / 16 : 8;
+  int nvb = 0;
+  long long rounds = 1LL << 62;
+  pipe_score<CT, D, P, 1>(N, nvb, rounds);
+  pipe_score<CT, D, P, V2>(N, nvb, rounds);
+  pipe_score<CT, D, P, V4>(N, nvb, rounds);
+  pipe_score<CT, D, P, V8>(N, nvb, rounds);
+  if constexpr (pipe_lds<CT, D, P, 1>() <= 160 * 1024)
+    if (nvb == 1) pipe_launch<CT, D, P, 1>(a, N, stream);
+  if constexpr (V2 != 1 && pipe_lds<CT, D, P, V2>() <= 160 * 1024)
+    if (nvb == V2) pipe_launch<CT, D, P, V2>(a, N, stream);
+  if constexpr (V4 != V2 && pipe_lds<CT, D, P, V4>() <= 160 * 1024)
+    if (nvb == V4) pipe_launch<CT, D, P, V4>(a, N, stream);
+  if constexpr (V8 != V4 && pipe_lds<CT, D, P, V8>() <= 160 * 1024)
+    if (nvb == V8) pipe_launch<CT, D, P, V8>(a, N, stream);
+  if (nvb == 0) return set_error(GDNX_ERR_SHAPE, "gdn3: no window split fits LDS");
+  return check_launch("gdn3_window_pipe_kernel");
+}
+
 template <typename CT, int D, int P>
 int launch_window(const G3FwdArgs& a, int N, hipStream_t stream) {
+  // intervals of several sub-chunks overlap one sub-chunk's algebra with the
+  // next one's grams and inverse
+  if (a.c1 - a.c0 >= 3) return launch_pipe<CT, D, P>(a, N, stream);
   constexpr int V2 = D / 16 < 2 ? D / 16 : 2, V4 = D / 16 < 4 ? D / 16 : 4, V8 = D / 16 < 8 ? D / 16 : 8;
   static_assert(win_fits<CT, D, P, V8>(), "the widest split fits");
   const int nvb = N >= 512 ? 1 : N >= 256 ? V2 : N >= 128 ? V4 : V8;

@@ -75,6 +75,15 @@ __device__ __forceinline__ f32x4 acc_frag(float*, const f32x4& t0, const f32x4&)
 
 __device__ __forceinline__ f32x4 zero4() { return (f32x4){0.f, 0.f, 0.f, 0.f}; }
 
+// Workgroup barrier for LDS traffic only.  __syncthreads() is a workgroup
+// release/acquire fence, which on CDNA (one vmcnt for loads and stores)
+// waits for every outstanding global load, a prefetch issued just before it
+// included.  Here only LDS operations complete before s_barrier, so loads
+// issued for a later step stay in flight across it; the memory clobber keeps
+// the compiler from moving memory accesses across the barrier.  Global
+// stores before it are not made visible to the other waves.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
 // 4 consecutive CT values from floats (for 8/16-byte LDS stores).
 __device__ __forceinline__ void st4(bf16* p, float a, float b, float c, float d) {
   *(bf16x4*)p = (bf16x4){(bf16)a, (bf16)b, (bf16)c, (bf16)d};
