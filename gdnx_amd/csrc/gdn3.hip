@@ -69,80 +69,97 @@ __device__ __forceinline__ void block_sum(double (&v)[NV], double* red, int tid)
   __syncthreads();
 }
 
-// LDS of one compaction.
-template <int D, int P>
+// LDS of one compaction.  STG: the window's writes and keys are staged
+// through ut / vt a block of 16 slots at a time (they come from global
+// memory); without, they are read where they lie (LDS of the fused kernel).
+template <int D, int P, bool STG = true>
 struct G3Compact {
-  alignas(16) float rm[D * D + kMN];      // R_mat: m rows of n + 1 floats
-  alignas(16) double y[kMN * kQ];         // range basis, rows of kQ
-  alignas(16) double z[kMN * kQ];         // R_mat^T Y, then Bm^T = R_mat^T Q (rows of kQ)
-  alignas(16) float gs[kMN * kQ];         // sketch, rows of kQ (zero padded)
-  alignas(16) float ut[16][D + 4];        // a block of 16 window slots: net writes U_p
-  alignas(16) float vt[16][D + 4];        // and keys Vb_p
-  alignas(16) double us[kRMax][kMN];      // leading left singular vectors of R_mat
-  alignas(16) double vs[kRMax][kMN];      // leading right singular vectors
+  static constexpr int m = G3D<D>::m, n = G3D<D>::n;
+  static constexpr int ldr = n + 4;                 // R_mat row stride: 16-byte rows, 4 banks apart
+  static constexpr int lym = m + 16, lzn = n + 16;  // strides of the column-major fp32 copies
+  alignas(16) float rm[m * ldr];          // R_mat
+  alignas(16) double y[m * kQ];           // range basis, rows of kQ
+  alignas(16) double z[n * kQ];           // R_mat^T Y, then Bm^T = R_mat^T Q (rows of kQ)
+  alignas(16) float yt[kQ * lym];         // y in fp32, column-major: the B operand of R_mat^T Y
+  alignas(16) float zt[kQ * lzn];         // the sketch (zero padded), then z, in fp32 column-major
+  alignas(16) float ut[STG ? 16 : 1][D + 4];   // a block of 16 window slots: net writes U_p
+  alignas(16) float vt[STG ? 16 : 1][D + 4];   // and keys Vb_p
+  alignas(16) double us[kRMax][m];        // leading left singular vectors of R_mat
+  alignas(16) double vs[kRMax][n];        // leading right singular vectors
   double red[4 * 64];
   double rinv[kQ * kQ];                   // the summed Gram Y^T Y of a Cholesky-QR pass (row-major)
   double ev[kQ * kQ];                     // eigenvectors of Bm Bm^T (columns)
   double lam[kQ];
   double sig[kRMax];
-  double amax[4][kRMax];
   double sgn[kRMax];
-  int aidx[4][kRMax];
   int order[kQ];
 };
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-// C[M x kQ] = A[M x K] B[K x kQ] on fp64 MFMA (v_mfma_f64_16x16x4f64: lane l
-// supplies A[l%16][l/16] and B[l/16][l%16] and holds D[l/16 + 4e][l%16]).
-// A is R_mat (fp32, row stride ldr) read as is (TRANS = false, M = m, K = n)
-// or transposed (TRANS = true, M = n, K = m); B and C are rows of kQ, B fp32
-// or fp64; the 16-column tile carries kQ = 8 live columns.  Wave w owns the
-// 16-row tiles w, w + 4, ...; the k loop is unrolled so that the operand
-// loads of later steps are issued under the MFMAs of earlier ones.  A wave
-// with one tile keeps 4 accumulator chains, one with several keeps one chain
-// per tile (the B operand of a step is shared by its tiles).
-template <bool TRANS, int M, int K, typename BT>
-__device__ __forceinline__ void rm_mfma(const float* rm, int ldr, const BT* b, double* c, int tid) {
-  static_assert(M % 64 == 0 && K % 16 == 0, "whole 16-row tiles on 4 waves, 16 k per step");
-  constexpr int TPW = M / 64, NA = TPW >= 4 ? 1 : 4 / TPW;
+// C[M x kQ] = A[M x K] B[K x kQ] on fp32 MFMA (v_mfma_f32_16x16x4f32): A is
+// R_mat (fp32, row stride ldr, a multiple of 4) read as is (TRANS = false,
+// M = m, K = n) or transposed (TRANS = true, M = n, K = m); B is fp32 and
+// column-major (column j at bt + j ldb, zero where it has no column), so
+// every product is exact and the sums are fp32.  The 16-column tile carries
+// kQ = 8 live columns.  In a step of 16 k, lane (g, r) supplies
+// k = kb + 4 g + s to the s-th MFMA: its B entries are one 16-byte load, and
+// so are its A entries of an untransposed row (rows of ldr = 4 mod 64 floats
+// put the 16 rows of a tile on distinct banks, and the 16 columns of a
+// transposed read too).  The operands of the next step are loaded before the
+// MFMAs of this one.  Wave w owns the 16-row tiles w, w + 4, ...; C goes to
+// c (rows of kQ, fp64) and, when ct is given, column-major in fp32 to ct
+// (stride ldc).
+template <bool TRANS, int M, int K, int ldr, int ldb, int ldc = 0>
+__device__ __forceinline__ void rm_mfma(const float* rm, const float* bt, double* c, float* ct, int tid) {
+  static_assert(M % 64 == 0 && K % 16 == 0 && ldr % 4 == 0 && ldb % 4 == 0, "whole 16-row tiles on 4 waves, 16 k per step");
+  constexpr int TPW = M / 64;
   const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, n16 = lane & 15;
   const bool live = n16 < kQ;
-  const int bcol = live ? n16 : 0;
-  f64x4 acc[TPW][NA];
+  // lanes of the dead columns 8..15 repeat the live ones (their outputs are dropped)
+  const float* bcol = bt + (n16 & (kQ - 1)) * ldb + 4 * g;
+  auto ldb4 = [&](int kb) { return *(const f32x4*)&bcol[kb]; };
+  auto lda4 = [&](int t, int kb) {
+    const int row = (wave + 4 * t) * 16 + n16;
+    f32x4 x;
+    if constexpr (TRANS) {
 #pragma unroll
-  for (int t = 0; t < TPW; ++t)
+      for (int s4 = 0; s4 < 4; ++s4) x[s4] = rm[(kb + 4 * g + s4) * ldr + row];
+    } else {
+      x = *(const f32x4*)&rm[row * ldr + kb + 4 * g];
+    }
+    return x;
+  };
+  f32x4 acc[TPW], av[TPW], bv = ldb4(0);
 #pragma unroll
-    for (int u = 0; u < NA; ++u) acc[t][u] = (f64x4){0.0, 0.0, 0.0, 0.0};
+  for (int t = 0; t < TPW; ++t) {
+    acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
+    av[t] = lda4(t, 0);
+  }
 #pragma unroll
   for (int kb = 0; kb < K; kb += 16) {
-    double a[TPW][4], bb[4];
+    f32x4 an[TPW], bn;
+    if (kb + 16 < K) {
+      bn = ldb4(kb + 16);
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int k = kb + 4 * u + g;
-      const double bv = (double)b[k * kQ + bcol];
-      bb[u] = live ? bv : 0.0;
-#pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        const int row = (wave + 4 * t) * 16 + n16;
-        a[t][u] = TRANS ? rm[k * ldr + row] : rm[row * ldr + k];
-      }
+      for (int t = 0; t < TPW; ++t) an[t] = lda4(t, kb + 16);
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u)
+    for (int t = 0; t < TPW; ++t) mma(acc[t], av[t], bv);
+    if (kb + 16 < K) {
+      bv = bn;
 #pragma unroll
-      for (int t = 0; t < TPW; ++t)
-        acc[t][u % NA] = __builtin_amdgcn_mfma_f64_16x16x4f64(a[t][u], bb[u], acc[t][u % NA], 0, 0, 0);
+      for (int t = 0; t < TPW; ++t) av[t] = an[t];
+    }
   }
   if (live)
 #pragma unroll
-    for (int t = 0; t < TPW; ++t)
+    for (int t = 0; t < TPW; ++t) {
+      const int r0 = (wave + 4 * t) * 16 + 4 * g;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        double v = acc[t][0][e];
-        if constexpr (NA == 4) v = (acc[t][0][e] + acc[t][1][e]) + (acc[t][2][e] + acc[t][3][e]);
-        c[((wave + 4 * t) * 16 + g + 4 * e) * kQ + n16] = v;
-      }
+      for (int e = 0; e < 4; ++e) c[(r0 + e) * kQ + n16] = (double)acc[t][e];
+      if constexpr (ldc > 0) *(f32x4*)&ct[n16 * ldc + r0] = acc[t];
+    }
 }
 
 // Jacobi rotation zeroing a_pq (Numerical Recipes convention):
@@ -198,11 +215,11 @@ __device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
 
 // Y <- Y R^{-1} with Y^T Y = R^T R (Cholesky QR, `passes` times: one pass
 // keeps the intermediate power-iteration bases well conditioned, the final
-// basis takes two).  Columns whose pivot falls below 1e-24 of the largest
+// basis takes two); the result also goes column-major in fp32 to yt.  Columns whose pivot falls below 1e-24 of the largest
 // diagonal are set to zero.  The Gram runs on fp64 MFMA over 4 row segments;
 // each row of Y is then solved against R by forward substitution.
-template <int D, int P, int M>
-__device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int tid, int passes) {
+template <int D, int P, int M, bool STG>
+__device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int passes) {
   static_assert(M % 16 == 0 && M <= kNT, "rows: 4 segments of whole MFMA steps, one row per thread");
   const int lane = tid & 63, wave = tid >> 6;
   constexpr int seg = M / 4;
@@ -257,7 +274,10 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P>& cs, int tid, int pass
         x[j] = sacc * rdv[j];
       }
 #pragma unroll
-      for (int j = 0; j < kQ; ++j) cs.y[tid * kQ + j] = x[j];
+      for (int j = 0; j < kQ; ++j) {
+        cs.y[tid * kQ + j] = x[j];
+        cs.yt[j * cs.lym + tid] = (float)x[j];
+      }
     }
     __syncthreads();
   }
@@ -293,17 +313,18 @@ __device__ __forceinline__ void col_sumsq(const double* y, double* red, double* 
 // sketch of qs = R columns, Q = the column-normalised R_mat G,
 // Bm = Q^T R_mat, A_svd_r = |Bm_r| Q_r, B_svd_r = Bm_r / |Bm_r| (norms
 // clamped at 1e-12); it reports no error (stats = (|R_mat|^2, |R_mat|^2)).
-template <int D, int P>
-__device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const float* __restrict__ U,
+template <int D, int P, bool STG>
+__device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, const float* __restrict__ U,
                                            const float* __restrict__ Vb, size_t u_sp, size_t u_sd, float gacc,
                                            float sdec, const float* __restrict__ sketch, double* stats, int tid,
                                            int mode = 0) {
   typedef G3D<D> Ge;
   constexpr int R = Ge::R, m = Ge::m, n = Ge::n, q = Ge::q, ak = Ge::ak, bk = Ge::bk;
   constexpr int lbv = Ge::lbv, lbk = Ge::lbk, ln = Ge::ln;
-  constexpr int ldr = n + 1;
+  constexpr int ldr = G3Compact<D, P, STG>::ldr, lym = G3Compact<D, P, STG>::lym, lzn = G3Compact<D, P, STG>::lzn;
   float* A = ab;
   float* Bv = ab + R * m;
+  tid = opaque(tid);
   const int lane = tid & 63, wave = tid >> 6;
 
   // the sketch's global loads are issued first and land in LDS after the
@@ -331,25 +352,36 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
 #pragma unroll
       for (int kt = 0; kt < NT16; ++kt) racc[vi][kt] = (f32x4){0.f, 0.f, 0.f, 0.f};
     for (int pb = 0; pb < P / 16; ++pb) {
-      if (pb > 0) __syncthreads();   // the previous block is consumed
-      for (int e = tid; e < 16 * D; e += kNT) {
-        const int i = e / D, d = e % D;
-        const size_t o = (size_t)(16 * pb + i) * u_sp + (size_t)d * u_sd;
-        cs.ut[i][d] = U[o];
-        cs.vt[i][d] = Vb[o];
+      if constexpr (STG) {
+        if (pb > 0) __syncthreads();   // the previous block is consumed
+        for (int e = tid; e < 16 * D; e += kNT) {
+          const int i = e / D, d = e % D;
+          const size_t o = (size_t)(16 * pb + i) * u_sp + (size_t)d * u_sd;
+          cs.ut[i][d] = U[o];
+          cs.vt[i][d] = Vb[o];
+        }
+        __syncthreads();
       }
-      __syncthreads();
+      // slot 16 pb + i, column d
+      auto uval = [&](int i, int d) {
+        if constexpr (STG) return cs.ut[i][d];
+        else return U[(size_t)(16 * pb + i) * u_sp + (size_t)d * u_sd];
+      };
+      auto vval = [&](int i, int d) {
+        if constexpr (STG) return cs.vt[i][d];
+        else return Vb[(size_t)(16 * pb + i) * u_sp + (size_t)d * u_sd];
+      };
 #pragma unroll
       for (int vi = 0; vi < VTW; ++vi) {
         const int vt = wave * VTW + vi;
         f32x4 ua;
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) ua[s4] = cs.ut[4 * g4 + s4][vt * 16 + n16];
+        for (int s4 = 0; s4 < 4; ++s4) ua[s4] = uval(4 * g4 + s4, vt * 16 + n16);
 #pragma unroll
         for (int kt = 0; kt < NT16; ++kt) {
           f32x4 kb4;
 #pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) kb4[s4] = cs.vt[4 * g4 + s4][kt * 16 + n16];
+          for (int s4 = 0; s4 < 4; ++s4) kb4[s4] = vval(4 * g4 + s4, kt * 16 + n16);
           mma(racc[vi][kt], ua, kb4);
         }
       }
@@ -371,7 +403,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
 #pragma unroll
   for (int u = 0; u < NGS; ++u) {
     const int e = tid + u * kNT;
-    if (e < n * kQ) cs.gs[e] = gsv[u];
+    if (e < n * kQ) cs.zt[(e % kQ) * lzn + e / kQ] = gsv[u];
   }
   __syncthreads();
   // Kronecker part (A, B each decayed by e^{gacc}) and the energy |R_mat|^2
@@ -410,15 +442,17 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
   block_sum<1>(en, cs.red, tid);
 
   if (mode) {   // 'sketch': one product, column and row normalisation
-    rm_mfma<false, m, n>(cs.rm, ldr, cs.gs, cs.y, tid);   // Y = R_mat G (columns >= R are zero)
+    rm_mfma<false, m, n, ldr, lzn>(cs.rm, cs.zt, cs.y, nullptr, tid);   // Y = R_mat G (columns >= R are zero)
     __syncthreads();
     col_sumsq<m>(cs.y, cs.red, cs.lam, tid);
     for (int e = tid; e < m * kQ; e += kNT) {
       const int j = e % kQ;
-      cs.y[e] = j < R ? cs.y[e] / fmax(sqrt(cs.lam[j]), 1e-12) : 0.0;   // Q
+      const double qv = j < R ? cs.y[e] / fmax(sqrt(cs.lam[j]), 1e-12) : 0.0;   // Q
+      cs.y[e] = qv;
+      cs.yt[j * lym + e / kQ] = (float)qv;
     }
     __syncthreads();
-    rm_mfma<true, n, m>(cs.rm, ldr, cs.y, cs.z, tid);      // Bm^T = R_mat^T Q
+    rm_mfma<true, n, m, ldr, lym>(cs.rm, cs.yt, cs.z, nullptr, tid);      // Bm^T = R_mat^T Q
     __syncthreads();
     col_sumsq<n>(cs.z, cs.red, cs.sig, tid);
     const float dk = expf(gacc);
@@ -443,18 +477,18 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P>& cs, float* ab, const
 
   // range finder with two power iterations; orthonormalising between the
   // products leaves the final basis unchanged (up to column signs)
-  rm_mfma<false, m, n>(cs.rm, ldr, cs.gs, cs.y, tid);
+  rm_mfma<false, m, n, ldr, lzn>(cs.rm, cs.zt, cs.y, nullptr, tid);
   __syncthreads();
-  orth_rows<D, P, m>(cs, tid, 1);
+  orth_rows<D, P, m, STG>(cs, tid, 1);
   for (int it = 0; it < 2; ++it) {
-    rm_mfma<true, n, m>(cs.rm, ldr, cs.y, cs.z, tid);
+    rm_mfma<true, n, m, ldr, lym, lzn>(cs.rm, cs.yt, cs.z, cs.zt, tid);
     __syncthreads();
-    rm_mfma<false, m, n>(cs.rm, ldr, cs.z, cs.y, tid);
+    rm_mfma<false, m, n, ldr, lzn>(cs.rm, cs.zt, cs.y, nullptr, tid);
     __syncthreads();
-    orth_rows<D, P, m>(cs, tid, it == 1 ? 2 : 1);
+    orth_rows<D, P, m, STG>(cs, tid, it == 1 ? 2 : 1);
   }
   // Bm^T = R_mat^T Q  [n][kQ]
-  rm_mfma<true, n, m>(cs.rm, ldr, cs.y, cs.z, tid);
+  rm_mfma<true, n, m, ldr, lym>(cs.rm, cs.yt, cs.z, nullptr, tid);
   __syncthreads();
   // eigen-decomposition of W = Bm Bm^T by cyclic Jacobi in wave 0: lane
   // (i, j) holds W[i][j] and V[i][j].  Each round rotates 4 disjoint pairs;
@@ -756,6 +790,284 @@ __device__ __forceinline__ float g3_unpack(const G3Raw<CT>& r, int gc, float* hf
   return part;
 }
 
+// The window LDS a sub-chunk step works on (pointers into one workgroup's
+// shared memory)
+template <typename CT, int D, int P>
+struct G3WinView {
+  CT (*x)[D + 8];               // rows: H (0..15), Q (16..31), K (32..47)
+  float (*u)[D + 4];            // w (.) v
+  float (*kr)[D + 4];           // Kronecker reads of H and Q
+  float (*pp)[kSC][kSC + 4];    // [4]: H K^T (then inverse scratch), Aq, T, inverse scratch
+  float (*po)[kSC][P + 4];      // [2]: Ho, Qo over the P slots
+  CT (*skron)[D + 8];           // this workgroup's rows of sum_r A_r (x) B_r
+  float (*vbd)[D + 4];          // window keys: block b decayed to e^{-boff_b} of now
+  CT (*vbx)[D + 8];             // the same in the compute dtype (bf16 IO)
+  float *G, *alpha, *lg, *kco, *qco, *gam, *vsc;
+  float* boff;                  // log decay of block b's keys since they were rebased
+};
+
+// One sub-chunk c of the single-stage window recurrence for one workgroup
+// (value tiles vb NVTW .. of chain): commit of its prefetched token rows (and
+// the loads of sub-chunk next, if >= 0), the grams, the inverse, the
+// Kronecker reads, the window algebra on the U tiles uo, y and the training
+// stash, then the window keys.  first: no sub-chunk before it in this launch.
+template <typename CT, int D, int P, int NVB>
+__device__ __forceinline__ void g3_window_step(const G3WinView<CT, D, P>& w, const G3FwdArgs& p, const G3Tok& tk,
+                                               int chain, int vb, int c, bool first, int next, bool live,
+                                               float& gacc, f32x4 (&uo)[P / kSC][(D / 16 / NVB + 3) / 4],
+                                               G3Raw<CT>& raw) {
+  constexpr int NB = P / kSC;
+  constexpr bool KF = sizeof(CT) == 4;
+  constexpr int DG = D / 8;  // 8-element load units per token row
+  constexpr int UNITS = kSC * DG;
+  constexpr int W16 = W16Of<CT>::value;
+  constexpr int KS = FragT<CT>::KSTEP;
+  typedef typename FragT<CT>::type Frag;
+  constexpr int NVTW = D / 16 / NVB;   // value tiles of this workgroup: vb NVTW + [0, NVTW)
+  constexpr int VPW = (NVTW + 3) / 4;
+  const int tid = opaque(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  const int g4 = lane >> 4, n16 = lane & 15;
+  const int T = p.T;
+  const bool has_unit = tid < UNITS;
+  const int ui = tid / DG, ud = 8 * (tid % DG);
+  auto fetch = [&](G3Raw<CT>& r, int cc) { g3_fetch<CT>(p, tk, r, cc * kSC + ui - p.t0, has_unit, ud); };
+  auto commit = [&](const G3Raw<CT>& r) {
+    if (!has_unit) return;
+    float hf[8], uu[8];
+    const float part = g3_unpack<CT, DG>(r, tk.gc, hf, uu);
+    store8(&w.x[ui][ud], hf);
+#pragma unroll
+    for (int q16 = 0; q16 < W16; ++q16) {
+      *(uint4*)&w.x[kSC + ui][ud + q16 * (16 / sizeof(CT))] = g3_raw(r, r.q[q16]);
+      *(uint4*)&w.x[2 * kSC + ui][ud + q16 * (16 / sizeof(CT))] = g3_raw(r, r.k[q16]);
+    }
+    *(f32x4*)&w.u[ui][ud] = (f32x4){uu[0], uu[1], uu[2], uu[3]};
+    *(f32x4*)&w.u[ui][ud + 4] = (f32x4){uu[4], uu[5], uu[6], uu[7]};
+    if (tid % DG == 0) {
+      w.alpha[ui] = stable_alpha_f(part);
+      w.lg[ui] = log_decay(r.ok ? r.dec : 1.f);
+    }
+  };
+  // after sub-chunk cc: its block is rebased (boff 0), the others decayed by its G_last
+  auto advance_boff = [&](int cc, float glast) {
+    if (tid < NB) w.boff[tid] = (tid == cc % NB) ? 0.f : w.boff[tid] + glast;
+  };
+  auto vown = [&](int a) { return wave + 4 * a < NVTW; };
+  auto vtile = [&](int a) { return vb * NVTW + wave + 4 * a; };
+
+    // slots [lo, hi) of block beta receive this call's tokens; the others (the
+    // head a previous call wrote, the tail after the last token) keep the
+    // writes they hold and stay visible to every token of the sub-chunk
+    const int lo = max(0, p.t0 - c * kSC), hi = min(kSC, p.t0 + T - c * kSC);
+    const int beta = c % NB;
+    __syncthreads();
+    if (!first) advance_boff(c - 1, w.G[kSC - 1]);
+    commit(raw);
+    if (next >= 0) fetch(raw, next);
+    __syncthreads();
+    // per-token scalars | grams and Kronecker reads (MFMA).  Every wave forms
+    // the log-decay prefix sums G (lane i holds G_i); wave 0 publishes the
+    // per-token coefficients.
+    float gl = lane < kSC ? w.lg[lane] : 0.f;
+#pragma unroll
+    for (int off = 1; off < kSC; off <<= 1) {
+      const float o = __shfl_up(gl, off, 64);
+      if (lane >= off) gl += o;
+    }
+    if (wave == 0) {
+      const float gl_last = __shfl(gl, kSC - 1, 64);
+      if (lane < kSC) {
+        const float e2 = expf(2.f * (gacc + gl));
+        w.G[lane] = gl;
+        w.gam[lane] = expf(gl);
+        w.kco[lane] = w.alpha[lane] * e2;
+        w.qco[lane] = e2;
+        w.vsc[lane] = expf(gl_last - gl);
+      }
+    }
+    // grams, 2 + 2 NB tiles over the waves (tile ti on wave ti mod 4):
+    //   0: H K^T (raw; wave 0 turns it into T),  1: Aq = [j <= i] e^{G_i - G_j} q_i.k_j,
+    //   2 + 2 b: Ho_b = vis alpha_i e^{G_i + boff_b} h_i.Vb_b[j],  3 + 2 b: Qo_b = vis e^{G_i + boff_b} q_i.Vb_b[j]
+    // with vis = [b != beta or j >= i or j < lo]
+    {
+      const float gj = __shfl(gl, n16, 64);
+      float gi[4];
+#pragma unroll
+      for (int s = 0; s < 4; ++s) gi[s] = __shfl(gl, 4 * g4 + s, 64);
+#pragma unroll
+      for (int r = 0; r < (2 + 2 * NB + 3) / 4; ++r) {
+        const int ti = wave + 4 * r;
+        if (ti < 2 + 2 * NB) {
+          const bool isq = ti & 1;
+          const CT* arow = &w.x[(isq ? kSC : 0) + n16][0];
+          const int bl = (ti - 2) >> 1;
+          const CT* brow;
+          if (ti < 2) brow = &w.x[2 * kSC + n16][0];
+          else if constexpr (KF) brow = (const CT*)&w.vbd[kSC * bl + n16][0];
+          else brow = &w.vbx[kSC * bl + n16][0];
+          const f32x4 acc = tile_nt<CT, D>(arow, brow, g4);
+          const int j = n16;
+          if (ti == 0) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) w.pp[0][4 * g4 + s][j] = acc[s];
+          } else if (ti == 1) {
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const int i = 4 * g4 + s;
+              w.pp[1][i][j] = (j <= i) ? expf(gi[s] - gj) * acc[s] : 0.f;
+            }
+          } else {
+            const float bo = w.boff[bl];
+#pragma unroll
+            for (int s = 0; s < 4; ++s) {
+              const int i = 4 * g4 + s;
+              const bool vis = bl != beta || j >= i || j < lo;
+              const float sc = expf(gi[s] + bo) * (isq ? 1.f : w.alpha[i]);
+              w.po[isq ? 1 : 0][i][kSC * bl + j] = vis ? sc * acc[s] : 0.f;
+            }
+          }
+        }
+      }
+    }
+    // T = (I + Lm)^-1 needs only wave 0's own Gram tile (H K^T), the decay
+    // scan and alpha: wave 0 forms it now, while waves 1..3 do the Kronecker
+    // reads
+    if (wave == 0) {
+      // the scan's G and the Gram tile were written by other lanes of this
+      // wave: order the LDS accesses (wave-local)
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      // Lm[i][j] = alpha_i e^{G_i - G_j} (h_i . k_j), j < i, is strictly lower
+      // (nilpotent): (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8), factors
+      // that commute; squarings and products on fp32 MFMA.  An accumulator
+      // tile is a k-fragment (B operand); the A operand of each square goes
+      // through LDS.
+      f32x4 xa, ta;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        xa[s] = (n16 < i) ? w.alpha[i] * expf(w.G[i] - w.G[n16]) * w.pp[0][i][n16] : 0.f;
+        w.pp[3][i][n16] = xa[s];
+        ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
+      }
+      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+      __builtin_amdgcn_wave_barrier();
+      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+      int src = 3;
+#pragma unroll
+      for (int step = 0; step < 3; ++step) {
+        const int dst = step & 1 ? 3 : 0;
+        f32x4 sq = zero4();
+        mma(sq, *(const f32x4*)&w.pp[src][n16][4 * g4], xa);  // X^2
+        xa = sq;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) w.pp[dst][4 * g4 + s][n16] = sq[s];
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+        mma(ta, *(const f32x4*)&w.pp[dst][n16][4 * g4], ta);  // T += X^2 T
+        src = dst;
+      }
+#pragma unroll
+      for (int s = 0; s < 4; ++s) w.pp[2][4 * g4 + s][n16] = ta[s];
+    }
+    if (live && wave > 0) {
+      // this workgroup's value tiles over waves 1..3 (wave 0 forms the inverse)
+      for (int l = wave - 1; l < NVTW; l += 3) {
+        const int vt = vb * NVTW + l;
+        Frag bf[D / KS];
+#pragma unroll
+        for (int kb = 0; kb < D / KS; ++kb) bf[kb] = ld_frag(&w.skron[l * 16 + n16][kb * KS], g4);
+#pragma unroll
+        for (int rt = 0; rt < 2; ++rt) {
+          f32x4 acc = zero4();
+#pragma unroll
+          for (int kb = 0; kb < D / KS; ++kb) mma(acc, ld_frag(&w.x[rt * 16 + n16][kb * KS], g4), bf[kb]);
+#pragma unroll
+          for (int s = 0; s < 4; ++s) w.kr[rt * 16 + 4 * g4 + s][vt * 16 + n16] = acc[s];
+        }
+      }
+    }
+    __syncthreads();
+    // window algebra on fp32 MFMA, per wave its VPW value tiles:
+    //   Rhs = alpha u - kco KRh - sum_b Ho_b U_b;  U = T Rhs
+    //   Y   = qco KRq + sum_b Qo_b U_b + Aq U
+    // (an accumulator tile over rows = tokens is directly a k-fragment)
+#pragma unroll
+    for (int a = 0; a < VPW; ++a) {
+      if (!vown(a)) continue;
+      const int v = vtile(a) * 16 + n16;
+      f32x4 acc = zero4();
+#pragma unroll
+      for (int bl = 0; bl < NB; ++bl) mma(acc, *(const f32x4*)&w.po[0][n16][kSC * bl + 4 * g4], uo[bl][a]);
+      f32x4 rhs;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        float r = w.alpha[i] * w.u[i][v] - acc[s];
+        if (live) r -= w.kco[i] * w.kr[i][v];
+        rhs[s] = r;
+      }
+      f32x4 un = zero4();
+      mma(un, *(const f32x4*)&w.pp[2][n16][4 * g4], rhs);
+      f32x4 yv = zero4();
+#pragma unroll
+      for (int bl = 0; bl < NB; ++bl) mma(yv, *(const f32x4*)&w.po[1][n16][kSC * bl + 4 * g4], uo[bl][a]);
+      mma(yv, *(const f32x4*)&w.pp[1][n16][4 * g4], un);
+      CT* yp = (CT*)p.y + tk.y_base + v;
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        float out = yv[s];
+        if (live) out += w.qco[i] * w.kr[kSC + i][v];
+        const int t = c * kSC + i - p.t0;
+        if (t >= 0 && t < T) yp[(size_t)t * tk.y_tok] = from_f<CT>(out);
+      }
+#pragma unroll
+      for (int bl = 0; bl < NB; ++bl)
+        if (bl == beta)
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int i = 4 * g4 + s;
+            if (i >= lo && i < hi) uo[bl][a][s] = un[s];
+          }
+      if (p.ts_u) {   // training stash: this sub-chunk's net writes
+        float* us = p.ts_u + ((size_t)chain * p.nch + c) * kSC * D + v;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) us[(size_t)(4 * g4 + s) * D] = un[s];
+      }
+    }
+    if (p.ts_g && tid == 0 && vb == 0) p.ts_g[(size_t)chain * p.nch + c] = gacc;
+    // block beta's keys for the next sub-chunks: the slots this sub-chunk
+    // wrote take k_j decayed to its end, the others their old keys decayed
+    // over it (8 consecutive keys per thread); the block's offset restarts
+    {
+      const float olds = expf(w.boff[beta] + w.G[kSC - 1]);
+      for (int u8 = tid; u8 < kSC * D / 8; u8 += kNT) {
+        const int j = u8 / DG, d = 8 * (u8 % DG), sl = kSC * beta + j;
+        uint4 kw[W16];
+#pragma unroll
+        for (int q16 = 0; q16 < W16; ++q16) kw[q16] = *(const uint4*)&w.x[2 * kSC + j][d + q16 * (16 / sizeof(CT))];
+        float kf[8];
+        unpack8(kw, kf, (const CT*)nullptr);
+        float sc = w.vsc[j];
+        if (j < lo || j >= hi) {
+          sc = olds;
+          const f32x4 o0 = *(const f32x4*)&w.vbd[sl][d], o1 = *(const f32x4*)&w.vbd[sl][d + 4];
+          kf[0] = o0[0], kf[1] = o0[1], kf[2] = o0[2], kf[3] = o0[3];
+          kf[4] = o1[0], kf[5] = o1[1], kf[6] = o1[2], kf[7] = o1[3];
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) kf[e] *= sc;
+        *(f32x4*)&w.vbd[sl][d] = (f32x4){kf[0], kf[1], kf[2], kf[3]};
+        *(f32x4*)&w.vbd[sl][d + 4] = (f32x4){kf[4], kf[5], kf[6], kf[7]};
+        if constexpr (!KF) store8(&w.vbx[sl][d], kf);
+      }
+    }
+    gacc += w.G[kSC - 1];
+}
+
 // Sub-chunks [c0, c1) of one compaction interval (or the tail) for every
 // chain; the window state enters and leaves through the workspace.  A
 // chain's value columns are split over NVB workgroups (D / 16 / NVB value
@@ -792,23 +1104,6 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
   const G3Tok tk(p, chain, D);
   // sub-chunk c covers global tokens [16 c, 16 c + 16): local token 16 c + i - t0
   auto fetch = [&](Raw& r, int c) { g3_fetch<CT>(p, tk, r, c * kSC + ui - p.t0, has_unit, ud); };
-  auto commit = [&](const Raw& r) {
-    if (!has_unit) return;
-    float hf[8], uu[8];
-    const float part = g3_unpack<CT, DG>(r, tk.gc, hf, uu);
-    store8(&sm.x[ui][ud], hf);
-#pragma unroll
-    for (int w = 0; w < W16; ++w) {
-      *(uint4*)&sm.x[kSC + ui][ud + w * (16 / sizeof(CT))] = g3_raw(r, r.q[w]);
-      *(uint4*)&sm.x[2 * kSC + ui][ud + w * (16 / sizeof(CT))] = g3_raw(r, r.k[w]);
-    }
-    *(f32x4*)&sm.u[ui][ud] = (f32x4){uu[0], uu[1], uu[2], uu[3]};
-    *(f32x4*)&sm.u[ui][ud + 4] = (f32x4){uu[4], uu[5], uu[6], uu[7]};
-    if (tid % DG == 0) {
-      sm.alpha[ui] = stable_alpha_f(part);
-      sm.lg[ui] = log_decay(r.ok ? r.dec : 1.f);
-    }
-  };
 
   // window state: zero for the first interval, else from the workspace.
   // Wave w holds value tiles vtile(a) = vb NVTW + w + 4 a of the workgroup's
@@ -853,228 +1148,17 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
     }
   }
   float gacc = 0.f;
-  // after sub-chunk c: its block is rebased (boff 0), the others decayed by its G_last
-  auto advance_boff = [&](int c, float glast) {
-    if (tid < NB) sm.boff[tid] = (tid == c % NB) ? 0.f : sm.boff[tid] + glast;
-  };
 
   Raw raw;
   fetch(raw, p.c0);
-  for (int c = p.c0; c < p.c1; ++c) {
-    // slots [lo, hi) of block beta receive this call's tokens; the others (the
-    // head a previous call wrote, the tail after the last token) keep the
-    // writes they hold and stay visible to every token of the sub-chunk
-    const int lo = max(0, p.t0 - c * kSC), hi = min(kSC, p.t0 + T - c * kSC);
-    const int beta = c % NB;
-    __syncthreads();
-    if (c > p.c0) advance_boff(c - 1, sm.G[kSC - 1]);
-    commit(raw);
-    if (c + 1 < p.c1) fetch(raw, c + 1);
-    __syncthreads();
-    // per-token scalars | grams and Kronecker reads (MFMA).  Every wave forms
-    // the log-decay prefix sums G (lane i holds G_i); wave 0 publishes the
-    // per-token coefficients.
-    float gl = lane < kSC ? sm.lg[lane] : 0.f;
-#pragma unroll
-    for (int off = 1; off < kSC; off <<= 1) {
-      const float o = __shfl_up(gl, off, 64);
-      if (lane >= off) gl += o;
-    }
-    if (wave == 0) {
-      const float gl_last = __shfl(gl, kSC - 1, 64);
-      if (lane < kSC) {
-        const float e2 = expf(2.f * (gacc + gl));
-        sm.G[lane] = gl;
-        sm.gam[lane] = expf(gl);
-        sm.kco[lane] = sm.alpha[lane] * e2;
-        sm.qco[lane] = e2;
-        sm.vsc[lane] = expf(gl_last - gl);
-      }
-    }
-    // grams, 2 + 2 NB tiles over the waves (tile ti on wave ti mod 4):
-    //   0: H K^T (raw; wave 0 turns it into T),  1: Aq = [j <= i] e^{G_i - G_j} q_i.k_j,
-    //   2 + 2 b: Ho_b = vis alpha_i e^{G_i + boff_b} h_i.Vb_b[j],  3 + 2 b: Qo_b = vis e^{G_i + boff_b} q_i.Vb_b[j]
-    // with vis = [b != beta or j >= i or j < lo]
-    {
-      const float gj = __shfl(gl, n16, 64);
-      float gi[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) gi[s] = __shfl(gl, 4 * g4 + s, 64);
-#pragma unroll
-      for (int r = 0; r < (2 + 2 * NB + 3) / 4; ++r) {
-        const int ti = wave + 4 * r;
-        if (ti < 2 + 2 * NB) {
-          const bool isq = ti & 1;
-          const CT* arow = &sm.x[(isq ? kSC : 0) + n16][0];
-          const int bl = (ti - 2) >> 1;
-          const CT* brow;
-          if (ti < 2) brow = &sm.x[2 * kSC + n16][0];
-          else if constexpr (Sm::KF) brow = (const CT*)&sm.vbd[kSC * bl + n16][0];
-          else brow = &sm.vbx[kSC * bl + n16][0];
-          const f32x4 acc = tile_nt<CT, D>(arow, brow, g4);
-          const int j = n16;
-          if (ti == 0) {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) sm.pp[0][4 * g4 + s][j] = acc[s];
-          } else if (ti == 1) {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              const int i = 4 * g4 + s;
-              sm.pp[1][i][j] = (j <= i) ? expf(gi[s] - gj) * acc[s] : 0.f;
-            }
-          } else {
-            const float bo = sm.boff[bl];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              const int i = 4 * g4 + s;
-              const bool vis = bl != beta || j >= i || j < lo;
-              const float sc = expf(gi[s] + bo) * (isq ? 1.f : sm.alpha[i]);
-              sm.po[isq ? 1 : 0][i][kSC * bl + j] = vis ? sc * acc[s] : 0.f;
-            }
-          }
-        }
-      }
-    }
-    // T = (I + Lm)^-1 needs only wave 0's own Gram tile (H K^T), the decay
-    // scan and alpha: wave 0 forms it now, while waves 1..3 do the Kronecker
-    // reads
-    if (wave == 0) {
-      // the scan's G and the Gram tile were written by other lanes of this
-      // wave: order the LDS accesses (wave-local)
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      // Lm[i][j] = alpha_i e^{G_i - G_j} (h_i . k_j), j < i, is strictly lower
-      // (nilpotent): (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8), factors
-      // that commute; squarings and products on fp32 MFMA.  An accumulator
-      // tile is a k-fragment (B operand); the A operand of each square goes
-      // through LDS.
-      f32x4 xa, ta;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int i = 4 * g4 + s;
-        xa[s] = (n16 < i) ? sm.alpha[i] * expf(sm.G[i] - sm.G[n16]) * sm.pp[0][i][n16] : 0.f;
-        sm.pp[3][i][n16] = xa[s];
-        ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      int src = 3;
-#pragma unroll
-      for (int step = 0; step < 3; ++step) {
-        const int dst = step & 1 ? 3 : 0;
-        f32x4 sq = zero4();
-        mma(sq, *(const f32x4*)&sm.pp[src][n16][4 * g4], xa);  // X^2
-        xa = sq;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) sm.pp[dst][4 * g4 + s][n16] = sq[s];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        mma(ta, *(const f32x4*)&sm.pp[dst][n16][4 * g4], ta);  // T += X^2 T
-        src = dst;
-      }
-#pragma unroll
-      for (int s = 0; s < 4; ++s) sm.pp[2][4 * g4 + s][n16] = ta[s];
-    }
-    if (live && wave > 0) {
-      // this workgroup's value tiles over waves 1..3 (wave 0 forms the inverse)
-      for (int l = wave - 1; l < NVTW; l += 3) {
-        const int vt = vb * NVTW + l;
-        Frag bf[D / KS];
-#pragma unroll
-        for (int kb = 0; kb < D / KS; ++kb) bf[kb] = ld_frag(&sm.skron[l * 16 + n16][kb * KS], g4);
-#pragma unroll
-        for (int rt = 0; rt < 2; ++rt) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int kb = 0; kb < D / KS; ++kb) mma(acc, ld_frag(&sm.x[rt * 16 + n16][kb * KS], g4), bf[kb]);
-#pragma unroll
-          for (int s = 0; s < 4; ++s) sm.kr[rt * 16 + 4 * g4 + s][vt * 16 + n16] = acc[s];
-        }
-      }
-    }
-    __syncthreads();
-    // window algebra on fp32 MFMA, per wave its VPW value tiles:
-    //   Rhs = alpha u - kco KRh - sum_b Ho_b U_b;  U = T Rhs
-    //   Y   = qco KRq + sum_b Qo_b U_b + Aq U
-    // (an accumulator tile over rows = tokens is directly a k-fragment)
-#pragma unroll
-    for (int a = 0; a < VPW; ++a) {
-      if (!vown(a)) continue;
-      const int v = vtile(a) * 16 + n16;
-      f32x4 acc = zero4();
-#pragma unroll
-      for (int bl = 0; bl < NB; ++bl) mma(acc, *(const f32x4*)&sm.po[0][n16][kSC * bl + 4 * g4], uo[bl][a]);
-      f32x4 rhs;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int i = 4 * g4 + s;
-        float r = sm.alpha[i] * sm.u[i][v] - acc[s];
-        if (live) r -= sm.kco[i] * sm.kr[i][v];
-        rhs[s] = r;
-      }
-      f32x4 un = zero4();
-      mma(un, *(const f32x4*)&sm.pp[2][n16][4 * g4], rhs);
-      f32x4 yv = zero4();
-#pragma unroll
-      for (int bl = 0; bl < NB; ++bl) mma(yv, *(const f32x4*)&sm.po[1][n16][kSC * bl + 4 * g4], uo[bl][a]);
-      mma(yv, *(const f32x4*)&sm.pp[1][n16][4 * g4], un);
-      CT* yp = (CT*)p.y + tk.y_base + v;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int i = 4 * g4 + s;
-        float out = yv[s];
-        if (live) out += sm.qco[i] * sm.kr[kSC + i][v];
-        const int t = c * kSC + i - p.t0;
-        if (t >= 0 && t < T) yp[(size_t)t * tk.y_tok] = from_f<CT>(out);
-      }
-#pragma unroll
-      for (int bl = 0; bl < NB; ++bl)
-        if (bl == beta)
-#pragma unroll
-          for (int s = 0; s < 4; ++s) {
-            const int i = 4 * g4 + s;
-            if (i >= lo && i < hi) uo[bl][a][s] = un[s];
-          }
-      if (p.ts_u) {   // training stash: this sub-chunk's net writes
-        float* us = p.ts_u + ((size_t)chain * p.nch + c) * kSC * D + v;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) us[(size_t)(4 * g4 + s) * D] = un[s];
-      }
-    }
-    if (p.ts_g && tid == 0 && vb == 0) p.ts_g[(size_t)chain * p.nch + c] = gacc;
-    // block beta's keys for the next sub-chunks: the slots this sub-chunk
-    // wrote take k_j decayed to its end, the others their old keys decayed
-    // over it (8 consecutive keys per thread); the block's offset restarts
-    {
-      const float olds = expf(sm.boff[beta] + sm.G[kSC - 1]);
-      for (int u8 = tid; u8 < kSC * D / 8; u8 += kNT) {
-        const int j = u8 / DG, d = 8 * (u8 % DG), sl = kSC * beta + j;
-        uint4 w[W16];
-#pragma unroll
-        for (int q16 = 0; q16 < W16; ++q16) w[q16] = *(const uint4*)&sm.x[2 * kSC + j][d + q16 * (16 / sizeof(CT))];
-        float kf[8];
-        unpack8(w, kf, (const CT*)nullptr);
-        float sc = sm.vsc[j];
-        if (j < lo || j >= hi) {
-          sc = olds;
-          const f32x4 o0 = *(const f32x4*)&sm.vbd[sl][d], o1 = *(const f32x4*)&sm.vbd[sl][d + 4];
-          kf[0] = o0[0], kf[1] = o0[1], kf[2] = o0[2], kf[3] = o0[3];
-          kf[4] = o1[0], kf[5] = o1[1], kf[6] = o1[2], kf[7] = o1[3];
-        }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) kf[e] *= sc;
-        *(f32x4*)&sm.vbd[sl][d] = (f32x4){kf[0], kf[1], kf[2], kf[3]};
-        *(f32x4*)&sm.vbd[sl][d + 4] = (f32x4){kf[4], kf[5], kf[6], kf[7]};
-        if constexpr (!Sm::KF) store8(&sm.vbx[sl][d], kf);
-      }
-    }
-    gacc += sm.G[kSC - 1];
-  }
+  const G3WinView<CT, D, P> w{sm.x, sm.u, sm.kr, sm.pp, sm.po, sm.skron, sm.vbd, sm.vbx, sm.G,
+                              sm.alpha, sm.lg, sm.kco, sm.qco, sm.gam, sm.vsc, sm.boff};
+  for (int c = p.c0; c < p.c1; ++c)
+    g3_window_step<CT, D, P, NVB>(w, p, tk, chain, vb, c, c == p.c0, c + 1 < p.c1 ? c + 1 : -1, live, gacc, uo,
+                                  raw);
   __syncthreads();
-  if (p.c1 > p.c0) advance_boff(p.c1 - 1, sm.G[kSC - 1]);
+  if (p.c1 > p.c0 && tid < NB)   // the last sub-chunk's block rebased, the others decayed
+    sm.boff[tid] = (tid == (p.c1 - 1) % NB) ? 0.f : sm.boff[tid] + sm.G[kSC - 1];
   __syncthreads();
   // window state out (and the final state after the last sub-chunk): the
   // value columns from their workgroup, the keys and decays from the first
@@ -1527,9 +1611,9 @@ struct G3CompactSmem {
 // from the factors Af [R][m], Bf [R][n] (LDS), in blocks: a thread takes one
 // factor entry (iv, ik) (TPP threads share one, splitting its b_v rows) and
 // writes the entries (iv b_v + jv, ik b_k + jk) it scales, 8 contiguous k
-// per store
+// per store (ld: the row stride of sk)
 template <int D, typename CT>
-__device__ __forceinline__ void write_skron(CT* sk, const float* Af, const float* Bf, int tid) {
+__device__ __forceinline__ void write_skron(CT* sk, const float* Af, const float* Bf, int tid, int ld = D) {
   typedef G3D<D> Ge;
   constexpr int TPP = kNT / Ge::m, RPT = Ge::bv / TPP;
   static_assert(kNT % Ge::m == 0 && Ge::bv % TPP == 0 && Ge::bk == 8, "skron blocking");
@@ -1554,8 +1638,134 @@ __device__ __forceinline__ void write_skron(CT* sk, const float* Af, const float
         sv[4 + jk] += a[r] * b1[jk];
       }
     }
-    store8(sk + (size_t)(iv * Ge::bv + jv) * D + ik * Ge::bk, sv);
+    store8(sk + (size_t)(iv * Ge::bv + jv) * ld + ik * Ge::bk, sv);
   }
+}
+
+// ---------------------------------------------------------------------------
+// fused forward for the layer's default regime (a compaction after every
+// 16-token window: K_c = P = 16): one workgroup per chain walks all of a
+// call's windows, each a window step followed by its compaction, with the
+// window state, the factors and the Kronecker matrix in LDS (no launch or
+// global round trip between the two)
+// ---------------------------------------------------------------------------
+template <typename CT, int D>
+struct G3FusedSmem {
+  static constexpr int P = kSC;
+  union alignas(16) Phase {
+    G3Compact<D, P, false> cs;          // the compaction's scratch
+    struct alignas(16) Win {            // the window step's
+      CT x[3 * kSC][D + 8];
+      float u[kSC][D + 4];
+      float kr[2 * kSC][D + 4];
+      float pp[4][kSC][kSC + 4];
+      float po[2][kSC][P + 4];
+      CT skron[D][D + 8];               // rebuilt from the factors after every compaction
+      float G[kSC], alpha[kSC], lg[kSC], kco[kSC], qco[kSC], gam[kSC], vsc[kSC];
+    } w;
+  } ph;
+  alignas(16) float ab[kAB];            // A | B of this chain
+  alignas(16) float uwin[P][D + 4];     // the window's net writes (slot-major)
+  alignas(16) float vbd[P][D + 4];      // its keys, decayed to now
+  alignas(16) CT vbx[sizeof(CT) == 4 ? 1 : P][D + 8];
+  float boff[1];
+};
+template <typename CT, int D>
+constexpr bool fused_fits() { return sizeof(G3FusedSmem<CT, D>) <= 160 * 1024; }
+
+template <typename CT, int D>
+__global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
+  constexpr int P = kSC;
+  typedef G3FusedSmem<CT, D> Sm;
+  __shared__ Sm sm;
+  static_assert(sizeof(Sm) <= 160 * 1024, "LDS budget");
+  typedef G3D<D> Ge;
+  constexpr int Rm = Ge::R * Ge::m, Rn = Ge::R * Ge::n, VPW = (D / 16 + 3) / 4;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g4 = lane >> 4, n16 = lane & 15;
+  const int N = p.B * p.H * p.M;
+  const int chain = xcd_remap(blockIdx.x, N);
+  const G3Tok tk(p, chain, D);
+  const int DG = D / 8, ui = tid / DG, ud = 8 * (tid % DG);
+  const bool has_unit = tid < kSC * DG;
+
+  // the call's sub-chunks, each its own compaction interval
+  const long long tend = (long long)p.t0 + p.T;
+  const int cg0 = p.t0 / kSC, cg1 = (int)((tend + kSC - 1) / kSC);
+  const bool carried = p.A0 != nullptr;
+  G3Raw<CT> raw;
+  g3_fetch<CT>(p, tk, raw, cg0 * kSC + ui - p.t0, has_unit, ud);
+
+  // initial state: the carried one (A0, B0 [N][R m|n], U0, Vb0 [N][D][P]) or zero
+  const size_t cb = (size_t)chain * D * P;
+  for (int e = tid; e < Rm; e += kNT) sm.ab[e] = carried ? p.A0[(size_t)chain * Rm + e] : 0.f;
+  for (int e = tid; e < Rn; e += kNT) sm.ab[Rm + e] = carried ? p.B0[(size_t)chain * Rn + e] : 0.f;
+  for (int e = tid; e < D * P; e += kNT) {
+    const int d = e / P, j = e % P;
+    const float uv = carried ? p.U0[cb + e] : 0.f, kv = carried ? p.Vb0[cb + e] : 0.f;
+    sm.uwin[j][d] = uv;
+    sm.vbd[j][d] = kv;
+    if constexpr (sizeof(CT) == 2) sm.vbx[j][d] = from_f<CT>(kv);
+  }
+  if (tid == 0) sm.boff[0] = 0.f;
+  __syncthreads();
+  if (carried) write_skron<D, CT>(&sm.ph.w.skron[0][0], sm.ab, sm.ab + Rm, tid, D + 8);
+  bool live = carried;
+  float gacc = 0.f;
+  int event = 0;
+  const G3WinView<CT, D, P> w{sm.ph.w.x, sm.ph.w.u, sm.ph.w.kr, sm.ph.w.pp, sm.ph.w.po, sm.ph.w.skron, sm.vbd,
+                              sm.vbx, sm.ph.w.G, sm.ph.w.alpha, sm.ph.w.lg, sm.ph.w.kco, sm.ph.w.qco,
+                              sm.ph.w.gam, sm.ph.w.vsc, sm.boff};
+  f32x4 uo[1][VPW];
+  for (int c = cg0; c < cg1; ++c) {
+    // the window step (its net writes through the registers of their waves)
+#pragma unroll
+    for (int a = 0; a < VPW; ++a)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int vt = wave + 4 * a;
+        uo[0][a][s] = vt < D / 16 ? sm.uwin[4 * g4 + s][vt * 16 + n16] : 0.f;
+      }
+    g3_window_step<CT, D, P, 1>(w, p, tk, chain, 0, c, true, -1, live, gacc, uo, raw);
+#pragma unroll
+    for (int a = 0; a < VPW; ++a)
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int vt = wave + 4 * a;
+        if (vt < D / 16) sm.uwin[4 * g4 + s][vt * 16 + n16] = uo[0][a][s];
+      }
+    const bool complete = (long long)(c + 1) * kSC <= tend;
+    __syncthreads();
+    if (!complete) break;   // the tail: no compaction follows
+    // its compaction (gdn3/gdn3_upgrade.py:650-719), the factors decayed by e^{gacc}
+    const int qs = p.cmode ? Ge::R : Ge::q;
+    g3_compact<D, P>(sm.ph.cs, sm.ab, &sm.uwin[0][0], &sm.vbd[0][0], (size_t)(D + 4), (size_t)1, gacc, p.sdec,
+                     p.sketch + (size_t)chain * Ge::n * qs,
+                     p.stats ? p.stats + ((size_t)event * N + chain) * 2 : nullptr, tid, p.cmode);
+    __syncthreads();
+    if (p.train_states) {   // the factors after every compaction, for the backward
+      const G3Stash ts = g3_stash(p.train_states, N, p.nch, p.T / p.Kc, D, kSC, Ge::RMN);
+      for (int e = tid; e < Rm + Rn; e += kNT) ts.ab[((size_t)event * N + chain) * Ge::RMN + e] = sm.ab[e];
+    }
+    ++event;
+    gacc = 0.f;
+    live = true;
+    if (c + 1 < cg1) {   // the next window's loads (under the Kronecker matrix's rebuild)
+      g3_fetch<CT>(p, tk, raw, (c + 1) * kSC + ui - p.t0, has_unit, ud);
+      write_skron<D, CT>(&sm.ph.w.skron[0][0], sm.ab, sm.ab + Rm, tid, D + 8);
+    }
+  }
+  __syncthreads();
+  // the final state: U, Vb [N][D][P]; A, B (decayed since the last compaction)
+  const float dk = expf(gacc);
+  for (int e = tid; e < D * P; e += kNT) {
+    const int d = e / P, j = e % P;
+    if (p.U_out) p.U_out[cb + e] = sm.uwin[j][d];
+    if (p.Vb_out) p.Vb_out[cb + e] = sm.vbd[j][d];
+  }
+  if (p.A_out)
+    for (int e = tid; e < Rm; e += kNT) p.A_out[(size_t)chain * Rm + e] = sm.ab[e] * dk;
+  if (p.B_out)
+    for (int e = tid; e < Rn; e += kNT) p.B_out[(size_t)chain * Rn + e] = sm.ab[Rm + e] * dk;
 }
 
 template <int D, int P, typename CT>
@@ -1793,6 +2003,17 @@ template <typename CT, int D, int P>
 int run_gdn3_fwd(G3FwdArgs a, hipStream_t stream) {
   typedef G3D<D> Ge;
   const int N = a.B * a.H * a.M;
+  if constexpr (P == kSC && fused_fits<CT, D>()) {
+    if (a.Kc == kSC) {   // the layer's default regime: one fused launch for the whole call
+      a.nch = (a.T + kSC - 1) / kSC;
+      G3Stash ts{nullptr, nullptr, nullptr};
+      if (a.train_states) ts = g3_stash(a.train_states, N, a.nch, a.T / a.Kc, D, kSC, Ge::RMN);
+      a.ts_u = ts.u;
+      a.ts_g = ts.gacc;
+      hipLaunchKernelGGL((gdn3_fused_kernel<CT, D>), dim3(N), dim3(kNT), 0, stream, a);
+      return check_launch("gdn3_fused_kernel");
+    }
+  }
   char* w = (char*)a.workspace;
   a.skron = w;
   w += align256((size_t)N * D * D * sizeof(CT));

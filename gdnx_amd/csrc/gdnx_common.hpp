@@ -84,6 +84,15 @@ __device__ __forceinline__ f32x4 zero4() { return (f32x4){0.f, 0.f, 0.f, 0.f}; }
 // stores before it are not made visible to the other waves.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
+// The thread index as a value the compiler cannot prove invariant: index
+// arithmetic derived from it is recomputed where it is used rather than
+// hoisted out of an enclosing loop and held in registers across the loop's
+// other phases (where those registers are wanted for loads in flight).
+__device__ __forceinline__ int opaque(int x) {
+  asm volatile("" : "+v"(x));
+  return x;
+}
+
 // 4 consecutive CT values from floats (for 8/16-byte LDS stores).
 __device__ __forceinline__ void st4(bf16* p, float a, float b, float c, float d) {
   *(bf16x4*)p = (bf16x4){(bf16)a, (bf16)b, (bf16)c, (bf16)d};
