@@ -92,12 +92,6 @@ struct alignas(16) BwdGradSmem {
   GradLaneBuf<C, NW, NP> lb[2];
 };
 
-// The value unchanged, but opaque to the optimizer.
-__device__ __forceinline__ int opaque(int x) {
-  asm volatile("" : "+v"(x));
-  return x;
-}
-
 // One lane's inputs to the gradient kernel, fetched a lane ahead: this
 // wave's rows of S0 and dS_C (raw tiles, one per 16 value columns, for each
 // of its key tiles), this thread's share of the R / dB tiles and of dY (all

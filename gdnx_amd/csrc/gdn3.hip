@@ -174,13 +174,18 @@ __device__ __forceinline__ void jacobi_rot(double app, double aqq, double apq, d
   // interleave.  h only sets the angle: it is x times the hardware reciprocal
   // square root (about 2^-23 relative, 0 at x = 0), and a rotation that
   // leaves 1e-7 of a_pq behind still converges within the same sweeps; c and
-  // s are normalised by the refined rsqrt, so c^2 + s^2 = 1 to rounding.
+  // s are normalised by the refined one, so c^2 + s^2 = 1 to rounding.
   const double d = aqq - app, e = 2.0 * apq;
   const double x = fma(d, d, e * e);
   const double h = x * __builtin_amdgcn_rsq(fmax(x, 2.2250738585072014e-308));
   const double w = fabs(d) + h;
   const double q = fma(w, w, e * e);
-  const double r = rsqrt(q);
+  // 1 / sqrt(q): the hardware estimate r0 and the Halley-order correction
+  // r0 (1 + t/2 + 3 t^2/8), t = 1 - q r0^2 (error O(t^3), below fp64 rounding);
+  // q = 0 gives a NaN here, which the selects below discard
+  const double r0 = __builtin_amdgcn_rsq(q);
+  const double t = fma(-q * r0, r0, 1.0);
+  const double r = fma(r0 * t, fma(t, 0.375, 0.5), r0);
   // sgn(th) |e| = sgn(d) e for d != 0, and |e| for d == 0 (th = +-0 counts as >= 0)
   const double num = d == 0.0 ? fabs(e) : (d > 0.0 ? e : -e);
   const bool ok = q > 0.0;  // false only when a_pq = 0 and a_pp = a_qq (or both underflow)
@@ -494,9 +499,13 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   // (i, j) holds W[i][j] and V[i][j].  Each round rotates 4 disjoint pairs;
   // a lane gathers every operand of its round in one exchange and forms the
   // rotations of both its pairs (that of i and that of j) itself, from the
-  // same entries the lanes of those indices use.
+  // same entries the lanes of those indices use.  The exchange goes through
+  // LDS (xa, xv): one wave's LDS accesses complete in issue order, so a
+  // round's reads see its writes and the next round's writes follow them.
   if (wave == 0) {
     const int i = lane >> 3, j = lane & 7;
+    double* xa = cs.rinv;   // 64 doubles each, free after the last Cholesky-QR pass
+    double* xv = cs.ev;
     double a;
     {  // W from the MFMA layout (lane l: W[l/16 + 4e][l%16]), upper entry for both (i, j) and (j, i)
       const f64x4 w = gram_mfma<n>(cs.z, lane);
@@ -513,10 +522,12 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
       for (int st = 0; st < 7; ++st) {
         const int pi = rr_partner(i, st), pj = rr_partner(j, st);
         const int i0 = min(i, pi), i1 = max(i, pi), j0 = min(j, pj), j1 = max(j, pj);
-        const double ai0 = __shfl(a, 9 * i0, 64), ai1 = __shfl(a, 9 * i1, 64), aio = __shfl(a, 8 * i0 + i1, 64);
-        const double aj0 = __shfl(a, 9 * j0, 64), aj1 = __shfl(a, 9 * j1, 64), ajo = __shfl(a, 8 * j0 + j1, 64);
-        const double a_ipj = __shfl(a, 8 * i + pj, 64), a_pij = __shfl(a, 8 * pi + j, 64);
-        const double a_pipj = __shfl(a, 8 * pi + pj, 64), v_ipj = __shfl(vv, 8 * i + pj, 64);
+        xa[lane] = a;
+        xv[lane] = vv;
+        const double ai0 = xa[9 * i0], ai1 = xa[9 * i1], aio = xa[8 * i0 + i1];
+        const double aj0 = xa[9 * j0], aj1 = xa[9 * j1], ajo = xa[8 * j0 + j1];
+        const double a_ipj = xa[8 * i + pj], a_pij = xa[8 * pi + j];
+        const double a_pipj = xa[8 * pi + pj], v_ipj = xv[8 * i + pj];
         double ci, si, cj, sj;
         jacobi_rot(ai0, ai1, aio, ci, si);
         jacobi_rot(aj0, aj1, ajo, cj, sj);
@@ -528,18 +539,18 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     }
     cs.ev[lane] = vv;  // ev[i][j]: component i of eigenvector j
     if (i == j) cs.lam[i] = a;
-  }
-  __syncthreads();
-  if (tid < kQ) {  // rank of eigenvalue tid, descending, ties by index
-    const double li = cs.lam[tid];
-    int rk = 0;
-    for (int j = 0; j < kQ; ++j) rk += (cs.lam[j] > li || (cs.lam[j] == li && j < tid)) ? 1 : 0;
-    cs.order[rk] = tid;
-  }
-  __syncthreads();
-  if (tid < R) {
-    const double l = cs.lam[cs.order[tid]];
-    cs.sig[tid] = l > 0.0 ? sqrt(l) : 0.0;
+    // (still wave 0 alone, in LDS issue order) rank of eigenvalue `lane`,
+    // descending, ties by index; then the kept singular values
+    if (lane < kQ) {
+      const double li = cs.lam[lane];
+      int rk = 0;
+      for (int k = 0; k < kQ; ++k) rk += (cs.lam[k] > li || (cs.lam[k] == li && k < lane)) ? 1 : 0;
+      cs.order[rk] = lane;
+    }
+    if (lane < R) {
+      const double l = cs.lam[cs.order[lane]];
+      cs.sig[lane] = l > 0.0 ? sqrt(l) : 0.0;
+    }
   }
   __syncthreads();
   // leading singular vectors: u_r = Q ev_r, v_r = Bm^T ev_r / sigma_r
