@@ -84,13 +84,12 @@ struct G3Compact {
   alignas(16) float zt[kQ * lzn];         // the sketch (zero padded), then z, in fp32 column-major
   alignas(16) float ut[STG ? 16 : 1][D + 4];   // a block of 16 window slots: net writes U_p
   alignas(16) float vt[STG ? 16 : 1][D + 4];   // and keys Vb_p
-  alignas(16) double us[kRMax][m];        // leading left singular vectors of R_mat
-  alignas(16) double vs[kRMax][n];        // leading right singular vectors
   double red[4 * 64];
   double rinv[kQ * kQ];                   // the summed Gram Y^T Y of a Cholesky-QR pass (row-major)
   double ev[kQ * kQ];                     // eigenvectors of Bm Bm^T (columns)
   double lam[kQ];
   double sig[kRMax];
+  double isig[kRMax];                     // 1 / sig (0 where sig is)
   double sgn[kRMax];
   int order[kQ];
 };
@@ -342,6 +341,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     const int e = tid + u * kNT, c = e / kQ, j = e % kQ;
     gsv[u] = (e < n * kQ && j < qs) ? sketch[c * qs + j] : 0.f;
   }
+  double en[1] = {0.0};
   // residual part rearrange(U Vb^T) on fp32 MFMA: out[v][k] = sum_p U_p[v] Vb_p[k]
   // (A[v][p] = U_p[v], B[p][k] = Vb_p[k]), accumulated over the window's
   // blocks of 16 slots staged through LDS; wave w owns the value-row tiles
@@ -391,58 +391,47 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
         }
       }
     }
+    // plus the Kronecker part sum_r A_r[iv][ik] B_r[jv][jk] (each factor decayed
+    // by e^{gacc}), and the energy |R_mat|^2.  With b_v = b_k = 8 a lane's
+    // jk = n16 mod 8 and jv = (4 g4 + i) mod 8 are fixed (its B entries load
+    // once), iv = 2 vt + g4 / 2 follows the value tile and ik = 2 kt + n16 / 8
+    // the key tile (R A entries per tile pair, 4 addresses per wave)
+    static_assert(Ge::bv == 8 && Ge::bk == 8, "lane-fixed Kronecker columns");
+    const float sc2 = expf(2.f * gacc);
+    float bl[4][kRMax];
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+#pragma unroll
+      for (int r = 0; r < kRMax; ++r)
+        bl[i][r] = r < R ? sc2 * Bv[r * n + ((4 * g4 + i) & 7) * bk + (n16 & 7)] : 0.f;
+    double e4[4] = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
     for (int vi = 0; vi < VTW; ++vi) {
-      const int vt = wave * VTW + vi;
+      const int vt = wave * VTW + vi, iv = 2 * vt + (g4 >> 1);
 #pragma unroll
       for (int kt = 0; kt < NT16; ++kt) {
-        const int k = kt * 16 + n16, ik = k >> lbk, jk = k & (bk - 1);
+        const int ik = 2 * kt + (n16 >> 3), jk = n16 & 7, row = iv * ak + ik;
+        float al[kRMax];
+#pragma unroll
+        for (int r = 0; r < kRMax; ++r) al[r] = r < R ? A[r * m + row] : 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int v = vt * 16 + 4 * g4 + i, iv = v >> lbv, jv = v & (Ge::bv - 1);
-          cs.rm[(iv * ak + ik) * ldr + jv * bk + jk] = racc[vi][kt][i];
+          const int jv = (4 * g4 + i) & 7;
+          float sv = racc[vi][kt][i];
+#pragma unroll
+          for (int r = 0; r < kRMax; ++r)
+            if (r < R) sv += al[r] * bl[i][r];
+          cs.rm[row * ldr + jv * bk + jk] = sv;
+          e4[i] += (double)sv * (double)sv;
         }
       }
     }
+    en[0] = (e4[0] + e4[1]) + (e4[2] + e4[3]);
   }
 #pragma unroll
   for (int u = 0; u < NGS; ++u) {
     const int e = tid + u * kNT;
     if (e < n * kQ) cs.zt[(e % kQ) * lzn + e / kQ] = gsv[u];
-  }
-  __syncthreads();
-  // Kronecker part (A, B each decayed by e^{gacc}) and the energy |R_mat|^2
-  const float sc2 = expf(2.f * gacc);
-  double en[1] = {0.0};
-  {
-    // n <= 256 is a power of two: thread (group, col) updates one column on
-    // the group's block of RPG consecutive rows; the A entries of 4 rows are
-    // one broadcast vector load per factor, the energy runs in 4 chains
-    constexpr int NG = kNT >> ln, RPG = m / NG;
-    static_assert(m % NG == 0 && RPG % 4 == 0, "row blocks of whole 4-row steps");
-    const int col = tid & (n - 1), r0 = (tid >> ln) * RPG;
-    float bcol[kRMax];
-#pragma unroll
-    for (int r = 0; r < kRMax; ++r) bcol[r] = r < R ? sc2 * Bv[r * n + col] : 0.f;
-    double e4[4] = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll 2
-    for (int rb = 0; rb < RPG; rb += 4) {
-      const int row = r0 + rb;
-      f32x4 av[kRMax];
-#pragma unroll
-      for (int r = 0; r < kRMax; ++r)
-        if (r < R) av[r] = *(const f32x4*)&A[r * m + row];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        float sv = cs.rm[(row + u) * ldr + col];
-#pragma unroll
-        for (int r = 0; r < kRMax; ++r)
-          if (r < R) sv += av[r][u] * bcol[r];
-        cs.rm[(row + u) * ldr + col] = sv;
-        e4[u] += (double)sv * (double)sv;
-      }
-    }
-    en[0] = (e4[0] + e4[1]) + (e4[2] + e4[3]);
   }
   block_sum<1>(en, cs.red, tid);
 
@@ -547,25 +536,41 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
       for (int k = 0; k < kQ; ++k) rk += (cs.lam[k] > li || (cs.lam[k] == li && k < lane)) ? 1 : 0;
       cs.order[rk] = lane;
     }
-    if (lane < R) {
+    if (lane < R) {   // sigma = l / sqrt(l) and 1 / sigma from one refined reciprocal square root
       const double l = cs.lam[cs.order[lane]];
-      cs.sig[lane] = l > 0.0 ? sqrt(l) : 0.0;
+      const double r0 = __builtin_amdgcn_rsq(fmax(l, 2.2250738585072014e-308));
+      const double t = fma(-l * r0, r0, 1.0);
+      const double rs = fma(r0 * t, fma(t, 0.375, 0.5), r0);
+      cs.sig[lane] = l > 0.0 ? l * rs : 0.0;
+      cs.isig[lane] = l > 0.0 ? rs : 0.0;
     }
   }
   __syncthreads();
-  // leading singular vectors: u_r = Q ev_r, v_r = Bm^T ev_r / sigma_r
-  for (int row = tid; row < m; row += kNT)
-    for (int r = 0; r < R; ++r) {
-      const int o = cs.order[r];
+  // leading singular vectors: u_r = Q ev_r (a row per thread, kept in
+  // registers for the blend), v_r = Bm^T ev_r / sigma_r
+  static_assert(m <= kNT && n <= 64, "left vectors: a row per thread; right vectors: a column per lane of a wave");
+  const float dk = expf(gacc);
+  const float s1 = sdec, s2 = 1.f - sdec;
+  int ord[kRMax];
+#pragma unroll
+  for (int r = 0; r < kRMax; ++r) ord[r] = r < R ? cs.order[r] : 0;
+  double ur[kRMax];
+  if (tid < m) {
+    double yv[kQ];
+#pragma unroll
+    for (int j = 0; j < kQ; ++j) yv[j] = cs.y[tid * kQ + j];
+#pragma unroll
+    for (int r = 0; r < kRMax; ++r) {
       double s = 0.0;
 #pragma unroll
-      for (int j = 0; j < kQ; ++j) s += cs.y[row * kQ + j] * cs.ev[j * kQ + o];
-      cs.us[r][row] = s;
+      for (int j = 0; j < kQ; ++j) s += yv[j] * cs.ev[j * kQ + ord[r]];
+      ur[r] = s;
     }
-  // v_r = Bm^T ev_r / sigma_r in wave 0 (one column per lane, n <= 64),
-  // which also fixes each pair's canonical sign: argmax_c |v_r[c]|, first
-  // index on ties (an xor butterfly, so every lane holds the same winner)
-  static_assert(n <= 64, "right singular vectors: one column per lane of a wave");
+  }
+  // wave 0: v_r (one column per lane) and each pair's canonical sign,
+  // argmax_c |v_r[c]| with the first index on ties (an all-reduce by row
+  // rotations inside each 16-lane row, then across the rows), then the
+  // blend of B, which needs nothing from the other waves
   if (wave == 0) {
     const int c = lane;
     const bool on = c < n;
@@ -575,50 +580,51 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     for (int r = 0; r < kRMax; ++r) {
       vr[r] = 0.0;
       if (r < R && on) {
-        const int o = cs.order[r];
-        const double sg = cs.sig[r];
         double sv = 0.0;
 #pragma unroll
-        for (int j = 0; j < kQ; ++j) sv += cs.z[c * kQ + j] * cs.ev[j * kQ + o];
-        vr[r] = sg > 0.0 ? sv / sg : (c == r ? 1.0 : 0.0);
-        cs.vs[r][c] = vr[r];
+        for (int j = 0; j < kQ; ++j) sv += cs.z[c * kQ + j] * cs.ev[j * kQ + ord[r]];
+        vr[r] = cs.sig[r] > 0.0 ? sv * cs.isig[r] : (c == r ? 1.0 : 0.0);
       }
       bv_[r] = on ? fabs(vr[r]) : -1.0;
       bi[r] = on ? c : 0x7fffffff;
     }
-    // the R reductions run side by side
+    auto take = [&](int r, double ov, int oi) {
+      const bool t = (ov > bv_[r]) | ((ov == bv_[r]) & (oi < bi[r]));  // selects, no branches
+      bv_[r] = t ? ov : bv_[r];
+      bi[r] = t ? oi : bi[r];
+    };
+#define G3_ARGMAX_ROT(CTL)                                                                     \
+    _Pragma("unroll") for (int r = 0; r < kRMax; ++r) if (r < R) {                            \
+      take(r, dpp_f64<CTL>(bv_[r]), __builtin_amdgcn_update_dpp(0, bi[r], CTL, 0xf, 0xf, false)); \
+    }
+    G3_ARGMAX_ROT(0x128)
+    G3_ARGMAX_ROT(0x124)
+    G3_ARGMAX_ROT(0x122)
+    G3_ARGMAX_ROT(0x121)
+#undef G3_ARGMAX_ROT
 #pragma unroll
-    for (int o2 = 32; o2 > 0; o2 >>= 1)
+    for (int o2 = 16; o2 <= 32; o2 <<= 1)
 #pragma unroll
       for (int r = 0; r < kRMax; ++r)
-        if (r < R) {
-          const double ov = __shfl_xor(bv_[r], o2, 64);
-          const int oi = __shfl_xor(bi[r], o2, 64);
-          const bool take = (ov > bv_[r]) | ((ov == bv_[r]) & (oi < bi[r]));  // selects, no branches
-          bv_[r] = take ? ov : bv_[r];
-          bi[r] = take ? oi : bi[r];
-        }
+        if (r < R) take(r, __shfl_xor(bv_[r], o2, 64), __shfl_xor(bi[r], o2, 64));
 #pragma unroll
     for (int r = 0; r < kRMax; ++r)
       if (r < R) {
         const double vb = __shfl(vr[r], bi[r] & 63, 64);
-        if (lane == 0) cs.sgn[r] = (bi[r] != 0x7fffffff && vb < 0.0) ? -1.0 : 1.0;
+        const double sg = (bi[r] != 0x7fffffff && vb < 0.0) ? -1.0 : 1.0;
+        if (lane == 0) cs.sgn[r] = sg;
+        if (on) Bv[r * n + c] = s1 * (Bv[r * n + c] * dk) + s2 * (float)(sg * vr[r]);
       }
   }
   __syncthreads();
-  // two-timescale blend of the decayed factors with the SVD factors
-  const float dk = expf(gacc);
-  const float s1 = sdec, s2 = 1.f - sdec;
-  for (int e = tid; e < R * m; e += kNT) {
-    const int r = e / m, row = e % m;
-    const double sv = cs.sgn[r] * cs.sig[r] * cs.us[r][row];
-    A[e] = s1 * (A[e] * dk) + s2 * (float)sv;
-  }
-  for (int e = tid; e < R * n; e += kNT) {
-    const int r = e / n, col = e % n;
-    const double sv = cs.sgn[r] * cs.vs[r][col];
-    Bv[e] = s1 * (Bv[e] * dk) + s2 * (float)sv;
-  }
+  // two-timescale blend of the decayed factors with the SVD factors (B above)
+  if (tid < m)
+#pragma unroll
+    for (int r = 0; r < kRMax; ++r)
+      if (r < R) {
+        const double sv = cs.sgn[r] * cs.sig[r] * ur[r];
+        A[r * m + tid] = s1 * (A[r * m + tid] * dk) + s2 * (float)sv;
+      }
   if (tid == 0 && stats) {
     double kept = 0.0;
     for (int r = 0; r < R; ++r) kept += cs.sig[r] * cs.sig[r];
