@@ -86,12 +86,11 @@ struct G3Compact {
   alignas(16) float vt[STG ? 16 : 1][D + 4];   // and keys Vb_p
   double red[4 * 64];
   double rinv[kQ * kQ];                   // the summed Gram Y^T Y of a Cholesky-QR pass (row-major)
-  double ev[kQ * kQ];                     // eigenvectors of Bm Bm^T (columns)
+  double ev[kQ * kQ];                     // eigenvectors of Bm Bm^T (rows, in rank order)
   double lam[kQ];
   double sig[kRMax];
   double isig[kRMax];                     // 1 / sig (0 where sig is)
   double sgn[kRMax];
-  int order[kQ];
 };
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
@@ -161,6 +160,15 @@ __device__ __forceinline__ void rm_mfma(const float* rm, const float* bt, double
     }
 }
 
+// 1 / sqrt(x) for x > 0 to fp64 rounding: the hardware estimate r0 and the
+// Halley-order correction r0 (1 + t/2 + 3 t^2/8), t = 1 - x r0^2 (error
+// O(t^3)).  x = 0 gives a NaN (callers select it away).
+__device__ __forceinline__ double rsqrt_f64(double x) {
+  const double r0 = __builtin_amdgcn_rsq(x);
+  const double t = fma(-x * r0, r0, 1.0);
+  return fma(r0 * t, fma(t, 0.375, 0.5), r0);
+}
+
 // Jacobi rotation zeroing a_pq (Numerical Recipes convention):
 // J[p][p] = J[q][q] = c, J[p][q] = s, J[q][p] = -s, with the smaller angle
 // t = sgn(th) / (|th| + sqrt(th^2 + 1)), th = (a_qq - a_pp) / (2 a_pq).
@@ -179,12 +187,7 @@ __device__ __forceinline__ void jacobi_rot(double app, double aqq, double apq, d
   const double h = x * __builtin_amdgcn_rsq(fmax(x, 2.2250738585072014e-308));
   const double w = fabs(d) + h;
   const double q = fma(w, w, e * e);
-  // 1 / sqrt(q): the hardware estimate r0 and the Halley-order correction
-  // r0 (1 + t/2 + 3 t^2/8), t = 1 - q r0^2 (error O(t^3), below fp64 rounding);
-  // q = 0 gives a NaN here, which the selects below discard
-  const double r0 = __builtin_amdgcn_rsq(q);
-  const double t = fma(-q * r0, r0, 1.0);
-  const double r = fma(r0 * t, fma(t, 0.375, 0.5), r0);
+  const double r = rsqrt_f64(q);   // q = 0: NaN, discarded by the selects below
   // sgn(th) |e| = sgn(d) e for d != 0, and |e| for d == 0 (th = +-0 counts as >= 0)
   const double num = d == 0.0 ? fabs(e) : (d > 0.0 ? e : -e);
   const bool ok = q > 0.0;  // false only when a_pq = 0 and a_pp = a_qq (or both underflow)
@@ -255,7 +258,7 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int
 #pragma unroll
     for (int k = 0; k < kQ; ++k) {
       const double akk = L[k][k];
-      const double rq = rsqrt(fmax(akk, 2.2250738585072014e-308));  // unconditional: a select, no branch
+      const double rq = rsqrt_f64(fmax(akk, 2.2250738585072014e-308));  // unconditional: a select, no branch
       const double rd = (akk > tol && akk > 0.0) ? rq : 0.0;
       rdv[k] = rd;   // 1 / R[k][k] (R[k][k] = akk rd = sqrt(akk))
 #pragma unroll
@@ -484,35 +487,46 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   // Bm^T = R_mat^T Q  [n][kQ]
   rm_mfma<true, n, m, ldr, lym>(cs.rm, cs.yt, cs.z, nullptr, tid);
   __syncthreads();
+  {  // W = Bm Bm^T: each wave's partial Gram over a quarter of the rows of Bm^T
+    static_assert(n % 16 == 0, "quarters of whole MFMA steps");
+    const f64x4 g = gram_mfma<n / 4>(cs.z + wave * (n / 4) * kQ, lane);
+    const int r = lane >> 4, c = lane & 15;
+    if (c < kQ) {
+      cs.red[wave * 64 + r * kQ + c] = g[0];
+      cs.red[wave * 64 + (r + 4) * kQ + c] = g[1];
+    }
+  }
+  __syncthreads();
   // eigen-decomposition of W = Bm Bm^T by cyclic Jacobi in wave 0: lane
   // (i, j) holds W[i][j] and V[i][j].  Each round rotates 4 disjoint pairs;
   // a lane gathers every operand of its round in one exchange and forms the
   // rotations of both its pairs (that of i and that of j) itself, from the
   // same entries the lanes of those indices use.  The exchange goes through
-  // LDS (xa, xv): one wave's LDS accesses complete in issue order, so a
-  // round's reads see its writes and the next round's writes follow them.
+  // LDS (xa, xv), ordered by wave_lds_sync (the next round's writes depend
+  // on this round's reads, so they cannot move above them).
   if (wave == 0) {
     const int i = lane >> 3, j = lane & 7;
     double* xa = cs.rinv;   // 64 doubles each, free after the last Cholesky-QR pass
     double* xv = cs.ev;
     double a;
-    {  // W from the MFMA layout (lane l: W[l/16 + 4e][l%16]), upper entry for both (i, j) and (j, i)
-      const f64x4 w = gram_mfma<n>(cs.z, lane);
-      const int r = min(i, j), c = max(i, j);
-      const double w0 = __shfl(w[0], (r & 3) * 16 + c, 64), w1 = __shfl(w[1], (r & 3) * 16 + c, 64);
-      a = r < 4 ? w0 : w1;
+    {  // the partials summed, upper entry for both (i, j) and (j, i)
+      const int e = min(i, j) * kQ + max(i, j);
+      a = (cs.red[e] + cs.red[64 + e]) + (cs.red[128 + e] + cs.red[192 + e]);
     }
     double vv = (i == j) ? 1.0 : 0.0;
     for (int sweep = 0; sweep < 12; ++sweep) {
-      const double off = wave_sum_f64(i != j ? a * a : 0.0);
-      const double dia = wave_sum_f64(i == j ? a * a : 0.0);
-      if (!(off > 1e-28 * dia)) break;  // uniform across the wave
+      if (sweep > 0) {   // (a first sweep over a diagonal W rotates by identities, to rounding)
+        const double off = wave_sum_f64(i != j ? a * a : 0.0);
+        const double dia = wave_sum_f64(i == j ? a * a : 0.0);
+        if (!(off > 1e-28 * dia)) break;  // uniform across the wave
+      }
 #pragma unroll
       for (int st = 0; st < 7; ++st) {
         const int pi = rr_partner(i, st), pj = rr_partner(j, st);
         const int i0 = min(i, pi), i1 = max(i, pi), j0 = min(j, pj), j1 = max(j, pj);
         xa[lane] = a;
         xv[lane] = vv;
+        wave_lds_sync();
         const double ai0 = xa[9 * i0], ai1 = xa[9 * i1], aio = xa[8 * i0 + i1];
         const double aj0 = xa[9 * j0], aj1 = xa[9 * j1], ajo = xa[8 * j0 + j1];
         const double a_ipj = xa[8 * i + pj], a_pij = xa[8 * pi + j];
@@ -526,23 +540,20 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
         vv = vv * cj + v_ipj * xj;
       }
     }
-    cs.ev[lane] = vv;  // ev[i][j]: component i of eigenvector j
+    // (still wave 0 alone, ordered by wave_lds_sync) the rank of eigenvalue j,
+    // descending, ties by index; the eigenvectors in rank order,
+    // ev[r][i] = component i of the r-th; the kept singular values
     if (i == j) cs.lam[i] = a;
-    // (still wave 0 alone, in LDS issue order) rank of eigenvalue `lane`,
-    // descending, ties by index; then the kept singular values
-    if (lane < kQ) {
-      const double li = cs.lam[lane];
-      int rk = 0;
-      for (int k = 0; k < kQ; ++k) rk += (cs.lam[k] > li || (cs.lam[k] == li && k < lane)) ? 1 : 0;
-      cs.order[rk] = lane;
-    }
-    if (lane < R) {   // sigma = l / sqrt(l) and 1 / sigma from one refined reciprocal square root
-      const double l = cs.lam[cs.order[lane]];
-      const double r0 = __builtin_amdgcn_rsq(fmax(l, 2.2250738585072014e-308));
-      const double t = fma(-l * r0, r0, 1.0);
-      const double rs = fma(r0 * t, fma(t, 0.375, 0.5), r0);
-      cs.sig[lane] = l > 0.0 ? l * rs : 0.0;
-      cs.isig[lane] = l > 0.0 ? rs : 0.0;
+    wave_lds_sync();
+    const double lj = cs.lam[j];
+    int rk = 0;
+#pragma unroll
+    for (int k = 0; k < kQ; ++k) rk += (cs.lam[k] > lj || (cs.lam[k] == lj && k < j)) ? 1 : 0;
+    cs.ev[rk * kQ + i] = vv;
+    if (i == 0 && rk < R) {   // sigma = l / sqrt(l) and 1 / sigma from one refined reciprocal square root
+      const double rs = rsqrt_f64(fmax(lj, 2.2250738585072014e-308));
+      cs.sig[rk] = lj > 0.0 ? lj * rs : 0.0;
+      cs.isig[rk] = lj > 0.0 ? rs : 0.0;
     }
   }
   __syncthreads();
@@ -551,9 +562,6 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   static_assert(m <= kNT && n <= 64, "left vectors: a row per thread; right vectors: a column per lane of a wave");
   const float dk = expf(gacc);
   const float s1 = sdec, s2 = 1.f - sdec;
-  int ord[kRMax];
-#pragma unroll
-  for (int r = 0; r < kRMax; ++r) ord[r] = r < R ? cs.order[r] : 0;
   double ur[kRMax];
   if (tid < m) {
     double yv[kQ];
@@ -563,7 +571,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     for (int r = 0; r < kRMax; ++r) {
       double s = 0.0;
 #pragma unroll
-      for (int j = 0; j < kQ; ++j) s += yv[j] * cs.ev[j * kQ + ord[r]];
+      for (int j = 0; j < kQ; ++j) s += yv[j] * cs.ev[r * kQ + j];
       ur[r] = s;
     }
   }
@@ -582,7 +590,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
       if (r < R && on) {
         double sv = 0.0;
 #pragma unroll
-        for (int j = 0; j < kQ; ++j) sv += cs.z[c * kQ + j] * cs.ev[j * kQ + ord[r]];
+        for (int j = 0; j < kQ; ++j) sv += cs.z[c * kQ + j] * cs.ev[r * kQ + j];
         vr[r] = cs.sig[r] > 0.0 ? sv * cs.isig[r] : (c == r ? 1.0 : 0.0);
       }
       bv_[r] = on ? fabs(vr[r]) : -1.0;

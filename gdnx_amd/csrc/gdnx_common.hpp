@@ -93,6 +93,18 @@ __device__ __forceinline__ int opaque(int x) {
   return x;
 }
 
+// Orders one wave's LDS accesses across its lanes: what a lane wrote before
+// this point is what the wave's other lanes read after it.  The hardware
+// completes a wave's LDS accesses in issue order; the wavefront-scope fences
+// keep the compiler from moving a lane's accesses across this point (to the
+// compiler, another lane's write is another thread's, so without them a
+// lane's read may be hoisted above a write it does not itself depend on).
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+
 // 4 consecutive CT values from floats (for 8/16-byte LDS stores).
 __device__ __forceinline__ void st4(bf16* p, float a, float b, float c, float d) {
   *(bf16x4*)p = (bf16x4){(bf16)a, (bf16)b, (bf16)c, (bf16)d};

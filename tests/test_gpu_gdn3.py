@@ -145,6 +145,35 @@ def test_gdn3_forward_matches_oracle(gpu_lib, case):
     assert abs(err.item() - err_r.item()) <= tol * max(1.0, abs(err_r.item()))
 
 
+@pytest.mark.parametrize("D,factors", [(128, (16, 16, 8, 8)), (64, (8, 8, 8, 8))])
+def test_gdn3_window_then_compaction_state(gpu_lib, D, factors):
+    """One window and the compaction that closes it in the layer-default
+    regime (K_c = P = 16, one workgroup per chain running both): the
+    compacted factors themselves, not only the outputs, at fp32 accuracy."""
+    from gdnx_amd import gdn3
+    B, T, H, M = 1, 16, 2, 2
+    print(f"case: gdn3 window + compaction state D={D}", flush=True)
+    q, k, v, bg, wg, dec = _g3_inputs(B, T, H, M, D, seed=3, io=torch.float32, gate="channel", per_lane=False)
+    N = B * H * M
+    a_v, a_k, b_v, b_k = factors
+    G = og.reference_sketch(N, b_v * b_k, min(8, a_v * a_k, b_v * b_k))
+    y, (A, Bk, U, Vb), err = gdn3.gdn3_recurrent_state(
+        *(t.to(DEV) for t in (q, k, v, bg, wg, dec)), R=4, P=16, factors=factors, compact_every=16,
+        sketch=G.to(DEV), return_state=True)
+    torch.cuda.synchronize()
+    oq, ok, ov, ob, ow = _oracle_args(q, k, v, bg, wg, M)
+    yr, (Ar, Br, _, _), err_r = og.gdn3_recurrence(oq, ok, ov, ob, ow, dec.double(), R=4, P=16, factors=factors,
+                                                   compact_every=16, sketch=G, sign_mode="canonical",
+                                                   return_state=True)
+    assert rel_l2(y, yr) <= 1e-4
+    # the singular vectors move by (the window's fp32 rounding of R_mat) /
+    # (singular-value gap): about 3e-4 at D = 64 on these inputs, while a
+    # wrong rotation, rank or sign moves them by O(1)
+    assert rel_l2(A, Ar) <= 1e-3
+    assert rel_l2(Bk, Br) <= 1e-3
+    assert abs(err.item() - err_r.item()) <= 1e-4 * abs(err_r.item())
+
+
 def test_gdn3_forward_ragged_tail(gpu_lib):
     """T not a multiple of P: the last partial window writes y only."""
     from gdnx_amd import gdn3
