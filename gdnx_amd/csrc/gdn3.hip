@@ -1633,37 +1633,28 @@ struct G3CompactSmem {
 };
 
 // sum_r A_r (x) B_r as a [D][D] (v, k) matrix for the window kernel's reads,
-// from the factors Af [R][m], Bf [R][n] (LDS), in blocks: a thread takes one
-// factor entry (iv, ik) (TPP threads share one, splitting its b_v rows) and
-// writes the entries (iv b_v + jv, ik b_k + jk) it scales, 8 contiguous k
-// per store (ld: the row stride of sk)
+// from the factors Af [R][m], Bf [R][n] (LDS), ld the row stride of sk.  With
+// p = iv a_k + ik running over A_r's entries and q = jv b_k + jk over B_r's,
+// S'^T[q][p] = sum_r B_r[q] A_r[p] is a product with K = R = 4: one fp32 MFMA
+// (16x16x4) per 16 x 16 tile.  Lane (g, l) supplies B_g[q0 + l] and A_g[p0 + l]
+// and holds q = q0 + 4 g + e (e < 4), p = p0 + l: the entries
+// (iv b_v + jv, ik b_k + jk .. jk + 3) of S_kron, one 4-element store.  The
+// tiles go round the 4 waves.
 template <int D, typename CT>
 __device__ __forceinline__ void write_skron(CT* sk, const float* Af, const float* Bf, int tid, int ld = D) {
   typedef G3D<D> Ge;
-  constexpr int TPP = kNT / Ge::m, RPT = Ge::bv / TPP;
-  static_assert(kNT % Ge::m == 0 && Ge::bv % TPP == 0 && Ge::bk == 8, "skron blocking");
-  const int pr = tid / TPP, part = tid % TPP;
-  const int iv = pr / Ge::ak, ik = pr % Ge::ak;
-  float a[Ge::R];
+  constexpr int QT = Ge::n / 16, NT = QT * (Ge::m / 16);
+  static_assert(Ge::R == 4 && Ge::bk % 4 == 0 && Ge::m % 16 == 0 && Ge::n % 16 == 0 && NT % 4 == 0,
+                "K = R = 4 MFMA tiles, runs of 4 jk");
+  const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
 #pragma unroll
-  for (int r = 0; r < Ge::R; ++r) a[r] = Af[r * Ge::m + pr];
-#pragma unroll
-  for (int jj = 0; jj < RPT; ++jj) {
-    const int jv = part * RPT + jj;
-    float sv[8];
-#pragma unroll
-    for (int jk = 0; jk < 8; ++jk) sv[jk] = 0.f;
-#pragma unroll
-    for (int r = 0; r < Ge::R; ++r) {
-      const f32x4 b0 = *(const f32x4*)&Bf[r * Ge::n + jv * Ge::bk];
-      const f32x4 b1 = *(const f32x4*)&Bf[r * Ge::n + jv * Ge::bk + 4];
-#pragma unroll
-      for (int jk = 0; jk < 4; ++jk) {
-        sv[jk] += a[r] * b0[jk];
-        sv[4 + jk] += a[r] * b1[jk];
-      }
-    }
-    store8(sk + (size_t)(iv * Ge::bv + jv) * ld + ik * Ge::bk, sv);
+  for (int u = 0; u < NT / 4; ++u) {
+    const int t = wave + 4 * u, q0 = (t % QT) * 16, p0 = (t / QT) * 16;
+    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Bf[g * Ge::n + q0 + l16], Af[g * Ge::m + p0 + l16], acc, 0, 0, 0);
+    const int p = p0 + l16, q = q0 + 4 * g;
+    const int iv = p / Ge::ak, ik = p % Ge::ak, jv = q / Ge::bk, jk = q % Ge::bk;
+    st4(sk + (size_t)(iv * Ge::bv + jv) * ld + ik * Ge::bk + jk, acc[0], acc[1], acc[2], acc[3]);
   }
 }
 
