@@ -345,36 +345,27 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
       __syncthreads();
       const float* Bf = st + Ge::R * Ge::m;
       if constexpr (SKL) {
-        // skt[k][v], k = ik b_k + jk, v = iv' b_v + jv.  A thread takes one row
-        // k and a group of 8 values of iv': the 8 x 8 products of A_r[iv'][ik]
-        // and B_r[jv][jk] are 64 consecutive v of that row (eight 16-byte
-        // stores); consecutive lanes take consecutive rows, so the stores
-        // spread over the banks
-        static_assert(Ge::bv == 8 && Ge::av % 8 == 0, "blocks of 8 x 8 factor entries");
-        constexpr int NGA = Ge::av / 8;                 // groups of iv' per row
-        if (tid < D * NGA) {
-          const int kr = tid % D, grp = tid / D, ik = kr / Ge::bk, jk = kr % Ge::bk;
-          float bb[Ge::R][8];
+        // skt[k][v] (k = ik b_k + jk, v = iv b_v + jv) = sum_r B_r[jv][jk] A_r[iv][ik]:
+        // for a tile of 16 (jk, jv) rows (16 / b_v values of jk) and 16
+        // (ik, iv) columns (16 / a_v values of ik) a product with K = R = 4,
+        // one fp32 MFMA.  Lane (g, l) holds rows 4 g .. 4 g + 3, i.e. 4
+        // consecutive jv of one jk, and column l: 4 consecutive v of row k, one
+        // 4-element store.  The tiles go round the 4 waves.
+        static_assert(Ge::R == 4 && 16 % Ge::bv == 0 && 16 % Ge::av == 0 && Ge::bv % 4 == 0, "K = R = 4 MFMA tiles");
+        constexpr int JKT = 16 / Ge::bv, IKT = 16 / Ge::av;   // jk and ik per tile
+        constexpr int NJ = Ge::bk / JKT, NT = NJ * (Ge::ak / IKT);
+        static_assert(NT % 4 == 0, "whole tiles per wave");
+        const int g = lane >> 4, l16 = lane & 15;
 #pragma unroll
-          for (int r = 0; r < Ge::R; ++r)
-#pragma unroll
-            for (int jv = 0; jv < 8; ++jv) bb[r][jv] = Bf[r * Ge::n + jv * Ge::bk + jk];
-#pragma unroll 2
-          for (int i8 = 0; i8 < 8; ++i8) {
-            const int ivv = grp * 8 + i8;
-            float a[Ge::R];
-#pragma unroll
-            for (int r = 0; r < Ge::R; ++r) a[r] = st[r * Ge::m + ivv * Ge::ak + ik];
-            float sv[8];
-#pragma unroll
-            for (int jv = 0; jv < 8; ++jv) {
-              float x = 0.f;
-#pragma unroll
-              for (int r = 0; r < Ge::R; ++r) x += a[r] * bb[r][jv];
-              sv[jv] = x;
-            }
-            store8c(&sm.skt[kr][ivv * Ge::bv], sv);
-          }
+        for (int u = 0; u < NT / 4; ++u) {
+          const int t = wave + 4 * u, jk0 = (t % NJ) * JKT, ik0 = (t / NJ) * IKT;
+          const float av = Bf[g * Ge::n + (l16 % Ge::bv) * Ge::bk + jk0 + l16 / Ge::bv];
+          const float bv = st[g * Ge::m + (l16 % Ge::av) * Ge::ak + ik0 + l16 / Ge::av];
+          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+          const int i0 = 4 * g, jk = jk0 + i0 / Ge::bv, jv = i0 % Ge::bv;
+          const int ik = ik0 + l16 / Ge::av, iv = l16 % Ge::av;
+          st4(&sm.skt[ik * Ge::bk + jk][iv * Ge::bv + jv], acc[0], acc[1], acc[2], acc[3]);
         }
       } else {
         // the fragments this lane feeds the Kronecker products: row k = d of
