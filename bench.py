@@ -337,7 +337,10 @@ def bench_gdn3(args, layer_default, train=False):
     if train:
         nbytes *= 3
     achieved = nbytes / sec / 1e9
-    name = "gdn3_window_kernel+gdn3_compact_kernel" + ("+gdn3_bwd_kernel" if train else "")
+    # the layer default runs one persistent workgroup per chain for the window steps and
+    # their compactions; config 3 a pipelined window launch and a compaction launch per interval
+    name = ("gdn3_fused_kernel" if layer_default else "gdn3_window_pipe_kernel+gdn3_compact_kernel") + \
+        ("+gdn3_bwd_kernel" if train else "")
     if train:
         metric = "GDN3 Kronecker-residual layer tokens/s fwd+bwd @B=4,T=4096, compaction every 16"
     elif layer_default:
