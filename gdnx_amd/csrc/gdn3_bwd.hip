@@ -291,7 +291,21 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
           dUc[a] = dUa[bl][a];
           dVc[a] = dVa[bl][a];
         }
-    __syncthreads();  // the previous sub-chunk is done with LDS
+    // the previous sub-chunk is done with LDS (an LDS-only barrier: its gradient
+    // stores to global memory stay in flight, nothing reads them back)
+    lds_barrier();
+    // the factors S_kron^T is rebuilt from (fetched a sub-chunk ahead) go to
+    // LDS before this sub-chunk's input loads are issued, so that waiting for
+    // them does not wait for those
+    const bool rebuild = live && rebuilds(c);
+    float* st = &sm.dr[0][0];
+    if (rebuild) {
+#pragma unroll
+      for (int u = 0; u < NAB; ++u) {
+        const int e = tid + u * kNT;
+        if (e < Ge::RMN) st[e] = abr[u];
+      }
+    }
 
     // the sub-chunk's inputs, the block entering the window (sub-chunk c -
     // NB) and the decays of the P tokens before the sub-chunk, loaded raw
@@ -300,7 +314,7 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     const bool tv = has_unit && t < T;
     Row8<CT> rk, rq, rv, rdy, rkp;
     Row8<float> rb, rw, ru, ruo;
-    float bs = 0.f, ws = 0.f, dv = 1.f, dvp = 1.f;
+    float bs = 0.f, ws = 0.f, dv = 1.f;
     zero8(rk), zero8(rq), zero8(rv), zero8(rdy), zero8(rb), zero8(rw), zero8(ru);
     if (tv) {
       raw8<CT>((const CT*)p.k + qkv_base + (size_t)t * qkv_tok + ud, rk);
@@ -329,20 +343,15 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
                                        : p.bg[gate_base + (size_t)tt_ * gate_tok]) : 0.f;
       }
     load_block(c - NB, rkp, ruo);
-    if (tid < P) {
-      const int tp = c * BP - P + tid;
-      if (tp >= 0) dvp = p.dec[dec_base + (size_t)tp * dec_tok];
-    }
+    // the decay of token c BP - P + tid (tid < P), loaded unconditionally at an
+    // in-bounds token and used raw in A: a load in a branch drew its clamp in
+    // after it, whose wait then held every input load issued above
+    const int tpv = c * BP - P + (tid < P ? tid : 0);
+    const float dvp = p.dec[dec_base + (size_t)(tpv > 0 ? tpv : 0) * dec_tok];
 
     // ---- S_kron^T of this interval (the factors of compaction iv - 1), rebuilt on entry ----
-    if (live && rebuilds(c)) {
-      float* st = &sm.dr[0][0];
-#pragma unroll
-      for (int u = 0; u < NAB; ++u) {
-        const int e = tid + u * kNT;
-        if (e < Ge::RMN) st[e] = abr[u];
-      }
-      __syncthreads();
+    if (rebuild) {
+      lds_barrier();   // the inputs loaded above stay in flight across it
       const float* Bf = st + Ge::R * Ge::m;
       if constexpr (SKL) {
         // skt[k][v] (k = ik b_k + jk, v = iv b_v + jv) = sum_r B_r[jv][jk] A_r[iv][ik]:
