@@ -1647,11 +1647,19 @@ __device__ __forceinline__ void write_skron(CT* sk, const float* Af, const float
   static_assert(Ge::R == 4 && Ge::bk % 4 == 0 && Ge::m % 16 == 0 && Ge::n % 16 == 0 && NT % 4 == 0,
                 "K = R = 4 MFMA tiles, runs of 4 jk");
   const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
+  // every tile's operands are loaded before the first MFMA
+  float ao[NT / 4], bo[NT / 4];
+#pragma unroll
+  for (int u = 0; u < NT / 4; ++u) {
+    const int t = wave + 4 * u, q0 = (t % QT) * 16, p0 = (t / QT) * 16;
+    ao[u] = Bf[g * Ge::n + q0 + l16];
+    bo[u] = Af[g * Ge::m + p0 + l16];
+  }
 #pragma unroll
   for (int u = 0; u < NT / 4; ++u) {
     const int t = wave + 4 * u, q0 = (t % QT) * 16, p0 = (t / QT) * 16;
     f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Bf[g * Ge::n + q0 + l16], Af[g * Ge::m + p0 + l16], acc, 0, 0, 0);
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ao[u], bo[u], acc, 0, 0, 0);
     const int p = p0 + l16, q = q0 + 4 * g;
     const int iv = p / Ge::ak, ik = p % Ge::ak, jv = q / Ge::bk, jk = q % Ge::bk;
     st4(sk + (size_t)(iv * Ge::bv + jv) * ld + ik * Ge::bk + jk, acc[0], acc[1], acc[2], acc[3]);
