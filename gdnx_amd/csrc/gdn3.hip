@@ -174,25 +174,26 @@ __device__ __forceinline__ double rsqrt_f64(double x) {
 // t = sgn(th) / (|th| + sqrt(th^2 + 1)), th = (a_qq - a_pp) / (2 a_pq).
 // Multiplying through by |2 a_pq| gives it without divisions: with
 // d = a_qq - a_pp, e = 2 a_pq, h = sqrt(d^2 + e^2) and w = |d| + h,
-// t = sgn(th) |e| / w, so c = w / sqrt(w^2 + e^2), s = sgn(th) |e| / sqrt(w^2 + e^2)
-// (c^2 + s^2 = 1 by construction).
+// t = sgn(d) e / w, so c = w / sqrt(w^2 + e^2), s = sgn(d) e / sqrt(w^2 + e^2)
+// (c^2 + s^2 = 1 by construction; d = +0 counts as positive, and at d = 0
+// either sign of the 45-degree rotation zeroes a_pq).
 __device__ __forceinline__ void jacobi_rot(double app, double aqq, double apq, double& c, double& s) {
-  // selects only (no branches), so the two rotations a lane forms per round
-  // interleave.  h only sets the angle: it is x times the hardware reciprocal
-  // square root (about 2^-23 relative, 0 at x = 0), and a rotation that
-  // leaves 1e-7 of a_pq behind still converges within the same sweeps; c and
-  // s are normalised by the refined one, so c^2 + s^2 = 1 to rounding.
+  // the round is bound by its instruction count (one wave issues it), so no
+  // selects: h only sets the angle (x times the hardware reciprocal square
+  // root, about 2^-23 relative, 0 at x = 0; a rotation that leaves 1e-7 of
+  // a_pq behind still converges within the same sweeps), w carries 2^-500,
+  // which vanishes against any |d| or h above 2^-447 and makes d = e = 0 give
+  // c = 1, s = 0, and sgn(d) e is a sign-bit copy.  c and s are normalised by
+  // the refined reciprocal square root, so c^2 + s^2 = 1 to rounding.
   const double d = aqq - app, e = 2.0 * apq;
-  const double x = fma(d, d, e * e);
+  const double e2 = e * e;
+  const double x = fma(d, d, e2);
   const double h = x * __builtin_amdgcn_rsq(fmax(x, 2.2250738585072014e-308));
-  const double w = fabs(d) + h;
-  const double q = fma(w, w, e * e);
-  const double r = rsqrt_f64(q);   // q = 0: NaN, discarded by the selects below
-  // sgn(th) |e| = sgn(d) e for d != 0, and |e| for d == 0 (th = +-0 counts as >= 0)
-  const double num = d == 0.0 ? fabs(e) : (d > 0.0 ? e : -e);
-  const bool ok = q > 0.0;  // false only when a_pq = 0 and a_pp = a_qq (or both underflow)
-  c = ok ? w * r : 1.0;
-  s = ok ? num * r : 0.0;
+  const double w = (fabs(d) + 3.0549363634996047e-151) + h;
+  const double r = rsqrt_f64(fma(w, w, e2));
+  const long long sb = __double_as_longlong(d) & (long long)0x8000000000000000ull;
+  c = w * r;
+  s = __longlong_as_double(__double_as_longlong(e) ^ sb) * r;
 }
 
 // Round-robin (circle method) partner of index x in round st of 7 for 8 indices.
@@ -536,7 +537,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
         jacobi_rot(aj0, aj1, ajo, cj, sj);
         // J[x][x] = c; J[partner][x] = -s if x < partner else +s
         const double xi = (i < pi) ? -si : si, xj = (j < pj) ? -sj : sj;
-        a = ci * cj * a + ci * xj * a_ipj + xi * cj * a_pij + xi * xj * a_pipj;
+        a = cj * fma(ci, a, xi * a_pij) + xj * fma(ci, a_ipj, xi * a_pipj);
         vv = vv * cj + v_ipj * xj;
       }
     }
