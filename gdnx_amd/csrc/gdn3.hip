@@ -309,6 +309,10 @@ __device__ __forceinline__ void col_sumsq(const double* y, double* red, double* 
   __syncthreads();
 }
 
+struct G3NoOp {
+  __device__ void operator()() const {}
+};
+
 // Compaction of one chain (gdn3/gdn3_upgrade.py:650-719): ab = [A (R x m) |
 // B (R x n)] in LDS as stored (the Kronecker part is decayed by e^{gacc} per
 // factor); the window's P net writes U and keys Vb (decayed to now) are read
@@ -321,11 +325,14 @@ __device__ __forceinline__ void col_sumsq(const double* y, double* red, double* 
 // sketch of qs = R columns, Q = the column-normalised R_mat G,
 // Bm = Q^T R_mat, A_svd_r = |Bm_r| Q_r, B_svd_r = Bm_r / |Bm_r| (norms
 // clamped at 1e-12); it reports no error (stats = (|R_mat|^2, |R_mat|^2)).
-template <int D, int P, bool STG>
+// issue / commit: work of the caller's that uses no compaction state and
+// runs in the eigen-solve's shadow (every thread calls issue before it; waves
+// 1-3 call commit while wave 0 solves, wave 0 after); 'svd' mode only.
+template <int D, int P, bool STG, typename Issue = G3NoOp, typename Commit = G3NoOp>
 __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, const float* __restrict__ U,
                                            const float* __restrict__ Vb, size_t u_sp, size_t u_sd, float gacc,
                                            float sdec, const float* __restrict__ sketch, double* stats, int tid,
-                                           int mode = 0) {
+                                           int mode = 0, Issue issue = Issue(), Commit commit = Commit()) {
   typedef G3D<D> Ge;
   constexpr int R = Ge::R, m = Ge::m, n = Ge::n, q = Ge::q, ak = Ge::ak, bk = Ge::bk;
   constexpr int lbv = Ge::lbv, lbk = Ge::lbk, ln = Ge::ln;
@@ -498,6 +505,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     }
   }
   __syncthreads();
+  issue();
   // eigen-decomposition of W = Bm Bm^T by cyclic Jacobi in wave 0: lane
   // (i, j) holds W[i][j] and V[i][j].  Each round rotates 4 disjoint pairs;
   // a lane gathers every operand of its round in one exchange and forms the
@@ -556,6 +564,9 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
       cs.sig[rk] = lj > 0.0 ? lj * rs : 0.0;
       cs.isig[rk] = lj > 0.0 ? rs : 0.0;
     }
+    commit();
+  } else {
+    commit();
   }
   __syncthreads();
   // leading singular vectors: u_r = Q ev_r (a row per thread, kept in
@@ -832,16 +843,41 @@ struct G3WinView {
   float* boff;                  // log decay of block b's keys since they were rebased
 };
 
+// The commit of a sub-chunk's prefetched token rows into the window LDS: H =
+// b (.) k, the Q and K rows, u = w (.) v, and per token alpha and the log
+// decay (thread tid holds load unit (tid / (D / 8), 8 (tid mod (D / 8)))).
+template <typename CT, int D, int P>
+__device__ __forceinline__ void g3_commit(const G3WinView<CT, D, P>& w, const G3Tok& tk, const G3Raw<CT>& r, int tid) {
+  constexpr int DG = D / 8, W16 = W16Of<CT>::value;
+  if (tid >= kSC * DG) return;
+  const int ui = tid / DG, ud = 8 * (tid % DG);
+  float hf[8], uu[8];
+  const float part = g3_unpack<CT, DG>(r, tk.gc, hf, uu);
+  store8(&w.x[ui][ud], hf);
+#pragma unroll
+  for (int q16 = 0; q16 < W16; ++q16) {
+    *(uint4*)&w.x[kSC + ui][ud + q16 * (16 / sizeof(CT))] = g3_raw(r, r.q[q16]);
+    *(uint4*)&w.x[2 * kSC + ui][ud + q16 * (16 / sizeof(CT))] = g3_raw(r, r.k[q16]);
+  }
+  *(f32x4*)&w.u[ui][ud] = (f32x4){uu[0], uu[1], uu[2], uu[3]};
+  *(f32x4*)&w.u[ui][ud + 4] = (f32x4){uu[4], uu[5], uu[6], uu[7]};
+  if (tid % DG == 0) {
+    w.alpha[ui] = stable_alpha_f(part);
+    w.lg[ui] = log_decay(r.ok ? r.dec : 1.f);
+  }
+}
+
 // One sub-chunk c of the single-stage window recurrence for one workgroup
 // (value tiles vb NVTW .. of chain): commit of its prefetched token rows (and
 // the loads of sub-chunk next, if >= 0), the grams, the inverse, the
 // Kronecker reads, the window algebra on the U tiles uo, y and the training
-// stash, then the window keys.  first: no sub-chunk before it in this launch.
+// stash, then the window keys.  first: no sub-chunk before it in this launch;
+// committed: its token rows are in LDS already (g3_commit ran earlier).
 template <typename CT, int D, int P, int NVB>
 __device__ __forceinline__ void g3_window_step(const G3WinView<CT, D, P>& w, const G3FwdArgs& p, const G3Tok& tk,
                                                int chain, int vb, int c, bool first, int next, bool live,
                                                float& gacc, f32x4 (&uo)[P / kSC][(D / 16 / NVB + 3) / 4],
-                                               G3Raw<CT>& raw) {
+                                               G3Raw<CT>& raw, bool committed = false) {
   constexpr int NB = P / kSC;
   constexpr bool KF = sizeof(CT) == 4;
   constexpr int DG = D / 8;  // 8-element load units per token row
@@ -857,23 +893,7 @@ __device__ __forceinline__ void g3_window_step(const G3WinView<CT, D, P>& w, con
   const bool has_unit = tid < UNITS;
   const int ui = tid / DG, ud = 8 * (tid % DG);
   auto fetch = [&](G3Raw<CT>& r, int cc) { g3_fetch<CT>(p, tk, r, cc * kSC + ui - p.t0, has_unit, ud); };
-  auto commit = [&](const G3Raw<CT>& r) {
-    if (!has_unit) return;
-    float hf[8], uu[8];
-    const float part = g3_unpack<CT, DG>(r, tk.gc, hf, uu);
-    store8(&w.x[ui][ud], hf);
-#pragma unroll
-    for (int q16 = 0; q16 < W16; ++q16) {
-      *(uint4*)&w.x[kSC + ui][ud + q16 * (16 / sizeof(CT))] = g3_raw(r, r.q[q16]);
-      *(uint4*)&w.x[2 * kSC + ui][ud + q16 * (16 / sizeof(CT))] = g3_raw(r, r.k[q16]);
-    }
-    *(f32x4*)&w.u[ui][ud] = (f32x4){uu[0], uu[1], uu[2], uu[3]};
-    *(f32x4*)&w.u[ui][ud + 4] = (f32x4){uu[4], uu[5], uu[6], uu[7]};
-    if (tid % DG == 0) {
-      w.alpha[ui] = stable_alpha_f(part);
-      w.lg[ui] = log_decay(r.ok ? r.dec : 1.f);
-    }
-  };
+  auto commit = [&](const G3Raw<CT>& r) { g3_commit<CT, D, P>(w, tk, r, tid); };
   // after sub-chunk cc: its block is rebased (boff 0), the others decayed by its G_last
   auto advance_boff = [&](int cc, float glast) {
     if (tid < NB) w.boff[tid] = (tid == cc % NB) ? 0.f : w.boff[tid] + glast;
@@ -888,7 +908,7 @@ __device__ __forceinline__ void g3_window_step(const G3WinView<CT, D, P>& w, con
     const int beta = c % NB;
     __syncthreads();
     if (!first) advance_boff(c - 1, w.G[kSC - 1]);
-    commit(raw);
+    if (!committed) commit(raw);
     if (next >= 0) fetch(raw, next);
     __syncthreads();
     // per-token scalars | grams and Kronecker reads (MFMA).  Every wave forms
@@ -1680,13 +1700,13 @@ struct G3FusedSmem {
   union alignas(16) Phase {
     G3Compact<D, P, false> cs;          // the compaction's scratch
     struct alignas(16) Win {            // the window step's
-      CT x[3 * kSC][D + 8];
-      float u[kSC][D + 4];
-      float kr[2 * kSC][D + 4];
+      CT x[3 * kSC][D + 8];             // x, u and the scalars first: the next window's commit
+      float u[kSC][D + 4];              // writes them while the compaction still uses all of
+      float G[kSC], alpha[kSC], lg[kSC], kco[kSC], qco[kSC], gam[kSC], vsc[kSC];   // its LDS but R_mat
+      alignas(16) float kr[2 * kSC][D + 4];
       float pp[4][kSC][kSC + 4];
       float po[2][kSC][P + 4];
       CT skron[D][D + 8];               // rebuilt from the factors after every compaction
-      float G[kSC], alpha[kSC], lg[kSC], kco[kSC], qco[kSC], gam[kSC], vsc[kSC];
     } w;
   } ph;
   alignas(16) float ab[kAB];            // A | B of this chain
@@ -1735,6 +1755,9 @@ __global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
   __syncthreads();
   if (carried) write_skron<D, CT>(&sm.ph.w.skron[0][0], sm.ab, sm.ab + Rm, tid, D + 8);
   bool live = carried;
+  bool committed = false;   // the window's token rows were committed during the last compaction
+  typedef typename Sm::Phase::Win WinT;
+  constexpr bool kEarly = offsetof(WinT, kr) <= sizeof(sm.ph.cs.rm);
   float gacc = 0.f;
   int event = 0;
   const G3WinView<CT, D, P> w{sm.ph.w.x, sm.ph.w.u, sm.ph.w.kr, sm.ph.w.pp, sm.ph.w.po, sm.ph.w.skron, sm.vbd,
@@ -1750,7 +1773,7 @@ __global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
         const int vt = wave + 4 * a;
         uo[0][a][s] = vt < D / 16 ? sm.uwin[4 * g4 + s][vt * 16 + n16] : 0.f;
       }
-    g3_window_step<CT, D, P, 1>(w, p, tk, chain, 0, c, true, -1, live, gacc, uo, raw);
+    g3_window_step<CT, D, P, 1>(w, p, tk, chain, 0, c, true, -1, live, gacc, uo, raw, committed);
 #pragma unroll
     for (int a = 0; a < VPW; ++a)
 #pragma unroll
@@ -1763,9 +1786,26 @@ __global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
     if (!complete) break;   // the tail: no compaction follows
     // its compaction (gdn3/gdn3_upgrade.py:650-719), the factors decayed by e^{gacc}
     const int qs = p.cmode ? Ge::R : Ge::q;
+    // the next window's token loads and their commit run in the eigen-solve's
+    // shadow when that window's commit targets lie in R_mat's LDS (dead by then)
+    const bool pre = kEarly && p.cmode == 0 && c + 1 < cg1;
+    // (waves 1-3 only: wave 0's units are loaded and committed by wave 1 after
+    // its own, so nothing is added to the eigen-solve's wave)
+    auto issue = [&]() {
+      if (pre && wave > 0) g3_fetch<CT>(p, tk, raw, (c + 1) * kSC + ui - p.t0, has_unit, ud);
+    };
+    auto commit = [&]() {
+      if (!pre || wave == 0) return;
+      g3_commit<CT, D, P>(w, tk, raw, tid);
+      if (wave == 1) {
+        const int t0 = tid - 64;
+        g3_fetch<CT>(p, tk, raw, (c + 1) * kSC + t0 / DG - p.t0, t0 < kSC * DG, 8 * (t0 % DG));
+        g3_commit<CT, D, P>(w, tk, raw, t0);
+      }
+    };
     g3_compact<D, P>(sm.ph.cs, sm.ab, &sm.uwin[0][0], &sm.vbd[0][0], (size_t)(D + 4), (size_t)1, gacc, p.sdec,
                      p.sketch + (size_t)chain * Ge::n * qs,
-                     p.stats ? p.stats + ((size_t)event * N + chain) * 2 : nullptr, tid, p.cmode);
+                     p.stats ? p.stats + ((size_t)event * N + chain) * 2 : nullptr, tid, p.cmode, issue, commit);
     __syncthreads();
     if (p.train_states) {   // the factors after every compaction, for the backward
       const G3Stash ts = g3_stash(p.train_states, N, p.nch, p.T / p.Kc, D, kSC, Ge::RMN);
@@ -1774,10 +1814,11 @@ __global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
     ++event;
     gacc = 0.f;
     live = true;
-    if (c + 1 < cg1) {   // the next window's loads (under the Kronecker matrix's rebuild)
-      g3_fetch<CT>(p, tk, raw, (c + 1) * kSC + ui - p.t0, has_unit, ud);
+    if (c + 1 < cg1) {   // the next window's loads (under the Kronecker matrix's rebuild), unless committed
+      if (!pre) g3_fetch<CT>(p, tk, raw, (c + 1) * kSC + ui - p.t0, has_unit, ud);
       write_skron<D, CT>(&sm.ph.w.skron[0][0], sm.ab, sm.ab + Rm, tid, D + 8);
     }
+    committed = pre;
   }
   __syncthreads();
   // the final state: U, Vb [N][D][P]; A, B (decayed since the last compaction)
