@@ -843,6 +843,112 @@ struct G3WinView {
   float* boff;                  // log decay of block b's keys since they were rebased
 };
 
+// The log-decay prefix sums of a sub-chunk (lane i < 16 holds G_i).
+template <typename CT, int D, int P>
+__device__ __forceinline__ float g3_scan_g(const G3WinView<CT, D, P>& w, int lane) {
+  float gl = lane < kSC ? w.lg[lane] : 0.f;
+#pragma unroll
+  for (int off = 1; off < kSC; off <<= 1) {
+    const float o = __shfl_up(gl, off, 64);
+    if (lane >= off) gl += o;
+  }
+  return gl;
+}
+
+// The per-token coefficients of a sub-chunk (one wave): G, e^G, kco = alpha
+// e^{2 (gacc + G)}, qco = e^{2 (gacc + G)} and the key scale e^{G_last - G}.
+template <typename CT, int D, int P>
+__device__ __forceinline__ void g3_scalars(const G3WinView<CT, D, P>& w, float gl, float gacc, int lane) {
+  const float gl_last = __shfl(gl, kSC - 1, 64);
+  if (lane < kSC) {
+    const float e2 = expf(2.f * (gacc + gl));
+    w.G[lane] = gl;
+    w.gam[lane] = expf(gl);
+    w.kco[lane] = w.alpha[lane] * e2;
+    w.qco[lane] = e2;
+    w.vsc[lane] = expf(gl_last - gl);
+  }
+}
+
+// Gram tile ti of a sub-chunk (one wave; 2 + 2 NB tiles):
+//   0: H K^T (raw; the inverse turns it into T),  1: Aq = [j <= i] e^{G_i - G_j} q_i.k_j,
+//   2 + 2 b: Ho_b = vis alpha_i e^{G_i + boff_b} h_i.Vb_b[j],  3 + 2 b: Qo_b = vis e^{G_i + boff_b} q_i.Vb_b[j]
+// with vis = [b != beta or j >= i or j < lo]
+template <typename CT, int D, int P>
+__device__ __forceinline__ void g3_gram_tile(const G3WinView<CT, D, P>& w, int ti, float gl, int beta, int lo,
+                                             int lane) {
+  constexpr bool KF = sizeof(CT) == 4;
+  const int g4 = lane >> 4, n16 = lane & 15;
+  const float gj = __shfl(gl, n16, 64);
+  float gi[4];
+#pragma unroll
+  for (int s = 0; s < 4; ++s) gi[s] = __shfl(gl, 4 * g4 + s, 64);
+  const bool isq = ti & 1;
+  const CT* arow = &w.x[(isq ? kSC : 0) + n16][0];
+  const int bl = (ti - 2) >> 1;
+  const CT* brow;
+  if (ti < 2) brow = &w.x[2 * kSC + n16][0];
+  else if constexpr (KF) brow = (const CT*)&w.vbd[kSC * bl + n16][0];
+  else brow = &w.vbx[kSC * bl + n16][0];
+  const f32x4 acc = tile_nt<CT, D>(arow, brow, g4);
+  const int j = n16;
+  if (ti == 0) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) w.pp[0][4 * g4 + s][j] = acc[s];
+  } else if (ti == 1) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int i = 4 * g4 + s;
+      w.pp[1][i][j] = (j <= i) ? expf(gi[s] - gj) * acc[s] : 0.f;
+    }
+  } else {
+    const float bo = w.boff[bl];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int i = 4 * g4 + s;
+      const bool vis = bl != beta || j >= i || j < lo;
+      const float sc = expf(gi[s] + bo) * (isq ? 1.f : w.alpha[i]);
+      w.po[isq ? 1 : 0][i][kSC * bl + j] = vis ? sc * acc[s] : 0.f;
+    }
+  }
+}
+
+// T = (I + Lm)^-1 into pp[2] (one wave, the one that formed tile 0 and the
+// coefficients: it reads what its own lanes wrote, ordered by the fences).
+// Lm[i][j] = alpha_i e^{G_i - G_j} (h_i . k_j), j < i, is strictly lower
+// (nilpotent): (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8), factors that
+// commute; squarings and products on fp32 MFMA.  An accumulator tile is a
+// k-fragment (B operand); the A operand of each square goes through LDS.
+template <typename CT, int D, int P>
+__device__ __forceinline__ void g3_inverse(const G3WinView<CT, D, P>& w, int lane) {
+  const int g4 = lane >> 4, n16 = lane & 15;
+  wave_lds_sync();
+  f32x4 xa, ta;
+#pragma unroll
+  for (int s = 0; s < 4; ++s) {
+    const int i = 4 * g4 + s;
+    xa[s] = (n16 < i) ? w.alpha[i] * expf(w.G[i] - w.G[n16]) * w.pp[0][i][n16] : 0.f;
+    w.pp[3][i][n16] = xa[s];
+    ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
+  }
+  wave_lds_sync();
+  int src = 3;
+#pragma unroll
+  for (int step = 0; step < 3; ++step) {
+    const int dst = step & 1 ? 3 : 0;
+    f32x4 sq = zero4();
+    mma(sq, *(const f32x4*)&w.pp[src][n16][4 * g4], xa);  // X^2
+    xa = sq;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) w.pp[dst][4 * g4 + s][n16] = sq[s];
+    wave_lds_sync();
+    mma(ta, *(const f32x4*)&w.pp[dst][n16][4 * g4], ta);  // T += X^2 T
+    src = dst;
+  }
+#pragma unroll
+  for (int s = 0; s < 4; ++s) w.pp[2][4 * g4 + s][n16] = ta[s];
+}
+
 // The commit of a sub-chunk's prefetched token rows into the window LDS: H =
 // b (.) k, the Q and K rows, u = w (.) v, and per token alpha and the log
 // decay (thread tid holds load unit (tid / (D / 8), 8 (tid mod (D / 8)))).
@@ -864,6 +970,46 @@ __device__ __forceinline__ void g3_commit(const G3WinView<CT, D, P>& w, const G3
   if (tid % DG == 0) {
     w.alpha[ui] = stable_alpha_f(part);
     w.lg[ui] = log_decay(r.ok ? r.dec : 1.f);
+  }
+}
+
+// The state-independent half of sub-chunk c's step, formed on waves 1..3
+// while wave 0 runs a compaction's eigen-solve (no workgroup barrier can be
+// used then): every one of the three waves loads and commits all 16 token
+// rows itself (identical values, so the concurrent writes agree), two load
+// passes in flight at a time, and reads only what it wrote; then wave 1 forms
+// the coefficients, H K^T and the inverse, wave 2 Aq and wave 3 the window
+// grams.  The commit's x, u and scalars and the tiles' pp, po must lie in LDS
+// the compaction no longer uses.
+template <typename CT, int D, int P>
+__device__ __forceinline__ void g3_stage_a_shadow(const G3WinView<CT, D, P>& w, const G3FwdArgs& p,
+                                                  const G3Tok& tk, G3Raw<CT>& ra, G3Raw<CT>& rb, int c,
+                                                  int wave, int lane) {
+  constexpr int NB = P / kSC, DG = D / 8, PASSES = kSC * DG / 64;
+  static_assert(PASSES % 2 == 0, "load passes in pairs");
+  auto fetch = [&](G3Raw<CT>& r, int pass) {
+    const int u = pass * 64 + lane;
+    g3_fetch<CT>(p, tk, r, c * kSC + u / DG - p.t0, true, 8 * (u % DG));
+  };
+#pragma unroll
+  for (int pass = 0; pass < PASSES; pass += 2) {
+    fetch(ra, pass);
+    fetch(rb, pass + 1);
+    g3_commit<CT, D, P>(w, tk, ra, pass * 64 + lane);
+    g3_commit<CT, D, P>(w, tk, rb, (pass + 1) * 64 + lane);
+  }
+  wave_lds_sync();
+  const int lo = max(0, p.t0 - c * kSC), beta = c % NB;
+  const float gl = g3_scan_g(w, lane);
+  if (wave == 1) {
+    g3_scalars(w, gl, 0.f, lane);
+    g3_gram_tile<CT, D, P>(w, 0, gl, beta, lo, lane);
+    g3_inverse(w, lane);
+  } else if (wave == 2) {
+    g3_gram_tile<CT, D, P>(w, 1, gl, beta, lo, lane);
+  } else {
+#pragma unroll
+    for (int ti = 2; ti < 2 + 2 * NB; ++ti) g3_gram_tile<CT, D, P>(w, ti, gl, beta, lo, lane);
   }
 }
 
@@ -913,114 +1059,21 @@ __device__ __forceinline__ void g3_window_step(const G3WinView<CT, D, P>& w, con
     __syncthreads();
     // per-token scalars | grams and Kronecker reads (MFMA).  Every wave forms
     // the log-decay prefix sums G (lane i holds G_i); wave 0 publishes the
-    // per-token coefficients.
-    float gl = lane < kSC ? w.lg[lane] : 0.f;
+    // per-token coefficients, the gram tiles go round the waves, and wave 0
+    // forms the inverse while waves 1..3 do the Kronecker reads.  A committed
+    // sub-chunk had all of this formed in the previous compaction's shadow.
+    if (!committed) {
+      const float gl = g3_scan_g(w, lane);
+      if (wave == 0) g3_scalars(w, gl, gacc, lane);
 #pragma unroll
-    for (int off = 1; off < kSC; off <<= 1) {
-      const float o = __shfl_up(gl, off, 64);
-      if (lane >= off) gl += o;
+      for (int r = 0; r < (2 + 2 * NB + 3) / 4; ++r)
+        if (wave + 4 * r < 2 + 2 * NB) g3_gram_tile<CT, D, P>(w, wave + 4 * r, gl, beta, lo, lane);
+      if (wave == 0) g3_inverse(w, lane);
     }
-    if (wave == 0) {
-      const float gl_last = __shfl(gl, kSC - 1, 64);
-      if (lane < kSC) {
-        const float e2 = expf(2.f * (gacc + gl));
-        w.G[lane] = gl;
-        w.gam[lane] = expf(gl);
-        w.kco[lane] = w.alpha[lane] * e2;
-        w.qco[lane] = e2;
-        w.vsc[lane] = expf(gl_last - gl);
-      }
-    }
-    // grams, 2 + 2 NB tiles over the waves (tile ti on wave ti mod 4):
-    //   0: H K^T (raw; wave 0 turns it into T),  1: Aq = [j <= i] e^{G_i - G_j} q_i.k_j,
-    //   2 + 2 b: Ho_b = vis alpha_i e^{G_i + boff_b} h_i.Vb_b[j],  3 + 2 b: Qo_b = vis e^{G_i + boff_b} q_i.Vb_b[j]
-    // with vis = [b != beta or j >= i or j < lo]
-    {
-      const float gj = __shfl(gl, n16, 64);
-      float gi[4];
-#pragma unroll
-      for (int s = 0; s < 4; ++s) gi[s] = __shfl(gl, 4 * g4 + s, 64);
-#pragma unroll
-      for (int r = 0; r < (2 + 2 * NB + 3) / 4; ++r) {
-        const int ti = wave + 4 * r;
-        if (ti < 2 + 2 * NB) {
-          const bool isq = ti & 1;
-          const CT* arow = &w.x[(isq ? kSC : 0) + n16][0];
-          const int bl = (ti - 2) >> 1;
-          const CT* brow;
-          if (ti < 2) brow = &w.x[2 * kSC + n16][0];
-          else if constexpr (KF) brow = (const CT*)&w.vbd[kSC * bl + n16][0];
-          else brow = &w.vbx[kSC * bl + n16][0];
-          const f32x4 acc = tile_nt<CT, D>(arow, brow, g4);
-          const int j = n16;
-          if (ti == 0) {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) w.pp[0][4 * g4 + s][j] = acc[s];
-          } else if (ti == 1) {
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              const int i = 4 * g4 + s;
-              w.pp[1][i][j] = (j <= i) ? expf(gi[s] - gj) * acc[s] : 0.f;
-            }
-          } else {
-            const float bo = w.boff[bl];
-#pragma unroll
-            for (int s = 0; s < 4; ++s) {
-              const int i = 4 * g4 + s;
-              const bool vis = bl != beta || j >= i || j < lo;
-              const float sc = expf(gi[s] + bo) * (isq ? 1.f : w.alpha[i]);
-              w.po[isq ? 1 : 0][i][kSC * bl + j] = vis ? sc * acc[s] : 0.f;
-            }
-          }
-        }
-      }
-    }
-    // T = (I + Lm)^-1 needs only wave 0's own Gram tile (H K^T), the decay
-    // scan and alpha: wave 0 forms it now, while waves 1..3 do the Kronecker
-    // reads
-    if (wave == 0) {
-      // the scan's G and the Gram tile were written by other lanes of this
-      // wave: order the LDS accesses (wave-local)
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      // Lm[i][j] = alpha_i e^{G_i - G_j} (h_i . k_j), j < i, is strictly lower
-      // (nilpotent): (I + Lm)^-1 = (I - L)(I + L^2)(I + L^4)(I + L^8), factors
-      // that commute; squarings and products on fp32 MFMA.  An accumulator
-      // tile is a k-fragment (B operand); the A operand of each square goes
-      // through LDS.
-      f32x4 xa, ta;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        const int i = 4 * g4 + s;
-        xa[s] = (n16 < i) ? w.alpha[i] * expf(w.G[i] - w.G[n16]) * w.pp[0][i][n16] : 0.f;
-        w.pp[3][i][n16] = xa[s];
-        ta[s] = (i == n16 ? 1.f : 0.f) - xa[s];
-      }
-      __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-      __builtin_amdgcn_wave_barrier();
-      __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-      int src = 3;
-#pragma unroll
-      for (int step = 0; step < 3; ++step) {
-        const int dst = step & 1 ? 3 : 0;
-        f32x4 sq = zero4();
-        mma(sq, *(const f32x4*)&w.pp[src][n16][4 * g4], xa);  // X^2
-        xa = sq;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) w.pp[dst][4 * g4 + s][n16] = sq[s];
-        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
-        __builtin_amdgcn_wave_barrier();
-        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
-        mma(ta, *(const f32x4*)&w.pp[dst][n16][4 * g4], ta);  // T += X^2 T
-        src = dst;
-      }
-#pragma unroll
-      for (int s = 0; s < 4; ++s) w.pp[2][4 * g4 + s][n16] = ta[s];
-    }
-    if (live && wave > 0) {
-      // this workgroup's value tiles over waves 1..3 (wave 0 forms the inverse)
-      for (int l = wave - 1; l < NVTW; l += 3) {
+    if (live && (committed || wave > 0)) {
+      // this workgroup's value tiles over waves 1..3 (wave 0 forms the inverse), or all four
+      const int w0 = committed ? wave : wave - 1, ws = committed ? 4 : 3;
+      for (int l = w0; l < NVTW; l += ws) {
         const int vt = vb * NVTW + l;
         Frag bf[D / KS];
 #pragma unroll
@@ -1757,7 +1810,8 @@ __global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
   bool live = carried;
   bool committed = false;   // the window's token rows were committed during the last compaction
   typedef typename Sm::Phase::Win WinT;
-  constexpr bool kEarly = offsetof(WinT, kr) <= sizeof(sm.ph.cs.rm);
+  constexpr bool kEarly = offsetof(WinT, skron) <= sizeof(sm.ph.cs.rm);   // x .. po inside R_mat's LDS
+  G3Raw<CT> raw2;
   float gacc = 0.f;
   int event = 0;
   const G3WinView<CT, D, P> w{sm.ph.w.x, sm.ph.w.u, sm.ph.w.kr, sm.ph.w.pp, sm.ph.w.po, sm.ph.w.skron, sm.vbd,
@@ -1789,19 +1843,11 @@ __global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
     // the next window's token loads and their commit run in the eigen-solve's
     // shadow when that window's commit targets lie in R_mat's LDS (dead by then)
     const bool pre = kEarly && p.cmode == 0 && c + 1 < cg1;
-    // (waves 1-3 only: wave 0's units are loaded and committed by wave 1 after
-    // its own, so nothing is added to the eigen-solve's wave)
-    auto issue = [&]() {
-      if (pre && wave > 0) g3_fetch<CT>(p, tk, raw, (c + 1) * kSC + ui - p.t0, has_unit, ud);
-    };
+    // (waves 1..3, all of the next window's state-independent half; nothing
+    // is added to the eigen-solve's wave)
+    auto issue = [&]() {};
     auto commit = [&]() {
-      if (!pre || wave == 0) return;
-      g3_commit<CT, D, P>(w, tk, raw, tid);
-      if (wave == 1) {
-        const int t0 = tid - 64;
-        g3_fetch<CT>(p, tk, raw, (c + 1) * kSC + t0 / DG - p.t0, t0 < kSC * DG, 8 * (t0 % DG));
-        g3_commit<CT, D, P>(w, tk, raw, t0);
-      }
+      if (pre && wave > 0) g3_stage_a_shadow<CT, D, P>(w, p, tk, raw, raw2, c + 1, wave, lane);
     };
     g3_compact<D, P>(sm.ph.cs, sm.ab, &sm.uwin[0][0], &sm.vbd[0][0], (size_t)(D + 4), (size_t)1, gacc, p.sdec,
                      p.sketch + (size_t)chain * Ge::n * qs,
