@@ -587,54 +587,38 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
       ur[r] = s;
     }
   }
-  // wave 0: v_r (one column per lane) and each pair's canonical sign,
+  // wave r: v_r (one column per lane) and the pair's canonical sign,
   // argmax_c |v_r[c]| with the first index on ties (an all-reduce by row
   // rotations inside each 16-lane row, then across the rows), then the
-  // blend of B, which needs nothing from the other waves
-  if (wave == 0) {
-    const int c = lane;
+  // blend of B's row r, which needs nothing from the other waves
+  static_assert(R <= 4, "one factor per wave");
+  if (wave < R) {
+    const int r = wave, c = lane;
     const bool on = c < n;
-    double vr[kRMax], bv_[kRMax];
-    int bi[kRMax];
+    double vr = 0.0;
+    if (on) {
+      double sv = 0.0;
 #pragma unroll
-    for (int r = 0; r < kRMax; ++r) {
-      vr[r] = 0.0;
-      if (r < R && on) {
-        double sv = 0.0;
-#pragma unroll
-        for (int j = 0; j < kQ; ++j) sv += cs.z[c * kQ + j] * cs.ev[r * kQ + j];
-        vr[r] = cs.sig[r] > 0.0 ? sv * cs.isig[r] : (c == r ? 1.0 : 0.0);
-      }
-      bv_[r] = on ? fabs(vr[r]) : -1.0;
-      bi[r] = on ? c : 0x7fffffff;
+      for (int j = 0; j < kQ; ++j) sv += cs.z[c * kQ + j] * cs.ev[r * kQ + j];
+      vr = cs.sig[r] > 0.0 ? sv * cs.isig[r] : (c == r ? 1.0 : 0.0);
     }
-    auto take = [&](int r, double ov, int oi) {
-      const bool t = (ov > bv_[r]) | ((ov == bv_[r]) & (oi < bi[r]));  // selects, no branches
-      bv_[r] = t ? ov : bv_[r];
-      bi[r] = t ? oi : bi[r];
+    double bv_ = on ? fabs(vr) : -1.0;
+    int bi = on ? c : 0x7fffffff;
+    auto take = [&](double ov, int oi) {
+      const bool t = (ov > bv_) | ((ov == bv_) & (oi < bi));  // selects, no branches
+      bv_ = t ? ov : bv_;
+      bi = t ? oi : bi;
     };
-#define G3_ARGMAX_ROT(CTL)                                                                     \
-    _Pragma("unroll") for (int r = 0; r < kRMax; ++r) if (r < R) {                            \
-      take(r, dpp_f64<CTL>(bv_[r]), __builtin_amdgcn_update_dpp(0, bi[r], CTL, 0xf, 0xf, false)); \
-    }
-    G3_ARGMAX_ROT(0x128)
-    G3_ARGMAX_ROT(0x124)
-    G3_ARGMAX_ROT(0x122)
-    G3_ARGMAX_ROT(0x121)
-#undef G3_ARGMAX_ROT
-#pragma unroll
-    for (int o2 = 16; o2 <= 32; o2 <<= 1)
-#pragma unroll
-      for (int r = 0; r < kRMax; ++r)
-        if (r < R) take(r, __shfl_xor(bv_[r], o2, 64), __shfl_xor(bi[r], o2, 64));
-#pragma unroll
-    for (int r = 0; r < kRMax; ++r)
-      if (r < R) {
-        const double vb = __shfl(vr[r], bi[r] & 63, 64);
-        const double sg = (bi[r] != 0x7fffffff && vb < 0.0) ? -1.0 : 1.0;
-        if (lane == 0) cs.sgn[r] = sg;
-        if (on) Bv[r * n + c] = s1 * (Bv[r * n + c] * dk) + s2 * (float)(sg * vr[r]);
-      }
+    take(dpp_f64<0x128>(bv_), __builtin_amdgcn_update_dpp(0, bi, 0x128, 0xf, 0xf, false));
+    take(dpp_f64<0x124>(bv_), __builtin_amdgcn_update_dpp(0, bi, 0x124, 0xf, 0xf, false));
+    take(dpp_f64<0x122>(bv_), __builtin_amdgcn_update_dpp(0, bi, 0x122, 0xf, 0xf, false));
+    take(dpp_f64<0x121>(bv_), __builtin_amdgcn_update_dpp(0, bi, 0x121, 0xf, 0xf, false));
+    take(__shfl_xor(bv_, 16, 64), __shfl_xor(bi, 16, 64));
+    take(__shfl_xor(bv_, 32, 64), __shfl_xor(bi, 32, 64));
+    const double vb = __shfl(vr, bi & 63, 64);
+    const double sg = (bi != 0x7fffffff && vb < 0.0) ? -1.0 : 1.0;
+    if (lane == 0) cs.sgn[r] = sg;
+    if (on) Bv[r * n + c] = s1 * (Bv[r * n + c] * dk) + s2 * (float)(sg * vr);
   }
   __syncthreads();
   // two-timescale blend of the decayed factors with the SVD factors (B above)
