@@ -107,9 +107,13 @@ typedef double f64x4 __attribute__((ext_vector_type(4)));
 // transposed read too).  The operands of the next step are loaded before the
 // MFMAs of this one.  Wave w owns the 16-row tiles w, w + 4, ...; C goes to
 // c (rows of kQ, fp64) and, when ct is given, column-major in fp32 to ct
-// (stride ldc).
-template <bool TRANS, int M, int K, int ldr, int ldb, int ldc = 0>
-__device__ __forceinline__ void rm_mfma(const float* rm, const float* bt, double* c, float* ct, int tid) {
+// (stride ldc).  GR: also this wave's partial Gram C^T C over its rows, from
+// the accumulators (fp64 MFMA; lane (g, r) holds C[row0 + 4 g + e][r], so
+// step e of a tile takes its element e as both operands), into *gp in the
+// layout of gram_mfma.
+template <bool TRANS, int M, int K, int ldr, int ldb, int ldc = 0, bool GR = false>
+__device__ __forceinline__ void rm_mfma(const float* rm, const float* bt, double* c, float* ct, int tid,
+                                        f64x4* gp = nullptr) {
   static_assert(M % 64 == 0 && K % 16 == 0 && ldr % 4 == 0 && ldb % 4 == 0, "whole 16-row tiles on 4 waves, 16 k per step");
   constexpr int TPW = M / 64;
   const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, n16 = lane & 15;
@@ -158,6 +162,17 @@ __device__ __forceinline__ void rm_mfma(const float* rm, const float* bt, double
       for (int e = 0; e < 4; ++e) c[(r0 + e) * kQ + n16] = (double)acc[t][e];
       if constexpr (ldc > 0) *(f32x4*)&ct[n16 * ldc + r0] = acc[t];
     }
+  if constexpr (GR) {
+    f64x4 g = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int t = 0; t < TPW; ++t)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const double x = live ? (double)acc[t][e] : 0.0;
+        g = __builtin_amdgcn_mfma_f64_16x16x4f64(x, x, g, 0, 0, 0);
+      }
+    *gp = g;
+  }
 }
 
 // 1 / sqrt(x) for x > 0 to fp64 rounding: the hardware estimate r0 and the
@@ -227,13 +242,13 @@ __device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
 // diagonal are set to zero.  The Gram runs on fp64 MFMA over 4 row segments;
 // each row of Y is then solved against R by forward substitution.
 template <int D, int P, int M, bool STG>
-__device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int passes) {
+__device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int passes, const f64x4* pre = nullptr) {
   static_assert(M % 16 == 0 && M <= kNT, "rows: 4 segments of whole MFMA steps, one row per thread");
   const int lane = tid & 63, wave = tid >> 6;
   constexpr int seg = M / 4;
   for (int pass = 0; pass < passes; ++pass) {
-    {
-      const f64x4 g = gram_mfma<seg>(cs.y + wave * seg * kQ, lane);
+    {   // this wave's partial Gram (the first pass's may come from the product that formed Y)
+      const f64x4 g = (pass == 0 && pre) ? *pre : gram_mfma<seg>(cs.y + wave * seg * kQ, lane);
       const int r = lane >> 4, c = lane & 15;
       if (c < kQ) {
         cs.red[wave * 64 + r * kQ + c] = g[0];
@@ -482,15 +497,16 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
 
   // range finder with two power iterations; orthonormalising between the
   // products leaves the final basis unchanged (up to column signs)
-  rm_mfma<false, m, n, ldr, lzn>(cs.rm, cs.zt, cs.y, nullptr, tid);
-  __syncthreads();
-  orth_rows<D, P, m, STG>(cs, tid, 1);
+  // (each Y = R_mat Z product hands its partial Grams straight to the first
+  // Cholesky-QR pass, whose barrier then also publishes Y)
+  f64x4 gp;
+  rm_mfma<false, m, n, ldr, lzn, 0, true>(cs.rm, cs.zt, cs.y, nullptr, tid, &gp);
+  orth_rows<D, P, m, STG>(cs, tid, 1, &gp);
   for (int it = 0; it < 2; ++it) {
     rm_mfma<true, n, m, ldr, lym, lzn>(cs.rm, cs.yt, cs.z, cs.zt, tid);
     __syncthreads();
-    rm_mfma<false, m, n, ldr, lzn>(cs.rm, cs.zt, cs.y, nullptr, tid);
-    __syncthreads();
-    orth_rows<D, P, m, STG>(cs, tid, it == 1 ? 2 : 1);
+    rm_mfma<false, m, n, ldr, lzn, 0, true>(cs.rm, cs.zt, cs.y, nullptr, tid, &gp);
+    orth_rows<D, P, m, STG>(cs, tid, it == 1 ? 2 : 1, &gp);
   }
   // Bm^T = R_mat^T Q  [n][kQ]
   rm_mfma<true, n, m, ldr, lym>(cs.rm, cs.yt, cs.z, nullptr, tid);
