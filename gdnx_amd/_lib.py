@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(_HERE, "libgdnx.so")
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_F64 = 2      # gdnx_check_finite only
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _c_int, _c_ll, _vp, _c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_float
 
@@ -28,6 +28,7 @@ SIGNATURES = {
     "gdnx_last_error": (ctypes.c_char_p, []),
     "gdnx_set_check_finite": (_c_int, [_c_int]),
     "gdnx_check_finite": (_c_int, [_vp, _c_ll, _c_int, _vp]),
+    "gdnx_lane_sum": (_c_int, [_vp, _vp, _c_ll, _c_int, _c_int, _c_int, _vp]),
     "gdnx_delta_chunk_size": (_c_int, [_c_int, _c_int]),
     "gdnx_delta_train_chunk_size": (_c_int, [_c_int, _c_int]),
     "gdnx_delta_chunk_states_bytes": (_c_ll, [_c_int] * 7),

@@ -540,7 +540,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     }
     double vv = (i == j) ? 1.0 : 0.0;
     for (int sweep = 0; sweep < 12; ++sweep) {
-      if (sweep > 0) {   // (a first sweep over a diagonal W rotates by identities, to rounding)
+      if (sweep >= 3) {   // (fewer than three sweeps rarely suffice; extra sweeps over a diagonal W rotate by identities)
         const double off = wave_sum_f64(i != j ? a * a : 0.0);
         const double dia = wave_sum_f64(i == j ? a * a : 0.0);
         if (!(off > 1e-28 * dia)) break;  // uniform across the wave

@@ -151,8 +151,9 @@ class _GDN3Chunk(torch.autograd.Function):
             return (None,) * 9
         dq, dk, dv, db, dw, ddec = ops.gdn3_chunk_bwd(q, k, v, bg, wg, dec, dy, tst, M=M, R=R, P=P,
                                                       factors=factors, compact_every=Kc)
-        if q.dim() == 4:   # q, k, v shared by the lanes
-            dq, dk, dv = dq.sum(3), dk.sum(3), dv.sum(3)
+        if q.dim() == 4:   # q, k, v shared by the lanes: their lane sums, in the IO dtype
+            return (ops.lane_sum(dq, q.dtype), ops.lane_sum(dk, k.dtype), ops.lane_sum(dv, v.dtype), db, dw,
+                    ddec, None, None, None)
         return dq.to(q.dtype), dk.to(k.dtype), dv.to(v.dtype), db, dw, ddec, None, None, None
 
 

@@ -707,6 +707,22 @@ def gdn3_chunk_bwd(q, k, v, b_gates, w_gates, decay, dy, train_states, *, M, R=4
     return dq, dk, dv, db, dw, ddec
 
 
+def lane_sum(x, dtype):
+    """gdnx_lane_sum: x float32 [..., M, D] (contiguous) summed over the lane
+    dim M in lane order, returned as [..., D] in dtype (bfloat16 or float32):
+    the gradient of a q, k or v its head's lanes share."""
+    lib = _lib.load()
+    _need(x.dtype == torch.float32 and x.is_contiguous() and x.dim() >= 2, "x must be contiguous float32 [..., M, D]")
+    _need(dtype in (torch.float32, torch.bfloat16), "dtype must be float32 or bfloat16")
+    M, D = x.shape[-2:]
+    out = torch.empty(*x.shape[:-2], D, dtype=dtype, device=x.device)
+    rows = out.numel() // D if D else 0
+    with torch.cuda.device(x.device):
+        rc = lib.gdnx_lane_sum(_lib.ptr(x), _lib.ptr(out), rows, M, D, _lib.dtype_code(dtype), _lib.stream_of(x))
+    _lib.check(rc, "gdnx_lane_sum")
+    return out
+
+
 # ---------------------------------------------------------------------------
 # GDN3 layer boundary (gdnx_gdn3_prologue_* / gdnx_gdn3_epilogue_*)
 # ---------------------------------------------------------------------------

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 9
+#define GDNX_ABI_VERSION 10
 
 enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1, GDNX_DTYPE_F64 = 2 /* gdnx_check_finite only */ };
 
@@ -404,6 +404,14 @@ int gdnx_gdn3_chunk_bwd(const void* q, const void* k, const void* v, int qkv_lan
                         float* dk, float* dv, float* db_gates, float* dw_gates, float* ddecay, int B,
                         int T, int H, int M, int head_dim, int R, int P, int compact_every, int a_v,
                         int a_k, int b_v, int b_k, int dtype, void* stream);
+
+/* Lane sum: out[r][d] = sum over m = 0 .. M-1, in that order, of x[r][m][d]
+ * (x float32 [rows][M][D]; out [rows][D] in dtype GDNX_DTYPE_F32 or _BF16;
+ * D a multiple of 8, both 16-byte aligned).  The gradient of q, k or v
+ * shared by a head's lanes: it replaces the backward of the reference's
+ * lane expand (gdn3/gdn3_upgrade.py:785-787), applied to the per-lane
+ * gradients gdnx_gdn3_chunk_bwd writes, and the cast to the IO dtype. */
+int gdnx_lane_sum(const float* x, void* out, long long rows, int M, int D, int dtype, void* stream);
 
 /* Rearrangement-SVD compaction with two-timescale blend, one chain per
  * block.  Replaces GDN3LinearAttn._compact_vec (gdn3/gdn3_upgrade.py:650-719)

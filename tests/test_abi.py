@@ -95,6 +95,18 @@ def test_prep_requires_workspace():
     assert rc == -1
 
 
+def test_lane_sum_rejects_bad_arguments():
+    """gdnx_lane_sum checks dtype, shape and pointers before any launch."""
+    lib = _lib.load()
+    vp = ctypes.c_void_p
+    assert lib.gdnx_lane_sum(vp(16), vp(16), 4, 4, 128, _lib.DTYPE_F64, None) == -1   # GDNX_ERR_ARG
+    assert lib.gdnx_lane_sum(vp(16), vp(16), 4, 4, 100, _lib.DTYPE_F32, None) == -2   # GDNX_ERR_SHAPE
+    assert lib.gdnx_lane_sum(vp(16), vp(16), 4, 0, 128, _lib.DTYPE_F32, None) == -2
+    assert lib.gdnx_lane_sum(None, vp(16), 4, 4, 128, _lib.DTYPE_BF16, None) == -1
+    assert lib.gdnx_lane_sum(vp(8), vp(16), 4, 4, 128, _lib.DTYPE_BF16, None) == -1     # misaligned
+    assert lib.gdnx_lane_sum(None, None, 0, 4, 128, _lib.DTYPE_BF16, None) == 0          # nothing to do
+
+
 @pytest.mark.parametrize("M,K", [(4, 128), (4, 64), (3, 96), (2, 8), (1, 4), (4, 256)])
 def test_lane_rope_pairs_follow_the_oracle_rule(M, K):
     """The library's lane RoPE pairs (host-only call) equal the oracle's

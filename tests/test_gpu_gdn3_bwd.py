@@ -200,3 +200,24 @@ def test_gdn3_training_call_returns_state_and_error(gpu_lib):
     assert torch.equal(e0, e1)
     grads = torch.autograd.grad(y1, leaves, dy.to(DEV))
     assert all(bool(torch.isfinite(g).all()) for g in grads)
+
+
+@pytest.mark.parametrize("M,D,dt", [(4, 128, torch.bfloat16), (4, 64, torch.float32), (3, 128, torch.float32),
+                                    (1, 64, torch.bfloat16)])
+def test_lane_sum_matches_torch(gpu_lib, M, D, dt):
+    """gdnx_lane_sum (the lane-shared q/k/v gradient): the sum over the lanes
+    in lane order, cast to the IO dtype, equals the float64 sum rounded once
+    to float32 (then to dtype) up to the float32 sums' own rounding."""
+    from gdnx_amd import ops
+    print(f"case: lane sum M={M} D={D} {dt}", flush=True)
+    g = torch.Generator().manual_seed(M * D)
+    x = torch.randn(2, 33, 3, M, D, generator=g)
+    out = ops.lane_sum(x.to(DEV), dt)
+    torch.cuda.synchronize()
+    ref = x.double().sum(3)
+    assert out.shape == (2, 33, 3, D) and out.dtype == dt
+    if dt == torch.float32:
+        torch.testing.assert_close(out.cpu().double(), ref, rtol=0, atol=4 * 2.0 ** -24 * float(x.abs().max()) * M)
+    else:   # within one bf16 rounding of the exact sum
+        err = (out.cpu().double() - ref).abs()
+        assert bool((err <= ref.abs() * 2.0 ** -8 + 1e-30).all())
