@@ -364,17 +364,29 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         constexpr int JKT = 16 / Ge::bv, IKT = 16 / Ge::av;   // jk and ik per tile
         constexpr int NJ = Ge::bk / JKT, NT = NJ * (Ge::ak / IKT);
         static_assert(NT % 4 == 0, "whole tiles per wave");
+        // Every operand is read before the first MFMA and every MFMA issued
+        // before the first store: in a read / MFMA / store chain per tile the
+        // stores (which might alias the factors, as far as the compiler can
+        // tell) would hold each next read, one LDS round trip per tile.
         const int g = lane >> 4, l16 = lane & 15;
+        constexpr int TW = NT / 4;   // tiles per wave
+        float av[TW], bv[TW];
 #pragma unroll
-        for (int u = 0; u < NT / 4; ++u) {
+        for (int u = 0; u < TW; ++u) {
           const int t = wave + 4 * u, jk0 = (t % NJ) * JKT, ik0 = (t / NJ) * IKT;
-          const float av = Bf[g * Ge::n + (l16 % Ge::bv) * Ge::bk + jk0 + l16 / Ge::bv];
-          const float bv = st[g * Ge::m + (l16 % Ge::av) * Ge::ak + ik0 + l16 / Ge::av];
-          f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+          av[u] = Bf[g * Ge::n + (l16 % Ge::bv) * Ge::bk + jk0 + l16 / Ge::bv];
+          bv[u] = st[g * Ge::m + (l16 % Ge::av) * Ge::ak + ik0 + l16 / Ge::av];
+        }
+        f32x4 acc[TW];
+#pragma unroll
+        for (int u = 0; u < TW; ++u)
+          acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(av[u], bv[u], zero4(), 0, 0, 0);
+#pragma unroll
+        for (int u = 0; u < TW; ++u) {
+          const int t = wave + 4 * u, jk0 = (t % NJ) * JKT, ik0 = (t / NJ) * IKT;
           const int i0 = 4 * g, jk = jk0 + i0 / Ge::bv, jv = i0 % Ge::bv;
           const int ik = ik0 + l16 / Ge::av, iv = l16 % Ge::av;
-          st4(&sm.skt[ik * Ge::bk + jk][iv * Ge::bv + jv], acc[0], acc[1], acc[2], acc[3]);
+          st4(&sm.skt[ik * Ge::bk + jk][iv * Ge::bv + jv], acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
         }
       } else {
         // the fragments this lane feeds the Kronecker products: row k = d of
