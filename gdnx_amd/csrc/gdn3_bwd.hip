@@ -52,7 +52,7 @@ struct alignas(16) G3BwdSmem {
   float hot[NB][BP][LP], qot[NB][BP][LP]; // Ho_b^T, Qo_b^T
   float vv[NB][BP][LP], wq[NB][BP][LP];   // dHo_b, dQo_b gradient factors
   float kd[P];                            // block slot: its key's decay to the start of the sub-chunk
-  float lg[BP], lgp[P], dec[BP], alpha[BP], cdot[BP];
+  float lg[BP], lgp[P], dec[BP], alpha[BP], cdot[BP], bsc[BP];   // bsc: scalar erase gates
   float G[BP], e2[BP], kco[BP], qco[BP], vsc[BP], dc[BP], su[BP];
   float red[8][4][BP];                    // per-wave partial per-token sums, slots kR*
   float carry[4];
@@ -98,6 +98,11 @@ __device__ __forceinline__ void raw8(const CT* p, Row8<CT>& r) {
 #pragma unroll
   for (int i = 0; i < (int)(sizeof(CT) / 2); ++i) r.w[i] = ((const uint4*)p)[i];
 }
+template <typename CT>
+__device__ __forceinline__ void zero8(Row8<CT>& r) {
+#pragma unroll
+  for (int i = 0; i < (int)(sizeof(CT) / 2); ++i) r.w[i] = make_uint4(0u, 0u, 0u, 0u);
+}
 __device__ __forceinline__ void cvt8(const Row8<bf16>& r, float* f) {
   const bf16x8 x = *(const bf16x8*)&r.w[0];
 #pragma unroll
@@ -111,11 +116,7 @@ __device__ __forceinline__ void cvt8(const Row8<float>& r, float* f) {
     f[4 + e] = b[e];
   }
 }
-template <typename CT>
-__device__ __forceinline__ void zero8(Row8<CT>& r) {
-#pragma unroll
-  for (int i = 0; i < (int)(sizeof(CT) / 2); ++i) r.w[i] = make_uint4(0u, 0u, 0u, 0u);
-}
+
 
 // A bf16 k-step fragment (k = 4 g + i and 16 + 4 g + i, i < 4) of an fp32 LDS
 // row as hi + lo bf16 parts: x - hi - lo is ~2^-17 of x
@@ -204,7 +205,7 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
   constexpr int KS = FragT<CT>::KSTEP;
   typedef typename FragT<CT>::type Frag;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g4 = lane >> 4, n16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), g4 = lane >> 4, n16 = lane & 15;
   const int H = p.H, M = p.M, T = p.T;
   const int N = p.B * H * M;
   const int chain = xcd_remap(blockIdx.x, N);
@@ -243,11 +244,10 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
   auto rebuilds = [&](int cc) { return cc / per > 0 && (cc == nch - 1 || (cc + 1) % per == 0); };
   auto fetch_ab = [&](int cc) {
     const float* ab = ts.ab + ((size_t)(cc / per - 1) * N + chain) * Ge::RMN;
+    // (a clamped index, no branch: a load under a branch drew a wait for every
+    // load issued before it)
 #pragma unroll
-    for (int u = 0; u < NAB; ++u) {
-      const int e = tid + u * kNT;
-      abr[u] = e < Ge::RMN ? ab[e] : 0.f;
-    }
+    for (int u = 0; u < NAB; ++u) abr[u] = ab[min(tid + u * kNT, Ge::RMN - 1)];
   };
   if (nch > 0 && rebuilds(nch - 1)) fetch_ab(nch - 1);
 
@@ -306,6 +306,8 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         if (e < Ge::RMN) st[e] = abr[u];
       }
     }
+    // the next rebuild's factors, issued ahead of this sub-chunk's input loads
+    if (c > 0 && rebuilds(c - 1)) fetch_ab(c - 1);
 
     // the sub-chunk's inputs, the block entering the window (sub-chunk c -
     // NB) and the decays of the P tokens before the sub-chunk, loaded raw
@@ -321,27 +323,35 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
       raw8<CT>((const CT*)p.q + qkv_base + (size_t)t * qkv_tok + ud, rq);
       raw8<CT>((const CT*)p.v + qkv_base + (size_t)t * qkv_tok + ud, rv);
       raw8<CT>((const CT*)p.dy + y_base + (size_t)t * y_tok + ud, rdy);
+      // the scalar gates (channel 0 of per-channel gates, unused then) load
+      // unconditionally: a value set in one branch and loaded in the other made
+      // the merge wait for every load issued before
+      bs = p.bg[gate_base + (size_t)t * gate_tok];
+      ws = p.wg[gate_base + (size_t)t * gate_tok];
       if (gc > 1) {
         raw8<float>(p.bg + gate_base + (size_t)t * gate_tok + ud, rb);
         raw8<float>(p.wg + gate_base + (size_t)t * gate_tok + ud, rw);
-      } else {
-        bs = p.bg[gate_base + (size_t)t * gate_tok];
-        ws = p.wg[gate_base + (size_t)t * gate_tok];
       }
       dv = p.dec[dec_base + (size_t)t * dec_tok];
       raw8<float>(ts.u + ((size_t)chain * nch + c) * BP * D + (size_t)ui * D + ud, ru);
     }
-    // the erase gates at this wave's key tiles (used in G), loaded with the rest:
-    // in G they would sit between stores the compiler cannot reorder them past
+    // per-channel erase gates at this wave's key tiles (used in G), loaded with
+    // the rest (in G they would sit between stores the compiler cannot reorder
+    // them past); scalar gates go through LDS from A
     float bgc[VPW][4];
 #pragma unroll
     for (int a = 0; a < VPW; ++a)
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) {
-        const int tt_ = c * BP + 4 * g4 + s4, d = 16 * (wave * VPW + a) + n16;
-        bgc[a][s4] = tt_ < T ? (gc > 1 ? p.bg[gate_base + (size_t)tt_ * gate_tok + d]
-                                       : p.bg[gate_base + (size_t)tt_ * gate_tok]) : 0.f;
-      }
+      for (int s4 = 0; s4 < 4; ++s4) bgc[a][s4] = 0.f;
+    if (gc > 1) {
+#pragma unroll
+      for (int a = 0; a < VPW; ++a)
+#pragma unroll
+        for (int s4 = 0; s4 < 4; ++s4) {
+          const int tt_ = c * BP + 4 * g4 + s4, d = 16 * (wave * VPW + a) + n16;
+          if (tt_ < T) bgc[a][s4] = p.bg[gate_base + (size_t)tt_ * gate_tok + d];
+        }
+    }
     load_block(c - NB, rkp, ruo);
     // the decay of token c BP - P + tid (tid < P), loaded unconditionally at an
     // in-bounds token and used raw in A: a load in a branch drew its clamp in
@@ -415,7 +425,6 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         }
       }
     }
-    if (c > 0 && rebuilds(c - 1)) fetch_ab(c - 1);
 
     // ---- A: the sub-chunk's inputs to LDS (h = b o k, alpha, log decays), the entering block ----
     float vf[8], wf[8];
@@ -461,6 +470,7 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         sm.alpha[ui] = stable_alpha_f(part);
         sm.lg[ui] = tv ? log_decay(dv) : 0.f;
         sm.dec[ui] = dv;
+        sm.bsc[ui] = bs;
       }
       if (tid < P) sm.lgp[tid] = c * BP - P + tid >= 0 ? log_decay(dvp) : 0.f;
     }
@@ -497,9 +507,14 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     {
       const int j = n16;
       const float Gj = __shfl(gl, j, 64);
-      float Gi[4];
+      // the rows' alpha read once, before the tile stores (a read after a store
+      // to LDS the compiler cannot tell apart waits for that store)
+      float Gi[4], ali[4];
 #pragma unroll
-      for (int s = 0; s < 4; ++s) Gi[s] = __shfl(gl, 4 * g4 + s, 64);
+      for (int s = 0; s < 4; ++s) {
+        Gi[s] = __shfl(gl, 4 * g4 + s, 64);
+        ali[s] = sm.alpha[4 * g4 + s];
+      }
 #pragma unroll
       for (int r = 0; r < TPW; ++r) {
         const int ti = wave + 4 * r;
@@ -521,7 +536,7 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
             for (int s = 0; s < 4; ++s) {
               const int i = 4 * g4 + s;
               sm.m0[i][j] = acc[s];
-              sm.lm[i][j] = (j < i) ? sm.alpha[i] * expf(Gi[s] - Gj) * acc[s] : 0.f;
+              sm.lm[i][j] = (j < i) ? ali[s] * expf(Gi[s] - Gj) * acc[s] : 0.f;
             }
           } else if (ti == 1) {
 #pragma unroll
@@ -540,7 +555,7 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
               const float ga = expf(Gi[s]), m2 = kdj * acc[s];
               if (!isq) {
                 sm.m2[bl][i][j] = m2;
-                sm.hot[bl][j][i] = vis ? sm.alpha[i] * ga * m2 : 0.f;
+                sm.hot[bl][j][i] = vis ? ali[s] * ga * m2 : 0.f;
               } else {
                 sm.qot[bl][j][i] = vis ? ga * m2 : 0.f;
               }
@@ -580,22 +595,34 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     __syncthreads();
 
     // ---- D: dU_tot = dU + Aq^T dY, dRhs = T^T dU_tot, the blocks' dU ----
-#pragma unroll
-    for (int a = 0; a < VPW; ++a) {
-      const int col = 16 * (wave * VPW + a) + n16;
-      const f32x4 dYf = col_frag<LR>(sm.dy, col, g4);
-      f32x4 dut = dUc[a];
-      mma(dut, ld_frag(&sm.aqt[n16][0], g4), dYf);
-      f32x4 drh = zero4();
-      mma(drh, ld_frag(&sm.tt[n16][0], g4), dut);
-#pragma unroll
-      for (int s = 0; s < 4; ++s) sm.dr[4 * g4 + s][col] = drh[s];
+    {
+      // every operand read before the first dRhs store (reads after a store the
+      // compiler cannot tell apart would wait for it)
+      const f32x4 aqf = ld_frag(&sm.aqt[n16][0], g4), ttf = ld_frag(&sm.tt[n16][0], g4);
+      f32x4 qof[NB], hof[NB], dYf[VPW];
 #pragma unroll
       for (int bl = 0; bl < NB; ++bl) {
-        f32x4 nd = zero4();
-        mma(nd, ld_frag(&sm.qot[bl][n16][0], g4), dYf);
-        mma(nd, ld_frag(&sm.hot[bl][n16][0], g4), -drh);
-        dUa[bl][a] = (bl == beta) ? nd : dUa[bl][a] + nd;
+        qof[bl] = ld_frag(&sm.qot[bl][n16][0], g4);
+        hof[bl] = ld_frag(&sm.hot[bl][n16][0], g4);
+      }
+#pragma unroll
+      for (int a = 0; a < VPW; ++a) dYf[a] = col_frag<LR>(sm.dy, 16 * (wave * VPW + a) + n16, g4);
+#pragma unroll
+      for (int a = 0; a < VPW; ++a) {
+        const int col = 16 * (wave * VPW + a) + n16;
+        f32x4 dut = dUc[a];
+        mma(dut, aqf, dYf[a]);
+        f32x4 drh = zero4();
+        mma(drh, ttf, dut);
+#pragma unroll
+        for (int s = 0; s < 4; ++s) sm.dr[4 * g4 + s][col] = drh[s];
+#pragma unroll
+        for (int bl = 0; bl < NB; ++bl) {
+          f32x4 nd = zero4();
+          mma(nd, qof[bl], dYf[a]);
+          mma(nd, hof[bl], -drh);
+          dUa[bl][a] = (bl == beta) ? nd : dUa[bl][a] + nd;
+        }
       }
     }
     __syncthreads();
@@ -620,12 +647,24 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
           else
             acc = tile_nt<float, D>(ar + n16 * LR, br + n16 * LR, g4);
           if (!isq) acc = -acc;
+          // the element loop's operands, read before its first store (a read
+          // after a store the compiler cannot tell apart waits for it)
+          float Gv[4], alv[4], o1[4], o2[4];
+          const int blc = bl < 0 ? 0 : bl;   // (tiles 0 and 1 read no block)
 #pragma unroll
           for (int s = 0; s < 4; ++s) {
             const int i = 4 * g4 + s;
-            const float Gi = sm.G[i], al = sm.alpha[i], ga = expf(Gi);
+            Gv[s] = sm.G[i];
+            alv[s] = sm.alpha[i];
+            o1[s] = ti == 0 ? sm.m0[i][j] : ti == 1 ? sm.aqt[j][i] : isq ? 0.f : sm.m2[blc][i][j];
+            o2[s] = ti < 2 ? 0.f : isq ? sm.qot[blc][j][i] : sm.hot[blc][j][i];
+          }
+#pragma unroll
+          for (int s = 0; s < 4; ++s) {
+            const int i = 4 * g4 + s;
+            const float Gi = Gv[s], al = alv[s], ga = expf(Gi);
             if (ti == 0) {          // dLm (j < i)
-              const float x = (j < i) ? acc[s] : 0.f, e = expf(Gi - Gj), m0 = sm.m0[i][j];
+              const float x = (j < i) ? acc[s] : 0.f, e = expf(Gi - Gj), m0 = o1[s];
               const float wv = x * al * e;
               sm.w[i][j] = wv;
               sm.wt[j][i] = wv;
@@ -638,7 +677,7 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
               const float zv = x * e;
               sm.z[i][j] = zv;
               sm.zt[j][i] = zv;
-              const float g = x * sm.aqt[j][i];
+              const float g = x * o1[s];
               rg[s] += g;
               cg += g;
             } else {
@@ -646,11 +685,11 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
               const float x = vis ? acc[s] : 0.f;
               if (!isq) {           // dHo_b
                 sm.vv[bl][i][j] = x * al * ga;
-                rda[s] += x * ga * sm.m2[bl][i][j];
-                rg[s] += x * sm.hot[bl][j][i];
+                rda[s] += x * ga * o1[s];
+                rg[s] += x * o2[s];
               } else {              // dQo_b
                 sm.wq[bl][i][j] = x * ga;
-                rg[s] += x * sm.qot[bl][j][i];
+                rg[s] += x * o2[s];
               }
             }
           }
@@ -704,24 +743,31 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         }
       }
     }
+    {
+      // all rows' partials before the first store to red (reads after it
+      // would wait for it)
+      float xh[4], xq[4], xv[4];
 #pragma unroll
-    for (int s = 0; s < 4; ++s) {
-      const int i = 4 * g4 + s;
-      float xh = 0.f, xq = 0.f, xv = 0.f;
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        xh[s] = xq[s] = xv[s] = 0.f;
 #pragma unroll
-      for (int a = 0; a < VPW; ++a) {
-        const int d = 16 * (wave * VPW + a) + n16;
-        xh += sm.h[i][d] * Gh[a][s];
-        xq += sm.q[i][d] * Gq[a][s];
-        xv += dVc[a][s] * sm.k[i][d];
+        for (int a = 0; a < VPW; ++a) {
+          const int d = 16 * (wave * VPW + a) + n16;
+          xh[s] += sm.h[i][d] * Gh[a][s];
+          xq[s] += sm.q[i][d] * Gq[a][s];
+          xv[s] += dVc[a][s] * sm.k[i][d];
+        }
       }
-      xh = row_prefix16(xh);
-      xq = row_prefix16(xq);
-      xv = row_prefix16(xv);
-      if (n16 == 15) {
-        sm.red[kRhG][wave][i] = xh;
-        sm.red[kRqG][wave][i] = xq;
-        sm.red[kRsvb][wave][i] = xv;   // times vsc_i below
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        const int i = 4 * g4 + s;
+        const float ph = row_prefix16(xh[s]), pq = row_prefix16(xq[s]), pv = row_prefix16(xv[s]);
+        if (n16 == 15) {
+          sm.red[kRhG][wave][i] = ph;
+          sm.red[kRqG][wave][i] = pq;
+          sm.red[kRsvb][wave][i] = pv;   // times vsc_i below
+        }
       }
     }
     // the blocks this sub-chunk leaves in the window decay by e^{G_last}:
@@ -864,7 +910,7 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         float dh = dH[s] + dci * Kc[s];
         if (live) dh -= sm.kco[i] * Gh[a][s];
         const float dq = dQ[s] + (live ? sm.qco[i] * Gq[a][s] : 0.f);
-        const float bgv = bgc[a][s];
+        const float bgv = gc > 1 ? bgc[a][s] : sm.bsc[i];
         const float dk = dK[s] + dci * Hc[s] + dVc[a][s] * sm.vsc[i] + bgv * dh;
         dbp[s] = Kc[s] * dh;
         dbs[s] += dbp[s];
