@@ -116,7 +116,7 @@ __device__ __forceinline__ void rm_mfma(const float* rm, const float* bt, double
                                         f64x4* gp = nullptr) {
   static_assert(M % 64 == 0 && K % 16 == 0 && ldr % 4 == 0 && ldb % 4 == 0, "whole 16-row tiles on 4 waves, 16 k per step");
   constexpr int TPW = M / 64;
-  const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, n16 = lane & 15;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = lane >> 4, n16 = lane & 15;
   const bool live = n16 < kQ;
   // lanes of the dead columns 8..15 repeat the live ones (their outputs are dropped)
   const float* bcol = bt + (n16 & (kQ - 1)) * ldb + 4 * g;
@@ -244,7 +244,7 @@ __device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
 template <int D, int P, int M, bool STG>
 __device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int passes, const f64x4* pre = nullptr) {
   static_assert(M % 16 == 0 && M <= kNT, "rows: 4 segments of whole MFMA steps, one row per thread");
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   constexpr int seg = M / 4;
   for (int pass = 0; pass < passes; ++pass) {
     {   // this wave's partial Gram (the first pass's may come from the product that formed Y)
@@ -310,7 +310,7 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int
 // array, into out[0..kRMax) (every thread waits for them).
 template <int M>
 __device__ __forceinline__ void col_sumsq(const double* y, double* red, double* out, int tid) {
-  const int r = tid & (kRMax - 1), lane = tid & 63, wave = tid >> 6;
+  const int r = tid & (kRMax - 1), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   double part = 0.0;
   for (int row = tid / kRMax; row < M; row += kNT / kRMax) {
     const double x = y[row * kQ + r];
@@ -355,7 +355,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   float* A = ab;
   float* Bv = ab + R * m;
   tid = opaque(tid);
-  const int lane = tid & 63, wave = tid >> 6;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
   // the sketch's global loads are issued first and land in LDS after the
   // residual part (which does not read them)
@@ -1033,7 +1033,7 @@ __device__ __forceinline__ void g3_window_step(const G3WinView<CT, D, P>& w, con
   typedef typename FragT<CT>::type Frag;
   constexpr int NVTW = D / 16 / NVB;   // value tiles of this workgroup: vb NVTW + [0, NVTW)
   constexpr int VPW = (NVTW + 3) / 4;
-  const int tid = opaque(threadIdx.x), lane = tid & 63, wave = tid >> 6;
+  const int tid = opaque(threadIdx.x), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, n16 = lane & 15;
   const int T = p.T;
   const bool has_unit = tid < UNITS;
@@ -1187,7 +1187,7 @@ __global__ void __launch_bounds__(kNT) gdn3_window_kernel(G3FwdArgs p) {
   static_assert(P % kSC == 0 && NB >= 1 && NB <= 4, "whole 16-slot blocks, at most 4");
   static_assert(sizeof(Sm) <= 160 * 1024, "LDS budget");
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, n16 = lane & 15;
   const int H = p.H, M = p.M, T = p.T;
   const int N = p.B * H * M;
@@ -1346,7 +1346,7 @@ __global__ void __launch_bounds__(kNT) gdn3_window_pipe_kernel(G3FwdArgs p) {
   static_assert(sizeof(Sm) <= 160 * 1024, "LDS budget");
   typedef G3D<D> Ge;
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g4 = lane >> 4, n16 = lane & 15;
   const int T = p.T;
   const int N = p.B * p.H * p.M;
@@ -1720,7 +1720,7 @@ __device__ __forceinline__ void write_skron(CT* sk, const float* Af, const float
   constexpr int QT = Ge::n / 16, NT = QT * (Ge::m / 16);
   static_assert(Ge::R == 4 && Ge::bk % 4 == 0 && Ge::m % 16 == 0 && Ge::n % 16 == 0 && NT % 4 == 0,
                 "K = R = 4 MFMA tiles, runs of 4 jk");
-  const int lane = tid & 63, wave = tid >> 6, g = lane >> 4, l16 = lane & 15;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = lane >> 4, l16 = lane & 15;
   // every tile's operands are loaded before the first MFMA
   float ao[NT / 4], bo[NT / 4];
 #pragma unroll
@@ -1779,7 +1779,7 @@ __global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
   static_assert(sizeof(Sm) <= 160 * 1024, "LDS budget");
   typedef G3D<D> Ge;
   constexpr int Rm = Ge::R * Ge::m, Rn = Ge::R * Ge::n, VPW = (D / 16 + 3) / 4;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, g4 = lane >> 4, n16 = lane & 15;
+  const int tid = threadIdx.x, lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), g4 = lane >> 4, n16 = lane & 15;
   const int N = p.B * p.H * p.M;
   const int chain = xcd_remap(blockIdx.x, N);
   const G3Tok tk(p, chain, D);
