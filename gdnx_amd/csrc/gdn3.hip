@@ -44,14 +44,21 @@ __device__ __forceinline__ double dpp_f64(double x) {
   const int hi = __builtin_amdgcn_update_dpp(0, (int)(b >> 32), CTL, 0xf, 0xf, false);
   return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
 }
+// lane l's x, wave-uniform (l uniform)
+__device__ __forceinline__ double readlane_f64(double x, int l) {
+  const long long b = __double_as_longlong(x);
+  const int lo = __builtin_amdgcn_readlane((int)(b & 0xffffffffll), l);
+  const int hi = __builtin_amdgcn_readlane((int)(b >> 32), l);
+  return __longlong_as_double(((long long)hi << 32) | (long long)(unsigned)lo);
+}
+// (the four row sums are read out of lanes 0, 16, 32, 48 and added as
+// (r0 + r1) + (r2 + r3): a uniform value, no LDS round trip)
 __device__ __forceinline__ double wave_sum_f64(double x) {
   x += dpp_f64<0x128>(x);
   x += dpp_f64<0x124>(x);
   x += dpp_f64<0x122>(x);
   x += dpp_f64<0x121>(x);
-  x += __shfl_xor(x, 16, 64);
-  x += __shfl_xor(x, 32, 64);
-  return x;
+  return (readlane_f64(x, 0) + readlane_f64(x, 16)) + (readlane_f64(x, 32) + readlane_f64(x, 48));
 }
 
 // Sum of NV doubles over the 256 threads of the block, in a fixed order;
@@ -629,10 +636,20 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     take(dpp_f64<0x124>(bv_), __builtin_amdgcn_update_dpp(0, bi, 0x124, 0xf, 0xf, false));
     take(dpp_f64<0x122>(bv_), __builtin_amdgcn_update_dpp(0, bi, 0x122, 0xf, 0xf, false));
     take(dpp_f64<0x121>(bv_), __builtin_amdgcn_update_dpp(0, bi, 0x121, 0xf, 0xf, false));
-    take(__shfl_xor(bv_, 16, 64), __shfl_xor(bi, 16, 64));
-    take(__shfl_xor(bv_, 32, 64), __shfl_xor(bi, 32, 64));
-    const double vb = __shfl(vr, bi & 63, 64);
-    const double sg = (bi != 0x7fffffff && vb < 0.0) ? -1.0 : 1.0;
+    // the four rows' results out of lanes 0, 16, 32, 48 (the order does not
+    // matter: max value, then least index, is a total order): wave-uniform
+    double mv = readlane_f64(bv_, 0);
+    int mi = __builtin_amdgcn_readlane(bi, 0);
+#pragma unroll
+    for (int rr = 1; rr < 4; ++rr) {
+      const double ov = readlane_f64(bv_, 16 * rr);
+      const int oi = __builtin_amdgcn_readlane(bi, 16 * rr);
+      const bool t = (ov > mv) | ((ov == mv) & (oi < mi));
+      mv = t ? ov : mv;
+      mi = t ? oi : mi;
+    }
+    const double vb = readlane_f64(vr, mi & 63);
+    const double sg = (mi != 0x7fffffff && vb < 0.0) ? -1.0 : 1.0;
     if (lane == 0) cs.sgn[r] = sg;
     if (on) Bv[r * n + c] = s1 * (Bv[r * n + c] * dk) + s2 * (float)(sg * vr);
   }
