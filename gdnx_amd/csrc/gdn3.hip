@@ -111,8 +111,7 @@ typedef double f64x4 __attribute__((ext_vector_type(4)));
 // k = kb + 4 g + s to the s-th MFMA: its B entries are one 16-byte load, and
 // so are its A entries of an untransposed row (rows of ldr = 4 mod 64 floats
 // put the 16 rows of a tile on distinct banks, and the 16 columns of a
-// transposed read too).  The operands of the next step are loaded before the
-// MFMAs of this one.  Wave w owns the 16-row tiles w, w + 4, ...; C goes to
+// transposed read too).  Wave w owns the 16-row tiles w, w + 4, ...; C goes to
 // c (rows of kQ, fp64) and, when ct is given, column-major in fp32 to ct
 // (stride ldc).  GR: also this wave's partial Gram C^T C over its rows, from
 // the accumulators (fp64 MFMA; lane (g, r) holds C[row0 + 4 g + e][r], so
@@ -139,27 +138,28 @@ __device__ __forceinline__ void rm_mfma(const float* rm, const float* bt, double
     }
     return x;
   };
-  f32x4 acc[TPW], av[TPW], bv = ldb4(0);
+  // the operands of BATCH steps are read before their MFMAs (one LDS round
+  // trip per batch; with one step ahead only, the compiler, short of
+  // registers, waited for each step's reads)
+  constexpr int NSTEP = K / 16, BATCH = TPW == 1 ? 4 : 2;
+  static_assert(NSTEP % BATCH == 0, "whole batches");
+  f32x4 acc[TPW];
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) {
-    acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-    av[t] = lda4(t, 0);
-  }
+  for (int t = 0; t < TPW; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-  for (int kb = 0; kb < K; kb += 16) {
-    f32x4 an[TPW], bn;
-    if (kb + 16 < K) {
-      bn = ldb4(kb + 16);
+  for (int s0 = 0; s0 < NSTEP; s0 += BATCH) {
+    f32x4 av[BATCH][TPW], bv[BATCH];
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) an[t] = lda4(t, kb + 16);
+    for (int u = 0; u < BATCH; ++u) {
+      bv[u] = ldb4(16 * (s0 + u));
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) av[u][t] = lda4(t, 16 * (s0 + u));
     }
+    __builtin_amdgcn_sched_barrier(0);   // (the scheduler would interleave them again)
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) mma(acc[t], av[t], bv);
-    if (kb + 16 < K) {
-      bv = bn;
+    for (int u = 0; u < BATCH; ++u)
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) av[t] = an[t];
-    }
+      for (int t = 0; t < TPW; ++t) mma(acc[t], av[u][t], bv[u]);
   }
   if (live)
 #pragma unroll
