@@ -409,20 +409,23 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
         if constexpr (STG) return cs.vt[i][d];
         else return Vb[(size_t)(16 * pb + i) * u_sp + (size_t)d * u_sd];
       };
+      // every operand read before the MFMAs, behind a scheduling barrier (the
+      // compiler, short of registers, waited for each tile's reads); the
+      // key fragments serve every value tile
+      f32x4 ua[VTW], kb4[NT16];
 #pragma unroll
-      for (int vi = 0; vi < VTW; ++vi) {
-        const int vt = wave * VTW + vi;
-        f32x4 ua;
+      for (int vi = 0; vi < VTW; ++vi)
 #pragma unroll
-        for (int s4 = 0; s4 < 4; ++s4) ua[s4] = uval(4 * g4 + s4, vt * 16 + n16);
+        for (int s4 = 0; s4 < 4; ++s4) ua[vi][s4] = uval(4 * g4 + s4, (wave * VTW + vi) * 16 + n16);
 #pragma unroll
-        for (int kt = 0; kt < NT16; ++kt) {
-          f32x4 kb4;
+      for (int kt = 0; kt < NT16; ++kt)
 #pragma unroll
-          for (int s4 = 0; s4 < 4; ++s4) kb4[s4] = vval(4 * g4 + s4, kt * 16 + n16);
-          mma(racc[vi][kt], ua, kb4);
-        }
-      }
+        for (int s4 = 0; s4 < 4; ++s4) kb4[kt][s4] = vval(4 * g4 + s4, kt * 16 + n16);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int vi = 0; vi < VTW; ++vi)
+#pragma unroll
+        for (int kt = 0; kt < NT16; ++kt) mma(racc[vi][kt], ua[vi], kb4[kt]);
     }
     // plus the Kronecker part sum_r A_r[iv][ik] B_r[jv][jk] (each factor decayed
     // by e^{gacc}), and the energy |R_mat|^2.  With b_v = b_k = 8 a lane's
@@ -441,12 +444,16 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
 #pragma unroll
     for (int vi = 0; vi < VTW; ++vi) {
       const int vt = wave * VTW + vi, iv = 2 * vt + (g4 >> 1);
+      float alv[NT16][kRMax];   // (read before use, as above)
+#pragma unroll
+      for (int kt = 0; kt < NT16; ++kt)
+#pragma unroll
+        for (int r = 0; r < kRMax; ++r) alv[kt][r] = r < R ? A[r * m + iv * ak + 2 * kt + (n16 >> 3)] : 0.f;
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int kt = 0; kt < NT16; ++kt) {
         const int ik = 2 * kt + (n16 >> 3), jk = n16 & 7, row = iv * ak + ik;
-        float al[kRMax];
-#pragma unroll
-        for (int r = 0; r < kRMax; ++r) al[r] = r < R ? A[r * m + row] : 0.f;
+        const float* al = alv[kt];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int jv = (4 * g4 + i) & 7;

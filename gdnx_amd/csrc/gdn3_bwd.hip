@@ -135,15 +135,38 @@ __device__ __forceinline__ void split_frag(const float* p, int g, bf16x8& hi, bf
 // 16x16 NT tile product over K of fp32 LDS rows on bf16 MFMA: each operand
 // enters as hi + lo parts (an operand that holds bf16 values exactly needs no
 // lo part); lo x lo is dropped, so the product is within ~2^-16 of fp32
+// (every step's operands are read before the first split and MFMA, behind a
+// scheduling barrier: the compiler, short of registers, waited for each
+// step's LDS reads)
+__device__ __forceinline__ void split8(const f32x4& x0, const f32x4& x1, bf16x8& hi, bf16x8& lo) {
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const bf16 h0 = (bf16)x0[i], h1 = (bf16)x1[i];
+    hi[i] = h0;
+    hi[4 + i] = h1;
+    lo[i] = (bf16)(x0[i] - (float)h0);
+    lo[4 + i] = (bf16)(x1[i] - (float)h1);
+  }
+}
 template <int K>
 __device__ __forceinline__ f32x4 tile_nt_split(const float* arow, const float* brow, int g4, bool a_exact,
                                                bool b_exact) {
+  constexpr int NS = K / 32;
+  f32x4 ra[NS][2], rb[NS][2];
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    ra[u][0] = *(const f32x4*)(arow + 32 * u + 4 * g4);
+    ra[u][1] = *(const f32x4*)(arow + 32 * u + 16 + 4 * g4);
+    rb[u][0] = *(const f32x4*)(brow + 32 * u + 4 * g4);
+    rb[u][1] = *(const f32x4*)(brow + 32 * u + 16 + 4 * g4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   f32x4 acc = zero4();
 #pragma unroll
-  for (int kb = 0; kb < K; kb += 32) {
+  for (int u = 0; u < NS; ++u) {
     bf16x8 ah, al, bh, bl;
-    split_frag(arow + kb, g4, ah, al);
-    split_frag(brow + kb, g4, bh, bl);
+    split8(ra[u][0], ra[u][1], ah, al);
+    split8(rb[u][0], rb[u][1], bh, bl);
     mma(acc, ah, bh);
     if (!b_exact) mma(acc, ah, bl);
     if (!a_exact) mma(acc, al, bh);
@@ -154,14 +177,23 @@ __device__ __forceinline__ f32x4 tile_nt_split(const float* arow, const float* b
 // The same with B a raw compute-dtype row: bf16 values are exact (no lo part)
 template <int K>
 __device__ __forceinline__ f32x4 tile_nt_fb(const float* arow, const bf16* brow, int g4, bool a_exact) {
+  constexpr int NS = K / 32;
+  f32x4 ra[NS][2];
+  bf16x8 bh[NS];
+#pragma unroll
+  for (int u = 0; u < NS; ++u) {
+    ra[u][0] = *(const f32x4*)(arow + 32 * u + 4 * g4);
+    ra[u][1] = *(const f32x4*)(arow + 32 * u + 16 + 4 * g4);
+    bh[u] = ld_frag(brow + 32 * u, g4);
+  }
+  __builtin_amdgcn_sched_barrier(0);
   f32x4 acc = zero4();
 #pragma unroll
-  for (int kb = 0; kb < K; kb += 32) {
+  for (int u = 0; u < NS; ++u) {
     bf16x8 ah, al;
-    split_frag(arow + kb, g4, ah, al);
-    const bf16x8 bh = ld_frag(brow + kb, g4);
-    mma(acc, ah, bh);
-    if (!a_exact) mma(acc, al, bh);
+    split8(ra[u][0], ra[u][1], ah, al);
+    mma(acc, ah, bh[u]);
+    if (!a_exact) mma(acc, al, bh[u]);
   }
   return acc;
 }
@@ -711,25 +743,48 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     // Kronecker products G_h = dRhs S_kron, G_q = dY S_kron on this wave's key tiles,
     // and per-token partials h . G_h, q . G_q, dVbd . Vbd
     f32x4 Gh[VPW], Gq[VPW];
+    // bf16 MFMA: S_kron^T is bf16, dY holds bf16 values exactly, dRhs enters as
+    // hi + lo parts; the dRhs and dY fragments are read and split once for
+    // both key tiles, every read ahead of its MFMAs behind a scheduling barrier
+    constexpr int NKB = D / 32;
+    bf16x8 rfh[sizeof(CT) == 2 ? NKB : 1], rfl[sizeof(CT) == 2 ? NKB : 1], yfh[sizeof(CT) == 2 ? NKB : 1];
+    if constexpr (sizeof(CT) == 2) {
+      if (live) {
+        f32x4 xr[NKB][2], xy[NKB][2];
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          xr[kb][0] = *(const f32x4*)&sm.dr[n16][kb * 32 + 4 * g4];
+          xr[kb][1] = *(const f32x4*)&sm.dr[n16][kb * 32 + 16 + 4 * g4];
+          xy[kb][0] = *(const f32x4*)&sm.dy[n16][kb * 32 + 4 * g4];
+          xy[kb][1] = *(const f32x4*)&sm.dy[n16][kb * 32 + 16 + 4 * g4];
+        }
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int kb = 0; kb < NKB; ++kb) {
+          bf16x8 yl;
+          split8(xr[kb][0], xr[kb][1], rfh[kb], rfl[kb]);
+          split8(xy[kb][0], xy[kb][1], yfh[kb], yl);
+        }
+      }
+    }
 #pragma unroll
     for (int a = 0; a < VPW; ++a) {
       const int kt = wave * VPW + a, d = 16 * kt + n16;
       Gh[a] = Gq[a] = zero4();
       if (live) {
         if constexpr (sizeof(CT) == 2) {
-          // bf16 MFMA: S_kron^T is bf16, dY holds bf16 values exactly, dRhs
-          // enters as hi + lo parts
-#pragma unroll 2
-          for (int kb = 0; kb < D / 32; ++kb) {
-            bf16x8 sf;
-            if constexpr (SKL) sf = ld_frag(&sm.skt[d][kb * 32], g4);
-            else sf = skf[a][kb];
-            bf16x8 rh, rl, yh, yl;
-            split_frag(&sm.dr[n16][kb * 32], g4, rh, rl);
-            split_frag(&sm.dy[n16][kb * 32], g4, yh, yl);
-            mma(Gh[a], rh, sf);
-            mma(Gh[a], rl, sf);
-            mma(Gq[a], yh, sf);
+          bf16x8 sf[NKB];
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) {
+            if constexpr (SKL) sf[kb] = ld_frag(&sm.skt[d][kb * 32], g4);
+            else sf[kb] = skf[a][kb];
+          }
+          __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+          for (int kb = 0; kb < NKB; ++kb) {
+            mma(Gh[a], rfh[kb], sf[kb]);
+            mma(Gh[a], rfl[kb], sf[kb]);
+            mma(Gq[a], yfh[kb], sf[kb]);
           }
         } else {
 #pragma unroll 4
