@@ -1097,16 +1097,25 @@ __device__ __forceinline__ void g3_window_step(const G3WinView<CT, D, P>& w, con
     if (live && (committed || wave > 0)) {
       // this workgroup's value tiles over waves 1..3 (wave 0 forms the inverse), or all four
       const int w0 = committed ? wave : wave - 1, ws = committed ? 4 : 3;
+      // the H and Q fragments serve every value tile; each tile's Kronecker
+      // fragments are read ahead of its MFMAs behind a scheduling barrier (the
+      // compiler, short of registers, waited for each MFMA's reads)
+      Frag xf[2][D / KS];
+#pragma unroll
+      for (int rt = 0; rt < 2; ++rt)
+#pragma unroll
+        for (int kb = 0; kb < D / KS; ++kb) xf[rt][kb] = ld_frag(&w.x[rt * 16 + n16][kb * KS], g4);
       for (int l = w0; l < NVTW; l += ws) {
         const int vt = vb * NVTW + l;
         Frag bf[D / KS];
 #pragma unroll
         for (int kb = 0; kb < D / KS; ++kb) bf[kb] = ld_frag(&w.skron[l * 16 + n16][kb * KS], g4);
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int rt = 0; rt < 2; ++rt) {
           f32x4 acc = zero4();
 #pragma unroll
-          for (int kb = 0; kb < D / KS; ++kb) mma(acc, ld_frag(&w.x[rt * 16 + n16][kb * KS], g4), bf[kb]);
+          for (int kb = 0; kb < D / KS; ++kb) mma(acc, xf[rt][kb], bf[kb]);
 #pragma unroll
           for (int s = 0; s < 4; ++s) w.kr[rt * 16 + 4 * g4 + s][vt * 16 + n16] = acc[s];
         }
@@ -1117,33 +1126,62 @@ __device__ __forceinline__ void g3_window_step(const G3WinView<CT, D, P>& w, con
     //   Rhs = alpha u - kco KRh - sum_b Ho_b U_b;  U = T Rhs
     //   Y   = qco KRq + sum_b Qo_b U_b + Aq U
     // (an accumulator tile over rows = tokens is directly a k-fragment)
+    // (every LDS operand read ahead, behind a scheduling barrier; the
+    // coefficient tiles and per-token scalars serve every value tile)
+    f32x4 po0[NB], po1[NB];
+#pragma unroll
+    for (int bl = 0; bl < NB; ++bl) {
+      po0[bl] = *(const f32x4*)&w.po[0][n16][kSC * bl + 4 * g4];
+      po1[bl] = *(const f32x4*)&w.po[1][n16][kSC * bl + 4 * g4];
+    }
+    const f32x4 ptf = *(const f32x4*)&w.pp[2][n16][4 * g4], paf = *(const f32x4*)&w.pp[1][n16][4 * g4];
+    float alv[4], kcv[4], qcv[4], uv[VPW][4], khv[VPW][4], kqv[VPW][4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int i = 4 * g4 + s;
+      alv[s] = w.alpha[i];
+      kcv[s] = w.kco[i];
+      qcv[s] = w.qco[i];
+    }
+#pragma unroll
+    for (int a = 0; a < VPW; ++a)
+      if (vown(a)) {
+        const int v = vtile(a) * 16 + n16;
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {
+          const int i = 4 * g4 + s;
+          uv[a][s] = w.u[i][v];
+          khv[a][s] = w.kr[i][v];
+          kqv[a][s] = w.kr[kSC + i][v];
+        }
+      }
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int a = 0; a < VPW; ++a) {
       if (!vown(a)) continue;
       const int v = vtile(a) * 16 + n16;
       f32x4 acc = zero4();
 #pragma unroll
-      for (int bl = 0; bl < NB; ++bl) mma(acc, *(const f32x4*)&w.po[0][n16][kSC * bl + 4 * g4], uo[bl][a]);
+      for (int bl = 0; bl < NB; ++bl) mma(acc, po0[bl], uo[bl][a]);
       f32x4 rhs;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
-        const int i = 4 * g4 + s;
-        float r = w.alpha[i] * w.u[i][v] - acc[s];
-        if (live) r -= w.kco[i] * w.kr[i][v];
+        float r = alv[s] * uv[a][s] - acc[s];
+        if (live) r -= kcv[s] * khv[a][s];
         rhs[s] = r;
       }
       f32x4 un = zero4();
-      mma(un, *(const f32x4*)&w.pp[2][n16][4 * g4], rhs);
+      mma(un, ptf, rhs);
       f32x4 yv = zero4();
 #pragma unroll
-      for (int bl = 0; bl < NB; ++bl) mma(yv, *(const f32x4*)&w.po[1][n16][kSC * bl + 4 * g4], uo[bl][a]);
-      mma(yv, *(const f32x4*)&w.pp[1][n16][4 * g4], un);
+      for (int bl = 0; bl < NB; ++bl) mma(yv, po1[bl], uo[bl][a]);
+      mma(yv, paf, un);
       CT* yp = (CT*)p.y + tk.y_base + v;
 #pragma unroll
       for (int s = 0; s < 4; ++s) {
         const int i = 4 * g4 + s;
         float out = yv[s];
-        if (live) out += w.qco[i] * w.kr[kSC + i][v];
+        if (live) out += qcv[s] * kqv[a][s];
         const int t = c * kSC + i - p.t0;
         if (t >= 0 && t < T) yp[(size_t)t * tk.y_tok] = from_f<CT>(out);
       }
