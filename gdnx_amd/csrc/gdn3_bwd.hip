@@ -924,36 +924,65 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
 
     // ---- G: dH, dQ, dK on this wave's key tiles; the blocks' dVbd ----
     float dbs[4] = {0.f, 0.f, 0.f, 0.f};   // per-token partial k . dh (scalar erase gates)
+    // every LDS operand read ahead of the MFMAs, behind a scheduling barrier
+    // (the compiler, short of registers, waited for each MFMA's reads); the
+    // coefficient fragments and per-token scalars serve both key tiles
+    const f32x4 fw = ld_frag(&sm.w[n16][0], g4), fz = ld_frag(&sm.z[n16][0], g4);
+    const f32x4 fwt = ld_frag(&sm.wt[n16][0], g4), fzt = ld_frag(&sm.zt[n16][0], g4);
+    f32x4 fvv[NB], fwq[NB], vvt[NB], wqt[NB];
+#pragma unroll
+    for (int bl = 0; bl < NB; ++bl) {
+      fvv[bl] = ld_frag(&sm.vv[bl][n16][0], g4);
+      fwq[bl] = ld_frag(&sm.wq[bl][n16][0], g4);
+#pragma unroll
+      for (int s = 0; s < 4; ++s) {
+        vvt[bl][s] = sm.vv[bl][4 * g4 + s][n16];
+        wqt[bl][s] = sm.wq[bl][4 * g4 + s][n16];
+      }
+    }
+    float dcv[4], kcv[4], qcv[4], vsv[4], bsv[4];
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int i = 4 * g4 + s;
+      dcv[s] = sm.dc[i];
+      kcv[s] = sm.kco[i];
+      qcv[s] = sm.qco[i];
+      vsv[s] = sm.vsc[i];
+      bsv[s] = sm.bsc[i];
+    }
+    f32x4 Kcv[VPW], Hcv[VPW], Qcv[VPW], Vcv[VPW][NB];
 #pragma unroll
     for (int a = 0; a < VPW; ++a) {
       const int d = 16 * (wave * VPW + a) + n16;
-      const f32x4 Kc = col_frag<LR>(sm.k, d, g4), Hc = col_frag<LR>(sm.h, d, g4);
-      const f32x4 Qc = col_frag<LR>(sm.q, d, g4);
+      Kcv[a] = col_frag<LR>(sm.k, d, g4);
+      Hcv[a] = col_frag<LR>(sm.h, d, g4);
+      Qcv[a] = col_frag<LR>(sm.q, d, g4);
+#pragma unroll
+      for (int bl = 0; bl < NB; ++bl)
+#pragma unroll
+        for (int s = 0; s < 4; ++s) {   // the block's keys decayed to the start of this sub-chunk (k = slot)
+          const int sl = BP * bl + 4 * g4 + s;
+          Vcv[a][bl][s] = (float)sm.kb[sl][d] * sm.kd[sl];
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int a = 0; a < VPW; ++a) {
+      const int d = 16 * (wave * VPW + a) + n16;
+      const f32x4 Kc = Kcv[a], Hc = Hcv[a], Qc = Qcv[a];
       f32x4 dH = zero4(), dQ = zero4(), dK = zero4();
-      mma(dH, ld_frag(&sm.w[n16][0], g4), Kc);
-      mma(dQ, ld_frag(&sm.z[n16][0], g4), Kc);
-      mma(dK, ld_frag(&sm.wt[n16][0], g4), Hc);
-      mma(dK, ld_frag(&sm.zt[n16][0], g4), Qc);
+      mma(dH, fw, Kc);
+      mma(dQ, fz, Kc);
+      mma(dK, fwt, Hc);
+      mma(dK, fzt, Qc);
 #pragma unroll
       for (int bl = 0; bl < NB; ++bl) {
-        // the block's keys decayed to the start of this sub-chunk (k = slot)
-        f32x4 Vc;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          const int sl = BP * bl + 4 * g4 + s;
-          Vc[s] = (float)sm.kb[sl][d] * sm.kd[sl];
-        }
-        mma(dH, ld_frag(&sm.vv[bl][n16][0], g4), Vc);
-        mma(dQ, ld_frag(&sm.wq[bl][n16][0], g4), Vc);
+        mma(dH, fvv[bl], Vcv[a][bl]);
+        mma(dQ, fwq[bl], Vcv[a][bl]);
         // d/dVbd_b = dHo_b^T H + dQo_b^T Q (A operand: the transposes, read by column)
-        f32x4 dVo = zero4(), vvt, wqt;
-#pragma unroll
-        for (int s = 0; s < 4; ++s) {
-          vvt[s] = sm.vv[bl][4 * g4 + s][n16];
-          wqt[s] = sm.wq[bl][4 * g4 + s][n16];
-        }
-        mma(dVo, vvt, Hc);
-        mma(dVo, wqt, Qc);
+        f32x4 dVo = zero4();
+        mma(dVo, vvt[bl], Hc);
+        mma(dVo, wqt[bl], Qc);
         dVa[bl][a] = (bl == beta) ? dVo : egl * dVa[bl][a] + dVo;
       }
       float dbp[4];
@@ -961,12 +990,12 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
       for (int s = 0; s < 4; ++s) {
         const int i = 4 * g4 + s, tt_ = c * BP + i;
         const bool ok = tt_ < T;
-        const float dci = sm.dc[i];
+        const float dci = dcv[s];
         float dh = dH[s] + dci * Kc[s];
-        if (live) dh -= sm.kco[i] * Gh[a][s];
-        const float dq = dQ[s] + (live ? sm.qco[i] * Gq[a][s] : 0.f);
-        const float bgv = gc > 1 ? bgc[a][s] : sm.bsc[i];
-        const float dk = dK[s] + dci * Hc[s] + dVc[a][s] * sm.vsc[i] + bgv * dh;
+        if (live) dh -= kcv[s] * Gh[a][s];
+        const float dq = dQ[s] + (live ? qcv[s] * Gq[a][s] : 0.f);
+        const float bgv = gc > 1 ? bgc[a][s] : bsv[s];
+        const float dk = dK[s] + dci * Hc[s] + dVc[a][s] * vsv[s] + bgv * dh;
         dbp[s] = Kc[s] * dh;
         dbs[s] += dbp[s];
         if (ok) {
