@@ -1791,14 +1791,17 @@ __device__ __forceinline__ void write_skron(CT* sk, const float* Af, const float
     ao[u] = Bf[g * Ge::n + q0 + l16];
     bo[u] = Af[g * Ge::m + p0 + l16];
   }
+  // and every MFMA issued before the first store
+  __builtin_amdgcn_sched_barrier(0);
+  f32x4 acc[NT / 4];
+#pragma unroll
+  for (int u = 0; u < NT / 4; ++u) acc[u] = __builtin_amdgcn_mfma_f32_16x16x4f32(ao[u], bo[u], zero4(), 0, 0, 0);
 #pragma unroll
   for (int u = 0; u < NT / 4; ++u) {
     const int t = wave + 4 * u, q0 = (t % QT) * 16, p0 = (t / QT) * 16;
-    f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(ao[u], bo[u], acc, 0, 0, 0);
     const int p = p0 + l16, q = q0 + 4 * g;
     const int iv = p / Ge::ak, ik = p % Ge::ak, jv = q / Ge::bk, jk = q % Ge::bk;
-    st4(sk + (size_t)(iv * Ge::bv + jv) * ld + ik * Ge::bk + jk, acc[0], acc[1], acc[2], acc[3]);
+    st4(sk + (size_t)(iv * Ge::bv + jv) * ld + ik * Ge::bk + jk, acc[u][0], acc[u][1], acc[u][2], acc[u][3]);
   }
 }
 
