@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(_HERE, "libgdnx.so")
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_F64 = 2      # gdnx_check_finite only
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _c_int, _c_ll, _vp, _c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_float
 
@@ -32,6 +32,7 @@ SIGNATURES = {
     "gdnx_delta_chunk_size": (_c_int, [_c_int, _c_int]),
     "gdnx_delta_train_chunk_size": (_c_int, [_c_int, _c_int]),
     "gdnx_delta_chunk_states_bytes": (_c_ll, [_c_int] * 7),
+    "gdnx_delta_bwd_workspace_bytes": (_c_ll, [_c_int] * 7),
     "gdnx_delta_chunk_fwd": (_c_int, [_vp] * 11 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_chunk_fwd_scored": (_c_int, [_vp] * 12 + [_c_int] * 7 + [_vp]),
     "gdnx_delta_fwd_workspace_bytes": (_c_ll, [_c_int] * 7),

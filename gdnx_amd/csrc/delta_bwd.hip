@@ -597,6 +597,7 @@ static int launch_bwd(const DeltaBwdArgs& a, int stages, hipStream_t stream) {
     const int rc = delta_scan_bwd_dispatch(a, stream);
     if (rc) return rc;
   }
+  if ((stages & 2) && a.cps > 1) return delta_grad_seg_dispatch(a, stream);   // checkpointed stash
   if (stages & 2) {
     constexpr int KH = GradDims<CT, D, C>::KH;
     hipLaunchKernelGGL((delta_bwd_grads_kernel<CT, D, C>), dim3(a.B * a.H * NC * KH), dim3(GradDims<CT, D, C>::NT),

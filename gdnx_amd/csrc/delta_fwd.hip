@@ -170,8 +170,8 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
 #pragma unroll
       for (int vt = 0; vt < NVT; ++vt)
         Sf[kb][vt] = acc_frag((CT*)nullptr, S[kb * TPS][vt], S[kb * TPS + TPS - 1][vt]);
-    if (p.chunk_states) {  // stash S0 for the backward (raw tiles)
-      CT* cst = (CT*)p.chunk_states + rec_index(chain, c, nchains) * (D * D);
+    if (p.chunk_states && c % p.cps == 0) {  // stash S0 for the backward (raw tiles), every cps-th chunk
+      CT* cst = (CT*)p.chunk_states + ((size_t)(c / p.cps) * nchains + chain) * (D * D);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
@@ -192,7 +192,8 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) delta_fwd_kernel(DeltaAr
       }
     }
     if (p.chunk_states) {  // stash R after all states: raw accumulator tiles (stash_tiles layout)
-      CT* rst = (CT*)p.chunk_states + (size_t)nchains * NC * D * D + rec_index(chain, c, nchains) * (C * D);
+      CT* rst = (CT*)p.chunk_states + stash_geom(nchains, p.T, D, C, p.cps).states +
+                rec_index(chain, c, nchains) * (C * D);
 #pragma unroll
       for (int it = 0; it < NCT; ++it)
 #pragma unroll
@@ -326,7 +327,8 @@ static int delta_fused_dispatch(const DeltaArgs& a, hipStream_t stream) {
 // prep records, which the reverse scan reads.
 int delta_fwd_dispatch(const DeltaArgs& a, hipStream_t stream) {
   DeltaArgs b = a;
-  if (a.chunk_states) b.prep = (char*)a.chunk_states + delta_stash_bytes(a.B * a.H * a.M, a.T, a.D, a.C, a.dtype);
+  if (a.chunk_states)
+    b.prep = (char*)a.chunk_states + delta_stash_bytes(a.B * a.H * a.M, a.T, a.D, a.C, a.dtype, a.cps);
   if (b.prep && !a.r_norm) {
     const int rc = delta_prep_dispatch(b, stream);
     return rc ? rc : delta_scan_fwd_dispatch(b, stream);

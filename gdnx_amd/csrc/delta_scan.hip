@@ -87,6 +87,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
   const size_t rs = (size_t)p.H * D;
   const size_t qoff = ((size_t)b * p.T * p.H + h) * D;
   const size_t NR = (size_t)nchains * NC;
+  const StashGeom sg = stash_geom(nchains, p.T, D, C, p.cps);
   // record of chunk c: rec_index(chain, c, nchains)
   const PrepPtrs<CT> pp = prep_ptrs<CT>(p.prep, NR, C);
   const CT* qg = (const CT*)p.q + qoff;
@@ -171,10 +172,16 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
     for (int kb = 0; kb < NDT / TPS; ++kb) Sf[kb] = acc_frag((CT*)nullptr, S[kb * TPS], S[kb * TPS + TPS - 1]);
     if constexpr (STASH) {
-      CT* cst = (CT*)p.chunk_states + rec * (D * D);
+      // the state entering every cps-th chunk (record c / cps); at other
+      // chunks the stores go through an empty buffer range and are dropped,
+      // so the loop carries no branch around a store
+      const size_t srec = (size_t)(c / p.cps) * nchains + chain;
+      const __amdgpu_buffer_rsrc_t sr =
+          buf_rsrc((CT*)p.chunk_states + srec * (D * D), c % p.cps == 0 ? (unsigned)(D * D * sizeof(CT)) : 0u);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
-        st4(cst + stash_tile_offset<CT, D>(dt, V, lane), S[dt][0], S[dt][1], S[dt][2], S[dt][3]);
+        buf_store4(sr, (unsigned)(stash_tile_offset<CT, D>(dt, V, lane) * sizeof(CT)), (const CT*)nullptr, S[dt][0],
+                   S[dt][1], S[dt][2], S[dt][3]);
     }
 
     // ---- X = diag(a_w) V - diag(aeg) (K S0) on this wave's columns ----
@@ -223,7 +230,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
       }
     }
     if constexpr (STASH) {
-      CT* rst = (CT*)p.chunk_states + NR * D * D + rec * (C * D);
+      CT* rst = (CT*)p.chunk_states + sg.states + rec * (C * D);
 #pragma unroll
       for (int it = 0; it < NCT; ++it)
         st4(rst + stash_tile_offset<CT, D>(it, V, lane), Racc[it][0], Racc[it][1], Racc[it][2], Racc[it][3]);
@@ -304,9 +311,10 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
   const size_t rsy = (size_t)p.H * p.M * D;
   const size_t yoff = (((size_t)b * p.T * p.H + h) * p.M + m) * D + vb * BV;
   const size_t NR = (size_t)nchains * NC;
+  const StashGeom sg = stash_geom(nchains, p.T, D, C, p.cps);
   // record of chunk c: rec_index(chain, c, nchains)
   // the forward's prep records sit after its state and net-write stashes
-  const PrepPtrs<CT> pp = prep_ptrs<CT>((CT*)p.s_stash + NR * ((size_t)D * D + (size_t)C * D), NR, C);
+  const PrepPtrs<CT> pp = prep_ptrs<CT>((CT*)p.s_stash + sg.states + sg.tiles, NR, C);
   const CT* qg = (const CT*)p.q + qoff;
   const CT* kg = (const CT*)p.k + qoff;
   const CT* yg = (const CT*)p.dy + yoff;
@@ -383,10 +391,16 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
     for (int kb = 0; kb < NDT / TPS; ++kb) dSf[kb] = acc_frag((CT*)nullptr, dS[kb * TPS], dS[kb * TPS + TPS - 1]);
     {
-      CT* cst = (CT*)p.ds_stash + rec * (D * D);
+      // the state gradient leaving every cps-th chunk and the last one
+      // (record c / cps); other chunks' stores are dropped (empty range)
+      const size_t srec = (size_t)(c / p.cps) * nchains + chain;
+      const bool keep = c % p.cps == p.cps - 1 || c == NC - 1;
+      const __amdgpu_buffer_rsrc_t sr =
+          buf_rsrc((CT*)p.ds_stash + srec * (D * D), keep ? (unsigned)(D * D * sizeof(CT)) : 0u);
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
-        st4(cst + stash_tile_offset<CT, D>(dt, V, lane), dS[dt][0], dS[dt][1], dS[dt][2], dS[dt][3]);
+        buf_store4(sr, (unsigned)(stash_tile_offset<CT, D>(dt, V, lane) * sizeof(CT)), (const CT*)nullptr, dS[dt][0],
+                   dS[dt][1], dS[dt][2], dS[dt][3]);
     }
     // ---- dR = diag(dec) K dS + Aq^T dY ----
     Frag dYf[C / KS];
@@ -416,7 +430,7 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
 #pragma unroll
         for (int kb = 0; kb < NCT / TPS; ++kb) mma(dB[it], ld_frag(&sb.tt[(it * 16 + n16) * LDC + kb * KS], g4), dRf[kb]);
       }
-      CT* bst = (CT*)p.ds_stash + NR * D * D + rec * (C * D);
+      CT* bst = (CT*)p.ds_stash + sg.states + rec * (C * D);
 #pragma unroll
       for (int it = 0; it < NCT; ++it)
         st4(bst + stash_tile_offset<CT, D>(it, V, lane), dB[it][0], dB[it][1], dB[it][2], dB[it][3]);

@@ -10,10 +10,16 @@
 // NaN or infinite; gdnx_check_finite scans one buffer on demand.  Off (the
 // default), nothing is added to the launch sequence.
 //
-// The flag the scans set is a per-device word in static device memory,
-// reached through the address hipGetSymbolAddress returns for the current
-// device; a lane that finds a non-finite value stores 1 there (a vector store
-// from a divergent branch: concurrent writers all store the same value).
+// The flags the scans set are words of a per-device array in static device
+// memory, reached through the address hipGetSymbolAddress returns for the
+// current device.  Each checked call holds a word of its own from clear to
+// read-back (taken from a free list, returned after its stream has
+// synchronised), so calls on different streams or threads do not share one;
+// at most kFlagWords checked calls may be in flight per device.  A lane that
+// finds a non-finite value stores 1 in the call's word (a vector store from a
+// divergent branch: concurrent writers all store the same value).  The check
+// reads the flag back and synchronises the stream, which a stream under HIP
+// graph capture cannot do: a checked call on a capturing stream is refused.
 #include <atomic>
 #include <mutex>
 
@@ -22,13 +28,15 @@
 
 namespace gdnx {
 
-static __device__ __align__(256) unsigned nonfinite_flag[64];
+constexpr int kFlagWords = 64;
+static __device__ __align__(256) unsigned nonfinite_flag[kFlagWords];
 
 namespace {
 std::atomic<int> g_check_on{0};
 std::mutex g_flag_mu;
 constexpr int kMaxDevices = 64;
 unsigned* g_flag_ptr[kMaxDevices] = {};
+unsigned long long g_flag_busy[kMaxDevices] = {};   // bit w: word w held by a call in flight
 
 __global__ void flag_clear_kernel(unsigned* flag) {
   if (threadIdx.x == 0) flag[0] = 0u;   // lane 0 only: a vector store
@@ -43,7 +51,7 @@ __device__ __forceinline__ bool finite_of<double>(double x) {
   return isfinite(x);
 }
 
-// any non-finite element of x[0, n) sets flag[0]
+// any non-finite element of x[0, n) sets *flag
 template <typename T>
 __global__ void __launch_bounds__(256) finite_scan_kernel(const T* __restrict__ x, long long n, unsigned* flag) {
   bool bad = false;
@@ -52,7 +60,9 @@ __global__ void __launch_bounds__(256) finite_scan_kernel(const T* __restrict__ 
   if (bad) flag[0] = 1u;
 }
 
-int flag_ptr(unsigned** out) {
+// a free flag word of the current device for one call: *out its address,
+// *dev_out / *word_out to hand back with flag_release
+int flag_acquire(unsigned** out, int* dev_out, int* word_out) {
   int dev = -1;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= kMaxDevices)
     return set_error(GDNX_ERR_HIP, "no current HIP device (or device index >= %d)", kMaxDevices);
@@ -63,17 +73,48 @@ int flag_ptr(unsigned** out) {
     if (e != hipSuccess || !p) return set_error(GDNX_ERR_HIP, "non-finite flag address: %s", hipGetErrorString(e));
     g_flag_ptr[dev] = (unsigned*)p;
   }
-  *out = g_flag_ptr[dev];
-  return GDNX_OK;
+  for (int w = 0; w < kFlagWords; ++w) {
+    if (!(g_flag_busy[dev] >> w & 1ull)) {
+      g_flag_busy[dev] |= 1ull << w;
+      *out = g_flag_ptr[dev] + w;
+      *dev_out = dev;
+      *word_out = w;
+      return GDNX_OK;
+    }
+  }
+  return set_error(GDNX_ERR_HIP, "non-finite check: more than %d checked calls in flight on device %d",
+                   kFlagWords, dev);
+}
+
+void flag_release(int dev, int word) {
+  std::lock_guard<std::mutex> lock(g_flag_mu);
+  g_flag_busy[dev] &= ~(1ull << word);
 }
 }  // namespace
 
 bool check_finite_on() { return g_check_on.load(std::memory_order_relaxed) != 0; }
 
+static int finite_check_word(const FiniteBuf* bufs, int nbuf, hipStream_t stream, unsigned* flag);
+
 int finite_check(const FiniteBuf* bufs, int nbuf, hipStream_t stream) {
   unsigned* flag = nullptr;
-  int rc = flag_ptr(&flag);
+  int dev = 0, word = 0;
+  int rc = flag_acquire(&flag, &dev, &word);
   if (rc) return rc;
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(stream, &cap) != hipSuccess)
+    rc = set_error(GDNX_ERR_HIP, "non-finite check: cannot query the stream's capture status on device %d", dev);
+  else if (cap != hipStreamCaptureStatusNone)
+    rc = set_error(GDNX_ERR_ARG, "non-finite checking synchronises the stream and cannot run under graph "
+                   "capture: turn it off (gdnx_set_check_finite(0)) while capturing");
+  else
+    rc = finite_check_word(bufs, nbuf, stream, flag);
+  flag_release(dev, word);
+  return rc;
+}
+
+static int finite_check_word(const FiniteBuf* bufs, int nbuf, hipStream_t stream, unsigned* flag) {
+  int rc;
   hipLaunchKernelGGL(flag_clear_kernel, dim3(1), dim3(64), 0, stream, flag);
   if ((rc = check_launch("flag_clear_kernel"))) return rc;
   for (int i = 0; i < nbuf; ++i) {

@@ -1953,7 +1953,8 @@ __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
   int chain = blockIdx.x;
   if (p.pos) {   // decode batch: only the rows whose token closes a compaction interval
     const int row = blockIdx.x / p.hm;
-    if ((p.pos[row] + 1) % p.Kc != 0) return;
+    const int pos = p.pos[row];
+    if (pos < 0 || (pos + 1) % p.Kc != 0) return;   // (a negative position is an empty row)
     if (p.slots) {
       const int sl = p.slots[row];
       if (sl < 0 || sl >= p.nslots) return;
@@ -2319,6 +2320,14 @@ size_t gdn3_train_states_bytes(int N, int T, int D, int P, int Kc) {
   const int nch = (T + kSC - 1) / kSC, ncomp = T / Kc;
   const int rmn = D == 128 ? G3D<128>::RMN : G3D<64>::RMN;
   return g3_stash_bytes(N, nch, ncomp, D, kSC, rmn);
+}
+
+// whether run_gdn3_fwd runs the call as one fused launch, which uses no
+// workspace (the layer's default regime, a compaction after every window)
+bool gdn3_fwd_fused(int D, int P, int Kc, int dtype) {
+  if (P != kSC || Kc != kSC) return false;
+  if (dtype == GDNX_DTYPE_BF16) return D == 128 ? fused_fits<bf16, 128>() : D == 64 && fused_fits<bf16, 64>();
+  return D == 128 ? fused_fits<float, 128>() : D == 64 && fused_fits<float, 64>();
 }
 
 int gdn3_fwd_dispatch(const G3FwdArgs& a, hipStream_t stream) {

@@ -59,12 +59,15 @@ __global__ void __launch_bounds__(kDT) gdn3_decode_kernel(G3DecArgs p) {
   const int sl = p.slots ? p.slots[row] : row;
   IO* yg = (IO*)p.y + (size_t)chain * D;
   if (p.stats && tid < 2) p.stats[(size_t)chain * 2 + tid] = 0.0;
-  if (sl < 0 || sl >= p.nslots) {               // an empty row: zero output, no state touched
+  const int pos = p.pos[row];
+  // an empty row (slot outside the pool, or a negative position, which has
+  // no residual slot): zero output, no state touched
+  if (sl < 0 || sl >= p.nslots || pos < 0) {
     for (int d = tid; d < D; d += kDT) yg[d] = from_f<IO>(0.f);
     return;
   }
   const size_t sidx = (size_t)sl * hm + ch;
-  const int slot = p.pos[row] % P;
+  const int slot = pos % P;
   float* Ag = p.A + sidx * RM;
   float* Bg = p.Bf + sidx * RN;
   float* Ug = p.U + sidx * DP;

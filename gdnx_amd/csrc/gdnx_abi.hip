@@ -29,13 +29,27 @@ int delta_chunk_size(int D, int dtype) {
   return dtype == GDNX_DTYPE_BF16 ? 64 : 32;
 }
 
-// chunk used when the forward stashes states for the backward: 32 for bf16,
-// 16 for float32.  A 64-token bf16 chunk halves the state stashes but ran
-// the config-2 step 40 % slower (the scans and the gradient kernel are bound
-// by the latency of a chunk's work, not by its bytes); it stays selectable.
+// chunk used when the forward stashes states for the backward: 32 for bf16
+// (with at most 4 lanes per head the stash keeps one state per 256-token
+// segment and the backward recomputes the rest), 16 for float32.  The
+// 64-token bf16 chunk, also checkpointed, stays selectable: its scans hold
+// one chunk's tiles in LDS instead of two (no overlap of the next chunk's
+// staging) and measured 1.5-2x slower on the config-2 step.
 int delta_train_chunk_size(int D, int dtype) {
   if (D != 64 && D != 128) return 0;
   return dtype == GDNX_DTYPE_BF16 ? 32 : 16;
+}
+
+size_t delta_bwd_workspace_bytes(int B, int T, int H, int M, int D, int C, int dtype) {
+  const int cps = delta_stash_cps(D, C, dtype, M);
+  size_t n = delta_stash_bytes(B * H * M, T, D, C, dtype, cps);
+  if (cps > 1) {
+    const size_t nseg = (size_t)((T + kSegTokens - 1) / kSegTokens);
+    n = (n + 255) / 256 * 256 + 3 * (size_t)B * H * nseg * kSegTokens * D * sizeof(float);
+  } else if (dtype == GDNX_DTYPE_BF16 && C == 64) {
+    n += 2 * 3 * (size_t)B * T * H * M * sizeof(float);   // the two key halves' per-token partials
+  }
+  return n;
 }
 
 static bool valid_chunk(int D, int dtype, int C) {
@@ -82,7 +96,18 @@ extern "C" long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, i
   if (C == 0 || !valid_chunk(head_dim, dtype, C) || B < 1 || T < 0 || H < 1 || M < 1 ||
       (head_dim != 64 && head_dim != 128))
     return -1;
-  return (long long)(delta_stash_bytes(B * H * M, T, head_dim, C, dtype) + delta_prep_bytes(B * H * M, T, C, dtype));
+  const int cps = delta_stash_cps(head_dim, C, dtype, M);
+  return (long long)(delta_stash_bytes(B * H * M, T, head_dim, C, dtype, cps) +
+                     delta_prep_bytes(B * H * M, T, C, dtype));
+}
+
+extern "C" long long gdnx_delta_bwd_workspace_bytes(int B, int T, int H, int M, int head_dim, int chunk,
+                                                    int dtype) {
+  const int C = chunk ? chunk : delta_train_chunk_size(head_dim, dtype);
+  if (C == 0 || !valid_chunk(head_dim, dtype, C) || B < 1 || T < 0 || H < 1 || M < 1 ||
+      (head_dim != 64 && head_dim != 128))
+    return -1;
+  return (long long)delta_bwd_workspace_bytes(B, T, H, M, head_dim, C, dtype);
 }
 
 static int fwd_common(const void* q, const void* k, const void* v, const float* a_e, const float* a_w,
@@ -100,7 +125,7 @@ static int fwd_common(const void* q, const void* k, const void* v, const float* 
   if (!valid_chunk(head_dim, dtype, C)) return set_error(GDNX_ERR_SHAPE, "chunk %d invalid for this dtype", chunk);
   if (T == 0) return GDNX_OK;
   DeltaArgs a{q, k, v, a_e, a_w, log_g, state0, y, state_out, chunk_states, B, T, H, M, head_dim, C, dtype,
-              r_norm, workspace};
+              r_norm, workspace, delta_stash_cps(head_dim, C, dtype, M)};
   if ((rc = delta_fwd_dispatch(a, (hipStream_t)stream))) return rc;
   const size_t rows = (size_t)B * T * H * M, D = head_dim;
   const FiniteBuf outs[] = {{y, rows * D, dtype}, {state_out, (size_t)B * H * M * D * D, GDNX_DTYPE_F32},
@@ -130,7 +155,7 @@ extern "C" int gdnx_delta_chunk_prep(const void* q, const void* k, const float* 
   if (!valid_chunk(head_dim, dtype, C)) return set_error(GDNX_ERR_SHAPE, "chunk %d invalid for this dtype", chunk);
   if (T == 0) return GDNX_OK;
   DeltaArgs a{q, k, nullptr, a_e, a_w, log_g, nullptr, nullptr, nullptr, nullptr, B, T, H, M, head_dim, C, dtype,
-              nullptr, workspace};
+              nullptr, workspace, 1};
   return delta_prep_dispatch(a, (hipStream_t)stream);
 }
 
@@ -171,7 +196,8 @@ static int bwd_common(const void* q, const void* k, const void* v, const float* 
   if (!valid_chunk(head_dim, dtype, C)) return set_error(GDNX_ERR_SHAPE, "chunk %d invalid for this dtype", chunk);
   if (T == 0) return GDNX_OK;
   DeltaBwdArgs a{q,  k,  v,  a_e,  a_w,  log_g, dy,      dstate_out, chunk_states, workspace, dq, dk,
-                 dv, da_e, da_w, dlog_g, dstate0, B, T, H, M, head_dim, C, dtype};
+                 dv, da_e, da_w, dlog_g, dstate0, B, T, H, M, head_dim, C, dtype,
+                 delta_stash_cps(head_dim, C, dtype, M)};
   if ((rc = delta_bwd_dispatch(a, stages, (hipStream_t)stream))) return rc;
   const size_t rows = (size_t)B * T * H * M, D = head_dim, tok = (size_t)B * T * H * D;
   const bool g = (stages & 2) != 0;
@@ -204,11 +230,11 @@ extern "C" int gdnx_delta_chunk_bwd_state(const void* q, const void* k, const fl
 
 extern "C" int gdnx_delta_chunk_bwd_grads(const void* q, const void* k, const void* v, const float* a_e,
                                           const float* a_w, const float* log_g, const void* dy,
-                                          const void* chunk_states, const void* workspace, void* dq,
+                                          const void* chunk_states, void* workspace, void* dq,
                                           void* dk, void* dv, float* da_e, float* da_w, float* dlog_g,
                                           int B, int T, int H, int M, int head_dim, int chunk, int dtype,
                                           void* stream) {
-  return bwd_common(q, k, v, a_e, a_w, log_g, dy, nullptr, chunk_states, (void*)workspace, dq, dk, dv,
+  return bwd_common(q, k, v, a_e, a_w, log_g, dy, nullptr, chunk_states, workspace, dq, dk, dv,
                     da_e, da_w, dlog_g, nullptr, B, T, H, M, head_dim, chunk, dtype, 2, stream);
 }
 
@@ -528,7 +554,9 @@ extern "C" int gdnx_gdn3_chunk_fwd_state_noalloc(const void* q, const void* k, c
                        b_v, b_k, slow_decay, dtype, compact_mode, /*need_workspace=*/false);
   if (rc) return rc;
   if ((rc = g3_state_check(A0, B0, U0, Vb0, t0, T))) return rc;
-  const size_t need = gdn3_workspace_bytes(B * H * M, head_dim, P, dtype);
+  // (the layer's default regime runs as one fused launch and needs no scratch)
+  const size_t need = gdn3_fwd_fused(head_dim, P, compact_every, dtype)
+                          ? 0 : gdn3_workspace_bytes(B * H * M, head_dim, P, dtype);
   if (need > kG3ScratchBytes)
     return set_error(GDNX_ERR_WORKSPACE,
                      "gdn3 no-alloc forward: %d chains need %zu bytes of scratch; the library's static scratch "

@@ -20,6 +20,7 @@ struct DeltaArgs {
   int B, T, H, M, D, C, dtype;
   float* r_norm;  // [B,T,H,M] |net write| per token, or null
   void* prep;     // per-chunk operand records (delta_prep_kernel), or null
+  int cps;        // chunks per stashed state record (delta_stash_cps)
 };
 
 struct DeltaBwdArgs {
@@ -41,6 +42,7 @@ struct DeltaBwdArgs {
   float* dg;
   float* ds0;
   int B, T, H, M, D, C, dtype;
+  int cps;                // chunks per stashed state record (delta_stash_cps)
 };
 
 struct GCoeffArgs {
@@ -305,6 +307,7 @@ struct G3EpiArgs {
 };
 
 int gdn3_fwd_dispatch(const G3FwdArgs& a, hipStream_t stream);
+bool gdn3_fwd_fused(int D, int P, int Kc, int dtype);
 // bytes of the static scratch of gdnx_gdn3_chunk_fwd_state_noalloc (per device)
 constexpr size_t kG3ScratchBytes = (size_t)64 << 20;
 // that scratch's address on the current device (resolved once per device)
@@ -323,12 +326,48 @@ int delta_prep_dispatch(const DeltaArgs& a, hipStream_t stream);
 int delta_scan_fwd_dispatch(const DeltaArgs& a, hipStream_t stream);
 int delta_scan_bwd_dispatch(const DeltaBwdArgs& a, hipStream_t stream);
 size_t delta_prep_bytes(int nchains, int T, int C, int dtype);
-// bytes of the state + net-write stash (the prep records follow it in chunk_states)
-inline size_t delta_stash_bytes(int nchains, int T, int D, int C, int dtype) {
-  const size_t NR = (size_t)nchains * ((T + C - 1) / C);
-  return NR * ((size_t)D * D + (size_t)C * D) * (dtype == GDNX_DTYPE_BF16 ? 2 : 4);
+// Tokens per recompute segment of the checkpointed backward: the forward
+// keeps the state entering every segment, the reverse scan the state
+// gradient leaving it, and the gradient kernel rebuilds the states and state
+// gradients in between.
+constexpr int kSegTokens = 256;
+// Chunks per stashed state record: 1 (the state entering every chunk and the
+// state gradient leaving it, read by delta_bwd_grads_kernel) or, for bf16 IO
+// with at most 4 lanes per head, one record per kSegTokens-token segment
+// (read by delta_grad_seg_kernel, which recomputes the rest).
+__host__ __device__ inline int delta_stash_cps(int D, int C, int dtype, int M) {
+  return (dtype == GDNX_DTYPE_BF16 && (C == 32 || C == 64) && M >= 1 && M <= 4 && (D == 64 || D == 128))
+             ? kSegTokens / C : 1;
 }
+// Per-chain stash geometry: NC chunks; a state record every cps chunks.
+struct StashGeom {
+  size_t nsrec;   // state records (ceil(NC / cps) per chain)
+  size_t nrec;    // chunk records (NC per chain)
+  size_t states;  // compute-dtype elements of the state region (nsrec D^2)
+  size_t tiles;   // compute-dtype elements of the tile region (R or dB: nrec C D)
+};
+__host__ __device__ inline StashGeom stash_geom(int nchains, int T, int D, int C, int cps) {
+  const size_t NC = (size_t)((T + C - 1) / C);
+  StashGeom g;
+  g.nsrec = (size_t)nchains * ((NC + cps - 1) / cps);
+  g.nrec = (size_t)nchains * NC;
+  g.states = g.nsrec * D * D;
+  g.tiles = g.nrec * C * D;
+  return g;
+}
+// bytes of the state + net-write stash (the prep records follow it in chunk_states)
+inline size_t delta_stash_bytes(int nchains, int T, int D, int C, int dtype, int cps) {
+  const StashGeom g = stash_geom(nchains, T, D, C, cps);
+  return (g.states + g.tiles) * (dtype == GDNX_DTYPE_BF16 ? 2 : 4);
+}
+// bytes of the backward's workspace: state gradients and dB like the
+// forward's stash, then (checkpointed form) the gradient kernel's float32
+// dq / dk / dv sums, [B, H, segments][3][kSegTokens][D], or (64-token
+// chunks in the per-chunk form) the key halves' per-token partials
+size_t delta_bwd_workspace_bytes(int B, int T, int H, int M, int D, int C, int dtype);
 int delta_bwd_dispatch(const DeltaBwdArgs& a, int stages, hipStream_t stream);
+// the gradient kernel of the checkpointed form (a.cps > 1, delta_grad_seg.hip)
+int delta_grad_seg_dispatch(const DeltaBwdArgs& a, hipStream_t stream);
 int gdn3_coeff_dispatch(const GCoeffArgs& a, bool bwd, hipStream_t stream);
 // Rank-r RLS T-factor scan (rls.hip); all tensors float32
 struct RlsDesc {

@@ -102,13 +102,16 @@ class DecodeStateCache:
         return self.pool[slot]
 
     def _slot_tensor(self, slots):
+        """The slots as an int32 device tensor, after checking on the host that
+        no live slot is named twice (two rows advancing one state would race in
+        the kernels).  A tensor is read back for the check (one sync)."""
+        host = [int(s) for s in (slots.tolist() if isinstance(slots, torch.Tensor) else slots)]
+        live = [s for s in host if 0 <= s < self.n_slots]
+        if len(set(live)) != len(live):
+            raise ValueError(f"slots {host} name a slot twice (rows sharing a slot would race)")
         if isinstance(slots, torch.Tensor):
             return slots.to(device=self.device, dtype=torch.int32).contiguous()
-        slots = [int(s) for s in slots]
-        live = [s for s in slots if 0 <= s < self.n_slots]
-        if len(set(live)) != len(live):
-            raise ValueError(f"slots {slots} name a slot twice (rows sharing a slot would race)")
-        return torch.as_tensor(slots, dtype=torch.int32, device=self.device)
+        return torch.as_tensor(host, dtype=torch.int32, device=self.device)
 
     # ---- compute ----
     def prefill(self, slots, q, k, v, a_e, a_w, log_g):

@@ -313,6 +313,8 @@ def gdn3_decode_step(q, k, v, b_gates, w_gates, decay_factors, state, pos, *, R=
     n_slots = A.shape[0]
     if not isinstance(pos, torch.Tensor):
         pos = [int(pos)] * NS if isinstance(pos, int) else [int(x) for x in pos]
+        if any(x < 0 for x in pos):
+            raise ValueError("gdn3_decode_step: token positions must be >= 0")
         pos = torch.tensor(pos, dtype=torch.int32)
     pos = pos.to(device=dev, dtype=torch.int32).contiguous()
     if slots is not None and not isinstance(slots, torch.Tensor):

@@ -128,7 +128,8 @@ def delta_chunk_bwd(q, k, v, a_e, a_w, log_g, dy, chunk_states, chunk, dstate_ou
         dstate_out = dstate_out.float().contiguous()
         _need(tuple(dstate_out.shape) == (B, H, M, D, D), "dstate_out must be [B,H,M,D,D]")
     dev = q.device
-    ws = torch.empty_like(chunk_states)
+    ws = torch.empty(max(lib.gdnx_delta_bwd_workspace_bytes(B, T, H, M, D, chunk, code), 16), dtype=torch.uint8,
+                     device=dev)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
     da_e, da_w, dlg = torch.empty_like(a_e), torch.empty_like(a_w), torch.empty_like(log_g)
     ds0 = torch.empty(B, H, M, D, D, dtype=torch.float32, device=dev) if want_dstate0 else None
@@ -191,7 +192,9 @@ def delta_chunk_bwd_stages(q, k, v, a_e, a_w, log_g, dy, chunk_states, chunk, ws
     B, T, H, M, D = _check_dense(q, k, v, a_e, a_w, log_g)
     code = _lib.dtype_code(q.dtype)
     st = _lib.stream_of(q)
-    ws = torch.empty_like(chunk_states) if ws is None else ws
+    if ws is None:
+        ws = torch.empty(max(lib.gdnx_delta_bwd_workspace_bytes(B, T, H, M, D, chunk, code), 16), dtype=torch.uint8,
+                         device=q.device)
     if out is None:
         out = (torch.empty_like(q), torch.empty_like(k), torch.empty_like(v),
                torch.empty_like(a_e), torch.empty_like(a_w), torch.empty_like(log_g))

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 10
+#define GDNX_ABI_VERSION 11
 
 enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1, GDNX_DTYPE_F64 = 2 /* gdnx_check_finite only */ };
 
@@ -46,7 +46,11 @@ const char* gdnx_last_error(void);
  * the recurrence entry points (delta, per-channel, GDN3 and RLS forwards and
  * backwards, the decode steps) scan the outputs they wrote, synchronise their
  * stream and return GDNX_ERR_NONFINITE if any is NaN or infinite.  Returns
- * the previous setting. */
+ * the previous setting.  Limits while on: each checked call holds one of 64
+ * per-device flag words until its stream has synchronised (a 65th concurrent
+ * checked call on a device returns GDNX_ERR_HIP), and a checked call on a
+ * stream under HIP graph capture returns GDNX_ERR_ARG (the check reads the
+ * flag back and synchronises, which capture forbids). */
 int gdnx_set_check_finite(int on);
 
 /* Scans x[0, n) (GDNX_DTYPE_F32, _BF16 or _F64) on the stream and waits for
@@ -61,16 +65,29 @@ int gdnx_delta_chunk_size(int head_dim, int dtype);
  * (32 for bf16, 16 for float32; the backward also takes 64 for bf16). */
 int gdnx_delta_train_chunk_size(int head_dim, int dtype);
 
-/* Bytes of the per-chunk stash for the given chunk (0 = default; -1 if
- * invalid).  Per chain and chunk, in order: the d x d state entering the
- * chunk and the chunk's C x d net writes R (compute dtype, MFMA-fragment
- * tile order; all states first, then all net writes), then the chunk's
+/* Bytes of the stash for the given chunk (0 = default; -1 if invalid).  In
+ * order: the d x d states (compute dtype, MFMA-fragment tile order), then
+ * every chunk's C x d net writes R (same order), then the chunk's
  * state-independent operands (T = (I + L)^-1 and the decay-masked Q K^T as
  * C x C compute-dtype matrices, and four float32 per-token factors), which
- * the backward's reverse scan reuses.  The backward's workspace is at least
- * this size (state gradients dS at chunk ends, then dB = T^T dR). */
+ * the backward's reverse scan reuses.  The states are the one entering every
+ * chunk, except for bf16 IO with at most 4 lanes per head (the training
+ * default): there only the state entering every 256-token segment is kept,
+ * and the backward recomputes the others from the net writes (checkpointed
+ * form). */
 long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim, int chunk,
                                         int dtype);
+
+/* Bytes of the backward's workspace for the given chunk (0 = train default;
+ * -1 if invalid): the state gradients leaving every chunk (every 256-token
+ * segment in the checkpointed form) and dB = T^T dR of every chunk, laid out
+ * as the forward's stash, then (checkpointed form) the gradient kernel's
+ * float32 sums of dq, dk and dv over the lanes processed so far, 3 x 256 x
+ * head_dim floats per (batch, head, segment).  New in ABI 11: before it the
+ * workspace was gdnx_delta_chunk_states_bytes bytes, which the per-chunk
+ * form still satisfies. */
+long long gdnx_delta_bwd_workspace_bytes(int B, int T, int H, int M, int head_dim, int chunk,
+                                         int dtype);
 
 /* Chunked decoupled-erase delta rule, forward.
  * Replaces the sequential token loop of
@@ -126,7 +143,7 @@ int gdnx_delta_chunk_fwd_scored(const void* q, const void* k, const void* v,
  * reference's chunk graph (gdn3/gdn3_upgrade.py:467-521) and its hand
  * backward of the KMD-2 TRSM (gdn3/kmd2_fast_scan.py:143-160).
  * chunk_states: the forward's stash, made with the same chunk (0 = train
- * default).  workspace: gdnx_delta_chunk_states_bytes bytes.  dstate_out:
+ * default).  workspace: gdnx_delta_bwd_workspace_bytes bytes.  dstate_out:
  * gradient w.r.t. the final state (or NULL).  Outputs: dq, dk, dv [B,T,H,D]
  * (summed over the M lanes), da_e, da_w, dlog_g [B,T,H,M] float32, dstate0
  * [B,H,M,D,D] float32 (or NULL).  dlog_g is zero where the forward clamped. */
@@ -142,9 +159,11 @@ int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v,
 /* The two stages of gdnx_delta_chunk_bwd, callable separately (e.g. to
  * time or overlap them).  Stage 1 runs the reverse state scan on the
  * forward's chunk operands (in chunk_states) and fills workspace with dS at
- * every chunk end and dB (plus dstate0); stage 2 reads the forward's
- * chunk_states and that workspace and writes every input gradient.  Same
- * arguments and layouts as gdnx_delta_chunk_bwd. */
+ * every chunk end (every segment end in the checkpointed form) and dB (plus
+ * dstate0); stage 2 reads the forward's chunk_states and that workspace and
+ * writes every input gradient (in the checkpointed form it also uses the
+ * workspace's float32 tail as scratch, so the workspace is not const since
+ * ABI 11).  Same arguments and layouts as gdnx_delta_chunk_bwd. */
 int gdnx_delta_chunk_bwd_state(const void* q, const void* k, const float* a_e,
                                const float* log_g, const void* dy, const float* dstate_out,
                                const void* chunk_states, void* workspace, float* dstate0,
@@ -152,7 +171,7 @@ int gdnx_delta_chunk_bwd_state(const void* q, const void* k, const float* a_e,
                                int dtype, void* stream);
 int gdnx_delta_chunk_bwd_grads(const void* q, const void* k, const void* v,
                                const float* a_e, const float* a_w, const float* log_g,
-                               const void* dy, const void* chunk_states, const void* workspace,
+                               const void* dy, const void* chunk_states, void* workspace,
                                void* dq, void* dk, void* dv,
                                float* da_e, float* da_w, float* dlog_g,
                                int B, int T, int H, int M, int head_dim, int chunk,

@@ -37,10 +37,26 @@ def test_abi_version_and_sizes():
     assert lib.gdnx_delta_chunk_size(128, _lib.DTYPE_BF16) == 64
     assert lib.gdnx_delta_train_chunk_size(128, _lib.DTYPE_BF16) == 32
     assert lib.gdnx_delta_chunk_size(100, _lib.DTYPE_BF16) == 0
-    # per chain and chunk: one d x d state and one C x d block of net writes, then
-    # the chunk operands (T and Aq as C x C, four float32 factors per token)
+    # per-chunk form (more than 4 lanes): per chain and chunk one d x d state and
+    # one C x d block of net writes, then the chunk operands (T and Aq as C x C,
+    # four float32 factors per token)
+    assert lib.gdnx_delta_chunk_states_bytes(1, 4096, 16, 5, 128, 32, _lib.DTYPE_BF16) == \
+        16 * 5 * 128 * ((128 * 128 + 32 * 128) * 2 + 2 * 32 * 32 * 2 + 4 * 32 * 4)
+    # checkpointed form (bf16, <= 4 lanes): one state per 256-token segment,
+    # the net writes and operands of every chunk
+    chains, nseg = 4 * 16 * 4, 16
+    assert lib.gdnx_delta_chunk_states_bytes(4, 4096, 16, 4, 128, 32, _lib.DTYPE_BF16) == \
+        chains * (nseg * 128 * 128 * 2 + 128 * (32 * 128 * 2 + 2 * 32 * 32 * 2 + 4 * 32 * 4))
+    nch = 64
     assert lib.gdnx_delta_chunk_states_bytes(4, 4096, 16, 4, 128, 64, _lib.DTYPE_BF16) == \
-        4 * 16 * 4 * 64 * ((128 * 128 + 64 * 128) * 2 + 2 * 64 * 64 * 2 + 4 * 64 * 4)
+        chains * (nseg * 128 * 128 * 2 + nch * (64 * 128 * 2 + 2 * 64 * 64 * 2 + 4 * 64 * 4))
+    stash = chains * (nseg * 128 * 128 + nch * 64 * 128) * 2
+    assert lib.gdnx_delta_bwd_workspace_bytes(4, 4096, 16, 4, 128, 64, _lib.DTYPE_BF16) == \
+        (stash + 255) // 256 * 256 + 3 * 4 * 16 * nseg * 256 * 128 * 4
+    # more than 4 lanes: the per-chunk form with its key-half partials
+    assert lib.gdnx_delta_bwd_workspace_bytes(1, 128, 1, 5, 128, 64, _lib.DTYPE_BF16) == \
+        5 * 2 * (128 * 128 + 64 * 128) * 2 + 2 * 3 * 128 * 5 * 4
+    assert lib.gdnx_delta_bwd_workspace_bytes(1, 100, 1, 1, 64, 48, _lib.DTYPE_F32) == -1
     assert lib.gdnx_delta_chunk_states_bytes(1, 100, 1, 1, 64, 0, _lib.DTYPE_F32) == \
         4 * ((64 * 64 + 32 * 64) * 4 + 2 * 32 * 32 * 4 + 4 * 32 * 4)
     assert lib.gdnx_delta_fwd_workspace_bytes(1, 100, 1, 1, 64, 0, _lib.DTYPE_F32) == 4 * (2 * 32 * 32 * 4 + 4 * 32 * 4)
@@ -236,6 +252,8 @@ def test_decode_cache_host_slot_logic():
         assert len(c._free) == 3
         with pytest.raises(ValueError):
             c._slot_tensor([d, -1, d])
+        with pytest.raises(ValueError):       # the same check on a slot tensor
+            c._slot_tensor(torch.tensor([d, -1, d], dtype=torch.int32))
         assert c._slot_tensor([d, -1, -1]).tolist() == [d, -1, -1]
     with pytest.raises(ValueError):
         DecodeStateCache(2, 2, 2, 64, device="cpu", kind="chan")
@@ -246,6 +264,20 @@ def test_decode_cache_host_slot_logic():
         g.prefill([s0, s1], *([torch.zeros(2, 3, 2, 64)] * 3 + [torch.zeros(2, 3, 2, 2)] * 3))
 
 
+def test_gdn3_decode_step_rejects_negative_positions():
+    """A negative token position has no residual slot: the host wrapper
+    refuses it before any launch (the kernels treat a negative device-side
+    position as an empty row)."""
+    from gdnx_amd import gdn3
+    NS, H, M, D = 2, 1, 1, 64
+    x = torch.zeros(NS, H, D)
+    gates = torch.zeros(NS, H, M)
+    N = NS * H * M
+    state = (torch.zeros(N, 4, 8, 8), torch.zeros(N, 4, 8, 8), torch.zeros(N, D, 16), torch.zeros(N, D, 16))
+    with pytest.raises(ValueError, match="positions"):
+        gdn3.gdn3_decode_step(x, x, x, gates, gates, gates, state, [3, -1], factors=(8, 8, 8, 8))
+
+
 def test_noalloc_forward_refuses_before_any_launch():
     """The allocation-free GDN3 forward checks its static scratch's size
     before touching a device: too many chains is GDNX_ERR_WORKSPACE here too."""
@@ -254,10 +286,18 @@ def test_noalloc_forward_refuses_before_any_launch():
     vp = ctypes.c_void_p
     rc = lib.gdnx_gdn3_chunk_fwd_state_noalloc(vp(256), vp(256), vp(256), 1, vp(256), vp(256), 1, vp(256), vp(256),
                                                None, None, None, None, 0, vp(256), None, None, None, None, None,
-                                               64, 32, 16, 4, 128, 4, 16, 16, 16, 16, 8, 8, 0.97,
+                                               64, 32, 16, 4, 128, 4, 16, 32, 16, 16, 8, 8, 0.97,
                                                _lib.DTYPE_BF16, 0, None)
     assert rc == -3
     assert "scratch" in lib.gdnx_last_error().decode()
+    if not torch.cuda.is_available():
+        # K_c = P = 16 is one fused launch with no scratch: not refused for its
+        # size (with no device it then fails at its first HIP call)
+        rc = lib.gdnx_gdn3_chunk_fwd_state_noalloc(vp(256), vp(256), vp(256), 1, vp(256), vp(256), 1, vp(256),
+                                                   vp(256), None, None, None, None, 0, vp(256), None, None, None,
+                                                   None, None, 64, 32, 16, 4, 128, 4, 16, 16, 16, 16, 8, 8, 0.97,
+                                                   _lib.DTYPE_BF16, 0, None)
+        assert rc == -4, lib.gdnx_last_error().decode()
 
 
 def test_hip_and_nonfinite_error_codes():

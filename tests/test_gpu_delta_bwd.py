@@ -16,6 +16,8 @@ def rel_l2(a, b):
 
 
 def _case(B, T, H, D, M, seed, dtype, decay="tau"):
+    if decay == "tau" and M > 4:
+        decay = "softplus"
     taus = (0.05, 0.02, 0.005, 0.001)[:M] if decay == "tau" else None
     x = inputs.dense_inputs(B, T, H, D, M=M, seed=seed, decay=decay, taus=taus, rope=True,
                             with_grad_out=True)
@@ -96,6 +98,45 @@ def test_bf16_state_gradients_ragged(gpu_lib, T):
     _check(vals, dO, 1e-2, state0=s0, dstate=ds)
 
 
+@pytest.mark.parametrize("D,T,M", [(128, 600, 3), (64, 520, 1), (128, 513, 2), (128, 300, 5)],
+                         ids=["d128-3seg-M3", "d64-3seg-M1", "d128-3seg-M2", "d128-M5"])
+def test_bf16_checkpointed_segments(gpu_lib, D, T, M):
+    """The bf16 training default (64-token chunks): the forward keeps one state
+    per 256-token segment and the gradient kernel rebuilds the states forward
+    and the state gradients backward inside each segment.  Several segments
+    with ragged tails (T = 513 leaves a one-token segment), an odd lane count
+    (a lane alone in the last resident pair), one lane, and M = 5 (more lanes
+    than the checkpointed kernel takes: the per-chunk stash), with initial and
+    final state gradients."""
+    print(f"case: bf16 checkpointed D={D} T={T} M={M}", flush=True)
+    vals, dO = _case(1, T, 2, D, M, seed=26, dtype=torch.bfloat16)
+    gen = torch.Generator().manual_seed(27)
+    s0 = torch.randn(1, 2, M, D, D, generator=gen) * 0.05
+    ds = torch.randn(1, 2, M, D, D, generator=gen) * 0.1
+    _check(vals, dO, 1e-2, state0=s0, dstate=ds)
+
+
+@pytest.mark.parametrize("chunk", [32, 64])
+def test_bf16_backward_bitwise_repeatable(gpu_lib, chunk):
+    """Two runs of the training forward + backward on the same inputs in one
+    process give bitwise equal outputs and gradients (fixed summation orders,
+    no atomics), as the reference pins its two scan paths bitwise
+    (tests/ablation/test_fast_scan_api.py:272,317)."""
+    from gdnx_amd import ops
+    print(f"case: bitwise repeat chunk={chunk}", flush=True)
+    vals, dO = _case(2, 400, 3, 128, 4, seed=28, dtype=torch.bfloat16)
+    dev = "cuda:0"
+    q, k, v, ae, aw, lg = (t.to(dev).contiguous() for t in vals)
+    runs = []
+    for _ in range(2):
+        y, s, cs = ops.delta_chunk_fwd(q, k, v, ae, aw, lg, return_state=True, save_states=True, chunk=chunk)
+        g = ops.delta_chunk_bwd(q, k, v, ae, aw, lg, dO.to(dev), cs, chunk)[:6]
+        runs.append([y, s] + list(g))
+    torch.cuda.synchronize()
+    for a_, b_ in zip(*runs):
+        assert torch.equal(a_, b_)
+
+
 def test_state_gradients_fp32(gpu_lib):
     print("case: state0/dstate grads", flush=True)
     vals, dO = _case(1, 70, 2, 64, 2, seed=23, dtype=torch.float32)
@@ -133,8 +174,9 @@ def test_config2_full_size_gradients(gpu_lib):
 @pytest.mark.parametrize("chunk", [32, 64])
 def test_bf16_gradients_explicit_chunk(gpu_lib, chunk):
     """The bf16 training forward and backward at both stash chunks (64, the
-    default: key-split gradient workgroups whose scalar gradients are summed
-    by a second kernel; 32: one workgroup per chunk), through the ops layer."""
+    default: one state per 256-token segment, recomputed by the checkpointed
+    gradient kernel; 32: every chunk's state stashed, one gradient workgroup
+    per chunk), through the ops layer."""
     from gdnx_amd import ops
     print(f"case: bf16 grads chunk={chunk}", flush=True)
     vals, dO = _case(2, 150, 3, 128, 4, seed=24, dtype=torch.bfloat16)

@@ -245,6 +245,36 @@ def test_gdn3_decode_config4_width(gpu_lib):
     assert rel_l2(state[0][:2, :2].reshape(2 * 2 * M, 4, 16, 16), Ar) <= 1e-2
 
 
+def test_gdn3_decode_negative_position_is_an_empty_row(gpu_lib):
+    """A row whose device-side position is negative has no residual slot: the
+    step writes y = 0 for it and leaves its state bitwise unchanged, and no
+    compaction runs on it (for pos = -1, (pos + 1) % K_c would be 0).  The
+    other row, whose token closes a compaction interval, still advances."""
+    from gdnx_amd import gdn3
+    print("case: gdn3 decode pos = -1", flush=True)
+    NS, H, M, D, P = 2, 1, 2, 64, 16
+    gen = torch.Generator().manual_seed(77)
+    N = NS * H * M
+    state = tuple(t.to(DEV) for t in (torch.randn(N, 4, 8, 8, generator=gen) * 0.3,
+                                      torch.randn(N, 4, 8, 8, generator=gen) * 0.3,
+                                      torch.randn(N, D, P, generator=gen) * 0.05,
+                                      F.normalize(torch.randn(N, D, P, generator=gen), dim=1)))
+    before = tuple(t.clone() for t in state)
+    q, k, v = (F.normalize(torch.randn(NS, H, D, generator=gen), dim=-1).to(DEV) for _ in range(3))
+    bg = torch.sigmoid(torch.randn(NS, H, M, generator=gen)).to(DEV)
+    wg = torch.sigmoid(torch.randn(NS, H, M, generator=gen)).to(DEV)
+    dec = torch.full((NS, H, M), 0.97, device=DEV)
+    pos = torch.tensor([P - 1, -1], dtype=torch.int32, device=DEV)
+    with torch.no_grad():
+        y = gdn3.gdn3_decode_step(q, k, v, bg, wg, dec, state, pos, R=4, P=P, factors=(8, 8, 8, 8),
+                                  compact_every=P)
+    torch.cuda.synchronize()
+    assert torch.equal(y[1], torch.zeros_like(y[1]))
+    for t, t0 in zip(state, before):
+        assert torch.equal(t[H * M:], t0[H * M:])      # row 1's chains untouched
+        assert not torch.equal(t[:H * M], t0[:H * M])  # row 0's chains advanced
+
+
 KMD2_CASES = [(128, 128, 1, torch.float32), (64, 64, 4, torch.float32), (8, 64, 4, torch.float32),
               (128, 128, 2, torch.bfloat16)]
 
