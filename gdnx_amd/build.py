@@ -61,6 +61,55 @@ def build(verbose: bool = True) -> str:
     return OUT
 
 
+ASAN_OUT = os.path.join(OBJ, "asan", "libgdnx_asan.so")
+
+
+def asan_runtime() -> str:
+    """The shared AddressSanitizer runtime of hipcc's clang (to preload)."""
+    clang = os.path.join(os.path.dirname(os.path.realpath(_hipcc())), "..", "lib", "llvm", "bin", "clang++")
+    if not os.path.exists(clang):
+        clang = "/opt/rocm/llvm/bin/clang++"
+    r = subprocess.run([clang, "--print-file-name=libclang_rt.asan-x86_64.so"], capture_output=True, text=True)
+    return r.stdout.strip()
+
+
+def build_asan(verbose: bool = False) -> str:
+    """libgdnx with its host code built under AddressSanitizer and
+    UndefinedBehaviorSanitizer (the device code is built as usual: the
+    sanitizers apply to the host pass only), into _build/asan/.  A process
+    that loads it must preload asan_runtime() first.  Used by
+    tests/test_abi_asan.py to run the C ABI's argument checks and size
+    arithmetic under the sanitizers on a machine without a GPU."""
+    hipcc = _hipcc()
+    odir = os.path.dirname(ASAN_OUT)
+    os.makedirs(odir, exist_ok=True)
+    san = ["-Xarch_host", "-fsanitize=address", "-Xarch_host", "-fsanitize=undefined",
+           "-Xarch_host", "-fno-sanitize-recover=undefined", "-Xarch_host", "-fno-omit-frame-pointer",
+           "-Xarch_host", "-shared-libasan"]
+    srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+
+    def comp(src):
+        obj = os.path.join(odir, os.path.basename(src) + ".o")
+        if os.path.exists(obj) and os.path.getmtime(obj) >= max(os.path.getmtime(src), *(
+                os.path.getmtime(os.path.join(CSRC, h)) for h in os.listdir(CSRC) if h.endswith(".hpp"))):
+            return obj
+        cmd = [hipcc, *FLAGS, "-O1", "-g", *san, "-c", src, "-o", obj]
+        r = subprocess.run(cmd, capture_output=True, text=True)
+        if r.returncode != 0:
+            raise RuntimeError(f"hipcc (sanitized) failed for {src}:\n{r.stderr[-6000:]}")
+        return obj
+    with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
+        objs = list(ex.map(comp, srcs))
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libasan", "-fsanitize=address,undefined",
+           "-fno-gpu-sanitize", *objs, "-o", ASAN_OUT]
+    r = subprocess.run(cmd, capture_output=True, text=True)
+    if r.returncode != 0:
+        raise RuntimeError(f"sanitized link failed:\n{r.stderr[-6000:]}")
+    if verbose:
+        print(f"built {ASAN_OUT}")
+    return ASAN_OUT
+
+
 if __name__ == "__main__":
     build()
     sys.exit(0)

@@ -60,6 +60,23 @@ static bool valid_chunk(int D, int dtype, int C) {
 
 static bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
 
+// Whether every factor is >= 0 and their product is at most limit (checked
+// without forming a product that could overflow).
+static bool prod_le(long long limit, std::initializer_list<long long> xs) {
+  long long p = 1;
+  for (long long x : xs) {
+    if (x < 0) return false;
+    if (x != 0 && p > limit / x) return false;
+    p *= x;
+  }
+  return true;
+}
+// The sizes a size query accepts: at most 2^30 chains (B * H * M) and 2^40
+// token-chains (B * T * H * M), so that every byte count below fits in 63 bits.
+static bool query_sizes_ok(int B, int T, int H, int M) {
+  return prod_le(1LL << 30, {B, H, M}) && prod_le(1LL << 40, {B, T, H, M});
+}
+
 static int check_common(const void* q, const void* k, const void* v, int B, int T, int H, int M,
                         int D, int dtype) {
   if (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16)
@@ -94,7 +111,7 @@ extern "C" long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, i
                                                    int dtype) {
   const int C = chunk ? chunk : delta_chunk_size(head_dim, dtype);
   if (C == 0 || !valid_chunk(head_dim, dtype, C) || B < 1 || T < 0 || H < 1 || M < 1 ||
-      (head_dim != 64 && head_dim != 128))
+      (head_dim != 64 && head_dim != 128) || !query_sizes_ok(B, T, H, M))
     return -1;
   const int cps = delta_stash_cps(head_dim, C, dtype, M);
   return (long long)(delta_stash_bytes(B * H * M, T, head_dim, C, dtype, cps) +
@@ -105,7 +122,7 @@ extern "C" long long gdnx_delta_bwd_workspace_bytes(int B, int T, int H, int M, 
                                                     int dtype) {
   const int C = chunk ? chunk : delta_train_chunk_size(head_dim, dtype);
   if (C == 0 || !valid_chunk(head_dim, dtype, C) || B < 1 || T < 0 || H < 1 || M < 1 ||
-      (head_dim != 64 && head_dim != 128))
+      (head_dim != 64 && head_dim != 128) || !query_sizes_ok(B, T, H, M))
     return -1;
   return (long long)delta_bwd_workspace_bytes(B, T, H, M, head_dim, C, dtype);
 }
@@ -137,7 +154,7 @@ extern "C" long long gdnx_delta_fwd_workspace_bytes(int B, int T, int H, int M, 
                                                     int dtype) {
   const int C = chunk ? chunk : delta_chunk_size(head_dim, dtype);
   if (C == 0 || !valid_chunk(head_dim, dtype, C) || B < 1 || T < 0 || H < 1 || M < 1 ||
-      (head_dim != 64 && head_dim != 128))
+      (head_dim != 64 && head_dim != 128) || !query_sizes_ok(B, T, H, M))
     return -1;
   return (long long)delta_prep_bytes(B * H * M, T, C, dtype);
 }
@@ -348,7 +365,7 @@ static int g3_layer_geom(int D, const G3Geom& ge) {
 
 extern "C" long long gdnx_gdn3_workspace_bytes(int B, int H, int M, int head_dim, int P, int dtype) {
   if (B < 1 || H < 1 || M < 1 || !g3_window_ok(head_dim, P) ||
-      (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16))
+      (dtype != GDNX_DTYPE_F32 && dtype != GDNX_DTYPE_BF16) || !query_sizes_ok(B, 1, H, M))
     return -1;
   return (long long)gdn3_workspace_bytes(B * H * M, head_dim, P, dtype);
 }
@@ -361,7 +378,7 @@ extern "C" int gdnx_gdn3_num_compactions(int T, int P, int compact_every) {
 extern "C" long long gdnx_gdn3_train_states_bytes(int B, int T, int H, int M, int head_dim, int P,
                                                   int compact_every) {
   if (B < 1 || T < 0 || H < 1 || M < 1 || !g3_window_ok(head_dim, P) || compact_every < P ||
-      compact_every % P != 0)
+      compact_every % P != 0 || !query_sizes_ok(B, T, H, M))
     return -1;
   return (long long)gdn3_train_states_bytes(B * H * M, T, head_dim, P, compact_every);
 }
@@ -779,12 +796,12 @@ static int chan_common(const float* q, const float* k, const float* v, const flo
 }
 
 extern "C" long long gdnx_delta_chan_states_bytes(int B, int T, int H, int head_dim) {
-  if (B < 1 || T < 0 || H < 1 || (head_dim != 64 && head_dim != 128)) return -1;
+  if (B < 1 || T < 0 || H < 1 || (head_dim != 64 && head_dim != 128) || !query_sizes_ok(B, T, H, 1)) return -1;
   return (long long)chan_states_bytes(B * H, T, head_dim);
 }
 
 extern "C" long long gdnx_delta_chan_fwd_workspace_bytes(int B, int T, int H, int head_dim) {
-  if (B < 1 || T < 0 || H < 1 || (head_dim != 64 && head_dim != 128)) return -1;
+  if (B < 1 || T < 0 || H < 1 || (head_dim != 64 && head_dim != 128) || !query_sizes_ok(B, T, H, 1)) return -1;
   return (long long)chan_fwd_workspace_bytes(B * H, T, head_dim);
 }
 
@@ -862,8 +879,8 @@ static bool all_aligned(std::initializer_list<const void*> ps) {
 
 extern "C" int gdnx_gdn3_lane_rope_pairs(int M, int key_dim, int* pairs) {
   g_err[0] = 0;
-  if (M < 1 || M > 4 || key_dim < 1 || !pairs)
-    return set_error(GDNX_ERR_ARG, "need 1 <= M <= 4, key_dim >= 1 and a pairs array");
+  if (M < 1 || M > 4 || key_dim < 1 || !pairs || ((uintptr_t)pairs & 3u))
+    return set_error(GDNX_ERR_ARG, "need 1 <= M <= 4, key_dim >= 1 and an aligned host int pairs array");
   int p[4];
   gdn3_lane_pairs(M, key_dim, p);
   for (int m = 0; m < M; ++m) pairs[m] = p[m];
@@ -920,7 +937,7 @@ extern "C" int gdnx_gdn3_prologue_bwd(const void* b_proj, const void* proj_a, co
 }
 
 extern "C" long long gdnx_gdn3_epilogue_workspace_bytes(int B, int T, int H, int value_dim) {
-  if (B < 1 || T < 0 || H < 1 || value_dim < 1) return -1;
+  if (B < 1 || T < 0 || H < 1 || value_dim < 1 || !query_sizes_ok(B, T, H, 1) || value_dim > (1 << 16)) return -1;
   return (long long)gdn3_epilogue_workspace_bytes((long long)B * T * H, value_dim);
 }
 

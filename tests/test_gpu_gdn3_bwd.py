@@ -88,6 +88,9 @@ def _check_backward(case, P=16):
     grads = torch.autograd.grad(y, leaves, dy.to(io).to(DEV))
     torch.cuda.synchronize()
     yr, gref = _oracle(xs, dy.to(io), M, P, Kc, factors, G, slow_decay=sdec)
+    # slow_decay = 0 (A, B replaced by the rank-R refit at every compaction, no
+    # blend) is a stress setting, not the layer's 0.97: every compaction's fp32
+    # rounding then reaches the outputs undamped, so those cases get 5e-4
     tol = 1e-2 if io == torch.bfloat16 else (5e-4 if sdec == 0.0 else 1e-4)
     assert rel_l2(y, yr) <= tol
     for name, a, r in zip(("dq", "dk", "dv", "db_gates", "dw_gates", "ddecay"), grads, gref):
@@ -98,7 +101,11 @@ def _check_backward(case, P=16):
         assert err <= tol, name
 
 
-@pytest.mark.parametrize("case", CASES, ids=[f"c{i}" for i in range(len(CASES))])
+def _case_id(i, case):
+    return f"c{i}-stress-sdec0" if case[-1] == 0.0 else f"c{i}"
+
+
+@pytest.mark.parametrize("case", CASES, ids=[_case_id(i, c) for i, c in enumerate(CASES)])
 def test_gdn3_backward_matches_oracle(gpu_lib, case):
     _check_backward(case)
 
@@ -116,7 +123,7 @@ P_CASES = [
 ]
 
 
-@pytest.mark.parametrize("P,case", P_CASES, ids=[f"p{c[0]}c{i}" for i, c in enumerate(P_CASES)])
+@pytest.mark.parametrize("P,case", P_CASES, ids=[f"p{c[0]}" + _case_id(i, c[1]) for i, c in enumerate(P_CASES)])
 def test_gdn3_backward_window_p(gpu_lib, P, case):
     _check_backward(case, P)
 

@@ -74,3 +74,53 @@ def test_gdn3_scan_gradients(gpu_lib, dtype, tol, D, T):
         err = rel_l2(gg, rr)
         print(f"  {name} rel-L2 {err:.2e}", flush=True)
         assert err <= tol, name
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float32])
+def test_gdn3_scan_bitwise_repeatable(gpu_lib, dtype):
+    """gdn3_scan forward and backward run twice on the same inputs in one
+    process give bitwise equal outputs and gradients (fixed summation orders,
+    no atomics; the reference pins its two scan paths bitwise,
+    tests/ablation/test_fast_scan_api.py:272,317)."""
+    from gdnx_amd import gdn3
+    print(f"case: gdn3_scan bitwise repeat {dtype}", flush=True)
+    x = inputs.dense_inputs(2, 300, 2, 128, M=4, seed=61, decay="tau", rope=True, with_grad_out=True)
+    runs = []
+    for _ in range(2):
+        ins = [(x[n].to(dtype) if n in "qkv" else x[n]).to(DEV).requires_grad_(True)
+               for n in ("q", "k", "v", "beta", "g")]
+        y = gdn3.gdn3_scan(*ins)
+        g = torch.autograd.grad(y, ins, grad_outputs=x["dO"].to(dtype).to(DEV))
+        runs.append([y.detach()] + list(g))
+    torch.cuda.synchronize()
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("P,Kc", [(16, 16), (32, 64)], ids=["layer-default", "p32"])
+def test_gdn3_recurrent_state_bitwise_repeatable(gpu_lib, P, Kc):
+    """The Kronecker-residual regime (window, compaction, backward) run twice
+    in one process: bitwise equal y, final state and gradients."""
+    import torch.nn.functional as F
+    from gdnx_amd import gdn3
+    from oracle import gdn3 as og
+    print(f"case: gdn3_recurrent_state bitwise repeat P={P} Kc={Kc}", flush=True)
+    g = torch.Generator().manual_seed(62)
+    B, T, H, M, D = 1, 200, 2, 2, 128
+    q = F.normalize(torch.randn(B, T, H, M, D, generator=g), dim=-1).bfloat16()
+    k = F.normalize(torch.randn(B, T, H, M, D, generator=g), dim=-1).bfloat16()
+    v = torch.randn(B, T, H, M, D, generator=g).bfloat16()
+    bg = torch.sigmoid(torch.randn(B, T, H, M, D, generator=g))
+    wg = torch.sigmoid(torch.randn(B, T, H, M, D, generator=g))
+    dec = torch.exp(-torch.rand(B, T, H, M, generator=g) * 0.05)
+    dy = torch.randn(B, T, H, M, D, generator=g).bfloat16()
+    G = og.reference_sketch(B * H * M, 64, 8).to(DEV)
+    runs = []
+    for _ in range(2):
+        leaves = [t.to(DEV).requires_grad_(True) for t in (q, k, v, bg, wg, dec)]
+        y, st, _ = gdn3.gdn3_recurrent_state(*leaves, P=P, compact_every=Kc, sketch=G, return_state=True)
+        grads = torch.autograd.grad(y, leaves, dy.to(DEV))
+        runs.append([y.detach()] + [s.detach() for s in st] + list(grads))
+    torch.cuda.synchronize()
+    for a, b in zip(*runs):
+        assert torch.equal(a, b)

@@ -17,10 +17,10 @@ non-finite status, on the GPU against the CPU oracle.
 
 Tolerances (rel-L2) as in the other GDN3 tests: 1e-4 for float32 IO, 1e-2
 for bf16; 1e-3 for the compacted factors at float32.  The long-horizon cases
-are given 2e-4 for y and the gradients (measured on MI355X: 1.2e-5 to
-7.7e-5): each compaction's SVD moves its singular vectors by (perturbation
+are held to the same 1e-4 for y and the gradients (measured on MI355X: 1.2e-5
+to 7.7e-5); each compaction's SVD moves its singular vectors by (perturbation
 of R_mat) / (singular-value gap), and 64 of them carry the fp32 rounding
-forward.
+forward, which is what the margin to 1e-4 covers.
 """
 import ctypes
 import types
@@ -214,11 +214,11 @@ def test_long_horizon_forward_backward(gpu_lib, case):
     yr, gref = _oracle(xs, M, 16, Kc, factors, G, dy=dy)
     err = rel_l2(y, yr)
     print(f"  y rel-L2 {err:.2e}", flush=True)
-    assert err <= 2e-4
+    assert err <= 1e-4
     for name, a, r in zip(("dq", "dk", "dv", "db_gates", "dw_gates", "ddecay"), grads, gref):
         err = rel_l2(a, r)
         print(f"  {name} rel-L2 {err:.2e}", flush=True)
-        assert err <= 2e-4, name
+        assert err <= 1e-4, name
 
 
 # ---------------------------------------------------------------------------
