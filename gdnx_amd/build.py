@@ -100,8 +100,8 @@ def build_asan(verbose: bool = False) -> str:
         return obj
     with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
         objs = list(ex.map(comp, srcs))
-    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", "-shared-libasan", "-fsanitize=address,undefined",
-           "-fno-gpu-sanitize", *objs, "-o", ASAN_OUT]
+    link_san = ["-shared-libasan", "-fsanitize=address,undefined", "-fno-gpu-sanitize"]   # host code only
+    cmd = [hipcc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *link_san, *objs, "-o", ASAN_OUT]
     r = subprocess.run(cmd, capture_output=True, text=True)
     if r.returncode != 0:
         raise RuntimeError(f"sanitized link failed:\n{r.stderr[-6000:]}")

@@ -511,6 +511,40 @@ __device__ __forceinline__ const CT* stash_state_ptr(const CT* rec, int dt, int 
   return rec + stash_tile_offset<CT, D>(dt, V, lane);
 }
 
+// One 16-byte unit of a [C][D] tile record in the scans' raw
+// accumulator-tile layout (unit u: tile u / 32 = (token tile, value tile),
+// lanes 2 (u % 32) and 2 (u % 32) + 1): 4 consecutive tokens of two
+// adjacent value columns.
+struct TileUnit {
+  int tok, col;   // first token (within the sub-chunk), first column
+};
+template <int D>
+__device__ __forceinline__ TileUnit tile_unit_of(int u) {
+  constexpr int NDT = D / 16;
+  const int tl = u >> 5, lp = u & 31;
+  const int it = tl / NDT, V = tl % NDT, g = lp >> 3, n0 = 2 * (lp & 7);
+  return TileUnit{16 * it + 4 * g, 16 * V + n0};
+}
+// rows [tok + i][col], [tok + i][col + 1], i = 0..3 (two bf16 per store)
+template <int LD>
+__device__ __forceinline__ void unit_commit_rows(bf16* dst, const uint4& x, TileUnit t) {
+  const unsigned w[4] = {x.x, x.y, x.z, x.w};   // x.x, x.y: column col, tokens 0..3; x.z, x.w: column col + 1
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const unsigned a = (w[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
+    const unsigned b = (w[2 + (i >> 1)] >> ((i & 1) * 16)) & 0xffffu;
+    *(unsigned*)&dst[(t.tok + i) * LD + t.col] = a | (b << 16);
+  }
+}
+// Sum of x over the four 16-lane rows of the wave, in every lane (gfx950
+// permlane swaps: lane l is added to l ^ 16, then to l ^ 32).
+__device__ __forceinline__ float sum_rows4(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Frag element e of a tile-native fragment sits at row offset frag_row(e, g4)
 // within the k-step (see gdnx_common.hpp).
 template <typename CT>

@@ -272,7 +272,13 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
 // ---------------------------------------------------------------------------
 // backward: reverse scan of the state gradient
 // ---------------------------------------------------------------------------
-template <typename CT, int D, int C, int NWV>
+// With P3S (the checkpointed form: bf16, one workgroup per chain) the scan
+// also forms, per chunk, P3 = R dS^T (the net writes against the gradient of
+// the state leaving the chunk, [C][key]) and stashes it as bf16 accumulator
+// tiles after dB: the gradient kernel then needs no state gradient but the
+// segment ends'.  dS is written to LDS as bf16 [key][value] rows so that
+// wave w contracts key tile w over every value column.
+template <typename CT, int D, int C, int NWV, bool P3S>
 struct alignas(16) ScanBwdBuf {
   typedef ScanDims<CT, D, C, NWV> Sd;
   CT k[C * Sd::LDD];        // K rows
@@ -282,21 +288,27 @@ struct alignas(16) ScanBwdBuf {
   CT tt[C * Sd::LDC];       // T^T
   CT aqt[C * Sd::LDC];      // Aq^T
   float sc[kNumSc * C];
+  CT r[(P3S ? C : 1) * Sd::LDD];   // R rows (the forward's net writes; P3S)
 };
 // staging double-buffered by chunk parity where it fits in LDS (see the forward)
-template <typename CT, int D, int C, int NWV>
+template <typename CT, int D, int C, int NWV, bool P3S>
 struct alignas(16) ScanBwdSmem {
-  static constexpr int NBUF = 2 * sizeof(ScanBwdBuf<CT, D, C, NWV>) <= 160 * 1024 ? 2 : 1;
-  ScanBwdBuf<CT, D, C, NWV> buf[NBUF];
+  typedef ScanDims<CT, D, C, NWV> Sd;
+  static constexpr size_t DSL = P3S ? (size_t)D * Sd::LDD : 8;
+  static constexpr int NBUF = 2 * sizeof(ScanBwdBuf<CT, D, C, NWV, P3S>) + DSL * sizeof(CT) <= 160 * 1024 ? 2 : 1;
+  ScanBwdBuf<CT, D, C, NWV, P3S> buf[NBUF];
+  CT dsl[DSL];              // dS rows [key][value] (P3S)
+  float kpr[2][P3S ? C : 1][NWV];   // per-wave parts of k.P3 per token, by chunk parity (P3S)
 };
 
-template <typename CT, int D, int C, int NWV>
+template <typename CT, int D, int C, int NWV, bool P3S>
 __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2))) delta_scan_bwd_kernel(DeltaBwdArgs p) {
   typedef ScanDims<CT, D, C, NWV> Sd;
   typedef typename Sd::Frag Frag;
   constexpr int KS = Sd::KS, TPS = Sd::TPS, NDT = Sd::NDT, NCT = Sd::NCT, NT = Sd::NT;
   constexpr int LDD = Sd::LDD, LDC = Sd::LDC, BV = Sd::BV;
-  __shared__ ScanBwdSmem<CT, D, C, NWV> sm;
+  static_assert(!P3S || (sizeof(CT) == 2 && Sd::NVB == 1), "P3 needs bf16 and one workgroup per chain");
+  __shared__ ScanBwdSmem<CT, D, C, NWV, P3S> sm;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
@@ -340,9 +352,32 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
   Stage<CT, C, BV, 4, GT> py;
   Stage<CT, C, C, 4, GT> pt, pa;
   ScalStage<3 * C, GT> ps;   // gam, dec, aeg
+  // P3S: the chunk's net-write record, one 16-byte unit (C = 32) or two per thread
+  constexpr int UPR = P3S ? C * D / (8 * NT) : 1;
+  static_assert(!P3S || UPR * 8 * NT == C * D, "R record: whole units per thread");
+  uint4 rx[UPR];
+  const CT* rst = (const CT*)p.s_stash + sg.states;   // the forward's net writes
+  CT* p3st = (CT*)p.ds_stash + sg.states + sg.tiles;   // P3 tiles, after dB
+  float* k3st = (float*)(p3st + sg.tiles);             // k.P3 per token, after P3
+  // k.P3 of chunk cc's tokens from the waves' parts (wave 0, once they are complete)
+  auto k3_out = [&](int cc) {
+    if constexpr (P3S) {
+      if (wave == 0 && lane < C) {
+        float x = 0.f;
+#pragma unroll
+        for (int w = 0; w < NWV; ++w) x += sm.kpr[cc & 1][lane][w];
+        k3st[rec_index(chain, cc, nchains) * C + lane] = x;
+      }
+    }
+  };
   const unsigned rsb = (unsigned)(rs * sizeof(CT));
   const unsigned ysb = (unsigned)(rsy * sizeof(CT));
   auto fetch = [&](int c) {
+    if constexpr (P3S) {
+      const CT* src = rst + rec_index(chain, c, nchains) * C * D;
+#pragma unroll
+      for (int u = 0; u < UPR; ++u) rx[u] = *(const uint4*)(src + 8 * (tid + u * NT));
+    }
     const int t0 = c * C;
     const int nv = min(C, p.T - t0);
     if (grp == 0) {
@@ -357,8 +392,12 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
       ps.fetch(pp.sc + rec_index(chain, c, nchains) * kNumSc * C, gt);
     }
   };
-  constexpr int NBUF = ScanBwdSmem<CT, D, C, NWV>::NBUF;
-  auto commit = [&](ScanBwdBuf<CT, D, C, NWV>& B) {
+  constexpr int NBUF = ScanBwdSmem<CT, D, C, NWV, P3S>::NBUF;
+  auto commit = [&](ScanBwdBuf<CT, D, C, NWV, P3S>& B) {
+    if constexpr (P3S) {
+#pragma unroll
+      for (int u = 0; u < UPR; ++u) unit_commit_rows<LDD>(B.r, rx[u], tile_unit_of<D>(tid + u * NT));
+    }
     if (grp == 0) {
       pq.template commit_tr<LDC>(B.qt, gt);
     } else if (grp == 1) {
@@ -390,6 +429,18 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
     Frag dSf[NDT / TPS];
 #pragma unroll
     for (int kb = 0; kb < NDT / TPS; ++kb) dSf[kb] = acc_frag((CT*)nullptr, dS[kb * TPS], dS[kb * TPS + TPS - 1]);
+    if constexpr (P3S) {
+      // dS as bf16 rows [key][value]: this wave's value columns of every key.
+      // Each tile is transposed first (lane (g, n): key 16 dt + n, values
+      // 16 V + 4 g ..), so a lane writes four values of one row at once.
+#pragma unroll
+      for (int dt = 0; dt < NDT; ++dt) {
+        const f32x4 y = tile_transpose((CT*)nullptr, dS[dt], lane);
+        *(bf16x4*)&sm.dsl[(dt * 16 + n16) * LDD + 16 * V + 4 * g4] = (bf16x4){(bf16)y[0], (bf16)y[1], (bf16)y[2], (bf16)y[3]};
+      }
+      lds_barrier();   // every wave's columns written (loads in flight stay in flight)
+      if (c + 1 < NC) k3_out(c + 1);   // (its parts were completed before the last step's barrier)
+    }
     {
       // the state gradient leaving every cps-th chunk and the last one
       // (record c / cps); other chunks' stores are dropped (empty range)
@@ -402,6 +453,32 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
         buf_store4(sr, (unsigned)(stash_tile_offset<CT, D>(dt, V, lane) * sizeof(CT)), (const CT*)nullptr, dS[dt][0],
                    dS[dt][1], dS[dt][2], dS[dt][3]);
     }
+    // ---- P3^T = dS R^T on key tile `wave` (lane (g, n): keys 16 wave + 4 g + e
+    // of token 16 it + n), stored as the gradient kernel's dk tile, and the
+    // per-wave parts of k.P3 ----
+    auto p3_block = [&]() {
+      if constexpr (P3S) {
+        f32x4 P3[NCT];
+#pragma unroll
+        for (int it = 0; it < NCT; ++it) P3[it] = zero4();
+#pragma unroll
+        for (int kb = 0; kb < D / KS; ++kb) {
+          const Frag a = ld_frag(&sm.dsl[(wave * 16 + n16) * LDD + kb * KS], g4);
+#pragma unroll
+          for (int it = 0; it < NCT; ++it) mma(P3[it], a, ld_frag(&sb.r[(it * 16 + n16) * LDD + kb * KS], g4));
+        }
+        CT* pst = p3st + rec * (C * D);
+#pragma unroll
+        for (int it = 0; it < NCT; ++it) {
+          st4(pst + stash_tile_offset<CT, D>(it, wave, lane), P3[it][0], P3[it][1], P3[it][2], P3[it][3]);
+          // the token's k.P3 over this wave's keys, in float32
+          const bf16x4 k4 = *(const bf16x4*)&sb.k[(it * 16 + n16) * LDD + wave * 16 + 4 * g4];
+          float x = (P3[it][0] * (float)k4[0] + P3[it][1] * (float)k4[1]) + (P3[it][2] * (float)k4[2] + P3[it][3] * (float)k4[3]);
+          x = sum_rows4(x);
+          if (g4 == 0) sm.kpr[c & 1][it * 16 + n16][wave] = x;
+        }
+      }
+    };
     // ---- dR = diag(dec) K dS + Aq^T dY ----
     Frag dYf[C / KS];
 #pragma unroll
@@ -458,12 +535,14 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
         }
       }
     }
+    p3_block();   // (off the dR -> dB -> dS path: measured fastest here)
     // ---- chunk c - 1's tiles into the other buffer, chunk c - 2's loads ----
     if constexpr (NBUF == 1) __syncthreads();   // (one buffer: every wave done with chunk c's tiles)
     if (c > 0) commit(sm.buf[(c - 1) % NBUF]);
     fetch(max(c - 2, 0));   // (the first chunks refetch, unused)
     __syncthreads();
   }
+  k3_out(0);
   if (p.ds0) {
 #pragma unroll
     for (int dt = 0; dt < NDT; ++dt)
@@ -480,7 +559,9 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
 template <typename CT, int D, int C>
 struct ScanCfg {
   static constexpr int NWV = D / 16;
-  static_assert(sizeof(ScanFwdSmem<CT, D, C, NWV>) <= 160 * 1024 && sizeof(ScanBwdSmem<CT, D, C, NWV>) <= 160 * 1024,
+  static_assert(sizeof(ScanFwdSmem<CT, D, C, NWV>) <= 160 * 1024 &&
+                    sizeof(ScanBwdSmem<CT, D, C, NWV, false>) <= 160 * 1024 &&
+                    (sizeof(CT) != 2 || C != 32 || sizeof(ScanBwdSmem<CT, D, C, NWV, true>) <= 160 * 1024),
                 "scan LDS budget");
 };
 
@@ -501,7 +582,14 @@ template <typename CT, int D, int C>
 static int launch_scan_bwd(const DeltaBwdArgs& a, hipStream_t stream) {
   constexpr int NWV = ScanCfg<CT, D, C>::NWV;
   typedef ScanDims<CT, D, C, NWV> Sd;
-  hipLaunchKernelGGL((delta_scan_bwd_kernel<CT, D, C, NWV>), dim3(a.B * a.H * a.M * Sd::NVB), dim3(Sd::NT), 0,
+  if constexpr (sizeof(CT) == 2 && C == 32) {
+    if (a.cps > 1) {   // checkpointed form: P3 tiles for delta_grad_seg_kernel
+      hipLaunchKernelGGL((delta_scan_bwd_kernel<CT, D, C, NWV, true>), dim3(a.B * a.H * a.M * Sd::NVB), dim3(Sd::NT),
+                         0, stream, a);
+      return check_launch("delta_scan_bwd_kernel");
+    }
+  }
+  hipLaunchKernelGGL((delta_scan_bwd_kernel<CT, D, C, NWV, false>), dim3(a.B * a.H * a.M * Sd::NVB), dim3(Sd::NT), 0,
                      stream, a);
   return check_launch("delta_scan_bwd_kernel");
 }

@@ -32,9 +32,10 @@ int delta_chunk_size(int D, int dtype) {
 // chunk used when the forward stashes states for the backward: 32 for bf16
 // (with at most 4 lanes per head the stash keeps one state per 256-token
 // segment and the backward recomputes the rest), 16 for float32.  The
-// 64-token bf16 chunk, also checkpointed, stays selectable: its scans hold
-// one chunk's tiles in LDS instead of two (no overlap of the next chunk's
-// staging) and measured 1.5-2x slower on the config-2 step.
+// 64-token bf16 chunk stays selectable in the per-chunk stash form: its
+// scans hold one chunk's tiles in LDS instead of two (no overlap of the next
+// chunk's staging), spill registers, and measured 1.5-2x slower on the
+// config-2 step.
 int delta_train_chunk_size(int D, int dtype) {
   if (D != 64 && D != 128) return 0;
   return dtype == GDNX_DTYPE_BF16 ? 32 : 16;
@@ -42,11 +43,13 @@ int delta_train_chunk_size(int D, int dtype) {
 
 size_t delta_bwd_workspace_bytes(int B, int T, int H, int M, int D, int C, int dtype) {
   const int cps = delta_stash_cps(D, C, dtype, M);
-  size_t n = delta_stash_bytes(B * H * M, T, D, C, dtype, cps);
-  if (cps > 1) {
+  if (cps > 1) {   // see delta_seg_carry_offset
     const size_t nseg = (size_t)((T + kSegTokens - 1) / kSegTokens);
-    n = (n + 255) / 256 * 256 + 3 * (size_t)B * H * nseg * kSegTokens * D * sizeof(float);
-  } else if (dtype == GDNX_DTYPE_BF16 && C == 64) {
+    return delta_seg_carry_offset(B * H * M, T, D, C, cps) +
+           (M > 2 ? 3 * (size_t)B * H * nseg * kSegTokens * D * sizeof(float) : 0);
+  }
+  size_t n = delta_stash_bytes(B * H * M, T, D, C, dtype, cps);
+  if (dtype == GDNX_DTYPE_BF16 && C == 64) {
     n += 2 * 3 * (size_t)B * T * H * M * sizeof(float);   // the two key halves' per-token partials
   }
   return n;

@@ -333,11 +333,12 @@ size_t delta_prep_bytes(int nchains, int T, int C, int dtype);
 constexpr int kSegTokens = 256;
 // Chunks per stashed state record: 1 (the state entering every chunk and the
 // state gradient leaving it, read by delta_bwd_grads_kernel) or, for bf16 IO
-// with at most 4 lanes per head, one record per kSegTokens-token segment
-// (read by delta_grad_seg_kernel, which recomputes the rest).
+// with 32-token chunks and at most 4 lanes per head, one record per
+// kSegTokens-token segment (read by delta_grad_seg_kernel, which recomputes
+// the rest in 32-token sub-chunks: the reverse scan's P3 = R dS^T is taken
+// at its chunk ends, so its chunk must be the sub-chunk).
 __host__ __device__ inline int delta_stash_cps(int D, int C, int dtype, int M) {
-  return (dtype == GDNX_DTYPE_BF16 && (C == 32 || C == 64) && M >= 1 && M <= 4 && (D == 64 || D == 128))
-             ? kSegTokens / C : 1;
+  return (dtype == GDNX_DTYPE_BF16 && C == 32 && M >= 1 && M <= 4 && (D == 64 || D == 128)) ? kSegTokens / C : 1;
 }
 // Per-chain stash geometry: NC chunks; a state record every cps chunks.
 struct StashGeom {
@@ -354,6 +355,14 @@ __host__ __device__ inline StashGeom stash_geom(int nchains, int T, int D, int C
   g.states = g.nsrec * D * D;
   g.tiles = g.nrec * C * D;
   return g;
+}
+// The checkpointed backward's workspace (bf16 IO): the state gradients at
+// segment ends, dB and P3 = R dS^T per token (bf16), k.P3 per token
+// (float32), then, with more than two lanes per head, the float32 carry of
+// the dq / dk / dv sums between lane pairs ([B H segments][3][kSegTokens][D]).
+__host__ __device__ inline size_t delta_seg_carry_offset(int nchains, int T, int D, int C, int cps) {
+  const StashGeom g = stash_geom(nchains, T, D, C, cps);
+  return ((g.states + 2 * g.tiles) * 2 + g.nrec * C * sizeof(float) + 255) / 256 * 256;
 }
 // bytes of the state + net-write stash (the prep records follow it in chunk_states)
 inline size_t delta_stash_bytes(int nchains, int T, int D, int C, int dtype, int cps) {

@@ -47,12 +47,19 @@ def test_abi_version_and_sizes():
     chains, nseg = 4 * 16 * 4, 16
     assert lib.gdnx_delta_chunk_states_bytes(4, 4096, 16, 4, 128, 32, _lib.DTYPE_BF16) == \
         chains * (nseg * 128 * 128 * 2 + 128 * (32 * 128 * 2 + 2 * 32 * 32 * 2 + 4 * 32 * 4))
+    # 64-token chunks: the per-chunk form whatever the lane count
     nch = 64
     assert lib.gdnx_delta_chunk_states_bytes(4, 4096, 16, 4, 128, 64, _lib.DTYPE_BF16) == \
-        chains * (nseg * 128 * 128 * 2 + nch * (64 * 128 * 2 + 2 * 64 * 64 * 2 + 4 * 64 * 4))
-    stash = chains * (nseg * 128 * 128 + nch * 64 * 128) * 2
-    assert lib.gdnx_delta_bwd_workspace_bytes(4, 4096, 16, 4, 128, 64, _lib.DTYPE_BF16) == \
-        (stash + 255) // 256 * 256 + 3 * 4 * 16 * nseg * 256 * 128 * 4
+        chains * nch * ((128 * 128 + 64 * 128) * 2 + 2 * 64 * 64 * 2 + 4 * 64 * 4)
+    # backward workspace, checkpointed form: the state gradient at every
+    # segment end, then dB and P3 = R dS^T per token (bf16), then k.P3 per
+    # token (float32), then (more than two lanes) the float32 dq / dk / dv
+    # carry between lane pairs
+    ckpt = chains * ((nseg * 128 * 128 + 2 * 128 * 32 * 128) * 2 + 128 * 32 * 4)
+    assert lib.gdnx_delta_bwd_workspace_bytes(4, 4096, 16, 4, 128, 32, _lib.DTYPE_BF16) == \
+        (ckpt + 255) // 256 * 256 + 3 * 4 * 16 * nseg * 256 * 128 * 4
+    ckpt2 = 4 * 16 * 2 * ((nseg * 128 * 128 + 2 * 128 * 32 * 128) * 2 + 128 * 32 * 4)
+    assert lib.gdnx_delta_bwd_workspace_bytes(4, 4096, 16, 2, 128, 32, _lib.DTYPE_BF16) == (ckpt2 + 255) // 256 * 256
     # more than 4 lanes: the per-chunk form with its key-half partials
     assert lib.gdnx_delta_bwd_workspace_bytes(1, 128, 1, 5, 128, 64, _lib.DTYPE_BF16) == \
         5 * 2 * (128 * 128 + 64 * 128) * 2 + 2 * 3 * 128 * 5 * 4

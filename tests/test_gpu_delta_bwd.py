@@ -101,13 +101,13 @@ def test_bf16_state_gradients_ragged(gpu_lib, T):
 @pytest.mark.parametrize("D,T,M", [(128, 600, 3), (64, 520, 1), (128, 513, 2), (128, 300, 5)],
                          ids=["d128-3seg-M3", "d64-3seg-M1", "d128-3seg-M2", "d128-M5"])
 def test_bf16_checkpointed_segments(gpu_lib, D, T, M):
-    """The bf16 training default (64-token chunks): the forward keeps one state
-    per 256-token segment and the gradient kernel rebuilds the states forward
-    and the state gradients backward inside each segment.  Several segments
-    with ragged tails (T = 513 leaves a one-token segment), an odd lane count
-    (a lane alone in the last resident pair), one lane, and M = 5 (more lanes
-    than the checkpointed kernel takes: the per-chunk stash), with initial and
-    final state gradients."""
+    """The bf16 training default (32-token chunks): the forward keeps one state
+    per 256-token segment, the reverse scan forms P3 = R dS^T at every chunk
+    end, and the gradient kernel rebuilds the states forward inside each
+    segment.  Several segments with ragged tails (T = 513 leaves a one-token
+    segment), three lanes, one lane, and M = 5 (more lanes than the
+    checkpointed kernel takes: the per-chunk stash), with initial and final
+    state gradients."""
     print(f"case: bf16 checkpointed D={D} T={T} M={M}", flush=True)
     vals, dO = _case(1, T, 2, D, M, seed=26, dtype=torch.bfloat16)
     gen = torch.Generator().manual_seed(27)
@@ -173,9 +173,9 @@ def test_config2_full_size_gradients(gpu_lib):
 
 @pytest.mark.parametrize("chunk", [32, 64])
 def test_bf16_gradients_explicit_chunk(gpu_lib, chunk):
-    """The bf16 training forward and backward at both stash chunks (64, the
+    """The bf16 training forward and backward at both stash chunks (32, the
     default: one state per 256-token segment, recomputed by the checkpointed
-    gradient kernel; 32: every chunk's state stashed, one gradient workgroup
+    gradient kernel; 64: every chunk's state stashed, one gradient workgroup
     per chunk), through the ops layer."""
     from gdnx_amd import ops
     print(f"case: bf16 grads chunk={chunk}", flush=True)
