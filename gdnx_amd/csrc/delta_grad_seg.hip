@@ -205,29 +205,35 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
   // token scalars; step j of a lane pair is sub-chunk j / ML, lane mb + j % ML ----
   struct Pf {
     uint4 y, r, x, p3;
-    ScalarRegs sc;
+    ScalarRegs sc;   // raw (a clamped token's), masked at commit
     float k3;
+    bool ok;         // the lane's token is in the sub-chunk and before T
   };
   auto tile_src = [&](const bf16* region, int c, int m) {
     const int t0 = t_seg + c * C, cs = t0 / CS, j = (t0 % CS) / C;
     return region + rec_index(chain_of(m), cs, (size_t)N) * CS * D + (size_t)j * C * D;
   };
+  // Loads retire in order and a wait counts every older load, so nothing
+  // here uses a loaded value: the scalars are issued first and masked at
+  // commit, and the tiles stay in flight through the next step.
   auto fetch_step = [&](Pf& f, int j, int tid) {
     const int c = j / ML, m = mb + j % ML;
     const int t0 = t_seg + c * C;
+    if (wave == SCW) {
+      const int lane = tid & 63, cs = t0 / CS, jj = (t0 % CS) / C;
+      const size_t so = ((size_t)b * p.T * p.H + h) * M + m + (size_t)min(t0 + lane, p.T - 1) * st;
+      f.sc.ae = p.ae[so];
+      f.sc.aw = p.aw[so];
+      f.sc.g = p.g[so];
+      f.k3 = k3st[rec_index(chain_of(m), cs, (size_t)N) * CS + jj * C + min(lane, C - 1)];
+      f.ok = lane < C && t0 + lane < p.T;
+    }
     f.r = *(const uint4*)(tile_src(rst, c, m) + 8 * tid);
     f.x = *(const uint4*)(tile_src(dxst, c, m) + 8 * tid);
     f.p3 = *(const uint4*)(tile_src(p3st, c, m) + 8 * tid);
     const bf16* yb = (const bf16*)p.dy + (((size_t)b * p.T + t0) * p.H + h) * M * D + (size_t)m * D;
     const __amdgpu_buffer_rsrc_t yr = buf_rsrc(yb, (unsigned)rows_left(t0) * ysb);
     f.y = buf_load16(yr, (unsigned)row_unit_tok(tid) * ysb + row_unit_d0(tid) * sizeof(bf16));
-    if (wave == SCW) {
-      const size_t so = ((size_t)b * p.T * p.H + h) * M + m;
-      const int lane = tid & 63, cs = t0 / CS, jj = (t0 % CS) / C;
-      scal_fetch_all<C>(f.sc, p.ae + so, p.aw + so, p.g + so, st, t0, p.T, lane);
-      const float k3 = k3st[rec_index(chain_of(m), cs, (size_t)N) * CS + jj * C + min(lane, C - 1)];
-      f.k3 = (lane < C && t0 + lane < p.T) ? k3 : 0.f;
-    }
   };
   auto commit_scalars = [&](const ScalarRegs& r, float (*sc)[C], int lane) {
     const float G = lane_prefix<C>(fmaxf(fminf(r.g, 0.f), kLogFloor), lane);
@@ -250,8 +256,9 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
     row_commit_nat<LDD>(L.dy, f.y, row_unit_tok(tid), row_unit_d0(tid));
     *(uint4*)&L.p3[8 * tid] = f.p3;
     if (wave == SCW) {
-      commit_scalars(f.sc, sc, tid & 63);
-      if ((tid & 63) < C) sc[kK3][tid & 63] = f.k3;
+      const ScalarRegs r{f.ok ? f.sc.ae : 0.f, f.ok ? f.sc.aw : 0.f, f.ok ? f.sc.g : 0.f};
+      commit_scalars(r, sc, tid & 63);
+      if ((tid & 63) < C) sc[kK3][tid & 63] = f.ok ? f.k3 : 0.f;
     }
   };
   // sub-chunk tiles q, k, v: one row-major unit each per thread
@@ -355,11 +362,7 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
     const int tid = opaque(tid0);
     const int lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
 #pragma unroll
-    for (int it = 0; it < NCT; ++it) {   // earlier pairs' sums
-      dQacc[it] = first ? zero4() : *(const f32x4*)(dqs + scr_off(c, it, lane));
-      dKacc[it] = first ? zero4() : *(const f32x4*)(dks + scr_off(c, it, lane));
-      dVacc[it] = first ? zero4() : *(const f32x4*)(dvs + scr_off(c, it, lane));
-    }
+    for (int it = 0; it < NCT; ++it) dQacc[it] = dKacc[it] = dVacc[it] = zero4();
 #pragma unroll
     for (int mm = 0; mm < kRes; ++mm) {
       if (mm >= ML) break;
@@ -382,7 +385,6 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
         }
       }
       if (mm > 0 && wave == SW) scalars(c, m - 1, (j - 1) % 3);   // (a sub-chunk's last step: in its epilogue)
-      if (mm == ML - 1) fetch_sub(spf, c + 1, tid);   // the next sub-chunk's q, k, v through this step
       const SegLane<D>& L = sm.ln[j & 1];
       const float(*sc)[C] = sm.sc[j3];
       // ---- P1^T = S dY^T, P2^T = S dB^T on this wave's key tile: lane
@@ -520,6 +522,17 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
       fetch_step(pf, min(j + 2, nstep - 1), tid);
     }
     // ---- sub-chunk epilogue: gram-gradient products; dq, dk, dv out ----
+    // the earlier pairs' sums, loaded here (after the steps' prefetches, whose
+    // waits they would otherwise join) and added before the stores
+    f32x4 cq[NCT], ck[NCT], cv[NCT];
+    if (!first) {
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) {
+        cq[it] = *(const f32x4*)(dqs + scr_off(c, it, lane));
+        ck[it] = *(const f32x4*)(dks + scr_off(c, it, lane));
+        cv[it] = *(const f32x4*)(dvs + scr_off(c, it, lane));
+      }
+    }
     __syncthreads();   // every lane's tile tasks and sums done
     if (wave == SW) scalars(c, mb + ML - 1, (c * ML + ML - 1) % 3);
 #pragma unroll
@@ -556,6 +569,14 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
         mma(dKacc[it], bkt, ld_frag(&sm.A3[(it * 16 + n16) * LDC], g4));
       }
     }
+    if (!first) {
+#pragma unroll
+      for (int it = 0; it < NCT; ++it) {
+        dQacc[it] += cq[it];
+        dKacc[it] += ck[it];
+        dVacc[it] += cv[it];
+      }
+    }
     if (!last) {   // the sums so far to the next pair
 #pragma unroll
       for (int it = 0; it < NCT; ++it) {
@@ -580,6 +601,7 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
       }
     }
     if (c + 1 < nsub) {
+      fetch_sub(spf, c + 1, tid);
       __syncthreads();   // every wave done with this sub-chunk's q / k / v tiles
       commit_sub(spf, tid);
     }
