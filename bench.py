@@ -4,18 +4,26 @@
 Workload: one GDN3 layer recurrence at B=4, T=4096,
 H=16, d_k=d_v=128, 4 MIMO lanes sharing q/k/v (bf16 IO, fp32 state), lane
 decays tau in {0.05, 0.02, 0.005, 0.001} plus N(0, 0.01^2) gate noise,
-partial RoPE on q/k dims 0..31; synthetic seeded inputs (oracle.inputs,
-seed 1002) already resident in HBM.  One step = gdnx_amd.gdn3.gdn3_scan
-forward + backward against a fixed bf16 upstream gradient dO, producing
-dq, dk, dv, dbeta, dlog_g.
+partial RoPE on q/k dims 0..31; synthetic seeded inputs
+(gdnx_amd.workloads, seed 1002) already resident in HBM.  One step =
+gdnx_amd.gdn3.gdn3_scan forward + backward against a fixed bf16 upstream
+gradient dO, producing dq, dk, dv, dbeta, dlog_g.
 
 Prints ONE JSON line.  Besides the step throughput it reports:
   roofline      the dominant kernel's algorithmic FLOP per launch divided by
                 its mean duration (HIP events on the launch stream), against
                 the 2.5 PFLOP/s dense bf16 MFMA peak;
+  roofline_intra_chunk  the intra-chunk phase (delta_prep_kernel) and the
+                fused single-kernel forward at C = 64, with MFMA-busy counters;
+  config1_fwd_ms, config1_fwd_fused_c64_ms  the inference forward (no
+                stash) at the config-1 shape: the default path, and the fused
+                single-kernel scan at C = 64;
+  decode_ms_per_step, decode_hbm_frac  the config-4 decode step;
+  gdn3_layer_fwd_bwd_ms  the GDN3 layer default regime (compaction every
+                16 tokens) forward + backward at B=4, T=4096;
   cpu_baseline  the repository's CPU oracle (a port of the reference's
                 sequential recurrence, fp32, torch autograd) on a bounded
-                sample of the same workload, scaled to the metric's unit.
+                sample of the same workload (4 of the 16 heads), as measured.
 """
 from __future__ import annotations
 
@@ -51,14 +59,20 @@ def flops_prep(B, T, H, M, D, C):
 
 def flops_bwd_state(B, T, H, M, D, C):
     """Reverse state scan: per lane and chunk K dS (2 C D^2), Aq^T dY and
-    T^T dR (2 C^2 D each) and the dS update (4 C D^2)."""
+    T^T dR (2 C^2 D each), the dS update (4 C D^2) and P3 = R dS^T
+    (2 C D^2)."""
     nchunks = B * H * ((T + C - 1) // C)
-    return nchunks * M * (6 * C * D * D + 4 * C * C * D)
+    return nchunks * M * (8 * C * D * D + 4 * C * C * D)
 
 
 def flops_bwd_grads(B, T, H, M, D, C):
-    """The rest of the backward: total backward = 2x forward."""
-    return 2 * flops_fwd(B, T, H, M, D, C) - flops_bwd_state(B, T, H, M, D, C)
+    """Gradient kernel (delta_grad_seg_kernel, 32-token sub-chunks): per lane
+    and sub-chunk P1 = dY S^T, P2 = dB S^T and the state update (2 C D^2
+    each), dAq = dY R^T and dL = -dB R^T (2 C^2 D each); per head and
+    sub-chunk the raw grams Q K^T, K K^T (2 C^2 D each) and the gram-gradient
+    products into dq and dk (three of 2 C^2 D)."""
+    nchunks = B * H * ((T + C - 1) // C)
+    return nchunks * (10 * C * C * D + M * (6 * C * D * D + 4 * C * C * D))
 
 
 def median_time(fn, runs=3):
@@ -75,8 +89,8 @@ def median_time(fn, runs=3):
 
 def cpu_baseline(T=2048, H=4):
     """Time the CPU oracle (fp32 sequential recurrence + autograd) on
-    B=1, H heads x 4 lanes, T tokens (one warm-up, median of 3); tokens/s
-    scaled to the 16-head layer."""
+    B=1, H heads x 4 lanes, T tokens (one warm-up, median of 3); tokens/s of
+    that sample as measured (tokens of the H-head sample per second)."""
     import torch
     from oracle import delta, inputs
     torch.set_num_threads(os.cpu_count() or 1)
@@ -89,12 +103,13 @@ def cpu_baseline(T=2048, H=4):
         (y * x["dO"].float()).sum().backward()
     secs = median_time(run)
     return {
-        "value": T * (H / 16.0) / secs,
+        "value": T / secs,
         "unit": "tokens/s",
         "cores": torch.get_num_threads(),
         "kind": "port",
         "sample": f"oracle.delta.lane_delta fp32 sequential fwd+bwd, B=1 T={T} H={H}x4 lanes "
-                  f"d=128, one warm-up then median of 3 ({secs:.1f} s), scaled by H/16 to the layer's 16 heads",
+                  f"d=128 (the headline layer has 16 heads), one warm-up then median of 3 ({secs:.1f} s); "
+                  f"value = tokens of this sample per second, not scaled",
     }
 
 
@@ -110,11 +125,20 @@ def measured_traffic(kernel):
     return None if entry is None else entry["traffic"]
 
 
-def intra_chunk_entry(t_prep, flop):
-    """Roofline of the intra-chunk phase (delta_prep_kernel, timed alone with
-    HIP events): algorithmic FLOP against the dense bf16 MFMA peak, its
-    measured HBM traffic against 8 TB/s, and the MFMA-busy fraction read by
-    the SQ_VALU_MFMA_BUSY_CYCLES counter in the committed profile."""
+def intra_chunk_entry(t_prep, flop, t_fused, flop_fused):
+    """Roofline of the intra-chunk phase as the default paths run it
+    (delta_prep_kernel at the training chunk, timed alone with HIP events):
+    algorithmic FLOP against the dense bf16 MFMA peak, its measured HBM
+    traffic against 8 TB/s, and the MFMA-busy fraction read by the
+    SQ_VALU_MFMA_BUSY_CYCLES counter in the committed profile.  "fused": the
+    same phase on-chip inside the single-kernel forward at C = 64
+    (delta_fwd_kernel, which also runs the inter-chunk scan), with its
+    counter."""
+    busy = {}
+    path = os.path.join(ROOT, "profiles", "mfma_busy.json")
+    if os.path.exists(path):
+        with open(path) as f:
+            busy = json.load(f).get("kernels", {})
     name = "delta_prep_kernel"
     achieved = flop / t_prep / 1e12
     traffic = measured_traffic(name)
@@ -122,11 +146,12 @@ def intra_chunk_entry(t_prep, flop):
              "peak_tflops": MFMA_BF16_PEAK / 1e12, "frac_mfma": achieved * 1e12 / MFMA_BF16_PEAK,
              "mean_us": t_prep * 1e6, "algorithmic_flop": flop, "traffic": traffic,
              "hbm_gbs": None if traffic is None else traffic / t_prep / 1e9,
-             "frac_hbm": None if traffic is None else traffic / t_prep / HBM_PEAK}
-    path = os.path.join(ROOT, "profiles", "mfma_busy.json")
-    if os.path.exists(path):
-        with open(path) as f:
-            entry["mfma_busy_counter"] = json.load(f).get("kernels", {}).get(name)
+             "frac_hbm": None if traffic is None else traffic / t_prep / HBM_PEAK,
+             "mfma_busy_counter": busy.get(name)}
+    entry["fused"] = {"kernel": "delta_fwd_kernel", "chunk": 64, "mean_us": t_fused * 1e6,
+                      "algorithmic_flop": flop_fused, "achieved_tflops": flop_fused / t_fused / 1e12,
+                      "frac_mfma": flop_fused / t_fused / MFMA_BF16_PEAK,
+                      "mfma_busy_counter": busy.get("delta_fwd_kernel")}
     return entry
 
 
@@ -167,15 +192,34 @@ def cpu_baseline_decode(NS_sample=64, H=16, NC=16, D=128, steps=8):
     }
 
 
-def bench_decode(args):
-    """Config 4: batched one-token decode, 256 sequences x 16 heads x (4 lanes
-    x 4 decays) chains of 128x128 fp32 state, bf16 q/k/v per step.  A step is
-    one gdnx_delta_decode_step over all chains; value = sequences decoded per
-    second (one token each)."""
+def gdn3_decode_bytes(N, NS, H, D, P=16, R=4, io_bytes=2):
+    """HBM bytes of one GDN3 decode step without a compaction: per chain the
+    Kronecker-residual state read whole (A: R 16x16, B: R 8x8, U and Vb:
+    D x P, fp32: 21.5 KB at D = 128, P = 16) and written back except U's
+    other slots (A, B, gamma Vb and one U column: 13.5 KB), its three gates
+    and its bf16 output; q, k, v once per head."""
+    read = (R * 256 + R * 64 + 2 * D * P) * 4
+    write = (R * 256 + R * 64 + D * P + D) * 4
+    return N * (read + write + 3 * 4 + D * io_bytes) + 3 * NS * H * D * io_bytes
+
+
+def decode_bytes_chan(NS, H, NC, D, io_bytes=2):
+    """The per-key-channel decode step: the dense step's bytes with a
+    log-decay per key channel (D floats per chain) in place of one."""
+    return decode_bytes(NS, H, NC, D, io_bytes) + NS * H * NC * (D - 1) * 4
+
+
+def decode_suite(steps, warmup, extras=True):
+    """Config-4 decode measurements (HIP events on the launch stream): the
+    dense step (gdnx_delta_decode_step) and, with extras, the same through
+    shuffled state slots, the per-key-channel step and the GDN3
+    Kronecker-residual step at the same width (256 sequences x 16 heads x 16
+    chains).  Returns a dict of ms per step and HBM fractions of the
+    algorithmic bytes."""
     import torch
-    from gdnx_amd import ops
     import torch.nn.functional as F
-    from oracle import inputs
+    from gdnx_amd import gdn3, ops
+    from gdnx_amd import workloads as inputs
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -195,47 +239,111 @@ def bench_decode(args):
     y = torch.empty(NS, H, NC, D, device=dev, dtype=torch.bfloat16)
     stream = torch.cuda.current_stream()
 
+    def timed(fn, n, w):
+        for i in range(w):
+            fn(i)
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for i in range(n):
+            fn(i)
+        e1.record(stream)
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) * 1e-3 / n
+
     def step(i):
         j = i % n_in
         ops.delta_decode_step(q[j], k[j], v[j], a[j], a[j], lg[j], state, out=y)
 
-    for i in range(args.warmup):
-        step(i)
-    torch.cuda.synchronize()
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    e0.record(stream)
-    for i in range(args.steps):
-        step(i)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    sec = e0.elapsed_time(e1) * 1e-3 / args.steps
+    sec = timed(step, steps, warmup)
     nbytes = decode_bytes(NS, H, NC, D)
-    achieved = nbytes / sec / 1e9
-    traffic = measured_traffic("delta_decode_kernel")
-    # the same steps through the decode-state cache: the states are a pool of
-    # NS slots and the batch rows name their slots in a shuffled order
+    out = {"dense": {"kernel": "delta_decode_kernel", "ms_per_step": sec * 1e3, "tokens_per_s": NS / sec,
+                     "algorithmic_bytes": nbytes, "hbm_gbs": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / HBM_PEAK,
+                     "traffic": measured_traffic("delta_decode_kernel")}}
+    if not extras:
+        return out
+    # the state pool addressed through shuffled slots
     perm = torch.randperm(NS, generator=torch.Generator().manual_seed(5)).to(torch.int32).to(dev)
 
     def step_slots(i):
         j = i % n_in
         ops.delta_decode_step_slots(q[j], k[j], v[j], a[j], a[j], lg[j], state, perm, out=y)
 
-    step_slots(0)
-    torch.cuda.synchronize()
-    e0.record(stream)
-    for i in range(args.steps):
-        step_slots(i)
-    e1.record(stream)
-    torch.cuda.synchronize()
-    sec_slots = e0.elapsed_time(e1) * 1e-3 / args.steps
+    sec = timed(step_slots, steps, 1)
+    out["slots"] = {"kernel": "delta_decode_kernel (slot-indexed)", "ms_per_step": sec * 1e3,
+                    "tokens_per_s": NS / sec, "hbm_frac": nbytes / sec / HBM_PEAK,
+                    "note": "rows name shuffled slots of a 256-slot state pool"}
+    # a log-decay per key channel (KMD-2's decay) on the same states
+    lgc = (lg[..., None] + 0.001 * torch.randn(n_in, NS, H, NC, D, device=dev, generator=gen)).contiguous()
+
+    def step_chan(i):
+        j = i % n_in
+        ops.delta_decode_step_chan(q[j], k[j], v[j], a[j], a[j], lgc[j], state, out=y)
+
+    sec = timed(step_chan, steps, 1)
+    nb = decode_bytes_chan(NS, H, NC, D)
+    out["chan"] = {"kernel": "delta_decode_chan_kernel", "ms_per_step": sec * 1e3, "tokens_per_s": NS / sec,
+                   "algorithmic_bytes": nb, "hbm_frac": nb / sec / HBM_PEAK}
+    del lgc
+    # the GDN3 Kronecker-residual step: 4 x (16x16 (x) 8x8) + a 16-slot window per chain
+    del state
+    torch.cuda.empty_cache()
+    P = 16
+    N = NS * H * NC
+    g2 = torch.Generator(device=dev).manual_seed(1005)
+    A = torch.randn(NS, H, NC, 4, 16, 16, device=dev, generator=g2) * \
+        torch.tensor([0.4, 0.2, 0.1, 0.05], device=dev).view(4, 1, 1)
+    Bk = torch.randn(NS, H, NC, 4, 8, 8, device=dev, generator=g2) * 0.5
+    U = torch.randn(NS, H, NC, D, P, device=dev, generator=g2) * 0.02
+    Vb = F.normalize(torch.randn(NS, H, NC, D, P, device=dev, generator=g2), dim=-2)
+    g3 = (A, Bk, U, Vb)
+    sk = torch.randn(N, 64, 8, device=dev, generator=g2) / 8.0
+    bg = torch.sigmoid(torch.randn(n_in, NS, H, NC, device=dev, generator=g2))
+    wg = torch.sigmoid(torch.randn(n_in, NS, H, NC, device=dev, generator=g2))
+    dec = torch.exp(lg).clamp(max=1.0)
+
+    def step_g3(pos):
+        def run(i):
+            j = i % n_in
+            gdn3.gdn3_decode_step(q[j], k[j], v[j], bg[j], wg[j], dec[j], g3, pos(i), R=4, P=P,
+                                  factors=(16, 16, 8, 8), compact_every=P, sketch=sk)
+        return run
+
+    # positions that close no interval, then whole intervals (15 plain steps and
+    # the step after which every row compacts); int32 device tensors, built once
+    n_int = 16 * max(1, steps // 16)
+    pos_t = [torch.full((NS,), i, dtype=torch.int32, device=dev) for i in range(max(n_int, 16 * steps + 2))]
+    with torch.no_grad():
+        sec_plain = timed(step_g3(lambda i: pos_t[16 * i + 1]), steps, 1)
+        sec_int = timed(step_g3(lambda i: pos_t[i]), n_int, 0)
+    nb = gdn3_decode_bytes(N, NS, H, D, P)
+    out["gdn3"] = {"kernel": "gdn3_decode_kernel", "ms_per_step": sec_plain * 1e3, "tokens_per_s": NS / sec_plain,
+                   "algorithmic_bytes": nb, "hbm_frac": nb / sec_plain / HBM_PEAK,
+                   "ms_per_step_with_compactions": sec_int * 1e3,
+                   "note": "ms_per_step: steps that close no compaction interval; "
+                           "ms_per_step_with_compactions: 16 consecutive positions, the last followed "
+                           "by every row's compaction (gdn3_compact_kernel)"}
+    return out
+
+
+def bench_decode(args):
+    """Config 4: batched one-token decode, 256 sequences x 16 heads x (4 lanes
+    x 4 decays) chains of 128x128 fp32 state, bf16 q/k/v per step.  A step is
+    one gdnx_delta_decode_step over all chains; value = sequences decoded per
+    second (one token each).  The same line reports the slot-indexed step,
+    the per-key-channel step and the GDN3 Kronecker-residual step at the
+    same width."""
+    NS, H, NC, D = 256, 16, 16, 128
+    r = decode_suite(args.steps, args.warmup)
+    d = r["dense"]
     line = {
         "metric": "GDN3 batched decode tokens/s @256 seq x 16 heads x 4 lanes x 4 decays, d=128",
-        "value": NS / sec,
+        "value": d["tokens_per_s"],
         "unit": "tokens/s",
         "n_gpus": 1,
         "steps": args.steps,
         "warmup": args.warmup,
-        "ms_per_step": sec * 1e3,
+        "ms_per_step": d["ms_per_step"],
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
@@ -245,12 +353,13 @@ def bench_decode(args):
                                "states (4.29 GB), bf16 q/k/v per step",
                    "sequences": NS, "heads": H, "chains_per_head": NC, "head_dim": D,
                    "parallelism": "single GPU"},
-        "roofline": {"bound": "hbm", "kernel": "delta_decode_kernel", "achieved": achieved,
-                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": achieved * 1e9 / HBM_PEAK,
-                     "traffic": traffic, "mean_us": sec * 1e6, "algorithmic_bytes": nbytes},
-        "decode_cache": {"kernel": "delta_decode_kernel (slot-indexed)", "ms_per_step": sec_slots * 1e3,
-                         "tokens_per_s": NS / sec_slots, "hbm_frac": nbytes / sec_slots / HBM_PEAK,
-                         "note": "rows name shuffled slots of a 256-slot state pool"},
+        "roofline": {"bound": "hbm", "kernel": d["kernel"], "achieved": d["hbm_gbs"],
+                     "peak": HBM_PEAK / 1e9, "unit": "GB/s", "frac": d["hbm_frac"],
+                     "traffic": d["traffic"], "mean_us": d["ms_per_step"] * 1e3,
+                     "algorithmic_bytes": d["algorithmic_bytes"]},
+        "decode_cache": r["slots"],
+        "decode_chan": r["chan"],
+        "decode_gdn3": r["gdn3"],
     }
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline_decode()
@@ -295,7 +404,7 @@ def bench_gdn3(args, layer_default, train=False):
     the decay against a fixed upstream gradient (gdn3-layer-train)."""
     import torch
     from gdnx_amd import gdn3
-    from oracle import inputs
+    from gdnx_amd import workloads as inputs
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -375,6 +484,37 @@ def bench_gdn3(args, layer_default, train=False):
         line["cpu_baseline"] = cpu_baseline_gdn3(T=256 if train else (512 if layer_default else 2048), B=B,
                                                  compact_every=Kc, train=train)
     print(json.dumps(line), flush=True)
+
+
+def gdn3_layer_train_ms(steps=3, warmup=1):
+    """The GDN3 layer's default regime (compaction every P = 16 tokens) at
+    config-1 width (B=4, T=4096, H=16, 4 lanes, d=128): ms of one
+    gdn3_recurrent_state forward + backward (gradients of q, k, v, both gates
+    and the decay against a fixed upstream gradient)."""
+    import torch
+    from gdnx_amd import gdn3
+    from gdnx_amd import workloads as inputs
+    dev = torch.device("cuda:0")
+    x = inputs.config3(T=4096, B=4, n_pairs=64, span=4096)
+    leaves = tuple(x[n].to(dev).contiguous().requires_grad_(True) for n in ("q", "k", "v", "b", "w", "dec"))
+    B, T, H, D = x["q"].shape
+    M = x["b"].shape[-1]
+    dy = torch.randn(B, T, H, M, D, generator=torch.Generator().manual_seed(7)).to(leaves[0].dtype).to(dev)
+    stream = torch.cuda.current_stream()
+
+    def step():
+        out = gdn3.gdn3_recurrent_state(*leaves, compact_every=16)
+        return torch.autograd.grad(out, leaves, dy)[0]
+    for _ in range(warmup):
+        step()
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(steps):
+        step()
+    e1.record(stream)
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / steps
 
 
 MFMA_FP32_PEAK = 157.3e12   # dense fp32 FLOP/s
@@ -900,7 +1040,7 @@ def main():
 
     import torch
     from gdnx_amd import gdn3, ops
-    from oracle import inputs
+    from gdnx_amd import workloads as inputs
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
@@ -961,10 +1101,16 @@ def main():
                       args.kernel_iters)
         pws = ops.delta_chunk_prep(qd, kd, a, a, lg, chunk=C)
         t_prep = timed(lambda: ops.delta_chunk_prep(qd, kd, a, a, lg, chunk=C, ws=pws), args.kernel_iters)
+        # the config-1 forward (inference, no stash) on the same inputs: the default path
+        # (two-pass at the training chunk for bf16) and the fused single-kernel scan at 64
+        bd = beta.detach()
+        t_c1 = timed(lambda: gdn3.gdn3_scan(qd, kd, vd, bd, lg), args.kernel_iters)
+        t_c1_fused = timed(lambda: ops.delta_chunk_fwd(qd, kd, vd, a, a, lg, chunk=64, two_pass=False),
+                           args.kernel_iters)
     kernels = {
         "delta_prep_kernel+delta_scan_fwd_kernel": (t_fwd, flops_fwd(B, T, H, M, D, C)),
         "delta_scan_bwd_kernel": (t_bst, flops_bwd_state(B, T, H, M, D, C)),
-        "delta_bwd_grads_kernel": (t_bgr, flops_bwd_grads(B, T, H, M, D, C)),
+        "delta_grad_seg_kernel": (t_bgr, flops_bwd_grads(B, T, H, M, D, C)),
     }
     dom = max(kernels, key=lambda n: kernels[n][0])
     t_dom, f_dom = kernels[dom]
@@ -992,10 +1138,19 @@ def main():
                      "peak": MFMA_BF16_PEAK / 1e12, "unit": "TFLOP/s",
                      "frac": achieved * 1e12 / MFMA_BF16_PEAK, "traffic": traffic,
                      "mean_us": t_dom * 1e6, "algorithmic_flop": f_dom},
-        "roofline_intra_chunk": intra_chunk_entry(t_prep, flops_prep(B, T, H, M, D, C)),
+        "roofline_intra_chunk": intra_chunk_entry(t_prep, flops_prep(B, T, H, M, D, C), t_c1_fused,
+                                                  flops_fwd(B, T, H, M, D, 64)),
         "kernels_us": {n: round(t * 1e6, 2) for n, (t, _) in kernels.items()},
         "grads_finite": finite,
+        "config1_fwd_ms": t_c1 * 1e3,
+        "config1_fwd_fused_c64_ms": t_c1_fused * 1e3,
     }
+    # config 4 decode (the dense step) and the layer-default GDN3 regime, timed here so
+    # the headline run carries them
+    dec = decode_suite(steps=20, warmup=3, extras=False)["dense"]
+    line["decode_ms_per_step"] = dec["ms_per_step"]
+    line["decode_hbm_frac"] = dec["hbm_frac"]
+    line["gdn3_layer_fwd_bwd_ms"] = gdn3_layer_train_ms()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
     print(json.dumps(line), flush=True)

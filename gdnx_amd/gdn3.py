@@ -49,9 +49,9 @@ class GDN3ScanFunction(torch.autograd.Function):
         train = any(ctx.needs_input_grad)
         D = q.shape[-1]
         a = ops.gdn3_coeff(k, beta)
-        chunk = ops.chunk_size(D, q.dtype, train=train)
+        chunk, two_pass = ops.forward_plan(D, q.dtype, train)
         y, s_out, cs = ops.delta_chunk_fwd(q, k, v, a, a, log_g, state0, return_state=True,
-                                           save_states=train, chunk=chunk)
+                                           save_states=train, chunk=chunk, two_pass=two_pass)
         if train:
             ctx.save_for_backward(q, k, v, beta, a, log_g, cs)
             ctx.chunk = chunk
