@@ -18,7 +18,7 @@ LIB_PATH = os.path.join(_HERE, "libgdnx.so")
 DTYPE_F32 = 0
 DTYPE_BF16 = 1
 DTYPE_F64 = 2      # gdnx_check_finite only
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _c_int, _c_ll, _vp, _c_float = ctypes.c_int, ctypes.c_longlong, ctypes.c_void_p, ctypes.c_float
 

@@ -21,7 +21,7 @@
 extern "C" {
 #endif
 
-#define GDNX_ABI_VERSION 11
+#define GDNX_ABI_VERSION 12
 
 enum { GDNX_DTYPE_F32 = 0, GDNX_DTYPE_BF16 = 1, GDNX_DTYPE_F64 = 2 /* gdnx_check_finite only */ };
 
@@ -71,21 +71,23 @@ int gdnx_delta_train_chunk_size(int head_dim, int dtype);
  * state-independent operands (T = (I + L)^-1 and the decay-masked Q K^T as
  * C x C compute-dtype matrices, and four float32 per-token factors), which
  * the backward's reverse scan reuses.  The states are the one entering every
- * chunk, except for bf16 IO with at most 4 lanes per head (the training
- * default): there only the state entering every 256-token segment is kept,
- * and the backward recomputes the others from the net writes (checkpointed
- * form). */
+ * chunk, except for bf16 IO with 32-token chunks and at most 4 lanes per head
+ * (the training default): there only the state entering every 256-token
+ * segment is kept, and the backward recomputes the others from the net
+ * writes (checkpointed form). */
 long long gdnx_delta_chunk_states_bytes(int B, int T, int H, int M, int head_dim, int chunk,
                                         int dtype);
 
 /* Bytes of the backward's workspace for the given chunk (0 = train default;
- * -1 if invalid): the state gradients leaving every chunk (every 256-token
- * segment in the checkpointed form) and dB = T^T dR of every chunk, laid out
- * as the forward's stash, then (checkpointed form) the gradient kernel's
- * float32 sums of dq, dk and dv over the lanes processed so far, 3 x 256 x
- * head_dim floats per (batch, head, segment).  New in ABI 11: before it the
- * workspace was gdnx_delta_chunk_states_bytes bytes, which the per-chunk
- * form still satisfies. */
+ * -1 if invalid, or beyond 2^30 chains or 2^40 token-chains): the state
+ * gradients leaving every chunk (every 256-token segment in the checkpointed
+ * form) and dB = T^T dR of every chunk, laid out as the forward's stash; in
+ * the checkpointed form then P3 = R dS^T of every chunk (bf16, the gradient
+ * kernel's dk tile layout) and k.P3 per token (float32), and with more than
+ * two lanes per head the gradient kernel's float32 carry of the dq, dk and dv
+ * sums between lane pairs, 3 x 256 x head_dim floats per (batch, head,
+ * segment).  Changed in ABI 12 (P3 and k.P3 added): query it, do not cache
+ * sizes across versions. */
 long long gdnx_delta_bwd_workspace_bytes(int B, int T, int H, int M, int head_dim, int chunk,
                                          int dtype);
 
@@ -159,11 +161,12 @@ int gdnx_delta_chunk_bwd(const void* q, const void* k, const void* v,
 /* The two stages of gdnx_delta_chunk_bwd, callable separately (e.g. to
  * time or overlap them).  Stage 1 runs the reverse state scan on the
  * forward's chunk operands (in chunk_states) and fills workspace with dS at
- * every chunk end (every segment end in the checkpointed form) and dB (plus
- * dstate0); stage 2 reads the forward's chunk_states and that workspace and
- * writes every input gradient (in the checkpointed form it also uses the
- * workspace's float32 tail as scratch, so the workspace is not const since
- * ABI 11).  Same arguments and layouts as gdnx_delta_chunk_bwd. */
+ * every chunk end (every segment end in the checkpointed form), dB and, in
+ * the checkpointed form, P3 and k.P3 (plus dstate0); stage 2 reads the
+ * forward's chunk_states and that workspace and writes every input gradient
+ * (in the checkpointed form it also uses the workspace's float32 tail as the
+ * lane pairs' carry, so the workspace is not const).  Same arguments and
+ * layouts as gdnx_delta_chunk_bwd. */
 int gdnx_delta_chunk_bwd_state(const void* q, const void* k, const float* a_e,
                                const float* log_g, const void* dy, const float* dstate_out,
                                const void* chunk_states, void* workspace, float* dstate0,
