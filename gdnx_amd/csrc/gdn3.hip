@@ -1945,22 +1945,11 @@ __global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
     for (int e = tid; e < Rn; e += kNT) p.B_out[(size_t)chain * Rn + e] = sm.ab[Rm + e] * dk;
 }
 
+// One chain's compaction; bi indexes the statistics (the chain's row in the
+// launch).
 template <int D, int P, typename CT>
-__global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
-  __shared__ G3CompactSmem<D, P> sm;
-  static_assert(sizeof(G3CompactSmem<D, P>) <= 160 * 1024, "LDS budget");
-  const int tid = threadIdx.x;
-  int chain = blockIdx.x;
-  if (p.pos) {   // decode batch: only the rows whose token closes a compaction interval
-    const int row = blockIdx.x / p.hm;
-    const int pos = p.pos[row];
-    if (pos < 0 || (pos + 1) % p.Kc != 0) return;   // (a negative position is an empty row)
-    if (p.slots) {
-      const int sl = p.slots[row];
-      if (sl < 0 || sl >= p.nslots) return;
-      chain = sl * p.hm + blockIdx.x % p.hm;
-    }
-  }
+__device__ __forceinline__ void compact_chain(const G3CompactArgs& p, G3CompactSmem<D, P>& sm, int chain, int bi,
+                                              int tid) {
   typedef G3D<D> Ge;
   constexpr int Rm = Ge::R * Ge::m, Rn = Ge::R * Ge::n;
   for (int e = tid; e < Rm; e += kNT) sm.ab[e] = p.A[(size_t)chain * Rm + e];
@@ -1970,7 +1959,7 @@ __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
   __syncthreads();
   const int qs = p.mode ? Ge::R : Ge::q;   // sketch columns
   g3_compact<D, P>(sm.k, sm.ab, p.U + cb, p.Vb + cb, (size_t)p.u_sp, (size_t)p.u_sd, gacc, p.sdec, p.sketch + (size_t)chain * Ge::n * qs,
-                   p.stats ? p.stats + (size_t)blockIdx.x * 2 : nullptr, tid, p.mode);
+                   p.stats ? p.stats + (size_t)bi * 2 : nullptr, tid, p.mode);
   for (int e = tid; e < Rm; e += kNT) {
     p.A_out[(size_t)chain * Rm + e] = sm.ab[e];
     if (p.A_fin) p.A_fin[(size_t)chain * Rm + e] = sm.ab[e];
@@ -1982,6 +1971,49 @@ __global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
   if (p.ab_stash)
     for (int e = tid; e < Rm + Rn; e += kNT) p.ab_stash[(size_t)chain * (Rm + Rn) + e] = sm.ab[e];
   if (p.skron) write_skron<D, CT>((CT*)p.skron + (size_t)chain * D * D, sm.ab, sm.ab + Rm, tid);
+}
+
+template <int D, int P, typename CT>
+__global__ void __launch_bounds__(kNT) gdn3_compact_kernel(G3CompactArgs p) {
+  __shared__ G3CompactSmem<D, P> sm;
+  static_assert(sizeof(G3CompactSmem<D, P>) <= 160 * 1024, "LDS budget");
+  const int tid = threadIdx.x;
+  if (!p.pos) {
+    compact_chain<D, P, CT>(p, sm, blockIdx.x, blockIdx.x, tid);
+    return;
+  }
+  // decode batch: only the rows whose token closes a compaction interval.
+  // The chains are strided over a grid of at most kDecCompactGrid
+  // workgroups; a workgroup's threads check up to kNT of its chains at once
+  // and list those that compact (the order of the list does not matter:
+  // the chains are independent), so a step that closes no interval costs
+  // one round of position reads.
+  __shared__ int todo[kNT];
+  __shared__ int ntodo;
+  const int K = (p.N - (int)blockIdx.x + (int)gridDim.x - 1) / (int)gridDim.x;   // this workgroup's chains
+  for (int base = 0; base < K; base += kNT) {
+    if (tid == 0) ntodo = 0;
+    __syncthreads();
+    if (base + tid < K) {
+      const int bi = blockIdx.x + (base + tid) * gridDim.x;
+      const int row = bi / p.hm;
+      const int pos = p.pos[row];
+      bool go = pos >= 0 && (pos + 1) % p.Kc == 0;   // (a negative position is an empty row)
+      if (go && p.slots) {
+        const int sl = p.slots[row];
+        go = sl >= 0 && sl < p.nslots;
+      }
+      if (go) todo[atomicAdd(&ntodo, 1)] = bi;
+    }
+    __syncthreads();
+    const int n = ntodo;
+    for (int i = 0; i < n; ++i) {
+      const int bi = todo[i];
+      const int chain = p.slots ? p.slots[bi / p.hm] * p.hm + bi % p.hm : bi;
+      compact_chain<D, P, CT>(p, sm, chain, bi, tid);
+      __syncthreads();   // the chain's last LDS reads before the next one's loads
+    }
+  }
 }
 
 // The carried state (A0, B0, U0, Vb0 in the output layouts) in the window
@@ -2066,12 +2098,16 @@ __global__ void __launch_bounds__(kNT) kron_read_kernel(KronReadArgs p) {
   }
 }
 
+// Workgroups of a decode batch's compaction launch (grid-stride over chains).
+constexpr int kDecCompactGrid = 2048;
+
 template <int D, int P>
 int launch_compact(const G3CompactArgs& a, hipStream_t stream) {
+  const int grid = a.pos ? (a.N < kDecCompactGrid ? a.N : kDecCompactGrid) : a.N;
   if (a.skron && a.skron_dtype == GDNX_DTYPE_BF16)
-    hipLaunchKernelGGL((gdn3_compact_kernel<D, P, bf16>), dim3(a.N), dim3(kNT), 0, stream, a);
+    hipLaunchKernelGGL((gdn3_compact_kernel<D, P, bf16>), dim3(grid), dim3(kNT), 0, stream, a);
   else
-    hipLaunchKernelGGL((gdn3_compact_kernel<D, P, float>), dim3(a.N), dim3(kNT), 0, stream, a);
+    hipLaunchKernelGGL((gdn3_compact_kernel<D, P, float>), dim3(grid), dim3(kNT), 0, stream, a);
   return check_launch("gdn3_compact_kernel");
 }
 
