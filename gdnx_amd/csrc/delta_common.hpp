@@ -258,11 +258,13 @@ __device__ __forceinline__ void tile_commit(const TileRegs& r, CT* nat, CT* tr, 
   if (tr) {
     if constexpr (sizeof(CT) == 2) {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int w = e >> 1, sh = (e & 1) * 16;
-        const unsigned a0 = (word_of(r.x[0], w) >> sh) & 0xffffu, a1 = (word_of(r.x[1], w) >> sh) & 0xffffu;
-        const unsigned a2 = (word_of(r.x[2], w) >> sh) & 0xffffu, a3 = (word_of(r.x[3], w) >> sh) & 0xffffu;
-        *(uint2*)&tr[(dg * VEC + e) * LDC + 4 * tg] = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
+      for (int w = 0; w < 4; ++w) {   // (byte permutes as in Stage::commit_tr)
+        const unsigned r0 = word_of(r.x[0], w), r1 = word_of(r.x[1], w);
+        const unsigned r2 = word_of(r.x[2], w), r3 = word_of(r.x[3], w);
+        *(uint2*)&tr[(dg * VEC + 2 * w) * LDC + 4 * tg] =
+            make_uint2(__builtin_amdgcn_perm(r1, r0, 0x05040100u), __builtin_amdgcn_perm(r3, r2, 0x05040100u));
+        *(uint2*)&tr[(dg * VEC + 2 * w + 1) * LDC + 4 * tg] =
+            make_uint2(__builtin_amdgcn_perm(r1, r0, 0x07060302u), __builtin_amdgcn_perm(r3, r2, 0x07060302u));
       }
     } else {
 #pragma unroll
@@ -530,11 +532,9 @@ template <int LD>
 __device__ __forceinline__ void unit_commit_rows(bf16* dst, const uint4& x, TileUnit t) {
   const unsigned w[4] = {x.x, x.y, x.z, x.w};   // x.x, x.y: column col, tokens 0..3; x.z, x.w: column col + 1
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const unsigned a = (w[i >> 1] >> ((i & 1) * 16)) & 0xffffu;
-    const unsigned b = (w[2 + (i >> 1)] >> ((i & 1) * 16)) & 0xffffu;
-    *(unsigned*)&dst[(t.tok + i) * LD + t.col] = a | (b << 16);
-  }
+  for (int i = 0; i < 4; ++i)   // token i: the low (even i) or high half of each column's word, one byte permute
+    *(unsigned*)&dst[(t.tok + i) * LD + t.col] =
+        __builtin_amdgcn_perm(w[2 + (i >> 1)], w[i >> 1], (i & 1) ? 0x07060302u : 0x05040100u);
 }
 // Sum of x over the four 16-lane rows of the wave, in every lane (gfx950
 // permlane swaps: lane l is added to l ^ 16, then to l ^ 32).
@@ -640,12 +640,18 @@ struct Stage {
       if (!owns(tid, u)) continue;
       const int e = tid + u * NTH, rg = e / CG, cg = e % CG;
       if constexpr (sizeof(CT) == 2) {
+        // word w of a row holds columns 2 w (low half) and 2 w + 1 (high
+        // half); one byte permute pairs the halves of two rows
+        // (v_perm_b32: selector bytes 0-3 pick the second operand's bytes,
+        // 4-7 the first's)
 #pragma unroll
-        for (int c = 0; c < 8; ++c) {
-          const int w = c >> 1, sh = (c & 1) * 16;
-          const unsigned a0 = (word_of(x[u][0], w) >> sh) & 0xffffu, a1 = (word_of(x[u][1], w) >> sh) & 0xffffu;
-          const unsigned a2 = (word_of(x[u][2], w) >> sh) & 0xffffu, a3 = (word_of(x[u][3], w) >> sh) & 0xffffu;
-          *(uint2*)&dst[(cg * VEC + c) * LD + 4 * rg] = make_uint2(a0 | (a1 << 16), a2 | (a3 << 16));
+        for (int w = 0; w < 4; ++w) {
+          const unsigned r0 = word_of(x[u][0], w), r1 = word_of(x[u][1], w);
+          const unsigned r2 = word_of(x[u][2], w), r3 = word_of(x[u][3], w);
+          *(uint2*)&dst[(cg * VEC + 2 * w) * LD + 4 * rg] =
+              make_uint2(__builtin_amdgcn_perm(r1, r0, 0x05040100u), __builtin_amdgcn_perm(r3, r2, 0x05040100u));
+          *(uint2*)&dst[(cg * VEC + 2 * w + 1) * LD + 4 * rg] =
+              make_uint2(__builtin_amdgcn_perm(r1, r0, 0x07060302u), __builtin_amdgcn_perm(r3, r2, 0x07060302u));
         }
       } else {
 #pragma unroll

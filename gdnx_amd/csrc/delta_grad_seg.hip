@@ -175,7 +175,9 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
   const int N = BH * M;
   const int t_seg = s * kSegTokens;
   const int nsub = min(Sd::NSUB, (p.T - t_seg + C - 1) / C);
-  const int CS = p.C;   // the scans' chunk: the stash's record length (the sub-chunk, checked at dispatch)
+  // the scans' chunk, which is the stash's record length and the sub-chunk
+  // (dispatch rejects any other p.C), so record offsets are shifts
+  constexpr int CS = C;
   const StashGeom sg = stash_geom(N, p.T, D, CS, p.cps);
   const bf16* sck = (const bf16*)p.s_stash;   // state records, then the net writes R
   const bf16* rst = sck + sg.states;
@@ -217,7 +219,8 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
   // here uses a loaded value: the scalars are issued first and masked at
   // commit, and the tiles stay in flight through the next step.
   auto fetch_step = [&](Pf& f, int j, int tid) {
-    const int c = j / ML, m = mb + j % ML;
+    static_assert(kRes == 2, "one or two resident lanes: step j splits by a shift");
+    const int c = ML == 2 ? j >> 1 : j, m = mb + (ML == 2 ? (j & 1) : 0);
     const int t0 = t_seg + c * C;
     if (wave == SCW) {
       const int lane = tid & 63, cs = t0 / CS, jj = (t0 % CS) / C;
@@ -435,19 +438,20 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
         }
       }
       if (wave == SW) {
-        // da_w = dB.v per token (lane: token lane % 32, values (lane / 32) D / 2 ..)
-        const int tok = lane & 31, h0 = (lane >> 5) * (D / 2);
-        float x = 0.f;
+        // da_w = dB.v per token: the diagonals of the two 16 x 16 tiles of
+        // dB V^T on MFMA (at D = 128 the scalar wave has no C x C tile
+        // task; the staging wave, which has none either, measured slower
+        // with it).  Lane (g, n)
+        // holds rows 4 g .. 4 g + 3 of column n, so the diagonal entry of
+        // token 16 it + n sits in lane (n / 4, n) at row n % 4.
 #pragma unroll
-        for (int d0 = 0; d0 < D / 2; d0 += 8) {
-          const bf16x8 xb = *(const bf16x8*)&L.dx[tok * LDD + h0 + d0];
-          const bf16x8 vb = *(const bf16x8*)&sm.v[tok * LDD + h0 + d0];
-#pragma unroll
-          for (int e = 0; e < 8; ++e) x += (float)xb[e] * (float)vb[e];
+        for (int it = 0; it < NCT; ++it) {
+          const f32x4 acc = tile_nt_pf<D>(&L.dx[(it * 16 + n16) * LDD], &sm.v[(it * 16 + n16) * LDD], g4);
+          const int ii = n16 & 3;
+          const float x = ii == 0 ? acc[0] : ii == 1 ? acc[1] : ii == 2 ? acc[2] : acc[3];
+          const int t = t_seg + c * C + it * 16 + n16;
+          if ((n16 >> 2) == g4 && t < p.T) p.daw[(((size_t)b * p.T + t) * p.H + h) * M + m] = x;
         }
-        x += __shfl_xor(x, 32, 64);
-        const int t = t_seg + c * C + tok;
-        if (lane < C && t < p.T) p.daw[(((size_t)b * p.T + t) * p.H + h) * M + m] = x;
       }
       // ---- dAq = dY R^T (j <= i) and dL = -dB R^T (j < i) on this wave's
       // C x C tile tasks: the lane sums dQK, dKK and the per-token terms ----
