@@ -538,6 +538,9 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
       }
     }
     __syncthreads();   // every lane's tile tasks and sums done
+    // the next sub-chunk's q / k / v, in flight through the epilogue (every
+    // wave is past its last read of this sub-chunk's row tiles)
+    if (c + 1 < nsub) fetch_sub(spf, c + 1, tid);
     if (wave == SW) scalars(c, mb + ML - 1, (c * ML + ML - 1) % 3);
 #pragma unroll
     for (int jj = 0; jj < NTASK; ++jj) {
@@ -605,7 +608,6 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
       }
     }
     if (c + 1 < nsub) {
-      fetch_sub(spf, c + 1, tid);
       __syncthreads();   // every wave done with this sub-chunk's q / k / v tiles
       commit_sub(spf, tid);
     }
