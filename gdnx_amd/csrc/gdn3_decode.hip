@@ -15,12 +15,16 @@
 // gdnx_gdn3_compact on those rows' chains (a second launch that returns at
 // once for the other rows).
 //
-// HBM-bound: a chain reads its 21.5 KB state (d = 128, P = 16) and writes
-// back A, B, Vb (decayed) and one column of U.  One 256-thread block per
-// chain stages the state in LDS with 16-byte loads (non-temporal for the
-// parts rewritten in full), forms the two reads S h, S q from LDS
-// (Vb^T x as per-slot partial sums folded across lanes, the Kronecker part as
+// A chain reads its 21.5 KB state (d = 128, P = 16) and writes back A, B,
+// Vb (decayed) and one column of U.  One 256-thread block per chain stages
+// the state in LDS with 16-byte loads (non-temporal for the parts rewritten
+// in full), forms the two reads S h, S q from LDS (Vb^T x as per-slot
+// partial sums over d ranges reduced across lanes, the Kronecker part as
 // A_r X, then (A_r X) B_r^T), and writes from the registers it loaded.
+// Every product reads its LDS operands as 16-byte vectors and keeps four
+// outputs per thread, so the LDS traffic per chain stays a few times the
+// state's size (with scalar reads the block was bound by LDS bandwidth,
+// not by HBM).
 #include "gdn3_common.hpp"
 #include "gdnx_common.hpp"
 #include "gdnx_internal.hpp"
@@ -33,24 +37,45 @@ constexpr int kDT = 256;   // threads per chain
 template <int D, int P>
 struct G3DecSmem {
   typedef G3D<D> Ge;
+  static constexpr int LDP = P + 4;   // U / Vb row length: 16-byte aligned rows, 16 lanes' rows on distinct banks
   float A[Ge::R * Ge::m];          // gamma A   [R][a_v][a_k]
   float B[Ge::R * Ge::n];          // gamma B   [R][b_v][b_k]
-  float U[D][P + 1];               // U [d][slot] (padded: column reads spread over banks)
-  float V[D][P + 1];               // gamma Vb
+  float U[D][LDP];                 // U [d][slot]
+  float V[D][LDP];                 // gamma Vb
   float x[2][D];                   // h, q
   float k[D], u[D];
   float ax[2][Ge::R][Ge::av][Ge::bk];   // A_r X for X = h, q
   float coef[2][P];                // (gamma Vb)^T h, (gamma Vb)^T q
+  float sx[2][D];                  // S h, S q
   float red[2];                    // k.h, k.q
 };
+
+// Sum over aligned groups of N consecutive lanes (N = 1 .. 32), in every
+// lane of the group: DPP quad permutes, half-row and row mirrors, then the
+// 16-lane row swap.
+template <int N>
+__device__ __forceinline__ float group_sum(float x) {
+  static_assert(N == 1 || N == 2 || N == 4 || N == 8 || N == 16 || N == 32, "power-of-two group up to 32");
+  if constexpr (N >= 2) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0xB1, 0xf, 0xf, false));
+  if constexpr (N >= 4) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x4E, 0xf, 0xf, false));
+  if constexpr (N >= 8) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x141, 0xf, 0xf, false));
+  if constexpr (N >= 16) x += __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), 0x140, 0xf, 0xf, false));
+  if constexpr (N >= 32) {
+    const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    x = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  }
+  return x;
+}
 
 template <typename IO, int D, int P>
 __global__ void __launch_bounds__(kDT) gdn3_decode_kernel(G3DecArgs p) {
   typedef G3D<D> Ge;
-  constexpr int RM = Ge::R * Ge::m, RN = Ge::R * Ge::n, DP = D * P;
+  typedef G3DecSmem<D, P> Sm;
+  constexpr int RM = Ge::R * Ge::m, RN = Ge::R * Ge::n, DP = D * P, LDP = Sm::LDP;
   constexpr int NA = (RM / 4 + kDT - 1) / kDT, NB = (RN / 4 + kDT - 1) / kDT, NU = (DP / 4 + kDT - 1) / kDT;
   static_assert(RM % 4 == 0 && RN % 4 == 0 && DP % 4 == 0 && P % 4 == 0, "16-byte units");
-  __shared__ G3DecSmem<D, P> sm;
+  static_assert(Ge::ak % 4 == 0 && Ge::bk % 4 == 0 && 2 * D <= kDT && D % 64 == 0, "decode geometry");
+  __shared__ __attribute__((aligned(16))) Sm sm;
 
   const int tid = threadIdx.x;
   const int hm = p.H * p.M;
@@ -116,76 +141,80 @@ __global__ void __launch_bounds__(kDT) gdn3_decode_kernel(G3DecArgs p) {
     if (tid + j * kDT < DP / 4) {
       const int e = 4 * (tid + j * kDT), d = e / P, s0 = e % P;
       rv[j] *= gam;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) {
-        sm.U[d][s0 + s] = ru[j][s];
-        sm.V[d][s0 + s] = rv[j][s];
-      }
+      *(f32x4*)&sm.U[d][s0] = ru[j];
+      *(f32x4*)&sm.V[d][s0] = rv[j];
     }
   __syncthreads();
 
-  // k.h and k.q (wave 0); Vb^T h, Vb^T q as per-slot partials over d ranges
-  // folded across the lanes that share a slot; A_r X
+  // k.h and k.q (wave 0)
   if (tid < 64) {
     float kh = 0.f, kq = 0.f;
     for (int d = tid; d < D; d += 64) {
       kh += sm.k[d] * sm.x[0][d];
       kq += sm.k[d] * sm.x[1][d];
     }
-#pragma unroll
-    for (int off = 32; off > 0; off >>= 1) {
-      kh += __shfl_xor(kh, off, 64);
-      kq += __shfl_xor(kq, off, 64);
-    }
+    kh = wave_sum(kh);
+    kq = wave_sum(kq);
     if (tid == 0) {
       sm.red[0] = kh;
       sm.red[1] = kq;
     }
   }
+  // Vb^T h, Vb^T q: a group of TPC lanes per (vector, 4 slots), lane `part`
+  // summing rows d = part, part + TPC, ... (consecutive lanes read
+  // consecutive rows), then the group's sum
   {
-    constexpr int TPO = kDT / (2 * P);          // threads per (vector, slot) output
-    static_assert(TPO >= 1 && (TPO & (TPO - 1)) == 0 && TPO <= 64 && D % TPO == 0, "coef split");
-    const int o = tid / TPO, part = tid % TPO, xi = o / P, s = o % P;
-    float acc = 0.f;
-    for (int d = part; d < D; d += TPO) acc += sm.V[d][s] * sm.x[xi][d];
+    constexpr int NCB = 2 * (P / 4);           // (vector, slot quad) combinations
+    constexpr int TPC = kDT / NCB;             // lanes per combination
+    static_assert(TPC >= 1 && TPC <= 32 && (TPC & (TPC - 1)) == 0 && D % TPC == 0, "coef split");
+    const int cb = tid / TPC, part = tid % TPC, xi = cb / (P / 4), s0 = 4 * (cb % (P / 4));
+    f32x4 acc = zero4();
+#pragma unroll 4
+    for (int d = part; d < D; d += TPC) acc += *(const f32x4*)&sm.V[d][s0] * sm.x[xi][d];
 #pragma unroll
-    for (int off = 1; off < TPO; off <<= 1) acc += __shfl_xor(acc, off, 64);
-    if (part == 0) sm.coef[xi][s] = acc;
+    for (int e = 0; e < 4; ++e) acc[e] = group_sum<TPC>(acc[e]);
+    if (part == 0) *(f32x4*)&sm.coef[xi][s0] = acc;
   }
+  // (A_r X)[iv][jb] = sum_ik A_r[iv][ik] x[ik b_k + jb], four jb per thread
   {
-    // (A_r X)[iv][jb] = sum_ik A_r[iv][ik] x[ik b_k + jb]
-    constexpr int NO = 2 * Ge::R * Ge::av * Ge::bk;
-    for (int o = tid; o < NO; o += kDT) {
-      const int jb = o % Ge::bk, iv = (o / Ge::bk) % Ge::av, r = (o / (Ge::bk * Ge::av)) % Ge::R,
-                xi = o / (Ge::bk * Ge::av * Ge::R);
+    constexpr int JG = Ge::bk / 4, NO4 = 2 * Ge::R * Ge::av * JG;
+#pragma unroll 1
+    for (int o = tid; o < NO4; o += kDT) {
+      const int jg = o % JG, iv = (o / JG) % Ge::av, r = (o / (JG * Ge::av)) % Ge::R, xi = o / (JG * Ge::av * Ge::R);
       const float* ar = &sm.A[r * Ge::m + iv * Ge::ak];
-      float acc = 0.f;
+      const float* xr = &sm.x[xi][4 * jg];
+      f32x4 acc = zero4();
 #pragma unroll
-      for (int ik = 0; ik < Ge::ak; ++ik) acc += ar[ik] * sm.x[xi][ik * Ge::bk + jb];
-      sm.ax[xi][r][iv][jb] = acc;
+      for (int i4 = 0; i4 < Ge::ak; i4 += 4) {
+        const f32x4 a4 = *(const f32x4*)&ar[i4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc += a4[e] * *(const f32x4*)&xr[(i4 + e) * Ge::bk];
+      }
+      *(f32x4*)&sm.ax[xi][r][iv][4 * jg] = acc;
     }
   }
   __syncthreads();
 
-  // S x at d = iv b_v + jv: sum_r sum_jb (A_r X)[iv][jb] B_r[jv][jb] + sum_p U[d][p] coef[p]
+  // (S x)[d] at d = iv b_v + jv, one thread per (x, d):
+  // sum_r sum_jb (A_r X)[iv][jb] B_r[jv][jb] + sum_p U[d][p] coef[p]
+  if (tid < 2 * D) {
+    const int xi = tid / D, d = tid % D, iv = d / Ge::bv, jv = d % Ge::bv;
+    f32x4 acc = zero4();
+#pragma unroll
+    for (int r = 0; r < Ge::R; ++r)
+#pragma unroll
+      for (int j4 = 0; j4 < Ge::bk; j4 += 4)
+        acc += *(const f32x4*)&sm.ax[xi][r][iv][j4] * *(const f32x4*)&sm.B[r * Ge::n + jv * Ge::bk + j4];
+#pragma unroll
+    for (int s4 = 0; s4 < P; s4 += 4) acc += *(const f32x4*)&sm.U[d][s4] * *(const f32x4*)&sm.coef[xi][s4];
+    sm.sx[xi][d] = (acc[0] + acc[1]) + (acc[2] + acc[3]);
+  }
+  __syncthreads();
   const float c = sm.red[0], kq = sm.red[1];
   const float alpha = stable_alpha_f(c);
   for (int d = tid; d < D; d += kDT) {
-    const int iv = d / Ge::bv, jv = d % Ge::bv;
-    float sx[2];
-#pragma unroll
-    for (int xi = 0; xi < 2; ++xi) {
-      float acc = 0.f;
-#pragma unroll
-      for (int r = 0; r < Ge::R; ++r)
-#pragma unroll
-        for (int jb = 0; jb < Ge::bk; ++jb) acc += sm.ax[xi][r][iv][jb] * sm.B[r * Ge::n + jv * Ge::bk + jb];
-#pragma unroll
-      for (int s = 0; s < P; ++s) acc += sm.U[d][s] * sm.coef[xi][s];
-      sx[xi] = acc;
-    }
-    const float r = sm.u[d] - sx[0];
-    yg[d] = from_f<IO>(sx[1] + alpha * kq * r);
+    const float r = sm.u[d] - sm.sx[0][d];
+    yg[d] = from_f<IO>(sm.sx[1][d] + alpha * kq * r);
     Ug[(size_t)d * P + slot] = alpha * r;    // the new write; the rest of U is unchanged
   }
   // decayed factors and keys back, the token's key in its slot
