@@ -171,13 +171,13 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
     Frag Sf[NDT / TPS];
 #pragma unroll
     for (int kb = 0; kb < NDT / TPS; ++kb) Sf[kb] = acc_frag((CT*)nullptr, S[kb * TPS], S[kb * TPS + TPS - 1]);
-    if constexpr (STASH) {
-      // the state entering every cps-th chunk (record c / cps); at other
-      // chunks the stores go through an empty buffer range and are dropped,
-      // so the loop carries no branch around a store
+    if (STASH && c % p.cps == 0) {
+      // the state entering every cps-th chunk (record c / cps), behind a
+      // branch: stores to an empty buffer range at the other chunks would
+      // still cost their issue (measured 11 us of the scan at config 2)
       const size_t srec = (size_t)(c / p.cps) * nchains + chain;
       const __amdgpu_buffer_rsrc_t sr =
-          buf_rsrc((CT*)p.chunk_states + srec * (D * D), c % p.cps == 0 ? (unsigned)(D * D * sizeof(CT)) : 0u);
+          buf_rsrc((CT*)p.chunk_states + srec * (D * D), (unsigned)(D * D * sizeof(CT)));
 #pragma unroll
       for (int dt = 0; dt < NDT; ++dt)
         buf_store4(sr, (unsigned)(stash_tile_offset<CT, D>(dt, V, lane) * sizeof(CT)), (const CT*)nullptr, S[dt][0],
@@ -443,7 +443,9 @@ __global__ void __launch_bounds__(64 * NWV) __attribute__((amdgpu_waves_per_eu(2
     }
     {
       // the state gradient leaving every cps-th chunk and the last one
-      // (record c / cps); other chunks' stores are dropped (empty range)
+      // (record c / cps); other chunks' stores are dropped (empty range),
+      // so the loop carries no branch around a store (here a branch
+      // measured slower)
       const size_t srec = (size_t)(c / p.cps) * nchains + chain;
       const bool keep = c % p.cps == p.cps - 1 || c == NC - 1;
       const __amdgpu_buffer_rsrc_t sr =
