@@ -347,75 +347,90 @@ __device__ __forceinline__ void chunk_grams(const CT* sk, const CT* sq, float* s
   }
 }
 
-#ifndef GDNX_INV_MARK
-#define GDNX_INV_MARK(k)
-#endif
+// Diagonal block b of T = (I + L)^-1, one column per thread: forward
+// substitution of column `col` of the unit-lower 16x16 block whose
+// transpose sits in sLT (rows 16 b .. 16 b + 15, row length 20).
+// Right-looking: after step j, x_j is final; row j of the transposed block
+// holds L[16b+i][16b+j] for all i.  Rows are loaded PF steps ahead so each
+// step's LDS latency overlaps earlier steps' FMAs.  Writes the column to
+// sTd and emits it (x[i] == 0 for i < col).
+template <typename Emit, typename F>
+__device__ __forceinline__ void diag_block_inverse(const float* sLT, float* sTd, int b, int col, F f, Emit emit) {
+  float x[16];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) x[i] = (i == col) ? 1.f : 0.f;
+  constexpr int PF = 4;
+  f32x4 win[PF][4];
+#pragma unroll
+  for (int r = 0; r < PF; ++r)
+#pragma unroll
+    for (int q = 0; q < 4; ++q) win[r][q] = *(const f32x4*)&sLT[(16 * b + r) * 20 + 4 * q];
+#pragma unroll
+  for (int j = 0; j < 15; ++j) {
+    f32x4 c4[4];
+#pragma unroll
+    for (int q = 0; q < 4; ++q) c4[q] = win[j % PF][q];
+    if (j + PF < 15) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q) win[j % PF][q] = *(const f32x4*)&sLT[(16 * b + j + PF) * 20 + 4 * q];
+    }
+#pragma unroll
+    for (int i = j + 1; i < 16; ++i) x[i] -= c4[i >> 2][i & 3] * x[j];
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    sTd[(16 * b + i) * 20 + col] = x[i];
+    emit(16 * b + i, 16 * b + col, x[i], f);
+  }
+}
+
+// Block column jb of T below the diagonal, by one wave, from L (row length
+// C + 4) and the diagonal blocks of T (sTd): T_ib,jb = -T_ib,ib sum_kb
+// L_ib,kb T_kb,jb on fp32 MFMA.
+template <int C, typename Emit, typename F>
+__device__ __forceinline__ void offdiag_block_column(const float* sL, const float* sTd, int jb, int lane, F f,
+                                                     Emit emit) {
+  constexpr int NCT = C / 16, LDF = C + 4;
+  const int g4 = lane >> 4, n16 = lane & 15;
+  f32x4 Tk[NCT];
+  // T_jj as a B fragment: lane (g, n) holds T_jj[4g+s][n]
+#pragma unroll
+  for (int s = 0; s < 4; ++s) Tk[jb][s] = sTd[(16 * jb + 4 * g4 + s) * 20 + n16];
+#pragma unroll
+  for (int ib = jb + 1; ib < NCT; ++ib) {
+    f32x4 X = zero4();
+#pragma unroll
+    for (int kb = jb; kb < ib; ++kb) {
+      const f32x4 a = *(const f32x4*)&sL[(16 * ib + n16) * LDF + 16 * kb + 4 * g4];
+      mma(X, a, Tk[kb]);
+    }
+    const f32x4 a = *(const f32x4*)&sTd[(16 * ib + n16) * 20 + 4 * g4];
+    f32x4 Y = zero4();
+    mma(Y, a, X);
+    Tk[ib] = -Y;
+#pragma unroll
+    for (int s = 0; s < 4; ++s) emit(16 * ib + 4 * g4 + s, 16 * jb + n16, Tk[ib][s], f);
+  }
+}
+
+// T = (I + L)^-1 of one unit-lower C x C matrix by the whole workgroup:
+// the diagonal blocks by waves 0 .. NCT - 1 (16 lanes each), then block
+// column jb by wave jb.
 template <int C, typename ColPrep, typename Emit>
 __device__ __forceinline__ void invert_unit_lower(const float* sL, const float* sLT, float* sTd, int wave,
                                                   int lane, ColPrep colprep, Emit emit) {
-  constexpr int NCT = C / 16, LDF = C + 4;
-  const int g4 = lane >> 4, n16 = lane & 15;
+  constexpr int NCT = C / 16;
+  const int n16 = lane & 15;
   if (wave < NCT && lane < 16) {
-    const int b = wave, col = lane;
-    float x[16];
-#pragma unroll
-    for (int i = 0; i < 16; ++i) x[i] = (i == col) ? 1.f : 0.f;
-    // right-looking: after step j, x_j is final; row j of the transposed
-    // block holds L[16b+i][16b+j] for all i.  Rows are loaded PF steps ahead
-    // so each step's LDS latency overlaps earlier steps' FMAs.
-    constexpr int PF = 4;
-    f32x4 win[PF][4];
-#pragma unroll
-    for (int r = 0; r < PF; ++r)
-#pragma unroll
-      for (int q = 0; q < 4; ++q) win[r][q] = *(const f32x4*)&sLT[(16 * b + r) * 20 + 4 * q];
-#pragma unroll
-    for (int j = 0; j < 15; ++j) {
-      f32x4 c4[4];
-#pragma unroll
-      for (int q = 0; q < 4; ++q) c4[q] = win[j % PF][q];
-      if (j + PF < 15) {
-#pragma unroll
-        for (int q = 0; q < 4; ++q) win[j % PF][q] = *(const f32x4*)&sLT[(16 * b + j + PF) * 20 + 4 * q];
-      }
-#pragma unroll
-      for (int i = j + 1; i < 16; ++i) x[i] -= c4[i >> 2][i & 3] * x[j];
-    }
-    GDNX_INV_MARK(0);
-    const auto f = colprep(16 * b + col);
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      sTd[(16 * b + i) * 20 + col] = x[i];
-      emit(16 * b + i, 16 * b + col, x[i], f);   // x[i] == 0 for i < col
-    }
-    GDNX_INV_MARK(1);
+    const auto f = colprep(16 * wave + lane);
+    diag_block_inverse(sLT, sTd, wave, lane, f, emit);
   }
   __syncthreads();
-  GDNX_INV_MARK(2);
 #pragma unroll
   for (int jb = 0; jb < NCT - 1; ++jb) {
     if (wave != jb) continue;   // block column jb (compile-time, so Tk stays in registers)
     const auto f = colprep(16 * jb + n16);
-    f32x4 Tk[NCT];
-    // T_jj as a B fragment: lane (g, n) holds T_jj[4g+s][n]
-#pragma unroll
-    for (int s = 0; s < 4; ++s) Tk[jb][s] = sTd[(16 * jb + 4 * g4 + s) * 20 + n16];
-#pragma unroll
-    for (int ib = jb + 1; ib < NCT; ++ib) {
-      f32x4 X = zero4();
-#pragma unroll
-      for (int kb = jb; kb < ib; ++kb) {
-        const f32x4 a = *(const f32x4*)&sL[(16 * ib + n16) * LDF + 16 * kb + 4 * g4];
-        mma(X, a, Tk[kb]);
-      }
-      const f32x4 a = *(const f32x4*)&sTd[(16 * ib + n16) * 20 + 4 * g4];
-      f32x4 Y = zero4();
-      mma(Y, a, X);
-      Tk[ib] = -Y;
-#pragma unroll
-      for (int s = 0; s < 4; ++s) emit(16 * ib + 4 * g4 + s, 16 * jb + n16, Tk[ib][s], f);
-    }
-    GDNX_INV_MARK(3);
+    offdiag_block_column<C>(sL, sTd, jb, lane, f, emit);
   }
 }
 

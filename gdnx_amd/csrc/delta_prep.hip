@@ -12,25 +12,43 @@
 // KMD-2 chunk derivation gdn3/kmd2_fast_scan.py:1-18, with the decay ratios
 // prefix_i / prefix_j replaced by log-space differences, which never
 // underflow).  One workgroup per (b, h, chunk): the raw grams K K^T and
-// Q K^T are formed once on MFMA and kept in registers, then each of the M
-// lanes (which share q and k) applies its own decay and erase scaling,
-// inverts its unit-lower L by 16x16 blocks and stores T, Aq and the scalars.
+// Q K^T are formed once on MFMA and kept in registers, then the M lanes
+// (which share q and k), LP at a time, apply their own decay and erase
+// scaling, invert their unit-lower L by 16x16 blocks and store T, Aq and
+// the scalars.  The LP lanes of a group go through each phase together:
+// wave w forms lane w's scalars, the diagonal blocks of every lane are
+// inverted at once (a 16-lane group per block), wave w forms lane w's
+// blocks below the diagonal, so a group costs one lane's chain of
+// dependent steps and barriers.
 #include "delta_common.hpp"
 #include "gdnx_internal.hpp"
 
 namespace gdnx {
 
 template <typename CT, int D, int C>
-struct alignas(16) PrepSmem {
+struct alignas(16) PrepLane {   // one lane's operands
   typedef Dims<CT, D, C> Dm;
-  CT q[C * Dm::LDD];
-  CT k[C * Dm::LDD];
-  CT t[C * Dm::LDC];    // T of the current lane (strictly upper tiles stay zero)
-  CT aq[C * Dm::LDC];   // Aq of the current lane (same)
+  CT t[C * Dm::LDC];    // T (strictly upper tiles stay zero)
+  CT aq[C * Dm::LDC];   // Aq (same)
   float L[C * Dm::LDF];
   float LT[C * Dm::LDT];
   float Td[C * Dm::LDT];
   float G[C], gam[C], dec[C], ae[C], aw[C];
+};
+template <typename CT, int D, int C, int LP>
+struct alignas(16) PrepSmem {
+  typedef Dims<CT, D, C> Dm;
+  CT q[C * Dm::LDD];
+  CT k[C * Dm::LDD];
+  PrepLane<CT, D, C> ln[LP];
+};
+// lanes prepared together: as many (of 4, 2, 1) as leave LDS for two
+// workgroups per CU
+template <typename CT, int D, int C>
+struct PrepCfg {
+  static constexpr int LP = sizeof(PrepSmem<CT, D, C, 4>) <= 80 * 1024   ? 4
+                            : sizeof(PrepSmem<CT, D, C, 2>) <= 80 * 1024 ? 2
+                                                                          : 1;
 };
 
 // [C][LDC] LDS tile -> row-major [C][C] global, 16-byte stores
@@ -45,12 +63,14 @@ __device__ __forceinline__ void store_cc(CT* __restrict__ dst, const CT* src, in
 }
 
 template <typename CT, int D, int C>
-__global__ void __launch_bounds__((Dims<CT, D, C>::NT)) __attribute__((amdgpu_waves_per_eu(3))) delta_prep_kernel(DeltaArgs p) {
+__global__ void __launch_bounds__((Dims<CT, D, C>::NT)) __attribute__((amdgpu_waves_per_eu(2))) delta_prep_kernel(DeltaArgs p) {
   typedef Dims<CT, D, C> Dm;
   constexpr int LDD = Dm::LDD, LDC = Dm::LDC, LDF = Dm::LDF, NT = Dm::NT, NW = Dm::NW, NCT = Dm::NCT;
   constexpr int NP = NCT * (NCT + 1) / 2;          // lower 16x16 tile pairs of a C x C gram
   constexpr int NTPW = (2 * NP + NW - 1) / NW;      // gram tiles per wave (K K^T and Q K^T)
-  __shared__ PrepSmem<CT, D, C> sm;
+  constexpr int LP = PrepCfg<CT, D, C>::LP;
+  static_assert(LP <= NW && LP * NCT <= 4 * NW, "a wave per lane; a 16-lane group per diagonal block");
+  __shared__ PrepSmem<CT, D, C, LP> sm;
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6, lane = tid & 63, g4 = lane >> 4, n16 = lane & 15;
@@ -65,10 +85,12 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) __attribute__((amdgpu_wa
   const size_t NR = (size_t)p.B * p.H * p.M * NC;
   const PrepPtrs<CT> po = prep_ptrs<CT>(p.prep, NR, C);
 
-  for (int i = tid; i < C * LDC; i += NT) {  // strictly upper tiles are never written
-    sm.t[i] = from_f<CT>(0.f);
-    sm.aq[i] = from_f<CT>(0.f);
-  }
+#pragma unroll
+  for (int l = 0; l < LP; ++l)
+    for (int i = tid; i < C * LDC; i += NT) {  // strictly upper tiles are never written
+      sm.ln[l].t[i] = from_f<CT>(0.f);
+      sm.ln[l].aq[i] = from_f<CT>(0.f);
+    }
   {
     Stage<CT, C, D, 1, NT> sq, sk;
     const unsigned rsb = (unsigned)(rs * sizeof(CT)), nb = (unsigned)min(C, p.T - t0) * rsb;
@@ -97,59 +119,94 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) __attribute__((amdgpu_wa
     }
   }
 
-  const ChunkScalars cs{sm.G, sm.gam, sm.dec, sm.ae, sm.aw, nullptr};
-  for (int m = 0; m < p.M; ++m) {
-    const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + m;
-    const size_t rec = rec_index(((size_t)b * p.H + h) * p.M + m, c, (size_t)p.B * p.H * p.M);
-    if (wave == 0) prep_scalars<C>(cs, p.ae + soff, p.aw + soff, p.g + soff, st, t0, p.T, lane);
+  for (int m0 = 0; m0 < p.M; m0 += LP) {
+    const int nl = min(LP, p.M - m0);
+    if (m0 > 0) __syncthreads();   // the previous group's stores have read its lanes' operands
+    // ---- the lanes' token scalars (wave w: lane m0 + w) ----
+    if (wave < nl) {
+      PrepLane<CT, D, C>& P = sm.ln[wave];
+      const ChunkScalars cs{P.G, P.gam, P.dec, P.ae, P.aw, nullptr};
+      const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + m0 + wave;
+      prep_scalars<C>(cs, p.ae + soff, p.aw + soff, p.g + soff, st, t0, p.T, lane);
+    }
     __syncthreads();
-    // this lane's L (fp32, plus transposed diagonal blocks) and Aq
+    // ---- each lane's L (fp32, plus transposed diagonal blocks) and Aq ----
 #pragma unroll
-    for (int s = 0; s < NTPW; ++s) {
-      const int task = wave + NW * s;
-      if (task < 2 * NP) {
-        int it, jt;
-        tri_pair(task >> 1, it, jt);
-        if ((task & 1) == 0) {
-          const f32x4 G4 = *(const f32x4*)&sm.G[it * 16 + 4 * g4];
-          const f32x4 ae4 = *(const f32x4*)&sm.ae[it * 16 + 4 * g4];
-          const int j = jt * 16 + n16;
-          const float Gj = sm.G[j];
-          f32x4 val;
+    for (int l = 0; l < LP; ++l) {
+      if (l >= nl) break;
+      PrepLane<CT, D, C>& P = sm.ln[l];
 #pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int i = it * 16 + 4 * g4 + ii;
-            val[ii] = (j < i) ? __expf(G4[ii] - Gj) * ae4[ii] * gram[s][ii] : 0.f;
-            sm.L[i * LDF + j] = val[ii];
+      for (int s = 0; s < NTPW; ++s) {
+        const int task = wave + NW * s;
+        if (task < 2 * NP) {
+          int it, jt;
+          tri_pair(task >> 1, it, jt);
+          if ((task & 1) == 0) {
+            const f32x4 G4 = *(const f32x4*)&P.G[it * 16 + 4 * g4];
+            const f32x4 ae4 = *(const f32x4*)&P.ae[it * 16 + 4 * g4];
+            const int j = jt * 16 + n16;
+            const float Gj = P.G[j];
+            f32x4 val;
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+              const int i = it * 16 + 4 * g4 + ii;
+              val[ii] = (j < i) ? __expf(G4[ii] - Gj) * ae4[ii] * gram[s][ii] : 0.f;
+              P.L[i * LDF + j] = val[ii];
+            }
+            if (jt == it) *(f32x4*)&P.LT[j * 20 + 4 * g4] = val;
+          } else {
+            const int i = it * 16 + n16;
+            const float Gi = P.G[i];
+            const f32x4 Gj4 = *(const f32x4*)&P.G[jt * 16 + 4 * g4];
+            float v[4];
+#pragma unroll
+            for (int ii = 0; ii < 4; ++ii) {
+              const int j = jt * 16 + 4 * g4 + ii;
+              v[ii] = (j <= i) ? __expf(Gi - Gj4[ii]) * gram[s][ii] : 0.f;
+            }
+            st4(&P.aq[i * LDC + jt * 16 + 4 * g4], v[0], v[1], v[2], v[3]);
           }
-          if (jt == it) *(f32x4*)&sm.LT[j * 20 + 4 * g4] = val;
-        } else {
-          const int i = it * 16 + n16;
-          const float Gi = sm.G[i];
-          const f32x4 Gj4 = *(const f32x4*)&sm.G[jt * 16 + 4 * g4];
-          float v[4];
-#pragma unroll
-          for (int ii = 0; ii < 4; ++ii) {
-            const int j = jt * 16 + 4 * g4 + ii;
-            v[ii] = (j <= i) ? __expf(Gi - Gj4[ii]) * gram[s][ii] : 0.f;
-          }
-          st4(&sm.aq[i * LDC + jt * 16 + 4 * g4], v[0], v[1], v[2], v[3]);
         }
       }
     }
     __syncthreads();
-    invert_unit_lower<C>(
-        sm.L, sm.LT, sm.Td, wave, lane, [&](int) { return 0; },
-        [&](int i, int j, float t, int) { sm.t[i * LDC + j] = from_f<CT>(t); });
+    // ---- T = (I + L)^-1: every lane's diagonal blocks at once (16-lane
+    // group g of wave w: block (4 w + g) mod NCT of lane (4 w + g) / NCT) ----
+    {
+      const int pair = 4 * wave + g4;
+      if (pair < nl * NCT) {
+        PrepLane<CT, D, C>& P = sm.ln[pair / NCT];
+        diag_block_inverse(P.LT, P.Td, pair % NCT, n16, 0,
+                           [&](int i, int j, float t, int) { P.t[i * LDC + j] = from_f<CT>(t); });
+      }
+    }
+    if constexpr (NCT > 1) {
+      __syncthreads();
+      // the blocks below the diagonal: wave w, lane m0 + w
+      if (wave < nl) {
+        PrepLane<CT, D, C>& P = sm.ln[wave];
+#pragma unroll
+        for (int jb = 0; jb < NCT - 1; ++jb)
+          offdiag_block_column<C>(P.L, P.Td, jb, lane, 0,
+                                  [&](int i, int j, float t, int) { P.t[i * LDC + j] = from_f<CT>(t); });
+      }
+    }
     __syncthreads();
-    store_cc<CT, C, LDC>(po.t + rec * C * C, sm.t, tid, NT);
-    store_cc<CT, C, LDC>(po.aq + rec * C * C, sm.aq, tid, NT);
-    if (wave == 0 && lane < C) {
-      float* sc = po.sc + rec * kNumSc * C;
-      sc[kScGam * C + lane] = sm.gam[lane];
-      sc[kScDec * C + lane] = sm.dec[lane];
-      sc[kScAeg * C + lane] = sm.ae[lane] * sm.gam[lane];
-      sc[kScAw * C + lane] = sm.aw[lane];
+    // ---- records: T, Aq and the scalars of each lane ----
+#pragma unroll
+    for (int l = 0; l < LP; ++l) {
+      if (l >= nl) break;
+      const PrepLane<CT, D, C>& P = sm.ln[l];
+      const size_t rec = rec_index(((size_t)b * p.H + h) * p.M + m0 + l, c, (size_t)p.B * p.H * p.M);
+      store_cc<CT, C, LDC>(po.t + rec * C * C, P.t, tid, NT);
+      store_cc<CT, C, LDC>(po.aq + rec * C * C, P.aq, tid, NT);
+      if (wave == l && lane < C) {
+        float* sc = po.sc + rec * kNumSc * C;
+        sc[kScGam * C + lane] = P.gam[lane];
+        sc[kScDec * C + lane] = P.dec[lane];
+        sc[kScAeg * C + lane] = P.ae[lane] * P.gam[lane];
+        sc[kScAw * C + lane] = P.aw[lane];
+      }
     }
   }
 }
