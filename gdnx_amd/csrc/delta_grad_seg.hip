@@ -19,9 +19,11 @@
 // (gdn3/gdn3_upgrade.py:467-521; its trainer recomputes the layer's forward
 // under gradient checkpointing, train/train_gdn3_distill.py:263-266).
 //
-// One workgroup per (b, h, segment) holds the M lanes that share q/k/v, so
-// their dq/dk/dv are summed on chip (fixed order, no atomics), in one pass
-// over the segment's sub-chunks with every lane's state resident.  Wave w
+// One workgroup per (b, h, segment) takes the M lanes that share q/k/v, so
+// their dq/dk/dv are summed in a fixed order with no atomics: two lanes'
+// states are resident at a time, the lane pairs run one after the other
+// over the segment's sub-chunks, and a pair's float32 dq/dk/dv sums go to
+// the next pair through the workspace.  Wave w
 // owns key tile w: its columns of a lane's S^T as fp32 accumulator tiles
 // [value rows][key columns], which are directly MFMA fragments over
 // k = value, and whose update is a product over the sub-chunk's tokens with
