@@ -19,6 +19,9 @@ Prints ONE JSON line.  Besides the step throughput it reports:
                 stash) at the config-1 shape: the default path, and the fused
                 single-kernel scan at C = 64;
   decode_ms_per_step, decode_hbm_frac  the config-4 decode step;
+  decode_gdn3_ms_per_step, decode_gdn3_hbm_frac  the GDN3 Kronecker-residual
+                decode step at the same width (a step that closes no
+                compaction interval);
   gdn3_layer_fwd_bwd_ms  the GDN3 layer default regime (compaction every
                 16 tokens) forward + backward at B=4, T=4096;
   cpu_baseline  the repository's CPU oracle (a port of the reference's
@@ -209,13 +212,47 @@ def decode_bytes_chan(NS, H, NC, D, io_bytes=2):
     return decode_bytes(NS, H, NC, D, io_bytes) + NS * H * NC * (D - 1) * 4
 
 
-def decode_suite(steps, warmup, extras=True):
+def decode_suite_extras(out, steps, q, k, v, a, lg, state, y, timed, gen, nbytes):
+    """decode_suite's slot-indexed and per-key-channel steps on its dense states."""
+    import torch
+    from gdnx_amd import ops
+    dev = state.device
+    NS, H, NC, D = state.shape[:4]
+    n_in = q.shape[0]
+    # the state pool addressed through shuffled slots
+    perm = torch.randperm(NS, generator=torch.Generator().manual_seed(5)).to(torch.int32).to(dev)
+
+    def step_slots(i):
+        j = i % n_in
+        ops.delta_decode_step_slots(q[j], k[j], v[j], a[j], a[j], lg[j], state, perm, out=y)
+
+    sec = timed(step_slots, steps, 1)
+    out["slots"] = {"kernel": "delta_decode_kernel (slot-indexed)", "ms_per_step": sec * 1e3,
+                    "tokens_per_s": NS / sec, "hbm_frac": nbytes / sec / HBM_PEAK,
+                    "note": "rows name shuffled slots of a 256-slot state pool"}
+    # a log-decay per key channel (KMD-2's decay) on the same states
+    lgc = (lg[..., None] + 0.001 * torch.randn(n_in, NS, H, NC, D, device=dev, generator=gen)).contiguous()
+
+    def step_chan(i):
+        j = i % n_in
+        ops.delta_decode_step_chan(q[j], k[j], v[j], a[j], a[j], lgc[j], state, out=y)
+
+    sec = timed(step_chan, steps, 1)
+    nb = decode_bytes_chan(NS, H, NC, D)
+    out["chan"] = {"kernel": "delta_decode_chan_kernel", "ms_per_step": sec * 1e3, "tokens_per_s": NS / sec,
+                   "algorithmic_bytes": nb, "hbm_frac": nb / sec / HBM_PEAK}
+    del lgc
+
+
+def decode_suite(steps, warmup, extras=True, gdn3_step=None):
     """Config-4 decode measurements (HIP events on the launch stream): the
     dense step (gdnx_delta_decode_step) and, with extras, the same through
-    shuffled state slots, the per-key-channel step and the GDN3
-    Kronecker-residual step at the same width (256 sequences x 16 heads x 16
-    chains).  Returns a dict of ms per step and HBM fractions of the
-    algorithmic bytes."""
+    shuffled state slots and the per-key-channel step; with gdn3_step (by
+    default as extras) the GDN3 Kronecker-residual step at the same width
+    (256 sequences x 16 heads x 16 chains).  Returns a dict of ms per step
+    and HBM fractions of the algorithmic bytes."""
+    if gdn3_step is None:
+        gdn3_step = extras
     import torch
     import torch.nn.functional as F
     from gdnx_amd import gdn3, ops
@@ -260,31 +297,10 @@ def decode_suite(steps, warmup, extras=True):
     out = {"dense": {"kernel": "delta_decode_kernel", "ms_per_step": sec * 1e3, "tokens_per_s": NS / sec,
                      "algorithmic_bytes": nbytes, "hbm_gbs": nbytes / sec / 1e9, "hbm_frac": nbytes / sec / HBM_PEAK,
                      "traffic": measured_traffic("delta_decode_kernel")}}
-    if not extras:
+    if extras:
+        decode_suite_extras(out, steps, q, k, v, a, lg, state, y, timed, gen, nbytes)
+    if not gdn3_step:
         return out
-    # the state pool addressed through shuffled slots
-    perm = torch.randperm(NS, generator=torch.Generator().manual_seed(5)).to(torch.int32).to(dev)
-
-    def step_slots(i):
-        j = i % n_in
-        ops.delta_decode_step_slots(q[j], k[j], v[j], a[j], a[j], lg[j], state, perm, out=y)
-
-    sec = timed(step_slots, steps, 1)
-    out["slots"] = {"kernel": "delta_decode_kernel (slot-indexed)", "ms_per_step": sec * 1e3,
-                    "tokens_per_s": NS / sec, "hbm_frac": nbytes / sec / HBM_PEAK,
-                    "note": "rows name shuffled slots of a 256-slot state pool"}
-    # a log-decay per key channel (KMD-2's decay) on the same states
-    lgc = (lg[..., None] + 0.001 * torch.randn(n_in, NS, H, NC, D, device=dev, generator=gen)).contiguous()
-
-    def step_chan(i):
-        j = i % n_in
-        ops.delta_decode_step_chan(q[j], k[j], v[j], a[j], a[j], lgc[j], state, out=y)
-
-    sec = timed(step_chan, steps, 1)
-    nb = decode_bytes_chan(NS, H, NC, D)
-    out["chan"] = {"kernel": "delta_decode_chan_kernel", "ms_per_step": sec * 1e3, "tokens_per_s": NS / sec,
-                   "algorithmic_bytes": nb, "hbm_frac": nb / sec / HBM_PEAK}
-    del lgc
     # the GDN3 Kronecker-residual step: 4 x (16x16 (x) 8x8) + a 16-slot window per chain
     del state
     torch.cuda.empty_cache()
@@ -1147,9 +1163,11 @@ def main():
     }
     # config 4 decode (the dense step) and the layer-default GDN3 regime, timed here so
     # the headline run carries them
-    dec = decode_suite(steps=20, warmup=3, extras=False)["dense"]
-    line["decode_ms_per_step"] = dec["ms_per_step"]
-    line["decode_hbm_frac"] = dec["hbm_frac"]
+    decs = decode_suite(steps=20, warmup=3, extras=False, gdn3_step=True)
+    line["decode_ms_per_step"] = decs["dense"]["ms_per_step"]
+    line["decode_hbm_frac"] = decs["dense"]["hbm_frac"]
+    line["decode_gdn3_ms_per_step"] = decs["gdn3"]["ms_per_step"]
+    line["decode_gdn3_hbm_frac"] = decs["gdn3"]["hbm_frac"]
     line["gdn3_layer_fwd_bwd_ms"] = gdn3_layer_train_ms()
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline()
