@@ -22,10 +22,11 @@ __global__ void __launch_bounds__(256) lane_sum_kernel(const float* __restrict__
   const long long row = e / (D / 8);
   const int d = 8 * (int)(e % (D / 8));
   const float* xp = x + (size_t)row * M * D + d;
-  f32x4 s0 = *(const f32x4*)xp, s1 = *(const f32x4*)(xp + 4);
+  // the lanes' partials are read once: non-temporal loads
+  f32x4 s0 = __builtin_nontemporal_load((const f32x4*)xp), s1 = __builtin_nontemporal_load((const f32x4*)(xp + 4));
   for (int m = 1; m < M; ++m) {
-    s0 += *(const f32x4*)(xp + (size_t)m * D);
-    s1 += *(const f32x4*)(xp + (size_t)m * D + 4);
+    s0 += __builtin_nontemporal_load((const f32x4*)(xp + (size_t)m * D));
+    s1 += __builtin_nontemporal_load((const f32x4*)(xp + (size_t)m * D + 4));
   }
   OT* op = out + (size_t)row * D + d;
   st4(op, s0[0], s0[1], s0[2], s0[3]);
