@@ -157,6 +157,13 @@ __device__ __forceinline__ void row_commit_nat(bf16* dst, const uint4& x, int to
   d[1] = make_uint2(x.z, x.w);
 }
 
+// a 16-byte unit of a record read once (non-temporal)
+__device__ __forceinline__ uint4 nt_load16(const bf16* p) {
+  typedef unsigned u32x4 __attribute__((ext_vector_type(4)));
+  const u32x4 v = __builtin_nontemporal_load((const u32x4*)p);
+  return make_uint4(v[0], v[1], v[2], v[3]);
+}
+
 template <int D>
 __global__ void __launch_bounds__(SegDims<D>::NT) __attribute__((amdgpu_waves_per_eu(2, 2)))
 delta_grad_seg_kernel(DeltaBwdArgs p) {
@@ -233,9 +240,9 @@ delta_grad_seg_kernel(DeltaBwdArgs p) {
       f.k3 = k3st[rec_index(chain_of(m), cs, (size_t)N) * CS + jj * C + min(lane, C - 1)];
       f.ok = lane < C && t0 + lane < p.T;
     }
-    f.r = *(const uint4*)(tile_src(rst, c, m) + 8 * tid);
-    f.x = *(const uint4*)(tile_src(dxst, c, m) + 8 * tid);
-    f.p3 = *(const uint4*)(tile_src(p3st, c, m) + 8 * tid);
+    f.r = nt_load16(tile_src(rst, c, m) + 8 * tid);
+    f.x = nt_load16(tile_src(dxst, c, m) + 8 * tid);
+    f.p3 = nt_load16(tile_src(p3st, c, m) + 8 * tid);
     const bf16* yb = (const bf16*)p.dy + (((size_t)b * p.T + t0) * p.H + h) * M * D + (size_t)m * D;
     const __amdgpu_buffer_rsrc_t yr = buf_rsrc(yb, (unsigned)rows_left(t0) * ysb);
     f.y = buf_load16(yr, (unsigned)row_unit_tok(tid) * ysb + row_unit_d0(tid) * sizeof(bf16));
