@@ -243,9 +243,15 @@ __device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
   return acc;
 }
 
-// Y <- Y R^{-1} with Y^T Y = R^T R (Cholesky QR, `passes` times: one pass
-// keeps the intermediate power-iteration bases well conditioned, the final
-// basis takes two); the result also goes column-major in fp32 to yt.  Columns whose pivot falls below 1e-24 of the largest
+// One Cholesky-QR pass leaves Q^T Q - I at about cond(Y)^2 * 1.1e-16 in fp64;
+// the pivots' spread (largest / smallest, about cond(Y)^2) below this bound
+// makes a second pass unnecessary (Q orthonormal to ~1e-10).
+constexpr double kOrthCut = 1e6;
+
+// Y <- Y R^{-1} with Y^T Y = R^T R (Cholesky QR, up to `passes` times: one
+// pass keeps the intermediate power-iteration bases well conditioned; the
+// final basis takes a second where the first pass's pivots spread by more
+// than kOrthCut or a column was dropped); the result also goes column-major in fp32 to yt.  Columns whose pivot falls below 1e-24 of the largest
 // diagonal are set to zero.  The Gram runs on fp64 MFMA over 4 row segments;
 // each row of Y is then solved against R by forward substitution.
 template <int D, int P, int M, bool STG>
@@ -278,9 +284,12 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int
 #pragma unroll
     for (int k = 0; k < kQ; ++k) dmax = fmax(dmax, L[k][k]);
     const double tol = dmax * 1e-24;
+    double pmin = dmax, pmax = 0.0;   // the spread of the pivots
 #pragma unroll
     for (int k = 0; k < kQ; ++k) {
       const double akk = L[k][k];
+      pmin = fmin(pmin, akk);
+      pmax = fmax(pmax, akk);
       const double rq = rsqrt_f64(fmax(akk, 2.2250738585072014e-308));  // unconditional: a select, no branch
       const double rd = (akk > tol && akk > 0.0) ? rq : 0.0;
       rdv[k] = rd;   // 1 / R[k][k] (R[k][k] = akk rd = sqrt(akk))
@@ -310,6 +319,9 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int
       }
     }
     __syncthreads();
+    // a later pass only where this one can have lost orthogonality: every
+    // thread factored the same Gram, so the test is uniform
+    if (pass + 1 < passes && __builtin_amdgcn_readfirstlane(pmin * kOrthCut > pmax ? 1 : 0)) break;
   }
 }
 
@@ -557,7 +569,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
       if (sweep >= 3) {   // (fewer than three sweeps rarely suffice; extra sweeps over a diagonal W rotate by identities)
         const double off = wave_sum_f64(i != j ? a * a : 0.0);
         const double dia = wave_sum_f64(i == j ? a * a : 0.0);
-        if (!(off > 1e-28 * dia)) break;  // uniform across the wave
+        if (!(off > 1e-20 * dia)) break;  // uniform across the wave
       }
 #pragma unroll
       for (int st = 0; st < 7; ++st) {
