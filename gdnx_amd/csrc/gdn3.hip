@@ -569,7 +569,10 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
       if (sweep >= 3) {   // (fewer than three sweeps rarely suffice; extra sweeps over a diagonal W rotate by identities)
         const double off = wave_sum_f64(i != j ? a * a : 0.0);
         const double dia = wave_sum_f64(i == j ? a * a : 0.0);
-        if (!(off > 1e-20 * dia)) break;  // uniform across the wave
+        // stop at off-diagonal entries ~1e-8 of the diagonal's (in norm): the
+        // eigenvectors then sit within ~1e-8 / (relative gap) of W's, an order
+        // below what the fp32 products that formed Bm already left in W
+        if (!(off > 1e-16 * dia)) break;  // uniform across the wave
       }
 #pragma unroll
       for (int st = 0; st < 7; ++st) {
