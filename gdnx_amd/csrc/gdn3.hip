@@ -79,14 +79,19 @@ __device__ __forceinline__ void block_sum(double (&v)[NV], double* red, int tid)
 // LDS of one compaction.  STG: the window's writes and keys are staged
 // through ut / vt a block of 16 slots at a time (they come from global
 // memory); without, they are read where they lie (LDS of the fused kernel).
+// Row stride (doubles) of the compaction's row-major [rows][kQ] double arrays:
+// where a thread reads or writes a whole row, 9 doubles put the 64 lanes' rows
+// on distinct bank pairs (a stride of 8 put 16 lanes on each).
+constexpr int kLQ = kQ + 1;
+
 template <int D, int P, bool STG = true>
 struct G3Compact {
   static constexpr int m = G3D<D>::m, n = G3D<D>::n;
   static constexpr int ldr = n + 4;                 // R_mat row stride: 16-byte rows, 4 banks apart
   static constexpr int lym = m + 16, lzn = n + 16;  // strides of the column-major fp32 copies
   alignas(16) float rm[m * ldr];          // R_mat
-  alignas(16) double y[m * kQ];           // range basis, rows of kQ
-  alignas(16) double z[n * kQ];           // R_mat^T Y, then Bm^T = R_mat^T Q (rows of kQ)
+  alignas(16) double y[m * kLQ];          // range basis, rows of kQ (stride kLQ)
+  alignas(16) double z[n * kLQ];          // R_mat^T Y, then Bm^T = R_mat^T Q (rows of kQ, stride kLQ)
   alignas(16) float yt[kQ * lym];         // y in fp32, column-major: the B operand of R_mat^T Y
   alignas(16) float zt[kQ * lzn];         // the sketch (zero padded), then z, in fp32 column-major
   alignas(16) float ut[STG ? 16 : 1][D + 4];   // a block of 16 window slots: net writes U_p
@@ -112,7 +117,7 @@ typedef double f64x4 __attribute__((ext_vector_type(4)));
 // so are its A entries of an untransposed row (rows of ldr = 4 mod 64 floats
 // put the 16 rows of a tile on distinct banks, and the 16 columns of a
 // transposed read too).  Wave w owns the 16-row tiles w, w + 4, ...; C goes to
-// c (rows of kQ, fp64) and, when ct is given, column-major in fp32 to ct
+// c (rows of kQ at stride kLQ, fp64) and, when ct is given, column-major in fp32 to ct
 // (stride ldc).  GR: also this wave's partial Gram C^T C over its rows, from
 // the accumulators (fp64 MFMA; lane (g, r) holds C[row0 + 4 g + e][r], so
 // step e of a tile takes its element e as both operands), into *gp in the
@@ -166,7 +171,7 @@ __device__ __forceinline__ void rm_mfma(const float* rm, const float* bt, double
     for (int t = 0; t < TPW; ++t) {
       const int r0 = (wave + 4 * t) * 16 + 4 * g;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) c[(r0 + e) * kQ + n16] = (double)acc[t][e];
+      for (int e = 0; e < 4; ++e) c[(r0 + e) * kLQ + n16] = (double)acc[t][e];
       if constexpr (ldc > 0) *(f32x4*)&ct[n16 * ldc + r0] = acc[t];
     }
   if constexpr (GR) {
@@ -225,7 +230,7 @@ __device__ __forceinline__ int rr_partner(int x, int st) {
   return (2 * st - x + 14) % 7;
 }
 
-// Partial Gram X^T X of NR rows of X (rows of kQ doubles) on fp64 MFMA: lane
+// Partial Gram X^T X of NR rows of X (rows of kQ doubles, stride kLQ) on fp64 MFMA: lane
 // l supplies X[k][l % 16] (zero for columns >= kQ) both as A[l % 16][l / 16]
 // of A = X^T and as B[l / 16][l % 16]; it returns G[l / 16 + 4e][l % 16] in
 // element e (rows and columns < kQ = 8 live, so e = 0, 1).
@@ -236,7 +241,7 @@ __device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
   f64x4 acc = {0.0, 0.0, 0.0, 0.0};
 #pragma unroll
   for (int k = 0; k < NR; k += 4) {
-    const double v = x[(k + g) * kQ + (n16 & (kQ - 1))];
+    const double v = x[(k + g) * kLQ + (n16 & (kQ - 1))];
     const double vl = n16 < kQ ? v : 0.0;
     acc = __builtin_amdgcn_mfma_f64_16x16x4f64(vl, vl, acc, 0, 0, 0);
   }
@@ -261,7 +266,7 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int
   constexpr int seg = M / 4;
   for (int pass = 0; pass < passes; ++pass) {
     {   // this wave's partial Gram (the first pass's may come from the product that formed Y)
-      const f64x4 g = (pass == 0 && pre) ? *pre : gram_mfma<seg>(cs.y + wave * seg * kQ, lane);
+      const f64x4 g = (pass == 0 && pre) ? *pre : gram_mfma<seg>(cs.y + wave * seg * kLQ, lane);
       const int r = lane >> 4, c = lane & 15;
       if (c < kQ) {
         cs.red[wave * 64 + r * kQ + c] = g[0];
@@ -303,7 +308,7 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int
     if (tid < M) {
       double x[kQ];
 #pragma unroll
-      for (int j = 0; j < kQ; ++j) x[j] = cs.y[tid * kQ + j];
+      for (int j = 0; j < kQ; ++j) x[j] = cs.y[tid * kLQ + j];
       // x R = y, column by column: x_j = (y_j - sum_{i<j} x_i R[i][j]) / R[j][j], R[i][j] = L[j][i]
 #pragma unroll
       for (int j = 0; j < kQ; ++j) {
@@ -314,7 +319,7 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int
       }
 #pragma unroll
       for (int j = 0; j < kQ; ++j) {
-        cs.y[tid * kQ + j] = x[j];
+        cs.y[tid * kLQ + j] = x[j];
         cs.yt[j * cs.lym + tid] = (float)x[j];
       }
     }
@@ -332,7 +337,7 @@ __device__ __forceinline__ void col_sumsq(const double* y, double* red, double* 
   const int r = tid & (kRMax - 1), lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   double part = 0.0;
   for (int row = tid / kRMax; row < M; row += kNT / kRMax) {
-    const double x = y[row * kQ + r];
+    const double x = y[row * kLQ + r];
     part += x * x;
   }
 #pragma unroll
@@ -493,8 +498,8 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     col_sumsq<m>(cs.y, cs.red, cs.lam, tid);
     for (int e = tid; e < m * kQ; e += kNT) {
       const int j = e % kQ;
-      const double qv = j < R ? cs.y[e] / fmax(sqrt(cs.lam[j]), 1e-12) : 0.0;   // Q
-      cs.y[e] = qv;
+      const double qv = j < R ? cs.y[(e / kQ) * kLQ + j] / fmax(sqrt(cs.lam[j]), 1e-12) : 0.0;   // Q
+      cs.y[(e / kQ) * kLQ + j] = qv;
       cs.yt[j * lym + e / kQ] = (float)qv;
     }
     __syncthreads();
@@ -505,12 +510,12 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     const float s1 = sdec, s2 = 1.f - sdec;
     for (int e = tid; e < R * m; e += kNT) {
       const int r = e / m, row = e % m;
-      const double sv = cs.y[row * kQ + r] * fmax(sqrt(cs.sig[r]), 1e-12);
+      const double sv = cs.y[row * kLQ + r] * fmax(sqrt(cs.sig[r]), 1e-12);
       A[e] = s1 * (A[e] * dk) + s2 * (float)sv;
     }
     for (int e = tid; e < R * n; e += kNT) {
       const int r = e / n, col = e % n;
-      const double sv = cs.z[col * kQ + r] / fmax(sqrt(cs.sig[r]), 1e-12);
+      const double sv = cs.z[col * kLQ + r] / fmax(sqrt(cs.sig[r]), 1e-12);
       Bv[e] = s1 * (Bv[e] * dk) + s2 * (float)sv;
     }
     if (tid == 0 && stats) {
@@ -539,7 +544,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   __syncthreads();
   {  // W = Bm Bm^T: each wave's partial Gram over a quarter of the rows of Bm^T
     static_assert(n % 16 == 0, "quarters of whole MFMA steps");
-    const f64x4 g = gram_mfma<n / 4>(cs.z + wave * (n / 4) * kQ, lane);
+    const f64x4 g = gram_mfma<n / 4>(cs.z + wave * (n / 4) * kLQ, lane);
     const int r = lane >> 4, c = lane & 15;
     if (c < kQ) {
       cs.red[wave * 64 + r * kQ + c] = g[0];
@@ -623,7 +628,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   if (tid < m) {
     double yv[kQ];
 #pragma unroll
-    for (int j = 0; j < kQ; ++j) yv[j] = cs.y[tid * kQ + j];
+    for (int j = 0; j < kQ; ++j) yv[j] = cs.y[tid * kLQ + j];
 #pragma unroll
     for (int r = 0; r < kRMax; ++r) {
       double s = 0.0;
@@ -644,7 +649,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     if (on) {
       double sv = 0.0;
 #pragma unroll
-      for (int j = 0; j < kQ; ++j) sv += cs.z[c * kQ + j] * cs.ev[r * kQ + j];
+      for (int j = 0; j < kQ; ++j) sv += cs.z[c * kLQ + j] * cs.ev[r * kQ + j];
       vr = cs.sig[r] > 0.0 ? sv * cs.isig[r] : (c == r ? 1.0 : 0.0);
     }
     double bv_ = on ? fabs(vr) : -1.0;
