@@ -223,6 +223,14 @@ __device__ __forceinline__ void jacobi_rot(double app, double aqq, double apq, d
   s = __longlong_as_double(__double_as_longlong(e) ^ sb) * r;
 }
 
+// x as held by lane src of the wave (ds_bpermute, one per 32-bit half)
+__device__ __forceinline__ double lane_f64(int src, double x) {
+  const long long v = __double_as_longlong(x);
+  const unsigned lo = (unsigned)__builtin_amdgcn_ds_bpermute(4 * src, (int)(unsigned)v);
+  const unsigned hi = (unsigned)__builtin_amdgcn_ds_bpermute(4 * src, (int)(unsigned)(v >> 32));
+  return __longlong_as_double((long long)(((unsigned long long)hi << 32) | lo));
+}
+
 // Round-robin (circle method) partner of index x in round st of 7 for 8 indices.
 __device__ __forceinline__ int rr_partner(int x, int st) {
   if (x == 7) return st;
@@ -556,8 +564,8 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   // eigen-decomposition of W = Bm Bm^T by cyclic Jacobi in wave 0: lane
   // (i, j) holds W[i][j] and V[i][j].  Each round rotates 4 disjoint pairs;
   // a lane gathers every operand of its round in one exchange and forms the
-  // rotations of both its pairs (that of i and that of j) itself, from the
-  // same entries the lanes of those indices use.  The exchange goes through
+  // rotation of its column's pair (that of j); the rotation of i it takes
+  // from lane (i, i), whose column pair that is.  The exchange goes through
   // LDS (xa, xv), ordered by wave_lds_sync (the next round's writes depend
   // on this round's reads, so they cannot move above them).
   if (wave == 0) {
@@ -571,7 +579,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
     }
     double vv = (i == j) ? 1.0 : 0.0;
     for (int sweep = 0; sweep < 12; ++sweep) {
-      if (sweep >= 3) {   // (fewer than three sweeps rarely suffice; extra sweeps over a diagonal W rotate by identities)
+      if (sweep >= 4) {   // (fewer than four sweeps rarely suffice; extra sweeps over a diagonal W rotate by identities)
         const double off = wave_sum_f64(i != j ? a * a : 0.0);
         const double dia = wave_sum_f64(i == j ? a * a : 0.0);
         // stop at off-diagonal entries ~1e-8 of the diagonal's (in norm): the
@@ -582,19 +590,19 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
 #pragma unroll
       for (int st = 0; st < 7; ++st) {
         const int pi = rr_partner(i, st), pj = rr_partner(j, st);
-        const int i0 = min(i, pi), i1 = max(i, pi), j0 = min(j, pj), j1 = max(j, pj);
+        const int j0 = min(j, pj), j1 = max(j, pj);
         xa[lane] = a;
         xv[lane] = vv;
         wave_lds_sync();
-        const double ai0 = xa[9 * i0], ai1 = xa[9 * i1], aio = xa[8 * i0 + i1];
         const double aj0 = xa[9 * j0], aj1 = xa[9 * j1], ajo = xa[8 * j0 + j1];
         const double a_ipj = xa[8 * i + pj], a_pij = xa[8 * pi + j];
         const double a_pipj = xa[8 * pi + pj], v_ipj = xv[8 * i + pj];
-        double ci, si, cj, sj;
-        jacobi_rot(ai0, ai1, aio, ci, si);
+        double cj, sj;
         jacobi_rot(aj0, aj1, ajo, cj, sj);
         // J[x][x] = c; J[partner][x] = -s if x < partner else +s
-        const double xi = (i < pi) ? -si : si, xj = (j < pj) ? -sj : sj;
+        const double xj = (j < pj) ? -sj : sj;
+        // the rotation of i: lane (i, i) formed it as the rotation of its column
+        const double ci = lane_f64(9 * i, cj), xi = lane_f64(9 * i, xj);
         a = cj * fma(ci, a, xi * a_pij) + xj * fma(ci, a_ipj, xi * a_pipj);
         vv = vv * cj + v_ipj * xj;
       }
