@@ -107,83 +107,101 @@ struct G3Compact {
 
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
-// C[M x kQ] = A[M x K] B[K x kQ] on fp32 MFMA (v_mfma_f32_16x16x4f32): A is
-// R_mat (fp32, row stride ldr, a multiple of 4) read as is (TRANS = false,
-// M = m, K = n) or transposed (TRANS = true, M = n, K = m); B is fp32 and
-// column-major (column j at bt + j ldb, zero where it has no column), so
-// every product is exact and the sums are fp32.  The 16-column tile carries
-// kQ = 8 live columns.  In a step of 16 k, lane (g, r) supplies
-// k = kb + 4 g + s to the s-th MFMA: its B entries are one 16-byte load, and
-// so are its A entries of an untransposed row (rows of ldr = 4 mod 64 floats
-// put the 16 rows of a tile on distinct banks, and the 16 columns of a
-// transposed read too).  Wave w owns the 16-row tiles w, w + 4, ...; C goes to
-// c (rows of kQ at stride kLQ, fp64) and, when ct is given, column-major in fp32 to ct
-// (stride ldc).  GR: also this wave's partial Gram C^T C over its rows, from
-// the accumulators (fp64 MFMA; lane (g, r) holds C[row0 + 4 g + e][r], so
-// step e of a tile takes its element e as both operands), into *gp in the
-// layout of gram_mfma.
+// Partial Gram X^T X of NR rows of X (rows of kQ doubles, stride kLQ) on fp64 MFMA: lane
+// l supplies X[k][l % 16] (zero for columns >= kQ) both as A[l % 16][l / 16]
+// of A = X^T and as B[l / 16][l % 16]; it returns G[l / 16 + 4e][l % 16] in
+// element e (rows and columns < kQ = 8 live, so e = 0, 1).
+template <int NR>
+__device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
+  static_assert(NR % 4 == 0, "4 rows per MFMA step");
+  const int g = lane >> 4, n16 = lane & 15;
+  f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+  for (int k = 0; k < NR; k += 4) {
+    const double v = x[(k + g) * kLQ + (n16 & (kQ - 1))];
+    const double vl = n16 < kQ ? v : 0.0;
+    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(vl, vl, acc, 0, 0, 0);
+  }
+  return acc;
+}
+
+// C[M x kQ] = A[M x K] B[K x kQ] on fp32 MFMA: A is R_mat (fp32, row stride
+// ldr, a multiple of 4) read as is (TRANS = false, M = m, K = n) or transposed
+// (TRANS = true, M = n, K = m); B is fp32 and column-major (column j at bt +
+// j ldb, zero where it has no column), so every product is exact and the sums
+// are fp32.  v_mfma_f32_4x4x1_16b_f32 (16 blocks of 4 x 4 x 1, a quarter of the
+// 16 x 16 x 4 instruction's cycles) takes the kQ = 8 columns as two blocks of
+// 4, so no MFMA column is dead (16 x 16 tiles left half of theirs unused).
+// Lane l = 4 b + q supplies row q of block b's A operand and column q of its B
+// operand and holds D[b][r][q] in element r.  A wave owns RW = M / 4 rows of C; its 16 blocks are RG = RW / 4
+// row groups times KP = 64 / RW partitions of k (k = 4 (KP t + p) + s for
+// partition p, which puts the lanes of every LDS read on distinct banks),
+// summed across the partitions (lane bits 4 and 5) at the end.  C goes to c
+// (rows of kQ at stride kLQ, fp64) and, when ct is given, column-major in fp32
+// to ct (stride ldc); GR: also this wave's partial Gram C^T C over its rows,
+// in the layout of gram_mfma, formed from its rows of c.
 template <bool TRANS, int M, int K, int ldr, int ldb, int ldc = 0, bool GR = false>
 __device__ __forceinline__ void rm_mfma(const float* rm, const float* bt, double* c, float* ct, int tid,
-                                        f64x4* gp = nullptr) {
-  static_assert(M % 64 == 0 && K % 16 == 0 && ldr % 4 == 0 && ldb % 4 == 0, "whole 16-row tiles on 4 waves, 16 k per step");
-  constexpr int TPW = M / 64;
-  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6), g = lane >> 4, n16 = lane & 15;
-  const bool live = n16 < kQ;
-  // lanes of the dead columns 8..15 repeat the live ones (their outputs are dropped)
-  const float* bcol = bt + (n16 & (kQ - 1)) * ldb + 4 * g;
-  auto ldb4 = [&](int kb) { return *(const f32x4*)&bcol[kb]; };
-  auto lda4 = [&](int t, int kb) {
-    const int row = (wave + 4 * t) * 16 + n16;
+                                         f64x4* gp = nullptr) {
+  constexpr int RW = M / 4, KP = 64 / RW, RG = RW / 4, NG = K / (4 * KP), BATCH = 4;
+  static_assert(RW == 16 || RW == 64, "a wave's rows: one or four partitions of k");
+  static_assert(NG % BATCH == 0 && ldr % 4 == 0 && ldb % 4 == 0 && ldc % 4 == 0, "whole batches, 16-byte rows");
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int b = lane >> 2, q = lane & 3, kp = b / RG, rg = b % RG;
+  const int row = wave * RW + 4 * rg + q;   // the A row this lane supplies
+  auto lda = [&](int t) {
+    const int k0 = 4 * (KP * t + kp);
     f32x4 x;
     if constexpr (TRANS) {
 #pragma unroll
-      for (int s4 = 0; s4 < 4; ++s4) x[s4] = rm[(kb + 4 * g + s4) * ldr + row];
+      for (int s4 = 0; s4 < 4; ++s4) x[s4] = rm[(k0 + s4) * ldr + row];
     } else {
-      x = *(const f32x4*)&rm[row * ldr + kb + 4 * g];
+      x = *(const f32x4*)&rm[row * ldr + k0];
     }
     return x;
   };
-  // the operands of BATCH steps are read before their MFMAs (one LDS round
-  // trip per batch; with one step ahead only, the compiler, short of
-  // registers, waited for each step's reads)
-  constexpr int NSTEP = K / 16, BATCH = TPW == 1 ? 4 : 2;
-  static_assert(NSTEP % BATCH == 0, "whole batches");
-  f32x4 acc[TPW];
+  f32x4 c1 = {0.f, 0.f, 0.f, 0.f}, c2 = {0.f, 0.f, 0.f, 0.f};   // columns q and 4 + q
 #pragma unroll
-  for (int t = 0; t < TPW; ++t) acc[t] = (f32x4){0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-  for (int s0 = 0; s0 < NSTEP; s0 += BATCH) {
-    f32x4 av[BATCH][TPW], bv[BATCH];
+  for (int t0 = 0; t0 < NG; t0 += BATCH) {
+    f32x4 av[BATCH], b1[BATCH], b2[BATCH];
 #pragma unroll
     for (int u = 0; u < BATCH; ++u) {
-      bv[u] = ldb4(16 * (s0 + u));
-#pragma unroll
-      for (int t = 0; t < TPW; ++t) av[u][t] = lda4(t, 16 * (s0 + u));
+      const int k0 = 4 * (KP * (t0 + u) + kp);
+      av[u] = lda(t0 + u);
+      b1[u] = *(const f32x4*)&bt[q * ldb + k0];
+      b2[u] = *(const f32x4*)&bt[(4 + q) * ldb + k0];
     }
     __builtin_amdgcn_sched_barrier(0);   // (the scheduler would interleave them again)
 #pragma unroll
     for (int u = 0; u < BATCH; ++u)
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) mma(acc[t], av[u][t], bv[u]);
-  }
-  if (live)
-#pragma unroll
-    for (int t = 0; t < TPW; ++t) {
-      const int r0 = (wave + 4 * t) * 16 + 4 * g;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) c[(r0 + e) * kLQ + n16] = (double)acc[t][e];
-      if constexpr (ldc > 0) *(f32x4*)&ct[n16 * ldc + r0] = acc[t];
-    }
-  if constexpr (GR) {
-    f64x4 g = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-    for (int t = 0; t < TPW; ++t)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const double x = live ? (double)acc[t][e] : 0.0;
-        g = __builtin_amdgcn_mfma_f64_16x16x4f64(x, x, g, 0, 0, 0);
+      for (int s4 = 0; s4 < 4; ++s4) {
+        c1 = __builtin_amdgcn_mfma_f32_4x4x1f32(av[u][s4], b1[u][s4], c1, 0, 0, 0);
+        c2 = __builtin_amdgcn_mfma_f32_4x4x1f32(av[u][s4], b2[u][s4], c2, 0, 0, 0);
       }
-    *gp = g;
+  }
+  if constexpr (KP > 1) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      c1[r] = sum_rows4(c1[r]);
+      c2[r] = sum_rows4(c2[r]);
+    }
+  }
+  // rows r0 + r of C; with KP = 4 the four partitions' lanes share the stores
+  const int r0 = wave * RW + 4 * rg;
+  if (KP == 1 || kp == 0)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) c[(r0 + r) * kLQ + q] = (double)c1[r];
+  if (KP == 1 || kp == 1)
+#pragma unroll
+    for (int r = 0; r < 4; ++r) c[(r0 + r) * kLQ + 4 + q] = (double)c2[r];
+  if constexpr (ldc > 0) {
+    if (KP == 1 || kp == 2) *(f32x4*)&ct[q * ldc + r0] = c1;
+    if (KP == 1 || kp == 3) *(f32x4*)&ct[(4 + q) * ldc + r0] = c2;
+  }
+  if constexpr (GR) {
+    wave_lds_sync();   // the wave's rows of c, written by its lanes above
+    *gp = gram_mfma<RW>(c + wave * RW * kLQ, lane);
   }
 }
 
@@ -236,24 +254,6 @@ __device__ __forceinline__ int rr_partner(int x, int st) {
   if (x == 7) return st;
   if (x == st) return 7;
   return (2 * st - x + 14) % 7;
-}
-
-// Partial Gram X^T X of NR rows of X (rows of kQ doubles, stride kLQ) on fp64 MFMA: lane
-// l supplies X[k][l % 16] (zero for columns >= kQ) both as A[l % 16][l / 16]
-// of A = X^T and as B[l / 16][l % 16]; it returns G[l / 16 + 4e][l % 16] in
-// element e (rows and columns < kQ = 8 live, so e = 0, 1).
-template <int NR>
-__device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
-  static_assert(NR % 4 == 0, "4 rows per MFMA step");
-  const int g = lane >> 4, n16 = lane & 15;
-  f64x4 acc = {0.0, 0.0, 0.0, 0.0};
-#pragma unroll
-  for (int k = 0; k < NR; k += 4) {
-    const double v = x[(k + g) * kLQ + (n16 & (kQ - 1))];
-    const double vl = n16 < kQ ? v : 0.0;
-    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(vl, vl, acc, 0, 0, 0);
-  }
-  return acc;
 }
 
 // One Cholesky-QR pass leaves Q^T Q - I at about cond(Y)^2 * 1.1e-16 in fp64;
