@@ -105,24 +105,30 @@ struct G3Compact {
   double sgn[kRMax];
 };
 
-typedef double f64x4 __attribute__((ext_vector_type(4)));
-
-// Partial Gram X^T X of NR rows of X (rows of kQ doubles, stride kLQ) on fp64 MFMA: lane
-// l supplies X[k][l % 16] (zero for columns >= kQ) both as A[l % 16][l / 16]
-// of A = X^T and as B[l / 16][l % 16]; it returns G[l / 16 + 4e][l % 16] in
-// element e (rows and columns < kQ = 8 live, so e = 0, 1).
+// Partial Gram X^T X (kQ x kQ) of NR rows of X (rows of kQ doubles, stride
+// kLQ) on v_mfma_f64_4x4x4_4b_f64, four rows per step: block b = 2 P + Q is
+// the 4 x 4 block (P, Q) of the Gram, so all 64 outputs are live (a 16 x 16
+// tile left three quarters of its outputs dead at four times the cycles).
+// Lane l = 16 k + 4 b + i supplies X[k][4 P + i] as A[b][i][k] and X[k][4 Q + i]
+// as B[b][k][i]; it returns G[4 P + l / 16][4 Q + l % 4], the row-major entry
+// gram_entry(l).  Two accumulation chains (even and odd steps) hide the
+// MFMA's dependent latency.
+__device__ __forceinline__ int gram_entry(int lane) {
+  const int b = (lane >> 2) & 3;
+  return (4 * (b >> 1) + (lane >> 4)) * kQ + 4 * (b & 1) + (lane & 3);
+}
 template <int NR>
-__device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
-  static_assert(NR % 4 == 0, "4 rows per MFMA step");
-  const int g = lane >> 4, n16 = lane & 15;
-  f64x4 acc = {0.0, 0.0, 0.0, 0.0};
+__device__ __forceinline__ double gram_mfma(const double* x, int lane) {
+  static_assert(NR % 8 == 0, "two chains of 4-row steps");
+  const int k = lane >> 4, b = (lane >> 2) & 3, i = lane & 3;
+  const int ca = 4 * (b >> 1) + i, cb = 4 * (b & 1) + i;
+  double acc0 = 0.0, acc1 = 0.0;
 #pragma unroll
-  for (int k = 0; k < NR; k += 4) {
-    const double v = x[(k + g) * kLQ + (n16 & (kQ - 1))];
-    const double vl = n16 < kQ ? v : 0.0;
-    acc = __builtin_amdgcn_mfma_f64_16x16x4f64(vl, vl, acc, 0, 0, 0);
+  for (int r = 0; r < NR; r += 8) {
+    acc0 = __builtin_amdgcn_mfma_f64_4x4x4f64(x[(r + k) * kLQ + ca], x[(r + k) * kLQ + cb], acc0, 0, 0, 0);
+    acc1 = __builtin_amdgcn_mfma_f64_4x4x4f64(x[(r + 4 + k) * kLQ + ca], x[(r + 4 + k) * kLQ + cb], acc1, 0, 0, 0);
   }
-  return acc;
+  return acc0 + acc1;
 }
 
 // C[M x kQ] = A[M x K] B[K x kQ] on fp32 MFMA: A is R_mat (fp32, row stride
@@ -142,7 +148,7 @@ __device__ __forceinline__ f64x4 gram_mfma(const double* x, int lane) {
 // in the layout of gram_mfma, formed from its rows of c.
 template <bool TRANS, int M, int K, int ldr, int ldb, int ldc = 0, bool GR = false>
 __device__ __forceinline__ void rm_mfma(const float* rm, const float* bt, double* c, float* ct, int tid,
-                                         f64x4* gp = nullptr) {
+                                         double* gp = nullptr) {
   constexpr int RW = M / 4, KP = 64 / RW, RG = RW / 4, NG = K / (4 * KP), BATCH = 4;
   static_assert(RW == 16 || RW == 64, "a wave's rows: one or four partitions of k");
   static_assert(NG % BATCH == 0 && ldr % 4 == 0 && ldb % 4 == 0 && ldc % 4 == 0, "whole batches, 16-byte rows");
@@ -268,18 +274,14 @@ constexpr double kOrthCut = 1e6;
 // diagonal are set to zero.  The Gram runs on fp64 MFMA over 4 row segments;
 // each row of Y is then solved against R by forward substitution.
 template <int D, int P, int M, bool STG>
-__device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int passes, const f64x4* pre = nullptr) {
+__device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int passes, const double* pre = nullptr) {
   static_assert(M % 16 == 0 && M <= kNT, "rows: 4 segments of whole MFMA steps, one row per thread");
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   constexpr int seg = M / 4;
   for (int pass = 0; pass < passes; ++pass) {
     {   // this wave's partial Gram (the first pass's may come from the product that formed Y)
-      const f64x4 g = (pass == 0 && pre) ? *pre : gram_mfma<seg>(cs.y + wave * seg * kLQ, lane);
-      const int r = lane >> 4, c = lane & 15;
-      if (c < kQ) {
-        cs.red[wave * 64 + r * kQ + c] = g[0];
-        cs.red[wave * 64 + (r + 4) * kQ + c] = g[1];
-      }
+      const double g = (pass == 0 && pre) ? *pre : gram_mfma<seg>(cs.y + wave * seg * kLQ, lane);
+      cs.red[wave * 64 + gram_entry(lane)] = g;
     }
     __syncthreads();
     if (wave == 0)   // the Gram, summed over the segments (rinv holds it row-major)
@@ -538,7 +540,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   // products leaves the final basis unchanged (up to column signs)
   // (each Y = R_mat Z product hands its partial Grams straight to the first
   // Cholesky-QR pass, whose barrier then also publishes Y)
-  f64x4 gp;
+  double gp;
   rm_mfma<false, m, n, ldr, lzn, 0, true>(cs.rm, cs.zt, cs.y, nullptr, tid, &gp);
   orth_rows<D, P, m, STG>(cs, tid, 1, &gp);
   for (int it = 0; it < 2; ++it) {
@@ -551,13 +553,8 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   rm_mfma<true, n, m, ldr, lym>(cs.rm, cs.yt, cs.z, nullptr, tid);
   __syncthreads();
   {  // W = Bm Bm^T: each wave's partial Gram over a quarter of the rows of Bm^T
-    static_assert(n % 16 == 0, "quarters of whole MFMA steps");
-    const f64x4 g = gram_mfma<n / 4>(cs.z + wave * (n / 4) * kLQ, lane);
-    const int r = lane >> 4, c = lane & 15;
-    if (c < kQ) {
-      cs.red[wave * 64 + r * kQ + c] = g[0];
-      cs.red[wave * 64 + (r + 4) * kQ + c] = g[1];
-    }
+    static_assert(n % 32 == 0, "quarters of whole MFMA steps");
+    cs.red[wave * 64 + gram_entry(lane)] = gram_mfma<n / 4>(cs.z + wave * (n / 4) * kLQ, lane);
   }
   __syncthreads();
   issue();
