@@ -340,6 +340,13 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
     }
     // the next rebuild's factors, issued ahead of this sub-chunk's input loads
     if (c > 0 && rebuilds(c - 1)) fetch_ab(c - 1);
+    // the decay of token c BP - P + tid (tid < P), loaded unconditionally at an
+    // in-bounds token and used raw in A: a load in a branch drew its clamp in
+    // after it, whose wait then held every input load issued above; issued
+    // before the inputs (its address arithmetic after them reused a register
+    // of a pending input load and so waited for all of them)
+    const int tpv = c * BP - P + (tid < P ? tid : 0);
+    const float dvp = p.dec[dec_base + (size_t)(tpv > 0 ? tpv : 0) * dec_tok];
 
     // the sub-chunk's inputs, the block entering the window (sub-chunk c -
     // NB) and the decays of the P tokens before the sub-chunk, loaded raw
@@ -385,11 +392,6 @@ __global__ void __launch_bounds__(kNT) gdn3_bwd_kernel(G3BwdArgs p) {
         }
     }
     load_block(c - NB, rkp, ruo);
-    // the decay of token c BP - P + tid (tid < P), loaded unconditionally at an
-    // in-bounds token and used raw in A: a load in a branch drew its clamp in
-    // after it, whose wait then held every input load issued above
-    const int tpv = c * BP - P + (tid < P ? tid : 0);
-    const float dvp = p.dec[dec_base + (size_t)(tpv > 0 ? tpv : 0) * dec_tok];
 
     // ---- S_kron^T of this interval (the factors of compaction iv - 1), rebuilt on entry ----
     if (rebuild) {
