@@ -377,11 +377,27 @@ struct G3NoOp {
 // issue / commit: work of the caller's that uses no compaction state and
 // runs in the eigen-solve's shadow (every thread calls issue before it; waves
 // 1-3 call commit while wave 0 solves, wave 0 after); 'svd' mode only.
+// pre: the sketch entries this thread stages, loaded by the caller (a chain's
+// sketch is the same at every compaction), else they are loaded here.
+template <int D>
+struct G3Sketch {
+  static constexpr int N = (G3D<D>::n * kQ + kNT - 1) / kNT;
+  float v[N];   // entry e = tid + u kNT: sketch row e / kQ, column e % kQ (zero past its qs columns)
+};
+template <int D>
+__device__ __forceinline__ void g3_sketch_load(G3Sketch<D>& g, const float* __restrict__ sketch, int qs, int tid) {
+#pragma unroll
+  for (int u = 0; u < G3Sketch<D>::N; ++u) {
+    const int e = tid + u * kNT, c = e / kQ, j = e % kQ;
+    g.v[u] = (e < G3D<D>::n * kQ && j < qs) ? sketch[c * qs + j] : 0.f;
+  }
+}
 template <int D, int P, bool STG, typename Issue = G3NoOp, typename Commit = G3NoOp>
 __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, const float* __restrict__ U,
                                            const float* __restrict__ Vb, size_t u_sp, size_t u_sd, float gacc,
                                            float sdec, const float* __restrict__ sketch, double* stats, int tid,
-                                           int mode = 0, Issue issue = Issue(), Commit commit = Commit()) {
+                                           int mode = 0, Issue issue = Issue(), Commit commit = Commit(),
+                                           const G3Sketch<D>* pre = nullptr) {
   typedef G3D<D> Ge;
   constexpr int R = Ge::R, m = Ge::m, n = Ge::n, q = Ge::q, ak = Ge::ak, bk = Ge::bk;
   constexpr int lbv = Ge::lbv, lbk = Ge::lbk, ln = Ge::ln;
@@ -391,16 +407,12 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   tid = opaque(tid);
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  // the sketch's global loads are issued first and land in LDS after the
-  // residual part (which does not read them)
-  constexpr int NGS = (n * kQ + kNT - 1) / kNT;
-  const int qs = mode ? R : q;   // the sketch's columns
-  float gsv[NGS];
-#pragma unroll
-  for (int u = 0; u < NGS; ++u) {
-    const int e = tid + u * kNT, c = e / kQ, j = e % kQ;
-    gsv[u] = (e < n * kQ && j < qs) ? sketch[c * qs + j] : 0.f;
-  }
+  // the sketch's global loads (unless the caller holds it) are issued first
+  // and land in LDS after the residual part (which does not read them)
+  constexpr int NGS = G3Sketch<D>::N;
+  G3Sketch<D> gs;
+  if (pre) gs = *pre;
+  else g3_sketch_load<D>(gs, sketch, mode ? R : q, tid);
   double en[1] = {0.0};
   // residual part rearrange(U Vb^T) on fp32 MFMA: out[v][k] = sum_p U_p[v] Vb_p[k]
   // (A[v][p] = U_p[v], B[p][k] = Vb_p[k]), accumulated over the window's
@@ -498,7 +510,7 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
 #pragma unroll
   for (int u = 0; u < NGS; ++u) {
     const int e = tid + u * kNT;
-    if (e < n * kQ) cs.zt[(e % kQ) * lzn + e / kQ] = gsv[u];
+    if (e < n * kQ) cs.zt[(e % kQ) * lzn + e / kQ] = gs.v[u];
   }
   block_sum<1>(en, cs.red, tid);
 
@@ -1908,6 +1920,14 @@ __global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
                               sm.vbx, sm.ph.w.G, sm.ph.w.alpha, sm.ph.w.lg, sm.ph.w.kco, sm.ph.w.qco,
                               sm.ph.w.gam, sm.ph.w.vsc, sm.boff};
   f32x4 uo[1][VPW];
+  // the chain's sketch, the same at every compaction, held from here (a load
+  // per compaction waited, in order, for the window's output stores before it)
+  G3Sketch<D> sk;
+  g3_sketch_load<D>(sk, p.sketch + (size_t)chain * Ge::n * (p.cmode ? Ge::R : Ge::q), p.cmode ? Ge::R : Ge::q, tid);
+  // (passed through an empty asm here, so that the loop sees register values,
+  // not loads it would wait for at every use)
+#pragma unroll
+  for (int u = 0; u < G3Sketch<D>::N; ++u) sk.v[u] = __int_as_float(opaque(__float_as_int(sk.v[u])));
   for (int c = cg0; c < cg1; ++c) {
     // the window step (its net writes through the registers of their waves)
 #pragma unroll
@@ -1941,7 +1961,7 @@ __global__ void __launch_bounds__(kNT) gdn3_fused_kernel(G3FwdArgs p) {
     };
     g3_compact<D, P>(sm.ph.cs, sm.ab, &sm.uwin[0][0], &sm.vbd[0][0], (size_t)(D + 4), (size_t)1, gacc, p.sdec,
                      p.sketch + (size_t)chain * Ge::n * qs,
-                     p.stats ? p.stats + ((size_t)event * N + chain) * 2 : nullptr, tid, p.cmode, issue, commit);
+                     p.stats ? p.stats + ((size_t)event * N + chain) * 2 : nullptr, tid, p.cmode, issue, commit, &sk);
     __syncthreads();
     if (p.train_states) {   // the factors after every compaction, for the backward
       const G3Stash ts = g3_stash(p.train_states, N, p.nch, p.T / p.Kc, D, kSC, Ge::RMN);
