@@ -266,6 +266,10 @@ __device__ __forceinline__ int rr_partner(int x, int st) {
 // the pivots' spread (largest / smallest, about cond(Y)^2) below this bound
 // makes a second pass unnecessary (Q orthonormal to ~1e-10).
 constexpr double kOrthCut = 1e6;
+// Pivot spread (about cond(Y)^2) below which an intermediate basis enters the
+// next product unnormalised: cond(Y) < 10 costs the fp32 products at most a
+// decimal digit in its weakest direction, against their 1e-7
+constexpr double kKeepCut = 1e2;
 
 // Y <- Y R^{-1} with Y^T Y = R^T R (Cholesky QR, up to `passes` times: one
 // pass keeps the intermediate power-iteration bases well conditioned; the
@@ -274,7 +278,8 @@ constexpr double kOrthCut = 1e6;
 // diagonal are set to zero.  The Gram runs on fp64 MFMA over 4 row segments;
 // each row of Y is then solved against R by forward substitution.
 template <int D, int P, int M, bool STG>
-__device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int passes, const double* pre = nullptr) {
+__device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int passes, const double* pre = nullptr,
+                                          double keep = 0.0) {
   static_assert(M % 16 == 0 && M <= kNT, "rows: 4 segments of whole MFMA steps, one row per thread");
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   constexpr int seg = M / 4;
@@ -315,6 +320,11 @@ __device__ __forceinline__ void orth_rows(G3Compact<D, P, STG>& cs, int tid, int
 #pragma unroll
         for (int j = k + 1; j <= i; ++j) L[i][j] -= L[i][k] * L[j][k];
     }
+    // keep > 0 (an intermediate basis, whose fp32 copy the product wrote):
+    // where the pivots spread by less than keep, Y is conditioned well enough
+    // to enter the next product as it is (the basis only has to stay well
+    // conditioned; its span is what the power iteration carries)
+    if (keep > 0.0 && __builtin_amdgcn_readfirstlane(pmin * keep > pmax ? 1 : 0)) return;
     if (tid < M) {
       double x[kQ];
 #pragma unroll
@@ -553,13 +563,13 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
   // (each Y = R_mat Z product hands its partial Grams straight to the first
   // Cholesky-QR pass, whose barrier then also publishes Y)
   double gp;
-  rm_mfma<false, m, n, ldr, lzn, 0, true>(cs.rm, cs.zt, cs.y, nullptr, tid, &gp);
-  orth_rows<D, P, m, STG>(cs, tid, 1, &gp);
+  rm_mfma<false, m, n, ldr, lzn, lym, true>(cs.rm, cs.zt, cs.y, cs.yt, tid, &gp);
+  orth_rows<D, P, m, STG>(cs, tid, 1, &gp, kKeepCut);
   for (int it = 0; it < 2; ++it) {
     rm_mfma<true, n, m, ldr, lym, lzn>(cs.rm, cs.yt, cs.z, cs.zt, tid);
     __syncthreads();
-    rm_mfma<false, m, n, ldr, lzn, 0, true>(cs.rm, cs.zt, cs.y, nullptr, tid, &gp);
-    orth_rows<D, P, m, STG>(cs, tid, it == 1 ? 2 : 1, &gp);
+    rm_mfma<false, m, n, ldr, lzn, lym, true>(cs.rm, cs.zt, cs.y, cs.yt, tid, &gp);
+    orth_rows<D, P, m, STG>(cs, tid, it == 1 ? 2 : 1, &gp, it == 1 ? 0.0 : kKeepCut);
   }
   // Bm^T = R_mat^T Q  [n][kQ]
   rm_mfma<true, n, m, ldr, lym>(cs.rm, cs.yt, cs.z, nullptr, tid);
