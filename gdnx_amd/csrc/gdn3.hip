@@ -597,14 +597,15 @@ __device__ __forceinline__ void g3_compact(G3Compact<D, P, STG>& cs, float* ab, 
       a = (cs.red[e] + cs.red[64 + e]) + (cs.red[128 + e] + cs.red[192 + e]);
     }
     double vv = (i == j) ? 1.0 : 0.0;
+    // |W|_F^2, which the rotations keep: the diagonal's mass is fro - off
+    const double fro = wave_sum_f64(a * a);
     for (int sweep = 0; sweep < 12; ++sweep) {
       if (sweep >= 4) {   // (fewer than four sweeps rarely suffice; extra sweeps over a diagonal W rotate by identities)
         const double off = wave_sum_f64(i != j ? a * a : 0.0);
-        const double dia = wave_sum_f64(i == j ? a * a : 0.0);
         // stop at off-diagonal entries ~1e-8 of the diagonal's (in norm): the
         // eigenvectors then sit within ~1e-8 / (relative gap) of W's, an order
         // below what the fp32 products that formed Bm already left in W
-        if (!(off > 1e-16 * dia)) break;  // uniform across the wave
+        if (!(off > 1e-16 * (fro - off))) break;  // uniform across the wave
       }
 #pragma unroll
       for (int st = 0; st < 7; ++st) {
