@@ -98,7 +98,22 @@ __global__ void __launch_bounds__(kDT) gdn3_decode_kernel(G3DecArgs p) {
   float* Ug = p.U + sidx * DP;
   float* Vg = p.Vb + sidx * DP;
 
-  // the state stream first
+  // the token's inputs first (a few scalars per thread), then the state
+  // stream: loads retire in order, so staging the inputs below waits only for
+  // them, not for the state behind them
+  const float gam = fminf(fmaxf(p.dec[chain], 0.f), 1.f);
+  const int L = p.qkv_lanes, gc = p.gate_ch;
+  const size_t io = (((size_t)row * p.H + h) * L + (L > 1 ? m : 0)) * D;
+  const size_t go = (size_t)chain * gc;
+  static_assert(D <= kDT, "one input element per thread");
+  float in_k = 0.f, in_q = 0.f, in_v = 0.f, in_b = 0.f, in_w = 0.f;
+  if (tid < D) {
+    in_k = to_f(((const IO*)p.k)[io + tid]);
+    in_q = to_f(((const IO*)p.q)[io + tid]);
+    in_v = to_f(((const IO*)p.v)[io + tid]);
+    in_b = p.bg[go + (gc > 1 ? tid : 0)];
+    in_w = p.wg[go + (gc > 1 ? tid : 0)];
+  }
   f32x4 ra[NA], rb[NB], ru[NU], rv[NU];
 #pragma unroll
   for (int j = 0; j < NA; ++j)
@@ -112,17 +127,11 @@ __global__ void __launch_bounds__(kDT) gdn3_decode_kernel(G3DecArgs p) {
       ru[j] = ((const f32x4*)Ug)[tid + j * kDT];
       rv[j] = __builtin_nontemporal_load((const f32x4*)Vg + tid + j * kDT);
     }
-  const float gam = fminf(fmaxf(p.dec[chain], 0.f), 1.f);
-  const int L = p.qkv_lanes, gc = p.gate_ch;
-  const size_t io = (((size_t)row * p.H + h) * L + (L > 1 ? m : 0)) * D;
-  const size_t go = (size_t)chain * gc;
-  for (int d = tid; d < D; d += kDT) {
-    const float kk = to_f(((const IO*)p.k)[io + d]);
-    const float bb = p.bg[go + (gc > 1 ? d : 0)], ww = p.wg[go + (gc > 1 ? d : 0)];
-    sm.k[d] = kk;
-    sm.x[0][d] = bb * kk;
-    sm.x[1][d] = to_f(((const IO*)p.q)[io + d]);
-    sm.u[d] = ww * to_f(((const IO*)p.v)[io + d]);
+  if (tid < D) {
+    sm.k[tid] = in_k;
+    sm.x[0][tid] = in_b * in_k;
+    sm.x[1][tid] = in_q;
+    sm.u[tid] = in_w * in_v;
   }
 #pragma unroll
   for (int j = 0; j < NA; ++j)
