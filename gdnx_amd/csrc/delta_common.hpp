@@ -183,17 +183,27 @@ __device__ __forceinline__ void scal_commit(const ChunkScalars& s, const ScalarR
   }
 }
 
+// The loads of prep_scalars (issued early, consumed later: loads retire in
+// order, so what is issued before a larger stream does not wait for it)
+struct ScalarVals {
+  float ae, aw, raw;
+};
 template <int C>
-__device__ __forceinline__ void prep_scalars(const ChunkScalars& s, const float* ae, const float* aw,
-                                             const float* g, size_t st, int t0, int T, int lane) {
-  float vae = 0.f, vaw = 0.f, vg = 0.f, raw = 0.f;
+__device__ __forceinline__ ScalarVals prep_scalars_load(const float* ae, const float* aw, const float* g, size_t st,
+                                                        int t0, int T, int lane) {
+  ScalarVals v{0.f, 0.f, 0.f};
   const int t = t0 + lane;
   if (lane < C && t < T) {
-    if (ae) vae = ae[(size_t)t * st];
-    if (aw) vaw = aw[(size_t)t * st];
-    raw = g[(size_t)t * st];
-    vg = fmaxf(fminf(raw, 0.f), kLogFloor);
+    if (ae) v.ae = ae[(size_t)t * st];
+    if (aw) v.aw = aw[(size_t)t * st];
+    v.raw = g[(size_t)t * st];
   }
+  return v;
+}
+template <int C>
+__device__ __forceinline__ void prep_scalars_commit(const ChunkScalars& s, const ScalarVals& v, int lane) {
+  const float vae = v.ae, vaw = v.aw, raw = v.raw;
+  const float vg = lane < C ? fmaxf(fminf(raw, 0.f), kLogFloor) : 0.f;
   const float G = lane_prefix<C>(vg, lane);
   const float Glast = lane_value(G, C - 1);
   if (lane < C) {
@@ -204,6 +214,12 @@ __device__ __forceinline__ void prep_scalars(const ChunkScalars& s, const float*
     if (s.aw) s.aw[lane] = vaw;
     if (s.graw) s.graw[lane] = raw;
   }
+}
+
+template <int C>
+__device__ __forceinline__ void prep_scalars(const ChunkScalars& s, const float* ae, const float* aw,
+                                             const float* g, size_t st, int t0, int T, int lane) {
+  prep_scalars_commit<C>(s, prep_scalars_load<C>(ae, aw, g, st, t0, T, lane), lane);
 }
 
 // Registers holding one thread's share of a chunk tile ([C][D] rows, 4

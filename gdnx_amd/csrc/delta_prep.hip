@@ -91,6 +91,11 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) __attribute__((amdgpu_wa
       sm.ln[l].t[i] = from_f<CT>(0.f);
       sm.ln[l].aq[i] = from_f<CT>(0.f);
     }
+  // the first lane group's token scalars are issued before the q/k tiles:
+  // loads retire in order, so issued after the tiles they would wait for them
+  const size_t sbase = ((size_t)b * p.T * p.H + h) * p.M + wave;
+  ScalarVals sv{0.f, 0.f, 0.f};
+  if (wave < min(LP, p.M)) sv = prep_scalars_load<C>(p.ae + sbase, p.aw + sbase, p.g + sbase, st, t0, p.T, lane);
   {
     Stage<CT, C, D, 1, NT> sq, sk;
     const unsigned rsb = (unsigned)(rs * sizeof(CT)), nb = (unsigned)min(C, p.T - t0) * rsb;
@@ -126,8 +131,8 @@ __global__ void __launch_bounds__((Dims<CT, D, C>::NT)) __attribute__((amdgpu_wa
     if (wave < nl) {
       PrepLane<CT, D, C>& P = sm.ln[wave];
       const ChunkScalars cs{P.G, P.gam, P.dec, P.ae, P.aw, nullptr};
-      const size_t soff = ((size_t)b * p.T * p.H + h) * p.M + m0 + wave;
-      prep_scalars<C>(cs, p.ae + soff, p.aw + soff, p.g + soff, st, t0, p.T, lane);
+      if (m0 > 0) sv = prep_scalars_load<C>(p.ae + sbase + m0, p.aw + sbase + m0, p.g + sbase + m0, st, t0, p.T, lane);
+      prep_scalars_commit<C>(cs, sv, lane);
     }
     __syncthreads();
     // ---- each lane's L (fp32, plus transposed diagonal blocks) and Aq ----
