@@ -210,7 +210,7 @@ def test_gdn3_training_call_returns_state_and_error(gpu_lib):
 
 
 @pytest.mark.parametrize("M,D,dt", [(4, 128, torch.bfloat16), (4, 64, torch.float32), (3, 128, torch.float32),
-                                    (1, 64, torch.bfloat16)])
+                                    (1, 64, torch.bfloat16), (8, 128, torch.float32)])
 def test_lane_sum_matches_torch(gpu_lib, M, D, dt):
     """gdnx_lane_sum (the lane-shared q/k/v gradient): the sum over the lanes
     in lane order, cast to the IO dtype, equals the float64 sum rounded once
@@ -225,6 +225,10 @@ def test_lane_sum_matches_torch(gpu_lib, M, D, dt):
     assert out.shape == (2, 33, 3, D) and out.dtype == dt
     if dt == torch.float32:
         torch.testing.assert_close(out.cpu().double(), ref, rtol=0, atol=4 * 2.0 ** -24 * float(x.abs().max()) * M)
+        seq = x[:, :, :, 0].clone()   # float32 adds in lane order: bit-exact
+        for m in range(1, M):
+            seq += x[:, :, :, m]
+        assert torch.equal(out.cpu(), seq)
     else:   # within one bf16 rounding of the exact sum
         err = (out.cpu().double() - ref).abs()
         assert bool((err <= ref.abs() * 2.0 ** -8 + 1e-30).all())
