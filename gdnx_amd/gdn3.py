@@ -47,6 +47,8 @@ class GDN3ScanFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, beta, log_g, state0):
         train = any(ctx.needs_input_grad)
+        # an unused output's gradient arrives as None (no zero tensor is filled)
+        ctx.set_materialize_grads(False)
         D = q.shape[-1]
         a = ops.gdn3_coeff(k, beta)
         chunk, two_pass = ops.forward_plan(D, q.dtype, train)
@@ -133,6 +135,8 @@ class _GDN3Chunk(torch.autograd.Function):
 
     @staticmethod
     def forward(ctx, q, k, v, bg, wg, dec, sketch, cfg, want_state):
+        # the statistics' and states' (non-differentiable) gradients arrive as None
+        ctx.set_materialize_grads(False)
         M, R, P, factors, slow_decay, Kc, cmode = cfg
         y, stats, state, tst = ops.gdn3_chunk_fwd(q, k, v, bg, wg, dec, sketch, M=M, R=R, P=P, factors=factors,
                                                   slow_decay=slow_decay, compact_every=Kc,

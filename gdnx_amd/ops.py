@@ -168,6 +168,8 @@ class DeltaRuleFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, a_e, a_w, log_g, state0=None, want_rnorm=False):
         train = any(ctx.needs_input_grad)
+        # an unused output's gradient arrives as None (no zero tensor is filled)
+        ctx.set_materialize_grads(False)
         D = q.shape[-1]
         chunk, two_pass = forward_plan(D, q.dtype, train, scored=want_rnorm)
         rn = torch.empty(a_e.shape, dtype=torch.float32, device=q.device) if want_rnorm else None
@@ -410,6 +412,8 @@ class ChanRuleFunction(torch.autograd.Function):
     @staticmethod
     def forward(ctx, q, k, v, beta_e, beta_w, log_g, state0=None, want_rnorm=False):
         train = any(ctx.needs_input_grad)
+        # an unused output's gradient arrives as None (no zero tensor is filled)
+        ctx.set_materialize_grads(False)
         rn = torch.empty(q.shape[:3], dtype=torch.float32, device=q.device) if want_rnorm else None
         y, s_out, cs = delta_chan_fwd(q, k, v, beta_e, beta_w, log_g, state0, save_states=train, r_norm=rn)
         if train:

@@ -146,6 +146,33 @@ def test_state_gradients_fp32(gpu_lib):
     _check(vals, dO, 1e-4, state0=s0, dstate=ds)
 
 
+def test_unused_output_gradients(gpu_lib):
+    """An output the loss does not use reaches the backward as None (no zero
+    tensor filled): a loss of y alone gives the gradients of y plus a zero
+    state gradient, and a loss of the final state alone those of the state
+    plus a zero dy, bit for bit."""
+    from gdnx_amd import ops
+    print("case: unused output gradients", flush=True)
+    dev = "cuda:0"
+    vals, dO = _case(1, 70, 2, 64, 2, seed=29, dtype=torch.float32)
+    ds = torch.randn(1, 2, 2, 64, 64, generator=torch.Generator().manual_seed(5)).to(dev)
+    dO = dO.to(dev).float()
+
+    def grads(use_y, use_s, zero_other):
+        ins = [t.to(dev).clone().requires_grad_(True) for t in vals]
+        y, sT = ops.delta_rule(*ins)
+        loss = (y.float() * (dO if use_y else 0 * dO)).sum() if use_y or zero_other else 0
+        if use_s or zero_other:
+            loss = loss + (sT * (ds if use_s else 0 * ds)).sum()
+        g = torch.autograd.grad(loss, ins)
+        torch.cuda.synchronize()
+        return [t.cpu() for t in g]
+
+    for use_y, use_s in ((True, False), (False, True)):
+        for a_, b_ in zip(grads(use_y, use_s, False), grads(use_y, use_s, True)):
+            assert torch.equal(a_, b_)
+
+
 def test_config2_full_size_gradients(gpu_lib):
     """Config 2 (B=4, T=4096, H=16, D=128, 4 lanes, bf16) end to end on the
     GPU; the float64 oracle checks batch 0 / head 0 (heads are independent,
